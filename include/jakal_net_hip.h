@@ -1,0 +1,99 @@
+/*
+ * jakal_net_hip.h -- C ABI of the MI355X (gfx950) Jakal-Net native hot path.
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer to
+ * a contiguous row-major float32 / int32 buffer on the current HIP device, and
+ * `stream` is a hipStream_t (passed as void*).  Calls are asynchronous on
+ * `stream`; none allocates device memory (scratch comes in through
+ * `workspace`, sized by the matching *_workspace_bytes query).
+ *
+ * Every entry point returns 0 on success and a non-zero jn status on error;
+ * jn_last_error() then holds a message for the calling host thread.
+ *
+ * Index conventions: B = flattened batch, N = nodes, r = rank, k = top-k.
+ * "projections" is one [B*N, 2r] buffer: columns [0, r) hold the target
+ * projection layer_val . U^T, columns [r, 2r) the unscaled source projection
+ * layer_val . V^T (U = target_proj.weight, V = source_proj.weight).
+ */
+#ifndef JAKAL_NET_HIP_H
+#define JAKAL_NET_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* jn_stream_t;
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* jn_last_error(void);
+
+/* ABI revision of this header (bumped on any signature change). */
+int jn_abi_version(void);
+
+/*
+ * Low-rank score + per-row top-k select, no score matrix materialised.
+ *   s[b,i,j] = ((sum_r query[b,i,r]*cq[r] * key[b,j,r]*ck[r]) + bias) / temperature
+ * where the scale vector multiplies the query rows when scale_on_query != 0,
+ * else the key rows.  Writes the k best (j, s) per row, sorted descending,
+ * ties toward the lower j.  1 <= k <= 32, k < nk, 1 <= rank <= 128.
+ * Replaces the score/select stage of
+ *   propagation_topk            (native/jakal_net_native.cpp:6399-6424)
+ *   low_rank_propagation_topk_forward_cuda (native/jakal_net_native_cuda.cu:1028-1110)
+ *   low_rank_pairwise_topk_forward_cuda    (native/jakal_net_native_cuda.cu:739-813)
+ */
+int jn_lowrank_topk_select(const float* query, int64_t ldq, int64_t query_batch_stride, const float* key,
+                           int64_t ldk, int64_t key_batch_stride, const float* scale, int32_t scale_on_query,
+                           const float* bias, float temperature, int64_t batch, int64_t nq, int64_t nk,
+                           int64_t rank, int64_t topk, int32_t* out_index, float* out_score, jn_stream_t stream);
+
+/*
+ * SparsePropagation(sparse_type="topk", LowRankBilinearPairwise) forward.
+ *   layer_val [B,N,Din], projected_state [B,N], projected_val [B,N,Dout],
+ *   target_weight U [r,Din], source_weight V [r,Din], core_weight w_hat [r]
+ *   (already normalised, kernel_common.py:185-192), bias scalar or NULL.
+ * Outputs delta_state [B,N], delta_val [B,N,Dout] and, for the backward,
+ * projections [B*N,2r], topk_index [B,N,k] (int32), topk_score [B,N,k].
+ * compress_kind: 0 softsign, 1 signed_abs_softmax.
+ * Replaces propagation_topk (native/jakal_net_native.cpp:6305-6447) and
+ * low_rank_propagation_topk_forward_cuda (native/jakal_net_native.cpp:191-213).
+ */
+int jn_propagation_topk_forward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                const float* target_weight, const float* source_weight, const float* core_weight,
+                                const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                int64_t rank, int64_t topk, int32_t compress_kind, float* delta_state,
+                                float* delta_val, float* projections, int32_t* topk_index, float* topk_score,
+                                jn_stream_t stream);
+
+/* Workspace needed by jn_propagation_topk_backward. */
+size_t jn_propagation_topk_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                           int64_t rank, int64_t topk);
+
+/*
+ * Backward of jn_propagation_topk_forward given grad_delta_state [B,N] and
+ * grad_delta_val [B,N,Dout].  Output pointers may be NULL to skip a gradient.
+ * When projected_val_is_layer_val != 0 (identity val_proj_fn) the value
+ * gradient is folded into grad_layer_val and grad_projected_val is unused.
+ * grad_core_weight is the gradient wrt w_hat; grad_bias a single float.
+ * Deterministic: no floating-point atomics.
+ * Replaces _LowRankPropagationTopK.backward (src/jakal_net/native_backend.py:4872-4964):
+ * query_topk_reduce_backward_cuda, softsign_backward_cuda and
+ * low_rank_pairwise_topk_backward_cuda (native/jakal_net_native.cpp:152-165, 398-416, 449-477).
+ */
+int jn_propagation_topk_backward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                 const float* target_weight, const float* source_weight, const float* core_weight,
+                                 const float* projections, const int32_t* topk_index, const float* topk_score,
+                                 const float* grad_delta_state, const float* grad_delta_val, int64_t batch,
+                                 int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t topk,
+                                 int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val,
+                                 float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
+                                 float* grad_source_weight, float* grad_core_weight, float* grad_bias,
+                                 void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JAKAL_NET_HIP_H */

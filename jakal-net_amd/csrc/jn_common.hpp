@@ -1,0 +1,128 @@
+// Shared device/host helpers for the Jakal-Net MI355X (gfx950) hot path.
+//
+// Everything here is written for CDNA4 wave64 execution: one wavefront = 64
+// lanes, cross-lane traffic through ds_bpermute / readlane, fp32 MFMA tiles
+// from __builtin_amdgcn_mfma_f32_16x16x4f32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+namespace jakal {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Host-side error channel.  Every C-ABI entry point returns 0 on success and a
+// non-zero code on failure; the message is kept per host thread and read back
+// through jn_last_error().
+// ---------------------------------------------------------------------------
+enum Status : int {
+  kOk = 0,
+  kInvalidArgument = 1,
+  kUnsupported = 2,
+  kHipError = 3,
+  kWorkspaceTooSmall = 4,
+};
+
+void set_error(const char* fmt, ...);
+const char* last_error();
+
+#define JN_REQUIRE(cond, code, ...)   \
+  do {                                \
+    if (!(cond)) {                    \
+      ::jakal::set_error(__VA_ARGS__);   \
+      return (code);                  \
+    }                                 \
+  } while (0)
+
+#define JN_HIP_TRY(expr)                                                        \
+  do {                                                                          \
+    hipError_t jn_err__ = (expr);                                               \
+    if (jn_err__ != hipSuccess) {                                               \
+      ::jakal::set_error("%s failed: %s", #expr, hipGetErrorString(jn_err__));     \
+      return ::jakal::kHipError;                                                   \
+    }                                                                           \
+  } while (0)
+
+#define JN_LAUNCH_CHECK()                                                       \
+  do {                                                                          \
+    hipError_t jn_err__ = hipGetLastError();                                    \
+    if (jn_err__ != hipSuccess) {                                               \
+      ::jakal::set_error("kernel launch failed at %s:%d: %s", __FILE__, __LINE__,  \
+                      hipGetErrorString(jn_err__));                             \
+      return ::jakal::kHipError;                                                   \
+    }                                                                           \
+  } while (0)
+
+// Bump allocator over a caller-provided workspace.  Offsets are 256-byte
+// aligned so every carved buffer is suitable for 16-byte vector access.
+struct Workspace {
+  char* base;
+  size_t size;
+  size_t used = 0;
+  bool sizing_only;
+
+  Workspace(void* ptr, size_t bytes) : base(static_cast<char*>(ptr)), size(bytes), sizing_only(ptr == nullptr) {}
+
+  template <typename T>
+  T* take(size_t count) {
+    size_t bytes = (count * sizeof(T) + 255) & ~size_t(255);
+    char* p = sizing_only ? nullptr : base + used;
+    used += bytes;
+    return reinterpret_cast<T*>(p);
+  }
+  bool overflow() const { return !sizing_only && used > size; }
+};
+
+// ---------------------------------------------------------------------------
+// Device helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  int lane = lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
+}
+__device__ __forceinline__ int shfl_xor_i(int v, int mask) {
+  int lane = lane_id();
+  return __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, v);
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ int readlane_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_f(v, m);
+  return v;
+}
+
+// Make LDS writes of this wavefront visible to later LDS reads of the same
+// wavefront by other lanes (compiler + hardware ordering, no workgroup barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Edge compression applied to a selected score (reference: propagation.py:85-88
+// softsign; transition softmax is applied per row elsewhere).
+__device__ __forceinline__ float softsign_f(float s) { return s / (1.0f + fabsf(s)); }
+__device__ __forceinline__ float softsign_grad_f(float s) {
+  float d = 1.0f + fabsf(s);
+  return 1.0f / (d * d);
+}
+
+// "a ranks before b" in a descending top-k with ties toward the lower index.
+__device__ __forceinline__ bool ranks_before(float as, int ai, float bs, int bi) {
+  return (as > bs) || (as == bs && ai < bi);
+}
+
+}  // namespace jakal

@@ -1,0 +1,117 @@
+// Launch interfaces shared between the kernel translation units and the C ABI.
+#pragma once
+
+#include "jn_common.hpp"
+
+namespace jakal {
+
+// ---- score + top-k select (jn_select.hip) ---------------------------------
+struct SelectArgs {
+  const float* q;       // query rows, row stride ldq, batch stride q_batch_stride
+  const float* key;     // key rows, row stride ldk, batch stride k_batch_stride
+  int64_t ldq, ldk;
+  int64_t q_batch_stride, k_batch_stride;
+  const float* scale;   // [r] or null
+  const float* bias;    // scalar or null
+  int scale_on_query;
+  float temperature;
+  int B, Nq, Nk, r, k;
+  int32_t* out_idx;     // [B, Nq, k]
+  float* out_score;     // [B, Nq, k]
+};
+int launch_topk_select(const SelectArgs& a, hipStream_t stream);
+constexpr int kSelectMaxK = 32;
+
+// ---- fp32 MFMA GEMMs (jn_gemm.hip) ----------------------------------------
+int gemm_project(const float* X, int64_t ldx, const float* W0, const float* W1, int split, int64_t ldw, float* C,
+                 int64_t ldc, int M, int N, int K, hipStream_t stream);
+int gemm_grad_input(const float* dP, int64_t ldp, const float* W0, const float* W1, int split, int64_t ldw,
+                    const float* addend, int64_t ld_add, float* dX, int64_t ldx, int M, int N, int K,
+                    hipStream_t stream);
+size_t gemm_grad_weight_workspace(int M, int N, int K);
+int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, float* out0, float* out1, int m_split,
+                     int M, int N, int K, float* partial, hipStream_t stream);
+
+// ---- edge-list kernels (jn_edges.hip) -------------------------------------
+struct RowsFwdArgs {
+  const int32_t* idx;
+  const float* score;
+  int k;
+  int compress;
+  const float* ps;   // [B, Nk]
+  const float* pv;   // [B, Nk, D] row stride ld_pv
+  int64_t ld_pv;
+  int Nq, Nk, D;
+  int64_t rows;
+  float* out_state;  // [rows]
+  float* out_val;    // [rows, D]
+};
+int launch_rows_forward(const RowsFwdArgs& a, hipStream_t stream);
+
+struct RowsBwdArgs {
+  const int32_t* idx;
+  const float* score;
+  int k;
+  int compress;
+  float inv_temperature;
+  const float* ps;        // [B, Nk]
+  const float* pv;        // [B, Nk, D], row stride ld_pv
+  int64_t ld_pv;
+  const float* gds;       // [rows]
+  const float* gdv;       // [rows, D]
+  const float* key;       // key projection rows, row stride ldk (batch stride Nk*ldk)
+  int64_t ldk;
+  const float* qscale;    // [r] scale applied to dQ (null = 1)
+  int r;
+  int Nq, Nk, D;
+  int64_t rows;
+  float* g_score;         // [rows, k]
+  float* coef;            // [rows, k]
+  float* dq;              // [rows, r], row stride lddq
+  int64_t lddq;
+  float* rowsum_gs;       // [rows]
+};
+int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream);
+
+struct CsrArgs {
+  const int32_t* idx;
+  int k;
+  int B, Nq, Nk;
+  int32_t* tile_base;  // [B, T, Nk]: per-tile counts, then exclusive bases
+  int32_t* seg_start;  // [B, Nk + 1]
+  int32_t* edges;      // [B * Nq * k] edge ids (row * k + e), grouped by key
+};
+constexpr int kCsrTile = 64;
+int launch_csr(const CsrArgs& a, hipStream_t stream);
+
+struct ColsBwdArgs {
+  const int32_t* seg_start;  // [B, Nk + 1]
+  const int32_t* edges;      // grouped by key, batch b at offset b*Nq*k
+  int k;
+  const float* coef;         // [rows, k]
+  const float* g_score;      // [rows, k]
+  const float* gds;          // [rows] (null: skip state)
+  const float* gdv;          // [rows, D]
+  const float* q;            // query projection rows (global row index), stride ldq
+  int64_t ldq;
+  const float* key;          // key projection rows (global column index), stride ldk
+  int64_t ldk;
+  const float* kscale;       // [r] (null = 1)
+  int r;
+  int B, Nq, Nk, D;
+  int cols_per_wave;
+  float* grad_pv;            // [B*Nk, D] (null: skip)
+  int64_t ld_gpv;
+  int accumulate_gpv;        // add into grad_pv instead of overwrite
+  float* grad_ps;            // [B*Nk] (null: skip)
+  float* dk;                 // [B*Nk, r], stride lddk
+  int64_t lddk;
+  float* part_c;             // [num_waves, r]
+};
+int cols_backward_waves(int64_t total_cols, int cols_per_wave);
+int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream);
+
+int launch_finalize_small_grads(const float* part_c, int nparts, int r, float* grad_c, int accumulate_c,
+                                const float* rowsum, int64_t nrows, float* grad_bias, hipStream_t stream);
+
+}  // namespace jakal

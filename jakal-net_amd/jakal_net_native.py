@@ -1,0 +1,330 @@
+"""jakal_net_native -- the native-backend module, backed by the gfx950 HIP library.
+
+Stands where the reference's pybind extension ``jakal_net_native``
+(``native/jakal_net_native.cpp:7379-7500``) stands: same module name, same
+``supported_ops() / supported_devices() / backend_name()`` contract and the
+same positional op signatures, so ``jakal_net.native_backend`` (and the
+reference's own loader) dispatch to it unchanged.
+
+Each op flattens batch dimensions, casts to fp32 contiguous buffers and calls
+the C ABI of ``lib/libjakal_net_hip.so`` (declared in ``include/jakal_net_hip.h``)
+through ctypes on the current HIP stream.  Gradients come from
+``torch.autograd.Function`` wrappers whose backward calls the library's
+backward entry points.  Importing this module fails if the library cannot be
+loaded; nothing here computes on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+from torch import Tensor
+
+LIB_ENV = "JAKAL_NET_HIP_LIB"
+_HERE = Path(__file__).resolve().parent
+
+
+def library_path() -> Path:
+    override = os.environ.get(LIB_ENV)
+    return Path(override) if override else _HERE / "lib" / "libjakal_net_hip.so"
+
+
+_LIB = ctypes.CDLL(str(library_path()))
+
+_P, _I64, _I32, _F, _SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float, ctypes.c_size_t
+
+
+def _declare(name: str, argtypes: list, restype=ctypes.c_int) -> None:
+    fn = getattr(_LIB, name)
+    fn.argtypes = argtypes
+    fn.restype = restype
+
+
+_declare("jn_last_error", [], ctypes.c_char_p)
+_declare("jn_abi_version", [])
+_declare(
+    "jn_lowrank_topk_select",
+    [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _F, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
+)
+_declare(
+    "jn_propagation_topk_forward",
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P],
+)
+_declare("jn_propagation_topk_workspace_bytes", [_I64, _I64, _I64, _I64, _I64, _I64], _SZ)
+_declare(
+    "jn_propagation_topk_backward",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
+     _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+
+ABI_VERSION = int(_LIB.jn_abi_version())
+
+_COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1}
+MAX_TOPK = 32
+
+_SUPPORTED_OPS = (
+    "propagation_topk",
+    "low_rank_topk_select",
+)
+
+
+def supported_ops() -> list[str]:
+    return list(_SUPPORTED_OPS)
+
+
+def supported_devices() -> list[str]:
+    # ROCm PyTorch reports HIP devices with device.type == "cuda".
+    return ["cuda"]
+
+
+def backend_name() -> str:
+    return "hip_gfx950"
+
+
+def loaded_library() -> str:
+    return str(library_path())
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"jakal_net HIP library error {rc}: {_LIB.jn_last_error().decode(errors='replace')}")
+
+
+def _ptr(t: Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(*tensors: Tensor | None) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(f"jakal_net_native ops need GPU tensors, got a tensor on {t.device}.")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise RuntimeError("jakal_net_native ops need all tensors on one device.")
+    assert device is not None
+    return device
+
+
+def _f32(t: Tensor | None) -> Tensor | None:
+    return None if t is None else t.float().contiguous()
+
+
+def _same_storage_view(a: Tensor, b: Tensor) -> bool:
+    return a is b or (
+        a.data_ptr() == b.data_ptr() and a.shape == b.shape and a.stride() == b.stride() and a.dtype == b.dtype
+    )
+
+
+# ---------------------------------------------------------------------------
+# top-k propagation
+# ---------------------------------------------------------------------------
+class _PropagationTopK(torch.autograd.Function):
+    """Differentiable top-k low-rank propagation on the HIP library.
+
+    Inputs (all fp32, contiguous): layer_val X [B,N,Din], projected_state
+    [B,N], projected_val [B,N,Dout] or None when it is X itself, V and U
+    [r,Din], w_hat [r], bias [] or None."""
+
+    @staticmethod
+    def forward(ctx, X, ps, pv, V, U, w_hat, bias, k: int, compress: int):  # noqa: N803
+        B, N, Din = X.shape
+        pv_is_x = pv is None
+        pv_t = X if pv_is_x else pv
+        Dout = pv_t.shape[-1]
+        r = U.shape[0]
+        dev = X.device
+        with torch.cuda.device(dev):
+            ds = torch.empty(B, N, device=dev, dtype=torch.float32)
+            dv = torch.empty(B, N, Dout, device=dev, dtype=torch.float32)
+            proj = torch.empty(B * N, 2 * r, device=dev, dtype=torch.float32)
+            idx = torch.empty(B, N, k, device=dev, dtype=torch.int32)
+            score = torch.empty(B, N, k, device=dev, dtype=torch.float32)
+            _check(
+                _LIB.jn_propagation_topk_forward(
+                    _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
+                    B, N, Din, Dout, r, k, compress,
+                    _ptr(ds), _ptr(dv), _ptr(proj), _ptr(idx), _ptr(score), _stream(dev),
+                )
+            )
+        ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, idx, score)
+        ctx.meta = (k, compress, pv_is_x, bias is not None)
+        ctx.mark_non_differentiable(idx, score)
+        return ds, dv, idx, score
+
+    @staticmethod
+    def backward(ctx, g_ds, g_dv, _g_idx=None, _g_score=None):
+        X, ps, pv, V, U, w_hat, proj, idx, score = ctx.saved_tensors
+        k, compress, pv_is_x, has_bias = ctx.meta
+        B, N, Din = X.shape
+        Dout = pv.shape[-1]
+        r = U.shape[0]
+        dev = X.device
+        need = ctx.needs_input_grad
+        with torch.cuda.device(dev):
+            g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
+            g_dv = torch.zeros(B, N, Dout, device=dev) if g_dv is None else g_dv.float().contiguous()
+            gX = torch.empty_like(X) if (need[0] or (pv_is_x and need[0])) else None
+            gps = torch.empty_like(ps) if need[1] else None
+            gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
+            gV = torch.empty_like(V)
+            gU = torch.empty_like(U)
+            gw = torch.empty_like(w_hat)
+            gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
+            ws_bytes = int(_LIB.jn_propagation_topk_workspace_bytes(B, N, Din, Dout, r, k))
+            ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            _check(
+                _LIB.jn_propagation_topk_backward(
+                    _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat),
+                    _ptr(proj), _ptr(idx), _ptr(score), _ptr(g_ds), _ptr(g_dv),
+                    B, N, Din, Dout, r, k, compress, 1 if pv_is_x else 0,
+                    _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
+                    _ptr(ws), ws_bytes, _stream(dev),
+                )
+            )
+        return (
+            gX,
+            gps,
+            gpv,
+            gV if need[3] else None,
+            gU if need[4] else None,
+            gw if need[5] else None,
+            gb if (has_bias and need[6]) else None,
+            None,
+            None,
+        )
+
+
+def _lowrank_pairwise_args(kind, weight, bias, in_weight, in_bias, out_weight, out_bias):
+    if kind != "low_rank_bilinear":
+        raise TypeError(f"jakal_net_native supports pairwise kind 'low_rank_bilinear', got {kind!r}.")
+    if in_weight is None or out_weight is None:
+        raise RuntimeError("Low-rank bilinear pairwise kernel is missing projection weights.")
+    if in_bias is not None or out_bias is not None:
+        raise TypeError("low_rank_bilinear projections carry no bias.")
+    return weight, bias, in_weight, out_weight
+
+
+def propagation_topk_selection(
+    pairwise_kind: str,
+    weight: Tensor,
+    bias: Tensor | None,
+    in_weight: Tensor | None,
+    in_bias: Tensor | None,
+    out_weight: Tensor | None,
+    out_bias: Tensor | None,
+    edge_compress_name: str,
+    layer_val: Tensor,
+    projected_state: Tensor,
+    projected_val: Tensor,
+    topk: int,
+    target_block_size: int,
+    source_block_size: int,
+) -> tuple[Tensor, Tensor]:
+    """Top-k propagation returning (delta_state, delta_val, topk_index, topk_score).
+
+    Same arguments as ``propagation_topk``; the selection (int32 source
+    indices and their scores, best first) is what the forward aggregated."""
+    w_hat, bias, V, U = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias)
+    if edge_compress_name not in _COMPRESS_KINDS:
+        raise RuntimeError(f"Unsupported edge_compress_name for the HIP backend: {edge_compress_name!r}.")
+    if topk <= 0:
+        raise RuntimeError("topk must be positive.")
+    if target_block_size <= 0 or source_block_size <= 0:
+        raise RuntimeError("block sizes must be positive.")
+    _require_gpu(layer_val, projected_state, projected_val, w_hat, V, U, bias)
+    batch_shape = tuple(layer_val.shape[:-2])
+    N, Din = layer_val.shape[-2], layer_val.shape[-1]
+    Dout = projected_val.shape[-1]
+    k = min(int(topk), N)
+    if k == N:
+        raise NotImplementedError("top-k with k == N is dense propagation; dense native op not available.")
+    if k > MAX_TOPK:
+        raise NotImplementedError(f"HIP top-k propagation supports k <= {MAX_TOPK} (got {k}).")
+    pv_is_x = _same_storage_view(projected_val, layer_val)
+    X = _f32(layer_val.reshape(-1, N, Din))
+    ps = _f32(projected_state.reshape(-1, N))
+    pv = None if pv_is_x else _f32(projected_val.reshape(-1, N, Dout))
+    ds, dv, idx, score = _PropagationTopK.apply(
+        X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias), k, _COMPRESS_KINDS[edge_compress_name]
+    )
+    return (
+        ds.reshape(*batch_shape, N).to(projected_state.dtype),
+        dv.reshape(*batch_shape, N, Dout).to(projected_val.dtype),
+        idx.reshape(*batch_shape, N, k),
+        score.reshape(*batch_shape, N, k),
+    )
+
+
+def propagation_topk(
+    pairwise_kind: str,
+    weight: Tensor,
+    bias: Tensor | None,
+    in_weight: Tensor | None,
+    in_bias: Tensor | None,
+    out_weight: Tensor | None,
+    out_bias: Tensor | None,
+    edge_compress_name: str,
+    layer_val: Tensor,
+    projected_state: Tensor,
+    projected_val: Tensor,
+    topk: int,
+    target_block_size: int,
+    source_block_size: int,
+) -> tuple[Tensor, Tensor]:
+    """Top-k propagation; signature of jakal_net_native.cpp:6305-6319.
+
+    ``weight`` is the normalised core weight, ``in_weight`` the source and
+    ``out_weight`` the target projection (kernel_common.py:185-192)."""
+    ds, dv, _, _ = propagation_topk_selection(
+        pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias, edge_compress_name, layer_val,
+        projected_state, projected_val, topk, target_block_size, source_block_size,
+    )
+    return ds, dv
+
+
+# ---------------------------------------------------------------------------
+# raw score + select (no autograd; used by tests and the benchmark)
+# ---------------------------------------------------------------------------
+def low_rank_topk_select(
+    query: Tensor,
+    key: Tensor,
+    scale: Tensor | None,
+    bias: Tensor | None,
+    scale_on_query: bool,
+    temperature: float,
+    topk: int,
+) -> tuple[Tensor, Tensor]:
+    """Per-row top-k of ((query*cq) . (key*ck) + bias) / temperature.
+
+    query [B,Nq,r], key [B,Nk,r] fp32; returns (index int32 [B,Nq,k], score fp32 [B,Nq,k])."""
+    dev = _require_gpu(query, key, scale, bias)
+    q = _f32(query)
+    kk = _f32(key)
+    B, Nq, r = q.shape
+    Nk = kk.shape[1]
+    idx = torch.empty(B, Nq, topk, device=dev, dtype=torch.int32)
+    score = torch.empty(B, Nq, topk, device=dev, dtype=torch.float32)
+    sc = _f32(scale)
+    bi = _f32(bias)
+    with torch.cuda.device(dev):
+        _check(
+            _LIB.jn_lowrank_topk_select(
+                _ptr(q), r, Nq * r, _ptr(kk), r, Nk * r, _ptr(sc), 1 if scale_on_query else 0, _ptr(bi),
+                float(temperature), B, Nq, Nk, r, topk, _ptr(idx), _ptr(score), _stream(dev),
+            )
+        )
+    return idx, score

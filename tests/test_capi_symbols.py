@@ -1,0 +1,53 @@
+"""The HIP library loads and exports every entry point declared in include/*.h.
+
+No compute call is made (this runs without a GPU)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+LIB = ROOT / "jakal-net_amd" / "lib" / "libjakal_net_hip.so"
+
+
+def _declared_symbols():
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = header.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(jn_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = _declared_symbols()
+    assert "jn_propagation_topk_forward" in names
+    assert "jn_last_error" in names
+
+
+def test_library_exports_every_declared_symbol():
+    assert LIB.exists(), f"{LIB} is not built (run __graft_entry__.build())"
+    lib = ctypes.CDLL(str(LIB))
+    missing = [n for n in _declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"undeclared exports missing from the library: {missing}"
+
+
+def test_error_channel_and_abi_version_without_gpu():
+    lib = ctypes.CDLL(str(LIB))
+    lib.jn_abi_version.restype = ctypes.c_int
+    assert lib.jn_abi_version() >= 1
+    lib.jn_last_error.restype = ctypes.c_char_p
+    # argument validation runs on the host before any device call
+    P, I64, I32, F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
+    fn = lib.jn_lowrank_topk_select
+    fn.argtypes = [P, I64, I64, P, I64, I64, P, I32, P, F, I64, I64, I64, I64, I64, P, P, P]
+    fn.restype = ctypes.c_int
+    rc = fn(None, 4, 0, None, 4, 0, None, 0, None, 1.0, 1, 8, 8, 4, 2, None, None, None)
+    assert rc != 0
+    assert b"null" in lib.jn_last_error()
+    ws = lib.jn_propagation_topk_workspace_bytes
+    ws.argtypes = [I64] * 6
+    ws.restype = ctypes.c_size_t
+    # dP [M, 2r] alone is 33.5 MB at B=16, N=4096, r=64
+    assert ws(16, 4096, 512, 512, 64, 32) > 16 * 4096 * 128 * 4

@@ -1,0 +1,220 @@
+"""Benchmark of the native hot path on one MI355X.
+
+Workload (top-k variant): SparsePropagation top-k with
+LowRankBilinearPairwise, B=16, N=4096, D=512, r=64, k=32, fp32, val rows
+unit-norm, state ~ N(0,1), default module init; one step = forward + backward
+of loss = sum(delta_state) + sum(delta_val) through the jakal_net API with
+implementation="native".  Inputs and parameters are resident in HBM before
+the timed region.
+
+Prints one JSON line:
+  value       routed pairs per second (E = B*N*k pairs per step / step time)
+  roofline    dominant kernel: algorithmic bytes (or flops) per launch / its
+              average duration, measured with HIP events inside the timed region
+  kernels     the same figures for every kernel of the step
+  cpu_baseline the numpy oracle (fp32) timed on a bounded sample on the host
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "jakal-net_amd"))
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+CONFIG = {"batch": 16, "nodes": 4096, "dim": 512, "rank": 64, "topk": 32}
+
+
+def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int) -> tuple[str, float] | None:
+    """(bound, algorithmic bytes or flops per launch) for the kernels of one step.
+
+    Bytes count every operand once per use (no cache reuse credited): an edge
+    (routed pair) gathers one D-row of fp32 values, its index and score."""
+    M, E = B * N, B * N * k
+    if name.startswith("lowrank_topk_select_kernel"):
+        return "mfma", 2.0 * B * N * N * r
+    if name.startswith("rows_forward_kernel"):
+        # idx+score+ps per edge, pv row per edge; delta_val row + delta_state per row
+        return "hbm", E * (12.0 + 4.0 * D) + M * (4.0 * D + 4.0)
+    if name.startswith("rows_backward_kernel"):
+        # idx+score, ps, pv row, key row per edge; gsc+coef writes per edge;
+        # grad-delta row + state, dq row, row sum per row
+        return "hbm", E * (8.0 + 4.0 + 4.0 * D + 4.0 * r + 8.0) + M * (4.0 * D + 4.0 + 4.0 * r + 4.0)
+    if name.startswith("cols_backward_kernel"):
+        # edge id, coef+gsc, grad-delta row + state, query row per edge;
+        # segment bounds, grad_pv row, grad_ps, dk row, key row per column
+        return "hbm", E * (4.0 + 8.0 + 4.0 * D + 4.0 + 4.0 * r) + M * (8.0 + 4.0 * D + 4.0 + 8.0 * r)
+    if name.startswith("gemm_f32_kernel"):
+        return "mfma", 2.0 * M * D * 2 * r
+    return None
+
+
+def cpu_baseline(B_sample: int = 1) -> dict:
+    """Oracle (numpy, fp32) forward+backward on B_sample batch elements of the workload."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import jakal_oracle as O
+
+    N, D, r, k = CONFIG["nodes"], CONFIG["dim"], CONFIG["rank"], CONFIG["topk"]
+    rng = np.random.default_rng(1004)
+    val = rng.standard_normal((B_sample, N, D)).astype(np.float32)
+    val /= np.linalg.norm(val, axis=-1, keepdims=True)
+    state = rng.standard_normal((B_sample, N)).astype(np.float32)
+    bound = 1.0 / math.sqrt(D)
+    U = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
+    V = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
+    w = np.ones(r, dtype=np.float32)
+    g_ds = np.ones((B_sample, N), np.float32)
+    g_dv = np.ones((B_sample, N, D), np.float32)
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads") or 0) for i in threadpool_info()) or None
+    except Exception:  # noqa: BLE001
+        pass
+    times = []
+    with O.compute_dtype(np.float32):
+        for rep in range(3):
+            t0 = time.perf_counter()
+            O.propagation_forward(val, state, val, U, V, w, 0.0, mode="topk", topk=k)
+            O.propagation_backward(val, state, val, U, V, w, 0.0, g_ds, g_dv, mode="topk", topk=k)
+            times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    return {
+        "value": B_sample * N * k / t,
+        "unit": "routed pairs/s",
+        "cores": threads or os.cpu_count(),
+        "kind": "port",
+        "sample": f"numpy oracle fp32, forward+backward, {B_sample} of {CONFIG['batch']} batch elements "
+                  f"(N={N}, D={D}, r={r}, k={k}), median of 3 ({t:.2f} s each)",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import jakal_net_native as jn
+    from jakal_net import Layer, LowRankBilinearPairwise, SparsePropagation
+
+    dev = torch.device("cuda:0")
+    B, N, D, r, k = CONFIG["batch"], CONFIG["nodes"], CONFIG["dim"], CONFIG["rank"], CONFIG["topk"]
+    g = torch.Generator().manual_seed(1004)
+    state = torch.randn(B, N, generator=g)
+    val = torch.randn(B, N, D, generator=g)
+    val = val / val.norm(dim=-1, keepdim=True)
+    torch.manual_seed(1004)
+    op = SparsePropagation(LowRankBilinearPairwise(D, r), sparse_type="topk", topk=k, implementation="native").to(dev)
+    layer = Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True), val=val.to(dev).requires_grad_(True))
+    ones_s = torch.ones(B, N, device=dev)
+    ones_v = torch.ones(B, N, D, device=dev)
+
+    def step() -> None:
+        op.zero_grad(set_to_none=True)
+        layer.val.grad = None
+        layer.state.grad = None
+        delta = op(layer)
+        torch.autograd.backward([delta.delta_state, delta.delta_val], [ones_s, ones_v])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    jn.profile_enable(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    prof = jn.profile_collect()
+    jn.profile_enable(False)
+
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    E = B * N * k
+    value = E / (ms_per_step / 1e3)
+
+    kernels = {}
+    for name, (count, total_ms) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        avg_ms = total_ms / count
+        entry = {"launches_per_step": count / args.steps, "avg_ms": round(avg_ms, 5),
+                 "ms_per_step": round(total_ms / args.steps, 5)}
+        model = kernel_model(name, B, N, D, r, k)
+        if model is not None:
+            bound, work = model
+            if bound == "hbm":
+                achieved = work / (avg_ms / 1e3) / 1e9
+                entry.update(bound="hbm", algorithmic_bytes=work, achieved_GBps=round(achieved, 1),
+                             frac=round(achieved / HBM_PEAK_GBS, 4))
+            else:
+                achieved = work / (avg_ms / 1e3) / 1e12
+                entry.update(bound="mfma", flops=work, achieved_TFLOPs=round(achieved, 2),
+                             frac=round(achieved / FP32_MFMA_PEAK_TFLOPS, 4))
+        kernels[name] = entry
+
+    modeled = [(n, e) for n, e in kernels.items() if "bound" in e]
+    dom_name, dom = max(modeled, key=lambda ne: ne[1]["ms_per_step"])
+    if dom["bound"] == "hbm":
+        roofline = {"kernel": dom_name, "bound": "hbm", "achieved": dom["achieved_GBps"], "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": dom["frac"], "traffic": None}
+    else:
+        roofline = {"kernel": dom_name, "bound": "mfma", "achieved": dom["achieved_TFLOPs"],
+                    "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"], "traffic": None}
+
+    sparse_bytes = 3 * 4 * D * (E + B * N) + 24 * E + 3 * 4 * (E + B * N)
+    result = {
+        "metric": "routed pairs/sec + HBM GB/s (% peak), SparsePropagation N=4096 D=512 k=32 fwd+bwd",
+        "value": value,
+        "unit": "routed pairs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) state, unit-norm N(0,1) val rows, default module init)",
+        "config": {"workload": "C4-topk SparsePropagation fwd+bwd, LowRankBilinearPairwise, native", **CONFIG},
+        "sparse_phase_GBps": round(sparse_bytes / (ms_per_step / 1e3) / 1e9, 1),
+        "roofline": roofline,
+        "kernels": kernels,
+        "wall_s_timed": round(wall, 3),
+        "device": torch.cuda.get_device_name(0),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -34,6 +34,16 @@ const char* jn_last_error(void);
 int jn_abi_version(void);
 
 /*
+ * Per-kernel timing (no counterpart in the reference; for benchmarks).
+ * jn_profile_enable(1) makes every later launch record a HIP event pair on
+ * its stream; jn_profile_collect() waits for the recorded events and writes
+ * one "kernel_name launches total_ms" line per kernel into `buffer`, then
+ * clears the records.  jn_profile_enable(0) stops recording.
+ */
+int jn_profile_enable(int32_t on);
+int jn_profile_collect(char* buffer, size_t size);
+
+/*
  * Low-rank score + per-row top-k select, no score matrix materialised.
  *   s[b,i,j] = ((sum_r query[b,i,r]*cq[r] * key[b,j,r]*ck[r]) + bias) / temperature
  * where the scale vector multiplies the query rows when scale_on_query != 0,

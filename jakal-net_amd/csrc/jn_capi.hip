@@ -3,6 +3,9 @@
 // workspace and enqueues kernels on the caller's stream.
 #include <algorithm>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <vector>
 
 #include "../../include/jakal_net_hip.h"
 #include "jn_internal.hpp"
@@ -23,6 +26,44 @@ void set_error(const char* fmt, ...) {
 }
 
 const char* last_error() { return g_last_error.c_str(); }
+
+namespace {
+struct ProfRecord {
+  const char* name;
+  hipEvent_t start, stop;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfRecord> g_prof_records;
+std::vector<hipEvent_t> g_prof_free;
+
+hipEvent_t prof_event() {
+  if (!g_prof_free.empty()) {
+    hipEvent_t e = g_prof_free.back();
+    g_prof_free.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+}  // namespace
+
+ProfileScope::ProfileScope(const char* name, hipStream_t s) : slot(-1), stream(s) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  if (!g_prof_on) return;
+  ProfRecord r{name, prof_event(), prof_event()};
+  if (!r.start || !r.stop) return;
+  if (hipEventRecord(r.start, s) != hipSuccess) return;
+  g_prof_records.push_back(r);
+  slot = (long)g_prof_records.size() - 1;
+}
+
+ProfileScope::~ProfileScope() {
+  if (slot < 0) return;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  if (slot < (long)g_prof_records.size()) (void)hipEventRecord(g_prof_records[slot].stop, stream);
+}
 
 namespace {
 
@@ -88,6 +129,43 @@ extern "C" {
 const char* jn_last_error(void) { return jakal::last_error(); }
 
 int jn_abi_version(void) { return 1; }
+
+int jn_profile_enable(int32_t on) {
+  std::lock_guard<std::mutex> lock(jakal::g_prof_mu);
+  for (auto& r : jakal::g_prof_records) {
+    jakal::g_prof_free.push_back(r.start);
+    jakal::g_prof_free.push_back(r.stop);
+  }
+  jakal::g_prof_records.clear();
+  jakal::g_prof_on = on != 0;
+  return kOk;
+}
+
+int jn_profile_collect(char* buffer, size_t size) {
+  std::lock_guard<std::mutex> lock(jakal::g_prof_mu);
+  std::map<std::string, std::pair<long, double>> agg;
+  for (auto& r : jakal::g_prof_records) {
+    float ms = 0.f;
+    JN_HIP_TRY(hipEventSynchronize(r.stop));
+    JN_HIP_TRY(hipEventElapsedTime(&ms, r.start, r.stop));
+    auto& a = agg[r.name];
+    a.first += 1;
+    a.second += ms;
+    jakal::g_prof_free.push_back(r.start);
+    jakal::g_prof_free.push_back(r.stop);
+  }
+  jakal::g_prof_records.clear();
+  std::string out;
+  char line[256];
+  for (auto& kv : agg) {
+    snprintf(line, sizeof(line), "%s %ld %.6f\n", kv.first.c_str(), kv.second.first, kv.second.second);
+    out += line;
+  }
+  JN_REQUIRE(buffer != nullptr && size > out.size(), kInvalidArgument, "profile buffer too small (%zu bytes needed)",
+             out.size() + 1);
+  memcpy(buffer, out.c_str(), out.size() + 1);
+  return kOk;
+}
 
 int jn_lowrank_topk_select(const float* query, int64_t ldq, int64_t query_batch_stride, const float* key,
                            int64_t ldk, int64_t key_batch_stride, const float* scale, int32_t scale_on_query,

@@ -59,6 +59,19 @@ const char* last_error();
     }                                                                           \
   } while (0)
 
+// Optional per-kernel timing with HIP events, off unless jn_profile_enable(1)
+// was called.  A scope records an event on `stream` before and after the
+// launch it encloses; jn_profile_collect() reads the elapsed times back.
+struct ProfileScope {
+  ProfileScope(const char* name, hipStream_t stream);
+  ~ProfileScope();
+  ProfileScope(const ProfileScope&) = delete;
+  ProfileScope& operator=(const ProfileScope&) = delete;
+  long slot;
+  hipStream_t stream;
+};
+#define JN_PROFILE(name, stream) ::jakal::ProfileScope jn_prof_scope__((name), (stream))
+
 // Bump allocator over a caller-provided workspace.  Offsets are 256-byte
 // aligned so every carved buffer is suitable for 16-byte vector access.
 struct Workspace {

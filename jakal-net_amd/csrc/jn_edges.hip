@@ -133,6 +133,7 @@ int launch_rows_forward(const RowsFwdArgs& a, hipStream_t stream) {
   JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
   const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.out_val) & 15) == 0);
+  JN_PROFILE("rows_forward_kernel", stream);
   if (vec) hipLaunchKernelGGL(rows_forward_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
   else hipLaunchKernelGGL(rows_forward_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
   JN_LAUNCH_CHECK();
@@ -202,10 +203,18 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
     for (int d = lane * W; d < a.D; d += kWave * W) {
       const float4 gv = load_w<W>(grow + d);
 #pragma unroll
-      for (int q = 0; q < KP; ++q) {
-        if (q < ne) {
-          const int jj = readlane_i(j, q);
-          if (jj >= 0) p[q] += dot4(gv, load_w<W>(pvb + (int64_t)jj * a.ld_pv + d));
+      for (int q0 = 0; q0 < KP; q0 += 8) {
+        if (q0 < ne) {  // uniform; absent edges (j < 0) read row 0 and are masked
+          float4 v[8];
+          float msk[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int jj = readlane_i(j, q0 + u);
+            msk[u] = jj >= 0 ? 1.f : 0.f;
+            v[u] = load_w<W>(pvb + (int64_t)(jj < 0 ? 0 : jj) * a.ld_pv + d);
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) p[q0 + u] += msk[u] * dot4(gv, v[u]);
         }
       }
     }
@@ -252,6 +261,7 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
   const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0);
   dim3 grid((unsigned)blocks), block(256);
+  JN_PROFILE("rows_backward_kernel", stream);
   if (a.k <= 16) {
     if (vec) hipLaunchKernelGGL((rows_backward_kernel<4, 16>), grid, block, 0, stream, a);
     else hipLaunchKernelGGL((rows_backward_kernel<1, 16>), grid, block, 0, stream, a);
@@ -388,15 +398,27 @@ int launch_csr(const CsrArgs& a, hipStream_t stream) {
   const int T = (a.Nq + kCsrTile - 1) / kCsrTile;
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
   dim3 g2(T, a.B);
-  hipLaunchKernelGGL(csr_count_kernel, g2, dim3(256), 0, stream, a);
-  JN_LAUNCH_CHECK();
+  {
+    JN_PROFILE("csr_count_kernel", stream);
+    hipLaunchKernelGGL(csr_count_kernel, g2, dim3(256), 0, stream, a);
+    JN_LAUNCH_CHECK();
+  }
   const int64_t n = (int64_t)a.B * a.Nk;
-  hipLaunchKernelGGL(csr_tile_scan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, T);
-  JN_LAUNCH_CHECK();
-  hipLaunchKernelGGL(csr_segment_scan_kernel, dim3(a.B), dim3(1024), 0, stream, a);
-  JN_LAUNCH_CHECK();
-  hipLaunchKernelGGL(csr_fill_kernel, g2, dim3(256), 0, stream, a);
-  JN_LAUNCH_CHECK();
+  {
+    JN_PROFILE("csr_tile_scan_kernel", stream);
+    hipLaunchKernelGGL(csr_tile_scan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, T);
+    JN_LAUNCH_CHECK();
+  }
+  {
+    JN_PROFILE("csr_segment_scan_kernel", stream);
+    hipLaunchKernelGGL(csr_segment_scan_kernel, dim3(a.B), dim3(1024), 0, stream, a);
+    JN_LAUNCH_CHECK();
+  }
+  {
+    JN_PROFILE("csr_fill_kernel", stream);
+    hipLaunchKernelGGL(csr_fill_kernel, g2, dim3(256), 0, stream, a);
+    JN_LAUNCH_CHECK();
+  }
   return kOk;
 }
 
@@ -444,30 +466,54 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
         }
         const int row_of = eid / a.k;
         if (first_pass && lane < n && a.gds) st += cf * a.gds[row_of];
-        for (int q = 0; q < n; ++q) {
-          const int64_t row = readlane_i(row_of, q);
-          const float c = readlane_f(cf, q);
+        const int row0 = readlane_i(row_of, 0);
+        for (int q0 = 0; q0 < n; q0 += 4) {
+          int64_t rw[4];
+          float cu[4], gg[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const bool ok = q0 + u < n;  // uniform
+            rw[u] = ok ? readlane_i(row_of, q0 + u) : row0;
+            cu[u] = ok ? readlane_f(cf, q0 + u) : 0.f;
+            gg[u] = ok ? readlane_f(gsv, q0 + u) : 0.f;
+          }
           if (a.grad_pv) {
-            const float* gr = a.gdv + row * a.D;
-            if (VEC) {
+            float4 v0[4], v1[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const float* gr = a.gdv + rw[u] * a.D;
+              if (dl0 < a.D) v0[u] = load_w<W>(gr + dl0);
+              if (dl1 < a.D) v1[u] = load_w<W>(gr + dl1);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
               if (dl0 < a.D) {
-                float4 v = *reinterpret_cast<const float4*>(gr + dl0);
-                acc[0][0] += c * v.x; acc[0][1] += c * v.y; acc[0][2] += c * v.z; acc[0][3] += c * v.w;
+                acc[0][0] += cu[u] * v0[u].x;
+                acc[0][1] += cu[u] * v0[u].y;
+                acc[0][2] += cu[u] * v0[u].z;
+                acc[0][3] += cu[u] * v0[u].w;
               }
               if (dl1 < a.D) {
-                float4 v = *reinterpret_cast<const float4*>(gr + dl1);
-                acc[1][0] += c * v.x; acc[1][1] += c * v.y; acc[1][2] += c * v.z; acc[1][3] += c * v.w;
+                acc[1][0] += cu[u] * v1[u].x;
+                acc[1][1] += cu[u] * v1[u].y;
+                acc[1][2] += cu[u] * v1[u].z;
+                acc[1][3] += cu[u] * v1[u].w;
               }
-            } else {
-              if (dl0 < a.D) acc[0][0] += c * gr[dl0];
-              if (dl1 < a.D) acc[1][0] += c * gr[dl1];
             }
           }
           if (first_pass) {
-            const float gg = readlane_f(gsv, q);
-            const float* qr = a.q + row * a.ldq;
-            if (lane < a.r) dk0 += gg * qr[lane];
-            if (lane + kWave < a.r) dk1 += gg * qr[lane + kWave];
+            float qa[4], qb2[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const float* qr = a.q + rw[u] * a.ldq;
+              qa[u] = lane < a.r ? qr[lane] : 0.f;
+              qb2[u] = lane + kWave < a.r ? qr[lane + kWave] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              dk0 += gg[u] * qa[u];
+              dk1 += gg[u] * qb2[u];
+            }
           }
         }
       }
@@ -522,6 +568,7 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   const int blocks = (waves + 3) / 4;
   const bool vec = (a.D % 4 == 0) && (a.ld_gpv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
                    (a.grad_pv == nullptr || (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0);
+  JN_PROFILE("cols_backward_kernel", stream);
   if (vec) hipLaunchKernelGGL(cols_backward_kernel<true>, dim3(blocks), dim3(256), 0, stream, a);
   else hipLaunchKernelGGL(cols_backward_kernel<false>, dim3(blocks), dim3(256), 0, stream, a);
   JN_LAUNCH_CHECK();
@@ -536,28 +583,34 @@ __global__ __launch_bounds__(256) void finalize_small_grads_kernel(const float* 
                                                                    float* grad_c, int accumulate_c,
                                                                    const float* rowsum, int64_t nrows,
                                                                    float* grad_bias) {
+  // block b < r sums column b of the [nparts, r] partials; block r sums the row sums
   __shared__ float red[256];
-  for (int rr = threadIdx.x; rr < r; rr += blockDim.x) {
-    float s = 0.f;
-    for (int w = 0; w < nparts; ++w) s += part_c[(int64_t)w * r + rr];
-    if (grad_c) grad_c[rr] = accumulate_c ? grad_c[rr] + s : s;
-  }
-  if (grad_bias) {
-    float s = 0.f;
+  const int b = blockIdx.x;
+  float s = 0.f;
+  if (b < r) {
+    for (int w = threadIdx.x; w < nparts; w += blockDim.x) s += part_c[(int64_t)w * r + b];
+  } else {
     for (int64_t i = threadIdx.x; i < nrows; i += blockDim.x) s += rowsum[i];
-    red[threadIdx.x] = s;
+  }
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-      if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-      __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (b < r) {
+      if (grad_c) grad_c[b] = accumulate_c ? grad_c[b] + red[0] : red[0];
+    } else if (grad_bias) {
+      grad_bias[0] = red[0];
     }
-    if (threadIdx.x == 0) grad_bias[0] = red[0];
   }
 }
 
 int launch_finalize_small_grads(const float* part_c, int nparts, int r, float* grad_c, int accumulate_c,
                                 const float* rowsum, int64_t nrows, float* grad_bias, hipStream_t stream) {
-  hipLaunchKernelGGL(finalize_small_grads_kernel, dim3(1), dim3(256), 0, stream, part_c, nparts, r, grad_c,
+  JN_PROFILE("finalize_small_grads_kernel", stream);
+  hipLaunchKernelGGL(finalize_small_grads_kernel, dim3(r + 1), dim3(256), 0, stream, part_c, nparts, r, grad_c,
                      accumulate_c, rowsum, nrows, grad_bias);
   JN_LAUNCH_CHECK();
   return kOk;

@@ -194,9 +194,10 @@ __global__ void splitk_reduce_kernel(const float* part, int splits, int M, int N
   }
 }
 
-int launch_gemm(const GemmArgs& g, bool a_kcontig, bool b_kcontig, int splits, hipStream_t stream) {
+int launch_gemm(const GemmArgs& g, bool a_kcontig, bool b_kcontig, int splits, hipStream_t stream, const char* name) {
   JN_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, kInvalidArgument, "negative GEMM extent");
   if (g.M == 0 || g.N == 0) return kOk;
+  JN_PROFILE(name, stream);
   dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, splits), block(256);
   if (a_kcontig && b_kcontig) hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, block, 0, stream, g);
   else if (a_kcontig && !b_kcontig) hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, block, 0, stream, g);
@@ -215,7 +216,7 @@ int gemm_project(const float* X, int64_t ldx, const float* W0, const float* W1, 
   g.C = C; g.ldc = ldc;
   g.M = M; g.N = N; g.K = K;
   g.k_chunk = K; g.c_split_stride = 0;
-  return launch_gemm(g, true, true, 1, stream);
+  return launch_gemm(g, true, true, 1, stream, "gemm_f32_kernel<project>");
 }
 
 // dX[M][N] = dP[M][K] . [W0;W1] (+ addend), W0 rows [0, split) of K.
@@ -229,7 +230,7 @@ int gemm_grad_input(const float* dP, int64_t ldp, const float* W0, const float* 
   g.addend = addend; g.ld_add = ld_add;
   g.M = M; g.N = N; g.K = K;
   g.k_chunk = K; g.c_split_stride = 0;
-  return launch_gemm(g, true, false, 1, stream);
+  return launch_gemm(g, true, false, 1, stream, "gemm_f32_kernel<grad_input>");
 }
 
 size_t gemm_grad_weight_workspace(int M, int N, int K) {
@@ -250,11 +251,12 @@ int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, 
   g.C = partial; g.ldc = N;
   g.M = M; g.N = N; g.K = K;
   g.k_chunk = k_chunk; g.c_split_stride = (int64_t)M * N;
-  int rc = launch_gemm(g, false, false, splits, stream);
+  int rc = launch_gemm(g, false, false, splits, stream, "gemm_f32_kernel<grad_weight>");
   if (rc != kOk) return rc;
   int64_t total = (int64_t)M * N;
   int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
   if (blocks < 1) blocks = 1;
+  JN_PROFILE("splitk_reduce_kernel", stream);
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, splits, M, N,
                      (int64_t)M * N, out0, out1, m_split);
   JN_LAUNCH_CHECK();

@@ -45,6 +45,8 @@ def _declare(name: str, argtypes: list, restype=ctypes.c_int) -> None:
 
 _declare("jn_last_error", [], ctypes.c_char_p)
 _declare("jn_abi_version", [])
+_declare("jn_profile_enable", [_I32])
+_declare("jn_profile_collect", [ctypes.c_char_p, _SZ])
 _declare(
     "jn_lowrank_topk_select",
     [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _F, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
@@ -86,6 +88,22 @@ def backend_name() -> str:
 
 def loaded_library() -> str:
     return str(library_path())
+
+
+def profile_enable(on: bool = True) -> None:
+    """Start (or stop) per-kernel HIP-event timing inside the library."""
+    _check(_LIB.jn_profile_enable(1 if on else 0))
+
+
+def profile_collect() -> dict[str, tuple[int, float]]:
+    """Wait for the recorded kernels; return {kernel: (launches, total_ms)} and clear."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    _check(_LIB.jn_profile_collect(buf, len(buf)))
+    out: dict[str, tuple[int, float]] = {}
+    for line in buf.value.decode().splitlines():
+        name, count, total = line.rsplit(" ", 2)
+        out[name] = (int(count), float(total))
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -21,9 +21,25 @@ at the k-th place are excluded from index parity by the 1e-5 gap rule.
 
 from __future__ import annotations
 
+import contextlib
+
 import numpy as np
 
+# Arithmetic type of the oracle.  float64 for parity checks; the benchmark's
+# CPU baseline switches to float32 (the reference backend's own precision).
 F64 = np.float64
+
+
+@contextlib.contextmanager
+def compute_dtype(dtype):
+    """Temporarily run the oracle in ``dtype`` (e.g. np.float32)."""
+    global F64
+    saved = F64
+    F64 = dtype
+    try:
+        yield
+    finally:
+        F64 = saved
 
 
 # ---------------------------------------------------------------------------
@@ -196,7 +212,8 @@ def propagation_backward(val, ps, pv, U, V, w, b, g_ds, g_dv, *, mode="topk", to
     g_U = flat(g_pt).T @ flat(val)
     g_V = flat(g_psrc).T @ flat(val)
     g_w = normalized_weight_backward(w, g_what)
-    return {"val": g_val, "ps": g_ps, "pv": g_pv, "U": g_U, "V": g_V, "w": g_w, "w_hat": g_what, "b": g_b}
+    return {"val": g_val, "ps": g_ps, "pv": g_pv, "U": g_U, "V": g_V, "w": g_w, "w_hat": g_what, "b": g_b,
+            "g_scores": g_s}
 
 
 def normalized_weight_backward(w, g_what):

@@ -34,6 +34,8 @@ def _np(t):
 def _close(got, want, rtol=RTOL, atol=ATOL, what=""):
     got = np.asarray(got, dtype=np.float64)
     want = np.asarray(want, dtype=np.float64)
+    if want.size == 0:
+        return
     err = np.abs(got - want) - (atol + rtol * np.abs(want))
     assert err.max() <= 0, f"{what}: max excess {err.max():.3e} (max abs diff {np.abs(got - want).max():.3e})"
 
@@ -148,10 +150,15 @@ def test_propagation_topk_forward_backward_matches_oracle(dev, compress, separat
     _close(_np(ps.grad), gr["ps"], what="grad projected_state")
     if separate_pv:
         _close(_np(pv.grad), gr["pv"], what="grad projected_val")
-    _close(_np(Ud.grad), gr["U"], what="grad target_proj")
-    _close(_np(Vd.grad), gr["V"], what="grad source_proj")
-    _close(_np(wd.grad), gr["w_hat"], what="grad w_hat")
-    _close(_np(bd.grad), gr["b"], what="grad bias")
+    # Parameter gradients are sums over all B*N*k edges.  fp32 error of such a
+    # sum grows with the size of its terms, not of the result (which can
+    # cancel to ~0), so atol scales with max|want| and with the root-mean L1
+    # size of the per-edge score gradients sum|g_s| / sqrt(#edges).
+    gs = gr["g_scores"][mask]
+    scale = max(1.0, float(np.abs(gs).sum() / math.sqrt(gs.size)))
+    for got, want, what in ((Ud.grad, gr["U"], "grad target_proj"), (Vd.grad, gr["V"], "grad source_proj"),
+                            (wd.grad, gr["w_hat"], "grad w_hat"), (bd.grad, gr["b"], "grad bias")):
+        _close(_np(got), want, atol=ATOL * max(scale, float(np.abs(want).max())), what=what)
 
 
 def test_sparse_propagation_api_native_matches_reference(dev):

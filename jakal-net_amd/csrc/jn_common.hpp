@@ -111,6 +111,39 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 }
 __device__ __forceinline__ int readlane_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
+// Exchange with lane ^ 16 / lane ^ 32 through the gfx950 permlane swaps
+// (VALU ops, no LDS round trip).
+__device__ __forceinline__ int xor16_i(int v) {
+  const auto p = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  return (int)((lane_id() & 16) ? p[0] : p[1]);
+}
+__device__ __forceinline__ int xor32_i(int v) {
+  const auto p = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return (int)((lane_id() & 32) ? p[0] : p[1]);
+}
+
+// Wave-wide reductions over DPP quad/mirror patterns plus the two permlane
+// swaps; every lane receives the result.
+template <typename Op>
+__device__ __forceinline__ int wave_reduce_i(int v, Op op) {
+  v = op(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+  v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+  v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xf, 0xf, false));  // row_mirror
+  v = op(v, xor16_i(v));
+  v = op(v, xor32_i(v));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return (uint32_t)wave_reduce_i((int)v, [](int a, int b) { return (int)max((uint32_t)a, (uint32_t)b); });
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  return (uint32_t)wave_reduce_i((int)v, [](int a, int b) { return (int)min((uint32_t)a, (uint32_t)b); });
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+  return wave_reduce_i(v, [](int a, int b) { return min(a, b); });
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_f(v, m);

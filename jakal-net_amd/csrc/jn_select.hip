@@ -15,23 +15,28 @@
 //     by the raw weight, key = destination projection, bias then /temperature,
 //     top-k per source over destinations (transition.py:439-444).
 //
-// Layout of one workgroup (256 threads = 4 waves):
-//   * 64 query rows per workgroup, 16 per wave.  A wave keeps the query
-//     fragment of its 16 rows in VGPRs for the whole kernel (B operand of
-//     v_mfma_f32_16x16x4f32; lane l owns query row l%16, rank slice l/16).
+// Layout of one workgroup (256 threads = 4 waves, 64 query rows):
+//   * 16 query rows per wave.  A wave keeps the query fragment of its rows in
+//     VGPRs for the whole kernel (B operand of v_mfma_f32_16x16x4f32; lane l
+//     owns row l%16, rank slice l/16).
 //   * Keys stream through LDS in chunks of 32 rows (two 16-row MFMA tiles,
 //     A operand), double buffered with a one-chunk register prefetch and one
 //     workgroup barrier per chunk.
 //   * After a chunk, lane l holds 8 scores of row l%16.  Scores above the
 //     row's current k-th best (theta) are appended to the row's slot array in
-//     LDS; the 4 lanes of a row find their write offsets with a 4-lane prefix
-//     sum (no LDS atomics).  Counts and thresholds live in registers.
-//   * A row with >= 32 waiting candidates (or any at the end) is merged: the
-//     wave loads the row's k kept entries plus candidates (up to 96 slots, two
-//     per lane), finds the k-th largest order key by a 32-step ballot radix
-//     select, and compacts the k winners back to the front of the slot array.
-//     Ties at the k-th value keep the lower key indices.  The kept set stays
-//     unsorted until one bitonic sort per row at the end.
+//     LDS; the 4 lanes of a row (l, l^16, l^32, l^48) exchange their counts
+//     with the gfx950 permlane swaps to get write offsets (no LDS atomics).
+//     Counts and thresholds live in registers.
+//   * Once any row of a wave has >= 64 waiting candidates (or any at the end),
+//     all 16 rows of the wave merge together: lane (g, row) loads 32 slots of
+//     its row into registers and a radix select over order keys finds each
+//     row's k-th largest key, counting per lane and summing over the row's 4
+//     lanes with permlane swaps; it starts below the bits shared by all of the
+//     row's keys and stops once exactly k keys remain.  The k winners are
+//     compacted to the front of the slot array.  A row whose k-th value is
+//     tied (more equal keys than places) is merged again by the exact per-row
+//     path, which keeps the lower key indices.  The kept set stays unsorted
+//     until one bitonic sort per row at the end.
 #include "jn_internal.hpp"
 
 namespace jakal {
@@ -43,11 +48,15 @@ constexpr int kSelRowsPerWave = 16;
 constexpr int kSelRows = kSelWaves * kSelRowsPerWave;  // 64 query rows / workgroup
 constexpr int kSelChunk = 32;                          // key rows per LDS chunk
 constexpr int kSelKeep = kSelectMaxK;                  // kept-entry region per row
-constexpr int kSelMergeAt = 32;                        // merge once this many candidates wait
-constexpr int kSelSlots = kSelKeep + kSelMergeAt - 1 + kSelChunk;  // 95 used
-constexpr int kSelSlotStride = 96;
-static_assert(kSelSlots <= kSelSlotStride, "slot array too small");
-static_assert(kSelSlotStride <= 128, "merge reads at most two slots per lane");
+constexpr int kSelMergeAt = 64;                        // merge once this many candidates wait
+constexpr int kSelSlots = kSelKeep + kSelMergeAt - 1 + kSelChunk;  // 127 used
+// Row strides are 16-byte multiples (vector reads) that shift successive rows by
+// 4 LDS banks, so the 16 rows of a wave read and write on distinct banks.
+constexpr int kSelScoreStride = 132;  // floats
+constexpr int kSelIndexStride = 136;  // uint16 (68 words)
+constexpr int kSelTrash = 127;        // slot that absorbs writes of non-winners
+constexpr int kSelMaxKeys = 65535;    // key indices are stored as uint16
+static_assert(kSelSlots <= 128, "merge reads at most two slots per lane");
 
 // Monotone map float -> uint32 (larger float -> larger key); -0 and +0 map together.
 __device__ __forceinline__ uint32_t order_key(float s) {
@@ -92,7 +101,7 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
 
 // Merge one row: keep the k best of its k kept entries and `cnt` candidates,
 // compacted to slots [0, k); returns the new k-th best score (wave-uniform).
-__device__ float merge_row(float* row_s, int* row_i, int k, int cnt) {
+__device__ float merge_row(float* row_s, uint16_t* row_i, int k, int cnt) {
   const int lane = lane_id();
   const int n_used = kSelKeep + cnt;
   const int sa = lane, sb = 64 + lane;
@@ -111,43 +120,67 @@ __device__ float merge_row(float* row_s, int* row_i, int k, int cnt) {
   const uint32_t ka = va ? order_key(fa) : 0u;
   const uint32_t kb = vb ? order_key(fb) : 0u;
 
-  // k-th largest key: the largest t with #(key >= t) >= k
-  uint32_t t = 0;
-#pragma unroll 4
-  for (int bit = 31; bit >= 0; --bit) {
+  // Radix select of the k-th largest key.  All valid keys lie in [lo, hi]; the
+  // bits above the highest bit where lo and hi differ are common to every
+  // candidate threshold, so the search starts below them.
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(wave_max_u32(max(ka, kb)));
+  const uint32_t lo =
+      __builtin_amdgcn_readfirstlane(wave_min_u32(min(va ? ka : 0xffffffffu, vb ? kb : 0xffffffffu)));
+  const uint32_t diff = hi ^ lo;
+  int bit = diff ? 31 - __builtin_clz(diff) : -1;
+  uint32_t t = diff ? (hi & ~((2u << bit) - 1u)) : hi;  // common prefix (bit 31 case handled below)
+  if (bit == 31) t = 0;
+  int n_at_t = k + 1;  // unknown; forces the tie path if the loop never lands on exactly k
+  for (; bit >= 0; --bit) {
     const uint32_t c = t | (1u << bit);
     const int n = popc64(__ballot(ka >= c)) + popc64(__ballot(kb >= c));
-    t = (n >= k) ? c : t;
+    if (n >= k) {
+      t = c;
+      n_at_t = n;
+      if (n == k) break;  // exactly k keys >= t: they are the winners
+    }
   }
-  bool keep_a = ka > t, keep_b = kb > t;
-  const int n_gt = popc64(__ballot(keep_a)) + popc64(__ballot(keep_b));
-  bool eq_a = (ka == t) && va, eq_b = (kb == t) && vb;
-  int need = k - n_gt;
-  const int n_eq = popc64(__ballot(eq_a)) + popc64(__ballot(eq_b));
-  if (n_eq == need) {
-    keep_a |= eq_a;
-    keep_b |= eq_b;
+  bool keep_a, keep_b;
+  uint32_t theta_key;
+  if (n_at_t == k) {
+    keep_a = va && ka >= t;
+    keep_b = vb && kb >= t;
+    uint32_t m = 0xffffffffu;
+    if (keep_a) m = ka;
+    if (keep_b) m = min(m, kb);
+    theta_key = __builtin_amdgcn_readfirstlane(wave_min_u32(m));
   } else {
-    // exact ties at the k-th value: take the lowest key indices, one at a time
-    for (; need > 0; --need) {
-      int m = 0x7fffffff;
-      if (eq_a) m = min(m, ia);
-      if (eq_b) m = min(m, ib);
-#pragma unroll
-      for (int s = 32; s >= 1; s >>= 1) m = min(m, shfl_xor_i(m, s));
-      if (eq_a && ia == m) {
-        keep_a = true;
-        eq_a = false;
-      }
-      if (eq_b && ib == m) {
-        keep_b = true;
-        eq_b = false;
+    // t is the k-th largest key itself; resolve ties at t toward lower indices
+    theta_key = t;
+    keep_a = ka > t;
+    keep_b = kb > t;
+    const int n_gt = popc64(__ballot(keep_a)) + popc64(__ballot(keep_b));
+    bool eq_a = va && (ka == t), eq_b = vb && (kb == t);
+    int need = k - n_gt;
+    const int n_eq = popc64(__ballot(eq_a)) + popc64(__ballot(eq_b));
+    if (n_eq == need) {
+      keep_a |= eq_a;
+      keep_b |= eq_b;
+    } else {
+      for (; need > 0; --need) {
+        int m = 0x7fffffff;
+        if (eq_a) m = min(m, ia);
+        if (eq_b) m = min(m, ib);
+        m = wave_min_i32(m);
+        if (eq_a && ia == m) {
+          keep_a = true;
+          eq_a = false;
+        }
+        if (eq_b && ib == m) {
+          keep_b = true;
+          eq_b = false;
+        }
       }
     }
   }
-  // the k-th best score: any element whose key equals t
-  const uint64_t eqm_a = __ballot((ka == t) && va);
-  const uint64_t eqm_b = __ballot((kb == t) && vb);
+  // the k-th best score: an element whose key equals theta_key
+  const uint64_t eqm_a = __ballot(va && ka == theta_key);
+  const uint64_t eqm_b = __ballot(vb && kb == theta_key);
   const float theta = eqm_a ? readlane_f(fa, __builtin_ctzll(eqm_a)) : readlane_f(fb, __builtin_ctzll(eqm_b));
 
   const uint64_t ma = __ballot(keep_a);
@@ -157,25 +190,143 @@ __device__ float merge_row(float* row_s, int* row_i, int k, int cnt) {
   // the reads above have returned (their values feed these stores)
   if (keep_a) {
     row_s[pa] = fa;
-    row_i[pa] = ia;
+    row_i[pa] = (uint16_t)ia;
   }
   if (keep_b) {
     row_s[pb] = fb;
-    row_i[pb] = ib;
+    row_i[pb] = (uint16_t)ib;
   }
   wave_lds_sync();
   return theta;
+}
+
+
+__device__ __forceinline__ float key_to_float(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+// Merge every row of the wave at once.  Lane (g, col) owns slots
+// [32g, 32g+32) of row col: the k kept entries (g == 0) or candidates.  The
+// radix select runs per lane over its 32 keys, with row counts summed over the
+// row's 4 lanes by permlane swaps.  Rows with exact ties at the k-th value
+// return fallback = true and are left untouched for merge_row.
+__device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int cnt_row, float& theta,
+                                   bool& fallback) {
+  const int lane = lane_id();
+  const int g = lane >> 4;
+  const int base = 32 * g;
+  const int n_valid = (g == 0) ? k : max(0, min(32, kSelKeep + cnt_row - base));
+  uint32_t key[32];
+  int id[32];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float4 v = *reinterpret_cast<const float4*>(row_s + base + 4 * q);
+    key[4 * q + 0] = (4 * q + 0 < n_valid) ? order_key(v.x) : 0u;
+    key[4 * q + 1] = (4 * q + 1 < n_valid) ? order_key(v.y) : 0u;
+    key[4 * q + 2] = (4 * q + 2 < n_valid) ? order_key(v.z) : 0u;
+    key[4 * q + 3] = (4 * q + 3 < n_valid) ? order_key(v.w) : 0u;
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row_i + base + 8 * q);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      id[8 * q + 2 * h] = (int)(w[h] & 0xffffu);
+      id[8 * q + 2 * h + 1] = (int)(w[h] >> 16);
+    }
+  }
+  // row range of valid keys
+  uint32_t hi = 0, lo = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    hi = max(hi, key[i]);
+    lo = min(lo, (i < n_valid) ? key[i] : 0xffffffffu);
+  }
+  hi = max(hi, (uint32_t)xor16_i((int)hi));
+  hi = max(hi, (uint32_t)xor32_i((int)hi));
+  lo = min(lo, (uint32_t)xor16_i((int)lo));
+  lo = min(lo, (uint32_t)xor32_i((int)lo));
+  const uint32_t diff = hi ^ lo;
+  const int start = diff ? 31 - __builtin_clz(diff) : -1;
+  uint32_t t = diff ? (hi & ~((2u << start) - 1u)) : hi;  // shared prefix of the row's keys
+  if (start == 31) t = 0;
+  const int wave_start = (int)wave_max_u32((uint32_t)(start + 1)) - 1;  // uniform loop bound
+  bool done = false;
+  for (int bit = wave_start; bit >= 0; --bit) {
+    if (!__ballot(!done)) break;
+    const uint32_t c = t | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) cnt += (key[i] >= c) ? 1 : 0;
+    int n = cnt + xor16_i(cnt);
+    n += xor32_i(n);
+    if (!done && n >= k) {
+      t = c;
+      done = (n == k);
+    }
+  }
+  // winners: exactly k keys >= t (done), or the k-th largest key is t itself
+  uint32_t keep_bits = 0;
+  uint32_t theta_key;
+  bool tie_row = false;
+  if (done) {
+    uint32_t m = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const bool kp = (i < n_valid) && key[i] >= t;
+      keep_bits |= kp ? (1u << i) : 0u;
+      m = kp ? min(m, key[i]) : m;
+    }
+    m = min(m, (uint32_t)xor16_i((int)m));
+    m = min(m, (uint32_t)xor32_i((int)m));
+    theta_key = m;
+  } else {
+    int gt = 0, eq = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      gt += (key[i] > t) ? 1 : 0;
+      eq += ((i < n_valid) && key[i] == t) ? 1 : 0;
+    }
+    gt += xor16_i(gt);
+    gt += xor32_i(gt);
+    eq += xor16_i(eq);
+    eq += xor32_i(eq);
+    tie_row = (eq != k - gt);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) keep_bits |= ((i < n_valid) && key[i] >= t) ? (1u << i) : 0u;
+    theta_key = t;
+  }
+  fallback = tie_row;
+  // compact the winners of non-tie rows to slots [0, k)
+  const int w = __builtin_popcount(keep_bits);
+  const int w1 = xor16_i(w);
+  const int w2 = xor32_i(w);
+  const int w3 = xor16_i(w2);
+  int pos = (g == 0) ? 0 : (g == 1) ? w1 : (g == 2) ? (w2 + w3) : (w1 + w2 + w3);
+  if (!tie_row) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const bool kp = (keep_bits >> i) & 1u;
+      const int dst = kp ? pos : kSelTrash;
+      row_s[dst] = key_to_float(key[i]);
+      row_i[dst] = (uint16_t)id[i];
+      pos += kp ? 1 : 0;
+    }
+    theta = key_to_float(theta_key);
+  }
+  wave_lds_sync();
 }
 
 // VEC: r == 4*RQ and 16-byte aligned key rows -> unconditional float4 chunk loads.
 template <int RQ, bool VEC>
 __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs a) {
   constexpr int RP = 4 * RQ;
-  constexpr int KSTRIDE = RP + 4;  // padded LDS row (floats)
+  constexpr int KSTRIDE = RP + 4;  // padded key row (floats)
 
   __shared__ __align__(16) float s_key[2][kSelChunk * KSTRIDE];
-  __shared__ float s_slot_s[kSelRows * kSelSlotStride];
-  __shared__ int s_slot_i[kSelRows * kSelSlotStride];
+  __shared__ __align__(16) float s_slot_s[kSelRows * kSelScoreStride];
+  __shared__ __align__(16) uint16_t s_slot_i[kSelRows * kSelIndexStride];
   __shared__ __align__(16) float s_scale[RP];
 
   const int tid = threadIdx.x;
@@ -201,13 +352,14 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
   // the kept region starts as k sentinels that lose to every finite score
   for (int i = tid; i < kSelRows * kSelKeep; i += blockDim.x) {
     const int rrow = i / kSelKeep, e = i % kSelKeep;
-    s_slot_s[rrow * kSelSlotStride + e] = -INFINITY;
-    s_slot_i[rrow * kSelSlotStride + e] = 0x7fffffff;
+    s_slot_s[rrow * kSelScoreStride + e] = -INFINITY;
+    s_slot_i[rrow * kSelIndexStride + e] = 0xffff;
   }
   __syncthreads();
 
   // ---- query fragment in registers ------------------------------------------
-  const int my_row = row0 + wave * kSelRowsPerWave + col;
+  const int lrow = wave * kSelRowsPerWave + col;  // row slot within the workgroup
+  const int my_row = row0 + lrow;
   const bool row_ok = my_row < a.Nq;
   float qf[RQ];
 #pragma unroll
@@ -239,7 +391,7 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
         const int f = tid + u * 256;
         if (kChunkF4 % 256 == 0 || f < kChunkF4) {
           const int rrow = f / RQ, c4 = f % RQ;
-          const int krow = min(c0 + rrow, a.Nk - 1);  // tail rows: a valid row, masked at the compare
+          const int krow = min(c0 + rrow, a.Nk - 1);  // tail rows: a valid row, masked later
           pf4[u] = *reinterpret_cast<const float4*>(kbase + (int64_t)krow * a.ldk + 4 * c4);
         }
       }
@@ -292,11 +444,8 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
 
   float theta = row_ok ? -INFINITY : INFINITY;  // invalid rows never admit
   int cnt = 0;                                  // candidates waiting for this lane's row
-  const int lrow = wave * kSelRowsPerWave + col;
-  float* my_slot_s = s_slot_s + lrow * kSelSlotStride;
-  int* my_slot_i = s_slot_i + lrow * kSelSlotStride;
-  // 4-lane prefix sources: the lanes of the same row in the lower rank slices
-  const int src16 = (lane - 16) & 63, src32 = (lane - 32) & 63, src_top = col + 48;
+  float* my_slot_s = s_slot_s + lrow * kSelScoreStride;
+  uint16_t* my_slot_i = s_slot_i + lrow * kSelIndexStride;
 
   for (int c = 0; c < nchunks; ++c) {
     const int cur = c & 1;
@@ -332,29 +481,35 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
 
     // -- threshold filter: lane holds keys c0 + 16t + 4g + v of its row --
     float sc[8];
-    uint32_t pass_mask = 0;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float s = (((u < 4) ? acc0[u & 3] : acc1[u & 3]) + bias) * inv_temp;
-      sc[u] = s;
-      const int key = c0 + (u >> 2) * 16 + 4 * g + (u & 3);
-      pass_mask |= ((key < a.Nk) & (s > theta)) ? (1u << u) : 0u;
+    for (int u = 0; u < 8; ++u) sc[u] = (((u < 4) ? acc0[u & 3] : acc1[u & 3]) + bias) * inv_temp;
+    if (c0 + kSelChunk > a.Nk) {  // uniform: only the last chunk holds padding keys
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (c0 + (u >> 2) * 16 + 4 * g + (u & 3) >= a.Nk) sc[u] = -INFINITY;
     }
-    if (__ballot(pass_mask != 0)) {
+    uint64_t any = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) any |= __ballot(sc[u] > theta);
+    if (any) {
+      uint32_t pass_mask = 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) pass_mask |= (sc[u] > theta) ? (1u << u) : 0u;
+      // counts of the row's 4 lanes (lane groups g^1, g^2, g^3) via permlane swaps
       const int np = __builtin_popcount(pass_mask);
-      const int up16 = __builtin_amdgcn_ds_bpermute(src16 << 2, np);
-      const int incl1 = np + (g >= 1 ? up16 : 0);
-      const int up32 = __builtin_amdgcn_ds_bpermute(src32 << 2, incl1);
-      const int incl2 = incl1 + (g >= 2 ? up32 : 0);
-      const int total = __builtin_amdgcn_ds_bpermute(src_top << 2, incl2);
-      int pos = kSelKeep + cnt + incl2 - np;
+      const int n1 = xor16_i(np);
+      const int n2 = xor32_i(np);
+      const int n3 = xor16_i(n2);
+      const int excl = (g == 0) ? 0 : (g == 1) ? n1 : (g == 2) ? (n2 + n3) : (n1 + n2 + n3);
+      const int total = np + n1 + n2 + n3;
+      int pos = kSelKeep + cnt + excl;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        if (pass_mask & (1u << u)) {
-          my_slot_s[pos] = sc[u];
-          my_slot_i[pos] = c0 + (u >> 2) * 16 + 4 * g + (u & 3);
-          ++pos;
-        }
+        const bool ok = (pass_mask >> u) & 1u;
+        const int dst = ok ? pos : kSelTrash;
+        my_slot_s[dst] = sc[u];
+        my_slot_i[dst] = (uint16_t)(c0 + (u >> 2) * 16 + 4 * g + (u & 3));
+        pos += ok ? 1 : 0;
       }
       cnt += total;
       wave_lds_sync();
@@ -362,17 +517,22 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
 
     // -- merge rows whose candidates filled up (or everything at the end) --
     const bool last = (c + 1 == nchunks);
-    uint64_t m = __ballot(lane < kSelRowsPerWave && (cnt >= kSelMergeAt || (last && cnt > 0)));
-    while (m) {
-      const int t = __builtin_ctzll(m);
-      m &= m - 1;
-      const int row_cnt = readlane_i(cnt, t);
-      const int slot = wave * kSelRowsPerWave + t;
-      const float th = merge_row(s_slot_s + slot * kSelSlotStride, s_slot_i + slot * kSelSlotStride, k, row_cnt);
-      if (col == t) {
-        theta = th;
-        cnt = 0;
+    if (__ballot(lane < kSelRowsPerWave && (cnt >= kSelMergeAt || (last && cnt > 0)))) {
+      bool fallback;
+      merge_rows_batched(my_slot_s, my_slot_i, k, cnt, theta, fallback);
+      // rows with exact ties at the k-th value: exact per-row merge
+      uint64_t m = __ballot(lane < kSelRowsPerWave && fallback);
+      while (m) {
+        const int t = __builtin_ctzll(m);
+        m &= m - 1;
+        const int row_cnt = readlane_i(cnt, t);
+        const int slot = wave * kSelRowsPerWave + t;
+        const float th =
+            merge_row(s_slot_s + slot * kSelScoreStride, s_slot_i + slot * kSelIndexStride, k, row_cnt);
+        if (col == t) theta = th;
       }
+      if (!row_ok) theta = INFINITY;  // rows past Nq stay closed
+      cnt = 0;
     }
 
     // -- next key chunk into the other LDS buffer --
@@ -388,8 +548,8 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
     float vs = -INFINITY;
     int vi = 0x7fffffff;
     if (lane < k) {
-      vs = s_slot_s[slot * kSelSlotStride + lane];
-      vi = s_slot_i[slot * kSelSlotStride + lane];
+      vs = s_slot_s[slot * kSelScoreStride + lane];
+      vi = s_slot_i[slot * kSelIndexStride + lane];
     }
     bitonic_sort64_desc(vs, vi);
     if (lane < k) {
@@ -409,6 +569,7 @@ static void launch_rq(const SelectArgs& a, bool vec, dim3 grid, hipStream_t stre
 int launch_topk_select(const SelectArgs& a, hipStream_t stream) {
   JN_REQUIRE(a.k >= 1 && a.k <= kSelKeep, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)", kSelKeep, a.k);
   JN_REQUIRE(a.k < a.Nk, kInvalidArgument, "top-k select needs k < key count (k=%d, Nk=%d)", a.k, a.Nk);
+  JN_REQUIRE(a.Nk <= kSelMaxKeys, kUnsupported, "top-k select supports at most %d keys (got %d)", kSelMaxKeys, a.Nk);
   JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128] (got %d)", a.r);
   JN_REQUIRE(a.temperature > 0.0f, kInvalidArgument, "temperature must be positive");
   const int tiles = (a.Nq + kSelRows - 1) / kSelRows;

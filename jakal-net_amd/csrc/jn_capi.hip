@@ -67,7 +67,7 @@ ProfileScope::~ProfileScope() {
 
 namespace {
 
-constexpr int kColsPerWave = 16;
+constexpr int kColsPerWave = 8;
 
 bool fits_int(int64_t v) { return v >= 0 && v < (1LL << 31); }
 

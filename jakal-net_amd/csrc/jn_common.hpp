@@ -144,10 +144,42 @@ __device__ __forceinline__ int wave_min_i32(int v) {
   return wave_reduce_i(v, [](int a, int b) { return min(a, b); });
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_f(v, m);
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float xor16_f(float v) { return __int_as_float(xor16_i(__float_as_int(v))); }
+__device__ __forceinline__ float xor32_f(float v) { return __int_as_float(xor32_i(__float_as_int(v))); }
+
+// Sum over the 16 lanes of each DPP row; every lane of the row receives it.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
   return v;
+}
+
+// Sum over the wave (fixed order, identical in every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v += xor16_f(v);
+  v += xor32_f(v);
+  return v;
+}
+
+// Raw buffer resource over [base, base + bytes): a load at a byte offset past
+// `bytes` returns zeros, which masks lanes without a branch.  The base must be
+// wave-uniform; offsets are 32-bit (callers keep bytes < 2^31).
+constexpr uint32_t kOobOffset = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+__device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
 }
 
 // Make LDS writes of this wavefront visible to later LDS reads of the same

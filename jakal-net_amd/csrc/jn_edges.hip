@@ -39,6 +39,13 @@ __device__ __forceinline__ void fma4(float4& acc, float c, float4 v) {
 __device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
 __device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
 
+// W consecutive floats at a byte offset of a buffer (zeros when out of range).
+template <int W>
+__device__ __forceinline__ float4 buf_load_w(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  if constexpr (W == 4) return buf_load4(r, byte_off);
+  else return make_float4(buf_load1(r, byte_off), 0.f, 0.f, 0.f);
+}
+
 __device__ __forceinline__ float sign_f(float s) { return (s > 0.f) ? 1.f : ((s < 0.f) ? -1.f : 0.f); }
 
 // ---------------------------------------------------------------------------
@@ -141,93 +148,99 @@ int launch_rows_forward(const RowsFwdArgs& a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Row backward: one wavefront per query row, edges in groups of KP (<= 64).
+// Row backward: one wavefront per query row.
 //   g_c[e]   = gds[i] * ps[j] + <gdv[i], pv[j]>        (grad wrt edge coefficient)
 //   g_s[e]   = compress backward of g_c, times 1/T      (grad wrt score)
 //   dQ[i, r] = qscale[r] * sum_e g_s[e] * key[j, r]      (grad wrt query projection)
 //   coef[e]  = c(s_e)                                    (kept for the column pass)
 //   rowsum_gs[i] = sum_e g_s[e]                          (bias gradient partial)
-// Per-edge dot products are accumulated per lane over D and reduced for all KP
-// edges at once with a halving butterfly (KP-1 cross-lane ops instead of 6*KP).
+// The four 16-lane groups of the wave take four edges at a time (group g takes
+// edges 4i + g): a group reads a whole value row with 16-byte loads, so each
+// edge's dot product is reduced inside the group by DPP (4 VALU ops) and the
+// key rows of the dQ sum are read 4 edges per instruction.
 // ---------------------------------------------------------------------------
 
-// Reduce p[0..KP) (one partial per edge, per lane) across the wave.  Returns,
-// in every lane, the total of edge (lane >> log2(64/KP)).
-template <int KP>
-__device__ __forceinline__ float multi_reduce(float (&p)[KP]) {
-  const int lane = lane_id();
-  int m = 32;
-#pragma unroll
-  for (int h = KP / 2; h >= 1; h >>= 1, m >>= 1) {
-    const bool upper = (lane & m) != 0;
-#pragma unroll
-    for (int q = 0; q < h; ++q) {
-      float send = upper ? p[q] : p[q + h];
-      float keep = upper ? p[q + h] : p[q];
-      p[q] = keep + shfl_xor_f(send, m);
-    }
-  }
-  float v = p[0];
-  for (; m >= 1; m >>= 1) v += shfl_xor_f(v, m);
-  return v;
-}
+// Round-robin edge -> group assignment: lane L (< KP) takes the edge held by
+// group L % 4 in iteration L / 4.
+__device__ __forceinline__ int edge_owner_lane(int lane) { return (lane & 3) * 16 + (lane >> 2); }
 
-template <int W, int KP>
+template <int W, int NV, int KP>
 __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
-  constexpr int kShift = (KP == 64) ? 0 : (KP == 32 ? 1 : (KP == 16 ? 2 : 3));
+  constexpr int NI = KP / 4;      // iterations per block of KP edges
+  constexpr int P = 16 * W * NV;  // D floats per pass of a 16-lane group
   const int lane = lane_id();
+  const int g = lane >> 4, c = lane & 15;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
   if (row >= a.rows) return;
   const int64_t b = row / a.Nq;
-  const float* pvb = a.pv + b * a.Nk * a.ld_pv;
   const float* psb = a.ps + b * a.Nk;
-  const float* keyb = a.key + b * a.Nk * a.ldk;
-  const float* grow = a.gdv + row * a.D;
   const float gs_row = a.gds[row];
+  // 32-bit offsets into buffers of this batch element (sizes checked on the host)
+  const auto rs_pv = make_rsrc(a.pv + b * a.Nk * a.ld_pv, (uint32_t)(a.Nk * a.ld_pv * 4));
+  const auto rs_key = make_rsrc(a.key + b * a.Nk * a.ldk, (uint32_t)(a.Nk * a.ldk * 4));
+  const auto rs_g = make_rsrc(a.gdv + row * a.D, (uint32_t)(a.D * 4));
+  // key rows as float4 when 16-byte aligned (rank slots 4c and 64 + 4c)
+  const bool kvec = (a.r % 4 == 0) && (a.ldk % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.key) & 15) == 0);
 
   float rmax = 0.f, rinv = 0.f;
   if (a.compress == 1) row_abs_softmax_stats(a.idx, a.score, row, a.k, rmax, rinv);
 
-  float dq_acc0 = 0.f, dq_acc1 = 0.f;  // rank lanes: lane and lane + 64
+  float4 dqa = make_float4(0.f, 0.f, 0.f, 0.f), dqb = dqa;  // kvec: ranks 4c.., 64+4c..
+  float dqs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // scalar: ranks c + 16m
   float gsum = 0.f;
   for (int e0 = 0; e0 < a.k; e0 += KP) {
     int j;
-    float c, s;
-    // lanes < KP hold edges e0 + lane
-    row_coefficients(a.idx, a.score, row, a.k, e0, a.compress, rmax, rinv, j, c, s);
+    float cf, s;
+    // lanes < KP hold edges e0 + lane (j = -1 past k)
+    row_coefficients(a.idx, a.score, row, a.k, e0, a.compress, rmax, rinv, j, cf, s);
     if (lane >= KP) j = -1;
     const int ne = min(KP, a.k - e0);
-    float p[KP];
+    int jg[NI];
 #pragma unroll
-    for (int q = 0; q < KP; ++q) p[q] = 0.f;
-    for (int d = lane * W; d < a.D; d += kWave * W) {
-      const float4 gv = load_w<W>(grow + d);
+    for (int i = 0; i < NI; ++i) jg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, j);
+
+    float dots[NI];
 #pragma unroll
-      for (int q0 = 0; q0 < KP; q0 += 8) {
-        if (q0 < ne) {  // uniform; absent edges (j < 0) read row 0 and are masked
-          float4 v[8];
-          float msk[8];
+    for (int i = 0; i < NI; ++i) dots[i] = 0.f;
+    for (int d0 = 0; d0 < a.D; d0 += P) {
+      // byte offsets of this lane's slice of the pass; past D -> out of range (zeros)
+      uint32_t loff[NV];
+      float4 gv[NV];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const int jj = readlane_i(j, q0 + u);
-            msk[u] = jj >= 0 ? 1.f : 0.f;
-            v[u] = load_w<W>(pvb + (int64_t)(jj < 0 ? 0 : jj) * a.ld_pv + d);
-          }
+      for (int t = 0; t < NV; ++t) {
+        const int off = d0 + (16 * t + c) * W;
+        loff[t] = off < a.D ? (uint32_t)off * 4u : kOobOffset;
+        gv[t] = buf_load_w<W>(rs_g, loff[t]);
+      }
 #pragma unroll
-          for (int u = 0; u < 8; ++u) p[q0 + u] += msk[u] * dot4(gv, v[u]);
-        }
+      for (int i = 0; i < NI; ++i) {
+        // absent edges read row 0 and are masked
+        const uint32_t roff = (uint32_t)max(jg[i], 0) * (uint32_t)a.ld_pv * 4u;
+        float4 v[NV];
+#pragma unroll
+        for (int t = 0; t < NV; ++t) v[t] = buf_load_w<W>(rs_pv, loff[t] == kOobOffset ? kOobOffset : roff + loff[t]);
+        float pdot = 0.f;
+#pragma unroll
+        for (int t = 0; t < NV; ++t) pdot += dot4(gv[t], v[t]);
+        dots[i] += jg[i] >= 0 ? pdot : 0.f;
+        // at most 16 row loads in flight per lane: keeps VGPRs (and occupancy) in check
+        if (((i + 1) * NV) % 16 == 0) __builtin_amdgcn_sched_barrier(0);
       }
     }
-    const float dot_all = multi_reduce<KP>(p);
-    // bring edge `lane` (for lane < KP) to its own lane
-    const float dot = __int_as_float(__builtin_amdgcn_ds_bpermute((lane << kShift) << 2, __float_as_int(dot_all)));
-    float gc = (j >= 0) ? gs_row * psb[j] + dot : 0.f;
+    float sel = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const float tot = row16_sum(dots[i]);
+      sel = (c == i) ? tot : sel;
+    }
+    const float dot = __int_as_float(__builtin_amdgcn_ds_bpermute(edge_owner_lane(lane) << 2, __float_as_int(sel)));
+    const float gc = (j >= 0) ? gs_row * psb[j] + dot : 0.f;
     float gsc = 0.f;
     if (a.compress == 1) {
-      const float row_dot = wave_sum(gc * c);  // single group: k <= KP enforced on the host
+      const float row_dot = wave_sum(gc * cf);  // single block: k <= 64 enforced on the host
       if (j >= 0) {
         const float sg = sign_f(s);
-        gsc = sg * (sg * c) * (sg * gc - row_dot);
+        gsc = sg * (sg * cf) * (sg * gc - row_dot);
       }
     } else if (j >= 0) {
       gsc = gc * softsign_grad_f(s);
@@ -235,22 +248,68 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
     gsc *= a.inv_temperature;
     if (lane < ne) {
       a.g_score[row * a.k + e0 + lane] = gsc;
-      a.coef[row * a.k + e0 + lane] = c;
+      a.coef[row * a.k + e0 + lane] = cf;
     }
     gsum += gsc;
-    for (int q = 0; q < ne; ++q) {
-      const int jj = readlane_i(j, q);
-      if (jj < 0) continue;
-      const float gg = readlane_f(gsc, q);
-      const float* kr = keyb + (int64_t)jj * a.ldk;
-      if (lane < a.r) dq_acc0 += gg * kr[lane];
-      if (lane + kWave < a.r) dq_acc1 += gg * kr[lane + kWave];
+
+    // dQ partials: group g sums its edges (absent edges carry gsc = 0)
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const float gg = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * i + g) << 2, __float_as_int(gsc)));
+      const uint32_t koff = (uint32_t)max(jg[i], 0) * (uint32_t)a.ldk * 4u;
+      if (kvec) {
+        fma4(dqa, gg, buf_load4(rs_key, 4 * c < a.r ? koff + 16u * c : kOobOffset));
+        if (a.r > 64) fma4(dqb, gg, buf_load4(rs_key, 64 + 4 * c < a.r ? koff + 256u + 16u * c : kOobOffset));
+      } else {
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+          if (16 * m < a.r) dqs[m] += gg * buf_load1(rs_key, c + 16 * m < a.r ? koff + 4u * (c + 16 * m) : kOobOffset);
+      }
+      if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
     }
   }
-  if (lane < a.r) a.dq[row * a.lddq + lane] = dq_acc0 * (a.qscale ? a.qscale[lane] : 1.f);
-  if (lane + kWave < a.r) a.dq[row * a.lddq + lane + kWave] = dq_acc1 * (a.qscale ? a.qscale[lane + kWave] : 1.f);
+  // sum the four groups; lane (g, c) then stores one rank per slot
+  float* dqrow = a.dq + row * a.lddq;
+  if (kvec) {
+    float v[8] = {dqa.x, dqa.y, dqa.z, dqa.w, dqb.x, dqb.y, dqb.z, dqb.w};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      v[u] += xor16_f(v[u]);
+      v[u] += xor32_f(v[u]);
+    }
+    // lane (g, c) stores component g of both slots: ranks 4c + g and 64 + 4c + g
+    float lo = v[0], hi = v[4];
+#pragma unroll
+    for (int u = 1; u < 4; ++u) {
+      lo = (g == u) ? v[u] : lo;
+      hi = (g == u) ? v[4 + u] : hi;
+    }
+    const int r0 = 4 * c + g, r1 = 64 + 4 * c + g;
+    if (r0 < a.r) dqrow[r0] = lo * (a.qscale ? a.qscale[r0] : 1.f);
+    if (r1 < a.r) dqrow[r1] = hi * (a.qscale ? a.qscale[r1] : 1.f);
+  } else {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      dqs[m] += xor16_f(dqs[m]);
+      dqs[m] += xor32_f(dqs[m]);
+    }
+    // lane (g, c) stores slots m = g and m = g + 4: ranks c + 16m
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int rr = c + 16 * m;
+      if ((m & 3) == g && rr < a.r) dqrow[rr] = dqs[m] * (a.qscale ? a.qscale[rr] : 1.f);
+    }
+  }
   gsum = wave_sum(gsum);
   if (lane == 0) a.rowsum_gs[row] = gsum;
+}
+
+template <int W, int NV>
+static void launch_rows_bwd_kp(const RowsBwdArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 8>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 16) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 16>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 32) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 32>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((rows_backward_kernel<W, NV, 64>), grid, dim3(256), 0, stream, a);
 }
 
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
@@ -258,20 +317,19 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
   JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
   JN_REQUIRE(a.compress == 0 || a.k <= 64, kUnsupported, "signed_abs_softmax backward supports k <= 64");
   const int64_t blocks = (a.rows + 3) / 4;
+  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
+  JN_REQUIRE((int64_t)a.Nk * a.ld_pv * 4 < (1LL << 31) && (int64_t)a.Nk * a.ldk * 4 < (1LL << 31) &&
+                 (int64_t)a.D * 4 < (1LL << 31),
+             kUnsupported, "one batch element of the value or key rows must stay below 2 GiB");
   const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0);
-  dim3 grid((unsigned)blocks), block(256);
+  dim3 grid((unsigned)blocks);
   JN_PROFILE("rows_backward_kernel", stream);
-  if (a.k <= 16) {
-    if (vec) hipLaunchKernelGGL((rows_backward_kernel<4, 16>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((rows_backward_kernel<1, 16>), grid, block, 0, stream, a);
-  } else if (a.k <= 32) {
-    if (vec) hipLaunchKernelGGL((rows_backward_kernel<4, 32>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((rows_backward_kernel<1, 32>), grid, block, 0, stream, a);
-  } else {
-    if (vec) hipLaunchKernelGGL((rows_backward_kernel<4, 64>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((rows_backward_kernel<1, 64>), grid, block, 0, stream, a);
-  }
+  if (!vec) launch_rows_bwd_kp<1, 4>(a, grid, stream);
+  else if (a.D > 256) launch_rows_bwd_kp<4, 8>(a, grid, stream);
+  else if (a.D > 128) launch_rows_bwd_kp<4, 4>(a, grid, stream);
+  else if (a.D > 64) launch_rows_bwd_kp<4, 2>(a, grid, stream);
+  else launch_rows_bwd_kp<4, 1>(a, grid, stream);
   JN_LAUNCH_CHECK();
   return kOk;
 }
@@ -423,134 +481,165 @@ int launch_csr(const CsrArgs& a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Column backward: one wavefront per key column j, walking its CSR segment.
+// Column backward: key columns j, walking their CSR segments.
 //   grad_pv[j]  = sum_in coef * gdv[i]
 //   grad_ps[j]  = sum_in coef * gds[i]
 //   dK[j, r]    = kscale[r] * sum_in g_s * q[i, r]
 //   part_c[w,r] += key[j, r] * sum_in g_s * q[i, r]      (scale-vector gradient)
-// Each wavefront owns a fixed run of columns so partials are reproducible.
+// A wavefront owns a fixed run of up to 64 columns and reads their segments as
+// one stream of incoming edges: the metadata (edge id -> row, coef, g_s) of 64
+// stream entries is fetched with one load per lane, then the gathers run over
+// the stream in groups of 8 edges and a column's sums are stored when the
+// stream passes its end.  The order of every sum is fixed, so the results are
+// run-to-run reproducible.
 // ---------------------------------------------------------------------------
 
-template <bool VEC>
+template <int W, int NV>
 __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
+  constexpr int P = kWave * W * NV;  // D floats per pass
+  constexpr int G = 8;               // edges per gather group
   const int lane = lane_id();
   const int64_t gw = (int64_t)blockIdx.x * 4 + wave_id();
   const int64_t total_cols = (int64_t)a.B * a.Nk;
   const int64_t nwaves = (total_cols + a.cols_per_wave - 1) / a.cols_per_wave;
   if (gw >= nwaves) return;  // padding waves of the last workgroup own no partial slot
-  const int64_t col_begin = gw * a.cols_per_wave;
-  float pc0 = 0.f, pc1 = 0.f;
-  constexpr int W = VEC ? 4 : 1;
-  for (int64_t cc = 0; cc < a.cols_per_wave; ++cc) {
-    const int64_t colg = col_begin + cc;
-    if (colg >= total_cols) break;
+  const int64_t c_begin = gw * a.cols_per_wave;
+  const int ncols = (int)min((int64_t)a.cols_per_wave, total_cols - c_begin);  // <= 64
+
+  // lane l < ncols describes column c_begin + l: its edges are stream entries
+  // [excl, incl) and stream entry q of it sits at edges[offc + q]
+  int len = 0, offc = 0;
+  if (lane < ncols) {
+    const int64_t colg = c_begin + lane;
     const int b = (int)(colg / a.Nk), j = (int)(colg % a.Nk);
     const int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
-    const int s_beg = seg[j], s_end = seg[j + 1];
-    const int32_t* el = a.edges + (int64_t)b * a.Nq * a.k;
+    const int beg = seg[j];
+    len = seg[j + 1] - beg;
+    offc = b * a.Nq * a.k + beg;  // < 2^31 (checked at CSR build)
+  }
+  int incl = len;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __builtin_amdgcn_ds_bpermute(((lane - o) & (kWave - 1)) << 2, incl);
+    if (lane >= o) incl += y;
+  }
+  offc -= incl - len;
+  const int total = readlane_i(incl, kWave - 1);
 
+  float pc0 = 0.f, pc1 = 0.f;
+  const int npass = a.grad_pv ? (a.D + P - 1) / P : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int d0 = pass * P;
+    const bool first = (pass == 0);
+    float4 acc[NV];
+#pragma unroll
+    for (int t = 0; t < NV; ++t) acc[t] = make_float4(0.f, 0.f, 0.f, 0.f);
     float dk0 = 0.f, dk1 = 0.f, st = 0.f;
-    // value gradient: loop D in passes of 64*W*2 so the accumulators stay in VGPRs
-    for (int d0 = 0; d0 < (a.grad_pv ? a.D : 1); d0 += kWave * W * 2) {
-      float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-      const int dl0 = d0 + lane * W, dl1 = d0 + kWave * W + lane * W;
-      const bool first_pass = (d0 == 0);
-      for (int p0 = s_beg; p0 < s_end; p0 += kWave) {
-        const int n = min(kWave, s_end - p0);
-        int eid = 0;
-        float cf = 0.f, gsv = 0.f;
-        if (lane < n) {
-          eid = el[p0 + lane];
-          cf = a.coef[eid];
-          if (first_pass) gsv = a.g_score[eid];
-        }
-        const int row_of = eid / a.k;
-        if (first_pass && lane < n && a.gds) st += cf * a.gds[row_of];
-        const int row0 = readlane_i(row_of, 0);
-        for (int q0 = 0; q0 < n; q0 += 4) {
-          int64_t rw[4];
-          float cu[4], gg[4];
+    int cur = 0;  // column being accumulated (wave-uniform)
+    uint32_t loff[NV];  // byte offsets of this lane's slice of the pass (past D: out of range)
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const bool ok = q0 + u < n;  // uniform
-            rw[u] = ok ? readlane_i(row_of, q0 + u) : row0;
-            cu[u] = ok ? readlane_f(cf, q0 + u) : 0.f;
-            gg[u] = ok ? readlane_f(gsv, q0 + u) : 0.f;
-          }
-          if (a.grad_pv) {
-            float4 v0[4], v1[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const float* gr = a.gdv + rw[u] * a.D;
-              if (dl0 < a.D) v0[u] = load_w<W>(gr + dl0);
-              if (dl1 < a.D) v1[u] = load_w<W>(gr + dl1);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              if (dl0 < a.D) {
-                acc[0][0] += cu[u] * v0[u].x;
-                acc[0][1] += cu[u] * v0[u].y;
-                acc[0][2] += cu[u] * v0[u].z;
-                acc[0][3] += cu[u] * v0[u].w;
-              }
-              if (dl1 < a.D) {
-                acc[1][0] += cu[u] * v1[u].x;
-                acc[1][1] += cu[u] * v1[u].y;
-                acc[1][2] += cu[u] * v1[u].z;
-                acc[1][3] += cu[u] * v1[u].w;
-              }
-            }
-          }
-          if (first_pass) {
-            float qa[4], qb2[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const float* qr = a.q + rw[u] * a.ldq;
-              qa[u] = lane < a.r ? qr[lane] : 0.f;
-              qb2[u] = lane + kWave < a.r ? qr[lane + kWave] : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              dk0 += gg[u] * qa[u];
-              dk1 += gg[u] * qb2[u];
-            }
-          }
-        }
-      }
+    for (int t = 0; t < NV; ++t) {
+      const int off = d0 + (kWave * t + lane) * W;
+      loff[t] = off < a.D ? (uint32_t)off * 4u : kOobOffset;
+    }
+
+    auto flush = [&](int cc) {
+      const int64_t colg = c_begin + cc;
       if (a.grad_pv) {
         float* out = a.grad_pv + colg * a.ld_gpv;
-        if (VEC) {
-          if (dl0 < a.D) {
-            float4 v = make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
-            float4* p = reinterpret_cast<float4*>(out + dl0);
-            if (a.accumulate_gpv) { float4 o = *p; v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w; }
-            *p = v;
+#pragma unroll
+        for (int t = 0; t < NV; ++t) {
+          const int off = d0 + (kWave * t + lane) * W;
+          if (off < a.D) {
+            float4 v = acc[t];
+            if (a.accumulate_gpv) v = add4(v, load_w<W>(out + off));
+            store_w<W>(out + off, v);
           }
-          if (dl1 < a.D) {
-            float4 v = make_float4(acc[1][0], acc[1][1], acc[1][2], acc[1][3]);
-            float4* p = reinterpret_cast<float4*>(out + dl1);
-            if (a.accumulate_gpv) { float4 o = *p; v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w; }
-            *p = v;
+          acc[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      if (first) {
+        if (a.grad_ps && lane == 0) a.grad_ps[colg] = st;
+        const float* kr = a.key + colg * a.ldk;
+        if (lane < a.r) {
+          a.dk[colg * a.lddk + lane] = dk0 * (a.kscale ? a.kscale[lane] : 1.f);
+          pc0 += kr[lane] * dk0;
+        }
+        if (lane + kWave < a.r) {
+          a.dk[colg * a.lddk + lane + kWave] = dk1 * (a.kscale ? a.kscale[lane + kWave] : 1.f);
+          pc1 += kr[lane + kWave] * dk1;
+        }
+        dk0 = dk1 = st = 0.f;
+      }
+    };
+
+    for (int q0 = 0; q0 < total; q0 += kWave) {
+      const int n = min(kWave, total - q0);
+      const int q = q0 + lane;
+      int ci = 0;
+      for (int cc = 0; cc < ncols; ++cc) ci += (readlane_i(incl, cc) <= q) ? 1 : 0;
+      const int pos = __builtin_amdgcn_ds_bpermute(min(ci, kWave - 1) << 2, offc) + q;
+      int rowq = 0;
+      float cf = 0.f, gsv = 0.f, gdsv = 0.f;
+      if (lane < n) {
+        const int eid = a.edges[pos];
+        cf = a.coef[eid];
+        rowq = eid / a.k;
+        if (first) {
+          gsv = a.g_score[eid];
+          if (a.gds) gdsv = a.gds[rowq];
+        }
+      }
+      for (int u0 = 0; u0 < n; u0 += G) {
+        int rw[G], cis[G];
+        float cu[G], gg[G], gd[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+          const bool ok = u0 + u < n;  // uniform
+          const int src = ok ? u0 + u : u0;
+          rw[u] = readlane_i(rowq, src);
+          cis[u] = readlane_i(ci, src);
+          cu[u] = ok ? readlane_f(cf, src) : 0.f;
+          gg[u] = ok ? readlane_f(gsv, src) : 0.f;
+          gd[u] = ok ? readlane_f(gdsv, src) : 0.f;
+        }
+        // rows are wave-uniform: one buffer resource per gathered row, lanes
+        // past the row end read zeros
+        float4 v[G][NV];
+        if (a.grad_pv) {
+#pragma unroll
+          for (int u = 0; u < G; ++u) {
+            const auto rs = make_rsrc(a.gdv + (int64_t)rw[u] * a.D, (uint32_t)a.D * 4u);
+#pragma unroll
+            for (int t = 0; t < NV; ++t) v[u][t] = buf_load_w<W>(rs, loff[t]);
           }
-        } else {
-          if (dl0 < a.D) out[dl0] = acc[0][0] + (a.accumulate_gpv ? out[dl0] : 0.f);
-          if (dl1 < a.D) out[dl1] = acc[1][0] + (a.accumulate_gpv ? out[dl1] : 0.f);
+        }
+        float qa[G], qb[G];
+        if (first) {
+#pragma unroll
+          for (int u = 0; u < G; ++u) {
+            const auto rs = make_rsrc(a.q + (int64_t)rw[u] * a.ldq, (uint32_t)a.r * 4u);
+            qa[u] = buf_load1(rs, 4u * lane);
+            qb[u] = a.r > kWave ? buf_load1(rs, 4u * (lane + kWave)) : 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+          if (u0 + u >= n) break;  // uniform
+          while (cur < cis[u]) flush(cur++);
+          if (a.grad_pv) {
+#pragma unroll
+            for (int t = 0; t < NV; ++t) fma4(acc[t], cu[u], v[u][t]);
+          }
+          if (first) {
+            dk0 += gg[u] * qa[u];
+            dk1 += gg[u] * qb[u];
+            st += cu[u] * gd[u];
+          }
         }
       }
     }
-    if (a.grad_ps) {
-      st = wave_sum(st);
-      if (lane == 0) a.grad_ps[colg] = st;
-    }
-    const float* kr = a.key + colg * a.ldk;
-    if (lane < a.r) {
-      a.dk[colg * a.lddk + lane] = dk0 * (a.kscale ? a.kscale[lane] : 1.f);
-      pc0 += kr[lane] * dk0;
-    }
-    if (lane + kWave < a.r) {
-      a.dk[colg * a.lddk + lane + kWave] = dk1 * (a.kscale ? a.kscale[lane + kWave] : 1.f);
-      pc1 += kr[lane + kWave] * dk1;
-    }
+    while (cur < ncols) flush(cur++);
   }
   if (lane < a.r) a.part_c[gw * a.r + lane] = pc0;
   if (lane + kWave < a.r) a.part_c[gw * a.r + lane + kWave] = pc1;
@@ -564,13 +653,17 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   const int64_t total_cols = (int64_t)a.B * a.Nk;
   if (total_cols == 0) return kOk;
   JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
+  JN_REQUIRE(a.cols_per_wave >= 1 && a.cols_per_wave <= kWave, kInvalidArgument, "columns per wave must be in [1, 64]");
+  JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
+  JN_REQUIRE((int64_t)a.D * 4 < (1LL << 31), kUnsupported, "value rows must stay below 2 GiB");
   const int waves = cols_backward_waves(total_cols, a.cols_per_wave);
   const int blocks = (waves + 3) / 4;
   const bool vec = (a.D % 4 == 0) && (a.ld_gpv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
                    (a.grad_pv == nullptr || (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0);
   JN_PROFILE("cols_backward_kernel", stream);
-  if (vec) hipLaunchKernelGGL(cols_backward_kernel<true>, dim3(blocks), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL(cols_backward_kernel<false>, dim3(blocks), dim3(256), 0, stream, a);
+  if (!vec) hipLaunchKernelGGL((cols_backward_kernel<1, 2>), dim3(blocks), dim3(256), 0, stream, a);
+  else if (a.D > 256) hipLaunchKernelGGL((cols_backward_kernel<4, 2>), dim3(blocks), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((cols_backward_kernel<4, 1>), dim3(blocks), dim3(256), 0, stream, a);
   JN_LAUNCH_CHECK();
   return kOk;
 }

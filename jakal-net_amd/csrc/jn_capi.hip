@@ -67,7 +67,7 @@ ProfileScope::~ProfileScope() {
 
 namespace {
 
-constexpr int kColsPerWave = 8;
+constexpr int kColsPerWave = 1;
 
 bool fits_int(int64_t v) { return v >= 0 && v < (1LL << 31); }
 
@@ -97,6 +97,7 @@ struct PropBwdScratch {
   int32_t* seg_start;
   int32_t* edges;
   float* part_c;
+  float* stage;
   float* splitk;
   size_t bytes;
 };
@@ -114,6 +115,7 @@ PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int
   s.seg_start = ws.take<int32_t>(B * (N + 1));
   s.edges = ws.take<int32_t>(M * k);
   s.part_c = ws.take<float>((size_t)cols_backward_waves(M, kColsPerWave) * r);
+  s.stage = ws.take<float>(finalize_stage_floats((int)r));
   s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)(2 * r), (int)Din, (int)M) / sizeof(float));
   s.bytes = ws.used;
   return s;
@@ -370,7 +372,7 @@ int jn_propagation_topk_backward(const float* layer_val, const float* projected_
 
   // 6. w_hat and bias grads
   const int nparts = cols_backward_waves(M, kColsPerWave);
-  return launch_finalize_small_grads(s.part_c, nparts, r, grad_core_weight, 0, s.rowsum, M, grad_bias, st);
+  return launch_finalize_small_grads(s.part_c, nparts, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st);
 }
 
 }  // extern "C"

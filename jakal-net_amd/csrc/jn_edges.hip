@@ -669,29 +669,58 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Final reduction of the small gradients (scale vector, bias); one workgroup,
-// fixed order.
+// Reduction of the small gradients (scale vector, bias) in two fixed-order
+// stages: kFinBlocks workgroups each reduce a contiguous share of the [nparts, r]
+// partials and of the row sums into stage[blk, 0..r]; then workgroup b <= r sums
+// column b of stage over the kFinBlocks rows.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void finalize_small_grads_kernel(const float* part_c, int nparts, int r,
-                                                                   float* grad_c, int accumulate_c,
-                                                                   const float* rowsum, int64_t nrows,
-                                                                   float* grad_bias) {
-  // block b < r sums column b of the [nparts, r] partials; block r sums the row sums
+constexpr int kFinBlocks = 256;
+
+size_t finalize_stage_floats(int r) { return (size_t)kFinBlocks * (r + 1); }
+
+__global__ __launch_bounds__(256) void finalize_partials_kernel(const float* part_c, int nparts, int r,
+                                                                const float* rowsum, int64_t nrows, float* stage) {
   __shared__ float red[256];
-  const int b = blockIdx.x;
+  const int t = threadIdx.x, blk = blockIdx.x;
+  // r_pad columns (power of two >= r, <= 128) x 256 / r_pad row lanes
+  int r_pad = 1;
+  while (r_pad < r) r_pad <<= 1;
+  const int col = t & (r_pad - 1), sub = t / r_pad, nsub = 256 / r_pad;
+  const int64_t p0 = (int64_t)nparts * blk / kFinBlocks, p1 = (int64_t)nparts * (blk + 1) / kFinBlocks;
   float s = 0.f;
-  if (b < r) {
-    for (int w = threadIdx.x; w < nparts; w += blockDim.x) s += part_c[(int64_t)w * r + b];
-  } else {
-    for (int64_t i = threadIdx.x; i < nrows; i += blockDim.x) s += rowsum[i];
-  }
-  red[threadIdx.x] = s;
+  if (col < r)
+    for (int64_t p = p0 + sub; p < p1; p += nsub) s += part_c[p * r + col];
+  red[t] = s;
   __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+  for (int o = 128; o >= r_pad; o >>= 1) {  // sum the row lanes of each column
+    if (t < o) red[t] += red[t + o];
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
+  if (t < r) stage[(int64_t)blk * (r + 1) + t] = red[t];
+  __syncthreads();
+  const int64_t i0 = nrows * blk / kFinBlocks, i1 = nrows * (blk + 1) / kFinBlocks;
+  float q = 0.f;
+  for (int64_t i = i0 + t; i < i1; i += 256) q += rowsum[i];
+  red[t] = q;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (t < o) red[t] += red[t + o];
+    __syncthreads();
+  }
+  if (t == 0) stage[(int64_t)blk * (r + 1) + r] = red[0];
+}
+
+__global__ __launch_bounds__(256) void finalize_small_grads_kernel(const float* stage, int r, float* grad_c,
+                                                                   int accumulate_c, float* grad_bias) {
+  __shared__ float red[256];
+  const int b = blockIdx.x, t = threadIdx.x;
+  red[t] = stage[(int64_t)t * (r + 1) + b];  // kFinBlocks == blockDim.x rows
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (t < o) red[t] += red[t + o];
+    __syncthreads();
+  }
+  if (t == 0) {
     if (b < r) {
       if (grad_c) grad_c[b] = accumulate_c ? grad_c[b] + red[0] : red[0];
     } else if (grad_bias) {
@@ -701,10 +730,19 @@ __global__ __launch_bounds__(256) void finalize_small_grads_kernel(const float* 
 }
 
 int launch_finalize_small_grads(const float* part_c, int nparts, int r, float* grad_c, int accumulate_c,
-                                const float* rowsum, int64_t nrows, float* grad_bias, hipStream_t stream) {
+                                const float* rowsum, int64_t nrows, float* grad_bias, float* stage,
+                                hipStream_t stream) {
+  JN_REQUIRE(r >= 1 && r <= 128, kUnsupported, "rank must be in [1, 128]");
+  static_assert(kFinBlocks == 256, "the second stage maps one thread per stage row");
+  {
+    JN_PROFILE("finalize_partials_kernel", stream);
+    hipLaunchKernelGGL(finalize_partials_kernel, dim3(kFinBlocks), dim3(256), 0, stream, part_c, nparts, r, rowsum,
+                       nrows, stage);
+    JN_LAUNCH_CHECK();
+  }
   JN_PROFILE("finalize_small_grads_kernel", stream);
-  hipLaunchKernelGGL(finalize_small_grads_kernel, dim3(r + 1), dim3(256), 0, stream, part_c, nparts, r, grad_c,
-                     accumulate_c, rowsum, nrows, grad_bias);
+  hipLaunchKernelGGL(finalize_small_grads_kernel, dim3(r + 1), dim3(256), 0, stream, stage, r, grad_c, accumulate_c,
+                     grad_bias);
   JN_LAUNCH_CHECK();
   return kOk;
 }

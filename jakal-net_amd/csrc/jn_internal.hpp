@@ -111,7 +111,9 @@ struct ColsBwdArgs {
 int cols_backward_waves(int64_t total_cols, int cols_per_wave);
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream);
 
+size_t finalize_stage_floats(int r);
 int launch_finalize_small_grads(const float* part_c, int nparts, int r, float* grad_c, int accumulate_c,
-                                const float* rowsum, int64_t nrows, float* grad_bias, hipStream_t stream);
+                                const float* rowsum, int64_t nrows, float* grad_bias, float* stage,
+                                hipStream_t stream);
 
 }  // namespace jakal

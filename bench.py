@@ -103,12 +103,30 @@ def cpu_baseline(B_sample: int = 1) -> dict:
     }
 
 
+COPY_BYTES = 1 << 30
+
+
+def calibrate_copy(torch) -> int:
+    """Five launches of a plain device-to-device copy of COPY_BYTES (read COPY_BYTES,
+    write COPY_BYTES); the per-dispatch FETCH_SIZE / WRITE_SIZE a profiler reads
+    for it scale those counters to bytes."""
+    src = torch.ones(COPY_BYTES // 4, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": COPY_BYTES, "copy_bytes_written": COPY_BYTES, "launches": 5}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain device copy of known size (scale for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
@@ -116,6 +134,9 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.calibrate_copy:
+        return calibrate_copy(torch)
 
     import jakal_net_native as jn
     from jakal_net import Layer, LowRankBilinearPairwise, SparsePropagation

@@ -168,6 +168,16 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (hardware id % 8).
+// Map the hardware id to a logical tile so that each XCD runs a contiguous
+// range of logical tiles (same batch element, same gathered rows) and they
+// share its L2.
+__device__ __forceinline__ int xcd_swizzle(int bid, int nblk) {
+  constexpr int kXcd = 8;
+  if (nblk % kXcd != 0) return bid;
+  return (bid % kXcd) * (nblk / kXcd) + bid / kXcd;
+}
+
 // Raw buffer resource over [base, base + bytes): a load at a byte offset past
 // `bytes` returns zeros, which masks lanes without a branch.  The base must be
 // wave-uniform; offsets are 32-bit (callers keep bytes < 2^31).

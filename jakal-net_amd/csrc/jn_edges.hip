@@ -89,7 +89,7 @@ __device__ __forceinline__ void row_coefficients(const int32_t* idx, const float
 template <int W>
 __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
   const int lane = lane_id();
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
   if (row >= a.rows) return;
   const int64_t b = row / a.Nq;
   const float* pvb = a.pv + b * a.Nk * a.ld_pv;
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
   constexpr int P = 16 * W * NV;  // D floats per pass of a 16-lane group
   const int lane = lane_id();
   const int g = lane >> 4, c = lane & 15;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
   if (row >= a.rows) return;
   const int64_t b = row / a.Nq;
   const float* psb = a.ps + b * a.Nk;
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
   constexpr int P = kWave * W * NV;  // D floats per pass
   constexpr int G = 8;               // edges per gather group
   const int lane = lane_id();
-  const int64_t gw = (int64_t)blockIdx.x * 4 + wave_id();
+  const int64_t gw = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
   const int64_t total_cols = (int64_t)a.B * a.Nk;
   const int64_t nwaves = (total_cols + a.cols_per_wave - 1) / a.cols_per_wave;
   if (gw >= nwaves) return;  // padding waves of the last workgroup own no partial slot

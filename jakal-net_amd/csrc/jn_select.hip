@@ -84,14 +84,6 @@ __device__ __forceinline__ void bitonic_sort64_desc(float& vs, int& vi) {
   }
 }
 
-// Map the hardware workgroup id to a logical tile so that consecutive logical
-// tiles (same batch element, same key set) run on the same XCD and share its L2.
-__device__ __forceinline__ int xcd_swizzle(int bid, int nblk) {
-  constexpr int kXcd = 8;
-  if (nblk % kXcd != 0) return bid;
-  return (bid % kXcd) * (nblk / kXcd) + bid / kXcd;
-}
-
 __device__ __forceinline__ int popc64(uint64_t m) { return __builtin_popcountll(m); }
 
 // Lanes whose id is below this lane, within mask m.

@@ -199,14 +199,26 @@ def main() -> int:
                              frac=round(achieved / FP32_MFMA_PEAK_TFLOPS, 4))
         kernels[name] = entry
 
+    # HBM-side bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    # of this same command (scaled by a copy kernel of known size), when present
+    measured = {}
+    traffic_file = ROOT / "profiles" / "c4_topk_hbm_traffic.json"
+    if traffic_file.exists():
+        measured = json.loads(traffic_file.read_text()).get("kernels", {})
+    for name, entry in kernels.items():
+        if name in measured:
+            entry["traffic_bytes"] = measured[name]["traffic_bytes"]
+            entry["traffic_GBps"] = round(measured[name]["traffic_bytes"] / (entry["avg_ms"] / 1e3) / 1e9, 1)
+
     modeled = [(n, e) for n, e in kernels.items() if "bound" in e]
     dom_name, dom = max(modeled, key=lambda ne: ne[1]["ms_per_step"])
     if dom["bound"] == "hbm":
         roofline = {"kernel": dom_name, "bound": "hbm", "achieved": dom["achieved_GBps"], "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": dom["frac"], "traffic": None}
+                    "unit": "GB/s", "frac": dom["frac"], "traffic": dom.get("traffic_bytes")}
     else:
         roofline = {"kernel": dom_name, "bound": "mfma", "achieved": dom["achieved_TFLOPs"],
-                    "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"], "traffic": None}
+                    "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
+                    "traffic": dom.get("traffic_bytes")}
 
     sparse_bytes = 3 * 4 * D * (E + B * N) + 24 * E + 3 * 4 * (E + B * N)
     result = {

@@ -102,6 +102,43 @@ int jn_propagation_topk_backward(const float* layer_val, const float* projected_
                                  float* grad_source_weight, float* grad_core_weight, float* grad_bias,
                                  void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
+/*
+ * SparsePropagation(sparse_type="window", LowRankBilinearPairwise) forward.
+ * Row i aggregates the sources j with i - window <= j <= i: its
+ * width = min(window + 1, nodes) edge slots hold j = i - (width - 1 - e) for
+ * slot e, index -1 (absent) where j < 0.  Arguments as
+ * jn_propagation_topk_forward; edge_index [B,N,width] (int32) and
+ * edge_score [B,N,width] receive the edge list for the backward.
+ * signed_abs_softmax (compress_kind 1) needs width <= 64.
+ * Replaces propagation_window (native/jakal_net_native.cpp:6190-6303) and
+ * low_rank_propagation_window_forward_cuda (native/jakal_net_native.cpp:268-288).
+ */
+int jn_propagation_window_forward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                  const float* target_weight, const float* source_weight, const float* core_weight,
+                                  const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                  int64_t rank, int64_t window, int32_t compress_kind, float* delta_state,
+                                  float* delta_val, float* projections, int32_t* edge_index, float* edge_score,
+                                  jn_stream_t stream);
+
+/* Workspace needed by jn_propagation_window_backward. */
+size_t jn_propagation_window_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                             int64_t rank, int64_t window);
+
+/*
+ * Backward of jn_propagation_window_forward; arguments as
+ * jn_propagation_topk_backward with the window edge list.
+ * Replaces _LowRankPropagationWindow.backward (src/jakal_net/native_backend.py:5143-5356).
+ */
+int jn_propagation_window_backward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                   const float* target_weight, const float* source_weight, const float* core_weight,
+                                   const float* projections, const int32_t* edge_index, const float* edge_score,
+                                   const float* grad_delta_state, const float* grad_delta_val, int64_t batch,
+                                   int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t window,
+                                   int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val,
+                                   float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
+                                   float* grad_source_weight, float* grad_core_weight, float* grad_bias,
+                                   void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,22 +71,33 @@ constexpr int kColsPerWave = 1;
 
 bool fits_int(int64_t v) { return v >= 0 && v < (1LL << 31); }
 
-int check_propagation_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
-                             int64_t topk, int32_t compress_kind) {
+// Shapes shared by every propagation entry point; `edges` = edge slots per row.
+int check_edge_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t edges,
+                      int32_t compress_kind) {
   JN_REQUIRE(batch >= 1 && nodes >= 1 && in_dim >= 1 && out_dim >= 1, kInvalidArgument,
              "batch, nodes and dims must be positive (B=%lld N=%lld Din=%lld Dout=%lld)", (long long)batch,
              (long long)nodes, (long long)in_dim, (long long)out_dim);
   JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
+  JN_REQUIRE(compress_kind == 0 || compress_kind == 1, kUnsupported,
+             "compress_kind must be 0 (softsign) or 1 (signed_abs_softmax), got %d", compress_kind);
+  JN_REQUIRE(compress_kind == 0 || edges <= 64, kUnsupported,
+             "signed_abs_softmax supports at most 64 edges per row (got %lld)", (long long)edges);
+  JN_REQUIRE(edges >= 1 && fits_int(batch * nodes) && fits_int(batch * nodes * edges) &&
+                 fits_int(nodes * 2 * rank) && fits_int(nodes * out_dim * 4),
+             kUnsupported, "problem too large for 32-bit edge ids and offsets");
+  return kOk;
+}
+
+int check_propagation_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                             int64_t topk, int32_t compress_kind) {
   JN_REQUIRE(topk >= 1 && topk <= kSelectMaxK, kUnsupported, "topk must be in [1, %d] (got %lld)", kSelectMaxK,
              (long long)topk);
   JN_REQUIRE(topk < nodes, kInvalidArgument, "topk (%lld) must be smaller than nodes (%lld); k == N is dense",
              (long long)topk, (long long)nodes);
-  JN_REQUIRE(compress_kind == 0 || compress_kind == 1, kUnsupported,
-             "compress_kind must be 0 (softsign) or 1 (signed_abs_softmax), got %d", compress_kind);
-  JN_REQUIRE(fits_int(batch * nodes) && fits_int(batch * nodes * topk) && fits_int(nodes * 2 * rank), kUnsupported,
-             "problem too large for 32-bit edge ids");
-  return kOk;
+  return check_edge_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
 }
+
+int64_t window_width(int64_t window, int64_t nodes) { return window + 1 < nodes ? window + 1 : nodes; }
 
 struct PropBwdScratch {
   float* dP;
@@ -119,6 +130,123 @@ PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int
   s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)(2 * r), (int)Din, (int)M) / sizeof(float));
   s.bytes = ws.used;
   return s;
+}
+
+// Backward of any edge-list propagation (top-k or window): the edge list
+// (edge_index, edge_score) [B*N, k] is what the forward aggregated.
+int propagation_edges_backward(const float* layer_val, const float* projected_state, const float* projected_val,
+                               const float* target_weight, const float* source_weight, const float* core_weight,
+                               const float* projections, const int32_t* topk_index, const float* topk_score,
+                               const float* grad_delta_state, const float* grad_delta_val, int64_t batch,
+                               int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t topk,
+                               int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val,
+                               float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
+                               float* grad_source_weight, float* grad_core_weight, float* grad_bias, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream) {
+  int rc;
+  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
+                 projections && topk_index && topk_score && grad_delta_state && grad_delta_val,
+             kInvalidArgument, "null tensor pointer");
+  JN_REQUIRE(!projected_val_is_layer_val || in_dim == out_dim, kInvalidArgument,
+             "projected_val_is_layer_val requires in_dim == out_dim");
+  PropBwdScratch s = carve_prop_bwd(workspace, workspace_bytes, batch, nodes, in_dim, rank, topk);
+  JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
+             "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
+  hipStream_t st = stream;
+  const int B = (int)batch, N = (int)nodes, r = (int)rank, k = (int)topk;
+  const int M = B * N;
+  const float* src_proj = projections + r;  // unscaled source projection, stride 2r
+
+  // 1. rows: edge-coefficient grads, compress backward, grad of target projection
+  RowsBwdArgs rb{};
+  rb.idx = topk_index;
+  rb.score = topk_score;
+  rb.k = k;
+  rb.compress = compress_kind;
+  rb.inv_temperature = 1.0f;
+  rb.ps = projected_state;
+  rb.pv = projected_val;
+  rb.ld_pv = out_dim;
+  rb.gds = grad_delta_state;
+  rb.gdv = grad_delta_val;
+  rb.key = src_proj;
+  rb.ldk = 2 * r;
+  rb.qscale = core_weight;
+  rb.r = r;
+  rb.Nq = N;
+  rb.Nk = N;
+  rb.D = (int)out_dim;
+  rb.rows = M;
+  rb.g_score = s.g_score;
+  rb.coef = s.coef;
+  rb.dq = s.dP;
+  rb.lddq = 2 * r;
+  rb.rowsum_gs = s.rowsum;
+  rc = launch_rows_backward(rb, st);
+  if (rc) return rc;
+
+  // 2. transpose the edge list to source-major order (deterministic)
+  CsrArgs ca{};
+  ca.idx = topk_index;
+  ca.k = k;
+  ca.B = B;
+  ca.Nq = N;
+  ca.Nk = N;
+  ca.tile_base = s.tile_base;
+  ca.seg_start = s.seg_start;
+  ca.edges = s.edges;
+  rc = launch_csr(ca, st);
+  if (rc) return rc;
+
+  // 3. columns: value/state grads of the sources, grad of source projection, w_hat grad partials
+  float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
+  ColsBwdArgs cb{};
+  cb.seg_start = s.seg_start;
+  cb.edges = s.edges;
+  cb.k = k;
+  cb.coef = s.coef;
+  cb.g_score = s.g_score;
+  cb.gds = grad_delta_state;
+  cb.gdv = grad_delta_val;
+  cb.q = projections;
+  cb.ldq = 2 * r;
+  cb.key = src_proj;
+  cb.ldk = 2 * r;
+  cb.kscale = core_weight;
+  cb.r = r;
+  cb.B = B;
+  cb.Nq = N;
+  cb.Nk = N;
+  cb.D = (int)out_dim;
+  cb.cols_per_wave = kColsPerWave;
+  cb.grad_pv = gpv;
+  cb.ld_gpv = out_dim;
+  cb.accumulate_gpv = 0;
+  cb.grad_ps = grad_projected_state;
+  cb.dk = s.dP + r;
+  cb.lddk = 2 * r;
+  cb.part_c = s.part_c;
+  rc = launch_cols_backward(cb, st);
+  if (rc) return rc;
+
+  // 4. projection weight grads: [dU; dV] = dP^T . X  (split-K, fixed order)
+  if (grad_target_weight && grad_source_weight) {
+    rc = gemm_grad_weight(s.dP, 2 * r, layer_val, in_dim, grad_target_weight, grad_source_weight, r, 2 * r,
+                          (int)in_dim, M, s.splitk, st);
+    if (rc) return rc;
+  }
+
+  // 5. grad of layer_val through both projections (+ value grad when pv is layer_val)
+  if (grad_layer_val) {
+    const float* addend = (projected_val_is_layer_val && gpv) ? grad_layer_val : nullptr;
+    rc = gemm_grad_input(s.dP, 2 * r, target_weight, source_weight, r, in_dim, addend, in_dim, grad_layer_val,
+                         in_dim, M, (int)in_dim, 2 * r, st);
+    if (rc) return rc;
+  }
+
+  // 6. w_hat and bias grads
+  const int nparts = cols_backward_waves(M, kColsPerWave);
+  return launch_finalize_small_grads(s.part_c, nparts, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st);
 }
 
 }  // namespace
@@ -268,111 +396,95 @@ int jn_propagation_topk_backward(const float* layer_val, const float* projected_
                                  float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
                                  float* grad_source_weight, float* grad_core_weight, float* grad_bias,
                                  void* workspace, size_t workspace_bytes, jn_stream_t stream) {
-  int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
+  const int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
+  if (rc) return rc;
+  return propagation_edges_backward(layer_val, projected_state, projected_val, target_weight, source_weight,
+                                    core_weight, projections, topk_index, topk_score, grad_delta_state,
+                                    grad_delta_val, batch, nodes, in_dim, out_dim, rank, topk, compress_kind,
+                                    projected_val_is_layer_val, grad_layer_val, grad_projected_state,
+                                    grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
+                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int jn_propagation_window_forward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                  const float* target_weight, const float* source_weight, const float* core_weight,
+                                  const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                  int64_t rank, int64_t window, int32_t compress_kind, float* delta_state,
+                                  float* delta_val, float* projections, int32_t* edge_index, float* edge_score,
+                                  jn_stream_t stream) {
+  JN_REQUIRE(window >= 0, kInvalidArgument, "window must be non-negative (got %lld)", (long long)window);
+  const int64_t width = window_width(window, nodes);
+  int rc = check_edge_shapes(batch, nodes, in_dim, out_dim, rank, width, compress_kind);
   if (rc) return rc;
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
-                 projections && topk_index && topk_score && grad_delta_state && grad_delta_val,
+                 delta_state && delta_val && projections && edge_index && edge_score,
              kInvalidArgument, "null tensor pointer");
-  JN_REQUIRE(!projected_val_is_layer_val || in_dim == out_dim, kInvalidArgument,
-             "projected_val_is_layer_val requires in_dim == out_dim");
-  PropBwdScratch s = carve_prop_bwd(workspace, workspace_bytes, batch, nodes, in_dim, rank, topk);
-  JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
-             "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int B = (int)batch, N = (int)nodes, r = (int)rank, k = (int)topk;
-  const int M = B * N;
-  const float* src_proj = projections + r;  // unscaled source projection, stride 2r
+  const int M = (int)(batch * nodes), r = (int)rank;
 
-  // 1. rows: edge-coefficient grads, compress backward, grad of target projection
-  RowsBwdArgs rb{};
-  rb.idx = topk_index;
-  rb.score = topk_score;
-  rb.k = k;
-  rb.compress = compress_kind;
-  rb.inv_temperature = 1.0f;
-  rb.ps = projected_state;
-  rb.pv = projected_val;
-  rb.ld_pv = out_dim;
-  rb.gds = grad_delta_state;
-  rb.gdv = grad_delta_val;
-  rb.key = src_proj;
-  rb.ldk = 2 * r;
-  rb.qscale = core_weight;
-  rb.r = r;
-  rb.Nq = N;
-  rb.Nk = N;
-  rb.D = (int)out_dim;
-  rb.rows = M;
-  rb.g_score = s.g_score;
-  rb.coef = s.coef;
-  rb.dq = s.dP;
-  rb.lddq = 2 * r;
-  rb.rowsum_gs = s.rowsum;
-  rc = launch_rows_backward(rb, st);
+  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, M, 2 * r,
+                    (int)in_dim, st);
   if (rc) return rc;
 
-  // 2. transpose the edge list to source-major order (deterministic)
-  CsrArgs ca{};
-  ca.idx = topk_index;
-  ca.k = k;
-  ca.B = B;
-  ca.Nq = N;
-  ca.Nk = N;
-  ca.tile_base = s.tile_base;
-  ca.seg_start = s.seg_start;
-  ca.edges = s.edges;
-  rc = launch_csr(ca, st);
+  WindowScoreArgs w{};
+  w.q = projections;
+  w.key = projections + r;
+  w.ldq = 2 * r;
+  w.ldk = 2 * r;
+  w.scale = core_weight;
+  w.bias = bias;
+  w.B = (int)batch;
+  w.N = (int)nodes;
+  w.r = r;
+  w.width = (int)width;
+  w.idx = edge_index;
+  w.score = edge_score;
+  rc = launch_window_scores(w, st);
   if (rc) return rc;
 
-  // 3. columns: value/state grads of the sources, grad of source projection, w_hat grad partials
-  float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
-  ColsBwdArgs cb{};
-  cb.seg_start = s.seg_start;
-  cb.edges = s.edges;
-  cb.k = k;
-  cb.coef = s.coef;
-  cb.g_score = s.g_score;
-  cb.gds = grad_delta_state;
-  cb.gdv = grad_delta_val;
-  cb.q = projections;
-  cb.ldq = 2 * r;
-  cb.key = src_proj;
-  cb.ldk = 2 * r;
-  cb.kscale = core_weight;
-  cb.r = r;
-  cb.B = B;
-  cb.Nq = N;
-  cb.Nk = N;
-  cb.D = (int)out_dim;
-  cb.cols_per_wave = kColsPerWave;
-  cb.grad_pv = gpv;
-  cb.ld_gpv = out_dim;
-  cb.accumulate_gpv = 0;
-  cb.grad_ps = grad_projected_state;
-  cb.dk = s.dP + r;
-  cb.lddk = 2 * r;
-  cb.part_c = s.part_c;
-  rc = launch_cols_backward(cb, st);
+  RowsFwdArgs f{};
+  f.idx = edge_index;
+  f.score = edge_score;
+  f.k = (int)width;
+  f.compress = compress_kind;
+  f.ps = projected_state;
+  f.pv = projected_val;
+  f.ld_pv = out_dim;
+  f.Nq = (int)nodes;
+  f.Nk = (int)nodes;
+  f.D = (int)out_dim;
+  f.rows = M;
+  f.out_state = delta_state;
+  f.out_val = delta_val;
+  return launch_rows_forward(f, st);
+}
+
+size_t jn_propagation_window_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                             int64_t rank, int64_t window) {
+  (void)out_dim;
+  if (window < 0 || nodes < 1) return 0;
+  return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank, window_width(window, nodes)).bytes;
+}
+
+int jn_propagation_window_backward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                   const float* target_weight, const float* source_weight, const float* core_weight,
+                                   const float* projections, const int32_t* edge_index, const float* edge_score,
+                                   const float* grad_delta_state, const float* grad_delta_val, int64_t batch,
+                                   int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t window,
+                                   int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val,
+                                   float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
+                                   float* grad_source_weight, float* grad_core_weight, float* grad_bias,
+                                   void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  JN_REQUIRE(window >= 0, kInvalidArgument, "window must be non-negative (got %lld)", (long long)window);
+  const int64_t width = window_width(window, nodes);
+  const int rc = check_edge_shapes(batch, nodes, in_dim, out_dim, rank, width, compress_kind);
   if (rc) return rc;
-
-  // 4. projection weight grads: [dU; dV] = dP^T . X  (split-K, fixed order)
-  if (grad_target_weight && grad_source_weight) {
-    rc = gemm_grad_weight(s.dP, 2 * r, layer_val, in_dim, grad_target_weight, grad_source_weight, r, 2 * r,
-                          (int)in_dim, M, s.splitk, st);
-    if (rc) return rc;
-  }
-
-  // 5. grad of layer_val through both projections (+ value grad when pv is layer_val)
-  if (grad_layer_val) {
-    const float* addend = (projected_val_is_layer_val && gpv) ? grad_layer_val : nullptr;
-    rc = gemm_grad_input(s.dP, 2 * r, target_weight, source_weight, r, in_dim, addend, in_dim, grad_layer_val,
-                         in_dim, M, (int)in_dim, 2 * r, st);
-    if (rc) return rc;
-  }
-
-  // 6. w_hat and bias grads
-  const int nparts = cols_backward_waves(M, kColsPerWave);
-  return launch_finalize_small_grads(s.part_c, nparts, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st);
+  return propagation_edges_backward(layer_val, projected_state, projected_val, target_weight, source_weight,
+                                    core_weight, projections, edge_index, edge_score, grad_delta_state,
+                                    grad_delta_val, batch, nodes, in_dim, out_dim, rank, width, compress_kind,
+                                    projected_val_is_layer_val, grad_layer_val, grad_projected_state,
+                                    grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
+                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

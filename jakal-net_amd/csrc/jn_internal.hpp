@@ -73,6 +73,18 @@ struct RowsBwdArgs {
 };
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream);
 
+struct WindowScoreArgs {
+  const float* q;      // query projection rows (global row index), stride ldq
+  const float* key;    // key projection rows (global row index), stride ldk
+  int64_t ldq, ldk;
+  const float* scale;  // [r] applied to the query (null = 1)
+  const float* bias;   // scalar or null
+  int B, N, r, width;
+  int32_t* idx;        // [B*N, width]
+  float* score;        // [B*N, width]
+};
+int launch_window_scores(const WindowScoreArgs& a, hipStream_t stream);
+
 struct CsrArgs {
   const int32_t* idx;
   int k;

@@ -61,6 +61,16 @@ _declare(
     [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
      _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
+_declare(
+    "jn_propagation_window_forward",
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P],
+)
+_declare("jn_propagation_window_workspace_bytes", [_I64, _I64, _I64, _I64, _I64, _I64], _SZ)
+_declare(
+    "jn_propagation_window_backward",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
+     _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
 
 ABI_VERSION = int(_LIB.jn_abi_version())
 
@@ -69,6 +79,7 @@ MAX_TOPK = 32
 
 _SUPPORTED_OPS = (
     "propagation_topk",
+    "propagation_window",
     "low_rank_topk_select",
 )
 
@@ -148,23 +159,39 @@ def _same_storage_view(a: Tensor, b: Tensor) -> bool:
 
 
 # ---------------------------------------------------------------------------
-# top-k propagation
+# edge-list propagation (top-k and window)
 # ---------------------------------------------------------------------------
-class _PropagationTopK(torch.autograd.Function):
-    """Differentiable top-k low-rank propagation on the HIP library.
+_EDGE_OPS = {
+    # mode: (forward, workspace_bytes, backward)
+    "topk": ("jn_propagation_topk_forward", "jn_propagation_topk_workspace_bytes", "jn_propagation_topk_backward"),
+    "window": ("jn_propagation_window_forward", "jn_propagation_window_workspace_bytes",
+               "jn_propagation_window_backward"),
+}
 
-    Inputs (all fp32, contiguous): layer_val X [B,N,Din], projected_state
-    [B,N], projected_val [B,N,Dout] or None when it is X itself, V and U
-    [r,Din], w_hat [r], bias [] or None."""
+
+def _edges_per_row(mode: str, param: int, N: int) -> int:
+    return param if mode == "topk" else min(param + 1, N)
+
+
+class _PropagationEdges(torch.autograd.Function):
+    """Differentiable low-rank propagation over an edge list on the HIP library.
+
+    mode "topk" (param = k) selects each row's k best sources; mode "window"
+    (param = window) takes the causal band j in [i - window, i].  Inputs (all
+    fp32, contiguous): layer_val X [B,N,Din], projected_state [B,N],
+    projected_val [B,N,Dout] or None when it is X itself, V and U [r,Din],
+    w_hat [r], bias [] or None."""
 
     @staticmethod
-    def forward(ctx, X, ps, pv, V, U, w_hat, bias, k: int, compress: int):  # noqa: N803
+    def forward(ctx, X, ps, pv, V, U, w_hat, bias, mode: str, param: int, compress: int):  # noqa: N803
         B, N, Din = X.shape
         pv_is_x = pv is None
         pv_t = X if pv_is_x else pv
         Dout = pv_t.shape[-1]
         r = U.shape[0]
+        k = _edges_per_row(mode, param, N)
         dev = X.device
+        fwd = getattr(_LIB, _EDGE_OPS[mode][0])
         with torch.cuda.device(dev):
             ds = torch.empty(B, N, device=dev, dtype=torch.float32)
             dv = torch.empty(B, N, Dout, device=dev, dtype=torch.float32)
@@ -172,21 +199,22 @@ class _PropagationTopK(torch.autograd.Function):
             idx = torch.empty(B, N, k, device=dev, dtype=torch.int32)
             score = torch.empty(B, N, k, device=dev, dtype=torch.float32)
             _check(
-                _LIB.jn_propagation_topk_forward(
+                fwd(
                     _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
-                    B, N, Din, Dout, r, k, compress,
+                    B, N, Din, Dout, r, param, compress,
                     _ptr(ds), _ptr(dv), _ptr(proj), _ptr(idx), _ptr(score), _stream(dev),
                 )
             )
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, idx, score)
-        ctx.meta = (k, compress, pv_is_x, bias is not None)
+        ctx.meta = (mode, param, compress, pv_is_x, bias is not None)
         ctx.mark_non_differentiable(idx, score)
         return ds, dv, idx, score
 
     @staticmethod
     def backward(ctx, g_ds, g_dv, _g_idx=None, _g_score=None):
         X, ps, pv, V, U, w_hat, proj, idx, score = ctx.saved_tensors
-        k, compress, pv_is_x, has_bias = ctx.meta
+        mode, param, compress, pv_is_x, has_bias = ctx.meta
+        _, ws_name, bwd_name = _EDGE_OPS[mode]
         B, N, Din = X.shape
         Dout = pv.shape[-1]
         r = U.shape[0]
@@ -195,20 +223,20 @@ class _PropagationTopK(torch.autograd.Function):
         with torch.cuda.device(dev):
             g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
             g_dv = torch.zeros(B, N, Dout, device=dev) if g_dv is None else g_dv.float().contiguous()
-            gX = torch.empty_like(X) if (need[0] or (pv_is_x and need[0])) else None
+            gX = torch.empty_like(X) if need[0] else None
             gps = torch.empty_like(ps) if need[1] else None
             gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
             gV = torch.empty_like(V)
             gU = torch.empty_like(U)
             gw = torch.empty_like(w_hat)
             gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
-            ws_bytes = int(_LIB.jn_propagation_topk_workspace_bytes(B, N, Din, Dout, r, k))
+            ws_bytes = int(getattr(_LIB, ws_name)(B, N, Din, Dout, r, param))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
             _check(
-                _LIB.jn_propagation_topk_backward(
+                getattr(_LIB, bwd_name)(
                     _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat),
                     _ptr(proj), _ptr(idx), _ptr(score), _ptr(g_ds), _ptr(g_dv),
-                    B, N, Din, Dout, r, k, compress, 1 if pv_is_x else 0,
+                    B, N, Din, Dout, r, param, compress, 1 if pv_is_x else 0,
                     _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
                     _ptr(ws), ws_bytes, _stream(dev),
                 )
@@ -223,6 +251,7 @@ class _PropagationTopK(torch.autograd.Function):
             gb if (has_bias and need[6]) else None,
             None,
             None,
+            None,
         )
 
 
@@ -234,6 +263,34 @@ def _lowrank_pairwise_args(kind, weight, bias, in_weight, in_bias, out_weight, o
     if in_bias is not None or out_bias is not None:
         raise TypeError("low_rank_bilinear projections carry no bias.")
     return weight, bias, in_weight, out_weight
+
+
+def _propagation_edges(mode, pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
+                       edge_compress_name, layer_val, projected_state, projected_val, param, target_block_size,
+                       source_block_size):
+    w_hat, bias, V, U = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias)
+    if edge_compress_name not in _COMPRESS_KINDS:
+        raise RuntimeError(f"Unsupported edge_compress_name for the HIP backend: {edge_compress_name!r}.")
+    if target_block_size <= 0 or source_block_size <= 0:
+        raise RuntimeError("block sizes must be positive.")
+    _require_gpu(layer_val, projected_state, projected_val, w_hat, V, U, bias)
+    batch_shape = tuple(layer_val.shape[:-2])
+    N, Din = layer_val.shape[-2], layer_val.shape[-1]
+    Dout = projected_val.shape[-1]
+    pv_is_x = _same_storage_view(projected_val, layer_val)
+    X = _f32(layer_val.reshape(-1, N, Din))
+    ps = _f32(projected_state.reshape(-1, N))
+    pv = None if pv_is_x else _f32(projected_val.reshape(-1, N, Dout))
+    ds, dv, idx, score = _PropagationEdges.apply(
+        X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias), mode, int(param), _COMPRESS_KINDS[edge_compress_name]
+    )
+    k = idx.shape[-1]
+    return (
+        ds.reshape(*batch_shape, N).to(projected_state.dtype),
+        dv.reshape(*batch_shape, N, Dout).to(projected_val.dtype),
+        idx.reshape(*batch_shape, N, k),
+        score.reshape(*batch_shape, N, k),
+    )
 
 
 def propagation_topk_selection(
@@ -251,40 +308,75 @@ def propagation_topk_selection(
     topk: int,
     target_block_size: int,
     source_block_size: int,
-) -> tuple[Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Top-k propagation returning (delta_state, delta_val, topk_index, topk_score).
 
     Same arguments as ``propagation_topk``; the selection (int32 source
     indices and their scores, best first) is what the forward aggregated."""
-    w_hat, bias, V, U = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias)
-    if edge_compress_name not in _COMPRESS_KINDS:
-        raise RuntimeError(f"Unsupported edge_compress_name for the HIP backend: {edge_compress_name!r}.")
     if topk <= 0:
         raise RuntimeError("topk must be positive.")
-    if target_block_size <= 0 or source_block_size <= 0:
-        raise RuntimeError("block sizes must be positive.")
-    _require_gpu(layer_val, projected_state, projected_val, w_hat, V, U, bias)
-    batch_shape = tuple(layer_val.shape[:-2])
-    N, Din = layer_val.shape[-2], layer_val.shape[-1]
-    Dout = projected_val.shape[-1]
+    N = layer_val.shape[-2]
     k = min(int(topk), N)
     if k == N:
         raise NotImplementedError("top-k with k == N is dense propagation; dense native op not available.")
     if k > MAX_TOPK:
         raise NotImplementedError(f"HIP top-k propagation supports k <= {MAX_TOPK} (got {k}).")
-    pv_is_x = _same_storage_view(projected_val, layer_val)
-    X = _f32(layer_val.reshape(-1, N, Din))
-    ps = _f32(projected_state.reshape(-1, N))
-    pv = None if pv_is_x else _f32(projected_val.reshape(-1, N, Dout))
-    ds, dv, idx, score = _PropagationTopK.apply(
-        X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias), k, _COMPRESS_KINDS[edge_compress_name]
+    return _propagation_edges("topk", pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
+                              edge_compress_name, layer_val, projected_state, projected_val, k, target_block_size,
+                              source_block_size)
+
+
+def propagation_window_edges(
+    pairwise_kind: str,
+    weight: Tensor,
+    bias: Tensor | None,
+    in_weight: Tensor | None,
+    in_bias: Tensor | None,
+    out_weight: Tensor | None,
+    out_bias: Tensor | None,
+    edge_compress_name: str,
+    layer_val: Tensor,
+    projected_state: Tensor,
+    projected_val: Tensor,
+    window: int,
+    target_block_size: int,
+    source_block_size: int,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Window propagation returning (delta_state, delta_val, edge_index, edge_score).
+
+    Row i's slots e < min(window + 1, N) hold source i - (width - 1 - e)
+    (index -1 where that is negative) and its score."""
+    if window < 0:
+        raise RuntimeError("window must be non-negative.")
+    if edge_compress_name == "signed_abs_softmax" and min(int(window) + 1, layer_val.shape[-2]) > 64:
+        raise NotImplementedError("HIP window propagation with signed_abs_softmax supports window <= 63.")
+    return _propagation_edges("window", pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
+                              edge_compress_name, layer_val, projected_state, projected_val, int(window),
+                              target_block_size, source_block_size)
+
+
+def propagation_window(
+    pairwise_kind: str,
+    weight: Tensor,
+    bias: Tensor | None,
+    in_weight: Tensor | None,
+    in_bias: Tensor | None,
+    out_weight: Tensor | None,
+    out_bias: Tensor | None,
+    edge_compress_name: str,
+    layer_val: Tensor,
+    projected_state: Tensor,
+    projected_val: Tensor,
+    window: int,
+    target_block_size: int,
+    source_block_size: int,
+) -> tuple[Tensor, Tensor]:
+    """Causal-window propagation; signature of jakal_net_native.cpp:6190-6204."""
+    ds, dv, _, _ = propagation_window_edges(
+        pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias, edge_compress_name, layer_val,
+        projected_state, projected_val, window, target_block_size, source_block_size,
     )
-    return (
-        ds.reshape(*batch_shape, N).to(projected_state.dtype),
-        dv.reshape(*batch_shape, N, Dout).to(projected_val.dtype),
-        idx.reshape(*batch_shape, N, k),
-        score.reshape(*batch_shape, N, k),
-    )
+    return ds, dv
 
 
 def propagation_topk(

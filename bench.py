@@ -1,20 +1,28 @@
 """Benchmark of the native hot path on one MI355X.
 
-Workload (top-k variant): SparsePropagation top-k with
-LowRankBilinearPairwise, B=16, N=4096, D=512, r=64, k=32, fp32, val rows
-unit-norm, state ~ N(0,1), default module init; one step = forward + backward
-of loss = sum(delta_state) + sum(delta_val) through the jakal_net API with
-implementation="native".  Inputs and parameters are resident in HBM before
-the timed region.
+Default workload (top-k variant, the headline metric):
+SparsePropagation top-k with LowRankBilinearPairwise, B=16, N=4096, D=512,
+r=64, k=32, fp32, val rows unit-norm, state ~ N(0,1), default module init; one
+step = forward + backward of loss = sum(delta_state) + sum(delta_val) through
+the jakal_net API with implementation="native".
+
+Other workloads (--workload), one per hot-path row, same output format:
+  c2-window   BASELINE config 2: window propagation, B=8, T=1024, D=384, r=32,
+              window 64, val and state ~ N(0,1), default init.
+
+Inputs and parameters are resident in HBM before the timed region.
 
 Prints one JSON line:
-  value       routed pairs per second (E = B*N*k pairs per step / step time)
-  roofline    dominant kernel: algorithmic bytes (or flops) per launch / its
-              average duration, measured with HIP events inside the timed region
-  kernels     the same figures for every kernel of the step
+  value        routed pairs per second (edges aggregated per step / step time)
+  roofline     dominant kernel: algorithmic bytes (or flops) per launch / its
+               average duration, measured with HIP events inside the timed
+               region; `traffic` = HBM-side bytes per launch measured by
+               rocprofv3 FETCH_SIZE/WRITE_SIZE passes of this command
+  kernels      the same figures for every kernel of the step
   cpu_baseline the numpy oracle (fp32) timed on a bounded sample on the host
 
-  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload c4-topk] [--no-cpu-baseline]
+  python bench.py --calibrate-copy     # plain 1 GiB device copy (counter scale)
 """
 
 from __future__ import annotations
@@ -33,17 +41,16 @@ sys.path.insert(0, str(ROOT / "jakal-net_amd"))
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
+# the headline workload (kept as module constants: the profile summaries use them)
 CONFIG = {"batch": 16, "nodes": 4096, "dim": 512, "rank": 64, "topk": 32}
 
 
-def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int) -> tuple[str, float] | None:
-    """(bound, algorithmic bytes or flops per launch) for the kernels of one step.
+def edge_kernel_model(name: str, M: int, E: int, D: int, r: int) -> tuple[str, float] | None:
+    """(bound, algorithmic bytes or flops per launch) of the edge-list kernels.
 
-    Bytes count every operand once per use (no cache reuse credited): an edge
-    (routed pair) gathers one D-row of fp32 values, its index and score."""
-    M, E = B * N, B * N * k
-    if name.startswith("lowrank_topk_select_kernel"):
-        return "mfma", 2.0 * B * N * N * r
+    M = aggregated rows, E = routed pairs.  Bytes count every operand once per
+    use (no cache reuse credited): an edge gathers one D-row of fp32 values,
+    its index and score."""
     if name.startswith("rows_forward_kernel"):
         # idx+score+ps per edge, pv row per edge; delta_val row + delta_state per row
         return "hbm", E * (12.0 + 4.0 * D) + M * (4.0 * D + 4.0)
@@ -55,53 +62,180 @@ def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int) -> tuple[str
         # edge id, coef+gsc, grad-delta row + state, query row per edge;
         # segment bounds, grad_pv row, grad_ps, dk row, key row per column
         return "hbm", E * (4.0 + 8.0 + 4.0 * D + 4.0 + 4.0 * r) + M * (8.0 + 4.0 * D + 4.0 + 8.0 * r)
+    if name.startswith("window_scores_kernel"):
+        # query row per row; key row per edge; idx + score written per edge
+        return "hbm", E * (4.0 * r + 8.0) + M * 4.0 * r
     if name.startswith("gemm_f32_kernel"):
         return "mfma", 2.0 * M * D * 2 * r
     return None
 
 
-def cpu_baseline(B_sample: int = 1) -> dict:
-    """Oracle (numpy, fp32) forward+backward on B_sample batch elements of the workload."""
-    import numpy as np
+def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int) -> tuple[str, float] | None:
+    """Kernel model of the headline (top-k) workload."""
+    if name.startswith("lowrank_topk_select_kernel"):
+        return "mfma", 2.0 * B * N * N * r
+    return edge_kernel_model(name, B * N, B * N * k, D, r)
 
-    sys.path.insert(0, str(ROOT / "oracle"))
-    import jakal_oracle as O
 
-    N, D, r, k = CONFIG["nodes"], CONFIG["dim"], CONFIG["rank"], CONFIG["topk"]
-    rng = np.random.default_rng(1004)
-    val = rng.standard_normal((B_sample, N, D)).astype(np.float32)
-    val /= np.linalg.norm(val, axis=-1, keepdims=True)
-    state = rng.standard_normal((B_sample, N)).astype(np.float32)
-    bound = 1.0 / math.sqrt(D)
-    U = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
-    V = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
-    w = np.ones(r, dtype=np.float32)
-    g_ds = np.ones((B_sample, N), np.float32)
-    g_dv = np.ones((B_sample, N, D), np.float32)
-    threads = None
+def _threads() -> int | None:
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max((i.get("num_threads") or 0) for i in threadpool_info()) or None
+        return max((i.get("num_threads") or 0) for i in threadpool_info()) or None
     except Exception:  # noqa: BLE001
-        pass
-    times = []
-    with O.compute_dtype(np.float32):
-        for rep in range(3):
-            t0 = time.perf_counter()
-            O.propagation_forward(val, state, val, U, V, w, 0.0, mode="topk", topk=k)
-            O.propagation_backward(val, state, val, U, V, w, 0.0, g_ds, g_dv, mode="topk", topk=k)
-            times.append(time.perf_counter() - t0)
-    t = sorted(times)[len(times) // 2]
-    return {
-        "value": B_sample * N * k / t,
-        "unit": "routed pairs/s",
-        "cores": threads or os.cpu_count(),
-        "kind": "port",
-        "sample": f"numpy oracle fp32, forward+backward, {B_sample} of {CONFIG['batch']} batch elements "
-                  f"(N={N}, D={D}, r={r}, k={k}), median of 3 ({t:.2f} s each)",
-    }
+        return None
 
+
+def _oracle():
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import jakal_oracle
+
+    return jakal_oracle
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+class TopkC4:
+    name = "c4-topk"
+    metric = "routed pairs/sec + HBM GB/s (% peak), SparsePropagation N=4096 D=512 k=32 fwd+bwd"
+    workload = "C4-topk SparsePropagation fwd+bwd, LowRankBilinearPairwise, native"
+    data = "synthetic (seeded N(0,1) state, unit-norm N(0,1) val rows, default module init)"
+    config = CONFIG
+    traffic_file = "c4_topk_hbm_traffic.json"
+
+    def edges(self) -> int:
+        c = self.config
+        return c["batch"] * c["nodes"] * c["topk"]
+
+    def model(self, name):
+        c = self.config
+        return kernel_model(name, c["batch"], c["nodes"], c["dim"], c["rank"], c["topk"])
+
+    def sparse_bytes(self) -> float:
+        # hot-path algorithmic bytes per fwd+bwd (gathers, scatters, edge records, state)
+        c = self.config
+        E, M, D = self.edges(), c["batch"] * c["nodes"], c["dim"]
+        return 3 * 4 * D * (E + M) + 24 * E + 3 * 4 * (E + M)
+
+    def build(self, torch, dev):
+        from jakal_net import Layer, LowRankBilinearPairwise, SparsePropagation
+
+        B, N, D, r, k = (self.config[x] for x in ("batch", "nodes", "dim", "rank", "topk"))
+        g = torch.Generator().manual_seed(1004)
+        state = torch.randn(B, N, generator=g)
+        val = torch.randn(B, N, D, generator=g)
+        val = val / val.norm(dim=-1, keepdim=True)
+        torch.manual_seed(1004)
+        op = SparsePropagation(LowRankBilinearPairwise(D, r), sparse_type="topk", topk=k,
+                               implementation="native").to(dev)
+        return op, Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True),
+                         val=val.to(dev).requires_grad_(True))
+
+    def cpu_baseline(self, B_sample: int = 1) -> dict:
+        """Oracle (numpy, fp32) forward+backward on B_sample batch elements."""
+        import numpy as np
+
+        O = _oracle()
+        N, D, r, k = (self.config[x] for x in ("nodes", "dim", "rank", "topk"))
+        rng = np.random.default_rng(1004)
+        val = rng.standard_normal((B_sample, N, D)).astype(np.float32)
+        val /= np.linalg.norm(val, axis=-1, keepdims=True)
+        state = rng.standard_normal((B_sample, N)).astype(np.float32)
+        bound = 1.0 / math.sqrt(D)
+        U = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
+        V = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
+        w = np.ones(r, dtype=np.float32)
+        g_ds = np.ones((B_sample, N), np.float32)
+        g_dv = np.ones((B_sample, N, D), np.float32)
+        times = []
+        with O.compute_dtype(np.float32):
+            for _ in range(3):
+                t0 = time.perf_counter()
+                O.propagation_forward(val, state, val, U, V, w, 0.0, mode="topk", topk=k)
+                O.propagation_backward(val, state, val, U, V, w, 0.0, g_ds, g_dv, mode="topk", topk=k)
+                times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2]
+        return {
+            "value": B_sample * N * k / t,
+            "unit": "routed pairs/s",
+            "cores": _threads() or os.cpu_count(),
+            "kind": "port",
+            "sample": f"numpy oracle fp32, forward+backward, {B_sample} of {self.config['batch']} batch elements "
+                      f"(N={N}, D={D}, r={r}, k={k}), median of 3 ({t:.2f} s each)",
+        }
+
+
+class WindowC2:
+    name = "c2-window"
+    metric = "routed pairs/sec + HBM GB/s (% peak), SparsePropagation window T=1024 D=384 w=64 fwd+bwd"
+    workload = "C2-window SparsePropagation fwd+bwd, LowRankBilinearPairwise, native"
+    data = "synthetic (seeded N(0,1) state and val, default module init)"
+    config = {"batch": 8, "nodes": 1024, "dim": 384, "rank": 32, "window": 64}
+    traffic_file = "c2_window_hbm_traffic.json"
+
+    def edges(self) -> int:
+        c = self.config
+        width = min(c["window"] + 1, c["nodes"])
+        return c["batch"] * sum(min(i + 1, width) for i in range(c["nodes"]))
+
+    def model(self, name):
+        c = self.config
+        return edge_kernel_model(name, c["batch"] * c["nodes"], self.edges(), c["dim"], c["rank"])
+
+    def sparse_bytes(self) -> float:
+        # contiguous bands: compulsory dense bytes (read val, write delta; bwd read grad, read val, write grad)
+        c = self.config
+        return 5 * 4 * c["batch"] * c["nodes"] * c["dim"]
+
+    def build(self, torch, dev):
+        from jakal_net import Layer, LowRankBilinearPairwise, SparsePropagation
+
+        B, N, D, r, w = (self.config[x] for x in ("batch", "nodes", "dim", "rank", "window"))
+        g = torch.Generator().manual_seed(1002)
+        state = torch.randn(B, N, generator=g)
+        val = torch.randn(B, N, D, generator=g)
+        torch.manual_seed(1002)
+        op = SparsePropagation(LowRankBilinearPairwise(D, r), sparse_type="window", window=w,
+                               implementation="native").to(dev)
+        return op, Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True),
+                         val=val.to(dev).requires_grad_(True))
+
+    def cpu_baseline(self, B_sample: int = 2) -> dict:
+        """Oracle (numpy, fp32) forward+backward on B_sample batch elements."""
+        import numpy as np
+
+        O = _oracle()
+        N, D, r, w = (self.config[x] for x in ("nodes", "dim", "rank", "window"))
+        rng = np.random.default_rng(1002)
+        val = rng.standard_normal((B_sample, N, D)).astype(np.float32)
+        state = rng.standard_normal((B_sample, N)).astype(np.float32)
+        bound = 1.0 / math.sqrt(D)
+        U = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
+        V = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
+        wv = np.ones(r, dtype=np.float32)
+        g_ds = np.ones((B_sample, N), np.float32)
+        g_dv = np.ones((B_sample, N, D), np.float32)
+        times = []
+        with O.compute_dtype(np.float32):
+            for _ in range(3):
+                t0 = time.perf_counter()
+                O.propagation_forward(val, state, val, U, V, wv, 0.0, mode="window", window=w)
+                O.propagation_backward(val, state, val, U, V, wv, 0.0, g_ds, g_dv, mode="window", window=w)
+                times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2]
+        pairs = self.edges() // self.config["batch"] * B_sample
+        return {
+            "value": pairs / t,
+            "unit": "routed pairs/s",
+            "cores": _threads() or os.cpu_count(),
+            "kind": "port",
+            "sample": f"numpy oracle fp32, forward+backward, {B_sample} of {self.config['batch']} batch elements "
+                      f"(T={N}, D={D}, r={r}, window={w}), median of 3 ({t:.2f} s each)",
+        }
+
+
+WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2())}
 
 COPY_BYTES = 1 << 30
 
@@ -124,6 +258,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c4-topk")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of known size (scale for HBM byte counters)")
@@ -139,19 +274,12 @@ def main() -> int:
         return calibrate_copy(torch)
 
     import jakal_net_native as jn
-    from jakal_net import Layer, LowRankBilinearPairwise, SparsePropagation
 
+    wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
-    B, N, D, r, k = CONFIG["batch"], CONFIG["nodes"], CONFIG["dim"], CONFIG["rank"], CONFIG["topk"]
-    g = torch.Generator().manual_seed(1004)
-    state = torch.randn(B, N, generator=g)
-    val = torch.randn(B, N, D, generator=g)
-    val = val / val.norm(dim=-1, keepdim=True)
-    torch.manual_seed(1004)
-    op = SparsePropagation(LowRankBilinearPairwise(D, r), sparse_type="topk", topk=k, implementation="native").to(dev)
-    layer = Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True), val=val.to(dev).requires_grad_(True))
-    ones_s = torch.ones(B, N, device=dev)
-    ones_v = torch.ones(B, N, D, device=dev)
+    op, layer = wl.build(torch, dev)
+    ones_s = torch.ones_like(layer.state)
+    ones_v = torch.ones_like(layer.val)
 
     def step() -> None:
         op.zero_grad(set_to_none=True)
@@ -178,7 +306,7 @@ def main() -> int:
     jn.profile_enable(False)
 
     ms_per_step = start.elapsed_time(stop) / args.steps
-    E = B * N * k
+    E = wl.edges()
     value = E / (ms_per_step / 1e3)
 
     kernels = {}
@@ -186,7 +314,7 @@ def main() -> int:
         avg_ms = total_ms / count
         entry = {"launches_per_step": count / args.steps, "avg_ms": round(avg_ms, 5),
                  "ms_per_step": round(total_ms / args.steps, 5)}
-        model = kernel_model(name, B, N, D, r, k)
+        model = wl.model(name)
         if model is not None:
             bound, work = model
             if bound == "hbm":
@@ -202,7 +330,7 @@ def main() -> int:
     # HBM-side bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes
     # of this same command (scaled by a copy kernel of known size), when present
     measured = {}
-    traffic_file = ROOT / "profiles" / "c4_topk_hbm_traffic.json"
+    traffic_file = ROOT / "profiles" / wl.traffic_file
     if traffic_file.exists():
         measured = json.loads(traffic_file.read_text()).get("kernels", {})
     for name, entry in kernels.items():
@@ -220,9 +348,8 @@ def main() -> int:
                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
                     "traffic": dom.get("traffic_bytes")}
 
-    sparse_bytes = 3 * 4 * D * (E + B * N) + 24 * E + 3 * 4 * (E + B * N)
     result = {
-        "metric": "routed pairs/sec + HBM GB/s (% peak), SparsePropagation N=4096 D=512 k=32 fwd+bwd",
+        "metric": wl.metric,
         "value": value,
         "unit": "routed pairs/s",
         "n_gpus": 1,
@@ -233,18 +360,15 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded N(0,1) state, unit-norm N(0,1) val rows, default module init)",
-        "config": {"workload": "C4-topk SparsePropagation fwd+bwd, LowRankBilinearPairwise, native", **CONFIG},
-        "sparse_phase_GBps": round(sparse_bytes / (ms_per_step / 1e3) / 1e9, 1),
+        "data": wl.data,
+        "config": {"workload": wl.workload, **wl.config},
+        "sparse_phase_GBps": round(wl.sparse_bytes() / (ms_per_step / 1e3) / 1e9, 1),
         "roofline": roofline,
         "kernels": kernels,
         "wall_s_timed": round(wall, 3),
         "device": torch.cuda.get_device_name(0),
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline()
-    else:
-        result["cpu_baseline"] = None
+    result["cpu_baseline"] = None if args.no_cpu_baseline else wl.cpu_baseline()
     print(json.dumps(result))
     return 0
 

@@ -96,7 +96,9 @@ struct Workspace {
 // Device helpers.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
-__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
+// Wave index within the workgroup, as a wave-uniform (scalar) value: values
+// derived from it (row ids, base pointers, buffer resources) stay in SGPRs.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   int lane = lane_id();

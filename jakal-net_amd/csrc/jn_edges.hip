@@ -214,11 +214,13 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
       }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        // absent edges read row 0 and are masked
-        const uint32_t roff = (uint32_t)max(jg[i], 0) * (uint32_t)a.ld_pv * 4u;
+        // absent edges, iterations past the block's last edge and lanes past D
+        // read out of range: zeros and no memory traffic, without a branch
+        const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ld_pv * 4u : kOobOffset;
         float4 v[NV];
 #pragma unroll
-        for (int t = 0; t < NV; ++t) v[t] = buf_load_w<W>(rs_pv, loff[t] == kOobOffset ? kOobOffset : roff + loff[t]);
+        for (int t = 0; t < NV; ++t)
+          v[t] = buf_load_w<W>(rs_pv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
         float pdot = 0.f;
 #pragma unroll
         for (int t = 0; t < NV; ++t) pdot += dot4(gv[t], v[t]);
@@ -256,7 +258,8 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const float gg = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * i + g) << 2, __float_as_int(gsc)));
-      const uint32_t koff = (uint32_t)max(jg[i], 0) * (uint32_t)a.ldk * 4u;
+      // absent edges read out of range (zeros, no traffic)
+      const uint32_t koff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ldk * 4u : kOobOffset;
       if (kvec) {
         fma4(dqa, gg, buf_load4(rs_key, 4 * c < a.r ? koff + 16u * c : kOobOffset));
         if (a.r > 64) fma4(dqb, gg, buf_load4(rs_key, 64 + 4 * c < a.r ? koff + 256u + 16u * c : kOobOffset));

@@ -182,15 +182,26 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 }
 
 // Sum split-K partials in a fixed order; rows < m_split go to out0, the rest to out1.
-__global__ void splitk_reduce_kernel(const float* part, int splits, int M, int N, int64_t split_stride, float* out0,
-                                     float* out1, int m_split) {
-  int64_t total = (int64_t)M * N;
-  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
-    int m = (int)(e / N), n = (int)(e % N);
-    float s = 0.0f;
-    for (int z = 0; z < splits; ++z) s += part[z * split_stride + (int64_t)m * N + n];
-    if (m < m_split) out0[(int64_t)m * N + n] = s;
-    else out1[(int64_t)(m - m_split) * N + n] = s;
+// out = sum over splits of part[z] (fixed order).  A workgroup owns 64
+// consecutive outputs; wave w sums splits z = w, w + 4, ... for its lane's
+// output, then the four partials are added in wave order.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, int splits, int M, int N,
+                                                            int64_t split_stride, float* out0, float* out1,
+                                                            int m_split) {
+  __shared__ float red[4][64];
+  const int lane = lane_id(), wave = wave_id();
+  const int64_t total = (int64_t)M * N;
+  const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+  float s = 0.0f;
+  if (e < total)
+    for (int z = wave; z < splits; z += 4) s += part[z * split_stride + e];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && e < total) {
+    const float t = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+    const int m = (int)(e / N), n = (int)(e % N);
+    if (m < m_split) out0[(int64_t)m * N + n] = t;
+    else out1[(int64_t)(m - m_split) * N + n] = t;
   }
 }
 
@@ -253,9 +264,9 @@ int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, 
   g.k_chunk = k_chunk; g.c_split_stride = (int64_t)M * N;
   int rc = launch_gemm(g, false, false, splits, stream, "gemm_f32_kernel<grad_weight>");
   if (rc != kOk) return rc;
-  int64_t total = (int64_t)M * N;
-  int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
-  if (blocks < 1) blocks = 1;
+  const int64_t total = (int64_t)M * N;
+  JN_REQUIRE((total + 63) / 64 < (1LL << 31), kUnsupported, "weight gradient too large");
+  const int blocks = (int)((total + 63) / 64);
   JN_PROFILE("splitk_reduce_kernel", stream);
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, splits, M, N,
                      (int64_t)M * N, out0, out1, m_split);

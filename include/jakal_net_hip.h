@@ -139,6 +139,56 @@ int jn_propagation_window_backward(const float* layer_val, const float* projecte
                                    float* grad_source_weight, float* grad_core_weight, float* grad_bias,
                                    void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
+/*
+ * SparseTransition with LowRankBilinearRoute (optionally temperature-scaled):
+ *   l[j,d]  = ((P_s[j] * w) . P_t[d] + b) / temperature,  P_s = src_val Ws^T,
+ *             P_t = dst_val Wt^T, w the raw core weight (modules.py:435-441)
+ *   each source row j keeps its k = min(topk, dst_nodes) best destinations
+ *   (transition.py:437-444); p = softmax over them (compress_kind 0) or
+ *   sign(l) * softmax(|l|) (compress_kind 1)
+ *   delta_state[d] = sum_j p[j,d] rho[j] projected_state[j]
+ *   delta_val[d]   = sum_j p[j,d] rho[j] projected_val[j]
+ * Shapes: sender_strength rho [B,Ns], src_val [B,Ns,Dsrc], dst_val [B,Nd,Ddst],
+ * projected_state [B,Ns], projected_val [B,Ns,Dv], Ws [r,Dsrc], Wt [r,Ddst],
+ * w [r], bias scalar or NULL.  Outputs delta_state [B,Nd], delta_val [B,Nd,Dv],
+ * and for the backward src_proj [B*Ns,r], dst_proj [B*Nd,r], route_index
+ * [B,Ns,k] (int32) and route_logit [B,Ns,k].  k <= 32 when k < dst_nodes;
+ * k == dst_nodes <= 64 takes every destination.  Deterministic (the
+ * destination sums are gathers over the edges grouped by destination).
+ * Replaces transition_pairwise_topk (native/jakal_net_native.cpp:6916-7087) and
+ * low_rank_pairwise_topk_forward_cuda (native/jakal_net_native.cpp:167-189).
+ */
+size_t jn_transition_topk_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                          int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk);
+
+int jn_transition_topk_forward(const float* sender_strength, const float* src_val, const float* dst_val,
+                               const float* projected_state, const float* projected_val, const float* source_weight,
+                               const float* target_weight, const float* core_weight, const float* bias,
+                               float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                               int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk,
+                               int32_t compress_kind, float* delta_state, float* delta_val, float* src_proj,
+                               float* dst_proj, int32_t* route_index, float* route_logit, void* workspace,
+                               size_t workspace_bytes, jn_stream_t stream);
+
+/*
+ * Backward of jn_transition_topk_forward given grad_delta_state [B,Nd] and
+ * grad_delta_val [B,Nd,Dv].  Output pointers may be NULL to skip a gradient.
+ * Replaces _LowRankTransitionPairwiseTopK.backward
+ * (src/jakal_net/native_backend.py:4408-4599): softmax_backward_cuda and
+ * low_rank_pairwise_topk_backward_cuda (native/jakal_net_native.cpp:398-416, 449-477).
+ */
+int jn_transition_topk_backward(const float* sender_strength, const float* src_val, const float* dst_val,
+                                const float* projected_state, const float* projected_val, const float* source_weight,
+                                const float* target_weight, const float* core_weight, const float* src_proj,
+                                const float* dst_proj, const int32_t* route_index, const float* route_logit,
+                                const float* grad_delta_state, const float* grad_delta_val, float temperature,
+                                int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk, int32_t compress_kind,
+                                float* grad_sender_strength, float* grad_src_val, float* grad_dst_val,
+                                float* grad_projected_state, float* grad_projected_val, float* grad_source_weight,
+                                float* grad_target_weight, float* grad_core_weight, float* grad_bias,
+                                void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -132,6 +132,65 @@ PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int
   return s;
 }
 
+struct TransitionScratch {
+  float* coef;
+  int32_t* tile_base;
+  int32_t* seg_start;
+  int32_t* edges;
+  float* dPs;
+  float* dPt;
+  float* g_logit;
+  float* rowsum;
+  float* part_c;
+  float* stage;
+  float* splitk;
+  size_t bytes;
+};
+
+int64_t route_edges(int64_t topk, int64_t dst_nodes) { return topk < dst_nodes ? topk : dst_nodes; }
+
+TransitionScratch carve_transition(void* base, size_t size, int64_t B, int64_t Ns, int64_t Nd, int64_t Dsrc,
+                                   int64_t Ddst, int64_t r, int64_t k) {
+  Workspace ws(base, size);
+  TransitionScratch s{};
+  const int64_t T = (Ns + kCsrTile - 1) / kCsrTile;
+  s.coef = ws.take<float>(B * Ns * k);
+  s.tile_base = ws.take<int32_t>(B * T * Nd);
+  s.seg_start = ws.take<int32_t>(B * (Nd + 1));
+  s.edges = ws.take<int32_t>(B * Ns * k);
+  s.dPs = ws.take<float>(B * Ns * r);
+  s.dPt = ws.take<float>(B * Nd * r);
+  s.g_logit = ws.take<float>(B * Ns * k);
+  s.rowsum = ws.take<float>(B * Ns);
+  s.part_c = ws.take<float>((size_t)cols_backward_waves(B * Nd, kColsPerWave) * r);
+  s.stage = ws.take<float>(finalize_stage_floats((int)r));
+  const size_t sk = std::max(gemm_grad_weight_workspace((int)r, (int)Dsrc, (int)(B * Ns)),
+                             gemm_grad_weight_workspace((int)r, (int)Ddst, (int)(B * Nd)));
+  s.splitk = ws.take<float>(sk / sizeof(float));
+  s.bytes = ws.used;
+  return s;
+}
+
+int check_transition_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t Dsrc, int64_t Ddst, int64_t Dv,
+                            int64_t rank, int64_t topk, int32_t compress_kind, float temperature) {
+  JN_REQUIRE(batch >= 1 && Ns >= 1 && Nd >= 1 && Dsrc >= 1 && Ddst >= 1 && Dv >= 1, kInvalidArgument,
+             "batch, node counts and dims must be positive");
+  JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
+  JN_REQUIRE(topk >= 1, kInvalidArgument, "topk must be positive");
+  const int64_t k = route_edges(topk, Nd);
+  JN_REQUIRE(k == Nd ? k <= 64 : k <= kSelectMaxK, kUnsupported,
+             "routes support topk <= %d below the destination count, or up to 64 destinations in all (topk=%lld, "
+             "dst_nodes=%lld)",
+             kSelectMaxK, (long long)topk, (long long)Nd);
+  JN_REQUIRE(compress_kind == 0 || compress_kind == 1, kUnsupported,
+             "route compress kind must be 0 (softmax) or 1 (signed_abs_softmax), got %d", compress_kind);
+  JN_REQUIRE(temperature > 0.0f, kInvalidArgument, "temperature must be positive");
+  JN_REQUIRE(fits_int(batch * Ns * k) && fits_int(batch * Nd * rank) && fits_int(batch * Ns * rank) &&
+                 fits_int(Nd * Dv * 4) && fits_int(Nd * rank * 4),
+             kUnsupported, "problem too large for 32-bit edge ids and offsets");
+  return kOk;
+}
+
 // Backward of any edge-list propagation (top-k or window): the edge list
 // (edge_index, edge_score) [B*N, k] is what the forward aggregated.
 int propagation_edges_backward(const float* layer_val, const float* projected_state, const float* projected_val,
@@ -433,10 +492,13 @@ int jn_propagation_window_forward(const float* layer_val, const float* projected
   w.ldk = 2 * r;
   w.scale = core_weight;
   w.bias = bias;
+  w.inv_temperature = 1.0f;
   w.B = (int)batch;
-  w.N = (int)nodes;
+  w.Nq = (int)nodes;
+  w.Nk = (int)nodes;
   w.r = r;
   w.width = (int)width;
+  w.all_keys = 0;
   w.idx = edge_index;
   w.score = edge_score;
   rc = launch_window_scores(w, st);
@@ -485,6 +547,242 @@ int jn_propagation_window_backward(const float* layer_val, const float* projecte
                                     projected_val_is_layer_val, grad_layer_val, grad_projected_state,
                                     grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
                                     grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+size_t jn_transition_topk_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                          int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk) {
+  (void)val_dim;
+  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || topk < 1) return 0;
+  return carve_transition(nullptr, 0, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank,
+                          route_edges(topk, dst_nodes))
+      .bytes;
+}
+
+int jn_transition_topk_forward(const float* sender_strength, const float* src_val, const float* dst_val,
+                               const float* projected_state, const float* projected_val, const float* source_weight,
+                               const float* target_weight, const float* core_weight, const float* bias,
+                               float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                               int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk,
+                               int32_t compress_kind, float* delta_state, float* delta_val, float* src_proj,
+                               float* dst_proj, int32_t* route_index, float* route_logit, void* workspace,
+                               size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_transition_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, topk, compress_kind,
+                                   temperature);
+  if (rc) return rc;
+  JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
+                 target_weight && core_weight && delta_state && delta_val && src_proj && dst_proj && route_index &&
+                 route_logit,
+             kInvalidArgument, "null tensor pointer");
+  const int64_t k = route_edges(topk, dst_nodes);
+  TransitionScratch s = carve_transition(workspace, workspace_bytes, batch, src_nodes, dst_nodes, src_dim, dst_dim,
+                                         rank, k);
+  JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
+             "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int B = (int)batch, Ns = (int)src_nodes, Nd = (int)dst_nodes, r = (int)rank;
+
+  // 1. projections P_s = src . Ws^T, P_t = dst . Wt^T  (modules.py:435-437)
+  rc = gemm_project(src_val, src_dim, source_weight, source_weight, r, src_dim, src_proj, r, B * Ns, r, (int)src_dim,
+                    st);
+  if (rc) return rc;
+  rc = gemm_project(dst_val, dst_dim, target_weight, target_weight, r, dst_dim, dst_proj, r, B * Nd, r, (int)dst_dim,
+                    st);
+  if (rc) return rc;
+
+  // 2. per-source edge list: logits ((P_s * w) . P_t + b) / T, top-k over destinations
+  if (k < dst_nodes) {
+    SelectArgs a{};
+    a.q = src_proj;
+    a.key = dst_proj;
+    a.ldq = r;
+    a.ldk = r;
+    a.q_batch_stride = src_nodes * r;
+    a.k_batch_stride = dst_nodes * r;
+    a.scale = core_weight;
+    a.bias = bias;
+    a.scale_on_query = 1;
+    a.temperature = temperature;
+    a.B = B;
+    a.Nq = Ns;
+    a.Nk = Nd;
+    a.r = r;
+    a.k = (int)k;
+    a.out_idx = route_index;
+    a.out_score = route_logit;
+    rc = launch_topk_select(a, st);
+  } else {
+    WindowScoreArgs w{};
+    w.q = src_proj;
+    w.key = dst_proj;
+    w.ldq = r;
+    w.ldk = r;
+    w.scale = core_weight;
+    w.bias = bias;
+    w.inv_temperature = 1.0f / temperature;
+    w.B = B;
+    w.Nq = Ns;
+    w.Nk = Nd;
+    w.r = r;
+    w.width = Nd;
+    w.all_keys = 1;
+    w.idx = route_index;
+    w.score = route_logit;
+    rc = launch_window_scores(w, st);
+  }
+  if (rc) return rc;
+
+  // 3. coefficients rho * p, then destination sums as gathers over the edges
+  //    transposed by destination
+  rc = launch_route_coef(route_index, route_logit, sender_strength, (int)k, compress_kind, batch * src_nodes, s.coef,
+                         st);
+  if (rc) return rc;
+  CsrArgs ca{};
+  ca.idx = route_index;
+  ca.k = (int)k;
+  ca.B = B;
+  ca.Nq = Ns;
+  ca.Nk = Nd;
+  ca.tile_base = s.tile_base;
+  ca.seg_start = s.seg_start;
+  ca.edges = s.edges;
+  rc = launch_csr(ca, st);
+  if (rc) return rc;
+  ColsBwdArgs cb{};
+  cb.seg_start = s.seg_start;
+  cb.edges = s.edges;
+  cb.k = (int)k;
+  cb.coef = s.coef;
+  cb.gds = projected_state;
+  cb.gdv = projected_val;
+  cb.B = B;
+  cb.Nq = Ns;
+  cb.Nk = Nd;
+  cb.D = (int)val_dim;
+  cb.cols_per_wave = kColsPerWave;
+  cb.grad_pv = delta_val;
+  cb.ld_gpv = val_dim;
+  cb.grad_ps = delta_state;
+  return launch_cols_backward(cb, st);
+}
+
+int jn_transition_topk_backward(const float* sender_strength, const float* src_val, const float* dst_val,
+                                const float* projected_state, const float* projected_val, const float* source_weight,
+                                const float* target_weight, const float* core_weight, const float* src_proj,
+                                const float* dst_proj, const int32_t* route_index, const float* route_logit,
+                                const float* grad_delta_state, const float* grad_delta_val, float temperature,
+                                int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk, int32_t compress_kind,
+                                float* grad_sender_strength, float* grad_src_val, float* grad_dst_val,
+                                float* grad_projected_state, float* grad_projected_val, float* grad_source_weight,
+                                float* grad_target_weight, float* grad_core_weight, float* grad_bias,
+                                void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_transition_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, topk, compress_kind,
+                                   temperature);
+  if (rc) return rc;
+  JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
+                 target_weight && core_weight && src_proj && dst_proj && route_index && route_logit &&
+                 grad_delta_state && grad_delta_val,
+             kInvalidArgument, "null tensor pointer");
+  const int64_t k = route_edges(topk, dst_nodes);
+  TransitionScratch s = carve_transition(workspace, workspace_bytes, batch, src_nodes, dst_nodes, src_dim, dst_dim,
+                                         rank, k);
+  JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
+             "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int B = (int)batch, Ns = (int)src_nodes, Nd = (int)dst_nodes, r = (int)rank;
+
+  // 1. source rows: coefficient grads, route compress backward, sender-strength,
+  //    projected state/value grads and the grad of the source projection
+  RouteRowsBwdArgs rb{};
+  rb.idx = route_index;
+  rb.logit = route_logit;
+  rb.k = (int)k;
+  rb.compress = compress_kind;
+  rb.inv_temperature = 1.0f / temperature;
+  rb.rho = sender_strength;
+  rb.ps = projected_state;
+  rb.pv = projected_val;
+  rb.ld_pv = val_dim;
+  rb.gds = grad_delta_state;
+  rb.gdv = grad_delta_val;
+  rb.key = dst_proj;
+  rb.ldk = r;
+  rb.qscale = core_weight;
+  rb.r = r;
+  rb.Ns = Ns;
+  rb.Nd = Nd;
+  rb.D = (int)val_dim;
+  rb.rows = batch * src_nodes;
+  rb.g_logit = s.g_logit;
+  rb.grad_rho = grad_sender_strength;
+  rb.grad_ps = grad_projected_state;
+  rb.grad_pv = grad_projected_val;
+  rb.ld_gpv = val_dim;
+  rb.dq = s.dPs;
+  rb.lddq = r;
+  rb.rowsum = s.rowsum;
+  rc = launch_route_rows_backward(rb, st);
+  if (rc) return rc;
+
+  // 2. destination columns: grad of the destination projection and w partials
+  CsrArgs ca{};
+  ca.idx = route_index;
+  ca.k = (int)k;
+  ca.B = B;
+  ca.Nq = Ns;
+  ca.Nk = Nd;
+  ca.tile_base = s.tile_base;
+  ca.seg_start = s.seg_start;
+  ca.edges = s.edges;
+  rc = launch_csr(ca, st);
+  if (rc) return rc;
+  ColsBwdArgs cb{};
+  cb.seg_start = s.seg_start;
+  cb.edges = s.edges;
+  cb.k = (int)k;
+  cb.g_score = s.g_logit;
+  cb.q = src_proj;
+  cb.ldq = r;
+  cb.key = dst_proj;
+  cb.ldk = r;
+  cb.kscale = core_weight;
+  cb.r = r;
+  cb.B = B;
+  cb.Nq = Ns;
+  cb.Nk = Nd;
+  cb.D = (int)val_dim;
+  cb.cols_per_wave = kColsPerWave;
+  cb.dk = s.dPt;
+  cb.lddk = r;
+  cb.part_c = s.part_c;
+  rc = launch_cols_backward(cb, st);
+  if (rc) return rc;
+
+  // 3. projection weight and input grads
+  if (grad_source_weight) {
+    rc = gemm_grad_weight(s.dPs, r, src_val, src_dim, grad_source_weight, grad_source_weight, r, r, (int)src_dim,
+                          B * Ns, s.splitk, st);
+    if (rc) return rc;
+  }
+  if (grad_target_weight) {
+    rc = gemm_grad_weight(s.dPt, r, dst_val, dst_dim, grad_target_weight, grad_target_weight, r, r, (int)dst_dim,
+                          B * Nd, s.splitk, st);
+    if (rc) return rc;
+  }
+  if (grad_src_val) {
+    rc = gemm_grad_input(s.dPs, r, source_weight, source_weight, r, src_dim, nullptr, 0, grad_src_val, src_dim,
+                         B * Ns, (int)src_dim, r, st);
+    if (rc) return rc;
+  }
+  if (grad_dst_val) {
+    rc = gemm_grad_input(s.dPt, r, target_weight, target_weight, r, dst_dim, nullptr, 0, grad_dst_val, dst_dim,
+                         B * Nd, (int)dst_dim, r, st);
+    if (rc) return rc;
+  }
+
+  // 4. core weight and bias grads
+  return launch_finalize_small_grads(s.part_c, cols_backward_waves((int64_t)B * Nd, kColsPerWave), r,
+                                     grad_core_weight, 0, s.rowsum, batch * src_nodes, grad_bias, s.stage, st);
 }
 
 }  // extern "C"

@@ -194,6 +194,43 @@ __device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t by
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
 }
 
+// ---------------------------------------------------------------------------
+// Vector helpers: a lane moves W consecutive floats (W = 4 when the row
+// stride and base are 16-byte aligned, else 1).
+// ---------------------------------------------------------------------------
+template <int W>
+__device__ __forceinline__ float4 load_w(const float* p) {
+  if constexpr (W == 4) return *reinterpret_cast<const float4*>(p);
+  else return make_float4(p[0], 0.f, 0.f, 0.f);
+}
+template <int W>
+__device__ __forceinline__ void store_w(float* p, float4 v) {
+  if constexpr (W == 4) *reinterpret_cast<float4*>(p) = v;
+  else p[0] = v.x;
+}
+__device__ __forceinline__ void fma4(float4& acc, float c, float4 v) {
+  acc.x += c * v.x;
+  acc.y += c * v.y;
+  acc.z += c * v.z;
+  acc.w += c * v.w;
+}
+__device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+
+// W consecutive floats at a byte offset of a buffer (zeros when out of range).
+template <int W>
+__device__ __forceinline__ float4 buf_load_w(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  if constexpr (W == 4) return buf_load4(r, byte_off);
+  else return make_float4(buf_load1(r, byte_off), 0.f, 0.f, 0.f);
+}
+
+__device__ __forceinline__ float sign_f(float s) { return (s > 0.f) ? 1.f : ((s < 0.f) ? -1.f : 0.f); }
+
+// Edges of a row processed four at a time by the wave's 16-lane groups (group g
+// takes edge 4i + g in iteration i): lane L (< 64) takes the edge held by group
+// L % 4 in iteration L / 4.
+__device__ __forceinline__ int edge_owner_lane(int lane) { return (lane & 3) * 16 + (lane >> 2); }
+
 // Make LDS writes of this wavefront visible to later LDS reads of the same
 // wavefront by other lanes (compiler + hardware ordering, no workgroup barrier).
 __device__ __forceinline__ void wave_lds_sync() {

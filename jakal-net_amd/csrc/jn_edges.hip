@@ -17,38 +17,6 @@
 namespace jakal {
 
 // ---------------------------------------------------------------------------
-// Vector helpers: a lane moves W consecutive floats (W = 4 when the row
-// stride and base are 16-byte aligned, else 1).
-// ---------------------------------------------------------------------------
-template <int W>
-__device__ __forceinline__ float4 load_w(const float* p) {
-  if constexpr (W == 4) return *reinterpret_cast<const float4*>(p);
-  else return make_float4(p[0], 0.f, 0.f, 0.f);
-}
-template <int W>
-__device__ __forceinline__ void store_w(float* p, float4 v) {
-  if constexpr (W == 4) *reinterpret_cast<float4*>(p) = v;
-  else p[0] = v.x;
-}
-__device__ __forceinline__ void fma4(float4& acc, float c, float4 v) {
-  acc.x += c * v.x;
-  acc.y += c * v.y;
-  acc.z += c * v.z;
-  acc.w += c * v.w;
-}
-__device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
-__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
-
-// W consecutive floats at a byte offset of a buffer (zeros when out of range).
-template <int W>
-__device__ __forceinline__ float4 buf_load_w(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  if constexpr (W == 4) return buf_load4(r, byte_off);
-  else return make_float4(buf_load1(r, byte_off), 0.f, 0.f, 0.f);
-}
-
-__device__ __forceinline__ float sign_f(float s) { return (s > 0.f) ? 1.f : ((s < 0.f) ? -1.f : 0.f); }
-
-// ---------------------------------------------------------------------------
 // Row forward: one wavefront per query row.
 // ---------------------------------------------------------------------------
 
@@ -159,10 +127,6 @@ int launch_rows_forward(const RowsFwdArgs& a, hipStream_t stream) {
 // edge's dot product is reduced inside the group by DPP (4 VALU ops) and the
 // key rows of the dQ sum are read 4 edges per instruction.
 // ---------------------------------------------------------------------------
-
-// Round-robin edge -> group assignment: lane L (< KP) takes the edge held by
-// group L % 4 in iteration L / 4.
-__device__ __forceinline__ int edge_owner_lane(int lane) { return (lane & 3) * 16 + (lane >> 2); }
 
 template <int W, int NV, int KP>
 __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
@@ -563,14 +527,16 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
       }
       if (first) {
         if (a.grad_ps && lane == 0) a.grad_ps[colg] = st;
-        const float* kr = a.key + colg * a.ldk;
-        if (lane < a.r) {
-          a.dk[colg * a.lddk + lane] = dk0 * (a.kscale ? a.kscale[lane] : 1.f);
-          pc0 += kr[lane] * dk0;
-        }
-        if (lane + kWave < a.r) {
-          a.dk[colg * a.lddk + lane + kWave] = dk1 * (a.kscale ? a.kscale[lane + kWave] : 1.f);
-          pc1 += kr[lane + kWave] * dk1;
+        if (a.q) {
+          const float* kr = a.key + colg * a.ldk;
+          if (lane < a.r) {
+            a.dk[colg * a.lddk + lane] = dk0 * (a.kscale ? a.kscale[lane] : 1.f);
+            pc0 += kr[lane] * dk0;
+          }
+          if (lane + kWave < a.r) {
+            a.dk[colg * a.lddk + lane + kWave] = dk1 * (a.kscale ? a.kscale[lane + kWave] : 1.f);
+            pc1 += kr[lane + kWave] * dk1;
+          }
         }
         dk0 = dk1 = st = 0.f;
       }
@@ -586,10 +552,10 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
       float cf = 0.f, gsv = 0.f, gdsv = 0.f;
       if (lane < n) {
         const int eid = a.edges[pos];
-        cf = a.coef[eid];
+        if (a.coef) cf = a.coef[eid];
         rowq = eid / a.k;
         if (first) {
-          gsv = a.g_score[eid];
+          if (a.g_score) gsv = a.g_score[eid];
           if (a.gds) gdsv = a.gds[rowq];
         }
       }
@@ -618,7 +584,7 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
           }
         }
         float qa[G], qb[G];
-        if (first) {
+        if (first && a.q) {
 #pragma unroll
           for (int u = 0; u < G; ++u) {
             const auto rs = make_rsrc(a.q + (int64_t)rw[u] * a.ldq, (uint32_t)a.r * 4u);
@@ -635,8 +601,10 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
             for (int t = 0; t < NV; ++t) fma4(acc[t], cu[u], v[u][t]);
           }
           if (first) {
-            dk0 += gg[u] * qa[u];
-            dk1 += gg[u] * qb[u];
+            if (a.q) {
+              dk0 += gg[u] * qa[u];
+              dk1 += gg[u] * qb[u];
+            }
             st += cu[u] * gd[u];
           }
         }
@@ -644,8 +612,10 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
     }
     while (cur < ncols) flush(cur++);
   }
-  if (lane < a.r) a.part_c[gw * a.r + lane] = pc0;
-  if (lane + kWave < a.r) a.part_c[gw * a.r + lane + kWave] = pc1;
+  if (a.q && a.part_c) {
+    if (lane < a.r) a.part_c[gw * a.r + lane] = pc0;
+    if (lane + kWave < a.r) a.part_c[gw * a.r + lane + kWave] = pc1;
+  }
 }
 
 int cols_backward_waves(int64_t total_cols, int cols_per_wave) {
@@ -655,7 +625,8 @@ int cols_backward_waves(int64_t total_cols, int cols_per_wave) {
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   const int64_t total_cols = (int64_t)a.B * a.Nk;
   if (total_cols == 0) return kOk;
-  JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
+  JN_REQUIRE(!a.q || (a.r >= 1 && a.r <= 128), kUnsupported, "rank must be in [1, 128]");
+  JN_REQUIRE(!a.q || (a.key && a.dk && a.g_score), kInvalidArgument, "key-side gradient needs key, dk and g_score");
   JN_REQUIRE(a.cols_per_wave >= 1 && a.cols_per_wave <= kWave, kInvalidArgument, "columns per wave must be in [1, 64]");
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
   JN_REQUIRE((int64_t)a.D * 4 < (1LL << 31), kUnsupported, "value rows must stay below 2 GiB");

@@ -73,17 +73,54 @@ struct RowsBwdArgs {
 };
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream);
 
+// Fixed edge lists with low-rank scores: the causal band (all_keys = 0: slot e
+// of query row i is key i - (width - 1 - e), absent when negative) or every
+// key (all_keys = 1: slot e is key e, width = Nk).
 struct WindowScoreArgs {
-  const float* q;      // query projection rows (global row index), stride ldq
-  const float* key;    // key projection rows (global row index), stride ldk
+  const float* q;        // query projection rows (global row b*Nq + i), stride ldq
+  const float* key;      // key projection rows (global row b*Nk + j), stride ldk
   int64_t ldq, ldk;
-  const float* scale;  // [r] applied to the query (null = 1)
-  const float* bias;   // scalar or null
-  int B, N, r, width;
-  int32_t* idx;        // [B*N, width]
-  float* score;        // [B*N, width]
+  const float* scale;    // [r] applied to the query (null = 1)
+  const float* bias;     // scalar or null
+  float inv_temperature; // score = (dot + bias) * inv_temperature
+  int B, Nq, Nk, r, width;
+  int all_keys;
+  int32_t* idx;          // [B*Nq, width]
+  float* score;          // [B*Nq, width]
 };
 int launch_window_scores(const WindowScoreArgs& a, hipStream_t stream);
+
+// ---- transition routing (jn_route.hip) -------------------------------------
+int launch_route_coef(const int32_t* idx, const float* logit, const float* rho, int k, int compress, int64_t rows,
+                      float* coef, hipStream_t stream);
+
+struct RouteRowsBwdArgs {
+  const int32_t* idx;    // [rows, k] destination per edge (-1 absent)
+  const float* logit;    // [rows, k]
+  int k;
+  int compress;          // 0 softmax, 1 signed |l| softmax
+  float inv_temperature;
+  const float* rho;      // [rows] sender strength
+  const float* ps;       // [rows] projected state of the sources
+  const float* pv;       // [rows, ld_pv] projected values of the sources
+  int64_t ld_pv;
+  const float* gds;      // [B*Nd] grad of delta_state
+  const float* gdv;      // [B*Nd, D] grad of delta_val
+  const float* key;      // destination projection rows [B*Nd], stride ldk
+  int64_t ldk;
+  const float* qscale;   // [r] core weight (scales dQ)
+  int r, Ns, Nd, D;
+  int64_t rows;          // B*Ns
+  float* g_logit;        // [rows, k]
+  float* grad_rho;       // [rows] (null: skip)
+  float* grad_ps;        // [rows] (null: skip)
+  float* grad_pv;        // [rows, ld_gpv] (null: skip)
+  int64_t ld_gpv;
+  float* dq;             // [rows, r], stride lddq
+  int64_t lddq;
+  float* rowsum;         // [rows]
+};
+int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream);
 
 struct CsrArgs {
   const int32_t* idx;

@@ -1,0 +1,265 @@
+// Transition routing over an edge list (gfx950).
+//
+// SparseTransition with a low-rank pairwise route (transition.py:431-452,
+// modules.py:415-441): every source row j of a batch element keeps k
+// destinations (edge list idx/logit [B*Ns, k], from the top-k select) and
+//   p[j, e]    = softmax over the row's edges of the logits (compress 0,
+//                kernel_common.py:420-423) or sign(l) * softmax(|l|)
+//                (compress 1, native_backend.py:2184-2188)
+//   coef[j, e] = rho[j] * p[j, e]          rho = sender strength (softplus(state))
+//   delta_state[k] = sum_{j->k} coef * ps[j],  delta_val[k] = sum_{j->k} coef * pv[j]
+// The destination sums run as gathers over the edge list transposed by
+// destination (the column kernel of jn_edges.hip), so no atomics are used.
+//
+//   route_coef_kernel          : coef per edge (one wavefront per source row)
+//   route_rows_backward_kernel : per source row, with its edges' destination
+//                                gradient rows gathered once:
+//       g_c[e]   = gds[k] * ps[j] + <gdv[k], pv[j]>
+//       grad pv[j] = sum_e coef[e] * gdv[k],  grad ps[j] = sum_e coef[e] * gds[k]
+//       grad rho[j] = sum_e p[e] * g_c[e]
+//       g_l[e]   = compress backward of rho * g_c, times 1/T
+//       dQ[j, r] = qscale[r] * sum_e g_l[e] * key[k, r]
+//       rowsum[j] = sum_e g_l[e]   (bias gradient partial)
+#include "jn_internal.hpp"
+
+namespace jakal {
+
+// Route probability of edge `lane` of a source row (signed for compress 1) and
+// the sign of its logit.  Lanes >= k, and absent edges, get p = 0.
+__device__ __forceinline__ float route_probability(int j, float s, int compress) {
+  const float a = compress == 0 ? s : fabsf(s);
+  float m = j >= 0 ? a : -INFINITY;
+  m = __int_as_float(wave_reduce_i(__float_as_int(m), [](int x, int y) {
+    return __float_as_int(fmaxf(__int_as_float(x), __int_as_float(y)));
+  }));
+  const float ex = j >= 0 ? __expf(a - m) : 0.0f;
+  const float sum = wave_sum(ex);
+  const float p = sum > 0.0f ? ex / sum : 0.0f;
+  return compress == 0 ? p : (s > 0.f ? p : (s < 0.f ? -p : 0.f));
+}
+
+__global__ __launch_bounds__(256) void route_coef_kernel(const int32_t* idx, const float* logit, const float* rho,
+                                                         int k, int compress, int64_t rows, float* coef) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  if (row >= rows) return;
+  int j = -1;
+  float s = 0.0f;
+  if (lane < k) {
+    j = idx[row * k + lane];
+    if (j >= 0) s = logit[row * k + lane];
+  }
+  const float p = route_probability(j, s, compress);
+  if (lane < k) coef[row * k + lane] = rho[row] * p;
+}
+
+int launch_route_coef(const int32_t* idx, const float* logit, const float* rho, int k, int compress, int64_t rows,
+                      float* coef, hipStream_t stream) {
+  JN_REQUIRE(k >= 1 && k <= kWave, kUnsupported, "routes support 1..64 edges per source (got %d)", k);
+  if (rows == 0) return kOk;
+  const int64_t blocks = (rows + 3) / 4;
+  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
+  JN_PROFILE("route_coef_kernel", stream);
+  hipLaunchKernelGGL(route_coef_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, idx, logit, rho, k, compress,
+                     rows, coef);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
+// One wavefront per source row; its four 16-lane groups take four edges at a
+// time (group g takes edges 4i + g) and read whole destination gradient rows
+// with 16-byte buffer loads.
+template <int W, int NV, int KP>
+__global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdArgs a) {
+  constexpr int NI = KP / 4;
+  constexpr int P = 16 * W * NV;
+  const int lane = lane_id();
+  const int g = lane >> 4, c = lane & 15;
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  if (row >= a.rows) return;
+  const int64_t b = row / a.Ns;
+  // 32-bit offsets into buffers of this batch element (sizes checked on the host)
+  const auto rs_gdv = make_rsrc(a.gdv + b * a.Nd * a.D, (uint32_t)(a.Nd * a.D * 4));
+  const auto rs_key = make_rsrc(a.key + b * a.Nd * a.ldk, (uint32_t)(a.Nd * a.ldk * 4));
+  const auto rs_pv = make_rsrc(a.pv + row * a.ld_pv, (uint32_t)(a.D * 4));
+  const float* gdsb = a.gds + b * a.Nd;
+  const float ps_row = a.ps[row];
+  const float rho = a.rho[row];
+  const bool kvec = (a.r % 4 == 0) && (a.ldk % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.key) & 15) == 0);
+
+  int j = -1;
+  float s = 0.0f;
+  if (lane < a.k) {
+    j = a.idx[row * a.k + lane];
+    if (j >= 0) s = a.logit[row * a.k + lane];
+  }
+  const float p = route_probability(j, s, a.compress);
+  const float cf = rho * p;
+  int jg[NI];
+  float cg[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    jg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, j);
+    cg[i] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * i + g) << 2, __float_as_int(cf)));
+  }
+
+  float dots[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) dots[i] = 0.f;
+  for (int d0 = 0; d0 < a.D; d0 += P) {
+    uint32_t loff[NV];
+    float4 pvv[NV], acc[NV];
+#pragma unroll
+    for (int t = 0; t < NV; ++t) {
+      const int off = d0 + (16 * t + c) * W;
+      loff[t] = off < a.D ? (uint32_t)off * 4u : kOobOffset;
+      pvv[t] = buf_load_w<W>(rs_pv, loff[t]);
+      acc[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      // absent edges and lanes past D read out of range: zeros, no traffic
+      const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.D * 4u : kOobOffset;
+      float4 v[NV];
+#pragma unroll
+      for (int t = 0; t < NV; ++t)
+        v[t] = buf_load_w<W>(rs_gdv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
+      float pdot = 0.f;
+#pragma unroll
+      for (int t = 0; t < NV; ++t) {
+        pdot += dot4(pvv[t], v[t]);
+        fma4(acc[t], cg[i], v[t]);
+      }
+      dots[i] += pdot;
+      if (((i + 1) * NV) % 16 == 0) __builtin_amdgcn_sched_barrier(0);
+    }
+    if (a.grad_pv) {
+      // sum the four groups' partial rows; group g stores slices t = g, g + 4
+      float* out = a.grad_pv + row * a.ld_gpv;
+#pragma unroll
+      for (int t = 0; t < NV; ++t) {
+        float4 x = acc[t];
+        x.x += xor16_f(x.x);
+        x.y += xor16_f(x.y);
+        x.z += xor16_f(x.z);
+        x.w += xor16_f(x.w);
+        x.x += xor32_f(x.x);
+        x.y += xor32_f(x.y);
+        x.z += xor32_f(x.z);
+        x.w += xor32_f(x.w);
+        const int off = d0 + (16 * t + c) * W;
+        if ((t & 3) == g && off < a.D) store_w<W>(out + off, x);
+      }
+    }
+  }
+  float sel = 0.f;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const float tot = row16_sum(dots[i]);
+    sel = (c == i) ? tot : sel;
+  }
+  const float dot = __int_as_float(__builtin_amdgcn_ds_bpermute(edge_owner_lane(lane) << 2, __float_as_int(sel)));
+  const float gd = j >= 0 ? gdsb[j] : 0.f;
+  const float gc = j >= 0 ? gd * ps_row + dot : 0.f;
+  const float gps = wave_sum(cf * gd);
+  const float grho = wave_sum(p * gc);
+  const float gp = rho * gc;
+  float gl;
+  if (a.compress == 0) {
+    const float pg = wave_sum(p * gp);
+    gl = p * (gp - pg);
+  } else {
+    const float pg = wave_sum(gp * p);
+    const float sg = sign_f(s);
+    gl = sg * (sg * p) * (sg * gp - pg);
+  }
+  gl = j >= 0 ? gl * a.inv_temperature : 0.f;
+  if (lane < a.k) a.g_logit[row * a.k + lane] = gl;
+  const float gsum = wave_sum(gl);
+  if (lane == 0) {
+    if (a.grad_ps) a.grad_ps[row] = gps;
+    if (a.grad_rho) a.grad_rho[row] = grho;
+    a.rowsum[row] = gsum;
+  }
+
+  // dQ partials: group g sums its edges (absent edges read zeros)
+  float4 dqa = make_float4(0.f, 0.f, 0.f, 0.f), dqb = dqa;
+  float dqs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const float gg = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * i + g) << 2, __float_as_int(gl)));
+    const uint32_t koff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ldk * 4u : kOobOffset;
+    if (kvec) {
+      fma4(dqa, gg, buf_load4(rs_key, 4 * c < a.r ? koff + 16u * c : kOobOffset));
+      if (a.r > 64) fma4(dqb, gg, buf_load4(rs_key, 64 + 4 * c < a.r ? koff + 256u + 16u * c : kOobOffset));
+    } else {
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        if (16 * m < a.r) dqs[m] += gg * buf_load1(rs_key, c + 16 * m < a.r ? koff + 4u * (c + 16 * m) : kOobOffset);
+    }
+    if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+  }
+  float* dqrow = a.dq + row * a.lddq;
+  if (kvec) {
+    float v[8] = {dqa.x, dqa.y, dqa.z, dqa.w, dqb.x, dqb.y, dqb.z, dqb.w};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      v[u] += xor16_f(v[u]);
+      v[u] += xor32_f(v[u]);
+    }
+    float lo = v[0], hi = v[4];
+#pragma unroll
+    for (int u = 1; u < 4; ++u) {
+      lo = (g == u) ? v[u] : lo;
+      hi = (g == u) ? v[4 + u] : hi;
+    }
+    const int r0 = 4 * c + g, r1 = 64 + 4 * c + g;
+    if (r0 < a.r) dqrow[r0] = lo * (a.qscale ? a.qscale[r0] : 1.f);
+    if (r1 < a.r) dqrow[r1] = hi * (a.qscale ? a.qscale[r1] : 1.f);
+  } else {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      dqs[m] += xor16_f(dqs[m]);
+      dqs[m] += xor32_f(dqs[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int rr = c + 16 * m;
+      if ((m & 3) == g && rr < a.r) dqrow[rr] = dqs[m] * (a.qscale ? a.qscale[rr] : 1.f);
+    }
+  }
+}
+
+template <int W, int NV>
+static void launch_route_bwd_kp(const RouteRowsBwdArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.k <= 8) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 8>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 16) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 16>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 32) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 32>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 64>), grid, dim3(256), 0, stream, a);
+}
+
+int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream) {
+  if (a.rows == 0) return kOk;
+  JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
+  JN_REQUIRE(a.k >= 1 && a.k <= kWave, kUnsupported, "routes support 1..64 edges per source (got %d)", a.k);
+  JN_REQUIRE(a.compress == 0 || a.compress == 1, kUnsupported, "route compress kind must be 0 or 1");
+  const int64_t blocks = (a.rows + 3) / 4;
+  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
+  JN_REQUIRE((int64_t)a.Nd * a.D * 4 < (1LL << 31) && (int64_t)a.Nd * a.ldk * 4 < (1LL << 31), kUnsupported,
+             "one batch element of the destination rows must stay below 2 GiB");
+  const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
+                   (a.grad_pv == nullptr ||
+                    ((a.ld_gpv % 4 == 0) && (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0));
+  dim3 grid((unsigned)blocks);
+  JN_PROFILE("route_rows_backward_kernel", stream);
+  if (!vec) launch_route_bwd_kp<1, 4>(a, grid, stream);
+  else if (a.D > 256) launch_route_bwd_kp<4, 8>(a, grid, stream);
+  else if (a.D > 128) launch_route_bwd_kp<4, 4>(a, grid, stream);
+  else if (a.D > 64) launch_route_bwd_kp<4, 2>(a, grid, stream);
+  else launch_route_bwd_kp<4, 1>(a, grid, stream);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
+}  // namespace jakal

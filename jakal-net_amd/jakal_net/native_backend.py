@@ -255,15 +255,15 @@ def transition_pairwise_topk_native(
 ) -> LayerDelta:
     if not supports_pairwise_route_kernel(route_fn):
         raise TypeError("Unsupported pairwise route_fn for native sparse transition.")
-    if route_compress_name != "softmax":
-        raise TypeError("Native sparse pairwise transition supports softmax routes only.")
+    if route_compress_name not in ("softmax", "signed_abs_softmax"):
+        raise TypeError("Native sparse pairwise transition supports softmax and signed_abs_softmax routes.")
     spec = pairwise_route_kernel_spec(route_fn)
     return _to_layer_delta(
         _native_module().transition_pairwise_topk(
             spec.kind, spec.source_weight, spec.source_bias, spec.target_weight, spec.target_bias,
             spec.core_weight, spec.bias, spec.hidden_weight, spec.hidden_bias, spec.out_weight, spec.out_bias,
             float(spec.temperature), sender_strength, src_val, dst_val, projected_state, projected_val, topk,
-            src_block_size, dst_block_size,
+            src_block_size, dst_block_size, route_compress_name=route_compress_name,
         )
     )
 

@@ -316,6 +316,15 @@ class SparseTransition(Transition):
     def _native_op_name(self) -> str:
         return "transition_pairwise_topk"
 
+    def _hot_path(self) -> bool:
+        # the HIP top-k route also covers signed |l| softmax routes
+        return (
+            self._route_expects_pairwise_inputs
+            and supports_pairwise_route_kernel(self.route_fn)
+            and self.route_compress_name in ("softmax", "signed_abs_softmax")
+            and not self.use_direction_only
+        )
+
     def _call_native(self, src_layer, dst_layer, projected_val, projected_state, sender) -> LayerDelta:
         return transition_pairwise_topk_native(
             route_fn=self.route_fn,

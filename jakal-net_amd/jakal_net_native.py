@@ -72,6 +72,18 @@ _declare(
      _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 
+_declare("jn_transition_topk_workspace_bytes", [_I64] * 8, _SZ)
+_declare(
+    "jn_transition_topk_forward",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32,
+     _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+_declare(
+    "jn_transition_topk_backward",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+     _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+
 ABI_VERSION = int(_LIB.jn_abi_version())
 
 _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1}
@@ -80,8 +92,11 @@ MAX_TOPK = 32
 _SUPPORTED_OPS = (
     "propagation_topk",
     "propagation_window",
+    "transition_pairwise_topk",
     "low_rank_topk_select",
 )
+_ROUTE_COMPRESS_KINDS = {"softmax": 0, "signed_abs_softmax": 1}
+MAX_ROUTE_TOPK = 32  # below the destination count; every destination up to 64
 
 
 def supported_ops() -> list[str]:
@@ -402,6 +417,182 @@ def propagation_topk(
     ds, dv, _, _ = propagation_topk_selection(
         pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias, edge_compress_name, layer_val,
         projected_state, projected_val, topk, target_block_size, source_block_size,
+    )
+    return ds, dv
+
+
+# ---------------------------------------------------------------------------
+# sparse transition (low-rank pairwise route, top-k destinations per source)
+# ---------------------------------------------------------------------------
+class _TransitionTopK(torch.autograd.Function):
+    """Differentiable SparseTransition routing on the HIP library.
+
+    Inputs (fp32, contiguous): sender strength rho [B,Ns], src_val [B,Ns,Dsrc],
+    dst_val [B,Nd,Ddst], projected_state [B,Ns], projected_val [B,Ns,Dv],
+    Ws [r,Dsrc], Wt [r,Ddst], w [r] (raw), bias [] or None."""
+
+    @staticmethod
+    def forward(ctx, rho, src, dst, ps, pv, Ws, Wt, w, bias, temperature: float, topk: int, compress: int):  # noqa: N803
+        B, Ns, Dsrc = src.shape
+        Nd, Ddst = dst.shape[1], dst.shape[2]
+        Dv = pv.shape[-1]
+        r = Ws.shape[0]
+        k = min(int(topk), Nd)
+        dev = src.device
+        with torch.cuda.device(dev):
+            ds = torch.empty(B, Nd, device=dev, dtype=torch.float32)
+            dv = torch.empty(B, Nd, Dv, device=dev, dtype=torch.float32)
+            sp = torch.empty(B * Ns, r, device=dev, dtype=torch.float32)
+            dp = torch.empty(B * Nd, r, device=dev, dtype=torch.float32)
+            idx = torch.empty(B, Ns, k, device=dev, dtype=torch.int32)
+            logit = torch.empty(B, Ns, k, device=dev, dtype=torch.float32)
+            ws_bytes = int(_LIB.jn_transition_topk_workspace_bytes(B, Ns, Nd, Dsrc, Ddst, Dv, r, topk))
+            ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            _check(
+                _LIB.jn_transition_topk_forward(
+                    _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w), _ptr(bias),
+                    float(temperature), B, Ns, Nd, Dsrc, Ddst, Dv, r, topk, compress,
+                    _ptr(ds), _ptr(dv), _ptr(sp), _ptr(dp), _ptr(idx), _ptr(logit), _ptr(ws), ws_bytes, _stream(dev),
+                )
+            )
+        ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, idx, logit)
+        ctx.meta = (float(temperature), int(topk), compress, bias is not None)
+        ctx.mark_non_differentiable(idx, logit)
+        return ds, dv, idx, logit
+
+    @staticmethod
+    def backward(ctx, g_ds, g_dv, _g_idx=None, _g_logit=None):
+        rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, idx, logit = ctx.saved_tensors
+        temperature, topk, compress, has_bias = ctx.meta
+        B, Ns, Dsrc = src.shape
+        Nd, Ddst = dst.shape[1], dst.shape[2]
+        Dv = pv.shape[-1]
+        r = Ws.shape[0]
+        dev = src.device
+        need = ctx.needs_input_grad
+        with torch.cuda.device(dev):
+            g_ds = torch.zeros(B, Nd, device=dev) if g_ds is None else g_ds.float().contiguous()
+            g_dv = torch.zeros(B, Nd, Dv, device=dev) if g_dv is None else g_dv.float().contiguous()
+            out = [torch.empty_like(t) if n else None for t, n in zip((rho, src, dst, ps, pv), need[:5])]
+            gWs = torch.empty_like(Ws) if need[5] else None
+            gWt = torch.empty_like(Wt) if need[6] else None
+            gw = torch.empty_like(w)
+            gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
+            ws_bytes = int(_LIB.jn_transition_topk_workspace_bytes(B, Ns, Nd, Dsrc, Ddst, Dv, r, topk))
+            ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            _check(
+                _LIB.jn_transition_topk_backward(
+                    _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w),
+                    _ptr(sp), _ptr(dp), _ptr(idx), _ptr(logit), _ptr(g_ds), _ptr(g_dv), float(temperature),
+                    B, Ns, Nd, Dsrc, Ddst, Dv, r, topk, compress,
+                    _ptr(out[0]), _ptr(out[1]), _ptr(out[2]), _ptr(out[3]), _ptr(out[4]), _ptr(gWs), _ptr(gWt),
+                    _ptr(gw), _ptr(gb), _ptr(ws), ws_bytes, _stream(dev),
+                )
+            )
+        return (*out, gWs, gWt, gw if need[7] else None, gb if (has_bias and need[8]) else None, None, None, None)
+
+
+def transition_pairwise_topk_routes(
+    route_kind: str,
+    source_weight: Tensor | None,
+    source_bias: Tensor | None,
+    target_weight: Tensor | None,
+    target_bias: Tensor | None,
+    core_weight: Tensor,
+    bias: Tensor | None,
+    hidden_weight: Tensor | None,
+    hidden_bias: Tensor | None,
+    out_weight: Tensor | None,
+    out_bias: Tensor | None,
+    temperature: float,
+    sender_strength: Tensor,
+    src_val: Tensor,
+    dst_val: Tensor,
+    projected_state: Tensor,
+    projected_val: Tensor,
+    topk: int,
+    src_block_size: int,
+    dst_block_size: int,
+    route_compress_name: str = "softmax",
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Sparse transition returning (delta_state, delta_val, route_index, route_logit).
+
+    Same arguments as ``transition_pairwise_topk``; route_index/route_logit
+    [..., Ns, k] are each source's selected destinations (best first) and
+    their logits."""
+    if route_kind != "low_rank_bilinear_route":
+        raise TypeError(f"jakal_net_native supports route kind 'low_rank_bilinear_route', got {route_kind!r}.")
+    if source_weight is None or target_weight is None:
+        raise RuntimeError("Low-rank bilinear route is missing projection weights.")
+    if source_bias is not None or target_bias is not None or hidden_weight is not None or out_weight is not None:
+        raise TypeError("low_rank_bilinear_route carries no projection biases or hidden layers.")
+    if route_compress_name not in _ROUTE_COMPRESS_KINDS:
+        raise TypeError(f"Unsupported route_compress_name for the HIP backend: {route_compress_name!r}.")
+    if topk <= 0:
+        raise RuntimeError("topk must be positive.")
+    if src_block_size <= 0 or dst_block_size <= 0:
+        raise RuntimeError("block sizes must be positive.")
+    if not temperature > 0:
+        raise RuntimeError("temperature must be positive.")
+    _require_gpu(sender_strength, src_val, dst_val, projected_state, projected_val, source_weight, target_weight,
+                 core_weight, bias)
+    batch_shape = tuple(src_val.shape[:-2])
+    Ns, Dsrc = src_val.shape[-2], src_val.shape[-1]
+    Nd, Ddst = dst_val.shape[-2], dst_val.shape[-1]
+    Dv = projected_val.shape[-1]
+    k = min(int(topk), Nd)
+    if k < Nd and k > MAX_ROUTE_TOPK:
+        raise NotImplementedError(f"HIP sparse transition supports topk <= {MAX_ROUTE_TOPK} (got {k}).")
+    if k == Nd and Nd > 64:
+        raise NotImplementedError("HIP sparse transition over every destination supports up to 64 destinations.")
+    ds, dv, idx, logit = _TransitionTopK.apply(
+        _f32(sender_strength.reshape(-1, Ns)), _f32(src_val.reshape(-1, Ns, Dsrc)),
+        _f32(dst_val.reshape(-1, Nd, Ddst)), _f32(projected_state.reshape(-1, Ns)),
+        _f32(projected_val.reshape(-1, Ns, Dv)), _f32(source_weight), _f32(target_weight), _f32(core_weight),
+        _f32(bias), float(temperature), k, _ROUTE_COMPRESS_KINDS[route_compress_name],
+    )
+    return (
+        ds.reshape(*batch_shape, Nd).to(projected_state.dtype),
+        dv.reshape(*batch_shape, Nd, Dv).to(projected_val.dtype),
+        idx.reshape(*batch_shape, Ns, k),
+        logit.reshape(*batch_shape, Ns, k),
+    )
+
+
+def transition_pairwise_topk(
+    route_kind: str,
+    source_weight: Tensor | None,
+    source_bias: Tensor | None,
+    target_weight: Tensor | None,
+    target_bias: Tensor | None,
+    core_weight: Tensor,
+    bias: Tensor | None,
+    hidden_weight: Tensor | None,
+    hidden_bias: Tensor | None,
+    out_weight: Tensor | None,
+    out_bias: Tensor | None,
+    temperature: float,
+    sender_strength: Tensor,
+    src_val: Tensor,
+    dst_val: Tensor,
+    projected_state: Tensor,
+    projected_val: Tensor,
+    topk: int,
+    src_block_size: int,
+    dst_block_size: int,
+    route_compress_name: str = "softmax",
+) -> tuple[Tensor, Tensor]:
+    """Sparse pairwise transition; signature of jakal_net_native.cpp:6916-6936.
+
+    ``core_weight`` is the raw route weight w; ``source_weight`` and
+    ``target_weight`` the route projections (kernel_common.py:285-294).  The
+    optional trailing ``route_compress_name`` ("softmax" or
+    "signed_abs_softmax") has no counterpart in the reference's composite op,
+    which is softmax-only."""
+    ds, dv, _, _ = transition_pairwise_topk_routes(
+        route_kind, source_weight, source_bias, target_weight, target_bias, core_weight, bias, hidden_weight,
+        hidden_bias, out_weight, out_bias, temperature, sender_strength, src_val, dst_val, projected_state,
+        projected_val, topk, src_block_size, dst_block_size, route_compress_name,
     )
     return ds, dv
 

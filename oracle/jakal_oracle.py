@@ -229,26 +229,48 @@ def normalized_weight_backward(w, g_what):
 # ---------------------------------------------------------------------------
 # transition (transition.py:431-452, kernel_common.py:420-423)
 # ---------------------------------------------------------------------------
-def transition_from_logits(logits, mask, sender, ps, pv):
-    """Per-source softmax over the masked destinations, weighted by the sender
-    strength, summed into destinations (transition.py:449-451)."""
-    p = masked_softmax(logits, mask)
+def route_compress(logits, mask, kind="softmax"):
+    """Route weights over the masked destinations of each source row:
+    softmax (kernel_common.py:420-423) or sign(l) * softmax(|l|)
+    (transition.py:53-67, native_backend.py:2184-2188)."""
+    if kind == "softmax":
+        return masked_softmax(logits, mask)
+    if kind == "signed_abs_softmax":
+        return compress(logits, mask, "signed_abs_softmax")
+    raise ValueError(kind)
+
+
+def route_compress_backward(logits, mask, kind, grad_routes):
+    if kind == "softmax":
+        p = masked_softmax(logits, mask)
+        g = np.asarray(grad_routes, F64)
+        return np.where(mask, p * (g - np.sum(p * g, axis=-1, keepdims=True)), 0.0)
+    if kind == "signed_abs_softmax":
+        return compress_backward(logits, mask, "signed_abs_softmax", grad_routes)
+    raise ValueError(kind)
+
+
+def transition_from_logits(logits, mask, sender, ps, pv, kind="softmax"):
+    """Per-source route weights over the masked destinations, weighted by the
+    sender strength, summed into destinations (transition.py:449-451)."""
+    p = route_compress(logits, mask, kind)
     wr = p * np.asarray(sender, F64)[..., :, None]
     ds = np.einsum("...jk,...j->...k", wr, np.asarray(ps, F64))
     dv = np.einsum("...jk,...jd->...kd", wr, np.asarray(pv, F64))
     return ds, dv, p
 
 
-def transition_forward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, *, topk, temperature=1.0, mask=None):
+def transition_forward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, *, topk, temperature=1.0, mask=None,
+                       kind="softmax"):
     l = lowrank_route_logits(src_val, dst_val, Ws, Wt, w, b, temperature)
     if mask is None:
         mask = topk_mask(l, topk)  # per source row, over destinations (transition.py:439-444)
-    ds, dv, p = transition_from_logits(l, mask, sender, ps, pv)
+    ds, dv, p = transition_from_logits(l, mask, sender, ps, pv, kind)
     return {"delta_state": ds, "delta_val": dv, "logits": l, "mask": mask, "routes": p}
 
 
 def transition_backward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, g_ds, g_dv, *, topk, temperature=1.0,
-                        mask=None):
+                        mask=None, kind="softmax"):
     src_val = np.asarray(src_val, F64)
     dst_val = np.asarray(dst_val, F64)
     sender = np.asarray(sender, F64)
@@ -260,16 +282,15 @@ def transition_backward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, g_ds, g_
     g_ds = np.asarray(g_ds, F64)
     g_dv = np.asarray(g_dv, F64)
     fwd = transition_forward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, topk=topk, temperature=temperature,
-                             mask=mask)
-    p, mask = fwd["routes"], fwd["mask"]
+                             mask=mask, kind=kind)
+    p, mask, logits = fwd["routes"], fwd["mask"], fwd["logits"]
     g_wr = ps[..., :, None] * g_ds[..., None, :] + pv @ np.swapaxes(g_dv, -1, -2)  # [.., Ns, Nd]
     wr = p * sender[..., :, None]
     g_ps = np.sum(wr * g_ds[..., None, :], axis=-1)
     g_pv = wr @ g_dv
     g_sender = np.sum(p * g_wr, axis=-1)
     g_p = g_wr * sender[..., :, None]
-    g_l = p * (g_p - np.sum(p * g_p, axis=-1, keepdims=True))
-    g_l = np.where(mask, g_l, 0.0)
+    g_l = route_compress_backward(logits, mask, kind, g_p)
     g_raw = g_l / float(temperature)
     psrc = src_val @ Ws.T
     psh = psrc * w
@@ -290,6 +311,7 @@ def transition_backward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, g_ds, g_
         "Wt": flat(g_pt).T @ flat(dst_val),
         "w": g_w,
         "b": g_b,
+        "g_logits": g_raw,
     }
 
 

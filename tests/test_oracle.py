@@ -196,7 +196,8 @@ def test_propagation_backward_matches_finite_differences(mode, kind):
     assert np.allclose(g["b"], _fd(loss, b), rtol=1e-5, atol=1e-6)
 
 
-def test_transition_backward_matches_finite_differences():
+@pytest.mark.parametrize("kind", ["softmax", "signed_abs_softmax"])
+def test_transition_backward_matches_finite_differences(kind):
     r = _rng(6)
     B, Ns, Nd, D, Dd, R = 2, 5, 4, 3, 2, 2
     src, dst = r.normal(size=(B, Ns, D)), r.normal(size=(B, Nd, D))
@@ -205,7 +206,7 @@ def test_transition_backward_matches_finite_differences():
     Ws, Wt, w = r.normal(size=(R, D)), r.normal(size=(R, D)), r.normal(size=R)
     b = np.array(-0.1)
     g_ds, g_dv = r.normal(size=(B, Nd)), r.normal(size=(B, Nd, Dd))
-    kw = dict(topk=2, temperature=1.7)
+    kw = dict(topk=2, temperature=1.7, kind=kind)
     mask0 = O.transition_forward(src, dst, sender, ps, pv, Ws, Wt, w, float(b), **kw)["mask"]
 
     def loss():

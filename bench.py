@@ -9,6 +9,9 @@ the jakal_net API with implementation="native".
 Other workloads (--workload), one per hot-path row, same output format:
   c2-window   BASELINE config 2: window propagation, B=8, T=1024, D=384, r=32,
               window 64, val and state ~ N(0,1), default init.
+  c3-transition BASELINE config 3: SparseTransition S->B (1024 -> 256 nodes) then
+              B->S (256 -> 1024), B=8, D=512, r=64, top-16 per source, softmax
+              routes, states and vals ~ N(0,1), default init.
 
 Inputs and parameters are resident in HBM before the timed region.
 
@@ -235,7 +238,120 @@ class WindowC2:
         }
 
 
-WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2())}
+class TransitionC3:
+    name = "c3-transition"
+    metric = "routed pairs/sec + HBM GB/s (% peak), SparseTransition S->B and B->S N_src=1024 N_dst=256 D=512 k=16 fwd+bwd"
+    workload = "C3 SparseTransition S->B then B->S fwd+bwd, LowRankBilinearRoute, softmax routes, native"
+    data = "synthetic (seeded N(0,1) states and vals, default module init)"
+    config = {"batch": 8, "s_nodes": 1024, "b_nodes": 256, "dim": 512, "rank": 64, "topk": 16}
+    traffic_file = "c3_transition_hbm_traffic.json"
+
+    def edges(self) -> int:
+        c = self.config
+        return c["batch"] * (c["s_nodes"] + c["b_nodes"]) * c["topk"]
+
+    def model(self, name):
+        c = self.config
+        B, S, Bn, D, r, k = (c[x] for x in ("batch", "s_nodes", "b_nodes", "dim", "rank", "topk"))
+        E, rows = self.edges(), B * (S + Bn)
+        if name.startswith("lowrank_topk_select_kernel"):
+            return "mfma", 2.0 * B * S * Bn * r * 2  # both directions score S x B pairs
+        if name.startswith("route_rows_backward_kernel"):
+            # per edge: idx + logit + grad-delta row of the destination + its key row + g_logit write;
+            # per source row: its value row, its grad-value write, dq write
+            return "hbm", E * (8.0 + 4.0 * D + 4.0 * r + 4.0) + rows * (8.0 * D + 4.0 * r + 16.0) / 2
+        if name.startswith("route_gather_kernel"):
+            # per edge: edge id + coef + source value row; per destination: delta row write
+            return "hbm", (E * (8.0 + 4.0 * D) + rows * (4.0 * D + 12.0)) / 2
+        if name.startswith("gemm_f32_kernel"):
+            return "mfma", 2.0 * rows * D * r / 2
+        return None
+
+    def sparse_bytes(self) -> float:
+        # SURVEY-style per direction: fwd scatter + bwd gather of dst rows (8DE), src val read twice +
+        # grad written (3*4*D*M_src), dst rows (8*D*M_dst), edge records (24E); summed over both directions
+        c = self.config
+        B, S, Bn, D, k = (c[x] for x in ("batch", "s_nodes", "b_nodes", "dim", "topk"))
+        tot = 0.0
+        for ns, nd in ((S, Bn), (Bn, S)):
+            E = B * ns * k
+            tot += 8 * D * E + 3 * 4 * D * B * ns + 8 * D * B * nd + 24 * E
+        return tot
+
+    def build(self, torch, dev):
+        from jakal_net import Layer, LowRankBilinearRoute, SparseTransition
+
+        c = self.config
+        B, S, Bn, D, r, k = (c[x] for x in ("batch", "s_nodes", "b_nodes", "dim", "rank", "topk"))
+        g = torch.Generator().manual_seed(1003)
+        s_state, s_val = torch.randn(B, S, generator=g), torch.randn(B, S, D, generator=g)
+        b_state, b_val = torch.randn(B, Bn, generator=g), torch.randn(B, Bn, D, generator=g)
+        torch.manual_seed(1003)
+        s_to_b = SparseTransition(LowRankBilinearRoute(D, D, rank=r), topk=k, implementation="native").to(dev)
+        b_to_s = SparseTransition(LowRankBilinearRoute(D, D, rank=r), topk=k, implementation="native").to(dev)
+        s_layer = Layer(dim=D, num_nodes=S, state=s_state.to(dev).requires_grad_(True),
+                        val=s_val.to(dev).requires_grad_(True))
+        b_layer = Layer(dim=D, num_nodes=Bn, state=b_state.to(dev).requires_grad_(True),
+                        val=b_val.to(dev).requires_grad_(True))
+        return _TwoWayTransition(torch, s_to_b, b_to_s, s_layer, b_layer), None
+
+    def cpu_baseline(self, B_sample: int = 2) -> dict:
+        """Oracle (numpy, fp32) forward+backward of both directions on B_sample batch elements."""
+        import numpy as np
+
+        O = _oracle()
+        c = self.config
+        S, Bn, D, r, k = (c[x] for x in ("s_nodes", "b_nodes", "dim", "rank", "topk"))
+        Bs = B_sample
+        rng = np.random.default_rng(1003)
+        bound = 1.0 / math.sqrt(D)
+        times = []
+        layers = {"S": (rng.standard_normal((Bs, S)), rng.standard_normal((Bs, S, D))),
+                  "B": (rng.standard_normal((Bs, Bn)), rng.standard_normal((Bs, Bn, D)))}
+        params = [rng.uniform(-bound, bound, (2, r, D)) for _ in range(2)]
+        with O.compute_dtype(np.float32):
+            for _ in range(3):
+                t0 = time.perf_counter()
+                for (src, dst), (Ws, Wt) in zip((("S", "B"), ("B", "S")), params):
+                    st, sv = layers[src]
+                    _, dv = layers[dst]
+                    rho = O.softplus(st)
+                    nd = dv.shape[1]
+                    O.transition_forward(sv, dv, rho, st, sv, Ws, Wt, np.ones(r), 0.0, topk=k)
+                    O.transition_backward(sv, dv, rho, st, sv, Ws, Wt, np.ones(r), 0.0, np.ones((Bs, nd)),
+                                          np.ones((Bs, nd, D)), topk=k)
+                times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2]
+        return {
+            "value": self.edges() // c["batch"] * Bs / t,
+            "unit": "routed pairs/s",
+            "cores": _threads() or os.cpu_count(),
+            "kind": "port",
+            "sample": f"numpy oracle fp32, forward+backward of both directions, {Bs} of {c['batch']} batch elements "
+                      f"(N_src=1024, N_dst=256, D={D}, r={r}, k={k}), median of 3 ({t:.2f} s each)",
+        }
+
+
+class _TwoWayTransition:
+    """S->B then B->S routing step with the bench's op/layer interface."""
+
+    def __init__(self, torch, s_to_b, b_to_s, s_layer, b_layer):
+        self.torch, self.s_to_b, self.b_to_s, self.s, self.b = torch, s_to_b, b_to_s, s_layer, b_layer
+
+    def zero_grad(self, set_to_none=True):
+        self.s_to_b.zero_grad(set_to_none=set_to_none)
+        self.b_to_s.zero_grad(set_to_none=set_to_none)
+        for layer in (self.s, self.b):
+            layer.val.grad = None
+            layer.state.grad = None
+
+    def loss_terms(self):
+        d1 = self.s_to_b.compute_delta(self.s, self.b)
+        d2 = self.b_to_s.compute_delta(self.b, self.s)
+        return [d1.delta_state, d1.delta_val, d2.delta_state, d2.delta_val]
+
+
+WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3())}
 
 COPY_BYTES = 1 << 30
 
@@ -278,15 +394,23 @@ def main() -> int:
     wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     op, layer = wl.build(torch, dev)
-    ones_s = torch.ones_like(layer.state)
-    ones_v = torch.ones_like(layer.val)
+    if layer is None:  # a multi-module step: op supplies its own loss terms
+        terms = op.loss_terms()
+        ones = [torch.ones_like(t) for t in terms]
 
-    def step() -> None:
-        op.zero_grad(set_to_none=True)
-        layer.val.grad = None
-        layer.state.grad = None
-        delta = op(layer)
-        torch.autograd.backward([delta.delta_state, delta.delta_val], [ones_s, ones_v])
+        def step() -> None:
+            op.zero_grad(set_to_none=True)
+            torch.autograd.backward(op.loss_terms(), ones)
+    else:
+        ones_s = torch.ones_like(layer.state)
+        ones_v = torch.ones_like(layer.val)
+
+        def step() -> None:
+            op.zero_grad(set_to_none=True)
+            layer.val.grad = None
+            layer.state.grad = None
+            delta = op(layer)
+            torch.autograd.backward([delta.delta_state, delta.delta_val], [ones_s, ones_v])
 
     for _ in range(args.warmup):
         step()

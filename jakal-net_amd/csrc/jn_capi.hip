@@ -662,6 +662,7 @@ int jn_transition_topk_forward(const float* sender_strength, const float* src_va
   cb.grad_pv = delta_val;
   cb.ld_gpv = val_dim;
   cb.grad_ps = delta_state;
+  cb.profile_name = "route_gather_kernel";
   return launch_cols_backward(cb, st);
 }
 

@@ -634,7 +634,7 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   const int blocks = (waves + 3) / 4;
   const bool vec = (a.D % 4 == 0) && (a.ld_gpv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
                    (a.grad_pv == nullptr || (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0);
-  JN_PROFILE("cols_backward_kernel", stream);
+  JN_PROFILE(a.profile_name ? a.profile_name : "cols_backward_kernel", stream);
   if (!vec) hipLaunchKernelGGL((cols_backward_kernel<1, 2>), dim3(blocks), dim3(256), 0, stream, a);
   else if (a.D > 256) hipLaunchKernelGGL((cols_backward_kernel<4, 2>), dim3(blocks), dim3(256), 0, stream, a);
   else hipLaunchKernelGGL((cols_backward_kernel<4, 1>), dim3(blocks), dim3(256), 0, stream, a);

@@ -156,6 +156,7 @@ struct ColsBwdArgs {
   float* dk;                 // [B*Nk, r], stride lddk
   int64_t lddk;
   float* part_c;             // [num_waves, r]
+  const char* profile_name;  // label for the kernel timer (null: "cols_backward_kernel")
 };
 int cols_backward_waves(int64_t total_cols, int cols_per_wave);
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream);

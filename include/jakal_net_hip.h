@@ -140,6 +140,44 @@ int jn_propagation_window_backward(const float* layer_val, const float* projecte
                                    void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
 /*
+ * Propagation (dense, every target row aggregates every source) with
+ * LowRankBilinearPairwise:  s = P_t diag(w_hat) P_s^T + b,  e = softsign(s)
+ * (compress_kind 0) or sign(s) * softmax(|s|) over the row (1),
+ * delta_state = e . ps, delta_val = e . pv.  Arguments as
+ * jn_propagation_topk_forward; `edges` [B,N,N] (fp32, caller-allocated)
+ * receives e for the backward.  The two N x N contractions run as batched
+ * MFMA GEMMs over the materialised edge matrix.
+ * Replaces propagation_dense (native/jakal_net_native.cpp:5962-6076) for
+ * source_state = None (the caller folds state weighting into ps and pv,
+ * propagation.py:162-170).
+ */
+int jn_propagation_dense_forward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                 const float* target_weight, const float* source_weight, const float* core_weight,
+                                 const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                 int64_t rank, int32_t compress_kind, float* delta_state, float* delta_val,
+                                 float* projections, float* edges, jn_stream_t stream);
+
+/* Workspace needed by jn_propagation_dense_backward (holds one [B,N,N] matrix). */
+size_t jn_propagation_dense_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                            int64_t rank);
+
+/*
+ * Backward of jn_propagation_dense_forward; arguments as
+ * jn_propagation_topk_backward with the edge matrix in place of the edge list.
+ * The reference differentiates its composite dense op with autograd
+ * (native/jakal_net_native.cpp:5962-6076 has no custom backward).
+ */
+int jn_propagation_dense_backward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                  const float* target_weight, const float* source_weight, const float* core_weight,
+                                  const float* projections, const float* edges, const float* grad_delta_state,
+                                  const float* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim,
+                                  int64_t out_dim, int64_t rank, int32_t compress_kind,
+                                  int32_t projected_val_is_layer_val, float* grad_layer_val,
+                                  float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
+                                  float* grad_source_weight, float* grad_core_weight, float* grad_bias,
+                                  void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+/*
  * SparseTransition with LowRankBilinearRoute (optionally temperature-scaled):
  *   l[j,d]  = ((P_s[j] * w) . P_t[d] + b) / temperature,  P_s = src_val Ws^T,
  *             P_t = dst_val Wt^T, w the raw core weight (modules.py:435-441)

@@ -191,6 +191,42 @@ int check_transition_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t Dsrc,
   return kOk;
 }
 
+struct DenseScratch {
+  float* G;       // [B, N, N] score gradient
+  float* dP;      // [M, 2r]
+  float* rowsum;  // [M]
+  float* part_c;  // [M, r]
+  float* stage;
+  float* splitk;
+  size_t bytes;
+};
+
+DenseScratch carve_dense(void* base, size_t size, int64_t B, int64_t N, int64_t Din, int64_t r) {
+  Workspace ws(base, size);
+  DenseScratch s{};
+  const int64_t M = B * N;
+  s.G = ws.take<float>(B * N * N);
+  s.dP = ws.take<float>(M * 2 * r);
+  s.rowsum = ws.take<float>(M);
+  s.part_c = ws.take<float>(M * r);
+  s.stage = ws.take<float>(finalize_stage_floats((int)r));
+  s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)(2 * r), (int)Din, (int)M) / sizeof(float));
+  s.bytes = ws.used;
+  return s;
+}
+
+int check_dense_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                       int32_t compress_kind) {
+  JN_REQUIRE(batch >= 1 && nodes >= 1 && in_dim >= 1 && out_dim >= 1, kInvalidArgument,
+             "batch, nodes and dims must be positive");
+  JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
+  JN_REQUIRE(compress_kind == 0 || compress_kind == 1, kUnsupported,
+             "compress_kind must be 0 (softsign) or 1 (signed_abs_softmax), got %d", compress_kind);
+  JN_REQUIRE(batch < 65536 && fits_int(batch * nodes) && nodes < (1LL << 22) && fits_int(nodes * out_dim),
+             kUnsupported, "dense propagation shape too large");
+  return kOk;
+}
+
 // Backward of any edge-list propagation (top-k or window): the edge list
 // (edge_index, edge_score) [B*N, k] is what the forward aggregated.
 int propagation_edges_backward(const float* layer_val, const float* projected_state, const float* projected_val,
@@ -784,6 +820,136 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
   // 4. core weight and bias grads
   return launch_finalize_small_grads(s.part_c, cols_backward_waves((int64_t)B * Nd, kColsPerWave), r,
                                      grad_core_weight, 0, s.rowsum, batch * src_nodes, grad_bias, s.stage, st);
+}
+
+int jn_propagation_dense_forward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                 const float* target_weight, const float* source_weight, const float* core_weight,
+                                 const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                 int64_t rank, int32_t compress_kind, float* delta_state, float* delta_val,
+                                 float* projections, float* edges, jn_stream_t stream) {
+  int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
+  if (rc) return rc;
+  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
+                 delta_state && delta_val && projections && edges,
+             kInvalidArgument, "null tensor pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int B = (int)batch, N = (int)nodes, r = (int)rank, D = (int)out_dim;
+  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, B * N, 2 * r,
+                    (int)in_dim, st);
+  if (rc) return rc;
+  // S_b = (P_t diag(w_hat)) P_s^T
+  BatchedGemm sg{};
+  sg.A = projections; sg.lda = 2 * r; sg.a_bs = (int64_t)N * 2 * r; sg.a_kcontig = true;
+  sg.B = projections + r; sg.ldb = 2 * r; sg.b_bs = (int64_t)N * 2 * r; sg.b_kcontig = true;
+  sg.C = edges; sg.ldc = N; sg.c_bs = (int64_t)N * N;
+  sg.a_kscale = core_weight;
+  sg.M = N; sg.N = N; sg.K = r; sg.batch = B;
+  rc = gemm_batched(sg, st, "gemm_f32_kernel<dense_scores>");
+  if (rc) return rc;
+  // E = compress(S + b) in place, delta_state = E ps
+  rc = launch_dense_compress(edges, bias, projected_state, B, N, compress_kind, delta_state, st);
+  if (rc) return rc;
+  // delta_val_b = E_b pv_b
+  BatchedGemm ag{};
+  ag.A = edges; ag.lda = N; ag.a_bs = (int64_t)N * N; ag.a_kcontig = true;
+  ag.B = projected_val; ag.ldb = D; ag.b_bs = (int64_t)N * D; ag.b_kcontig = false;
+  ag.C = delta_val; ag.ldc = D; ag.c_bs = (int64_t)N * D;
+  ag.M = N; ag.N = D; ag.K = N; ag.batch = B;
+  return gemm_batched(ag, st, "gemm_f32_kernel<dense_aggregate>");
+}
+
+size_t jn_propagation_dense_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                            int64_t rank) {
+  (void)out_dim;
+  if (batch < 1 || nodes < 1 || rank < 1) return 0;
+  return carve_dense(nullptr, 0, batch, nodes, in_dim, rank).bytes;
+}
+
+int jn_propagation_dense_backward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                  const float* target_weight, const float* source_weight, const float* core_weight,
+                                  const float* projections, const float* edges, const float* grad_delta_state,
+                                  const float* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim,
+                                  int64_t out_dim, int64_t rank, int32_t compress_kind,
+                                  int32_t projected_val_is_layer_val, float* grad_layer_val,
+                                  float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
+                                  float* grad_source_weight, float* grad_core_weight, float* grad_bias,
+                                  void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
+  if (rc) return rc;
+  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
+                 projections && edges && grad_delta_state && grad_delta_val,
+             kInvalidArgument, "null tensor pointer");
+  JN_REQUIRE(!projected_val_is_layer_val || in_dim == out_dim, kInvalidArgument,
+             "projected_val_is_layer_val requires in_dim == out_dim");
+  DenseScratch s = carve_dense(workspace, workspace_bytes, batch, nodes, in_dim, rank);
+  JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
+             "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int B = (int)batch, N = (int)nodes, r = (int)rank, D = (int)out_dim;
+  const int M = B * N;
+
+  // 1. G_b = gdv_b pv_b^T, then the score gradient in place (+ row sums)
+  BatchedGemm gg{};
+  gg.A = grad_delta_val; gg.lda = D; gg.a_bs = (int64_t)N * D; gg.a_kcontig = true;
+  gg.B = projected_val; gg.ldb = D; gg.b_bs = (int64_t)N * D; gg.b_kcontig = true;
+  gg.C = s.G; gg.ldc = N; gg.c_bs = (int64_t)N * N;
+  gg.M = N; gg.N = N; gg.K = D; gg.batch = B;
+  rc = gemm_batched(gg, st, "gemm_f32_kernel<dense_edge_grad>");
+  if (rc) return rc;
+  rc = launch_dense_compress_backward(s.G, edges, grad_delta_state, projected_state, B, N, compress_kind, s.rowsum,
+                                      st);
+  if (rc) return rc;
+
+  // 2. value and state grads of the sources: E^T gdv, E^T gds
+  float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
+  if (gpv) {
+    BatchedGemm vg{};
+    vg.A = edges; vg.lda = N; vg.a_bs = (int64_t)N * N; vg.a_kcontig = false;
+    vg.B = grad_delta_val; vg.ldb = D; vg.b_bs = (int64_t)N * D; vg.b_kcontig = false;
+    vg.C = gpv; vg.ldc = D; vg.c_bs = (int64_t)N * D;
+    vg.M = N; vg.N = D; vg.K = N; vg.batch = B;
+    rc = gemm_batched(vg, st, "gemm_f32_kernel<dense_value_grad>");
+    if (rc) return rc;
+  }
+  if (grad_projected_state) {
+    rc = launch_dense_colsum(edges, grad_delta_state, B, N, grad_projected_state, st);
+    if (rc) return rc;
+  }
+
+  // 3. projection grads: dP_t = w_hat * (G_s P_s), dP_s = w_hat * (G_s^T P_t) (+ w_hat partials)
+  BatchedGemm tg{};
+  tg.A = s.G; tg.lda = N; tg.a_bs = (int64_t)N * N; tg.a_kcontig = true;
+  tg.B = projections + r; tg.ldb = 2 * r; tg.b_bs = (int64_t)N * 2 * r; tg.b_kcontig = false;
+  tg.C = s.dP; tg.ldc = 2 * r; tg.c_bs = (int64_t)N * 2 * r;
+  tg.c_nscale = core_weight;
+  tg.M = N; tg.N = r; tg.K = N; tg.batch = B;
+  rc = gemm_batched(tg, st, "gemm_f32_kernel<dense_target_grad>");
+  if (rc) return rc;
+  BatchedGemm sg2{};
+  sg2.A = s.G; sg2.lda = N; sg2.a_bs = (int64_t)N * N; sg2.a_kcontig = false;
+  sg2.B = projections; sg2.ldb = 2 * r; sg2.b_bs = (int64_t)N * 2 * r; sg2.b_kcontig = false;
+  sg2.C = s.dP + r; sg2.ldc = 2 * r; sg2.c_bs = (int64_t)N * 2 * r;
+  sg2.M = N; sg2.N = r; sg2.K = N; sg2.batch = B;
+  rc = gemm_batched(sg2, st, "gemm_f32_kernel<dense_source_grad>");
+  if (rc) return rc;
+  rc = launch_scale_grad_partials(s.dP + r, 2 * r, projections + r, 2 * r, core_weight, r, M, s.part_c, st);
+  if (rc) return rc;
+
+  // 4. projection weight and input grads
+  if (grad_target_weight && grad_source_weight) {
+    rc = gemm_grad_weight(s.dP, 2 * r, layer_val, in_dim, grad_target_weight, grad_source_weight, r, 2 * r,
+                          (int)in_dim, M, s.splitk, st);
+    if (rc) return rc;
+  }
+  if (grad_layer_val) {
+    const float* addend = (projected_val_is_layer_val && gpv) ? grad_layer_val : nullptr;
+    rc = gemm_grad_input(s.dP, 2 * r, target_weight, source_weight, r, in_dim, addend, in_dim, grad_layer_val,
+                         in_dim, M, (int)in_dim, 2 * r, st);
+    if (rc) return rc;
+  }
+
+  // 5. w_hat and bias grads
+  return launch_finalize_small_grads(s.part_c, M, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st);
 }
 
 }  // extern "C"

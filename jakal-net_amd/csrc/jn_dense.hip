@@ -1,0 +1,214 @@
+// Dense low-rank propagation over all N x N pairs (gfx950).
+//
+// Propagation with a LowRankBilinearPairwise score (propagation.py:207-220,
+// jakal_net_native.cpp:5962-6076): every target row i aggregates every source
+// j with e[i, j] = compress(s[i, j]),
+//     s = P_t diag(w_hat) P_s^T + b,
+//     compress = softsign (elementwise) or sign(s) * softmax(|s|) over the row,
+//     delta_state[i] = sum_j e[i,j] ps[j],   delta_val[i] = sum_j e[i,j] pv[j].
+// Like the reference's full-dense branch, the edge matrix E [B, N, N] is
+// materialised (in HBM, fp32): the two N x N contractions run as batched MFMA
+// GEMMs (jn_gemm.hip) and the kernels here are the row-wise passes between
+// them (one wavefront per row, float4 lanes over the row):
+//   dense_compress_kernel          : E = compress(S + b) in place, delta_state
+//   dense_compress_backward_kernel : G_s = compress'(E, G + gds (x) ps) in place,
+//                                    and its row sums (bias gradient)
+//   dense_colsum_kernel            : grad ps[j] = sum_i E[i, j] gds[i] (fixed order)
+//   scale_grad_partials_kernel     : w_hat partials and scaling of dP_s
+#include "jn_internal.hpp"
+
+namespace jakal {
+
+// Row r of a [rows, N] matrix: lane l covers floats 4l + 256t (VEC) or l + 64t.
+template <bool VEC>
+__global__ __launch_bounds__(256) void dense_compress_kernel(float* S, const float* bias, const float* ps, int N,
+                                                             int64_t rows, int compress, float* delta_state) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  if (row >= rows) return;
+  const int64_t b = row / N;
+  float* s = S + row * N;
+  const float* psb = ps + b * N;
+  const float bb = bias ? bias[0] : 0.0f;
+  float acc = 0.0f;
+  if (compress == 0) {
+    if constexpr (VEC) {
+      for (int j = 4 * lane; j < N; j += 256) {
+        float4 v = *reinterpret_cast<float4*>(s + j);
+        const float4 p = *reinterpret_cast<const float4*>(psb + j);
+        v.x = softsign_f(v.x + bb);
+        v.y = softsign_f(v.y + bb);
+        v.z = softsign_f(v.z + bb);
+        v.w = softsign_f(v.w + bb);
+        acc += v.x * p.x + v.y * p.y + v.z * p.z + v.w * p.w;
+        *reinterpret_cast<float4*>(s + j) = v;
+      }
+    } else {
+      for (int j = lane; j < N; j += kWave) {
+        const float e = softsign_f(s[j] + bb);
+        acc += e * psb[j];
+        s[j] = e;
+      }
+    }
+  } else {
+    // sign(s) * softmax(|s|) over the row: max, sum of exponentials, then write
+    float m = -INFINITY;
+    for (int j = lane; j < N; j += kWave) m = fmaxf(m, fabsf(s[j] + bb));
+    m = __int_as_float(wave_reduce_i(__float_as_int(m), [](int x, int y) {
+      return __float_as_int(fmaxf(__int_as_float(x), __int_as_float(y)));
+    }));
+    float sum = 0.0f;
+    for (int j = lane; j < N; j += kWave) sum += __expf(fabsf(s[j] + bb) - m);
+    const float inv = 1.0f / wave_sum(sum);
+    for (int j = lane; j < N; j += kWave) {
+      const float x = s[j] + bb;
+      const float e = sign_f(x) * __expf(fabsf(x) - m) * inv;
+      acc += e * psb[j];
+      s[j] = e;
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) delta_state[row] = acc;
+}
+
+// G holds gdv . pv^T on entry; on exit the score gradient
+//   g_e = G + gds[i] ps[j]; softsign: g_s = g_e (1 - |e|)^2 (= g_e / (1 + |s|)^2);
+//   signed |s| softmax: g_s = |e| g_e - e sum_j(g_e e).
+template <bool VEC>
+__global__ __launch_bounds__(256) void dense_compress_backward_kernel(float* G, const float* E, const float* gds,
+                                                                      const float* ps, int N, int64_t rows,
+                                                                      int compress, float* rowsum) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  if (row >= rows) return;
+  const int64_t b = row / N;
+  float* g = G + row * N;
+  const float* e = E + row * N;
+  const float* psb = ps + b * N;
+  const float gs = gds[row];
+  float row_dot = 0.0f;
+  if (compress == 1) {
+    for (int j = lane; j < N; j += kWave) row_dot += (g[j] + gs * psb[j]) * e[j];
+    row_dot = wave_sum(row_dot);
+  }
+  float acc = 0.0f;
+  if (VEC && compress == 0) {
+    for (int j = 4 * lane; j < N; j += 256) {
+      float4 gv = *reinterpret_cast<float4*>(g + j);
+      const float4 ev = *reinterpret_cast<const float4*>(e + j);
+      const float4 pv = *reinterpret_cast<const float4*>(psb + j);
+      const float d0 = 1.0f - fabsf(ev.x), d1 = 1.0f - fabsf(ev.y), d2 = 1.0f - fabsf(ev.z), d3 = 1.0f - fabsf(ev.w);
+      gv.x = (gv.x + gs * pv.x) * d0 * d0;
+      gv.y = (gv.y + gs * pv.y) * d1 * d1;
+      gv.z = (gv.z + gs * pv.z) * d2 * d2;
+      gv.w = (gv.w + gs * pv.w) * d3 * d3;
+      acc += gv.x + gv.y + gv.z + gv.w;
+      *reinterpret_cast<float4*>(g + j) = gv;
+    }
+  } else {
+    for (int j = lane; j < N; j += kWave) {
+      const float ge = g[j] + gs * psb[j];
+      const float ej = e[j];
+      float gsj;
+      if (compress == 0) {
+        const float d = 1.0f - fabsf(ej);
+        gsj = ge * d * d;
+      } else {
+        gsj = fabsf(ej) * ge - ej * row_dot;
+      }
+      acc += gsj;
+      g[j] = gsj;
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) rowsum[row] = acc;
+}
+
+// out[b, j] = sum_i E[b, i, j] * w[b, i]: a workgroup owns 64 columns; wave q
+// sums rows i = q, q + 4, ... and the four partials are added in wave order.
+__global__ __launch_bounds__(256) void dense_colsum_kernel(const float* E, const float* w, int N, int B,
+                                                           float* out) {
+  __shared__ float red[4][64];
+  const int lane = lane_id(), wave = wave_id();
+  const int tiles = (N + 63) / 64;
+  const int b = blockIdx.x / tiles;
+  const int j = (blockIdx.x % tiles) * 64 + lane;
+  float s = 0.0f;
+  if (b < B && j < N) {
+    const float* eb = E + (int64_t)b * N * N;
+    const float* wb = w + (int64_t)b * N;
+    for (int i = wave; i < N; i += 4) s += eb[(int64_t)i * N + j] * wb[i];
+  }
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && b < B && j < N)
+    out[(int64_t)b * N + j] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+}
+
+// part[m, c] = dps[m, c] * ps[m, c] (w_hat gradient partials), then dps *= w_hat.
+__global__ __launch_bounds__(256) void scale_grad_partials_kernel(float* dps, int64_t ld_dps, const float* src,
+                                                                  int64_t ld_src, const float* w_hat, int r,
+                                                                  int64_t rows, float* part) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= rows * r) return;
+  const int64_t m = t / r;
+  const int c = (int)(t % r);
+  const float g = dps[m * ld_dps + c];
+  part[m * r + c] = g * src[m * ld_src + c];
+  dps[m * ld_dps + c] = g * w_hat[c];
+}
+
+int launch_dense_compress(float* S, const float* bias, const float* ps, int B, int N, int compress,
+                          float* delta_state, hipStream_t stream) {
+  const int64_t rows = (int64_t)B * N;
+  const int64_t blocks = (rows + 3) / 4;
+  JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "too many rows");
+  const bool vec = (N % 4 == 0) && ((reinterpret_cast<uintptr_t>(S) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(ps) & 15) == 0);
+  JN_PROFILE("dense_compress_kernel", stream);
+  if (vec) hipLaunchKernelGGL(dense_compress_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, S, bias, ps,
+                              N, rows, compress, delta_state);
+  else hipLaunchKernelGGL(dense_compress_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, S, bias, ps,
+                          N, rows, compress, delta_state);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
+int launch_dense_compress_backward(float* G, const float* E, const float* gds, const float* ps, int B, int N,
+                                   int compress, float* rowsum, hipStream_t stream) {
+  const int64_t rows = (int64_t)B * N;
+  const int64_t blocks = (rows + 3) / 4;
+  JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "too many rows");
+  const bool vec = (N % 4 == 0) && ((reinterpret_cast<uintptr_t>(G) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(E) & 15) == 0) && ((reinterpret_cast<uintptr_t>(ps) & 15) == 0);
+  JN_PROFILE("dense_compress_backward_kernel", stream);
+  if (vec) hipLaunchKernelGGL(dense_compress_backward_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, G,
+                              E, gds, ps, N, rows, compress, rowsum);
+  else hipLaunchKernelGGL(dense_compress_backward_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, G, E,
+                          gds, ps, N, rows, compress, rowsum);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
+int launch_dense_colsum(const float* E, const float* w, int B, int N, float* out, hipStream_t stream) {
+  const int64_t blocks = (int64_t)B * ((N + 63) / 64);
+  JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "too many columns");
+  JN_PROFILE("dense_colsum_kernel", stream);
+  hipLaunchKernelGGL(dense_colsum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, E, w, N, B, out);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
+int launch_scale_grad_partials(float* dps, int64_t ld_dps, const float* src, int64_t ld_src, const float* w_hat,
+                               int r, int64_t rows, float* part, hipStream_t stream) {
+  const int64_t n = rows * r;
+  if (n == 0) return kOk;
+  JN_REQUIRE((n + 255) / 256 < (1LL << 31), kUnsupported, "too many rows");
+  JN_PROFILE("scale_grad_partials_kernel", stream);
+  hipLaunchKernelGGL(scale_grad_partials_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, dps,
+                     ld_dps, src, ld_src, w_hat, r, rows, part);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
+}  // namespace jakal

@@ -32,6 +32,11 @@ struct GemmArgs {
   int M, N, K;
   int k_chunk;             // K range per blockIdx.z (split-K)
   int64_t c_split_stride;  // C offset per blockIdx.z
+  // batched mode (batch > 1): blockIdx.z is the batch index (no split-K)
+  int batch;
+  int64_t a_bs, b_bs, c_bs, add_bs;  // per-batch element strides
+  const float* a_kscale;   // optional: A(m, k) *= a_kscale[k]
+  const float* c_nscale;   // optional: C(m, n) = acc * c_nscale[n] (+ addend)
 };
 
 constexpr int kGBM = 64, kGBN = 64, kGBK = 16, kGStride = kGBK + 4;
@@ -53,9 +58,16 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 
   const int m0 = blockIdx.y * kGBM;
   const int n0 = blockIdx.x * kGBN;
-  const int kbeg = blockIdx.z * g.k_chunk;
+  const bool batched = g.batch > 1;
+  const int split = batched ? 0 : blockIdx.z;
+  const int64_t bz = batched ? blockIdx.z : 0;
+  const int kbeg = split * g.k_chunk;
   const int kend = min(g.K, kbeg + g.k_chunk);
-  float* C = g.C + (int64_t)blockIdx.z * g.c_split_stride;
+  const float* gA = g.A + bz * g.a_bs;
+  const float* gB0 = g.B0 + bz * g.b_bs;
+  const float* gB1 = g.B1 + bz * g.b_bs;
+  const float* gadd = g.addend ? g.addend + bz * g.add_bs : nullptr;
+  float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
 
   // Each thread moves 4 A values and 4 B values per K slice.
   float ra[4], rb[4];
@@ -64,7 +76,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
     // ---- A ----
     if (A_KC) {
       int m = m0 + tid / 4, kq = k0 + (tid % 4) * 4;
-      const float* p = g.A + (int64_t)m * g.lda + kq;
+      const float* p = gA + (int64_t)m * g.lda + kq;
       if (m < g.M && kq + 3 < kend && aligned16(p)) {
         float4 v = *reinterpret_cast<const float4*>(p);
         ra[0] = v.x; ra[1] = v.y; ra[2] = v.z; ra[3] = v.w;
@@ -74,7 +86,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
       }
     } else {
       int kk = k0 + tid / 16, mq = m0 + (tid % 16) * 4;
-      const float* p = g.A + (int64_t)kk * g.lda + mq;
+      const float* p = gA + (int64_t)kk * g.lda + mq;
       if (kk < kend && mq + 3 < g.M && aligned16(p)) {
         float4 v = *reinterpret_cast<const float4*>(p);
         ra[0] = v.x; ra[1] = v.y; ra[2] = v.z; ra[3] = v.w;
@@ -83,10 +95,22 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
         for (int q = 0; q < 4; ++q) ra[q] = (kk < kend && mq + q < g.M) ? p[q] : 0.0f;
       }
     }
+    if (g.a_kscale) {
+      if (A_KC) {
+        const int kq = k0 + (tid % 4) * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ra[q] *= (kq + q < kend) ? g.a_kscale[kq + q] : 0.0f;
+      } else {
+        const int kk = k0 + tid / 16;
+        const float sc = kk < kend ? g.a_kscale[kk] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ra[q] *= sc;
+      }
+    }
     // ---- B ----
     if (B_KC) {
       int n = n0 + tid / 4, kq = k0 + (tid % 4) * 4;
-      const float* base = (n < g.b_split) ? g.B0 + (int64_t)n * g.ldb : g.B1 + (int64_t)(n - g.b_split) * g.ldb;
+      const float* base = (n < g.b_split) ? gB0 + (int64_t)n * g.ldb : gB1 + (int64_t)(n - g.b_split) * g.ldb;
       const float* p = base + kq;
       if (n < g.N && kq + 3 < kend && aligned16(p)) {
         float4 v = *reinterpret_cast<const float4*>(p);
@@ -97,7 +121,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
       }
     } else {
       int kk = k0 + tid / 16, nq = n0 + (tid % 16) * 4;
-      const float* base = (kk < g.b_split) ? g.B0 + (int64_t)kk * g.ldb : g.B1 + (int64_t)(kk - g.b_split) * g.ldb;
+      const float* base = (kk < g.b_split) ? gB0 + (int64_t)kk * g.ldb : gB1 + (int64_t)(kk - g.b_split) * g.ldb;
       const float* p = base + nq;
       if (kk < kend && nq + 3 < g.N && aligned16(p)) {
         float4 v = *reinterpret_cast<const float4*>(p);
@@ -175,7 +199,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
         int n = n0 + wn * 32 + nt * 16 + col;
         if (m < g.M && n < g.N) {
           float x = acc[mt][nt][v];
-          if (g.addend) x += g.addend[(int64_t)m * g.ld_add + n];
+          if (g.c_nscale) x *= g.c_nscale[n];
+          if (gadd) x += gadd[(int64_t)m * g.ld_add + n];
           C[(int64_t)m * g.ldc + n] = x;
         }
       }
@@ -209,13 +234,31 @@ int launch_gemm(const GemmArgs& g, bool a_kcontig, bool b_kcontig, int splits, h
   JN_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, kInvalidArgument, "negative GEMM extent");
   if (g.M == 0 || g.N == 0) return kOk;
   JN_PROFILE(name, stream);
-  dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, splits), block(256);
+  JN_REQUIRE(g.batch <= 1 || splits == 1, kInvalidArgument, "batched GEMM has no split-K");
+  JN_REQUIRE(g.batch < 65536 && splits < 65536, kUnsupported, "GEMM batch or split count too large");
+  JN_REQUIRE((g.M + kGBM - 1) / kGBM < 65536, kUnsupported, "GEMM M extent too large");
+  dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, g.batch > 1 ? g.batch : splits), block(256);
   if (a_kcontig && b_kcontig) hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, block, 0, stream, g);
   else if (a_kcontig && !b_kcontig) hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, block, 0, stream, g);
   else if (!a_kcontig && !b_kcontig) hipLaunchKernelGGL((gemm_f32_kernel<false, false>), grid, block, 0, stream, g);
   else hipLaunchKernelGGL((gemm_f32_kernel<false, true>), grid, block, 0, stream, g);
   JN_LAUNCH_CHECK();
   return kOk;
+}
+
+// Batched C_b = op(A_b) . op(B_b) for b < batch (see BatchedGemm).
+int gemm_batched(const BatchedGemm& m, hipStream_t stream, const char* name) {
+  GemmArgs g{};
+  g.A = m.A; g.lda = m.lda; g.a_bs = m.a_bs;
+  g.B0 = m.B; g.B1 = m.B; g.ldb = m.ldb; g.b_bs = m.b_bs; g.b_split = 1 << 30;
+  g.C = m.C; g.ldc = m.ldc; g.c_bs = m.c_bs;
+  g.addend = m.addend; g.ld_add = m.ld_add; g.add_bs = m.add_bs;
+  g.M = m.M; g.N = m.N; g.K = m.K;
+  g.k_chunk = m.K; g.c_split_stride = 0;
+  g.batch = m.batch;
+  g.a_kscale = m.a_kscale;
+  g.c_nscale = m.c_nscale;
+  return launch_gemm(g, m.a_kcontig, m.b_kcontig, 1, stream, name);
 }
 
 // C[M][N] = X[M][K] . [W0;W1]^T with W0 rows [0, split) and W1 rows [split, N).

@@ -29,6 +29,20 @@ int gemm_grad_input(const float* dP, int64_t ldp, const float* W0, const float* 
                     const float* addend, int64_t ld_add, float* dX, int64_t ldx, int M, int N, int K,
                     hipStream_t stream);
 size_t gemm_grad_weight_workspace(int M, int N, int K);
+// Batched fp32 GEMM C_b[M][N] = A_b . B_b (+ addend_b), b < batch.
+//   A(m, k) = a_kcontig ? A[m*lda + k] : A[k*lda + m], times a_kscale[k] if given
+//   B(k, n) = b_kcontig ? B[n*ldb + k] : B[k*ldb + n]
+//   C(m, n) = sum_k A(m,k) B(k,n), times c_nscale[n] if given, plus addend
+struct BatchedGemm {
+  const float* A; int64_t lda, a_bs; bool a_kcontig;
+  const float* B; int64_t ldb, b_bs; bool b_kcontig;
+  float* C; int64_t ldc, c_bs;
+  const float* addend; int64_t ld_add, add_bs;
+  const float* a_kscale;
+  const float* c_nscale;
+  int M, N, K, batch;
+};
+int gemm_batched(const BatchedGemm& m, hipStream_t stream, const char* name);
 int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, float* out0, float* out1, int m_split,
                      int M, int N, int K, float* partial, hipStream_t stream);
 
@@ -121,6 +135,15 @@ struct RouteRowsBwdArgs {
   float* rowsum;         // [rows]
 };
 int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream);
+
+// ---- dense propagation (jn_dense.hip) --------------------------------------
+int launch_dense_compress(float* S, const float* bias, const float* ps, int B, int N, int compress,
+                          float* delta_state, hipStream_t stream);
+int launch_dense_compress_backward(float* G, const float* E, const float* gds, const float* ps, int B, int N,
+                                   int compress, float* rowsum, hipStream_t stream);
+int launch_dense_colsum(const float* E, const float* w, int B, int N, float* out, hipStream_t stream);
+int launch_scale_grad_partials(float* dps, int64_t ld_dps, const float* src, int64_t ld_src, const float* w_hat,
+                               int r, int64_t rows, float* part, hipStream_t stream);
 
 struct CsrArgs {
   const int32_t* idx;

@@ -84,6 +84,17 @@ _declare(
      _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 
+_declare(
+    "jn_propagation_dense_forward",
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P],
+)
+_declare("jn_propagation_dense_workspace_bytes", [_I64] * 5, _SZ)
+_declare(
+    "jn_propagation_dense_backward",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
+     _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+
 ABI_VERSION = int(_LIB.jn_abi_version())
 
 _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1}
@@ -92,6 +103,7 @@ MAX_TOPK = 32
 _SUPPORTED_OPS = (
     "propagation_topk",
     "propagation_window",
+    "propagation_dense",
     "transition_pairwise_topk",
     "low_rank_topk_select",
 )
@@ -270,6 +282,107 @@ class _PropagationEdges(torch.autograd.Function):
         )
 
 
+class _PropagationDense(torch.autograd.Function):
+    """Differentiable dense low-rank propagation on the HIP library (edge
+    matrix materialised).  Inputs as _PropagationEdges."""
+
+    @staticmethod
+    def forward(ctx, X, ps, pv, V, U, w_hat, bias, compress: int):  # noqa: N803
+        B, N, Din = X.shape
+        pv_is_x = pv is None
+        pv_t = X if pv_is_x else pv
+        Dout = pv_t.shape[-1]
+        r = U.shape[0]
+        dev = X.device
+        with torch.cuda.device(dev):
+            ds = torch.empty(B, N, device=dev, dtype=torch.float32)
+            dv = torch.empty(B, N, Dout, device=dev, dtype=torch.float32)
+            proj = torch.empty(B * N, 2 * r, device=dev, dtype=torch.float32)
+            edges = torch.empty(B, N, N, device=dev, dtype=torch.float32)
+            _check(
+                _LIB.jn_propagation_dense_forward(
+                    _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
+                    B, N, Din, Dout, r, compress, _ptr(ds), _ptr(dv), _ptr(proj), _ptr(edges), _stream(dev),
+                )
+            )
+        ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, edges)
+        ctx.meta = (compress, pv_is_x, bias is not None)
+        return ds, dv
+
+    @staticmethod
+    def backward(ctx, g_ds, g_dv):
+        X, ps, pv, V, U, w_hat, proj, edges = ctx.saved_tensors
+        compress, pv_is_x, has_bias = ctx.meta
+        B, N, Din = X.shape
+        Dout = pv.shape[-1]
+        r = U.shape[0]
+        dev = X.device
+        need = ctx.needs_input_grad
+        with torch.cuda.device(dev):
+            g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
+            g_dv = torch.zeros(B, N, Dout, device=dev) if g_dv is None else g_dv.float().contiguous()
+            gX = torch.empty_like(X) if need[0] else None
+            gps = torch.empty_like(ps) if need[1] else None
+            gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
+            gV, gU, gw = torch.empty_like(V), torch.empty_like(U), torch.empty_like(w_hat)
+            gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
+            ws_bytes = int(_LIB.jn_propagation_dense_workspace_bytes(B, N, Din, Dout, r))
+            ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            _check(
+                _LIB.jn_propagation_dense_backward(
+                    _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(proj), _ptr(edges),
+                    _ptr(g_ds), _ptr(g_dv), B, N, Din, Dout, r, compress, 1 if pv_is_x else 0,
+                    _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
+                    _ptr(ws), ws_bytes, _stream(dev),
+                )
+            )
+        return (gX, gps, gpv, gV if need[3] else None, gU if need[4] else None, gw if need[5] else None,
+                gb if (has_bias and need[6]) else None, None)
+
+
+def propagation_dense(
+    pairwise_kind: str,
+    weight: Tensor,
+    bias: Tensor | None,
+    in_weight: Tensor | None,
+    in_bias: Tensor | None,
+    out_weight: Tensor | None,
+    out_bias: Tensor | None,
+    edge_compress_name: str,
+    layer_val: Tensor,
+    projected_state: Tensor,
+    projected_val: Tensor,
+    source_state: Tensor | None,
+    target_block_size: int,
+    source_block_size: int,
+) -> tuple[Tensor, Tensor]:
+    """Dense propagation over all N x N pairs; signature of jakal_net_native.cpp:5962-5976.
+
+    With ``source_state`` the edges are weighted by it per source, which
+    equals the unweighted op on (source_state, source_state * projected_val)
+    (jakal_net_native.cpp:5991-6015); the fold is done here, differentiably."""
+    w_hat, bias, V, U = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias)
+    if edge_compress_name not in _COMPRESS_KINDS:
+        raise RuntimeError(f"Unsupported edge_compress_name for the HIP backend: {edge_compress_name!r}.")
+    if target_block_size <= 0 or source_block_size <= 0:
+        raise RuntimeError("block sizes must be positive.")
+    _require_gpu(layer_val, projected_state, projected_val, w_hat, V, U, bias, source_state)
+    if source_state is not None and source_state.numel() > 0:
+        projected_val = projected_val * source_state.unsqueeze(-1)
+        projected_state = source_state
+    batch_shape = tuple(layer_val.shape[:-2])
+    N, Din = layer_val.shape[-2], layer_val.shape[-1]
+    Dout = projected_val.shape[-1]
+    pv_is_x = _same_storage_view(projected_val, layer_val)
+    X = _f32(layer_val.reshape(-1, N, Din))
+    ps = _f32(projected_state.reshape(-1, N))
+    pv = None if pv_is_x else _f32(projected_val.reshape(-1, N, Dout))
+    ds, dv = _PropagationDense.apply(X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias),
+                                     _COMPRESS_KINDS[edge_compress_name])
+    return (ds.reshape(*batch_shape, N).to(projected_state.dtype),
+            dv.reshape(*batch_shape, N, Dout).to(projected_val.dtype))
+
+
 def _lowrank_pairwise_args(kind, weight, bias, in_weight, in_bias, out_weight, out_bias):
     if kind != "low_rank_bilinear":
         raise TypeError(f"jakal_net_native supports pairwise kind 'low_rank_bilinear', got {kind!r}.")
@@ -413,7 +526,13 @@ def propagation_topk(
     """Top-k propagation; signature of jakal_net_native.cpp:6305-6319.
 
     ``weight`` is the normalised core weight, ``in_weight`` the source and
-    ``out_weight`` the target projection (kernel_common.py:185-192)."""
+    ``out_weight`` the target projection (kernel_common.py:185-192).  With
+    k >= N every source is kept, which is dense propagation
+    (propagation.py:471, kernel_common.py:433-440)."""
+    if topk >= layer_val.shape[-2]:
+        return propagation_dense(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
+                                 edge_compress_name, layer_val, projected_state, projected_val, None,
+                                 target_block_size, source_block_size)
     ds, dv, _, _ = propagation_topk_selection(
         pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias, edge_compress_name, layer_val,
         projected_state, projected_val, topk, target_block_size, source_block_size,

@@ -1,0 +1,194 @@
+"""GPU parity of dense low-rank propagation (HIP library) against the numpy oracle.
+
+Dense propagation keeps every (target, source) pair (propagation.py:207-220);
+values and gradients are compared with the float64 oracle within rtol 1e-4 /
+atol 1e-5 (fp32).  Gradients are long sums (over N sources and D dims) whose
+terms can cancel, so their atol is 1e-5 times the largest magnitude in the
+tensor (norm-wise).  At the full C4-dense shape the oracle is evaluated on
+sampled rows.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import jakal_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-5
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import jakal_net_native  # noqa: F401  (fails loudly when the library is missing)
+
+    return torch.device("cuda:0")
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _close(got, want, rtol=RTOL, atol=ATOL, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    err = np.abs(got - want) - (atol + rtol * np.abs(want))
+    assert err.max() <= 0, f"{what}: max excess {err.max():.3e} (max abs diff {np.abs(got - want).max():.3e})"
+
+
+def _normwise(got, want, what):
+    want = np.asarray(want, dtype=np.float64)
+    _close(got, want, atol=ATOL * max(1.0, float(np.abs(want).max())), what=what)
+
+
+def _inputs(seed, B, N, D, r):
+    g = torch.Generator().manual_seed(seed)
+    state = torch.randn(B, N, generator=g)
+    val = torch.randn(B, N, D, generator=g)
+    bound = math.sqrt(6.0 / (D + r))
+    U = torch.empty(r, D).uniform_(-bound, bound, generator=g)
+    V = torch.empty(r, D).uniform_(-bound, bound, generator=g)
+    w = torch.rand(r, generator=g) + 0.5
+    return g, state, val, U, V, w
+
+
+@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax"])
+@pytest.mark.parametrize("separate_pv", [False, True])
+@pytest.mark.parametrize("N,with_bias", [(64, True), (37, False)])
+def test_dense_forward_backward_matches_oracle(dev, compress, separate_pv, N, with_bias):
+    import jakal_net_native as jn
+
+    B, D, r = 2, 24, 6
+    g, state, val, U, V, w = _inputs(4001 + N, B, N, D, r)
+    b = torch.tensor(0.15) if with_bias else None
+    pv_cpu = torch.randn(B, N, D, generator=g) if separate_pv else val
+    w_hat = w / w.norm()
+    X = val.to(dev).requires_grad_(True)
+    ps = state.to(dev).requires_grad_(True)
+    pv = pv_cpu.to(dev).requires_grad_(True) if separate_pv else X
+    Ud, Vd = U.to(dev).requires_grad_(True), V.to(dev).requires_grad_(True)
+    wd = w_hat.to(dev).requires_grad_(True)
+    bd = b.to(dev).requires_grad_(True) if with_bias else None
+    ds, dv = jn.propagation_dense("low_rank_bilinear", wd, bd, Vd, None, Ud, None, compress, X, ps, pv, None, N, N)
+    gds = torch.randn(B, N, generator=g)
+    gdv = torch.randn(B, N, D, generator=g)
+    torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
+
+    bval = float(b) if with_bias else 0.0
+    ref = O.propagation_forward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), bval, mode="dense",
+                                kind=compress)
+    _close(_np(ds), ref["delta_state"], what="delta_state")
+    _close(_np(dv), ref["delta_val"], what="delta_val")
+    gr = O.propagation_backward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), bval, _np(gds),
+                                _np(gdv), mode="dense", kind=compress)
+    _normwise(_np(X.grad), gr["val"] + (0.0 if separate_pv else gr["pv"]), "grad layer_val")
+    _normwise(_np(ps.grad), gr["ps"], "grad projected_state")
+    if separate_pv:
+        _normwise(_np(pv.grad), gr["pv"], "grad projected_val")
+    gs = gr["g_scores"]
+    scale = max(1.0, float(np.abs(gs).sum() / math.sqrt(gs.size)))
+    params = [(Ud, "U"), (Vd, "V"), (wd, "w_hat")] + ([(bd, "b")] if with_bias else [])
+    for t, name in params:
+        want = np.asarray(gr[name])
+        _close(_np(t.grad), want, atol=ATOL * max(scale, float(np.abs(want).max())), what=f"grad {name}")
+
+
+def test_topk_with_k_at_least_n_is_dense(dev):
+    import jakal_net_native as jn
+
+    B, N, D, r = 2, 40, 16, 4
+    _, state, val, U, V, w = _inputs(4101, B, N, D, r)
+    w_hat = (w / w.norm()).to(dev)
+    args = ("low_rank_bilinear", w_hat, None, V.to(dev), None, U.to(dev), None, "softsign", val.to(dev),
+            state.to(dev), val.to(dev))
+    a = jn.propagation_topk(*args, N + 5, N, N)
+    b = jn.propagation_dense(*args, None, N, N)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    ref = O.propagation_forward(_np(val), _np(state), _np(val), _np(U), _np(V), _np(w), 0.0, mode="dense",
+                                kind="softsign")
+    _close(_np(a[1]), ref["delta_val"], what="delta_val")
+
+
+def test_dense_source_state_weighting(dev):
+    # edges weighted by the source state == unweighted op on (w, w * pv) (jakal_net_native.cpp:5991-6015)
+    import jakal_net_native as jn
+
+    B, N, D, r = 2, 32, 8, 4
+    g, state, val, U, V, w = _inputs(4201, B, N, D, r)
+    sw = torch.rand(B, N, generator=g) + 0.1
+    w_hat = w / w.norm()
+    ds, dv = jn.propagation_dense("low_rank_bilinear", w_hat.to(dev), None, V.to(dev), None, U.to(dev), None,
+                                  "softsign", val.to(dev), state.to(dev), val.to(dev), sw.to(dev), N, N)
+    s = O.lowrank_pairwise_scores(_np(val), _np(val), _np(U), _np(V), _np(w), 0.0)
+    e = (s / (1 + np.abs(s))) * _np(sw)[:, None, :]
+    _close(_np(ds), e.sum(-1), what="state-weighted delta_state")
+    _close(_np(dv), e @ _np(val), what="state-weighted delta_val")
+
+
+def test_dense_propagation_api_native_matches_reference(dev):
+    from jakal_net import Layer, LowRankBilinearPairwise, Propagation
+
+    torch.manual_seed(61)
+    layer = Layer(dim=6, num_nodes=13, state=torch.randn(2, 13, device=dev), val=torch.randn(2, 13, 6, device=dev))
+    kw = dict(state_proj_fn=lambda s: s * 0.75 + 0.5, val_proj_fn=lambda v: v * 2.0 - 1.0)
+    ref = Propagation(LowRankBilinearPairwise(6, 3).to(dev), implementation="reference", **kw)
+    nat = Propagation(LowRankBilinearPairwise(6, 3).to(dev), implementation="native", **kw)
+    nat.pairwise_fn.load_state_dict(ref.pairwise_fn.state_dict())
+    a, b = ref.compute_delta(layer), nat.compute_delta(layer)
+    assert torch.allclose(a.delta_state, b.delta_state, atol=1e-5, rtol=1e-5)
+    assert torch.allclose(a.delta_val, b.delta_val, atol=1e-5, rtol=1e-5)
+
+
+def test_dense_medium_shape_backward(dev):
+    """B=2, N=512, D=64, r=16: full oracle forward and backward."""
+    import jakal_net_native as jn
+
+    B, N, D, r = 2, 512, 64, 16
+    g, state, val, U, V, w = _inputs(4301, B, N, D, r)
+    w_hat = w / w.norm()
+    X = val.to(dev).requires_grad_(True)
+    ps = state.to(dev).requires_grad_(True)
+    Ud, Vd, wd = (t.to(dev).requires_grad_(True) for t in (U, V, w_hat))
+    ds, dv = jn.propagation_dense("low_rank_bilinear", wd, None, Vd, None, Ud, None, "signed_abs_softmax", X, ps, X,
+                                  None, N, N)
+    gds, gdv = torch.randn(B, N, generator=g), torch.randn(B, N, D, generator=g)
+    torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
+    ref = O.propagation_forward(_np(val), _np(state), _np(val), _np(U), _np(V), _np(w), 0.0, mode="dense",
+                                kind="signed_abs_softmax")
+    _close(_np(ds), ref["delta_state"], what="delta_state")
+    _close(_np(dv), ref["delta_val"], what="delta_val")
+    gr = O.propagation_backward(_np(val), _np(state), _np(val), _np(U), _np(V), _np(w), 0.0, _np(gds), _np(gdv),
+                                mode="dense", kind="signed_abs_softmax")
+    _normwise(_np(X.grad), gr["val"] + gr["pv"], "grad layer_val")
+    _normwise(_np(ps.grad), gr["ps"], "grad projected_state")
+    for t, name in ((Ud, "U"), (Vd, "V"), (wd, "w_hat")):
+        _normwise(_np(t.grad), gr[name], f"grad {name}")
+
+
+def test_c4_dense_shape_forward_sampled_rows(dev):
+    """BASELINE config 4, dense variant: B=16, N=4096, D=512, r=64, softsign;
+    delta rows recomputed in float64 for sampled (batch, row) pairs."""
+    import jakal_net_native as jn
+
+    g = torch.Generator().manual_seed(1004)
+    B, N, D, r = 16, 4096, 512, 64
+    state = torch.randn(B, N, generator=g)
+    val = torch.randn(B, N, D, generator=g)
+    val = val / val.norm(dim=-1, keepdim=True)
+    U = torch.nn.Linear(D, r, bias=False).weight.detach()
+    V = torch.nn.Linear(D, r, bias=False).weight.detach()
+    w_hat = torch.ones(r) / math.sqrt(r)
+    Xd = val.to(dev)
+    ds, dv = jn.propagation_dense("low_rank_bilinear", w_hat.to(dev), None, V.to(dev), None, U.to(dev), None,
+                                  "softsign", Xd, state.to(dev), Xd, None, N, N)
+    rows = torch.randint(0, N, (6,), generator=g)
+    for bb in (0, 9, 15):
+        vb = val[bb].double()
+        s = (vb[rows] @ U.double().T) @ ((vb @ V.double().T) * w_hat.double()).T  # [6, N]
+        e = s / (1 + s.abs())
+        _close(_np(dv[bb, rows]), (e @ vb).numpy(), what="C4-dense delta_val rows")
+        _close(_np(ds[bb, rows]), (e @ state[bb].double()).numpy(), what="C4-dense delta_state rows")

@@ -12,6 +12,8 @@ Other workloads (--workload), one per hot-path row, same output format:
   c3-transition BASELINE config 3: SparseTransition S->B (1024 -> 256 nodes) then
               B->S (256 -> 1024), B=8, D=512, r=64, top-16 per source, softmax
               routes, states and vals ~ N(0,1), default init.
+  c4-dense    BASELINE config 4, dense variant: Propagation over all N x N pairs,
+              B=16, N=4096, D=512, r=64, softsign, inputs as c4-topk.
 
 Inputs and parameters are resident in HBM before the timed region.
 
@@ -332,6 +334,93 @@ class TransitionC3:
         }
 
 
+class DenseC4:
+    name = "c4-dense"
+    metric = "routed pairs/sec + MFMA TFLOP/s (% peak), Propagation dense N=4096 D=512 r=64 fwd+bwd"
+    workload = "C4-dense Propagation fwd+bwd (all N x N pairs), LowRankBilinearPairwise, softsign, native"
+    data = "synthetic (seeded N(0,1) state, unit-norm N(0,1) val rows, default module init)"
+    config = {"batch": 16, "nodes": 4096, "dim": 512, "rank": 64}
+    traffic_file = "c4_dense_hbm_traffic.json"
+
+    def edges(self) -> int:
+        c = self.config
+        return c["batch"] * c["nodes"] * c["nodes"]
+
+    def model(self, name):
+        c = self.config
+        B, N, D, r = (c[x] for x in ("batch", "nodes", "dim", "rank"))
+        dense = {
+            "gemm_f32_kernel<dense_scores>": 2.0 * B * N * N * r,
+            "gemm_f32_kernel<dense_aggregate>": 2.0 * B * N * N * D,
+            "gemm_f32_kernel<dense_edge_grad>": 2.0 * B * N * N * D,
+            "gemm_f32_kernel<dense_value_grad>": 2.0 * B * N * N * D,
+            "gemm_f32_kernel<dense_target_grad>": 2.0 * B * N * N * r,
+            "gemm_f32_kernel<dense_source_grad>": 2.0 * B * N * N * r,
+        }
+        if name in dense:
+            return "mfma", dense[name]
+        if name.startswith("dense_compress_backward_kernel"):
+            return "hbm", 4.0 * 3 * B * N * N  # read G and E, write G_s
+        if name.startswith("dense_compress_kernel"):
+            return "hbm", 4.0 * 2 * B * N * N  # read S, write E
+        if name.startswith("dense_colsum_kernel"):
+            return "hbm", 4.0 * B * N * N
+        if name.startswith("gemm_f32_kernel"):
+            return "mfma", 2.0 * B * N * D * 2 * r
+        return None
+
+    def sparse_bytes(self) -> float:
+        # dense: no gathers; the MFMA work is the bound (see roofline)
+        c = self.config
+        return 4.0 * 6 * c["batch"] * c["nodes"] * c["nodes"]
+
+    def build(self, torch, dev):
+        from jakal_net import Layer, LowRankBilinearPairwise, Propagation
+
+        B, N, D, r = (self.config[x] for x in ("batch", "nodes", "dim", "rank"))
+        g = torch.Generator().manual_seed(1004)
+        state = torch.randn(B, N, generator=g)
+        val = torch.randn(B, N, D, generator=g)
+        val = val / val.norm(dim=-1, keepdim=True)
+        torch.manual_seed(1004)
+        op = Propagation(LowRankBilinearPairwise(D, r), implementation="native").to(dev)
+        return op, Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True),
+                         val=val.to(dev).requires_grad_(True))
+
+    def cpu_baseline(self, B_sample: int = 1) -> dict:
+        """Oracle (numpy, fp32) dense forward+backward on B_sample batch elements."""
+        import numpy as np
+
+        O = _oracle()
+        N, D, r = (self.config[x] for x in ("nodes", "dim", "rank"))
+        rng = np.random.default_rng(1004)
+        val = rng.standard_normal((B_sample, N, D)).astype(np.float32)
+        val /= np.linalg.norm(val, axis=-1, keepdims=True)
+        state = rng.standard_normal((B_sample, N)).astype(np.float32)
+        bound = 1.0 / math.sqrt(D)
+        U = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
+        V = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
+        w = np.ones(r, dtype=np.float32)
+        g_ds = np.ones((B_sample, N), np.float32)
+        g_dv = np.ones((B_sample, N, D), np.float32)
+        times = []
+        with O.compute_dtype(np.float32):
+            for _ in range(3):
+                t0 = time.perf_counter()
+                O.propagation_forward(val, state, val, U, V, w, 0.0, mode="dense")
+                O.propagation_backward(val, state, val, U, V, w, 0.0, g_ds, g_dv, mode="dense")
+                times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2]
+        return {
+            "value": B_sample * N * N / t,
+            "unit": "routed pairs/s",
+            "cores": _threads() or os.cpu_count(),
+            "kind": "port",
+            "sample": f"numpy oracle fp32, dense forward+backward, {B_sample} of {self.config['batch']} batch "
+                      f"elements (N={N}, D={D}, r={r}), median of 3 ({t:.2f} s each)",
+        }
+
+
 class _TwoWayTransition:
     """S->B then B->S routing step with the bench's op/layer interface."""
 
@@ -351,7 +440,7 @@ class _TwoWayTransition:
         return [d1.delta_state, d1.delta_val, d2.delta_state, d2.delta_val]
 
 
-WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3())}
+WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3(), DenseC4())}
 
 COPY_BYTES = 1 << 30
 

@@ -844,7 +844,7 @@ int jn_propagation_dense_forward(const float* layer_val, const float* projected_
   sg.C = edges; sg.ldc = N; sg.c_bs = (int64_t)N * N;
   sg.a_kscale = core_weight;
   sg.M = N; sg.N = N; sg.K = r; sg.batch = B;
-  rc = gemm_batched(sg, st, "gemm_f32_kernel<dense_scores>");
+  rc = gemm_batched(sg, kGemmDenseScores, st);
   if (rc) return rc;
   // E = compress(S + b) in place, delta_state = E ps
   rc = launch_dense_compress(edges, bias, projected_state, B, N, compress_kind, delta_state, st);
@@ -855,7 +855,7 @@ int jn_propagation_dense_forward(const float* layer_val, const float* projected_
   ag.B = projected_val; ag.ldb = D; ag.b_bs = (int64_t)N * D; ag.b_kcontig = false;
   ag.C = delta_val; ag.ldc = D; ag.c_bs = (int64_t)N * D;
   ag.M = N; ag.N = D; ag.K = N; ag.batch = B;
-  return gemm_batched(ag, st, "gemm_f32_kernel<dense_aggregate>");
+  return gemm_batched(ag, kGemmDenseAggregate, st);
 }
 
 size_t jn_propagation_dense_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
@@ -894,7 +894,7 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
   gg.B = projected_val; gg.ldb = D; gg.b_bs = (int64_t)N * D; gg.b_kcontig = true;
   gg.C = s.G; gg.ldc = N; gg.c_bs = (int64_t)N * N;
   gg.M = N; gg.N = N; gg.K = D; gg.batch = B;
-  rc = gemm_batched(gg, st, "gemm_f32_kernel<dense_edge_grad>");
+  rc = gemm_batched(gg, kGemmDenseEdgeGrad, st);
   if (rc) return rc;
   rc = launch_dense_compress_backward(s.G, edges, grad_delta_state, projected_state, B, N, compress_kind, s.rowsum,
                                       st);
@@ -908,7 +908,7 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
     vg.B = grad_delta_val; vg.ldb = D; vg.b_bs = (int64_t)N * D; vg.b_kcontig = false;
     vg.C = gpv; vg.ldc = D; vg.c_bs = (int64_t)N * D;
     vg.M = N; vg.N = D; vg.K = N; vg.batch = B;
-    rc = gemm_batched(vg, st, "gemm_f32_kernel<dense_value_grad>");
+    rc = gemm_batched(vg, kGemmDenseValueGrad, st);
     if (rc) return rc;
   }
   if (grad_projected_state) {
@@ -923,14 +923,14 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
   tg.C = s.dP; tg.ldc = 2 * r; tg.c_bs = (int64_t)N * 2 * r;
   tg.c_nscale = core_weight;
   tg.M = N; tg.N = r; tg.K = N; tg.batch = B;
-  rc = gemm_batched(tg, st, "gemm_f32_kernel<dense_target_grad>");
+  rc = gemm_batched(tg, kGemmDenseTargetGrad, st);
   if (rc) return rc;
   BatchedGemm sg2{};
   sg2.A = s.G; sg2.lda = N; sg2.a_bs = (int64_t)N * N; sg2.a_kcontig = false;
   sg2.B = projections; sg2.ldb = 2 * r; sg2.b_bs = (int64_t)N * 2 * r; sg2.b_kcontig = false;
   sg2.C = s.dP + r; sg2.ldc = 2 * r; sg2.c_bs = (int64_t)N * 2 * r;
   sg2.M = N; sg2.N = r; sg2.K = N; sg2.batch = B;
-  rc = gemm_batched(sg2, st, "gemm_f32_kernel<dense_source_grad>");
+  rc = gemm_batched(sg2, kGemmDenseSourceGrad, st);
   if (rc) return rc;
   rc = launch_scale_grad_partials(s.dP + r, 2 * r, projections + r, 2 * r, core_weight, r, M, s.part_c, st);
   if (rc) return rc;

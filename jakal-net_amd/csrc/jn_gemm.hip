@@ -45,7 +45,10 @@ __device__ __forceinline__ bool aligned16(const float* p) { return (reinterpret_
 
 // A(m,k): A_KC -> A[m*lda + k] else A[k*lda + m]
 // B(k,n): B_KC -> Bsel(n)[n'*ldb + k] (split along n), else Bsel(k)[k'*ldb + n] (split along k)
-template <bool A_KC, bool B_KC>
+// USE tags the call site (GemmUse): the code is the same for a given layout,
+// but every use gets its own kernel symbol so profilers attribute time and
+// traffic per use.
+template <bool A_KC, bool B_KC, int USE>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
   __shared__ __align__(16) float sA[2][kGBM * kGStride];
   __shared__ __align__(16) float sB[2][kGBN * kGStride];
@@ -230,24 +233,58 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
   }
 }
 
-int launch_gemm(const GemmArgs& g, bool a_kcontig, bool b_kcontig, int splits, hipStream_t stream, const char* name) {
+// Layout (A k-contiguous, B k-contiguous) and timer label of every GEMM use.
+struct GemmUseInfo {
+  bool a_kc, b_kc;
+  const char* name;
+};
+constexpr GemmUseInfo kGemmUses[] = {
+    {true, true, "gemm_f32_kernel<project>"},
+    {true, false, "gemm_f32_kernel<grad_input>"},
+    {false, false, "gemm_f32_kernel<grad_weight>"},
+    {true, true, "gemm_f32_kernel<dense_scores>"},
+    {true, false, "gemm_f32_kernel<dense_aggregate>"},
+    {true, true, "gemm_f32_kernel<dense_edge_grad>"},
+    {false, false, "gemm_f32_kernel<dense_value_grad>"},
+    {true, false, "gemm_f32_kernel<dense_target_grad>"},
+    {false, false, "gemm_f32_kernel<dense_source_grad>"},
+};
+
+template <int USE>
+static void launch_use(const GemmArgs& g, dim3 grid, hipStream_t stream) {
+  constexpr GemmUseInfo u = kGemmUses[USE];
+  hipLaunchKernelGGL((gemm_f32_kernel<u.a_kc, u.b_kc, USE>), grid, dim3(256), 0, stream, g);
+}
+
+int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) {
   JN_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, kInvalidArgument, "negative GEMM extent");
   if (g.M == 0 || g.N == 0) return kOk;
-  JN_PROFILE(name, stream);
   JN_REQUIRE(g.batch <= 1 || splits == 1, kInvalidArgument, "batched GEMM has no split-K");
   JN_REQUIRE(g.batch < 65536 && splits < 65536, kUnsupported, "GEMM batch or split count too large");
   JN_REQUIRE((g.M + kGBM - 1) / kGBM < 65536, kUnsupported, "GEMM M extent too large");
-  dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, g.batch > 1 ? g.batch : splits), block(256);
-  if (a_kcontig && b_kcontig) hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, block, 0, stream, g);
-  else if (a_kcontig && !b_kcontig) hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, block, 0, stream, g);
-  else if (!a_kcontig && !b_kcontig) hipLaunchKernelGGL((gemm_f32_kernel<false, false>), grid, block, 0, stream, g);
-  else hipLaunchKernelGGL((gemm_f32_kernel<false, true>), grid, block, 0, stream, g);
+  dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, g.batch > 1 ? g.batch : splits);
+  JN_PROFILE(kGemmUses[use].name, stream);
+  switch (use) {
+    case kGemmProject: launch_use<kGemmProject>(g, grid, stream); break;
+    case kGemmGradInput: launch_use<kGemmGradInput>(g, grid, stream); break;
+    case kGemmGradWeight: launch_use<kGemmGradWeight>(g, grid, stream); break;
+    case kGemmDenseScores: launch_use<kGemmDenseScores>(g, grid, stream); break;
+    case kGemmDenseAggregate: launch_use<kGemmDenseAggregate>(g, grid, stream); break;
+    case kGemmDenseEdgeGrad: launch_use<kGemmDenseEdgeGrad>(g, grid, stream); break;
+    case kGemmDenseValueGrad: launch_use<kGemmDenseValueGrad>(g, grid, stream); break;
+    case kGemmDenseTargetGrad: launch_use<kGemmDenseTargetGrad>(g, grid, stream); break;
+    case kGemmDenseSourceGrad: launch_use<kGemmDenseSourceGrad>(g, grid, stream); break;
+    default: JN_REQUIRE(false, kInvalidArgument, "unknown GEMM use %d", (int)use);
+  }
   JN_LAUNCH_CHECK();
   return kOk;
 }
 
 // Batched C_b = op(A_b) . op(B_b) for b < batch (see BatchedGemm).
-int gemm_batched(const BatchedGemm& m, hipStream_t stream, const char* name) {
+int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
+  JN_REQUIRE(use >= kGemmDenseScores && use <= kGemmDenseSourceGrad && m.a_kcontig == kGemmUses[use].a_kc &&
+                 m.b_kcontig == kGemmUses[use].b_kc,
+             kInvalidArgument, "batched GEMM layout does not match its use");
   GemmArgs g{};
   g.A = m.A; g.lda = m.lda; g.a_bs = m.a_bs;
   g.B0 = m.B; g.B1 = m.B; g.ldb = m.ldb; g.b_bs = m.b_bs; g.b_split = 1 << 30;
@@ -258,7 +295,7 @@ int gemm_batched(const BatchedGemm& m, hipStream_t stream, const char* name) {
   g.batch = m.batch;
   g.a_kscale = m.a_kscale;
   g.c_nscale = m.c_nscale;
-  return launch_gemm(g, m.a_kcontig, m.b_kcontig, 1, stream, name);
+  return launch_gemm(g, use, 1, stream);
 }
 
 // C[M][N] = X[M][K] . [W0;W1]^T with W0 rows [0, split) and W1 rows [split, N).
@@ -270,7 +307,7 @@ int gemm_project(const float* X, int64_t ldx, const float* W0, const float* W1, 
   g.C = C; g.ldc = ldc;
   g.M = M; g.N = N; g.K = K;
   g.k_chunk = K; g.c_split_stride = 0;
-  return launch_gemm(g, true, true, 1, stream, "gemm_f32_kernel<project>");
+  return launch_gemm(g, kGemmProject, 1, stream);
 }
 
 // dX[M][N] = dP[M][K] . [W0;W1] (+ addend), W0 rows [0, split) of K.
@@ -284,7 +321,7 @@ int gemm_grad_input(const float* dP, int64_t ldp, const float* W0, const float* 
   g.addend = addend; g.ld_add = ld_add;
   g.M = M; g.N = N; g.K = K;
   g.k_chunk = K; g.c_split_stride = 0;
-  return launch_gemm(g, true, false, 1, stream, "gemm_f32_kernel<grad_input>");
+  return launch_gemm(g, kGemmGradInput, 1, stream);
 }
 
 size_t gemm_grad_weight_workspace(int M, int N, int K) {
@@ -305,7 +342,7 @@ int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, 
   g.C = partial; g.ldc = N;
   g.M = M; g.N = N; g.K = K;
   g.k_chunk = k_chunk; g.c_split_stride = (int64_t)M * N;
-  int rc = launch_gemm(g, false, false, splits, stream, "gemm_f32_kernel<grad_weight>");
+  int rc = launch_gemm(g, kGemmGradWeight, splits, stream);
   if (rc != kOk) return rc;
   const int64_t total = (int64_t)M * N;
   JN_REQUIRE((total + 63) / 64 < (1LL << 31), kUnsupported, "weight gradient too large");

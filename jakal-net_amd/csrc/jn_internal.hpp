@@ -42,7 +42,12 @@ struct BatchedGemm {
   const float* c_nscale;
   int M, N, K, batch;
 };
-int gemm_batched(const BatchedGemm& m, hipStream_t stream, const char* name);
+enum GemmUse {
+  kGemmProject, kGemmGradInput, kGemmGradWeight,
+  kGemmDenseScores, kGemmDenseAggregate, kGemmDenseEdgeGrad, kGemmDenseValueGrad, kGemmDenseTargetGrad,
+  kGemmDenseSourceGrad,
+};
+int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream);
 int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, float* out0, float* out1, int m_split,
                      int M, int N, int K, float* partial, hipStream_t stream);
 

@@ -20,7 +20,7 @@ struct SelectArgs {
   float* out_score;     // [B, Nq, k]
 };
 int launch_topk_select(const SelectArgs& a, hipStream_t stream);
-constexpr int kSelectMaxK = 32;
+constexpr int kSelectMaxK = 64;
 
 // ---- fp32 MFMA GEMMs (jn_gemm.hip) ----------------------------------------
 int gemm_project(const float* X, int64_t ldx, const float* W0, const float* W1, int split, int64_t ldw, float* C,

@@ -47,9 +47,14 @@ constexpr int kSelWaves = 4;
 constexpr int kSelRowsPerWave = 16;
 constexpr int kSelRows = kSelWaves * kSelRowsPerWave;  // 64 query rows / workgroup
 constexpr int kSelChunk = 32;                          // key rows per LDS chunk
-constexpr int kSelKeep = kSelectMaxK;                  // kept-entry region per row
-constexpr int kSelMergeAt = 64;                        // merge once this many candidates wait
-constexpr int kSelSlots = kSelKeep + kSelMergeAt - 1 + kSelChunk;  // 127 used
+// A row's 128 slots hold a kept region of KEEP entries (the k <= KEEP best so
+// far; KEEP = 32 for k <= 32, 64 for k <= 64) followed by the candidates
+// appended since the last merge.  A merge runs once a row holds
+// merge_at(KEEP) candidates; one more chunk can add 32, so the largest slot
+// used is KEEP + merge_at - 1 + 32 - 1 = 126 either way.
+__host__ __device__ constexpr int merge_at(int keep) { return keep == 32 ? 64 : 32; }
+constexpr int kSelSlots = 32 + merge_at(32) - 1 + kSelChunk;  // 127 used (KEEP = 32)
+static_assert(64 + merge_at(64) - 1 + kSelChunk == kSelSlots, "both kept-region sizes use the same slots");
 // Row strides are 16-byte multiples (vector reads) that shift successive rows by
 // 4 LDS banks, so the 16 rows of a wave read and write on distinct banks.
 constexpr int kSelScoreStride = 132;  // floats
@@ -91,13 +96,15 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// Merge one row: keep the k best of its k kept entries and `cnt` candidates,
-// compacted to slots [0, k); returns the new k-th best score (wave-uniform).
-__device__ float merge_row(float* row_s, uint16_t* row_i, int k, int cnt) {
+// Merge one row: keep the k best of its `kept` kept entries (slots [0, kept))
+// and `cnt` candidates (slots [KEEP, KEEP + cnt)), k < kept + cnt, compacted
+// to slots [0, k); returns the new k-th best score (wave-uniform).
+template <int KEEP>
+__device__ float merge_row(float* row_s, uint16_t* row_i, int k, int kept, int cnt) {
   const int lane = lane_id();
-  const int n_used = kSelKeep + cnt;
+  const int n_used = KEEP + cnt;
   const int sa = lane, sb = 64 + lane;
-  const bool va = (sa < k) || (sa >= kSelKeep && sa < n_used);
+  const bool va = (sa < kept) || (sa >= KEEP && sa < n_used);
   const bool vb = sb < n_used;
   float fa = 0.f, fb = 0.f;
   int ia = 0, ib = 0;
@@ -198,16 +205,22 @@ __device__ __forceinline__ float key_to_float(uint32_t key) {
 }
 
 // Merge every row of the wave at once.  Lane (g, col) owns slots
-// [32g, 32g+32) of row col: the k kept entries (g == 0) or candidates.  The
-// radix select runs per lane over its 32 keys, with row counts summed over the
-// row's 4 lanes by permlane swaps.  Rows with exact ties at the k-th value
-// return fallback = true and are left untouched for merge_row.
-__device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int cnt_row, float& theta,
+// [32g, 32g+32) of row col: kept entries or candidates.  A row keeps the
+// min(k, kept + cnt) best of its `kept` kept entries and `cnt` candidates (a
+// row that has not yet seen k keys keeps them all and its threshold stays
+// -inf).  The radix select runs per lane over its 32 keys, with row counts
+// summed over the row's 4 lanes by permlane swaps.  Rows with exact ties at
+// the k-th value return fallback = true and are left untouched for merge_row.
+template <int KEEP>
+__device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kept, int cnt_row, float& theta,
                                    bool& fallback) {
   const int lane = lane_id();
   const int g = lane >> 4;
   const int base = 32 * g;
-  const int n_valid = (g == 0) ? k : max(0, min(32, kSelKeep + cnt_row - base));
+  const int total = kept + cnt_row;
+  const int kk = min(k, total);  // entries the row keeps
+  // kept entries [0, kept), then cnt_row candidates from KEEP on
+  const int n_valid = base < KEEP ? max(0, min(32, kept - base)) : max(0, min(32, KEEP + cnt_row - base));
   uint32_t key[32];
   int id[32];
 #pragma unroll
@@ -244,7 +257,9 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int cnt
   uint32_t t = diff ? (hi & ~((2u << start) - 1u)) : hi;  // shared prefix of the row's keys
   if (start == 31) t = 0;
   const int wave_start = (int)wave_max_u32((uint32_t)(start + 1)) - 1;  // uniform loop bound
-  bool done = false;
+  // a row whose entries all fit keeps every valid key (valid keys are > 0)
+  bool done = total <= k;
+  if (done) t = 0;
   for (int bit = wave_start; bit >= 0; --bit) {
     if (!__ballot(!done)) break;
     const uint32_t c = t | (1u << bit);
@@ -253,9 +268,9 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int cnt
     for (int i = 0; i < 32; ++i) cnt += (key[i] >= c) ? 1 : 0;
     int n = cnt + xor16_i(cnt);
     n += xor32_i(n);
-    if (!done && n >= k) {
+    if (!done && n >= kk) {
       t = c;
-      done = (n == k);
+      done = (n == kk);
     }
   }
   // winners: exactly k keys >= t (done), or the k-th largest key is t itself
@@ -284,7 +299,7 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int cnt
     gt += xor32_i(gt);
     eq += xor16_i(eq);
     eq += xor32_i(eq);
-    tie_row = (eq != k - gt);
+    tie_row = (eq != kk - gt);
 #pragma unroll
     for (int i = 0; i < 32; ++i) keep_bits |= ((i < n_valid) && key[i] >= t) ? (1u << i) : 0u;
     theta_key = t;
@@ -305,14 +320,15 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int cnt
       row_i[dst] = (uint16_t)id[i];
       pos += kp ? 1 : 0;
     }
-    theta = key_to_float(theta_key);
+    theta = total < k ? -INFINITY : key_to_float(theta_key);
   }
   wave_lds_sync();
 }
 
 // VEC: r == 4*RQ and 16-byte aligned key rows -> unconditional float4 chunk loads.
-template <int RQ, bool VEC>
+template <int RQ, bool VEC, int KEEP>
 __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs a) {
+  constexpr int kMergeAt = merge_at(KEEP);
   constexpr int RP = 4 * RQ;
   constexpr int KSTRIDE = RP + 4;  // padded key row (floats)
 
@@ -341,12 +357,6 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
   for (int i = tid; i < RP; i += blockDim.x) s_scale[i] = (i < a.r) ? (a.scale ? a.scale[i] : 1.0f) : 0.0f;
   if (!VEC)
     for (int i = tid; i < 2 * kSelChunk * KSTRIDE; i += blockDim.x) (&s_key[0][0])[i] = 0.0f;
-  // the kept region starts as k sentinels that lose to every finite score
-  for (int i = tid; i < kSelRows * kSelKeep; i += blockDim.x) {
-    const int rrow = i / kSelKeep, e = i % kSelKeep;
-    s_slot_s[rrow * kSelScoreStride + e] = -INFINITY;
-    s_slot_i[rrow * kSelIndexStride + e] = 0xffff;
-  }
   __syncthreads();
 
   // ---- query fragment in registers ------------------------------------------
@@ -436,6 +446,7 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
 
   float theta = row_ok ? -INFINITY : INFINITY;  // invalid rows never admit
   int cnt = 0;                                  // candidates waiting for this lane's row
+  int kept = 0;                                 // valid kept entries of this lane's row (<= k)
   float* my_slot_s = s_slot_s + lrow * kSelScoreStride;
   uint16_t* my_slot_i = s_slot_i + lrow * kSelIndexStride;
 
@@ -494,7 +505,7 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
       const int n3 = xor16_i(n2);
       const int excl = (g == 0) ? 0 : (g == 1) ? n1 : (g == 2) ? (n2 + n3) : (n1 + n2 + n3);
       const int total = np + n1 + n2 + n3;
-      int pos = kSelKeep + cnt + excl;
+      int pos = KEEP + cnt + excl;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const bool ok = (pass_mask >> u) & 1u;
@@ -509,21 +520,24 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
 
     // -- merge rows whose candidates filled up (or everything at the end) --
     const bool last = (c + 1 == nchunks);
-    if (__ballot(lane < kSelRowsPerWave && (cnt >= kSelMergeAt || (last && cnt > 0)))) {
+    if (__ballot(lane < kSelRowsPerWave && (cnt >= kMergeAt || (last && cnt > 0)))) {
       bool fallback;
-      merge_rows_batched(my_slot_s, my_slot_i, k, cnt, theta, fallback);
-      // rows with exact ties at the k-th value: exact per-row merge
+      merge_rows_batched<KEEP>(my_slot_s, my_slot_i, k, kept, cnt, theta, fallback);
+      // rows with exact ties at the k-th value: exact per-row merge (such a
+      // row holds more than k entries, so the merge fills it)
       uint64_t m = __ballot(lane < kSelRowsPerWave && fallback);
       while (m) {
         const int t = __builtin_ctzll(m);
         m &= m - 1;
         const int row_cnt = readlane_i(cnt, t);
+        const int row_kept = readlane_i(kept, t);
         const int slot = wave * kSelRowsPerWave + t;
-        const float th =
-            merge_row(s_slot_s + slot * kSelScoreStride, s_slot_i + slot * kSelIndexStride, k, row_cnt);
+        const float th = merge_row<KEEP>(s_slot_s + slot * kSelScoreStride, s_slot_i + slot * kSelIndexStride, k,
+                                         row_kept, row_cnt);
         if (col == t) theta = th;
       }
       if (!row_ok) theta = INFINITY;  // rows past Nq stay closed
+      kept = min(k, kept + cnt);
       cnt = 0;
     }
 
@@ -554,12 +568,18 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
 
 template <int RQ>
 static void launch_rq(const SelectArgs& a, bool vec, dim3 grid, hipStream_t stream) {
-  if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false>), grid, dim3(256), 0, stream, a);
+  if (a.k <= 32) {
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 32>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 32>), grid, dim3(256), 0, stream, a);
+  } else {
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 64>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 64>), grid, dim3(256), 0, stream, a);
+  }
 }
 
 int launch_topk_select(const SelectArgs& a, hipStream_t stream) {
-  JN_REQUIRE(a.k >= 1 && a.k <= kSelKeep, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)", kSelKeep, a.k);
+  JN_REQUIRE(a.k >= 1 && a.k <= kSelectMaxK, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)", kSelectMaxK,
+             a.k);
   JN_REQUIRE(a.k < a.Nk, kInvalidArgument, "top-k select needs k < key count (k=%d, Nk=%d)", a.k, a.Nk);
   JN_REQUIRE(a.Nk <= kSelMaxKeys, kUnsupported, "top-k select supports at most %d keys (got %d)", kSelMaxKeys, a.Nk);
   JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128] (got %d)", a.r);

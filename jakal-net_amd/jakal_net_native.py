@@ -98,7 +98,7 @@ _declare(
 ABI_VERSION = int(_LIB.jn_abi_version())
 
 _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1}
-MAX_TOPK = 32
+MAX_TOPK = 64
 
 _SUPPORTED_OPS = (
     "propagation_topk",
@@ -108,7 +108,7 @@ _SUPPORTED_OPS = (
     "low_rank_topk_select",
 )
 _ROUTE_COMPRESS_KINDS = {"softmax": 0, "signed_abs_softmax": 1}
-MAX_ROUTE_TOPK = 32  # below the destination count; every destination up to 64
+MAX_ROUTE_TOPK = 64  # below the destination count; every destination up to 64
 
 
 def supported_ops() -> list[str]:

@@ -65,7 +65,8 @@ def _check_select(idx, score, ref_scores, k):
 
 
 @pytest.mark.parametrize("r,k,Nq,Nk", [(3, 2, 9, 9), (16, 8, 256, 256), (64, 32, 200, 333), (64, 1, 70, 50),
-                                       (32, 16, 130, 1024), (100, 5, 64, 97)])
+                                       (32, 16, 130, 1024), (100, 5, 64, 97), (64, 33, 100, 300),
+                                       (16, 48, 150, 49), (64, 64, 257, 2000), (8, 64, 64, 65)])
 def test_select_matches_oracle(dev, r, k, Nq, Nk):
     import jakal_net_native as jn
 
@@ -110,13 +111,12 @@ def _c1_inputs(seed=1001, B=2, N=256, D=64, r=16):
 
 
 @pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax"])
-@pytest.mark.parametrize("separate_pv", [False, True])
-def test_propagation_topk_forward_backward_matches_oracle(dev, compress, separate_pv):
+@pytest.mark.parametrize("separate_pv,k", [(False, 8), (True, 8), (True, 64)])
+def test_propagation_topk_forward_backward_matches_oracle(dev, compress, separate_pv, k):
     import jakal_net_native as jn
 
     state, val, U, V, w, b = _c1_inputs()
     B, N, D = val.shape
-    k = 8
     g = torch.Generator().manual_seed(7)
     pv_cpu = torch.randn(B, N, D, generator=g) if separate_pv else val
     w_hat = w / w.norm()
@@ -136,7 +136,7 @@ def test_propagation_topk_forward_backward_matches_oracle(dev, compress, separat
     # the selection the forward aggregated, against float64 scores
     scores = O.lowrank_pairwise_scores(_np(val), _np(val), _np(U), _np(V), _np(w), float(b))
     frac = _check_select(idx.cpu().numpy(), score.cpu().numpy(), scores, k)
-    assert frac > 0.9
+    assert frac > (0.9 if k <= 8 else 0.5)  # deeper cuts sit in denser parts of the score distribution
     mask = O.mask_from_indices(idx.cpu().numpy(), N)
     ref = O.propagation_forward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), float(b),
                                 mode="topk", topk=k, kind=compress, mask=mask)

@@ -113,6 +113,10 @@ def test_transition_forward_backward_matches_oracle(dev, kind, temperature):
     _run(dev, 3001, B=2, Ns=64, Nd=16, Dsrc=32, Ddst=24, r=8, topk=4, temperature=temperature, kind=kind)
 
 
+def test_transition_topk_above_32(dev):
+    _run(dev, 3004, B=2, Ns=80, Nd=100, Dsrc=16, Ddst=12, r=4, topk=48, temperature=1.1, kind="signed_abs_softmax")
+
+
 @pytest.mark.parametrize("topk", [16, 40])
 def test_transition_every_destination(dev, topk):
     # k >= Nd keeps every destination (transition.py:437-440)

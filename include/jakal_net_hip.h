@@ -48,7 +48,7 @@ int jn_profile_collect(char* buffer, size_t size);
  *   s[b,i,j] = ((sum_r query[b,i,r]*cq[r] * key[b,j,r]*ck[r]) + bias) / temperature
  * where the scale vector multiplies the query rows when scale_on_query != 0,
  * else the key rows.  Writes the k best (j, s) per row, sorted descending,
- * ties toward the lower j.  1 <= k <= 32, k < nk, 1 <= rank <= 128.
+ * ties toward the lower j.  1 <= k <= 64, k < nk, 1 <= rank <= 128.
  * Replaces the score/select stage of
  *   propagation_topk            (native/jakal_net_native.cpp:6399-6424)
  *   low_rank_propagation_topk_forward_cuda (native/jakal_net_native_cuda.cu:1028-1110)
@@ -190,7 +190,7 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
  * projected_state [B,Ns], projected_val [B,Ns,Dv], Ws [r,Dsrc], Wt [r,Ddst],
  * w [r], bias scalar or NULL.  Outputs delta_state [B,Nd], delta_val [B,Nd,Dv],
  * and for the backward src_proj [B*Ns,r], dst_proj [B*Nd,r], route_index
- * [B,Ns,k] (int32) and route_logit [B,Ns,k].  k <= 32 when k < dst_nodes;
+ * [B,Ns,k] (int32) and route_logit [B,Ns,k].  k <= 64 when k < dst_nodes;
  * k == dst_nodes <= 64 takes every destination.  Deterministic (the
  * destination sums are gathers over the edges grouped by destination).
  * Replaces transition_pairwise_topk (native/jakal_net_native.cpp:6916-7087) and

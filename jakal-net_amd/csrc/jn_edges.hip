@@ -54,11 +54,18 @@ __device__ __forceinline__ void row_coefficients(const int32_t* idx, const float
   }
 }
 
+// The D columns are processed in slabs of a.slab columns, slab-major over the
+// grid: while an XCD works on one slab of a batch element, the value rows it
+// gathers (N x slab floats) stay within its L2.  Slab 0 also sums the state.
 template <int W>
 __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
   const int lane = lane_id();
-  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  const int64_t row_blocks = (a.rows + 3) / 4;
+  const int64_t logical = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int slab = (int)(logical / row_blocks);
+  const int64_t row = (logical % row_blocks) * 4 + wave_id();
   if (row >= a.rows) return;
+  const int d_begin = slab * a.slab, d_end = min(a.D, d_begin + a.slab);
   const int64_t b = row / a.Nq;
   const float* pvb = a.pv + b * a.Nk * a.ld_pv;
   const float* psb = a.ps + b * a.Nk;
@@ -72,9 +79,9 @@ __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
     int j;
     float c, s;
     row_coefficients(a.idx, a.score, row, a.k, e0, a.compress, rmax, rinv, j, c, s);
-    if (j >= 0) st += c * psb[j];
+    if (slab == 0 && j >= 0) st += c * psb[j];
     const int ne = min(kWave, a.k - e0);
-    for (int d = lane * W; d < a.D; d += kWave * W) {
+    for (int d = d_begin + lane * W; d < d_end; d += kWave * W) {
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
       int q = 0;
       for (; q + 8 <= ne; q += 8) {
@@ -98,16 +105,25 @@ __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
       store_w<W>(out + d, acc);
     }
   }
-  st = wave_sum(st);
-  if (lane == 0) a.out_state[row] = st;
+  if (slab == 0) {
+    st = wave_sum(st);
+    if (lane == 0) a.out_state[row] = st;
+  }
 }
 
-int launch_rows_forward(const RowsFwdArgs& a, hipStream_t stream) {
-  if (a.rows == 0) return kOk;
-  const int64_t blocks = (a.rows + 3) / 4;
-  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
+int launch_rows_forward(const RowsFwdArgs& args, hipStream_t stream) {
+  if (args.rows == 0) return kOk;
+  RowsFwdArgs a = args;
   const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.out_val) & 15) == 0);
+  // slabs of 256 columns (one float4 per lane) while a batch element's value
+  // rows exceed 2 MiB; a slab's rows then fit an XCD's 4 MiB L2
+  a.slab = a.D;
+  if (vec)
+    while (a.slab > 256 && a.slab % 512 == 0 && (int64_t)a.Nk * a.slab * 4 > (2LL << 20)) a.slab /= 2;
+  const int64_t slabs = (a.D + a.slab - 1) / a.slab;
+  const int64_t blocks = (a.rows + 3) / 4 * slabs;
+  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
   JN_PROFILE("rows_forward_kernel", stream);
   if (vec) hipLaunchKernelGGL(rows_forward_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
   else hipLaunchKernelGGL(rows_forward_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
@@ -466,9 +482,14 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
   constexpr int P = kWave * W * NV;  // D floats per pass
   constexpr int G = 8;               // edges per gather group
   const int lane = lane_id();
-  const int64_t gw = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
   const int64_t total_cols = (int64_t)a.B * a.Nk;
   const int64_t nwaves = (total_cols + a.cols_per_wave - 1) / a.cols_per_wave;
+  // slab-major grid: workgroup (slab, w) handles columns [d0, d0 + P) of its
+  // waves' value rows; slab 0 also accumulates the state and key gradients
+  const int64_t wave_blocks = (nwaves + 3) / 4;
+  const int64_t logical = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int pass = (int)(logical / wave_blocks);
+  const int64_t gw = (logical % wave_blocks) * 4 + wave_id();
   if (gw >= nwaves) return;  // padding waves of the last workgroup own no partial slot
   const int64_t c_begin = gw * a.cols_per_wave;
   const int ncols = (int)min((int64_t)a.cols_per_wave, total_cols - c_begin);  // <= 64
@@ -494,8 +515,7 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
   const int total = readlane_i(incl, kWave - 1);
 
   float pc0 = 0.f, pc1 = 0.f;
-  const int npass = a.grad_pv ? (a.D + P - 1) / P : 1;
-  for (int pass = 0; pass < npass; ++pass) {
+  {
     const int d0 = pass * P;
     const bool first = (pass == 0);
     float4 acc[NV];
@@ -612,7 +632,7 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
     }
     while (cur < ncols) flush(cur++);
   }
-  if (a.q && a.part_c) {
+  if (pass == 0 && a.q && a.part_c) {
     if (lane < a.r) a.part_c[gw * a.r + lane] = pc0;
     if (lane + kWave < a.r) a.part_c[gw * a.r + lane + kWave] = pc1;
   }
@@ -630,14 +650,20 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   JN_REQUIRE(a.cols_per_wave >= 1 && a.cols_per_wave <= kWave, kInvalidArgument, "columns per wave must be in [1, 64]");
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
   JN_REQUIRE((int64_t)a.D * 4 < (1LL << 31), kUnsupported, "value rows must stay below 2 GiB");
-  const int waves = cols_backward_waves(total_cols, a.cols_per_wave);
-  const int blocks = (waves + 3) / 4;
+  const int64_t waves = cols_backward_waves(total_cols, a.cols_per_wave);
   const bool vec = (a.D % 4 == 0) && (a.ld_gpv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
                    (a.grad_pv == nullptr || (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0);
+  // D columns per pass (grid slab): 512, two float4 per lane.  Narrower
+  // slabs would fit an XCD's L2 better but repeat the per-edge metadata work,
+  // which costs more than it saves here.
+  const int P = !vec ? kWave * 2 : 512;
+  const int64_t passes = a.grad_pv ? (a.D + P - 1) / P : 1;
+  const int64_t blocks = (waves + 3) / 4 * passes;
+  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
   JN_PROFILE(a.profile_name ? a.profile_name : "cols_backward_kernel", stream);
-  if (!vec) hipLaunchKernelGGL((cols_backward_kernel<1, 2>), dim3(blocks), dim3(256), 0, stream, a);
-  else if (a.D > 256) hipLaunchKernelGGL((cols_backward_kernel<4, 2>), dim3(blocks), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((cols_backward_kernel<4, 1>), dim3(blocks), dim3(256), 0, stream, a);
+  if (!vec) hipLaunchKernelGGL((cols_backward_kernel<1, 2>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  else if (P == 512) hipLaunchKernelGGL((cols_backward_kernel<4, 2>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((cols_backward_kernel<4, 1>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
   JN_LAUNCH_CHECK();
   return kOk;
 }

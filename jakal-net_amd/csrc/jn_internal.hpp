@@ -64,6 +64,7 @@ struct RowsFwdArgs {
   int64_t rows;
   float* out_state;  // [rows]
   float* out_val;    // [rows, D]
+  int slab;          // columns per slab (set by the launcher)
 };
 int launch_rows_forward(const RowsFwdArgs& a, hipStream_t stream);
 

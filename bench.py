@@ -465,6 +465,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c4-topk")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gemm-tile", type=int, choices=[0, 64, 128], default=0,
+                    help="force the GEMM workgroup tile (0: chosen per call)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of known size (scale for HBM byte counters)")
     args = ap.parse_args()
@@ -480,6 +482,7 @@ def main() -> int:
 
     import jakal_net_native as jn
 
+    jn.set_gemm_tile(args.gemm_tile)
     wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     op, layer = wl.build(torch, dev)

@@ -44,6 +44,16 @@ int jn_profile_enable(int32_t on);
 int jn_profile_collect(char* buffer, size_t size);
 
 /*
+ * GEMM tiling control (no counterpart in the reference; for tests and tuning).
+ * tile = 64 or 128 forces that square workgroup tile on every later dense
+ * product (projections, their gradients, the dense-mode score, aggregation and
+ * gradient products); 0 (the default) picks per call: 128 when both output
+ * extents are >= 128 and the grid still has >= 256 workgroups, else 64.
+ * Process-wide; results are the same up to fp32 summation order.
+ */
+int jn_set_gemm_tile(int32_t tile);
+
+/*
  * Low-rank score + per-row top-k select, no score matrix materialised.
  *   s[b,i,j] = ((sum_r query[b,i,r]*cq[r] * key[b,j,r]*ck[r]) + bias) / temperature
  * where the scale vector multiplies the query rows when scale_on_query != 0,

@@ -366,6 +366,13 @@ int jn_profile_enable(int32_t on) {
   return kOk;
 }
 
+int jn_set_gemm_tile(int32_t tile) {
+  JN_REQUIRE(tile == 0 || tile == 64 || tile == 128, kInvalidArgument, "GEMM tile must be 0, 64 or 128, got %d",
+             (int)tile);
+  jakal::set_gemm_tile(tile);
+  return kOk;
+}
+
 int jn_profile_collect(char* buffer, size_t size) {
   std::lock_guard<std::mutex> lock(jakal::g_prof_mu);
   std::map<std::string, std::pair<long, double>> agg;

@@ -8,10 +8,12 @@
 // stay separate buffers: the B-operand loader switches pointer at `b_split`
 // along N (NT) or K (NN), so no concatenated copy is needed.
 //
-// Tiling: 256 threads = 4 waves in a 2x2 grid, workgroup tile 64x64, K staged
-// through LDS in slices of 16 (double buffered, register prefetch).  Each wave
-// owns a 32x32 block = 2x2 tiles of v_mfma_f32_16x16x4f32; lane group l/16
-// owns a 4-wide k sub-slice so operand fetches are single ds_read_b128s.
+// Tiling: 256 threads = 4 waves in a 2x2 grid, workgroup tile 128x128 (64x64
+// for small extents), K staged through LDS in slices of 16 (double buffered,
+// register prefetch).  Each wave owns a 64x64 (32x32) block of
+// v_mfma_f32_16x16x4f32 tiles; lane group l/16 owns a 4-wide k sub-slice so
+// operand fetches are single ds_read_b128s.
+#include <atomic>
 #include "jn_internal.hpp"
 
 namespace jakal {
@@ -39,19 +41,23 @@ struct GemmArgs {
   const float* c_nscale;   // optional: C(m, n) = acc * c_nscale[n] (+ addend)
 };
 
-constexpr int kGBM = 64, kGBN = 64, kGBK = 16, kGStride = kGBK + 4;
+constexpr int kGBM = 64, kGBK = 16, kGStride = kGBK + 4;
 
 __device__ __forceinline__ bool aligned16(const float* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // A(m,k): A_KC -> A[m*lda + k] else A[k*lda + m]
 // B(k,n): B_KC -> Bsel(n)[n'*ldb + k] (split along n), else Bsel(k)[k'*ldb + n] (split along k)
+// TILE x TILE output tile per workgroup (TILE = 64 or 128); wave (wm, wn) owns
+// the (TILE/2) x (TILE/2) quadrant as (TILE/32)^2 tiles of 16 x 16.
 // USE tags the call site (GemmUse): the code is the same for a given layout,
 // but every use gets its own kernel symbol so profilers attribute time and
 // traffic per use.
-template <bool A_KC, bool B_KC, int USE>
+template <bool A_KC, bool B_KC, int USE, int TILE>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
-  __shared__ __align__(16) float sA[2][kGBM * kGStride];
-  __shared__ __align__(16) float sB[2][kGBN * kGStride];
+  constexpr int LPT = TILE / 64;   // float4 loads per thread per operand and K slice
+  constexpr int MT = TILE / 32;    // 16x16 tiles per wave along M (and N)
+  __shared__ __align__(16) float sA[2][TILE * kGStride];
+  __shared__ __align__(16) float sB[2][TILE * kGStride];
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -59,8 +65,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
   const int wm = wave >> 1, wn = wave & 1;
   const int grp = lane >> 4, col = lane & 15;
 
-  const int m0 = blockIdx.y * kGBM;
-  const int n0 = blockIdx.x * kGBN;
+  const int m0 = blockIdx.y * TILE;
+  const int n0 = blockIdx.x * TILE;
   const bool batched = g.batch > 1;
   const int split = batched ? 0 : blockIdx.z;
   const int64_t bz = batched ? blockIdx.z : 0;
@@ -72,93 +78,97 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
   const float* gadd = g.addend ? g.addend + bz * g.add_bs : nullptr;
   float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
 
-  // Each thread moves 4 A values and 4 B values per K slice.
-  float ra[4], rb[4];
+  float ra[LPT][4], rb[LPT][4];
 
   auto load_slice = [&](int k0) {
-    // ---- A ----
-    if (A_KC) {
-      int m = m0 + tid / 4, kq = k0 + (tid % 4) * 4;
-      const float* p = gA + (int64_t)m * g.lda + kq;
-      if (m < g.M && kq + 3 < kend && aligned16(p)) {
-        float4 v = *reinterpret_cast<const float4*>(p);
-        ra[0] = v.x; ra[1] = v.y; ra[2] = v.z; ra[3] = v.w;
-      } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ra[q] = (m < g.M && kq + q < kend) ? p[q] : 0.0f;
-      }
-    } else {
-      int kk = k0 + tid / 16, mq = m0 + (tid % 16) * 4;
-      const float* p = gA + (int64_t)kk * g.lda + mq;
-      if (kk < kend && mq + 3 < g.M && aligned16(p)) {
-        float4 v = *reinterpret_cast<const float4*>(p);
-        ra[0] = v.x; ra[1] = v.y; ra[2] = v.z; ra[3] = v.w;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) ra[q] = (kk < kend && mq + q < g.M) ? p[q] : 0.0f;
-      }
-    }
-    if (g.a_kscale) {
+    for (int u = 0; u < LPT; ++u) {
+      const int e = tid + 256 * u;
+      // ---- A ----
       if (A_KC) {
-        const int kq = k0 + (tid % 4) * 4;
+        const int m = m0 + e / 4, kq = k0 + (e % 4) * 4;
+        const float* p = gA + (int64_t)m * g.lda + kq;
+        if (m < g.M && kq + 3 < kend && aligned16(p)) {
+          const float4 v = *reinterpret_cast<const float4*>(p);
+          ra[u][0] = v.x; ra[u][1] = v.y; ra[u][2] = v.z; ra[u][3] = v.w;
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ra[q] *= (kq + q < kend) ? g.a_kscale[kq + q] : 0.0f;
+          for (int q = 0; q < 4; ++q) ra[u][q] = (m < g.M && kq + q < kend) ? p[q] : 0.0f;
+        }
+        if (g.a_kscale) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ra[u][q] *= (kq + q < kend) ? g.a_kscale[kq + q] : 0.0f;
+        }
       } else {
-        const int kk = k0 + tid / 16;
-        const float sc = kk < kend ? g.a_kscale[kk] : 0.0f;
+        const int kk = k0 + e / (TILE / 4), mq = m0 + (e % (TILE / 4)) * 4;
+        const float* p = gA + (int64_t)kk * g.lda + mq;
+        if (kk < kend && mq + 3 < g.M && aligned16(p)) {
+          const float4 v = *reinterpret_cast<const float4*>(p);
+          ra[u][0] = v.x; ra[u][1] = v.y; ra[u][2] = v.z; ra[u][3] = v.w;
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ra[q] *= sc;
+          for (int q = 0; q < 4; ++q) ra[u][q] = (kk < kend && mq + q < g.M) ? p[q] : 0.0f;
+        }
+        if (g.a_kscale) {
+          const float sc = kk < kend ? g.a_kscale[kk] : 0.0f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ra[u][q] *= sc;
+        }
       }
-    }
-    // ---- B ----
-    if (B_KC) {
-      int n = n0 + tid / 4, kq = k0 + (tid % 4) * 4;
-      const float* base = (n < g.b_split) ? gB0 + (int64_t)n * g.ldb : gB1 + (int64_t)(n - g.b_split) * g.ldb;
-      const float* p = base + kq;
-      if (n < g.N && kq + 3 < kend && aligned16(p)) {
-        float4 v = *reinterpret_cast<const float4*>(p);
-        rb[0] = v.x; rb[1] = v.y; rb[2] = v.z; rb[3] = v.w;
-      } else {
+      // ---- B ----
+      if (B_KC) {
+        const int n = n0 + e / 4, kq = k0 + (e % 4) * 4;
+        const float* base = (n < g.b_split) ? gB0 + (int64_t)n * g.ldb : gB1 + (int64_t)(n - g.b_split) * g.ldb;
+        const float* p = base + kq;
+        if (n < g.N && kq + 3 < kend && aligned16(p)) {
+          const float4 v = *reinterpret_cast<const float4*>(p);
+          rb[u][0] = v.x; rb[u][1] = v.y; rb[u][2] = v.z; rb[u][3] = v.w;
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) rb[q] = (n < g.N && kq + q < kend) ? p[q] : 0.0f;
-      }
-    } else {
-      int kk = k0 + tid / 16, nq = n0 + (tid % 16) * 4;
-      const float* base = (kk < g.b_split) ? gB0 + (int64_t)kk * g.ldb : gB1 + (int64_t)(kk - g.b_split) * g.ldb;
-      const float* p = base + nq;
-      if (kk < kend && nq + 3 < g.N && aligned16(p)) {
-        float4 v = *reinterpret_cast<const float4*>(p);
-        rb[0] = v.x; rb[1] = v.y; rb[2] = v.z; rb[3] = v.w;
+          for (int q = 0; q < 4; ++q) rb[u][q] = (n < g.N && kq + q < kend) ? p[q] : 0.0f;
+        }
       } else {
+        const int kk = k0 + e / (TILE / 4), nq = n0 + (e % (TILE / 4)) * 4;
+        const float* base = (kk < g.b_split) ? gB0 + (int64_t)kk * g.ldb : gB1 + (int64_t)(kk - g.b_split) * g.ldb;
+        const float* p = base + nq;
+        if (kk < kend && nq + 3 < g.N && aligned16(p)) {
+          const float4 v = *reinterpret_cast<const float4*>(p);
+          rb[u][0] = v.x; rb[u][1] = v.y; rb[u][2] = v.z; rb[u][3] = v.w;
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) rb[q] = (kk < kend && nq + q < g.N) ? p[q] : 0.0f;
+          for (int q = 0; q < 4; ++q) rb[u][q] = (kk < kend && nq + q < g.N) ? p[q] : 0.0f;
+        }
       }
     }
   };
   auto store_slice = [&](int buf) {
-    if (A_KC) {
-      float* d = &sA[buf][(tid / 4) * kGStride + (tid % 4) * 4];
-      *reinterpret_cast<float4*>(d) = make_float4(ra[0], ra[1], ra[2], ra[3]);
-    } else {
-      int kk = tid / 16, mq = (tid % 16) * 4;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) sA[buf][(mq + q) * kGStride + kk] = ra[q];
-    }
-    if (B_KC) {
-      float* d = &sB[buf][(tid / 4) * kGStride + (tid % 4) * 4];
-      *reinterpret_cast<float4*>(d) = make_float4(rb[0], rb[1], rb[2], rb[3]);
-    } else {
-      int kk = tid / 16, nq = (tid % 16) * 4;
+    for (int u = 0; u < LPT; ++u) {
+      const int e = tid + 256 * u;
+      if (A_KC) {
+        *reinterpret_cast<float4*>(&sA[buf][(e / 4) * kGStride + (e % 4) * 4]) =
+            make_float4(ra[u][0], ra[u][1], ra[u][2], ra[u][3]);
+      } else {
+        const int kk = e / (TILE / 4), mq = (e % (TILE / 4)) * 4;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) sB[buf][(nq + q) * kGStride + kk] = rb[q];
+        for (int q = 0; q < 4; ++q) sA[buf][(mq + q) * kGStride + kk] = ra[u][q];
+      }
+      if (B_KC) {
+        *reinterpret_cast<float4*>(&sB[buf][(e / 4) * kGStride + (e % 4) * 4]) =
+            make_float4(rb[u][0], rb[u][1], rb[u][2], rb[u][3]);
+      } else {
+        const int kk = e / (TILE / 4), nq = (e % (TILE / 4)) * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sB[buf][(nq + q) * kGStride + kk] = rb[u][q];
+      }
     }
   };
 
-  floatx4 acc[2][2];
+  floatx4 acc[MT][MT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < MT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int nslices = (kend - kbeg + kGBK - 1) / kGBK;
   if (nslices > 0) {
@@ -171,16 +181,16 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
     const int cur = s & 1;
     if (s + 1 < nslices) load_slice(kbeg + (s + 1) * kGBK);
 
-    float4 av[2], bv[2];
+    float4 av[MT], bv[MT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      av[t] = *reinterpret_cast<const float4*>(&sA[cur][(wm * 32 + t * 16 + col) * kGStride + grp * 4]);
-      bv[t] = *reinterpret_cast<const float4*>(&sB[cur][(wn * 32 + t * 16 + col) * kGStride + grp * 4]);
+    for (int t = 0; t < MT; ++t) {
+      av[t] = *reinterpret_cast<const float4*>(&sA[cur][(wm * (TILE / 2) + t * 16 + col) * kGStride + grp * 4]);
+      bv[t] = *reinterpret_cast<const float4*>(&sB[cur][(wn * (TILE / 2) + t * 16 + col) * kGStride + grp * 4]);
     }
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < MT; ++nt) {
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].x, bv[nt].x, acc[mt][nt], 0, 0, 0);
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].y, bv[nt].y, acc[mt][nt], 0, 0, 0);
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].z, bv[nt].z, acc[mt][nt], 0, 0, 0);
@@ -193,13 +203,13 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 
   // Epilogue: lane holds rows 4*grp+v of each 16x16 tile, column col.
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < MT; ++nt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        int m = m0 + wm * 32 + mt * 16 + grp * 4 + v;
-        int n = n0 + wn * 32 + nt * 16 + col;
+        const int m = m0 + wm * (TILE / 2) + mt * 16 + grp * 4 + v;
+        const int n = n0 + wn * (TILE / 2) + nt * 16 + col;
         if (m < g.M && n < g.N) {
           float x = acc[mt][nt][v];
           if (g.c_nscale) x *= g.c_nscale[n];
@@ -207,6 +217,273 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
           C[(int64_t)m * g.ldc + n] = x;
         }
       }
+}
+
+// Layout (A k-contiguous, B k-contiguous), optional operand features (A
+// scaled along k, B rows split over two buffers) and timer label of every use.
+struct GemmUseInfo {
+  bool a_kc, b_kc, a_kscale, b_split;
+  const char* name;
+};
+constexpr GemmUseInfo kGemmUses[] = {
+    {true, true, false, true, "gemm_f32_kernel<project>"},
+    {true, false, false, true, "gemm_f32_kernel<grad_input>"},
+    {false, false, false, false, "gemm_f32_kernel<grad_weight>"},
+    {true, true, true, false, "gemm_f32_kernel<dense_scores>"},
+    {true, false, false, false, "gemm_f32_kernel<dense_aggregate>"},
+    {true, true, false, false, "gemm_f32_kernel<dense_edge_grad>"},
+    {false, false, false, false, "gemm_f32_kernel<dense_value_grad>"},
+    {true, false, false, false, "gemm_f32_kernel<dense_target_grad>"},
+    {false, false, false, false, "gemm_f32_kernel<dense_source_grad>"},
+};
+
+// ---- 128 x 128 path --------------------------------------------------------
+// Workgroup tile 128 x 128, K staged through LDS in slices of BK (double
+// buffered, register prefetch of the next slice); each wave owns a 64 x 64
+// quadrant as 4 x 4 tiles of v_mfma_f32_16x16x4f32.
+//
+// Preconditions (checked by the host; otherwise the 64 x 64 kernel runs):
+// every float4 the loaders fetch lies wholly inside or wholly outside its
+// operand -- K and the split-K chunk are multiples of 4, so is M (N) when A (B)
+// is K-major, row strides, batch strides and base pointers are float4
+// aligned -- and row strides are below 2^20 floats so that 32-bit buffer
+// offsets from a per-slice base reach every row of a slice.  A float4 outside
+// the operand is fetched at an offset past the buffer resource and reads as
+// zeros, so the loaders have no branches.
+//
+// LDS layouts: a K-contiguous operand is stored [row][BK + 4] and read as one
+// ds_read_b128 per lane (4 consecutive k); a K-major operand is stored
+// [k][128 + 4] (float4 stores, no transpose) and read as four ds_read_b32 at
+// stride 132 (conflict-free: 4 rows apart = 16 banks).
+constexpr int kFT = 128;
+constexpr uint32_t kFastRecords = 0x80000000u;
+
+template <bool KC, int BK>
+struct FastLds {
+  static constexpr int stride = KC ? BK + 4 : kFT + 4;
+  static constexpr int floats = KC ? kFT * stride : BK * stride;
+};
+
+// Operand fragment of 16x16 tile `t` (of the wave's 4) for k sub-block kb:
+// lane (col, grp) gets element (row = base + t*16 + col, k = kb*16 + grp*4 + q)
+// in component q.
+template <bool KC, int BK>
+__device__ __forceinline__ float4 fast_fragment(const float* s, int base, int t, int kb, int col, int grp) {
+  constexpr int S = FastLds<KC, BK>::stride;
+  if constexpr (KC) {
+    return *reinterpret_cast<const float4*>(&s[(base + t * 16 + col) * S + kb * 16 + grp * 4]);
+  } else {
+    const float* p = &s[(kb * 16 + grp * 4) * S + base + t * 16 + col];
+    return make_float4(p[0], p[S], p[2 * S], p[3 * S]);
+  }
+}
+
+template <bool A_KC, bool B_KC, int USE, int BK>
+__global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int tiles_m, int tiles_n, int vec_out) {
+  constexpr int LPT = kFT * BK / 4 / 256;  // float4 per thread, per operand and slice
+  constexpr int KCH = BK / 4;              // float4 per K-contiguous row of a slice
+  constexpr int MCH = kFT / 4;             // float4 per K-major row of a slice
+  using LA = FastLds<A_KC, BK>;
+  using LB = FastLds<B_KC, BK>;
+  constexpr int kStageStride = 68;         // epilogue strip: 16 rows x 64 columns per wave
+  static_assert(4 * 16 * kStageStride <= 2 * (LA::floats + LB::floats), "epilogue strips must fit in LDS");
+  __shared__ __align__(16) float smem[2 * (LA::floats + LB::floats)];
+  float(*sA)[LA::floats] = reinterpret_cast<float(*)[LA::floats]>(smem);
+  float(*sB)[LB::floats] = reinterpret_cast<float(*)[LB::floats]>(smem + 2 * LA::floats);
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int wm = wave >> 1, wn = wave & 1;
+  const int grp = lane >> 4, col = lane & 15;
+
+  // Logical tile: each XCD runs a contiguous range; inside it, bands of 8
+  // M-tiles sweep N so that concurrently running tiles share A and B rows.
+  const int id = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int per = tiles_m * tiles_n;
+  const int z = id / per;
+  const int t = id - z * per;
+  constexpr int kBand = 8;
+  const int band = t / (kBand * tiles_n);
+  const int bm = min(kBand, tiles_m - band * kBand);
+  const int tb = t - band * kBand * tiles_n;
+  const int m0 = (band * kBand + tb % bm) * kFT;
+  const int n0 = (tb / bm) * kFT;
+
+  const bool batched = g.batch > 1;
+  const int split = batched ? 0 : z;
+  const int64_t bz = batched ? z : 0;
+  const int kbeg = split * g.k_chunk;
+  const int kend = min(g.K, kbeg + g.k_chunk);
+  const float* gA = g.A + bz * g.a_bs;
+  const float* gB0 = g.B0 + bz * g.b_bs;
+  const float* gB1 = g.B1 + bz * g.b_bs;
+  const float* gadd = g.addend ? g.addend + bz * g.add_bs : nullptr;
+  float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
+  const int lda = (int)g.lda, ldb = (int)g.ldb;
+
+  // Registers of the prefetched slice.  Everything that combines loaded
+  // values (the k scale) waits until the slice is stored to LDS, after the
+  // MFMAs, so that the loads stay in flight meanwhile.
+  constexpr bool KSCALE = kGemmUses[USE].a_kscale;
+  constexpr bool BSPLIT = kGemmUses[USE].b_split;
+  constexpr int NSC = KSCALE ? (A_KC ? 4 : 1) : 0;
+  float4 ra[LPT], rb[LPT];
+  [[maybe_unused]] float rs[LPT][NSC > 0 ? NSC : 1];
+
+  auto load_slice = [&](int k0) {
+    // ---- A ----
+    const float* abase = A_KC ? gA + (int64_t)m0 * lda + k0 : gA + (int64_t)k0 * lda + m0;
+    const auto ars = make_rsrc(abase, kFastRecords);
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int e = tid + 256 * u;
+      const int row = A_KC ? e / KCH : e / MCH;  // m (A_KC) or k offset in the slice
+      const int c4 = A_KC ? (e % KCH) * 4 : (e % MCH) * 4;
+      const bool ok = A_KC ? (m0 + row < g.M && k0 + c4 < kend) : (k0 + row < kend && m0 + c4 < g.M);
+      ra[u] = buf_load4(ars, ok ? (uint32_t)(row * lda + c4) * 4u : kOobOffset);
+      if constexpr (KSCALE) {
+        const auto srs = make_rsrc(g.a_kscale + k0, kFastRecords);
+        if constexpr (A_KC) {
+          const float4 sc = buf_load4(srs, k0 + c4 < kend ? (uint32_t)c4 * 4u : kOobOffset);
+          rs[u][0] = sc.x; rs[u][NSC > 1 ? 1 : 0] = sc.y; rs[u][NSC > 2 ? 2 : 0] = sc.z; rs[u][NSC - 1] = sc.w;
+        } else {
+          rs[u][0] = buf_load1(srs, k0 + row < kend ? (uint32_t)row * 4u : kOobOffset);
+        }
+      }
+    }
+    // ---- B: rows below b_split come from B0, the rest from B1 ----
+    // The rows one wave fetches with one instruction (16 for a K-contiguous B,
+    // 2 for a K-major B) never straddle b_split (the host requires b_split to
+    // be a multiple of 16), so the buffer is chosen per wave and instruction;
+    // both resources address rows relative to the slice's first row.
+    const int s0 = B_KC ? n0 : k0;
+    const float* base0 = B_KC ? gB0 + (int64_t)n0 * ldb + k0 : gB0 + (int64_t)k0 * ldb + n0;
+    const auto brs0 = make_rsrc(base0, kFastRecords);
+    [[maybe_unused]] const auto brs1 =
+        make_rsrc(BSPLIT ? (B_KC ? gB1 + (int64_t)(n0 - g.b_split) * ldb + k0
+                                 : gB1 + (int64_t)(k0 - g.b_split) * ldb + n0)
+                         : base0,
+                  kFastRecords);
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int e = tid + 256 * u;
+      const int row = B_KC ? e / KCH : e / MCH;  // n (B_KC) or k offset in the slice
+      const int c4 = B_KC ? (e % KCH) * 4 : (e % MCH) * 4;
+      const bool ok = B_KC ? (n0 + row < g.N && k0 + c4 < kend) : (k0 + row < kend && n0 + c4 < g.N);
+      const uint32_t off = ok ? (uint32_t)(row * ldb + c4) * 4u : kOobOffset;
+      if constexpr (BSPLIT) {
+        const int wrow = B_KC ? (wave * 64 + 256 * u) / KCH : (wave * 64 + 256 * u) / MCH;  // wave-uniform
+        rb[u] = buf_load4(s0 + wrow < g.b_split ? brs0 : brs1, off);
+      } else {
+        rb[u] = buf_load4(brs0, off);
+      }
+    }
+  };
+  auto store_slice = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int e = tid + 256 * u;
+      const int ia = A_KC ? (e / KCH) * LA::stride + (e % KCH) * 4 : (e / MCH) * LA::stride + (e % MCH) * 4;
+      const int ib = B_KC ? (e / KCH) * LB::stride + (e % KCH) * 4 : (e / MCH) * LB::stride + (e % MCH) * 4;
+      float4 a = ra[u];
+      if constexpr (KSCALE) {
+        a.x *= rs[u][0]; a.y *= rs[u][NSC > 1 ? 1 : 0]; a.z *= rs[u][NSC > 2 ? 2 : 0]; a.w *= rs[u][NSC - 1];
+      }
+      *reinterpret_cast<float4*>(&sA[buf][ia]) = a;
+      *reinterpret_cast<float4*>(&sB[buf][ib]) = rb[u];
+    }
+  };
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int nslices = (kend - kbeg + BK - 1) / BK;
+  if (nslices > 0) {
+    load_slice(kbeg);
+    store_slice(0);
+  }
+  __syncthreads();
+
+  for (int s = 0; s < nslices; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < nslices) load_slice(kbeg + (s + 1) * BK);
+#pragma unroll
+    for (int kb = 0; kb < BK / 16; ++kb) {
+      float4 av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        av[i] = fast_fragment<A_KC, BK>(sA[cur], wm * 64, i, kb, col, grp);
+        bv[i] = fast_fragment<B_KC, BK>(sB[cur], wn * 64, i, kb, col, grp);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].x, bv[nt].x, acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].y, bv[nt].y, acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].z, bv[nt].z, acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].w, bv[nt].w, acc[mt][nt], 0, 0, 0);
+        }
+    }
+    if (s + 1 < nslices) store_slice(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue.  With vec_out (N, ldc, ld_add and the batch/split strides
+  // multiples of 4, C and the addend float4 aligned) each wave stages a 16 x 64
+  // strip of its quadrant in LDS and writes whole float4 rows: 16 lanes cover
+  // 256 contiguous bytes of a row.  Otherwise each lane stores its own
+  // elements (rows 4*grp+v of each 16x16 tile, column col).
+  if (vec_out) {
+    float* stage = smem + wave * 16 * kStageStride;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) stage[(grp * 4 + v) * kStageStride + nt * 16 + col] = acc[mt][nt][v];
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = grp + 4 * i, c4 = col * 4;
+        const int m = m0 + wm * 64 + mt * 16 + r;
+        const int n = n0 + wn * 64 + c4;
+        float4 x = *reinterpret_cast<const float4*>(&stage[r * kStageStride + c4]);
+        if (m < g.M && n < g.N) {
+          if (g.c_nscale) {
+            const float4 sc = *reinterpret_cast<const float4*>(&g.c_nscale[n]);
+            x.x *= sc.x; x.y *= sc.y; x.z *= sc.z; x.w *= sc.w;
+          }
+          if (gadd) {
+            const float4 a = *reinterpret_cast<const float4*>(&gadd[(int64_t)m * g.ld_add + n]);
+            x.x += a.x; x.y += a.y; x.z += a.z; x.w += a.w;
+          }
+          *reinterpret_cast<float4*>(&C[(int64_t)m * g.ldc + n]) = x;
+        }
+      }
+      __syncthreads();
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = m0 + wm * 64 + mt * 16 + grp * 4 + v;
+          const int n = n0 + wn * 64 + nt * 16 + col;
+          if (m < g.M && n < g.N) {
+            float x = acc[mt][nt][v];
+            if (g.c_nscale) x *= g.c_nscale[n];
+            if (gadd) x += gadd[(int64_t)m * g.ld_add + n];
+            C[(int64_t)m * g.ldc + n] = x;
+          }
+        }
+  }
 }
 
 // Sum split-K partials in a fixed order; rows < m_split go to out0, the rest to out1.
@@ -233,27 +510,41 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
   }
 }
 
-// Layout (A k-contiguous, B k-contiguous) and timer label of every GEMM use.
-struct GemmUseInfo {
-  bool a_kc, b_kc;
-  const char* name;
-};
-constexpr GemmUseInfo kGemmUses[] = {
-    {true, true, "gemm_f32_kernel<project>"},
-    {true, false, "gemm_f32_kernel<grad_input>"},
-    {false, false, "gemm_f32_kernel<grad_weight>"},
-    {true, true, "gemm_f32_kernel<dense_scores>"},
-    {true, false, "gemm_f32_kernel<dense_aggregate>"},
-    {true, true, "gemm_f32_kernel<dense_edge_grad>"},
-    {false, false, "gemm_f32_kernel<dense_value_grad>"},
-    {true, false, "gemm_f32_kernel<dense_target_grad>"},
-    {false, false, "gemm_f32_kernel<dense_source_grad>"},
-};
+
+constexpr int kFastBK = 16;
+
+static bool f4_aligned(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 
 template <int USE>
-static void launch_use(const GemmArgs& g, dim3 grid, hipStream_t stream) {
+static void launch_use(const GemmArgs& g, bool fast, int zdim, hipStream_t stream) {
   constexpr GemmUseInfo u = kGemmUses[USE];
-  hipLaunchKernelGGL((gemm_f32_kernel<u.a_kc, u.b_kc, USE>), grid, dim3(256), 0, stream, g);
+  if (fast) {
+    const int tm = (g.M + kFT - 1) / kFT, tn = (g.N + kFT - 1) / kFT;
+    const bool vec = g.N % 4 == 0 && g.ldc % 4 == 0 && g.c_bs % 4 == 0 && g.c_split_stride % 4 == 0 &&
+                     f4_aligned(g.C) && f4_aligned(g.c_nscale) &&
+                     (g.addend == nullptr || (g.ld_add % 4 == 0 && g.add_bs % 4 == 0 && f4_aligned(g.addend)));
+    hipLaunchKernelGGL((gemm_f32_fast_kernel<u.a_kc, u.b_kc, USE, kFastBK>), dim3(tm * tn * zdim), dim3(256), 0,
+                       stream, g, tm, tn, vec ? 1 : 0);
+  } else {
+    dim3 grid((g.N + kGBM - 1) / kGBM, (g.M + kGBM - 1) / kGBM, zdim);
+    hipLaunchKernelGGL((gemm_f32_kernel<u.a_kc, u.b_kc, USE, kGBM>), grid, dim3(256), 0, stream, g);
+  }
+}
+
+static std::atomic<int> g_gemm_tile{0};
+
+void set_gemm_tile(int tile) { g_gemm_tile.store(tile, std::memory_order_relaxed); }
+
+// Whether the 128 x 128 kernel's preconditions hold (see gemm_f32_fast_kernel).
+static bool fast_path_ok(const GemmArgs& g, bool a_kc, bool b_kc) {
+  constexpr int64_t kMaxLd = 1 << 20;
+  if (g.b_split < (b_kc ? g.N : g.K) && g.b_split % 16 != 0) return false;
+  if (g.K % 4 != 0 || g.k_chunk % 4 != 0) return false;
+  if ((!a_kc && g.M % 4 != 0) || (!b_kc && g.N % 4 != 0)) return false;
+  if (g.lda % 4 != 0 || g.ldb % 4 != 0 || g.a_bs % 4 != 0 || g.b_bs % 4 != 0) return false;
+  if (g.lda >= kMaxLd || g.ldb >= kMaxLd) return false;
+  return f4_aligned(g.A) && f4_aligned(g.B0) && f4_aligned(g.B1) && f4_aligned(g.a_kscale);
 }
 
 int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) {
@@ -261,19 +552,30 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
   if (g.M == 0 || g.N == 0) return kOk;
   JN_REQUIRE(g.batch <= 1 || splits == 1, kInvalidArgument, "batched GEMM has no split-K");
   JN_REQUIRE(g.batch < 65536 && splits < 65536, kUnsupported, "GEMM batch or split count too large");
+  JN_REQUIRE(g.batch > 1 || (int64_t)splits * g.k_chunk >= g.K, kInvalidArgument, "split-K chunks do not cover K");
+  const GemmUseInfo& info = kGemmUses[use];
+  JN_REQUIRE(g.a_kscale == nullptr || info.a_kscale, kInvalidArgument, "GEMM use %s takes no k scale", info.name);
+  JN_REQUIRE(g.b_split >= (info.b_kc ? g.N : g.K) || info.b_split, kInvalidArgument,
+             "GEMM use %s takes one B buffer", info.name);
+  const int64_t zdim = g.batch > 1 ? g.batch : splits;
   JN_REQUIRE((g.M + kGBM - 1) / kGBM < 65536, kUnsupported, "GEMM M extent too large");
-  dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, g.batch > 1 ? g.batch : splits);
-  JN_PROFILE(kGemmUses[use].name, stream);
+  // 128 x 128 tiles halve the operand traffic per flop; 64 x 64 when an
+  // extent is too small to fill them or the grid would be too small
+  const int64_t tiles128 = (int64_t)((g.M + kFT - 1) / kFT) * ((g.N + kFT - 1) / kFT) * zdim;
+  const int forced = g_gemm_tile.load(std::memory_order_relaxed);
+  const bool big = forced ? forced == kFT : (g.M >= kFT && g.N >= kFT && tiles128 >= 256);
+  const bool fast = big && tiles128 < (1LL << 31) && fast_path_ok(g, info.a_kc, info.b_kc);
+  JN_PROFILE(info.name, stream);
   switch (use) {
-    case kGemmProject: launch_use<kGemmProject>(g, grid, stream); break;
-    case kGemmGradInput: launch_use<kGemmGradInput>(g, grid, stream); break;
-    case kGemmGradWeight: launch_use<kGemmGradWeight>(g, grid, stream); break;
-    case kGemmDenseScores: launch_use<kGemmDenseScores>(g, grid, stream); break;
-    case kGemmDenseAggregate: launch_use<kGemmDenseAggregate>(g, grid, stream); break;
-    case kGemmDenseEdgeGrad: launch_use<kGemmDenseEdgeGrad>(g, grid, stream); break;
-    case kGemmDenseValueGrad: launch_use<kGemmDenseValueGrad>(g, grid, stream); break;
-    case kGemmDenseTargetGrad: launch_use<kGemmDenseTargetGrad>(g, grid, stream); break;
-    case kGemmDenseSourceGrad: launch_use<kGemmDenseSourceGrad>(g, grid, stream); break;
+    case kGemmProject: launch_use<kGemmProject>(g, fast, (int)zdim, stream); break;
+    case kGemmGradInput: launch_use<kGemmGradInput>(g, fast, (int)zdim, stream); break;
+    case kGemmGradWeight: launch_use<kGemmGradWeight>(g, fast, (int)zdim, stream); break;
+    case kGemmDenseScores: launch_use<kGemmDenseScores>(g, fast, (int)zdim, stream); break;
+    case kGemmDenseAggregate: launch_use<kGemmDenseAggregate>(g, fast, (int)zdim, stream); break;
+    case kGemmDenseEdgeGrad: launch_use<kGemmDenseEdgeGrad>(g, fast, (int)zdim, stream); break;
+    case kGemmDenseValueGrad: launch_use<kGemmDenseValueGrad>(g, fast, (int)zdim, stream); break;
+    case kGemmDenseTargetGrad: launch_use<kGemmDenseTargetGrad>(g, fast, (int)zdim, stream); break;
+    case kGemmDenseSourceGrad: launch_use<kGemmDenseSourceGrad>(g, fast, (int)zdim, stream); break;
     default: JN_REQUIRE(false, kInvalidArgument, "unknown GEMM use %d", (int)use);
   }
   JN_LAUNCH_CHECK();

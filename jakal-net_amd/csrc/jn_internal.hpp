@@ -48,6 +48,8 @@ enum GemmUse {
   kGemmDenseSourceGrad,
 };
 int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream);
+// Workgroup tile of every later GEMM launch: 0 = chosen per call, 64 or 128 = forced.
+void set_gemm_tile(int tile);
 int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, float* out0, float* out1, int m_split,
                      int M, int N, int K, float* partial, hipStream_t stream);
 

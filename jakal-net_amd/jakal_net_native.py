@@ -47,6 +47,7 @@ _declare("jn_last_error", [], ctypes.c_char_p)
 _declare("jn_abi_version", [])
 _declare("jn_profile_enable", [_I32])
 _declare("jn_profile_collect", [ctypes.c_char_p, _SZ])
+_declare("jn_set_gemm_tile", [_I32])
 _declare(
     "jn_lowrank_topk_select",
     [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _F, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
@@ -131,6 +132,11 @@ def loaded_library() -> str:
 def profile_enable(on: bool = True) -> None:
     """Start (or stop) per-kernel HIP-event timing inside the library."""
     _check(_LIB.jn_profile_enable(1 if on else 0))
+
+
+def set_gemm_tile(tile: int = 0) -> None:
+    """Force the GEMM workgroup tile (64 or 128) for later calls; 0 restores the per-call choice."""
+    _check(_LIB.jn_set_gemm_tile(int(tile)))
 
 
 def profile_collect() -> dict[str, tuple[int, float]]:

@@ -1,0 +1,82 @@
+"""Both GEMM workgroup tiles (64 x 64 and 128 x 128) against the oracle.
+
+The library picks the tile per call from the output extents; these tests force
+each tile in turn (jn_set_gemm_tile) on ops whose extents are ragged against
+both tiles, so every GEMM of the forward and backward passes (projections,
+their input and weight gradients, dense scores, aggregation and its
+gradients) runs partial tiles, unaligned rows and split-K under both tilings.
+The 128 x 128 kernel has preconditions (extents and strides in float4 units,
+B split at a multiple of 16); shapes that miss them run the 64 x 64 kernel
+even when 128 is forced, and are included too.
+Tolerances are those of the per-op tests (fp32: rtol 1e-4, atol 1e-5,
+norm-wise for long sums).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import jakal_oracle as O
+import test_gpu_dense as TD
+import test_gpu_topk as TT
+import test_gpu_transition as TR
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=[64, 128])
+def tile(request):
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import jakal_net_native as jn
+
+    jn.set_gemm_tile(request.param)
+    yield request.param
+    jn.set_gemm_tile(0)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return torch.device("cuda:0")
+
+
+def test_dense_ragged(dev, tile):
+    import jakal_net_native as jn
+
+    B, N, D, r = 2, 200, 72, 12
+    g, state, val, U, V, w = TD._inputs(4401, B, N, D, r)
+    pv_cpu = torch.randn(B, N, D, generator=g)
+    w_hat = w / w.norm()
+    X = val.to(dev).requires_grad_(True)
+    ps = state.to(dev).requires_grad_(True)
+    pv = pv_cpu.to(dev).requires_grad_(True)
+    Ud, Vd, wd = (t.to(dev).requires_grad_(True) for t in (U, V, w_hat))
+    bd = torch.tensor(0.1, device=dev, requires_grad=True)
+    ds, dv = jn.propagation_dense("low_rank_bilinear", wd, bd, Vd, None, Ud, None, "softsign", X, ps, pv, None, N, N)
+    gds, gdv = torch.randn(B, N, generator=g), torch.randn(B, N, D, generator=g)
+    torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
+    ref = O.propagation_forward(TD._np(val), TD._np(state), TD._np(pv_cpu), TD._np(U), TD._np(V), TD._np(w), 0.1,
+                                mode="dense", kind="softsign")
+    TD._close(TD._np(ds), ref["delta_state"], what="delta_state")
+    TD._close(TD._np(dv), ref["delta_val"], what="delta_val")
+    gr = O.propagation_backward(TD._np(val), TD._np(state), TD._np(pv_cpu), TD._np(U), TD._np(V), TD._np(w), 0.1,
+                                TD._np(gds), TD._np(gdv), mode="dense", kind="softsign")
+    for t, name in ((X, "val"), (ps, "ps"), (pv, "pv"), (Ud, "U"), (Vd, "V"), (wd, "w_hat"), (bd, "b")):
+        TD._normwise(TD._np(t.grad), np.asarray(gr[name]), f"grad {name}")
+
+
+def test_dense_small(dev, tile):
+    TD.test_dense_forward_backward_matches_oracle(dev, "signed_abs_softmax", True, 37, False)
+
+
+def test_topk_propagation(dev, tile):
+    TT.test_propagation_topk_forward_backward_matches_oracle(dev, "softsign", True, 8)
+
+
+def test_transition_odd(dev, tile):
+    TR._run(dev, 3003, B=3, Ns=37, Nd=29, Dsrc=13, Ddst=7, r=3, topk=5, temperature=0.9, kind="signed_abs_softmax",
+            with_bias=False)
+
+
+@pytest.mark.parametrize("r", [40, 48])  # route weights split at r: 48 keeps the 128 x 128 kernel, 40 does not
+def test_transition_medium(dev, tile, r):
+    TR._run(dev, 3005, B=2, Ns=300, Nd=140, Dsrc=136, Ddst=72, r=r, topk=8, temperature=1.2, kind="softmax")

@@ -23,20 +23,22 @@
 //     A operand), double buffered with a one-chunk register prefetch and one
 //     workgroup barrier per chunk.
 //   * After a chunk, lane l holds 8 scores of row l%16.  Scores above the
-//     row's current k-th best (theta) are appended to the row's slot array in
-//     LDS; the 4 lanes of a row (l, l^16, l^32, l^48) exchange their counts
-//     with the gfx950 permlane swaps to get write offsets (no LDS atomics).
-//     Counts and thresholds live in registers.
-//   * Once any row of a wave has >= 64 waiting candidates (or any at the end),
-//     all 16 rows of the wave merge together: lane (g, row) loads 32 slots of
-//     its row into registers and a radix select over order keys finds each
-//     row's k-th largest key, counting per lane and summing over the row's 4
-//     lanes with permlane swaps; it starts below the bits shared by all of the
-//     row's keys and stops once exactly k keys remain.  The k winners are
-//     compacted to the front of the slot array.  A row whose k-th value is
-//     tied (more equal keys than places) is merged again by the exact per-row
-//     path, which keeps the lower key indices.  The kept set stays unsorted
-//     until one bitonic sort per row at the end.
+//     row's threshold theta are appended to the lane's own candidate region
+//     of the row (the row's 4 lanes never share a region, so appends need no
+//     cross-lane offsets).  Counts and thresholds live in registers.
+//   * Once any lane of a wave has filled its region to within one chunk of
+//     its capacity (or at the end), all 16 rows of the wave merge together:
+//     lane (g, row) loads a quarter of the row's kept entries and its own
+//     candidates into registers, and a radix select over order keys finds
+//     each row's k-th largest key, counting per lane and summing over the
+//     row's 4 lanes with permlane swaps; it starts below the bits shared by
+//     all of the row's keys and stops once exactly k keys remain.  The k
+//     winners are compacted into the row's kept region.  A row whose k-th
+//     value is tied (more equal keys than places) is merged again by the
+//     exact per-row path, which keeps the lower key indices.  The kept set
+//     stays unsorted until one bitonic sort per row at the end.
+#include <type_traits>
+
 #include "jn_internal.hpp"
 
 namespace jakal {
@@ -47,26 +49,30 @@ constexpr int kSelWaves = 4;
 constexpr int kSelRowsPerWave = 16;
 constexpr int kSelRows = kSelWaves * kSelRowsPerWave;  // 64 query rows / workgroup
 constexpr int kSelChunk = 32;                          // key rows per LDS chunk
-// A row's 128 slots hold a kept region of KEEP entries (the k <= KEEP best so
-// far; KEEP = 32 for k <= 32, 64 for k <= 64) followed by the candidates
-// appended since the last merge.  A merge runs once a row holds
-// merge_at(KEEP) candidates; one more chunk can add 32, so the largest slot
-// used is KEEP + merge_at - 1 + 32 - 1 = 126 either way.
-__host__ __device__ constexpr int merge_at(int keep) { return keep == 32 ? 64 : 32; }
-constexpr int kSelSlots = 32 + merge_at(32) - 1 + kSelChunk;  // 127 used (KEEP = 32)
-static_assert(64 + merge_at(64) - 1 + kSelChunk == kSelSlots, "both kept-region sizes use the same slots");
+// A row's slots: a kept region of KEEP entries (the k <= KEEP best so far;
+// KEEP = 32 for k <= 32, 64 for k <= 64), then one candidate region of
+// sel_lane_cap(KEEP) slots per lane of the row.  A lane takes at most 8
+// candidates per chunk, so merging once a lane holds more than cap - 8 keeps
+// every region within its capacity.
+constexpr int kSelRowSlots = 144;
+__host__ __device__ constexpr int sel_lane_cap(int keep) { return (kSelRowSlots - keep) / 4; }
+static_assert(sel_lane_cap(32) % 4 == 0 && sel_lane_cap(64) % 4 == 0, "candidate regions hold whole float4s");
+static_assert(32 / 4 + sel_lane_cap(32) == 64 / 4 + sel_lane_cap(64), "both kept-region sizes merge as many keys");
+constexpr int kSelMergeKeys = 32 / 4 + sel_lane_cap(32);  // keys per lane in a batched merge (36)
 // Row strides are 16-byte multiples (vector reads) that shift successive rows by
-// 4 LDS banks, so the 16 rows of a wave read and write on distinct banks.
-constexpr int kSelScoreStride = 132;  // floats
-constexpr int kSelIndexStride = 136;  // uint16 (68 words)
-constexpr int kSelTrash = 127;        // slot that absorbs writes of non-winners
+// 20 (scores) LDS banks, so the 16 rows of a wave read on distinct banks.
+constexpr int kSelScoreStride = 148;  // floats
+constexpr int kSelIndexStride = 152;  // uint16 (76 words)
 constexpr int kSelMaxKeys = 65535;    // key indices are stored as uint16
-static_assert(kSelSlots <= 128, "merge reads at most two slots per lane");
 
 // Monotone map float -> uint32 (larger float -> larger key); -0 and +0 map together.
 __device__ __forceinline__ uint32_t order_key(float s) {
   uint32_t u = __float_as_uint(s + 0.0f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_to_float(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
 // Branchless bitonic sort of 64 (score, index) pairs into descending score,
@@ -96,157 +102,186 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// Merge one row: keep the k best of its `kept` kept entries (slots [0, kept))
-// and `cnt` candidates (slots [KEEP, KEEP + cnt)), k < kept + cnt, compacted
-// to slots [0, k); returns the new k-th best score (wave-uniform).
+// Sum over the 4 lanes of a row (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ int row_sum4(int v) {
+  v += xor16_i(v);
+  return v + xor32_i(v);
+}
+
+// Exact merge of one row by the whole wave: keep the k best (ties toward the
+// lower key index) of its `kept` kept entries and the c[g] candidates of lane
+// region g, compacted to slots [0, k); k < kept + sum(c).  Returns the new
+// k-th best score (wave-uniform).  Lane l holds slots l, l + 64, l + 128.
 template <int KEEP>
-__device__ float merge_row(float* row_s, uint16_t* row_i, int k, int kept, int cnt) {
+__device__ float merge_row_exact(float* row_s, uint16_t* row_i, int k, int kept, const int (&c)[4]) {
+  constexpr int CAP = sel_lane_cap(KEEP);
   const int lane = lane_id();
-  const int n_used = KEEP + cnt;
-  const int sa = lane, sb = 64 + lane;
-  const bool va = (sa < kept) || (sa >= KEEP && sa < n_used);
-  const bool vb = sb < n_used;
-  float fa = 0.f, fb = 0.f;
-  int ia = 0, ib = 0;
-  if (va) {
-    fa = row_s[sa];
-    ia = row_i[sa];
+  float f[3];
+  int ix[3];
+  uint32_t kk[3];
+  bool v[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int s = lane + 64 * j;
+    bool ok;
+    if (s < KEEP) {
+      ok = s < kept;
+    } else if (s < kSelRowSlots) {
+      const int rg = (s - KEEP) / CAP;
+      const int ri = s - KEEP - rg * CAP;
+      const int cr = rg == 0 ? c[0] : rg == 1 ? c[1] : rg == 2 ? c[2] : c[3];
+      ok = ri < cr;
+    } else {
+      ok = false;
+    }
+    v[j] = ok;
+    f[j] = ok ? row_s[s] : 0.f;
+    ix[j] = ok ? (int)row_i[s] : 0;
+    kk[j] = ok ? order_key(f[j]) : 0u;
   }
-  if (vb) {
-    fb = row_s[sb];
-    ib = row_i[sb];
-  }
-  const uint32_t ka = va ? order_key(fa) : 0u;
-  const uint32_t kb = vb ? order_key(fb) : 0u;
 
   // Radix select of the k-th largest key.  All valid keys lie in [lo, hi]; the
   // bits above the highest bit where lo and hi differ are common to every
   // candidate threshold, so the search starts below them.
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(wave_max_u32(max(ka, kb)));
-  const uint32_t lo =
-      __builtin_amdgcn_readfirstlane(wave_min_u32(min(va ? ka : 0xffffffffu, vb ? kb : 0xffffffffu)));
+  uint32_t hmax = 0, lmin = 0xffffffffu;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    hmax = max(hmax, kk[j]);
+    lmin = min(lmin, v[j] ? kk[j] : 0xffffffffu);
+  }
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(wave_max_u32(hmax));
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(wave_min_u32(lmin));
   const uint32_t diff = hi ^ lo;
   int bit = diff ? 31 - __builtin_clz(diff) : -1;
   uint32_t t = diff ? (hi & ~((2u << bit) - 1u)) : hi;  // common prefix (bit 31 case handled below)
   if (bit == 31) t = 0;
   int n_at_t = k + 1;  // unknown; forces the tie path if the loop never lands on exactly k
   for (; bit >= 0; --bit) {
-    const uint32_t c = t | (1u << bit);
-    const int n = popc64(__ballot(ka >= c)) + popc64(__ballot(kb >= c));
+    const uint32_t cth = t | (1u << bit);
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) n += popc64(__ballot(kk[j] >= cth));
     if (n >= k) {
-      t = c;
+      t = cth;
       n_at_t = n;
       if (n == k) break;  // exactly k keys >= t: they are the winners
     }
   }
-  bool keep_a, keep_b;
+  bool keep[3];
   uint32_t theta_key;
   if (n_at_t == k) {
-    keep_a = va && ka >= t;
-    keep_b = vb && kb >= t;
     uint32_t m = 0xffffffffu;
-    if (keep_a) m = ka;
-    if (keep_b) m = min(m, kb);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      keep[j] = v[j] && kk[j] >= t;
+      if (keep[j]) m = min(m, kk[j]);
+    }
     theta_key = __builtin_amdgcn_readfirstlane(wave_min_u32(m));
   } else {
     // t is the k-th largest key itself; resolve ties at t toward lower indices
     theta_key = t;
-    keep_a = ka > t;
-    keep_b = kb > t;
-    const int n_gt = popc64(__ballot(keep_a)) + popc64(__ballot(keep_b));
-    bool eq_a = va && (ka == t), eq_b = vb && (kb == t);
+    int n_gt = 0, n_eq = 0;
+    bool eq[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      keep[j] = kk[j] > t;
+      eq[j] = v[j] && kk[j] == t;
+      n_gt += popc64(__ballot(keep[j]));
+      n_eq += popc64(__ballot(eq[j]));
+    }
     int need = k - n_gt;
-    const int n_eq = popc64(__ballot(eq_a)) + popc64(__ballot(eq_b));
     if (n_eq == need) {
-      keep_a |= eq_a;
-      keep_b |= eq_b;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) keep[j] |= eq[j];
     } else {
       for (; need > 0; --need) {
         int m = 0x7fffffff;
-        if (eq_a) m = min(m, ia);
-        if (eq_b) m = min(m, ib);
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+          if (eq[j]) m = min(m, ix[j]);
         m = wave_min_i32(m);
-        if (eq_a && ia == m) {
-          keep_a = true;
-          eq_a = false;
-        }
-        if (eq_b && ib == m) {
-          keep_b = true;
-          eq_b = false;
-        }
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+          if (eq[j] && ix[j] == m) {
+            keep[j] = true;
+            eq[j] = false;
+          }
       }
     }
   }
   // the k-th best score: an element whose key equals theta_key
-  const uint64_t eqm_a = __ballot(va && ka == theta_key);
-  const uint64_t eqm_b = __ballot(vb && kb == theta_key);
-  const float theta = eqm_a ? readlane_f(fa, __builtin_ctzll(eqm_a)) : readlane_f(fb, __builtin_ctzll(eqm_b));
-
-  const uint64_t ma = __ballot(keep_a);
-  const uint64_t mb = __ballot(keep_b);
-  const int pa = mbcnt64(ma);
-  const int pb = popc64(ma) + mbcnt64(mb);
+  float theta = 0.f;
+#pragma unroll
+  for (int j = 2; j >= 0; --j) {
+    const uint64_t e = __ballot(v[j] && kk[j] == theta_key);
+    if (e) theta = readlane_f(f[j], __builtin_ctzll(e));
+  }
+  int base = 0;
+  int pos[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const uint64_t m = __ballot(keep[j]);
+    pos[j] = base + mbcnt64(m);
+    base += popc64(m);
+  }
   // the reads above have returned (their values feed these stores)
-  if (keep_a) {
-    row_s[pa] = fa;
-    row_i[pa] = (uint16_t)ia;
-  }
-  if (keep_b) {
-    row_s[pb] = fb;
-    row_i[pb] = (uint16_t)ib;
-  }
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+    if (keep[j]) {
+      row_s[pos[j]] = f[j];
+      row_i[pos[j]] = (uint16_t)ix[j];
+    }
   wave_lds_sync();
   return theta;
 }
 
-
-__device__ __forceinline__ float key_to_float(uint32_t key) {
-  return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
-}
-
-// Merge every row of the wave at once.  Lane (g, col) owns slots
-// [32g, 32g+32) of row col: kept entries or candidates.  A row keeps the
-// min(k, kept + cnt) best of its `kept` kept entries and `cnt` candidates (a
-// row that has not yet seen k keys keeps them all and its threshold stays
-// -inf).  The radix select runs per lane over its 32 keys, with row counts
-// summed over the row's 4 lanes by permlane swaps.  Rows with exact ties at
-// the k-th value return fallback = true and are left untouched for merge_row.
+// Merge every row of the wave at once.  Lane (g, col) holds a quarter of row
+// col's kept entries (slots [g*KEEP/4, (g+1)*KEEP/4), valid below `kept`) and
+// its own `cnt` candidates.  A row keeps the min(k, total) best of its
+// `total` = kept + candidates entries (a row that has not yet seen k keys keeps
+// them all and its threshold is unchanged).  The radix select runs per lane
+// over its keys, with row counts summed over the row's 4 lanes by permlane
+// swaps.  Rows with exact ties at the k-th value return fallback = true and
+// are left untouched for merge_row_exact.
 template <int KEEP>
-__device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kept, int cnt_row, float& theta,
+__device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kept, int cnt, int total, float& theta,
                                    bool& fallback) {
+  constexpr int KQ = KEEP / 4;
+  constexpr int CAP = sel_lane_cap(KEEP);
+  constexpr int NK = KQ + CAP;
+  static_assert(NK == kSelMergeKeys, "merge width");
   const int lane = lane_id();
   const int g = lane >> 4;
-  const int base = 32 * g;
-  const int total = kept + cnt_row;
   const int kk = min(k, total);  // entries the row keeps
-  // kept entries [0, kept), then cnt_row candidates from KEEP on
-  const int n_valid = base < KEEP ? max(0, min(32, kept - base)) : max(0, min(32, KEEP + cnt_row - base));
-  uint32_t key[32];
-  int id[32];
+  const int kv = max(0, min(KQ, kept - g * KQ));
+  const float* kept_s = row_s + g * KQ;
+  const float* cand_s = row_s + KEEP + g * CAP;
+  const uint16_t* kept_i = row_i + g * KQ;
+  const uint16_t* cand_i = row_i + KEEP + g * CAP;
+  uint32_t key[NK];
+  int id[NK];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const float4 v = *reinterpret_cast<const float4*>(row_s + base + 4 * q);
-    key[4 * q + 0] = (4 * q + 0 < n_valid) ? order_key(v.x) : 0u;
-    key[4 * q + 1] = (4 * q + 1 < n_valid) ? order_key(v.y) : 0u;
-    key[4 * q + 2] = (4 * q + 2 < n_valid) ? order_key(v.z) : 0u;
-    key[4 * q + 3] = (4 * q + 3 < n_valid) ? order_key(v.w) : 0u;
+  for (int q = 0; q < NK / 4; ++q) {
+    const bool kpt = 4 * q < KQ;
+    const int o = kpt ? 4 * q : 4 * q - KQ;
+    const int lim = kpt ? kv : cnt;
+    const float4 s4 = *reinterpret_cast<const float4*>((kpt ? kept_s : cand_s) + o);
+    const uint2 i4 = *reinterpret_cast<const uint2*>((kpt ? kept_i : cand_i) + o);
+    key[4 * q + 0] = (o + 0 < lim) ? order_key(s4.x) : 0u;
+    key[4 * q + 1] = (o + 1 < lim) ? order_key(s4.y) : 0u;
+    key[4 * q + 2] = (o + 2 < lim) ? order_key(s4.z) : 0u;
+    key[4 * q + 3] = (o + 3 < lim) ? order_key(s4.w) : 0u;
+    id[4 * q + 0] = (int)(i4.x & 0xffffu);
+    id[4 * q + 1] = (int)(i4.x >> 16);
+    id[4 * q + 2] = (int)(i4.y & 0xffffu);
+    id[4 * q + 3] = (int)(i4.y >> 16);
   }
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint4 v = *reinterpret_cast<const uint4*>(row_i + base + 8 * q);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      id[8 * q + 2 * h] = (int)(w[h] & 0xffffu);
-      id[8 * q + 2 * h + 1] = (int)(w[h] >> 16);
-    }
-  }
-  // row range of valid keys
+  // valid keys are > 0 (order keys of finite or infinite floats are nonzero)
   uint32_t hi = 0, lo = 0xffffffffu;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
+  for (int i = 0; i < NK; ++i) {
     hi = max(hi, key[i]);
-    lo = min(lo, (i < n_valid) ? key[i] : 0xffffffffu);
+    lo = min(lo, key[i] ? key[i] : 0xffffffffu);
   }
   hi = max(hi, (uint32_t)xor16_i((int)hi));
   hi = max(hi, (uint32_t)xor32_i((int)hi));
@@ -257,32 +292,31 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kep
   uint32_t t = diff ? (hi & ~((2u << start) - 1u)) : hi;  // shared prefix of the row's keys
   if (start == 31) t = 0;
   const int wave_start = (int)wave_max_u32((uint32_t)(start + 1)) - 1;  // uniform loop bound
-  // a row whose entries all fit keeps every valid key (valid keys are > 0)
+  // a row whose entries all fit keeps every valid key
   bool done = total <= k;
-  if (done) t = 0;
+  if (done) t = 1;
   for (int bit = wave_start; bit >= 0; --bit) {
     if (!__ballot(!done)) break;
     const uint32_t c = t | (1u << bit);
-    int cnt = 0;
+    int n = 0;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) cnt += (key[i] >= c) ? 1 : 0;
-    int n = cnt + xor16_i(cnt);
-    n += xor32_i(n);
+    for (int i = 0; i < NK; ++i) n += (key[i] >= c) ? 1 : 0;
+    n = row_sum4(n);
     if (!done && n >= kk) {
       t = c;
       done = (n == kk);
     }
   }
-  // winners: exactly k keys >= t (done), or the k-th largest key is t itself
-  uint32_t keep_bits = 0;
+  // winners: exactly kk keys >= t (done), or the k-th largest key is t itself
+  uint64_t keep_bits = 0;
   uint32_t theta_key;
   bool tie_row = false;
   if (done) {
     uint32_t m = 0xffffffffu;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const bool kp = (i < n_valid) && key[i] >= t;
-      keep_bits |= kp ? (1u << i) : 0u;
+    for (int i = 0; i < NK; ++i) {
+      const bool kp = key[i] >= t;
+      keep_bits |= kp ? (1ull << i) : 0ull;
       m = kp ? min(m, key[i]) : m;
     }
     m = min(m, (uint32_t)xor16_i((int)m));
@@ -291,44 +325,44 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kep
   } else {
     int gt = 0, eq = 0;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < NK; ++i) {
       gt += (key[i] > t) ? 1 : 0;
-      eq += ((i < n_valid) && key[i] == t) ? 1 : 0;
+      eq += (key[i] == t) ? 1 : 0;
     }
-    gt += xor16_i(gt);
-    gt += xor32_i(gt);
-    eq += xor16_i(eq);
-    eq += xor32_i(eq);
+    gt = row_sum4(gt);
+    eq = row_sum4(eq);
     tie_row = (eq != kk - gt);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) keep_bits |= ((i < n_valid) && key[i] >= t) ? (1u << i) : 0u;
+    for (int i = 0; i < NK; ++i) keep_bits |= (key[i] >= t) ? (1ull << i) : 0ull;
     theta_key = t;
   }
   fallback = tie_row;
-  // compact the winners of non-tie rows to slots [0, k)
-  const int w = __builtin_popcount(keep_bits);
-  const int w1 = xor16_i(w);
-  const int w2 = xor32_i(w);
-  const int w3 = xor16_i(w2);
-  int pos = (g == 0) ? 0 : (g == 1) ? w1 : (g == 2) ? (w2 + w3) : (w1 + w2 + w3);
+  // compact the winners of non-tie rows to kept slots [0, kk): lane g starts
+  // after the winners of the row's lanes g' < g
+  const int w = popc64(keep_bits);
+  const int w1 = xor16_i(w);   // lane g ^ 1
+  const int w2 = xor32_i(w);   // lane g ^ 2
+  const int w3 = xor16_i(w2);  // lane g ^ 3
+  int pos = ((g & 1) ? w1 : 0) + ((g & 2) ? (w2 + w3) : 0);
   if (!tie_row) {
+    // the reads above have returned (their values feed these stores)
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const bool kp = (keep_bits >> i) & 1u;
-      const int dst = kp ? pos : kSelTrash;
-      row_s[dst] = key_to_float(key[i]);
-      row_i[dst] = (uint16_t)id[i];
-      pos += kp ? 1 : 0;
+    for (int i = 0; i < NK; ++i) {
+      if ((keep_bits >> i) & 1ull) {
+        row_s[pos] = key_to_float(key[i]);
+        row_i[pos] = (uint16_t)id[i];
+        ++pos;
+      }
     }
-    theta = total < k ? -INFINITY : key_to_float(theta_key);
+    if (total >= k) theta = key_to_float(theta_key);
   }
   wave_lds_sync();
 }
 
-// VEC: r == 4*RQ and 16-byte aligned key rows -> unconditional float4 chunk loads.
+// VEC: r == 4*RQ and 16-byte aligned key rows -> float4 chunk loads.
 template <int RQ, bool VEC, int KEEP>
 __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs a) {
-  constexpr int kMergeAt = merge_at(KEEP);
+  constexpr int CAP = sel_lane_cap(KEEP);
   constexpr int RP = 4 * RQ;
   constexpr int KSTRIDE = RP + 4;  // padded key row (floats)
 
@@ -352,11 +386,10 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
   const float* qb = a.q + (int64_t)b * a.q_batch_stride;
   const float* kbase = a.key + (int64_t)b * a.k_batch_stride;
   const int k = a.k;
+  const int ldk = (int)a.ldk;
 
   // ---- set-up -------------------------------------------------------------
   for (int i = tid; i < RP; i += blockDim.x) s_scale[i] = (i < a.r) ? (a.scale ? a.scale[i] : 1.0f) : 0.0f;
-  if (!VEC)
-    for (int i = tid; i < 2 * kSelChunk * KSTRIDE; i += blockDim.x) (&s_key[0][0])[i] = 0.0f;
   __syncthreads();
 
   // ---- query fragment in registers ------------------------------------------
@@ -380,21 +413,28 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
   const float inv_temp = 1.0f / a.temperature;
   const bool scale_key = !a.scale_on_query;
 
-  // ---- key chunk loader ---------------------------------------------------
+  // ---- key chunk loader: buffer loads relative to the chunk's first row;
+  // rows past Nk (and padding columns) read as zeros and are masked later.
+  // Two register sets hold the chunks two and three ahead of the one being
+  // scored, so a load has two chunk iterations to return before its store.
   constexpr int kChunkVals = kSelChunk * RP;
   constexpr int kChunkF4 = kChunkVals / 4;
   constexpr int kLoads = VEC ? (kChunkF4 + 255) / 256 : (kChunkVals + 255) / 256;
-  float4 pf4[VEC ? kLoads : 1];
-  float pf1[VEC ? 1 : kLoads];
-  auto load_chunk = [&](int c0) {
+  float4 pf4[2][VEC ? kLoads : 1];
+  float pf1[2][VEC ? 1 : kLoads];
+  // SET is a compile-time register set (std::integral_constant), so the
+  // prefetch registers stay in VGPRs.
+  auto load_chunk = [&](auto SET, int c) {
+    constexpr int S = decltype(SET)::value;
+    const int c0 = c * kSelChunk;
+    const auto rs = make_rsrc(kbase + (int64_t)c0 * ldk, 0x80000000u);
     if constexpr (VEC) {
 #pragma unroll
       for (int u = 0; u < kLoads; ++u) {
         const int f = tid + u * 256;
         if (kChunkF4 % 256 == 0 || f < kChunkF4) {
           const int rrow = f / RQ, c4 = f % RQ;
-          const int krow = min(c0 + rrow, a.Nk - 1);  // tail rows: a valid row, masked later
-          pf4[u] = *reinterpret_cast<const float4*>(kbase + (int64_t)krow * a.ldk + 4 * c4);
+          pf4[S][u] = buf_load4(rs, c0 + rrow < a.Nk ? (uint32_t)(rrow * ldk + 4 * c4) * 4u : kOobOffset);
         }
       }
     } else {
@@ -402,21 +442,20 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
       for (int u = 0; u < kLoads; ++u) {
         const int e = tid + u * 256;
         const int rrow = e / RP, rc = e % RP;
-        const int krow = c0 + rrow;
-        float v = 0.0f;
-        if (e < kChunkVals && rc < a.r && krow < a.Nk) v = kbase[(int64_t)krow * a.ldk + rc];
-        pf1[u] = v;
+        const bool ok = e < kChunkVals && rc < a.r && c0 + rrow < a.Nk;
+        pf1[S][u] = buf_load1(rs, ok ? (uint32_t)(rrow * ldk + rc) * 4u : kOobOffset);
       }
     }
   };
-  auto store_chunk = [&](int buf) {
+  auto store_chunk = [&](auto SET) {
+    constexpr int S = decltype(SET)::value;  // register set == LDS buffer
     if constexpr (VEC) {
 #pragma unroll
       for (int u = 0; u < kLoads; ++u) {
         const int f = tid + u * 256;
         if (kChunkF4 % 256 == 0 || f < kChunkF4) {
           const int rrow = f / RQ, c4 = f % RQ;
-          float4 v = pf4[u];
+          float4 v = pf4[S][u];
           if (scale_key) {
             const float4 sc = *reinterpret_cast<const float4*>(&s_scale[4 * c4]);
             v.x *= sc.x;
@@ -424,7 +463,7 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
             v.z *= sc.z;
             v.w *= sc.w;
           }
-          *reinterpret_cast<float4*>(&s_key[buf][rrow * KSTRIDE + 4 * c4]) = v;
+          *reinterpret_cast<float4*>(&s_key[S][rrow * KSTRIDE + 4 * c4]) = v;
         }
       }
     } else {
@@ -433,27 +472,45 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
         const int e = tid + u * 256;
         if (e < kChunkVals) {
           const int rrow = e / RP, rc = e % RP;
-          s_key[buf][rrow * KSTRIDE + rc] = scale_key ? pf1[u] * s_scale[rc] : pf1[u];
+          s_key[S][rrow * KSTRIDE + rc] = scale_key ? pf1[S][u] * s_scale[rc] : pf1[S][u];
         }
       }
     }
   };
+  constexpr std::integral_constant<int, 0> kSet0{};
+  constexpr std::integral_constant<int, 1> kSet1{};
 
   const int nchunks = (a.Nk + kSelChunk - 1) / kSelChunk;
-  load_chunk(0);
-  store_chunk(0);
-  __syncthreads();
 
   float theta = row_ok ? -INFINITY : INFINITY;  // invalid rows never admit
-  int cnt = 0;                                  // candidates waiting for this lane's row
-  int kept = 0;                                 // valid kept entries of this lane's row (<= k)
+  int cnt = 0;   // candidates in this lane's region of its row
+  int kept = 0;  // valid kept entries of this lane's row (<= k)
   float* my_slot_s = s_slot_s + lrow * kSelScoreStride;
   uint16_t* my_slot_i = s_slot_i + lrow * kSelIndexStride;
+  float* my_cand_s = my_slot_s + KEEP + g * CAP;
+  uint16_t* my_cand_i = my_slot_i + KEEP + g * CAP;
+
+  // chunk c lives in register set c & 1 and LDS buffer c & 1
+  load_chunk(kSet0, 0);
+  store_chunk(kSet0);
+  if (nchunks > 1) load_chunk(kSet1, 1);
+  if (nchunks > 2) load_chunk(kSet0, 2);
+  __syncthreads();
 
   for (int c = 0; c < nchunks; ++c) {
     const int cur = c & 1;
     const int c0 = c * kSelChunk;
-    if (c + 1 < nchunks) load_chunk(c0 + kSelChunk);
+    // chunk c + 1 into the other LDS buffer (read by everyone before the last
+    // barrier), then reuse its registers for chunk c + 3
+    if (c + 1 < nchunks) {
+      if (cur == 0) {
+        store_chunk(kSet1);
+        if (c + 3 < nchunks) load_chunk(kSet1, c + 3);
+      } else {
+        store_chunk(kSet0);
+        if (c + 3 < nchunks) load_chunk(kSet0, c + 3);
+      }
+    }
 
     // -- scores for 32 keys x 16 query rows (two MFMA tiles) --
     floatx4 acc0 = {0.f, 0.f, 0.f, 0.f};
@@ -476,9 +533,9 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
       }
     } else {
 #pragma unroll
-      for (int s = 0; s < RQ; ++s) {
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[s], qf[s], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[s], qf[s], acc1, 0, 0, 0);
+      for (int q = 0; q < RQ; ++q) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[q], qf[q], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[q], qf[q], acc1, 0, 0, 0);
       }
     }
 
@@ -495,54 +552,40 @@ __global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs 
 #pragma unroll
     for (int u = 0; u < 8; ++u) any |= __ballot(sc[u] > theta);
     if (any) {
-      uint32_t pass_mask = 0;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) pass_mask |= (sc[u] > theta) ? (1u << u) : 0u;
-      // counts of the row's 4 lanes (lane groups g^1, g^2, g^3) via permlane swaps
-      const int np = __builtin_popcount(pass_mask);
-      const int n1 = xor16_i(np);
-      const int n2 = xor32_i(np);
-      const int n3 = xor16_i(n2);
-      const int excl = (g == 0) ? 0 : (g == 1) ? n1 : (g == 2) ? (n2 + n3) : (n1 + n2 + n3);
-      const int total = np + n1 + n2 + n3;
-      int pos = KEEP + cnt + excl;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const bool ok = (pass_mask >> u) & 1u;
-        const int dst = ok ? pos : kSelTrash;
-        my_slot_s[dst] = sc[u];
-        my_slot_i[dst] = (uint16_t)(c0 + (u >> 2) * 16 + 4 * g + (u & 3));
-        pos += ok ? 1 : 0;
+        if (sc[u] > theta) {
+          my_cand_s[cnt] = sc[u];
+          my_cand_i[cnt] = (uint16_t)(c0 + (u >> 2) * 16 + 4 * g + (u & 3));
+          ++cnt;
+        }
       }
-      cnt += total;
-      wave_lds_sync();
     }
 
-    // -- merge rows whose candidates filled up (or everything at the end) --
+    // -- merge rows once a lane region is nearly full (or everything at the end) --
     const bool last = (c + 1 == nchunks);
-    if (__ballot(lane < kSelRowsPerWave && (cnt >= kMergeAt || (last && cnt > 0)))) {
+    if (__ballot(cnt > CAP - 8 || (last && cnt > 0))) {
+      wave_lds_sync();
+      const int total = kept + row_sum4(cnt);
       bool fallback;
-      merge_rows_batched<KEEP>(my_slot_s, my_slot_i, k, kept, cnt, theta, fallback);
+      merge_rows_batched<KEEP>(my_slot_s, my_slot_i, k, kept, cnt, total, theta, fallback);
       // rows with exact ties at the k-th value: exact per-row merge (such a
       // row holds more than k entries, so the merge fills it)
       uint64_t m = __ballot(lane < kSelRowsPerWave && fallback);
       while (m) {
         const int t = __builtin_ctzll(m);
         m &= m - 1;
-        const int row_cnt = readlane_i(cnt, t);
-        const int row_kept = readlane_i(kept, t);
+        const int rc[4] = {readlane_i(cnt, t), readlane_i(cnt, t + 16), readlane_i(cnt, t + 32),
+                           readlane_i(cnt, t + 48)};
         const int slot = wave * kSelRowsPerWave + t;
-        const float th = merge_row<KEEP>(s_slot_s + slot * kSelScoreStride, s_slot_i + slot * kSelIndexStride, k,
-                                         row_kept, row_cnt);
+        const float th = merge_row_exact<KEEP>(s_slot_s + slot * kSelScoreStride, s_slot_i + slot * kSelIndexStride,
+                                               k, readlane_i(kept, t), rc);
         if (col == t) theta = th;
       }
       if (!row_ok) theta = INFINITY;  // rows past Nq stay closed
-      kept = min(k, kept + cnt);
+      kept = min(k, total);
       cnt = 0;
     }
-
-    // -- next key chunk into the other LDS buffer --
-    if (c + 1 < nchunks) store_chunk(cur ^ 1);
     __syncthreads();
   }
 
@@ -584,6 +627,8 @@ int launch_topk_select(const SelectArgs& a, hipStream_t stream) {
   JN_REQUIRE(a.Nk <= kSelMaxKeys, kUnsupported, "top-k select supports at most %d keys (got %d)", kSelMaxKeys, a.Nk);
   JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128] (got %d)", a.r);
   JN_REQUIRE(a.temperature > 0.0f, kInvalidArgument, "temperature must be positive");
+  JN_REQUIRE(a.ldk >= a.r && a.ldk < (1 << 22), kUnsupported, "key row stride must be in [r, 2^22) (got %lld)",
+             (long long)a.ldk);
   const int tiles = (a.Nq + kSelRows - 1) / kSelRows;
   const int64_t blocks = (int64_t)tiles * a.B;
   JN_REQUIRE(blocks > 0 && blocks < (1LL << 31), kInvalidArgument, "bad grid size");

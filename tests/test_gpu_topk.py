@@ -66,7 +66,9 @@ def _check_select(idx, score, ref_scores, k):
 
 @pytest.mark.parametrize("r,k,Nq,Nk", [(3, 2, 9, 9), (16, 8, 256, 256), (64, 32, 200, 333), (64, 1, 70, 50),
                                        (32, 16, 130, 1024), (100, 5, 64, 97), (64, 33, 100, 300),
-                                       (16, 48, 150, 49), (64, 64, 257, 2000), (8, 64, 64, 65)])
+                                       (16, 48, 150, 49), (64, 64, 257, 2000), (8, 64, 64, 65),
+                                       (64, 32, 130, 4096), (16, 8, 70, 2048), (64, 64, 100, 3001),
+                                       (5, 3, 64, 2500)])
 def test_select_matches_oracle(dev, r, k, Nq, Nk):
     import jakal_net_native as jn
 
@@ -85,15 +87,43 @@ def test_select_matches_oracle(dev, r, k, Nq, Nk):
         _check_select(idx.cpu().numpy(), score.cpu().numpy(), ref, k)
 
 
-def test_select_exact_ties_go_to_lower_index(dev):
+@pytest.mark.parametrize("Nk", [200, 2100])
+def test_select_exact_ties_go_to_lower_index(dev, Nk):
     import jakal_net_native as jn
 
     # all keys identical -> all scores tie; the k lowest indices must win
-    B, Nq, Nk, r, k = 1, 64, 200, 8, 5
+    B, Nq, r, k = 1, 64, 8, 5
     q = torch.randn(B, Nq, r)
     key = torch.ones(B, Nk, r)
     idx, _ = jn.low_rank_topk_select(q.to(dev), key.to(dev), None, None, False, 1.0, k)
     assert (idx.cpu() == torch.arange(k, dtype=torch.int32)).all()
+
+
+@pytest.mark.parametrize("k,groups", [(8, (4, 2)), (40, (4, 4))])
+def test_select_few_dominant_keys(dev, k, groups):
+    """Even rows score a few keys near the start (one in each 4-key group of
+    several 16-key tiles) far above everything else, so fewer than k keys stand
+    out and the rest of the selection comes from the ordinary keys.  Odd rows
+    see ordinary random scores."""
+    import jakal_net_native as jn
+
+    g = torch.Generator().manual_seed(77 + k)
+    B, Nq, Nk, r = 1, 128, 2048, 4
+    ng, nh = groups
+    span = 256 // nh
+    special = [4 * gi + span * h for h in range(nh) for gi in range(ng)]
+    key = torch.zeros(B, Nk, r)
+    key[..., 0] = torch.randn(B, Nk, generator=g)
+    key[..., 1] = torch.randn(B, Nk, generator=g)
+    key[0, special, 0] = 100.0 + 0.5 * torch.arange(len(special), dtype=torch.float32)
+    q = torch.zeros(B, Nq, r)
+    q[0, 0::2, 0] = 1.0
+    q[0, 1::2, 1] = 1.0
+    idx, score = jn.low_rank_topk_select(q.to(dev), key.to(dev), None, None, False, 1.0, k)
+    ref = q.double().numpy() @ np.swapaxes(key.double().numpy(), 1, 2)
+    _check_select(idx.cpu().numpy(), score.cpu().numpy(), ref, k)
+    top = np.sort(idx.cpu().numpy()[0, 0::2], axis=-1)
+    assert set(special) <= set(top[0].tolist())
 
 
 def _c1_inputs(seed=1001, B=2, N=256, D=64, r=16):

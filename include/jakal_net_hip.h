@@ -237,6 +237,49 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
                                 float* grad_target_weight, float* grad_core_weight, float* grad_bias,
                                 void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
+/*
+ * Dense pairwise transition: every source routes to every destination.
+ *   l[b,j,k] = ((P_s[j] * w) . P_t[k] + bias) / temperature,
+ *   P_s = src_val . Ws^T [B*Ns, r], P_t = dst_val . Wt^T [B*Nd, r];
+ *   R[b,j,:] = compress(l[b,j,:]) over destinations: compress_kind 0 softmax,
+ *   1 sign(l) * softmax(|l|);
+ *   delta_state[b,k] = sum_j R[b,j,k] rho_j ps_j, delta_val[b,k] = sum_j R[b,j,k] rho_j pv_j.
+ * Writes src_proj [B*Ns, r], dst_proj [B*Nd, r] and routes [B,Ns,Nd] (all
+ * caller-allocated) for the backward.  Allocates nothing.
+ * Replaces transition_pairwise_dense (native/jakal_net_native.cpp:6705-6914),
+ * signature at :6705-6725, called from transition_pairwise_dense_native
+ * (src/jakal_net/native_backend.py:5755-5822).
+ */
+int jn_transition_dense_forward(const float* sender_strength, const float* src_val, const float* dst_val,
+                                const float* projected_state, const float* projected_val, const float* source_weight,
+                                const float* target_weight, const float* core_weight, const float* bias,
+                                float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                                int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                int32_t compress_kind, float* delta_state, float* delta_val, float* src_proj,
+                                float* dst_proj, float* routes, jn_stream_t stream);
+
+/* Workspace bytes jn_transition_dense_backward needs (0 on invalid sizes). */
+size_t jn_transition_dense_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                           int64_t dst_dim, int64_t val_dim, int64_t rank);
+
+/*
+ * Backward of jn_transition_dense_forward given grad_delta_state [B,Nd] and
+ * grad_delta_val [B,Nd,Dv]; src_proj, dst_proj and routes are the forward's.
+ * Output pointers may be NULL to skip a gradient (grad_core_weight is always
+ * written).  The reference differentiates its composite dense transition with
+ * autograd (native/jakal_net_native.cpp:6745-6774 records ATen ops).
+ */
+int jn_transition_dense_backward(const float* sender_strength, const float* src_val, const float* dst_val,
+                                 const float* projected_state, const float* projected_val, const float* source_weight,
+                                 const float* target_weight, const float* core_weight, const float* src_proj,
+                                 const float* dst_proj, const float* routes, const float* grad_delta_state,
+                                 const float* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes,
+                                 int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                 int32_t compress_kind, float* grad_sender_strength, float* grad_src_val,
+                                 float* grad_dst_val, float* grad_projected_state, float* grad_projected_val,
+                                 float* grad_source_weight, float* grad_target_weight, float* grad_core_weight,
+                                 float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

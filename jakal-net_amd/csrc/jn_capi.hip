@@ -227,6 +227,48 @@ int check_dense_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out
   return kOk;
 }
 
+struct TransitionDenseScratch {
+  float* G;       // [B, Ns, Nd] route / logit gradient
+  float* dPs;     // [B*Ns, r]
+  float* dPt;     // [B*Nd, r]
+  float* rowsum;  // [B*Ns]
+  float* part_c;  // [B*Ns, r]
+  float* stage;
+  float* splitk;
+  size_t bytes;
+};
+
+TransitionDenseScratch carve_transition_dense(void* base, size_t size, int64_t B, int64_t Ns, int64_t Nd,
+                                              int64_t Dsrc, int64_t Ddst, int64_t r) {
+  Workspace ws(base, size);
+  TransitionDenseScratch s{};
+  s.G = ws.take<float>(B * Ns * Nd);
+  s.dPs = ws.take<float>(B * Ns * r);
+  s.dPt = ws.take<float>(B * Nd * r);
+  s.rowsum = ws.take<float>(B * Ns);
+  s.part_c = ws.take<float>(B * Ns * r);
+  s.stage = ws.take<float>(finalize_stage_floats((int)r));
+  const size_t sk = std::max(gemm_grad_weight_workspace((int)r, (int)Dsrc, (int)(B * Ns)),
+                             gemm_grad_weight_workspace((int)r, (int)Ddst, (int)(B * Nd)));
+  s.splitk = ws.take<float>(sk / sizeof(float));
+  s.bytes = ws.used;
+  return s;
+}
+
+int check_transition_dense_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t Dsrc, int64_t Ddst, int64_t Dv,
+                                  int64_t rank, int32_t compress_kind, float temperature) {
+  JN_REQUIRE(batch >= 1 && Ns >= 1 && Nd >= 1 && Dsrc >= 1 && Ddst >= 1 && Dv >= 1, kInvalidArgument,
+             "batch, node counts and dims must be positive");
+  JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
+  JN_REQUIRE(compress_kind == 0 || compress_kind == 1, kUnsupported,
+             "route compress kind must be 0 (softmax) or 1 (signed_abs_softmax), got %d", compress_kind);
+  JN_REQUIRE(temperature > 0.0f, kInvalidArgument, "temperature must be positive");
+  JN_REQUIRE(batch < 65536 && fits_int(batch * Ns) && fits_int(batch * Nd) && Ns < (1LL << 22) &&
+                 Nd < (1LL << 22) && fits_int(Ns * Dv) && fits_int(Nd * Dv) && fits_int(Ns * Nd),
+             kUnsupported, "dense transition shape too large");
+  return kOk;
+}
+
 // Backward of any edge-list propagation (top-k or window): the edge list
 // (edge_index, edge_score) [B*N, k] is what the forward aggregated.
 int propagation_edges_backward(const float* layer_val, const float* projected_state, const float* projected_val,
@@ -957,6 +999,151 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
 
   // 5. w_hat and bias grads
   return launch_finalize_small_grads(s.part_c, M, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st);
+}
+
+int jn_transition_dense_forward(const float* sender_strength, const float* src_val, const float* dst_val,
+                                const float* projected_state, const float* projected_val, const float* source_weight,
+                                const float* target_weight, const float* core_weight, const float* bias,
+                                float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                                int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                int32_t compress_kind, float* delta_state, float* delta_val, float* src_proj,
+                                float* dst_proj, float* routes, jn_stream_t stream) {
+  int rc = check_transition_dense_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, compress_kind,
+                                         temperature);
+  if (rc) return rc;
+  JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
+                 target_weight && core_weight && delta_state && delta_val && src_proj && dst_proj && routes,
+             kInvalidArgument, "null tensor pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int B = (int)batch, Ns = (int)src_nodes, Nd = (int)dst_nodes, r = (int)rank, Dv = (int)val_dim;
+
+  // 1. projections P_s = src . Ws^T, P_t = dst . Wt^T  (modules.py:435-437)
+  rc = gemm_project(src_val, src_dim, source_weight, source_weight, r, src_dim, src_proj, r, B * Ns, r, (int)src_dim,
+                    st);
+  if (rc) return rc;
+  rc = gemm_project(dst_val, dst_dim, target_weight, target_weight, r, dst_dim, dst_proj, r, B * Nd, r, (int)dst_dim,
+                    st);
+  if (rc) return rc;
+  // 2. raw logits L_b = (P_s diag(w)) P_t^T
+  BatchedGemm lg{};
+  lg.A = src_proj; lg.lda = r; lg.a_bs = (int64_t)Ns * r; lg.a_kcontig = true;
+  lg.B = dst_proj; lg.ldb = r; lg.b_bs = (int64_t)Nd * r; lg.b_kcontig = true;
+  lg.C = routes; lg.ldc = Nd; lg.c_bs = (int64_t)Ns * Nd;
+  lg.a_kscale = core_weight;
+  lg.M = Ns; lg.N = Nd; lg.K = r; lg.batch = B;
+  rc = gemm_batched(lg, kGemmRouteLogits, st);
+  if (rc) return rc;
+  // 3. routes R = compress((L + b) / T) over destinations, in place
+  rc = launch_route_dense_compress(routes, bias, 1.0f / temperature, B, Ns, Nd, compress_kind, st);
+  if (rc) return rc;
+  // 4. delta_state = R^T (rho * ps), delta_val = R^T diag(rho) pv
+  rc = launch_route_dense_colsum(routes, sender_strength, projected_state, B, Ns, Nd, delta_state, st);
+  if (rc) return rc;
+  BatchedGemm ag{};
+  ag.A = routes; ag.lda = Nd; ag.a_bs = (int64_t)Ns * Nd; ag.a_kcontig = false;
+  ag.B = projected_val; ag.ldb = Dv; ag.b_bs = (int64_t)Ns * Dv; ag.b_kcontig = false;
+  ag.C = delta_val; ag.ldc = Dv; ag.c_bs = (int64_t)Nd * Dv;
+  ag.a_kscale = sender_strength; ag.ks_bs = Ns;
+  ag.M = Nd; ag.N = Dv; ag.K = Ns; ag.batch = B;
+  return gemm_batched(ag, kGemmRouteAggregate, st);
+}
+
+size_t jn_transition_dense_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                           int64_t dst_dim, int64_t val_dim, int64_t rank) {
+  (void)val_dim;
+  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || rank < 1) return 0;
+  return carve_transition_dense(nullptr, 0, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank).bytes;
+}
+
+int jn_transition_dense_backward(const float* sender_strength, const float* src_val, const float* dst_val,
+                                 const float* projected_state, const float* projected_val, const float* source_weight,
+                                 const float* target_weight, const float* core_weight, const float* src_proj,
+                                 const float* dst_proj, const float* routes, const float* grad_delta_state,
+                                 const float* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes,
+                                 int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                 int32_t compress_kind, float* grad_sender_strength, float* grad_src_val,
+                                 float* grad_dst_val, float* grad_projected_state, float* grad_projected_val,
+                                 float* grad_source_weight, float* grad_target_weight, float* grad_core_weight,
+                                 float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_transition_dense_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, compress_kind,
+                                         temperature);
+  if (rc) return rc;
+  JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
+                 target_weight && core_weight && src_proj && dst_proj && routes && grad_delta_state &&
+                 grad_delta_val,
+             kInvalidArgument, "null tensor pointer");
+  TransitionDenseScratch s =
+      carve_transition_dense(workspace, workspace_bytes, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank);
+  JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
+             "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int B = (int)batch, Ns = (int)src_nodes, Nd = (int)dst_nodes, r = (int)rank, Dv = (int)val_dim;
+
+  // 1. H_b = pv_b gdv_b^T, then the raw-logit gradient in place (+ sender, state grads, row sums)
+  BatchedGemm hg{};
+  hg.A = projected_val; hg.lda = Dv; hg.a_bs = (int64_t)Ns * Dv; hg.a_kcontig = true;
+  hg.B = grad_delta_val; hg.ldb = Dv; hg.b_bs = (int64_t)Nd * Dv; hg.b_kcontig = true;
+  hg.C = s.G; hg.ldc = Nd; hg.c_bs = (int64_t)Ns * Nd;
+  hg.M = Ns; hg.N = Nd; hg.K = Dv; hg.batch = B;
+  rc = gemm_batched(hg, kGemmRouteEdgeGrad, st);
+  if (rc) return rc;
+  rc = launch_route_dense_compress_backward(s.G, routes, sender_strength, projected_state, grad_delta_state, B, Ns,
+                                            Nd, compress_kind, 1.0f / temperature, grad_sender_strength,
+                                            grad_projected_state, s.rowsum, st);
+  if (rc) return rc;
+  // 2. grad pv = diag(rho) R gdv
+  if (grad_projected_val) {
+    BatchedGemm vg{};
+    vg.A = routes; vg.lda = Nd; vg.a_bs = (int64_t)Ns * Nd; vg.a_kcontig = true;
+    vg.B = grad_delta_val; vg.ldb = Dv; vg.b_bs = (int64_t)Nd * Dv; vg.b_kcontig = false;
+    vg.C = grad_projected_val; vg.ldc = Dv; vg.c_bs = (int64_t)Ns * Dv;
+    vg.c_mscale = sender_strength; vg.ms_bs = Ns;
+    vg.M = Ns; vg.N = Dv; vg.K = Nd; vg.batch = B;
+    rc = gemm_batched(vg, kGemmRouteValueGrad, st);
+    if (rc) return rc;
+  }
+  // 3. projection grads: dP_s = w * (G P_t) (+ w partials), dP_t = w * (G^T P_s)
+  BatchedGemm sg{};
+  sg.A = s.G; sg.lda = Nd; sg.a_bs = (int64_t)Ns * Nd; sg.a_kcontig = true;
+  sg.B = dst_proj; sg.ldb = r; sg.b_bs = (int64_t)Nd * r; sg.b_kcontig = false;
+  sg.C = s.dPs; sg.ldc = r; sg.c_bs = (int64_t)Ns * r;
+  sg.M = Ns; sg.N = r; sg.K = Nd; sg.batch = B;
+  rc = gemm_batched(sg, kGemmRouteSourceGrad, st);
+  if (rc) return rc;
+  rc = launch_scale_grad_partials(s.dPs, r, src_proj, r, core_weight, r, (int64_t)B * Ns, s.part_c, st);
+  if (rc) return rc;
+  BatchedGemm tg{};
+  tg.A = s.G; tg.lda = Nd; tg.a_bs = (int64_t)Ns * Nd; tg.a_kcontig = false;
+  tg.B = src_proj; tg.ldb = r; tg.b_bs = (int64_t)Ns * r; tg.b_kcontig = false;
+  tg.C = s.dPt; tg.ldc = r; tg.c_bs = (int64_t)Nd * r;
+  tg.c_nscale = core_weight;
+  tg.M = Nd; tg.N = r; tg.K = Ns; tg.batch = B;
+  rc = gemm_batched(tg, kGemmRouteTargetGrad, st);
+  if (rc) return rc;
+  // 4. projection weight and input grads
+  const int Ms = B * Ns, Mt = B * Nd;
+  if (grad_source_weight) {
+    rc = gemm_grad_weight(s.dPs, r, src_val, src_dim, grad_source_weight, grad_source_weight, r, r, (int)src_dim, Ms,
+                          s.splitk, st);
+    if (rc) return rc;
+  }
+  if (grad_target_weight) {
+    rc = gemm_grad_weight(s.dPt, r, dst_val, dst_dim, grad_target_weight, grad_target_weight, r, r, (int)dst_dim, Mt,
+                          s.splitk, st);
+    if (rc) return rc;
+  }
+  if (grad_src_val) {
+    rc = gemm_grad_input(s.dPs, r, source_weight, source_weight, r, src_dim, nullptr, src_dim, grad_src_val, src_dim,
+                         Ms, (int)src_dim, r, st);
+    if (rc) return rc;
+  }
+  if (grad_dst_val) {
+    rc = gemm_grad_input(s.dPt, r, target_weight, target_weight, r, dst_dim, nullptr, dst_dim, grad_dst_val, dst_dim,
+                         Mt, (int)dst_dim, r, st);
+    if (rc) return rc;
+  }
+  // 5. w and bias grads
+  return launch_finalize_small_grads(s.part_c, Ms, r, grad_core_weight, 0, s.rowsum, Ms, grad_bias, s.stage, st);
 }
 
 }  // extern "C"

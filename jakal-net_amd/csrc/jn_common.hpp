@@ -145,6 +145,11 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 __device__ __forceinline__ int wave_min_i32(int v) {
   return wave_reduce_i(v, [](int a, int b) { return min(a, b); });
 }
+__device__ __forceinline__ float wave_max_f(float v) {
+  return __int_as_float(wave_reduce_i(__float_as_int(v), [](int a, int b) {
+    return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
+  }));
+}
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {

@@ -39,6 +39,8 @@ struct GemmArgs {
   int64_t a_bs, b_bs, c_bs, add_bs;  // per-batch element strides
   const float* a_kscale;   // optional: A(m, k) *= a_kscale[k]
   const float* c_nscale;   // optional: C(m, n) = acc * c_nscale[n] (+ addend)
+  const float* c_mscale;   // optional: C(m, n) *= c_mscale[m] (before the addend)
+  int64_t ks_bs, ms_bs;    // per-batch element strides of a_kscale and c_mscale
 };
 
 constexpr int kGBM = 64, kGBK = 16, kGStride = kGBK + 4;
@@ -76,6 +78,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
   const float* gB0 = g.B0 + bz * g.b_bs;
   const float* gB1 = g.B1 + bz * g.b_bs;
   const float* gadd = g.addend ? g.addend + bz * g.add_bs : nullptr;
+  const float* kscale = g.a_kscale ? g.a_kscale + bz * g.ks_bs : nullptr;
+  const float* mscale = g.c_mscale ? g.c_mscale + bz * g.ms_bs : nullptr;
   float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
 
   float ra[LPT][4], rb[LPT][4];
@@ -95,9 +99,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) ra[u][q] = (m < g.M && kq + q < kend) ? p[q] : 0.0f;
         }
-        if (g.a_kscale) {
+        if (kscale) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) ra[u][q] *= (kq + q < kend) ? g.a_kscale[kq + q] : 0.0f;
+          for (int q = 0; q < 4; ++q) ra[u][q] *= (kq + q < kend) ? kscale[kq + q] : 0.0f;
         }
       } else {
         const int kk = k0 + e / (TILE / 4), mq = m0 + (e % (TILE / 4)) * 4;
@@ -109,8 +113,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) ra[u][q] = (kk < kend && mq + q < g.M) ? p[q] : 0.0f;
         }
-        if (g.a_kscale) {
-          const float sc = kk < kend ? g.a_kscale[kk] : 0.0f;
+        if (kscale) {
+          const float sc = kk < kend ? kscale[kk] : 0.0f;
 #pragma unroll
           for (int q = 0; q < 4; ++q) ra[u][q] *= sc;
         }
@@ -213,6 +217,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
         if (m < g.M && n < g.N) {
           float x = acc[mt][nt][v];
           if (g.c_nscale) x *= g.c_nscale[n];
+          if (mscale) x *= mscale[m];
           if (gadd) x += gadd[(int64_t)m * g.ld_add + n];
           C[(int64_t)m * g.ldc + n] = x;
         }
@@ -235,7 +240,14 @@ constexpr GemmUseInfo kGemmUses[] = {
     {false, false, false, false, "gemm_f32_kernel<dense_value_grad>"},
     {true, false, false, false, "gemm_f32_kernel<dense_target_grad>"},
     {false, false, false, false, "gemm_f32_kernel<dense_source_grad>"},
+    {true, true, true, false, "gemm_f32_kernel<route_logits>"},
+    {false, false, true, false, "gemm_f32_kernel<route_aggregate>"},
+    {true, true, false, false, "gemm_f32_kernel<route_edge_grad>"},
+    {true, false, false, false, "gemm_f32_kernel<route_value_grad>"},
+    {true, false, false, false, "gemm_f32_kernel<route_source_grad>"},
+    {false, false, false, false, "gemm_f32_kernel<route_target_grad>"},
 };
+static_assert(sizeof(kGemmUses) / sizeof(kGemmUses[0]) == kGemmRouteTargetGrad + 1, "one entry per GemmUse");
 
 // ---- 128 x 128 path --------------------------------------------------------
 // Workgroup tile 128 x 128, K staged through LDS in slices of BK (double
@@ -319,6 +331,8 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
   const float* gB0 = g.B0 + bz * g.b_bs;
   const float* gB1 = g.B1 + bz * g.b_bs;
   const float* gadd = g.addend ? g.addend + bz * g.add_bs : nullptr;
+  const float* kscale = g.a_kscale ? g.a_kscale + bz * g.ks_bs : nullptr;
+  const float* mscale = g.c_mscale ? g.c_mscale + bz * g.ms_bs : nullptr;
   float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
   const int lda = (int)g.lda, ldb = (int)g.ldb;
 
@@ -343,7 +357,7 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
       const bool ok = A_KC ? (m0 + row < g.M && k0 + c4 < kend) : (k0 + row < kend && m0 + c4 < g.M);
       ra[u] = buf_load4(ars, ok ? (uint32_t)(row * lda + c4) * 4u : kOobOffset);
       if constexpr (KSCALE) {
-        const auto srs = make_rsrc(g.a_kscale + k0, kFastRecords);
+        const auto srs = make_rsrc(kscale + k0, kFastRecords);
         if constexpr (A_KC) {
           const float4 sc = buf_load4(srs, k0 + c4 < kend ? (uint32_t)c4 * 4u : kOobOffset);
           rs[u][0] = sc.x; rs[u][NSC > 1 ? 1 : 0] = sc.y; rs[u][NSC > 2 ? 2 : 0] = sc.z; rs[u][NSC - 1] = sc.w;
@@ -458,6 +472,10 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
             const float4 sc = *reinterpret_cast<const float4*>(&g.c_nscale[n]);
             x.x *= sc.x; x.y *= sc.y; x.z *= sc.z; x.w *= sc.w;
           }
+          if (mscale) {
+            const float sm = mscale[m];
+            x.x *= sm; x.y *= sm; x.z *= sm; x.w *= sm;
+          }
           if (gadd) {
             const float4 a = *reinterpret_cast<const float4*>(&gadd[(int64_t)m * g.ld_add + n]);
             x.x += a.x; x.y += a.y; x.z += a.z; x.w += a.w;
@@ -479,6 +497,7 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
           if (m < g.M && n < g.N) {
             float x = acc[mt][nt][v];
             if (g.c_nscale) x *= g.c_nscale[n];
+            if (mscale) x *= mscale[m];
             if (gadd) x += gadd[(int64_t)m * g.ld_add + n];
             C[(int64_t)m * g.ldc + n] = x;
           }
@@ -542,7 +561,7 @@ static bool fast_path_ok(const GemmArgs& g, bool a_kc, bool b_kc) {
   if (g.b_split < (b_kc ? g.N : g.K) && g.b_split % 16 != 0) return false;
   if (g.K % 4 != 0 || g.k_chunk % 4 != 0) return false;
   if ((!a_kc && g.M % 4 != 0) || (!b_kc && g.N % 4 != 0)) return false;
-  if (g.lda % 4 != 0 || g.ldb % 4 != 0 || g.a_bs % 4 != 0 || g.b_bs % 4 != 0) return false;
+  if (g.lda % 4 != 0 || g.ldb % 4 != 0 || g.a_bs % 4 != 0 || g.b_bs % 4 != 0 || g.ks_bs % 4 != 0) return false;
   if (g.lda >= kMaxLd || g.ldb >= kMaxLd) return false;
   return f4_aligned(g.A) && f4_aligned(g.B0) && f4_aligned(g.B1) && f4_aligned(g.a_kscale);
 }
@@ -564,7 +583,9 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
   const int64_t tiles128 = (int64_t)((g.M + kFT - 1) / kFT) * ((g.N + kFT - 1) / kFT) * zdim;
   const int forced = g_gemm_tile.load(std::memory_order_relaxed);
   const bool big = forced ? forced == kFT : (g.M >= kFT && g.N >= kFT && tiles128 >= 256);
-  const bool fast = big && tiles128 < (1LL << 31) && fast_path_ok(g, info.a_kc, info.b_kc);
+  // (the 128 x 128 kernel applies the k scale of a scaled use unconditionally)
+  const bool fast = big && tiles128 < (1LL << 31) && fast_path_ok(g, info.a_kc, info.b_kc) &&
+                    (!info.a_kscale || g.a_kscale != nullptr);
   JN_PROFILE(info.name, stream);
   switch (use) {
     case kGemmProject: launch_use<kGemmProject>(g, fast, (int)zdim, stream); break;
@@ -576,6 +597,12 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
     case kGemmDenseValueGrad: launch_use<kGemmDenseValueGrad>(g, fast, (int)zdim, stream); break;
     case kGemmDenseTargetGrad: launch_use<kGemmDenseTargetGrad>(g, fast, (int)zdim, stream); break;
     case kGemmDenseSourceGrad: launch_use<kGemmDenseSourceGrad>(g, fast, (int)zdim, stream); break;
+    case kGemmRouteLogits: launch_use<kGemmRouteLogits>(g, fast, (int)zdim, stream); break;
+    case kGemmRouteAggregate: launch_use<kGemmRouteAggregate>(g, fast, (int)zdim, stream); break;
+    case kGemmRouteEdgeGrad: launch_use<kGemmRouteEdgeGrad>(g, fast, (int)zdim, stream); break;
+    case kGemmRouteValueGrad: launch_use<kGemmRouteValueGrad>(g, fast, (int)zdim, stream); break;
+    case kGemmRouteSourceGrad: launch_use<kGemmRouteSourceGrad>(g, fast, (int)zdim, stream); break;
+    case kGemmRouteTargetGrad: launch_use<kGemmRouteTargetGrad>(g, fast, (int)zdim, stream); break;
     default: JN_REQUIRE(false, kInvalidArgument, "unknown GEMM use %d", (int)use);
   }
   JN_LAUNCH_CHECK();
@@ -584,7 +611,7 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
 
 // Batched C_b = op(A_b) . op(B_b) for b < batch (see BatchedGemm).
 int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
-  JN_REQUIRE(use >= kGemmDenseScores && use <= kGemmDenseSourceGrad && m.a_kcontig == kGemmUses[use].a_kc &&
+  JN_REQUIRE(use >= kGemmDenseScores && use <= kGemmRouteTargetGrad && m.a_kcontig == kGemmUses[use].a_kc &&
                  m.b_kcontig == kGemmUses[use].b_kc,
              kInvalidArgument, "batched GEMM layout does not match its use");
   GemmArgs g{};
@@ -595,8 +622,9 @@ int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
   g.M = m.M; g.N = m.N; g.K = m.K;
   g.k_chunk = m.K; g.c_split_stride = 0;
   g.batch = m.batch;
-  g.a_kscale = m.a_kscale;
+  g.a_kscale = m.a_kscale; g.ks_bs = m.ks_bs;
   g.c_nscale = m.c_nscale;
+  g.c_mscale = m.c_mscale; g.ms_bs = m.ms_bs;
   return launch_gemm(g, use, 1, stream);
 }
 

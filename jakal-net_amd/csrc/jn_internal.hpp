@@ -38,14 +38,17 @@ struct BatchedGemm {
   const float* B; int64_t ldb, b_bs; bool b_kcontig;
   float* C; int64_t ldc, c_bs;
   const float* addend; int64_t ld_add, add_bs;
-  const float* a_kscale;
+  const float* a_kscale; int64_t ks_bs;  // optional, per batch element at stride ks_bs
   const float* c_nscale;
+  const float* c_mscale; int64_t ms_bs;  // optional: C(m, n) *= c_mscale[m], per batch element at stride ms_bs
   int M, N, K, batch;
 };
 enum GemmUse {
   kGemmProject, kGemmGradInput, kGemmGradWeight,
   kGemmDenseScores, kGemmDenseAggregate, kGemmDenseEdgeGrad, kGemmDenseValueGrad, kGemmDenseTargetGrad,
   kGemmDenseSourceGrad,
+  kGemmRouteLogits, kGemmRouteAggregate, kGemmRouteEdgeGrad, kGemmRouteValueGrad, kGemmRouteSourceGrad,
+  kGemmRouteTargetGrad,
 };
 int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream);
 // Workgroup tile of every later GEMM launch: 0 = chosen per call, 64 or 128 = forced.
@@ -150,6 +153,15 @@ int launch_dense_compress(float* S, const float* bias, const float* ps, int B, i
 int launch_dense_compress_backward(float* G, const float* E, const float* gds, const float* ps, int B, int N,
                                    int compress, float* rowsum, hipStream_t stream);
 int launch_dense_colsum(const float* E, const float* w, int B, int N, float* out, hipStream_t stream);
+
+// ---- dense transitions (jn_route_dense.hip) --------------------------------
+int launch_route_dense_compress(float* L, const float* bias, float inv_temp, int B, int Ns, int Nd, int kind,
+                                hipStream_t stream);
+int launch_route_dense_colsum(const float* R, const float* a, const float* c, int B, int Nr, int Nc, float* out,
+                              hipStream_t stream);
+int launch_route_dense_compress_backward(float* H, const float* R, const float* rho, const float* ps,
+                                         const float* gds, int B, int Ns, int Nd, int kind, float inv_temp,
+                                         float* grad_rho, float* grad_ps, float* rowsum, hipStream_t stream);
 int launch_scale_grad_partials(float* dps, int64_t ld_dps, const float* src, int64_t ld_src, const float* w_hat,
                                int r, int64_t rows, float* part, hipStream_t stream);
 

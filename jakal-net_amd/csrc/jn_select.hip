@@ -361,7 +361,7 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kep
 
 // VEC: r == 4*RQ and 16-byte aligned key rows -> float4 chunk loads.
 template <int RQ, bool VEC, int KEEP>
-__global__ __launch_bounds__(256, 2) void lowrank_topk_select_kernel(SelectArgs a) {
+__global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kernel(SelectArgs a) {
   constexpr int CAP = sel_lane_cap(KEEP);
   constexpr int RP = 4 * RQ;
   constexpr int KSTRIDE = RP + 4;  // padded key row (floats)

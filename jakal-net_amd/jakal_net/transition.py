@@ -12,7 +12,7 @@ Operator semantics follow the reference's ``src/jakal_net/transition.py``:
   (:449-451) and ``forward`` adds the delta to ``dst`` (:389-392).
 
 Backends as in ``jakal_net.propagation``: the native path (HIP library) covers
-``LowRankBilinearRoute`` (optionally temperature-wrapped) with softmax routes.
+``LowRankBilinearRoute`` (optionally temperature-wrapped) with softmax or signed |l| softmax routes.
 """
 
 from __future__ import annotations
@@ -206,10 +206,11 @@ class Transition(nn.Module):
         return "transition_pairwise_dense"
 
     def _hot_path(self) -> bool:
+        # the HIP dense route covers softmax and signed |l| softmax routes
         return (
             self._route_expects_pairwise_inputs
             and supports_pairwise_route_kernel(self.route_fn)
-            and self.route_compress_name == "softmax"
+            and self.route_compress_name in ("softmax", "signed_abs_softmax")
             and not self.use_direction_only
         )
 

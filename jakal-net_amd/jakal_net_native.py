@@ -86,6 +86,18 @@ _declare(
 )
 
 _declare(
+    "jn_transition_dense_forward",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P,
+     _P],
+)
+_declare("jn_transition_dense_workspace_bytes", [_I64] * 7, _SZ)
+_declare(
+    "jn_transition_dense_backward",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32,
+     _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+
+_declare(
     "jn_propagation_dense_forward",
     [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P],
 )
@@ -106,6 +118,7 @@ _SUPPORTED_OPS = (
     "propagation_window",
     "propagation_dense",
     "transition_pairwise_topk",
+    "transition_pairwise_dense",
     "low_rank_topk_select",
 )
 _ROUTE_COMPRESS_KINDS = {"softmax": 0, "signed_abs_softmax": 1}
@@ -714,12 +727,144 @@ def transition_pairwise_topk(
     optional trailing ``route_compress_name`` ("softmax" or
     "signed_abs_softmax") has no counterpart in the reference's composite op,
     which is softmax-only."""
+    if topk >= dst_val.shape[-2] > 64:
+        # every destination kept (transition.py:437-440): the dense transition
+        return transition_pairwise_dense(
+            route_kind, source_weight, source_bias, target_weight, target_bias, core_weight, bias, hidden_weight,
+            hidden_bias, out_weight, out_bias, route_compress_name, temperature, sender_strength, src_val, dst_val,
+            projected_state, projected_val, src_block_size, dst_block_size,
+        )
     ds, dv, _, _ = transition_pairwise_topk_routes(
         route_kind, source_weight, source_bias, target_weight, target_bias, core_weight, bias, hidden_weight,
         hidden_bias, out_weight, out_bias, temperature, sender_strength, src_val, dst_val, projected_state,
         projected_val, topk, src_block_size, dst_block_size, route_compress_name,
     )
     return ds, dv
+
+
+class _TransitionDense(torch.autograd.Function):
+    """Differentiable dense pairwise Transition on the HIP library.
+
+    Inputs (fp32, contiguous): sender strength rho [B,Ns], src_val [B,Ns,Dsrc],
+    dst_val [B,Nd,Ddst], projected_state [B,Ns], projected_val [B,Ns,Dv],
+    Ws [r,Dsrc], Wt [r,Ddst], w [r] (raw), bias [] or None."""
+
+    @staticmethod
+    def forward(ctx, rho, src, dst, ps, pv, Ws, Wt, w, bias, temperature: float, compress: int):  # noqa: N803
+        B, Ns, Dsrc = src.shape
+        Nd, Ddst = dst.shape[1], dst.shape[2]
+        Dv = pv.shape[-1]
+        r = Ws.shape[0]
+        dev = src.device
+        with torch.cuda.device(dev):
+            ds = torch.empty(B, Nd, device=dev, dtype=torch.float32)
+            dv = torch.empty(B, Nd, Dv, device=dev, dtype=torch.float32)
+            sp = torch.empty(B * Ns, r, device=dev, dtype=torch.float32)
+            dp = torch.empty(B * Nd, r, device=dev, dtype=torch.float32)
+            routes = torch.empty(B, Ns, Nd, device=dev, dtype=torch.float32)
+            _check(
+                _LIB.jn_transition_dense_forward(
+                    _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w), _ptr(bias),
+                    float(temperature), B, Ns, Nd, Dsrc, Ddst, Dv, r, compress,
+                    _ptr(ds), _ptr(dv), _ptr(sp), _ptr(dp), _ptr(routes), _stream(dev),
+                )
+            )
+        ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, routes)
+        ctx.meta = (float(temperature), compress, bias is not None)
+        return ds, dv
+
+    @staticmethod
+    def backward(ctx, g_ds, g_dv):
+        rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, routes = ctx.saved_tensors
+        temperature, compress, has_bias = ctx.meta
+        B, Ns, Dsrc = src.shape
+        Nd, Ddst = dst.shape[1], dst.shape[2]
+        Dv = pv.shape[-1]
+        r = Ws.shape[0]
+        dev = src.device
+        need = ctx.needs_input_grad
+        with torch.cuda.device(dev):
+            g_ds = torch.zeros(B, Nd, device=dev) if g_ds is None else g_ds.float().contiguous()
+            g_dv = torch.zeros(B, Nd, Dv, device=dev) if g_dv is None else g_dv.float().contiguous()
+            out = [torch.empty_like(t) if n else None for t, n in zip((rho, src, dst, ps, pv), need[:5])]
+            gWs = torch.empty_like(Ws) if need[5] else None
+            gWt = torch.empty_like(Wt) if need[6] else None
+            gw = torch.empty_like(w)
+            gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
+            ws_bytes = int(_LIB.jn_transition_dense_workspace_bytes(B, Ns, Nd, Dsrc, Ddst, Dv, r))
+            ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            _check(
+                _LIB.jn_transition_dense_backward(
+                    _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w),
+                    _ptr(sp), _ptr(dp), _ptr(routes), _ptr(g_ds), _ptr(g_dv), float(temperature),
+                    B, Ns, Nd, Dsrc, Ddst, Dv, r, compress,
+                    _ptr(out[0]), _ptr(out[1]), _ptr(out[2]), _ptr(out[3]), _ptr(out[4]), _ptr(gWs), _ptr(gWt),
+                    _ptr(gw), _ptr(gb), _ptr(ws), ws_bytes, _stream(dev),
+                )
+            )
+        return (*out, gWs, gWt, gw if need[7] else None, gb if (has_bias and need[8]) else None, None, None)
+
+
+def _check_route_spec(route_kind, source_weight, source_bias, target_weight, target_bias, hidden_weight, out_weight,
+                      route_compress_name, temperature):
+    if route_kind != "low_rank_bilinear_route":
+        raise TypeError(f"jakal_net_native supports route kind 'low_rank_bilinear_route', got {route_kind!r}.")
+    if source_weight is None or target_weight is None:
+        raise RuntimeError("Low-rank bilinear route is missing projection weights.")
+    if source_bias is not None or target_bias is not None or hidden_weight is not None or out_weight is not None:
+        raise TypeError("low_rank_bilinear_route carries no projection biases or hidden layers.")
+    if route_compress_name not in _ROUTE_COMPRESS_KINDS:
+        raise TypeError(f"Unsupported route_compress_name for the HIP backend: {route_compress_name!r}.")
+    if not temperature > 0:
+        raise RuntimeError("temperature must be positive.")
+
+
+def transition_pairwise_dense(
+    route_kind: str,
+    source_weight: Tensor | None,
+    source_bias: Tensor | None,
+    target_weight: Tensor | None,
+    target_bias: Tensor | None,
+    core_weight: Tensor,
+    bias: Tensor | None,
+    hidden_weight: Tensor | None,
+    hidden_bias: Tensor | None,
+    out_weight: Tensor | None,
+    out_bias: Tensor | None,
+    route_compress_name: str,
+    temperature: float,
+    sender_strength: Tensor,
+    src_val: Tensor,
+    dst_val: Tensor,
+    projected_state: Tensor,
+    projected_val: Tensor,
+    src_block_size: int,
+    dst_block_size: int,
+) -> tuple[Tensor, Tensor]:
+    """Dense pairwise transition; signature of jakal_net_native.cpp:6705-6725.
+
+    Every source routes to every destination with routes
+    compress(((P_s * w) . P_t + b) / T) over destinations ("softmax" or
+    "signed_abs_softmax").  The block sizes are validated and otherwise
+    ignored: the HIP kernels tile for gfx950 themselves."""
+    _check_route_spec(route_kind, source_weight, source_bias, target_weight, target_bias, hidden_weight, out_weight,
+                      route_compress_name, temperature)
+    if src_block_size < 0 or dst_block_size < 0:
+        raise RuntimeError("block sizes must be non-negative.")
+    _require_gpu(sender_strength, src_val, dst_val, projected_state, projected_val, source_weight, target_weight,
+                 core_weight, bias)
+    batch_shape = tuple(src_val.shape[:-2])
+    Ns, Dsrc = src_val.shape[-2], src_val.shape[-1]
+    Nd, Ddst = dst_val.shape[-2], dst_val.shape[-1]
+    Dv = projected_val.shape[-1]
+    ds, dv = _TransitionDense.apply(
+        _f32(sender_strength.reshape(-1, Ns)), _f32(src_val.reshape(-1, Ns, Dsrc)),
+        _f32(dst_val.reshape(-1, Nd, Ddst)), _f32(projected_state.reshape(-1, Ns)),
+        _f32(projected_val.reshape(-1, Ns, Dv)), _f32(source_weight), _f32(target_weight), _f32(core_weight),
+        _f32(bias), float(temperature), _ROUTE_COMPRESS_KINDS[route_compress_name],
+    )
+    return ds.reshape(*batch_shape, Nd).to(projected_state.dtype), dv.reshape(*batch_shape, Nd, Dv).to(
+        projected_val.dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -30,7 +30,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change). */
+/* ABI revision of this header (bumped on any signature change); this is 2. */
 int jn_abi_version(void);
 
 /*
@@ -159,13 +159,17 @@ int jn_propagation_window_backward(const float* layer_val, const float* projecte
  * MFMA GEMMs over the materialised edge matrix.
  * Replaces propagation_dense (native/jakal_net_native.cpp:5962-6076) for
  * source_state = None (the caller folds state weighting into ps and pv,
- * propagation.py:162-170).
+ * propagation.py:162-170).  causal != 0 keeps only sources j <= i in row i
+ * (softmax of the signed variant over those): the full causal window that
+ * propagation_window computes for window >= N - 1 (kernel_common.py:443-456;
+ * the causal dense query propagation of scripts/progressive_b_example.py:
+ * 1990-2003), on the same MFMA path.
  */
 int jn_propagation_dense_forward(const float* layer_val, const float* projected_state, const float* projected_val,
                                  const float* target_weight, const float* source_weight, const float* core_weight,
                                  const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
-                                 int64_t rank, int32_t compress_kind, float* delta_state, float* delta_val,
-                                 float* projections, float* edges, jn_stream_t stream);
+                                 int64_t rank, int32_t compress_kind, int32_t causal, float* delta_state,
+                                 float* delta_val, float* projections, float* edges, jn_stream_t stream);
 
 /* Workspace needed by jn_propagation_dense_backward (holds one [B,N,N] matrix). */
 size_t jn_propagation_dense_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
@@ -181,7 +185,7 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
                                   const float* target_weight, const float* source_weight, const float* core_weight,
                                   const float* projections, const float* edges, const float* grad_delta_state,
                                   const float* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim,
-                                  int64_t out_dim, int64_t rank, int32_t compress_kind,
+                                  int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
                                   int32_t projected_val_is_layer_val, float* grad_layer_val,
                                   float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
                                   float* grad_source_weight, float* grad_core_weight, float* grad_bias,

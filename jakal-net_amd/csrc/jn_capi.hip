@@ -395,7 +395,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 1; }
+int jn_abi_version(void) { return 2; }
 
 int jn_profile_enable(int32_t on) {
   std::lock_guard<std::mutex> lock(jakal::g_prof_mu);
@@ -874,8 +874,8 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
 int jn_propagation_dense_forward(const float* layer_val, const float* projected_state, const float* projected_val,
                                  const float* target_weight, const float* source_weight, const float* core_weight,
                                  const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
-                                 int64_t rank, int32_t compress_kind, float* delta_state, float* delta_val,
-                                 float* projections, float* edges, jn_stream_t stream) {
+                                 int64_t rank, int32_t compress_kind, int32_t causal, float* delta_state,
+                                 float* delta_val, float* projections, float* edges, jn_stream_t stream) {
   int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
   if (rc) return rc;
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
@@ -896,7 +896,7 @@ int jn_propagation_dense_forward(const float* layer_val, const float* projected_
   rc = gemm_batched(sg, kGemmDenseScores, st);
   if (rc) return rc;
   // E = compress(S + b) in place, delta_state = E ps
-  rc = launch_dense_compress(edges, bias, projected_state, B, N, compress_kind, delta_state, st);
+  rc = launch_dense_compress(edges, bias, projected_state, B, N, compress_kind, causal != 0, delta_state, st);
   if (rc) return rc;
   // delta_val_b = E_b pv_b
   BatchedGemm ag{};
@@ -918,7 +918,7 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
                                   const float* target_weight, const float* source_weight, const float* core_weight,
                                   const float* projections, const float* edges, const float* grad_delta_state,
                                   const float* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim,
-                                  int64_t out_dim, int64_t rank, int32_t compress_kind,
+                                  int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
                                   int32_t projected_val_is_layer_val, float* grad_layer_val,
                                   float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
                                   float* grad_source_weight, float* grad_core_weight, float* grad_bias,
@@ -945,7 +945,8 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
   gg.M = N; gg.N = N; gg.K = D; gg.batch = B;
   rc = gemm_batched(gg, kGemmDenseEdgeGrad, st);
   if (rc) return rc;
-  rc = launch_dense_compress_backward(s.G, edges, grad_delta_state, projected_state, B, N, compress_kind, s.rowsum,
+  rc = launch_dense_compress_backward(s.G, edges, grad_delta_state, projected_state, B, N, compress_kind,
+                                      causal != 0, s.rowsum,
                                       st);
   if (rc) return rc;
 

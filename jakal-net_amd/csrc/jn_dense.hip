@@ -10,7 +10,8 @@
 // materialised (in HBM, fp32): the two N x N contractions run as batched MFMA
 // GEMMs (jn_gemm.hip) and the kernels here are the row-wise passes between
 // them (one wavefront per row, float4 lanes over the row):
-//   dense_compress_kernel          : E = compress(S + b) in place, delta_state
+//   dense_compress_kernel          : E = compress(S + b) in place (optionally causal:
+//                                    row i keeps sources j <= i), delta_state
 //   dense_compress_backward_kernel : G_s = compress'(E, G + gds (x) ps) in place,
 //                                    and its row sums (bias gradient)
 //   dense_colsum_kernel            : grad ps[j] = sum_i E[i, j] gds[i] (fixed order)
@@ -20,13 +21,17 @@
 namespace jakal {
 
 // Row r of a [rows, N] matrix: lane l covers floats 4l + 256t (VEC) or l + 64t.
+// causal: row i keeps sources j <= i only (the rest are written as 0 and not
+// read; a full causal window, kernel_common.py:443-456 with window >= N - 1).
 template <bool VEC>
 __global__ __launch_bounds__(256) void dense_compress_kernel(float* S, const float* bias, const float* ps, int N,
-                                                             int64_t rows, int compress, float* delta_state) {
+                                                             int64_t rows, int compress, int causal,
+                                                             float* delta_state) {
   const int lane = lane_id();
   const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
   if (row >= rows) return;
   const int64_t b = row / N;
+  const int lim = causal ? (int)(row - b * N) + 1 : N;  // sources [0, lim)
   float* s = S + row * N;
   const float* psb = ps + b * N;
   const float bb = bias ? bias[0] : 0.0f;
@@ -34,36 +39,40 @@ __global__ __launch_bounds__(256) void dense_compress_kernel(float* S, const flo
   if (compress == 0) {
     if constexpr (VEC) {
       for (int j = 4 * lane; j < N; j += 256) {
-        float4 v = *reinterpret_cast<float4*>(s + j);
-        const float4 p = *reinterpret_cast<const float4*>(psb + j);
-        v.x = softsign_f(v.x + bb);
-        v.y = softsign_f(v.y + bb);
-        v.z = softsign_f(v.z + bb);
-        v.w = softsign_f(v.w + bb);
-        acc += v.x * p.x + v.y * p.y + v.z * p.z + v.w * p.w;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j < lim) {
+          const float4 x = *reinterpret_cast<float4*>(s + j);
+          const float4 p = *reinterpret_cast<const float4*>(psb + j);
+          v.x = softsign_f(x.x + bb);
+          v.y = j + 1 < lim ? softsign_f(x.y + bb) : 0.f;
+          v.z = j + 2 < lim ? softsign_f(x.z + bb) : 0.f;
+          v.w = j + 3 < lim ? softsign_f(x.w + bb) : 0.f;
+          acc += v.x * p.x + v.y * p.y + v.z * p.z + v.w * p.w;
+        }
         *reinterpret_cast<float4*>(s + j) = v;
       }
     } else {
       for (int j = lane; j < N; j += kWave) {
-        const float e = softsign_f(s[j] + bb);
-        acc += e * psb[j];
+        const float e = j < lim ? softsign_f(s[j] + bb) : 0.f;
+        if (j < lim) acc += e * psb[j];
         s[j] = e;
       }
     }
   } else {
-    // sign(s) * softmax(|s|) over the row: max, sum of exponentials, then write
+    // sign(s) * softmax(|s|) over the row's sources: max, sum of exponentials, then write
     float m = -INFINITY;
-    for (int j = lane; j < N; j += kWave) m = fmaxf(m, fabsf(s[j] + bb));
-    m = __int_as_float(wave_reduce_i(__float_as_int(m), [](int x, int y) {
-      return __float_as_int(fmaxf(__int_as_float(x), __int_as_float(y)));
-    }));
+    for (int j = lane; j < lim; j += kWave) m = fmaxf(m, fabsf(s[j] + bb));
+    m = wave_max_f(m);
     float sum = 0.0f;
-    for (int j = lane; j < N; j += kWave) sum += __expf(fabsf(s[j] + bb) - m);
+    for (int j = lane; j < lim; j += kWave) sum += __expf(fabsf(s[j] + bb) - m);
     const float inv = 1.0f / wave_sum(sum);
     for (int j = lane; j < N; j += kWave) {
-      const float x = s[j] + bb;
-      const float e = sign_f(x) * __expf(fabsf(x) - m) * inv;
-      acc += e * psb[j];
+      float e = 0.f;
+      if (j < lim) {
+        const float x = s[j] + bb;
+        e = sign_f(x) * __expf(fabsf(x) - m) * inv;
+        acc += e * psb[j];
+      }
       s[j] = e;
     }
   }
@@ -73,48 +82,56 @@ __global__ __launch_bounds__(256) void dense_compress_kernel(float* S, const flo
 
 // G holds gdv . pv^T on entry; on exit the score gradient
 //   g_e = G + gds[i] ps[j]; softsign: g_s = g_e (1 - |e|)^2 (= g_e / (1 + |s|)^2);
-//   signed |s| softmax: g_s = |e| g_e - e sum_j(g_e e).
+//   signed |s| softmax: g_s = |e| g_e - e sum_j(g_e e);
+// and 0 for the sources a causal row does not keep (not read).
 template <bool VEC>
 __global__ __launch_bounds__(256) void dense_compress_backward_kernel(float* G, const float* E, const float* gds,
                                                                       const float* ps, int N, int64_t rows,
-                                                                      int compress, float* rowsum) {
+                                                                      int compress, int causal, float* rowsum) {
   const int lane = lane_id();
   const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
   if (row >= rows) return;
   const int64_t b = row / N;
+  const int lim = causal ? (int)(row - b * N) + 1 : N;
   float* g = G + row * N;
   const float* e = E + row * N;
   const float* psb = ps + b * N;
   const float gs = gds[row];
   float row_dot = 0.0f;
   if (compress == 1) {
-    for (int j = lane; j < N; j += kWave) row_dot += (g[j] + gs * psb[j]) * e[j];
+    for (int j = lane; j < lim; j += kWave) row_dot += (g[j] + gs * psb[j]) * e[j];
     row_dot = wave_sum(row_dot);
   }
   float acc = 0.0f;
   if (VEC && compress == 0) {
     for (int j = 4 * lane; j < N; j += 256) {
-      float4 gv = *reinterpret_cast<float4*>(g + j);
-      const float4 ev = *reinterpret_cast<const float4*>(e + j);
-      const float4 pv = *reinterpret_cast<const float4*>(psb + j);
-      const float d0 = 1.0f - fabsf(ev.x), d1 = 1.0f - fabsf(ev.y), d2 = 1.0f - fabsf(ev.z), d3 = 1.0f - fabsf(ev.w);
-      gv.x = (gv.x + gs * pv.x) * d0 * d0;
-      gv.y = (gv.y + gs * pv.y) * d1 * d1;
-      gv.z = (gv.z + gs * pv.z) * d2 * d2;
-      gv.w = (gv.w + gs * pv.w) * d3 * d3;
-      acc += gv.x + gv.y + gv.z + gv.w;
+      float4 gv = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (j < lim) {
+        gv = *reinterpret_cast<float4*>(g + j);
+        const float4 ev = *reinterpret_cast<const float4*>(e + j);
+        const float4 pv = *reinterpret_cast<const float4*>(psb + j);
+        const float d0 = 1.0f - fabsf(ev.x), d1 = 1.0f - fabsf(ev.y), d2 = 1.0f - fabsf(ev.z),
+                    d3 = 1.0f - fabsf(ev.w);
+        gv.x = (gv.x + gs * pv.x) * d0 * d0;
+        gv.y = j + 1 < lim ? (gv.y + gs * pv.y) * d1 * d1 : 0.f;
+        gv.z = j + 2 < lim ? (gv.z + gs * pv.z) * d2 * d2 : 0.f;
+        gv.w = j + 3 < lim ? (gv.w + gs * pv.w) * d3 * d3 : 0.f;
+        acc += gv.x + gv.y + gv.z + gv.w;
+      }
       *reinterpret_cast<float4*>(g + j) = gv;
     }
   } else {
     for (int j = lane; j < N; j += kWave) {
-      const float ge = g[j] + gs * psb[j];
-      const float ej = e[j];
-      float gsj;
-      if (compress == 0) {
-        const float d = 1.0f - fabsf(ej);
-        gsj = ge * d * d;
-      } else {
-        gsj = fabsf(ej) * ge - ej * row_dot;
+      float gsj = 0.f;
+      if (j < lim) {
+        const float ge = g[j] + gs * psb[j];
+        const float ej = e[j];
+        if (compress == 0) {
+          const float d = 1.0f - fabsf(ej);
+          gsj = ge * d * d;
+        } else {
+          gsj = fabsf(ej) * ge - ej * row_dot;
+        }
       }
       acc += gsj;
       g[j] = gsj;
@@ -158,7 +175,7 @@ __global__ __launch_bounds__(256) void scale_grad_partials_kernel(float* dps, in
   dps[m * ld_dps + c] = g * w_hat[c];
 }
 
-int launch_dense_compress(float* S, const float* bias, const float* ps, int B, int N, int compress,
+int launch_dense_compress(float* S, const float* bias, const float* ps, int B, int N, int compress, int causal,
                           float* delta_state, hipStream_t stream) {
   const int64_t rows = (int64_t)B * N;
   const int64_t blocks = (rows + 3) / 4;
@@ -167,15 +184,15 @@ int launch_dense_compress(float* S, const float* bias, const float* ps, int B, i
                    ((reinterpret_cast<uintptr_t>(ps) & 15) == 0);
   JN_PROFILE("dense_compress_kernel", stream);
   if (vec) hipLaunchKernelGGL(dense_compress_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, S, bias, ps,
-                              N, rows, compress, delta_state);
+                              N, rows, compress, causal, delta_state);
   else hipLaunchKernelGGL(dense_compress_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, S, bias, ps,
-                          N, rows, compress, delta_state);
+                          N, rows, compress, causal, delta_state);
   JN_LAUNCH_CHECK();
   return kOk;
 }
 
 int launch_dense_compress_backward(float* G, const float* E, const float* gds, const float* ps, int B, int N,
-                                   int compress, float* rowsum, hipStream_t stream) {
+                                   int compress, int causal, float* rowsum, hipStream_t stream) {
   const int64_t rows = (int64_t)B * N;
   const int64_t blocks = (rows + 3) / 4;
   JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "too many rows");
@@ -183,9 +200,9 @@ int launch_dense_compress_backward(float* G, const float* E, const float* gds, c
                    ((reinterpret_cast<uintptr_t>(E) & 15) == 0) && ((reinterpret_cast<uintptr_t>(ps) & 15) == 0);
   JN_PROFILE("dense_compress_backward_kernel", stream);
   if (vec) hipLaunchKernelGGL(dense_compress_backward_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, G,
-                              E, gds, ps, N, rows, compress, rowsum);
+                              E, gds, ps, N, rows, compress, causal, rowsum);
   else hipLaunchKernelGGL(dense_compress_backward_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, G, E,
-                          gds, ps, N, rows, compress, rowsum);
+                          gds, ps, N, rows, compress, causal, rowsum);
   JN_LAUNCH_CHECK();
   return kOk;
 }

@@ -148,10 +148,10 @@ struct RouteRowsBwdArgs {
 int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream);
 
 // ---- dense propagation (jn_dense.hip) --------------------------------------
-int launch_dense_compress(float* S, const float* bias, const float* ps, int B, int N, int compress,
+int launch_dense_compress(float* S, const float* bias, const float* ps, int B, int N, int compress, int causal,
                           float* delta_state, hipStream_t stream);
 int launch_dense_compress_backward(float* G, const float* E, const float* gds, const float* ps, int B, int N,
-                                   int compress, float* rowsum, hipStream_t stream);
+                                   int compress, int causal, float* rowsum, hipStream_t stream);
 int launch_dense_colsum(const float* E, const float* w, int B, int N, float* out, hipStream_t stream);
 
 // ---- dense transitions (jn_route_dense.hip) --------------------------------

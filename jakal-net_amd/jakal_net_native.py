@@ -99,12 +99,12 @@ _declare(
 
 _declare(
     "jn_propagation_dense_forward",
-    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P],
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P, _P],
 )
 _declare("jn_propagation_dense_workspace_bytes", [_I64] * 5, _SZ)
 _declare(
     "jn_propagation_dense_backward",
-    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32,
      _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 
@@ -112,6 +112,7 @@ ABI_VERSION = int(_LIB.jn_abi_version())
 
 _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1}
 MAX_TOPK = 64
+CAUSAL_DENSE_MIN_NODES = 128  # full causal windows from this many nodes run on the dense MFMA path
 
 _SUPPORTED_OPS = (
     "propagation_topk",
@@ -303,10 +304,11 @@ class _PropagationEdges(torch.autograd.Function):
 
 class _PropagationDense(torch.autograd.Function):
     """Differentiable dense low-rank propagation on the HIP library (edge
-    matrix materialised).  Inputs as _PropagationEdges."""
+    matrix materialised).  Inputs as _PropagationEdges; causal keeps only
+    sources j <= i in row i."""
 
     @staticmethod
-    def forward(ctx, X, ps, pv, V, U, w_hat, bias, compress: int):  # noqa: N803
+    def forward(ctx, X, ps, pv, V, U, w_hat, bias, compress: int, causal: bool = False):  # noqa: N803
         B, N, Din = X.shape
         pv_is_x = pv is None
         pv_t = X if pv_is_x else pv
@@ -321,17 +323,18 @@ class _PropagationDense(torch.autograd.Function):
             _check(
                 _LIB.jn_propagation_dense_forward(
                     _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
-                    B, N, Din, Dout, r, compress, _ptr(ds), _ptr(dv), _ptr(proj), _ptr(edges), _stream(dev),
+                    B, N, Din, Dout, r, compress, 1 if causal else 0, _ptr(ds), _ptr(dv), _ptr(proj), _ptr(edges),
+                    _stream(dev),
                 )
             )
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, edges)
-        ctx.meta = (compress, pv_is_x, bias is not None)
+        ctx.meta = (compress, pv_is_x, bias is not None, bool(causal))
         return ds, dv
 
     @staticmethod
     def backward(ctx, g_ds, g_dv):
         X, ps, pv, V, U, w_hat, proj, edges = ctx.saved_tensors
-        compress, pv_is_x, has_bias = ctx.meta
+        compress, pv_is_x, has_bias, causal = ctx.meta
         B, N, Din = X.shape
         Dout = pv.shape[-1]
         r = U.shape[0]
@@ -350,13 +353,13 @@ class _PropagationDense(torch.autograd.Function):
             _check(
                 _LIB.jn_propagation_dense_backward(
                     _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(proj), _ptr(edges),
-                    _ptr(g_ds), _ptr(g_dv), B, N, Din, Dout, r, compress, 1 if pv_is_x else 0,
+                    _ptr(g_ds), _ptr(g_dv), B, N, Din, Dout, r, compress, 1 if causal else 0, 1 if pv_is_x else 0,
                     _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
                     _ptr(ws), ws_bytes, _stream(dev),
                 )
             )
         return (gX, gps, gpv, gV if need[3] else None, gU if need[4] else None, gw if need[5] else None,
-                gb if (has_bias and need[6]) else None, None)
+                gb if (has_bias and need[6]) else None, None, None)
 
 
 def propagation_dense(
@@ -374,8 +377,12 @@ def propagation_dense(
     source_state: Tensor | None,
     target_block_size: int,
     source_block_size: int,
+    _causal: bool = False,
 ) -> tuple[Tensor, Tensor]:
     """Dense propagation over all N x N pairs; signature of jakal_net_native.cpp:5962-5976.
+
+    The trailing ``_causal`` (no counterpart in the reference signature) keeps
+    only sources j <= i in row i: propagation_window's full causal window.
 
     With ``source_state`` the edges are weighted by it per source, which
     equals the unweighted op on (source_state, source_state * projected_val)
@@ -397,7 +404,7 @@ def propagation_dense(
     ps = _f32(projected_state.reshape(-1, N))
     pv = None if pv_is_x else _f32(projected_val.reshape(-1, N, Dout))
     ds, dv = _PropagationDense.apply(X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias),
-                                     _COMPRESS_KINDS[edge_compress_name])
+                                     _COMPRESS_KINDS[edge_compress_name], _causal)
     return (ds.reshape(*batch_shape, N).to(projected_state.dtype),
             dv.reshape(*batch_shape, N, Dout).to(projected_val.dtype))
 
@@ -518,7 +525,19 @@ def propagation_window(
     target_block_size: int,
     source_block_size: int,
 ) -> tuple[Tensor, Tensor]:
-    """Causal-window propagation; signature of jakal_net_native.cpp:6190-6204."""
+    """Causal-window propagation; signature of jakal_net_native.cpp:6190-6204.
+
+    A window covering every earlier source (window >= N - 1, the causal dense
+    query propagation of progressive_b_example.py:1990-2003) on at least
+    CAUSAL_DENSE_MIN_NODES nodes runs as causal dense propagation on MFMA
+    GEMMs instead of an N-wide edge list."""
+    N = layer_val.shape[-2]
+    if window >= N - 1 and N >= CAUSAL_DENSE_MIN_NODES:
+        if window < 0:
+            raise RuntimeError("window must be non-negative.")
+        return propagation_dense(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
+                                 edge_compress_name, layer_val, projected_state, projected_val, None,
+                                 target_block_size, source_block_size, _causal=True)
     ds, dv, _, _ = propagation_window_edges(
         pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias, edge_compress_name, layer_val,
         projected_state, projected_val, window, target_block_size, source_block_size,

@@ -133,3 +133,44 @@ def test_sparse_propagation_window_api_native_matches_reference(dev):
     a, b = ref(layer), nat(layer)
     assert torch.allclose(a.delta_state, b.delta_state, atol=1e-5, rtol=1e-5)
     assert torch.allclose(a.delta_val, b.delta_val, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax"])
+@pytest.mark.parametrize("separate_pv,window_extra", [(False, 0), (True, 7)])
+def test_full_causal_window_runs_dense(dev, compress, separate_pv, window_extra):
+    """window >= N - 1 on N >= 128 nodes: every earlier source, computed as
+    causal dense propagation (MFMA GEMMs); forward and every gradient against
+    the oracle's window mode."""
+    import jakal_net_native as jn
+
+    B, N, D, r = 2, 200, 48, 12
+    window = N - 1 + window_extra
+    assert N >= jn.CAUSAL_DENSE_MIN_NODES
+    g, state, val, U, V, w, b = _inputs(2101, B, N, D, r)
+    pv_cpu = torch.randn(B, N, D, generator=g) if separate_pv else val
+    w_hat = w / w.norm()
+    X = val.to(dev).requires_grad_(True)
+    ps = state.to(dev).requires_grad_(True)
+    pv = pv_cpu.to(dev).requires_grad_(True) if separate_pv else X
+    Ud, Vd = U.to(dev).requires_grad_(True), V.to(dev).requires_grad_(True)
+    wd, bd = w_hat.to(dev).requires_grad_(True), b.to(dev).requires_grad_(True)
+    ds, dv = jn.propagation_window("low_rank_bilinear", wd, bd, Vd, None, Ud, None, compress, X, ps, pv, window, N, N)
+    gds = torch.randn(B, N, generator=g)
+    gdv = torch.randn(B, N, D, generator=g)
+    torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
+    ref = O.propagation_forward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), float(b), mode="window",
+                                window=window, kind=compress)
+    _close(_np(ds), ref["delta_state"], atol=ATOL * max(1.0, float(np.abs(ref["delta_state"]).max())),
+           what="delta_state")
+    _close(_np(dv), ref["delta_val"], atol=ATOL * max(1.0, float(np.abs(ref["delta_val"]).max())), what="delta_val")
+    gr = O.propagation_backward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), float(b), _np(gds),
+                                _np(gdv), mode="window", window=window, kind=compress)
+    g_val = gr["val"] + (0.0 if separate_pv else gr["pv"])
+    for got, want, what in ((X.grad, g_val, "grad layer_val"), (ps.grad, gr["ps"], "grad projected_state")) + (
+            ((pv.grad, gr["pv"], "grad projected_val"),) if separate_pv else ()):
+        _close(_np(got), want, atol=ATOL * max(1.0, float(np.abs(want).max())), what=what)
+    gs = gr["g_scores"][ref["mask"]]
+    scale = max(1.0, float(np.abs(gs).sum() / math.sqrt(gs.size)))
+    for got, want, what in ((Ud.grad, gr["U"], "grad target_proj"), (Vd.grad, gr["V"], "grad source_proj"),
+                            (wd.grad, gr["w_hat"], "grad w_hat"), (bd.grad, gr["b"], "grad bias")):
+        _close(_np(got), want, atol=ATOL * max(scale, float(np.abs(want).max())), what=what)

@@ -76,7 +76,9 @@ int jn_lowrank_topk_select(const float* query, int64_t ldq, int64_t query_batch_
  *   (already normalised, kernel_common.py:185-192), bias scalar or NULL.
  * Outputs delta_state [B,N], delta_val [B,N,Dout] and, for the backward,
  * projections [B*N,2r], topk_index [B,N,k] (int32), topk_score [B,N,k].
- * compress_kind: 0 softsign, 1 signed_abs_softmax.
+ * compress_kind: 0 softsign, 1 signed_abs_softmax (sign(s) * softmax(|s|) over the
+ * row's k edges), 2 signed_entmax15 (sign(s) * entmax15(|s|) over them,
+ * native/jakal_net_native.cpp:1133-1205); 1 and 2 need k <= 64.
  * Replaces propagation_topk (native/jakal_net_native.cpp:6305-6447) and
  * low_rank_propagation_topk_forward_cuda (native/jakal_net_native.cpp:191-213).
  */
@@ -119,7 +121,7 @@ int jn_propagation_topk_backward(const float* layer_val, const float* projected_
  * slot e, index -1 (absent) where j < 0.  Arguments as
  * jn_propagation_topk_forward; edge_index [B,N,width] (int32) and
  * edge_score [B,N,width] receive the edge list for the backward.
- * signed_abs_softmax (compress_kind 1) needs width <= 64.
+ * signed_abs_softmax and signed_entmax15 (compress_kind 1, 2) need width <= 64.
  * Replaces propagation_window (native/jakal_net_native.cpp:6190-6303) and
  * low_rank_propagation_window_forward_cuda (native/jakal_net_native.cpp:268-288).
  */
@@ -152,7 +154,8 @@ int jn_propagation_window_backward(const float* layer_val, const float* projecte
 /*
  * Propagation (dense, every target row aggregates every source) with
  * LowRankBilinearPairwise:  s = P_t diag(w_hat) P_s^T + b,  e = softsign(s)
- * (compress_kind 0) or sign(s) * softmax(|s|) over the row (1),
+ * (compress_kind 0), sign(s) * softmax(|s|) over the row (1) or
+ * sign(s) * entmax15(|s|) over the row (2),
  * delta_state = e . ps, delta_val = e . pv.  Arguments as
  * jn_propagation_topk_forward; `edges` [B,N,N] (fp32, caller-allocated)
  * receives e for the backward.  The two N x N contractions run as batched
@@ -196,8 +199,8 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
  *   l[j,d]  = ((P_s[j] * w) . P_t[d] + b) / temperature,  P_s = src_val Ws^T,
  *             P_t = dst_val Wt^T, w the raw core weight (modules.py:435-441)
  *   each source row j keeps its k = min(topk, dst_nodes) best destinations
- *   (transition.py:437-444); p = softmax over them (compress_kind 0) or
- *   sign(l) * softmax(|l|) (compress_kind 1)
+ *   (transition.py:437-444); p = softmax over them (compress_kind 0),
+ *   sign(l) * softmax(|l|) (compress_kind 1) or sign(l) * entmax15(|l|) (2)
  *   delta_state[d] = sum_j p[j,d] rho[j] projected_state[j]
  *   delta_val[d]   = sum_j p[j,d] rho[j] projected_val[j]
  * Shapes: sender_strength rho [B,Ns], src_val [B,Ns,Dsrc], dst_val [B,Nd,Ddst],
@@ -246,7 +249,7 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
  *   l[b,j,k] = ((P_s[j] * w) . P_t[k] + bias) / temperature,
  *   P_s = src_val . Ws^T [B*Ns, r], P_t = dst_val . Wt^T [B*Nd, r];
  *   R[b,j,:] = compress(l[b,j,:]) over destinations: compress_kind 0 softmax,
- *   1 sign(l) * softmax(|l|);
+ *   1 sign(l) * softmax(|l|), 2 sign(l) * entmax15(|l|);
  *   delta_state[b,k] = sum_j R[b,j,k] rho_j ps_j, delta_val[b,k] = sum_j R[b,j,k] rho_j pv_j.
  * Writes src_proj [B*Ns, r], dst_proj [B*Nd, r] and routes [B,Ns,Nd] (all
  * caller-allocated) for the backward.  Allocates nothing.

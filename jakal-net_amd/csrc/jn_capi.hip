@@ -78,10 +78,11 @@ int check_edge_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_
              "batch, nodes and dims must be positive (B=%lld N=%lld Din=%lld Dout=%lld)", (long long)batch,
              (long long)nodes, (long long)in_dim, (long long)out_dim);
   JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
-  JN_REQUIRE(compress_kind == 0 || compress_kind == 1, kUnsupported,
-             "compress_kind must be 0 (softsign) or 1 (signed_abs_softmax), got %d", compress_kind);
+  JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported,
+             "compress_kind must be 0 (softsign), 1 (signed_abs_softmax) or 2 (signed_entmax15), got %d",
+             compress_kind);
   JN_REQUIRE(compress_kind == 0 || edges <= 64, kUnsupported,
-             "signed_abs_softmax supports at most 64 edges per row (got %lld)", (long long)edges);
+             "signed_abs_softmax and signed_entmax15 support at most 64 edges per row (got %lld)", (long long)edges);
   JN_REQUIRE(edges >= 1 && fits_int(batch * nodes) && fits_int(batch * nodes * edges) &&
                  fits_int(nodes * 2 * rank) && fits_int(nodes * out_dim * 4),
              kUnsupported, "problem too large for 32-bit edge ids and offsets");
@@ -182,8 +183,9 @@ int check_transition_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t Dsrc,
              "routes support topk <= %d below the destination count, or up to 64 destinations in all (topk=%lld, "
              "dst_nodes=%lld)",
              kSelectMaxK, (long long)topk, (long long)Nd);
-  JN_REQUIRE(compress_kind == 0 || compress_kind == 1, kUnsupported,
-             "route compress kind must be 0 (softmax) or 1 (signed_abs_softmax), got %d", compress_kind);
+  JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported,
+             "route compress kind must be 0 (softmax), 1 (signed_abs_softmax) or 2 (signed_entmax15), got %d",
+             compress_kind);
   JN_REQUIRE(temperature > 0.0f, kInvalidArgument, "temperature must be positive");
   JN_REQUIRE(fits_int(batch * Ns * k) && fits_int(batch * Nd * rank) && fits_int(batch * Ns * rank) &&
                  fits_int(Nd * Dv * 4) && fits_int(Nd * rank * 4),
@@ -220,8 +222,9 @@ int check_dense_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out
   JN_REQUIRE(batch >= 1 && nodes >= 1 && in_dim >= 1 && out_dim >= 1, kInvalidArgument,
              "batch, nodes and dims must be positive");
   JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
-  JN_REQUIRE(compress_kind == 0 || compress_kind == 1, kUnsupported,
-             "compress_kind must be 0 (softsign) or 1 (signed_abs_softmax), got %d", compress_kind);
+  JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported,
+             "compress_kind must be 0 (softsign), 1 (signed_abs_softmax) or 2 (signed_entmax15), got %d",
+             compress_kind);
   JN_REQUIRE(batch < 65536 && fits_int(batch * nodes) && nodes < (1LL << 22) && fits_int(nodes * out_dim),
              kUnsupported, "dense propagation shape too large");
   return kOk;
@@ -260,8 +263,9 @@ int check_transition_dense_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t
   JN_REQUIRE(batch >= 1 && Ns >= 1 && Nd >= 1 && Dsrc >= 1 && Ddst >= 1 && Dv >= 1, kInvalidArgument,
              "batch, node counts and dims must be positive");
   JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
-  JN_REQUIRE(compress_kind == 0 || compress_kind == 1, kUnsupported,
-             "route compress kind must be 0 (softmax) or 1 (signed_abs_softmax), got %d", compress_kind);
+  JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported,
+             "route compress kind must be 0 (softmax), 1 (signed_abs_softmax) or 2 (signed_entmax15), got %d",
+             compress_kind);
   JN_REQUIRE(temperature > 0.0f, kInvalidArgument, "temperature must be positive");
   JN_REQUIRE(batch < 65536 && fits_int(batch * Ns) && fits_int(batch * Nd) && Ns < (1LL << 22) &&
                  Nd < (1LL << 22) && fits_int(Ns * Dv) && fits_int(Nd * Dv) && fits_int(Ns * Nd),

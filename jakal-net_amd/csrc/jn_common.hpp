@@ -175,6 +175,83 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---- signed entmax-1.5 ------------------------------------------------------
+// entmax15(z) = max(x - tau, 0)^2 with x = (z - max z) / 2 and tau such that
+// the result sums to 1 (native/jakal_net_native.cpp:1133-1169).  The
+// threshold is found by support refinement: start from every entry, take the
+// closed-form threshold of the support S,
+//   tau(S) = mean_S x - sqrt(max(0, (1 - |S| var_S x) / |S|)),
+// keep the entries at or above it and repeat until the support stops changing.
+// This solves the same equation as the reference's sort (whose support is the
+// set of the |S| largest entries).
+constexpr int kEntmaxMaxIter = 256;
+
+__device__ __forceinline__ float entmax15_tau_of(float s1, float s2, float n) {
+  const float mean = s1 / n, msq = s2 / n;
+  return mean - sqrtf(fmaxf(0.0f, (1.0f - n * (msq - mean * mean)) / n));
+}
+
+// One entry per lane: returns this lane's entmax15 weight (0 where !ok).
+__device__ __forceinline__ float entmax15_lane(float z, bool ok) {
+  const float zmax = wave_max_f(ok ? z : -INFINITY);
+  const float x = ok ? 0.5f * (z - zmax) : -INFINITY;
+  float tau = -INFINITY;
+  int n_prev = -1;
+  for (int it = 0; it < kEntmaxMaxIter; ++it) {
+    const bool in = ok && x >= tau;
+    const float n = wave_sum(in ? 1.0f : 0.0f);
+    if ((int)n == n_prev) break;
+    n_prev = (int)n;
+    tau = entmax15_tau_of(wave_sum(in ? x : 0.0f), wave_sum(in ? x * x : 0.0f), n);
+  }
+  const float d = ok ? fmaxf(x - tau, 0.0f) : 0.0f;
+  const float p = d * d;
+  const float den = wave_sum(p);
+  return den > 0.0f ? p / den : 0.0f;
+}
+
+// A whole row of n entries per wavefront (lane l reads entries l, l + 64, ...
+// through zf(j) >= 0): returns tau and sets zmax; the weights are then
+// max(0.5 (z - zmax) - tau, 0)^2 over their sum.
+template <class F>
+__device__ __forceinline__ float entmax15_row_tau(F zf, int n, float& zmax) {
+  const int lane = lane_id();
+  float m = -INFINITY;
+  for (int j = lane; j < n; j += kWave) m = fmaxf(m, zf(j));
+  m = wave_max_f(m);
+  zmax = m;
+  float tau = -INFINITY;
+  int n_prev = -1;
+  for (int it = 0; it < kEntmaxMaxIter; ++it) {
+    float s1 = 0.0f, s2 = 0.0f, c = 0.0f;
+    for (int j = lane; j < n; j += kWave) {
+      const float x = 0.5f * (zf(j) - m);
+      if (x >= tau) {
+        s1 += x;
+        s2 += x * x;
+        c += 1.0f;
+      }
+    }
+    c = wave_sum(c);
+    if ((int)c == n_prev) break;
+    n_prev = (int)c;
+    tau = entmax15_tau_of(wave_sum(s1), wave_sum(s2), c);
+  }
+  return tau;
+}
+
+// Backward of sign(s) * entmax15(|s|) (native/jakal_net_native.cpp:1183-1205):
+// with u = sqrt(|r|) for the lane's output r, gi = sign(s) g u,
+//   grad s = (gi - u * sum(gi) / sum(u)) * sign(s).
+__device__ __forceinline__ float signed_entmax15_backward_lane(float s, float r, float g) {
+  const float sg = (s > 0.f) ? 1.f : ((s < 0.f) ? -1.f : 0.f);
+  const float u = sqrtf(fabsf(r));
+  const float gi = g * sg * u;
+  const float us = wave_sum(u);
+  const float corr = us > 0.0f ? wave_sum(gi) / us : 0.0f;
+  return (gi - corr * u) * sg;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (hardware id % 8).
 // Map the hardware id to a logical tile so that each XCD runs a contiguous
 // range of logical tiles (same batch element, same gathered rows) and they

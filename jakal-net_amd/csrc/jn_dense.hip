@@ -4,7 +4,7 @@
 // jakal_net_native.cpp:5962-6076): every target row i aggregates every source
 // j with e[i, j] = compress(s[i, j]),
 //     s = P_t diag(w_hat) P_s^T + b,
-//     compress = softsign (elementwise) or sign(s) * softmax(|s|) over the row,
+//     compress = softsign (elementwise), sign(s) * softmax(|s|) or sign(s) * entmax15(|s|) over the row,
 //     delta_state[i] = sum_j e[i,j] ps[j],   delta_val[i] = sum_j e[i,j] pv[j].
 // Like the reference's full-dense branch, the edge matrix E [B, N, N] is
 // materialised (in HBM, fp32): the two N x N contractions run as batched MFMA
@@ -58,6 +58,28 @@ __global__ __launch_bounds__(256) void dense_compress_kernel(float* S, const flo
         s[j] = e;
       }
     }
+  } else if (compress == 2) {
+    // sign(s) * entmax15(|s|) over the row's sources
+    float zmax;
+    auto zf = [&](int j) { return fabsf(s[j] + bb); };
+    const float tau = entmax15_row_tau(zf, lim, zmax);
+    float den = 0.0f;
+    for (int j = lane; j < lim; j += kWave) {
+      const float d = fmaxf(0.5f * (zf(j) - zmax) - tau, 0.0f);
+      den += d * d;
+    }
+    den = wave_sum(den);
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    for (int j = lane; j < N; j += kWave) {
+      float e = 0.f;
+      if (j < lim) {
+        const float x = s[j] + bb;
+        const float d = fmaxf(0.5f * (fabsf(x) - zmax) - tau, 0.0f);
+        e = sign_f(x) * (d * d) * inv;
+        acc += e * psb[j];
+      }
+      s[j] = e;
+    }
   } else {
     // sign(s) * softmax(|s|) over the row's sources: max, sum of exponentials, then write
     float m = -INFINITY;
@@ -83,6 +105,7 @@ __global__ __launch_bounds__(256) void dense_compress_kernel(float* S, const flo
 // G holds gdv . pv^T on entry; on exit the score gradient
 //   g_e = G + gds[i] ps[j]; softsign: g_s = g_e (1 - |e|)^2 (= g_e / (1 + |s|)^2);
 //   signed |s| softmax: g_s = |e| g_e - e sum_j(g_e e);
+//   signed entmax-1.5 (u = sqrt|e|): g_s = sign(e) (sign(e) g_e u - u sum_j(sign(e) g_e u) / sum_j u);
 // and 0 for the sources a causal row does not keep (not read).
 template <bool VEC>
 __global__ __launch_bounds__(256) void dense_compress_backward_kernel(float* G, const float* E, const float* gds,
@@ -101,6 +124,17 @@ __global__ __launch_bounds__(256) void dense_compress_backward_kernel(float* G, 
   if (compress == 1) {
     for (int j = lane; j < lim; j += kWave) row_dot += (g[j] + gs * psb[j]) * e[j];
     row_dot = wave_sum(row_dot);
+  } else if (compress == 2) {
+    // entmax-1.5 backward: u = sqrt(|e|), gi = sign(e) g_e u (sign(e) = sign(s) where u > 0);
+    // row_dot = sum(gi) / sum(u)
+    float gis = 0.0f, us = 0.0f;
+    for (int j = lane; j < lim; j += kWave) {
+      const float u = sqrtf(fabsf(e[j]));
+      gis += (g[j] + gs * psb[j]) * sign_f(e[j]) * u;
+      us += u;
+    }
+    us = wave_sum(us);
+    row_dot = us > 0.0f ? wave_sum(gis) / us : 0.0f;
   }
   float acc = 0.0f;
   if (VEC && compress == 0) {
@@ -129,6 +163,9 @@ __global__ __launch_bounds__(256) void dense_compress_backward_kernel(float* G, 
         if (compress == 0) {
           const float d = 1.0f - fabsf(ej);
           gsj = ge * d * d;
+        } else if (compress == 2) {
+          const float sg = sign_f(ej), u = sqrtf(fabsf(ej));
+          gsj = (ge * sg * u - row_dot * u) * sg;
         } else {
           gsj = fabsf(ej) * ge - ej * row_dot;
         }

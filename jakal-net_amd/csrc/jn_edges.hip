@@ -11,7 +11,8 @@
 //   cols_backward  : scatter-side grads (grad pv, grad ps, grad key projection) as gathers
 //
 // Compress kinds: 0 softsign (propagation.py:85-88), 1 signed |s| softmax over the
-// row's selected edges (propagation.py:74-82).
+// row's selected edges (propagation.py:74-82), 2 signed entmax-1.5 over them
+// (kernels.py:221-237; native/jakal_net_native.cpp:1171-1205).
 #include "jn_internal.hpp"
 
 namespace jakal {
@@ -51,6 +52,10 @@ __device__ __forceinline__ void row_coefficients(const int32_t* idx, const float
       s = score[row * k + e];
       c = (compress == 0) ? softsign_f(s) : sign_f(s) * __expf(fabsf(s) - row_max) * row_inv_sum;
     }
+  }
+  if (compress == 2) {  // uniform; the whole row is this wavefront's (k <= 64 checked on the host)
+    const float p = entmax15_lane(fabsf(s), j >= 0);
+    c = j >= 0 ? sign_f(s) * p : 0.0f;
   }
 }
 
@@ -224,6 +229,8 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
         const float sg = sign_f(s);
         gsc = sg * (sg * cf) * (sg * gc - row_dot);
       }
+    } else if (a.compress == 2) {
+      gsc = signed_entmax15_backward_lane(s, cf, gc);  // absent edges: s = cf = gc = 0
     } else if (j >= 0) {
       gsc = gc * softsign_grad_f(s);
     }

@@ -5,7 +5,8 @@
 // destinations (edge list idx/logit [B*Ns, k], from the top-k select) and
 //   p[j, e]    = softmax over the row's edges of the logits (compress 0,
 //                kernel_common.py:420-423) or sign(l) * softmax(|l|)
-//                (compress 1, native_backend.py:2184-2188)
+//                (compress 1, native_backend.py:2184-2188) or sign(l) *
+//                entmax15(|l|) (compress 2, transition.py:70-75)
 //   coef[j, e] = rho[j] * p[j, e]          rho = sender strength (softplus(state))
 //   delta_state[k] = sum_{j->k} coef * ps[j],  delta_val[k] = sum_{j->k} coef * pv[j]
 // The destination sums run as gathers over the edge list transposed by
@@ -27,6 +28,7 @@ namespace jakal {
 // Route probability of edge `lane` of a source row (signed for compress 1) and
 // the sign of its logit.  Lanes >= k, and absent edges, get p = 0.
 __device__ __forceinline__ float route_probability(int j, float s, int compress) {
+  if (compress == 2) return sign_f(s) * entmax15_lane(fabsf(s), j >= 0);
   const float a = compress == 0 ? s : fabsf(s);
   float m = j >= 0 ? a : -INFINITY;
   m = __int_as_float(wave_reduce_i(__float_as_int(m), [](int x, int y) {
@@ -168,6 +170,8 @@ __global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdAr
   if (a.compress == 0) {
     const float pg = wave_sum(p * gp);
     gl = p * (gp - pg);
+  } else if (a.compress == 2) {
+    gl = signed_entmax15_backward_lane(s, p, gp);
   } else {
     const float pg = wave_sum(gp * p);
     const float sg = sign_f(s);
@@ -242,7 +246,7 @@ int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream) {
   if (a.rows == 0) return kOk;
   JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
   JN_REQUIRE(a.k >= 1 && a.k <= kWave, kUnsupported, "routes support 1..64 edges per source (got %d)", a.k);
-  JN_REQUIRE(a.compress == 0 || a.compress == 1, kUnsupported, "route compress kind must be 0 or 1");
+  JN_REQUIRE(a.compress >= 0 && a.compress <= 2, kUnsupported, "route compress kind must be 0, 1 or 2");
   const int64_t blocks = (a.rows + 3) / 4;
   JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
   JN_REQUIRE((int64_t)a.Nd * a.D * 4 < (1LL << 31) && (int64_t)a.Nd * a.ldk * 4 < (1LL << 31), kUnsupported,

@@ -1,7 +1,8 @@
 // Dense pairwise transitions (gfx950): every source routes to every destination.
 //
 //   l[j, k]   = ((P_src[j] * w) . P_dst[k] + b) / T         LowRankBilinearRoute
-//   R[j, :]   = compress(l[j, :])     softmax or sign(l) * softmax(|l|) over destinations
+//   R[j, :]   = compress(l[j, :])     softmax, sign(l) * softmax(|l|) or sign(l) * entmax15(|l|)
+//                                     over destinations
 //   dstate[k] = sum_j R[j, k] rho_j ps_j,   dval[k] = sum_j R[j, k] rho_j pv_j
 //
 // Reference: transition_pairwise_dense (native/jakal_net_native.cpp:6705-6914;
@@ -31,14 +32,33 @@ __global__ __launch_bounds__(256) void route_dense_compress_kernel(float* L, con
   if (row >= rows) return;
   float* x = L + row * N;
   const float bb = bias ? bias[0] : 0.0f;
-  const bool sgn = kind == 1;
+  const bool sgn = kind >= 1;
   // logit as the reference forms it, NaN -> 0 and +-inf -> +-FLT_MAX for the
-  // signed variant (torch.nan_to_num)
+  // signed variants (torch.nan_to_num)
   auto logit = [&](float s) {
     float v = (s + bb) * inv_temp;
     if (sgn) v = (v != v) ? 0.0f : fminf(fmaxf(v, -FLT_MAX), FLT_MAX);
     return v;
   };
+  if (kind == 2) {
+    // sign(l) * entmax15(|l|) over the row
+    float zmax;
+    auto zf = [&](int j) { return fabsf(logit(x[j])); };
+    const float tau = entmax15_row_tau(zf, N, zmax);
+    float den = 0.0f;
+    for (int j = lane; j < N; j += kWave) {
+      const float d = fmaxf(0.5f * (zf(j) - zmax) - tau, 0.0f);
+      den += d * d;
+    }
+    den = wave_sum(den);
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    for (int j = lane; j < N; j += kWave) {
+      const float a = logit(x[j]);
+      const float d = fmaxf(0.5f * (fabsf(a) - zmax) - tau, 0.0f);
+      x[j] = sign_f(a) * (d * d) * inv;
+    }
+    return;
+  }
   float m = -INFINITY;
   if constexpr (VEC) {
     for (int j = 4 * lane; j < N; j += 256) {
@@ -116,6 +136,7 @@ __global__ __launch_bounds__(256) void route_dense_colsum_kernel(const float* R,
 //   grad rho_j = sum_k R[j, k] h_k,  grad ps_j = rho_j sum_k R[j, k] gds[b, k]
 //   softmax:            g_l = R (g - sum R g)
 //   sign * softmax(|l|): g_l = |R| g - R sum R g   (0 where l == 0, as R is)
+//   sign * entmax15(|l|): with u = sqrt|R|, g_l = sign(R) (sign(R) g u - u sum(sign(R) g u) / sum u)
 //   H[j, k] <- g_l / T (gradient of the raw bilinear logit); rowsum[j] = sum_k H[j, k]
 template <bool VEC>
 __global__ __launch_bounds__(256) void route_dense_compress_backward_kernel(
@@ -150,8 +171,23 @@ __global__ __launch_bounds__(256) void route_dense_compress_backward_kernel(
   srh = wave_sum(srh);
   srg = wave_sum(srg);
   dot = rj * srh;  // sum_k R g = rho_j sum_k R h
+  if (kind == 2) {
+    // entmax-1.5: u = sqrt(|R|), gi = sign(R) g u; dot <- sum(gi) / sum(u)
+    float gis = 0.0f, us = 0.0f;
+    for (int k = lane; k < Nd; k += kWave) {
+      const float u = sqrtf(fabsf(rr[k]));
+      gis += rj * (h[k] + pj * gb[k]) * sign_f(rr[k]) * u;
+      us += u;
+    }
+    us = wave_sum(us);
+    dot = us > 0.0f ? wave_sum(gis) / us : 0.0f;
+  }
   auto grad = [&](float r, float hk) {
     const float g = rj * hk;
+    if (kind == 2) {
+      const float sg = sign_f(r), u = sqrtf(fabsf(r));
+      return (g * sg * u - dot * u) * sg * inv_temp;
+    }
     return ((sgn ? fabsf(r) : r) * g - r * dot) * inv_temp;
   };
   float rs = 0.0f;

@@ -92,6 +92,38 @@ def masked_softmax(logits: Tensor, mask: Tensor, dim: int = -1) -> Tensor:
     return torch.softmax(logits.masked_fill(~mask, floor), dim=dim)
 
 
+def entmax15(logits: Tensor, *, mask: Tensor | None = None) -> Tensor:
+    """1.5-entmax over the last dimension (reference kernels.py:155-202):
+    masked entries -> min, shift by the max, halve, sort-based threshold."""
+    clean = torch.nan_to_num(logits)
+    if mask is not None:
+        clean = clean.masked_fill(~mask.to(dtype=torch.bool), torch.finfo(clean.dtype).min)
+    x = (clean - clean.max(dim=-1, keepdim=True).values) / 2
+    srt = torch.sort(x, dim=-1, descending=True).values
+    rho = torch.arange(1, x.shape[-1] + 1, device=x.device, dtype=x.dtype)
+    mean = srt.cumsum(-1) / rho
+    mean_sq = (srt * srt).cumsum(-1) / rho
+    delta = torch.clamp((1 - rho * (mean_sq - mean.square())) / rho, min=0)
+    tau = mean - torch.sqrt(delta)
+    support = (tau <= srt).sum(dim=-1, keepdim=True).clamp_min(1)
+    p = torch.clamp(x - tau.gather(-1, support - 1), min=0).square()
+    if mask is not None:
+        p = p * mask.to(dtype=p.dtype)
+    den = p.sum(dim=-1, keepdim=True)
+    return torch.where(den > 0, p / den.clamp_min(torch.finfo(p.dtype).eps), torch.zeros_like(p))
+
+
+def signed_entmax15(logits: Tensor, *, dim: int = -1, mask: Tensor | None = None) -> Tensor:
+    """sign(l) * entmax15(|l|) (reference kernels.py:221-237)."""
+    if dim != -1:
+        raise ValueError("signed_entmax15 supports dim=-1 only.")
+    clean = torch.nan_to_num(logits)
+    out = torch.sign(clean) * entmax15(clean.abs(), mask=mask)
+    if mask is not None:
+        out = out * mask.to(dtype=out.dtype)
+    return torch.nan_to_num(out)
+
+
 def select_topk(scores: Tensor, topk: int, *, dim: int = -1) -> torch.return_types.topk:
     if topk <= 0:
         raise ValueError("topk must be positive.")

@@ -255,8 +255,9 @@ def transition_pairwise_topk_native(
 ) -> LayerDelta:
     if not supports_pairwise_route_kernel(route_fn):
         raise TypeError("Unsupported pairwise route_fn for native sparse transition.")
-    if route_compress_name not in ("softmax", "signed_abs_softmax"):
-        raise TypeError("Native sparse pairwise transition supports softmax and signed_abs_softmax routes.")
+    if route_compress_name not in ("softmax", "signed_abs_softmax", "signed_entmax15"):
+        raise TypeError("Native sparse pairwise transition supports softmax, signed_abs_softmax and signed_entmax15 "
+                        "routes.")
     spec = pairwise_route_kernel_spec(route_fn)
     return _to_layer_delta(
         _native_module().transition_pairwise_topk(

@@ -45,7 +45,7 @@ from jakal_net.core import (
     validate_projected_state,
     validate_projected_val,
 )
-from jakal_net.kernel_common import build_topk_mask, causal_window_mask, supports_pairwise_kernel
+from jakal_net.kernel_common import build_topk_mask, causal_window_mask, signed_entmax15, supports_pairwise_kernel
 from jakal_net.native_backend import (
     native_disabled_by_env,
     native_supports,
@@ -78,7 +78,7 @@ def edge_compress_name(edge_compress_fn: Callable[[Tensor], Tensor]) -> str | No
     return None
 
 
-_NATIVE_EDGE_COMPRESS = ("softsign", "signed_abs_softmax")
+_NATIVE_EDGE_COMPRESS = ("softsign", "signed_abs_softmax", "signed_entmax15")
 
 
 def compress_edges(scores: Tensor, edge_compress_fn: Callable[[Tensor], Tensor], *, mask: Tensor | None = None) -> Tensor:
@@ -95,7 +95,7 @@ def compress_edges(scores: Tensor, edge_compress_fn: Callable[[Tensor], Tensor],
             magnitudes = magnitudes.masked_fill(~mask, -torch.inf)
         return torch.nan_to_num(signs * torch.softmax(magnitudes, dim=-1))
     if edge_compress_name(edge_compress_fn) == "signed_entmax15":
-        raise NotImplementedError("signed_entmax15 edges are not part of this build's hot path.")
+        return signed_entmax15(scores, mask=mask)
     edges = edge_compress_fn(scores)
     if mask is not None:
         edges = edges * mask.to(dtype=edges.dtype)

@@ -38,7 +38,7 @@ from jakal_net.core import (
     validate_route_block_logits,
     validate_route_logits,
 )
-from jakal_net.kernel_common import build_topk_mask, masked_softmax, supports_pairwise_route_kernel
+from jakal_net.kernel_common import build_topk_mask, masked_softmax, signed_entmax15, supports_pairwise_route_kernel
 from jakal_net.native_backend import (
     native_disabled_by_env,
     native_supports,
@@ -144,7 +144,7 @@ class Transition(nn.Module):
         if self.route_compress_name == "signed_abs_softmax":
             return signed_abs_softmax(logits, dim=-1, mask=mask)
         if self.route_compress_name == "signed_entmax15":
-            raise NotImplementedError("signed_entmax15 routes are not part of this build's hot path.")
+            return signed_entmax15(logits, dim=-1, mask=mask)
         if mask is not None:
             return masked_softmax(logits, mask, dim=-1)
         return torch.softmax(logits, dim=-1)
@@ -210,7 +210,7 @@ class Transition(nn.Module):
         return (
             self._route_expects_pairwise_inputs
             and supports_pairwise_route_kernel(self.route_fn)
-            and self.route_compress_name in ("softmax", "signed_abs_softmax")
+            and self.route_compress_name in ("softmax", "signed_abs_softmax", "signed_entmax15")
             and not self.use_direction_only
         )
 
@@ -322,7 +322,7 @@ class SparseTransition(Transition):
         return (
             self._route_expects_pairwise_inputs
             and supports_pairwise_route_kernel(self.route_fn)
-            and self.route_compress_name in ("softmax", "signed_abs_softmax")
+            and self.route_compress_name in ("softmax", "signed_abs_softmax", "signed_entmax15")
             and not self.use_direction_only
         )
 

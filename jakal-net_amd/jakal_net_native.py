@@ -110,7 +110,7 @@ _declare(
 
 ABI_VERSION = int(_LIB.jn_abi_version())
 
-_COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1}
+_COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
 MAX_TOPK = 64
 CAUSAL_DENSE_MIN_NODES = 128  # full causal windows from this many nodes run on the dense MFMA path
 
@@ -122,7 +122,7 @@ _SUPPORTED_OPS = (
     "transition_pairwise_dense",
     "low_rank_topk_select",
 )
-_ROUTE_COMPRESS_KINDS = {"softmax": 0, "signed_abs_softmax": 1}
+_ROUTE_COMPRESS_KINDS = {"softmax": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
 MAX_ROUTE_TOPK = 64  # below the destination count; every destination up to 64
 
 
@@ -743,8 +743,8 @@ def transition_pairwise_topk(
 
     ``core_weight`` is the raw route weight w; ``source_weight`` and
     ``target_weight`` the route projections (kernel_common.py:285-294).  The
-    optional trailing ``route_compress_name`` ("softmax" or
-    "signed_abs_softmax") has no counterpart in the reference's composite op,
+    optional trailing ``route_compress_name`` ("softmax", "signed_abs_softmax"
+    or "signed_entmax15") has no counterpart in the reference's composite op,
     which is softmax-only."""
     if topk >= dst_val.shape[-2] > 64:
         # every destination kept (transition.py:437-440): the dense transition
@@ -863,8 +863,8 @@ def transition_pairwise_dense(
     """Dense pairwise transition; signature of jakal_net_native.cpp:6705-6725.
 
     Every source routes to every destination with routes
-    compress(((P_s * w) . P_t + b) / T) over destinations ("softmax" or
-    "signed_abs_softmax").  The block sizes are validated and otherwise
+    compress(((P_s * w) . P_t + b) / T) over destinations ("softmax",
+    "signed_abs_softmax" or "signed_entmax15").  The block sizes are validated and otherwise
     ignored: the HIP kernels tile for gfx950 themselves."""
     _check_route_spec(route_kind, source_weight, source_bias, target_weight, target_bias, hidden_weight, out_weight,
                       route_compress_name, temperature)

@@ -118,6 +118,48 @@ def softplus(x):
     return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
 
 
+def entmax15(z, mask):
+    """1.5-entmax over the unmasked entries of each row, sort-based as the
+    reference computes it (native/jakal_net_native.cpp:1133-1169,
+    src/jakal_net/kernels.py:155-202): masked entries -> -1e4, shift by the row
+    max, halve, sort descending; tau_rho = mean_rho - sqrt(max(0, (1 -
+    rho (meansq_rho - mean_rho^2)) / rho)) over the top rho entries; support =
+    #{rho : tau_rho <= sorted_rho} (at least 1); p = max(x - tau*, 0)^2, then
+    normalised by its sum and zeroed where masked."""
+    z = np.where(mask, np.asarray(z, F64), -1e4)
+    x = (z - np.max(z, axis=-1, keepdims=True)) / 2.0
+    srt = -np.sort(-x, axis=-1)
+    rho = np.arange(1, x.shape[-1] + 1, dtype=F64)
+    mean = np.cumsum(srt, axis=-1) / rho
+    mean_sq = np.cumsum(srt * srt, axis=-1) / rho
+    ss = rho * (mean_sq - mean * mean)
+    delta = np.maximum((1.0 - ss) / rho, 0.0)
+    tau = mean - np.sqrt(delta)
+    support = np.maximum(np.sum(tau <= srt, axis=-1, keepdims=True), 1)
+    tau_star = np.take_along_axis(tau, support - 1, axis=-1)
+    p = np.maximum(x - tau_star, 0.0) ** 2 * mask
+    den = np.sum(p, axis=-1, keepdims=True)
+    return np.where(den > 0, p / np.where(den > 0, den, 1.0), 0.0)
+
+
+def signed_entmax15(scores, mask):
+    """sign(s) * entmax15(|s|) over the unmasked entries (cpp:1171-1181)."""
+    s = np.nan_to_num(np.asarray(scores, F64))
+    return np.sign(s) * entmax15(np.abs(s), mask) * mask
+
+
+def signed_entmax15_backward(scores, mask, grad_routes):
+    """cpp:1183-1205: with P = |routes|, u = sqrt(P), gi = sign(s) g u:
+    grad s = (gi - u * sum(gi) / sum(u)) * sign(s), masked entries 0."""
+    s = np.nan_to_num(np.asarray(scores, F64))
+    sg = np.sign(s)
+    u = np.sqrt(np.abs(signed_entmax15(s, mask)))
+    gi = np.asarray(grad_routes, F64) * sg * u
+    us = np.sum(u, axis=-1, keepdims=True)
+    corr = np.where(us > 0, np.sum(gi, axis=-1, keepdims=True) / np.where(us > 0, us, 1.0), 0.0)
+    return np.where(mask, (gi - corr * u) * sg, 0.0)
+
+
 # ---------------------------------------------------------------------------
 # edge compression (propagation.py:67-88)
 # ---------------------------------------------------------------------------
@@ -127,6 +169,8 @@ def compress(scores, mask, kind):
         return np.where(mask, s / (1.0 + np.abs(s)), 0.0)
     if kind == "signed_abs_softmax":
         return np.sign(s) * masked_softmax(np.abs(s), mask)
+    if kind == "signed_entmax15":
+        return signed_entmax15(s, mask)
     raise ValueError(kind)
 
 
@@ -141,6 +185,8 @@ def compress_backward(scores, mask, kind, grad_edges):
         e = sg * p
         dot = np.sum(g * e, axis=-1, keepdims=True)
         return np.where(mask, sg * p * (sg * g - dot), 0.0)
+    if kind == "signed_entmax15":
+        return signed_entmax15_backward(s, mask, g)
     raise ValueError(kind)
 
 
@@ -232,11 +278,12 @@ def normalized_weight_backward(w, g_what):
 def route_compress(logits, mask, kind="softmax"):
     """Route weights over the masked destinations of each source row:
     softmax (kernel_common.py:420-423) or sign(l) * softmax(|l|)
-    (transition.py:53-67, native_backend.py:2184-2188)."""
+    (transition.py:53-67, native_backend.py:2184-2188) or sign(l) *
+    entmax15(|l|) (transition.py:70-75)."""
     if kind == "softmax":
         return masked_softmax(logits, mask)
-    if kind == "signed_abs_softmax":
-        return compress(logits, mask, "signed_abs_softmax")
+    if kind in ("signed_abs_softmax", "signed_entmax15"):
+        return compress(logits, mask, kind)
     raise ValueError(kind)
 
 
@@ -245,8 +292,8 @@ def route_compress_backward(logits, mask, kind, grad_routes):
         p = masked_softmax(logits, mask)
         g = np.asarray(grad_routes, F64)
         return np.where(mask, p * (g - np.sum(p * g, axis=-1, keepdims=True)), 0.0)
-    if kind == "signed_abs_softmax":
-        return compress_backward(logits, mask, "signed_abs_softmax", grad_routes)
+    if kind in ("signed_abs_softmax", "signed_entmax15"):
+        return compress_backward(logits, mask, kind, grad_routes)
     raise ValueError(kind)
 
 

@@ -56,7 +56,7 @@ def _inputs(seed, B, N, D, r):
     return g, state, val, U, V, w
 
 
-@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax"])
+@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax", "signed_entmax15"])
 @pytest.mark.parametrize("separate_pv", [False, True])
 @pytest.mark.parametrize("N,with_bias", [(64, True), (37, False)])
 def test_dense_forward_backward_matches_oracle(dev, compress, separate_pv, N, with_bias):

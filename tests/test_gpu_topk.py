@@ -140,7 +140,7 @@ def _c1_inputs(seed=1001, B=2, N=256, D=64, r=16):
     return state, val, U, V, w, b
 
 
-@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax"])
+@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax", "signed_entmax15"])
 @pytest.mark.parametrize("separate_pv,k", [(False, 8), (True, 8), (True, 64)])
 def test_propagation_topk_forward_backward_matches_oracle(dev, compress, separate_pv, k):
     import jakal_net_native as jn

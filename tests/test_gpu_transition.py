@@ -107,14 +107,15 @@ def _run(dev, seed, B, Ns, Nd, Dsrc, Ddst, r, topk, temperature, kind, init="xav
         _close(_np(t.grad), want, atol=ATOL * max(scale, float(np.abs(want).max())), what=f"grad {name}")
 
 
-@pytest.mark.parametrize("kind", ["softmax", "signed_abs_softmax"])
+@pytest.mark.parametrize("kind", ["softmax", "signed_abs_softmax", "signed_entmax15"])
 @pytest.mark.parametrize("temperature", [1.0, 1.7])
 def test_transition_forward_backward_matches_oracle(dev, kind, temperature):
     _run(dev, 3001, B=2, Ns=64, Nd=16, Dsrc=32, Ddst=24, r=8, topk=4, temperature=temperature, kind=kind)
 
 
-def test_transition_topk_above_32(dev):
-    _run(dev, 3004, B=2, Ns=80, Nd=100, Dsrc=16, Ddst=12, r=4, topk=48, temperature=1.1, kind="signed_abs_softmax")
+@pytest.mark.parametrize("kind", ["signed_abs_softmax", "signed_entmax15"])
+def test_transition_topk_above_32(dev, kind):
+    _run(dev, 3004, B=2, Ns=80, Nd=100, Dsrc=16, Ddst=12, r=4, topk=48, temperature=1.1, kind=kind)
 
 
 @pytest.mark.parametrize("topk", [16, 40])

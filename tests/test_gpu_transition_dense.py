@@ -102,7 +102,7 @@ def _run(dev, seed, B, Ns, Nd, Dsrc, Ddst, r, temperature, kind, init="xavier", 
         _close(_np(bd.grad), gr["b"], atol=ATOL * scale_b, what="grad b")
 
 
-@pytest.mark.parametrize("kind", ["softmax", "signed_abs_softmax"])
+@pytest.mark.parametrize("kind", ["softmax", "signed_abs_softmax", "signed_entmax15"])
 @pytest.mark.parametrize("temperature", [1.0, 1.7])
 def test_dense_transition_matches_oracle(dev, kind, temperature):
     _run(dev, 3101, B=2, Ns=64, Nd=16, Dsrc=32, Ddst=24, r=8, temperature=temperature, kind=kind)
@@ -113,8 +113,9 @@ def test_dense_transition_odd_shapes_without_bias(dev):
          with_bias=False)
 
 
-def test_dense_transition_medium(dev):
-    _run(dev, 3103, B=2, Ns=300, Nd=140, Dsrc=136, Ddst=72, r=48, temperature=1.2, kind="softmax")
+@pytest.mark.parametrize("kind", ["softmax", "signed_entmax15"])
+def test_dense_transition_medium(dev, kind):
+    _run(dev, 3103, B=2, Ns=300, Nd=140, Dsrc=136, Ddst=72, r=48, temperature=1.2, kind=kind)
 
 
 def test_topk_over_every_destination_runs_dense(dev):
@@ -134,7 +135,7 @@ def test_dense_transition_api_native_matches_reference(dev):
     src = Layer(dim=6, num_nodes=12, state=torch.randn(2, 12, device=dev), val=torch.randn(2, 12, 6, device=dev))
     dst = Layer(dim=5, num_nodes=9, state=torch.randn(2, 9, device=dev), val=torch.randn(2, 9, 5, device=dev))
     kw = dict(val_proj_fn=torch.nn.Linear(6, 5).to(dev), state_proj_fn=lambda s: s * 0.5 + 1.0)
-    for compress in ("softmax", "signed_abs_softmax"):
+    for compress in ("softmax", "signed_abs_softmax", "signed_entmax15"):
         ref = Transition(LowRankBilinearRoute(6, 5, rank=4).to(dev), implementation="reference",
                          route_compress_name=compress, **kw)
         nat = Transition(LowRankBilinearRoute(6, 5, rank=4).to(dev), implementation="native",

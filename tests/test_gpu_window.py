@@ -103,7 +103,7 @@ def _run(dev, seed, B, N, D, r, window, compress, separate_pv, init="xavier"):
         _close(_np(got), want, atol=ATOL * max(scale, float(np.abs(want).max())), what=what)
 
 
-@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax"])
+@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax", "signed_entmax15"])
 @pytest.mark.parametrize("separate_pv", [False, True])
 def test_window_forward_backward_matches_oracle(dev, compress, separate_pv):
     _run(dev, 2001, B=2, N=64, D=32, r=8, window=8, compress=compress, separate_pv=separate_pv)
@@ -135,7 +135,7 @@ def test_sparse_propagation_window_api_native_matches_reference(dev):
     assert torch.allclose(a.delta_val, b.delta_val, atol=1e-5, rtol=1e-5)
 
 
-@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax"])
+@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax", "signed_entmax15"])
 @pytest.mark.parametrize("separate_pv,window_extra", [(False, 0), (True, 7)])
 def test_full_causal_window_runs_dense(dev, compress, separate_pv, window_extra):
     """window >= N - 1 on N >= 128 nodes: every earlier source, computed as

@@ -144,6 +144,81 @@ def test_softsign_and_signed_abs_softmax_closed_forms():
     assert np.allclose(e, [[-z[0] / z.sum(), 0.0, 0.0, z[2] / z.sum()]])  # sign(0) == 0
 
 
+def test_entmax15_closed_forms():
+    m2 = np.ones((1, 2), dtype=bool)
+    assert np.allclose(O.entmax15(np.array([[0.0, 0.0]]), m2), [[0.5, 0.5]])
+    # [1, 0]: x = [0, -1/2], both in the support: tau = -1/4 - sqrt(7/16)
+    tau = -0.25 - np.sqrt(7.0 / 16.0)
+    want = np.array([(0 - tau) ** 2, (-0.5 - tau) ** 2])
+    assert np.allclose(O.entmax15(np.array([[1.0, 0.0]]), m2), [want / want.sum()])
+    assert np.isclose(want.sum(), 1.0)
+    # a dominant entry takes all the mass; masked entries stay 0
+    m3 = np.array([[True, True, True, False]])
+    assert np.allclose(O.entmax15(np.array([[3.0, 0.0, 0.0, 9.0]]), m3), [[1.0, 0.0, 0.0, 0.0]])
+    # sign(0) == 0 drops an entry after the distribution is formed
+    e = O.signed_entmax15(np.array([[-1.0, 0.0]]), m2)
+    assert e[0, 1] == 0.0 and e[0, 0] < 0
+
+
+def _entmax_tau_bisection(x, iters=200):
+    lo, hi = np.max(x) - 1.0, np.max(x)
+    for _ in range(iters):
+        mid = 0.5 * (lo + hi)
+        if np.sum(np.maximum(x - mid, 0.0) ** 2) >= 1.0:
+            lo = mid
+        else:
+            hi = mid
+    return 0.5 * (lo + hi)
+
+
+def _entmax_tau_support_iteration(x):
+    """Support refinement the HIP kernels use: start from every entry, take the
+    closed-form threshold of the current support, keep the entries at or above
+    it, repeat until the support no longer changes."""
+    tau, n_prev = -np.inf, -1
+    for _ in range(x.size + 1):
+        s = x[x >= tau]
+        if s.size == n_prev:
+            break
+        n_prev = s.size
+        mean, mean_sq = s.mean(), (s * s).mean()
+        tau = mean - np.sqrt(max(0.0, (1.0 - s.size * (mean_sq - mean * mean)) / s.size))
+    return tau
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 17, 64, 300])
+def test_entmax15_threshold_solves_its_defining_equation(n):
+    """p = max(x - tau, 0)^2 with sum p = 1 (x = z/2 shifted): the sort-based
+    restatement, bisection on the defining equation and the support iteration
+    of the kernels agree."""
+    r = _rng(40 + n)
+    for scale in (0.1, 1.0, 10.0):
+        z = r.normal(size=(8, n)) * scale
+        mask = r.random(size=(8, n)) < 0.8
+        mask[:, 0] = True
+        p = O.entmax15(z, mask)
+        assert np.allclose(p.sum(-1), 1.0)
+        for row in range(8):
+            zz = z[row][mask[row]]
+            x = (zz - zz.max()) / 2.0
+            tau_b = _entmax_tau_bisection(x)
+            tau_i = _entmax_tau_support_iteration(x)
+            assert abs(tau_i - tau_b) < 1e-9
+            assert np.allclose(p[row][mask[row]], np.maximum(x - tau_b, 0.0) ** 2, atol=1e-9)
+            assert (p[row][~mask[row]] == 0).all()
+
+
+def test_signed_entmax15_backward_matches_finite_differences():
+    r = _rng(41)
+    s = r.normal(size=(3, 7)) * 1.5
+    mask = r.random(size=(3, 7)) < 0.8
+    mask[:, 0] = True
+    g = r.normal(size=(3, 7))
+    got = O.signed_entmax15_backward(s, mask, g)
+    want = _fd(lambda: float(np.sum(O.signed_entmax15(s, mask) * g)), s)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-7)
+
+
 def test_transition_rows_are_distributions_over_k_destinations():
     r = _rng(4)
     l = r.normal(size=(2, 6, 5))
@@ -171,7 +246,9 @@ def _fd(f, x, eps=1e-6):
 
 
 @pytest.mark.parametrize("mode,kind", [("topk", "softsign"), ("window", "softsign"), ("dense", "softsign"),
-                                       ("topk", "signed_abs_softmax"), ("window", "signed_abs_softmax")])
+                                       ("topk", "signed_abs_softmax"), ("window", "signed_abs_softmax"),
+                                       ("topk", "signed_entmax15"), ("window", "signed_entmax15"),
+                                       ("dense", "signed_entmax15")])
 def test_propagation_backward_matches_finite_differences(mode, kind):
     r = _rng(5)
     B, N, D, R = 2, 6, 3, 2
@@ -196,7 +273,7 @@ def test_propagation_backward_matches_finite_differences(mode, kind):
     assert np.allclose(g["b"], _fd(loss, b), rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("kind", ["softmax", "signed_abs_softmax"])
+@pytest.mark.parametrize("kind", ["softmax", "signed_abs_softmax", "signed_entmax15"])
 def test_transition_backward_matches_finite_differences(kind):
     r = _rng(6)
     B, Ns, Nd, D, Dd, R = 2, 5, 4, 3, 2, 2

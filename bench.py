@@ -421,6 +421,101 @@ class DenseC4:
         }
 
 
+class TransitionDenseC3:
+    name = "c3-transition-dense"
+    metric = "routed pairs/sec + MFMA TFLOP/s (% peak), Transition (dense) S->B and B->S N_src=1024 N_dst=256 D=512 fwd+bwd"
+    workload = "C3 sizes, dense Transition S->B then B->S fwd+bwd (every destination), LowRankBilinearRoute, softmax routes, native"
+    data = "synthetic (seeded N(0,1) states and vals, default module init)"
+    config = {"batch": 8, "s_nodes": 1024, "b_nodes": 256, "dim": 512, "rank": 64}
+    traffic_file = "c3_transition_dense_hbm_traffic.json"
+
+    def edges(self) -> int:
+        c = self.config
+        return 2 * c["batch"] * c["s_nodes"] * c["b_nodes"]
+
+    def model(self, name):
+        c = self.config
+        B, S, Bn, D, r = (c[x] for x in ("batch", "s_nodes", "b_nodes", "dim", "rank"))
+        pairs = B * S * Bn  # per direction (both directions route S x B pairs)
+        dense = {
+            "gemm_f32_kernel<route_logits>": 2.0 * pairs * r,
+            "gemm_f32_kernel<route_aggregate>": 2.0 * pairs * D,
+            "gemm_f32_kernel<route_edge_grad>": 2.0 * pairs * D,
+            "gemm_f32_kernel<route_value_grad>": 2.0 * pairs * D,
+            "gemm_f32_kernel<route_source_grad>": 2.0 * pairs * r,
+            "gemm_f32_kernel<route_target_grad>": 2.0 * pairs * r,
+        }
+        if name in dense:
+            return "mfma", dense[name]
+        if name.startswith("route_dense_compress_backward_kernel"):
+            return "hbm", 4.0 * 3 * pairs  # read H and R, write G
+        if name.startswith("route_dense_compress_kernel"):
+            return "hbm", 4.0 * 2 * pairs
+        if name.startswith("route_dense_colsum_kernel"):
+            return "hbm", 4.0 * pairs
+        if name.startswith("gemm_f32_kernel"):
+            return "mfma", 2.0 * B * (S + Bn) / 2 * D * r  # projections, averaged over the two sides
+        return None
+
+    def sparse_bytes(self) -> float:
+        # dense: no gathers; the route matrices are the bytes that move
+        return 4.0 * 6 * self.edges()
+
+    def build(self, torch, dev):
+        from jakal_net import Layer, LowRankBilinearRoute, Transition
+
+        c = self.config
+        B, S, Bn, D, r = (c[x] for x in ("batch", "s_nodes", "b_nodes", "dim", "rank"))
+        g = torch.Generator().manual_seed(1003)
+        s_state, s_val = torch.randn(B, S, generator=g), torch.randn(B, S, D, generator=g)
+        b_state, b_val = torch.randn(B, Bn, generator=g), torch.randn(B, Bn, D, generator=g)
+        torch.manual_seed(1003)
+        s_to_b = Transition(LowRankBilinearRoute(D, D, rank=r), implementation="native").to(dev)
+        b_to_s = Transition(LowRankBilinearRoute(D, D, rank=r), implementation="native").to(dev)
+        s_layer = Layer(dim=D, num_nodes=S, state=s_state.to(dev).requires_grad_(True),
+                        val=s_val.to(dev).requires_grad_(True))
+        b_layer = Layer(dim=D, num_nodes=Bn, state=b_state.to(dev).requires_grad_(True),
+                        val=b_val.to(dev).requires_grad_(True))
+        return _TwoWayTransition(torch, s_to_b, b_to_s, s_layer, b_layer), None
+
+    def cpu_baseline(self, B_sample: int = 1) -> dict:
+        """Oracle (numpy, fp32) dense forward+backward of both directions on B_sample batch elements."""
+        import numpy as np
+
+        O = _oracle()
+        c = self.config
+        S, Bn, D, r = (c[x] for x in ("s_nodes", "b_nodes", "dim", "rank"))
+        Bs = B_sample
+        rng = np.random.default_rng(1003)
+        bound = 1.0 / math.sqrt(D)
+        layers = {"S": (rng.standard_normal((Bs, S)), rng.standard_normal((Bs, S, D))),
+                  "B": (rng.standard_normal((Bs, Bn)), rng.standard_normal((Bs, Bn, D)))}
+        params = [rng.uniform(-bound, bound, (2, r, D)) for _ in range(2)]
+        times = []
+        with O.compute_dtype(np.float32):
+            for _ in range(3):
+                t0 = time.perf_counter()
+                for (src, dst), (Ws, Wt) in zip((("S", "B"), ("B", "S")), params):
+                    st, sv = layers[src]
+                    _, dv = layers[dst]
+                    rho = O.softplus(st)
+                    nd = dv.shape[1]
+                    mask = np.ones((Bs, sv.shape[1], nd), dtype=bool)
+                    O.transition_forward(sv, dv, rho, st, sv, Ws, Wt, np.ones(r), 0.0, topk=nd, mask=mask)
+                    O.transition_backward(sv, dv, rho, st, sv, Ws, Wt, np.ones(r), 0.0, np.ones((Bs, nd)),
+                                          np.ones((Bs, nd, D)), topk=nd, mask=mask)
+                times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2]
+        return {
+            "value": self.edges() // c["batch"] * Bs / t,
+            "unit": "routed pairs/s",
+            "cores": _threads() or os.cpu_count(),
+            "kind": "port",
+            "sample": f"numpy oracle fp32, dense forward+backward of both directions, {Bs} of {c['batch']} batch "
+                      f"elements (N_src=1024, N_dst=256, D={D}, r={r}), median of 3 ({t:.2f} s each)",
+        }
+
+
 class _TwoWayTransition:
     """S->B then B->S routing step with the bench's op/layer interface."""
 
@@ -440,7 +535,7 @@ class _TwoWayTransition:
         return [d1.delta_state, d1.delta_val, d2.delta_state, d2.delta_val]
 
 
-WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3(), DenseC4())}
+WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3(), DenseC4(), TransitionDenseC3())}
 
 COPY_BYTES = 1 << 30
 

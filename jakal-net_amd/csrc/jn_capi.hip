@@ -107,7 +107,7 @@ struct PropBwdScratch {
   float* rowsum;
   int32_t* tile_base;
   int32_t* seg_start;
-  int32_t* edges;
+  float4* rec;
   float* part_c;
   float* stage;
   float* splitk;
@@ -125,7 +125,7 @@ PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int
   s.rowsum = ws.take<float>(M);
   s.tile_base = ws.take<int32_t>(B * T * N);
   s.seg_start = ws.take<int32_t>(B * (N + 1));
-  s.edges = ws.take<int32_t>(M * k);
+  s.rec = ws.take<float4>(M * k);
   s.part_c = ws.take<float>((size_t)cols_backward_waves(M, kColsPerWave) * r);
   s.stage = ws.take<float>(finalize_stage_floats((int)r));
   s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)(2 * r), (int)Din, (int)M) / sizeof(float));
@@ -137,7 +137,7 @@ struct TransitionScratch {
   float* coef;
   int32_t* tile_base;
   int32_t* seg_start;
-  int32_t* edges;
+  float4* rec;
   float* dPs;
   float* dPt;
   float* g_logit;
@@ -158,7 +158,7 @@ TransitionScratch carve_transition(void* base, size_t size, int64_t B, int64_t N
   s.coef = ws.take<float>(B * Ns * k);
   s.tile_base = ws.take<int32_t>(B * T * Nd);
   s.seg_start = ws.take<int32_t>(B * (Nd + 1));
-  s.edges = ws.take<int32_t>(B * Ns * k);
+  s.rec = ws.take<float4>(B * Ns * k);
   s.dPs = ws.take<float>(B * Ns * r);
   s.dPt = ws.take<float>(B * Nd * r);
   s.g_logit = ws.take<float>(B * Ns * k);
@@ -335,7 +335,10 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   ca.Nk = N;
   ca.tile_base = s.tile_base;
   ca.seg_start = s.seg_start;
-  ca.edges = s.edges;
+  ca.rec = s.rec;
+  ca.coef = s.coef;
+  ca.g_score = s.g_score;
+  ca.gds = grad_delta_state;
   rc = launch_csr(ca, st);
   if (rc) return rc;
 
@@ -343,11 +346,8 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
   ColsBwdArgs cb{};
   cb.seg_start = s.seg_start;
-  cb.edges = s.edges;
+  cb.rec = s.rec;
   cb.k = k;
-  cb.coef = s.coef;
-  cb.g_score = s.g_score;
-  cb.gds = grad_delta_state;
   cb.gdv = grad_delta_val;
   cb.q = projections;
   cb.ldq = 2 * r;
@@ -733,15 +733,15 @@ int jn_transition_topk_forward(const float* sender_strength, const float* src_va
   ca.Nk = Nd;
   ca.tile_base = s.tile_base;
   ca.seg_start = s.seg_start;
-  ca.edges = s.edges;
+  ca.rec = s.rec;
+  ca.coef = s.coef;
+  ca.gds = projected_state;
   rc = launch_csr(ca, st);
   if (rc) return rc;
   ColsBwdArgs cb{};
   cb.seg_start = s.seg_start;
-  cb.edges = s.edges;
+  cb.rec = s.rec;
   cb.k = (int)k;
-  cb.coef = s.coef;
-  cb.gds = projected_state;
   cb.gdv = projected_val;
   cb.B = B;
   cb.Nq = Ns;
@@ -823,14 +823,14 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
   ca.Nk = Nd;
   ca.tile_base = s.tile_base;
   ca.seg_start = s.seg_start;
-  ca.edges = s.edges;
+  ca.rec = s.rec;
+  ca.g_score = s.g_logit;
   rc = launch_csr(ca, st);
   if (rc) return rc;
   ColsBwdArgs cb{};
   cb.seg_start = s.seg_start;
-  cb.edges = s.edges;
+  cb.rec = s.rec;
   cb.k = (int)k;
-  cb.g_score = s.g_logit;
   cb.q = src_proj;
   cb.ldq = r;
   cb.key = dst_proj;

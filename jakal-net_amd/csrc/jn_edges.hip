@@ -147,9 +147,67 @@ int launch_rows_forward(const RowsFwdArgs& args, hipStream_t stream) {
 // edges 4i + g): a group reads a whole value row with 16-byte loads, so each
 // edge's dot product is reduced inside the group by DPP (4 VALU ops) and the
 // key rows of the dQ sum are read 4 edges per instruction.
+//
+// When a batch element's value rows outgrow an XCD's L2, the dot products run
+// first, in two column slabs (rows_backward_dots_kernel: slab 0 into g_score,
+// slab 1 into coef), and this kernel (SPLIT) reads their sum back in place.
 // ---------------------------------------------------------------------------
 
-template <int W, int NV, int KP>
+// Partial dot products <gdv[i], pv[j]> of every edge over one slab of the D
+// columns: slab s of the grid writes into g_score (s = 0) or coef (s = 1).  The
+// grid is slab-major, so an XCD gathers value rows of one slab of one batch
+// element at a time (Nk x slab floats, sized to its L2).
+template <int NV, int KP>
+__global__ __launch_bounds__(256) void rows_backward_dots_kernel(RowsBwdArgs a, int slab) {
+  constexpr int NI = KP / 4;
+  const int lane = lane_id();
+  const int g = lane >> 4, c = lane & 15;
+  const int64_t row_blocks = (a.rows + 3) / 4;
+  const int64_t logical = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int s = (int)(logical / row_blocks);
+  const int64_t row = (logical % row_blocks) * 4 + wave_id();
+  if (row >= a.rows) return;
+  const int d_begin = s * slab, d_end = min(a.D, d_begin + slab);
+  float* part = (s == 0) ? a.g_score : a.coef;
+  const int64_t b = row / a.Nq;
+  const auto rs_pv = make_rsrc(a.pv + b * a.Nk * a.ld_pv, (uint32_t)(a.Nk * a.ld_pv * 4));
+  const auto rs_g = make_rsrc(a.gdv + row * a.D, (uint32_t)(a.D * 4));
+  uint32_t loff[NV];  // byte offsets of this lane's columns; past the slab -> out of range (zeros)
+  float4 gv[NV];
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    const int off = d_begin + (16 * t + c) * 4;
+    loff[t] = off < d_end ? (uint32_t)off * 4u : kOobOffset;
+    gv[t] = buf_load4(rs_g, loff[t]);
+  }
+  for (int e0 = 0; e0 < a.k; e0 += KP) {
+    const int e = e0 + lane;
+    const int j = (lane < KP && e < a.k) ? a.idx[row * a.k + e] : -1;
+    const int ne = min(KP, a.k - e0);
+    int jg[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) jg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, j);
+    float sel = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ld_pv * 4u : kOobOffset;
+      float4 v[NV];
+#pragma unroll
+      for (int t = 0; t < NV; ++t)
+        v[t] = buf_load4(rs_pv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
+      float pdot = 0.f;
+#pragma unroll
+      for (int t = 0; t < NV; ++t) pdot += dot4(gv[t], v[t]);
+      const float tot = row16_sum(pdot);
+      sel = (c == i) ? tot : sel;
+      if (((i + 1) * NV) % 16 == 0) __builtin_amdgcn_sched_barrier(0);
+    }
+    const float dot = __int_as_float(__builtin_amdgcn_ds_bpermute(edge_owner_lane(lane) << 2, __float_as_int(sel)));
+    if (lane < ne) part[row * a.k + e] = dot;
+  }
+}
+
+template <int W, int NV, int KP, bool SPLIT>
 __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
   constexpr int NI = KP / 4;      // iterations per block of KP edges
   constexpr int P = 16 * W * NV;  // D floats per pass of a 16-lane group
@@ -161,9 +219,7 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
   const float* psb = a.ps + b * a.Nk;
   const float gs_row = a.gds[row];
   // 32-bit offsets into buffers of this batch element (sizes checked on the host)
-  const auto rs_pv = make_rsrc(a.pv + b * a.Nk * a.ld_pv, (uint32_t)(a.Nk * a.ld_pv * 4));
   const auto rs_key = make_rsrc(a.key + b * a.Nk * a.ldk, (uint32_t)(a.Nk * a.ldk * 4));
-  const auto rs_g = make_rsrc(a.gdv + row * a.D, (uint32_t)(a.D * 4));
   // key rows as float4 when 16-byte aligned (rank slots 4c and 64 + 4c)
   const bool kvec = (a.r % 4 == 0) && (a.ldk % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.key) & 15) == 0);
 
@@ -184,43 +240,51 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) jg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, j);
 
-    float dots[NI];
+    float dot = 0.f;
+    if constexpr (SPLIT) {
+      // slab partials of this lane's edge, summed in slab order
+      if (lane < ne) dot = a.g_score[row * a.k + e0 + lane] + a.coef[row * a.k + e0 + lane];
+    } else {
+      const auto rs_pv = make_rsrc(a.pv + b * a.Nk * a.ld_pv, (uint32_t)(a.Nk * a.ld_pv * 4));
+      const auto rs_g = make_rsrc(a.gdv + row * a.D, (uint32_t)(a.D * 4));
+      float dots[NI];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) dots[i] = 0.f;
-    for (int d0 = 0; d0 < a.D; d0 += P) {
-      // byte offsets of this lane's slice of the pass; past D -> out of range (zeros)
-      uint32_t loff[NV];
-      float4 gv[NV];
+      for (int i = 0; i < NI; ++i) dots[i] = 0.f;
+      for (int d0 = 0; d0 < a.D; d0 += P) {
+        // byte offsets of this lane's slice of the pass; past D -> out of range (zeros)
+        uint32_t loff[NV];
+        float4 gv[NV];
 #pragma unroll
-      for (int t = 0; t < NV; ++t) {
-        const int off = d0 + (16 * t + c) * W;
-        loff[t] = off < a.D ? (uint32_t)off * 4u : kOobOffset;
-        gv[t] = buf_load_w<W>(rs_g, loff[t]);
+        for (int t = 0; t < NV; ++t) {
+          const int off = d0 + (16 * t + c) * W;
+          loff[t] = off < a.D ? (uint32_t)off * 4u : kOobOffset;
+          gv[t] = buf_load_w<W>(rs_g, loff[t]);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          // absent edges, iterations past the block's last edge and lanes past D
+          // read out of range: zeros and no memory traffic, without a branch
+          const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ld_pv * 4u : kOobOffset;
+          float4 v[NV];
+#pragma unroll
+          for (int t = 0; t < NV; ++t)
+            v[t] = buf_load_w<W>(rs_pv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
+          float pdot = 0.f;
+#pragma unroll
+          for (int t = 0; t < NV; ++t) pdot += dot4(gv[t], v[t]);
+          dots[i] += jg[i] >= 0 ? pdot : 0.f;
+          // at most 16 row loads in flight per lane: keeps VGPRs (and occupancy) in check
+          if (((i + 1) * NV) % 16 == 0) __builtin_amdgcn_sched_barrier(0);
+        }
       }
+      float sel = 0.f;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        // absent edges, iterations past the block's last edge and lanes past D
-        // read out of range: zeros and no memory traffic, without a branch
-        const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ld_pv * 4u : kOobOffset;
-        float4 v[NV];
-#pragma unroll
-        for (int t = 0; t < NV; ++t)
-          v[t] = buf_load_w<W>(rs_pv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
-        float pdot = 0.f;
-#pragma unroll
-        for (int t = 0; t < NV; ++t) pdot += dot4(gv[t], v[t]);
-        dots[i] += jg[i] >= 0 ? pdot : 0.f;
-        // at most 16 row loads in flight per lane: keeps VGPRs (and occupancy) in check
-        if (((i + 1) * NV) % 16 == 0) __builtin_amdgcn_sched_barrier(0);
+        const float tot = row16_sum(dots[i]);
+        sel = (c == i) ? tot : sel;
       }
+      dot = __int_as_float(__builtin_amdgcn_ds_bpermute(edge_owner_lane(lane) << 2, __float_as_int(sel)));
     }
-    float sel = 0.f;
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const float tot = row16_sum(dots[i]);
-      sel = (c == i) ? tot : sel;
-    }
-    const float dot = __int_as_float(__builtin_amdgcn_ds_bpermute(edge_owner_lane(lane) << 2, __float_as_int(sel)));
     const float gc = (j >= 0) ? gs_row * psb[j] + dot : 0.f;
     float gsc = 0.f;
     if (a.compress == 1) {
@@ -294,12 +358,28 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
   if (lane == 0) a.rowsum_gs[row] = gsum;
 }
 
-template <int W, int NV>
+template <int W, int NV, bool SPLIT = false>
 static void launch_rows_bwd_kp(const RowsBwdArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 8>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 16) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 16>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 32) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 32>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((rows_backward_kernel<W, NV, 64>), grid, dim3(256), 0, stream, a);
+  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 8, SPLIT>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 16) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 16, SPLIT>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 32) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 32, SPLIT>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((rows_backward_kernel<W, NV, 64, SPLIT>), grid, dim3(256), 0, stream, a);
+}
+
+template <int NV>
+static void launch_rows_bwd_dots(const RowsBwdArgs& a, dim3 grid, int slab, hipStream_t stream) {
+  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_dots_kernel<NV, 8>), grid, dim3(256), 0, stream, a, slab);
+  else if (a.k <= 16) hipLaunchKernelGGL((rows_backward_dots_kernel<NV, 16>), grid, dim3(256), 0, stream, a, slab);
+  else if (a.k <= 32) hipLaunchKernelGGL((rows_backward_dots_kernel<NV, 32>), grid, dim3(256), 0, stream, a, slab);
+  else hipLaunchKernelGGL((rows_backward_dots_kernel<NV, 64>), grid, dim3(256), 0, stream, a, slab);
+}
+
+// Column slab of the split row backward (0: no split).  Two slabs of 256 or
+// 512 columns when a batch element's value rows exceed 2 MiB (an XCD's L2 is
+// 4 MiB) and 256 < D <= 1024.
+int rows_backward_slab(int64_t Nk, int D, bool vec) {
+  if (!vec || D <= 256 || D > 1024 || Nk * (int64_t)D * 4 <= (2LL << 20)) return 0;
+  return D <= 512 ? 256 : 512;
 }
 
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
@@ -307,13 +387,26 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
   JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
   JN_REQUIRE(a.compress == 0 || a.k <= 64, kUnsupported, "signed_abs_softmax backward supports k <= 64");
   const int64_t blocks = (a.rows + 3) / 4;
-  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
+  JN_REQUIRE(2 * blocks < (1LL << 31), kInvalidArgument, "too many rows");
   JN_REQUIRE((int64_t)a.Nk * a.ld_pv * 4 < (1LL << 31) && (int64_t)a.Nk * a.ldk * 4 < (1LL << 31) &&
                  (int64_t)a.D * 4 < (1LL << 31),
              kUnsupported, "one batch element of the value or key rows must stay below 2 GiB");
   const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0);
   dim3 grid((unsigned)blocks);
+  const int slab = rows_backward_slab(a.Nk, a.D, vec);
+  if (slab) {
+    {
+      JN_PROFILE("rows_backward_dots_kernel", stream);
+      if (slab == 256) launch_rows_bwd_dots<4>(a, dim3((unsigned)(2 * blocks)), slab, stream);
+      else launch_rows_bwd_dots<8>(a, dim3((unsigned)(2 * blocks)), slab, stream);
+      JN_LAUNCH_CHECK();
+    }
+    JN_PROFILE("rows_backward_kernel", stream);
+    launch_rows_bwd_kp<4, 1, true>(a, grid, stream);
+    JN_LAUNCH_CHECK();
+    return kOk;
+  }
   JN_PROFILE("rows_backward_kernel", stream);
   if (!vec) launch_rows_bwd_kp<1, 4>(a, grid, stream);
   else if (a.D > 256) launch_rows_bwd_kp<4, 8>(a, grid, stream);
@@ -331,7 +424,9 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
 // form a 64-bit mask in LDS.  The position of edge (row, j) in j's segment is
 //   seg_start[j] + rows of earlier tiles hitting j + popcount(mask_j below row).
 // Segments therefore list incoming edges in increasing row order and every
-// reduction over them is run-to-run reproducible.
+// reduction over them is run-to-run reproducible.  Each slot receives the
+// edge's record (row, coef, g_s, coef * gds[row]), so the column pass reads
+// one contiguous 16-byte entry per incoming edge instead of chasing edge ids.
 // ---------------------------------------------------------------------------
 constexpr int kCsrSlice = 8192;  // key columns per LDS pass (64 KiB of masks)
 
@@ -427,19 +522,15 @@ __global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs a) {
       if (j >= s0 && j < s1) {
         unsigned long long below = masks[j - s0] & ((1ull << rl) - 1ull);
         int pos = seg[j] + a.tile_base[((int64_t)b * T + t) * a.Nk + j] + __popcll(below);
-        a.edges[batch_base + pos] = (int32_t)eid;
+        const int row = b * a.Nq + r0 + rl;
+        const float cf = a.coef ? a.coef[eid] : 0.f;
+        const float gs = a.g_score ? a.g_score[eid] : 0.f;
+        const float cd = a.gds ? cf * a.gds[row] : 0.f;
+        a.rec[batch_base + pos] = make_float4(__int_as_float(row), cf, gs, cd);
       }
     }
     __syncthreads();
   }
-}
-
-size_t csr_workspace_ints(int B, int Nq, int Nk, int k, size_t& tile_ints, size_t& seg_ints, size_t& edge_ints) {
-  const int T = (Nq + kCsrTile - 1) / kCsrTile;
-  tile_ints = (size_t)B * T * Nk;
-  seg_ints = (size_t)B * (Nk + 1);
-  edge_ints = (size_t)B * Nq * k;
-  return tile_ints + seg_ints + edge_ints;
 }
 
 int launch_csr(const CsrArgs& a, hipStream_t stream) {
@@ -477,8 +568,8 @@ int launch_csr(const CsrArgs& a, hipStream_t stream) {
 //   dK[j, r]    = kscale[r] * sum_in g_s * q[i, r]
 //   part_c[w,r] += key[j, r] * sum_in g_s * q[i, r]      (scale-vector gradient)
 // A wavefront owns a fixed run of up to 64 columns and reads their segments as
-// one stream of incoming edges: the metadata (edge id -> row, coef, g_s) of 64
-// stream entries is fetched with one load per lane, then the gathers run over
+// one stream of incoming edges: the records (row, coef, g_s, coef * gds) of 64
+// stream entries are fetched with one 16-byte load per lane, then the gathers run over
 // the stream in groups of 8 edges and a column's sums are stored when the
 // stream passes its end.  The order of every sum is fixed, so the results are
 // run-to-run reproducible.
@@ -576,15 +667,13 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
       for (int cc = 0; cc < ncols; ++cc) ci += (readlane_i(incl, cc) <= q) ? 1 : 0;
       const int pos = __builtin_amdgcn_ds_bpermute(min(ci, kWave - 1) << 2, offc) + q;
       int rowq = 0;
-      float cf = 0.f, gsv = 0.f, gdsv = 0.f;
+      float cf = 0.f, gsv = 0.f, gdsv = 0.f;  // gdsv: coef * gds[row]
       if (lane < n) {
-        const int eid = a.edges[pos];
-        if (a.coef) cf = a.coef[eid];
-        rowq = eid / a.k;
-        if (first) {
-          if (a.g_score) gsv = a.g_score[eid];
-          if (a.gds) gdsv = a.gds[rowq];
-        }
+        const float4 rc = a.rec[pos];
+        rowq = __float_as_int(rc.x);
+        cf = rc.y;
+        gsv = rc.z;
+        gdsv = rc.w;
       }
       for (int u0 = 0; u0 < n; u0 += G) {
         int rw[G], cis[G];
@@ -632,7 +721,7 @@ __global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
               dk0 += gg[u] * qa[u];
               dk1 += gg[u] * qb[u];
             }
-            st += cu[u] * gd[u];
+            st += gd[u];
           }
         }
       }
@@ -653,7 +742,7 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   const int64_t total_cols = (int64_t)a.B * a.Nk;
   if (total_cols == 0) return kOk;
   JN_REQUIRE(!a.q || (a.r >= 1 && a.r <= 128), kUnsupported, "rank must be in [1, 128]");
-  JN_REQUIRE(!a.q || (a.key && a.dk && a.g_score), kInvalidArgument, "key-side gradient needs key, dk and g_score");
+  JN_REQUIRE(!a.q || (a.key && a.dk), kInvalidArgument, "key-side gradient needs key and dk");
   JN_REQUIRE(a.cols_per_wave >= 1 && a.cols_per_wave <= kWave, kInvalidArgument, "columns per wave must be in [1, 64]");
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
   JN_REQUIRE((int64_t)a.D * 4 < (1LL << 31), kUnsupported, "value rows must stay below 2 GiB");

@@ -171,18 +171,20 @@ struct CsrArgs {
   int B, Nq, Nk;
   int32_t* tile_base;  // [B, T, Nk]: per-tile counts, then exclusive bases
   int32_t* seg_start;  // [B, Nk + 1]
-  int32_t* edges;      // [B * Nq * k] edge ids (row * k + e), grouped by key
+  // [B * Nq * k] edge records grouped by key: {row (int bits), coef[e],
+  // g_score[e], coef[e] * gds[row]}; a null source pointer gives 0
+  float4* rec;
+  const float* coef;     // [B * Nq, k] or null
+  const float* g_score;  // [B * Nq, k] or null
+  const float* gds;      // [B * Nq] or null
 };
 constexpr int kCsrTile = 64;
 int launch_csr(const CsrArgs& a, hipStream_t stream);
 
 struct ColsBwdArgs {
   const int32_t* seg_start;  // [B, Nk + 1]
-  const int32_t* edges;      // grouped by key, batch b at offset b*Nq*k
+  const float4* rec;         // edge records grouped by key (CsrArgs), batch b at offset b*Nq*k
   int k;
-  const float* coef;         // [rows, k]
-  const float* g_score;      // [rows, k]
-  const float* gds;          // [rows] (null: skip state)
   const float* gdv;          // [rows, D]
   const float* q;            // query projection rows (global row index), stride ldq
   int64_t ldq;

@@ -50,23 +50,39 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 CONFIG = {"batch": 16, "nodes": 4096, "dim": 512, "rank": 64, "topk": 32}
 
 
-def edge_kernel_model(name: str, M: int, E: int, D: int, r: int) -> tuple[str, float] | None:
+def rows_backward_split(nk: int, D: int) -> bool:
+    """Whether the library runs the row backward's dot products as two column
+    slabs first (rows_backward_dots_kernel): value rows of a batch element above
+    2 MiB with 256 < D <= 1024 (jn_edges.hip, rows_backward_slab)."""
+    return 256 < D <= 1024 and nk * D * 4 > (2 << 20)
+
+
+def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = False) -> tuple[str, float] | None:
     """(bound, algorithmic bytes or flops per launch) of the edge-list kernels.
 
     M = aggregated rows, E = routed pairs.  Bytes count every operand once per
     use (no cache reuse credited): an edge gathers one D-row of fp32 values,
-    its index and score."""
+    its index and score.  split: the row backward runs as dots + finish."""
     if name.startswith("rows_forward_kernel"):
         # idx+score+ps per edge, pv row per edge; delta_val row + delta_state per row
         return "hbm", E * (12.0 + 4.0 * D) + M * (4.0 * D + 4.0)
+    if name.startswith("rows_backward_dots_kernel"):
+        # idx, pv row, partial-dot write per edge; grad-delta row per row
+        return "hbm", E * (4.0 + 4.0 * D + 4.0) + M * 4.0 * D
     if name.startswith("rows_backward_kernel"):
+        if split:
+            # idx+score, two partial dots, ps, key row, gsc+coef writes per edge;
+            # grad-delta state, dq row, row sum per row
+            return "hbm", E * (8.0 + 8.0 + 4.0 + 4.0 * r + 8.0) + M * (4.0 + 4.0 * r + 4.0)
         # idx+score, ps, pv row, key row per edge; gsc+coef writes per edge;
         # grad-delta row + state, dq row, row sum per row
         return "hbm", E * (8.0 + 4.0 + 4.0 * D + 4.0 * r + 8.0) + M * (4.0 * D + 4.0 + 4.0 * r + 4.0)
-    if name.startswith("cols_backward_kernel"):
-        # edge id, coef+gsc, grad-delta row + state, query row per edge;
-        # segment bounds, grad_pv row, grad_ps, dk row, key row per column
-        return "hbm", E * (4.0 + 8.0 + 4.0 * D + 4.0 + 4.0 * r) + M * (8.0 + 4.0 * D + 4.0 + 8.0 * r)
+    if name.startswith("cols_gather_kernel"):
+        # edge record, grad-delta row per edge; segment bounds, grad_pv row, grad_ps per column
+        return "hbm", E * (16.0 + 4.0 * D) + M * (8.0 + 4.0 * D + 4.0)
+    if name.startswith("cols_keygrad_kernel"):
+        # edge record, query row per edge; segment bounds, dk row, key row per column
+        return "hbm", E * (16.0 + 4.0 * r) + M * (8.0 + 8.0 * r)
     if name.startswith("window_scores_kernel"):
         # query row per row; key row per edge; idx + score written per edge
         return "hbm", E * (4.0 * r + 8.0) + M * 4.0 * r
@@ -79,7 +95,7 @@ def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int) -> tuple[str
     """Kernel model of the headline (top-k) workload."""
     if name.startswith("lowrank_topk_select_kernel"):
         return "mfma", 2.0 * B * N * N * r
-    return edge_kernel_model(name, B * N, B * N * k, D, r)
+    return edge_kernel_model(name, B * N, B * N * k, D, r, rows_backward_split(N, D))
 
 
 def _threads() -> int | None:
@@ -186,7 +202,8 @@ class WindowC2:
 
     def model(self, name):
         c = self.config
-        return edge_kernel_model(name, c["batch"] * c["nodes"], self.edges(), c["dim"], c["rank"])
+        return edge_kernel_model(name, c["batch"] * c["nodes"], self.edges(), c["dim"], c["rank"],
+                                 rows_backward_split(c["nodes"], c["dim"]))
 
     def sparse_bytes(self) -> float:
         # contiguous bands: compulsory dense bytes (read val, write delta; bwd read grad, read val, write grad)
@@ -263,8 +280,8 @@ class TransitionC3:
             # per source row: its value row, its grad-value write, dq write
             return "hbm", E * (8.0 + 4.0 * D + 4.0 * r + 4.0) + rows * (8.0 * D + 4.0 * r + 16.0) / 2
         if name.startswith("route_gather_kernel"):
-            # per edge: edge id + coef + source value row; per destination: delta row write
-            return "hbm", (E * (8.0 + 4.0 * D) + rows * (4.0 * D + 12.0)) / 2
+            # per edge: edge record + source value row; per destination: delta row write
+            return "hbm", (E * (16.0 + 4.0 * D) + rows * (4.0 * D + 12.0)) / 2
         if name.startswith("gemm_f32_kernel"):
             return "mfma", 2.0 * rows * D * r / 2
         return None

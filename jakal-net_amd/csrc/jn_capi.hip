@@ -67,8 +67,6 @@ ProfileScope::~ProfileScope() {
 
 namespace {
 
-constexpr int kColsPerWave = 1;
-
 bool fits_int(int64_t v) { return v >= 0 && v < (1LL << 31); }
 
 // Shapes shared by every propagation entry point; `edges` = edge slots per row.
@@ -126,7 +124,7 @@ PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int
   s.tile_base = ws.take<int32_t>(B * T * N);
   s.seg_start = ws.take<int32_t>(B * (N + 1));
   s.rec = ws.take<float4>(M * k);
-  s.part_c = ws.take<float>((size_t)cols_backward_waves(M, kColsPerWave) * r);
+  s.part_c = ws.take<float>((size_t)cols_backward_parts(M) * r);
   s.stage = ws.take<float>(finalize_stage_floats((int)r));
   s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)(2 * r), (int)Din, (int)M) / sizeof(float));
   s.bytes = ws.used;
@@ -163,7 +161,7 @@ TransitionScratch carve_transition(void* base, size_t size, int64_t B, int64_t N
   s.dPt = ws.take<float>(B * Nd * r);
   s.g_logit = ws.take<float>(B * Ns * k);
   s.rowsum = ws.take<float>(B * Ns);
-  s.part_c = ws.take<float>((size_t)cols_backward_waves(B * Nd, kColsPerWave) * r);
+  s.part_c = ws.take<float>((size_t)cols_backward_parts(B * Nd) * r);
   s.stage = ws.take<float>(finalize_stage_floats((int)r));
   const size_t sk = std::max(gemm_grad_weight_workspace((int)r, (int)Dsrc, (int)(B * Ns)),
                              gemm_grad_weight_workspace((int)r, (int)Ddst, (int)(B * Nd)));
@@ -359,10 +357,8 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   cb.Nq = N;
   cb.Nk = N;
   cb.D = (int)out_dim;
-  cb.cols_per_wave = kColsPerWave;
   cb.grad_pv = gpv;
   cb.ld_gpv = out_dim;
-  cb.accumulate_gpv = 0;
   cb.grad_ps = grad_projected_state;
   cb.dk = s.dP + r;
   cb.lddk = 2 * r;
@@ -386,7 +382,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   }
 
   // 6. w_hat and bias grads
-  const int nparts = cols_backward_waves(M, kColsPerWave);
+  const int nparts = cols_backward_parts(M);
   return launch_finalize_small_grads(s.part_c, nparts, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st);
 }
 
@@ -747,7 +743,6 @@ int jn_transition_topk_forward(const float* sender_strength, const float* src_va
   cb.Nq = Ns;
   cb.Nk = Nd;
   cb.D = (int)val_dim;
-  cb.cols_per_wave = kColsPerWave;
   cb.grad_pv = delta_val;
   cb.ld_gpv = val_dim;
   cb.grad_ps = delta_state;
@@ -841,7 +836,6 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
   cb.Nq = Ns;
   cb.Nk = Nd;
   cb.D = (int)val_dim;
-  cb.cols_per_wave = kColsPerWave;
   cb.dk = s.dPt;
   cb.lddk = r;
   cb.part_c = s.part_c;
@@ -871,7 +865,7 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
   }
 
   // 4. core weight and bias grads
-  return launch_finalize_small_grads(s.part_c, cols_backward_waves((int64_t)B * Nd, kColsPerWave), r,
+  return launch_finalize_small_grads(s.part_c, cols_backward_parts((int64_t)B * Nd), r,
                                      grad_core_weight, 0, s.rowsum, batch * src_nodes, grad_bias, s.stage, st);
 }
 

@@ -562,205 +562,200 @@ int launch_csr(const CsrArgs& a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Column backward: key columns j, walking their CSR segments.
-//   grad_pv[j]  = sum_in coef * gdv[i]
+// Column backward: key columns j, walking their CSR segments (edge records in
+// increasing row order, so every sum below has a fixed order and the results
+// are run-to-run reproducible).
+//   grad_pv[j]  = sum_in coef * gdv[i]                   (cols_gather_kernel)
 //   grad_ps[j]  = sum_in coef * gds[i]
-//   dK[j, r]    = kscale[r] * sum_in g_s * q[i, r]
-//   part_c[w,r] += key[j, r] * sum_in g_s * q[i, r]      (scale-vector gradient)
-// A wavefront owns a fixed run of up to 64 columns and reads their segments as
-// one stream of incoming edges: the records (row, coef, g_s, coef * gds) of 64
-// stream entries are fetched with one 16-byte load per lane, then the gathers run over
-// the stream in groups of 8 edges and a column's sums are stored when the
-// stream passes its end.  The order of every sum is fixed, so the results are
-// run-to-run reproducible.
+//   dK[j, r]    = kscale[r] * sum_in g_s * q[i, r]       (cols_keygrad_kernel)
+//   part_c[w,r] = sum over the 16 columns of workgroup w of key[j, r] * sum_in g_s * q[i, r]
 // ---------------------------------------------------------------------------
 
-template <int W, int NV>
-__global__ __launch_bounds__(256) void cols_backward_kernel(ColsBwdArgs a) {
-  constexpr int P = kWave * W * NV;  // D floats per pass
-  constexpr int G = 8;               // edges per gather group
+// One wavefront per column and column slab: the gather-accumulate of
+// rows_forward_kernel over the column's records.  The grid is slab-major, so an
+// XCD gathers rows of one slab of one batch element at a time (Nq x slab floats,
+// sized to its L2).  Slab 0 also sums the state.
+template <int W>
+__global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int slab_cols) {
   const int lane = lane_id();
   const int64_t total_cols = (int64_t)a.B * a.Nk;
-  const int64_t nwaves = (total_cols + a.cols_per_wave - 1) / a.cols_per_wave;
-  // slab-major grid: workgroup (slab, w) handles columns [d0, d0 + P) of its
-  // waves' value rows; slab 0 also accumulates the state and key gradients
-  const int64_t wave_blocks = (nwaves + 3) / 4;
+  const int64_t col_blocks = (total_cols + 3) / 4;
   const int64_t logical = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int pass = (int)(logical / wave_blocks);
-  const int64_t gw = (logical % wave_blocks) * 4 + wave_id();
-  if (gw >= nwaves) return;  // padding waves of the last workgroup own no partial slot
-  const int64_t c_begin = gw * a.cols_per_wave;
-  const int ncols = (int)min((int64_t)a.cols_per_wave, total_cols - c_begin);  // <= 64
+  const int slab = (int)(logical / col_blocks);
+  const int64_t col = (logical % col_blocks) * 4 + wave_id();
+  if (col >= total_cols) return;
+  const int b = (int)(col / a.Nk), j = (int)(col % a.Nk);
+  const int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
+  const int beg = seg[j], len = seg[j + 1] - beg;
+  const float4* rec = a.rec + (int64_t)b * a.Nq * a.k + beg;
+  const int d_begin = slab * slab_cols, d_end = min(a.D, d_begin + slab_cols);
+  float* out = a.grad_pv ? a.grad_pv + col * a.ld_gpv : nullptr;
 
-  // lane l < ncols describes column c_begin + l: its edges are stream entries
-  // [excl, incl) and stream entry q of it sits at edges[offc + q]
-  int len = 0, offc = 0;
-  if (lane < ncols) {
-    const int64_t colg = c_begin + lane;
-    const int b = (int)(colg / a.Nk), j = (int)(colg % a.Nk);
+  float st = 0.0f;
+  const int nblk = max(1, (len + kWave - 1) / kWave);  // a column without edges still writes zeros
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int q0 = blk * kWave;
+    const int n = min(kWave, len - q0);
+    int row = 0;
+    float cf = 0.f, cd = 0.f;
+    if (lane < n) {
+      const float4 r = rec[q0 + lane];
+      row = __float_as_int(r.x);
+      cf = r.y;
+      cd = r.w;
+    }
+    st += cd;  // lanes past the segment hold 0
+    if (!out) continue;
+    for (int d = d_begin + lane * W; d < d_end; d += kWave * W) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      int q = 0;
+      for (; q + 8 <= n; q += 8) {
+        float4 v[8];
+        float cc[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          cc[u] = readlane_f(cf, q + u);
+          v[u] = load_w<W>(a.gdv + (int64_t)readlane_i(row, q + u) * a.D + d);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) fma4(acc, cc[u], v[u]);
+      }
+      for (; q < n; ++q) fma4(acc, readlane_f(cf, q), load_w<W>(a.gdv + (int64_t)readlane_i(row, q) * a.D + d));
+      if (blk > 0) acc = add4(acc, load_w<W>(out + d));
+      store_w<W>(out + d, acc);
+    }
+  }
+  if (slab == 0 && a.grad_ps) {
+    st = wave_sum(st);
+    if (lane == 0) a.grad_ps[col] = st;
+  }
+}
+
+// One 16-lane group per column (16 columns per workgroup).  Lane c of a group
+// holds 8 rank slots: ranks 4c..4c+3 and 64+4c..64+4c+3 when the query rows are
+// read as float4 (VEC), else ranks c + 16m.  The group walks its column's
+// records 16 at a time; each lane loads one record and the group's lanes take
+// turns broadcasting theirs (ds_bpermute), so the 4 columns of a wave advance
+// together.  The scale-vector partials of the 16 columns are summed in a fixed
+// order into one row of part_c per workgroup.
+template <bool VEC>
+__global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
+  __shared__ float red[4][128];
+  const int lane = lane_id(), g = lane >> 4, c = lane & 15, w = wave_id();
+  const int64_t total_cols = (int64_t)a.B * a.Nk;
+  const int64_t blk = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int64_t col = blk * 16 + w * 4 + g;
+  const bool valid = col < total_cols;
+  int len = 0;
+  const float4* rec = a.rec;
+  if (valid) {
+    const int b = (int)(col / a.Nk), j = (int)(col % a.Nk);
     const int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
     const int beg = seg[j];
     len = seg[j + 1] - beg;
-    offc = b * a.Nq * a.k + beg;  // < 2^31 (checked at CSR build)
+    rec = a.rec + (int64_t)b * a.Nq * a.k + beg;
   }
-  int incl = len;
+  int rk[8];  // rank of each slot
 #pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int y = __builtin_amdgcn_ds_bpermute(((lane - o) & (kWave - 1)) << 2, incl);
-    if (lane >= o) incl += y;
-  }
-  offc -= incl - len;
-  const int total = readlane_i(incl, kWave - 1);
-
-  float pc0 = 0.f, pc1 = 0.f;
-  {
-    const int d0 = pass * P;
-    const bool first = (pass == 0);
-    float4 acc[NV];
-#pragma unroll
-    for (int t = 0; t < NV; ++t) acc[t] = make_float4(0.f, 0.f, 0.f, 0.f);
-    float dk0 = 0.f, dk1 = 0.f, st = 0.f;
-    int cur = 0;  // column being accumulated (wave-uniform)
-    uint32_t loff[NV];  // byte offsets of this lane's slice of the pass (past D: out of range)
-#pragma unroll
-    for (int t = 0; t < NV; ++t) {
-      const int off = d0 + (kWave * t + lane) * W;
-      loff[t] = off < a.D ? (uint32_t)off * 4u : kOobOffset;
+  for (int m = 0; m < 8; ++m) rk[m] = VEC ? (m < 4 ? 4 * c + m : 64 + 4 * c + (m - 4)) : c + 16 * m;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // wave-uniform trip count: the longest of the wave's four columns
+  const int wlen = max(max(readlane_i(len, 0), readlane_i(len, 16)), max(readlane_i(len, 32), readlane_i(len, 48)));
+  for (int q0 = 0; q0 < wlen; q0 += 16) {
+    int row = -1;
+    float gs = 0.f;
+    if (q0 + c < len) {
+      const float4 r = rec[q0 + c];
+      row = __float_as_int(r.x);
+      gs = r.z;
     }
-
-    auto flush = [&](int cc) {
-      const int64_t colg = c_begin + cc;
-      if (a.grad_pv) {
-        float* out = a.grad_pv + colg * a.ld_gpv;
+    const int nu = min(16, wlen - q0);
+    for (int u0 = 0; u0 < nu; u0 += 8) {
+      float qv[8][8];
+      float gg[8];
 #pragma unroll
-        for (int t = 0; t < NV; ++t) {
-          const int off = d0 + (kWave * t + lane) * W;
-          if (off < a.D) {
-            float4 v = acc[t];
-            if (a.accumulate_gpv) v = add4(v, load_w<W>(out + off));
-            store_w<W>(out + off, v);
-          }
-          acc[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int u = 0; u < 8; ++u) {
+        const int src = (g * 16 + ((u0 + u) & 15)) << 2;
+        const int rw = __builtin_amdgcn_ds_bpermute(src, row);
+        gg[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(gs)));
+        const bool ok = (u0 + u < nu) && rw >= 0;  // past the column's end: row -1, gs 0
+        const float* qr = a.q + (int64_t)(ok ? rw : 0) * a.ldq;
+        if (VEC) {
+          const float4 lo = (ok && 4 * c < a.r) ? *reinterpret_cast<const float4*>(qr + 4 * c)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+          const float4 hi = (ok && 64 + 4 * c < a.r) ? *reinterpret_cast<const float4*>(qr + 64 + 4 * c)
+                                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+          qv[u][0] = lo.x; qv[u][1] = lo.y; qv[u][2] = lo.z; qv[u][3] = lo.w;
+          qv[u][4] = hi.x; qv[u][5] = hi.y; qv[u][6] = hi.z; qv[u][7] = hi.w;
+        } else {
+#pragma unroll
+          for (int m = 0; m < 8; ++m) qv[u][m] = (ok && rk[m] < a.r) ? qr[rk[m]] : 0.f;
         }
       }
-      if (first) {
-        if (a.grad_ps && lane == 0) a.grad_ps[colg] = st;
-        if (a.q) {
-          const float* kr = a.key + colg * a.ldk;
-          if (lane < a.r) {
-            a.dk[colg * a.lddk + lane] = dk0 * (a.kscale ? a.kscale[lane] : 1.f);
-            pc0 += kr[lane] * dk0;
-          }
-          if (lane + kWave < a.r) {
-            a.dk[colg * a.lddk + lane + kWave] = dk1 * (a.kscale ? a.kscale[lane + kWave] : 1.f);
-            pc1 += kr[lane + kWave] * dk1;
-          }
-        }
-        dk0 = dk1 = st = 0.f;
-      }
-    };
-
-    for (int q0 = 0; q0 < total; q0 += kWave) {
-      const int n = min(kWave, total - q0);
-      const int q = q0 + lane;
-      int ci = 0;
-      for (int cc = 0; cc < ncols; ++cc) ci += (readlane_i(incl, cc) <= q) ? 1 : 0;
-      const int pos = __builtin_amdgcn_ds_bpermute(min(ci, kWave - 1) << 2, offc) + q;
-      int rowq = 0;
-      float cf = 0.f, gsv = 0.f, gdsv = 0.f;  // gdsv: coef * gds[row]
-      if (lane < n) {
-        const float4 rc = a.rec[pos];
-        rowq = __float_as_int(rc.x);
-        cf = rc.y;
-        gsv = rc.z;
-        gdsv = rc.w;
-      }
-      for (int u0 = 0; u0 < n; u0 += G) {
-        int rw[G], cis[G];
-        float cu[G], gg[G], gd[G];
 #pragma unroll
-        for (int u = 0; u < G; ++u) {
-          const bool ok = u0 + u < n;  // uniform
-          const int src = ok ? u0 + u : u0;
-          rw[u] = readlane_i(rowq, src);
-          cis[u] = readlane_i(ci, src);
-          cu[u] = ok ? readlane_f(cf, src) : 0.f;
-          gg[u] = ok ? readlane_f(gsv, src) : 0.f;
-          gd[u] = ok ? readlane_f(gdsv, src) : 0.f;
-        }
-        // rows are wave-uniform: one buffer resource per gathered row, lanes
-        // past the row end read zeros
-        float4 v[G][NV];
-        if (a.grad_pv) {
+      for (int u = 0; u < 8; ++u)
 #pragma unroll
-          for (int u = 0; u < G; ++u) {
-            const auto rs = make_rsrc(a.gdv + (int64_t)rw[u] * a.D, (uint32_t)a.D * 4u);
-#pragma unroll
-            for (int t = 0; t < NV; ++t) v[u][t] = buf_load_w<W>(rs, loff[t]);
-          }
-        }
-        float qa[G], qb[G];
-        if (first && a.q) {
-#pragma unroll
-          for (int u = 0; u < G; ++u) {
-            const auto rs = make_rsrc(a.q + (int64_t)rw[u] * a.ldq, (uint32_t)a.r * 4u);
-            qa[u] = buf_load1(rs, 4u * lane);
-            qb[u] = a.r > kWave ? buf_load1(rs, 4u * (lane + kWave)) : 0.f;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < G; ++u) {
-          if (u0 + u >= n) break;  // uniform
-          while (cur < cis[u]) flush(cur++);
-          if (a.grad_pv) {
-#pragma unroll
-            for (int t = 0; t < NV; ++t) fma4(acc[t], cu[u], v[u][t]);
-          }
-          if (first) {
-            if (a.q) {
-              dk0 += gg[u] * qa[u];
-              dk1 += gg[u] * qb[u];
-            }
-            st += gd[u];
-          }
-        }
-      }
+        for (int m = 0; m < 8; ++m) acc[m] += gg[u] * qv[u][m];
     }
-    while (cur < ncols) flush(cur++);
   }
-  if (pass == 0 && a.q && a.part_c) {
-    if (lane < a.r) a.part_c[gw * a.r + lane] = pc0;
-    if (lane + kWave < a.r) a.part_c[gw * a.r + lane + kWave] = pc1;
+  float pc[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    pc[m] = 0.f;
+    if (valid && rk[m] < a.r) {
+      a.dk[col * a.lddk + rk[m]] = acc[m] * (a.kscale ? a.kscale[rk[m]] : 1.f);
+      pc[m] = a.key[col * a.ldk + rk[m]] * acc[m];
+    }
   }
+  if (!a.part_c) return;  // uniform
+  // sum the wave's four columns (groups), then the workgroup's four waves
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    pc[m] += xor16_f(pc[m]);
+    pc[m] += xor32_f(pc[m]);
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+      if (rk[m] < 128) red[w][rk[m]] = pc[m];
+  }
+  __syncthreads();
+  for (int rr = threadIdx.x; rr < a.r; rr += blockDim.x)
+    a.part_c[blk * a.r + rr] = (red[0][rr] + red[1][rr]) + (red[2][rr] + red[3][rr]);
 }
 
-int cols_backward_waves(int64_t total_cols, int cols_per_wave) {
-  return (int)((total_cols + cols_per_wave - 1) / cols_per_wave);
-}
+int cols_backward_parts(int64_t total_cols) { return (int)((total_cols + 15) / 16); }
 
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   const int64_t total_cols = (int64_t)a.B * a.Nk;
   if (total_cols == 0) return kOk;
   JN_REQUIRE(!a.q || (a.r >= 1 && a.r <= 128), kUnsupported, "rank must be in [1, 128]");
   JN_REQUIRE(!a.q || (a.key && a.dk), kInvalidArgument, "key-side gradient needs key and dk");
-  JN_REQUIRE(a.cols_per_wave >= 1 && a.cols_per_wave <= kWave, kInvalidArgument, "columns per wave must be in [1, 64]");
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
-  JN_REQUIRE((int64_t)a.D * 4 < (1LL << 31), kUnsupported, "value rows must stay below 2 GiB");
-  const int64_t waves = cols_backward_waves(total_cols, a.cols_per_wave);
-  const bool vec = (a.D % 4 == 0) && (a.ld_gpv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
-                   (a.grad_pv == nullptr || (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0);
-  // D columns per pass (grid slab): 512, two float4 per lane.  Narrower
-  // slabs would fit an XCD's L2 better but repeat the per-edge metadata work,
-  // which costs more than it saves here.
-  const int P = !vec ? kWave * 2 : 512;
-  const int64_t passes = a.grad_pv ? (a.D + P - 1) / P : 1;
-  const int64_t blocks = (waves + 3) / 4 * passes;
-  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
-  JN_PROFILE(a.profile_name ? a.profile_name : "cols_backward_kernel", stream);
-  if (!vec) hipLaunchKernelGGL((cols_backward_kernel<1, 2>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
-  else if (P == 512) hipLaunchKernelGGL((cols_backward_kernel<4, 2>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((cols_backward_kernel<4, 1>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
-  JN_LAUNCH_CHECK();
+  if (a.grad_pv || a.grad_ps) {
+    const bool vec = (a.D % 4 == 0) && (a.ld_gpv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
+                     (a.grad_pv == nullptr || (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0);
+    // slabs of 256 columns while a batch element's gathered rows exceed 2 MiB
+    int slab = a.D;
+    if (vec)
+      while (slab > 256 && slab % 512 == 0 && (int64_t)a.Nq * slab * 4 > (2LL << 20)) slab /= 2;
+    const int64_t slabs = a.grad_pv ? (a.D + slab - 1) / slab : 1;
+    const int64_t blocks = (total_cols + 3) / 4 * slabs;
+    JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
+    JN_PROFILE(a.profile_name ? a.profile_name : "cols_gather_kernel", stream);
+    if (vec) hipLaunchKernelGGL(cols_gather_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, a, slab);
+    else hipLaunchKernelGGL(cols_gather_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, a, slab);
+    JN_LAUNCH_CHECK();
+  }
+  if (a.q) {
+    const bool vec = (a.r % 4 == 0) && (a.ldq % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0);
+    const int64_t blocks = cols_backward_parts(total_cols);
+    JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
+    JN_PROFILE("cols_keygrad_kernel", stream);
+    if (vec) hipLaunchKernelGGL(cols_keygrad_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(cols_keygrad_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    JN_LAUNCH_CHECK();
+  }
   return kOk;
 }
 

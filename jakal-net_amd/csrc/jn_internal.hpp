@@ -193,17 +193,15 @@ struct ColsBwdArgs {
   const float* kscale;       // [r] (null = 1)
   int r;
   int B, Nq, Nk, D;
-  int cols_per_wave;
   float* grad_pv;            // [B*Nk, D] (null: skip)
   int64_t ld_gpv;
-  int accumulate_gpv;        // add into grad_pv instead of overwrite
   float* grad_ps;            // [B*Nk] (null: skip)
-  float* dk;                 // [B*Nk, r], stride lddk
+  float* dk;                 // [B*Nk, r], stride lddk (null q: skip dk and part_c)
   int64_t lddk;
-  float* part_c;             // [num_waves, r]
-  const char* profile_name;  // label for the kernel timer (null: "cols_backward_kernel")
+  float* part_c;             // [cols_backward_parts(B*Nk), r] or null
+  const char* profile_name;  // label for the gather's kernel timer (null: "cols_gather_kernel")
 };
-int cols_backward_waves(int64_t total_cols, int cols_per_wave);
+int cols_backward_parts(int64_t total_cols);
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream);
 
 size_t finalize_stage_floats(int r);

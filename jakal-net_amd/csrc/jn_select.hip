@@ -19,9 +19,10 @@
 //   * 16 query rows per wave.  A wave keeps the query fragment of its rows in
 //     VGPRs for the whole kernel (B operand of v_mfma_f32_16x16x4f32; lane l
 //     owns row l%16, rank slice l/16).
-//   * Keys stream through LDS in chunks of 32 rows (two 16-row MFMA tiles,
-//     A operand), double buffered with a one-chunk register prefetch and one
-//     workgroup barrier per chunk.
+//   * Each wave streams the keys itself, in chunks of 32 rows (two 16-row MFMA
+//     tiles, A operand), loaded straight into VGPRs one chunk ahead.  The waves
+//     of a workgroup share nothing but the LDS allocation, so no barrier
+//     couples them: one wave's merge overlaps the others' MFMAs.
 //   * After a chunk, lane l holds 8 scores of row l%16.  Scores above the
 //     row's threshold theta are appended to the lane's own candidate region
 //     of the row (the row's 4 lanes never share a region, so appends need no
@@ -359,19 +360,15 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kep
   wave_lds_sync();
 }
 
-// VEC: r == 4*RQ and 16-byte aligned key rows -> float4 chunk loads.
+// VEC: r == 4*RQ and 16-byte aligned key rows -> float4 key loads (RQ % 4 == 0).
 template <int RQ, bool VEC, int KEEP>
 __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kernel(SelectArgs a) {
   constexpr int CAP = sel_lane_cap(KEEP);
-  constexpr int RP = 4 * RQ;
-  constexpr int KSTRIDE = RP + 4;  // padded key row (floats)
+  constexpr bool V4 = VEC && RQ % 4 == 0;
 
-  __shared__ __align__(16) float s_key[2][kSelChunk * KSTRIDE];
   __shared__ __align__(16) float s_slot_s[kSelRows * kSelScoreStride];
   __shared__ __align__(16) uint16_t s_slot_i[kSelRows * kSelIndexStride];
-  __shared__ __align__(16) float s_scale[RP];
 
-  const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = wave_id();
   const int g = lane >> 4;    // rank slice owned by this lane group
@@ -388,92 +385,60 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
   const int k = a.k;
   const int ldk = (int)a.ldk;
 
-  // ---- set-up -------------------------------------------------------------
-  for (int i = tid; i < RP; i += blockDim.x) s_scale[i] = (i < a.r) ? (a.scale ? a.scale[i] : 1.0f) : 0.0f;
-  __syncthreads();
-
-  // ---- query fragment in registers ------------------------------------------
+  // ---- query fragment in registers, times the scale vector: both score forms
+  // (scaled query or scaled key) equal sum_r q[r] * c[r] * key[r] ---------------
   const int lrow = wave * kSelRowsPerWave + col;  // row slot within the workgroup
   const int my_row = row0 + lrow;
   const bool row_ok = my_row < a.Nq;
+  // unconditional loads (invalid rows and ranks read row 0 / rank 0 and are
+  // zeroed after), so they all issue before one wait
   float qf[RQ];
+  {
+    const float* qrow = qb + (int64_t)(row_ok ? my_row : 0) * a.ldq;
+    float qs[RQ];
 #pragma unroll
-  for (int s = 0; s < RQ; ++s) {
-    const int rr = g * RQ + s;
-    float v = 0.0f;
-    if (row_ok && rr < a.r) {
-      v = qb[(int64_t)my_row * a.ldq + rr];
-      if (a.scale_on_query) v *= s_scale[rr];
+    for (int s = 0; s < RQ; ++s) {
+      const int rr = g * RQ + s;
+      qf[s] = qrow[rr < a.r ? rr : 0];
+      qs[s] = a.scale ? a.scale[rr < a.r ? rr : 0] : 1.0f;
     }
-    qf[s] = v;
+#pragma unroll
+    for (int s = 0; s < RQ; ++s) qf[s] = (row_ok && g * RQ + s < a.r) ? qf[s] * qs[s] : 0.0f;
   }
   const float bias = a.bias ? a.bias[0] : 0.0f;
   // (dot + bias) / T as a multiply by the reciprocal: exact for T == 1, within
   // 1.5 ulp of the division otherwise
   const float inv_temp = 1.0f / a.temperature;
-  const bool scale_key = !a.scale_on_query;
 
-  // ---- key chunk loader: buffer loads relative to the chunk's first row;
-  // rows past Nk (and padding columns) read as zeros and are masked later.
-  // Two register sets hold the chunks two and three ahead of the one being
-  // scored, so a load has two chunk iterations to return before its store.
-  constexpr int kChunkVals = kSelChunk * RP;
-  constexpr int kChunkF4 = kChunkVals / 4;
-  constexpr int kLoads = VEC ? (kChunkF4 + 255) / 256 : (kChunkVals + 255) / 256;
-  float4 pf4[2][VEC ? kLoads : 1];
-  float pf1[2][VEC ? 1 : kLoads];
-  // SET is a compile-time register set (std::integral_constant), so the
-  // prefetch registers stay in VGPRs.
-  auto load_chunk = [&](auto SET, int c) {
+  // ---- key fragments straight from memory: every wave streams the keys on its
+  // own (no LDS staging, no workgroup barrier in the loop), so a wave that
+  // merges does not hold up the others.  Lane (g, col) reads key rows
+  // c0 + col and c0 + 16 + col, ranks [g*RQ, g*RQ + RQ): the A operand of its
+  // two MFMA tiles.  Buffer loads are relative to the chunk's first row; rows
+  // past Nk read as zeros and are masked later.  Two register sets: the next
+  // chunk loads while the current one is scored.
+  float kx[2][2][RQ];
+  auto load_keys = [&](auto SET, int c) {
     constexpr int S = decltype(SET)::value;
     const int c0 = c * kSelChunk;
     const auto rs = make_rsrc(kbase + (int64_t)c0 * ldk, 0x80000000u);
-    if constexpr (VEC) {
 #pragma unroll
-      for (int u = 0; u < kLoads; ++u) {
-        const int f = tid + u * 256;
-        if (kChunkF4 % 256 == 0 || f < kChunkF4) {
-          const int rrow = f / RQ, c4 = f % RQ;
-          pf4[S][u] = buf_load4(rs, c0 + rrow < a.Nk ? (uint32_t)(rrow * ldk + 4 * c4) * 4u : kOobOffset);
+    for (int t = 0; t < 2; ++t) {
+      const int rrow = 16 * t + col;
+      const bool rok = c0 + rrow < a.Nk;
+      const uint32_t base = (uint32_t)(rrow * ldk + g * RQ) * 4u;
+      if constexpr (V4) {
+#pragma unroll
+        for (int q = 0; q < RQ / 4; ++q) {
+          const float4 v = buf_load4(rs, rok ? base + 16u * q : kOobOffset);
+          kx[S][t][4 * q + 0] = v.x;
+          kx[S][t][4 * q + 1] = v.y;
+          kx[S][t][4 * q + 2] = v.z;
+          kx[S][t][4 * q + 3] = v.w;
         }
-      }
-    } else {
+      } else {
 #pragma unroll
-      for (int u = 0; u < kLoads; ++u) {
-        const int e = tid + u * 256;
-        const int rrow = e / RP, rc = e % RP;
-        const bool ok = e < kChunkVals && rc < a.r && c0 + rrow < a.Nk;
-        pf1[S][u] = buf_load1(rs, ok ? (uint32_t)(rrow * ldk + rc) * 4u : kOobOffset);
-      }
-    }
-  };
-  auto store_chunk = [&](auto SET) {
-    constexpr int S = decltype(SET)::value;  // register set == LDS buffer
-    if constexpr (VEC) {
-#pragma unroll
-      for (int u = 0; u < kLoads; ++u) {
-        const int f = tid + u * 256;
-        if (kChunkF4 % 256 == 0 || f < kChunkF4) {
-          const int rrow = f / RQ, c4 = f % RQ;
-          float4 v = pf4[S][u];
-          if (scale_key) {
-            const float4 sc = *reinterpret_cast<const float4*>(&s_scale[4 * c4]);
-            v.x *= sc.x;
-            v.y *= sc.y;
-            v.z *= sc.z;
-            v.w *= sc.w;
-          }
-          *reinterpret_cast<float4*>(&s_key[S][rrow * KSTRIDE + 4 * c4]) = v;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < kLoads; ++u) {
-        const int e = tid + u * 256;
-        if (e < kChunkVals) {
-          const int rrow = e / RP, rc = e % RP;
-          s_key[S][rrow * KSTRIDE + rc] = scale_key ? pf1[S][u] * s_scale[rc] : pf1[S][u];
-        }
+        for (int q = 0; q < RQ; ++q) kx[S][t][q] = buf_load1(rs, (rok && g * RQ + q < a.r) ? base + 4u * q : kOobOffset);
       }
     }
   };
@@ -490,53 +455,16 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
   float* my_cand_s = my_slot_s + KEEP + g * CAP;
   uint16_t* my_cand_i = my_slot_i + KEEP + g * CAP;
 
-  // chunk c lives in register set c & 1 and LDS buffer c & 1
-  load_chunk(kSet0, 0);
-  store_chunk(kSet0);
-  if (nchunks > 1) load_chunk(kSet1, 1);
-  if (nchunks > 2) load_chunk(kSet0, 2);
-  __syncthreads();
-
-  for (int c = 0; c < nchunks; ++c) {
-    const int cur = c & 1;
+  auto process = [&](auto SET, int c) {
+    constexpr int S = decltype(SET)::value;
     const int c0 = c * kSelChunk;
-    // chunk c + 1 into the other LDS buffer (read by everyone before the last
-    // barrier), then reuse its registers for chunk c + 3
-    if (c + 1 < nchunks) {
-      if (cur == 0) {
-        store_chunk(kSet1);
-        if (c + 3 < nchunks) load_chunk(kSet1, c + 3);
-      } else {
-        store_chunk(kSet0);
-        if (c + 3 < nchunks) load_chunk(kSet0, c + 3);
-      }
-    }
-
     // -- scores for 32 keys x 16 query rows (two MFMA tiles) --
     floatx4 acc0 = {0.f, 0.f, 0.f, 0.f};
     floatx4 acc1 = {0.f, 0.f, 0.f, 0.f};
-    const float* k0 = &s_key[cur][(0 * 16 + col) * KSTRIDE + g * RQ];
-    const float* k1 = &s_key[cur][(1 * 16 + col) * KSTRIDE + g * RQ];
-    if constexpr (RQ % 4 == 0) {
 #pragma unroll
-      for (int s4 = 0; s4 < RQ / 4; ++s4) {
-        const float4 x0 = *reinterpret_cast<const float4*>(k0 + 4 * s4);
-        const float4 x1 = *reinterpret_cast<const float4*>(k1 + 4 * s4);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(x0.x, qf[4 * s4 + 0], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(x1.x, qf[4 * s4 + 0], acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(x0.y, qf[4 * s4 + 1], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(x1.y, qf[4 * s4 + 1], acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(x0.z, qf[4 * s4 + 2], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(x1.z, qf[4 * s4 + 2], acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(x0.w, qf[4 * s4 + 3], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(x1.w, qf[4 * s4 + 3], acc1, 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < RQ; ++q) {
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[q], qf[q], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[q], qf[q], acc1, 0, 0, 0);
-      }
+    for (int q = 0; q < RQ; ++q) {
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[S][0][q], qf[q], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[S][1][q], qf[q], acc1, 0, 0, 0);
     }
 
     // -- threshold filter: lane holds keys c0 + 16t + 4g + v of its row --
@@ -552,13 +480,14 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
 #pragma unroll
     for (int u = 0; u < 8; ++u) any |= __ballot(sc[u] > theta);
     if (any) {
+      // branchless append: every entry is written at the running count, which
+      // advances only past candidates, so the next write overwrites a
+      // rejected entry (cnt <= CAP - 8 on entry keeps all 8 writes in the region)
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        if (sc[u] > theta) {
-          my_cand_s[cnt] = sc[u];
-          my_cand_i[cnt] = (uint16_t)(c0 + (u >> 2) * 16 + 4 * g + (u & 3));
-          ++cnt;
-        }
+        my_cand_s[cnt] = sc[u];
+        my_cand_i[cnt] = (uint16_t)(c0 + (u >> 2) * 16 + 4 * g + (u & 3));
+        cnt += (sc[u] > theta) ? 1 : 0;
       }
     }
 
@@ -586,8 +515,21 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
       kept = min(k, total);
       cnt = 0;
     }
-    __syncthreads();
+  };
+
+  // chunk c lives in register set c & 1.  The loads are unconditional (chunks
+  // past the end read rows >= Nk: zeros, no memory access), so the wait before
+  // a chunk's MFMAs covers only its own loads, not the prefetch behind them.
+  load_keys(kSet0, 0);
+  for (int c = 0; c < nchunks; c += 2) {
+    load_keys(kSet1, c + 1);
+    process(kSet0, c);
+    if (c + 1 < nchunks) {
+      load_keys(kSet0, c + 2);
+      process(kSet1, c + 1);
+    }
   }
+  wave_lds_sync();
 
   // ---- sort each row's k winners and write them -----------------------------
   for (int t = 0; t < kSelRowsPerWave; ++t) {

@@ -417,20 +417,25 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
   // two MFMA tiles.  Buffer loads are relative to the chunk's first row; rows
   // past Nk read as zeros and are masked later.  Two register sets: the next
   // chunk loads while the current one is scored.
+  // The resource of a chunk ends after its last row below Nk, so rows past
+  // the end read as zeros with loop-invariant lane offsets.
   float kx[2][2][RQ];
+  uint32_t kbase_off[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) kbase_off[t] = (uint32_t)((16 * t + col) * ldk + g * RQ) * 4u;
   auto load_keys = [&](auto SET, int c) {
     constexpr int S = decltype(SET)::value;
     const int c0 = c * kSelChunk;
-    const auto rs = make_rsrc(kbase + (int64_t)c0 * ldk, 0x80000000u);
+    const int rows = max(0, min(kSelChunk, a.Nk - c0));
+    // uniform (readfirstlane keeps the resource in SGPRs)
+    const uint32_t nrec = __builtin_amdgcn_readfirstlane((uint32_t)(rows * ldk) * 4u);
+    const auto rs = make_rsrc(kbase + (int64_t)c0 * ldk, nrec);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const int rrow = 16 * t + col;
-      const bool rok = c0 + rrow < a.Nk;
-      const uint32_t base = (uint32_t)(rrow * ldk + g * RQ) * 4u;
       if constexpr (V4) {
 #pragma unroll
         for (int q = 0; q < RQ / 4; ++q) {
-          const float4 v = buf_load4(rs, rok ? base + 16u * q : kOobOffset);
+          const float4 v = buf_load4(rs, kbase_off[t] + 16u * q);
           kx[S][t][4 * q + 0] = v.x;
           kx[S][t][4 * q + 1] = v.y;
           kx[S][t][4 * q + 2] = v.z;
@@ -438,7 +443,7 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
         }
       } else {
 #pragma unroll
-        for (int q = 0; q < RQ; ++q) kx[S][t][q] = buf_load1(rs, (rok && g * RQ + q < a.r) ? base + 4u * q : kOobOffset);
+        for (int q = 0; q < RQ; ++q) kx[S][t][q] = buf_load1(rs, (g * RQ + q < a.r) ? kbase_off[t] + 4u * q : kOobOffset);
       }
     }
   };
@@ -470,7 +475,14 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
     // -- threshold filter: lane holds keys c0 + 16t + 4g + v of its row --
     float sc[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) sc[u] = (((u < 4) ? acc0[u & 3] : acc1[u & 3]) + bias) * inv_temp;
+    for (int u = 0; u < 8; ++u) sc[u] = (u < 4) ? acc0[u & 3] : acc1[u & 3];
+    if (inv_temp != 1.0f) {  // uniform
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sc[u] = (sc[u] + bias) * inv_temp;
+    } else if (bias != 0.0f) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sc[u] += bias;
+    }
     if (c0 + kSelChunk > a.Nk) {  // uniform: only the last chunk holds padding keys
 #pragma unroll
       for (int u = 0; u < 8; ++u)

@@ -3,8 +3,9 @@
 Each source row selects its top-k destinations (transition.py:437-444).  Index
 parity is exact on rows whose k-th/(k+1)-th logit gap exceeds 1e-5; values
 and gradients are compared with the oracle evaluated on the selection the GPU
-made, within rtol 1e-4 / atol 1e-5 (fp32).  Gradients are sums over edges
-and over D- or r-long dot products whose terms can cancel: their fp32 error
+made, within rtol 1e-4 / atol 1e-5 (fp32).  The outputs (sums over a
+destination's incoming routes) and the gradients (sums over edges and over D-
+or r-long dot products) have terms that can cancel: their fp32 error
 scales with the magnitude of the terms, not of the (possibly small) result, so
 their atol is 1e-5 times the largest magnitude in the tensor (norm-wise), and
 for the parameter gradients (sums over every edge) at least 1e-5 times the
@@ -92,8 +93,12 @@ def _run(dev, seed, B, Ns, Nd, Dsrc, Ddst, r, topk, temperature, kind, init="xav
     mask = O.mask_from_indices(got_idx, Nd)
     ref = O.transition_forward(_np(src), _np(dst), _np(rho_cpu), _np(state), _np(pv_cpu), _np(Ws), _np(Wt), _np(w),
                                bval, topk=k, temperature=temperature, mask=mask, kind=kind)
-    _close(_np(ds), ref["delta_state"], what="delta_state")
-    _close(_np(dv), ref["delta_val"], what="delta_val")
+    # destination sums run over every incoming route (about Ns * k / Nd terms):
+    # norm-wise absolute tolerance, as for the gradients below
+    _close(_np(ds), ref["delta_state"], atol=ATOL * max(1.0, float(np.abs(ref["delta_state"]).max())),
+           what="delta_state")
+    _close(_np(dv), ref["delta_val"], atol=ATOL * max(1.0, float(np.abs(ref["delta_val"]).max())),
+           what="delta_val")
     gr = O.transition_backward(_np(src), _np(dst), _np(rho_cpu), _np(state), _np(pv_cpu), _np(Ws), _np(Wt), _np(w),
                                bval, _np(gds), _np(gdv), topk=k, temperature=temperature, mask=mask, kind=kind)
     for t, name in ((rho, "sender"), (srcd, "src_val"), (dstd, "dst_val"), (psd, "ps"), (pvd, "pv")):

@@ -279,9 +279,12 @@ class TransitionC3:
             # per edge: idx + logit + grad-delta row of the destination + its key row + g_logit write;
             # per source row: its value row, its grad-value write, dq write
             return "hbm", E * (8.0 + 4.0 * D + 4.0 * r + 4.0) + rows * (8.0 * D + 4.0 * r + 16.0) / 2
-        if name.startswith("route_gather_kernel"):
+        if name.startswith("route_gather_kernel") or name.startswith("cols_gather_kernel"):
             # per edge: edge record + source value row; per destination: delta row write
             return "hbm", (E * (16.0 + 4.0 * D) + rows * (4.0 * D + 12.0)) / 2
+        if name.startswith("cols_keygrad_kernel"):
+            # per edge: edge record + source projection row; per destination: dk row + its projection row
+            return "hbm", (E * (16.0 + 4.0 * r) + rows * (8.0 + 8.0 * r)) / 2
         if name.startswith("gemm_f32_kernel"):
             return "mfma", 2.0 * rows * D * r / 2
         return None

@@ -19,11 +19,11 @@
 //   * 16 query rows per wave.  A wave keeps the query fragment of its rows in
 //     VGPRs for the whole kernel (B operand of v_mfma_f32_16x16x4f32; lane l
 //     owns row l%16, rank slice l/16).
-//   * Each wave streams the keys itself, in chunks of 32 rows (two 16-row MFMA
+//   * Each wave streams the keys itself, in chunks of 48 rows (three 16-row MFMA
 //     tiles, A operand), loaded straight into VGPRs one chunk ahead.  The waves
 //     of a workgroup share nothing but the LDS allocation, so no barrier
 //     couples them: one wave's merge overlaps the others' MFMAs.
-//   * After a chunk, lane l holds 8 scores of row l%16.  Scores above the
+//   * After a chunk, lane l holds 12 scores of row l%16.  Scores above the
 //     row's threshold theta are appended to the lane's own candidate region
 //     of the row (the row's 4 lanes never share a region, so appends need no
 //     cross-lane offsets).  Counts and thresholds live in registers.
@@ -49,12 +49,14 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kSelWaves = 4;
 constexpr int kSelRowsPerWave = 16;
 constexpr int kSelRows = kSelWaves * kSelRowsPerWave;  // 64 query rows / workgroup
-constexpr int kSelChunk = 32;                          // key rows per LDS chunk
+constexpr int kSelTiles = 3;                           // 16-key MFMA tiles per chunk
+constexpr int kSelChunk = 16 * kSelTiles;              // key rows per chunk
+constexpr int kSelLaneKeys = 4 * kSelTiles;            // scores of one row per lane and chunk
 // A row's slots: a kept region of KEEP entries (the k <= KEEP best so far;
 // KEEP = 32 for k <= 32, 64 for k <= 64), then one candidate region of
-// sel_lane_cap(KEEP) slots per lane of the row.  A lane takes at most 8
-// candidates per chunk, so merging once a lane holds more than cap - 8 keeps
-// every region within its capacity.
+// sel_lane_cap(KEEP) slots per lane of the row.  A lane takes at most
+// kSelLaneKeys candidates per chunk, so merging once a lane holds more than
+// cap - kSelLaneKeys keeps every region within its capacity.
 constexpr int kSelRowSlots = 144;
 __host__ __device__ constexpr int sel_lane_cap(int keep) { return (kSelRowSlots - keep) / 4; }
 static_assert(sel_lane_cap(32) % 4 == 0 && sel_lane_cap(64) % 4 == 0, "candidate regions hold whole float4s");
@@ -419,10 +421,10 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
   // chunk loads while the current one is scored.
   // The resource of a chunk ends after its last row below Nk, so rows past
   // the end read as zeros with loop-invariant lane offsets.
-  float kx[2][2][RQ];
-  uint32_t kbase_off[2];
+  float kx[2][kSelTiles][RQ];
+  uint32_t kbase_off[kSelTiles];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) kbase_off[t] = (uint32_t)((16 * t + col) * ldk + g * RQ) * 4u;
+  for (int t = 0; t < kSelTiles; ++t) kbase_off[t] = (uint32_t)((16 * t + col) * ldk + g * RQ) * 4u;
   auto load_keys = [&](auto SET, int c) {
     constexpr int S = decltype(SET)::value;
     const int c0 = c * kSelChunk;
@@ -431,7 +433,7 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
     const uint32_t nrec = __builtin_amdgcn_readfirstlane((uint32_t)(rows * ldk) * 4u);
     const auto rs = make_rsrc(kbase + (int64_t)c0 * ldk, nrec);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < kSelTiles; ++t) {
       if constexpr (V4) {
 #pragma unroll
         for (int q = 0; q < RQ / 4; ++q) {
@@ -464,39 +466,41 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
     constexpr int S = decltype(SET)::value;
     const int c0 = c * kSelChunk;
     // -- scores for 32 keys x 16 query rows (two MFMA tiles) --
-    floatx4 acc0 = {0.f, 0.f, 0.f, 0.f};
-    floatx4 acc1 = {0.f, 0.f, 0.f, 0.f};
+    floatx4 acc[kSelTiles];
 #pragma unroll
-    for (int q = 0; q < RQ; ++q) {
-      acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[S][0][q], qf[q], acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[S][1][q], qf[q], acc1, 0, 0, 0);
-    }
+    for (int t = 0; t < kSelTiles; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < RQ; ++q)
+#pragma unroll
+      for (int t = 0; t < kSelTiles; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[S][t][q], qf[q], acc[t], 0, 0, 0);
 
     // -- threshold filter: lane holds keys c0 + 16t + 4g + v of its row --
-    float sc[8];
+    float sc[kSelLaneKeys];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) sc[u] = (u < 4) ? acc0[u & 3] : acc1[u & 3];
+    for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = acc[u >> 2][u & 3];
     if (inv_temp != 1.0f) {  // uniform
 #pragma unroll
-      for (int u = 0; u < 8; ++u) sc[u] = (sc[u] + bias) * inv_temp;
+      for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = (sc[u] + bias) * inv_temp;
     } else if (bias != 0.0f) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) sc[u] += bias;
+      for (int u = 0; u < kSelLaneKeys; ++u) sc[u] += bias;
     }
     if (c0 + kSelChunk > a.Nk) {  // uniform: only the last chunk holds padding keys
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < kSelLaneKeys; ++u)
         if (c0 + (u >> 2) * 16 + 4 * g + (u & 3) >= a.Nk) sc[u] = -INFINITY;
     }
     uint64_t any = 0;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) any |= __ballot(sc[u] > theta);
+    for (int u = 0; u < kSelLaneKeys; ++u) any |= __ballot(sc[u] > theta);
     if (any) {
       // branchless append: every entry is written at the running count, which
       // advances only past candidates, so the next write overwrites a
-      // rejected entry (cnt <= CAP - 8 on entry keeps all 8 writes in the region)
+      // rejected entry (cnt <= CAP - kSelLaneKeys on entry keeps every write in
+      // the region)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < kSelLaneKeys; ++u) {
         my_cand_s[cnt] = sc[u];
         my_cand_i[cnt] = (uint16_t)(c0 + (u >> 2) * 16 + 4 * g + (u & 3));
         cnt += (sc[u] > theta) ? 1 : 0;
@@ -505,7 +509,7 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
 
     // -- merge rows once a lane region is nearly full (or everything at the end) --
     const bool last = (c + 1 == nchunks);
-    if (__ballot(cnt > CAP - 8 || (last && cnt > 0))) {
+    if (__ballot(cnt > CAP - kSelLaneKeys || (last && cnt > 0))) {
       wave_lds_sync();
       const int total = kept + row_sum4(cnt);
       bool fallback;

@@ -22,7 +22,7 @@
 //   * Each wave streams the keys itself, in chunks of 48 rows (three 16-row MFMA
 //     tiles, A operand), loaded straight into VGPRs one chunk ahead.  The waves
 //     of a workgroup share nothing but the LDS allocation, so no barrier
-//     couples them: one wave's merge overlaps the others' MFMAs.
+//     couples them: a wave that merges does not hold up the others.
 //   * After a chunk, lane l holds 12 scores of row l%16.  Scores above the
 //     row's threshold theta are appended to the lane's own candidate region
 //     of the row (the row's 4 lanes never share a region, so appends need no

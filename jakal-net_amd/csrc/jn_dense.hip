@@ -14,7 +14,7 @@
 //                                    row i keeps sources j <= i), delta_state
 //   dense_compress_backward_kernel : G_s = compress'(E, G + gds (x) ps) in place,
 //                                    and its row sums (bias gradient)
-//   dense_colsum_kernel            : grad ps[j] = sum_i E[i, j] gds[i] (fixed order)
+//   colsum_rows_kernel             : grad ps[j] = sum_i E[i, j] gds[i] (fixed order)
 //   scale_grad_partials_kernel     : w_hat partials and scaling of dP_s
 #include "jn_internal.hpp"
 
@@ -178,25 +178,76 @@ __global__ __launch_bounds__(256) void dense_compress_backward_kernel(float* G, 
   if (lane == 0) rowsum[row] = acc;
 }
 
-// out[b, j] = sum_i E[b, i, j] * w[b, i]: a workgroup owns 64 columns; wave q
-// sums rows i = q, q + 4, ... and the four partials are added in wave order.
-__global__ __launch_bounds__(256) void dense_colsum_kernel(const float* E, const float* w, int N, int B,
-                                                           float* out) {
-  __shared__ float red[4][64];
+// out[b, j] = sum_i M[b, i, j] * a[b, i] (* c[b, i]) over the Nr rows i in a
+// fixed order.  A workgroup of 16 waves owns a tile of 256 columns (VEC: four
+// per lane, float4 loads) or 64 (one per lane); wave w sums rows i = w, w + 16,
+// ... four at a time, and the 16 partials are added in wave order.
+template <bool VEC>
+__global__ __launch_bounds__(1024) void colsum_rows_kernel(const float* M, const float* a, const float* c, int B,
+                                                           int Nr, int Nc, float* out) {
+  constexpr int CT = VEC ? 256 : 64;
+  constexpr int W = VEC ? 4 : 1;
+  __shared__ float red[16][CT];
   const int lane = lane_id(), wave = wave_id();
-  const int tiles = (N + 63) / 64;
+  const int tiles = (Nc + CT - 1) / CT;
   const int b = blockIdx.x / tiles;
-  const int j = (blockIdx.x % tiles) * 64 + lane;
-  float s = 0.0f;
-  if (b < B && j < N) {
-    const float* eb = E + (int64_t)b * N * N;
-    const float* wb = w + (int64_t)b * N;
-    for (int i = wave; i < N; i += 4) s += eb[(int64_t)i * N + j] * wb[i];
+  const int j = (blockIdx.x % tiles) * CT + W * lane;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (b < B && j < Nc) {
+    const float* mb = M + (int64_t)b * Nr * Nc + j;
+    const float* ab = a + (int64_t)b * Nr;
+    const float* cb = c ? c + (int64_t)b * Nr : nullptr;
+    auto wt = [&](int i) { return cb ? ab[i] * cb[i] : ab[i]; };
+    int i = wave;
+    for (; i + 48 < Nr; i += 64) {
+      float4 v[4];
+      float f[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v[u] = load_w<W>(mb + (int64_t)(i + 16 * u) * Nc);
+        f[u] = wt(i + 16 * u);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) fma4(s, f[u], v[u]);
+    }
+    for (; i < Nr; i += 16) fma4(s, wt(i), load_w<W>(mb + (int64_t)i * Nc));
   }
-  red[wave][lane] = s;
+  if constexpr (VEC) {
+    *reinterpret_cast<float4*>(&red[wave][4 * lane]) = s;
+  } else {
+    red[wave][lane] = s.x;
+  }
   __syncthreads();
-  if (wave == 0 && b < B && j < N)
-    out[(int64_t)b * N + j] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+  // wave 0 adds the 16 partials of its columns in wave order
+  if (wave == 0 && b < B && j < Nc) {
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      if constexpr (VEC) {
+        t = add4(t, *reinterpret_cast<const float4*>(&red[w][4 * lane]));
+      } else {
+        t.x += red[w][lane];
+      }
+    }
+    store_w<W>(out + (int64_t)b * Nc + j, t);
+  }
+}
+
+int launch_colsum_rows(const float* M, const float* a, const float* c, int B, int Nr, int Nc, float* out,
+                       const char* name, hipStream_t stream) {
+  // 256-column tiles with float4 loads when they still give every CU a workgroup
+  const bool vec = (Nc % 4 == 0) && ((reinterpret_cast<uintptr_t>(M) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(out) & 15) == 0) && (int64_t)B * ((Nc + 255) / 256) >= 256;
+  const int ct = vec ? 256 : 64;
+  const int64_t blocks = (int64_t)B * ((Nc + ct - 1) / ct);
+  JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "too many columns");
+  JN_PROFILE(name, stream);
+  if (vec) hipLaunchKernelGGL(colsum_rows_kernel<true>, dim3((unsigned)blocks), dim3(1024), 0, stream, M, a, c, B, Nr,
+                              Nc, out);
+  else hipLaunchKernelGGL(colsum_rows_kernel<false>, dim3((unsigned)blocks), dim3(1024), 0, stream, M, a, c, B, Nr,
+                          Nc, out);
+  JN_LAUNCH_CHECK();
+  return kOk;
 }
 
 // part[m, c] = dps[m, c] * ps[m, c] (w_hat gradient partials), then dps *= w_hat.
@@ -245,12 +296,7 @@ int launch_dense_compress_backward(float* G, const float* E, const float* gds, c
 }
 
 int launch_dense_colsum(const float* E, const float* w, int B, int N, float* out, hipStream_t stream) {
-  const int64_t blocks = (int64_t)B * ((N + 63) / 64);
-  JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "too many columns");
-  JN_PROFILE("dense_colsum_kernel", stream);
-  hipLaunchKernelGGL(dense_colsum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, E, w, N, B, out);
-  JN_LAUNCH_CHECK();
-  return kOk;
+  return launch_colsum_rows(E, w, nullptr, B, N, N, out, "dense_colsum_kernel", stream);
 }
 
 int launch_scale_grad_partials(float* dps, int64_t ld_dps, const float* src, int64_t ld_src, const float* w_hat,

@@ -153,6 +153,9 @@ int launch_dense_compress(float* S, const float* bias, const float* ps, int B, i
 int launch_dense_compress_backward(float* G, const float* E, const float* gds, const float* ps, int B, int N,
                                    int compress, int causal, float* rowsum, hipStream_t stream);
 int launch_dense_colsum(const float* E, const float* w, int B, int N, float* out, hipStream_t stream);
+// out[b, j] = sum_i M[b, i, j] a[b, i] (c[b, i] if given), i < Nr, j < Nc, fixed order
+int launch_colsum_rows(const float* M, const float* a, const float* c, int B, int Nr, int Nc, float* out,
+                       const char* name, hipStream_t stream);
 
 // ---- dense transitions (jn_route_dense.hip) --------------------------------
 int launch_route_dense_compress(float* L, const float* bias, float inv_temp, int B, int Ns, int Nd, int kind,

@@ -14,7 +14,7 @@
 // The score products are MFMA GEMMs (jn_gemm.hip); this file holds the
 // row-wise kernels between them:
 //   route_dense_compress_kernel          : R = compress((L + b) / T) in place, one wave per source row
-//   route_dense_colsum_kernel            : out[k] = sum_j R[j, k] a_j c_j (fixed order)
+//   (column sums out[k] = sum_j R[j, k] a_j c_j run on colsum_rows_kernel, jn_dense.hip)
 //   route_dense_compress_backward_kernel : logit gradient in place, sender / state grads, row sums
 #include <cfloat>
 
@@ -106,28 +106,6 @@ __global__ __launch_bounds__(256) void route_dense_compress_kernel(float* L, con
   } else {
     for (int j = lane; j < N; j += kWave) x[j] = route(x[j]);
   }
-}
-
-// out[b, k] = sum_j R[b, j, k] a[b, j] (c[b, j]) over j in a fixed order:
-// wave w of a workgroup sums rows j = w, w + 4, ... of a 64-column tile.
-__global__ __launch_bounds__(256) void route_dense_colsum_kernel(const float* R, const float* a, const float* c,
-                                                                 int B, int Nr, int Nc, float* out) {
-  __shared__ float red[4][64];
-  const int lane = lane_id(), wave = wave_id();
-  const int tiles = (Nc + 63) / 64;
-  const int b = blockIdx.x / tiles;
-  const int k = (blockIdx.x % tiles) * 64 + lane;
-  float s = 0.0f;
-  if (b < B && k < Nc) {
-    const float* rb = R + (int64_t)b * Nr * Nc;
-    const float* ab = a + (int64_t)b * Nr;
-    const float* cb = c ? c + (int64_t)b * Nr : nullptr;
-    for (int j = wave; j < Nr; j += 4) s += rb[(int64_t)j * Nc + k] * (cb ? ab[j] * cb[j] : ab[j]);
-  }
-  red[wave][lane] = s;
-  __syncthreads();
-  if (wave == 0 && b < B && k < Nc)
-    out[(int64_t)b * Nc + k] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
 }
 
 // Row j of source rows (batch element b):
@@ -241,13 +219,7 @@ int launch_route_dense_compress(float* L, const float* bias, float inv_temp, int
 
 int launch_route_dense_colsum(const float* R, const float* a, const float* c, int B, int Nr, int Nc, float* out,
                               hipStream_t stream) {
-  const int64_t blocks = (int64_t)B * ((Nc + 63) / 64);
-  JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "too many columns");
-  JN_PROFILE("route_dense_colsum_kernel", stream);
-  hipLaunchKernelGGL(route_dense_colsum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, R, a, c, B, Nr, Nc,
-                     out);
-  JN_LAUNCH_CHECK();
-  return kOk;
+  return launch_colsum_rows(R, a, c, B, Nr, Nc, out, "route_dense_colsum_kernel", stream);
 }
 
 int launch_route_dense_compress_backward(float* H, const float* R, const float* rho, const float* ps,

@@ -207,7 +207,7 @@ DenseScratch carve_dense(void* base, size_t size, int64_t B, int64_t N, int64_t 
   const int64_t M = B * N;
   s.G = ws.take<float>(B * N * N);
   s.dP = ws.take<float>(M * 2 * r);
-  s.rowsum = ws.take<float>(M);
+  s.rowsum = ws.take<float>(M * dense_epi_parts((int)N));  // per-row totals, or the epilogue's block partials
   s.part_c = ws.take<float>(M * r);
   s.stage = ws.take<float>(finalize_stage_floats((int)r));
   s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)(2 * r), (int)Din, (int)M) / sizeof(float));
@@ -891,10 +891,20 @@ int jn_propagation_dense_forward(const float* layer_val, const float* projected_
   sg.C = edges; sg.ldc = N; sg.c_bs = (int64_t)N * N;
   sg.a_kscale = core_weight;
   sg.M = N; sg.N = N; sg.K = r; sg.batch = B;
+  // Softsign runs in the GEMM's epilogue, whose per-block partials of
+  // delta_state are staged in delta_val's storage (the aggregate GEMM below
+  // overwrites it); the row-wise compressions run as a pass of their own.
+  const int parts = dense_epi_parts(N);
+  const bool fused = compress_kind == 0 && parts <= D;
+  if (fused) {
+    sg.epi = 1; sg.epi_causal = causal != 0; sg.epi_bias = bias; sg.epi_ps = projected_state;
+    sg.epi_part = delta_val;
+  }
   rc = gemm_batched(sg, kGemmDenseScores, st);
   if (rc) return rc;
-  // E = compress(S + b) in place, delta_state = E ps
-  rc = launch_dense_compress(edges, bias, projected_state, B, N, compress_kind, causal != 0, delta_state, st);
+  // E = compress(S + b) (in place when not fused), delta_state = E ps
+  rc = fused ? launch_dense_part_rowsum(delta_val, parts, (int64_t)B * N, delta_state, st)
+             : launch_dense_compress(edges, bias, projected_state, B, N, compress_kind, causal != 0, delta_state, st);
   if (rc) return rc;
   // delta_val_b = E_b pv_b
   BatchedGemm ag{};
@@ -941,12 +951,21 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
   gg.B = projected_val; gg.ldb = D; gg.b_bs = (int64_t)N * D; gg.b_kcontig = true;
   gg.C = s.G; gg.ldc = N; gg.c_bs = (int64_t)N * N;
   gg.M = N; gg.N = N; gg.K = D; gg.batch = B;
+  // softsign's derivative runs in the GEMM's epilogue (row-block partials of
+  // the bias gradient into s.rowsum); the row-wise compressions afterwards
+  const bool fused = compress_kind == 0;
+  if (fused) {
+    gg.epi = 1; gg.epi_causal = causal != 0; gg.epi_ps = projected_state; gg.epi_gds = grad_delta_state;
+    gg.epi_E = edges; gg.epi_part = s.rowsum;
+  }
   rc = gemm_batched(gg, kGemmDenseEdgeGrad, st);
   if (rc) return rc;
-  rc = launch_dense_compress_backward(s.G, edges, grad_delta_state, projected_state, B, N, compress_kind,
-                                      causal != 0, s.rowsum,
-                                      st);
-  if (rc) return rc;
+  if (!fused) {
+    rc = launch_dense_compress_backward(s.G, edges, grad_delta_state, projected_state, B, N, compress_kind,
+                                        causal != 0, s.rowsum, st);
+    if (rc) return rc;
+  }
+  const int64_t n_rowsum = fused ? (int64_t)M * dense_epi_parts(N) : M;
 
   // 2. value and state grads of the sources: E^T gdv, E^T gds
   float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
@@ -997,7 +1016,8 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
   }
 
   // 5. w_hat and bias grads
-  return launch_finalize_small_grads(s.part_c, M, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st);
+  return launch_finalize_small_grads(s.part_c, M, r, grad_core_weight, 0, s.rowsum, n_rowsum, grad_bias, s.stage,
+                                     st);
 }
 
 int jn_transition_dense_forward(const float* sender_strength, const float* src_val, const float* dst_val,

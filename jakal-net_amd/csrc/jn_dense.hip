@@ -14,6 +14,10 @@
 //                                    row i keeps sources j <= i), delta_state
 //   dense_compress_backward_kernel : G_s = compress'(E, G + gds (x) ps) in place,
 //                                    and its row sums (bias gradient)
+//   dense_part_rowsum_kernel       : delta_state from the per-block partial sums
+//                                    of the scores GEMM's softsign epilogue
+// Softsign (elementwise) instead runs inside the two score GEMMs' epilogues
+// (jn_gemm.hip), which saves the two in-place passes over the N x N matrix.
 //   colsum_rows_kernel             : grad ps[j] = sum_i E[i, j] gds[i] (fixed order)
 //   scale_grad_partials_kernel     : w_hat partials and scaling of dP_s
 #include "jn_internal.hpp"
@@ -291,6 +295,28 @@ int launch_dense_compress_backward(float* G, const float* E, const float* gds, c
                               E, gds, ps, N, rows, compress, causal, rowsum);
   else hipLaunchKernelGGL(dense_compress_backward_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, G, E,
                           gds, ps, N, rows, compress, causal, rowsum);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
+// out[row] = sum_t part[row, t], t < P, in a fixed order: one wave per row,
+// lane l sums t = l, l + 64, ..., then the wave's butterfly.
+__global__ __launch_bounds__(256) void dense_part_rowsum_kernel(const float* part, int P, int64_t rows, float* out) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  if (row >= rows) return;
+  const float* p = part + row * P;
+  float s = 0.0f;
+  for (int t = lane; t < P; t += kWave) s += p[t];
+  s = wave_sum(s);
+  if (lane == 0) out[row] = s;
+}
+
+int launch_dense_part_rowsum(const float* part, int P, int64_t rows, float* out, hipStream_t stream) {
+  const int64_t blocks = (rows + 3) / 4;
+  JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "too many rows");
+  JN_PROFILE("dense_part_rowsum_kernel", stream);
+  hipLaunchKernelGGL(dense_part_rowsum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, part, P, rows, out);
   JN_LAUNCH_CHECK();
   return kOk;
 }

@@ -41,7 +41,83 @@ struct GemmArgs {
   const float* c_nscale;   // optional: C(m, n) = acc * c_nscale[n] (+ addend)
   const float* c_mscale;   // optional: C(m, n) *= c_mscale[m] (before the addend)
   int64_t ks_bs, ms_bs;    // per-batch element strides of a_kscale and c_mscale
+  // Softsign epilogue of the dense uses (epi != 0; batched over square N x N
+  // score matrices, m and n index rows and columns of one batch element):
+  //   dense_scores:    C = softsign(acc + bias),                  part += C ps[n]
+  //   dense_edge_grad: C = (acc + gds[m] ps[n]) (1 - |E[m, n]|)^2, part += C
+  // with C = 0 where a causal row does not keep source n (n > m).  part holds
+  // one sum per row and 32-column block: epi_part[(b M + m) P + n / 32], P =
+  // ceil(N / 32), each written once, in a fixed order.
+  int epi, epi_causal;
+  const float* epi_bias;   // scalar or null
+  const float* epi_ps;     // [batch, N]
+  const float* epi_gds;    // [batch, M]
+  const float* epi_E;      // indexed like C
+  float* epi_part;
 };
+
+constexpr int kEpiBlock = 32;  // columns per epilogue partial sum
+
+// One element of the softsign epilogue: returns the value to store and adds
+// its share of the row's partial sum to `part`.
+template <int USE>
+__device__ __forceinline__ float dense_epilogue(float x, bool keep, float bias, float ps_n, float gds_m, float e_mn,
+                                                float& part) {
+  if constexpr (USE == kGemmDenseScores) {
+    const float e = keep ? softsign_f(x + bias) : 0.0f;
+    part += e * ps_n;
+    return e;
+  } else {
+    const float d = 1.0f - fabsf(e_mn);
+    const float gs = keep ? (x + gds_m * ps_n) * d * d : 0.0f;
+    part += gs;
+    return gs;
+  }
+}
+
+// Softsign epilogue straight from one wave's accumulators: MT x MT tiles of
+// 16 x 16, lane (grp, col) holding rows mb + 16 mt + 4 grp + v and columns
+// nb + 16 nt + col (nb a multiple of 32, so tiles 2h and 2h + 1 form block h).
+// C (and E) point at the batch element's matrix.
+template <int USE, int MT>
+__device__ __forceinline__ void dense_epilogue_tiles(const GemmArgs& g, int64_t bz, const floatx4 (&acc)[MT][MT],
+                                                     int mb, int nb, float* C, int lane) {
+  const int grp = lane >> 4, col = lane & 15;
+  const int P = (g.N + kEpiBlock - 1) / kEpiBlock;
+  const float* ps = g.epi_ps + bz * g.N;
+  [[maybe_unused]] const float* gds = USE == kGemmDenseEdgeGrad ? g.epi_gds + bz * g.M : nullptr;
+  [[maybe_unused]] const float* E = USE == kGemmDenseEdgeGrad ? g.epi_E + bz * g.c_bs : nullptr;
+  float* part = g.epi_part + bz * (int64_t)g.M * P;
+  const float bias = g.epi_bias ? g.epi_bias[0] : 0.0f;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = mb + mt * 16 + grp * 4 + v;
+      float gm = 0.0f;
+      if constexpr (USE == kGemmDenseEdgeGrad) gm = m < g.M ? gds[m] : 0.0f;
+#pragma unroll
+      for (int h = 0; h < MT / 2; ++h) {
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int n = nb + (2 * h + q) * 16 + col;
+          if (m < g.M && n < g.N) {
+            float e = 0.0f;
+            if constexpr (USE == kGemmDenseEdgeGrad) e = E[(int64_t)m * g.ldc + n];
+            C[(int64_t)m * g.ldc + n] =
+                dense_epilogue<USE>(acc[mt][2 * h + q][v], !g.epi_causal || n <= m, bias, ps[n], gm, e, s);
+          }
+        }
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        s += __shfl_xor(s, 4);
+        s += __shfl_xor(s, 8);
+        const int blk = nb / kEpiBlock + h;
+        if (col == 0 && m < g.M && blk < P) part[(int64_t)m * P + blk] = s;
+      }
+    }
+}
 
 constexpr int kGBM = 64, kGBK = 16, kGStride = kGBK + 4;
 
@@ -206,6 +282,12 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
   }
 
   // Epilogue: lane holds rows 4*grp+v of each 16x16 tile, column col.
+  if constexpr (USE == kGemmDenseScores || USE == kGemmDenseEdgeGrad) {
+    if (g.epi) {
+      dense_epilogue_tiles<USE, MT>(g, bz, acc, m0 + wm * (TILE / 2), n0 + wn * (TILE / 2), C, lane);
+      return;
+    }
+  }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -467,6 +549,35 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
         const int m = m0 + wm * 64 + mt * 16 + r;
         const int n = n0 + wn * 64 + c4;
         float4 x = *reinterpret_cast<const float4*>(&stage[r * kStageStride + c4]);
+        if constexpr (USE == kGemmDenseScores || USE == kGemmDenseEdgeGrad) {
+          if (g.epi) {
+            // softsign epilogue; lanes col..col+7 of a group hold one row's 32-column block
+            const int P = (g.N + kEpiBlock - 1) / kEpiBlock;
+            float part = 0.0f;
+            if (m < g.M && n < g.N) {
+              const float4 p4 = *reinterpret_cast<const float4*>(&g.epi_ps[bz * g.N + n]);
+              float4 e4 = make_float4(0.f, 0.f, 0.f, 0.f);
+              float gm = 0.0f;
+              if constexpr (USE == kGemmDenseEdgeGrad) {
+                e4 = *reinterpret_cast<const float4*>(&g.epi_E[bz * g.c_bs + (int64_t)m * g.ldc + n]);
+                gm = g.epi_gds[bz * g.M + m];
+              }
+              const float bias = g.epi_bias ? g.epi_bias[0] : 0.0f;
+              const bool all = !g.epi_causal;
+              x.x = dense_epilogue<USE>(x.x, all || n <= m, bias, p4.x, gm, e4.x, part);
+              x.y = dense_epilogue<USE>(x.y, all || n + 1 <= m, bias, p4.y, gm, e4.y, part);
+              x.z = dense_epilogue<USE>(x.z, all || n + 2 <= m, bias, p4.z, gm, e4.z, part);
+              x.w = dense_epilogue<USE>(x.w, all || n + 3 <= m, bias, p4.w, gm, e4.w, part);
+              *reinterpret_cast<float4*>(&C[(int64_t)m * g.ldc + n]) = x;
+            }
+            part += __shfl_xor(part, 1);
+            part += __shfl_xor(part, 2);
+            part += __shfl_xor(part, 4);
+            const int blk = (n0 + wn * 64) / kEpiBlock + (col >> 3);
+            if ((col & 7) == 0 && m < g.M && blk < P) g.epi_part[(bz * g.M + m) * P + blk] = part;
+            continue;
+          }
+        }
         if (m < g.M && n < g.N) {
           if (g.c_nscale) {
             const float4 sc = *reinterpret_cast<const float4*>(&g.c_nscale[n]);
@@ -486,6 +597,12 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
       __syncthreads();
     }
   } else {
+    if constexpr (USE == kGemmDenseScores || USE == kGemmDenseEdgeGrad) {
+      if (g.epi) {
+        dense_epilogue_tiles<USE, 4>(g, bz, acc, m0 + wm * 64, n0 + wn * 64, C, lane);
+        return;
+      }
+    }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -541,7 +658,7 @@ static void launch_use(const GemmArgs& g, bool fast, int zdim, hipStream_t strea
   if (fast) {
     const int tm = (g.M + kFT - 1) / kFT, tn = (g.N + kFT - 1) / kFT;
     const bool vec = g.N % 4 == 0 && g.ldc % 4 == 0 && g.c_bs % 4 == 0 && g.c_split_stride % 4 == 0 &&
-                     f4_aligned(g.C) && f4_aligned(g.c_nscale) &&
+                     f4_aligned(g.C) && f4_aligned(g.c_nscale) && f4_aligned(g.epi_ps) && f4_aligned(g.epi_E) &&
                      (g.addend == nullptr || (g.ld_add % 4 == 0 && g.add_bs % 4 == 0 && f4_aligned(g.addend)));
     hipLaunchKernelGGL((gemm_f32_fast_kernel<u.a_kc, u.b_kc, USE, kFastBK>), dim3(tm * tn * zdim), dim3(256), 0,
                        stream, g, tm, tn, vec ? 1 : 0);
@@ -625,6 +742,15 @@ int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
   g.a_kscale = m.a_kscale; g.ks_bs = m.ks_bs;
   g.c_nscale = m.c_nscale;
   g.c_mscale = m.c_mscale; g.ms_bs = m.ms_bs;
+  if (m.epi) {
+    JN_REQUIRE((use == kGemmDenseScores || use == kGemmDenseEdgeGrad) && m.M == m.N && m.epi_ps && m.epi_part &&
+                   (use == kGemmDenseScores || (m.epi_gds && m.epi_E)) && m.addend == nullptr &&
+                   m.c_nscale == nullptr && m.c_mscale == nullptr,
+               kInvalidArgument, "softsign epilogue needs a square dense score use and its operands");
+    g.epi = 1; g.epi_causal = m.epi_causal ? 1 : 0;
+    g.epi_bias = m.epi_bias; g.epi_ps = m.epi_ps; g.epi_gds = m.epi_gds; g.epi_E = m.epi_E;
+    g.epi_part = m.epi_part;
+  }
   return launch_gemm(g, use, 1, stream);
 }
 

@@ -42,7 +42,17 @@ struct BatchedGemm {
   const float* c_nscale;
   const float* c_mscale; int64_t ms_bs;  // optional: C(m, n) *= c_mscale[m], per batch element at stride ms_bs
   int M, N, K, batch;
+  // softsign epilogue of kGemmDenseScores / kGemmDenseEdgeGrad (M == N): see
+  // GemmArgs in jn_gemm.hip; part is [batch, M, dense_epi_parts(N)]
+  int epi, epi_causal;
+  const float* epi_bias;
+  const float* epi_ps;
+  const float* epi_gds;
+  const float* epi_E;
+  float* epi_part;
 };
+// Partial sums per row that the dense softsign epilogue writes (32 columns each).
+inline int dense_epi_parts(int n) { return (n + 31) / 32; }
 enum GemmUse {
   kGemmProject, kGemmGradInput, kGemmGradWeight,
   kGemmDenseScores, kGemmDenseAggregate, kGemmDenseEdgeGrad, kGemmDenseValueGrad, kGemmDenseTargetGrad,
@@ -153,6 +163,8 @@ int launch_dense_compress(float* S, const float* bias, const float* ps, int B, i
 int launch_dense_compress_backward(float* G, const float* E, const float* gds, const float* ps, int B, int N,
                                    int compress, int causal, float* rowsum, hipStream_t stream);
 int launch_dense_colsum(const float* E, const float* w, int B, int N, float* out, hipStream_t stream);
+// out[row] = sum_t part[row * P + t], t < P (fixed order)
+int launch_dense_part_rowsum(const float* part, int P, int64_t rows, float* out, hipStream_t stream);
 // out[b, j] = sum_i M[b, i, j] a[b, i] (c[b, i] if given), i < Nr, j < Nc, fixed order
 int launch_colsum_rows(const float* M, const float* a, const float* c, int B, int Nr, int Nc, float* out,
                        const char* name, hipStream_t stream);

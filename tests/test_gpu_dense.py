@@ -60,9 +60,19 @@ def _inputs(seed, B, N, D, r):
 @pytest.mark.parametrize("separate_pv", [False, True])
 @pytest.mark.parametrize("N,with_bias", [(64, True), (37, False)])
 def test_dense_forward_backward_matches_oracle(dev, compress, separate_pv, N, with_bias):
+    _check_dense(dev, compress, separate_pv, N, with_bias, B=2, D=24, r=6)
+
+
+@pytest.mark.parametrize("separate_pv", [False, True])
+def test_dense_softsign_more_blocks_than_value_columns(dev, separate_pv):
+    # 300 sources = 10 blocks of 32 columns per row > D = 8 value columns: the
+    # forward computes softsign in its own pass, the backward keeps the fused epilogue
+    _check_dense(dev, "softsign", separate_pv, 300, True, B=2, D=8, r=5)
+
+
+def _check_dense(dev, compress, separate_pv, N, with_bias, B, D, r):
     import jakal_net_native as jn
 
-    B, D, r = 2, 24, 6
     g, state, val, U, V, w = _inputs(4001 + N, B, N, D, r)
     b = torch.tensor(0.15) if with_bias else None
     pv_cpu = torch.randn(B, N, D, generator=g) if separate_pv else val

@@ -68,6 +68,11 @@ def test_dense_small(dev, tile):
     TD.test_dense_forward_backward_matches_oracle(dev, "signed_abs_softmax", True, 37, False)
 
 
+def test_dense_softsign_odd_columns(dev, tile):
+    # 150 columns (not a multiple of 4): the softsign epilogue stores element-wise from the accumulators
+    TD._check_dense(dev, "softsign", True, 150, True, B=2, D=24, r=6)
+
+
 def test_topk_propagation(dev, tile):
     TT.test_propagation_topk_forward_backward_matches_oracle(dev, "softsign", True, 8)
 

@@ -26,7 +26,14 @@ Prints one JSON line:
   kernels      the same figures for every kernel of the step
   cpu_baseline the numpy oracle (fp32) timed on a bounded sample on the host
 
+The top-k select's flops are fp32-equivalent score products (2 r per pair),
+priced against the fp32 MFMA peak.  With --select-mode split-f16 (the
+library default) the MFMA pipe runs three fp16 products for each (hi.hi +
+hi.lo + lo.hi of two-term fp16 operand splits, fp32 accumulation); that
+kernel entry also reports the executed fp16 MFMA rate against its own peak.
+
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload c4-topk] [--no-cpu-baseline]
+                  [--select-mode split-f16|f32] [--gemm-tile 0|64|128]
   python bench.py --calibrate-copy     # plain 1 GiB device copy (counter scale)
 """
 
@@ -45,6 +52,9 @@ sys.path.insert(0, str(ROOT / "jakal-net_amd"))
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+# split-fp16 select: fp16 MFMA products per fp32-equivalent product (hi.hi + hi.lo + lo.hi)
+SPLIT_PRODUCTS = 3
 
 # the headline workload (kept as module constants: the profile summaries use them)
 CONFIG = {"batch": 16, "nodes": 4096, "dim": 512, "rank": 64, "topk": 32}
@@ -91,10 +101,24 @@ def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = F
     return None
 
 
+def split_prep_model(name: str, key_rows: float, r: int) -> tuple[str, float] | None:
+    """The split-fp16 select's two prep kernels over key_rows key rows per launch:
+    a max-|key| pass (reads the keys) and the split (reads them again, writes
+    hi and lo fp16 planes of the rank rounded up to 32)."""
+    rp = -(-r // 32) * 32
+    if name.startswith("select_split_absmax_kernel"):
+        return "hbm", key_rows * 4.0 * r
+    if name.startswith("select_split_keys_kernel"):
+        return "hbm", key_rows * (4.0 * r + 4.0 * rp)
+    return None
+
+
 def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int) -> tuple[str, float] | None:
     """Kernel model of the headline (top-k) workload."""
     if name.startswith("lowrank_topk_select_kernel"):
         return "mfma", 2.0 * B * N * N * r
+    if name.startswith("select_split_"):
+        return split_prep_model(name, B * N, r)
     return edge_kernel_model(name, B * N, B * N * k, D, r, rows_backward_split(N, D))
 
 
@@ -275,6 +299,8 @@ class TransitionC3:
         E, rows = self.edges(), B * (S + Bn)
         if name.startswith("lowrank_topk_select_kernel"):
             return "mfma", 2.0 * B * S * Bn * r * 2  # both directions score S x B pairs
+        if name.startswith("select_split_"):
+            return split_prep_model(name, B * (S + Bn) / 2, r)  # keys: B rows one way, S rows the other
         if name.startswith("route_rows_backward_kernel"):
             # per edge: idx + logit + grad-delta row of the destination + its key row + g_logit write;
             # per source row: its value row, its grad-value write, dq write
@@ -580,6 +606,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c4-topk")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--select-mode", choices=["split-f16", "f32"], default="split-f16",
+                    help="score arithmetic of the top-k select (library default: split-f16)")
     ap.add_argument("--gemm-tile", type=int, choices=[0, 64, 128], default=0,
                     help="force the GEMM workgroup tile (0: chosen per call)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -598,6 +626,7 @@ def main() -> int:
     import jakal_net_native as jn
 
     jn.set_gemm_tile(args.gemm_tile)
+    jn.set_select_mode(jn.SELECT_SPLIT_F16 if args.select_mode == "split-f16" else jn.SELECT_F32)
     wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     op, layer = wl.build(torch, dev)
@@ -656,6 +685,16 @@ def main() -> int:
                 achieved = work / (avg_ms / 1e3) / 1e12
                 entry.update(bound="mfma", flops=work, achieved_TFLOPs=round(achieved, 2),
                              frac=round(achieved / FP32_MFMA_PEAK_TFLOPS, 4))
+                if name.startswith("lowrank_topk_select_kernel"):
+                    if args.select_mode == "split-f16":
+                        # flops count fp32-equivalent score products; the MFMA pipe runs
+                        # SPLIT_PRODUCTS fp16 products for each
+                        f16 = SPLIT_PRODUCTS * achieved
+                        entry.update(arith="split-fp16 MFMA (hi.hi + hi.lo + lo.hi), fp32 accumulate",
+                                     mfma_f16_TFLOPs=round(f16, 2),
+                                     mfma_f16_frac=round(f16 / FP16_MFMA_PEAK_TFLOPS, 4))
+                    else:
+                        entry.update(arith="fp32 MFMA")
         kernels[name] = entry
 
     # HBM-side bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes
@@ -678,6 +717,8 @@ def main() -> int:
         roofline = {"kernel": dom_name, "bound": "mfma", "achieved": dom["achieved_TFLOPs"],
                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
                     "traffic": dom.get("traffic_bytes")}
+        if "arith" in dom:
+            roofline["arith"] = dom["arith"]
 
     result = {
         "metric": wl.metric,

@@ -30,7 +30,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 2. */
+/* ABI revision of this header (bumped on any signature change); this is 3. */
 int jn_abi_version(void);
 
 /*
@@ -54,6 +54,20 @@ int jn_profile_collect(char* buffer, size_t size);
 int jn_set_gemm_tile(int32_t tile);
 
 /*
+ * Score arithmetic of the top-k select (no counterpart in the reference; for
+ * tests and tuning).  mode 0 (the default) computes the low-rank score tiles
+ * on fp16 MFMAs over two-term fp16 splits of the operands: every operand is
+ * scaled by a power of two and written as hi + lo (22 significant bits), and
+ * a score is hi.hi + hi.lo + lo.hi accumulated in fp32, within about
+ * 3 * 2^-22 * sum_r |q_r k_r| of the exact value (fp32 accumulation itself is
+ * within r * 2^-24 of it).  mode 1 computes them on fp32 MFMAs.  Mode 0 needs
+ * the select workspace below (the *_workspace_bytes queries report 0 in
+ * mode 1).  Process-wide; takes effect for later calls, including their
+ * workspace queries.
+ */
+int jn_set_select_mode(int32_t mode);
+
+/*
  * Low-rank score + per-row top-k select, no score matrix materialised.
  *   s[b,i,j] = ((sum_r query[b,i,r]*cq[r] * key[b,j,r]*ck[r]) + bias) / temperature
  * where the scale vector multiplies the query rows when scale_on_query != 0,
@@ -67,7 +81,11 @@ int jn_set_gemm_tile(int32_t tile);
 int jn_lowrank_topk_select(const float* query, int64_t ldq, int64_t query_batch_stride, const float* key,
                            int64_t ldk, int64_t key_batch_stride, const float* scale, int32_t scale_on_query,
                            const float* bias, float temperature, int64_t batch, int64_t nq, int64_t nk,
-                           int64_t rank, int64_t topk, int32_t* out_index, float* out_score, jn_stream_t stream);
+                           int64_t rank, int64_t topk, int32_t* out_index, float* out_score, void* workspace,
+                           size_t workspace_bytes, jn_stream_t stream);
+
+/* Workspace of jn_lowrank_topk_select (split key rows; 0 in select mode 1). */
+size_t jn_lowrank_topk_select_workspace_bytes(int64_t batch, int64_t nk, int64_t rank);
 
 /*
  * SparsePropagation(sparse_type="topk", LowRankBilinearPairwise) forward.
@@ -87,7 +105,10 @@ int jn_propagation_topk_forward(const float* layer_val, const float* projected_s
                                 const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                 int64_t rank, int64_t topk, int32_t compress_kind, float* delta_state,
                                 float* delta_val, float* projections, int32_t* topk_index, float* topk_score,
-                                jn_stream_t stream);
+                                void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+/* Workspace of jn_propagation_topk_forward (the select's; 0 in select mode 1). */
+size_t jn_propagation_topk_forward_workspace_bytes(int64_t batch, int64_t nodes, int64_t rank);
 
 /* Workspace needed by jn_propagation_topk_backward. */
 size_t jn_propagation_topk_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,

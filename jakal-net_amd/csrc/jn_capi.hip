@@ -143,6 +143,8 @@ struct TransitionScratch {
   float* part_c;
   float* stage;
   float* splitk;
+  void* select_ws;  // split-fp16 key rows of the forward's select
+  size_t select_ws_bytes;
   size_t bytes;
 };
 
@@ -166,6 +168,8 @@ TransitionScratch carve_transition(void* base, size_t size, int64_t B, int64_t N
   const size_t sk = std::max(gemm_grad_weight_workspace((int)r, (int)Dsrc, (int)(B * Ns)),
                              gemm_grad_weight_workspace((int)r, (int)Ddst, (int)(B * Nd)));
   s.splitk = ws.take<float>(sk / sizeof(float));
+  s.select_ws_bytes = select_workspace_bytes(B, Nd, r);
+  s.select_ws = ws.take<char>(s.select_ws_bytes);
   s.bytes = ws.used;
   return s;
 }
@@ -395,7 +399,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 2; }
+int jn_abi_version(void) { return 3; }
 
 int jn_profile_enable(int32_t on) {
   std::lock_guard<std::mutex> lock(jakal::g_prof_mu);
@@ -413,6 +417,17 @@ int jn_set_gemm_tile(int32_t tile) {
              (int)tile);
   jakal::set_gemm_tile(tile);
   return kOk;
+}
+
+int jn_set_select_mode(int32_t mode) {
+  JN_REQUIRE(mode == jakal::kSelectSplitF16 || mode == jakal::kSelectF32, kInvalidArgument,
+             "select mode must be 0 (split fp16) or 1 (fp32), got %d", (int)mode);
+  jakal::set_select_mode(mode);
+  return kOk;
+}
+
+size_t jn_lowrank_topk_select_workspace_bytes(int64_t batch, int64_t nk, int64_t rank) {
+  return jakal::select_workspace_bytes(batch, nk, rank);
 }
 
 int jn_profile_collect(char* buffer, size_t size) {
@@ -444,7 +459,8 @@ int jn_profile_collect(char* buffer, size_t size) {
 int jn_lowrank_topk_select(const float* query, int64_t ldq, int64_t query_batch_stride, const float* key,
                            int64_t ldk, int64_t key_batch_stride, const float* scale, int32_t scale_on_query,
                            const float* bias, float temperature, int64_t batch, int64_t nq, int64_t nk,
-                           int64_t rank, int64_t topk, int32_t* out_index, float* out_score, jn_stream_t stream) {
+                           int64_t rank, int64_t topk, int32_t* out_index, float* out_score, void* workspace,
+                           size_t workspace_bytes, jn_stream_t stream) {
   JN_REQUIRE(query && key && out_index && out_score, kInvalidArgument, "null tensor pointer");
   JN_REQUIRE(batch >= 1 && nq >= 1 && nk >= 1, kInvalidArgument, "batch, nq, nk must be positive");
   JN_REQUIRE(fits_int(batch * nq * topk), kUnsupported, "problem too large");
@@ -466,6 +482,8 @@ int jn_lowrank_topk_select(const float* query, int64_t ldq, int64_t query_batch_
   a.k = (int)topk;
   a.out_idx = out_index;
   a.out_score = out_score;
+  a.ws = workspace;
+  a.ws_bytes = workspace_bytes;
   return launch_topk_select(a, static_cast<hipStream_t>(stream));
 }
 
@@ -474,7 +492,7 @@ int jn_propagation_topk_forward(const float* layer_val, const float* projected_s
                                 const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                 int64_t rank, int64_t topk, int32_t compress_kind, float* delta_state,
                                 float* delta_val, float* projections, int32_t* topk_index, float* topk_score,
-                                jn_stream_t stream) {
+                                void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
   if (rc) return rc;
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
@@ -505,6 +523,8 @@ int jn_propagation_topk_forward(const float* layer_val, const float* projected_s
   s.k = k;
   s.out_idx = topk_index;
   s.out_score = topk_score;
+  s.ws = workspace;
+  s.ws_bytes = workspace_bytes;
   rc = launch_topk_select(s, st);
   if (rc) return rc;
 
@@ -523,6 +543,10 @@ int jn_propagation_topk_forward(const float* layer_val, const float* projected_s
   f.out_state = delta_state;
   f.out_val = delta_val;
   return launch_rows_forward(f, st);
+}
+
+size_t jn_propagation_topk_forward_workspace_bytes(int64_t batch, int64_t nodes, int64_t rank) {
+  return jakal::select_workspace_bytes(batch, nodes, rank);
 }
 
 size_t jn_propagation_topk_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
@@ -694,6 +718,8 @@ int jn_transition_topk_forward(const float* sender_strength, const float* src_va
     a.k = (int)k;
     a.out_idx = route_index;
     a.out_score = route_logit;
+    a.ws = s.select_ws;
+    a.ws_bytes = s.select_ws_bytes;
     rc = launch_topk_select(a, st);
   } else {
     WindowScoreArgs w{};

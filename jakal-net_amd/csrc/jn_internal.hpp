@@ -18,9 +18,24 @@ struct SelectArgs {
   int B, Nq, Nk, r, k;
   int32_t* out_idx;     // [B, Nq, k]
   float* out_score;     // [B, Nq, k]
+  void* ws;             // scratch of select_workspace_bytes(B, Nk, r) bytes (split mode)
+  size_t ws_bytes;
+  // set by launch_topk_select from ws (split mode): split key rows (fp16 bits)
+  // and one key exponent per batch element
+  const uint16_t* split_key;
+  const int* split_exp;
 };
 int launch_topk_select(const SelectArgs& a, hipStream_t stream);
 constexpr int kSelectMaxK = 64;
+// Score arithmetic of the select: kSelectSplitF16 (default) runs the score
+// tiles on fp16 MFMAs over two-term fp16 splits of the operands (about 22
+// significant bits per operand, fp32 accumulation); kSelectF32 runs them on
+// fp32 MFMAs.  The split needs select_workspace_bytes() of scratch.
+constexpr int kSelectSplitF16 = 0;
+constexpr int kSelectF32 = 1;
+int select_mode();
+void set_select_mode(int mode);
+size_t select_workspace_bytes(int64_t B, int64_t Nk, int64_t r);
 
 // ---- fp32 MFMA GEMMs (jn_gemm.hip) ----------------------------------------
 int gemm_project(const float* X, int64_t ldx, const float* W0, const float* W1, int split, int64_t ldw, float* C,

@@ -362,11 +362,93 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kep
   wave_lds_sync();
 }
 
+// ---- split-fp16 score operands ------------------------------------------------
+// A value x, first scaled by a power of two 2^e that puts the largest magnitude
+// of its group in [2^14, 2^15), is carried as hi = fp16(x), lo = fp16(x - hi):
+// |x - hi - lo| <= 2^-22 |x| with no fp16 overflow.  A score is then
+//   q.k = 2^-(eq+ek) * (hi_q.hi_k + hi_q.lo_k + lo_q.hi_k)   (+ lo_q.lo_k, dropped)
+// with each product exact in fp32 and an error of about 3 * 2^-22 sum_r |q_r k_r|,
+// the size of fp32 accumulation error over a rank-64 dot product.  Keys share
+// one exponent per batch element (so a score needs no per-key factor); a query
+// row has its own, applied in registers.
+// Split key rows: [hi: RP halves][lo: RP halves], RP = r rounded up to 32 (the
+// K extent of one v_mfma_f32_16x16x32_f16); ranks past r are zero.
+constexpr int kSplitRows = 64;  // key rows per block of the two prep kernels
+
+__device__ __forceinline__ int split_exponent(float maxabs) {
+  int e = 0;
+  if (!(maxabs > 0.0f) || !(maxabs < INFINITY)) return 0;  // zeros, inf, NaN: unscaled
+  (void)frexpf(maxabs, &e);                                // maxabs in [2^(e-1), 2^e)
+  return 15 - e;
+}
+
+__device__ __forceinline__ float block_max_256(float m) {
+  __shared__ float s_max[4];
+  m = wave_max_f(m);
+  if (lane_id() == 0) s_max[threadIdx.x / kWave] = m;
+  __syncthreads();
+  return fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+}
+
+// partial[b][blk] = max |key| over rows [64 blk, 64 blk + 64) of batch element b.
+__global__ __launch_bounds__(256) void select_split_absmax_kernel(const float* __restrict__ key, int64_t ldk,
+                                                                  int64_t kbs, int Nk, int r, int nblk,
+                                                                  float* __restrict__ partial) {
+  const int blk = blockIdx.x, b = blockIdx.y;
+  const int row0 = blk * kSplitRows;
+  const int rows = min(kSplitRows, Nk - row0);
+  const float* kb = key + (int64_t)b * kbs + (int64_t)row0 * ldk;
+  float m = 0.0f;
+  for (int e = threadIdx.x; e < rows * r; e += 256) {
+    const int row = e / r;
+    m = fmaxf(m, fabsf(kb[(int64_t)row * ldk + (e - row * r)]));
+  }
+  m = block_max_256(m);
+  if (threadIdx.x == 0) partial[(int64_t)b * nblk + blk] = m;
+}
+
+// Writes the split rows of [64 blk, 64 blk + 64) and, from block 0, the batch
+// element's key exponent.  Every block reduces the same partials in the same
+// order, so all agree on the exponent.
+__global__ __launch_bounds__(256) void select_split_keys_kernel(const float* __restrict__ key, int64_t ldk,
+                                                                int64_t kbs, int Nk, int r, int RP, int nblk,
+                                                                const float* __restrict__ partial,
+                                                                _Float16* __restrict__ split, int* __restrict__ kexp) {
+  const int blk = blockIdx.x, b = blockIdx.y;
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < nblk; i += 256) m = fmaxf(m, partial[(int64_t)b * nblk + i]);
+  const int ek = split_exponent(block_max_256(m));
+  if (blk == 0 && threadIdx.x == 0) kexp[b] = ek;
+  const int row0 = blk * kSplitRows;
+  const int rows = min(kSplitRows, Nk - row0);
+  const float* kb = key + (int64_t)b * kbs + (int64_t)row0 * ldk;
+  _Float16* out = split + ((int64_t)b * Nk + row0) * (2 * RP);
+  for (int e = threadIdx.x; e < rows * RP; e += 256) {
+    const int row = e / RP;
+    const int c = e - row * RP;
+    const float x = c < r ? ldexpf(kb[(int64_t)row * ldk + c], ek) : 0.0f;
+    const _Float16 hi = (_Float16)x;
+    out[(int64_t)row * 2 * RP + c] = hi;
+    out[(int64_t)row * 2 * RP + RP + c] = (_Float16)(x - (float)hi);
+  }
+}
+
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ halfx8 as_halfx8(float a, float b, float c, float d) {
+  return __builtin_bit_cast(halfx8, floatx4{a, b, c, d});
+}
+
 // VEC: r == 4*RQ and 16-byte aligned key rows -> float4 key loads (RQ % 4 == 0).
-template <int RQ, bool VEC, int KEEP>
-__global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kernel(SelectArgs a) {
+// KS > 0: split-fp16 scores over KS K-steps of 32 ranks (RQ and VEC unused);
+// the keys are the split rows in a.ws, the queries are split in registers.
+template <int RQ, bool VEC, int KEEP, int KS>
+__global__ __launch_bounds__(256, (KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2) void lowrank_topk_select_kernel(SelectArgs a) {
   constexpr int CAP = sel_lane_cap(KEEP);
+  constexpr bool SPLIT = KS > 0;
   constexpr bool V4 = VEC && RQ % 4 == 0;
+  constexpr int FR = SPLIT ? 8 * KS : RQ;  // key fragment registers per tile
+  constexpr int RP = 32 * KS;              // split row: ranks per plane
 
   __shared__ __align__(16) float s_slot_s[kSelRows * kSelScoreStride];
   __shared__ __align__(16) uint16_t s_slot_i[kSelRows * kSelIndexStride];
@@ -394,23 +476,55 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
   const bool row_ok = my_row < a.Nq;
   // unconditional loads (invalid rows and ranks read row 0 / rank 0 and are
   // zeroed after), so they all issue before one wait
-  float qf[RQ];
+  // fp32 path: lane (g, col) holds ranks g*RQ + s of row col (K-step s).
+  // Split path: ranks 32 s + 8 g + e (K-step s, e < 8), as hi/lo halves, and
+  // the row's score exponent E: MFMA results are the scores times 2^E.
+  constexpr int QN = SPLIT ? 8 * KS : RQ;
+  float qf[QN];
   {
     const float* qrow = qb + (int64_t)(row_ok ? my_row : 0) * a.ldq;
-    float qs[RQ];
+    float qs[QN];
 #pragma unroll
-    for (int s = 0; s < RQ; ++s) {
-      const int rr = g * RQ + s;
+    for (int s = 0; s < QN; ++s) {
+      const int rr = SPLIT ? 32 * (s / 8) + 8 * g + (s % 8) : g * RQ + s;
       qf[s] = qrow[rr < a.r ? rr : 0];
       qs[s] = a.scale ? a.scale[rr < a.r ? rr : 0] : 1.0f;
     }
 #pragma unroll
-    for (int s = 0; s < RQ; ++s) qf[s] = (row_ok && g * RQ + s < a.r) ? qf[s] * qs[s] : 0.0f;
+    for (int s = 0; s < QN; ++s) {
+      const int rr = SPLIT ? 32 * (s / 8) + 8 * g + (s % 8) : g * RQ + s;
+      qf[s] = (row_ok && rr < a.r) ? qf[s] * qs[s] : 0.0f;
+    }
+  }
+  halfx8 qh[SPLIT ? KS : 1], ql[SPLIT ? KS : 1];
+  int score_exp = 0;  // E (split path)
+  if constexpr (SPLIT) {
+    float m = 0.0f;
+#pragma unroll
+    for (int s = 0; s < QN; ++s) m = fmaxf(m, fabsf(qf[s]));
+    m = fmaxf(m, xor16_f(m));
+    m = fmaxf(m, xor32_f(m));
+    const int eq = split_exponent(m);
+    score_exp = eq + a.split_exp[b];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = ldexpf(qf[8 * s + e], eq);
+        const _Float16 hi = (_Float16)x;
+        qh[s][e] = hi;
+        ql[s][e] = (_Float16)(x - (float)hi);
+      }
+    }
   }
   const float bias = a.bias ? a.bias[0] : 0.0f;
   // (dot + bias) / T as a multiply by the reciprocal: exact for T == 1, within
   // 1.5 ulp of the division otherwise
   const float inv_temp = 1.0f / a.temperature;
+  // Split path without bias or temperature: rows are filtered and merged on
+  // the scaled scores (scaling a row by 2^E keeps its order and its ties) and
+  // only the k winners are scaled back.
+  const bool scaled_domain = SPLIT && inv_temp == 1.0f && bias == 0.0f;
 
   // ---- key fragments straight from memory: every wave streams the keys on its
   // own (no LDS staging, no workgroup barrier in the loop), so a wave that
@@ -421,20 +535,38 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
   // chunk loads while the current one is scored.
   // The resource of a chunk ends after its last row below Nk, so rows past
   // the end read as zeros with loop-invariant lane offsets.
-  float kx[2][kSelTiles][RQ];
+  float kx[2][kSelTiles][FR];
   uint32_t kbase_off[kSelTiles];
+  // split rows: 4 RP bytes each; lane group g reads ranks [8g, 8g + 8) of every K-step
 #pragma unroll
-  for (int t = 0; t < kSelTiles; ++t) kbase_off[t] = (uint32_t)((16 * t + col) * ldk + g * RQ) * 4u;
+  for (int t = 0; t < kSelTiles; ++t)
+    kbase_off[t] = SPLIT ? (uint32_t)((16 * t + col) * 4 * RP + 16 * g) : (uint32_t)((16 * t + col) * ldk + g * RQ) * 4u;
+  const _Float16* split_b =
+      SPLIT ? reinterpret_cast<const _Float16*>(a.split_key) + (int64_t)b * a.Nk * 2 * RP : nullptr;
   auto load_keys = [&](auto SET, int c) {
     constexpr int S = decltype(SET)::value;
     const int c0 = c * kSelChunk;
     const int rows = max(0, min(kSelChunk, a.Nk - c0));
     // uniform (readfirstlane keeps the resource in SGPRs)
-    const uint32_t nrec = __builtin_amdgcn_readfirstlane((uint32_t)(rows * ldk) * 4u);
-    const auto rs = make_rsrc(kbase + (int64_t)c0 * ldk, nrec);
+    const uint32_t nrec = __builtin_amdgcn_readfirstlane(SPLIT ? (uint32_t)(rows * 4 * RP) : (uint32_t)(rows * ldk) * 4u);
+    const auto rs = SPLIT ? make_rsrc(split_b + (int64_t)c0 * 2 * RP, nrec) : make_rsrc(kbase + (int64_t)c0 * ldk, nrec);
 #pragma unroll
     for (int t = 0; t < kSelTiles; ++t) {
-      if constexpr (V4) {
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const float4 h = buf_load4(rs, kbase_off[t] + 64u * s);
+          const float4 l = buf_load4(rs, kbase_off[t] + 64u * s + 2u * RP);
+          kx[S][t][8 * s + 0] = h.x;
+          kx[S][t][8 * s + 1] = h.y;
+          kx[S][t][8 * s + 2] = h.z;
+          kx[S][t][8 * s + 3] = h.w;
+          kx[S][t][8 * s + 4] = l.x;
+          kx[S][t][8 * s + 5] = l.y;
+          kx[S][t][8 * s + 6] = l.z;
+          kx[S][t][8 * s + 7] = l.w;
+        }
+      } else if constexpr (V4) {
 #pragma unroll
         for (int q = 0; q < RQ / 4; ++q) {
           const float4 v = buf_load4(rs, kbase_off[t] + 16u * q);
@@ -448,6 +580,10 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
         for (int q = 0; q < RQ; ++q) kx[S][t][q] = buf_load1(rs, (g * RQ + q < a.r) ? kbase_off[t] + 4u * q : kOobOffset);
       }
     }
+    // keep every load of the chunk ahead of the MFMAs that follow: left alone,
+    // the scheduler sinks most of them below the current chunk's MFMAs, and
+    // the prefetch then has only the filter to hide its latency behind
+    __builtin_amdgcn_sched_barrier(0);
   };
   constexpr std::integral_constant<int, 0> kSet0{};
   constexpr std::integral_constant<int, 1> kSet1{};
@@ -469,17 +605,43 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
     floatx4 acc[kSelTiles];
 #pragma unroll
     for (int t = 0; t < kSelTiles; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (SPLIT) {
+      // small products first: lo.hi + hi.lo, then hi.hi
 #pragma unroll
-    for (int q = 0; q < RQ; ++q)
+      for (int s = 0; s < KS; ++s) {
 #pragma unroll
-      for (int t = 0; t < kSelTiles; ++t)
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[S][t][q], qf[q], acc[t], 0, 0, 0);
+        for (int t = 0; t < kSelTiles; ++t) {
+          const halfx8 kh = as_halfx8(kx[S][t][8 * s], kx[S][t][8 * s + 1], kx[S][t][8 * s + 2], kx[S][t][8 * s + 3]);
+          const halfx8 kl =
+              as_halfx8(kx[S][t][8 * s + 4], kx[S][t][8 * s + 5], kx[S][t][8 * s + 6], kx[S][t][8 * s + 7]);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[s], acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[s], acc[t], 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < kSelTiles; ++t) {
+          const halfx8 kh = as_halfx8(kx[S][t][8 * s], kx[S][t][8 * s + 1], kx[S][t][8 * s + 2], kx[S][t][8 * s + 3]);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[s], acc[t], 0, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < RQ; ++q)
+#pragma unroll
+        for (int t = 0; t < kSelTiles; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[S][t][q], qf[q], acc[t], 0, 0, 0);
+    }
 
     // -- threshold filter: lane holds keys c0 + 16t + 4g + v of its row --
     float sc[kSelLaneKeys];
 #pragma unroll
     for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = acc[u >> 2][u & 3];
-    if (inv_temp != 1.0f) {  // uniform
+    if (SPLIT && !scaled_domain) {  // uniform
+#pragma unroll
+      for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = ldexpf(sc[u], -score_exp);
+    }
+    if (scaled_domain) {
+      // compared as they are
+    } else if (inv_temp != 1.0f) {  // uniform
 #pragma unroll
       for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = (sc[u] + bias) * inv_temp;
     } else if (bias != 0.0f) {
@@ -559,6 +721,7 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
       vi = s_slot_i[slot * kSelIndexStride + lane];
     }
     bitonic_sort64_desc(vs, vi);
+    if (scaled_domain) vs = ldexpf(vs, -readlane_i(score_exp, t));
     if (lane < k) {
       const int64_t o = ((int64_t)b * a.Nq + row) * k + lane;
       a.out_idx[o] = vi;
@@ -570,15 +733,53 @@ __global__ __launch_bounds__(256, RQ > 16 ? 1 : 2) void lowrank_topk_select_kern
 template <int RQ>
 static void launch_rq(const SelectArgs& a, bool vec, dim3 grid, hipStream_t stream) {
   if (a.k <= 32) {
-    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 32>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 32>), grid, dim3(256), 0, stream, a);
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 32, 0>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 32, 0>), grid, dim3(256), 0, stream, a);
   } else {
-    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 64>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 64>), grid, dim3(256), 0, stream, a);
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 64, 0>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 64, 0>), grid, dim3(256), 0, stream, a);
   }
 }
 
-int launch_topk_select(const SelectArgs& a, hipStream_t stream) {
+template <int KS>
+static void launch_split(const SelectArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 32, KS>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 64, KS>), grid, dim3(256), 0, stream, a);
+}
+
+namespace {
+int g_select_mode = kSelectSplitF16;
+
+int split_ranks(int64_t r) { return (int)((r + 31) / 32) * 32; }
+
+struct SelectScratch {
+  uint16_t* split;  // [B, Nk, 2 RP] fp16 bits
+  int* kexp;        // [B]
+  float* partial;   // [B, ceil(Nk / kSplitRows)]
+  size_t bytes;
+};
+
+SelectScratch carve_select(void* base, size_t size, int64_t B, int64_t Nk, int64_t r) {
+  Workspace ws(base, size);
+  SelectScratch s{};
+  s.split = ws.take<uint16_t>(B * Nk * 2 * split_ranks(r));
+  s.kexp = ws.take<int>(B);
+  s.partial = ws.take<float>(B * ((Nk + kSplitRows - 1) / kSplitRows));
+  s.bytes = ws.used;
+  return s;
+}
+}  // namespace
+
+int select_mode() { return g_select_mode; }
+void set_select_mode(int mode) { g_select_mode = mode; }
+
+size_t select_workspace_bytes(int64_t B, int64_t Nk, int64_t r) {
+  if (g_select_mode != kSelectSplitF16 || B < 1 || Nk < 1 || r < 1) return 0;
+  return carve_select(nullptr, 0, B, Nk, r).bytes;
+}
+
+int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
+  SelectArgs a = a_in;
   JN_REQUIRE(a.k >= 1 && a.k <= kSelectMaxK, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)", kSelectMaxK,
              a.k);
   JN_REQUIRE(a.k < a.Nk, kInvalidArgument, "top-k select needs k < key count (k=%d, Nk=%d)", a.k, a.Nk);
@@ -591,6 +792,39 @@ int launch_topk_select(const SelectArgs& a, hipStream_t stream) {
   const int64_t blocks = (int64_t)tiles * a.B;
   JN_REQUIRE(blocks > 0 && blocks < (1LL << 31), kInvalidArgument, "bad grid size");
   dim3 grid((unsigned)blocks);
+
+  if (g_select_mode == kSelectSplitF16) {
+    const SelectScratch s = carve_select(a.ws, a.ws_bytes, a.B, a.Nk, a.r);
+    JN_REQUIRE(a.ws != nullptr && s.bytes <= a.ws_bytes, kWorkspaceTooSmall,
+               "select workspace too small: need %zu bytes, got %zu", s.bytes, a.ws_bytes);
+    const int RP = split_ranks(a.r);
+    const int nblk = (a.Nk + kSplitRows - 1) / kSplitRows;
+    dim3 pgrid((unsigned)nblk, (unsigned)a.B);
+    {
+      JN_PROFILE("select_split_absmax_kernel", stream);
+      hipLaunchKernelGGL(select_split_absmax_kernel, pgrid, dim3(256), 0, stream, a.key, a.ldk, a.k_batch_stride,
+                         a.Nk, a.r, nblk, s.partial);
+      JN_LAUNCH_CHECK();
+    }
+    {
+      JN_PROFILE("select_split_keys_kernel", stream);
+      hipLaunchKernelGGL(select_split_keys_kernel, pgrid, dim3(256), 0, stream, a.key, a.ldk, a.k_batch_stride, a.Nk,
+                         a.r, RP, nblk, s.partial, reinterpret_cast<_Float16*>(s.split), s.kexp);
+      JN_LAUNCH_CHECK();
+    }
+    a.split_key = s.split;
+    a.split_exp = s.kexp;
+    JN_PROFILE("lowrank_topk_select_kernel", stream);
+    switch (RP / 32) {
+      case 1: launch_split<1>(a, grid, stream); break;
+      case 2: launch_split<2>(a, grid, stream); break;
+      case 3: launch_split<3>(a, grid, stream); break;
+      default: launch_split<4>(a, grid, stream); break;
+    }
+    JN_LAUNCH_CHECK();
+    return kOk;
+  }
+
   int rq = (a.r + 3) / 4;
   rq = rq <= 1 ? 1 : rq <= 2 ? 2 : rq <= 4 ? 4 : rq <= 8 ? 8 : rq <= 16 ? 16 : 32;
   const bool vec = (a.r == 4 * rq) && (a.ldk % 4 == 0) && (a.k_batch_stride % 4 == 0) &&

@@ -48,14 +48,17 @@ _declare("jn_abi_version", [])
 _declare("jn_profile_enable", [_I32])
 _declare("jn_profile_collect", [ctypes.c_char_p, _SZ])
 _declare("jn_set_gemm_tile", [_I32])
+_declare("jn_set_select_mode", [_I32])
 _declare(
     "jn_lowrank_topk_select",
-    [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _F, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
+    [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _F, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
 )
+_declare("jn_lowrank_topk_select_workspace_bytes", [_I64] * 3, _SZ)
 _declare(
     "jn_propagation_topk_forward",
-    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P],
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
+_declare("jn_propagation_topk_forward_workspace_bytes", [_I64] * 3, _SZ)
 _declare("jn_propagation_topk_workspace_bytes", [_I64, _I64, _I64, _I64, _I64, _I64], _SZ)
 _declare(
     "jn_propagation_topk_backward",
@@ -153,6 +156,16 @@ def set_gemm_tile(tile: int = 0) -> None:
     _check(_LIB.jn_set_gemm_tile(int(tile)))
 
 
+SELECT_SPLIT_F16 = 0
+SELECT_F32 = 1
+
+
+def set_select_mode(mode: int = SELECT_SPLIT_F16) -> None:
+    """Score arithmetic of the top-k select for later calls: SELECT_SPLIT_F16 (default, fp16 MFMAs over
+    two-term fp16 operand splits, fp32 accumulation) or SELECT_F32 (fp32 MFMAs)."""
+    _check(_LIB.jn_set_select_mode(int(mode)))
+
+
 def profile_collect() -> dict[str, tuple[int, float]]:
     """Wait for the recorded kernels; return {kernel: (launches, total_ms)} and clear."""
     buf = ctypes.create_string_buffer(1 << 16)
@@ -245,13 +258,16 @@ class _PropagationEdges(torch.autograd.Function):
             proj = torch.empty(B * N, 2 * r, device=dev, dtype=torch.float32)
             idx = torch.empty(B, N, k, device=dev, dtype=torch.int32)
             score = torch.empty(B, N, k, device=dev, dtype=torch.float32)
-            _check(
-                fwd(
-                    _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
-                    B, N, Din, Dout, r, param, compress,
-                    _ptr(ds), _ptr(dv), _ptr(proj), _ptr(idx), _ptr(score), _stream(dev),
-                )
-            )
+            args = [
+                _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
+                B, N, Din, Dout, r, param, compress,
+                _ptr(ds), _ptr(dv), _ptr(proj), _ptr(idx), _ptr(score),
+            ]
+            if mode == "topk":  # the select's scratch
+                ws_bytes = int(_LIB.jn_propagation_topk_forward_workspace_bytes(B, N, r))
+                ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+                args += [_ptr(ws), ws_bytes]
+            _check(fwd(*args, _stream(dev)))
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, idx, score)
         ctx.meta = (mode, param, compress, pv_is_x, bias is not None)
         ctx.mark_non_differentiable(idx, score)
@@ -911,10 +927,12 @@ def low_rank_topk_select(
     sc = _f32(scale)
     bi = _f32(bias)
     with torch.cuda.device(dev):
+        ws_bytes = int(_LIB.jn_lowrank_topk_select_workspace_bytes(B, Nk, r))
+        ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
         _check(
             _LIB.jn_lowrank_topk_select(
                 _ptr(q), r, Nq * r, _ptr(kk), r, Nk * r, _ptr(sc), 1 if scale_on_query else 0, _ptr(bi),
-                float(temperature), B, Nq, Nk, r, topk, _ptr(idx), _ptr(score), _stream(dev),
+                float(temperature), B, Nq, Nk, r, topk, _ptr(idx), _ptr(score), _ptr(ws), ws_bytes, _stream(dev),
             )
         )
     return idx, score

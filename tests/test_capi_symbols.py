@@ -41,9 +41,9 @@ def test_error_channel_and_abi_version_without_gpu():
     # argument validation runs on the host before any device call
     P, I64, I32, F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
     fn = lib.jn_lowrank_topk_select
-    fn.argtypes = [P, I64, I64, P, I64, I64, P, I32, P, F, I64, I64, I64, I64, I64, P, P, P]
+    fn.argtypes = [P, I64, I64, P, I64, I64, P, I32, P, F, I64, I64, I64, I64, I64, P, P, P, ctypes.c_size_t, P]
     fn.restype = ctypes.c_int
-    rc = fn(None, 4, 0, None, 4, 0, None, 0, None, 1.0, 1, 8, 8, 4, 2, None, None, None)
+    rc = fn(None, 4, 0, None, 4, 0, None, 0, None, 1.0, 1, 8, 8, 4, 2, None, None, None, 0, None)
     assert rc != 0
     assert b"null" in lib.jn_last_error()
     ws = lib.jn_propagation_topk_workspace_bytes
@@ -51,3 +51,24 @@ def test_error_channel_and_abi_version_without_gpu():
     ws.restype = ctypes.c_size_t
     # dP [M, 2r] alone is 33.5 MB at B=16, N=4096, r=64
     assert ws(16, 4096, 512, 512, 64, 32) > 16 * 4096 * 128 * 4
+
+
+def test_select_mode_sets_the_forward_workspace_without_gpu():
+    lib = ctypes.CDLL(str(LIB))
+    I64 = ctypes.c_int64
+    lib.jn_set_select_mode.argtypes = [ctypes.c_int32]
+    for name in ("jn_propagation_topk_forward_workspace_bytes", "jn_lowrank_topk_select_workspace_bytes"):
+        getattr(lib, name).argtypes = [I64] * 3
+        getattr(lib, name).restype = ctypes.c_size_t
+    fwd = lib.jn_propagation_topk_forward_workspace_bytes
+    try:
+        assert lib.jn_set_select_mode(0) == 0
+        # split key rows: hi and lo fp16 planes of the rank rounded up to 32
+        assert fwd(16, 4096, 64) >= 16 * 4096 * 2 * 64 * 2
+        assert fwd(2, 100, 20) >= 2 * 100 * 2 * 32 * 2
+        assert lib.jn_lowrank_topk_select_workspace_bytes(16, 4096, 64) == fwd(16, 4096, 64)
+        assert lib.jn_set_select_mode(1) == 0
+        assert fwd(16, 4096, 64) == 0
+        assert lib.jn_set_select_mode(7) != 0
+    finally:
+        lib.jn_set_select_mode(0)

@@ -1,0 +1,131 @@
+"""Both score arithmetics of the top-k select against the oracle.
+
+The per-op tests run the default split-fp16 select (fp16 MFMAs over two-term
+fp16 splits of power-of-two-scaled operands, fp32 accumulation).  These tests
+cover the fp32-MFMA select (jn_set_select_mode(1)) on the same select, top-k
+propagation and transition cases, and the split path on what its scaling has
+to survive: key and query rows whose magnitudes span many octaves, all-zero
+rows, ranks that are not a multiple of the 32-rank K-step, and bias and
+temperature on the unscaled-domain path.  Tolerances are the hot path's
+(index parity where the k-th/(k+1)-th gap exceeds 1e-5, values rtol 1e-4 /
+atol 1e-5).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import test_gpu_topk as TT
+import test_gpu_transition as TR
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import jakal_net_native  # noqa: F401
+
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(params=["split_f16", "f32"])
+def mode(request):
+    import jakal_net_native as jn
+
+    jn.set_select_mode(jn.SELECT_SPLIT_F16 if request.param == "split_f16" else jn.SELECT_F32)
+    yield request.param
+    jn.set_select_mode(jn.SELECT_SPLIT_F16)
+
+
+@pytest.fixture
+def f32_mode():
+    import jakal_net_native as jn
+
+    jn.set_select_mode(jn.SELECT_F32)
+    yield
+    jn.set_select_mode(jn.SELECT_SPLIT_F16)
+
+
+def _select(dev, q, key, scale, bias, scale_on_query, temp, k):
+    import jakal_net_native as jn
+
+    idx, score = jn.low_rank_topk_select(q.to(dev), key.to(dev), None if scale is None else scale.to(dev),
+                                         None if bias is None else bias.to(dev), scale_on_query, temp, k)
+    sq = q.double().numpy() * (scale.double().numpy() if (scale is not None and scale_on_query) else 1.0)
+    sk = key.double().numpy() * (scale.double().numpy() if (scale is not None and not scale_on_query) else 1.0)
+    ref = (sq @ np.swapaxes(sk, 1, 2) + (0.0 if bias is None else float(bias))) / temp
+    return idx.cpu().numpy(), score.cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("r,k,Nq,Nk", [(64, 32, 200, 333), (20, 8, 130, 1024), (100, 5, 64, 97), (64, 64, 257, 2000),
+                                       (128, 16, 64, 700), (33, 33, 70, 500)])
+def test_select_both_modes(dev, mode, r, k, Nq, Nk):
+    g = torch.Generator().manual_seed(300 + r + k)
+    # O(1) scores: the regime of the absolute 1e-5 index and k-th score checks
+    q = torch.randn(2, Nq, r, generator=g) * 0.3
+    key = torch.randn(2, Nk, r, generator=g) * 0.3
+    scale = torch.rand(r, generator=g) + 0.5
+    for scale_on_query, temp, bias in ((False, 1.0, None), (True, 1.7, torch.tensor(0.25)),
+                                       (False, 1.0, torch.tensor(-0.5))):
+        idx, score, ref = _select(dev, q, key, scale, bias, scale_on_query, temp, k)
+        TT._check_select(idx, score, ref, k)
+
+
+@pytest.mark.parametrize("Nk", [200, 2100])
+def test_select_ties_both_modes(dev, mode, Nk):
+    import jakal_net_native as jn
+
+    q = torch.randn(1, 64, 8)
+    key = torch.ones(1, Nk, 8)
+    idx, _ = jn.low_rank_topk_select(q.to(dev), key.to(dev), None, None, False, 1.0, 5)
+    assert (idx.cpu() == torch.arange(5, dtype=torch.int32)).all()
+
+
+def test_select_wide_row_magnitudes(dev, mode):
+    """Key rows spread over 2^-20 .. 2^20 and query rows over 2^-30 .. 2^30
+    (each batch element gets its own key exponent, each query row its own);
+    some query and key rows are all zero."""
+    g = torch.Generator().manual_seed(4242)
+    B, Nq, Nk, r, k = 2, 96, 1500, 64, 16
+    q = torch.randn(B, Nq, r, generator=g) * torch.pow(2.0, torch.randint(-30, 31, (B, Nq, 1), generator=g).float())
+    key = torch.randn(B, Nk, r, generator=g) * torch.pow(2.0, torch.randint(-20, 21, (B, Nk, 1), generator=g).float())
+    key[1] *= 2.0 ** 40  # a batch element on another scale altogether
+    q[0, 5] = 0.0
+    key[0, 100:140] = 0.0
+    idx, score, ref = _select(dev, q, key, None, None, False, 1.0, k)
+    # relative tolerances per row: scores of a row live on that row's scale
+    scale = np.abs(ref).max(-1, keepdims=True)
+    scale[scale == 0] = 1.0
+    TT._check_select(idx, score / scale, ref / scale, k)
+
+
+def test_split_scores_track_f32_scores(dev):
+    """The split path's selected scores agree with the fp32-MFMA path's to well
+    within the parity tolerance."""
+    import jakal_net_native as jn
+
+    g = torch.Generator().manual_seed(99)
+    q = torch.randn(2, 128, 64, generator=g)
+    key = torch.randn(2, 4096, 64, generator=g)
+    outs = {}
+    try:
+        for m in (jn.SELECT_SPLIT_F16, jn.SELECT_F32):
+            jn.set_select_mode(m)
+            outs[m] = jn.low_rank_topk_select(q.to(dev), key.to(dev), None, None, False, 1.0, 32)
+    finally:
+        jn.set_select_mode(jn.SELECT_SPLIT_F16)
+    ref = (q.double().numpy() @ np.swapaxes(key.double().numpy(), 1, 2))
+    for m, (idx, score) in outs.items():
+        picked = np.take_along_axis(ref, idx.cpu().numpy(), axis=-1)
+        rel = np.abs(score.cpu().numpy() - picked).max() / np.abs(ref).max()
+        assert rel < 5e-6, f"mode {m}: relative score error {rel:.2e}"
+
+
+@pytest.mark.parametrize("compress", ["softsign", "signed_entmax15"])
+def test_propagation_topk_f32_mode(dev, f32_mode, compress):
+    TT.test_propagation_topk_forward_backward_matches_oracle(dev, compress, True, 8)
+
+
+def test_transition_f32_mode(dev, f32_mode):
+    TR.test_transition_forward_backward_matches_oracle(dev, "softmax", 1.7)

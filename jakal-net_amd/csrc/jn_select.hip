@@ -17,8 +17,8 @@
 //
 // Layout of one workgroup (256 threads = 4 waves, 64 query rows):
 //   * 16 query rows per wave.  A wave keeps the query fragment of its rows in
-//     VGPRs for the whole kernel (B operand of v_mfma_f32_16x16x4f32; lane l
-//     owns row l%16, rank slice l/16).
+//     VGPRs for the whole kernel (B operand of the MFMAs; lane l owns row
+//     l%16, rank slice l/16).
 //   * Each wave streams the keys itself, in chunks of 48 rows (three 16-row MFMA
 //     tiles, A operand), loaded straight into VGPRs one chunk ahead.  The waves
 //     of a workgroup share nothing but the LDS allocation, so no barrier
@@ -30,14 +30,19 @@
 //   * Once any lane of a wave has filled its region to within one chunk of
 //     its capacity (or at the end), all 16 rows of the wave merge together:
 //     lane (g, row) loads a quarter of the row's kept entries and its own
-//     candidates into registers, and a radix select over order keys finds
-//     each row's k-th largest key, counting per lane and summing over the
-//     row's 4 lanes with permlane swaps; it starts below the bits shared by
-//     all of the row's keys and stops once exactly k keys remain.  The k
-//     winners are compacted into the row's kept region.  A row whose k-th
-//     value is tied (more equal keys than places) is merged again by the
-//     exact per-row path, which keeps the lower key indices.  The kept set
-//     stays unsorted until one bitonic sort per row at the end.
+//     candidates into registers, and a radix select over order keys counts
+//     per lane and sums over the row's 4 lanes with permlane swaps; it starts
+//     below the bits shared by all of the row's keys.  A merge during the scan
+//     stops as soon as the entries at or above its threshold fit the kept
+//     region (between k and 48 of them for k <= 32): any threshold not above
+//     the k-th best filters safely, and this halves the radix steps.  The
+//     merge after the last chunk keeps exactly k.  Winners are compacted into
+//     the row's kept region without branches.  A row whose k-th value is tied
+//     (more equal keys than places) is merged again by the exact per-row
+//     path, which keeps the lower key indices.  The kept set stays unsorted
+//     until one bitonic sort per row at the end.
+//   * Score arithmetic: fp16 MFMAs over two-term fp16 splits of the operands
+//     (see select_split_keys_kernel), or fp32 MFMAs (select mode 1).
 #include <type_traits>
 
 #include "jn_internal.hpp"
@@ -52,20 +57,26 @@ constexpr int kSelRows = kSelWaves * kSelRowsPerWave;  // 64 query rows / workgr
 constexpr int kSelTiles = 3;                           // 16-key MFMA tiles per chunk
 constexpr int kSelChunk = 16 * kSelTiles;              // key rows per chunk
 constexpr int kSelLaneKeys = 4 * kSelTiles;            // scores of one row per lane and chunk
-// A row's slots: a kept region of KEEP entries (the k <= KEEP best so far;
-// KEEP = 32 for k <= 32, 64 for k <= 64), then one candidate region of
-// sel_lane_cap(KEEP) slots per lane of the row.  A lane takes at most
-// kSelLaneKeys candidates per chunk, so merging once a lane holds more than
-// cap - kSelLaneKeys keeps every region within its capacity.
-constexpr int kSelRowSlots = 144;
+// A row's slots: a kept region of KEEP entries, then one candidate region of
+// sel_lane_cap(KEEP) slots per lane of the row.  The kept region holds between
+// k and KEEP of the best entries so far: a merge during the scan only needs a
+// threshold no higher than the k-th best, so it stops as soon as the number of
+// entries at or above its threshold fits (KEEP = 48 for k <= 32, 80 for
+// k <= 64); the merge after the last chunk keeps exactly k.  A lane takes at
+// most kSelLaneKeys candidates per chunk, so merging once a lane holds more
+// than cap - kSelLaneKeys keeps every region within its capacity.
+constexpr int kSelRowSlots = 160;
 __host__ __device__ constexpr int sel_lane_cap(int keep) { return (kSelRowSlots - keep) / 4; }
-static_assert(sel_lane_cap(32) % 4 == 0 && sel_lane_cap(64) % 4 == 0, "candidate regions hold whole float4s");
-static_assert(32 / 4 + sel_lane_cap(32) == 64 / 4 + sel_lane_cap(64), "both kept-region sizes merge as many keys");
-constexpr int kSelMergeKeys = 32 / 4 + sel_lane_cap(32);  // keys per lane in a batched merge (36)
+__host__ __device__ constexpr int sel_keep_for(int k) { return k <= 32 ? 48 : 80; }
+static_assert(sel_lane_cap(48) % 4 == 0 && sel_lane_cap(80) % 4 == 0, "candidate regions hold whole float4s");
+static_assert(48 / 4 + sel_lane_cap(48) == 80 / 4 + sel_lane_cap(80), "both kept-region sizes merge as many keys");
+static_assert(sel_keep_for(32) - 32 >= 16 && sel_keep_for(64) - 64 >= 16, "kept regions leave room above k");
+constexpr int kSelMergeKeys = 48 / 4 + sel_lane_cap(48);  // keys per lane in a batched merge (40)
 // Row strides are 16-byte multiples (vector reads) that shift successive rows by
-// 20 (scores) LDS banks, so the 16 rows of a wave read on distinct banks.
-constexpr int kSelScoreStride = 148;  // floats
-constexpr int kSelIndexStride = 152;  // uint16 (76 words)
+// 36 (scores) and 20 (indices) LDS banks, so the 16 rows of a wave read on
+// distinct banks.
+constexpr int kSelScoreStride = 164;  // floats
+constexpr int kSelIndexStride = 168;  // uint16 (84 words)
 constexpr int kSelMaxKeys = 65535;    // key indices are stored as uint16
 
 // Monotone map float -> uint32 (larger float -> larger key); -0 and +0 map together.
@@ -112,11 +123,11 @@ __device__ __forceinline__ int row_sum4(int v) {
 }
 
 // Exact merge of one row by the whole wave: keep the k best (ties toward the
-// lower key index) of its `kept` kept entries and the c[g] candidates of lane
+// lower key index) of its `kept` kept entries and the c_g candidates of lane
 // region g, compacted to slots [0, k); k < kept + sum(c).  Returns the new
 // k-th best score (wave-uniform).  Lane l holds slots l, l + 64, l + 128.
 template <int KEEP>
-__device__ float merge_row_exact(float* row_s, uint16_t* row_i, int k, int kept, const int (&c)[4]) {
+__device__ float merge_row_exact(float* row_s, uint16_t* row_i, int k, int kept, int c0, int c1, int c2, int c3) {
   constexpr int CAP = sel_lane_cap(KEEP);
   const int lane = lane_id();
   float f[3];
@@ -132,7 +143,7 @@ __device__ float merge_row_exact(float* row_s, uint16_t* row_i, int k, int kept,
     } else if (s < kSelRowSlots) {
       const int rg = (s - KEEP) / CAP;
       const int ri = s - KEEP - rg * CAP;
-      const int cr = rg == 0 ? c[0] : rg == 1 ? c[1] : rg == 2 ? c[2] : c[3];
+      const int cr = rg == 0 ? c0 : rg == 1 ? c1 : rg == 2 ? c2 : c3;
       ok = ri < cr;
     } else {
       ok = false;
@@ -240,22 +251,32 @@ __device__ float merge_row_exact(float* row_s, uint16_t* row_i, int k, int kept,
 
 // Merge every row of the wave at once.  Lane (g, col) holds a quarter of row
 // col's kept entries (slots [g*KEEP/4, (g+1)*KEEP/4), valid below `kept`) and
-// its own `cnt` candidates.  A row keeps the min(k, total) best of its
-// `total` = kept + candidates entries (a row that has not yet seen k keys keeps
-// them all and its threshold is unchanged).  The radix select runs per lane
-// over its keys, with row counts summed over the row's 4 lanes by permlane
-// swaps.  Rows with exact ties at the k-th value return fallback = true and
-// are left untouched for merge_row_exact.
+// its own `cnt` candidates.  Of its `total` = kept + candidates entries a row
+// keeps every entry at or above a threshold t with kk <= count(>= t) <= hi,
+// kk = min(k, total): hi = kk in the final merge (exactly the kk best), up to
+// KEEP during the scan, where any t not above the k-th best serves and the
+// search stops as soon as the count fits.  The search is a radix select over
+// order keys per lane, with row counts summed over the row's 4 lanes by
+// permlane swaps.  Returns the row's kept count (or -1 for a row with exact
+// ties at t that the window cannot separate: its slots are left untouched
+// for merge_row_exact).  The row's threshold becomes the smallest kept value
+// once it has seen k keys (else it stays `theta`).
+struct MergeResult {
+  int kept;     // entries now in the kept region, -1 for a tie row
+  float theta;  // the row's new threshold
+};
+
 template <int KEEP>
-__device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kept, int cnt, int total, float& theta,
-                                   bool& fallback) {
+__device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kept, int cnt, int total,
+                                          int hi_target, float theta) {
   constexpr int KQ = KEEP / 4;
   constexpr int CAP = sel_lane_cap(KEEP);
   constexpr int NK = KQ + CAP;
   static_assert(NK == kSelMergeKeys, "merge width");
   const int lane = lane_id();
   const int g = lane >> 4;
-  const int kk = min(k, total);  // entries the row keeps
+  const int kk = min(k, total);  // entries the row keeps at least
+  const int hi = max(kk, min(hi_target, KEEP));
   const int kv = max(0, min(KQ, kept - g * KQ));
   const float* kept_s = row_s + g * KQ;
   const float* cand_s = row_s + KEEP + g * CAP;
@@ -280,23 +301,24 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kep
     id[4 * q + 3] = (int)(i4.y >> 16);
   }
   // valid keys are > 0 (order keys of finite or infinite floats are nonzero)
-  uint32_t hi = 0, lo = 0xffffffffu;
+  uint32_t khi = 0, klo = 0xffffffffu;
 #pragma unroll
   for (int i = 0; i < NK; ++i) {
-    hi = max(hi, key[i]);
-    lo = min(lo, key[i] ? key[i] : 0xffffffffu);
+    khi = max(khi, key[i]);
+    klo = min(klo, key[i] ? key[i] : 0xffffffffu);
   }
-  hi = max(hi, (uint32_t)xor16_i((int)hi));
-  hi = max(hi, (uint32_t)xor32_i((int)hi));
-  lo = min(lo, (uint32_t)xor16_i((int)lo));
-  lo = min(lo, (uint32_t)xor32_i((int)lo));
-  const uint32_t diff = hi ^ lo;
+  khi = max(khi, (uint32_t)xor16_i((int)khi));
+  khi = max(khi, (uint32_t)xor32_i((int)khi));
+  klo = min(klo, (uint32_t)xor16_i((int)klo));
+  klo = min(klo, (uint32_t)xor32_i((int)klo));
+  const uint32_t diff = khi ^ klo;
   const int start = diff ? 31 - __builtin_clz(diff) : -1;
-  uint32_t t = diff ? (hi & ~((2u << start) - 1u)) : hi;  // shared prefix of the row's keys
+  uint32_t t = diff ? (khi & ~((2u << start) - 1u)) : khi;  // shared prefix of the row's keys
   if (start == 31) t = 0;
   const int wave_start = (int)wave_max_u32((uint32_t)(start + 1)) - 1;  // uniform loop bound
-  // a row whose entries all fit keeps every valid key
-  bool done = total <= k;
+  // a row whose entries all fit keeps every valid key; every valid key is >= t,
+  // so a row whose entries fit the window is done before the search
+  bool done = total <= hi;
   if (done) t = 1;
   for (int bit = wave_start; bit >= 0; --bit) {
     if (!__ballot(!done)) break;
@@ -307,10 +329,11 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kep
     n = row_sum4(n);
     if (!done && n >= kk) {
       t = c;
-      done = (n == kk);
+      done = (n <= hi);
     }
   }
-  // winners: exactly kk keys >= t (done), or the k-th largest key is t itself
+  // winners: the keys >= t (done), or the kk-th largest key is t itself with
+  // more ties at t than the window holds
   uint64_t keep_bits = 0;
   uint32_t theta_key;
   bool tie_row = false;
@@ -339,27 +362,31 @@ __device__ void merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kep
     for (int i = 0; i < NK; ++i) keep_bits |= (key[i] >= t) ? (1ull << i) : 0ull;
     theta_key = t;
   }
-  fallback = tie_row;
-  // compact the winners of non-tie rows to kept slots [0, kk): lane g starts
-  // after the winners of the row's lanes g' < g
+  // compact the winners of non-tie rows to kept slots [0, n): lane g starts
+  // after the winners of the row's lanes g' < g.  Branch-free: a lane writes
+  // every entry, losers to a slot of its own candidate region (dead after the
+  // merge), so no lane writes over another's winners.
   const int w = popc64(keep_bits);
   const int w1 = xor16_i(w);   // lane g ^ 1
   const int w2 = xor32_i(w);   // lane g ^ 2
   const int w3 = xor16_i(w2);  // lane g ^ 3
+  const int n_row = w + w1 + w2 + w3;
   int pos = ((g & 1) ? w1 : 0) + ((g & 2) ? (w2 + w3) : 0);
   if (!tie_row) {
+    const int trash = KEEP + g * CAP + CAP - 1;
     // the reads above have returned (their values feed these stores)
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
-      if ((keep_bits >> i) & 1ull) {
-        row_s[pos] = key_to_float(key[i]);
-        row_i[pos] = (uint16_t)id[i];
-        ++pos;
-      }
+      const bool kp = (keep_bits >> i) & 1ull;
+      const int at = kp ? pos : trash;
+      row_s[at] = key_to_float(key[i]);
+      row_i[at] = (uint16_t)id[i];
+      pos += kp ? 1 : 0;
     }
     if (total >= k) theta = key_to_float(theta_key);
   }
   wave_lds_sync();
+  return MergeResult{tie_row ? -1 : n_row, theta};
 }
 
 // ---- split-fp16 score operands ------------------------------------------------
@@ -669,28 +696,30 @@ __global__ __launch_bounds__(256, (KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2) void lowr
       }
     }
 
-    // -- merge rows once a lane region is nearly full (or everything at the end) --
+    // -- merge rows once a lane region is nearly full; after the last chunk,
+    // every row still holding more than k entries merges exactly --
     const bool last = (c + 1 == nchunks);
-    if (__ballot(cnt > CAP - kSelLaneKeys || (last && cnt > 0))) {
+    if (__ballot(cnt > CAP - kSelLaneKeys || (last && (cnt > 0 || kept > k)))) {
       wave_lds_sync();
       const int total = kept + row_sum4(cnt);
-      bool fallback;
-      merge_rows_batched<KEEP>(my_slot_s, my_slot_i, k, kept, cnt, total, theta, fallback);
+      const MergeResult mr =
+          merge_rows_batched<KEEP>(my_slot_s, my_slot_i, k, kept, cnt, total, last ? k : KEEP, theta);
+      const int n_kept = mr.kept;
+      theta = mr.theta;
       // rows with exact ties at the k-th value: exact per-row merge (such a
       // row holds more than k entries, so the merge fills it)
-      uint64_t m = __ballot(lane < kSelRowsPerWave && fallback);
+      uint64_t m = __ballot(lane < kSelRowsPerWave && n_kept < 0);
       while (m) {
         const int t = __builtin_ctzll(m);
         m &= m - 1;
-        const int rc[4] = {readlane_i(cnt, t), readlane_i(cnt, t + 16), readlane_i(cnt, t + 32),
-                           readlane_i(cnt, t + 48)};
         const int slot = wave * kSelRowsPerWave + t;
         const float th = merge_row_exact<KEEP>(s_slot_s + slot * kSelScoreStride, s_slot_i + slot * kSelIndexStride,
-                                               k, readlane_i(kept, t), rc);
+                                               k, readlane_i(kept, t), readlane_i(cnt, t), readlane_i(cnt, t + 16),
+                                               readlane_i(cnt, t + 32), readlane_i(cnt, t + 48));
         if (col == t) theta = th;
       }
       if (!row_ok) theta = INFINITY;  // rows past Nq stay closed
-      kept = min(k, total);
+      kept = n_kept < 0 ? k : n_kept;
       cnt = 0;
     }
   };
@@ -733,18 +762,18 @@ __global__ __launch_bounds__(256, (KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2) void lowr
 template <int RQ>
 static void launch_rq(const SelectArgs& a, bool vec, dim3 grid, hipStream_t stream) {
   if (a.k <= 32) {
-    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 32, 0>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 32, 0>), grid, dim3(256), 0, stream, a);
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 48, 0>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 48, 0>), grid, dim3(256), 0, stream, a);
   } else {
-    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 64, 0>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 64, 0>), grid, dim3(256), 0, stream, a);
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 80, 0>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 80, 0>), grid, dim3(256), 0, stream, a);
   }
 }
 
 template <int KS>
 static void launch_split(const SelectArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 32, KS>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 64, KS>), grid, dim3(256), 0, stream, a);
+  if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS>), grid, dim3(256), 0, stream, a);
 }
 
 namespace {

@@ -420,8 +420,10 @@ int jn_set_gemm_tile(int32_t tile) {
 }
 
 int jn_set_select_mode(int32_t mode) {
-  JN_REQUIRE(mode == jakal::kSelectSplitF16 || mode == jakal::kSelectF32, kInvalidArgument,
-             "select mode must be 0 (split fp16) or 1 (fp32), got %d", (int)mode);
+  JN_REQUIRE(mode >= jakal::kSelectSplitF16 && mode <= jakal::kSelectSplitF16Coop, kInvalidArgument,
+             "select mode must be 0 (split fp16), 1 (fp32), 2 (split fp16, per-wave kernel) or 3 (split fp16, "
+             "cooperative kernel), got %d",
+             (int)mode);
   jakal::set_select_mode(mode);
   return kOk;
 }

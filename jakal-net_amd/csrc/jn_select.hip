@@ -469,26 +469,43 @@ __device__ __forceinline__ halfx8 as_halfx8(float a, float b, float c, float d) 
 // VEC: r == 4*RQ and 16-byte aligned key rows -> float4 key loads (RQ % 4 == 0).
 // KS > 0: split-fp16 scores over KS K-steps of 32 ranks (RQ and VEC unused);
 // the keys are the split rows in a.ws, the queries are split in registers.
-template <int RQ, bool VEC, int KEEP, int KS>
-__global__ __launch_bounds__(256, (KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2) void lowrank_topk_select_kernel(SelectArgs a) {
+// COOP (split keys of rank <= 64 only): 8 waves, 128 query rows, one workgroup
+// per CU.  The workgroup stages each key chunk once in LDS (double-buffered,
+// one barrier per chunk) and every wave reads its MFMA fragments from there,
+// instead of each wave streaming all keys through L1 on its own: per CU that
+// is one global read of each key chunk instead of eight.  A wave that needs
+// to merge raises a workgroup flag before the barrier and then every wave
+// merges after it, so a merge holds up no other wave at the next barrier.
+template <int RQ, bool VEC, int KEEP, int KS, bool COOP>
+__global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2)) void lowrank_topk_select_kernel(SelectArgs a) {
   constexpr int CAP = sel_lane_cap(KEEP);
   constexpr bool SPLIT = KS > 0;
   constexpr bool V4 = VEC && RQ % 4 == 0;
   constexpr int FR = SPLIT ? 8 * KS : RQ;  // key fragment registers per tile
   constexpr int RP = 32 * KS;              // split row: ranks per plane
+  constexpr int ROWS = (COOP ? 2 : 1) * kSelRows;  // query rows per workgroup
+  static_assert(!COOP || (KS >= 1 && KS <= 2), "the cooperative select stages split keys of rank <= 64");
+  // staged chunk: kSelChunk split rows of 2 RP halves plus 8 halves of padding,
+  // so the 16 rows one fragment read touches start 68 dwords apart (4 banks)
+  constexpr int KROW = 2 * RP + 8;
+  constexpr int KBUF = kSelChunk * KROW;
+  constexpr int F4 = kSelChunk * RP / 4;   // float4s per staged chunk
+  constexpr int PER = (F4 + 511) / 512;    // of them per thread
 
-  __shared__ __align__(16) float s_slot_s[kSelRows * kSelScoreStride];
-  __shared__ __align__(16) uint16_t s_slot_i[kSelRows * kSelIndexStride];
+  __shared__ __align__(16) float s_slot_s[ROWS * kSelScoreStride];
+  __shared__ __align__(16) uint16_t s_slot_i[ROWS * kSelIndexStride];
+  __shared__ __align__(16) _Float16 s_key[COOP ? 2 * KBUF : 8];
+  __shared__ int s_flag[3];
 
   const int lane = lane_id();
   const int wave = wave_id();
   const int g = lane >> 4;    // rank slice owned by this lane group
   const int col = lane & 15;  // query row within the wave's 16
 
-  const int tiles_per_batch = (a.Nq + kSelRows - 1) / kSelRows;
+  const int tiles_per_batch = (a.Nq + ROWS - 1) / ROWS;
   const int logical = xcd_swizzle(blockIdx.x, gridDim.x);
   const int b = logical / tiles_per_batch;
-  const int row0 = (logical % tiles_per_batch) * kSelRows;
+  const int row0 = (logical % tiles_per_batch) * ROWS;
   if (b >= a.B) return;
 
   const float* qb = a.q + (int64_t)b * a.q_batch_stride;
@@ -628,6 +645,26 @@ __global__ __launch_bounds__(256, (KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2) void lowr
   auto process = [&](auto SET, int c) {
     constexpr int S = decltype(SET)::value;
     const int c0 = c * kSelChunk;
+    if constexpr (COOP) {
+      // this wave's fragments of the staged chunk: lane (g, col) reads ranks
+      // [32 s + 8 g, +8) of row 16 t + col from each plane
+      const _Float16* kb = s_key + (c & 1) * KBUF + col * KROW + 8 * g;
+#pragma unroll
+      for (int t = 0; t < kSelTiles; ++t)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const float4 h = *reinterpret_cast<const float4*>(kb + 16 * t * KROW + 32 * s);
+          const float4 l = *reinterpret_cast<const float4*>(kb + 16 * t * KROW + 32 * s + RP);
+          kx[S][t][8 * s + 0] = h.x;
+          kx[S][t][8 * s + 1] = h.y;
+          kx[S][t][8 * s + 2] = h.z;
+          kx[S][t][8 * s + 3] = h.w;
+          kx[S][t][8 * s + 4] = l.x;
+          kx[S][t][8 * s + 5] = l.y;
+          kx[S][t][8 * s + 6] = l.z;
+          kx[S][t][8 * s + 7] = l.w;
+        }
+    }
     // -- scores for 32 keys x 16 query rows (two MFMA tiles) --
     floatx4 acc[kSelTiles];
 #pragma unroll
@@ -696,10 +733,12 @@ __global__ __launch_bounds__(256, (KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2) void lowr
       }
     }
 
-    // -- merge rows once a lane region is nearly full; after the last chunk,
-    // every row still holding more than k entries merges exactly --
-    const bool last = (c + 1 == nchunks);
-    if (__ballot(cnt > CAP - kSelLaneKeys || (last && (cnt > 0 || kept > k)))) {
+  };
+
+  // -- merge the wave's rows (`go`: wave-uniform).  After the last chunk every
+  // row still holding more than k entries merges exactly --
+  auto merge = [&](bool go, bool last) {
+    if (go) {
       wave_lds_sync();
       const int total = kept + row_sum4(cnt);
       const MergeResult mr =
@@ -723,17 +762,74 @@ __global__ __launch_bounds__(256, (KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2) void lowr
       cnt = 0;
     }
   };
+  // a wave must merge once any lane region is within one chunk of its capacity
+  auto need_merge = [&]() { return __ballot(cnt > CAP - kSelLaneKeys) != 0; };
+  auto need_final = [&]() { return __ballot(cnt > 0 || kept > k) != 0; };
 
   // chunk c lives in register set c & 1.  The loads are unconditional (chunks
   // past the end read rows >= Nk: zeros, no memory access), so the wait before
   // a chunk's MFMAs covers only its own loads, not the prefetch behind them.
-  load_keys(kSet0, 0);
-  for (int c = 0; c < nchunks; c += 2) {
-    load_keys(kSet1, c + 1);
-    process(kSet0, c);
-    if (c + 1 < nchunks) {
-      load_keys(kSet0, c + 2);
-      process(kSet1, c + 1);
+  if constexpr (COOP) {
+    // cooperative staging: thread x moves float4s x + 512 p of the chunk
+    float4 pre[PER];
+    auto stage_load = [&](int c) {
+      const int c0 = c * kSelChunk;
+      const int rows = max(0, min(kSelChunk, a.Nk - c0));
+      const uint32_t nrec = __builtin_amdgcn_readfirstlane((uint32_t)(rows * 4 * RP));
+      const auto rs = make_rsrc(split_b + (int64_t)c0 * 2 * RP, nrec);
+#pragma unroll
+      for (int p = 0; p < PER; ++p) {
+        const int f = (int)threadIdx.x + 512 * p;
+        pre[p] = buf_load4(rs, f < F4 ? (uint32_t)f * 16u : kOobOffset);
+      }
+    };
+    auto stage_store = [&](int buf) {
+#pragma unroll
+      for (int p = 0; p < PER; ++p) {
+        const int f = (int)threadIdx.x + 512 * p;
+        if (f < F4) {
+          const int row = f / (RP / 4), part = f - row * (RP / 4);
+          *reinterpret_cast<float4*>(s_key + buf * KBUF + row * KROW + 8 * part) = pre[p];
+        }
+      }
+    };
+    if (threadIdx.x < 3) s_flag[threadIdx.x] = 0;
+    stage_load(0);
+    stage_store(0);
+    if (nchunks > 1) stage_load(1);
+    __syncthreads();
+    // Chunk c: score buffer c & 1, raise flag c % 3 if this wave must merge,
+    // stage chunk c + 1 into the other buffer, barrier, issue the loads of
+    // chunk c + 2, merge every wave if the flag is up.  Wave 0 clears flag
+    // (c + 1) % 3 = (c - 2) % 3, read by all before the previous barrier and
+    // raised again only after this one.
+    int fl = 0;  // c % 3
+    for (int c = 0; c < nchunks; ++c) {
+      process(kSet0, c);
+      const bool last = c + 1 == nchunks;
+      if (need_merge() && lane == 0) s_flag[fl] = 1;
+      const int fl_next = fl == 2 ? 0 : fl + 1;
+      if (wave == 0 && lane == 0) s_flag[fl_next] = 0;
+      if (!last) stage_store((c + 1) & 1);
+      __syncthreads();
+      if (c + 2 < nchunks) stage_load(c + 2);
+      const bool go = last ? need_final() : __builtin_amdgcn_readfirstlane(s_flag[fl]) != 0;
+      merge(go, last);
+      fl = fl_next;
+    }
+  } else {
+    load_keys(kSet0, 0);
+    for (int c = 0; c < nchunks; c += 2) {
+      load_keys(kSet1, c + 1);
+      process(kSet0, c);
+      const bool last0 = c + 1 == nchunks;
+      merge(need_merge() || (last0 && need_final()), last0);
+      if (c + 1 < nchunks) {
+        load_keys(kSet0, c + 2);
+        process(kSet1, c + 1);
+        const bool last1 = c + 2 == nchunks;
+        merge(need_merge() || (last1 && need_final()), last1);
+      }
     }
   }
   wave_lds_sync();
@@ -762,19 +858,24 @@ __global__ __launch_bounds__(256, (KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2) void lowr
 template <int RQ>
 static void launch_rq(const SelectArgs& a, bool vec, dim3 grid, hipStream_t stream) {
   if (a.k <= 32) {
-    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 48, 0>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 48, 0>), grid, dim3(256), 0, stream, a);
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 48, 0, false>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 48, 0, false>), grid, dim3(256), 0, stream, a);
   } else {
-    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 80, 0>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 80, 0>), grid, dim3(256), 0, stream, a);
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 80, 0, false>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 80, 0, false>), grid, dim3(256), 0, stream, a);
   }
 }
 
-template <int KS>
+template <int KS, bool COOP>
 static void launch_split(const SelectArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS>), grid, dim3(256), 0, stream, a);
+  const dim3 block(COOP ? 512 : 256);
+  if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, COOP>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS, COOP>), grid, block, 0, stream, a);
 }
+
+// The cooperative kernel holds one workgroup per CU; below one workgroup per
+// CU the per-wave kernel (two workgroups of 64 rows per CU) spreads wider.
+constexpr int64_t kSelCoopMinBlocks = 256;
 
 namespace {
 int g_select_mode = kSelectSplitF16;
@@ -803,7 +904,7 @@ int select_mode() { return g_select_mode; }
 void set_select_mode(int mode) { g_select_mode = mode; }
 
 size_t select_workspace_bytes(int64_t B, int64_t Nk, int64_t r) {
-  if (g_select_mode != kSelectSplitF16 || B < 1 || Nk < 1 || r < 1) return 0;
+  if (g_select_mode == kSelectF32 || B < 1 || Nk < 1 || r < 1) return 0;
   return carve_select(nullptr, 0, B, Nk, r).bytes;
 }
 
@@ -822,7 +923,7 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   JN_REQUIRE(blocks > 0 && blocks < (1LL << 31), kInvalidArgument, "bad grid size");
   dim3 grid((unsigned)blocks);
 
-  if (g_select_mode == kSelectSplitF16) {
+  if (g_select_mode != kSelectF32) {
     const SelectScratch s = carve_select(a.ws, a.ws_bytes, a.B, a.Nk, a.r);
     JN_REQUIRE(a.ws != nullptr && s.bytes <= a.ws_bytes, kWorkspaceTooSmall,
                "select workspace too small: need %zu bytes, got %zu", s.bytes, a.ws_bytes);
@@ -843,12 +944,21 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
     }
     a.split_key = s.split;
     a.split_exp = s.kexp;
+    const int64_t coop_blocks = (int64_t)((a.Nq + 2 * kSelRows - 1) / (2 * kSelRows)) * a.B;
+    const bool coop = RP <= 64 && (g_select_mode == kSelectSplitF16Coop ||
+                                   (g_select_mode == kSelectSplitF16 && coop_blocks >= kSelCoopMinBlocks));
     JN_PROFILE("lowrank_topk_select_kernel", stream);
-    switch (RP / 32) {
-      case 1: launch_split<1>(a, grid, stream); break;
-      case 2: launch_split<2>(a, grid, stream); break;
-      case 3: launch_split<3>(a, grid, stream); break;
-      default: launch_split<4>(a, grid, stream); break;
+    if (coop) {
+      const dim3 cgrid((unsigned)coop_blocks);
+      if (RP == 32) launch_split<1, true>(a, cgrid, stream);
+      else launch_split<2, true>(a, cgrid, stream);
+    } else {
+      switch (RP / 32) {
+        case 1: launch_split<1, false>(a, grid, stream); break;
+        case 2: launch_split<2, false>(a, grid, stream); break;
+        case 3: launch_split<3, false>(a, grid, stream); break;
+        default: launch_split<4, false>(a, grid, stream); break;
+      }
     }
     JN_LAUNCH_CHECK();
     return kOk;

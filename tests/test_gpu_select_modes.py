@@ -2,8 +2,10 @@
 
 The per-op tests run the default split-fp16 select (fp16 MFMAs over two-term
 fp16 splits of power-of-two-scaled operands, fp32 accumulation).  These tests
-cover the fp32-MFMA select (jn_set_select_mode(1)) on the same select, top-k
-propagation and transition cases, and the split path on what its scaling has
+cover the fp32-MFMA select (jn_set_select_mode(1)) and each split-fp16 kernel
+on its own (per-wave streaming, mode 2; LDS-staged cooperative, mode 3) on the
+same select, top-k propagation and transition cases, check that the two split
+kernels pick identical entries and values up to the C4 shape, and the split path on what its scaling has
 to survive: key and query rows whose magnitudes span many octaves, all-zero
 rows, ranks that are not a multiple of the 32-rank K-step, and bias and
 temperature on the unscaled-domain path.  Tolerances are the hot path's
@@ -29,11 +31,18 @@ def dev():
     return torch.device("cuda:0")
 
 
-@pytest.fixture(params=["split_f16", "f32"])
+def _mode_value(name):
+    import jakal_net_native as jn
+
+    return {"split_f16": jn.SELECT_SPLIT_F16, "f32": jn.SELECT_F32, "split_wave": jn.SELECT_SPLIT_F16_WAVE,
+            "split_coop": jn.SELECT_SPLIT_F16_COOP}[name]
+
+
+@pytest.fixture(params=["split_f16", "f32", "split_wave", "split_coop"])
 def mode(request):
     import jakal_net_native as jn
 
-    jn.set_select_mode(jn.SELECT_SPLIT_F16 if request.param == "split_f16" else jn.SELECT_F32)
+    jn.set_select_mode(_mode_value(request.param))
     yield request.param
     jn.set_select_mode(jn.SELECT_SPLIT_F16)
 
@@ -129,3 +138,39 @@ def test_propagation_topk_f32_mode(dev, f32_mode, compress):
 
 def test_transition_f32_mode(dev, f32_mode):
     TR.test_transition_forward_backward_matches_oracle(dev, "softmax", 1.7)
+
+
+@pytest.mark.parametrize("r,k,B,Nq,Nk,dominant", [(64, 32, 16, 4096, 4096, False), (64, 64, 2, 700, 3001, False),
+                                                  (32, 7, 3, 300, 5000, False), (17, 16, 1, 129, 48, False),
+                                                  (64, 32, 2, 256, 4000, True)])
+def test_split_kernels_agree(dev, r, k, B, Nq, Nk, dominant):
+    """The per-wave and the cooperative kernel compute every score with the same
+    MFMA sequence and keep the k best by the same rule, so their outputs are
+    bit-identical (the C4 shape included); the cooperative kernel merges at
+    other chunks, which must not change the result."""
+    import jakal_net_native as jn
+
+    g = torch.Generator().manual_seed(7000 + r + k + Nk)
+    q = torch.randn(B, Nq, r, generator=g)
+    key = torch.randn(B, Nk, r, generator=g)
+    key = key / key.norm(dim=-1, keepdim=True)  # many close scores, as in C4
+    if dominant:  # a few keys win every row late in the scan: merges with many ties
+        key[:, -40:] = key[:, -40:] * 0 + key[:, -40:-39]
+    scale = torch.rand(r, generator=g) + 0.5
+    out = {}
+    try:
+        for m in (jn.SELECT_SPLIT_F16_WAVE, jn.SELECT_SPLIT_F16_COOP):
+            jn.set_select_mode(m)
+            idx, score = jn.low_rank_topk_select(q.to(dev), key.to(dev), scale.to(dev), None, False, 1.0, k)
+            out[m] = (idx.cpu(), score.cpu())
+    finally:
+        jn.set_select_mode(jn.SELECT_SPLIT_F16)
+    wi, ws = out[jn.SELECT_SPLIT_F16_WAVE]
+    ci, cs = out[jn.SELECT_SPLIT_F16_COOP]
+    assert torch.equal(wi, ci)
+    assert torch.equal(ws, cs)
+    # and the result is a top-k: sorted, in range, no repeats
+    assert bool((ws[..., :-1] >= ws[..., 1:]).all())
+    assert int(wi.min()) >= 0 and int(wi.max()) < Nk
+    srt = wi.sort(dim=-1).values
+    assert bool((srt[..., 1:] != srt[..., :-1]).all())

@@ -109,6 +109,26 @@ __device__ __forceinline__ void bitonic_sort64_desc(float& vs, int& vi) {
   }
 }
 
+// The same network on each half-wave: two independent 32-entry sorts (the
+// final merge stage leaves both halves descending).
+__device__ __forceinline__ void bitonic_sort32x2_desc(float& vs, int& vi) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int size = 2; size <= 32; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const float ps = shfl_xor_f(vs, stride);
+      const int pi = shfl_xor_i(vi, stride);
+      const bool partner_better = (ps > vs) | ((ps == vs) & (pi < vi));
+      const bool self_better = (vs > ps) | ((vs == ps) & (vi < pi));
+      const bool keep_better = ((lane & stride) == 0) == ((lane & size & 31) == 0);
+      const bool take = keep_better ? partner_better : self_better;
+      vs = take ? ps : vs;
+      vi = take ? pi : vi;
+    }
+  }
+}
+
 __device__ __forceinline__ int popc64(uint64_t m) { return __builtin_popcountll(m); }
 
 // Lanes whose id is below this lane, within mask m.
@@ -257,7 +277,10 @@ __device__ float merge_row_exact(float* row_s, uint16_t* row_i, int k, int kept,
 // KEEP during the scan, where any t not above the k-th best serves and the
 // search stops as soon as the count fits.  The search is a radix select over
 // order keys per lane, with row counts summed over the row's 4 lanes by
-// permlane swaps.  Returns the row's kept count (or -1 for a row with exact
+// permlane swaps.  Only the first `cq` quads of each candidate region (the
+// wave's largest candidate count, rounded up to 4) are read and searched: a
+// wave that merges because another wave of its workgroup had to merges only
+// what it holds.  Returns the row's kept count (or -1 for a row with exact
 // ties at t that the window cannot separate: its slots are left untouched
 // for merge_row_exact).  The row's threshold becomes the smallest kept value
 // once it has seen k keys (else it stays `theta`).
@@ -268,7 +291,7 @@ struct MergeResult {
 
 template <int KEEP>
 __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kept, int cnt, int total,
-                                          int hi_target, float theta) {
+                                          int hi_target, float theta, int cq) {
   constexpr int KQ = KEEP / 4;
   constexpr int CAP = sel_lane_cap(KEEP);
   constexpr int NK = KQ + CAP;
@@ -284,8 +307,19 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
   const uint16_t* cand_i = row_i + KEEP + g * CAP;
   uint32_t key[NK];
   int id[NK];
+  // quad q of the lane's keys is in use (wave-uniform; q is a constant in
+  // every unrolled loop below, so each test is one scalar branch)
+  auto act = [&](int q) { return 4 * q < KQ || q - KQ / 4 < cq; };
 #pragma unroll
   for (int q = 0; q < NK / 4; ++q) {
+    if (!act(q)) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        key[4 * q + v] = 0u;
+        id[4 * q + v] = 0;
+      }
+      continue;
+    }
     const bool kpt = 4 * q < KQ;
     const int o = kpt ? 4 * q : 4 * q - KQ;
     const int lim = kpt ? kv : cnt;
@@ -304,6 +338,7 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
   uint32_t khi = 0, klo = 0xffffffffu;
 #pragma unroll
   for (int i = 0; i < NK; ++i) {
+    if (!act(i / 4)) continue;
     khi = max(khi, key[i]);
     klo = min(klo, key[i] ? key[i] : 0xffffffffu);
   }
@@ -325,7 +360,11 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
     const uint32_t c = t | (1u << bit);
     int n = 0;
 #pragma unroll
-    for (int i = 0; i < NK; ++i) n += (key[i] >= c) ? 1 : 0;
+    for (int q = 0; q < NK / 4; ++q) {
+      if (!act(q)) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) n += (key[4 * q + v] >= c) ? 1 : 0;
+    }
     n = row_sum4(n);
     if (!done && n >= kk) {
       t = c;
@@ -341,6 +380,7 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
     uint32_t m = 0xffffffffu;
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
+      if (!act(i / 4)) continue;
       const bool kp = key[i] >= t;
       keep_bits |= kp ? (1ull << i) : 0ull;
       m = kp ? min(m, key[i]) : m;
@@ -377,6 +417,7 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
     // the reads above have returned (their values feed these stores)
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
+      if (!act(i / 4)) continue;
       const bool kp = (keep_bits >> i) & 1ull;
       const int at = kp ? pos : trash;
       row_s[at] = key_to_float(key[i]);
@@ -741,8 +782,9 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
     if (go) {
       wave_lds_sync();
       const int total = kept + row_sum4(cnt);
+      const int cq = (int)(__builtin_amdgcn_readfirstlane(wave_max_u32((uint32_t)cnt)) + 3) / 4;
       const MergeResult mr =
-          merge_rows_batched<KEEP>(my_slot_s, my_slot_i, k, kept, cnt, total, last ? k : KEEP, theta);
+          merge_rows_batched<KEEP>(my_slot_s, my_slot_i, k, kept, cnt, total, last ? k : KEEP, theta, cq);
       const int n_kept = mr.kept;
       theta = mr.theta;
       // rows with exact ties at the k-th value: exact per-row merge (such a
@@ -835,6 +877,31 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
   wave_lds_sync();
 
   // ---- sort each row's k winners and write them -----------------------------
+  if constexpr (KEEP == 48) {
+    // k <= 32: two rows per pass, row t + h on half-wave h
+    const int h = lane >> 5, e = lane & 31;
+    for (int t = 0; t < kSelRowsPerWave; t += 2) {
+      if (row0 + wave * kSelRowsPerWave + t >= a.Nq) break;
+      const int row = row0 + wave * kSelRowsPerWave + t + h;
+      const int slot = wave * kSelRowsPerWave + t + h;
+      float vs = -INFINITY;
+      int vi = 0x7fffffff;
+      if (e < k) {
+        vs = s_slot_s[slot * kSelScoreStride + e];
+        vi = s_slot_i[slot * kSelIndexStride + e];
+      }
+      bitonic_sort32x2_desc(vs, vi);
+      if (scaled_domain) {
+        const int e0 = readlane_i(score_exp, t), e1 = readlane_i(score_exp, t + 1);
+        vs = ldexpf(vs, -(h ? e1 : e0));
+      }
+      if (e < k && row < a.Nq) {
+        const int64_t o = ((int64_t)b * a.Nq + row) * k + e;
+        a.out_idx[o] = vi;
+        a.out_score[o] = vs;
+      }
+    }
+  } else
   for (int t = 0; t < kSelRowsPerWave; ++t) {
     const int row = row0 + wave * kSelRowsPerWave + t;
     if (row >= a.Nq) break;

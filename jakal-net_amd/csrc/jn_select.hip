@@ -26,7 +26,9 @@
 //   * After a chunk, lane l holds 12 scores of row l%16.  Scores above the
 //     row's threshold theta are appended to the lane's own candidate region
 //     of the row (the row's 4 lanes never share a region, so appends need no
-//     cross-lane offsets).  Counts and thresholds live in registers.
+//     cross-lane offsets; regions are stored slot-major per wave, so the
+//     appends are free of bank conflicts).  Counts and thresholds live in
+//     registers.
 //   * Once any lane of a wave has filled its region to within one chunk of
 //     its capacity (or at the end), all 16 rows of the wave merge together:
 //     lane (g, row) loads a quarter of the row's kept entries and its own
@@ -65,6 +67,9 @@ constexpr int kSelLaneKeys = 4 * kSelTiles;            // scores of one row per 
 // k <= 64); the merge after the last chunk keeps exactly k.  A lane takes at
 // most kSelLaneKeys candidates per chunk, so merging once a lane holds more
 // than cap - kSelLaneKeys keeps every region within its capacity.
+// Candidate regions are stored slot-major per wave: slot j of lane l is word
+// j * 64 + l of the wave's candidate array, so the 64 appends of a wave (each
+// lane at its own count) and a merge's per-slot reads hit 64 distinct banks.
 constexpr int kSelRowSlots = 160;
 __host__ __device__ constexpr int sel_lane_cap(int keep) { return (kSelRowSlots - keep) / 4; }
 __host__ __device__ constexpr int sel_keep_for(int k) { return k <= 32 ? 48 : 80; }
@@ -72,11 +77,11 @@ static_assert(sel_lane_cap(48) % 4 == 0 && sel_lane_cap(80) % 4 == 0, "candidate
 static_assert(48 / 4 + sel_lane_cap(48) == 80 / 4 + sel_lane_cap(80), "both kept-region sizes merge as many keys");
 static_assert(sel_keep_for(32) - 32 >= 16 && sel_keep_for(64) - 64 >= 16, "kept regions leave room above k");
 constexpr int kSelMergeKeys = 48 / 4 + sel_lane_cap(48);  // keys per lane in a batched merge (40)
-// Row strides are 16-byte multiples (vector reads) that shift successive rows by
-// 36 (scores) and 20 (indices) LDS banks, so the 16 rows of a wave read on
-// distinct banks.
-constexpr int kSelScoreStride = 164;  // floats
-constexpr int kSelIndexStride = 168;  // uint16 (84 words)
+// Kept rows are KEEP + 4 scores / KEEP + 8 indices apart: 16-byte multiples
+// (vector reads) that shift successive rows by 52 or 84 (scores) and 28 or 44
+// (indices) banks.
+__host__ __device__ constexpr int sel_kept_stride(int keep) { return keep + 4; }
+__host__ __device__ constexpr int sel_kept_idx_stride(int keep) { return keep + 8; }
 constexpr int kSelMaxKeys = 65535;    // key indices are stored as uint16
 
 // Monotone map float -> uint32 (larger float -> larger key); -0 and +0 map together.
@@ -142,12 +147,15 @@ __device__ __forceinline__ int row_sum4(int v) {
   return v + xor32_i(v);
 }
 
-// Exact merge of one row by the whole wave: keep the k best (ties toward the
-// lower key index) of its `kept` kept entries and the c_g candidates of lane
-// region g, compacted to slots [0, k); k < kept + sum(c).  Returns the new
-// k-th best score (wave-uniform).  Lane l holds slots l, l + 64, l + 128.
+// Exact merge of row `trow` of the wave by the whole wave: keep the k best
+// (ties toward the lower key index) of its `kept` kept entries and the c_g
+// candidates of lane region g (lane g * 16 + trow of the wave's slot-major
+// candidate arrays), compacted to kept slots [0, k); k < kept + sum(c).
+// Returns the new k-th best score (wave-uniform).  Lane l holds row slots l,
+// l + 64, l + 128 (kept slots first, then region 0, 1, 2, 3).
 template <int KEEP>
-__device__ float merge_row_exact(float* row_s, uint16_t* row_i, int k, int kept, int c0, int c1, int c2, int c3) {
+__device__ float merge_row_exact(float* row_s, uint16_t* row_i, const float* cand_s, const uint16_t* cand_i, int trow, int k,
+                                 int kept, int c0, int c1, int c2, int c3) {
   constexpr int CAP = sel_lane_cap(KEEP);
   const int lane = lane_id();
   float f[3];
@@ -158,6 +166,7 @@ __device__ float merge_row_exact(float* row_s, uint16_t* row_i, int k, int kept,
   for (int j = 0; j < 3; ++j) {
     const int s = lane + 64 * j;
     bool ok;
+    int w = 0;  // word of the slot in the candidate arrays
     if (s < KEEP) {
       ok = s < kept;
     } else if (s < kSelRowSlots) {
@@ -165,12 +174,13 @@ __device__ float merge_row_exact(float* row_s, uint16_t* row_i, int k, int kept,
       const int ri = s - KEEP - rg * CAP;
       const int cr = rg == 0 ? c0 : rg == 1 ? c1 : rg == 2 ? c2 : c3;
       ok = ri < cr;
+      w = ri * kWave + rg * 16 + trow;
     } else {
       ok = false;
     }
     v[j] = ok;
-    f[j] = ok ? row_s[s] : 0.f;
-    ix[j] = ok ? (int)row_i[s] : 0;
+    f[j] = ok ? (s < KEEP ? row_s[s] : cand_s[w]) : 0.f;
+    ix[j] = ok ? (int)(s < KEEP ? row_i[s] : cand_i[w]) : 0;
     kk[j] = ok ? order_key(f[j]) : 0u;
   }
 
@@ -290,8 +300,9 @@ struct MergeResult {
 };
 
 template <int KEEP>
-__device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t* row_i, int k, int kept, int cnt, int total,
-                                          int hi_target, float theta, int cq) {
+__device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t* row_i, float* cand_s, uint16_t* cand_i,
+                                                          int k, int kept, int cnt, int total, int hi_target, float theta,
+                                                          int cq) {
   constexpr int KQ = KEEP / 4;
   constexpr int CAP = sel_lane_cap(KEEP);
   constexpr int NK = KQ + CAP;
@@ -302,37 +313,59 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
   const int hi = max(kk, min(hi_target, KEEP));
   const int kv = max(0, min(KQ, kept - g * KQ));
   const float* kept_s = row_s + g * KQ;
-  const float* cand_s = row_s + KEEP + g * CAP;
   const uint16_t* kept_i = row_i + g * KQ;
-  const uint16_t* cand_i = row_i + KEEP + g * CAP;
   uint32_t key[NK];
   int id[NK];
   // quad q of the lane's keys is in use (wave-uniform; q is a constant in
   // every unrolled loop below, so each test is one scalar branch)
   auto act = [&](int q) { return 4 * q < KQ || q - KQ / 4 < cq; };
+  // Every load of the active quads is issued first and each value passes an
+  // empty asm before its validity select: left alone, the compiler turns
+  // "valid ? f(load) : 0" into a branch around the load and waits for each
+  // load on its own.
+  float sv[NK];
 #pragma unroll
   for (int q = 0; q < NK / 4; ++q) {
     if (!act(q)) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        key[4 * q + v] = 0u;
+        sv[4 * q + v] = 0.0f;
         id[4 * q + v] = 0;
       }
       continue;
     }
+    if (4 * q < KQ) {
+      const int o = 4 * q;
+      const float4 s4 = *reinterpret_cast<const float4*>(kept_s + o);
+      const uint2 i4 = *reinterpret_cast<const uint2*>(kept_i + o);
+      sv[4 * q + 0] = s4.x;
+      sv[4 * q + 1] = s4.y;
+      sv[4 * q + 2] = s4.z;
+      sv[4 * q + 3] = s4.w;
+      id[4 * q + 0] = (int)(i4.x & 0xffffu);
+      id[4 * q + 1] = (int)(i4.x >> 16);
+      id[4 * q + 2] = (int)(i4.y & 0xffffu);
+      id[4 * q + 3] = (int)(i4.y >> 16);
+    } else {
+      const int o = 4 * q - KQ;  // candidate slots o .. o + 3 of this lane
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        sv[4 * q + v] = cand_s[(o + v) * kWave];
+        id[4 * q + v] = (int)cand_i[(o + v) * kWave];
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NK / 4; ++q) {
     const bool kpt = 4 * q < KQ;
     const int o = kpt ? 4 * q : 4 * q - KQ;
     const int lim = kpt ? kv : cnt;
-    const float4 s4 = *reinterpret_cast<const float4*>((kpt ? kept_s : cand_s) + o);
-    const uint2 i4 = *reinterpret_cast<const uint2*>((kpt ? kept_i : cand_i) + o);
-    key[4 * q + 0] = (o + 0 < lim) ? order_key(s4.x) : 0u;
-    key[4 * q + 1] = (o + 1 < lim) ? order_key(s4.y) : 0u;
-    key[4 * q + 2] = (o + 2 < lim) ? order_key(s4.z) : 0u;
-    key[4 * q + 3] = (o + 3 < lim) ? order_key(s4.w) : 0u;
-    id[4 * q + 0] = (int)(i4.x & 0xffffu);
-    id[4 * q + 1] = (int)(i4.x >> 16);
-    id[4 * q + 2] = (int)(i4.y & 0xffffu);
-    id[4 * q + 3] = (int)(i4.y >> 16);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float x = sv[4 * q + v];
+      if (act(q)) asm volatile("" : "+v"(x));
+      key[4 * q + v] = (act(q) && o + v < lim) ? order_key(x) : 0u;
+    }
   }
   // valid keys are > 0 (order keys of finite or infinite floats are nonzero)
   uint32_t khi = 0, klo = 0xffffffffu;
@@ -413,15 +446,15 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
   const int n_row = w + w1 + w2 + w3;
   int pos = ((g & 1) ? w1 : 0) + ((g & 2) ? (w2 + w3) : 0);
   if (!tie_row) {
-    const int trash = KEEP + g * CAP + CAP - 1;
+    float* trash_s = cand_s + (CAP - 1) * kWave;
+    uint16_t* trash_i = cand_i + (CAP - 1) * kWave;
     // the reads above have returned (their values feed these stores)
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
       if (!act(i / 4)) continue;
       const bool kp = (keep_bits >> i) & 1ull;
-      const int at = kp ? pos : trash;
-      row_s[at] = key_to_float(key[i]);
-      row_i[at] = (uint16_t)id[i];
+      *(kp ? row_s + pos : trash_s) = key_to_float(key[i]);
+      *(kp ? row_i + pos : trash_i) = (uint16_t)id[i];
       pos += kp ? 1 : 0;
     }
     if (total >= k) theta = key_to_float(theta_key);
@@ -533,8 +566,11 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
   constexpr int F4 = kSelChunk * RP / 4;   // float4s per staged chunk
   constexpr int PER = (F4 + 511) / 512;    // of them per thread
 
-  __shared__ __align__(16) float s_slot_s[ROWS * kSelScoreStride];
-  __shared__ __align__(16) uint16_t s_slot_i[ROWS * kSelIndexStride];
+  constexpr int KST = sel_kept_stride(KEEP), KIST = sel_kept_idx_stride(KEEP);
+  __shared__ __align__(16) float s_kept_s[ROWS * KST];
+  __shared__ __align__(16) uint16_t s_kept_i[ROWS * KIST];
+  __shared__ __align__(16) float s_cand_s[ROWS / kSelRowsPerWave * CAP * kWave];
+  __shared__ __align__(16) uint16_t s_cand_i[ROWS / kSelRowsPerWave * CAP * kWave];
   __shared__ __align__(16) _Float16 s_key[COOP ? 2 * KBUF : 8];
   __shared__ int s_flag[3];
 
@@ -678,10 +714,12 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
   float theta = row_ok ? -INFINITY : INFINITY;  // invalid rows never admit
   int cnt = 0;   // candidates in this lane's region of its row
   int kept = 0;  // valid kept entries of this lane's row (<= k)
-  float* my_slot_s = s_slot_s + lrow * kSelScoreStride;
-  uint16_t* my_slot_i = s_slot_i + lrow * kSelIndexStride;
-  float* my_cand_s = my_slot_s + KEEP + g * CAP;
-  uint16_t* my_cand_i = my_slot_i + KEEP + g * CAP;
+  float* my_kept_s = s_kept_s + lrow * KST;
+  uint16_t* my_kept_i = s_kept_i + lrow * KIST;
+  float* wave_cand_s = s_cand_s + wave * CAP * kWave;
+  uint16_t* wave_cand_i = s_cand_i + wave * CAP * kWave;
+  float* my_cand_s = wave_cand_s + lane;
+  uint16_t* my_cand_i = wave_cand_i + lane;
 
   auto process = [&](auto SET, int c) {
     constexpr int S = decltype(SET)::value;
@@ -768,8 +806,8 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
       // the region)
 #pragma unroll
       for (int u = 0; u < kSelLaneKeys; ++u) {
-        my_cand_s[cnt] = sc[u];
-        my_cand_i[cnt] = (uint16_t)(c0 + (u >> 2) * 16 + 4 * g + (u & 3));
+        my_cand_s[cnt * kWave] = sc[u];
+        my_cand_i[cnt * kWave] = (uint16_t)(c0 + (u >> 2) * 16 + 4 * g + (u & 3));
         cnt += (sc[u] > theta) ? 1 : 0;
       }
     }
@@ -784,7 +822,8 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
       const int total = kept + row_sum4(cnt);
       const int cq = (int)(__builtin_amdgcn_readfirstlane(wave_max_u32((uint32_t)cnt)) + 3) / 4;
       const MergeResult mr =
-          merge_rows_batched<KEEP>(my_slot_s, my_slot_i, k, kept, cnt, total, last ? k : KEEP, theta, cq);
+          merge_rows_batched<KEEP>(my_kept_s, my_kept_i, my_cand_s, my_cand_i, k, kept, cnt, total, last ? k : KEEP,
+                                   theta, cq);
       const int n_kept = mr.kept;
       theta = mr.theta;
       // rows with exact ties at the k-th value: exact per-row merge (such a
@@ -794,7 +833,7 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
         const int t = __builtin_ctzll(m);
         m &= m - 1;
         const int slot = wave * kSelRowsPerWave + t;
-        const float th = merge_row_exact<KEEP>(s_slot_s + slot * kSelScoreStride, s_slot_i + slot * kSelIndexStride,
+        const float th = merge_row_exact<KEEP>(s_kept_s + slot * KST, s_kept_i + slot * KIST, wave_cand_s, wave_cand_i, t,
                                                k, readlane_i(kept, t), readlane_i(cnt, t), readlane_i(cnt, t + 16),
                                                readlane_i(cnt, t + 32), readlane_i(cnt, t + 48));
         if (col == t) theta = th;
@@ -887,8 +926,8 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
       float vs = -INFINITY;
       int vi = 0x7fffffff;
       if (e < k) {
-        vs = s_slot_s[slot * kSelScoreStride + e];
-        vi = s_slot_i[slot * kSelIndexStride + e];
+        vs = s_kept_s[slot * KST + e];
+        vi = s_kept_i[slot * KIST + e];
       }
       bitonic_sort32x2_desc(vs, vi);
       if (scaled_domain) {
@@ -909,8 +948,8 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
     float vs = -INFINITY;
     int vi = 0x7fffffff;
     if (lane < k) {
-      vs = s_slot_s[slot * kSelScoreStride + lane];
-      vi = s_slot_i[slot * kSelIndexStride + lane];
+      vs = s_kept_s[slot * KST + lane];
+      vi = s_kept_i[slot * KIST + lane];
     }
     bitonic_sort64_desc(vs, vi);
     if (scaled_domain) vs = ldexpf(vs, -readlane_i(score_exp, t));

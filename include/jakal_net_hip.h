@@ -60,12 +60,13 @@ int jn_set_gemm_tile(int32_t tile);
  * scaled by a power of two and written as hi + lo (22 significant bits), and
  * a score is hi.hi + hi.lo + lo.hi accumulated in fp32, within about
  * 3 * 2^-22 * sum_r |q_r k_r| of the exact value (fp32 accumulation itself is
- * within r * 2^-24 of it).  mode 1 computes them on fp32 MFMAs.  Modes 2
- * and 3 are mode 0 on one kernel only: 2 the per-wave streaming kernel, 3 the
- * cooperative kernel (key chunks staged once per workgroup in LDS) whenever
- * rank <= 64; mode 0 picks the cooperative one for rank <= 64 when the grid
- * has at least 256 of its 128-row workgroups.  All pick the same entries.
- * Modes 0, 2 and 3 need the select workspace below (the *_workspace_bytes
+ * within r * 2^-24 of it).  mode 1 computes them on fp32 MFMAs.  Modes 2-4
+ * are mode 0 on one kernel only: 2 the per-wave streaming kernel, 3 and 4 a
+ * cooperative kernel (key chunks staged once per workgroup in LDS; 8 waves
+ * and one workgroup per CU, or 4 waves and two) whenever rank <= 64; mode 0
+ * picks the 4-wave cooperative kernel for rank <= 64 when the grid has at
+ * least 512 of its 64-row workgroups.  All pick the same entries.
+ * Modes 0 and 2-4 need the select workspace below (the *_workspace_bytes
  * queries report 0 in mode 1).  Process-wide; takes effect for later calls,
  * including their workspace queries.
  */

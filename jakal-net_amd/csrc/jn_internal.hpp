@@ -32,12 +32,14 @@ constexpr int kSelectMaxK = 64;
 // significant bits per operand, fp32 accumulation); kSelectF32 runs them on
 // fp32 MFMAs.  The split needs select_workspace_bytes() of scratch.
 constexpr int kSelectSplitF16 = 0;
-// Split fp16 on one kernel only (tests): the per-wave streaming kernel, or the
-// cooperative (LDS-staged, 8-wave) kernel whenever the rank is at most 64.
-// kSelectSplitF16 picks the cooperative kernel for rank <= 64 when the grid has
-// at least one of its workgroups per CU.
+// Split fp16 on one kernel only (tests): the per-wave streaming kernel, or a
+// cooperative (LDS-staged) kernel whenever the rank is at most 64: 8 waves
+// and one workgroup per CU, or 4 waves and two per CU.  kSelectSplitF16 picks
+// the 4-wave cooperative kernel for rank <= 64 on grids of at least 512
+// workgroups, else the per-wave kernel.
 constexpr int kSelectSplitF16Wave = 2;
 constexpr int kSelectSplitF16Coop = 3;
+constexpr int kSelectSplitF16Coop4 = 4;
 constexpr int kSelectF32 = 1;
 int select_mode();
 void set_select_mode(int mode);

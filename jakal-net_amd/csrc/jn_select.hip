@@ -550,28 +550,34 @@ __device__ __forceinline__ halfx8 as_halfx8(float a, float b, float c, float d) 
 // is one global read of each key chunk instead of eight.  A wave that needs
 // to merge raises a workgroup flag before the barrier and then every wave
 // merges after it, so a merge holds up no other wave at the next barrier.
-template <int RQ, bool VEC, int KEEP, int KS, bool COOP>
-__global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2)) void lowrank_topk_select_kernel(SelectArgs a) {
+// CW = 4 is the same with 4 waves (64 rows) and one staging buffer (two
+// barriers per chunk), two workgroups per CU whose phases drift apart.
+template <int RQ, bool VEC, int KEEP, int KS, int CW>
+__global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
+                             CW == 8 ? 1 : CW == 4 ? 2 : ((KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2)) void lowrank_topk_select_kernel(SelectArgs a) {
+  constexpr bool COOP = CW > 0;
+  constexpr int NT = COOP ? CW * kWave : 256;  // threads
+  constexpr int NBUF = CW == 8 ? 2 : 1;        // staging buffers
   constexpr int CAP = sel_lane_cap(KEEP);
   constexpr bool SPLIT = KS > 0;
   constexpr bool V4 = VEC && RQ % 4 == 0;
   constexpr int FR = SPLIT ? 8 * KS : RQ;  // key fragment registers per tile
   constexpr int RP = 32 * KS;              // split row: ranks per plane
-  constexpr int ROWS = (COOP ? 2 : 1) * kSelRows;  // query rows per workgroup
+  constexpr int ROWS = COOP ? CW * kSelRowsPerWave : kSelRows;  // query rows per workgroup
   static_assert(!COOP || (KS >= 1 && KS <= 2), "the cooperative select stages split keys of rank <= 64");
   // staged chunk: kSelChunk split rows of 2 RP halves plus 8 halves of padding,
   // so the 16 rows one fragment read touches start 68 dwords apart (4 banks)
   constexpr int KROW = 2 * RP + 8;
   constexpr int KBUF = kSelChunk * KROW;
   constexpr int F4 = kSelChunk * RP / 4;   // float4s per staged chunk
-  constexpr int PER = (F4 + 511) / 512;    // of them per thread
+  constexpr int PER = (F4 + NT - 1) / NT;  // of them per thread
 
   constexpr int KST = sel_kept_stride(KEEP), KIST = sel_kept_idx_stride(KEEP);
   __shared__ __align__(16) float s_kept_s[ROWS * KST];
   __shared__ __align__(16) uint16_t s_kept_i[ROWS * KIST];
   __shared__ __align__(16) float s_cand_s[ROWS / kSelRowsPerWave * CAP * kWave];
   __shared__ __align__(16) uint16_t s_cand_i[ROWS / kSelRowsPerWave * CAP * kWave];
-  __shared__ __align__(16) _Float16 s_key[COOP ? 2 * KBUF : 8];
+  __shared__ __align__(16) _Float16 s_key[COOP ? NBUF * KBUF : 8];
   __shared__ int s_flag[3];
 
   const int lane = lane_id();
@@ -727,7 +733,7 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
     if constexpr (COOP) {
       // this wave's fragments of the staged chunk: lane (g, col) reads ranks
       // [32 s + 8 g, +8) of row 16 t + col from each plane
-      const _Float16* kb = s_key + (c & 1) * KBUF + col * KROW + 8 * g;
+      const _Float16* kb = s_key + (NBUF == 2 ? (c & 1) : 0) * KBUF + col * KROW + 8 * g;
 #pragma unroll
       for (int t = 0; t < kSelTiles; ++t)
 #pragma unroll
@@ -851,7 +857,7 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
   // past the end read rows >= Nk: zeros, no memory access), so the wait before
   // a chunk's MFMAs covers only its own loads, not the prefetch behind them.
   if constexpr (COOP) {
-    // cooperative staging: thread x moves float4s x + 512 p of the chunk
+    // cooperative staging: thread x moves float4s x + NT p of the chunk
     float4 pre[PER];
     auto stage_load = [&](int c) {
       const int c0 = c * kSelChunk;
@@ -860,14 +866,14 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
       const auto rs = make_rsrc(split_b + (int64_t)c0 * 2 * RP, nrec);
 #pragma unroll
       for (int p = 0; p < PER; ++p) {
-        const int f = (int)threadIdx.x + 512 * p;
+        const int f = (int)threadIdx.x + NT * p;
         pre[p] = buf_load4(rs, f < F4 ? (uint32_t)f * 16u : kOobOffset);
       }
     };
     auto stage_store = [&](int buf) {
 #pragma unroll
       for (int p = 0; p < PER; ++p) {
-        const int f = (int)threadIdx.x + 512 * p;
+        const int f = (int)threadIdx.x + NT * p;
         if (f < F4) {
           const int row = f / (RP / 4), part = f - row * (RP / 4);
           *reinterpret_cast<float4*>(s_key + buf * KBUF + row * KROW + 8 * part) = pre[p];
@@ -884,6 +890,8 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
     // chunk c + 2, merge every wave if the flag is up.  Wave 0 clears flag
     // (c + 1) % 3 = (c - 2) % 3, read by all before the previous barrier and
     // raised again only after this one.
+    // With one buffer (CW = 4) a second barrier separates the last reads of
+    // chunk c from the stores of chunk c + 1.
     int fl = 0;  // c % 3
     for (int c = 0; c < nchunks; ++c) {
       process(kSet0, c);
@@ -891,7 +899,8 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
       if (need_merge() && lane == 0) s_flag[fl] = 1;
       const int fl_next = fl == 2 ? 0 : fl + 1;
       if (wave == 0 && lane == 0) s_flag[fl_next] = 0;
-      if (!last) stage_store((c + 1) & 1);
+      if constexpr (NBUF == 1) __syncthreads();
+      if (!last) stage_store(NBUF == 2 ? (c + 1) & 1 : 0);
       __syncthreads();
       if (c + 2 < nchunks) stage_load(c + 2);
       const bool go = last ? need_final() : __builtin_amdgcn_readfirstlane(s_flag[fl]) != 0;
@@ -964,24 +973,26 @@ __global__ __launch_bounds__(COOP ? 512 : 256, COOP ? 1 : ((KS > 0 ? KS > 2 : RQ
 template <int RQ>
 static void launch_rq(const SelectArgs& a, bool vec, dim3 grid, hipStream_t stream) {
   if (a.k <= 32) {
-    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 48, 0, false>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 48, 0, false>), grid, dim3(256), 0, stream, a);
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 48, 0, 0>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 48, 0, 0>), grid, dim3(256), 0, stream, a);
   } else {
-    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 80, 0, false>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 80, 0, false>), grid, dim3(256), 0, stream, a);
+    if (vec) hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, true, 80, 0, 0>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<RQ, false, 80, 0, 0>), grid, dim3(256), 0, stream, a);
   }
 }
 
-template <int KS, bool COOP>
+template <int KS, int CW>
 static void launch_split(const SelectArgs& a, dim3 grid, hipStream_t stream) {
-  const dim3 block(COOP ? 512 : 256);
-  if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, COOP>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS, COOP>), grid, block, 0, stream, a);
+  const dim3 block(CW > 0 ? CW * kWave : 256);
+  if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, CW>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS, CW>), grid, block, 0, stream, a);
 }
 
-// The cooperative kernel holds one workgroup per CU; below one workgroup per
-// CU the per-wave kernel (two workgroups of 64 rows per CU) spreads wider.
-constexpr int64_t kSelCoopMinBlocks = 256;
+// The cooperative kernels pay for their barriers with shared key staging,
+// which wins once every CU holds two 64-row workgroups (C4: 0.40 ms against
+// 0.53 for the per-wave kernel); on smaller grids (C3's 128 and 32
+// workgroups) the per-wave kernel is as fast or faster.
+constexpr int64_t kSelCoop4MinBlocks = 512;
 
 namespace {
 int g_select_mode = kSelectSplitF16;
@@ -1051,19 +1062,23 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
     a.split_key = s.split;
     a.split_exp = s.kexp;
     const int64_t coop_blocks = (int64_t)((a.Nq + 2 * kSelRows - 1) / (2 * kSelRows)) * a.B;
-    const bool coop = RP <= 64 && (g_select_mode == kSelectSplitF16Coop ||
-                                   (g_select_mode == kSelectSplitF16 && coop_blocks >= kSelCoopMinBlocks));
+    const bool coop4 = RP <= 64 && (g_select_mode == kSelectSplitF16Coop4 ||
+                                    (g_select_mode == kSelectSplitF16 && blocks >= kSelCoop4MinBlocks));
+    const bool coop = RP <= 64 && g_select_mode == kSelectSplitF16Coop;
     JN_PROFILE("lowrank_topk_select_kernel", stream);
-    if (coop) {
+    if (coop4) {
+      if (RP == 32) launch_split<1, 4>(a, grid, stream);
+      else launch_split<2, 4>(a, grid, stream);
+    } else if (coop) {
       const dim3 cgrid((unsigned)coop_blocks);
-      if (RP == 32) launch_split<1, true>(a, cgrid, stream);
-      else launch_split<2, true>(a, cgrid, stream);
+      if (RP == 32) launch_split<1, 8>(a, cgrid, stream);
+      else launch_split<2, 8>(a, cgrid, stream);
     } else {
       switch (RP / 32) {
-        case 1: launch_split<1, false>(a, grid, stream); break;
-        case 2: launch_split<2, false>(a, grid, stream); break;
-        case 3: launch_split<3, false>(a, grid, stream); break;
-        default: launch_split<4, false>(a, grid, stream); break;
+        case 1: launch_split<1, 0>(a, grid, stream); break;
+        case 2: launch_split<2, 0>(a, grid, stream); break;
+        case 3: launch_split<3, 0>(a, grid, stream); break;
+        default: launch_split<4, 0>(a, grid, stream); break;
       }
     }
     JN_LAUNCH_CHECK();

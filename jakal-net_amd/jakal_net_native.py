@@ -160,12 +160,14 @@ SELECT_SPLIT_F16 = 0
 SELECT_F32 = 1
 SELECT_SPLIT_F16_WAVE = 2
 SELECT_SPLIT_F16_COOP = 3
+SELECT_SPLIT_F16_COOP4 = 4
 
 
 def set_select_mode(mode: int = SELECT_SPLIT_F16) -> None:
     """Score arithmetic of the top-k select for later calls: SELECT_SPLIT_F16 (default, fp16 MFMAs over
     two-term fp16 operand splits, fp32 accumulation) or SELECT_F32 (fp32 MFMAs); SELECT_SPLIT_F16_WAVE and
-    SELECT_SPLIT_F16_COOP run the split arithmetic on the per-wave or the cooperative (LDS-staged) kernel only."""
+    SELECT_SPLIT_F16_COOP / SELECT_SPLIT_F16_COOP4 run the split arithmetic on the per-wave or an 8- or 4-wave
+    cooperative (LDS-staged) kernel only."""
     _check(_LIB.jn_set_select_mode(int(mode)))
 
 

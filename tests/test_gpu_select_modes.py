@@ -3,8 +3,9 @@
 The per-op tests run the default split-fp16 select (fp16 MFMAs over two-term
 fp16 splits of power-of-two-scaled operands, fp32 accumulation).  These tests
 cover the fp32-MFMA select (jn_set_select_mode(1)) and each split-fp16 kernel
-on its own (per-wave streaming, mode 2; LDS-staged cooperative, mode 3) on the
-same select, top-k propagation and transition cases, check that the two split
+on its own (per-wave streaming, mode 2; LDS-staged cooperative with 8 or 4
+waves, modes 3 and 4) on the
+same select, top-k propagation and transition cases, check that the split
 kernels pick identical entries and values up to the C4 shape, and the split path on what its scaling has
 to survive: key and query rows whose magnitudes span many octaves, all-zero
 rows, ranks that are not a multiple of the 32-rank K-step, and bias and
@@ -35,10 +36,10 @@ def _mode_value(name):
     import jakal_net_native as jn
 
     return {"split_f16": jn.SELECT_SPLIT_F16, "f32": jn.SELECT_F32, "split_wave": jn.SELECT_SPLIT_F16_WAVE,
-            "split_coop": jn.SELECT_SPLIT_F16_COOP}[name]
+            "split_coop": jn.SELECT_SPLIT_F16_COOP, "split_coop4": jn.SELECT_SPLIT_F16_COOP4}[name]
 
 
-@pytest.fixture(params=["split_f16", "f32", "split_wave", "split_coop"])
+@pytest.fixture(params=["split_f16", "f32", "split_wave", "split_coop", "split_coop4"])
 def mode(request):
     import jakal_net_native as jn
 
@@ -144,9 +145,9 @@ def test_transition_f32_mode(dev, f32_mode):
                                                   (32, 7, 3, 300, 5000, False), (17, 16, 1, 129, 48, False),
                                                   (64, 32, 2, 256, 4000, True)])
 def test_split_kernels_agree(dev, r, k, B, Nq, Nk, dominant):
-    """The per-wave and the cooperative kernel compute every score with the same
-    MFMA sequence and keep the k best by the same rule, so their outputs are
-    bit-identical (the C4 shape included); the cooperative kernel merges at
+    """The per-wave and both cooperative kernels compute every score with the
+    same MFMA sequence and keep the k best by the same rule, so their outputs
+    are bit-identical (the C4 shape included); the cooperative kernels merge at
     other chunks, which must not change the result."""
     import jakal_net_native as jn
 
@@ -159,16 +160,17 @@ def test_split_kernels_agree(dev, r, k, B, Nq, Nk, dominant):
     scale = torch.rand(r, generator=g) + 0.5
     out = {}
     try:
-        for m in (jn.SELECT_SPLIT_F16_WAVE, jn.SELECT_SPLIT_F16_COOP):
+        for m in (jn.SELECT_SPLIT_F16_WAVE, jn.SELECT_SPLIT_F16_COOP, jn.SELECT_SPLIT_F16_COOP4):
             jn.set_select_mode(m)
             idx, score = jn.low_rank_topk_select(q.to(dev), key.to(dev), scale.to(dev), None, False, 1.0, k)
             out[m] = (idx.cpu(), score.cpu())
     finally:
         jn.set_select_mode(jn.SELECT_SPLIT_F16)
     wi, ws = out[jn.SELECT_SPLIT_F16_WAVE]
-    ci, cs = out[jn.SELECT_SPLIT_F16_COOP]
-    assert torch.equal(wi, ci)
-    assert torch.equal(ws, cs)
+    for m in (jn.SELECT_SPLIT_F16_COOP, jn.SELECT_SPLIT_F16_COOP4):
+        ci, cs = out[m]
+        assert torch.equal(wi, ci)
+        assert torch.equal(ws, cs)
     # and the result is a top-k: sorted, in range, no repeats
     assert bool((ws[..., :-1] >= ws[..., 1:]).all())
     assert int(wi.min()) >= 0 and int(wi.max()) < Nk

@@ -267,3 +267,44 @@ def test_c4_shape_forward_sampled_rows(dev):
         _close(_np(dv[bb, rows]), want_v.numpy(), what="C4 delta_val rows")
         _close(_np(ds[bb, rows]), want_s.numpy(), what="C4 delta_state rows")
     print(f"C4 sampled rows with unambiguous top-k: {checked}/24")
+
+
+def test_c4_shape_select_every_row(dev):
+    """The select at the full C4 shape (B=16, N=4096, r=64, k=32, unit-norm value
+    rows, default init) on every one of the 65,536 rows, against fp32 scores of
+    all 2.7e8 pairs from torch (scored one batch element at a time): each row's
+    k indices are distinct and in range, its scores are sorted descending and
+    within 1e-6 of the torch scores of those indices, and no index left out
+    scores more than 1e-5 above the row's k-th score (the gap rule).  A
+    dropped key, a wrong index, a misplaced merge or a lost candidate fails one
+    of these on some row."""
+    import jakal_net_native as jn
+
+    B, N, D, r, k = 16, 4096, 512, 64, 32
+    g = torch.Generator().manual_seed(1004)
+    val = torch.randn(B, N, D, generator=g)
+    val = val / val.norm(dim=-1, keepdim=True)
+    bound = 1.0 / D ** 0.5
+    U = (torch.rand(r, D, generator=g) * 2 - 1) * bound
+    V = (torch.rand(r, D, generator=g) * 2 - 1) * bound
+    w_hat = torch.ones(r) / r ** 0.5
+    P = val.to(dev) @ torch.cat([U, V]).to(dev).T
+    q = P[..., :r].contiguous()
+    key = P[..., r:].contiguous()
+    idx, score = jn.low_rank_topk_select(q, key, w_hat.to(dev), None, False, 1.0, k)
+    idx = idx.long()
+    assert int(idx.min()) >= 0 and int(idx.max()) < N
+    srt = idx.sort(dim=-1).values
+    assert bool((srt[..., 1:] != srt[..., :-1]).all()), "repeated index in a row"
+    assert bool((score[..., :-1] >= score[..., 1:]).all()), "scores not sorted"
+    worst_val, worst_gap = 0.0, -1.0
+    for b in range(B):
+        S = q[b] @ (key[b] * w_hat.to(dev)).T  # fp32 [N, N]
+        picked = S.gather(1, idx[b])
+        worst_val = max(worst_val, float((picked - score[b]).abs().max()))
+        kth = score[b, :, -1:]
+        S.scatter_(1, idx[b], -float("inf"))  # leave out the selected keys
+        worst_gap = max(worst_gap, float((S.max(dim=1, keepdim=True).values - kth).max()))
+    print(f"C4 select, all rows: max |score - torch score| {worst_val:.2e}, max excluded-over-kth {worst_gap:.2e}")
+    assert worst_val <= 1e-6
+    assert worst_gap <= 1e-5

@@ -65,8 +65,11 @@ int jn_set_gemm_tile(int32_t tile);
  * cooperative kernel (key chunks staged once per workgroup in LDS; 8 waves
  * and one workgroup per CU, or 4 waves and two) whenever rank <= 64; mode 0
  * picks the 4-wave cooperative kernel for rank <= 64 when the grid has at
- * least 512 of its 64-row workgroups.  All pick the same entries.
- * Modes 0 and 2-4 need the select workspace below (the *_workspace_bytes
+ * least 512 of its 64-row workgroups, and for k <= 16 on grids below 256 of
+ * them with >= 192 keys a key-split per-wave kernel (the four waves of a
+ * workgroup share 16 query rows, each over a quarter of the keys; mode 5
+ * forces it whenever k <= 16).  All pick the same entries.
+ * Modes 0 and 2-5 need the select workspace below (the *_workspace_bytes
  * queries report 0 in mode 1).  Process-wide; takes effect for later calls,
  * including their workspace queries.
  */

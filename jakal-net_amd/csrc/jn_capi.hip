@@ -420,9 +420,9 @@ int jn_set_gemm_tile(int32_t tile) {
 }
 
 int jn_set_select_mode(int32_t mode) {
-  JN_REQUIRE(mode >= jakal::kSelectSplitF16 && mode <= jakal::kSelectSplitF16Coop4, kInvalidArgument,
+  JN_REQUIRE(mode >= jakal::kSelectSplitF16 && mode <= jakal::kSelectSplitF16KeySplit, kInvalidArgument,
              "select mode must be 0 (split fp16), 1 (fp32), 2 (split fp16, per-wave kernel), 3 or 4 (split "
-             "fp16, 8- or 4-wave cooperative kernel), got %d",
+             "fp16, 8- or 4-wave cooperative kernel) or 5 (split fp16, key-split per-wave kernel), got %d",
              (int)mode);
   jakal::set_select_mode(mode);
   return kOk;

@@ -40,6 +40,9 @@ constexpr int kSelectSplitF16 = 0;
 constexpr int kSelectSplitF16Wave = 2;
 constexpr int kSelectSplitF16Coop = 3;
 constexpr int kSelectSplitF16Coop4 = 4;
+// Split fp16 on the key-split per-wave kernel whenever k <= 16 (tests); mode 0
+// picks it for k <= 16 on grids below 256 workgroups with >= 192 keys.
+constexpr int kSelectSplitF16KeySplit = 5;
 constexpr int kSelectF32 = 1;
 int select_mode();
 void set_select_mode(int mode);

@@ -552,10 +552,16 @@ __device__ __forceinline__ halfx8 as_halfx8(float a, float b, float c, float d) 
 // merges after it, so a merge holds up no other wave at the next barrier.
 // CW = 4 is the same with 4 waves (64 rows) and one staging buffer (two
 // barriers per chunk), two workgroups per CU whose phases drift apart.
+// CW = -1 (k <= 16, small grids): the per-wave form with the four waves of a
+// workgroup on the same 16 query rows, each over a quarter of the key chunks;
+// each keeps the exact top-k of its quarter, and a 64-entry sort per row
+// merges the four lists at the end.  Four times the workgroups and a quarter
+// of the serial chunk chain per wave.
 template <int RQ, bool VEC, int KEEP, int KS, int CW>
 __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
                              CW == 8 ? 1 : CW == 4 ? 2 : ((KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2)) void lowrank_topk_select_kernel(SelectArgs a) {
   constexpr bool COOP = CW > 0;
+  constexpr bool KSP = CW < 0;
   constexpr int NT = COOP ? CW * kWave : 256;  // threads
   constexpr int NBUF = CW == 8 ? 2 : 1;        // staging buffers
   constexpr int CAP = sel_lane_cap(KEEP);
@@ -563,7 +569,9 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   constexpr bool V4 = VEC && RQ % 4 == 0;
   constexpr int FR = SPLIT ? 8 * KS : RQ;  // key fragment registers per tile
   constexpr int RP = 32 * KS;              // split row: ranks per plane
-  constexpr int ROWS = COOP ? CW * kSelRowsPerWave : kSelRows;  // query rows per workgroup
+  constexpr int ROWS = COOP ? CW * kSelRowsPerWave : KSP ? kSelRowsPerWave : kSelRows;  // query rows per workgroup
+  constexpr int SLOTS = COOP ? CW * kSelRowsPerWave : kSelRows;  // row slots (16 per wave)
+  static_assert(!KSP || KEEP == 48, "the key-split form serves k <= 16");
   static_assert(!COOP || (KS >= 1 && KS <= 2), "the cooperative select stages split keys of rank <= 64");
   // staged chunk: kSelChunk split rows of 2 RP halves plus 8 halves of padding,
   // so the 16 rows one fragment read touches start 68 dwords apart (4 banks)
@@ -573,10 +581,10 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   constexpr int PER = (F4 + NT - 1) / NT;  // of them per thread
 
   constexpr int KST = sel_kept_stride(KEEP), KIST = sel_kept_idx_stride(KEEP);
-  __shared__ __align__(16) float s_kept_s[ROWS * KST];
-  __shared__ __align__(16) uint16_t s_kept_i[ROWS * KIST];
-  __shared__ __align__(16) float s_cand_s[ROWS / kSelRowsPerWave * CAP * kWave];
-  __shared__ __align__(16) uint16_t s_cand_i[ROWS / kSelRowsPerWave * CAP * kWave];
+  __shared__ __align__(16) float s_kept_s[SLOTS * KST];
+  __shared__ __align__(16) uint16_t s_kept_i[SLOTS * KIST];
+  __shared__ __align__(16) float s_cand_s[SLOTS / kSelRowsPerWave * CAP * kWave];
+  __shared__ __align__(16) uint16_t s_cand_i[SLOTS / kSelRowsPerWave * CAP * kWave];
   __shared__ __align__(16) _Float16 s_key[COOP ? NBUF * KBUF : 8];
   __shared__ int s_flag[3];
 
@@ -595,11 +603,20 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   const float* kbase = a.key + (int64_t)b * a.k_batch_stride;
   const int k = a.k;
   const int ldk = (int)a.ldk;
+  // key chunks of this wave: all of them, or a quarter in the key-split form
+  const int nchunks_all = (a.Nk + kSelChunk - 1) / kSelChunk;
+  int chunk0 = 0, nchunks = nchunks_all, key_end = a.Nk;
+  if constexpr (KSP) {
+    const int per = (nchunks_all + kSelWaves - 1) / kSelWaves;
+    chunk0 = min(nchunks_all, wave * per);
+    nchunks = min(nchunks_all, chunk0 + per) - chunk0;
+    key_end = min(a.Nk, (chunk0 + nchunks) * kSelChunk);
+  }
 
   // ---- query fragment in registers, times the scale vector: both score forms
   // (scaled query or scaled key) equal sum_r q[r] * c[r] * key[r] ---------------
   const int lrow = wave * kSelRowsPerWave + col;  // row slot within the workgroup
-  const int my_row = row0 + lrow;
+  const int my_row = row0 + (KSP ? col : lrow);
   const bool row_ok = my_row < a.Nq;
   // unconditional loads (invalid rows and ranks read row 0 / rank 0 and are
   // zeroed after), so they all issue before one wait
@@ -672,8 +689,8 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
       SPLIT ? reinterpret_cast<const _Float16*>(a.split_key) + (int64_t)b * a.Nk * 2 * RP : nullptr;
   auto load_keys = [&](auto SET, int c) {
     constexpr int S = decltype(SET)::value;
-    const int c0 = c * kSelChunk;
-    const int rows = max(0, min(kSelChunk, a.Nk - c0));
+    const int c0 = (chunk0 + c) * kSelChunk;
+    const int rows = max(0, min(kSelChunk, key_end - c0));
     // uniform (readfirstlane keeps the resource in SGPRs)
     const uint32_t nrec = __builtin_amdgcn_readfirstlane(SPLIT ? (uint32_t)(rows * 4 * RP) : (uint32_t)(rows * ldk) * 4u);
     const auto rs = SPLIT ? make_rsrc(split_b + (int64_t)c0 * 2 * RP, nrec) : make_rsrc(kbase + (int64_t)c0 * ldk, nrec);
@@ -715,7 +732,6 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   constexpr std::integral_constant<int, 0> kSet0{};
   constexpr std::integral_constant<int, 1> kSet1{};
 
-  const int nchunks = (a.Nk + kSelChunk - 1) / kSelChunk;
 
   float theta = row_ok ? -INFINITY : INFINITY;  // invalid rows never admit
   int cnt = 0;   // candidates in this lane's region of its row
@@ -729,7 +745,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
 
   auto process = [&](auto SET, int c) {
     constexpr int S = decltype(SET)::value;
-    const int c0 = c * kSelChunk;
+    const int c0 = (chunk0 + c) * kSelChunk;
     if constexpr (COOP) {
       // this wave's fragments of the staged chunk: lane (g, col) reads ranks
       // [32 s + 8 g, +8) of row 16 t + col from each plane
@@ -797,10 +813,10 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
 #pragma unroll
       for (int u = 0; u < kSelLaneKeys; ++u) sc[u] += bias;
     }
-    if (c0 + kSelChunk > a.Nk) {  // uniform: only the last chunk holds padding keys
+    if (c0 + kSelChunk > key_end) {  // uniform: only the last chunk holds padding keys
 #pragma unroll
       for (int u = 0; u < kSelLaneKeys; ++u)
-        if (c0 + (u >> 2) * 16 + 4 * g + (u & 3) >= a.Nk) sc[u] = -INFINITY;
+        if (c0 + (u >> 2) * 16 + 4 * g + (u & 3) >= key_end) sc[u] = -INFINITY;
     }
     uint64_t any = 0;
 #pragma unroll
@@ -924,6 +940,35 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   }
   wave_lds_sync();
 
+  if constexpr (KSP) {
+    // every wave holds the exact top-k of its key quarter for the workgroup's
+    // 16 rows, unsorted in its own kept slots; wave w merges rows 4w .. 4w + 3
+    // over the four lists (lane (src, e): entry e of wave src's list)
+    __shared__ int s_kcnt[kSelRows];
+    if (lane < kSelRowsPerWave) s_kcnt[wave * kSelRowsPerWave + lane] = kept;
+    __syncthreads();
+    const int src = lane >> 4, e = lane & 15;
+    for (int t = 0; t < kSelRowsPerWave / kSelWaves; ++t) {
+      const int rcol = (kSelRowsPerWave / kSelWaves) * wave + t;
+      const int row = row0 + rcol;
+      const int slot = src * kSelRowsPerWave + rcol;
+      float vs = -INFINITY;
+      int vi = 0x7fffffff;
+      if (e < s_kcnt[slot]) {
+        vs = s_kept_s[slot * KST + e];
+        vi = s_kept_i[slot * KIST + e];
+      }
+      bitonic_sort64_desc(vs, vi);
+      if (scaled_domain) vs = ldexpf(vs, -readlane_i(score_exp, rcol));
+      if (lane < k && row < a.Nq) {
+        const int64_t o = ((int64_t)b * a.Nq + row) * k + lane;
+        a.out_idx[o] = vi;
+        a.out_score[o] = vs;
+      }
+    }
+    return;
+  }
+
   // ---- sort each row's k winners and write them -----------------------------
   if constexpr (KEEP == 48) {
     // k <= 32: two rows per pass, row t + h on half-wave h
@@ -984,8 +1029,12 @@ static void launch_rq(const SelectArgs& a, bool vec, dim3 grid, hipStream_t stre
 template <int KS, int CW>
 static void launch_split(const SelectArgs& a, dim3 grid, hipStream_t stream) {
   const dim3 block(CW > 0 ? CW * kWave : 256);
-  if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, CW>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS, CW>), grid, block, 0, stream, a);
+  if constexpr (CW < 0) {
+    hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, CW>), grid, block, 0, stream, a);
+  } else {
+    if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, CW>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS, CW>), grid, block, 0, stream, a);
+  }
 }
 
 // The cooperative kernels pay for their barriers with shared key staging,
@@ -993,6 +1042,10 @@ static void launch_split(const SelectArgs& a, dim3 grid, hipStream_t stream) {
 // 0.53 for the per-wave kernel); on smaller grids (C3's 128 and 32
 // workgroups) the per-wave kernel is as fast or faster.
 constexpr int64_t kSelCoop4MinBlocks = 512;
+// Below one 64-row workgroup per CU, with k <= 16 and at least four key chunks,
+// the key-split per-wave form runs a quarter of the serial chunk chain.
+constexpr int64_t kSelKspMaxBlocks = 256;
+constexpr int kSelKspMinKeys = 4 * kSelChunk;
 
 namespace {
 int g_select_mode = kSelectSplitF16;
@@ -1065,6 +1118,9 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
     const bool coop4 = RP <= 64 && (g_select_mode == kSelectSplitF16Coop4 ||
                                     (g_select_mode == kSelectSplitF16 && blocks >= kSelCoop4MinBlocks));
     const bool coop = RP <= 64 && g_select_mode == kSelectSplitF16Coop;
+    const bool ksp = !coop4 && !coop && a.k <= 16 &&
+                     (g_select_mode == kSelectSplitF16KeySplit ||
+                      (g_select_mode == kSelectSplitF16 && blocks < kSelKspMaxBlocks && a.Nk >= kSelKspMinKeys));
     JN_PROFILE("lowrank_topk_select_kernel", stream);
     if (coop4) {
       if (RP == 32) launch_split<1, 4>(a, grid, stream);
@@ -1073,6 +1129,14 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
       const dim3 cgrid((unsigned)coop_blocks);
       if (RP == 32) launch_split<1, 8>(a, cgrid, stream);
       else launch_split<2, 8>(a, cgrid, stream);
+    } else if (ksp) {
+      const dim3 kgrid((unsigned)((int64_t)((a.Nq + kSelRowsPerWave - 1) / kSelRowsPerWave) * a.B));
+      switch (RP / 32) {
+        case 1: launch_split<1, -1>(a, kgrid, stream); break;
+        case 2: launch_split<2, -1>(a, kgrid, stream); break;
+        case 3: launch_split<3, -1>(a, kgrid, stream); break;
+        default: launch_split<4, -1>(a, kgrid, stream); break;
+      }
     } else {
       switch (RP / 32) {
         case 1: launch_split<1, 0>(a, grid, stream); break;

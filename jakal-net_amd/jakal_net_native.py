@@ -161,6 +161,7 @@ SELECT_F32 = 1
 SELECT_SPLIT_F16_WAVE = 2
 SELECT_SPLIT_F16_COOP = 3
 SELECT_SPLIT_F16_COOP4 = 4
+SELECT_SPLIT_F16_KEYSPLIT = 5
 
 
 def set_select_mode(mode: int = SELECT_SPLIT_F16) -> None:

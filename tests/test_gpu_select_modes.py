@@ -36,10 +36,11 @@ def _mode_value(name):
     import jakal_net_native as jn
 
     return {"split_f16": jn.SELECT_SPLIT_F16, "f32": jn.SELECT_F32, "split_wave": jn.SELECT_SPLIT_F16_WAVE,
-            "split_coop": jn.SELECT_SPLIT_F16_COOP, "split_coop4": jn.SELECT_SPLIT_F16_COOP4}[name]
+            "split_coop": jn.SELECT_SPLIT_F16_COOP, "split_coop4": jn.SELECT_SPLIT_F16_COOP4,
+            "split_keysplit": jn.SELECT_SPLIT_F16_KEYSPLIT}[name]
 
 
-@pytest.fixture(params=["split_f16", "f32", "split_wave", "split_coop", "split_coop4"])
+@pytest.fixture(params=["split_f16", "f32", "split_wave", "split_coop", "split_coop4", "split_keysplit"])
 def mode(request):
     import jakal_net_native as jn
 
@@ -143,12 +144,15 @@ def test_transition_f32_mode(dev, f32_mode):
 
 @pytest.mark.parametrize("r,k,B,Nq,Nk,dominant", [(64, 32, 16, 4096, 4096, False), (64, 64, 2, 700, 3001, False),
                                                   (32, 7, 3, 300, 5000, False), (17, 16, 1, 129, 48, False),
-                                                  (64, 32, 2, 256, 4000, True)])
+                                                  (64, 32, 2, 256, 4000, True), (64, 16, 8, 1024, 256, False),
+                                                  (64, 16, 8, 256, 1024, False), (100, 12, 2, 77, 1000, False),
+                                                  (64, 16, 2, 300, 2000, True)])
 def test_split_kernels_agree(dev, r, k, B, Nq, Nk, dominant):
-    """The per-wave and both cooperative kernels compute every score with the
-    same MFMA sequence and keep the k best by the same rule, so their outputs
-    are bit-identical (the C4 shape included); the cooperative kernels merge at
-    other chunks, which must not change the result."""
+    """The per-wave, both cooperative and (k <= 16) the key-split kernels
+    compute every score with the same MFMA sequence and keep the k best by the
+    same rule, so their outputs are bit-identical (the C4 and C3 shapes
+    included); the others merge at other chunks or over key quarters, which
+    must not change the result."""
     import jakal_net_native as jn
 
     g = torch.Generator().manual_seed(7000 + r + k + Nk)
@@ -160,14 +164,15 @@ def test_split_kernels_agree(dev, r, k, B, Nq, Nk, dominant):
     scale = torch.rand(r, generator=g) + 0.5
     out = {}
     try:
-        for m in (jn.SELECT_SPLIT_F16_WAVE, jn.SELECT_SPLIT_F16_COOP, jn.SELECT_SPLIT_F16_COOP4):
+        for m in (jn.SELECT_SPLIT_F16_WAVE, jn.SELECT_SPLIT_F16_COOP, jn.SELECT_SPLIT_F16_COOP4,
+                  jn.SELECT_SPLIT_F16_KEYSPLIT):
             jn.set_select_mode(m)
             idx, score = jn.low_rank_topk_select(q.to(dev), key.to(dev), scale.to(dev), None, False, 1.0, k)
             out[m] = (idx.cpu(), score.cpu())
     finally:
         jn.set_select_mode(jn.SELECT_SPLIT_F16)
     wi, ws = out[jn.SELECT_SPLIT_F16_WAVE]
-    for m in (jn.SELECT_SPLIT_F16_COOP, jn.SELECT_SPLIT_F16_COOP4):
+    for m in (jn.SELECT_SPLIT_F16_COOP, jn.SELECT_SPLIT_F16_COOP4, jn.SELECT_SPLIT_F16_KEYSPLIT):
         ci, cs = out[m]
         assert torch.equal(wi, ci)
         assert torch.equal(ws, cs)

@@ -15,7 +15,15 @@
 //     by the raw weight, key = destination projection, bias then /temperature,
 //     top-k per source over destinations (transition.py:439-444).
 //
-// Layout of one workgroup (256 threads = 4 waves, 64 query rows):
+// Three forms share the scoring, filter, merge and sort code below:
+//   * per-wave (described next): every wave streams all keys itself;
+//   * cooperative (rank <= 64, large grids): the workgroup stages each key
+//     chunk once in LDS and every wave reads its fragments from there, with a
+//     barrier per chunk and workgroup-wide merges (see the kernel template);
+//   * key-split (k <= 16, small grids): the four waves share 16 query rows,
+//     each over a quarter of the keys, merged by one sort per row at the end.
+//
+// Layout of one per-wave workgroup (256 threads = 4 waves, 64 query rows):
 //   * 16 query rows per wave.  A wave keeps the query fragment of its rows in
 //     VGPRs for the whole kernel (B operand of the MFMAs; lane l owns row
 //     l%16, rank slice l/16).

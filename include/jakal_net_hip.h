@@ -60,18 +60,18 @@ int jn_set_gemm_tile(int32_t tile);
  * scaled by a power of two and written as hi + lo (22 significant bits), and
  * a score is hi.hi + hi.lo + lo.hi accumulated in fp32, within about
  * 3 * 2^-22 * sum_r |q_r k_r| of the exact value (fp32 accumulation itself is
- * within r * 2^-24 of it).  mode 1 computes them on fp32 MFMAs.  Modes 2-4
- * are mode 0 on one kernel only: 2 the per-wave streaming kernel, 3 and 4 a
- * cooperative kernel (key chunks staged once per workgroup in LDS; 8 waves
- * and one workgroup per CU, or 4 waves and two) whenever rank <= 64; mode 0
- * picks the 4-wave cooperative kernel for rank <= 64 when the grid has at
- * least 512 of its 64-row workgroups, and for k <= 16 on grids below 256 of
- * them with >= 192 keys a key-split per-wave kernel (the four waves of a
- * workgroup share 16 query rows, each over a quarter of the keys; mode 5
- * forces it whenever k <= 16).  All pick the same entries.
- * Modes 0 and 2-5 need the select workspace below (the *_workspace_bytes
- * queries report 0 in mode 1).  Process-wide; takes effect for later calls,
- * including their workspace queries.
+ * within r * 2^-24 of it).  mode 1 computes them on fp32 MFMAs.  Modes 2, 4
+ * and 5 are mode 0 on one kernel only: 2 the per-wave streaming kernel, 4 the
+ * cooperative kernel (key chunks staged once per 4-wave workgroup in LDS,
+ * two workgroups per CU) whenever rank <= 64, 5 a key-split per-wave kernel
+ * (the four waves of a workgroup share 16 query rows, each over a quarter of
+ * the keys) whenever k <= 16.  Mode 0 picks the cooperative kernel for
+ * rank <= 64 when the grid has at least 512 of its 64-row workgroups, the
+ * key-split kernel for k <= 16 on grids below 256 of them with >= 192 keys,
+ * else the per-wave kernel.  All pick the same entries.  Mode 3 is retired
+ * (rejected).  The *_workspace_bytes queries report the split workspace in
+ * every mode, so a size query and a later launch agree whatever mode another
+ * thread sets in between.  Process-wide (atomic); each launch reads it once.
  */
 int jn_set_select_mode(int32_t mode);
 
@@ -92,7 +92,7 @@ int jn_lowrank_topk_select(const float* query, int64_t ldq, int64_t query_batch_
                            int64_t rank, int64_t topk, int32_t* out_index, float* out_score, void* workspace,
                            size_t workspace_bytes, jn_stream_t stream);
 
-/* Workspace of jn_lowrank_topk_select (split key rows; 0 in select mode 1). */
+/* Workspace of jn_lowrank_topk_select (split key rows; unused in select mode 1). */
 size_t jn_lowrank_topk_select_workspace_bytes(int64_t batch, int64_t nk, int64_t rank);
 
 /*
@@ -115,7 +115,7 @@ int jn_propagation_topk_forward(const float* layer_val, const float* projected_s
                                 float* delta_val, float* projections, int32_t* topk_index, float* topk_score,
                                 void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
-/* Workspace of jn_propagation_topk_forward (the select's; 0 in select mode 1). */
+/* Workspace of jn_propagation_topk_forward (the select's; unused in select mode 1). */
 size_t jn_propagation_topk_forward_workspace_bytes(int64_t batch, int64_t nodes, int64_t rank);
 
 /* Workspace needed by jn_propagation_topk_backward. */

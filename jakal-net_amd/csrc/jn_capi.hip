@@ -420,9 +420,10 @@ int jn_set_gemm_tile(int32_t tile) {
 }
 
 int jn_set_select_mode(int32_t mode) {
-  JN_REQUIRE(mode >= jakal::kSelectSplitF16 && mode <= jakal::kSelectSplitF16KeySplit, kInvalidArgument,
-             "select mode must be 0 (split fp16), 1 (fp32), 2 (split fp16, per-wave kernel), 3 or 4 (split "
-             "fp16, 8- or 4-wave cooperative kernel) or 5 (split fp16, key-split per-wave kernel), got %d",
+  JN_REQUIRE(mode >= jakal::kSelectSplitF16 && mode <= jakal::kSelectSplitF16KeySplit && mode != 3,
+             kInvalidArgument,
+             "select mode must be 0 (split fp16), 1 (fp32), 2 (split fp16, per-wave kernel), 4 (split fp16, "
+             "cooperative kernel) or 5 (split fp16, key-split per-wave kernel), got %d",
              (int)mode);
   jakal::set_select_mode(mode);
   return kOk;
@@ -892,9 +893,10 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
     if (rc) return rc;
   }
 
-  // 4. core weight and bias grads
-  return launch_finalize_small_grads(s.part_c, cols_backward_parts((int64_t)B * Nd), r,
-                                     grad_core_weight, 0, s.rowsum, batch * src_nodes, grad_bias, s.stage, st);
+  // 4. core weight and bias grads.  Softmax routes do not change when a row's
+  // logits shift together, so their bias gradient is exactly 0 (no rows summed).
+  return launch_finalize_small_grads(s.part_c, cols_backward_parts((int64_t)B * Nd), r, grad_core_weight, 0,
+                                     s.rowsum, compress_kind == 0 ? 0 : batch * src_nodes, grad_bias, s.stage, st);
 }
 
 int jn_propagation_dense_forward(const float* layer_val, const float* projected_state, const float* projected_val,
@@ -1189,8 +1191,9 @@ int jn_transition_dense_backward(const float* sender_strength, const float* src_
                          Mt, (int)dst_dim, r, st);
     if (rc) return rc;
   }
-  // 5. w and bias grads
-  return launch_finalize_small_grads(s.part_c, Ms, r, grad_core_weight, 0, s.rowsum, Ms, grad_bias, s.stage, st);
+  // 5. w and bias grads (exactly 0 for softmax routes: shifting a row's logits leaves it unchanged)
+  return launch_finalize_small_grads(s.part_c, Ms, r, grad_core_weight, 0, s.rowsum, compress_kind == 0 ? 0 : Ms,
+                                     grad_bias, s.stage, st);
 }
 
 }  // extern "C"

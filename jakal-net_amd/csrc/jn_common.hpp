@@ -308,6 +308,16 @@ __device__ __forceinline__ float4 buf_load_w(__amdgpu_buffer_rsrc_t r, uint32_t 
 
 __device__ __forceinline__ float sign_f(float s) { return (s > 0.f) ? 1.f : ((s < 0.f) ? -1.f : 0.f); }
 
+// True when every present edge of the wavefront's row (lanes with `present`)
+// has a score of one strict sign.  The row-normalising compressions (signed
+// |s| softmax, signed entmax-1.5) then do not change when all of the row's
+// scores shift together, so the row's contribution to the bias gradient,
+// sum_e g_s[e], is exactly 0 (its fp32 sum would only be rounding noise).
+__device__ __forceinline__ bool row_one_sign(bool present, float s) {
+  const uint64_t live = __ballot(present);
+  return __ballot(present && s > 0.f) == live || __ballot(present && s < 0.f) == live;
+}
+
 // Edges of a row processed four at a time by the wave's 16-lane groups (group g
 // takes edge 4i + g in iteration i): lane L (< 64) takes the edge held by group
 // L % 4 in iteration L / 4.

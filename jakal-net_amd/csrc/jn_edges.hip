@@ -87,7 +87,8 @@ __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
     if (slab == 0 && j >= 0) st += c * psb[j];
     const int ne = min(kWave, a.k - e0);
     for (int d = d_begin + lane * W; d < d_end; d += kWave * W) {
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      // two accumulation chains (even / odd edges), summed at the end
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f), acc1 = acc;
       int q = 0;
       for (; q + 8 <= ne; q += 8) {
         float4 v[8];
@@ -99,13 +100,17 @@ __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
           v[u] = load_w<W>(pvb + (int64_t)(jj < 0 ? 0 : jj) * a.ld_pv + d);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) fma4(acc, cc[u], v[u]);
+        for (int u = 0; u < 8; u += 2) {
+          fma4(acc, cc[u], v[u]);
+          fma4(acc1, cc[u + 1], v[u + 1]);
+        }
       }
       for (; q < ne; ++q) {
         const int jj = readlane_i(j, q);
         if (jj < 0) continue;
-        fma4(acc, readlane_f(c, q), load_w<W>(pvb + (int64_t)jj * a.ld_pv + d));
+        fma4((q & 1) ? acc1 : acc, readlane_f(c, q), load_w<W>(pvb + (int64_t)jj * a.ld_pv + d));
       }
+      acc = add4(acc, acc1);
       if (e0 > 0) acc = add4(acc, load_w<W>(out + d));
       store_w<W>(out + d, acc);
     }
@@ -303,7 +308,9 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
       a.g_score[row * a.k + e0 + lane] = gsc;
       a.coef[row * a.k + e0 + lane] = cf;
     }
-    gsum += gsc;
+    // kinds 1 and 2 hold the whole row in this pass (k <= 64)
+    const bool shift_free = a.compress != 0 && row_one_sign(j >= 0, s);
+    gsum += shift_free ? 0.f : gsc;
 
     // dQ partials: group g sums its edges (absent edges carry gsc = 0)
 #pragma unroll
@@ -607,7 +614,8 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
     st += cd;  // lanes past the segment hold 0
     if (!out) continue;
     for (int d = d_begin + lane * W; d < d_end; d += kWave * W) {
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      // two accumulation chains (even / odd records), summed at the end
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f), acc1 = acc;
       int q = 0;
       for (; q + 8 <= n; q += 8) {
         float4 v[8];
@@ -618,9 +626,14 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
           v[u] = load_w<W>(a.gdv + (int64_t)readlane_i(row, q + u) * a.D + d);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) fma4(acc, cc[u], v[u]);
+        for (int u = 0; u < 8; u += 2) {
+          fma4(acc, cc[u], v[u]);
+          fma4(acc1, cc[u + 1], v[u + 1]);
+        }
       }
-      for (; q < n; ++q) fma4(acc, readlane_f(cf, q), load_w<W>(a.gdv + (int64_t)readlane_i(row, q) * a.D + d));
+      for (; q < n; ++q)
+        fma4((q & 1) ? acc1 : acc, readlane_f(cf, q), load_w<W>(a.gdv + (int64_t)readlane_i(row, q) * a.D + d));
+      acc = add4(acc, acc1);
       if (blk > 0) acc = add4(acc, load_w<W>(out + d));
       store_w<W>(out + d, acc);
     }

@@ -244,11 +244,19 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
     }
   };
 
-  floatx4 acc[MT][MT];
+  // Four accumulation chains per output tile (one per k step of a slice),
+  // summed in the epilogue: each chain adds a quarter of the K products, so
+  // the fp32 rounding of long reductions (K = node counts in the dense and
+  // weight-gradient products) grows half as fast as with one chain.
+  floatx4 acc[MT][MT], chain[3][MT][MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < MT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < MT; ++j) {
+      acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 3; ++c) chain[c][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
 
   const int nslices = (kend - kbeg + kGBK - 1) / kGBK;
   if (nslices > 0) {
@@ -272,14 +280,21 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
       for (int nt = 0; nt < MT; ++nt) {
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].x, bv[nt].x, acc[mt][nt], 0, 0, 0);
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].y, bv[nt].y, acc[mt][nt], 0, 0, 0);
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].z, bv[nt].z, acc[mt][nt], 0, 0, 0);
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].w, bv[nt].w, acc[mt][nt], 0, 0, 0);
+        chain[0][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].y, bv[nt].y, chain[0][mt][nt], 0, 0, 0);
+        chain[1][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].z, bv[nt].z, chain[1][mt][nt], 0, 0, 0);
+        chain[2][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].w, bv[nt].w, chain[2][mt][nt], 0, 0, 0);
       }
 
     if (s + 1 < nslices) store_slice(cur ^ 1);
     __syncthreads();
   }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < MT; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        acc[mt][nt][v] = (acc[mt][nt][v] + chain[0][mt][nt][v]) + (chain[1][mt][nt][v] + chain[2][mt][nt][v]);
 
   // Epilogue: lane holds rows 4*grp+v of each 16x16 tile, column col.
   if constexpr (USE == kGemmDenseScores || USE == kGemmDenseEdgeGrad) {

@@ -30,20 +30,21 @@ constexpr int kSelectMaxK = 64;
 // Score arithmetic of the select: kSelectSplitF16 (default) runs the score
 // tiles on fp16 MFMAs over two-term fp16 splits of the operands (about 22
 // significant bits per operand, fp32 accumulation); kSelectF32 runs them on
-// fp32 MFMAs.  The split needs select_workspace_bytes() of scratch.
+// fp32 MFMAs.  The split needs select_workspace_bytes() of scratch, which is
+// reported for every mode so that a size query and a later launch agree even
+// when another thread changes the mode in between.
 constexpr int kSelectSplitF16 = 0;
-// Split fp16 on one kernel only (tests): the per-wave streaming kernel, or a
-// cooperative (LDS-staged) kernel whenever the rank is at most 64: 8 waves
-// and one workgroup per CU, or 4 waves and two per CU.  kSelectSplitF16 picks
-// the 4-wave cooperative kernel for rank <= 64 on grids of at least 512
-// workgroups, else the per-wave kernel.
+// Split fp16 on one kernel only (tests): the per-wave streaming kernel, or the
+// 4-wave cooperative (LDS-staged) kernel whenever the rank is at most 64.
+// kSelectSplitF16 picks the cooperative kernel for rank <= 64 on grids of at
+// least 512 workgroups, else the per-wave kernel.  (Mode 3 is retired.)
 constexpr int kSelectSplitF16Wave = 2;
-constexpr int kSelectSplitF16Coop = 3;
 constexpr int kSelectSplitF16Coop4 = 4;
 // Split fp16 on the key-split per-wave kernel whenever k <= 16 (tests); mode 0
 // picks it for k <= 16 on grids below 256 workgroups with >= 192 keys.
 constexpr int kSelectSplitF16KeySplit = 5;
 constexpr int kSelectF32 = 1;
+// The mode is process-wide and atomic; each launch reads it once.
 int select_mode();
 void set_select_mode(int mode);
 size_t select_workspace_bytes(int64_t B, int64_t Nk, int64_t r);

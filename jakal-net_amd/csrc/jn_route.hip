@@ -179,7 +179,8 @@ __global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdAr
   }
   gl = j >= 0 ? gl * a.inv_temperature : 0.f;
   if (lane < a.k) a.g_logit[row * a.k + lane] = gl;
-  const float gsum = wave_sum(gl);
+  // one-sign rows of the signed compressions: exactly 0 (softmax rows are not summed at all)
+  const float gsum = (a.compress != 0 && row_one_sign(j >= 0, s)) ? 0.f : wave_sum(gl);
   if (lane == 0) {
     if (a.grad_ps) a.grad_ps[row] = gps;
     if (a.grad_rho) a.grad_rho[row] = grho;

@@ -53,6 +53,7 @@
 //     until one bitonic sort per row at the end.
 //   * Score arithmetic: fp16 MFMAs over two-term fp16 splits of the operands
 //     (see select_split_keys_kernel), or fp32 MFMAs (select mode 1).
+#include <atomic>
 #include <type_traits>
 
 #include "jn_internal.hpp"
@@ -1056,7 +1057,7 @@ constexpr int64_t kSelKspMaxBlocks = 256;
 constexpr int kSelKspMinKeys = 4 * kSelChunk;
 
 namespace {
-int g_select_mode = kSelectSplitF16;
+std::atomic<int> g_select_mode{kSelectSplitF16};
 
 int split_ranks(int64_t r) { return (int)((r + 31) / 32) * 32; }
 
@@ -1078,11 +1079,12 @@ SelectScratch carve_select(void* base, size_t size, int64_t B, int64_t Nk, int64
 }
 }  // namespace
 
-int select_mode() { return g_select_mode; }
-void set_select_mode(int mode) { g_select_mode = mode; }
+int select_mode() { return g_select_mode.load(std::memory_order_relaxed); }
+void set_select_mode(int mode) { g_select_mode.store(mode, std::memory_order_relaxed); }
 
+// Every mode reports the split workspace (fp32 MFMAs leave it unused).
 size_t select_workspace_bytes(int64_t B, int64_t Nk, int64_t r) {
-  if (g_select_mode == kSelectF32 || B < 1 || Nk < 1 || r < 1) return 0;
+  if (B < 1 || Nk < 1 || r < 1) return 0;
   return carve_select(nullptr, 0, B, Nk, r).bytes;
 }
 
@@ -1100,8 +1102,9 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   const int64_t blocks = (int64_t)tiles * a.B;
   JN_REQUIRE(blocks > 0 && blocks < (1LL << 31), kInvalidArgument, "bad grid size");
   dim3 grid((unsigned)blocks);
+  const int mode = select_mode();
 
-  if (g_select_mode != kSelectF32) {
+  if (mode != kSelectF32) {
     const SelectScratch s = carve_select(a.ws, a.ws_bytes, a.B, a.Nk, a.r);
     JN_REQUIRE(a.ws != nullptr && s.bytes <= a.ws_bytes, kWorkspaceTooSmall,
                "select workspace too small: need %zu bytes, got %zu", s.bytes, a.ws_bytes);
@@ -1122,21 +1125,15 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
     }
     a.split_key = s.split;
     a.split_exp = s.kexp;
-    const int64_t coop_blocks = (int64_t)((a.Nq + 2 * kSelRows - 1) / (2 * kSelRows)) * a.B;
-    const bool coop4 = RP <= 64 && (g_select_mode == kSelectSplitF16Coop4 ||
-                                    (g_select_mode == kSelectSplitF16 && blocks >= kSelCoop4MinBlocks));
-    const bool coop = RP <= 64 && g_select_mode == kSelectSplitF16Coop;
-    const bool ksp = !coop4 && !coop && a.k <= 16 &&
-                     (g_select_mode == kSelectSplitF16KeySplit ||
-                      (g_select_mode == kSelectSplitF16 && blocks < kSelKspMaxBlocks && a.Nk >= kSelKspMinKeys));
+    const bool coop4 = RP <= 64 && (mode == kSelectSplitF16Coop4 ||
+                                    (mode == kSelectSplitF16 && blocks >= kSelCoop4MinBlocks));
+    const bool ksp = !coop4 && a.k <= 16 &&
+                     (mode == kSelectSplitF16KeySplit ||
+                      (mode == kSelectSplitF16 && blocks < kSelKspMaxBlocks && a.Nk >= kSelKspMinKeys));
     JN_PROFILE("lowrank_topk_select_kernel", stream);
     if (coop4) {
       if (RP == 32) launch_split<1, 4>(a, grid, stream);
       else launch_split<2, 4>(a, grid, stream);
-    } else if (coop) {
-      const dim3 cgrid((unsigned)coop_blocks);
-      if (RP == 32) launch_split<1, 8>(a, cgrid, stream);
-      else launch_split<2, 8>(a, cgrid, stream);
     } else if (ksp) {
       const dim3 kgrid((unsigned)((int64_t)((a.Nq + kSelRowsPerWave - 1) / kSelRowsPerWave) * a.B));
       switch (RP / 32) {

@@ -1,26 +1,27 @@
 """Same-layer message passing: dense ``Propagation`` and ``SparsePropagation``.
 
-Operator semantics follow the reference's ``src/jakal_net/propagation.py``:
+Semantics of the reference operators (src/jakal_net/propagation.py):
 
-* scores ``s = pairwise_fn(val, val)`` over all (target i, source j) pairs;
-* dense: ``e = compress(s)``; window: ``e = compress(s)`` on ``i-w <= j <= i``
-  (:459-470); top-k: ``e = compress(s)`` on the k best sources of each target
-  (:471), all other edges zero;
-* ``delta_state = e @ projected_state``, ``delta_val = e @ projected_val``
-  (:473-479), or with ``state_weight_edges`` the edges are multiplied by
-  ``softplus(state_j)`` and ``delta_state = sum_j e`` (:474-478).
+* scores ``s[..., i, j] = pairwise_fn(val, val)`` for target i and source j;
+* dense: every pair is an edge; window: the sources ``i - window <= j <= i``
+  (:459-470); top-k: the k best sources of each target (:471);
+* edge weights ``e = compress(s)`` on the kept pairs, 0 elsewhere;
+* ``delta_state[i] = sum_j e_ij ps_j`` and ``delta_val[i] = sum_j e_ij pv_j``
+  with ``ps = state_proj_fn(state)``, ``pv = val_proj_fn(val)`` (:473-479);
+  with ``state_weight_edges`` every edge is scaled by ``softplus(state_j)``
+  and ``delta_state[i] = sum_j e_ij`` (:474-478).
 
-Backends (``implementation=``):
+``implementation=``:
 
-* ``"reference"`` -- dense masked PyTorch form (reference :207-220, :453-480);
-* ``"streaming"`` -- blockwise PyTorch over target blocks;
-* ``"native"``    -- the HIP library through ``jakal_net_native`` for the hot-path
-  configuration (``LowRankBilinearPairwise`` with softsign or signed_abs_softmax
-  edges).  On a GPU tensor a missing or disabled library is an error, never a
-  silent CPU/PyTorch fallback.  Configurations outside the hot path (custom
-  score callables, other compress functions) run the streaming path, as the
-  reference runs them in its Python kernel backend;
-* ``"kernel"``    -- the native op when it is available for the device, else streaming.
+* ``"reference"`` -- the dense masked PyTorch form (:207-220, :453-480);
+* ``"streaming"`` -- the same math over blocks of target rows;
+* ``"native"`` -- the HIP library (``jakal_net_native``) for the hot-path
+  configuration: ``LowRankBilinearPairwise`` with softsign,
+  signed_abs_softmax or signed_entmax15 edges.  For GPU tensors a missing or
+  disabled library, or a shape outside the library's limits, raises; other
+  configurations (custom score callables or compressions) run the streaming
+  form, as the reference runs them in its PyTorch backends;
+* ``"kernel"`` -- the HIP library when it accepts the call, else streaming.
 """
 
 from __future__ import annotations
@@ -31,21 +32,19 @@ import torch
 from torch import Tensor, nn
 from torch.nn import functional as F
 
+from jakal_net.compress import compress_edges, edge_compress_name, topk_keep_mask, window_keep_mask
 from jakal_net.core import (
     ImplementationMode,
     Layer,
     LayerDelta,
     SparsePropagationType,
-    apply_optional_layer_fn,
-    iter_blocks,
-    resolve_accumulator_dtype,
-    validate_implementation,
-    validate_pairwise_block_scores,
-    validate_pairwise_scores,
-    validate_projected_state,
-    validate_projected_val,
+    accumulation_dtype,
+    block_ranges,
+    check_implementation,
+    expect_shape,
+    finish_layer,
 )
-from jakal_net.kernel_common import build_topk_mask, causal_window_mask, signed_entmax15, supports_pairwise_kernel
+from jakal_net.kernel_common import supports_pairwise_kernel
 from jakal_net.native_backend import (
     native_disabled_by_env,
     native_supports,
@@ -56,50 +55,13 @@ from jakal_net.native_backend import (
     require_native_for_device,
 )
 
-
-def _cuda_graph_capture_active(device_type: str) -> bool:
-    if device_type != "cuda":
-        return False
-    try:
-        return bool(torch.cuda.is_current_stream_capturing())
-    except Exception:  # noqa: BLE001
-        return False
+NATIVE_EDGE_COMPRESSIONS = ("softsign", "signed_abs_softmax", "signed_entmax15")
 
 
-def edge_compress_name(edge_compress_fn: Callable[[Tensor], Tensor]) -> str | None:
-    """Canonical name of a compress function (reference propagation.py:56-64)."""
-    name = getattr(edge_compress_fn, "__name__", "")
-    if edge_compress_fn is F.softsign or name == "softsign":
-        return "softsign"
-    if name in {"signed_abs_softmax", "signed_abs_softmax_edges", "_signed_abs_softmax_edges"}:
-        return "signed_abs_softmax"
-    if name in {"signed_entmax15", "_signed_entmax15_edges"}:
-        return "signed_entmax15"
-    return None
-
-
-_NATIVE_EDGE_COMPRESS = ("softsign", "signed_abs_softmax", "signed_entmax15")
-
-
-def compress_edges(scores: Tensor, edge_compress_fn: Callable[[Tensor], Tensor], *, mask: Tensor | None = None) -> Tensor:
-    """Apply the edge compression; masked edges are exactly zero.
-
-    ``signed_abs_softmax`` normalises over the unmasked entries only
-    (reference propagation.py:67-88)."""
-    if edge_compress_name(edge_compress_fn) == "signed_abs_softmax":
-        clean = torch.nan_to_num(scores)
-        signs = torch.sign(clean)
-        magnitudes = clean.abs()
-        if mask is not None:
-            signs = signs * mask.to(dtype=signs.dtype)
-            magnitudes = magnitudes.masked_fill(~mask, -torch.inf)
-        return torch.nan_to_num(signs * torch.softmax(magnitudes, dim=-1))
-    if edge_compress_name(edge_compress_fn) == "signed_entmax15":
-        return signed_entmax15(scores, mask=mask)
-    edges = edge_compress_fn(scores)
-    if mask is not None:
-        edges = edges * mask.to(dtype=edges.dtype)
-    return edges
+def capturing_graph(t: Tensor) -> bool:
+    """True while ``t``'s device stream is being captured into a graph (the
+    reference sends such calls to its PyTorch form, propagation.py:775-776)."""
+    return t.is_cuda and torch.cuda.is_current_stream_capturing()
 
 
 class Propagation(nn.Module):
@@ -123,11 +85,11 @@ class Propagation(nn.Module):
         use_direction_only: bool = False,
     ) -> None:
         super().__init__()
-        validate_implementation(implementation)
+        check_implementation(implementation)
         self.pairwise_fn = pairwise_fn
         self.edge_compress_fn = edge_compress_fn
-        self.val_proj_fn = nn.Identity() if val_proj_fn is None else val_proj_fn
-        self.state_proj_fn = nn.Identity() if state_proj_fn is None else state_proj_fn
+        self.val_proj_fn = val_proj_fn if val_proj_fn is not None else nn.Identity()
+        self.state_proj_fn = state_proj_fn if state_proj_fn is not None else nn.Identity()
         self.norm_fn = norm_fn
         self.residual = residual
         self.return_delta = return_delta
@@ -136,125 +98,119 @@ class Propagation(nn.Module):
         self.target_block_size = target_block_size
         self.source_block_size = source_block_size
         self.accumulator_dtype = accumulator_dtype
+        # kept for the constructor contract; same-layer scores use the values as they are
         self.use_direction_only = use_direction_only
 
-    # ---- shared pieces -------------------------------------------------------
+    # ---- scores, edges and what each source carries --------------------------
     def compute_scores(self, layer: Layer) -> Tensor:
         scores = self.pairwise_fn(layer.val, layer.val)
-        validate_pairwise_scores(scores, layer)
+        expect_shape(scores, (*layer.batch_shape, layer.num_nodes, layer.num_nodes), "pairwise_fn")
         return scores
 
     def compute_edges(self, layer: Layer) -> Tensor:
         return self.edge_compress_fn(self.compute_scores(layer))
 
-    def _edge_source_strength(self, source_state: Tensor) -> Tensor:
-        return F.softplus(source_state)
-
-    def _project_inputs(self, layer: Layer) -> tuple[Tensor, Tensor]:
-        projected_state = self.state_proj_fn(layer.state)
-        projected_val = self.val_proj_fn(layer.val)
-        validate_projected_state(projected_state, layer)
-        validate_projected_val(projected_val, layer)
-        return projected_state, projected_val
-
-    def _aggregation_inputs(self, layer: Layer) -> tuple[Tensor, Tensor]:
-        """(per-source state weight, per-source value) so that delta = e @ each.
-
-        With ``state_weight_edges`` the source strength softplus(state_j) is
-        folded into both (reference propagation.py:165-174)."""
-        projected_state, projected_val = self._project_inputs(layer)
+    def _source_terms(self, layer: Layer) -> tuple[Tensor, Tensor]:
+        """(w, v) per source node such that delta_state = e @ w and delta_val = e @ v."""
+        state = self.state_proj_fn(layer.state)
+        val = self.val_proj_fn(layer.val)
+        expect_shape(state, layer.state.shape, "state_proj_fn")
+        expect_shape(val, layer.val.shape, "val_proj_fn")
         if not self.state_weight_edges:
-            return projected_state, projected_val
-        strength = self._edge_source_strength(layer.state)
-        return strength, projected_val * strength.unsqueeze(-1)
+            return state, val
+        strength = F.softplus(layer.state)  # edge scale softplus(state_j), reference propagation.py:157-174
+        return strength, val * strength.unsqueeze(-1)
 
-    def _edge_mask(self, scores: Tensor, layer: Layer, target_start: int, target_end: int) -> Tensor | None:
+    # the kept pairs of target rows t0..t1 and source columns s0..s1 (None: all)
+    def _keep(self, scores: Tensor, layer: Layer, t0: int, t1: int, s0: int, s1: int) -> Tensor | None:
         return None
 
-    def _compute_delta_reference(self, layer: Layer) -> LayerDelta:
-        scores = self.compute_scores(layer)
-        mask = self._edge_mask(scores, layer, 0, layer.num_nodes)
-        edges = compress_edges(scores, self.edge_compress_fn, mask=mask)
-        weights, values = self._aggregation_inputs(layer)
-        delta_state = torch.einsum("...ij,...j->...i", edges, weights)
-        delta_val = torch.einsum("...ij,...jd->...id", edges, values)
-        return LayerDelta(delta_state=delta_state, delta_val=delta_val)
-
-    def _source_range(self, layer: Layer, target_start: int, target_end: int) -> tuple[int, int]:
+    # the source columns target rows t0..t1 can reach
+    def _source_span(self, layer: Layer, t0: int, t1: int) -> tuple[int, int]:
         return 0, layer.num_nodes
 
+    # ---- PyTorch forms -------------------------------------------------------
+    def _delta_from_scores(self, scores: Tensor, keep: Tensor | None, w: Tensor, v: Tensor,
+                           acc: tuple[torch.dtype, torch.dtype] | None = None) -> tuple[Tensor, Tensor]:
+        edges = compress_edges(scores, self.edge_compress_fn, mask=keep)
+        if acc is None:
+            return (edges * w.unsqueeze(-2)).sum(-1), edges @ v
+        ds, dv = acc
+        return (edges.to(ds) * w.unsqueeze(-2).to(ds)).sum(-1), edges.to(dv) @ v.to(dv)
+
+    def _compute_delta_reference(self, layer: Layer) -> LayerDelta:
+        n = layer.num_nodes
+        scores = self.compute_scores(layer)
+        w, v = self._source_terms(layer)
+        ds, dv = self._delta_from_scores(scores, self._keep(scores, layer, 0, n, 0, n), w, v)
+        return LayerDelta(delta_state=ds, delta_val=dv)
+
     def _compute_delta_streaming(self, layer: Layer) -> LayerDelta:
-        weights, values = self._aggregation_inputs(layer)
-        state_dtype = resolve_accumulator_dtype(weights.dtype, self.accumulator_dtype)
-        val_dtype = resolve_accumulator_dtype(values.dtype, self.accumulator_dtype)
-        state_parts: list[Tensor] = []
-        val_parts: list[Tensor] = []
-        for t0, t1 in iter_blocks(layer.num_nodes, self.target_block_size, name="target_block_size"):
-            s0, s1 = self._source_range(layer, t0, t1)
+        w, v = self._source_terms(layer)
+        acc = (accumulation_dtype(w.dtype, self.accumulator_dtype), accumulation_dtype(v.dtype, self.accumulator_dtype))
+        parts_s, parts_v = [], []
+        for t0, t1 in block_ranges(layer.num_nodes, self.target_block_size):
+            s0, s1 = self._source_span(layer, t0, t1)
             scores = self.pairwise_fn(layer.val[..., t0:t1, :], layer.val[..., s0:s1, :])
-            validate_pairwise_block_scores(
-                scores, batch_shape=layer.batch_shape, target_nodes=t1 - t0, source_nodes=s1 - s0
-            )
-            mask = self._block_mask(scores, layer, t0, t1, s0, s1)
-            edges = compress_edges(scores, self.edge_compress_fn, mask=mask)
-            state_parts.append(
-                torch.einsum("...ij,...j->...i", edges.to(state_dtype), weights[..., s0:s1].to(state_dtype))
-            )
-            val_parts.append(
-                torch.einsum("...ij,...jd->...id", edges.to(val_dtype), values[..., s0:s1, :].to(val_dtype))
-            )
-        return LayerDelta(
-            delta_state=torch.cat(state_parts, dim=-1).to(weights.dtype),
-            delta_val=torch.cat(val_parts, dim=-2).to(values.dtype),
-        )
+            expect_shape(scores, (*layer.batch_shape, t1 - t0, s1 - s0), "pairwise_fn")
+            ds, dv = self._delta_from_scores(scores, self._keep(scores, layer, t0, t1, s0, s1), w[..., s0:s1],
+                                             v[..., s0:s1, :], acc)
+            parts_s.append(ds)
+            parts_v.append(dv)
+        return LayerDelta(delta_state=torch.cat(parts_s, dim=-1).to(w.dtype),
+                          delta_val=torch.cat(parts_v, dim=-2).to(v.dtype))
 
-    def _block_mask(self, scores: Tensor, layer: Layer, t0: int, t1: int, s0: int, s1: int) -> Tensor | None:
-        return None
-
-    # ---- native dispatch -----------------------------------------------------
+    # ---- the HIP library -----------------------------------------------------
     def _native_op_name(self) -> str:
         return "propagation_dense"
 
-    def _hot_path_config(self) -> str | None:
-        """Compress name when this operator is on the native hot path, else None."""
+    def _native_compression(self) -> str | None:
+        """The compression's name when this operator is on the native hot path, else None."""
         name = edge_compress_name(self.edge_compress_fn)
-        if name in _NATIVE_EDGE_COMPRESS and supports_pairwise_kernel(self.pairwise_fn):
+        if name in NATIVE_EDGE_COMPRESSIONS and supports_pairwise_kernel(self.pairwise_fn):
             return name
         return None
 
-    def _try_native(self, layer: Layer, *, strict: bool) -> LayerDelta | None:
-        compress = self._hot_path_config()
+    def _compute_delta_native(self, layer: Layer, *, strict: bool) -> LayerDelta | None:
+        """The library's result, or None when this call is not the library's to run.
+
+        strict (implementation="native"): a GPU tensor the library cannot take
+        raises instead of returning None."""
+        compress = self._native_compression()
         if compress is None or native_disabled_by_env():
             return None
-        device_type = layer.val.device.type
-        op = self._native_op_name()
-        if native_supports(op) and native_supports_device(device_type):
-            weights, values = self._aggregation_inputs(layer)
-            return self._call_native(compress, layer, weights, values)
-        if strict:
-            require_native_for_device(op, device_type)
-        return None
+        op, device_type = self._native_op_name(), layer.val.device.type
+        if not (native_supports(op) and native_supports_device(device_type)):
+            if strict:
+                require_native_for_device(op, device_type)
+            return None
+        w, v = self._source_terms(layer)
+        try:
+            return self._call_native(compress, layer, w, v)
+        except NotImplementedError:  # outside the library's limits (k, rank, widths)
+            if strict:
+                raise
+            return None
 
-    def _call_native(self, compress: str, layer: Layer, weights: Tensor, values: Tensor) -> LayerDelta:
+    def _call_native(self, compress: str, layer: Layer, w: Tensor, v: Tensor) -> LayerDelta:
         return propagation_dense_native(
             pairwise_fn=self.pairwise_fn,
             edge_compress_name=compress,
             layer_val=layer.val,
-            projected_state=weights,
-            projected_val=values,
+            projected_state=w,
+            projected_val=v,
             source_state=None,
             target_block_size=self.target_block_size or layer.num_nodes,
             source_block_size=self.source_block_size or layer.num_nodes,
         )
 
+    # ---- dispatch ------------------------------------------------------------
     def compute_delta(self, layer: Layer) -> LayerDelta:
         impl = self.implementation
-        if impl == "native" and _cuda_graph_capture_active(layer.val.device.type):
-            return self._compute_delta_reference(layer)
-        if impl == "reference":
+        if impl == "reference" or (impl == "native" and capturing_graph(layer.val)):
             return self._compute_delta_reference(layer)
         if impl in ("native", "kernel"):
-            delta = self._try_native(layer, strict=(impl == "native"))
+            delta = self._compute_delta_native(layer, strict=impl == "native")
             if delta is not None:
                 return delta
         return self._compute_delta_streaming(layer)
@@ -263,8 +219,7 @@ class Propagation(nn.Module):
         delta = self.compute_delta(layer)
         if self.return_delta:
             return delta
-        updated = layer.apply_delta(delta, merge_mode="add" if self.residual else "replace")
-        return apply_optional_layer_fn(updated, self.norm_fn)
+        return finish_layer(layer.apply_delta(delta, "add" if self.residual else "replace"), self.norm_fn)
 
 
 class SparsePropagation(Propagation):
@@ -291,7 +246,7 @@ class SparsePropagation(Propagation):
         use_direction_only: bool = False,
     ) -> None:
         super().__init__(
-            pairwise_fn=pairwise_fn,
+            pairwise_fn,
             edge_compress_fn=edge_compress_fn,
             val_proj_fn=val_proj_fn,
             state_proj_fn=state_proj_fn,
@@ -305,60 +260,39 @@ class SparsePropagation(Propagation):
             accumulator_dtype=accumulator_dtype,
             use_direction_only=use_direction_only,
         )
-        if sparse_type not in ("window", "topk"):
-            raise ValueError(f"Unsupported sparse_type: {sparse_type!r}.")
-        if sparse_type == "window" and window is None:
-            raise ValueError("window sparse propagation requires window.")
-        if sparse_type == "topk" and topk is None:
-            raise ValueError("topk sparse propagation requires topk.")
+        needed = {"topk": topk, "window": window}
+        if sparse_type not in needed:
+            raise ValueError(f"sparse_type must be 'window' or 'topk', got {sparse_type!r}.")
+        if needed[sparse_type] is None:
+            raise ValueError(f"sparse_type={sparse_type!r} needs the {sparse_type} argument.")
         self.sparse_type = sparse_type
         self.topk = topk
         self.window = window
 
-    def _edge_mask(self, scores: Tensor, layer: Layer, target_start: int, target_end: int) -> Tensor | None:
+    def _keep(self, scores: Tensor, layer: Layer, t0: int, t1: int, s0: int, s1: int) -> Tensor | None:
         if self.sparse_type == "window":
-            mask = causal_window_mask(0, layer.num_nodes, 0, layer.num_nodes, self.window or 0, device=scores.device)
-            return mask.view((1,) * (scores.ndim - 2) + tuple(mask.shape))
-        return build_topk_mask(scores, self.topk or layer.num_nodes)
+            return window_keep_mask(t0, t1, s0, s1, self.window or 0, device=scores.device)
+        # every block of target rows sees all sources, so the row-wise top-k is exact
+        return topk_keep_mask(scores, self.topk or layer.num_nodes)
 
-    def _source_range(self, layer: Layer, target_start: int, target_end: int) -> tuple[int, int]:
+    def _source_span(self, layer: Layer, t0: int, t1: int) -> tuple[int, int]:
         if self.sparse_type == "window":
-            return max(0, target_start - (self.window or 0)), target_end
+            return max(0, t0 - (self.window or 0)), t1
         return 0, layer.num_nodes
 
-    def _block_mask(self, scores: Tensor, layer: Layer, t0: int, t1: int, s0: int, s1: int) -> Tensor | None:
-        if self.sparse_type == "window":
-            mask = causal_window_mask(t0, t1, s0, s1, self.window or 0, device=scores.device)
-            return mask.view((1,) * (scores.ndim - 2) + tuple(mask.shape))
-        # each target block sees every source, so a row-wise top-k mask is exact
-        return build_topk_mask(scores, self.topk or layer.num_nodes)
-
     def _native_op_name(self) -> str:
-        if self.sparse_type == "window":
-            return "propagation_window"
-        return "propagation_topk"
+        return "propagation_window" if self.sparse_type == "window" else "propagation_topk"
 
-    def _call_native(self, compress: str, layer: Layer, weights: Tensor, values: Tensor) -> LayerDelta:
-        tbs = self.target_block_size or layer.num_nodes
-        sbs = self.source_block_size or layer.num_nodes
-        if self.sparse_type == "window":
-            return propagation_window_native(
-                pairwise_fn=self.pairwise_fn,
-                edge_compress_name=compress,
-                layer_val=layer.val,
-                projected_state=weights,
-                projected_val=values,
-                window=self.window or 0,
-                target_block_size=tbs,
-                source_block_size=sbs,
-            )
-        return propagation_topk_native(
+    def _call_native(self, compress: str, layer: Layer, w: Tensor, v: Tensor) -> LayerDelta:
+        common = dict(
             pairwise_fn=self.pairwise_fn,
             edge_compress_name=compress,
             layer_val=layer.val,
-            projected_state=weights,
-            projected_val=values,
-            topk=self.topk or layer.num_nodes,
-            target_block_size=tbs,
-            source_block_size=sbs,
+            projected_state=w,
+            projected_val=v,
+            target_block_size=self.target_block_size or layer.num_nodes,
+            source_block_size=self.source_block_size or layer.num_nodes,
         )
+        if self.sparse_type == "window":
+            return propagation_window_native(window=self.window or 0, **common)
+        return propagation_topk_native(topk=self.topk or layer.num_nodes, **common)

@@ -114,7 +114,13 @@ _declare(
 ABI_VERSION = int(_LIB.jn_abi_version())
 
 _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
-MAX_TOPK = 64
+# Limits of the library's kernels.  A call beyond one raises NotImplementedError
+# (a RuntimeError subclass) before anything is launched, so callers that have
+# another path for such shapes (implementation="kernel") can take it.
+MAX_TOPK = 64          # edges kept per row by the top-k select
+MAX_RANK = 128         # low-rank score rank
+MAX_SELECT_KEYS = 65535  # keys a top-k select ranks per batch element
+MAX_ROW_COMPRESS_EDGES = 64  # edges per row of the row-normalising compressions on edge lists
 CAUSAL_DENSE_MIN_NODES = 128  # full causal windows from this many nodes run on the dense MFMA path
 
 _SUPPORTED_OPS = (
@@ -159,16 +165,19 @@ def set_gemm_tile(tile: int = 0) -> None:
 SELECT_SPLIT_F16 = 0
 SELECT_F32 = 1
 SELECT_SPLIT_F16_WAVE = 2
-SELECT_SPLIT_F16_COOP = 3
 SELECT_SPLIT_F16_COOP4 = 4
 SELECT_SPLIT_F16_KEYSPLIT = 5
 
 
 def set_select_mode(mode: int = SELECT_SPLIT_F16) -> None:
-    """Score arithmetic of the top-k select for later calls: SELECT_SPLIT_F16 (default, fp16 MFMAs over
-    two-term fp16 operand splits, fp32 accumulation) or SELECT_F32 (fp32 MFMAs); SELECT_SPLIT_F16_WAVE and
-    SELECT_SPLIT_F16_COOP / SELECT_SPLIT_F16_COOP4 run the split arithmetic on the per-wave or an 8- or 4-wave
-    cooperative (LDS-staged) kernel only."""
+    """Score arithmetic of the top-k select for later calls (process-wide).
+
+    SELECT_SPLIT_F16 (default): fp16 MFMAs over two-term fp16 operand splits,
+    fp32 accumulation, the kernel chosen per call; SELECT_F32: fp32 MFMAs.
+    The split arithmetic on one kernel only: SELECT_SPLIT_F16_WAVE (per-wave
+    streaming), SELECT_SPLIT_F16_COOP4 (LDS-staged cooperative, rank <= 64)
+    and SELECT_SPLIT_F16_KEYSPLIT (the four waves of a workgroup split the keys
+    of 16 query rows, k <= 16).  Every mode selects the same entries."""
     _check(_LIB.jn_set_select_mode(int(mode)))
 
 
@@ -438,7 +447,27 @@ def _lowrank_pairwise_args(kind, weight, bias, in_weight, in_bias, out_weight, o
         raise RuntimeError("Low-rank bilinear pairwise kernel is missing projection weights.")
     if in_bias is not None or out_bias is not None:
         raise TypeError("low_rank_bilinear projections carry no bias.")
+    _check_rank(out_weight.shape[0])
     return weight, bias, in_weight, out_weight
+
+
+def _check_rank(rank: int) -> None:
+    if rank > MAX_RANK:
+        raise NotImplementedError(f"the HIP library scores ranks up to {MAX_RANK} (got {rank}).")
+
+
+def _check_select(k: int, keys: int) -> None:
+    """A top-k select of k of `keys` candidates per row."""
+    if k > MAX_TOPK:
+        raise NotImplementedError(f"the HIP top-k select keeps up to {MAX_TOPK} edges per row (got {k}).")
+    if keys > MAX_SELECT_KEYS:
+        raise NotImplementedError(f"the HIP top-k select ranks up to {MAX_SELECT_KEYS} keys per row (got {keys}).")
+
+
+def _check_row_compress(compress: str, edges: int) -> None:
+    if compress != "softsign" and edges > MAX_ROW_COMPRESS_EDGES:
+        raise NotImplementedError(f"HIP {compress} edge lists hold up to {MAX_ROW_COMPRESS_EDGES} edges per row "
+                                  f"(got {edges}).")
 
 
 def _propagation_edges(mode, pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
@@ -494,9 +523,10 @@ def propagation_topk_selection(
     N = layer_val.shape[-2]
     k = min(int(topk), N)
     if k == N:
-        raise NotImplementedError("top-k with k == N is dense propagation; dense native op not available.")
-    if k > MAX_TOPK:
-        raise NotImplementedError(f"HIP top-k propagation supports k <= {MAX_TOPK} (got {k}).")
+        raise NotImplementedError("top-k with k == N keeps every source: that is dense propagation "
+                                  "(propagation_dense, or propagation_topk, which routes it there).")
+    _check_select(k, N)
+    _check_row_compress(edge_compress_name, k)
     return _propagation_edges("topk", pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
                               edge_compress_name, layer_val, projected_state, projected_val, k, target_block_size,
                               source_block_size)
@@ -524,8 +554,7 @@ def propagation_window_edges(
     (index -1 where that is negative) and its score."""
     if window < 0:
         raise RuntimeError("window must be non-negative.")
-    if edge_compress_name == "signed_abs_softmax" and min(int(window) + 1, layer_val.shape[-2]) > 64:
-        raise NotImplementedError("HIP window propagation with signed_abs_softmax supports window <= 63.")
+    _check_row_compress(edge_compress_name, min(int(window) + 1, layer_val.shape[-2]))
     return _propagation_edges("window", pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
                               edge_compress_name, layer_val, projected_state, projected_val, int(window),
                               target_block_size, source_block_size)
@@ -552,9 +581,12 @@ def propagation_window(
     A window covering every earlier source (window >= N - 1, the causal dense
     query propagation of progressive_b_example.py:1990-2003) on at least
     CAUSAL_DENSE_MIN_NODES nodes runs as causal dense propagation on MFMA
-    GEMMs instead of an N-wide edge list."""
+    GEMMs instead of an N-wide edge list, and so does one whose rows are too
+    wide for a row-normalising compression on an edge list."""
     N = layer_val.shape[-2]
-    if window >= N - 1 and N >= CAUSAL_DENSE_MIN_NODES:
+    full_causal = window >= N - 1
+    if full_causal and (N >= CAUSAL_DENSE_MIN_NODES or (edge_compress_name != "softsign"
+                                                        and N > MAX_ROW_COMPRESS_EDGES)):
         if window < 0:
             raise RuntimeError("window must be non-negative.")
         return propagation_dense(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
@@ -720,10 +752,12 @@ def transition_pairwise_topk_routes(
     Nd, Ddst = dst_val.shape[-2], dst_val.shape[-1]
     Dv = projected_val.shape[-1]
     k = min(int(topk), Nd)
-    if k < Nd and k > MAX_ROUTE_TOPK:
-        raise NotImplementedError(f"HIP sparse transition supports topk <= {MAX_ROUTE_TOPK} (got {k}).")
-    if k == Nd and Nd > 64:
-        raise NotImplementedError("HIP sparse transition over every destination supports up to 64 destinations.")
+    _check_rank(source_weight.shape[0])
+    if k < Nd:
+        _check_select(k, Nd)
+    elif Nd > MAX_ROUTE_TOPK:
+        raise NotImplementedError("HIP sparse transition over every destination supports up to 64 destinations "
+                                  "(transition_pairwise_topk runs more as the dense transition).")
     ds, dv, idx, logit = _TransitionTopK.apply(
         _f32(sender_strength.reshape(-1, Ns)), _f32(src_val.reshape(-1, Ns, Dsrc)),
         _f32(dst_val.reshape(-1, Nd, Ddst)), _f32(projected_state.reshape(-1, Ns)),
@@ -890,6 +924,7 @@ def transition_pairwise_dense(
     ignored: the HIP kernels tile for gfx950 themselves."""
     _check_route_spec(route_kind, source_weight, source_bias, target_weight, target_bias, hidden_weight, out_weight,
                       route_compress_name, temperature)
+    _check_rank(source_weight.shape[0])
     if src_block_size < 0 or dst_block_size < 0:
         raise RuntimeError("block sizes must be non-negative.")
     _require_gpu(sender_strength, src_val, dst_val, projected_state, projected_val, source_weight, target_weight,

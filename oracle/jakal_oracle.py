@@ -259,7 +259,7 @@ def propagation_backward(val, ps, pv, U, V, w, b, g_ds, g_dv, *, mode="topk", to
     g_V = flat(g_psrc).T @ flat(val)
     g_w = normalized_weight_backward(w, g_what)
     return {"val": g_val, "ps": g_ps, "pv": g_pv, "U": g_U, "V": g_V, "w": g_w, "w_hat": g_what, "b": g_b,
-            "g_scores": g_s}
+            "g_scores": g_s, "delta_state": fwd["delta_state"], "delta_val": fwd["delta_val"]}
 
 
 def normalized_weight_backward(w, g_what):
@@ -359,6 +359,8 @@ def transition_backward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, g_ds, g_
         "w": g_w,
         "b": g_b,
         "g_logits": g_raw,
+        "delta_state": fwd["delta_state"],
+        "delta_val": fwd["delta_val"],
     }
 
 

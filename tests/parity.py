@@ -1,0 +1,234 @@
+"""Shared checks of the GPU parity tests (imported by tests/test_gpu_*.py).
+
+``check`` compares a HIP result with the float64 oracle.  It passes when the
+hot path's literal fp32 tolerance holds elementwise (rtol 1e-4 / atol 1e-5).
+Long fp32 sums whose terms cancel (destination sums, gradients over every
+edge, D- and N-long dot products) can miss that literal bound in any fp32
+implementation; for those the check is calibrated instead: the HIP error,
+max |hip - f64| over the tensor, must be at most twice the error of a plain
+fp32 PyTorch evaluation of the same op on the same inputs and the same
+selection (``torch32_propagation`` / ``torch32_transition``), measured the
+same way.  Every check prints both errors and the largest excess under the
+literal tolerance, so the logs show how far each tensor is from it.
+
+The fp32 evaluations are the dense masked formulation of the reference
+backend (src/jakal_net/propagation.py:453-480, transition.py:431-452) in
+torch fp32 on the GPU, differentiated by autograd, one chunk of batch
+elements at a time.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+from torch.nn import functional as F
+
+RTOL, ATOL = 1e-4, 1e-5
+FACTOR = 2.0
+
+
+def np64(t) -> np.ndarray:
+    if isinstance(t, torch.Tensor):
+        return t.detach().double().cpu().numpy()
+    return np.asarray(t, dtype=np.float64)
+
+
+def check(what, got, want, ref32=None, rtol=RTOL, atol=ATOL, factor=FACTOR) -> None:
+    """Literal rtol/atol elementwise, else HIP error <= factor x the fp32 torch error."""
+    got, want = np64(got), np64(want)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"
+    if want.size == 0:
+        return
+    err = np.abs(got - want)
+    excess = float((err - (atol + rtol * np.abs(want))).max())
+    line = f"{what}: max|hip-f64| {err.max():.3e}"
+    e32 = None
+    if ref32 is not None:
+        e32 = float(np.abs(np64(ref32) - want).max())
+        line += f", max|torch32-f64| {e32:.3e}"
+    line += f", excess under rtol {rtol:g}/atol {atol:g}: {excess:.3e} (max|f64| {np.abs(want).max():.3e})"
+    print(line, flush=True)
+    if excess <= 0:
+        return
+    assert e32 is not None, line + " -- literal tolerance missed and no fp32 reference given"
+    assert err.max() <= factor * e32, line + f" -- HIP error above {factor:g}x the fp32 reference error"
+
+
+def _bool_mask(mask, dev, b0, b1):
+    m = torch.from_numpy(np.ascontiguousarray(mask[b0:b1])).to(dev)
+    return m
+
+
+def _compress32(s, m, kind):
+    """Edge compression on the masked entries (propagation.py:67-88); masked entries 0."""
+    if kind == "softsign":
+        return torch.where(m, F.softsign(s), torch.zeros_like(s))
+    if kind == "signed_abs_softmax":
+        p = torch.softmax(s.abs().masked_fill(~m, -torch.inf), dim=-1)
+        return torch.where(m, torch.sign(s) * p, torch.zeros_like(s))
+    if kind == "signed_entmax15":
+        from jakal_net.compress import signed_entmax15
+
+        return signed_entmax15(s, mask=m)
+    raise ValueError(kind)
+
+
+def _route32(l, m, kind):
+    """Route weights over each source row's masked destinations (transition.py:187-194, 439-446)."""
+    if kind == "softmax":
+        if m is None:
+            return torch.softmax(l, dim=-1)
+        p = torch.softmax(l.masked_fill(~m, torch.finfo(l.dtype).min), dim=-1)
+        return torch.where(m, p, torch.zeros_like(p))
+    if m is None:
+        m = torch.ones_like(l, dtype=torch.bool)
+    return _compress32(l, m, kind)
+
+
+def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, chunk=4) -> dict:
+    """fp32 torch forward + autograd backward of low-rank propagation on a given mask.
+
+    val [B,N,D], ps [B,N], pv [B,N,Dv] or None (pv is val itself), U/V [r,D],
+    w_hat [r] (the normalised core weight), b float or None, mask [B,N,N]
+    bool (numpy), gds [B,N] / gdv [B,N,Dv] the upstream gradients.  Returns
+    the oracle's keys: delta_state, delta_val, val (whole gradient of val),
+    ps, pv, U, V, w_hat, b."""
+    f32 = dict(device=dev, dtype=torch.float32)
+    Ud = torch.as_tensor(U).to(**f32).requires_grad_(True)
+    Vd = torch.as_tensor(V).to(**f32).requires_grad_(True)
+    wd = torch.as_tensor(w_hat).to(**f32).requires_grad_(True)
+    bd = None if b is None else torch.tensor(float(b), **f32).requires_grad_(True)
+    params = [Ud, Vd, wd] + ([bd] if bd is not None else [])
+    out = {k: [] for k in ("delta_state", "delta_val", "val", "ps", "pv")}
+    acc = [torch.zeros_like(p) for p in params]
+    B = val.shape[0]
+    for b0 in range(0, B, chunk):
+        b1 = min(B, b0 + chunk)
+        x = torch.as_tensor(val[b0:b1]).to(**f32).requires_grad_(True)
+        p_s = torch.as_tensor(ps[b0:b1]).to(**f32).requires_grad_(True)
+        p_v = x if pv is None else torch.as_tensor(pv[b0:b1]).to(**f32).requires_grad_(True)
+        m = _bool_mask(mask, dev, b0, b1)
+        key = ((x @ Vd.T) * wd).transpose(-1, -2).contiguous()
+        s = (x @ Ud.T) @ key
+        if bd is not None:
+            s = s + bd
+        e = _compress32(s, m, kind)
+        ds = (e * p_s[:, None, :]).sum(-1)
+        dv = e @ p_v
+        loss = (ds * torch.as_tensor(gds[b0:b1]).to(**f32)).sum() + (dv * torch.as_tensor(gdv[b0:b1]).to(**f32)).sum()
+        leaves = [x, p_s] + ([p_v] if pv is not None else []) + params
+        grads = torch.autograd.grad(loss, leaves)
+        out["delta_state"].append(ds.detach().cpu())
+        out["delta_val"].append(dv.detach().cpu())
+        out["val"].append(grads[0].cpu())
+        out["ps"].append(grads[1].cpu())
+        if pv is not None:
+            out["pv"].append(grads[2].cpu())
+        for a, g in zip(acc, grads[-len(params):]):
+            a += g
+    res = {k: torch.cat(v).double().numpy() for k, v in out.items() if v}
+    names = ["U", "V", "w_hat"] + (["b"] if bd is not None else [])
+    for n, a in zip(names, acc):
+        res[n] = a.double().cpu().numpy()
+    return res
+
+
+def torch32_transition(dev, src, dst, rho, ps, pv, Ws, Wt, w, b, temperature, mask, kind, gds, gdv,
+                       chunk=4) -> dict:
+    """fp32 torch forward + autograd backward of low-rank routing on a given mask.
+
+    src [B,Ns,Ds], dst [B,Nd,Dd], rho [B,Ns] (sender strength, a leaf), ps
+    [B,Ns], pv [B,Ns,Dv], Ws [r,Ds], Wt [r,Dd], w [r] (raw), b float or None,
+    mask [B,Ns,Nd] bool (numpy) or None (every destination).  Returns the
+    oracle's keys: delta_state, delta_val, sender, src_val, dst_val, ps, pv,
+    Ws, Wt, w, b."""
+    f32 = dict(device=dev, dtype=torch.float32)
+    Wsd = torch.as_tensor(Ws).to(**f32).requires_grad_(True)
+    Wtd = torch.as_tensor(Wt).to(**f32).requires_grad_(True)
+    wd = torch.as_tensor(w).to(**f32).requires_grad_(True)
+    bd = None if b is None else torch.tensor(float(b), **f32).requires_grad_(True)
+    params = [Wsd, Wtd, wd] + ([bd] if bd is not None else [])
+    keys = ("delta_state", "delta_val", "sender", "src_val", "dst_val", "ps", "pv")
+    out = {k: [] for k in keys}
+    acc = [torch.zeros_like(p) for p in params]
+    B = src.shape[0]
+    for b0 in range(0, B, chunk):
+        b1 = min(B, b0 + chunk)
+        leaves = [torch.as_tensor(t[b0:b1]).to(**f32).requires_grad_(True) for t in (rho, src, dst, ps, pv)]
+        r_, s_, d_, p_s, p_v = leaves
+        m = None if mask is None else _bool_mask(mask, dev, b0, b1)
+        tgt = (d_ @ Wtd.T).transpose(-1, -2).contiguous()
+        l = ((s_ @ Wsd.T) * wd) @ tgt
+        if bd is not None:
+            l = l + bd
+        l = l / float(temperature)
+        wr = _route32(l, m, kind) * r_[..., :, None]
+        ds = (wr * p_s[..., :, None]).sum(-2)
+        dv = wr.transpose(-1, -2).contiguous() @ p_v
+        loss = (ds * torch.as_tensor(gds[b0:b1]).to(**f32)).sum() + (dv * torch.as_tensor(gdv[b0:b1]).to(**f32)).sum()
+        grads = torch.autograd.grad(loss, leaves + params)
+        out["delta_state"].append(ds.detach().cpu())
+        out["delta_val"].append(dv.detach().cpu())
+        for k, g in zip(keys[2:], grads[:5]):
+            out[k].append(g.cpu())
+        for a, g in zip(acc, grads[5:]):
+            a += g
+    res = {k: torch.cat(v).double().numpy() for k, v in out.items()}
+    names = ["Ws", "Wt", "w"] + (["b"] if bd is not None else [])
+    for n, a in zip(names, acc):
+        res[n] = a.double().cpu().numpy()
+    return res
+
+
+def check_selection(idx, score, ref_scores, k, gap=1e-5) -> float:
+    """A GPU top-k selection [B, Nq, k] against float64 scores [B, Nq, Nk].
+
+    Indices in range and distinct per row; the reported scores are the
+    oracle scores of the reported indices (1e-5) and sorted descending; the
+    index set equals the oracle's on every row whose k-th/(k+1)-th gap exceeds
+    ``gap``; on the other rows the k-th reported score equals the oracle's k-th
+    best within 1e-5.  Returns the fraction of rows with an unambiguous set."""
+    idx = np.asarray(idx)
+    score = np.asarray(score, np.float64)
+    B, Nq, Nk = ref_scores.shape
+    assert idx.shape == (B, Nq, k)
+    assert (idx >= 0).all() and (idx < Nk).all()
+    srt = np.sort(idx, axis=-1)
+    assert (np.diff(srt, axis=-1) > 0).all(), "repeated index in a row"
+    picked = np.take_along_axis(ref_scores, idx.astype(np.int64), axis=-1)
+    err = np.abs(score - picked) - (1e-5 + 1e-5 * np.abs(picked))
+    assert err.max() <= 0, f"selected scores: max excess {err.max():.3e}"
+    assert (np.diff(score, axis=-1) <= 1e-6).all(), "scores not sorted descending"
+    if k < Nk:
+        # the k+1 best scores of each row (a partition, not a full sort: rows of 4096 keys)
+        part = np.partition(-ref_scores, k, axis=-1)[..., :k + 1]
+        top = -np.sort(part, axis=-1)
+        kth, nxt = top[..., k - 1], top[..., k]
+        ok = (kth - nxt) > gap
+        ref_idx = np.sort(np.argpartition(-ref_scores, k - 1, axis=-1)[..., :k], axis=-1)
+    else:
+        kth = ref_scores.min(axis=-1)
+        ok = np.ones((B, Nq), dtype=bool)
+        ref_idx = np.broadcast_to(np.arange(Nk), (B, Nq, Nk))
+    same = (srt == ref_idx).all(-1)
+    assert same[ok].all(), f"{(~same[ok]).sum()} unambiguous rows select a different set"
+    assert np.abs(score[..., -1] - kth).max() <= 1e-5
+    return float(ok.mean())
+
+
+BF16_RTOL = 2e-2
+
+
+def check_bf16(what, got, want, terms=None, rtol=BF16_RTOL) -> None:
+    """bf16 results: |got - want| <= rtol |want| plus an absolute floor of
+    rtol * 1e-2 * max|want|.  A bf16 leaf reached by several autograd paths
+    receives their bf16-rounded sum, so its error scales with the summed
+    magnitude of the path gradients (``terms``) rather than of the result."""
+    got, want = np64(got), np64(want)
+    mag = np.abs(want) if terms is None else sum(np.abs(np64(t)) for t in terms)
+    atol = rtol * 1e-2 * max(1.0, float(np.abs(want).max()))
+    err = np.abs(got - want) - (atol + rtol * mag)
+    rel = float((np.abs(got - want) / np.maximum(mag, atol)).max())
+    print(f"{what} (bf16): max|got-f64| {np.abs(got - want).max():.3e}, max relative {rel:.3e}, "
+          f"excess under rtol {rtol:g}: {err.max():.3e}", flush=True)
+    assert err.max() <= 0, f"{what}: max excess {err.max():.3e}"

@@ -1,0 +1,186 @@
+"""Full-shape GPU parity of the benchmarked workloads, forward and backward.
+
+The inputs are the benchmark's (bench.py): the same seeds, the same module
+initialisation, the same shapes.  The HIP results are compared with the
+float64 oracle evaluated on the selection the GPU made (one batch element at
+a time), and every tensor's error is set beside that of a plain fp32 torch
+evaluation of the same op on the same selection (tests/parity.py):
+
+* C4 top-k (B=16, N=4096, D=512, r=64, k=32; unit-norm value rows, default
+  init): the selection on every row, delta_state / delta_val and the
+  gradients of the layer values and states on every batch element, the
+  gradients of U, V, w_hat and b over all 2,097,152 edges;
+* C4 dense (same inputs, every pair): the same tensors;
+* C3 (B=8, D=512, r=64, top-16 per source, both directions) with bf16
+  layers, at the bf16 tolerance rtol 2e-2.
+
+Reference semantics: src/jakal_net/propagation.py:207-220, 453-480;
+src/jakal_net/transition.py:431-452.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import jakal_oracle as O
+from parity import check, check_bf16, check_selection, np64, torch32_propagation
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import jakal_net_native  # noqa: F401  (fails loudly when the library is missing)
+
+    return torch.device("cuda:0")
+
+
+def _c4_inputs():
+    """bench.py TopkC4.build: seeded state / unit-norm val rows, module init under torch.manual_seed(1004)."""
+    from jakal_net import LowRankBilinearPairwise
+
+    B, N, D, r = 16, 4096, 512, 64
+    g = torch.Generator().manual_seed(1004)
+    state = torch.randn(B, N, generator=g)
+    val = torch.randn(B, N, D, generator=g)
+    val = val / val.norm(dim=-1, keepdim=True)
+    torch.manual_seed(1004)
+    mod = LowRankBilinearPairwise(D, r)
+    U = mod.target_proj.weight.detach().clone()
+    V = mod.source_proj.weight.detach().clone()
+    w_hat = mod.normalized_weight().detach().clone()
+    b = float(mod.bias.detach())
+    gg = torch.Generator().manual_seed(2004)
+    gds = torch.randn(B, N, generator=gg)
+    gdv = torch.randn(B, N, D, generator=gg)
+    return state, val, U, V, w_hat, b, gds, gdv
+
+
+def _oracle_by_batch(val, state, U, V, w, b, gds, gdv, mode, masks=None):
+    """Oracle forward + backward one batch element at a time; parameter gradients summed."""
+    B = val.shape[0]
+    node = {k: [] for k in ("delta_state", "delta_val", "val", "ps")}
+    par = {k: 0.0 for k in ("U", "V", "w_hat", "b")}
+    for bb in range(B):
+        sl = slice(bb, bb + 1)
+        mask = None if masks is None else masks(bb)
+        gr = O.propagation_backward(val[sl], state[sl], val[sl], U, V, w, b, gds[sl], gdv[sl], mode=mode,
+                                    kind="softsign", mask=mask)
+        node["delta_state"].append(gr["delta_state"])
+        node["delta_val"].append(gr["delta_val"])
+        node["val"].append(gr["val"] + gr["pv"])  # projected_val is layer_val (identity val_proj_fn)
+        node["ps"].append(gr["ps"])
+        for k in par:
+            par[k] = par[k] + np.asarray(gr[k])
+        print(f"  oracle batch element {bb + 1}/{B} done", flush=True)
+    out = {k: np.concatenate(v) for k, v in node.items()}
+    out.update(par)
+    return out
+
+
+def _run_hip(dev, mode, state, val, U, V, w_hat, b, gds, gdv, k=None):
+    import jakal_net_native as jn
+
+    X = val.to(dev).requires_grad_(True)
+    ps = state.to(dev).requires_grad_(True)
+    Ud, Vd, wd = (t.to(dev).requires_grad_(True) for t in (U, V, w_hat))
+    bd = torch.tensor(b, device=dev).requires_grad_(True)
+    args = ("low_rank_bilinear", wd, bd, Vd, None, Ud, None, "softsign", X, ps, X)
+    idx = score = None
+    if mode == "topk":
+        ds, dv, idx, score = jn.propagation_topk_selection(*args, k, 128, 128)
+    else:
+        ds, dv = jn.propagation_dense(*args, None, 128, 128)
+    torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
+    torch.cuda.synchronize()
+    got = {"delta_state": ds, "delta_val": dv, "val": X.grad, "ps": ps.grad, "U": Ud.grad, "V": Vd.grad,
+           "w_hat": wd.grad, "b": bd.grad}
+    got = {n: np64(t) for n, t in got.items()}
+    return got, idx, score
+
+
+def _compare(got, want, ref32):
+    for name in ("delta_state", "delta_val", "val", "ps", "U", "V", "w_hat", "b"):
+        check(f"C4 {name}", got[name], want[name], ref32[name])
+
+
+def test_c4_topk_forward_backward_full_shape(dev):
+    state, val, U, V, w_hat, b, gds, gdv = _c4_inputs()
+    B, N, D = val.shape
+    k = 32
+    print("C4 top-k: HIP forward + backward", flush=True)
+    got, idx, score = _run_hip(dev, "topk", state, val, U, V, w_hat, b, gds, gdv, k=k)
+    idx_np = idx.cpu().numpy()
+    score_np = score.cpu().numpy()
+    # the selection on every row, against float64 scores (one batch element at a time)
+    vn, Un, Vn, wn = np64(val), np64(U), np64(V), np64(w_hat)
+    fracs = []
+    for bb in range(B):
+        s = O.lowrank_pairwise_scores(vn[bb:bb + 1], vn[bb:bb + 1], Un, Vn, wn, b)
+        fracs.append(check_selection(idx_np[bb:bb + 1], score_np[bb:bb + 1], s, k))
+    print(f"C4 top-k selection: rows with an unambiguous set {np.mean(fracs):.4f}", flush=True)
+    want = _oracle_by_batch(vn, np64(state), Un, Vn, wn, b, np64(gds), np64(gdv), "topk",
+                            masks=lambda bb: O.mask_from_indices(idx_np[bb:bb + 1], N))
+    mask = O.mask_from_indices(idx_np, N)
+    ref32 = torch32_propagation(dev, val, state, None, U, V, w_hat, b, mask, "softsign", gds, gdv)
+    _compare(got, want, ref32)
+
+
+def test_c4_dense_forward_backward_full_shape(dev):
+    state, val, U, V, w_hat, b, gds, gdv = _c4_inputs()
+    B, N, D = val.shape
+    print("C4 dense: HIP forward + backward", flush=True)
+    got, _, _ = _run_hip(dev, "dense", state, val, U, V, w_hat, b, gds, gdv)
+    want = _oracle_by_batch(np64(val), np64(state), np64(U), np64(V), np64(w_hat), b, np64(gds), np64(gdv),
+                            "dense")
+    mask = np.ones((B, N, N), dtype=bool)
+    ref32 = torch32_propagation(dev, val, state, None, U, V, w_hat, b, mask, "softsign", gds, gdv)
+    _compare(got, want, ref32)
+
+
+@pytest.mark.parametrize("Ns,Nd", [(1024, 256), (256, 1024)])
+def test_c3_bf16_transition_full_shape(dev, Ns, Nd):
+    """BASELINE config 3 with bf16 layers: B=8, D=512, r=64, top-16 per source,
+    softmax routes, default init, T=1; projected_val is the source values and
+    the sender strength softplus(state) is differentiated with the state."""
+    import jakal_net_native as jn
+    from jakal_net import LowRankBilinearRoute
+
+    B, D, r, k = 8, 512, 64, 16
+    g = torch.Generator().manual_seed(1003)
+    src = torch.randn(B, Ns, D, generator=g).bfloat16()
+    dst = torch.randn(B, Nd, D, generator=g).bfloat16()
+    state = torch.randn(B, Ns, generator=g).bfloat16()
+    torch.manual_seed(1003)
+    route = LowRankBilinearRoute(D, D, rank=r)
+    Ws, Wt = route.source_proj.weight.detach(), route.target_proj.weight.detach()
+    w, bias = route.weight.detach(), float(route.bias.detach())
+    srcd = src.to(dev).requires_grad_(True)
+    dstd = dst.to(dev).requires_grad_(True)
+    psd = state.to(dev).requires_grad_(True)
+    rho = torch.nn.functional.softplus(psd)
+    ds, dv, idx, logit = jn.transition_pairwise_topk_routes(
+        "low_rank_bilinear_route", Ws.to(dev), None, Wt.to(dev), None, w.to(dev),
+        torch.tensor(bias, device=dev), None, None, None, None, 1.0, rho, srcd, dstd, psd, srcd, k, Ns, Nd)
+    assert ds.dtype == torch.bfloat16 and dv.dtype == torch.bfloat16
+    gg = torch.Generator().manual_seed(2003)
+    gds = torch.randn(B, Nd, generator=gg).bfloat16()
+    gdv = torch.randn(B, Nd, D, generator=gg).bfloat16()
+    torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
+    assert srcd.grad.dtype == torch.bfloat16
+
+    logits = O.lowrank_route_logits(np64(src), np64(dst), np64(Ws), np64(Wt), np64(w), bias)
+    frac = check_selection(idx.cpu().numpy(), logit.cpu().numpy(), logits, k)
+    print(f"C3 bf16 {Ns}->{Nd}: rows with an unambiguous set {frac:.4f}", flush=True)
+    assert frac > 0.5
+    mask = O.mask_from_indices(idx.cpu().numpy(), Nd)
+    rho_np = np64(rho)
+    gr = O.transition_backward(np64(src), np64(dst), rho_np, np64(state), np64(src), np64(Ws), np64(Wt), np64(w),
+                               bias, np64(gds), np64(gdv), topk=k, mask=mask)
+    check_bf16("delta_state", ds, gr["delta_state"])
+    check_bf16("delta_val", dv, gr["delta_val"])
+    check_bf16("grad src_val", srcd.grad, gr["src_val"] + gr["pv"], terms=(gr["src_val"], gr["pv"]))
+    check_bf16("grad dst_val", dstd.grad, gr["dst_val"])
+    sig = 1.0 / (1.0 + np.exp(-np64(state)))
+    check_bf16("grad state", psd.grad, gr["ps"] + gr["sender"] * sig, terms=(gr["ps"], gr["sender"] * sig))

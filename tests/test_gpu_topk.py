@@ -3,7 +3,9 @@
 Index parity is exact on rows whose k-th/(k+1)-th score gap exceeds 1e-5;
 values and gradients are compared to the oracle evaluated on the selection the
 GPU made (identical to the oracle's on every checkable row), fp32 tolerance
-rtol 1e-4 / atol 1e-5 as stated for the hot path.
+rtol 1e-4 / atol 1e-5 as stated for the hot path, or, for long sums that miss
+it, at most twice the error of an fp32 torch evaluation (tests/parity.py).
+The full C4 shape, forward and backward, is in test_gpu_full_shape.py.
 """
 
 import math
@@ -13,6 +15,7 @@ import pytest
 import torch
 
 import jakal_oracle as O
+from parity import check, check_selection, torch32_propagation
 
 pytestmark = pytest.mark.gpu
 
@@ -40,30 +43,6 @@ def _close(got, want, rtol=RTOL, atol=ATOL, what=""):
     assert err.max() <= 0, f"{what}: max excess {err.max():.3e} (max abs diff {np.abs(got - want).max():.3e})"
 
 
-def _check_select(idx, score, ref_scores, k):
-    """idx/score from the GPU vs dense oracle scores [B, Nq, Nk]."""
-    B, Nq, Nk = ref_scores.shape
-    assert idx.shape == (B, Nq, k)
-    assert (idx >= 0).all() and (idx < Nk).all()
-    # unique per row
-    srt = np.sort(idx, axis=-1)
-    assert (np.diff(srt, axis=-1) > 0).all()
-    # reported scores are the scores of the reported indices
-    picked = np.take_along_axis(ref_scores, idx, axis=-1)
-    _close(score, picked, rtol=1e-5, atol=1e-5, what="selected scores")
-    # descending order
-    assert (np.diff(score, axis=-1) <= 1e-6).all()
-    # exact index-set parity on checkable rows
-    ok = O.checkable_rows(ref_scores, k)
-    ref_idx = np.sort(O.topk_indices(ref_scores, k), axis=-1)
-    same = (srt == ref_idx).all(-1)
-    assert same[ok].all(), f"{(~same[ok]).sum()} checkable rows differ"
-    # on ambiguous rows the k-th best score still agrees
-    kth = np.sort(ref_scores, axis=-1)[..., ::-1][..., k - 1]
-    assert np.abs(score[..., -1] - kth).max() <= 1e-5
-    return ok.mean()
-
-
 @pytest.mark.parametrize("r,k,Nq,Nk", [(3, 2, 9, 9), (16, 8, 256, 256), (64, 32, 200, 333), (64, 1, 70, 50),
                                        (32, 16, 130, 1024), (100, 5, 64, 97), (64, 33, 100, 300),
                                        (16, 48, 150, 49), (64, 64, 257, 2000), (8, 64, 64, 65),
@@ -84,7 +63,7 @@ def test_select_matches_oracle(dev, r, k, Nq, Nk):
         sq = q.double().numpy() * (scale.double().numpy() if scale_on_query else 1.0)
         sk = key.double().numpy() * (1.0 if scale_on_query else scale.double().numpy())
         ref = (sq @ np.swapaxes(sk, 1, 2) + 0.25) / temp
-        _check_select(idx.cpu().numpy(), score.cpu().numpy(), ref, k)
+        check_selection(idx.cpu().numpy(), score.cpu().numpy(), ref, k)
 
 
 @pytest.mark.parametrize("Nk", [200, 2100])
@@ -121,7 +100,7 @@ def test_select_few_dominant_keys(dev, k, groups):
     q[0, 1::2, 1] = 1.0
     idx, score = jn.low_rank_topk_select(q.to(dev), key.to(dev), None, None, False, 1.0, k)
     ref = q.double().numpy() @ np.swapaxes(key.double().numpy(), 1, 2)
-    _check_select(idx.cpu().numpy(), score.cpu().numpy(), ref, k)
+    check_selection(idx.cpu().numpy(), score.cpu().numpy(), ref, k)
     top = np.sort(idx.cpu().numpy()[0, 0::2], axis=-1)
     assert set(special) <= set(top[0].tolist())
 
@@ -152,14 +131,14 @@ def test_propagation_topk_split_row_backward(dev, N, D, k, compress):
     """Value rows of a batch element above 2 MiB with 256 < D <= 1024: the row
     backward computes its dot products in two column slabs first (ragged second
     slab for D = 520 and 388)."""
-    _run_topk(dev, _c1_inputs(seed=1100 + k, B=1, N=N, D=D, r=24), compress, True, k, min_checkable=0.3,
-              normwise=True)
+    _run_topk(dev, _c1_inputs(seed=1100 + k, B=1, N=N, D=D, r=24), compress, True, k, min_checkable=0.3)
 
 
-def _run_topk(dev, inputs, compress, separate_pv, k, min_checkable, normwise=False):
-    """normwise: the absolute tolerance of the outputs and node gradients
-    scales with the tensor's largest entry (at larger D, r and k they are long
-    sums of terms far larger than the entries that cancel to near 0)."""
+def _run_topk(dev, inputs, compress, separate_pv, k, min_checkable):
+    """Outputs and gradients against the float64 oracle on the GPU's selection;
+    tensors that miss the literal tolerance (long fp32 sums at larger D, r and
+    k) must stay within twice the error of an fp32 torch evaluation of the
+    same op on the same selection (parity.check)."""
     import jakal_net_native as jn
 
     state, val, U, V, w, b = inputs
@@ -182,34 +161,21 @@ def _run_topk(dev, inputs, compress, separate_pv, k, min_checkable, normwise=Fal
 
     # the selection the forward aggregated, against float64 scores
     scores = O.lowrank_pairwise_scores(_np(val), _np(val), _np(U), _np(V), _np(w), float(b))
-    frac = _check_select(idx.cpu().numpy(), score.cpu().numpy(), scores, k)
+    frac = check_selection(idx.cpu().numpy(), score.cpu().numpy(), scores, k)
     assert frac > min_checkable  # deeper cuts sit in denser parts of the score distribution
     mask = O.mask_from_indices(idx.cpu().numpy(), N)
-    ref = O.propagation_forward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), float(b),
-                                mode="topk", topk=k, kind=compress, mask=mask)
-
-    def node_atol(want):
-        return ATOL * max(1.0, float(np.abs(want).max())) if normwise else ATOL
-
-    _close(_np(ds), ref["delta_state"], atol=node_atol(ref["delta_state"]), what="delta_state")
-    _close(_np(dv), ref["delta_val"], atol=node_atol(ref["delta_val"]), what="delta_val")
-
     gr = O.propagation_backward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), float(b), _np(gds),
                                 _np(gdv), mode="topk", topk=k, kind=compress, mask=mask)
-    g_val = gr["val"] + (0.0 if separate_pv else gr["pv"])
-    _close(_np(X.grad), g_val, atol=node_atol(g_val), what="grad layer_val")
-    _close(_np(ps.grad), gr["ps"], atol=node_atol(gr["ps"]), what="grad projected_state")
+    t32 = torch32_propagation(dev, val, state, pv_cpu if separate_pv else None, U, V, w_hat, float(b), mask,
+                              compress, gds, gdv)
+    check("delta_state", ds, gr["delta_state"], t32["delta_state"])
+    check("delta_val", dv, gr["delta_val"], t32["delta_val"])
+    check("grad layer_val", X.grad, gr["val"] + (0.0 if separate_pv else gr["pv"]), t32["val"])
+    check("grad projected_state", ps.grad, gr["ps"], t32["ps"])
     if separate_pv:
-        _close(_np(pv.grad), gr["pv"], atol=node_atol(gr["pv"]), what="grad projected_val")
-    # Parameter gradients are sums over all B*N*k edges.  fp32 error of such a
-    # sum grows with the size of its terms, not of the result (which can
-    # cancel to ~0), so atol scales with max|want| and with the root-mean L1
-    # size of the per-edge score gradients sum|g_s| / sqrt(#edges).
-    gs = gr["g_scores"][mask]
-    scale = max(1.0, float(np.abs(gs).sum() / math.sqrt(gs.size)))
-    for got, want, what in ((Ud.grad, gr["U"], "grad target_proj"), (Vd.grad, gr["V"], "grad source_proj"),
-                            (wd.grad, gr["w_hat"], "grad w_hat"), (bd.grad, gr["b"], "grad bias")):
-        _close(_np(got), want, atol=ATOL * max(scale, float(np.abs(want).max())), what=what)
+        check("grad projected_val", pv.grad, gr["pv"], t32["pv"])
+    for t, name in ((Ud, "U"), (Vd, "V"), (wd, "w_hat"), (bd, "b")):
+        check(f"grad {name}", t.grad, gr[name], t32[name])
 
 
 def test_sparse_propagation_api_native_matches_reference(dev):
@@ -227,46 +193,6 @@ def test_sparse_propagation_api_native_matches_reference(dev):
     a, b = ref(layer), nat(layer)
     assert torch.allclose(a.delta_state, b.delta_state, atol=1e-5, rtol=1e-5)
     assert torch.allclose(a.delta_val, b.delta_val, atol=1e-5, rtol=1e-5)
-
-
-def test_c4_shape_forward_sampled_rows(dev):
-    """Full C4 shape (B=16, N=4096, D=512, r=64, k=32): index parity on sampled
-    rows against float64 scores, and delta rows recomputed from the selection."""
-    import jakal_net_native as jn
-
-    g = torch.Generator().manual_seed(1004)
-    B, N, D, r, k = 16, 4096, 512, 64, 32
-    state = torch.randn(B, N, generator=g)
-    val = torch.randn(B, N, D, generator=g)
-    val = val / val.norm(dim=-1, keepdim=True)
-    lin_t = torch.nn.Linear(D, r, bias=False)
-    lin_s = torch.nn.Linear(D, r, bias=False)
-    U, V = lin_t.weight.detach(), lin_s.weight.detach()
-    w_hat = torch.ones(r) / math.sqrt(r)
-    Xd = val.to(dev)
-    ds, dv, idx, score = jn.propagation_topk_selection("low_rank_bilinear", w_hat.to(dev), None, V.to(dev), None,
-                                                       U.to(dev), None, "softsign", Xd, state.to(dev), Xd, k,
-                                                       128, 128)
-    pt = (val.double() @ U.double().T)
-    psh = (val.double() @ V.double().T) * w_hat.double()
-    rows = torch.randint(0, N, (8,), generator=g)
-    checked = 0
-    for bb in (0, 7, 15):
-        s = (pt[bb, rows] @ psh[bb].T).numpy()[None]  # [1, 8, N]
-        ii = idx[bb, rows].cpu().numpy()[None]
-        ok = O.checkable_rows(s, k)
-        ref_idx = np.sort(O.topk_indices(s, k), -1)
-        assert (np.sort(ii, -1) == ref_idx).all(-1)[ok].all()
-        checked += ok.sum()
-        # delta rows from the GPU selection
-        e = torch.from_numpy(np.take_along_axis(s, ii.astype(np.int64), -1)[0])
-        e = e / (1 + e.abs())
-        sel = torch.from_numpy(ii[0].astype(np.int64))
-        want_v = (e[:, :, None] * val.double()[bb][sel]).sum(1)
-        want_s = (e * state.double()[bb][sel]).sum(1)
-        _close(_np(dv[bb, rows]), want_v.numpy(), what="C4 delta_val rows")
-        _close(_np(ds[bb, rows]), want_s.numpy(), what="C4 delta_state rows")
-    print(f"C4 sampled rows with unambiguous top-k: {checked}/24")
 
 
 def test_c4_shape_select_every_row(dev):

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import jakal_oracle as O
+from parity import check, torch32_propagation
 
 pytestmark = pytest.mark.gpu
 
@@ -58,9 +59,7 @@ def _expected_window_index(N, window):
     return np.where(j >= 0, j, -1)
 
 
-def _run(dev, seed, B, N, D, r, window, compress, separate_pv, init="xavier", normwise=False):
-    """normwise: the absolute tolerance of the outputs and node gradients
-    scales with the tensor's largest entry (long sums at larger D and widths)."""
+def _run(dev, seed, B, N, D, r, window, compress, separate_pv, init="xavier"):
     import jakal_net_native as jn
 
     g, state, val, U, V, w, b = _inputs(seed, B, N, D, r, init)
@@ -87,26 +86,24 @@ def _run(dev, seed, B, N, D, r, window, compress, separate_pv, init="xavier", no
     got_score = score.cpu().numpy()
     _close(got_score[:, valid], picked[:, valid], rtol=1e-5, atol=1e-5, what="edge scores")
 
-    ref = O.propagation_forward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), float(b), mode="window",
-                                window=window, kind=compress)
-
-    def node_atol(want):
-        return ATOL * max(1.0, float(np.abs(want).max())) if normwise else ATOL
-
-    _close(_np(ds), ref["delta_state"], atol=node_atol(ref["delta_state"]), what="delta_state")
-    _close(_np(dv), ref["delta_val"], atol=node_atol(ref["delta_val"]), what="delta_val")
     gr = O.propagation_backward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), float(b), _np(gds),
                                 _np(gdv), mode="window", window=window, kind=compress)
-    g_val = gr["val"] + (0.0 if separate_pv else gr["pv"])
-    _close(_np(X.grad), g_val, atol=node_atol(g_val), what="grad layer_val")
-    _close(_np(ps.grad), gr["ps"], atol=node_atol(gr["ps"]), what="grad projected_state")
-    if separate_pv:
-        _close(_np(pv.grad), gr["pv"], atol=node_atol(gr["pv"]), what="grad projected_val")
-    gs = gr["g_scores"][ref["mask"]]
-    scale = max(1.0, float(np.abs(gs).sum() / math.sqrt(gs.size)))
-    for got, want, what in ((Ud.grad, gr["U"], "grad target_proj"), (Vd.grad, gr["V"], "grad source_proj"),
-                            (wd.grad, gr["w_hat"], "grad w_hat"), (bd.grad, gr["b"], "grad bias")):
-        _close(_np(got), want, atol=ATOL * max(scale, float(np.abs(want).max())), what=what)
+    mask = np.broadcast_to(O.causal_window_mask(N, window), (B, N, N))
+    t32 = torch32_propagation(dev, val, state, pv_cpu if separate_pv else None, U, V, w_hat, float(b), mask,
+                              compress, gds, gdv)
+    _compare(gr, t32, ds, dv, X, ps, pv if separate_pv else None, Ud, Vd, wd, bd)
+
+
+def _compare(gr, t32, ds, dv, X, ps, pv, Ud, Vd, wd, bd):
+    """Every output and gradient against the oracle (parity.check, calibrated by the fp32 torch run)."""
+    check("delta_state", ds, gr["delta_state"], t32["delta_state"])
+    check("delta_val", dv, gr["delta_val"], t32["delta_val"])
+    check("grad layer_val", X.grad, gr["val"] + (0.0 if pv is not None else gr["pv"]), t32["val"])
+    check("grad projected_state", ps.grad, gr["ps"], t32["ps"])
+    if pv is not None:
+        check("grad projected_val", pv.grad, gr["pv"], t32["pv"])
+    for t, name in ((Ud, "U"), (Vd, "V"), (wd, "w_hat"), (bd, "b")):
+        check(f"grad {name}", t.grad, gr[name], t32[name])
 
 
 @pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax", "signed_entmax15"])
@@ -126,8 +123,7 @@ def test_window_edge_cases(dev, window, N):
 def test_window_split_row_backward(dev, window, compress):
     """Value rows of a batch element above 2 MiB with 256 < D <= 1024 (two column
     slabs for the row backward's dot products); width 101 takes two edge blocks."""
-    _run(dev, 2100 + window, B=1, N=1100, D=520, r=16, window=window, compress=compress, separate_pv=True,
-         normwise=True)
+    _run(dev, 2100 + window, B=1, N=1100, D=520, r=16, window=window, compress=compress, separate_pv=True)
 
 
 def test_window_c2_shape(dev):
@@ -172,19 +168,9 @@ def test_full_causal_window_runs_dense(dev, compress, separate_pv, window_extra)
     gds = torch.randn(B, N, generator=g)
     gdv = torch.randn(B, N, D, generator=g)
     torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
-    ref = O.propagation_forward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), float(b), mode="window",
-                                window=window, kind=compress)
-    _close(_np(ds), ref["delta_state"], atol=ATOL * max(1.0, float(np.abs(ref["delta_state"]).max())),
-           what="delta_state")
-    _close(_np(dv), ref["delta_val"], atol=ATOL * max(1.0, float(np.abs(ref["delta_val"]).max())), what="delta_val")
     gr = O.propagation_backward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), float(b), _np(gds),
                                 _np(gdv), mode="window", window=window, kind=compress)
-    g_val = gr["val"] + (0.0 if separate_pv else gr["pv"])
-    for got, want, what in ((X.grad, g_val, "grad layer_val"), (ps.grad, gr["ps"], "grad projected_state")) + (
-            ((pv.grad, gr["pv"], "grad projected_val"),) if separate_pv else ()):
-        _close(_np(got), want, atol=ATOL * max(1.0, float(np.abs(want).max())), what=what)
-    gs = gr["g_scores"][ref["mask"]]
-    scale = max(1.0, float(np.abs(gs).sum() / math.sqrt(gs.size)))
-    for got, want, what in ((Ud.grad, gr["U"], "grad target_proj"), (Vd.grad, gr["V"], "grad source_proj"),
-                            (wd.grad, gr["w_hat"], "grad w_hat"), (bd.grad, gr["b"], "grad bias")):
-        _close(_np(got), want, atol=ATOL * max(scale, float(np.abs(want).max())), what=what)
+    mask = np.broadcast_to(O.causal_window_mask(N, window), (B, N, N))
+    t32 = torch32_propagation(dev, val, state, pv_cpu if separate_pv else None, U, V, w_hat, float(b), mask,
+                              compress, gds, gdv)
+    _compare(gr, t32, ds, dv, X, ps, pv if separate_pv else None, Ud, Vd, wd, bd)

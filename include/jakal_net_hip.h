@@ -118,6 +118,29 @@ int jn_propagation_topk_forward(const float* layer_val, const float* projected_s
 /* Workspace of jn_propagation_topk_forward (the select's; unused in select mode 1). */
 size_t jn_propagation_topk_forward_workspace_bytes(int64_t batch, int64_t nodes, int64_t rank);
 
+/*
+ * jn_propagation_topk_forward without a workspace argument: it allocates
+ * nothing and takes its scratch from a static device array of
+ * jn_static_scratch_bytes() bytes (48 MiB) held by each GPU the library runs
+ * on.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as
+ * jn_propagation_topk_forward; a shape whose select scratch
+ * (jn_propagation_topk_forward_workspace_bytes) exceeds the array is rejected
+ * with kUnsupported before anything is launched.  Calls that overlap on one
+ * GPU (other streams or host threads) share the array and race on it.
+ */
+int jn_propagation_topk_forward_static(const float* layer_val, const float* projected_state,
+                                       const float* projected_val, const float* target_weight,
+                                       const float* source_weight, const float* core_weight, const float* bias,
+                                       int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                       int64_t topk, int32_t compress_kind, float* delta_state, float* delta_val,
+                                       float* projections, int32_t* topk_index, float* topk_score,
+                                       jn_stream_t stream);
+
+/* Size in bytes of the static scratch array of jn_propagation_topk_forward_static. */
+size_t jn_static_scratch_bytes(void);
+
 /* Workspace needed by jn_propagation_topk_backward. */
 size_t jn_propagation_topk_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                            int64_t rank, int64_t topk);

@@ -24,7 +24,8 @@ Prints one JSON line:
                region; `traffic` = HBM-side bytes per launch measured by
                rocprofv3 FETCH_SIZE/WRITE_SIZE passes of this command
   kernels      the same figures for every kernel of the step
-  cpu_baseline the numpy oracle (fp32) timed on a bounded sample on the host
+  cpu_baseline the same workload through the operator API's implementation="reference"
+               backend on the host cores (warmup 1, median of 3)
 
 The top-k select's flops are fp32-equivalent score products (2 r per pair),
 priced against the fp32 MFMA peak.  With --select-mode split-f16 (the
@@ -67,75 +68,148 @@ def rows_backward_split(nk: int, D: int) -> bool:
     return 256 < D <= 1024 and nk * D * 4 > (2 << 20)
 
 
-def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = False) -> tuple[str, float] | None:
-    """(bound, algorithmic bytes or flops per launch) of the edge-list kernels.
+def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = False,
+                      Mk: int | None = None) -> tuple | None:
+    """(bound, algorithmic bytes or flops, compulsory bytes) of the edge-list kernels.
 
-    M = aggregated rows, E = routed pairs.  Bytes count every operand once per
-    use (no cache reuse credited): an edge gathers one D-row of fp32 values,
-    its index and score.  split: the row backward runs as dots + finish."""
+    M = aggregated (query) rows, Mk = source (key) rows (M for propagation),
+    E = routed pairs.  Algorithmic bytes count every operand once per use (an
+    edge gathers one D-row of fp32 values, its index and score), so they
+    credit no cache reuse; compulsory bytes count each distinct input row once
+    and each output once: the HBM bytes no schedule can avoid.  The gathers
+    reuse each value row about k times from L2, so their algorithmic rate is an
+    L2-side figure and their HBM roofline fraction is priced on compulsory bytes.
+    split: the row backward runs as dots + finish."""
+    Mk = M if Mk is None else Mk
     if name.startswith("rows_forward_kernel"):
         # idx+score+ps per edge, pv row per edge; delta_val row + delta_state per row
-        return "hbm", E * (12.0 + 4.0 * D) + M * (4.0 * D + 4.0)
+        return ("hbm", E * (12.0 + 4.0 * D) + M * (4.0 * D + 4.0),
+                E * 8.0 + Mk * (4.0 * D + 4.0) + M * (4.0 * D + 4.0))
     if name.startswith("rows_backward_dots_kernel"):
         # idx, pv row, partial-dot write per edge; grad-delta row per row
-        return "hbm", E * (4.0 + 4.0 * D + 4.0) + M * 4.0 * D
+        return ("hbm", E * (4.0 + 4.0 * D + 4.0) + M * 4.0 * D,
+                E * 12.0 + (M + Mk) * 4.0 * D)
     if name.startswith("rows_backward_kernel"):
         if split:
             # idx+score, two partial dots, ps, key row, gsc+coef writes per edge;
             # grad-delta state, dq row, row sum per row
-            return "hbm", E * (8.0 + 8.0 + 4.0 + 4.0 * r + 8.0) + M * (4.0 + 4.0 * r + 4.0)
+            return ("hbm", E * (8.0 + 8.0 + 4.0 + 4.0 * r + 8.0) + M * (4.0 + 4.0 * r + 4.0),
+                    E * 24.0 + Mk * (4.0 + 4.0 * r) + M * (8.0 + 4.0 * r))
         # idx+score, ps, pv row, key row per edge; gsc+coef writes per edge;
         # grad-delta row + state, dq row, row sum per row
-        return "hbm", E * (8.0 + 4.0 + 4.0 * D + 4.0 * r + 8.0) + M * (4.0 * D + 4.0 + 4.0 * r + 4.0)
+        return ("hbm", E * (8.0 + 4.0 + 4.0 * D + 4.0 * r + 8.0) + M * (4.0 * D + 4.0 + 4.0 * r + 4.0),
+                E * 16.0 + Mk * (4.0 * D + 4.0 * r + 4.0) + M * (4.0 * D + 4.0 * r + 8.0))
     if name.startswith("cols_gather_kernel"):
         # edge record, grad-delta row per edge; segment bounds, grad_pv row, grad_ps per column
-        return "hbm", E * (16.0 + 4.0 * D) + M * (8.0 + 4.0 * D + 4.0)
+        return ("hbm", E * (16.0 + 4.0 * D) + Mk * (8.0 + 4.0 * D + 4.0),
+                E * 16.0 + M * 4.0 * D + Mk * (4.0 * D + 8.0))
     if name.startswith("cols_keygrad_kernel"):
         # edge record, query row per edge; segment bounds, dk row, key row per column
-        return "hbm", E * (16.0 + 4.0 * r) + M * (8.0 + 8.0 * r)
+        return ("hbm", E * (16.0 + 4.0 * r) + Mk * (8.0 + 8.0 * r),
+                E * 16.0 + M * 4.0 * r + Mk * (8.0 * r + 4.0))
     if name.startswith("window_scores_kernel"):
         # query row per row; key row per edge; idx + score written per edge
-        return "hbm", E * (4.0 * r + 8.0) + M * 4.0 * r
+        return ("hbm", E * (4.0 * r + 8.0) + M * 4.0 * r, E * 8.0 + (M + Mk) * 4.0 * r)
     if name.startswith("gemm_f32_kernel"):
-        return "mfma", 2.0 * M * D * 2 * r
+        return ("mfma", 2.0 * M * D * 2 * r, None)
     return None
 
 
-def split_prep_model(name: str, key_rows: float, r: int) -> tuple[str, float] | None:
+def split_prep_model(name: str, key_rows: float, r: int) -> tuple | None:
     """The split-fp16 select's two prep kernels over key_rows key rows per launch:
     a max-|key| pass (reads the keys) and the split (reads them again, writes
     hi and lo fp16 planes of the rank rounded up to 32)."""
     rp = -(-r // 32) * 32
     if name.startswith("select_split_absmax_kernel"):
-        return "hbm", key_rows * 4.0 * r
+        return "hbm", key_rows * 4.0 * r, key_rows * 4.0 * r
     if name.startswith("select_split_keys_kernel"):
-        return "hbm", key_rows * (4.0 * r + 4.0 * rp)
+        return "hbm", key_rows * (4.0 * r + 4.0 * rp), key_rows * (4.0 * r + 4.0 * rp)
     return None
 
 
-def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int) -> tuple[str, float] | None:
+def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int) -> tuple | None:
     """Kernel model of the headline (top-k) workload."""
     if name.startswith("lowrank_topk_select_kernel"):
-        return "mfma", 2.0 * B * N * N * r
+        return "mfma", 2.0 * B * N * N * r, None
     if name.startswith("select_split_"):
         return split_prep_model(name, B * N, r)
     return edge_kernel_model(name, B * N, B * N * k, D, r, rows_backward_split(N, D))
 
 
-def _threads() -> int | None:
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-        return max((i.get("num_threads") or 0) for i in threadpool_info()) or None
-    except Exception:  # noqa: BLE001
-        return None
+
+def cpu_baseline(wl, torch) -> dict:
+    """The same workload through the operator API's implementation="reference"
+    backend (the dense masked PyTorch form of propagation.py:453-480 /
+    transition.py:431-452) on the host cores: torch threads = the host's
+    cores (capped by OMP_NUM_THREADS when set, the CPU share a GPU box grants),
+    one warmup, the median of three timed forward+backward steps of loss =
+    sum(delta_state) + sum(delta_val).  The sample is the whole workload, or
+    `cpu_batch` of its batch elements where the dense [B, N, N] reference form
+    would take tens of seconds per step; pairs/s is scaled to the sample."""
+    cores = os.cpu_count() or 1
+    share = os.environ.get("OMP_NUM_THREADS")
+    threads = min(cores, int(share)) if share and share.isdigit() and int(share) > 0 else cores
+    full = wl.config["batch"]
+    batch = min(full, getattr(wl, "cpu_batch", full))
+    saved = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        op, layer = wl.build(torch, torch.device("cpu"), impl="reference", batch=batch)
+        step = _make_step(torch, op, layer)
+        step()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(saved)
+    t = sorted(times)[1]
+    what = "the whole workload" if batch == full else f"{batch} of its {full} batch elements"
+    return {
+        "value": wl.edges() * batch / full / t,
+        "unit": "routed pairs/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{what} ({wl.workload.replace(', native', '')}) through implementation='reference' on "
+                  f"the CPU, fp32, torch threads {threads} (os.cpu_count() {cores}), warmup 1, median of 3: "
+                  f"{t:.3f} s per step",
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": cores,
+        "torch_threads": threads,
+        "step_s": [round(x, 4) for x in times],
+    }
 
 
-def _oracle():
-    sys.path.insert(0, str(ROOT / "oracle"))
-    import jakal_oracle
+def _make_step(torch, op, layer):
+    """One forward+backward of loss = sum of every delta tensor (grads cleared first)."""
+    if layer is None:  # a multi-module step: op supplies its own loss terms
+        ones = [torch.ones_like(t) for t in op.loss_terms()]
 
-    return jakal_oracle
+        def step() -> None:
+            op.zero_grad(set_to_none=True)
+            torch.autograd.backward(op.loss_terms(), ones)
+        return step
+
+    ones_s = torch.ones_like(layer.state)
+    ones_v = torch.ones_like(layer.val)
+
+    def step() -> None:
+        op.zero_grad(set_to_none=True)
+        layer.val.grad = None
+        layer.state.grad = None
+        delta = op(layer)
+        torch.autograd.backward([delta.delta_state, delta.delta_val], [ones_s, ones_v])
+    return step
 
 
 # ---------------------------------------------------------------------------
@@ -148,6 +222,7 @@ class TopkC4:
     data = "synthetic (seeded N(0,1) state, unit-norm N(0,1) val rows, default module init)"
     config = CONFIG
     traffic_file = "c4_topk_hbm_traffic.json"
+    cpu_batch = 2  # CPU baseline sample: 2 of the 16 batch elements (about 3 s per step on 16 cores)
 
     def edges(self) -> int:
         c = self.config
@@ -163,52 +238,20 @@ class TopkC4:
         E, M, D = self.edges(), c["batch"] * c["nodes"], c["dim"]
         return 3 * 4 * D * (E + M) + 24 * E + 3 * 4 * (E + M)
 
-    def build(self, torch, dev):
+    def build(self, torch, dev, impl: str = "native", batch: int | None = None):
         from jakal_net import Layer, LowRankBilinearPairwise, SparsePropagation
 
         B, N, D, r, k = (self.config[x] for x in ("batch", "nodes", "dim", "rank", "topk"))
+        B = batch or B
         g = torch.Generator().manual_seed(1004)
         state = torch.randn(B, N, generator=g)
         val = torch.randn(B, N, D, generator=g)
         val = val / val.norm(dim=-1, keepdim=True)
         torch.manual_seed(1004)
         op = SparsePropagation(LowRankBilinearPairwise(D, r), sparse_type="topk", topk=k,
-                               implementation="native").to(dev)
+                               implementation=impl).to(dev)
         return op, Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True),
                          val=val.to(dev).requires_grad_(True))
-
-    def cpu_baseline(self, B_sample: int = 1) -> dict:
-        """Oracle (numpy, fp32) forward+backward on B_sample batch elements."""
-        import numpy as np
-
-        O = _oracle()
-        N, D, r, k = (self.config[x] for x in ("nodes", "dim", "rank", "topk"))
-        rng = np.random.default_rng(1004)
-        val = rng.standard_normal((B_sample, N, D)).astype(np.float32)
-        val /= np.linalg.norm(val, axis=-1, keepdims=True)
-        state = rng.standard_normal((B_sample, N)).astype(np.float32)
-        bound = 1.0 / math.sqrt(D)
-        U = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
-        V = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
-        w = np.ones(r, dtype=np.float32)
-        g_ds = np.ones((B_sample, N), np.float32)
-        g_dv = np.ones((B_sample, N, D), np.float32)
-        times = []
-        with O.compute_dtype(np.float32):
-            for _ in range(3):
-                t0 = time.perf_counter()
-                O.propagation_forward(val, state, val, U, V, w, 0.0, mode="topk", topk=k)
-                O.propagation_backward(val, state, val, U, V, w, 0.0, g_ds, g_dv, mode="topk", topk=k)
-                times.append(time.perf_counter() - t0)
-        t = sorted(times)[len(times) // 2]
-        return {
-            "value": B_sample * N * k / t,
-            "unit": "routed pairs/s",
-            "cores": _threads() or os.cpu_count(),
-            "kind": "port",
-            "sample": f"numpy oracle fp32, forward+backward, {B_sample} of {self.config['batch']} batch elements "
-                      f"(N={N}, D={D}, r={r}, k={k}), median of 3 ({t:.2f} s each)",
-        }
 
 
 class WindowC2:
@@ -234,51 +277,19 @@ class WindowC2:
         c = self.config
         return 5 * 4 * c["batch"] * c["nodes"] * c["dim"]
 
-    def build(self, torch, dev):
+    def build(self, torch, dev, impl: str = "native", batch: int | None = None):
         from jakal_net import Layer, LowRankBilinearPairwise, SparsePropagation
 
         B, N, D, r, w = (self.config[x] for x in ("batch", "nodes", "dim", "rank", "window"))
+        B = batch or B
         g = torch.Generator().manual_seed(1002)
         state = torch.randn(B, N, generator=g)
         val = torch.randn(B, N, D, generator=g)
         torch.manual_seed(1002)
         op = SparsePropagation(LowRankBilinearPairwise(D, r), sparse_type="window", window=w,
-                               implementation="native").to(dev)
+                               implementation=impl).to(dev)
         return op, Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True),
                          val=val.to(dev).requires_grad_(True))
-
-    def cpu_baseline(self, B_sample: int = 2) -> dict:
-        """Oracle (numpy, fp32) forward+backward on B_sample batch elements."""
-        import numpy as np
-
-        O = _oracle()
-        N, D, r, w = (self.config[x] for x in ("nodes", "dim", "rank", "window"))
-        rng = np.random.default_rng(1002)
-        val = rng.standard_normal((B_sample, N, D)).astype(np.float32)
-        state = rng.standard_normal((B_sample, N)).astype(np.float32)
-        bound = 1.0 / math.sqrt(D)
-        U = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
-        V = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
-        wv = np.ones(r, dtype=np.float32)
-        g_ds = np.ones((B_sample, N), np.float32)
-        g_dv = np.ones((B_sample, N, D), np.float32)
-        times = []
-        with O.compute_dtype(np.float32):
-            for _ in range(3):
-                t0 = time.perf_counter()
-                O.propagation_forward(val, state, val, U, V, wv, 0.0, mode="window", window=w)
-                O.propagation_backward(val, state, val, U, V, wv, 0.0, g_ds, g_dv, mode="window", window=w)
-                times.append(time.perf_counter() - t0)
-        t = sorted(times)[len(times) // 2]
-        pairs = self.edges() // self.config["batch"] * B_sample
-        return {
-            "value": pairs / t,
-            "unit": "routed pairs/s",
-            "cores": _threads() or os.cpu_count(),
-            "kind": "port",
-            "sample": f"numpy oracle fp32, forward+backward, {B_sample} of {self.config['batch']} batch elements "
-                      f"(T={N}, D={D}, r={r}, window={w}), median of 3 ({t:.2f} s each)",
-        }
 
 
 class TransitionC3:
@@ -301,16 +312,22 @@ class TransitionC3:
             return "mfma", 2.0 * B * S * Bn * r * 2  # both directions score S x B pairs
         if name.startswith("select_split_"):
             return split_prep_model(name, B * (S + Bn) / 2, r)  # keys: B rows one way, S rows the other
+        # per launch = half of both directions; `rows` counts source rows of both
+        # directions, which are also the destination rows of both
         if name.startswith("route_rows_backward_kernel"):
             # per edge: idx + logit + grad-delta row of the destination + its key row + g_logit write;
-            # per source row: its value row, its grad-value write, dq write
-            return "hbm", E * (8.0 + 4.0 * D + 4.0 * r + 4.0) + rows * (8.0 * D + 4.0 * r + 16.0) / 2
+            # per source row: its value row, its grad-value write, dq write.  Compulsory: each
+            # destination's grad-delta and key rows once
+            return ("hbm", (E * (8.0 + 4.0 * D + 4.0 * r + 4.0) + rows * (8.0 * D + 4.0 * r + 16.0)) / 2,
+                    (E * 12.0 + rows * (8.0 * D + 4.0 * r + 16.0) + rows * (4.0 * D + 4.0 * r)) / 2)
         if name.startswith("route_gather_kernel") or name.startswith("cols_gather_kernel"):
             # per edge: edge record + source value row; per destination: delta row write
-            return "hbm", (E * (16.0 + 4.0 * D) + rows * (4.0 * D + 12.0)) / 2
+            return ("hbm", (E * (16.0 + 4.0 * D) + rows * (4.0 * D + 12.0)) / 2,
+                    (E * 16.0 + rows * (8.0 * D + 12.0)) / 2)
         if name.startswith("cols_keygrad_kernel"):
             # per edge: edge record + source projection row; per destination: dk row + its projection row
-            return "hbm", (E * (16.0 + 4.0 * r) + rows * (8.0 + 8.0 * r)) / 2
+            return ("hbm", (E * (16.0 + 4.0 * r) + rows * (8.0 + 8.0 * r)) / 2,
+                    (E * 16.0 + rows * (12.0 * r + 4.0)) / 2)
         if name.startswith("gemm_f32_kernel"):
             return "mfma", 2.0 * rows * D * r / 2
         return None
@@ -326,58 +343,23 @@ class TransitionC3:
             tot += 8 * D * E + 3 * 4 * D * B * ns + 8 * D * B * nd + 24 * E
         return tot
 
-    def build(self, torch, dev):
+    def build(self, torch, dev, impl: str = "native", batch: int | None = None):
         from jakal_net import Layer, LowRankBilinearRoute, SparseTransition
 
         c = self.config
         B, S, Bn, D, r, k = (c[x] for x in ("batch", "s_nodes", "b_nodes", "dim", "rank", "topk"))
+        B = batch or B
         g = torch.Generator().manual_seed(1003)
         s_state, s_val = torch.randn(B, S, generator=g), torch.randn(B, S, D, generator=g)
         b_state, b_val = torch.randn(B, Bn, generator=g), torch.randn(B, Bn, D, generator=g)
         torch.manual_seed(1003)
-        s_to_b = SparseTransition(LowRankBilinearRoute(D, D, rank=r), topk=k, implementation="native").to(dev)
-        b_to_s = SparseTransition(LowRankBilinearRoute(D, D, rank=r), topk=k, implementation="native").to(dev)
+        s_to_b = SparseTransition(LowRankBilinearRoute(D, D, rank=r), topk=k, implementation=impl).to(dev)
+        b_to_s = SparseTransition(LowRankBilinearRoute(D, D, rank=r), topk=k, implementation=impl).to(dev)
         s_layer = Layer(dim=D, num_nodes=S, state=s_state.to(dev).requires_grad_(True),
                         val=s_val.to(dev).requires_grad_(True))
         b_layer = Layer(dim=D, num_nodes=Bn, state=b_state.to(dev).requires_grad_(True),
                         val=b_val.to(dev).requires_grad_(True))
         return _TwoWayTransition(torch, s_to_b, b_to_s, s_layer, b_layer), None
-
-    def cpu_baseline(self, B_sample: int = 2) -> dict:
-        """Oracle (numpy, fp32) forward+backward of both directions on B_sample batch elements."""
-        import numpy as np
-
-        O = _oracle()
-        c = self.config
-        S, Bn, D, r, k = (c[x] for x in ("s_nodes", "b_nodes", "dim", "rank", "topk"))
-        Bs = B_sample
-        rng = np.random.default_rng(1003)
-        bound = 1.0 / math.sqrt(D)
-        times = []
-        layers = {"S": (rng.standard_normal((Bs, S)), rng.standard_normal((Bs, S, D))),
-                  "B": (rng.standard_normal((Bs, Bn)), rng.standard_normal((Bs, Bn, D)))}
-        params = [rng.uniform(-bound, bound, (2, r, D)) for _ in range(2)]
-        with O.compute_dtype(np.float32):
-            for _ in range(3):
-                t0 = time.perf_counter()
-                for (src, dst), (Ws, Wt) in zip((("S", "B"), ("B", "S")), params):
-                    st, sv = layers[src]
-                    _, dv = layers[dst]
-                    rho = O.softplus(st)
-                    nd = dv.shape[1]
-                    O.transition_forward(sv, dv, rho, st, sv, Ws, Wt, np.ones(r), 0.0, topk=k)
-                    O.transition_backward(sv, dv, rho, st, sv, Ws, Wt, np.ones(r), 0.0, np.ones((Bs, nd)),
-                                          np.ones((Bs, nd, D)), topk=k)
-                times.append(time.perf_counter() - t0)
-        t = sorted(times)[len(times) // 2]
-        return {
-            "value": self.edges() // c["batch"] * Bs / t,
-            "unit": "routed pairs/s",
-            "cores": _threads() or os.cpu_count(),
-            "kind": "port",
-            "sample": f"numpy oracle fp32, forward+backward of both directions, {Bs} of {c['batch']} batch elements "
-                      f"(N_src=1024, N_dst=256, D={D}, r={r}, k={k}), median of 3 ({t:.2f} s each)",
-        }
 
 
 class DenseC4:
@@ -387,6 +369,7 @@ class DenseC4:
     data = "synthetic (seeded N(0,1) state, unit-norm N(0,1) val rows, default module init)"
     config = {"batch": 16, "nodes": 4096, "dim": 512, "rank": 64}
     traffic_file = "c4_dense_hbm_traffic.json"
+    cpu_batch = 4  # CPU baseline sample: 4 of the 16 batch elements
 
     def edges(self) -> int:
         c = self.config
@@ -420,51 +403,19 @@ class DenseC4:
         c = self.config
         return 4.0 * 6 * c["batch"] * c["nodes"] * c["nodes"]
 
-    def build(self, torch, dev):
+    def build(self, torch, dev, impl: str = "native", batch: int | None = None):
         from jakal_net import Layer, LowRankBilinearPairwise, Propagation
 
         B, N, D, r = (self.config[x] for x in ("batch", "nodes", "dim", "rank"))
+        B = batch or B
         g = torch.Generator().manual_seed(1004)
         state = torch.randn(B, N, generator=g)
         val = torch.randn(B, N, D, generator=g)
         val = val / val.norm(dim=-1, keepdim=True)
         torch.manual_seed(1004)
-        op = Propagation(LowRankBilinearPairwise(D, r), implementation="native").to(dev)
+        op = Propagation(LowRankBilinearPairwise(D, r), implementation=impl).to(dev)
         return op, Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True),
                          val=val.to(dev).requires_grad_(True))
-
-    def cpu_baseline(self, B_sample: int = 1) -> dict:
-        """Oracle (numpy, fp32) dense forward+backward on B_sample batch elements."""
-        import numpy as np
-
-        O = _oracle()
-        N, D, r = (self.config[x] for x in ("nodes", "dim", "rank"))
-        rng = np.random.default_rng(1004)
-        val = rng.standard_normal((B_sample, N, D)).astype(np.float32)
-        val /= np.linalg.norm(val, axis=-1, keepdims=True)
-        state = rng.standard_normal((B_sample, N)).astype(np.float32)
-        bound = 1.0 / math.sqrt(D)
-        U = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
-        V = rng.uniform(-bound, bound, (r, D)).astype(np.float32)
-        w = np.ones(r, dtype=np.float32)
-        g_ds = np.ones((B_sample, N), np.float32)
-        g_dv = np.ones((B_sample, N, D), np.float32)
-        times = []
-        with O.compute_dtype(np.float32):
-            for _ in range(3):
-                t0 = time.perf_counter()
-                O.propagation_forward(val, state, val, U, V, w, 0.0, mode="dense")
-                O.propagation_backward(val, state, val, U, V, w, 0.0, g_ds, g_dv, mode="dense")
-                times.append(time.perf_counter() - t0)
-        t = sorted(times)[len(times) // 2]
-        return {
-            "value": B_sample * N * N / t,
-            "unit": "routed pairs/s",
-            "cores": _threads() or os.cpu_count(),
-            "kind": "port",
-            "sample": f"numpy oracle fp32, dense forward+backward, {B_sample} of {self.config['batch']} batch "
-                      f"elements (N={N}, D={D}, r={r}), median of 3 ({t:.2f} s each)",
-        }
 
 
 class TransitionDenseC3:
@@ -507,59 +458,23 @@ class TransitionDenseC3:
         # dense: no gathers; the route matrices are the bytes that move
         return 4.0 * 6 * self.edges()
 
-    def build(self, torch, dev):
+    def build(self, torch, dev, impl: str = "native", batch: int | None = None):
         from jakal_net import Layer, LowRankBilinearRoute, Transition
 
         c = self.config
         B, S, Bn, D, r = (c[x] for x in ("batch", "s_nodes", "b_nodes", "dim", "rank"))
+        B = batch or B
         g = torch.Generator().manual_seed(1003)
         s_state, s_val = torch.randn(B, S, generator=g), torch.randn(B, S, D, generator=g)
         b_state, b_val = torch.randn(B, Bn, generator=g), torch.randn(B, Bn, D, generator=g)
         torch.manual_seed(1003)
-        s_to_b = Transition(LowRankBilinearRoute(D, D, rank=r), implementation="native").to(dev)
-        b_to_s = Transition(LowRankBilinearRoute(D, D, rank=r), implementation="native").to(dev)
+        s_to_b = Transition(LowRankBilinearRoute(D, D, rank=r), implementation=impl).to(dev)
+        b_to_s = Transition(LowRankBilinearRoute(D, D, rank=r), implementation=impl).to(dev)
         s_layer = Layer(dim=D, num_nodes=S, state=s_state.to(dev).requires_grad_(True),
                         val=s_val.to(dev).requires_grad_(True))
         b_layer = Layer(dim=D, num_nodes=Bn, state=b_state.to(dev).requires_grad_(True),
                         val=b_val.to(dev).requires_grad_(True))
         return _TwoWayTransition(torch, s_to_b, b_to_s, s_layer, b_layer), None
-
-    def cpu_baseline(self, B_sample: int = 1) -> dict:
-        """Oracle (numpy, fp32) dense forward+backward of both directions on B_sample batch elements."""
-        import numpy as np
-
-        O = _oracle()
-        c = self.config
-        S, Bn, D, r = (c[x] for x in ("s_nodes", "b_nodes", "dim", "rank"))
-        Bs = B_sample
-        rng = np.random.default_rng(1003)
-        bound = 1.0 / math.sqrt(D)
-        layers = {"S": (rng.standard_normal((Bs, S)), rng.standard_normal((Bs, S, D))),
-                  "B": (rng.standard_normal((Bs, Bn)), rng.standard_normal((Bs, Bn, D)))}
-        params = [rng.uniform(-bound, bound, (2, r, D)) for _ in range(2)]
-        times = []
-        with O.compute_dtype(np.float32):
-            for _ in range(3):
-                t0 = time.perf_counter()
-                for (src, dst), (Ws, Wt) in zip((("S", "B"), ("B", "S")), params):
-                    st, sv = layers[src]
-                    _, dv = layers[dst]
-                    rho = O.softplus(st)
-                    nd = dv.shape[1]
-                    mask = np.ones((Bs, sv.shape[1], nd), dtype=bool)
-                    O.transition_forward(sv, dv, rho, st, sv, Ws, Wt, np.ones(r), 0.0, topk=nd, mask=mask)
-                    O.transition_backward(sv, dv, rho, st, sv, Ws, Wt, np.ones(r), 0.0, np.ones((Bs, nd)),
-                                          np.ones((Bs, nd, D)), topk=nd, mask=mask)
-                times.append(time.perf_counter() - t0)
-        t = sorted(times)[len(times) // 2]
-        return {
-            "value": self.edges() // c["batch"] * Bs / t,
-            "unit": "routed pairs/s",
-            "cores": _threads() or os.cpu_count(),
-            "kind": "port",
-            "sample": f"numpy oracle fp32, dense forward+backward of both directions, {Bs} of {c['batch']} batch "
-                      f"elements (N_src=1024, N_dst=256, D={D}, r={r}), median of 3 ({t:.2f} s each)",
-        }
 
 
 class _TwoWayTransition:
@@ -630,23 +545,7 @@ def main() -> int:
     wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     op, layer = wl.build(torch, dev)
-    if layer is None:  # a multi-module step: op supplies its own loss terms
-        terms = op.loss_terms()
-        ones = [torch.ones_like(t) for t in terms]
-
-        def step() -> None:
-            op.zero_grad(set_to_none=True)
-            torch.autograd.backward(op.loss_terms(), ones)
-    else:
-        ones_s = torch.ones_like(layer.state)
-        ones_v = torch.ones_like(layer.val)
-
-        def step() -> None:
-            op.zero_grad(set_to_none=True)
-            layer.val.grad = None
-            layer.state.grad = None
-            delta = op(layer)
-            torch.autograd.backward([delta.delta_state, delta.delta_val], [ones_s, ones_v])
+    step = _make_step(torch, op, layer)
 
     for _ in range(args.warmup):
         step()
@@ -676,11 +575,15 @@ def main() -> int:
                  "ms_per_step": round(total_ms / args.steps, 5)}
         model = wl.model(name)
         if model is not None:
-            bound, work = model
+            bound, work = model[0], model[1]
             if bound == "hbm":
-                achieved = work / (avg_ms / 1e3) / 1e9
-                entry.update(bound="hbm", algorithmic_bytes=work, achieved_GBps=round(achieved, 1),
-                             frac=round(achieved / HBM_PEAK_GBS, 4))
+                # HBM roofline on compulsory bytes; the algorithmic (every operand
+                # once per use) rate is reported beside it as an L2-side figure
+                compulsory = model[2] if len(model) > 2 and model[2] is not None else work
+                achieved = compulsory / (avg_ms / 1e3) / 1e9
+                entry.update(bound="hbm", compulsory_bytes=compulsory, achieved_GBps=round(achieved, 1),
+                             frac=round(achieved / HBM_PEAK_GBS, 4), algorithmic_bytes=work,
+                             l2_side_GBps=round(work / (avg_ms / 1e3) / 1e9, 1))
             else:
                 achieved = work / (avg_ms / 1e3) / 1e12
                 entry.update(bound="mfma", flops=work, achieved_TFLOPs=round(achieved, 2),
@@ -740,7 +643,10 @@ def main() -> int:
         "wall_s_timed": round(wall, 3),
         "device": torch.cuda.get_device_name(0),
     }
-    result["cpu_baseline"] = None if args.no_cpu_baseline else wl.cpu_baseline()
+    if not args.no_cpu_baseline:
+        del op, layer, step
+        torch.cuda.empty_cache()
+    result["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline(wl, torch)
     print(json.dumps(result))
     return 0
 

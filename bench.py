@@ -163,8 +163,7 @@ def cpu_baseline(wl, torch) -> dict:
     saved = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
-        op, layer = wl.build(torch, torch.device("cpu"), impl="reference", batch=batch)
-        step = _make_step(torch, op, layer)
+        step = workload_step(wl, torch, torch.device("cpu"), impl="reference", batch=batch)
         step()
         times = []
         for _ in range(3):
@@ -177,7 +176,7 @@ def cpu_baseline(wl, torch) -> dict:
     what = "the whole workload" if batch == full else f"{batch} of its {full} batch elements"
     return {
         "value": wl.edges() * batch / full / t,
-        "unit": "routed pairs/s",
+        "unit": getattr(wl, "unit", "routed pairs/s"),
         "cores": threads,
         "kind": "port",
         "sample": f"{what} ({wl.workload.replace(', native', '')}) through implementation='reference' on "
@@ -496,7 +495,73 @@ class _TwoWayTransition:
         return [d1.delta_state, d1.delta_val, d2.delta_state, d2.delta_val]
 
 
-WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3(), DenseC4(), TransitionDenseC3())}
+class ProgressiveC5:
+    """the Progressive-B query-block training step
+    (jakal_net.progressive.ProgressiveBStep) -- prefix encoding through S
+    warmup windows, 4 joint blocks (expand, expanded top-k, B->S, compress,
+    S->B, compressed top-k) and S refine windows, then 64 teacher-forced query
+    slots refined by query transitions and causal dense query propagation,
+    the vocabulary head and the cross entropy -- forward, backward and an AdamW
+    update of the fp32 master weights, under bf16 autocast.  The unit is
+    processed tokens (prefix + query slots) per second."""
+
+    name = "c5-progressive-b"
+    metric = ("tokens/sec, Progressive-B query-block fwd+bwd+AdamW step (vocab 16384, d=512, prefix 512, "
+              "4 joint blocks, B_exp 256, B_cmp 64, top-k 16, rank 64, 64 query slots, batch 16), bf16 autocast")
+    workload = "C5 Progressive-B query-block training step (fwd+bwd+AdamW), LowRankBilinear operators, native"
+    data = "synthetic (uniform random token ids seeded 1005, random init, fp32 master weights)"
+    unit = "tokens/s"
+    dtype = "bf16 autocast (fp32 master weights; the hot-path ops compute in fp32)"
+    config = {"batch": 16, "vocab": 16384, "dim": 512, "prefix": 512, "query": 64, "rank": 64, "topk": 16,
+              "blocks": 4, "expanded": 256, "compressed": 64, "s_window": 32}
+    traffic_file = "c5_progressive_b_hbm_traffic.json"
+    cpu_batch = 2
+
+    def edges(self) -> int:  # tokens per step
+        c = self.config
+        return c["batch"] * (c["prefix"] + c["query"])
+
+    def model(self, name):
+        return None  # an end-to-end step: no single roofline (BASELINE.md)
+
+    def sparse_bytes(self):
+        return None
+
+    def make_step(self, torch, dev, impl: str = "native", batch: int | None = None):
+        from jakal_net.progressive import ProgressiveBConfig, ProgressiveBStep
+
+        c = self.config
+        B = batch or c["batch"]
+        cfg = ProgressiveBConfig(vocab=c["vocab"], dim=c["dim"], prefix=c["prefix"], query=c["query"],
+                                 rank=c["rank"], topk=c["topk"], blocks=c["blocks"], expanded=c["expanded"],
+                                 compressed=c["compressed"], s_window=c["s_window"])
+        torch.manual_seed(1005)
+        model = ProgressiveBStep(cfg, implementation=impl).to(dev)
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+        g = torch.Generator().manual_seed(1005)
+        prefix = torch.randint(0, c["vocab"] - 1, (B, c["prefix"]), generator=g).to(dev)
+        target = torch.randint(0, c["vocab"] - 1, (B, c["query"]), generator=g).to(dev)
+        use_autocast = dev.type == "cuda"  # the CPU baseline runs fp32
+
+        def step() -> None:
+            opt.zero_grad(set_to_none=True)
+            with torch.autocast(device_type=dev.type, dtype=torch.bfloat16, enabled=use_autocast):
+                loss = model(prefix, target)
+            loss.backward()
+            opt.step()
+        return step
+
+
+WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3(), DenseC4(), TransitionDenseC3(),
+                                 ProgressiveC5())}
+
+
+def workload_step(wl, torch, dev, impl: str = "native", batch: int | None = None):
+    """The timed step of a workload: its own make_step, or forward+backward of its operator."""
+    if hasattr(wl, "make_step"):
+        return wl.make_step(torch, dev, impl, batch)
+    op, layer = wl.build(torch, dev, impl=impl, batch=batch)
+    return _make_step(torch, op, layer)
 
 COPY_BYTES = 1 << 30
 
@@ -544,8 +609,7 @@ def main() -> int:
     jn.set_select_mode(jn.SELECT_SPLIT_F16 if args.select_mode == "split-f16" else jn.SELECT_F32)
     wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
-    op, layer = wl.build(torch, dev)
-    step = _make_step(torch, op, layer)
+    step = workload_step(wl, torch, dev)
 
     for _ in range(args.warmup):
         step()
@@ -612,8 +676,12 @@ def main() -> int:
             entry["traffic_GBps"] = round(measured[name]["traffic_bytes"] / (entry["avg_ms"] / 1e3) / 1e9, 1)
 
     modeled = [(n, e) for n, e in kernels.items() if "bound" in e]
-    dom_name, dom = max(modeled, key=lambda ne: ne[1]["ms_per_step"])
-    if dom["bound"] == "hbm":
+    dom_name, dom = max(modeled or list(kernels.items()), key=lambda ne: ne[1]["ms_per_step"])
+    if not modeled:  # an end-to-end step: the hottest kernel, without a roofline
+        roofline = {"kernel": dom_name, "bound": None, "achieved": None, "peak": None, "unit": None, "frac": None,
+                    "traffic": dom.get("traffic_bytes"),
+                    "note": "end-to-end step of many small operators; per-kernel figures under 'kernels'"}
+    elif dom["bound"] == "hbm":
         roofline = {"kernel": dom_name, "bound": "hbm", "achieved": dom["achieved_GBps"], "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": dom["frac"], "traffic": dom.get("traffic_bytes")}
     else:
@@ -626,7 +694,7 @@ def main() -> int:
     result = {
         "metric": wl.metric,
         "value": value,
-        "unit": "routed pairs/s",
+        "unit": getattr(wl, "unit", "routed pairs/s"),
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -634,17 +702,18 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": getattr(wl, "dtype", "f32"),
         "data": wl.data,
         "config": {"workload": wl.workload, **wl.config},
-        "sparse_phase_GBps": round(wl.sparse_bytes() / (ms_per_step / 1e3) / 1e9, 1),
+        "sparse_phase_GBps": (None if wl.sparse_bytes() is None
+                              else round(wl.sparse_bytes() / (ms_per_step / 1e3) / 1e9, 1)),
         "roofline": roofline,
         "kernels": kernels,
         "wall_s_timed": round(wall, 3),
         "device": torch.cuda.get_device_name(0),
     }
     if not args.no_cpu_baseline:
-        del op, layer, step
+        del step
         torch.cuda.empty_cache()
     result["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline(wl, torch)
     print(json.dumps(result))

@@ -310,3 +310,35 @@ def test_cpu_tensors_in_native_mode_run_streaming_without_a_cpu_module():
     ref, _ = _topk_case("reference")
     ref.pairwise_fn.load_state_dict(op.pairwise_fn.state_dict())
     assert torch.allclose(op(layer).delta_val, ref(layer).delta_val)
+
+
+# ---------------------------------------------------------------------------
+# the Progressive-B query-block step (a caller of the hot path)
+# ---------------------------------------------------------------------------
+def _small_progressive():
+    from jakal_net.progressive import ProgressiveBConfig
+
+    return ProgressiveBConfig(vocab=97, dim=32, prefix=48, query=8, rank=8, topk=4, s_window=6, warmup=1,
+                              blocks=2, expanded=24, compressed=8, refine=1, query_refine=2)
+
+
+def test_progressive_step_matches_oracle_composition():
+    import progressive_oracle as PO
+    from jakal_net.progressive import ProgressiveBStep
+
+    cfg = _small_progressive()
+    torch.manual_seed(21)
+    model = ProgressiveBStep(cfg, implementation="reference")
+    g = torch.Generator().manual_seed(22)
+    prefix = torch.randint(0, cfg.vocab - 1, (2, cfg.prefix), generator=g)
+    target = torch.randint(0, cfg.vocab - 1, (2, cfg.query), generator=g)
+    logits = model.query_logits(model.encode_prefix(prefix), target)
+    params = {k: v.detach().numpy() for k, v in model.state_dict().items()}
+    want = PO.progressive_logits(params, cfg, prefix.numpy(), target.numpy())
+    np.testing.assert_allclose(_np(logits), want, rtol=1e-9, atol=1e-10)
+    loss = float(model(prefix, target).detach())
+    assert loss == pytest.approx(PO.cross_entropy(want, target.numpy()), rel=1e-10)
+    # the streaming forms give the same step
+    stream = ProgressiveBStep(cfg, implementation="streaming")
+    stream.load_state_dict(model.state_dict())
+    assert float(stream(prefix, target).detach()) == pytest.approx(loss, rel=1e-10)

@@ -1,0 +1,118 @@
+"""The Progressive-B query-block step (jakal_net.progressive) with every
+operator on the HIP library, on a reduced configuration.
+
+* the logits and loss of the native step (fp32) against the composition of
+  oracle calls (tests/progressive_oracle.py, float64 numpy);
+* the gradient of every parameter against the same step run through the
+  operators' implementation="reference" backend in float64 on the CPU (the
+  reference backend is pinned to the oracle by tests/test_api_cpu.py), each
+  within the literal fp32 tolerance or twice the error of that backend run in
+  fp32 on the GPU (tests/parity.py);
+* the step under bf16 autocast (bf16 activations, fp32 master weights, as
+  BASELINE config 5 runs) against the float64 logits at the bf16 tolerance.
+
+Reference composition: scripts/progressive_b_example.py:1108-1323, 1957-2021,
+2059-2152.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import progressive_oracle as PO
+from parity import check, np64
+
+pytestmark = pytest.mark.gpu
+
+
+def _cfg():
+    from jakal_net.progressive import ProgressiveBConfig
+
+    return ProgressiveBConfig(vocab=97, dim=32, prefix=48, query=8, rank=8, topk=4, s_window=6, warmup=1,
+                              blocks=2, expanded=24, compressed=8, refine=1, query_refine=2)
+
+
+def _models_and_batch(seed=21):
+    from jakal_net.progressive import ProgressiveBStep
+
+    cfg = _cfg()
+    torch.manual_seed(seed)
+    native = ProgressiveBStep(cfg, implementation="native")
+    g = torch.Generator().manual_seed(seed + 1)
+    prefix = torch.randint(0, cfg.vocab - 1, (2, cfg.prefix), generator=g)
+    target = torch.randint(0, cfg.vocab - 1, (2, cfg.query), generator=g)
+    return cfg, native, prefix, target
+
+
+def _unused(model):
+    """Parameters outside the loss: the last block's updates of B_cmp (compress, S -> B_cmp, its top-k
+    propagation and norm) feed only the next block, as in the reference's query-block step."""
+    last = f"blocks.{model.cfg.blocks - 1}."
+    return {n for n, _ in model.named_parameters()
+            if n.startswith(tuple(last + m for m in ("compress.", "s_to_b.", "cmp_prop.", "cmp_norm.")))}
+
+
+def _grads(model, prefix, target):
+    model.zero_grad(set_to_none=True)
+    loss = model(prefix, target)
+    loss.backward()
+    return float(loss.detach()), {n: p.grad for n, p in model.named_parameters() if p.grad is not None}
+
+
+def test_progressive_step_native_matches_oracle_and_reference():
+    from jakal_net.progressive import ProgressiveBStep
+
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import jakal_net_native  # noqa: F401  (fails loudly when the library is missing)
+
+    dev = torch.device("cuda:0")
+    cfg, native, prefix, target = _models_and_batch()
+    ref64 = ProgressiveBStep(cfg, implementation="reference").double()
+    ref64.load_state_dict(native.state_dict())
+    ref32 = ProgressiveBStep(cfg, implementation="reference").to(dev)
+    ref32.load_state_dict(native.state_dict())
+    native = native.to(dev)
+
+    with torch.no_grad():
+        logits = native.query_logits(native.encode_prefix(prefix.to(dev)), target.to(dev))
+        logits32 = ref32.query_logits(ref32.encode_prefix(prefix.to(dev)), target.to(dev))
+    params = {k: v.detach().double().cpu().numpy() for k, v in native.state_dict().items()}
+    want = PO.progressive_logits(params, cfg, prefix.numpy(), target.numpy())
+    check("C5 logits vs oracle composition", logits, want, logits32)
+
+    loss_n, g_n = _grads(native, prefix.to(dev), target.to(dev))
+    loss_64, g_64 = _grads(ref64, prefix, target)
+    loss_32, g_32 = _grads(ref32, prefix.to(dev), target.to(dev))
+    check("C5 loss", np.array([loss_n]), np.array([PO.cross_entropy(want, target.numpy())]))
+    assert abs(loss_64 - PO.cross_entropy(want, target.numpy())) < 1e-9
+    assert set(g_n) == set(g_64), "the native and reference steps differ in which parameters get gradients"
+    assert _unused(native) == {n for n, _ in native.named_parameters()} - set(g_n)
+    for name in sorted(g_64):
+        check(f"C5 grad {name}", g_n[name], g_64[name], g_32[name])
+
+
+def test_progressive_step_bf16_autocast():
+    from jakal_net.progressive import ProgressiveBStep
+
+    dev = torch.device("cuda:0")
+    cfg, native, prefix, target = _models_and_batch(seed=31)
+    ref64 = ProgressiveBStep(cfg, implementation="reference").double()
+    ref64.load_state_dict(native.state_dict())
+    native = native.to(dev)
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        loss = native(prefix.to(dev), target.to(dev))
+        logits = native.query_logits(native.encode_prefix(prefix.to(dev)), target.to(dev))
+    loss.backward()
+    got = {n for n, p in native.named_parameters() if p.grad is not None}
+    assert got == {n for n, _ in native.named_parameters()} - _unused(native)
+    assert all(bool(torch.isfinite(p.grad).all()) for p in native.parameters() if p.grad is not None)
+    with torch.no_grad():
+        want = ref64.query_logits(ref64.encode_prefix(prefix), target)
+    # the logits carry the bf16 rounding of the linear layers' inputs and weights
+    # (fp32 accumulation): within the bf16 tolerance 2e-2, norm-wise
+    err = float(np.abs(np64(logits) - np64(want)).max())
+    scale = float(np.abs(np64(want)).max())
+    print(f"C5 bf16 autocast: max|logits - f64| {err:.3e} of max|logit| {scale:.3e}", flush=True)
+    assert err <= 2e-2 * scale
+    want_loss = float(ref64(prefix, target).detach())
+    assert abs(float(loss) - want_loss) <= 2e-2 * abs(want_loss)

@@ -417,6 +417,46 @@ class DenseC4:
                          val=val.to(dev).requires_grad_(True))
 
 
+class DenseCausalC4(DenseC4):
+    """C4 shapes with a full causal window (window = N - 1): row i keeps the
+    sources j <= i (the causal dense query propagation of
+    scripts/progressive_b_example.py:1977-2012, at the C4 size).  The library
+    runs it on the dense path with causal K ranges; the algorithmic work is
+    the causal half of every N x N product."""
+
+    name = "c4-dense-causal"
+    metric = "routed pairs/sec + MFMA TFLOP/s (% peak), Propagation causal dense N=4096 D=512 r=64 fwd+bwd"
+    workload = "C4-dense causal (window N-1) SparsePropagation fwd+bwd, LowRankBilinearPairwise, softsign, native"
+    traffic_file = "c4_dense_causal_hbm_traffic.json"
+
+    def edges(self) -> int:
+        c = self.config
+        return c["batch"] * c["nodes"] * (c["nodes"] + 1) // 2
+
+    def model(self, name):
+        m = super().model(name)
+        if m is not None and m[0] == "mfma" and name.startswith("gemm_f32_kernel<dense_"):
+            c = self.config
+            N = c["nodes"]
+            return m[0], m[1] * (N + 1) / (2 * N), None  # the causal half of the N x N products
+        return m
+
+    def build(self, torch, dev, impl: str = "native", batch: int | None = None):
+        from jakal_net import Layer, LowRankBilinearPairwise, SparsePropagation
+
+        B, N, D, r = (self.config[x] for x in ("batch", "nodes", "dim", "rank"))
+        B = batch or B
+        g = torch.Generator().manual_seed(1004)
+        state = torch.randn(B, N, generator=g)
+        val = torch.randn(B, N, D, generator=g)
+        val = val / val.norm(dim=-1, keepdim=True)
+        torch.manual_seed(1004)
+        op = SparsePropagation(LowRankBilinearPairwise(D, r), sparse_type="window", window=N - 1,
+                               implementation=impl).to(dev)
+        return op, Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True),
+                         val=val.to(dev).requires_grad_(True))
+
+
 class TransitionDenseC3:
     name = "c3-transition-dense"
     metric = "routed pairs/sec + MFMA TFLOP/s (% peak), Transition (dense) S->B and B->S N_src=1024 N_dst=256 D=512 fwd+bwd"
@@ -552,8 +592,8 @@ class ProgressiveC5:
         return step
 
 
-WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3(), DenseC4(), TransitionDenseC3(),
-                                 ProgressiveC5())}
+WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3(), DenseC4(), DenseCausalC4(),
+                                 TransitionDenseC3(), ProgressiveC5())}
 
 
 def workload_step(wl, torch, dev, impl: str = "native", batch: int | None = None):

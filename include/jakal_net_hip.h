@@ -30,7 +30,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 3. */
+/* ABI revision of this header (bumped on any signature change); this is 4. */
 int jn_abi_version(void);
 
 /*
@@ -226,22 +226,31 @@ int jn_propagation_dense_forward(const float* layer_val, const float* projected_
                                  int64_t rank, int32_t compress_kind, int32_t causal, float* delta_state,
                                  float* delta_val, float* projections, float* edges, jn_stream_t stream);
 
-/* Workspace needed by jn_propagation_dense_backward (holds one [B,N,N] matrix). */
+/*
+ * Workspace needed by jn_propagation_dense_backward: one [B,N,N] matrix for
+ * the score gradient, except for softsign (compress_kind 0) with
+ * reuse_edges != 0, where that gradient overwrites the edge matrix (a few MB
+ * of row partials and projection gradients remain).
+ */
 size_t jn_propagation_dense_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
-                                            int64_t rank);
+                                            int64_t rank, int32_t compress_kind, int32_t reuse_edges);
 
 /*
  * Backward of jn_propagation_dense_forward; arguments as
  * jn_propagation_topk_backward with the edge matrix in place of the edge list.
+ * reuse_edges != 0 lets a softsign backward write the score gradient over
+ * `edges` (the edge matrix is then consumed: a second backward needs the
+ * forward again); otherwise `edges` is only read.  In causal mode the
+ * products over the edge matrix skip its zero upper triangle.
  * The reference differentiates its composite dense op with autograd
  * (native/jakal_net_native.cpp:5962-6076 has no custom backward).
  */
 int jn_propagation_dense_backward(const float* layer_val, const float* projected_state, const float* projected_val,
                                   const float* target_weight, const float* source_weight, const float* core_weight,
-                                  const float* projections, const float* edges, const float* grad_delta_state,
+                                  const float* projections, float* edges, const float* grad_delta_state,
                                   const float* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim,
                                   int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
-                                  int32_t projected_val_is_layer_val, float* grad_layer_val,
+                                  int32_t projected_val_is_layer_val, int32_t reuse_edges, float* grad_layer_val,
                                   float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
                                   float* grad_source_weight, float* grad_core_weight, float* grad_bias,
                                   void* workspace, size_t workspace_bytes, jn_stream_t stream);

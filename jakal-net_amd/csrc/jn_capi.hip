@@ -196,7 +196,7 @@ int check_transition_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t Dsrc,
 }
 
 struct DenseScratch {
-  float* G;       // [B, N, N] score gradient
+  float* G;       // [B, N, N] score gradient (absent when it overwrites the edge matrix)
   float* dP;      // [M, 2r]
   float* rowsum;  // [M]
   float* part_c;  // [M, r]
@@ -205,11 +205,11 @@ struct DenseScratch {
   size_t bytes;
 };
 
-DenseScratch carve_dense(void* base, size_t size, int64_t B, int64_t N, int64_t Din, int64_t r) {
+DenseScratch carve_dense(void* base, size_t size, int64_t B, int64_t N, int64_t Din, int64_t r, bool with_g) {
   Workspace ws(base, size);
   DenseScratch s{};
   const int64_t M = B * N;
-  s.G = ws.take<float>(B * N * N);
+  s.G = with_g ? ws.take<float>(B * N * N) : nullptr;
   s.dP = ws.take<float>(M * 2 * r);
   s.rowsum = ws.take<float>(M * dense_epi_parts((int)N));  // per-row totals, or the epilogue's block partials
   s.part_c = ws.take<float>(M * r);
@@ -399,7 +399,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 3; }
+int jn_abi_version(void) { return 4; }
 
 int jn_profile_enable(int32_t on) {
   std::lock_guard<std::mutex> lock(jakal::g_prof_mu);
@@ -942,22 +942,23 @@ int jn_propagation_dense_forward(const float* layer_val, const float* projected_
   ag.B = projected_val; ag.ldb = D; ag.b_bs = (int64_t)N * D; ag.b_kcontig = false;
   ag.C = delta_val; ag.ldc = D; ag.c_bs = (int64_t)N * D;
   ag.M = N; ag.N = D; ag.K = N; ag.batch = B;
+  ag.causal_k = causal ? kCausalKLower : kCausalKNone;  // row i reads sources j <= i
   return gemm_batched(ag, kGemmDenseAggregate, st);
 }
 
 size_t jn_propagation_dense_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
-                                            int64_t rank) {
+                                            int64_t rank, int32_t compress_kind, int32_t reuse_edges) {
   (void)out_dim;
   if (batch < 1 || nodes < 1 || rank < 1) return 0;
-  return carve_dense(nullptr, 0, batch, nodes, in_dim, rank).bytes;
+  return carve_dense(nullptr, 0, batch, nodes, in_dim, rank, !(compress_kind == 0 && reuse_edges != 0)).bytes;
 }
 
 int jn_propagation_dense_backward(const float* layer_val, const float* projected_state, const float* projected_val,
                                   const float* target_weight, const float* source_weight, const float* core_weight,
-                                  const float* projections, const float* edges, const float* grad_delta_state,
+                                  const float* projections, float* edges, const float* grad_delta_state,
                                   const float* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim,
                                   int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
-                                  int32_t projected_val_is_layer_val, float* grad_layer_val,
+                                  int32_t projected_val_is_layer_val, int32_t reuse_edges, float* grad_layer_val,
                                   float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
                                   float* grad_source_weight, float* grad_core_weight, float* grad_bias,
                                   void* workspace, size_t workspace_bytes, jn_stream_t stream) {
@@ -968,36 +969,22 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
              kInvalidArgument, "null tensor pointer");
   JN_REQUIRE(!projected_val_is_layer_val || in_dim == out_dim, kInvalidArgument,
              "projected_val_is_layer_val requires in_dim == out_dim");
-  DenseScratch s = carve_dense(workspace, workspace_bytes, batch, nodes, in_dim, rank);
+  // softsign's derivative runs in the score-gradient GEMM's epilogue, which
+  // reads each edge once before writing its gradient: with reuse_edges that
+  // gradient overwrites the edge matrix and no [B, N, N] workspace is needed
+  const bool fused = compress_kind == 0;
+  const bool in_place = fused && reuse_edges != 0;
+  DenseScratch s = carve_dense(workspace, workspace_bytes, batch, nodes, in_dim, rank, !in_place);
   JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
              "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int B = (int)batch, N = (int)nodes, r = (int)rank, D = (int)out_dim;
   const int M = B * N;
+  float* G = in_place ? edges : s.G;
+  const int lower = causal ? kCausalKLower : kCausalKNone;  // A(i, j) = 0 for j > i
+  const int upper = causal ? kCausalKUpper : kCausalKNone;  // A = E^T: A(j, i) = 0 for i < j
 
-  // 1. G_b = gdv_b pv_b^T, then the score gradient in place (+ row sums)
-  BatchedGemm gg{};
-  gg.A = grad_delta_val; gg.lda = D; gg.a_bs = (int64_t)N * D; gg.a_kcontig = true;
-  gg.B = projected_val; gg.ldb = D; gg.b_bs = (int64_t)N * D; gg.b_kcontig = true;
-  gg.C = s.G; gg.ldc = N; gg.c_bs = (int64_t)N * N;
-  gg.M = N; gg.N = N; gg.K = D; gg.batch = B;
-  // softsign's derivative runs in the GEMM's epilogue (row-block partials of
-  // the bias gradient into s.rowsum); the row-wise compressions afterwards
-  const bool fused = compress_kind == 0;
-  if (fused) {
-    gg.epi = 1; gg.epi_causal = causal != 0; gg.epi_ps = projected_state; gg.epi_gds = grad_delta_state;
-    gg.epi_E = edges; gg.epi_part = s.rowsum;
-  }
-  rc = gemm_batched(gg, kGemmDenseEdgeGrad, st);
-  if (rc) return rc;
-  if (!fused) {
-    rc = launch_dense_compress_backward(s.G, edges, grad_delta_state, projected_state, B, N, compress_kind,
-                                        causal != 0, s.rowsum, st);
-    if (rc) return rc;
-  }
-  const int64_t n_rowsum = fused ? (int64_t)M * dense_epi_parts(N) : M;
-
-  // 2. value and state grads of the sources: E^T gdv, E^T gds
+  // 1. value and state grads of the sources: E^T gdv, E^T gds (before E is overwritten)
   float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
   if (gpv) {
     BatchedGemm vg{};
@@ -1005,6 +992,7 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
     vg.B = grad_delta_val; vg.ldb = D; vg.b_bs = (int64_t)N * D; vg.b_kcontig = false;
     vg.C = gpv; vg.ldc = D; vg.c_bs = (int64_t)N * D;
     vg.M = N; vg.N = D; vg.K = N; vg.batch = B;
+    vg.causal_k = upper;
     rc = gemm_batched(vg, kGemmDenseValueGrad, st);
     if (rc) return rc;
   }
@@ -1013,20 +1001,41 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
     if (rc) return rc;
   }
 
+  // 2. G_b = gdv_b pv_b^T, then the score gradient (+ row sums)
+  BatchedGemm gg{};
+  gg.A = grad_delta_val; gg.lda = D; gg.a_bs = (int64_t)N * D; gg.a_kcontig = true;
+  gg.B = projected_val; gg.ldb = D; gg.b_bs = (int64_t)N * D; gg.b_kcontig = true;
+  gg.C = G; gg.ldc = N; gg.c_bs = (int64_t)N * N;
+  gg.M = N; gg.N = N; gg.K = D; gg.batch = B;
+  if (fused) {
+    gg.epi = 1; gg.epi_causal = causal != 0; gg.epi_ps = projected_state; gg.epi_gds = grad_delta_state;
+    gg.epi_E = edges; gg.epi_part = s.rowsum;
+  }
+  rc = gemm_batched(gg, kGemmDenseEdgeGrad, st);
+  if (rc) return rc;
+  if (!fused) {
+    rc = launch_dense_compress_backward(G, edges, grad_delta_state, projected_state, B, N, compress_kind,
+                                        causal != 0, s.rowsum, st);
+    if (rc) return rc;
+  }
+  const int64_t n_rowsum = fused ? (int64_t)M * dense_epi_parts(N) : M;
+
   // 3. projection grads: dP_t = w_hat * (G_s P_s), dP_s = w_hat * (G_s^T P_t) (+ w_hat partials)
   BatchedGemm tg{};
-  tg.A = s.G; tg.lda = N; tg.a_bs = (int64_t)N * N; tg.a_kcontig = true;
+  tg.A = G; tg.lda = N; tg.a_bs = (int64_t)N * N; tg.a_kcontig = true;
   tg.B = projections + r; tg.ldb = 2 * r; tg.b_bs = (int64_t)N * 2 * r; tg.b_kcontig = false;
   tg.C = s.dP; tg.ldc = 2 * r; tg.c_bs = (int64_t)N * 2 * r;
   tg.c_nscale = core_weight;
   tg.M = N; tg.N = r; tg.K = N; tg.batch = B;
+  tg.causal_k = lower;
   rc = gemm_batched(tg, kGemmDenseTargetGrad, st);
   if (rc) return rc;
   BatchedGemm sg2{};
-  sg2.A = s.G; sg2.lda = N; sg2.a_bs = (int64_t)N * N; sg2.a_kcontig = false;
+  sg2.A = G; sg2.lda = N; sg2.a_bs = (int64_t)N * N; sg2.a_kcontig = false;
   sg2.B = projections; sg2.ldb = 2 * r; sg2.b_bs = (int64_t)N * 2 * r; sg2.b_kcontig = false;
   sg2.C = s.dP + r; sg2.ldc = 2 * r; sg2.c_bs = (int64_t)N * 2 * r;
   sg2.M = N; sg2.N = r; sg2.K = N; sg2.batch = B;
+  sg2.causal_k = upper;
   rc = gemm_batched(sg2, kGemmDenseSourceGrad, st);
   if (rc) return rc;
   rc = launch_scale_grad_partials(s.dP + r, 2 * r, projections + r, 2 * r, core_weight, r, M, s.part_c, st);

@@ -48,7 +48,8 @@ struct GemmArgs {
   // with C = 0 where a causal row does not keep source n (n > m).  part holds
   // one sum per row and 32-column block: epi_part[(b M + m) P + n / 32], P =
   // ceil(N / 32), each written once, in a fixed order.
-  int epi, epi_causal;
+  int epi, epi_causal;     // epi_causal: also skips the K loop of tiles wholly above the diagonal
+  int causal_k;            // kCausalK*: per-tile K range of a causal square product (BatchedGemm)
   const float* epi_bias;   // scalar or null
   const float* epi_ps;     // [batch, N]
   const float* epi_gds;    // [batch, M]
@@ -121,6 +122,18 @@ __device__ __forceinline__ void dense_epilogue_tiles(const GemmArgs& g, int64_t 
 
 constexpr int kGBM = 64, kGBK = 16, kGStride = kGBK + 4;
 
+// The K range [kbeg, kend) of the output tile whose rows start at m0 (TILE rows,
+// columns from n0): a causal product reads only the k its rows can reach, and a
+// causal softsign epilogue tile wholly above the diagonal needs no products at
+// all (it stores zeros).  m0 is a multiple of TILE, so the bounds stay float4
+// aligned.
+template <int TILE>
+__device__ __forceinline__ void causal_k_range(const GemmArgs& g, int m0, int n0, int& kbeg, int& kend) {
+  if (g.causal_k == kCausalKLower) kend = min(kend, m0 + TILE);
+  else if (g.causal_k == kCausalKUpper) kbeg = max(kbeg, m0);
+  if (g.epi && g.epi_causal && n0 > m0 + TILE - 1) kend = kbeg;
+}
+
 __device__ __forceinline__ bool aligned16(const float* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // A(m,k): A_KC -> A[m*lda + k] else A[k*lda + m]
@@ -148,8 +161,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
   const bool batched = g.batch > 1;
   const int split = batched ? 0 : blockIdx.z;
   const int64_t bz = batched ? blockIdx.z : 0;
-  const int kbeg = split * g.k_chunk;
-  const int kend = min(g.K, kbeg + g.k_chunk);
+  int kbeg = split * g.k_chunk;
+  int kend = min(g.K, kbeg + g.k_chunk);
+  causal_k_range<TILE>(g, m0, n0, kbeg, kend);
   const float* gA = g.A + bz * g.a_bs;
   const float* gB0 = g.B0 + bz * g.b_bs;
   const float* gB1 = g.B1 + bz * g.b_bs;
@@ -258,7 +272,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
       for (int c = 0; c < 3; ++c) chain[c][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
 
-  const int nslices = (kend - kbeg + kGBK - 1) / kGBK;
+  const int nslices = kend > kbeg ? (kend - kbeg + kGBK - 1) / kGBK : 0;
   if (nslices > 0) {
     load_slice(kbeg);
     store_slice(0);
@@ -416,14 +430,21 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
   const int band = t / (kBand * tiles_n);
   const int bm = min(kBand, tiles_m - band * kBand);
   const int tb = t - band * kBand * tiles_n;
-  const int m0 = (band * kBand + tb % bm) * kFT;
+  int mi = band * kBand + tb % bm;
+  // A causal product's tiles of rows differ in work: with kCausalKLower (and
+  // score tiles above the diagonal skipped) the work grows with the row, so
+  // the rows run last to first -- longest first, the short tiles fill the
+  // tail.  kCausalKUpper tiles already come longest first.
+  if (g.causal_k == kCausalKLower || (g.epi && g.epi_causal)) mi = tiles_m - 1 - mi;
+  const int m0 = mi * kFT;
   const int n0 = (tb / bm) * kFT;
 
   const bool batched = g.batch > 1;
   const int split = batched ? 0 : z;
   const int64_t bz = batched ? z : 0;
-  const int kbeg = split * g.k_chunk;
-  const int kend = min(g.K, kbeg + g.k_chunk);
+  int kbeg = split * g.k_chunk;
+  int kend = min(g.K, kbeg + g.k_chunk);
+  causal_k_range<kFT>(g, m0, n0, kbeg, kend);
   const float* gA = g.A + bz * g.a_bs;
   const float* gB0 = g.B0 + bz * g.b_bs;
   const float* gB1 = g.B1 + bz * g.b_bs;
@@ -512,7 +533,7 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int nslices = (kend - kbeg + BK - 1) / BK;
+  const int nslices = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
   if (nslices > 0) {
     load_slice(kbeg);
     store_slice(0);
@@ -757,6 +778,10 @@ int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
   g.a_kscale = m.a_kscale; g.ks_bs = m.ks_bs;
   g.c_nscale = m.c_nscale;
   g.c_mscale = m.c_mscale; g.ms_bs = m.ms_bs;
+  JN_REQUIRE(m.causal_k == kCausalKNone || (m.causal_k == kCausalKLower && m.M == m.K) ||
+                 (m.causal_k == kCausalKUpper && m.M == m.K),
+             kInvalidArgument, "a causal K range needs a square A over one element's nodes");
+  g.causal_k = m.causal_k;
   if (m.epi) {
     JN_REQUIRE((use == kGemmDenseScores || use == kGemmDenseEdgeGrad) && m.M == m.N && m.epi_ps && m.epi_part &&
                    (use == kGemmDenseScores || (m.epi_gds && m.epi_E)) && m.addend == nullptr &&

@@ -69,6 +69,12 @@ struct BatchedGemm {
   const float* c_nscale;
   const float* c_mscale; int64_t ms_bs;  // optional: C(m, n) *= c_mscale[m], per batch element at stride ms_bs
   int M, N, K, batch;
+  // Causal structure of a square dense product (M == K or N == K over one
+  // batch element's nodes): kCausalKLower when A(m, k) = 0 for k > m (each
+  // tile of rows stops its K loop after its last row), kCausalKUpper when
+  // A(m, k) = 0 for k < m (it starts at its first row).  Skipped terms are
+  // exact zeros of the causal edge matrix, so results do not change.
+  int causal_k;
   // softsign epilogue of kGemmDenseScores / kGemmDenseEdgeGrad (M == N): see
   // GemmArgs in jn_gemm.hip; part is [batch, M, dense_epi_parts(N)]
   int epi, epi_causal;
@@ -78,6 +84,7 @@ struct BatchedGemm {
   const float* epi_E;
   float* epi_part;
 };
+constexpr int kCausalKNone = 0, kCausalKLower = 1, kCausalKUpper = 2;
 // Partial sums per row that the dense softsign epilogue writes (32 columns each).
 inline int dense_epi_parts(int n) { return (n + 31) / 32; }
 enum GemmUse {

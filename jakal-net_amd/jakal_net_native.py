@@ -104,10 +104,10 @@ _declare(
     "jn_propagation_dense_forward",
     [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P, _P],
 )
-_declare("jn_propagation_dense_workspace_bytes", [_I64] * 5, _SZ)
+_declare("jn_propagation_dense_workspace_bytes", [_I64] * 5 + [_I32, _I32], _SZ)
 _declare(
     "jn_propagation_dense_backward",
-    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32,
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32,
      _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 
@@ -360,12 +360,20 @@ class _PropagationDense(torch.autograd.Function):
             )
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, edges)
         ctx.meta = (compress, pv_is_x, bias is not None, bool(causal))
+        ctx.edges_consumed = False
         return ds, dv
 
     @staticmethod
     def backward(ctx, g_ds, g_dv):
         X, ps, pv, V, U, w_hat, proj, edges = ctx.saved_tensors
         compress, pv_is_x, has_bias, causal = ctx.meta
+        # a softsign backward writes the score gradient over the saved edge
+        # matrix (no [B, N, N] workspace); it can therefore run once per forward
+        if ctx.edges_consumed:
+            raise RuntimeError("the dense propagation backward consumed its saved edge matrix; run the forward "
+                               "again instead of back-propagating through it twice (retain_graph).")
+        reuse = 1 if compress == 0 else 0
+        ctx.edges_consumed = bool(reuse)
         B, N, Din = X.shape
         Dout = pv.shape[-1]
         r = U.shape[0]
@@ -379,13 +387,13 @@ class _PropagationDense(torch.autograd.Function):
             gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
             gV, gU, gw = torch.empty_like(V), torch.empty_like(U), torch.empty_like(w_hat)
             gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
-            ws_bytes = int(_LIB.jn_propagation_dense_workspace_bytes(B, N, Din, Dout, r))
+            ws_bytes = int(_LIB.jn_propagation_dense_workspace_bytes(B, N, Din, Dout, r, compress, reuse))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
             _check(
                 _LIB.jn_propagation_dense_backward(
                     _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(proj), _ptr(edges),
                     _ptr(g_ds), _ptr(g_dv), B, N, Din, Dout, r, compress, 1 if causal else 0, 1 if pv_is_x else 0,
-                    _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
+                    reuse, _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
                     _ptr(ws), ws_bytes, _stream(dev),
                 )
             )

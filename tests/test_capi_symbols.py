@@ -76,3 +76,18 @@ def test_select_workspace_is_mode_independent_without_gpu():
         assert lib.jn_set_select_mode(7) != 0
     finally:
         lib.jn_set_select_mode(0)
+
+
+def test_dense_backward_workspace_without_the_score_matrix():
+    """A softsign dense backward that may overwrite the edge matrix needs no
+    [B, N, N] workspace; the row-normalising kinds (and softsign without
+    reuse) keep one."""
+    lib = ctypes.CDLL(str(LIB))
+    I64, I32 = ctypes.c_int64, ctypes.c_int32
+    ws = lib.jn_propagation_dense_workspace_bytes
+    ws.argtypes = [I64] * 5 + [I32, I32]
+    ws.restype = ctypes.c_size_t
+    square = 16 * 4096 * 4096 * 4
+    assert ws(16, 4096, 512, 512, 64, 0, 1) < 100 << 20
+    assert ws(16, 4096, 512, 512, 64, 0, 0) > square
+    assert ws(16, 4096, 512, 512, 64, 1, 1) > square

@@ -21,6 +21,7 @@ from parity import torch32_propagation
 import test_gpu_dense as TD
 import test_gpu_topk as TT
 import test_gpu_transition as TR
+import test_gpu_window as TW
 
 pytestmark = pytest.mark.gpu
 
@@ -83,3 +84,10 @@ def test_transition_odd(dev, tile):
 @pytest.mark.parametrize("r", [40, 48])  # route weights split at r: 48 keeps the 128 x 128 kernel, 40 does not
 def test_transition_medium(dev, tile, r):
     TR._run(dev, 3005, B=2, Ns=300, Nd=140, Dsrc=136, Ddst=72, r=r, topk=8, temperature=1.2, kind="softmax")
+
+
+@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax"])
+def test_causal_dense(dev, tile, compress):
+    # full causal windows run the dense products with causal K ranges and skip
+    # the score tiles above the diagonal (softsign epilogue), under both tiles
+    TW.test_full_causal_window_runs_dense(dev, compress, True, 0)

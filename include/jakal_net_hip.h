@@ -30,7 +30,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 4. */
+/* ABI revision of this header (bumped on any signature change); this is 5. */
 int jn_abi_version(void);
 
 /*
@@ -347,6 +347,96 @@ int jn_transition_dense_backward(const float* sender_strength, const float* src_
                                  float* grad_dst_val, float* grad_projected_state, float* grad_projected_val,
                                  float* grad_source_weight, float* grad_target_weight, float* grad_core_weight,
                                  float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+/*
+ * Multi-head max-aggregated scores (MultiHeadPairwise / MultiHeadRoute with
+ * aggregate="max" over low-rank heads, src/jakal_net/modules.py:259-301,
+ * 470-529).  H = heads (2..8) heads of rank r each score every pair; the pair's
+ * score is the largest head score, max_h (dot_h + bias[h]) (/ T for routes),
+ * and its gradient reaches only that head (the first winning head on exact
+ * ties).  The heads' parameters come stacked as the reference's kernel spec
+ * stacks them (kernel_common.py:152-178, 240-270): projection weights
+ * [H, r, D] (= [H*r, D] row-major), core weights [H, r] (= [H*r]), bias [H] or
+ * NULL.  Projections hold all H*r ranks, head h in columns [h*r, (h+1)*r):
+ * projections [B*N, 2*H*r] for propagation, src_proj [B*Ns, H*r] and dst_proj
+ * [B*Nd, H*r] for transitions.  The forward also writes each edge's winning
+ * head (uint8, shaped like the edge index) for the backward.  Limits:
+ * H*r <= 128, and where the edges come from a top-k select
+ * H * ceil(r / 32) <= 4 (each head scores on whole 32-rank MFMA K-steps).
+ * One head is the single-head entry point.  grad_core_weight is [H, r],
+ * grad_bias [H]; other arguments as the single-head entry points.
+ *
+ * Replace the multi-head branches of pairwise_scores and route_scores
+ * (native/jakal_net_native.cpp:724-752, 889-917) under propagation_topk,
+ * propagation_window and transition_pairwise_topk, and the multi-head CUDA
+ * forwards low_rank_propagation_topk_forward_multihead_kernel and
+ * low_rank_pairwise_topk_forward_multihead_kernel
+ * (native/jakal_net_native_cuda.cu:1185-1347, 880-1026), whose heads share one
+ * bias; here each head keeps its own, as the composite's do.
+ */
+size_t jn_propagation_topk_forward_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t rank,
+                                                             int64_t heads);
+int jn_propagation_topk_forward_multihead(const float* layer_val, const float* projected_state,
+                                          const float* projected_val, const float* target_weight,
+                                          const float* source_weight, const float* core_weight, const float* bias,
+                                          int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                          int64_t rank, int64_t heads, int64_t topk, int32_t compress_kind,
+                                          float* delta_state, float* delta_val, float* projections,
+                                          int32_t* topk_index, float* topk_score, uint8_t* topk_head,
+                                          void* workspace, size_t workspace_bytes, jn_stream_t stream);
+size_t jn_propagation_topk_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                                     int64_t rank, int64_t heads, int64_t topk);
+int jn_propagation_topk_backward_multihead(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* projections, const int32_t* topk_index,
+    const float* topk_score, const uint8_t* topk_head, const float* grad_delta_state, const float* grad_delta_val,
+    int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t heads, int64_t topk,
+    int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
+    float* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
+    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+int jn_propagation_window_forward_multihead(const float* layer_val, const float* projected_state,
+                                            const float* projected_val, const float* target_weight,
+                                            const float* source_weight, const float* core_weight, const float* bias,
+                                            int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                            int64_t rank, int64_t heads, int64_t window, int32_t compress_kind,
+                                            float* delta_state, float* delta_val, float* projections,
+                                            int32_t* edge_index, float* edge_score, uint8_t* edge_head,
+                                            jn_stream_t stream);
+size_t jn_propagation_window_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim,
+                                                       int64_t out_dim, int64_t rank, int64_t heads, int64_t window);
+int jn_propagation_window_backward_multihead(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* projections, const int32_t* edge_index,
+    const float* edge_score, const uint8_t* edge_head, const float* grad_delta_state, const float* grad_delta_val,
+    int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t heads, int64_t window,
+    int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
+    float* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
+    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+size_t jn_transition_topk_multihead_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                                                    int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                                    int64_t heads, int64_t topk);
+int jn_transition_topk_forward_multihead(const float* sender_strength, const float* src_val, const float* dst_val,
+                                         const float* projected_state, const float* projected_val,
+                                         const float* source_weight, const float* target_weight,
+                                         const float* core_weight, const float* bias, float temperature,
+                                         int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                         int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads, int64_t topk,
+                                         int32_t compress_kind, float* delta_state, float* delta_val,
+                                         float* src_proj, float* dst_proj, int32_t* route_index, float* route_logit,
+                                         uint8_t* route_head, void* workspace, size_t workspace_bytes,
+                                         jn_stream_t stream);
+int jn_transition_topk_backward_multihead(
+    const float* sender_strength, const float* src_val, const float* dst_val, const float* projected_state,
+    const float* projected_val, const float* source_weight, const float* target_weight, const float* core_weight,
+    const float* src_proj, const float* dst_proj, const int32_t* route_index, const float* route_logit,
+    const uint8_t* route_head, const float* grad_delta_state, const float* grad_delta_val, float temperature,
+    int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim,
+    int64_t rank, int64_t heads, int64_t topk, int32_t compress_kind, float* grad_sender_strength,
+    float* grad_src_val, float* grad_dst_val, float* grad_projected_state, float* grad_projected_val,
+    float* grad_source_weight, float* grad_target_weight, float* grad_core_weight, float* grad_bias,
+    void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -98,6 +98,21 @@ int check_propagation_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64
 
 int64_t window_width(int64_t window, int64_t nodes) { return window + 1 < nodes ? window + 1 : nodes; }
 
+// Heads of a multi-head entry point (rank = one head's rank).  `select`: the
+// edges come from a top-k select, which scores at most four 32-rank K-steps.
+int check_heads(int64_t rank, int64_t heads, bool select) {
+  JN_REQUIRE(heads >= 2 && heads <= kMaxHeads, kUnsupported,
+             "multi-head entry points take 2..%d heads (got %lld); one head is the single-head entry point",
+             kMaxHeads, (long long)heads);
+  JN_REQUIRE(rank >= 1 && heads * rank <= 128, kUnsupported, "heads x rank must be in [1, 128] (heads=%lld rank=%lld)",
+             (long long)heads, (long long)rank);
+  JN_REQUIRE(!select || select_heads_fit(rank, heads), kUnsupported,
+             "a multi-head top-k select scores heads x ceil(rank / 32) <= 4 K-steps of 32 ranks (heads=%lld "
+             "rank=%lld)",
+             (long long)heads, (long long)rank);
+  return kOk;
+}
+
 struct PropBwdScratch {
   float* dP;
   float* g_score;
@@ -112,7 +127,9 @@ struct PropBwdScratch {
   size_t bytes;
 };
 
-PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int64_t Din, int64_t r, int64_t k) {
+// r: all ranks (heads * head rank); heads > 1 keeps one bias column per head.
+PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int64_t Din, int64_t r, int64_t k,
+                              int64_t heads = 1) {
   Workspace ws(base, size);
   PropBwdScratch s{};
   const int64_t M = B * N;
@@ -120,12 +137,12 @@ PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int
   s.dP = ws.take<float>(M * 2 * r);
   s.g_score = ws.take<float>(M * k);
   s.coef = ws.take<float>(M * k);
-  s.rowsum = ws.take<float>(M);
+  s.rowsum = ws.take<float>(M * heads);
   s.tile_base = ws.take<int32_t>(B * T * N);
   s.seg_start = ws.take<int32_t>(B * (N + 1));
   s.rec = ws.take<float4>(M * k);
   s.part_c = ws.take<float>((size_t)cols_backward_parts(M) * r);
-  s.stage = ws.take<float>(finalize_stage_floats((int)r));
+  s.stage = ws.take<float>(finalize_stage_floats((int)r, (int)heads));
   s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)(2 * r), (int)Din, (int)M) / sizeof(float));
   s.bytes = ws.used;
   return s;
@@ -150,8 +167,9 @@ struct TransitionScratch {
 
 int64_t route_edges(int64_t topk, int64_t dst_nodes) { return topk < dst_nodes ? topk : dst_nodes; }
 
+// r: all ranks (heads * head rank).
 TransitionScratch carve_transition(void* base, size_t size, int64_t B, int64_t Ns, int64_t Nd, int64_t Dsrc,
-                                   int64_t Ddst, int64_t r, int64_t k) {
+                                   int64_t Ddst, int64_t r, int64_t k, int64_t heads = 1) {
   Workspace ws(base, size);
   TransitionScratch s{};
   const int64_t T = (Ns + kCsrTile - 1) / kCsrTile;
@@ -162,13 +180,14 @@ TransitionScratch carve_transition(void* base, size_t size, int64_t B, int64_t N
   s.dPs = ws.take<float>(B * Ns * r);
   s.dPt = ws.take<float>(B * Nd * r);
   s.g_logit = ws.take<float>(B * Ns * k);
-  s.rowsum = ws.take<float>(B * Ns);
+  s.rowsum = ws.take<float>(B * Ns * heads);
   s.part_c = ws.take<float>((size_t)cols_backward_parts(B * Nd) * r);
-  s.stage = ws.take<float>(finalize_stage_floats((int)r));
+  s.stage = ws.take<float>(finalize_stage_floats((int)r, (int)heads));
   const size_t sk = std::max(gemm_grad_weight_workspace((int)r, (int)Dsrc, (int)(B * Ns)),
                              gemm_grad_weight_workspace((int)r, (int)Ddst, (int)(B * Nd)));
   s.splitk = ws.take<float>(sk / sizeof(float));
-  s.select_ws_bytes = select_workspace_bytes(B, Nd, r);
+  s.select_ws_bytes = heads > 1 ? select_workspace_bytes_heads(B, Nd, r / heads, heads)
+                                : select_workspace_bytes(B, Nd, r);
   s.select_ws = ws.take<char>(s.select_ws_bytes);
   s.bytes = ws.used;
   return s;
@@ -277,22 +296,26 @@ int check_transition_dense_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t
 
 // Backward of any edge-list propagation (top-k or window): the edge list
 // (edge_index, edge_score) [B*N, k] is what the forward aggregated.
+// rank: all ranks (heads * head rank); heads > 1 takes each edge's head.
 int propagation_edges_backward(const float* layer_val, const float* projected_state, const float* projected_val,
                                const float* target_weight, const float* source_weight, const float* core_weight,
                                const float* projections, const int32_t* topk_index, const float* topk_score,
-                               const float* grad_delta_state, const float* grad_delta_val, int64_t batch,
-                               int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t topk,
-                               int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val,
-                               float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
-                               float* grad_source_weight, float* grad_core_weight, float* grad_bias, void* workspace,
-                               size_t workspace_bytes, hipStream_t stream) {
+                               const uint8_t* edge_head, const float* grad_delta_state, const float* grad_delta_val,
+                               int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                               int64_t heads, int64_t topk, int32_t compress_kind,
+                               int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
+                               float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
+                               float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
   int rc;
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
-                 projections && topk_index && topk_score && grad_delta_state && grad_delta_val,
+                 projections && topk_index && topk_score && grad_delta_state && grad_delta_val &&
+                 (heads <= 1 || edge_head),
              kInvalidArgument, "null tensor pointer");
   JN_REQUIRE(!projected_val_is_layer_val || in_dim == out_dim, kInvalidArgument,
              "projected_val_is_layer_val requires in_dim == out_dim");
-  PropBwdScratch s = carve_prop_bwd(workspace, workspace_bytes, batch, nodes, in_dim, rank, topk);
+  const bool mh = heads > 1;
+  PropBwdScratch s = carve_prop_bwd(workspace, workspace_bytes, batch, nodes, in_dim, rank, topk, mh ? heads : 1);
   JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
              "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
   hipStream_t st = stream;
@@ -325,6 +348,11 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   rb.dq = s.dP;
   rb.lddq = 2 * r;
   rb.rowsum_gs = s.rowsum;
+  if (mh) {
+    rb.ehead = edge_head;
+    rb.heads = (int)heads;
+    rb.head_rank = (int)(rank / heads);
+  }
   rc = launch_rows_backward(rb, st);
   if (rc) return rc;
 
@@ -341,6 +369,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   ca.coef = s.coef;
   ca.g_score = s.g_score;
   ca.gds = grad_delta_state;
+  ca.ehead = mh ? edge_head : nullptr;
   rc = launch_csr(ca, st);
   if (rc) return rc;
 
@@ -367,6 +396,10 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   cb.dk = s.dP + r;
   cb.lddk = 2 * r;
   cb.part_c = s.part_c;
+  if (mh) {
+    cb.heads = (int)heads;
+    cb.head_rank = (int)(rank / heads);
+  }
   rc = launch_cols_backward(cb, st);
   if (rc) return rc;
 
@@ -385,9 +418,161 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
     if (rc) return rc;
   }
 
-  // 6. w_hat and bias grads
+  // 6. w_hat and bias grads (one bias per head)
   const int nparts = cols_backward_parts(M);
-  return launch_finalize_small_grads(s.part_c, nparts, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st);
+  return launch_finalize_small_grads(s.part_c, nparts, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st,
+                                     mh ? (int)heads : 1);
+}
+
+// Top-k propagation forward over all ranks (heads * head rank); heads > 1
+// also writes each edge's winning head.
+int propagation_topk_forward_impl(const float* layer_val, const float* projected_state, const float* projected_val,
+                                  const float* target_weight, const float* source_weight, const float* core_weight,
+                                  const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                  int64_t rank, int64_t heads, int64_t topk, int32_t compress_kind,
+                                  float* delta_state, float* delta_val, float* projections, int32_t* topk_index,
+                                  float* topk_score, uint8_t* topk_head, void* workspace, size_t workspace_bytes,
+                                  hipStream_t st) {
+  int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
+  if (rc) return rc;
+  const bool mh = heads > 1;
+  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
+                 delta_state && delta_val && projections && topk_index && topk_score && (!mh || topk_head),
+             kInvalidArgument, "null tensor pointer");
+  const int M = (int)(batch * nodes), r = (int)rank, k = (int)topk;
+
+  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, M, 2 * r,
+                    (int)in_dim, st);
+  if (rc) return rc;
+
+  SelectArgs s{};
+  s.q = projections;
+  s.key = projections + r;
+  s.ldq = 2 * r;
+  s.ldk = 2 * r;
+  s.q_batch_stride = nodes * 2 * r;
+  s.k_batch_stride = nodes * 2 * r;
+  s.scale = core_weight;
+  s.bias = bias;
+  s.scale_on_query = 0;
+  s.temperature = 1.0f;
+  s.B = (int)batch;
+  s.Nq = (int)nodes;
+  s.Nk = (int)nodes;
+  s.r = r;
+  s.k = k;
+  s.out_idx = topk_index;
+  s.out_score = topk_score;
+  s.ws = workspace;
+  s.ws_bytes = workspace_bytes;
+  if (mh) {
+    s.heads = (int)heads;
+    s.head_rank = (int)(rank / heads);
+  }
+  rc = launch_topk_select(s, st);
+  if (rc) return rc;
+
+  if (mh) {  // the winning head of every selected edge
+    WindowScoreArgs w{};
+    w.q = projections;
+    w.key = projections + r;
+    w.ldq = 2 * r;
+    w.ldk = 2 * r;
+    w.scale = core_weight;
+    w.bias = bias;
+    w.inv_temperature = 1.0f;
+    w.B = (int)batch;
+    w.Nq = (int)nodes;
+    w.Nk = (int)nodes;
+    w.r = r;
+    w.width = k;
+    w.all_keys = 2;
+    w.idx = topk_index;
+    w.score = topk_score;
+    w.heads = (int)heads;
+    w.head_rank = (int)(rank / heads);
+    w.head = topk_head;
+    rc = launch_window_scores(w, st);
+    if (rc) return rc;
+  }
+
+  RowsFwdArgs f{};
+  f.idx = topk_index;
+  f.score = topk_score;
+  f.k = k;
+  f.compress = compress_kind;
+  f.ps = projected_state;
+  f.pv = projected_val;
+  f.ld_pv = out_dim;
+  f.Nq = (int)nodes;
+  f.Nk = (int)nodes;
+  f.D = (int)out_dim;
+  f.rows = M;
+  f.out_state = delta_state;
+  f.out_val = delta_val;
+  return launch_rows_forward(f, st);
+}
+
+// Window propagation forward over all ranks; heads > 1 also writes each edge's head.
+int propagation_window_forward_impl(const float* layer_val, const float* projected_state, const float* projected_val,
+                                    const float* target_weight, const float* source_weight, const float* core_weight,
+                                    const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                    int64_t rank, int64_t heads, int64_t window, int32_t compress_kind,
+                                    float* delta_state, float* delta_val, float* projections, int32_t* edge_index,
+                                    float* edge_score, uint8_t* edge_head, hipStream_t st) {
+  JN_REQUIRE(window >= 0, kInvalidArgument, "window must be non-negative (got %lld)", (long long)window);
+  const int64_t width = window_width(window, nodes);
+  int rc = check_edge_shapes(batch, nodes, in_dim, out_dim, rank, width, compress_kind);
+  if (rc) return rc;
+  const bool mh = heads > 1;
+  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
+                 delta_state && delta_val && projections && edge_index && edge_score && (!mh || edge_head),
+             kInvalidArgument, "null tensor pointer");
+  const int M = (int)(batch * nodes), r = (int)rank;
+
+  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, M, 2 * r,
+                    (int)in_dim, st);
+  if (rc) return rc;
+
+  WindowScoreArgs w{};
+  w.q = projections;
+  w.key = projections + r;
+  w.ldq = 2 * r;
+  w.ldk = 2 * r;
+  w.scale = core_weight;
+  w.bias = bias;
+  w.inv_temperature = 1.0f;
+  w.B = (int)batch;
+  w.Nq = (int)nodes;
+  w.Nk = (int)nodes;
+  w.r = r;
+  w.width = (int)width;
+  w.all_keys = 0;
+  w.idx = edge_index;
+  w.score = edge_score;
+  if (mh) {
+    w.heads = (int)heads;
+    w.head_rank = (int)(rank / heads);
+    w.head = edge_head;
+  }
+  rc = launch_window_scores(w, st);
+  if (rc) return rc;
+
+  RowsFwdArgs f{};
+  f.idx = edge_index;
+  f.score = edge_score;
+  f.k = (int)width;
+  f.compress = compress_kind;
+  f.ps = projected_state;
+  f.pv = projected_val;
+  f.ld_pv = out_dim;
+  f.Nq = (int)nodes;
+  f.Nk = (int)nodes;
+  f.D = (int)out_dim;
+  f.rows = M;
+  f.out_state = delta_state;
+  f.out_val = delta_val;
+  return launch_rows_forward(f, st);
 }
 
 }  // namespace
@@ -399,7 +584,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 4; }
+int jn_abi_version(void) { return 5; }
 
 int jn_profile_enable(int32_t on) {
   std::lock_guard<std::mutex> lock(jakal::g_prof_mu);
@@ -496,56 +681,10 @@ int jn_propagation_topk_forward(const float* layer_val, const float* projected_s
                                 int64_t rank, int64_t topk, int32_t compress_kind, float* delta_state,
                                 float* delta_val, float* projections, int32_t* topk_index, float* topk_score,
                                 void* workspace, size_t workspace_bytes, jn_stream_t stream) {
-  int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
-  if (rc) return rc;
-  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
-                 delta_state && delta_val && projections && topk_index && topk_score,
-             kInvalidArgument, "null tensor pointer");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int M = (int)(batch * nodes), r = (int)rank, k = (int)topk;
-
-  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, M, 2 * r,
-                    (int)in_dim, st);
-  if (rc) return rc;
-
-  SelectArgs s{};
-  s.q = projections;
-  s.key = projections + r;
-  s.ldq = 2 * r;
-  s.ldk = 2 * r;
-  s.q_batch_stride = nodes * 2 * r;
-  s.k_batch_stride = nodes * 2 * r;
-  s.scale = core_weight;
-  s.bias = bias;
-  s.scale_on_query = 0;
-  s.temperature = 1.0f;
-  s.B = (int)batch;
-  s.Nq = (int)nodes;
-  s.Nk = (int)nodes;
-  s.r = r;
-  s.k = k;
-  s.out_idx = topk_index;
-  s.out_score = topk_score;
-  s.ws = workspace;
-  s.ws_bytes = workspace_bytes;
-  rc = launch_topk_select(s, st);
-  if (rc) return rc;
-
-  RowsFwdArgs f{};
-  f.idx = topk_index;
-  f.score = topk_score;
-  f.k = k;
-  f.compress = compress_kind;
-  f.ps = projected_state;
-  f.pv = projected_val;
-  f.ld_pv = out_dim;
-  f.Nq = (int)nodes;
-  f.Nk = (int)nodes;
-  f.D = (int)out_dim;
-  f.rows = M;
-  f.out_state = delta_state;
-  f.out_val = delta_val;
-  return launch_rows_forward(f, st);
+  return propagation_topk_forward_impl(layer_val, projected_state, projected_val, target_weight, source_weight,
+                                       core_weight, bias, batch, nodes, in_dim, out_dim, rank, 1, topk, compress_kind,
+                                       delta_state, delta_val, projections, topk_index, topk_score, nullptr,
+                                       workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 size_t jn_propagation_topk_forward_workspace_bytes(int64_t batch, int64_t nodes, int64_t rank) {
@@ -570,8 +709,8 @@ int jn_propagation_topk_backward(const float* layer_val, const float* projected_
   const int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
   if (rc) return rc;
   return propagation_edges_backward(layer_val, projected_state, projected_val, target_weight, source_weight,
-                                    core_weight, projections, topk_index, topk_score, grad_delta_state,
-                                    grad_delta_val, batch, nodes, in_dim, out_dim, rank, topk, compress_kind,
+                                    core_weight, projections, topk_index, topk_score, nullptr, grad_delta_state,
+                                    grad_delta_val, batch, nodes, in_dim, out_dim, rank, 1, topk, compress_kind,
                                     projected_val_is_layer_val, grad_layer_val, grad_projected_state,
                                     grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
                                     grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
@@ -583,54 +722,10 @@ int jn_propagation_window_forward(const float* layer_val, const float* projected
                                   int64_t rank, int64_t window, int32_t compress_kind, float* delta_state,
                                   float* delta_val, float* projections, int32_t* edge_index, float* edge_score,
                                   jn_stream_t stream) {
-  JN_REQUIRE(window >= 0, kInvalidArgument, "window must be non-negative (got %lld)", (long long)window);
-  const int64_t width = window_width(window, nodes);
-  int rc = check_edge_shapes(batch, nodes, in_dim, out_dim, rank, width, compress_kind);
-  if (rc) return rc;
-  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
-                 delta_state && delta_val && projections && edge_index && edge_score,
-             kInvalidArgument, "null tensor pointer");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int M = (int)(batch * nodes), r = (int)rank;
-
-  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, M, 2 * r,
-                    (int)in_dim, st);
-  if (rc) return rc;
-
-  WindowScoreArgs w{};
-  w.q = projections;
-  w.key = projections + r;
-  w.ldq = 2 * r;
-  w.ldk = 2 * r;
-  w.scale = core_weight;
-  w.bias = bias;
-  w.inv_temperature = 1.0f;
-  w.B = (int)batch;
-  w.Nq = (int)nodes;
-  w.Nk = (int)nodes;
-  w.r = r;
-  w.width = (int)width;
-  w.all_keys = 0;
-  w.idx = edge_index;
-  w.score = edge_score;
-  rc = launch_window_scores(w, st);
-  if (rc) return rc;
-
-  RowsFwdArgs f{};
-  f.idx = edge_index;
-  f.score = edge_score;
-  f.k = (int)width;
-  f.compress = compress_kind;
-  f.ps = projected_state;
-  f.pv = projected_val;
-  f.ld_pv = out_dim;
-  f.Nq = (int)nodes;
-  f.Nk = (int)nodes;
-  f.D = (int)out_dim;
-  f.rows = M;
-  f.out_state = delta_state;
-  f.out_val = delta_val;
-  return launch_rows_forward(f, st);
+  return propagation_window_forward_impl(layer_val, projected_state, projected_val, target_weight, source_weight,
+                                         core_weight, bias, batch, nodes, in_dim, out_dim, rank, 1, window,
+                                         compress_kind, delta_state, delta_val, projections, edge_index, edge_score,
+                                         nullptr, static_cast<hipStream_t>(stream));
 }
 
 size_t jn_propagation_window_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
@@ -654,8 +749,8 @@ int jn_propagation_window_backward(const float* layer_val, const float* projecte
   const int rc = check_edge_shapes(batch, nodes, in_dim, out_dim, rank, width, compress_kind);
   if (rc) return rc;
   return propagation_edges_backward(layer_val, projected_state, projected_val, target_weight, source_weight,
-                                    core_weight, projections, edge_index, edge_score, grad_delta_state,
-                                    grad_delta_val, batch, nodes, in_dim, out_dim, rank, width, compress_kind,
+                                    core_weight, projections, edge_index, edge_score, nullptr, grad_delta_state,
+                                    grad_delta_val, batch, nodes, in_dim, out_dim, rank, 1, width, compress_kind,
                                     projected_val_is_layer_val, grad_layer_val, grad_projected_state,
                                     grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
                                     grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
@@ -670,27 +765,28 @@ size_t jn_transition_topk_workspace_bytes(int64_t batch, int64_t src_nodes, int6
       .bytes;
 }
 
-int jn_transition_topk_forward(const float* sender_strength, const float* src_val, const float* dst_val,
-                               const float* projected_state, const float* projected_val, const float* source_weight,
-                               const float* target_weight, const float* core_weight, const float* bias,
-                               float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
-                               int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk,
-                               int32_t compress_kind, float* delta_state, float* delta_val, float* src_proj,
-                               float* dst_proj, int32_t* route_index, float* route_logit, void* workspace,
-                               size_t workspace_bytes, jn_stream_t stream) {
+// rank: all ranks (heads * head rank); heads > 1 also writes each route's head.
+static int transition_topk_forward_impl(const float* sender_strength, const float* src_val, const float* dst_val,
+                                 const float* projected_state, const float* projected_val, const float* source_weight,
+                                 const float* target_weight, const float* core_weight, const float* bias,
+                                 float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                                 int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
+                                 int64_t topk, int32_t compress_kind, float* delta_state, float* delta_val,
+                                 float* src_proj, float* dst_proj, int32_t* route_index, float* route_logit,
+                                 uint8_t* route_head, void* workspace, size_t workspace_bytes, hipStream_t st) {
   int rc = check_transition_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, topk, compress_kind,
                                    temperature);
   if (rc) return rc;
+  const bool mh = heads > 1;
   JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
                  target_weight && core_weight && delta_state && delta_val && src_proj && dst_proj && route_index &&
-                 route_logit,
+                 route_logit && (!mh || route_head),
              kInvalidArgument, "null tensor pointer");
   const int64_t k = route_edges(topk, dst_nodes);
   TransitionScratch s = carve_transition(workspace, workspace_bytes, batch, src_nodes, dst_nodes, src_dim, dst_dim,
-                                         rank, k);
+                                         rank, k, mh ? heads : 1);
   JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
              "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const int B = (int)batch, Ns = (int)src_nodes, Nd = (int)dst_nodes, r = (int)rank;
 
   // 1. projections P_s = src . Ws^T, P_t = dst . Wt^T  (modules.py:435-437)
@@ -723,6 +819,10 @@ int jn_transition_topk_forward(const float* sender_strength, const float* src_va
     a.out_score = route_logit;
     a.ws = s.select_ws;
     a.ws_bytes = s.select_ws_bytes;
+    if (mh) {
+      a.heads = (int)heads;
+      a.head_rank = (int)(rank / heads);
+    }
     rc = launch_topk_select(a, st);
   } else {
     WindowScoreArgs w{};
@@ -741,9 +841,37 @@ int jn_transition_topk_forward(const float* sender_strength, const float* src_va
     w.all_keys = 1;
     w.idx = route_index;
     w.score = route_logit;
+    if (mh) {
+      w.heads = (int)heads;
+      w.head_rank = (int)(rank / heads);
+      w.head = route_head;
+    }
     rc = launch_window_scores(w, st);
   }
   if (rc) return rc;
+  if (mh && k < dst_nodes) {  // the winning head of every selected route
+    WindowScoreArgs w{};
+    w.q = src_proj;
+    w.key = dst_proj;
+    w.ldq = r;
+    w.ldk = r;
+    w.scale = core_weight;
+    w.bias = bias;
+    w.inv_temperature = 1.0f / temperature;
+    w.B = B;
+    w.Nq = Ns;
+    w.Nk = Nd;
+    w.r = r;
+    w.width = (int)k;
+    w.all_keys = 2;
+    w.idx = route_index;
+    w.score = route_logit;
+    w.heads = (int)heads;
+    w.head_rank = (int)(rank / heads);
+    w.head = route_head;
+    rc = launch_window_scores(w, st);
+    if (rc) return rc;
+  }
 
   // 3. coefficients rho * p, then destination sums as gathers over the edges
   //    transposed by destination
@@ -779,30 +907,31 @@ int jn_transition_topk_forward(const float* sender_strength, const float* src_va
   return launch_cols_backward(cb, st);
 }
 
-int jn_transition_topk_backward(const float* sender_strength, const float* src_val, const float* dst_val,
-                                const float* projected_state, const float* projected_val, const float* source_weight,
-                                const float* target_weight, const float* core_weight, const float* src_proj,
-                                const float* dst_proj, const int32_t* route_index, const float* route_logit,
-                                const float* grad_delta_state, const float* grad_delta_val, float temperature,
-                                int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
-                                int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk, int32_t compress_kind,
-                                float* grad_sender_strength, float* grad_src_val, float* grad_dst_val,
-                                float* grad_projected_state, float* grad_projected_val, float* grad_source_weight,
-                                float* grad_target_weight, float* grad_core_weight, float* grad_bias,
-                                void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+static int transition_topk_backward_impl(const float* sender_strength, const float* src_val, const float* dst_val,
+                                  const float* projected_state, const float* projected_val,
+                                  const float* source_weight, const float* target_weight, const float* core_weight,
+                                  const float* src_proj, const float* dst_proj, const int32_t* route_index,
+                                  const float* route_logit, const uint8_t* route_head, const float* grad_delta_state,
+                                  const float* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes,
+                                  int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                  int64_t heads, int64_t topk, int32_t compress_kind, float* grad_sender_strength,
+                                  float* grad_src_val, float* grad_dst_val, float* grad_projected_state,
+                                  float* grad_projected_val, float* grad_source_weight, float* grad_target_weight,
+                                  float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
+                                  hipStream_t st) {
   int rc = check_transition_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, topk, compress_kind,
                                    temperature);
   if (rc) return rc;
+  const bool mh = heads > 1;
   JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
                  target_weight && core_weight && src_proj && dst_proj && route_index && route_logit &&
-                 grad_delta_state && grad_delta_val,
+                 grad_delta_state && grad_delta_val && (!mh || route_head),
              kInvalidArgument, "null tensor pointer");
   const int64_t k = route_edges(topk, dst_nodes);
   TransitionScratch s = carve_transition(workspace, workspace_bytes, batch, src_nodes, dst_nodes, src_dim, dst_dim,
-                                         rank, k);
+                                         rank, k, mh ? heads : 1);
   JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
              "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const int B = (int)batch, Ns = (int)src_nodes, Nd = (int)dst_nodes, r = (int)rank;
 
   // 1. source rows: coefficient grads, route compress backward, sender-strength,
@@ -835,6 +964,11 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
   rb.dq = s.dPs;
   rb.lddq = r;
   rb.rowsum = s.rowsum;
+  if (mh) {
+    rb.ehead = route_head;
+    rb.heads = (int)heads;
+    rb.head_rank = (int)(rank / heads);
+  }
   rc = launch_route_rows_backward(rb, st);
   if (rc) return rc;
 
@@ -849,6 +983,7 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
   ca.seg_start = s.seg_start;
   ca.rec = s.rec;
   ca.g_score = s.g_logit;
+  ca.ehead = mh ? route_head : nullptr;
   rc = launch_csr(ca, st);
   if (rc) return rc;
   ColsBwdArgs cb{};
@@ -868,6 +1003,10 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
   cb.dk = s.dPt;
   cb.lddk = r;
   cb.part_c = s.part_c;
+  if (mh) {
+    cb.heads = (int)heads;
+    cb.head_rank = (int)(rank / heads);
+  }
   rc = launch_cols_backward(cb, st);
   if (rc) return rc;
 
@@ -894,9 +1033,193 @@ int jn_transition_topk_backward(const float* sender_strength, const float* src_v
   }
 
   // 4. core weight and bias grads.  Softmax routes do not change when a row's
-  // logits shift together, so their bias gradient is exactly 0 (no rows summed).
+  // logits shift together, so their bias gradient is exactly 0 (no rows summed);
+  // one head's bias shifts only its own routes, so every head's column is summed.
   return launch_finalize_small_grads(s.part_c, cols_backward_parts((int64_t)B * Nd), r, grad_core_weight, 0,
-                                     s.rowsum, compress_kind == 0 ? 0 : batch * src_nodes, grad_bias, s.stage, st);
+                                     s.rowsum, (compress_kind == 0 && !mh) ? 0 : batch * src_nodes, grad_bias,
+                                     s.stage, st, mh ? (int)heads : 1);
+}
+
+int jn_transition_topk_forward(const float* sender_strength, const float* src_val, const float* dst_val,
+                               const float* projected_state, const float* projected_val, const float* source_weight,
+                               const float* target_weight, const float* core_weight, const float* bias,
+                               float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                               int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk,
+                               int32_t compress_kind, float* delta_state, float* delta_val, float* src_proj,
+                               float* dst_proj, int32_t* route_index, float* route_logit, void* workspace,
+                               size_t workspace_bytes, jn_stream_t stream) {
+  return transition_topk_forward_impl(sender_strength, src_val, dst_val, projected_state, projected_val,
+                                      source_weight, target_weight, core_weight, bias, temperature, batch, src_nodes,
+                                      dst_nodes, src_dim, dst_dim, val_dim, rank, 1, topk, compress_kind, delta_state,
+                                      delta_val, src_proj, dst_proj, route_index, route_logit, nullptr, workspace,
+                                      workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int jn_transition_topk_backward(const float* sender_strength, const float* src_val, const float* dst_val,
+                                const float* projected_state, const float* projected_val, const float* source_weight,
+                                const float* target_weight, const float* core_weight, const float* src_proj,
+                                const float* dst_proj, const int32_t* route_index, const float* route_logit,
+                                const float* grad_delta_state, const float* grad_delta_val, float temperature,
+                                int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk, int32_t compress_kind,
+                                float* grad_sender_strength, float* grad_src_val, float* grad_dst_val,
+                                float* grad_projected_state, float* grad_projected_val, float* grad_source_weight,
+                                float* grad_target_weight, float* grad_core_weight, float* grad_bias,
+                                void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  return transition_topk_backward_impl(sender_strength, src_val, dst_val, projected_state, projected_val,
+                                       source_weight, target_weight, core_weight, src_proj, dst_proj, route_index,
+                                       route_logit, nullptr, grad_delta_state, grad_delta_val, temperature, batch,
+                                       src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, 1, topk, compress_kind,
+                                       grad_sender_strength, grad_src_val, grad_dst_val, grad_projected_state,
+                                       grad_projected_val, grad_source_weight, grad_target_weight, grad_core_weight,
+                                       grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+// ---- multi-head max-aggregated scores ---------------------------------------
+size_t jn_propagation_topk_forward_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t rank,
+                                                             int64_t heads) {
+  if (batch < 1 || nodes < 1 || heads < 2) return 0;
+  return select_workspace_bytes_heads(batch, nodes, rank, heads);
+}
+
+size_t jn_propagation_topk_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                                     int64_t rank, int64_t heads, int64_t topk) {
+  (void)out_dim;
+  if (batch < 1 || nodes < 1 || heads < 2 || topk < 1) return 0;
+  return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank * heads, topk, heads).bytes;
+}
+
+int jn_propagation_topk_forward_multihead(const float* layer_val, const float* projected_state,
+                                          const float* projected_val, const float* target_weight,
+                                          const float* source_weight, const float* core_weight, const float* bias,
+                                          int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                          int64_t rank, int64_t heads, int64_t topk, int32_t compress_kind,
+                                          float* delta_state, float* delta_val, float* projections,
+                                          int32_t* topk_index, float* topk_score, uint8_t* topk_head,
+                                          void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  const int rc = check_heads(rank, heads, true);
+  if (rc) return rc;
+  return propagation_topk_forward_impl(layer_val, projected_state, projected_val, target_weight, source_weight,
+                                       core_weight, bias, batch, nodes, in_dim, out_dim, rank * heads, heads, topk,
+                                       compress_kind, delta_state, delta_val, projections, topk_index, topk_score,
+                                       topk_head, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int jn_propagation_topk_backward_multihead(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* projections, const int32_t* topk_index,
+    const float* topk_score, const uint8_t* topk_head, const float* grad_delta_state, const float* grad_delta_val,
+    int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t heads, int64_t topk,
+    int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
+    float* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
+    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_heads(rank, heads, true);
+  if (rc) return rc;
+  rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank * heads, topk, compress_kind);
+  if (rc) return rc;
+  return propagation_edges_backward(layer_val, projected_state, projected_val, target_weight, source_weight,
+                                    core_weight, projections, topk_index, topk_score, topk_head, grad_delta_state,
+                                    grad_delta_val, batch, nodes, in_dim, out_dim, rank * heads, heads, topk,
+                                    compress_kind, projected_val_is_layer_val, grad_layer_val, grad_projected_state,
+                                    grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
+                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+size_t jn_propagation_window_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim,
+                                                       int64_t out_dim, int64_t rank, int64_t heads, int64_t window) {
+  (void)out_dim;
+  if (window < 0 || nodes < 1 || batch < 1 || heads < 2) return 0;
+  return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank * heads, window_width(window, nodes), heads).bytes;
+}
+
+int jn_propagation_window_forward_multihead(const float* layer_val, const float* projected_state,
+                                            const float* projected_val, const float* target_weight,
+                                            const float* source_weight, const float* core_weight, const float* bias,
+                                            int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                            int64_t rank, int64_t heads, int64_t window, int32_t compress_kind,
+                                            float* delta_state, float* delta_val, float* projections,
+                                            int32_t* edge_index, float* edge_score, uint8_t* edge_head,
+                                            jn_stream_t stream) {
+  const int rc = check_heads(rank, heads, false);
+  if (rc) return rc;
+  return propagation_window_forward_impl(layer_val, projected_state, projected_val, target_weight, source_weight,
+                                         core_weight, bias, batch, nodes, in_dim, out_dim, rank * heads, heads,
+                                         window, compress_kind, delta_state, delta_val, projections, edge_index,
+                                         edge_score, edge_head, static_cast<hipStream_t>(stream));
+}
+
+int jn_propagation_window_backward_multihead(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* projections, const int32_t* edge_index,
+    const float* edge_score, const uint8_t* edge_head, const float* grad_delta_state, const float* grad_delta_val,
+    int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t heads, int64_t window,
+    int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
+    float* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
+    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_heads(rank, heads, false);
+  if (rc) return rc;
+  JN_REQUIRE(window >= 0, kInvalidArgument, "window must be non-negative (got %lld)", (long long)window);
+  const int64_t width = window_width(window, nodes);
+  rc = check_edge_shapes(batch, nodes, in_dim, out_dim, rank * heads, width, compress_kind);
+  if (rc) return rc;
+  return propagation_edges_backward(layer_val, projected_state, projected_val, target_weight, source_weight,
+                                    core_weight, projections, edge_index, edge_score, edge_head, grad_delta_state,
+                                    grad_delta_val, batch, nodes, in_dim, out_dim, rank * heads, heads, width,
+                                    compress_kind, projected_val_is_layer_val, grad_layer_val, grad_projected_state,
+                                    grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
+                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+size_t jn_transition_topk_multihead_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                                                    int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                                    int64_t heads, int64_t topk) {
+  (void)val_dim;
+  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || topk < 1 || heads < 2) return 0;
+  if (route_edges(topk, dst_nodes) < dst_nodes && !select_heads_fit(rank, heads)) return 0;
+  return carve_transition(nullptr, 0, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank * heads,
+                          route_edges(topk, dst_nodes), heads)
+      .bytes;
+}
+
+int jn_transition_topk_forward_multihead(const float* sender_strength, const float* src_val, const float* dst_val,
+                                         const float* projected_state, const float* projected_val,
+                                         const float* source_weight, const float* target_weight,
+                                         const float* core_weight, const float* bias, float temperature,
+                                         int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                         int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads, int64_t topk,
+                                         int32_t compress_kind, float* delta_state, float* delta_val,
+                                         float* src_proj, float* dst_proj, int32_t* route_index, float* route_logit,
+                                         uint8_t* route_head, void* workspace, size_t workspace_bytes,
+                                         jn_stream_t stream) {
+  const int rc = check_heads(rank, heads, route_edges(topk, dst_nodes) < dst_nodes);
+  if (rc) return rc;
+  return transition_topk_forward_impl(sender_strength, src_val, dst_val, projected_state, projected_val,
+                                      source_weight, target_weight, core_weight, bias, temperature, batch, src_nodes,
+                                      dst_nodes, src_dim, dst_dim, val_dim, rank * heads, heads, topk, compress_kind,
+                                      delta_state, delta_val, src_proj, dst_proj, route_index, route_logit,
+                                      route_head, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int jn_transition_topk_backward_multihead(
+    const float* sender_strength, const float* src_val, const float* dst_val, const float* projected_state,
+    const float* projected_val, const float* source_weight, const float* target_weight, const float* core_weight,
+    const float* src_proj, const float* dst_proj, const int32_t* route_index, const float* route_logit,
+    const uint8_t* route_head, const float* grad_delta_state, const float* grad_delta_val, float temperature,
+    int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim,
+    int64_t rank, int64_t heads, int64_t topk, int32_t compress_kind, float* grad_sender_strength,
+    float* grad_src_val, float* grad_dst_val, float* grad_projected_state, float* grad_projected_val,
+    float* grad_source_weight, float* grad_target_weight, float* grad_core_weight, float* grad_bias,
+    void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  const int rc = check_heads(rank, heads, route_edges(topk, dst_nodes) < dst_nodes);
+  if (rc) return rc;
+  return transition_topk_backward_impl(sender_strength, src_val, dst_val, projected_state, projected_val,
+                                       source_weight, target_weight, core_weight, src_proj, dst_proj, route_index,
+                                       route_logit, route_head, grad_delta_state, grad_delta_val, temperature, batch,
+                                       src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank * heads, heads, topk,
+                                       compress_kind, grad_sender_strength, grad_src_val, grad_dst_val,
+                                       grad_projected_state, grad_projected_val, grad_source_weight,
+                                       grad_target_weight, grad_core_weight, grad_bias, workspace, workspace_bytes,
+                                       static_cast<hipStream_t>(stream));
 }
 
 int jn_propagation_dense_forward(const float* layer_val, const float* projected_state, const float* projected_val,

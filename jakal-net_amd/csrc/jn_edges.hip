@@ -212,7 +212,9 @@ __global__ __launch_bounds__(256) void rows_backward_dots_kernel(RowsBwdArgs a, 
   }
 }
 
-template <int W, int NV, int KP, bool SPLIT>
+// MH: multi-head scores (a.heads > 1): edge e's gradient reaches only the
+// ranks of its head a.ehead[e] in dq, and the bias partials are per head.
+template <int W, int NV, int KP, bool SPLIT, bool MH>
 __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
   constexpr int NI = KP / 4;      // iterations per block of KP edges
   constexpr int P = 16 * W * NV;  // D floats per pass of a 16-lane group
@@ -225,8 +227,16 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
   const float gs_row = a.gds[row];
   // 32-bit offsets into buffers of this batch element (sizes checked on the host)
   const auto rs_key = make_rsrc(a.key + b * a.Nk * a.ldk, (uint32_t)(a.Nk * a.ldk * 4));
-  // key rows as float4 when 16-byte aligned (rank slots 4c and 64 + 4c)
-  const bool kvec = (a.r % 4 == 0) && (a.ldk % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.key) & 15) == 0);
+  // key rows as float4 when 16-byte aligned (rank slots 4c and 64 + 4c; with
+  // several heads a float4 must not straddle two of them)
+  const bool kvec = (a.r % 4 == 0) && (a.ldk % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.key) & 15) == 0) &&
+                    (!MH || a.head_rank % 4 == 0);
+  // MH: head of each rank slot of this lane (kvec: slots 4c and 64 + 4c; scalar: c + 16m)
+  int hslot[8];
+  if constexpr (MH) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) hslot[m] = (kvec ? (m == 0 ? 4 * c : 64 + 4 * c) : c + 16 * m) / a.head_rank;
+  }
 
   float rmax = 0.f, rinv = 0.f;
   if (a.compress == 1) row_abs_softmax_stats(a.idx, a.score, row, a.k, rmax, rinv);
@@ -234,6 +244,7 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
   float4 dqa = make_float4(0.f, 0.f, 0.f, 0.f), dqb = dqa;  // kvec: ranks 4c.., 64+4c..
   float dqs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // scalar: ranks c + 16m
   float gsum = 0.f;
+  float hsum[MH ? kMaxHeads : 1] = {};
   for (int e0 = 0; e0 < a.k; e0 += KP) {
     int j;
     float cf, s;
@@ -244,6 +255,12 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
     int jg[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) jg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, j);
+    int eh = 0, hg[MH ? NI : 1];
+    if constexpr (MH) {
+      if (j >= 0) eh = a.ehead[row * a.k + e0 + lane];  // j >= 0: lane < KP and e0 + lane < k
+#pragma unroll
+      for (int i = 0; i < NI; ++i) hg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, eh);
+    }
 
     float dot = 0.f;
     if constexpr (SPLIT) {
@@ -308,9 +325,15 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
       a.g_score[row * a.k + e0 + lane] = gsc;
       a.coef[row * a.k + e0 + lane] = cf;
     }
-    // kinds 1 and 2 hold the whole row in this pass (k <= 64)
-    const bool shift_free = a.compress != 0 && row_one_sign(j >= 0, s);
-    gsum += shift_free ? 0.f : gsc;
+    if constexpr (MH) {
+      // per-head bias partials (a shift of one head's scores is no shift of the row)
+#pragma unroll
+      for (int h = 0; h < kMaxHeads; ++h) hsum[h] += (eh == h) ? gsc : 0.f;
+    } else {
+      // kinds 1 and 2 hold the whole row in this pass (k <= 64)
+      const bool shift_free = a.compress != 0 && row_one_sign(j >= 0, s);
+      gsum += shift_free ? 0.f : gsc;
+    }
 
     // dQ partials: group g sums its edges (absent edges carry gsc = 0)
 #pragma unroll
@@ -318,13 +341,17 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
       const float gg = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * i + g) << 2, __float_as_int(gsc)));
       // absent edges read out of range (zeros, no traffic)
       const uint32_t koff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ldk * 4u : kOobOffset;
+      // MH: slots of other heads read out of range (zeros)
+      auto mine = [&](int m) { return !MH || hslot[m] == hg[MH ? i : 0]; };
       if (kvec) {
-        fma4(dqa, gg, buf_load4(rs_key, 4 * c < a.r ? koff + 16u * c : kOobOffset));
-        if (a.r > 64) fma4(dqb, gg, buf_load4(rs_key, 64 + 4 * c < a.r ? koff + 256u + 16u * c : kOobOffset));
+        fma4(dqa, gg, buf_load4(rs_key, (4 * c < a.r && mine(0)) ? koff + 16u * c : kOobOffset));
+        if (a.r > 64)
+          fma4(dqb, gg, buf_load4(rs_key, (64 + 4 * c < a.r && mine(1)) ? koff + 256u + 16u * c : kOobOffset));
       } else {
 #pragma unroll
         for (int m = 0; m < 8; ++m)
-          if (16 * m < a.r) dqs[m] += gg * buf_load1(rs_key, c + 16 * m < a.r ? koff + 4u * (c + 16 * m) : kOobOffset);
+          if (16 * m < a.r)
+            dqs[m] += gg * buf_load1(rs_key, (c + 16 * m < a.r && mine(m)) ? koff + 4u * (c + 16 * m) : kOobOffset);
       }
       if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
     }
@@ -361,16 +388,26 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
       if ((m & 3) == g && rr < a.r) dqrow[rr] = dqs[m] * (a.qscale ? a.qscale[rr] : 1.f);
     }
   }
-  gsum = wave_sum(gsum);
-  if (lane == 0) a.rowsum_gs[row] = gsum;
+  if constexpr (MH) {
+    for (int h = 0; h < a.heads; ++h) {  // uniform
+      float t = 0.f;
+#pragma unroll
+      for (int q = 0; q < kMaxHeads; ++q) t = (q == h) ? hsum[q] : t;
+      t = wave_sum(t);
+      if (lane == 0) a.rowsum_gs[row * a.heads + h] = t;
+    }
+  } else {
+    gsum = wave_sum(gsum);
+    if (lane == 0) a.rowsum_gs[row] = gsum;
+  }
 }
 
-template <int W, int NV, bool SPLIT = false>
+template <int W, int NV, bool SPLIT = false, bool MH = false>
 static void launch_rows_bwd_kp(const RowsBwdArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 8, SPLIT>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 16) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 16, SPLIT>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 32) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 32, SPLIT>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((rows_backward_kernel<W, NV, 64, SPLIT>), grid, dim3(256), 0, stream, a);
+  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 8, SPLIT, MH>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 16) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 16, SPLIT, MH>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 32) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 32, SPLIT, MH>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((rows_backward_kernel<W, NV, 64, SPLIT, MH>), grid, dim3(256), 0, stream, a);
 }
 
 template <int NV>
@@ -401,6 +438,18 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
   const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0);
   dim3 grid((unsigned)blocks);
+  if (a.heads > 1) {
+    JN_REQUIRE(a.ehead && a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r, kInvalidArgument,
+               "multi-head row backward needs edge heads and %d..%d heads of equal rank", 2, kMaxHeads);
+    JN_PROFILE("rows_backward_kernel", stream);
+    if (!vec) launch_rows_bwd_kp<1, 4, false, true>(a, grid, stream);
+    else if (a.D > 256) launch_rows_bwd_kp<4, 8, false, true>(a, grid, stream);
+    else if (a.D > 128) launch_rows_bwd_kp<4, 4, false, true>(a, grid, stream);
+    else if (a.D > 64) launch_rows_bwd_kp<4, 2, false, true>(a, grid, stream);
+    else launch_rows_bwd_kp<4, 1, false, true>(a, grid, stream);
+    JN_LAUNCH_CHECK();
+    return kOk;
+  }
   const int slab = rows_backward_slab(a.Nk, a.D, vec);
   if (slab) {
     {
@@ -533,7 +582,8 @@ __global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs a) {
         const float cf = a.coef ? a.coef[eid] : 0.f;
         const float gs = a.g_score ? a.g_score[eid] : 0.f;
         const float cd = a.gds ? cf * a.gds[row] : 0.f;
-        a.rec[batch_base + pos] = make_float4(__int_as_float(row), cf, gs, cd);
+        const int hd = a.ehead ? (int)a.ehead[eid] << kRecHeadShift : 0;
+        a.rec[batch_base + pos] = make_float4(__int_as_float(row | hd), cf, gs, cd);
       }
     }
     __syncthreads();
@@ -543,6 +593,8 @@ __global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs a) {
 int launch_csr(const CsrArgs& a, hipStream_t stream) {
   const int T = (a.Nq + kCsrTile - 1) / kCsrTile;
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
+  JN_REQUIRE((int64_t)a.B * a.Nq <= kRecRowMask, kUnsupported,
+             "edge records hold rows below 2^%d (B * rows = %lld)", kRecHeadShift, (long long)a.B * a.Nq);
   dim3 g2(T, a.B);
   {
     JN_PROFILE("csr_count_kernel", stream);
@@ -607,7 +659,7 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
     float cf = 0.f, cd = 0.f;
     if (lane < n) {
       const float4 r = rec[q0 + lane];
-      row = __float_as_int(r.x);
+      row = __float_as_int(r.x) & kRecRowMask;
       cf = r.y;
       cd = r.w;
     }
@@ -651,7 +703,8 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
 // turns broadcasting theirs (ds_bpermute), so the 4 columns of a wave advance
 // together.  The scale-vector partials of the 16 columns are summed in a fixed
 // order into one row of part_c per workgroup.
-template <bool VEC>
+// MH: each record's head (its row word's top bits) selects the ranks it reaches.
+template <bool VEC, bool MH>
 __global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
   __shared__ float red[4][128];
   const int lane = lane_id(), g = lane >> 4, c = lane & 15, w = wave_id();
@@ -671,6 +724,11 @@ __global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
   int rk[8];  // rank of each slot
 #pragma unroll
   for (int m = 0; m < 8; ++m) rk[m] = VEC ? (m < 4 ? 4 * c + m : 64 + 4 * c + (m - 4)) : c + 16 * m;
+  int hk[8];  // MH: head of each slot (a float4 never straddles two heads: head_rank % 4 == 0 with VEC)
+  if constexpr (MH) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) hk[m] = rk[m] / a.head_rank;
+  }
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   // wave-uniform trip count: the longest of the wave's four columns
   const int wlen = max(max(readlane_i(len, 0), readlane_i(len, 16)), max(readlane_i(len, 32), readlane_i(len, 48)));
@@ -689,20 +747,23 @@ __global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int src = (g * 16 + ((u0 + u) & 15)) << 2;
-        const int rw = __builtin_amdgcn_ds_bpermute(src, row);
+        const int rw_word = __builtin_amdgcn_ds_bpermute(src, row);
         gg[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(gs)));
-        const bool ok = (u0 + u < nu) && rw >= 0;  // past the column's end: row -1, gs 0
+        const bool ok = (u0 + u < nu) && rw_word >= 0;  // past the column's end: row -1, gs 0
+        const int rw = MH ? (rw_word & kRecRowMask) : rw_word;
+        const int eh = MH ? (rw_word >> kRecHeadShift) : 0;
+        auto mine = [&](int m) { return !MH || hk[m] == eh; };
         const float* qr = a.q + (int64_t)(ok ? rw : 0) * a.ldq;
         if (VEC) {
-          const float4 lo = (ok && 4 * c < a.r) ? *reinterpret_cast<const float4*>(qr + 4 * c)
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
-          const float4 hi = (ok && 64 + 4 * c < a.r) ? *reinterpret_cast<const float4*>(qr + 64 + 4 * c)
-                                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+          const float4 lo = (ok && 4 * c < a.r && mine(0)) ? *reinterpret_cast<const float4*>(qr + 4 * c)
+                                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+          const float4 hi = (ok && 64 + 4 * c < a.r && mine(4)) ? *reinterpret_cast<const float4*>(qr + 64 + 4 * c)
+                                                                : make_float4(0.f, 0.f, 0.f, 0.f);
           qv[u][0] = lo.x; qv[u][1] = lo.y; qv[u][2] = lo.z; qv[u][3] = lo.w;
           qv[u][4] = hi.x; qv[u][5] = hi.y; qv[u][6] = hi.z; qv[u][7] = hi.w;
         } else {
 #pragma unroll
-          for (int m = 0; m < 8; ++m) qv[u][m] = (ok && rk[m] < a.r) ? qr[rk[m]] : 0.f;
+          for (int m = 0; m < 8; ++m) qv[u][m] = (ok && rk[m] < a.r && mine(m)) ? qr[rk[m]] : 0.f;
         }
       }
 #pragma unroll
@@ -761,12 +822,22 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
     JN_LAUNCH_CHECK();
   }
   if (a.q) {
-    const bool vec = (a.r % 4 == 0) && (a.ldq % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0);
+    const bool mh = a.heads > 1;
+    JN_REQUIRE(!mh || (a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r), kInvalidArgument,
+               "multi-head column backward needs 2..%d heads of equal rank", kMaxHeads);
+    const bool vec = (a.r % 4 == 0) && (a.ldq % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                     (!mh || a.head_rank % 4 == 0);
     const int64_t blocks = cols_backward_parts(total_cols);
     JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
     JN_PROFILE("cols_keygrad_kernel", stream);
-    if (vec) hipLaunchKernelGGL(cols_keygrad_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(cols_keygrad_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    const dim3 grid((unsigned)blocks);
+    if (mh) {
+      if (vec) hipLaunchKernelGGL((cols_keygrad_kernel<true, true>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((cols_keygrad_kernel<false, true>), grid, dim3(256), 0, stream, a);
+    } else {
+      if (vec) hipLaunchKernelGGL((cols_keygrad_kernel<true, false>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((cols_keygrad_kernel<false, false>), grid, dim3(256), 0, stream, a);
+    }
     JN_LAUNCH_CHECK();
   }
   return kOk;
@@ -775,17 +846,19 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 // Reduction of the small gradients (scale vector, bias) in two fixed-order
 // stages: kFinBlocks workgroups each reduce a contiguous share of the [nparts, r]
-// partials and of the row sums into stage[blk, 0..r]; then workgroup b <= r sums
-// column b of stage over the kFinBlocks rows.
+// partials and of the [nrows, nbias] row sums into stage[blk, 0..r + nbias);
+// then workgroup b < r + nbias sums column b of stage over the kFinBlocks rows.
 // ---------------------------------------------------------------------------
 constexpr int kFinBlocks = 256;
 
-size_t finalize_stage_floats(int r) { return (size_t)kFinBlocks * (r + 1); }
+size_t finalize_stage_floats(int r, int nbias) { return (size_t)kFinBlocks * (r + nbias); }
 
 __global__ __launch_bounds__(256) void finalize_partials_kernel(const float* part_c, int nparts, int r,
-                                                                const float* rowsum, int64_t nrows, float* stage) {
+                                                                const float* rowsum, int64_t nrows, int nbias,
+                                                                float* stage) {
   __shared__ float red[256];
   const int t = threadIdx.x, blk = blockIdx.x;
+  const int64_t width = r + nbias;
   // r_pad columns (power of two >= r, <= 128) x 256 / r_pad row lanes
   int r_pad = 1;
   while (r_pad < r) r_pad <<= 1;
@@ -800,25 +873,28 @@ __global__ __launch_bounds__(256) void finalize_partials_kernel(const float* par
     if (t < o) red[t] += red[t + o];
     __syncthreads();
   }
-  if (t < r) stage[(int64_t)blk * (r + 1) + t] = red[t];
-  __syncthreads();
+  if (t < r) stage[blk * width + t] = red[t];
   const int64_t i0 = nrows * blk / kFinBlocks, i1 = nrows * (blk + 1) / kFinBlocks;
-  float q = 0.f;
-  for (int64_t i = i0 + t; i < i1; i += 256) q += rowsum[i];
-  red[t] = q;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (t < o) red[t] += red[t + o];
+  for (int h = 0; h < nbias; ++h) {
     __syncthreads();
+    float q = 0.f;
+    for (int64_t i = i0 + t; i < i1; i += 256) q += rowsum[i * nbias + h];
+    red[t] = q;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+      if (t < o) red[t] += red[t + o];
+      __syncthreads();
+    }
+    if (t == 0) stage[blk * width + r + h] = red[0];
   }
-  if (t == 0) stage[(int64_t)blk * (r + 1) + r] = red[0];
 }
 
-__global__ __launch_bounds__(256) void finalize_small_grads_kernel(const float* stage, int r, float* grad_c,
-                                                                   int accumulate_c, float* grad_bias) {
+__global__ __launch_bounds__(256) void finalize_small_grads_kernel(const float* stage, int r, int nbias,
+                                                                   float* grad_c, int accumulate_c,
+                                                                   float* grad_bias) {
   __shared__ float red[256];
   const int b = blockIdx.x, t = threadIdx.x;
-  red[t] = stage[(int64_t)t * (r + 1) + b];  // kFinBlocks == blockDim.x rows
+  red[t] = stage[(int64_t)t * (r + nbias) + b];  // kFinBlocks == blockDim.x rows
   __syncthreads();
   for (int o = 128; o > 0; o >>= 1) {
     if (t < o) red[t] += red[t + o];
@@ -828,25 +904,26 @@ __global__ __launch_bounds__(256) void finalize_small_grads_kernel(const float* 
     if (b < r) {
       if (grad_c) grad_c[b] = accumulate_c ? grad_c[b] + red[0] : red[0];
     } else if (grad_bias) {
-      grad_bias[0] = red[0];
+      grad_bias[b - r] = red[0];
     }
   }
 }
 
 int launch_finalize_small_grads(const float* part_c, int nparts, int r, float* grad_c, int accumulate_c,
                                 const float* rowsum, int64_t nrows, float* grad_bias, float* stage,
-                                hipStream_t stream) {
+                                hipStream_t stream, int nbias) {
   JN_REQUIRE(r >= 1 && r <= 128, kUnsupported, "rank must be in [1, 128]");
+  JN_REQUIRE(nbias >= 1 && nbias <= kMaxHeads, kUnsupported, "1..%d bias columns", kMaxHeads);
   static_assert(kFinBlocks == 256, "the second stage maps one thread per stage row");
   {
     JN_PROFILE("finalize_partials_kernel", stream);
     hipLaunchKernelGGL(finalize_partials_kernel, dim3(kFinBlocks), dim3(256), 0, stream, part_c, nparts, r, rowsum,
-                       nrows, stage);
+                       nrows, nbias, stage);
     JN_LAUNCH_CHECK();
   }
   JN_PROFILE("finalize_small_grads_kernel", stream);
-  hipLaunchKernelGGL(finalize_small_grads_kernel, dim3(r + 1), dim3(256), 0, stream, stage, r, grad_c, accumulate_c,
-                     grad_bias);
+  hipLaunchKernelGGL(finalize_small_grads_kernel, dim3(r + nbias), dim3(256), 0, stream, stage, r, nbias, grad_c,
+                     accumulate_c, grad_bias);
   JN_LAUNCH_CHECK();
   return kOk;
 }

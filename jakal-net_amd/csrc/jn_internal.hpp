@@ -24,6 +24,10 @@ struct SelectArgs {
   // and one key exponent per batch element
   const uint16_t* split_key;
   const int* split_exp;
+  // Multi-head max aggregation (heads > 1): r = heads * head_rank ranks, head h
+  // owning ranks [h * head_rank, (h + 1) * head_rank) of q, key and scale; bias
+  // is [heads] or null.  A pair's score is max_h (dot_h + bias[h]) / T.
+  int heads, head_rank;
 };
 int launch_topk_select(const SelectArgs& a, hipStream_t stream);
 constexpr int kSelectMaxK = 64;
@@ -48,6 +52,12 @@ constexpr int kSelectF32 = 1;
 int select_mode();
 void set_select_mode(int mode);
 size_t select_workspace_bytes(int64_t B, int64_t Nk, int64_t r);
+// Multi-head: each head's ranks padded to whole 32-rank MFMA K-steps.
+size_t select_workspace_bytes_heads(int64_t B, int64_t Nk, int64_t head_rank, int64_t heads);
+// Heads per pair score (all kernels); the select takes at most 4 K-steps of 32
+// ranks over all heads (heads * ceil(head_rank / 32) <= 4).
+constexpr int kMaxHeads = 8;
+bool select_heads_fit(int64_t head_rank, int64_t heads);
 
 // ---- fp32 MFMA GEMMs (jn_gemm.hip) ----------------------------------------
 int gemm_project(const float* X, int64_t ldx, const float* W0, const float* W1, int split, int64_t ldw, float* C,
@@ -138,7 +148,12 @@ struct RowsBwdArgs {
   float* coef;            // [rows, k]
   float* dq;              // [rows, r], row stride lddq
   int64_t lddq;
-  float* rowsum_gs;       // [rows]
+  float* rowsum_gs;       // [rows] ([rows, heads] with heads > 1)
+  // Multi-head (heads > 1): edge e's score is head ehead[e]'s, so its gradient
+  // reaches only that head's ranks [h * head_rank, (h + 1) * head_rank) of dq
+  // and its bias partial column h.
+  const uint8_t* ehead;   // [rows, k]
+  int heads, head_rank;
 };
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream);
 
@@ -153,9 +168,13 @@ struct WindowScoreArgs {
   const float* bias;     // scalar or null
   float inv_temperature; // score = (dot + bias) * inv_temperature
   int B, Nq, Nk, r, width;
-  int all_keys;
+  int all_keys;          // 2: the edge list idx is given (only the heads are written)
   int32_t* idx;          // [B*Nq, width]
   float* score;          // [B*Nq, width]
+  // Multi-head (heads > 1): score = max_h (dot_h + bias[h]) * inv_temperature
+  // over head rank slices of head_rank; head[e] = the first head attaining it.
+  int heads, head_rank;
+  uint8_t* head;         // [B*Nq, width] or null
 };
 int launch_window_scores(const WindowScoreArgs& a, hipStream_t stream);
 
@@ -187,7 +206,9 @@ struct RouteRowsBwdArgs {
   int64_t ld_gpv;
   float* dq;             // [rows, r], stride lddq
   int64_t lddq;
-  float* rowsum;         // [rows]
+  float* rowsum;         // [rows] ([rows, heads] with heads > 1)
+  const uint8_t* ehead;  // multi-head: [rows, k] head of each edge (see RowsBwdArgs)
+  int heads, head_rank;
 };
 int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream);
 
@@ -220,14 +241,20 @@ struct CsrArgs {
   int B, Nq, Nk;
   int32_t* tile_base;  // [B, T, Nk]: per-tile counts, then exclusive bases
   int32_t* seg_start;  // [B, Nk + 1]
-  // [B * Nq * k] edge records grouped by key: {row (int bits), coef[e],
-  // g_score[e], coef[e] * gds[row]}; a null source pointer gives 0
+  // [B * Nq * k] edge records grouped by key: {row | head << kRecHeadShift
+  // (int bits), coef[e], g_score[e], coef[e] * gds[row]}; a null source
+  // pointer gives 0
   float4* rec;
   const float* coef;     // [B * Nq, k] or null
   const float* g_score;  // [B * Nq, k] or null
   const float* gds;      // [B * Nq] or null
+  const uint8_t* ehead;  // [B * Nq, k] head of each edge, or null (head 0)
 };
 constexpr int kCsrTile = 64;
+// An edge record's first word holds its row below bit kRecHeadShift and its
+// head above (multi-head scores), so rows stay below 2^27.
+constexpr int kRecHeadShift = 27;
+constexpr int kRecRowMask = (1 << kRecHeadShift) - 1;
 int launch_csr(const CsrArgs& a, hipStream_t stream);
 
 struct ColsBwdArgs {
@@ -249,13 +276,17 @@ struct ColsBwdArgs {
   int64_t lddk;
   float* part_c;             // [cols_backward_parts(B*Nk), r] or null
   const char* profile_name;  // label for the gather's kernel timer (null: "cols_gather_kernel")
+  // Multi-head (heads > 1): a record's g_score reaches only its head's ranks of dk.
+  int heads, head_rank;
 };
 int cols_backward_parts(int64_t total_cols);
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream);
 
-size_t finalize_stage_floats(int r);
+// Scale-vector and bias gradients: grad_c[r] from the [nparts, r] partials,
+// grad_bias[nbias] from the [nrows, nbias] row sums (column h: head h's bias).
+size_t finalize_stage_floats(int r, int nbias = 1);
 int launch_finalize_small_grads(const float* part_c, int nparts, int r, float* grad_c, int accumulate_c,
                                 const float* rowsum, int64_t nrows, float* grad_bias, float* stage,
-                                hipStream_t stream);
+                                hipStream_t stream, int nbias = 1);
 
 }  // namespace jakal

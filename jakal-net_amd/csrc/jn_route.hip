@@ -20,7 +20,8 @@
 //       grad rho[j] = sum_e p[e] * g_c[e]
 //       g_l[e]   = compress backward of rho * g_c, times 1/T
 //       dQ[j, r] = qscale[r] * sum_e g_l[e] * key[k, r]
-//       rowsum[j] = sum_e g_l[e]   (bias gradient partial)
+//       rowsum[j] = sum_e g_l[e]   (bias gradient partial; per head with
+//                   multi-head logits, whose dQ reaches each edge's head only)
 #include "jn_internal.hpp"
 
 namespace jakal {
@@ -71,7 +72,9 @@ int launch_route_coef(const int32_t* idx, const float* logit, const float* rho, 
 // One wavefront per source row; its four 16-lane groups take four edges at a
 // time (group g takes edges 4i + g) and read whole destination gradient rows
 // with 16-byte buffer loads.
-template <int W, int NV, int KP>
+// MH: multi-head logits (a.heads > 1): edge e's gradient reaches only the ranks
+// of its head a.ehead[e] in dq, and the bias partials are per head.
+template <int W, int NV, int KP, bool MH>
 __global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdArgs a) {
   constexpr int NI = KP / 4;
   constexpr int P = 16 * W * NV;
@@ -87,13 +90,16 @@ __global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdAr
   const float* gdsb = a.gds + b * a.Nd;
   const float ps_row = a.ps[row];
   const float rho = a.rho[row];
-  const bool kvec = (a.r % 4 == 0) && (a.ldk % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.key) & 15) == 0);
+  const bool kvec = (a.r % 4 == 0) && (a.ldk % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.key) & 15) == 0) &&
+                    (!MH || a.head_rank % 4 == 0);
 
   int j = -1;
   float s = 0.0f;
+  int eh = 0;
   if (lane < a.k) {
     j = a.idx[row * a.k + lane];
     if (j >= 0) s = a.logit[row * a.k + lane];
+    if (MH && j >= 0) eh = a.ehead[row * a.k + lane];
   }
   const float p = route_probability(j, s, a.compress);
   const float cf = rho * p;
@@ -179,28 +185,47 @@ __global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdAr
   }
   gl = j >= 0 ? gl * a.inv_temperature : 0.f;
   if (lane < a.k) a.g_logit[row * a.k + lane] = gl;
-  // one-sign rows of the signed compressions: exactly 0 (softmax rows are not summed at all)
-  const float gsum = (a.compress != 0 && row_one_sign(j >= 0, s)) ? 0.f : wave_sum(gl);
+  if constexpr (MH) {
+    // per-head bias partials (a shift of one head's logits is no shift of the row)
+    for (int h = 0; h < a.heads; ++h) {  // uniform
+      const float t = wave_sum(eh == h ? gl : 0.f);
+      if (lane == 0) a.rowsum[row * a.heads + h] = t;
+    }
+  } else {
+    // one-sign rows of the signed compressions: exactly 0 (softmax rows are not summed at all)
+    const float gsum = (a.compress != 0 && row_one_sign(j >= 0, s)) ? 0.f : wave_sum(gl);
+    if (lane == 0) a.rowsum[row] = gsum;
+  }
   if (lane == 0) {
     if (a.grad_ps) a.grad_ps[row] = gps;
     if (a.grad_rho) a.grad_rho[row] = grho;
-    a.rowsum[row] = gsum;
   }
 
   // dQ partials: group g sums its edges (absent edges read zeros)
   float4 dqa = make_float4(0.f, 0.f, 0.f, 0.f), dqb = dqa;
   float dqs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // MH: head of each rank slot of this lane (kvec: slots 4c and 64 + 4c; scalar: c + 16m)
+  int hslot[8];
+  if constexpr (MH) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) hslot[m] = (kvec ? (m == 0 ? 4 * c : 64 + 4 * c) : c + 16 * m) / a.head_rank;
+  }
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const float gg = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * i + g) << 2, __float_as_int(gl)));
     const uint32_t koff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ldk * 4u : kOobOffset;
+    const int hgi = MH ? __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, eh) : 0;
+    // MH: slots of other heads read out of range (zeros)
+    auto mine = [&](int m) { return !MH || hslot[m] == hgi; };
     if (kvec) {
-      fma4(dqa, gg, buf_load4(rs_key, 4 * c < a.r ? koff + 16u * c : kOobOffset));
-      if (a.r > 64) fma4(dqb, gg, buf_load4(rs_key, 64 + 4 * c < a.r ? koff + 256u + 16u * c : kOobOffset));
+      fma4(dqa, gg, buf_load4(rs_key, (4 * c < a.r && mine(0)) ? koff + 16u * c : kOobOffset));
+      if (a.r > 64)
+        fma4(dqb, gg, buf_load4(rs_key, (64 + 4 * c < a.r && mine(1)) ? koff + 256u + 16u * c : kOobOffset));
     } else {
 #pragma unroll
       for (int m = 0; m < 8; ++m)
-        if (16 * m < a.r) dqs[m] += gg * buf_load1(rs_key, c + 16 * m < a.r ? koff + 4u * (c + 16 * m) : kOobOffset);
+        if (16 * m < a.r)
+          dqs[m] += gg * buf_load1(rs_key, (c + 16 * m < a.r && mine(m)) ? koff + 4u * (c + 16 * m) : kOobOffset);
     }
     if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
   }
@@ -235,12 +260,21 @@ __global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdAr
   }
 }
 
-template <int W, int NV>
+template <int W, int NV, bool MH>
 static void launch_route_bwd_kp(const RouteRowsBwdArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.k <= 8) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 8>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 16) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 16>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 32) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 32>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 64>), grid, dim3(256), 0, stream, a);
+  if (a.k <= 8) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 8, MH>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 16) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 16, MH>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 32) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 32, MH>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 64, MH>), grid, dim3(256), 0, stream, a);
+}
+
+template <bool MH>
+static void launch_route_bwd(const RouteRowsBwdArgs& a, bool vec, dim3 grid, hipStream_t stream) {
+  if (!vec) launch_route_bwd_kp<1, 4, MH>(a, grid, stream);
+  else if (a.D > 256) launch_route_bwd_kp<4, 8, MH>(a, grid, stream);
+  else if (a.D > 128) launch_route_bwd_kp<4, 4, MH>(a, grid, stream);
+  else if (a.D > 64) launch_route_bwd_kp<4, 2, MH>(a, grid, stream);
+  else launch_route_bwd_kp<4, 1, MH>(a, grid, stream);
 }
 
 int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream) {
@@ -257,12 +291,12 @@ int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream) {
                    (a.grad_pv == nullptr ||
                     ((a.ld_gpv % 4 == 0) && (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0));
   dim3 grid((unsigned)blocks);
+  const bool mh = a.heads > 1;
+  JN_REQUIRE(!mh || (a.ehead && a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r),
+             kInvalidArgument, "multi-head route backward needs edge heads and 2..%d heads of equal rank", kMaxHeads);
   JN_PROFILE("route_rows_backward_kernel", stream);
-  if (!vec) launch_route_bwd_kp<1, 4>(a, grid, stream);
-  else if (a.D > 256) launch_route_bwd_kp<4, 8>(a, grid, stream);
-  else if (a.D > 128) launch_route_bwd_kp<4, 4>(a, grid, stream);
-  else if (a.D > 64) launch_route_bwd_kp<4, 2>(a, grid, stream);
-  else launch_route_bwd_kp<4, 1>(a, grid, stream);
+  if (mh) launch_route_bwd<true>(a, vec, grid, stream);
+  else launch_route_bwd<false>(a, vec, grid, stream);
   JN_LAUNCH_CHECK();
   return kOk;
 }

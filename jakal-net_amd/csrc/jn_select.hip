@@ -520,9 +520,12 @@ __global__ __launch_bounds__(256) void select_split_absmax_kernel(const float* _
 // Writes the split rows of [64 blk, 64 blk + 64) and, from block 0, the batch
 // element's key exponent.  Every block reduces the same partials in the same
 // order, so all agree on the exponent.
+// Split position c of a row holds rank h * head_rank + (c - h * head_rp) of head
+// h = c / head_rp (zero past head_rank): each head starts on a whole K-step.
+// One head: head_rank = r, head_rp = RP.
 __global__ __launch_bounds__(256) void select_split_keys_kernel(const float* __restrict__ key, int64_t ldk,
-                                                                int64_t kbs, int Nk, int r, int RP, int nblk,
-                                                                const float* __restrict__ partial,
+                                                                int64_t kbs, int Nk, int head_rank, int head_rp,
+                                                                int RP, int nblk, const float* __restrict__ partial,
                                                                 _Float16* __restrict__ split, int* __restrict__ kexp) {
   const int blk = blockIdx.x, b = blockIdx.y;
   float m = 0.0f;
@@ -536,7 +539,8 @@ __global__ __launch_bounds__(256) void select_split_keys_kernel(const float* __r
   for (int e = threadIdx.x; e < rows * RP; e += 256) {
     const int row = e / RP;
     const int c = e - row * RP;
-    const float x = c < r ? ldexpf(kb[(int64_t)row * ldk + c], ek) : 0.0f;
+    const int h = c / head_rp, cc = c - h * head_rp;
+    const float x = cc < head_rank ? ldexpf(kb[(int64_t)row * ldk + h * head_rank + cc], ek) : 0.0f;
     const _Float16 hi = (_Float16)x;
     out[(int64_t)row * 2 * RP + c] = hi;
     out[(int64_t)row * 2 * RP + RP + c] = (_Float16)(x - (float)hi);
@@ -566,7 +570,11 @@ __device__ __forceinline__ halfx8 as_halfx8(float a, float b, float c, float d) 
 // each keeps the exact top-k of its quarter, and a 64-entry sort per row
 // merges the four lists at the end.  Four times the workgroups and a quarter
 // of the serial chunk chain per wave.
-template <int RQ, bool VEC, int KEEP, int KS, int CW>
+// MH (split keys, per-wave form only): multi-head max aggregation.  Head h owns
+// K-steps [h * head_ks, (h + 1) * head_ks) of the split rows; after a head's
+// last K-step its scores, unscaled and with its bias, are folded into a
+// running maximum, so the filter and merges see max_h (dot_h + bias[h]) / T.
+template <int RQ, bool VEC, int KEEP, int KS, int CW, bool MH = false>
 __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
                              CW == 8 ? 1 : CW == 4 ? 2 : ((KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2)) void lowrank_topk_select_kernel(SelectArgs a) {
   constexpr bool COOP = CW > 0;
@@ -582,6 +590,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   constexpr int SLOTS = COOP ? CW * kSelRowsPerWave : kSelRows;  // row slots (16 per wave)
   static_assert(!KSP || KEEP == 48, "the key-split form serves k <= 16");
   static_assert(!COOP || (KS >= 1 && KS <= 2), "the cooperative select stages split keys of rank <= 64");
+  static_assert(!MH || (SPLIT && CW == 0), "multi-head scores run on the per-wave split kernel");
   // staged chunk: kSelChunk split rows of 2 RP halves plus 8 halves of padding,
   // so the 16 rows one fragment read touches start 68 dwords apart (4 banks)
   constexpr int KROW = 2 * RP + 8;
@@ -633,21 +642,30 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   // Split path: ranks 32 s + 8 g + e (K-step s, e < 8), as hi/lo halves, and
   // the row's score exponent E: MFMA results are the scores times 2^E.
   constexpr int QN = SPLIT ? 8 * KS : RQ;
+  // MH: K-steps per head (each head's ranks padded to whole K-steps)
+  const int head_ks = MH ? (a.head_rank + 31) / 32 : KS;
+  // source rank of fragment slot s, or -1 for padding
+  auto qrank = [&](int s) {
+    if constexpr (MH) {
+      const int ks = s / 8, h = ks / head_ks, c = 32 * (ks - h * head_ks) + 8 * g + (s % 8);
+      return (h < a.heads && c < a.head_rank) ? h * a.head_rank + c : -1;
+    } else {
+      const int rr = SPLIT ? 32 * (s / 8) + 8 * g + (s % 8) : g * RQ + s;
+      return rr < a.r ? rr : -1;
+    }
+  };
   float qf[QN];
   {
     const float* qrow = qb + (int64_t)(row_ok ? my_row : 0) * a.ldq;
     float qs[QN];
 #pragma unroll
     for (int s = 0; s < QN; ++s) {
-      const int rr = SPLIT ? 32 * (s / 8) + 8 * g + (s % 8) : g * RQ + s;
-      qf[s] = qrow[rr < a.r ? rr : 0];
-      qs[s] = a.scale ? a.scale[rr < a.r ? rr : 0] : 1.0f;
+      const int rr = qrank(s);
+      qf[s] = qrow[rr >= 0 ? rr : 0];
+      qs[s] = a.scale ? a.scale[rr >= 0 ? rr : 0] : 1.0f;
     }
 #pragma unroll
-    for (int s = 0; s < QN; ++s) {
-      const int rr = SPLIT ? 32 * (s / 8) + 8 * g + (s % 8) : g * RQ + s;
-      qf[s] = (row_ok && rr < a.r) ? qf[s] * qs[s] : 0.0f;
-    }
+    for (int s = 0; s < QN; ++s) qf[s] = (row_ok && qrank(s) >= 0) ? qf[s] * qs[s] : 0.0f;
   }
   halfx8 qh[SPLIT ? KS : 1], ql[SPLIT ? KS : 1];
   int score_exp = 0;  // E (split path)
@@ -677,7 +695,20 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   // Split path without bias or temperature: rows are filtered and merged on
   // the scaled scores (scaling a row by 2^E keeps its order and its ties) and
   // only the k winners are scaled back.
-  const bool scaled_domain = SPLIT && inv_temp == 1.0f && bias == 0.0f;
+  const bool scaled_domain = !MH && SPLIT && inv_temp == 1.0f && bias == 0.0f;
+  // MH: K-step s closes head (s + 1) / head_ks - 1 when fold bit s is set;
+  // fold_bias[s] is that head's bias
+  uint32_t fold_bits = 0;
+  float fold_bias[MH ? KS : 1];
+  if constexpr (MH) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const bool closes = (s + 1) % head_ks == 0;
+      const int h = (s + 1) / head_ks - 1;
+      fold_bits |= closes ? (1u << s) : 0u;
+      fold_bias[s] = (closes && a.bias && h < a.heads) ? a.bias[h] : 0.0f;
+    }
+  }
 
   // ---- key fragments straight from memory: every wave streams the keys on its
   // own (no LDS staging, no workgroup barrier in the loop), so a wave that
@@ -780,6 +811,11 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
 #pragma unroll
     for (int t = 0; t < kSelTiles; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
     if constexpr (SPLIT) {
+      floatx4 best[MH ? kSelTiles : 1];
+      if constexpr (MH) {
+#pragma unroll
+        for (int t = 0; t < kSelTiles; ++t) best[t] = floatx4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      }
       // small products first: lo.hi + hi.lo, then hi.hi
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
@@ -796,6 +832,21 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
           const halfx8 kh = as_halfx8(kx[S][t][8 * s], kx[S][t][8 * s + 1], kx[S][t][8 * s + 2], kx[S][t][8 * s + 3]);
           acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[s], acc[t], 0, 0, 0);
         }
+        if constexpr (MH) {
+          if ((fold_bits >> s) & 1u) {  // uniform: the last K-step of a head
+#pragma unroll
+            for (int t = 0; t < kSelTiles; ++t) {
+#pragma unroll
+              for (int v = 0; v < 4; ++v)
+                best[t][v] = fmaxf(best[t][v], (ldexpf(acc[t][v], -score_exp) + fold_bias[s]) * inv_temp);
+              acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+          }
+        }
+      }
+      if constexpr (MH) {
+#pragma unroll
+        for (int t = 0; t < kSelTiles; ++t) acc[t] = best[t];
       }
     } else {
 #pragma unroll
@@ -809,18 +860,20 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
     float sc[kSelLaneKeys];
 #pragma unroll
     for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = acc[u >> 2][u & 3];
-    if (SPLIT && !scaled_domain) {  // uniform
+    if constexpr (!MH) {  // multi-head scores are final after the fold
+      if (SPLIT && !scaled_domain) {  // uniform
 #pragma unroll
-      for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = ldexpf(sc[u], -score_exp);
-    }
-    if (scaled_domain) {
-      // compared as they are
-    } else if (inv_temp != 1.0f) {  // uniform
+        for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = ldexpf(sc[u], -score_exp);
+      }
+      if (scaled_domain) {
+        // compared as they are
+      } else if (inv_temp != 1.0f) {  // uniform
 #pragma unroll
-      for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = (sc[u] + bias) * inv_temp;
-    } else if (bias != 0.0f) {
+        for (int u = 0; u < kSelLaneKeys; ++u) sc[u] = (sc[u] + bias) * inv_temp;
+      } else if (bias != 0.0f) {
 #pragma unroll
-      for (int u = 0; u < kSelLaneKeys; ++u) sc[u] += bias;
+        for (int u = 0; u < kSelLaneKeys; ++u) sc[u] += bias;
+      }
     }
     if (c0 + kSelChunk > key_end) {  // uniform: only the last chunk holds padding keys
 #pragma unroll
@@ -1035,6 +1088,14 @@ static void launch_rq(const SelectArgs& a, bool vec, dim3 grid, hipStream_t stre
   }
 }
 
+template <int KS>
+static void launch_split_heads(const SelectArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.k <= 32)
+    hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, 0, true>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS, 0, true>), grid, dim3(256), 0, stream, a);
+}
+
 template <int KS, int CW>
 static void launch_split(const SelectArgs& a, dim3 grid, hipStream_t stream) {
   const dim3 block(CW > 0 ? CW * kWave : 256);
@@ -1088,6 +1149,16 @@ size_t select_workspace_bytes(int64_t B, int64_t Nk, int64_t r) {
   return carve_select(nullptr, 0, B, Nk, r).bytes;
 }
 
+bool select_heads_fit(int64_t head_rank, int64_t heads) {
+  return heads >= 2 && heads <= kMaxHeads && head_rank >= 1 && heads * split_ranks(head_rank) <= 128;
+}
+
+size_t select_workspace_bytes_heads(int64_t B, int64_t Nk, int64_t head_rank, int64_t heads) {
+  if (heads <= 1) return select_workspace_bytes(B, Nk, head_rank);
+  if (!select_heads_fit(head_rank, heads)) return 0;
+  return select_workspace_bytes(B, Nk, heads * split_ranks(head_rank));
+}
+
 int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   SelectArgs a = a_in;
   JN_REQUIRE(a.k >= 1 && a.k <= kSelectMaxK, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)", kSelectMaxK,
@@ -1102,13 +1173,19 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   const int64_t blocks = (int64_t)tiles * a.B;
   JN_REQUIRE(blocks > 0 && blocks < (1LL << 31), kInvalidArgument, "bad grid size");
   dim3 grid((unsigned)blocks);
-  const int mode = select_mode();
+  const bool mh = a.heads > 1;
+  JN_REQUIRE(!mh || (select_heads_fit(a.head_rank, a.heads) && a.heads * a.head_rank == a.r), kUnsupported,
+             "multi-head top-k select: %d heads of rank %d must fill 4 K-steps of 32 ranks at most (rank %d)",
+             a.heads, a.head_rank, a.r);
+  // multi-head scores always run on the per-wave split kernel
+  const int mode = mh ? kSelectSplitF16Wave : select_mode();
 
   if (mode != kSelectF32) {
-    const SelectScratch s = carve_select(a.ws, a.ws_bytes, a.B, a.Nk, a.r);
+    const int head_rp = mh ? split_ranks(a.head_rank) : split_ranks(a.r);
+    const int RP = mh ? a.heads * head_rp : head_rp;
+    const SelectScratch s = carve_select(a.ws, a.ws_bytes, a.B, a.Nk, RP);
     JN_REQUIRE(a.ws != nullptr && s.bytes <= a.ws_bytes, kWorkspaceTooSmall,
                "select workspace too small: need %zu bytes, got %zu", s.bytes, a.ws_bytes);
-    const int RP = split_ranks(a.r);
     const int nblk = (a.Nk + kSplitRows - 1) / kSplitRows;
     dim3 pgrid((unsigned)nblk, (unsigned)a.B);
     {
@@ -1120,7 +1197,8 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
     {
       JN_PROFILE("select_split_keys_kernel", stream);
       hipLaunchKernelGGL(select_split_keys_kernel, pgrid, dim3(256), 0, stream, a.key, a.ldk, a.k_batch_stride, a.Nk,
-                         a.r, RP, nblk, s.partial, reinterpret_cast<_Float16*>(s.split), s.kexp);
+                         mh ? a.head_rank : a.r, head_rp, RP, nblk, s.partial,
+                         reinterpret_cast<_Float16*>(s.split), s.kexp);
       JN_LAUNCH_CHECK();
     }
     a.split_key = s.split;
@@ -1131,7 +1209,13 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
                      (mode == kSelectSplitF16KeySplit ||
                       (mode == kSelectSplitF16 && blocks < kSelKspMaxBlocks && a.Nk >= kSelKspMinKeys));
     JN_PROFILE("lowrank_topk_select_kernel", stream);
-    if (coop4) {
+    if (mh) {
+      switch (RP / 32) {
+        case 2: launch_split_heads<2>(a, grid, stream); break;
+        case 3: launch_split_heads<3>(a, grid, stream); break;
+        default: launch_split_heads<4>(a, grid, stream); break;
+      }
+    } else if (coop4) {
       if (RP == 32) launch_split<1, 4>(a, grid, stream);
       else launch_split<2, 4>(a, grid, stream);
     } else if (ksp) {

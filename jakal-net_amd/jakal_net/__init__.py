@@ -6,7 +6,13 @@ score modules and the native-backend status calls.
 """
 
 from jakal_net.core import Layer, LayerDelta
-from jakal_net.modules import LowRankBilinearPairwise, LowRankBilinearRoute, TemperatureScaledRoute
+from jakal_net.modules import (
+    LowRankBilinearPairwise,
+    LowRankBilinearRoute,
+    MultiHeadPairwise,
+    MultiHeadRoute,
+    TemperatureScaledRoute,
+)
 from jakal_net.native_backend import native_available, native_status
 from jakal_net.propagation import Propagation, SparsePropagation
 from jakal_net.transition import SparseTransition, Transition
@@ -16,6 +22,8 @@ __all__ = [
     "LayerDelta",
     "LowRankBilinearPairwise",
     "LowRankBilinearRoute",
+    "MultiHeadPairwise",
+    "MultiHeadRoute",
     "Propagation",
     "SparsePropagation",
     "SparseTransition",

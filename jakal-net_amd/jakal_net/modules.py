@@ -8,12 +8,18 @@ Only the low-rank families are hot-path modules:
   ``l_jk = (w * (Ws src_j)) . (Wt dst_k) + b`` with the raw ``w``.
 * ``TemperatureScaledRoute`` (reference ``scripts/progressive_b_example.py:58-68``)
   divides the wrapped route's logits by a fixed temperature.
+* ``MultiHeadPairwise`` / ``MultiHeadRoute`` (reference ``modules.py:259-301``,
+  ``:470-529``) combine several heads' scores; the native path runs the
+  max aggregation over low-rank heads.
 
 Parameter creation order (source projection, target projection, weight, bias)
 is the reference's, so a given torch seed yields the same initial parameters.
 """
 
 from __future__ import annotations
+
+import math
+from collections.abc import Sequence
 
 import torch
 from torch import Tensor, nn
@@ -84,3 +90,79 @@ class TemperatureScaledRoute(nn.Module):
 
     def forward(self, *args: Tensor) -> Tensor:
         return self.route_fn(*args) / self.temperature
+
+
+PAIRWISE_AGGREGATES = ("max", "mean", "sum", "head_mean", "smoothmax", "signed_smoothmax")
+ROUTE_AGGREGATES = ("max", "mean", "sum", "head_mean")
+
+
+def _combine_heads(scores: list[Tensor], aggregate: str) -> Tensor:
+    """Combine per-head scores (reference modules.py:275-301, 497-529).
+
+    max: elementwise maximum; mean: sum / H; sum and head_mean: sum;
+    smoothmax: logsumexp - log H; signed_smoothmax: the heads weighted by
+    softmax(|s_h|) over the heads."""
+    if aggregate == "max":
+        out = scores[0]
+        for s in scores[1:]:
+            out = torch.maximum(out, s)
+        return out
+    if aggregate in ("smoothmax", "signed_smoothmax"):
+        stacked = torch.stack(scores, dim=-1)
+        if aggregate == "smoothmax":
+            return torch.logsumexp(stacked, dim=-1) - math.log(len(scores))
+        return (stacked * torch.softmax(stacked.abs(), dim=-1)).sum(dim=-1)
+    out = scores[0]
+    for s in scores[1:]:
+        out = out + s
+    return out / len(scores) if aggregate == "mean" else out
+
+
+class MultiHeadPairwise(nn.Module):
+    """Several pairwise heads combined per pair by ``aggregate``."""
+
+    def __init__(self, heads: Sequence[nn.Module], *, aggregate: str = "max") -> None:
+        super().__init__()
+        if len(heads) == 0:
+            raise ValueError("heads must contain at least one pairwise module.")
+        if aggregate not in PAIRWISE_AGGREGATES:
+            raise ValueError(f"Unsupported aggregate mode: {aggregate!r}.")
+        self.heads = nn.ModuleList(heads)
+        self.aggregate = aggregate
+        self.num_heads = len(self.heads)
+
+    def head_scores(self, target_val: Tensor, source_val: Tensor) -> Tensor:
+        """Per-head scores stacked on a trailing head axis."""
+        return torch.stack([head(target_val, source_val) for head in self.heads], dim=-1)
+
+    def forward(self, target_val: Tensor, source_val: Tensor) -> Tensor:
+        return _combine_heads([head(target_val, source_val) for head in self.heads], self.aggregate)
+
+
+class MultiHeadRoute(nn.Module):
+    """Several route heads combined per (source, destination) by ``aggregate``."""
+
+    def __init__(self, heads: Sequence[nn.Module], *, aggregate: str = "max") -> None:
+        super().__init__()
+        if len(heads) == 0:
+            raise ValueError("heads must contain at least one route module.")
+        if aggregate not in ROUTE_AGGREGATES:
+            raise ValueError(f"Unsupported aggregate mode: {aggregate!r}.")
+        self.heads = nn.ModuleList(heads)
+        self.aggregate = aggregate
+        self.num_heads = len(self.heads)
+        self.expects_pairwise_inputs = any(getattr(h, "expects_pairwise_inputs", False) for h in self.heads)
+
+    def _head(self, head: nn.Module, source_val: Tensor, target_val: Tensor | None) -> Tensor:
+        if getattr(head, "expects_pairwise_inputs", False):
+            if target_val is None:
+                raise ValueError("target_val is required for MultiHeadRoute heads with pairwise inputs.")
+            return head(source_val, target_val)
+        return head(source_val)
+
+    def head_logits(self, source_val: Tensor, target_val: Tensor | None = None) -> Tensor:
+        """Per-head logits stacked on a trailing head axis."""
+        return torch.stack([self._head(h, source_val, target_val) for h in self.heads], dim=-1)
+
+    def forward(self, source_val: Tensor, target_val: Tensor | None = None) -> Tensor:
+        return _combine_heads([self._head(h, source_val, target_val) for h in self.heads], self.aggregate)

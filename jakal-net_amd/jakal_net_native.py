@@ -111,6 +111,40 @@ _declare(
      _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 
+_declare("jn_propagation_topk_forward_multihead_workspace_bytes", [_I64] * 4, _SZ)
+_declare(
+    "jn_propagation_topk_forward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ,
+     _P],
+)
+_declare("jn_propagation_topk_multihead_workspace_bytes", [_I64] * 7, _SZ)
+_declare(
+    "jn_propagation_topk_backward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
+     _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+_declare(
+    "jn_propagation_window_forward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P],
+)
+_declare("jn_propagation_window_multihead_workspace_bytes", [_I64] * 7, _SZ)
+_declare(
+    "jn_propagation_window_backward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
+     _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+_declare("jn_transition_topk_multihead_workspace_bytes", [_I64] * 9, _SZ)
+_declare(
+    "jn_transition_topk_forward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32,
+     _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+_declare(
+    "jn_transition_topk_backward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+     _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+
 ABI_VERSION = int(_LIB.jn_abi_version())
 
 _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
@@ -122,6 +156,7 @@ MAX_RANK = 128         # low-rank score rank
 MAX_SELECT_KEYS = 65535  # keys a top-k select ranks per batch element
 MAX_ROW_COMPRESS_EDGES = 64  # edges per row of the row-normalising compressions on edge lists
 CAUSAL_DENSE_MIN_NODES = 128  # full causal windows from this many nodes run on the dense MFMA path
+MAX_HEADS = 8          # heads of a max-aggregated multi-head score
 
 _SUPPORTED_OPS = (
     "propagation_topk",
@@ -237,10 +272,15 @@ def _same_storage_view(a: Tensor, b: Tensor) -> bool:
 # edge-list propagation (top-k and window)
 # ---------------------------------------------------------------------------
 _EDGE_OPS = {
-    # mode: (forward, workspace_bytes, backward)
-    "topk": ("jn_propagation_topk_forward", "jn_propagation_topk_workspace_bytes", "jn_propagation_topk_backward"),
-    "window": ("jn_propagation_window_forward", "jn_propagation_window_workspace_bytes",
-               "jn_propagation_window_backward"),
+    # (mode, multi-head): (forward, workspace_bytes, backward)
+    ("topk", False): ("jn_propagation_topk_forward", "jn_propagation_topk_workspace_bytes",
+                      "jn_propagation_topk_backward"),
+    ("window", False): ("jn_propagation_window_forward", "jn_propagation_window_workspace_bytes",
+                        "jn_propagation_window_backward"),
+    ("topk", True): ("jn_propagation_topk_forward_multihead", "jn_propagation_topk_multihead_workspace_bytes",
+                     "jn_propagation_topk_backward_multihead"),
+    ("window", True): ("jn_propagation_window_forward_multihead", "jn_propagation_window_multihead_workspace_bytes",
+                       "jn_propagation_window_backward_multihead"),
 }
 
 
@@ -255,47 +295,56 @@ class _PropagationEdges(torch.autograd.Function):
     (param = window) takes the causal band j in [i - window, i].  Inputs (all
     fp32, contiguous): layer_val X [B,N,Din], projected_state [B,N],
     projected_val [B,N,Dout] or None when it is X itself, V and U [r,Din],
-    w_hat [r], bias [] or None."""
+    w_hat [r], bias [] or None.  With heads > 1 the r ranks are `heads`
+    equal head slices (max-aggregated scores) and bias is [heads]."""
 
     @staticmethod
-    def forward(ctx, X, ps, pv, V, U, w_hat, bias, mode: str, param: int, compress: int):  # noqa: N803
+    def forward(ctx, X, ps, pv, V, U, w_hat, bias, mode: str, param: int, compress: int, heads: int = 1):  # noqa: N803
         B, N, Din = X.shape
         pv_is_x = pv is None
         pv_t = X if pv_is_x else pv
         Dout = pv_t.shape[-1]
         r = U.shape[0]
+        mh = heads > 1
+        rank_arg = [r // heads, heads] if mh else [r]
         k = _edges_per_row(mode, param, N)
         dev = X.device
-        fwd = getattr(_LIB, _EDGE_OPS[mode][0])
+        fwd = getattr(_LIB, _EDGE_OPS[mode, mh][0])
         with torch.cuda.device(dev):
             ds = torch.empty(B, N, device=dev, dtype=torch.float32)
             dv = torch.empty(B, N, Dout, device=dev, dtype=torch.float32)
             proj = torch.empty(B * N, 2 * r, device=dev, dtype=torch.float32)
             idx = torch.empty(B, N, k, device=dev, dtype=torch.int32)
             score = torch.empty(B, N, k, device=dev, dtype=torch.float32)
+            head = torch.empty(B, N, k, device=dev, dtype=torch.uint8) if mh else None
             args = [
                 _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
-                B, N, Din, Dout, r, param, compress,
+                B, N, Din, Dout, *rank_arg, param, compress,
                 _ptr(ds), _ptr(dv), _ptr(proj), _ptr(idx), _ptr(score),
             ]
+            if mh:
+                args.append(_ptr(head))
             if mode == "topk":  # the select's scratch
-                ws_bytes = int(_LIB.jn_propagation_topk_forward_workspace_bytes(B, N, r))
+                ws_bytes = int(_LIB.jn_propagation_topk_forward_multihead_workspace_bytes(B, N, *rank_arg) if mh
+                               else _LIB.jn_propagation_topk_forward_workspace_bytes(B, N, r))
                 ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
                 args += [_ptr(ws), ws_bytes]
             _check(fwd(*args, _stream(dev)))
-        ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, idx, score)
-        ctx.meta = (mode, param, compress, pv_is_x, bias is not None)
+        ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, idx, score, head)
+        ctx.meta = (mode, param, compress, pv_is_x, bias is not None, heads)
         ctx.mark_non_differentiable(idx, score)
         return ds, dv, idx, score
 
     @staticmethod
     def backward(ctx, g_ds, g_dv, _g_idx=None, _g_score=None):
-        X, ps, pv, V, U, w_hat, proj, idx, score = ctx.saved_tensors
-        mode, param, compress, pv_is_x, has_bias = ctx.meta
-        _, ws_name, bwd_name = _EDGE_OPS[mode]
+        X, ps, pv, V, U, w_hat, proj, idx, score, head = ctx.saved_tensors
+        mode, param, compress, pv_is_x, has_bias, heads = ctx.meta
+        mh = heads > 1
+        _, ws_name, bwd_name = _EDGE_OPS[mode, mh]
         B, N, Din = X.shape
         Dout = pv.shape[-1]
         r = U.shape[0]
+        rank_arg = [r // heads, heads] if mh else [r]
         dev = X.device
         need = ctx.needs_input_grad
         with torch.cuda.device(dev):
@@ -307,14 +356,15 @@ class _PropagationEdges(torch.autograd.Function):
             gV = torch.empty_like(V)
             gU = torch.empty_like(U)
             gw = torch.empty_like(w_hat)
-            gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
-            ws_bytes = int(getattr(_LIB, ws_name)(B, N, Din, Dout, r, param))
+            gb = torch.empty((heads,) if mh else (), device=dev, dtype=torch.float32) if has_bias else None
+            ws_bytes = int(getattr(_LIB, ws_name)(B, N, Din, Dout, *rank_arg, param))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            edge_args = [_ptr(idx), _ptr(score)] + ([_ptr(head)] if mh else [])
             _check(
                 getattr(_LIB, bwd_name)(
                     _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat),
-                    _ptr(proj), _ptr(idx), _ptr(score), _ptr(g_ds), _ptr(g_dv),
-                    B, N, Din, Dout, r, param, compress, 1 if pv_is_x else 0,
+                    _ptr(proj), *edge_args, _ptr(g_ds), _ptr(g_dv),
+                    B, N, Din, Dout, *rank_arg, param, compress, 1 if pv_is_x else 0,
                     _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
                     _ptr(ws), ws_bytes, _stream(dev),
                 )
@@ -327,6 +377,7 @@ class _PropagationEdges(torch.autograd.Function):
             gU if need[4] else None,
             gw if need[5] else None,
             gb if (has_bias and need[6]) else None,
+            None,
             None,
             None,
             None,
@@ -426,7 +477,11 @@ def propagation_dense(
     With ``source_state`` the edges are weighted by it per source, which
     equals the unweighted op on (source_state, source_state * projected_val)
     (jakal_net_native.cpp:5991-6015); the fold is done here, differentiably."""
-    w_hat, bias, V, U = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias)
+    w_hat, bias, V, U, heads = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight,
+                                                      out_bias)
+    if heads > 1:
+        raise NotImplementedError("the HIP library runs multi-head scores on edge lists (top-k and window), "
+                                  "not on the dense path.")
     if edge_compress_name not in _COMPRESS_KINDS:
         raise RuntimeError(f"Unsupported edge_compress_name for the HIP backend: {edge_compress_name!r}.")
     if target_block_size <= 0 or source_block_size <= 0:
@@ -449,14 +504,45 @@ def propagation_dense(
 
 
 def _lowrank_pairwise_args(kind, weight, bias, in_weight, in_bias, out_weight, out_bias):
-    if kind != "low_rank_bilinear":
-        raise TypeError(f"jakal_net_native supports pairwise kind 'low_rank_bilinear', got {kind!r}.")
+    """(w_hat [R], bias, V [R, D], U [R, D], heads) of a low-rank pairwise spec.
+
+    A ``multihead_max_low_rank_bilinear`` spec stacks H heads on a leading axis
+    (weight [H, r], bias [H], projections [H, r, D]); they are passed flat as
+    R = H * r ranks, head h owning ranks [h * r, (h + 1) * r)."""
+    if kind not in ("low_rank_bilinear", "multihead_max_low_rank_bilinear"):
+        raise TypeError(f"jakal_net_native supports pairwise kinds 'low_rank_bilinear' and "
+                        f"'multihead_max_low_rank_bilinear', got {kind!r}.")
     if in_weight is None or out_weight is None:
         raise RuntimeError("Low-rank bilinear pairwise kernel is missing projection weights.")
     if in_bias is not None or out_bias is not None:
         raise TypeError("low_rank_bilinear projections carry no bias.")
-    _check_rank(out_weight.shape[0])
-    return weight, bias, in_weight, out_weight
+    if kind == "low_rank_bilinear":
+        _check_rank(out_weight.shape[0])
+        return weight, bias, in_weight, out_weight, 1
+    return _flatten_heads(weight, bias, in_weight, out_weight)
+
+
+def _flatten_heads(core, bias, first, second):
+    """Stacked heads ([H, r] core, [H] bias, [H, r, D] projections) as flat ranks, plus H."""
+    if core.dim() != 2 or first.dim() != 3 or second.dim() != 3:
+        raise RuntimeError("multi-head weights must be stacked [heads, rank] and [heads, rank, dim].")
+    heads, rank = core.shape
+    if heads > MAX_HEADS:
+        raise NotImplementedError(f"the HIP library takes up to {MAX_HEADS} heads (got {heads}).")
+    _check_rank(heads * rank)
+    if bias is not None and bias.numel() != heads:
+        raise RuntimeError("multi-head bias must hold one value per head.")
+    flat_bias = None if bias is None else bias.reshape(heads)
+    if heads == 1:
+        return core[0], None if bias is None else bias.reshape(()), first[0], second[0], 1
+    return core.reshape(-1), flat_bias, first.reshape(heads * rank, -1), second.reshape(heads * rank, -1), heads
+
+
+def _check_select_heads(rank: int, heads: int) -> None:
+    """A multi-head top-k select scores each head on whole 32-rank K-steps, four at most."""
+    if heads > 1 and heads * (-(-rank // 32)) > 4:
+        raise NotImplementedError(f"the HIP multi-head top-k select takes heads x ceil(rank / 32) <= 4 "
+                                  f"(heads={heads}, rank={rank}).")
 
 
 def _check_rank(rank: int) -> None:
@@ -481,7 +567,10 @@ def _check_row_compress(compress: str, edges: int) -> None:
 def _propagation_edges(mode, pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
                        edge_compress_name, layer_val, projected_state, projected_val, param, target_block_size,
                        source_block_size):
-    w_hat, bias, V, U = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias)
+    w_hat, bias, V, U, heads = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight,
+                                                      out_bias)
+    if mode == "topk":
+        _check_select_heads(U.shape[0] // heads, heads)
     if edge_compress_name not in _COMPRESS_KINDS:
         raise RuntimeError(f"Unsupported edge_compress_name for the HIP backend: {edge_compress_name!r}.")
     if target_block_size <= 0 or source_block_size <= 0:
@@ -495,7 +584,8 @@ def _propagation_edges(mode, pairwise_kind, weight, bias, in_weight, in_bias, ou
     ps = _f32(projected_state.reshape(-1, N))
     pv = None if pv_is_x else _f32(projected_val.reshape(-1, N, Dout))
     ds, dv, idx, score = _PropagationEdges.apply(
-        X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias), mode, int(param), _COMPRESS_KINDS[edge_compress_name]
+        X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias), mode, int(param), _COMPRESS_KINDS[edge_compress_name],
+        heads,
     )
     k = idx.shape[-1]
     return (
@@ -590,9 +680,10 @@ def propagation_window(
     query propagation of progressive_b_example.py:1990-2003) on at least
     CAUSAL_DENSE_MIN_NODES nodes runs as causal dense propagation on MFMA
     GEMMs instead of an N-wide edge list, and so does one whose rows are too
-    wide for a row-normalising compression on an edge list."""
+    wide for a row-normalising compression on an edge list (single-head
+    scores; multi-head ones stay on the edge list)."""
     N = layer_val.shape[-2]
-    full_causal = window >= N - 1
+    full_causal = window >= N - 1 and not pairwise_kind.startswith("multihead_")
     if full_causal and (N >= CAUSAL_DENSE_MIN_NODES or (edge_compress_name != "softsign"
                                                         and N > MAX_ROW_COMPRESS_EDGES)):
         if window < 0:
@@ -651,11 +742,14 @@ class _TransitionTopK(torch.autograd.Function):
     Ws [r,Dsrc], Wt [r,Ddst], w [r] (raw), bias [] or None."""
 
     @staticmethod
-    def forward(ctx, rho, src, dst, ps, pv, Ws, Wt, w, bias, temperature: float, topk: int, compress: int):  # noqa: N803
+    def forward(ctx, rho, src, dst, ps, pv, Ws, Wt, w, bias, temperature: float, topk: int, compress: int,  # noqa: N803
+                heads: int = 1):
         B, Ns, Dsrc = src.shape
         Nd, Ddst = dst.shape[1], dst.shape[2]
         Dv = pv.shape[-1]
         r = Ws.shape[0]
+        mh = heads > 1
+        rank_arg = [r // heads, heads] if mh else [r]
         k = min(int(topk), Nd)
         dev = src.device
         with torch.cuda.device(dev):
@@ -665,28 +759,34 @@ class _TransitionTopK(torch.autograd.Function):
             dp = torch.empty(B * Nd, r, device=dev, dtype=torch.float32)
             idx = torch.empty(B, Ns, k, device=dev, dtype=torch.int32)
             logit = torch.empty(B, Ns, k, device=dev, dtype=torch.float32)
-            ws_bytes = int(_LIB.jn_transition_topk_workspace_bytes(B, Ns, Nd, Dsrc, Ddst, Dv, r, topk))
+            head = torch.empty(B, Ns, k, device=dev, dtype=torch.uint8) if mh else None
+            ws_fn = _LIB.jn_transition_topk_multihead_workspace_bytes if mh else _LIB.jn_transition_topk_workspace_bytes
+            ws_bytes = int(ws_fn(B, Ns, Nd, Dsrc, Ddst, Dv, *rank_arg, topk))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            fwd = _LIB.jn_transition_topk_forward_multihead if mh else _LIB.jn_transition_topk_forward
             _check(
-                _LIB.jn_transition_topk_forward(
+                fwd(
                     _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w), _ptr(bias),
-                    float(temperature), B, Ns, Nd, Dsrc, Ddst, Dv, r, topk, compress,
-                    _ptr(ds), _ptr(dv), _ptr(sp), _ptr(dp), _ptr(idx), _ptr(logit), _ptr(ws), ws_bytes, _stream(dev),
+                    float(temperature), B, Ns, Nd, Dsrc, Ddst, Dv, *rank_arg, topk, compress,
+                    _ptr(ds), _ptr(dv), _ptr(sp), _ptr(dp), _ptr(idx), _ptr(logit), *([_ptr(head)] if mh else []),
+                    _ptr(ws), ws_bytes, _stream(dev),
                 )
             )
-        ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, idx, logit)
-        ctx.meta = (float(temperature), int(topk), compress, bias is not None)
+        ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, idx, logit, head)
+        ctx.meta = (float(temperature), int(topk), compress, bias is not None, heads)
         ctx.mark_non_differentiable(idx, logit)
         return ds, dv, idx, logit
 
     @staticmethod
     def backward(ctx, g_ds, g_dv, _g_idx=None, _g_logit=None):
-        rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, idx, logit = ctx.saved_tensors
-        temperature, topk, compress, has_bias = ctx.meta
+        rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, idx, logit, head = ctx.saved_tensors
+        temperature, topk, compress, has_bias, heads = ctx.meta
         B, Ns, Dsrc = src.shape
         Nd, Ddst = dst.shape[1], dst.shape[2]
         Dv = pv.shape[-1]
         r = Ws.shape[0]
+        mh = heads > 1
+        rank_arg = [r // heads, heads] if mh else [r]
         dev = src.device
         need = ctx.needs_input_grad
         with torch.cuda.device(dev):
@@ -696,19 +796,22 @@ class _TransitionTopK(torch.autograd.Function):
             gWs = torch.empty_like(Ws) if need[5] else None
             gWt = torch.empty_like(Wt) if need[6] else None
             gw = torch.empty_like(w)
-            gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
-            ws_bytes = int(_LIB.jn_transition_topk_workspace_bytes(B, Ns, Nd, Dsrc, Ddst, Dv, r, topk))
+            gb = torch.empty((heads,) if mh else (), device=dev, dtype=torch.float32) if has_bias else None
+            ws_fn = _LIB.jn_transition_topk_multihead_workspace_bytes if mh else _LIB.jn_transition_topk_workspace_bytes
+            ws_bytes = int(ws_fn(B, Ns, Nd, Dsrc, Ddst, Dv, *rank_arg, topk))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            bwd = _LIB.jn_transition_topk_backward_multihead if mh else _LIB.jn_transition_topk_backward
             _check(
-                _LIB.jn_transition_topk_backward(
+                bwd(
                     _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w),
-                    _ptr(sp), _ptr(dp), _ptr(idx), _ptr(logit), _ptr(g_ds), _ptr(g_dv), float(temperature),
-                    B, Ns, Nd, Dsrc, Ddst, Dv, r, topk, compress,
+                    _ptr(sp), _ptr(dp), _ptr(idx), _ptr(logit), *([_ptr(head)] if mh else []), _ptr(g_ds), _ptr(g_dv),
+                    float(temperature), B, Ns, Nd, Dsrc, Ddst, Dv, *rank_arg, topk, compress,
                     _ptr(out[0]), _ptr(out[1]), _ptr(out[2]), _ptr(out[3]), _ptr(out[4]), _ptr(gWs), _ptr(gWt),
                     _ptr(gw), _ptr(gb), _ptr(ws), ws_bytes, _stream(dev),
                 )
             )
-        return (*out, gWs, gWt, gw if need[7] else None, gb if (has_bias and need[8]) else None, None, None, None)
+        return (*out, gWs, gWt, gw if need[7] else None, gb if (has_bias and need[8]) else None, None, None, None,
+                None)
 
 
 def transition_pairwise_topk_routes(
@@ -739,10 +842,15 @@ def transition_pairwise_topk_routes(
     Same arguments as ``transition_pairwise_topk``; route_index/route_logit
     [..., Ns, k] are each source's selected destinations (best first) and
     their logits."""
-    if route_kind != "low_rank_bilinear_route":
-        raise TypeError(f"jakal_net_native supports route kind 'low_rank_bilinear_route', got {route_kind!r}.")
+    if route_kind not in ("low_rank_bilinear_route", "multihead_max_low_rank_bilinear_route"):
+        raise TypeError(f"jakal_net_native supports route kinds 'low_rank_bilinear_route' and "
+                        f"'multihead_max_low_rank_bilinear_route', got {route_kind!r}.")
     if source_weight is None or target_weight is None:
         raise RuntimeError("Low-rank bilinear route is missing projection weights.")
+    heads = 1
+    if route_kind.startswith("multihead_"):
+        core_weight, bias, source_weight, target_weight, heads = _flatten_heads(core_weight, bias, source_weight,
+                                                                                target_weight)
     if source_bias is not None or target_bias is not None or hidden_weight is not None or out_weight is not None:
         raise TypeError("low_rank_bilinear_route carries no projection biases or hidden layers.")
     if route_compress_name not in _ROUTE_COMPRESS_KINDS:
@@ -763,6 +871,7 @@ def transition_pairwise_topk_routes(
     _check_rank(source_weight.shape[0])
     if k < Nd:
         _check_select(k, Nd)
+        _check_select_heads(source_weight.shape[0] // heads, heads)
     elif Nd > MAX_ROUTE_TOPK:
         raise NotImplementedError("HIP sparse transition over every destination supports up to 64 destinations "
                                   "(transition_pairwise_topk runs more as the dense transition).")
@@ -770,7 +879,7 @@ def transition_pairwise_topk_routes(
         _f32(sender_strength.reshape(-1, Ns)), _f32(src_val.reshape(-1, Ns, Dsrc)),
         _f32(dst_val.reshape(-1, Nd, Ddst)), _f32(projected_state.reshape(-1, Ns)),
         _f32(projected_val.reshape(-1, Ns, Dv)), _f32(source_weight), _f32(target_weight), _f32(core_weight),
-        _f32(bias), float(temperature), k, _ROUTE_COMPRESS_KINDS[route_compress_name],
+        _f32(bias), float(temperature), k, _ROUTE_COMPRESS_KINDS[route_compress_name], heads,
     )
     return (
         ds.reshape(*batch_shape, Nd).to(projected_state.dtype),
@@ -811,6 +920,9 @@ def transition_pairwise_topk(
     or "signed_entmax15") has no counterpart in the reference's composite op,
     which is softmax-only."""
     if topk >= dst_val.shape[-2] > 64:
+        if route_kind.startswith("multihead_"):
+            raise NotImplementedError("the HIP library runs multi-head routes on edge lists (top-k, or every "
+                                      "destination up to 64), not on the dense transition.")
         # every destination kept (transition.py:437-440): the dense transition
         return transition_pairwise_dense(
             route_kind, source_weight, source_bias, target_weight, target_bias, core_weight, bias, hidden_weight,
@@ -890,6 +1002,9 @@ class _TransitionDense(torch.autograd.Function):
 
 def _check_route_spec(route_kind, source_weight, source_bias, target_weight, target_bias, hidden_weight, out_weight,
                       route_compress_name, temperature):
+    if route_kind.startswith("multihead_"):
+        raise NotImplementedError("the HIP library runs multi-head routes on edge lists (top-k, or every "
+                                  "destination up to 64), not on the dense transition.")
     if route_kind != "low_rank_bilinear_route":
         raise TypeError(f"jakal_net_native supports route kind 'low_rank_bilinear_route', got {route_kind!r}.")
     if source_weight is None or target_weight is None:

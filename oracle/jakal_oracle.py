@@ -13,7 +13,9 @@ Pinning (see tests/test_oracle.py):
     tests/test_jakal_net.py:438-458, 810-831, 833-862;
   * closed forms (low-rank score = P_t diag(w_hat) P_s^T + b, softsign, window mask);
   * brute-force top-k by full sort on tiny inputs;
-  * every backward against float64 central finite differences of the forward.
+  * every backward against float64 central finite differences of the forward;
+  * multi-head max aggregation: one head reduces to the single-head form, the
+    score is the largest head's and its gradient reaches only that head.
 Tie order: the oracle breaks exact score ties toward the lower index (stable
 sort).  CPU torch.topk does not (it is implementation-defined), so exact ties
 at the k-th place are excluded from index parity by the 1e-5 gap rule.
@@ -74,6 +76,41 @@ def lowrank_route_logits(src_val, dst_val, Ws, Wt, w, b, temperature=1.0):
     if b is not None:
         l = l + float(b)
     return l / float(temperature)
+
+
+def multihead_pairwise_scores(target_val, source_val, U, V, w, b):
+    """Max-aggregated multi-head low-rank scores: s = max_h s_h with s_h the
+    low-rank score of head h (its own projections, normalised core weight and
+    bias).  MultiHeadPairwise(aggregate="max") (modules.py:259-301, :284-291)
+    over LowRankBilinearPairwise heads; the native composite stacks the heads'
+    parameters and takes the max over the head axis
+    (jakal_net_native.cpp:724-752, kernel_common.py:152-178).
+
+    U, V [H, r, D]; w [H, r] (raw, normalised per head); b [H] or None.
+    Returns (scores, head, per_head): head is the first head attaining the max."""
+    H = np.shape(U)[0]
+    per = np.stack([lowrank_pairwise_scores(target_val, source_val, U[h], V[h], w[h], None if b is None else b[h])
+                    for h in range(H)])
+    head = np.argmax(per, axis=0)
+    return np.take_along_axis(per, head[None], 0)[0], head, per
+
+
+def multihead_route_logits(src_val, dst_val, Ws, Wt, w, b, temperature=1.0):
+    """Max-aggregated multi-head low-rank route logits, max_h l_h
+    (MultiHeadRoute(aggregate="max"), modules.py:470-529, :497-514;
+    jakal_net_native.cpp:889-917).  Ws [H, r, Ds], Wt [H, r, Dd], w [H, r]
+    (raw), b [H] or None; the heads share one temperature.  Returns
+    (logits, head, per_head) as multihead_pairwise_scores."""
+    H = np.shape(Ws)[0]
+    per = np.stack([lowrank_route_logits(src_val, dst_val, Ws[h], Wt[h], w[h], None if b is None else b[h],
+                                         temperature) for h in range(H)])
+    head = np.argmax(per, axis=0)
+    return np.take_along_axis(per, head[None], 0)[0], head, per
+
+
+def is_multihead(weights):
+    """Projection weights of H heads come stacked [H, r, D]; one head is [r, D]."""
+    return np.ndim(weights) == 3
 
 
 # ---------------------------------------------------------------------------
@@ -218,12 +255,47 @@ def propagation_forward(val, ps, pv, U, V, w, b, *, mode="topk", topk=None, wind
     """Low-rank propagation forward; returns a dict with deltas and intermediates.
 
     ``mask`` overrides the selection (used to evaluate the math on a selection
-    made elsewhere, e.g. by the GPU, when rows have near-ties)."""
-    s = lowrank_pairwise_scores(val, val, U, V, w, b)
+    made elsewhere, e.g. by the GPU, when rows have near-ties).  Stacked
+    [H, r, D] projections select the max-aggregated multi-head scores
+    (multihead_pairwise_scores); "head" is then each pair's winning head."""
+    head = None
+    if is_multihead(U):
+        s, head, _ = multihead_pairwise_scores(val, val, U, V, w, b)
+    else:
+        s = lowrank_pairwise_scores(val, val, U, V, w, b)
     if mask is None:
         mask = propagation_mask(s, mode, topk=topk, window=window)
     ds, dv, e = propagation_from_scores(s, mask, kind, ps, pv)
-    return {"delta_state": ds, "delta_val": dv, "scores": s, "mask": mask, "edges": e}
+    return {"delta_state": ds, "delta_val": dv, "scores": s, "mask": mask, "edges": e, "head": head}
+
+
+def _pairwise_score_backward(val, U, V, w, g_s):
+    """Gradients of s = (val U^T) diag(w_hat) (val V^T)^T + b given dL/ds."""
+    what = normalized_weight(w)
+    pt, psrc = lowrank_projections(val, U, V)
+    psh = psrc * what
+    g_pt = g_s @ psh
+    g_psh = np.swapaxes(g_s, -1, -2) @ pt
+    g_psrc = g_psh * what
+    g_what = np.sum(g_psh * psrc, axis=tuple(range(g_psh.ndim - 1)))
+    flat = lambda x: x.reshape(-1, x.shape[-1])  # noqa: E731
+    return {"val": g_pt @ U + g_psrc @ V, "U": flat(g_pt).T @ flat(val), "V": flat(g_psrc).T @ flat(val),
+            "w": normalized_weight_backward(w, g_what), "w_hat": g_what, "b": float(np.sum(g_s))}
+
+
+def _per_head_backward(score_backward, head, H, g_s):
+    """A max over heads passes each pair's score gradient to its winning head
+    only; the heads' gradients are stacked on a leading head axis and the
+    input gradients summed."""
+    parts = [score_backward(h, np.where(head == h, g_s, 0.0)) for h in range(H)]
+    out = {}
+    for name in parts[0]:
+        vals = [p[name] for p in parts]
+        if name in ("val", "src_val", "dst_val"):
+            out[name] = np.sum(vals, axis=0)
+        else:
+            out[name] = np.stack([np.asarray(v, F64) for v in vals])
+    return out
 
 
 def propagation_backward(val, ps, pv, U, V, w, b, g_ds, g_dv, *, mode="topk", topk=None, window=None,
@@ -241,25 +313,17 @@ def propagation_backward(val, ps, pv, U, V, w, b, g_ds, g_dv, *, mode="topk", to
     g_dv = np.asarray(g_dv, F64)
     fwd = propagation_forward(val, ps, pv, U, V, w, b, mode=mode, topk=topk, window=window, kind=kind, mask=mask)
     s, mask, e = fwd["scores"], fwd["mask"], fwd["edges"]
-    what = normalized_weight(w)
-    pt, psrc = lowrank_projections(val, U, V)
-    psh = psrc * what
     g_e = g_ds[..., :, None] * ps[..., None, :] + g_dv @ np.swapaxes(pv, -1, -2)
     g_s = compress_backward(s, mask, kind, g_e)
     g_ps = np.einsum("...ij,...i->...j", e, g_ds)
     g_pv = np.einsum("...ij,...id->...jd", e, g_dv)
-    g_pt = g_s @ psh
-    g_psh = np.swapaxes(g_s, -1, -2) @ pt
-    g_psrc = g_psh * what
-    g_what = np.sum(g_psh * psrc, axis=tuple(range(g_psh.ndim - 1)))
-    g_b = float(np.sum(g_s))
-    g_val = g_pt @ U + g_psrc @ V
-    flat = lambda x: x.reshape(-1, x.shape[-1])  # noqa: E731
-    g_U = flat(g_pt).T @ flat(val)
-    g_V = flat(g_psrc).T @ flat(val)
-    g_w = normalized_weight_backward(w, g_what)
-    return {"val": g_val, "ps": g_ps, "pv": g_pv, "U": g_U, "V": g_V, "w": g_w, "w_hat": g_what, "b": g_b,
-            "g_scores": g_s, "delta_state": fwd["delta_state"], "delta_val": fwd["delta_val"]}
+    if is_multihead(U):
+        g = _per_head_backward(lambda h, gh: _pairwise_score_backward(val, U[h], V[h], w[h], gh), fwd["head"],
+                               U.shape[0], g_s)
+    else:
+        g = _pairwise_score_backward(val, U, V, w, g_s)
+    return {**g, "ps": g_ps, "pv": g_pv, "g_scores": g_s, "delta_state": fwd["delta_state"],
+            "delta_val": fwd["delta_val"], "head": fwd["head"]}
 
 
 def normalized_weight_backward(w, g_what):
@@ -309,11 +373,29 @@ def transition_from_logits(logits, mask, sender, ps, pv, kind="softmax"):
 
 def transition_forward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, *, topk, temperature=1.0, mask=None,
                        kind="softmax"):
-    l = lowrank_route_logits(src_val, dst_val, Ws, Wt, w, b, temperature)
+    head = None
+    if is_multihead(Ws):
+        l, head, _ = multihead_route_logits(src_val, dst_val, Ws, Wt, w, b, temperature)
+    else:
+        l = lowrank_route_logits(src_val, dst_val, Ws, Wt, w, b, temperature)
     if mask is None:
         mask = topk_mask(l, topk)  # per source row, over destinations (transition.py:439-444)
     ds, dv, p = transition_from_logits(l, mask, sender, ps, pv, kind)
-    return {"delta_state": ds, "delta_val": dv, "logits": l, "mask": mask, "routes": p}
+    return {"delta_state": ds, "delta_val": dv, "logits": l, "mask": mask, "routes": p, "head": head}
+
+
+def _route_logit_backward(src_val, dst_val, Ws, Wt, w, g_raw):
+    """Gradients of l_raw = ((w * (src Ws^T)) . (dst Wt^T)) + b given dL/dl_raw."""
+    psrc = src_val @ Ws.T
+    psh = psrc * w
+    pt = dst_val @ Wt.T
+    g_psh = g_raw @ pt
+    g_pt = np.swapaxes(g_raw, -1, -2) @ psh
+    g_psrc = g_psh * w
+    flat = lambda x: x.reshape(-1, x.shape[-1])  # noqa: E731
+    return {"src_val": g_psrc @ Ws, "dst_val": g_pt @ Wt, "Ws": flat(g_psrc).T @ flat(src_val),
+            "Wt": flat(g_pt).T @ flat(dst_val), "w": np.sum(g_psh * psrc, axis=tuple(range(g_psh.ndim - 1))),
+            "b": float(np.sum(g_raw))}
 
 
 def transition_backward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, g_ds, g_dv, *, topk, temperature=1.0,
@@ -339,29 +421,13 @@ def transition_backward(src_val, dst_val, sender, ps, pv, Ws, Wt, w, b, g_ds, g_
     g_p = g_wr * sender[..., :, None]
     g_l = route_compress_backward(logits, mask, kind, g_p)
     g_raw = g_l / float(temperature)
-    psrc = src_val @ Ws.T
-    psh = psrc * w
-    pt = dst_val @ Wt.T
-    g_psh = g_raw @ pt
-    g_pt = np.swapaxes(g_raw, -1, -2) @ psh
-    g_psrc = g_psh * w
-    g_w = np.sum(g_psh * psrc, axis=tuple(range(g_psh.ndim - 1)))
-    g_b = float(np.sum(g_raw))
-    flat = lambda x: x.reshape(-1, x.shape[-1])  # noqa: E731
-    return {
-        "src_val": g_psrc @ Ws,
-        "dst_val": g_pt @ Wt,
-        "sender": g_sender,
-        "ps": g_ps,
-        "pv": g_pv,
-        "Ws": flat(g_psrc).T @ flat(src_val),
-        "Wt": flat(g_pt).T @ flat(dst_val),
-        "w": g_w,
-        "b": g_b,
-        "g_logits": g_raw,
-        "delta_state": fwd["delta_state"],
-        "delta_val": fwd["delta_val"],
-    }
+    if is_multihead(Ws):
+        g = _per_head_backward(lambda h, gh: _route_logit_backward(src_val, dst_val, Ws[h], Wt[h], w[h], gh),
+                               fwd["head"], Ws.shape[0], g_raw)
+    else:
+        g = _route_logit_backward(src_val, dst_val, Ws, Wt, w, g_raw)
+    return {**g, "sender": g_sender, "ps": g_ps, "pv": g_pv, "g_logits": g_raw,
+            "delta_state": fwd["delta_state"], "delta_val": fwd["delta_val"], "head": fwd["head"]}
 
 
 # ---------------------------------------------------------------------------

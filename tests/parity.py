@@ -89,7 +89,8 @@ def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, 
     """fp32 torch forward + autograd backward of low-rank propagation on a given mask.
 
     val [B,N,D], ps [B,N], pv [B,N,Dv] or None (pv is val itself), U/V [r,D],
-    w_hat [r] (the normalised core weight), b float or None, mask [B,N,N]
+    w_hat [r] (the normalised core weight), b float or None -- or, for
+    max-aggregated heads, U/V [H,r,D], w_hat [H,r], b [H] -- mask [B,N,N]
     bool (numpy), gds [B,N] / gdv [B,N,Dv] the upstream gradients.  Returns
     the oracle's keys: delta_state, delta_val, val (whole gradient of val),
     ps, pv, U, V, w_hat, b."""
@@ -97,7 +98,7 @@ def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, 
     Ud = torch.as_tensor(U).to(**f32).requires_grad_(True)
     Vd = torch.as_tensor(V).to(**f32).requires_grad_(True)
     wd = torch.as_tensor(w_hat).to(**f32).requires_grad_(True)
-    bd = None if b is None else torch.tensor(float(b), **f32).requires_grad_(True)
+    bd = None if b is None else torch.as_tensor(np.asarray(b, dtype=np.float64)).to(**f32).requires_grad_(True)
     params = [Ud, Vd, wd] + ([bd] if bd is not None else [])
     out = {k: [] for k in ("delta_state", "delta_val", "val", "ps", "pv")}
     acc = [torch.zeros_like(p) for p in params]
@@ -108,10 +109,17 @@ def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, 
         p_s = torch.as_tensor(ps[b0:b1]).to(**f32).requires_grad_(True)
         p_v = x if pv is None else torch.as_tensor(pv[b0:b1]).to(**f32).requires_grad_(True)
         m = _bool_mask(mask, dev, b0, b1)
-        key = ((x @ Vd.T) * wd).transpose(-1, -2).contiguous()
-        s = (x @ Ud.T) @ key
-        if bd is not None:
-            s = s + bd
+        if Ud.dim() == 3:  # stacked heads [H, r, D]: the max over the heads' scores
+            key = ((x[:, None] @ Vd.transpose(-1, -2)) * wd[:, None, :]).transpose(-1, -2).contiguous()
+            s = (x[:, None] @ Ud.transpose(-1, -2)) @ key
+            if bd is not None:
+                s = s + bd[:, None, None]
+            s = s.max(dim=1).values
+        else:
+            key = ((x @ Vd.T) * wd).transpose(-1, -2).contiguous()
+            s = (x @ Ud.T) @ key
+            if bd is not None:
+                s = s + bd
         e = _compress32(s, m, kind)
         ds = (e * p_s[:, None, :]).sum(-1)
         dv = e @ p_v
@@ -138,15 +146,16 @@ def torch32_transition(dev, src, dst, rho, ps, pv, Ws, Wt, w, b, temperature, ma
     """fp32 torch forward + autograd backward of low-rank routing on a given mask.
 
     src [B,Ns,Ds], dst [B,Nd,Dd], rho [B,Ns] (sender strength, a leaf), ps
-    [B,Ns], pv [B,Ns,Dv], Ws [r,Ds], Wt [r,Dd], w [r] (raw), b float or None,
-    mask [B,Ns,Nd] bool (numpy) or None (every destination).  Returns the
+    [B,Ns], pv [B,Ns,Dv], Ws [r,Ds], Wt [r,Dd], w [r] (raw), b float or None
+    (stacked heads: [H,r,Ds], [H,r,Dd], [H,r], [H]), mask [B,Ns,Nd] bool
+    (numpy) or None (every destination).  Returns the
     oracle's keys: delta_state, delta_val, sender, src_val, dst_val, ps, pv,
     Ws, Wt, w, b."""
     f32 = dict(device=dev, dtype=torch.float32)
     Wsd = torch.as_tensor(Ws).to(**f32).requires_grad_(True)
     Wtd = torch.as_tensor(Wt).to(**f32).requires_grad_(True)
     wd = torch.as_tensor(w).to(**f32).requires_grad_(True)
-    bd = None if b is None else torch.tensor(float(b), **f32).requires_grad_(True)
+    bd = None if b is None else torch.as_tensor(np.asarray(b, dtype=np.float64)).to(**f32).requires_grad_(True)
     params = [Wsd, Wtd, wd] + ([bd] if bd is not None else [])
     keys = ("delta_state", "delta_val", "sender", "src_val", "dst_val", "ps", "pv")
     out = {k: [] for k in keys}
@@ -157,10 +166,17 @@ def torch32_transition(dev, src, dst, rho, ps, pv, Ws, Wt, w, b, temperature, ma
         leaves = [torch.as_tensor(t[b0:b1]).to(**f32).requires_grad_(True) for t in (rho, src, dst, ps, pv)]
         r_, s_, d_, p_s, p_v = leaves
         m = None if mask is None else _bool_mask(mask, dev, b0, b1)
-        tgt = (d_ @ Wtd.T).transpose(-1, -2).contiguous()
-        l = ((s_ @ Wsd.T) * wd) @ tgt
-        if bd is not None:
-            l = l + bd
+        if Wsd.dim() == 3:  # stacked heads [H, r, D]: the max over the heads' logits
+            tgt = (d_[:, None] @ Wtd.transpose(-1, -2)).transpose(-1, -2).contiguous()
+            l = ((s_[:, None] @ Wsd.transpose(-1, -2)) * wd[:, None, :]) @ tgt
+            if bd is not None:
+                l = l + bd[:, None, None]
+            l = l.max(dim=1).values
+        else:
+            tgt = (d_ @ Wtd.T).transpose(-1, -2).contiguous()
+            l = ((s_ @ Wsd.T) * wd) @ tgt
+            if bd is not None:
+                l = l + bd
         l = l / float(temperature)
         wr = _route32(l, m, kind) * r_[..., :, None]
         ds = (wr * p_s[..., :, None]).sum(-2)

@@ -13,8 +13,10 @@ import torch
 from torch.nn import functional as F
 
 import jakal_oracle as O
-from jakal_net import (Layer, LayerDelta, LowRankBilinearPairwise, LowRankBilinearRoute, Propagation,
-                       SparsePropagation, SparseTransition, TemperatureScaledRoute, Transition)
+from jakal_net import (Layer, LayerDelta, LowRankBilinearPairwise, LowRankBilinearRoute, MultiHeadPairwise,
+                       MultiHeadRoute, Propagation, SparsePropagation, SparseTransition, TemperatureScaledRoute,
+                       Transition)
+from jakal_net import kernel_common as KC
 from jakal_net import native_backend as NB
 from jakal_net.compress import signed_abs_softmax, signed_entmax15
 
@@ -342,3 +344,137 @@ def test_progressive_step_matches_oracle_composition():
     stream = ProgressiveBStep(cfg, implementation="streaming")
     stream.load_state_dict(model.state_dict())
     assert float(stream(prefix, target).detach()) == pytest.approx(loss, rel=1e-10)
+
+
+# ---------------------------------------------------------------------------
+# multi-head scores (reference modules.py:259-301, 470-529)
+# ---------------------------------------------------------------------------
+def _heads(H, D, r, seed, *, bias=True):
+    torch.manual_seed(seed)
+    heads = [LowRankBilinearPairwise(D, r, bias=bias) for _ in range(H)]
+    with torch.no_grad():
+        for i, h in enumerate(heads):
+            h.weight.copy_(torch.rand(r) + 0.5)
+            if bias:
+                h.bias.fill_(0.1 * (i - 1))
+    return heads
+
+
+def _stacked(heads, route=False):
+    if route:
+        return (np.stack([_np(h.source_proj.weight) for h in heads]), np.stack([_np(h.target_proj.weight) for h in heads]),
+                np.stack([_np(h.weight) for h in heads]), np.array([float(h.bias.detach()) for h in heads]))
+    return (np.stack([_np(h.target_proj.weight) for h in heads]), np.stack([_np(h.source_proj.weight) for h in heads]),
+            np.stack([_np(h.weight) for h in heads]), np.array([float(h.bias.detach()) for h in heads]))
+
+
+def test_kat_multihead_pairwise_is_the_max_of_its_heads():
+    # tests/test_jakal_net.py:138-152 with low-rank heads of hand-set weights
+    a, b = LowRankBilinearPairwise(2, 1), LowRankBilinearPairwise(2, 1)
+    with torch.no_grad():
+        a.target_proj.weight.copy_(torch.tensor([[1.0, 0.0]]))
+        a.source_proj.weight.copy_(torch.tensor([[1.0, 0.0]]))
+        b.target_proj.weight.copy_(torch.tensor([[0.0, 2.0]]))
+        b.source_proj.weight.copy_(torch.tensor([[0.0, 1.0]]))
+        a.bias.fill_(1.0)
+        b.bias.zero_()
+    x = torch.tensor([[[1.0, 2.0], [0.5, -1.0], [-2.0, 1.0]]])
+    got = MultiHeadPairwise([a, b])(x, x)
+    want = torch.maximum(x[..., :1] @ x[..., :1].transpose(-1, -2) + 1.0, 2.0 * x[..., 1:] @ x[..., 1:].transpose(-1, -2))
+    assert torch.allclose(got, want)
+
+
+@pytest.mark.parametrize("aggregate", ["mean", "sum", "head_mean", "smoothmax", "signed_smoothmax"])
+def test_multihead_pairwise_aggregates(aggregate):
+    heads = _heads(3, 4, 2, 21)
+    x = torch.randn(2, 5, 4)
+    per = torch.stack([h(x, x) for h in heads], dim=-1)
+    want = {"mean": per.mean(-1), "sum": per.sum(-1), "head_mean": per.sum(-1),
+            "smoothmax": torch.logsumexp(per, -1) - np.log(3.0),
+            "signed_smoothmax": (per * torch.softmax(per.abs(), -1)).sum(-1)}[aggregate]
+    mod = MultiHeadPairwise(heads, aggregate=aggregate)
+    assert torch.allclose(mod(x, x), want)
+    assert torch.allclose(mod.head_scores(x, x), per)
+    assert not KC.supports_pairwise_kernel(mod)  # the library runs the max aggregation only
+
+
+@pytest.mark.parametrize("mode", ["dense", "topk", "window"])
+@pytest.mark.parametrize("kind", ["softsign", "signed_entmax15"])
+def test_multihead_propagation_forms_match_oracle(mode, kind):
+    heads = _heads(3, 6, 4, 22)
+    layer = Layer(dim=6, num_nodes=19, state=torch.randn(2, 19), val=torch.randn(2, 19, 6))
+    extra = {} if mode == "dense" else (dict(topk=4) if mode == "topk" else dict(window=3))
+    mk = (lambda impl: Propagation(MultiHeadPairwise(heads), edge_compress_fn=_fn(kind), implementation=impl,
+                                   target_block_size=5)) if mode == "dense" else (
+        lambda impl: SparsePropagation(MultiHeadPairwise(heads), sparse_type=mode, edge_compress_fn=_fn(kind),
+                                       implementation=impl, target_block_size=5, **extra))
+    U, V, w, b = _stacked(heads)
+    want = O.propagation_forward(_np(layer.val), _np(layer.state), _np(layer.val), U, V, w, b, mode=mode, kind=kind,
+                                 **extra)
+    assert len(np.unique(want["head"])) == 3
+    for impl in ("reference", "streaming"):
+        d = mk(impl)(layer)
+        np.testing.assert_allclose(_np(d.delta_state), want["delta_state"], rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(_np(d.delta_val), want["delta_val"], rtol=1e-10, atol=1e-12)
+
+
+def test_multihead_transition_forms_match_oracle():
+    torch.manual_seed(23)
+    B, Ns, Nd, D, r = 2, 13, 9, 5, 3
+    src = Layer(dim=D, num_nodes=Ns, state=torch.randn(B, Ns), val=torch.randn(B, Ns, D))
+    dst = Layer(dim=D, num_nodes=Nd, state=torch.randn(B, Nd), val=torch.randn(B, Nd, D))
+    heads = [LowRankBilinearRoute(D, D, rank=r) for _ in range(2)]
+    with torch.no_grad():
+        for i, h in enumerate(heads):
+            h.weight.copy_(torch.rand(r) + 0.5)
+            h.bias.fill_(0.3 * i - 0.1)
+    route = TemperatureScaledRoute(MultiHeadRoute(heads), 1.4)
+    Ws, Wt, w, b = _stacked(heads, route=True)
+    want = O.transition_forward(_np(src.val), _np(dst.val), O.softplus(_np(src.state)), _np(src.state), _np(src.val),
+                                Ws, Wt, w, b, topk=3, temperature=1.4, kind="signed_abs_softmax")
+    for impl in ("reference", "streaming"):
+        d = SparseTransition(route, topk=3, route_compress_name="signed_abs_softmax", implementation=impl,
+                             src_block_size=4).compute_delta(src, dst)
+        np.testing.assert_allclose(_np(d.delta_state), want["delta_state"], rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(_np(d.delta_val), want["delta_val"], rtol=1e-10, atol=1e-12)
+
+
+def test_multihead_kernel_specs_stack_the_heads():
+    heads = _heads(3, 6, 4, 24)
+    spec = KC.pairwise_kernel_spec(MultiHeadPairwise(heads))
+    assert spec.kind == "multihead_max_low_rank_bilinear"
+    assert spec.weight.shape == (3, 4) and spec.bias.shape == (3,)
+    assert spec.in_weight.shape == (3, 4, 6) and spec.out_weight.shape == (3, 4, 6)
+    assert torch.allclose(spec.weight[1], heads[1].normalized_weight())
+    assert KC.pairwise_kernel_spec(MultiHeadPairwise(_heads(2, 6, 4, 25, bias=False))).bias is None
+    # heads of different ranks, or a mix of biased and unbiased heads, are not one stacked spec
+    assert not KC.supports_pairwise_kernel(MultiHeadPairwise([LowRankBilinearPairwise(6, 4), LowRankBilinearPairwise(6, 3)]))
+    assert not KC.supports_pairwise_kernel(MultiHeadPairwise([LowRankBilinearPairwise(6, 4),
+                                                              LowRankBilinearPairwise(6, 4, bias=False)]))
+    # route heads: one temperature each, times an outer TemperatureScaledRoute's
+    rheads = [TemperatureScaledRoute(LowRankBilinearRoute(5, 5, rank=2), 2.0) for _ in range(2)]
+    route = TemperatureScaledRoute(MultiHeadRoute(rheads), 1.5)
+    rspec = KC.pairwise_route_kernel_spec(route)
+    assert rspec.kind == "multihead_max_low_rank_bilinear_route" and rspec.temperature == pytest.approx(3.0)
+    assert rspec.source_weight.shape == (2, 2, 5) and rspec.core_weight.shape == (2, 2)
+    x, y = torch.randn(1, 4, 5), torch.randn(1, 3, 5)
+    raw = torch.maximum(rheads[0].route_fn(x, y), rheads[1].route_fn(x, y))
+    assert torch.allclose(route(x, y), raw / 3.0)
+    mixed = MultiHeadRoute([TemperatureScaledRoute(LowRankBilinearRoute(5, 5, rank=2), 2.0),
+                            LowRankBilinearRoute(5, 5, rank=2)])
+    assert not KC.supports_pairwise_route_kernel(mixed)
+
+
+def test_native_mode_passes_stacked_multihead_specs(fake_native):
+    fake = fake_native()
+    heads = _heads(2, 4, 3, 26)
+    layer = Layer(dim=4, num_nodes=9, state=torch.randn(2, 9), val=torch.randn(2, 9, 4))
+    SparsePropagation(MultiHeadPairwise(heads), sparse_type="topk", topk=3, implementation="native")(layer)
+    (name, args), = fake.calls
+    assert name == "propagation_topk" and args[0] == "multihead_max_low_rank_bilinear"
+    assert args[1].shape == (2, 3) and args[2].shape == (2,) and args[3].shape == (2, 3, 4)
+    # a smoothmax aggregate is not the library's: native mode runs the streaming form
+    fake.calls.clear()
+    SparsePropagation(MultiHeadPairwise(heads, aggregate="smoothmax"), sparse_type="topk", topk=3,
+                      implementation="native")(layer)
+    assert fake.calls == []

@@ -91,3 +91,47 @@ def test_dense_backward_workspace_without_the_score_matrix():
     assert ws(16, 4096, 512, 512, 64, 0, 1) < 100 << 20
     assert ws(16, 4096, 512, 512, 64, 0, 0) > square
     assert ws(16, 4096, 512, 512, 64, 1, 1) > square
+
+
+def _declared_parameter_counts():
+    counts = {}
+    for header in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        for m in re.finditer(r"\b(jn_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+            params = m.group(2).strip()
+            counts[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
+    return counts
+
+
+def test_python_bindings_match_the_header_arity():
+    import jakal_net_native as JN  # loads the library; no device call
+
+    counts = _declared_parameter_counts()
+    bound = {name: getattr(JN._LIB, name).argtypes for name in counts if getattr(JN._LIB, name).argtypes is not None}
+    assert len(bound) >= 30
+    wrong = {n: (len(a), counts[n]) for n, a in bound.items() if len(a) != counts[n]}
+    assert not wrong, f"ctypes argtypes disagree with include/*.h (bound, declared): {wrong}"
+
+
+def test_multihead_workspace_queries_without_gpu():
+    lib = ctypes.CDLL(str(LIB))
+    I64 = ctypes.c_int64
+    fwd = lib.jn_propagation_topk_forward_multihead_workspace_bytes
+    fwd.argtypes, fwd.restype = [I64] * 4, ctypes.c_size_t
+    one = lib.jn_propagation_topk_forward_workspace_bytes
+    one.argtypes, one.restype = [I64] * 3, ctypes.c_size_t
+    # each head's ranks are padded to 32: 2 heads of rank 20 take the split rows of rank 64
+    assert fwd(2, 100, 20, 2) == one(2, 100, 64)
+    assert fwd(2, 100, 64, 2) == one(2, 100, 128)
+    assert fwd(2, 100, 64, 3) == 0  # 3 x 64 ranks exceed the select's four K-steps
+    bwd = lib.jn_propagation_topk_multihead_workspace_bytes
+    bwd.argtypes, bwd.restype = [I64] * 7, ctypes.c_size_t
+    single = lib.jn_propagation_topk_workspace_bytes
+    single.argtypes, single.restype = [I64] * 6, ctypes.c_size_t
+    # one more bias column per extra head in the row sums and the reduction stage
+    assert bwd(2, 100, 16, 16, 8, 4, 5) > single(2, 100, 16, 16, 32, 5)
+    tr = lib.jn_transition_topk_multihead_workspace_bytes
+    tr.argtypes, tr.restype = [I64] * 9, ctypes.c_size_t
+    assert tr(2, 50, 40, 8, 8, 8, 16, 2, 4) > 0
+    assert tr(2, 50, 40, 8, 8, 8, 64, 3, 4) == 0
+    assert tr(2, 50, 40, 8, 8, 8, 40, 3, 40) > 0  # every destination: no select, 3 x 40 <= 128 ranks

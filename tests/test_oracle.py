@@ -323,3 +323,117 @@ def test_planted_mistake_is_caught_by_finite_differences():
 def test_checkable_rows_gap_rule():
     s = np.array([[3.0, 2.0, 2.0 - 1e-7, 0.0], [3.0, 2.0, 1.0, 0.0]])
     assert O.checkable_rows(s, 2).tolist() == [False, True]
+
+
+# ---- multi-head max aggregation ---------------------------------------------------
+
+def _heads(r, H, R, D):
+    return r.normal(size=(H, R, D)), r.normal(size=(H, R, D)), r.normal(size=(H, R)), r.normal(size=H)
+
+
+def test_multihead_single_head_reduces_to_the_single_head_form():
+    r = _rng(11)
+    B, N, D, R = 2, 7, 3, 2
+    val, ps, pv = r.normal(size=(B, N, D)), r.normal(size=(B, N)), r.normal(size=(B, N, D))
+    U, V, w, b = _heads(r, 1, R, D)
+    g_ds, g_dv = r.normal(size=(B, N)), r.normal(size=(B, N, D))
+    kw = dict(mode="topk", topk=3, kind="signed_abs_softmax")
+    one = O.propagation_backward(val, ps, pv, U[0], V[0], w[0], float(b[0]), g_ds, g_dv, **kw)
+    many = O.propagation_backward(val, ps, pv, U, V, w, b, g_ds, g_dv, **kw)
+    for name in ("delta_state", "delta_val", "val", "ps", "pv"):
+        assert np.allclose(one[name], many[name], rtol=1e-12, atol=1e-12), name
+    for name in ("U", "V", "w", "b"):
+        assert np.allclose(np.asarray(one[name])[None], many[name], rtol=1e-12, atol=1e-12), name
+
+
+def test_kat_multihead_scores_are_the_largest_head_score():
+    # reference known-answer form (tests/test_jakal_net.py:138-152): the multi-head
+    # score is the elementwise maximum of the heads' scores.  Two rank-1 heads
+    # with hand-set weights: head 0 scores x_i0 * x_j0 + 1, head 1 scores
+    # 2 x_i1 * x_j1 (w_hat = +-1 after normalisation).
+    U = np.array([[[1.0, 0.0]], [[0.0, 2.0]]])
+    V = np.array([[[1.0, 0.0]], [[0.0, 1.0]]])
+    w = np.array([[3.0], [0.5]])
+    b = np.array([1.0, 0.0])
+    x = np.array([[[1.0, 2.0], [0.5, -1.0], [-2.0, 1.0]]])
+    s, head, _ = O.multihead_pairwise_scores(x, x, U, V, w, b)
+    h0 = np.outer(x[0, :, 0], x[0, :, 0]) + 1.0
+    h1 = 2.0 * np.outer(x[0, :, 1], x[0, :, 1])
+    assert np.allclose(s[0], np.maximum(h0, h1))
+    assert (head[0] == np.where(h1 > h0, 1, 0)).all()
+    l, lhead, _ = O.multihead_route_logits(x, x[:, :2], U, V, w, b, temperature=2.0)
+    r0 = 3.0 * np.outer(x[0, :, 0], x[0, :2, 0]) + 1.0
+    r1 = 0.5 * 2.0 * np.outer(x[0, :, 1], x[0, :2, 1])
+    assert np.allclose(l[0], np.maximum(r0, r1) / 2.0)
+    assert (lhead[0] == np.where(r1 > r0, 1, 0)).all()
+
+
+@pytest.mark.parametrize("mode,kind", [("topk", "softsign"), ("window", "signed_abs_softmax"),
+                                       ("dense", "signed_entmax15"), ("topk", "signed_entmax15")])
+def test_multihead_propagation_backward_matches_finite_differences(mode, kind):
+    r = _rng(12)
+    B, N, D, R, H = 2, 6, 3, 2, 3
+    val, ps, pv = r.normal(size=(B, N, D)), r.normal(size=(B, N)), r.normal(size=(B, N, D))
+    U, V, w, b = _heads(r, H, R, D)
+    g_ds, g_dv = r.normal(size=(B, N)), r.normal(size=(B, N, D))
+    kw = dict(mode=mode, topk=2, window=2, kind=kind)
+    f0 = O.propagation_forward(val, ps, pv, U, V, w, b, **kw)
+    assert len(np.unique(f0["head"])) == H, "every head should win some pairs"
+
+    def loss():
+        out = O.propagation_forward(val, ps, pv, U, V, w, b, **kw)
+        assert (out["mask"] == f0["mask"]).all() and (out["head"] == f0["head"]).all()
+        return float(np.sum(out["delta_state"] * g_ds) + np.sum(out["delta_val"] * g_dv))
+
+    g = O.propagation_backward(val, ps, pv, U, V, w, b, g_ds, g_dv, **kw)
+    for name, arr in (("val", val), ("ps", ps), ("pv", pv), ("U", U), ("V", V), ("w", w), ("b", b)):
+        assert np.allclose(g[name], _fd(loss, arr), rtol=1e-5, atol=1e-6), name
+
+
+@pytest.mark.parametrize("kind", ["softmax", "signed_entmax15"])
+def test_multihead_transition_backward_matches_finite_differences(kind):
+    r = _rng(13)
+    B, Ns, Nd, D, Dd, R, H = 2, 5, 4, 3, 2, 2, 2
+    src, dst = r.normal(size=(B, Ns, D)), r.normal(size=(B, Nd, D))
+    sender = r.normal(size=(B, Ns)) ** 2 + 0.1
+    ps, pv = r.normal(size=(B, Ns)), r.normal(size=(B, Ns, Dd))
+    Ws, Wt, w, b = _heads(r, H, R, D)
+    g_ds, g_dv = r.normal(size=(B, Nd)), r.normal(size=(B, Nd, Dd))
+    kw = dict(topk=2, temperature=1.3, kind=kind)
+    f0 = O.transition_forward(src, dst, sender, ps, pv, Ws, Wt, w, b, **kw)
+
+    def loss():
+        out = O.transition_forward(src, dst, sender, ps, pv, Ws, Wt, w, b, **kw)
+        assert (out["mask"] == f0["mask"]).all() and (out["head"] == f0["head"]).all()
+        return float(np.sum(out["delta_state"] * g_ds) + np.sum(out["delta_val"] * g_dv))
+
+    g = O.transition_backward(src, dst, sender, ps, pv, Ws, Wt, w, b, g_ds, g_dv, **kw)
+    for name, arr in (("src_val", src), ("dst_val", dst), ("sender", sender), ("ps", ps), ("pv", pv),
+                      ("Ws", Ws), ("Wt", Wt), ("w", w), ("b", b)):
+        assert np.allclose(g[name], _fd(loss, arr), rtol=1e-5, atol=1e-6), name
+
+
+def test_planted_multihead_mistake_is_caught():
+    # Passing every pair's score gradient to all heads (not just the winner) must fail the FD check.
+    r = _rng(14)
+    B, N, D, R, H = 1, 5, 2, 2, 2
+    val, ps, pv = r.normal(size=(B, N, D)), r.normal(size=(B, N)), r.normal(size=(B, N, D))
+    U, V, w, b = _heads(r, H, R, D)
+    g_ds, g_dv = r.normal(size=(B, N)), r.normal(size=(B, N, D))
+    kw = dict(mode="dense", kind="softsign")
+
+    def loss():
+        out = O.propagation_forward(val, ps, pv, U, V, w, b, **kw)
+        return float(np.sum(out["delta_state"] * g_ds) + np.sum(out["delta_val"] * g_dv))
+
+    def unmasked(score_backward, head, n_heads, g_s):  # planted: no per-head mask
+        parts = [score_backward(h, g_s) for h in range(n_heads)]
+        return {k: np.stack([np.asarray(p[k]) for p in parts]) for k in parts[0] if k != "val"}
+
+    orig = O._per_head_backward
+    try:
+        O._per_head_backward = unmasked
+        bad = O.propagation_backward(val, ps, pv, U, V, w, b, g_ds, g_dv, **kw)
+    finally:
+        O._per_head_backward = orig
+    assert not np.allclose(bad["U"], _fd(loss, U), rtol=1e-4, atol=1e-6)

@@ -14,6 +14,9 @@ Other workloads (--workload), one per hot-path row, same output format:
               routes, states and vals ~ N(0,1), default init.
   c4-dense    BASELINE config 4, dense variant: Propagation over all N x N pairs,
               B=16, N=4096, D=512, r=64, softsign, inputs as c4-topk.
+  c4-topk-bf16 BASELINE config 4 (C4-topk bf16 row): c4-topk with bf16 layer
+              states and values; the value rows move as bf16 and the top-k
+              scores run on bf16 MFMAs (sparse-byte budget 6.72 GB).
 
 Inputs and parameters are resident in HBM before the timed region.
 
@@ -54,6 +57,7 @@ sys.path.insert(0, str(ROOT / "jakal-net_amd"))
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 FP16_MFMA_PEAK_TFLOPS = 2500.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
 # split-fp16 select: fp16 MFMA products per fp32-equivalent product (hi.hi + hi.lo + lo.hi)
 SPLIT_PRODUCTS = 3
 
@@ -61,15 +65,16 @@ SPLIT_PRODUCTS = 3
 CONFIG = {"batch": 16, "nodes": 4096, "dim": 512, "rank": 64, "topk": 32}
 
 
-def rows_backward_split(nk: int, D: int) -> bool:
+def rows_backward_split(nk: int, D: int, vb: int = 4) -> bool:
     """Whether the library runs the row backward's dot products as two column
     slabs first (rows_backward_dots_kernel): value rows of a batch element above
-    2 MiB with 256 < D <= 1024 (jn_edges.hip, rows_backward_slab)."""
-    return 256 < D <= 1024 and nk * D * 4 > (2 << 20)
+    2 MiB with 256 < D <= 1024 (jn_edges.hip, rows_backward_slab); vb bytes per
+    value element."""
+    return 256 < D <= 1024 and nk * D * vb > (2 << 20)
 
 
 def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = False,
-                      Mk: int | None = None) -> tuple | None:
+                      Mk: int | None = None, vb: float = 4.0) -> tuple | None:
     """(bound, algorithmic bytes or flops, compulsory bytes) of the edge-list kernels.
 
     M = aggregated (query) rows, Mk = source (key) rows (M for propagation),
@@ -79,16 +84,18 @@ def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = F
     and each output once: the HBM bytes no schedule can avoid.  The gathers
     reuse each value row about k times from L2, so their algorithmic rate is an
     L2-side figure and their HBM roofline fraction is priced on compulsory bytes.
-    split: the row backward runs as dots + finish."""
+    split: the row backward runs as dots + finish.  vb: bytes per value-row
+    element (4 fp32, 2 bf16); projections, scores and edge records stay fp32."""
     Mk = M if Mk is None else Mk
+    D4 = vb * D  # bytes of one value row
     if name.startswith("rows_forward_kernel"):
         # idx+score+ps per edge, pv row per edge; delta_val row + delta_state per row
-        return ("hbm", E * (12.0 + 4.0 * D) + M * (4.0 * D + 4.0),
-                E * 8.0 + Mk * (4.0 * D + 4.0) + M * (4.0 * D + 4.0))
+        return ("hbm", E * (12.0 + D4) + M * (D4 + 4.0),
+                E * 8.0 + Mk * (D4 + 4.0) + M * (D4 + 4.0))
     if name.startswith("rows_backward_dots_kernel"):
         # idx, pv row, partial-dot write per edge; grad-delta row per row
-        return ("hbm", E * (4.0 + 4.0 * D + 4.0) + M * 4.0 * D,
-                E * 12.0 + (M + Mk) * 4.0 * D)
+        return ("hbm", E * (4.0 + D4 + 4.0) + M * D4,
+                E * 12.0 + (M + Mk) * D4)
     if name.startswith("rows_backward_kernel"):
         if split:
             # idx+score, two partial dots, ps, key row, gsc+coef writes per edge;
@@ -97,12 +104,12 @@ def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = F
                     E * 24.0 + Mk * (4.0 + 4.0 * r) + M * (8.0 + 4.0 * r))
         # idx+score, ps, pv row, key row per edge; gsc+coef writes per edge;
         # grad-delta row + state, dq row, row sum per row
-        return ("hbm", E * (8.0 + 4.0 + 4.0 * D + 4.0 * r + 8.0) + M * (4.0 * D + 4.0 + 4.0 * r + 4.0),
-                E * 16.0 + Mk * (4.0 * D + 4.0 * r + 4.0) + M * (4.0 * D + 4.0 * r + 8.0))
+        return ("hbm", E * (8.0 + 4.0 + D4 + 4.0 * r + 8.0) + M * (D4 + 4.0 + 4.0 * r + 4.0),
+                E * 16.0 + Mk * (D4 + 4.0 * r + 4.0) + M * (D4 + 4.0 * r + 8.0))
     if name.startswith("cols_gather_kernel"):
         # edge record, grad-delta row per edge; segment bounds, grad_pv row, grad_ps per column
-        return ("hbm", E * (16.0 + 4.0 * D) + Mk * (8.0 + 4.0 * D + 4.0),
-                E * 16.0 + M * 4.0 * D + Mk * (4.0 * D + 8.0))
+        return ("hbm", E * (16.0 + D4) + Mk * (8.0 + D4 + 4.0),
+                E * 16.0 + M * D4 + Mk * (D4 + 8.0))
     if name.startswith("cols_keygrad_kernel"):
         # edge record, query row per edge; segment bounds, dk row, key row per column
         return ("hbm", E * (16.0 + 4.0 * r) + Mk * (8.0 + 8.0 * r),
@@ -127,13 +134,19 @@ def split_prep_model(name: str, key_rows: float, r: int) -> tuple | None:
     return None
 
 
-def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int) -> tuple | None:
-    """Kernel model of the headline (top-k) workload."""
+def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int, bf16: bool = False) -> tuple | None:
+    """Kernel model of the top-k workload (bf16: bf16 value rows and bf16 select
+    operands, priced against the bf16 MFMA peak)."""
     if name.startswith("lowrank_topk_select_kernel"):
-        return "mfma", 2.0 * B * N * N * r, None
+        return "mfma", 2.0 * B * N * N * r, None, BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
     if name.startswith("select_split_"):
         return split_prep_model(name, B * N, r)
-    return edge_kernel_model(name, B * N, B * N * k, D, r, rows_backward_split(N, D))
+    if name.startswith("select_bf16_keys_kernel"):
+        # reads the fp32 key rows, writes bf16 rows of the rank rounded up to 32
+        rp = -(-r // 32) * 32
+        return "hbm", B * N * (4.0 * r + 2.0 * rp), B * N * (4.0 * r + 2.0 * rp)
+    vb = 2 if bf16 else 4
+    return edge_kernel_model(name, B * N, B * N * k, D, r, rows_backward_split(N, D, vb), vb=float(vb))
 
 
 def _cpu_model() -> str:
@@ -251,6 +264,37 @@ class TopkC4:
                                implementation=impl).to(dev)
         return op, Layer(dim=D, num_nodes=N, state=state.to(dev).requires_grad_(True),
                          val=val.to(dev).requires_grad_(True))
+
+
+class TopkC4Bf16(TopkC4):
+    """c4-topk with bf16 layer states and values (BASELINE C4-topk bf16 row)."""
+
+    name = "c4-topk-bf16"
+    metric = ("routed pairs/sec + HBM GB/s (% peak), SparsePropagation N=4096 D=512 k=32 fwd+bwd, "
+              "bf16 activations")
+    workload = "C4-topk bf16 SparsePropagation fwd+bwd, LowRankBilinearPairwise, bf16 layers, native"
+    data = ("synthetic (seeded N(0,1) state, unit-norm N(0,1) val rows, both rounded to bf16; default module "
+            "init, fp32 weights)")
+    dtype = "bf16"
+    traffic_file = "c4_topk_bf16_hbm_traffic.json"
+    cpu_batch = 1
+
+    def model(self, name):
+        c = self.config
+        return kernel_model(name, c["batch"], c["nodes"], c["dim"], c["rank"], c["topk"], bf16=True)
+
+    def sparse_bytes(self) -> float:
+        # TopkC4's budget with 2-byte value rows (6.72 GB per step)
+        c = self.config
+        E, M, D = self.edges(), c["batch"] * c["nodes"], c["dim"]
+        return 3 * 2 * D * (E + M) + 24 * E + 3 * 4 * (E + M)
+
+    def build(self, torch, dev, impl: str = "native", batch: int | None = None):
+        from jakal_net import Layer
+
+        op, layer = super().build(torch, dev, impl=impl, batch=batch)
+        bf = lambda t: t.detach().bfloat16().requires_grad_(True)  # noqa: E731
+        return op, Layer(dim=layer.dim, num_nodes=layer.num_nodes, state=bf(layer.state), val=bf(layer.val))
 
 
 class WindowC2:
@@ -592,7 +636,7 @@ class ProgressiveC5:
         return step
 
 
-WORKLOADS = {w.name: w for w in (TopkC4(), WindowC2(), TransitionC3(), DenseC4(), DenseCausalC4(),
+WORKLOADS = {w.name: w for w in (TopkC4(), TopkC4Bf16(), WindowC2(), TransitionC3(), DenseC4(), DenseCausalC4(),
                                  TransitionDenseC3(), ProgressiveC5())}
 
 
@@ -690,10 +734,13 @@ def main() -> int:
                              l2_side_GBps=round(work / (avg_ms / 1e3) / 1e9, 1))
             else:
                 achieved = work / (avg_ms / 1e3) / 1e12
-                entry.update(bound="mfma", flops=work, achieved_TFLOPs=round(achieved, 2),
-                             frac=round(achieved / FP32_MFMA_PEAK_TFLOPS, 4))
+                peak = model[3] if len(model) > 3 else FP32_MFMA_PEAK_TFLOPS
+                entry.update(bound="mfma", flops=work, achieved_TFLOPs=round(achieved, 2), peak_TFLOPs=peak,
+                             frac=round(achieved / peak, 4))
                 if name.startswith("lowrank_topk_select_kernel"):
-                    if args.select_mode == "split-f16":
+                    if getattr(wl, "dtype", "f32") == "bf16":
+                        entry.update(arith="bf16 MFMA (v_mfma_f32_16x16x32_bf16), fp32 accumulate")
+                    elif args.select_mode == "split-f16":
                         # flops count fp32-equivalent score products; the MFMA pipe runs
                         # SPLIT_PRODUCTS fp16 products for each
                         f16 = SPLIT_PRODUCTS * achieved
@@ -726,7 +773,7 @@ def main() -> int:
                     "unit": "GB/s", "frac": dom["frac"], "traffic": dom.get("traffic_bytes")}
     else:
         roofline = {"kernel": dom_name, "bound": "mfma", "achieved": dom["achieved_TFLOPs"],
-                    "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
+                    "peak": dom["peak_TFLOPs"], "unit": "TFLOP/s", "frac": dom["frac"],
                     "traffic": dom.get("traffic_bytes")}
         if "arith" in dom:
             roofline["arith"] = dom["arith"]

@@ -30,7 +30,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 5. */
+/* ABI revision of this header (bumped on any signature change); this is 6. */
 int jn_abi_version(void);
 
 /*
@@ -437,6 +437,69 @@ int jn_transition_topk_backward_multihead(
     float* grad_src_val, float* grad_dst_val, float* grad_projected_state, float* grad_projected_val,
     float* grad_source_weight, float* grad_target_weight, float* grad_core_weight, float* grad_bias,
     void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+/*
+ * bf16 layers (layer values under autocast, src/jakal_net/modules.py:95-97;
+ * bf16/fp16 score operands of native/jakal_net_native_cuda.cu:2492-2497).
+ * The uint16_t tensors hold bf16 bit patterns: layer_val, projected_val and
+ * delta_val, and in the backward grad_delta_val, grad_layer_val and
+ * grad_projected_val (src_val, dst_val and their gradients for transitions).
+ * States, weights, projections, edge lists and their gradients stay fp32.
+ * Every value row the gathers move is bf16 (half the bytes of the fp32 entry
+ * points); projections accumulate bf16 x fp32 products in fp32; top-k scores
+ * are bf16(q * core_weight) . bf16(key) accumulated in fp32 on
+ * v_mfma_f32_16x16x32_bf16; sums accumulate in fp32 and round to bf16 once
+ * per stored element.  Workspaces, limits and the other arguments are those of
+ * the fp32 entry point of the same name.
+ */
+int jn_propagation_topk_forward_bf16(const uint16_t* layer_val, const float* projected_state,
+                                     const uint16_t* projected_val, const float* target_weight,
+                                     const float* source_weight, const float* core_weight, const float* bias,
+                                     int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                     int64_t topk, int32_t compress_kind, float* delta_state, uint16_t* delta_val,
+                                     float* projections, int32_t* topk_index, float* topk_score, void* workspace,
+                                     size_t workspace_bytes, jn_stream_t stream);
+int jn_propagation_topk_backward_bf16(
+    const uint16_t* layer_val, const float* projected_state, const uint16_t* projected_val,
+    const float* target_weight, const float* source_weight, const float* core_weight, const float* projections,
+    const int32_t* topk_index, const float* topk_score, const float* grad_delta_state,
+    const uint16_t* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+    int64_t topk, int32_t compress_kind, int32_t projected_val_is_layer_val, uint16_t* grad_layer_val,
+    float* grad_projected_state, uint16_t* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+int jn_propagation_window_forward_bf16(const uint16_t* layer_val, const float* projected_state,
+                                       const uint16_t* projected_val, const float* target_weight,
+                                       const float* source_weight, const float* core_weight, const float* bias,
+                                       int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                       int64_t window, int32_t compress_kind, float* delta_state,
+                                       uint16_t* delta_val, float* projections, int32_t* edge_index,
+                                       float* edge_score, jn_stream_t stream);
+int jn_propagation_window_backward_bf16(
+    const uint16_t* layer_val, const float* projected_state, const uint16_t* projected_val,
+    const float* target_weight, const float* source_weight, const float* core_weight, const float* projections,
+    const int32_t* edge_index, const float* edge_score, const float* grad_delta_state,
+    const uint16_t* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+    int64_t window, int32_t compress_kind, int32_t projected_val_is_layer_val, uint16_t* grad_layer_val,
+    float* grad_projected_state, uint16_t* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+int jn_transition_topk_forward_bf16(const float* sender_strength, const uint16_t* src_val, const uint16_t* dst_val,
+                                    const float* projected_state, const uint16_t* projected_val,
+                                    const float* source_weight, const float* target_weight, const float* core_weight,
+                                    const float* bias, float temperature, int64_t batch, int64_t src_nodes,
+                                    int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim,
+                                    int64_t rank, int64_t topk, int32_t compress_kind, float* delta_state,
+                                    uint16_t* delta_val, float* src_proj, float* dst_proj, int32_t* route_index,
+                                    float* route_logit, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+int jn_transition_topk_backward_bf16(
+    const float* sender_strength, const uint16_t* src_val, const uint16_t* dst_val, const float* projected_state,
+    const uint16_t* projected_val, const float* source_weight, const float* target_weight, const float* core_weight,
+    const float* src_proj, const float* dst_proj, const int32_t* route_index, const float* route_logit,
+    const float* grad_delta_state, const uint16_t* grad_delta_val, float temperature, int64_t batch,
+    int64_t src_nodes, int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+    int64_t topk, int32_t compress_kind, float* grad_sender_strength, uint16_t* grad_src_val,
+    uint16_t* grad_dst_val, float* grad_projected_state, uint16_t* grad_projected_val, float* grad_source_weight,
+    float* grad_target_weight, float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
+    jn_stream_t stream);
 
 #ifdef __cplusplus
 }

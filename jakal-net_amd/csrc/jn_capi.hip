@@ -306,7 +306,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
                                int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
                                float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
                                float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
-                               hipStream_t stream) {
+                               hipStream_t stream, bool bf16 = false) {
   int rc;
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
                  projections && topk_index && topk_score && grad_delta_state && grad_delta_val &&
@@ -348,6 +348,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   rb.dq = s.dP;
   rb.lddq = 2 * r;
   rb.rowsum_gs = s.rowsum;
+  rb.bf16 = bf16 ? 1 : 0;
   if (mh) {
     rb.ehead = edge_head;
     rb.heads = (int)heads;
@@ -396,6 +397,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   cb.dk = s.dP + r;
   cb.lddk = 2 * r;
   cb.part_c = s.part_c;
+  cb.bf16 = bf16 ? 1 : 0;
   if (mh) {
     cb.heads = (int)heads;
     cb.head_rank = (int)(rank / heads);
@@ -406,7 +408,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   // 4. projection weight grads: [dU; dV] = dP^T . X  (split-K, fixed order)
   if (grad_target_weight && grad_source_weight) {
     rc = gemm_grad_weight(s.dP, 2 * r, layer_val, in_dim, grad_target_weight, grad_source_weight, r, 2 * r,
-                          (int)in_dim, M, s.splitk, st);
+                          (int)in_dim, M, s.splitk, st, bf16);
     if (rc) return rc;
   }
 
@@ -414,7 +416,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   if (grad_layer_val) {
     const float* addend = (projected_val_is_layer_val && gpv) ? grad_layer_val : nullptr;
     rc = gemm_grad_input(s.dP, 2 * r, target_weight, source_weight, r, in_dim, addend, in_dim, grad_layer_val,
-                         in_dim, M, (int)in_dim, 2 * r, st);
+                         in_dim, M, (int)in_dim, 2 * r, st, bf16);
     if (rc) return rc;
   }
 
@@ -432,7 +434,7 @@ int propagation_topk_forward_impl(const float* layer_val, const float* projected
                                   int64_t rank, int64_t heads, int64_t topk, int32_t compress_kind,
                                   float* delta_state, float* delta_val, float* projections, int32_t* topk_index,
                                   float* topk_score, uint8_t* topk_head, void* workspace, size_t workspace_bytes,
-                                  hipStream_t st) {
+                                  hipStream_t st, bool bf16 = false) {
   int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
   if (rc) return rc;
   const bool mh = heads > 1;
@@ -442,7 +444,7 @@ int propagation_topk_forward_impl(const float* layer_val, const float* projected
   const int M = (int)(batch * nodes), r = (int)rank, k = (int)topk;
 
   rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, M, 2 * r,
-                    (int)in_dim, st);
+                    (int)in_dim, st, bf16);
   if (rc) return rc;
 
   SelectArgs s{};
@@ -465,6 +467,7 @@ int propagation_topk_forward_impl(const float* layer_val, const float* projected
   s.out_score = topk_score;
   s.ws = workspace;
   s.ws_bytes = workspace_bytes;
+  s.bf16 = bf16 ? 1 : 0;
   if (mh) {
     s.heads = (int)heads;
     s.head_rank = (int)(rank / heads);
@@ -510,6 +513,7 @@ int propagation_topk_forward_impl(const float* layer_val, const float* projected
   f.rows = M;
   f.out_state = delta_state;
   f.out_val = delta_val;
+  f.bf16 = bf16 ? 1 : 0;
   return launch_rows_forward(f, st);
 }
 
@@ -519,7 +523,7 @@ int propagation_window_forward_impl(const float* layer_val, const float* project
                                     const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                     int64_t rank, int64_t heads, int64_t window, int32_t compress_kind,
                                     float* delta_state, float* delta_val, float* projections, int32_t* edge_index,
-                                    float* edge_score, uint8_t* edge_head, hipStream_t st) {
+                                    float* edge_score, uint8_t* edge_head, hipStream_t st, bool bf16 = false) {
   JN_REQUIRE(window >= 0, kInvalidArgument, "window must be non-negative (got %lld)", (long long)window);
   const int64_t width = window_width(window, nodes);
   int rc = check_edge_shapes(batch, nodes, in_dim, out_dim, rank, width, compress_kind);
@@ -531,7 +535,7 @@ int propagation_window_forward_impl(const float* layer_val, const float* project
   const int M = (int)(batch * nodes), r = (int)rank;
 
   rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, M, 2 * r,
-                    (int)in_dim, st);
+                    (int)in_dim, st, bf16);
   if (rc) return rc;
 
   WindowScoreArgs w{};
@@ -572,6 +576,7 @@ int propagation_window_forward_impl(const float* layer_val, const float* project
   f.rows = M;
   f.out_state = delta_state;
   f.out_val = delta_val;
+  f.bf16 = bf16 ? 1 : 0;
   return launch_rows_forward(f, st);
 }
 
@@ -584,7 +589,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 5; }
+int jn_abi_version(void) { return 6; }
 
 int jn_profile_enable(int32_t on) {
   std::lock_guard<std::mutex> lock(jakal::g_prof_mu);
@@ -773,7 +778,8 @@ static int transition_topk_forward_impl(const float* sender_strength, const floa
                                  int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
                                  int64_t topk, int32_t compress_kind, float* delta_state, float* delta_val,
                                  float* src_proj, float* dst_proj, int32_t* route_index, float* route_logit,
-                                 uint8_t* route_head, void* workspace, size_t workspace_bytes, hipStream_t st) {
+                                 uint8_t* route_head, void* workspace, size_t workspace_bytes, hipStream_t st,
+                                 bool bf16 = false) {
   int rc = check_transition_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, topk, compress_kind,
                                    temperature);
   if (rc) return rc;
@@ -791,10 +797,10 @@ static int transition_topk_forward_impl(const float* sender_strength, const floa
 
   // 1. projections P_s = src . Ws^T, P_t = dst . Wt^T  (modules.py:435-437)
   rc = gemm_project(src_val, src_dim, source_weight, source_weight, r, src_dim, src_proj, r, B * Ns, r, (int)src_dim,
-                    st);
+                    st, bf16);
   if (rc) return rc;
   rc = gemm_project(dst_val, dst_dim, target_weight, target_weight, r, dst_dim, dst_proj, r, B * Nd, r, (int)dst_dim,
-                    st);
+                    st, bf16);
   if (rc) return rc;
 
   // 2. per-source edge list: logits ((P_s * w) . P_t + b) / T, top-k over destinations
@@ -819,6 +825,7 @@ static int transition_topk_forward_impl(const float* sender_strength, const floa
     a.out_score = route_logit;
     a.ws = s.select_ws;
     a.ws_bytes = s.select_ws_bytes;
+    a.bf16 = bf16 ? 1 : 0;
     if (mh) {
       a.heads = (int)heads;
       a.head_rank = (int)(rank / heads);
@@ -904,6 +911,7 @@ static int transition_topk_forward_impl(const float* sender_strength, const floa
   cb.ld_gpv = val_dim;
   cb.grad_ps = delta_state;
   cb.profile_name = "route_gather_kernel";
+  cb.bf16 = bf16 ? 1 : 0;
   return launch_cols_backward(cb, st);
 }
 
@@ -918,7 +926,7 @@ static int transition_topk_backward_impl(const float* sender_strength, const flo
                                   float* grad_src_val, float* grad_dst_val, float* grad_projected_state,
                                   float* grad_projected_val, float* grad_source_weight, float* grad_target_weight,
                                   float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
-                                  hipStream_t st) {
+                                  hipStream_t st, bool bf16 = false) {
   int rc = check_transition_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, topk, compress_kind,
                                    temperature);
   if (rc) return rc;
@@ -964,6 +972,7 @@ static int transition_topk_backward_impl(const float* sender_strength, const flo
   rb.dq = s.dPs;
   rb.lddq = r;
   rb.rowsum = s.rowsum;
+  rb.bf16 = bf16 ? 1 : 0;
   if (mh) {
     rb.ehead = route_head;
     rb.heads = (int)heads;
@@ -1013,22 +1022,22 @@ static int transition_topk_backward_impl(const float* sender_strength, const flo
   // 3. projection weight and input grads
   if (grad_source_weight) {
     rc = gemm_grad_weight(s.dPs, r, src_val, src_dim, grad_source_weight, grad_source_weight, r, r, (int)src_dim,
-                          B * Ns, s.splitk, st);
+                          B * Ns, s.splitk, st, bf16);
     if (rc) return rc;
   }
   if (grad_target_weight) {
     rc = gemm_grad_weight(s.dPt, r, dst_val, dst_dim, grad_target_weight, grad_target_weight, r, r, (int)dst_dim,
-                          B * Nd, s.splitk, st);
+                          B * Nd, s.splitk, st, bf16);
     if (rc) return rc;
   }
   if (grad_src_val) {
     rc = gemm_grad_input(s.dPs, r, source_weight, source_weight, r, src_dim, nullptr, 0, grad_src_val, src_dim,
-                         B * Ns, (int)src_dim, r, st);
+                         B * Ns, (int)src_dim, r, st, bf16);
     if (rc) return rc;
   }
   if (grad_dst_val) {
     rc = gemm_grad_input(s.dPt, r, target_weight, target_weight, r, dst_dim, nullptr, 0, grad_dst_val, dst_dim,
-                         B * Nd, (int)dst_dim, r, st);
+                         B * Nd, (int)dst_dim, r, st, bf16);
     if (rc) return rc;
   }
 
@@ -1220,6 +1229,112 @@ int jn_transition_topk_backward_multihead(
                                        grad_projected_state, grad_projected_val, grad_source_weight,
                                        grad_target_weight, grad_core_weight, grad_bias, workspace, workspace_bytes,
                                        static_cast<hipStream_t>(stream));
+}
+
+// ---- bf16 layers -------------------------------------------------------------------
+// The bf16 tensors arrive as bf16 bit patterns; every kernel that touches them
+// reads and writes bf16 (the reinterpret_casts only carry the pointers).
+int jn_propagation_topk_forward_bf16(const uint16_t* layer_val, const float* projected_state,
+                                     const uint16_t* projected_val, const float* target_weight,
+                                     const float* source_weight, const float* core_weight, const float* bias,
+                                     int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                     int64_t topk, int32_t compress_kind, float* delta_state, uint16_t* delta_val,
+                                     float* projections, int32_t* topk_index, float* topk_score, void* workspace,
+                                     size_t workspace_bytes, jn_stream_t stream) {
+  return propagation_topk_forward_impl(reinterpret_cast<const float*>(layer_val), projected_state, reinterpret_cast<const float*>(projected_val), target_weight,
+                                       source_weight, core_weight, bias, batch, nodes, in_dim, out_dim, rank, 1, topk,
+                                       compress_kind, delta_state, reinterpret_cast<float*>(delta_val), projections, topk_index,
+                                       topk_score, nullptr, workspace, workspace_bytes,
+                                       static_cast<hipStream_t>(stream), true);
+}
+
+int jn_propagation_topk_backward_bf16(
+    const uint16_t* layer_val, const float* projected_state, const uint16_t* projected_val,
+    const float* target_weight, const float* source_weight, const float* core_weight, const float* projections,
+    const int32_t* topk_index, const float* topk_score, const float* grad_delta_state,
+    const uint16_t* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+    int64_t topk, int32_t compress_kind, int32_t projected_val_is_layer_val, uint16_t* grad_layer_val,
+    float* grad_projected_state, uint16_t* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  const int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
+  if (rc) return rc;
+  return propagation_edges_backward(reinterpret_cast<const float*>(layer_val), projected_state, reinterpret_cast<const float*>(projected_val), target_weight,
+                                    source_weight, core_weight, projections, topk_index, topk_score, nullptr,
+                                    grad_delta_state, reinterpret_cast<const float*>(grad_delta_val), batch, nodes, in_dim, out_dim, rank, 1,
+                                    topk, compress_kind, projected_val_is_layer_val, reinterpret_cast<float*>(grad_layer_val),
+                                    grad_projected_state, reinterpret_cast<float*>(grad_projected_val), grad_target_weight,
+                                    grad_source_weight, grad_core_weight, grad_bias, workspace, workspace_bytes,
+                                    static_cast<hipStream_t>(stream), true);
+}
+
+int jn_propagation_window_forward_bf16(const uint16_t* layer_val, const float* projected_state,
+                                       const uint16_t* projected_val, const float* target_weight,
+                                       const float* source_weight, const float* core_weight, const float* bias,
+                                       int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                       int64_t window, int32_t compress_kind, float* delta_state,
+                                       uint16_t* delta_val, float* projections, int32_t* edge_index,
+                                       float* edge_score, jn_stream_t stream) {
+  return propagation_window_forward_impl(reinterpret_cast<const float*>(layer_val), projected_state, reinterpret_cast<const float*>(projected_val), target_weight,
+                                         source_weight, core_weight, bias, batch, nodes, in_dim, out_dim, rank, 1,
+                                         window, compress_kind, delta_state, reinterpret_cast<float*>(delta_val), projections, edge_index,
+                                         edge_score, nullptr, static_cast<hipStream_t>(stream), true);
+}
+
+int jn_propagation_window_backward_bf16(
+    const uint16_t* layer_val, const float* projected_state, const uint16_t* projected_val,
+    const float* target_weight, const float* source_weight, const float* core_weight, const float* projections,
+    const int32_t* edge_index, const float* edge_score, const float* grad_delta_state,
+    const uint16_t* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+    int64_t window, int32_t compress_kind, int32_t projected_val_is_layer_val, uint16_t* grad_layer_val,
+    float* grad_projected_state, uint16_t* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  JN_REQUIRE(window >= 0, kInvalidArgument, "window must be non-negative (got %lld)", (long long)window);
+  const int64_t width = window_width(window, nodes);
+  const int rc = check_edge_shapes(batch, nodes, in_dim, out_dim, rank, width, compress_kind);
+  if (rc) return rc;
+  return propagation_edges_backward(reinterpret_cast<const float*>(layer_val), projected_state, reinterpret_cast<const float*>(projected_val), target_weight,
+                                    source_weight, core_weight, projections, edge_index, edge_score, nullptr,
+                                    grad_delta_state, reinterpret_cast<const float*>(grad_delta_val), batch, nodes, in_dim, out_dim, rank, 1,
+                                    width, compress_kind, projected_val_is_layer_val, reinterpret_cast<float*>(grad_layer_val),
+                                    grad_projected_state, reinterpret_cast<float*>(grad_projected_val), grad_target_weight,
+                                    grad_source_weight, grad_core_weight, grad_bias, workspace, workspace_bytes,
+                                    static_cast<hipStream_t>(stream), true);
+}
+
+int jn_transition_topk_forward_bf16(const float* sender_strength, const uint16_t* src_val, const uint16_t* dst_val,
+                                    const float* projected_state, const uint16_t* projected_val,
+                                    const float* source_weight, const float* target_weight, const float* core_weight,
+                                    const float* bias, float temperature, int64_t batch, int64_t src_nodes,
+                                    int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim,
+                                    int64_t rank, int64_t topk, int32_t compress_kind, float* delta_state,
+                                    uint16_t* delta_val, float* src_proj, float* dst_proj, int32_t* route_index,
+                                    float* route_logit, void* workspace, size_t workspace_bytes,
+                                    jn_stream_t stream) {
+  return transition_topk_forward_impl(sender_strength, reinterpret_cast<const float*>(src_val), reinterpret_cast<const float*>(dst_val), projected_state,
+                                      reinterpret_cast<const float*>(projected_val), source_weight, target_weight, core_weight, bias,
+                                      temperature, batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, 1,
+                                      topk, compress_kind, delta_state, reinterpret_cast<float*>(delta_val), src_proj, dst_proj,
+                                      route_index, route_logit, nullptr, workspace, workspace_bytes,
+                                      static_cast<hipStream_t>(stream), true);
+}
+
+int jn_transition_topk_backward_bf16(
+    const float* sender_strength, const uint16_t* src_val, const uint16_t* dst_val, const float* projected_state,
+    const uint16_t* projected_val, const float* source_weight, const float* target_weight, const float* core_weight,
+    const float* src_proj, const float* dst_proj, const int32_t* route_index, const float* route_logit,
+    const float* grad_delta_state, const uint16_t* grad_delta_val, float temperature, int64_t batch,
+    int64_t src_nodes, int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+    int64_t topk, int32_t compress_kind, float* grad_sender_strength, uint16_t* grad_src_val,
+    uint16_t* grad_dst_val, float* grad_projected_state, uint16_t* grad_projected_val, float* grad_source_weight,
+    float* grad_target_weight, float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
+    jn_stream_t stream) {
+  return transition_topk_backward_impl(
+      sender_strength, reinterpret_cast<const float*>(src_val), reinterpret_cast<const float*>(dst_val), projected_state, reinterpret_cast<const float*>(projected_val), source_weight,
+      target_weight, core_weight, src_proj, dst_proj, route_index, route_logit, nullptr, grad_delta_state,
+      reinterpret_cast<const float*>(grad_delta_val), temperature, batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, 1, topk,
+      compress_kind, grad_sender_strength, reinterpret_cast<float*>(grad_src_val), reinterpret_cast<float*>(grad_dst_val), grad_projected_state,
+      reinterpret_cast<float*>(grad_projected_val), grad_source_weight, grad_target_weight, grad_core_weight, grad_bias, workspace,
+      workspace_bytes, static_cast<hipStream_t>(stream), true);
 }
 
 int jn_propagation_dense_forward(const float* layer_val, const float* projected_state, const float* projected_val,

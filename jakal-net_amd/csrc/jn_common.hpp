@@ -306,6 +306,109 @@ __device__ __forceinline__ float4 buf_load_w(__amdgpu_buffer_rsrc_t r, uint32_t 
   else return make_float4(buf_load1(r, byte_off), 0.f, 0.f, 0.f);
 }
 
+// ---------------------------------------------------------------------------
+// Value-row packs: a lane moves W consecutive elements of a value row of
+// element type T, held as W floats.  fp32 rows: W = 4 (one 16-byte load) or 1;
+// bf16 rows: W = 8 (one 16-byte load) or 1.  bf16 widens exactly; a store
+// rounds to nearest even (v_cvt_pk_bf16_f32).
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16_t;
+
+template <int W>
+struct Pack {
+  float v[W];
+};
+
+__device__ __forceinline__ void unpack_bf16x2(uint32_t x, float& lo, float& hi) {
+  lo = __uint_as_float(x << 16);
+  hi = __uint_as_float(x & 0xffff0000u);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (bf16_t)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (bf16_t)hi) << 16);
+}
+
+template <typename T, int W>
+__device__ __forceinline__ Pack<W> unpack16(uint4 x) {
+  Pack<W> r;
+  if constexpr (sizeof(T) == 4) {
+    r.v[0] = __uint_as_float(x.x);
+    r.v[1] = __uint_as_float(x.y);
+    r.v[2] = __uint_as_float(x.z);
+    r.v[3] = __uint_as_float(x.w);
+  } else {
+    unpack_bf16x2(x.x, r.v[0], r.v[1]);
+    unpack_bf16x2(x.y, r.v[2], r.v[3]);
+    unpack_bf16x2(x.z, r.v[4], r.v[5]);
+    unpack_bf16x2(x.w, r.v[6], r.v[7]);
+  }
+  return r;
+}
+
+template <typename T, int W>
+__device__ __forceinline__ Pack<W> pack_zero() {
+  Pack<W> r;
+#pragma unroll
+  for (int i = 0; i < W; ++i) r.v[i] = 0.f;
+  return r;
+}
+
+template <typename T, int W>
+__device__ __forceinline__ Pack<W> load_pack(const T* p) {
+  static_assert(W == 1 || W * sizeof(T) == 16, "a pack is one element or 16 bytes");
+  if constexpr (W == 1) {
+    Pack<1> r;
+    r.v[0] = (float)p[0];
+    return r;
+  } else {
+    return unpack16<T, W>(*reinterpret_cast<const uint4*>(p));
+  }
+}
+
+template <typename T, int W>
+__device__ __forceinline__ void store_pack(T* p, const Pack<W>& x) {
+  if constexpr (W == 1) {
+    p[0] = (T)x.v[0];
+  } else if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(x.v[0], x.v[1], x.v[2], x.v[3]);
+  } else {
+    *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(x.v[0], x.v[1]), pack_bf16x2(x.v[2], x.v[3]),
+                                              pack_bf16x2(x.v[4], x.v[5]), pack_bf16x2(x.v[6], x.v[7]));
+  }
+}
+
+// W elements at a byte offset of a buffer (zeros when out of range).
+template <typename T, int W>
+__device__ __forceinline__ Pack<W> buf_load_pack(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  if constexpr (W == 1) {
+    Pack<1> x;
+    if constexpr (sizeof(T) == 4) x.v[0] = buf_load1(r, byte_off);
+    else x.v[0] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, byte_off, 0, 0) << 16);
+    return x;
+  } else {
+    return unpack16<T, W>(__builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0)));
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void fma_pack(Pack<W>& acc, float c, const Pack<W>& v) {
+#pragma unroll
+  for (int i = 0; i < W; ++i) acc.v[i] += c * v.v[i];
+}
+template <int W>
+__device__ __forceinline__ float dot_pack(const Pack<W>& a, const Pack<W>& b) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < W; ++i) s += a.v[i] * b.v[i];
+  return s;
+}
+template <int W>
+__device__ __forceinline__ Pack<W> add_pack(const Pack<W>& a, const Pack<W>& b) {
+  Pack<W> r;
+#pragma unroll
+  for (int i = 0; i < W; ++i) r.v[i] = a.v[i] + b.v[i];
+  return r;
+}
+
 __device__ __forceinline__ float sign_f(float s) { return (s > 0.f) ? 1.f : ((s < 0.f) ? -1.f : 0.f); }
 
 // True when every present edge of the wavefront's row (lanes with `present`)

@@ -61,8 +61,9 @@ __device__ __forceinline__ void row_coefficients(const int32_t* idx, const float
 
 // The D columns are processed in slabs of a.slab columns, slab-major over the
 // grid: while an XCD works on one slab of a batch element, the value rows it
-// gathers (N x slab floats) stay within its L2.  Slab 0 also sums the state.
-template <int W>
+// gathers (N x slab elements) stay within its L2.  Slab 0 also sums the state.
+// T: element type of the value rows and of delta_val (float or bf16).
+template <typename T, int W>
 __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
   const int lane = lane_id();
   const int64_t row_blocks = (a.rows + 3) / 4;
@@ -72,9 +73,9 @@ __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
   if (row >= a.rows) return;
   const int d_begin = slab * a.slab, d_end = min(a.D, d_begin + a.slab);
   const int64_t b = row / a.Nq;
-  const float* pvb = a.pv + b * a.Nk * a.ld_pv;
+  const T* pvb = reinterpret_cast<const T*>(a.pv) + b * a.Nk * a.ld_pv;
   const float* psb = a.ps + b * a.Nk;
-  float* out = a.out_val + row * a.D;
+  T* out = reinterpret_cast<T*>(a.out_val) + row * a.D;
 
   float rmax = 0.f, rinv = 0.f;
   if (a.compress == 1) row_abs_softmax_stats(a.idx, a.score, row, a.k, rmax, rinv);
@@ -88,31 +89,31 @@ __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
     const int ne = min(kWave, a.k - e0);
     for (int d = d_begin + lane * W; d < d_end; d += kWave * W) {
       // two accumulation chains (even / odd edges), summed at the end
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f), acc1 = acc;
+      Pack<W> acc = pack_zero<T, W>(), acc1 = acc;
       int q = 0;
       for (; q + 8 <= ne; q += 8) {
-        float4 v[8];
+        Pack<W> v[8];
         float cc[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int jj = readlane_i(j, q + u);
           cc[u] = jj < 0 ? 0.f : readlane_f(c, q + u);
-          v[u] = load_w<W>(pvb + (int64_t)(jj < 0 ? 0 : jj) * a.ld_pv + d);
+          v[u] = load_pack<T, W>(pvb + (int64_t)(jj < 0 ? 0 : jj) * a.ld_pv + d);
         }
 #pragma unroll
         for (int u = 0; u < 8; u += 2) {
-          fma4(acc, cc[u], v[u]);
-          fma4(acc1, cc[u + 1], v[u + 1]);
+          fma_pack(acc, cc[u], v[u]);
+          fma_pack(acc1, cc[u + 1], v[u + 1]);
         }
       }
       for (; q < ne; ++q) {
         const int jj = readlane_i(j, q);
         if (jj < 0) continue;
-        fma4((q & 1) ? acc1 : acc, readlane_f(c, q), load_w<W>(pvb + (int64_t)jj * a.ld_pv + d));
+        fma_pack((q & 1) ? acc1 : acc, readlane_f(c, q), load_pack<T, W>(pvb + (int64_t)jj * a.ld_pv + d));
       }
-      acc = add4(acc, acc1);
-      if (e0 > 0) acc = add4(acc, load_w<W>(out + d));
-      store_w<W>(out + d, acc);
+      acc = add_pack(acc, acc1);
+      if (e0 > 0) acc = add_pack(acc, load_pack<T, W>(out + d));
+      store_pack<T, W>(out + d, acc);
     }
   }
   if (slab == 0) {
@@ -124,19 +125,27 @@ __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
 int launch_rows_forward(const RowsFwdArgs& args, hipStream_t stream) {
   if (args.rows == 0) return kOk;
   RowsFwdArgs a = args;
-  const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
+  // one 16-byte pack per lane: 4 fp32 or 8 bf16 elements
+  const int eb = a.bf16 ? 2 : 4, pw = 16 / eb;
+  const bool vec = (a.D % pw == 0) && (a.ld_pv % pw == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.out_val) & 15) == 0);
-  // slabs of 256 columns (one float4 per lane) while a batch element's value
-  // rows exceed 2 MiB; a slab's rows then fit an XCD's 4 MiB L2
+  // slabs of 64 packs while a batch element's value rows exceed 2 MiB; a
+  // slab's rows then fit an XCD's 4 MiB L2
   a.slab = a.D;
   if (vec)
-    while (a.slab > 256 && a.slab % 512 == 0 && (int64_t)a.Nk * a.slab * 4 > (2LL << 20)) a.slab /= 2;
+    while (a.slab > 64 * pw && a.slab % (128 * pw) == 0 && (int64_t)a.Nk * a.slab * eb > (2LL << 20)) a.slab /= 2;
   const int64_t slabs = (a.D + a.slab - 1) / a.slab;
   const int64_t blocks = (a.rows + 3) / 4 * slabs;
   JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
   JN_PROFILE("rows_forward_kernel", stream);
-  if (vec) hipLaunchKernelGGL(rows_forward_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL(rows_forward_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  const dim3 grid((unsigned)blocks);
+  if (a.bf16) {
+    if (vec) hipLaunchKernelGGL((rows_forward_kernel<bf16_t, 8>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((rows_forward_kernel<bf16_t, 1>), grid, dim3(256), 0, stream, a);
+  } else {
+    if (vec) hipLaunchKernelGGL((rows_forward_kernel<float, 4>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((rows_forward_kernel<float, 1>), grid, dim3(256), 0, stream, a);
+  }
   JN_LAUNCH_CHECK();
   return kOk;
 }
@@ -162,9 +171,11 @@ int launch_rows_forward(const RowsFwdArgs& args, hipStream_t stream) {
 // columns: slab s of the grid writes into g_score (s = 0) or coef (s = 1).  The
 // grid is slab-major, so an XCD gathers value rows of one slab of one batch
 // element at a time (Nk x slab floats, sized to its L2).
-template <int NV, int KP>
+template <typename T, int NV, int KP>
 __global__ __launch_bounds__(256) void rows_backward_dots_kernel(RowsBwdArgs a, int slab) {
   constexpr int NI = KP / 4;
+  constexpr int W = 16 / (int)sizeof(T);  // elements per 16-byte pack
+  constexpr uint32_t EB = sizeof(T);
   const int lane = lane_id();
   const int g = lane >> 4, c = lane & 15;
   const int64_t row_blocks = (a.rows + 3) / 4;
@@ -175,15 +186,15 @@ __global__ __launch_bounds__(256) void rows_backward_dots_kernel(RowsBwdArgs a, 
   const int d_begin = s * slab, d_end = min(a.D, d_begin + slab);
   float* part = (s == 0) ? a.g_score : a.coef;
   const int64_t b = row / a.Nq;
-  const auto rs_pv = make_rsrc(a.pv + b * a.Nk * a.ld_pv, (uint32_t)(a.Nk * a.ld_pv * 4));
-  const auto rs_g = make_rsrc(a.gdv + row * a.D, (uint32_t)(a.D * 4));
+  const auto rs_pv = make_rsrc(reinterpret_cast<const T*>(a.pv) + b * a.Nk * a.ld_pv, (uint32_t)(a.Nk * a.ld_pv * EB));
+  const auto rs_g = make_rsrc(reinterpret_cast<const T*>(a.gdv) + row * a.D, (uint32_t)(a.D * EB));
   uint32_t loff[NV];  // byte offsets of this lane's columns; past the slab -> out of range (zeros)
-  float4 gv[NV];
+  Pack<W> gv[NV];
 #pragma unroll
   for (int t = 0; t < NV; ++t) {
-    const int off = d_begin + (16 * t + c) * 4;
-    loff[t] = off < d_end ? (uint32_t)off * 4u : kOobOffset;
-    gv[t] = buf_load4(rs_g, loff[t]);
+    const int off = d_begin + (16 * t + c) * W;
+    loff[t] = off < d_end ? (uint32_t)off * EB : kOobOffset;
+    gv[t] = buf_load_pack<T, W>(rs_g, loff[t]);
   }
   for (int e0 = 0; e0 < a.k; e0 += KP) {
     const int e = e0 + lane;
@@ -195,14 +206,14 @@ __global__ __launch_bounds__(256) void rows_backward_dots_kernel(RowsBwdArgs a, 
     float sel = 0.f;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ld_pv * 4u : kOobOffset;
-      float4 v[NV];
+      const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ld_pv * EB : kOobOffset;
+      Pack<W> v[NV];
 #pragma unroll
       for (int t = 0; t < NV; ++t)
-        v[t] = buf_load4(rs_pv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
+        v[t] = buf_load_pack<T, W>(rs_pv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
       float pdot = 0.f;
 #pragma unroll
-      for (int t = 0; t < NV; ++t) pdot += dot4(gv[t], v[t]);
+      for (int t = 0; t < NV; ++t) pdot += dot_pack(gv[t], v[t]);
       const float tot = row16_sum(pdot);
       sel = (c == i) ? tot : sel;
       if (((i + 1) * NV) % 16 == 0) __builtin_amdgcn_sched_barrier(0);
@@ -214,10 +225,11 @@ __global__ __launch_bounds__(256) void rows_backward_dots_kernel(RowsBwdArgs a, 
 
 // MH: multi-head scores (a.heads > 1): edge e's gradient reaches only the
 // ranks of its head a.ehead[e] in dq, and the bias partials are per head.
-template <int W, int NV, int KP, bool SPLIT, bool MH>
+template <typename T, int W, int NV, int KP, bool SPLIT, bool MH>
 __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
   constexpr int NI = KP / 4;      // iterations per block of KP edges
-  constexpr int P = 16 * W * NV;  // D floats per pass of a 16-lane group
+  constexpr int P = 16 * W * NV;  // D elements per pass of a 16-lane group
+  constexpr uint32_t EB = sizeof(T);
   const int lane = lane_id();
   const int g = lane >> 4, c = lane & 15;
   const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
@@ -267,33 +279,35 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
       // slab partials of this lane's edge, summed in slab order
       if (lane < ne) dot = a.g_score[row * a.k + e0 + lane] + a.coef[row * a.k + e0 + lane];
     } else {
-      const auto rs_pv = make_rsrc(a.pv + b * a.Nk * a.ld_pv, (uint32_t)(a.Nk * a.ld_pv * 4));
-      const auto rs_g = make_rsrc(a.gdv + row * a.D, (uint32_t)(a.D * 4));
+      const auto rs_pv =
+          make_rsrc(reinterpret_cast<const T*>(a.pv) + b * a.Nk * a.ld_pv, (uint32_t)(a.Nk * a.ld_pv * EB));
+      const auto rs_g = make_rsrc(reinterpret_cast<const T*>(a.gdv) + row * a.D, (uint32_t)(a.D * EB));
       float dots[NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) dots[i] = 0.f;
       for (int d0 = 0; d0 < a.D; d0 += P) {
         // byte offsets of this lane's slice of the pass; past D -> out of range (zeros)
         uint32_t loff[NV];
-        float4 gv[NV];
+        Pack<W> gv[NV];
 #pragma unroll
         for (int t = 0; t < NV; ++t) {
           const int off = d0 + (16 * t + c) * W;
-          loff[t] = off < a.D ? (uint32_t)off * 4u : kOobOffset;
-          gv[t] = buf_load_w<W>(rs_g, loff[t]);
+          loff[t] = off < a.D ? (uint32_t)off * EB : kOobOffset;
+          gv[t] = buf_load_pack<T, W>(rs_g, loff[t]);
         }
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
           // absent edges, iterations past the block's last edge and lanes past D
           // read out of range: zeros and no memory traffic, without a branch
-          const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ld_pv * 4u : kOobOffset;
-          float4 v[NV];
+          const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.ld_pv * EB : kOobOffset;
+          Pack<W> v[NV];
 #pragma unroll
           for (int t = 0; t < NV; ++t)
-            v[t] = buf_load_w<W>(rs_pv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
+            v[t] = buf_load_pack<T, W>(rs_pv,
+                                       (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
           float pdot = 0.f;
 #pragma unroll
-          for (int t = 0; t < NV; ++t) pdot += dot4(gv[t], v[t]);
+          for (int t = 0; t < NV; ++t) pdot += dot_pack(gv[t], v[t]);
           dots[i] += jg[i] >= 0 ? pdot : 0.f;
           // at most 16 row loads in flight per lane: keeps VGPRs (and occupancy) in check
           if (((i + 1) * NV) % 16 == 0) __builtin_amdgcn_sched_barrier(0);
@@ -402,27 +416,41 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
   }
 }
 
-template <int W, int NV, bool SPLIT = false, bool MH = false>
+template <typename T, int W, int NV, bool SPLIT = false, bool MH = false>
 static void launch_rows_bwd_kp(const RowsBwdArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 8, SPLIT, MH>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 16) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 16, SPLIT, MH>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 32) hipLaunchKernelGGL((rows_backward_kernel<W, NV, 32, SPLIT, MH>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((rows_backward_kernel<W, NV, 64, SPLIT, MH>), grid, dim3(256), 0, stream, a);
+  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_kernel<T, W, NV, 8, SPLIT, MH>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 16)
+    hipLaunchKernelGGL((rows_backward_kernel<T, W, NV, 16, SPLIT, MH>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 32)
+    hipLaunchKernelGGL((rows_backward_kernel<T, W, NV, 32, SPLIT, MH>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((rows_backward_kernel<T, W, NV, 64, SPLIT, MH>), grid, dim3(256), 0, stream, a);
 }
 
-template <int NV>
+// Value-row widths of the row backward: one 16-byte pack per lane and pass
+// slice, NV slices per 16-lane group (16 * W * NV elements per pass).
+template <typename T, bool MH>
+static void launch_rows_bwd_width(const RowsBwdArgs& a, bool vec, dim3 grid, hipStream_t stream) {
+  constexpr int W = 16 / (int)sizeof(T);  // passes of 512, 256, 128 (or 64) elements
+  if (!vec) launch_rows_bwd_kp<T, 1, 4, false, MH>(a, grid, stream);
+  else if (a.D > 256) launch_rows_bwd_kp<T, W, 512 / (16 * W), false, MH>(a, grid, stream);
+  else if (a.D > 128) launch_rows_bwd_kp<T, W, 256 / (16 * W), false, MH>(a, grid, stream);
+  else if (a.D > 64 || W == 8) launch_rows_bwd_kp<T, W, 128 / (16 * W), false, MH>(a, grid, stream);
+  else launch_rows_bwd_kp<T, W, 1, false, MH>(a, grid, stream);
+}
+
+template <typename T, int NV>
 static void launch_rows_bwd_dots(const RowsBwdArgs& a, dim3 grid, int slab, hipStream_t stream) {
-  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_dots_kernel<NV, 8>), grid, dim3(256), 0, stream, a, slab);
-  else if (a.k <= 16) hipLaunchKernelGGL((rows_backward_dots_kernel<NV, 16>), grid, dim3(256), 0, stream, a, slab);
-  else if (a.k <= 32) hipLaunchKernelGGL((rows_backward_dots_kernel<NV, 32>), grid, dim3(256), 0, stream, a, slab);
-  else hipLaunchKernelGGL((rows_backward_dots_kernel<NV, 64>), grid, dim3(256), 0, stream, a, slab);
+  if (a.k <= 8) hipLaunchKernelGGL((rows_backward_dots_kernel<T, NV, 8>), grid, dim3(256), 0, stream, a, slab);
+  else if (a.k <= 16) hipLaunchKernelGGL((rows_backward_dots_kernel<T, NV, 16>), grid, dim3(256), 0, stream, a, slab);
+  else if (a.k <= 32) hipLaunchKernelGGL((rows_backward_dots_kernel<T, NV, 32>), grid, dim3(256), 0, stream, a, slab);
+  else hipLaunchKernelGGL((rows_backward_dots_kernel<T, NV, 64>), grid, dim3(256), 0, stream, a, slab);
 }
 
 // Column slab of the split row backward (0: no split).  Two slabs of 256 or
 // 512 columns when a batch element's value rows exceed 2 MiB (an XCD's L2 is
 // 4 MiB) and 256 < D <= 1024.
-int rows_backward_slab(int64_t Nk, int D, bool vec) {
-  if (!vec || D <= 256 || D > 1024 || Nk * (int64_t)D * 4 <= (2LL << 20)) return 0;
+int rows_backward_slab(int64_t Nk, int D, bool vec, int elem_bytes) {
+  if (!vec || D <= 256 || D > 1024 || Nk * (int64_t)D * elem_bytes <= (2LL << 20)) return 0;
   return D <= 512 ? 256 : 512;
 }
 
@@ -435,40 +463,41 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
   JN_REQUIRE((int64_t)a.Nk * a.ld_pv * 4 < (1LL << 31) && (int64_t)a.Nk * a.ldk * 4 < (1LL << 31) &&
                  (int64_t)a.D * 4 < (1LL << 31),
              kUnsupported, "one batch element of the value or key rows must stay below 2 GiB");
-  const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
+  const int eb = a.bf16 ? 2 : 4, pw = 16 / eb;  // one 16-byte pack: 4 fp32 or 8 bf16 elements
+  const bool vec = (a.D % pw == 0) && (a.ld_pv % pw == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0);
   dim3 grid((unsigned)blocks);
   if (a.heads > 1) {
     JN_REQUIRE(a.ehead && a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r, kInvalidArgument,
                "multi-head row backward needs edge heads and %d..%d heads of equal rank", 2, kMaxHeads);
     JN_PROFILE("rows_backward_kernel", stream);
-    if (!vec) launch_rows_bwd_kp<1, 4, false, true>(a, grid, stream);
-    else if (a.D > 256) launch_rows_bwd_kp<4, 8, false, true>(a, grid, stream);
-    else if (a.D > 128) launch_rows_bwd_kp<4, 4, false, true>(a, grid, stream);
-    else if (a.D > 64) launch_rows_bwd_kp<4, 2, false, true>(a, grid, stream);
-    else launch_rows_bwd_kp<4, 1, false, true>(a, grid, stream);
+    if (a.bf16) launch_rows_bwd_width<bf16_t, true>(a, vec, grid, stream);
+    else launch_rows_bwd_width<float, true>(a, vec, grid, stream);
     JN_LAUNCH_CHECK();
     return kOk;
   }
-  const int slab = rows_backward_slab(a.Nk, a.D, vec);
+  const int slab = rows_backward_slab(a.Nk, a.D, vec, eb);
   if (slab) {
     {
       JN_PROFILE("rows_backward_dots_kernel", stream);
-      if (slab == 256) launch_rows_bwd_dots<4>(a, dim3((unsigned)(2 * blocks)), slab, stream);
-      else launch_rows_bwd_dots<8>(a, dim3((unsigned)(2 * blocks)), slab, stream);
+      const dim3 g2((unsigned)(2 * blocks));
+      if (a.bf16) {  // 8 bf16 per pack: 16 x 8 x NV columns per group pass
+        if (slab == 256) launch_rows_bwd_dots<bf16_t, 2>(a, g2, slab, stream);
+        else launch_rows_bwd_dots<bf16_t, 4>(a, g2, slab, stream);
+      } else {
+        if (slab == 256) launch_rows_bwd_dots<float, 4>(a, g2, slab, stream);
+        else launch_rows_bwd_dots<float, 8>(a, g2, slab, stream);
+      }
       JN_LAUNCH_CHECK();
     }
     JN_PROFILE("rows_backward_kernel", stream);
-    launch_rows_bwd_kp<4, 1, true>(a, grid, stream);
+    launch_rows_bwd_kp<float, 4, 1, true>(a, grid, stream);  // reads the dot partials, no value rows
     JN_LAUNCH_CHECK();
     return kOk;
   }
   JN_PROFILE("rows_backward_kernel", stream);
-  if (!vec) launch_rows_bwd_kp<1, 4>(a, grid, stream);
-  else if (a.D > 256) launch_rows_bwd_kp<4, 8>(a, grid, stream);
-  else if (a.D > 128) launch_rows_bwd_kp<4, 4>(a, grid, stream);
-  else if (a.D > 64) launch_rows_bwd_kp<4, 2>(a, grid, stream);
-  else launch_rows_bwd_kp<4, 1>(a, grid, stream);
+  if (a.bf16) launch_rows_bwd_width<bf16_t, false>(a, vec, grid, stream);
+  else launch_rows_bwd_width<float, false>(a, vec, grid, stream);
   JN_LAUNCH_CHECK();
   return kOk;
 }
@@ -634,7 +663,8 @@ int launch_csr(const CsrArgs& a, hipStream_t stream) {
 // rows_forward_kernel over the column's records.  The grid is slab-major, so an
 // XCD gathers rows of one slab of one batch element at a time (Nq x slab floats,
 // sized to its L2).  Slab 0 also sums the state.
-template <int W>
+// T: element type of the gathered rows (gdv) and of grad_pv.
+template <typename T, int W>
 __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int slab_cols) {
   const int lane = lane_id();
   const int64_t total_cols = (int64_t)a.B * a.Nk;
@@ -648,7 +678,8 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
   const int beg = seg[j], len = seg[j + 1] - beg;
   const float4* rec = a.rec + (int64_t)b * a.Nq * a.k + beg;
   const int d_begin = slab * slab_cols, d_end = min(a.D, d_begin + slab_cols);
-  float* out = a.grad_pv ? a.grad_pv + col * a.ld_gpv : nullptr;
+  const T* gdv = reinterpret_cast<const T*>(a.gdv);
+  T* out = a.grad_pv ? reinterpret_cast<T*>(a.grad_pv) + col * a.ld_gpv : nullptr;
 
   float st = 0.0f;
   const int nblk = max(1, (len + kWave - 1) / kWave);  // a column without edges still writes zeros
@@ -667,27 +698,27 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
     if (!out) continue;
     for (int d = d_begin + lane * W; d < d_end; d += kWave * W) {
       // two accumulation chains (even / odd records), summed at the end
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f), acc1 = acc;
+      Pack<W> acc = pack_zero<T, W>(), acc1 = acc;
       int q = 0;
       for (; q + 8 <= n; q += 8) {
-        float4 v[8];
+        Pack<W> v[8];
         float cc[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           cc[u] = readlane_f(cf, q + u);
-          v[u] = load_w<W>(a.gdv + (int64_t)readlane_i(row, q + u) * a.D + d);
+          v[u] = load_pack<T, W>(gdv + (int64_t)readlane_i(row, q + u) * a.D + d);
         }
 #pragma unroll
         for (int u = 0; u < 8; u += 2) {
-          fma4(acc, cc[u], v[u]);
-          fma4(acc1, cc[u + 1], v[u + 1]);
+          fma_pack(acc, cc[u], v[u]);
+          fma_pack(acc1, cc[u + 1], v[u + 1]);
         }
       }
       for (; q < n; ++q)
-        fma4((q & 1) ? acc1 : acc, readlane_f(cf, q), load_w<W>(a.gdv + (int64_t)readlane_i(row, q) * a.D + d));
-      acc = add4(acc, acc1);
-      if (blk > 0) acc = add4(acc, load_w<W>(out + d));
-      store_w<W>(out + d, acc);
+        fma_pack((q & 1) ? acc1 : acc, readlane_f(cf, q), load_pack<T, W>(gdv + (int64_t)readlane_i(row, q) * a.D + d));
+      acc = add_pack(acc, acc1);
+      if (blk > 0) acc = add_pack(acc, load_pack<T, W>(out + d));
+      store_pack<T, W>(out + d, acc);
     }
   }
   if (slab == 0 && a.grad_ps) {
@@ -807,18 +838,25 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   JN_REQUIRE(!a.q || (a.key && a.dk), kInvalidArgument, "key-side gradient needs key and dk");
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
   if (a.grad_pv || a.grad_ps) {
-    const bool vec = (a.D % 4 == 0) && (a.ld_gpv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
+    const int eb = a.bf16 ? 2 : 4, pw = 16 / eb;  // one 16-byte pack: 4 fp32 or 8 bf16 elements
+    const bool vec = (a.D % pw == 0) && (a.ld_gpv % pw == 0) && ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
                      (a.grad_pv == nullptr || (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0);
-    // slabs of 256 columns while a batch element's gathered rows exceed 2 MiB
+    // slabs of 64 packs while a batch element's gathered rows exceed 2 MiB
     int slab = a.D;
     if (vec)
-      while (slab > 256 && slab % 512 == 0 && (int64_t)a.Nq * slab * 4 > (2LL << 20)) slab /= 2;
+      while (slab > 64 * pw && slab % (128 * pw) == 0 && (int64_t)a.Nq * slab * eb > (2LL << 20)) slab /= 2;
     const int64_t slabs = a.grad_pv ? (a.D + slab - 1) / slab : 1;
     const int64_t blocks = (total_cols + 3) / 4 * slabs;
     JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
     JN_PROFILE(a.profile_name ? a.profile_name : "cols_gather_kernel", stream);
-    if (vec) hipLaunchKernelGGL(cols_gather_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, a, slab);
-    else hipLaunchKernelGGL(cols_gather_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, a, slab);
+    const dim3 grid((unsigned)blocks);
+    if (a.bf16) {
+      if (vec) hipLaunchKernelGGL((cols_gather_kernel<bf16_t, 8>), grid, dim3(256), 0, stream, a, slab);
+      else hipLaunchKernelGGL((cols_gather_kernel<bf16_t, 1>), grid, dim3(256), 0, stream, a, slab);
+    } else {
+      if (vec) hipLaunchKernelGGL((cols_gather_kernel<float, 4>), grid, dim3(256), 0, stream, a, slab);
+      else hipLaunchKernelGGL((cols_gather_kernel<float, 1>), grid, dim3(256), 0, stream, a, slab);
+    }
     JN_LAUNCH_CHECK();
   }
   if (a.q) {

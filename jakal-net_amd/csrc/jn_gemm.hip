@@ -8,6 +8,12 @@
 // stay separate buffers: the B-operand loader switches pointer at `b_split`
 // along N (NT) or K (NN), so no concatenated copy is needed.
 //
+// bf16 layers: the *_bf16 uses read X (the projection's A, the weight
+// gradient's B) as bf16 and write dX (and read its addend) as bf16.  Operands
+// are widened to fp32 on their way into LDS and multiplied on the fp32 MFMA:
+// a bf16 x fp32 product is exact in fp32, so the results are those of
+// bf16-in/fp32-accumulate arithmetic with half the bytes of X moved.
+//
 // Tiling: 256 threads = 4 waves in a 2x2 grid, workgroup tile 128x128 (64x64
 // for small extents), K staged through LDS in slices of 16 (double buffered,
 // register prefetch).  Each wave owns a 64x64 (32x32) block of
@@ -147,6 +153,11 @@ template <bool A_KC, bool B_KC, int USE, int TILE>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
   constexpr int LPT = TILE / 64;   // float4 loads per thread per operand and K slice
   constexpr int MT = TILE / 32;    // 16x16 tiles per wave along M (and N)
+  constexpr bool A_BF = USE == kGemmProjectBf16;     // A (k-contiguous) holds bf16
+  constexpr bool B_BF = USE == kGemmGradWeightBf16;  // B (k-major) holds bf16
+  constexpr bool C_BF = USE == kGemmGradInputBf16;   // C and the addend hold bf16
+  static_assert(!A_BF || A_KC, "bf16 A is k-contiguous");
+  static_assert(!B_BF || !B_KC, "bf16 B is k-major");
   __shared__ __align__(16) float sA[2][TILE * kGStride];
   __shared__ __align__(16) float sB[2][TILE * kGStride];
 
@@ -179,7 +190,18 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
     for (int u = 0; u < LPT; ++u) {
       const int e = tid + 256 * u;
       // ---- A ----
-      if (A_KC) {
+      if constexpr (A_BF) {
+        const int m = m0 + e / 4, kq = k0 + (e % 4) * 4;
+        const bf16_t* p = reinterpret_cast<const bf16_t*>(g.A) + bz * g.a_bs + (int64_t)m * g.lda + kq;
+        if (m < g.M && kq + 3 < kend && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+          const uint2 v = *reinterpret_cast<const uint2*>(p);
+          unpack_bf16x2(v.x, ra[u][0], ra[u][1]);
+          unpack_bf16x2(v.y, ra[u][2], ra[u][3]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ra[u][q] = (m < g.M && kq + q < kend) ? (float)p[q] : 0.0f;
+        }
+      } else if (A_KC) {
         const int m = m0 + e / 4, kq = k0 + (e % 4) * 4;
         const float* p = gA + (int64_t)m * g.lda + kq;
         if (m < g.M && kq + 3 < kend && aligned16(p)) {
@@ -220,6 +242,19 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q) rb[u][q] = (n < g.N && kq + q < kend) ? p[q] : 0.0f;
+        }
+      } else if constexpr (B_BF) {
+        const int kk = k0 + e / (TILE / 4), nq = n0 + (e % (TILE / 4)) * 4;
+        const bf16_t* base = reinterpret_cast<const bf16_t*>(kk < g.b_split ? g.B0 : g.B1) + bz * g.b_bs +
+                             (int64_t)(kk < g.b_split ? kk : kk - g.b_split) * g.ldb;
+        const bf16_t* p = base + nq;
+        if (kk < kend && nq + 3 < g.N && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+          const uint2 v = *reinterpret_cast<const uint2*>(p);
+          unpack_bf16x2(v.x, rb[u][0], rb[u][1]);
+          unpack_bf16x2(v.y, rb[u][2], rb[u][3]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) rb[u][q] = (kk < kend && nq + q < g.N) ? (float)p[q] : 0.0f;
         }
       } else {
         const int kk = k0 + e / (TILE / 4), nq = n0 + (e % (TILE / 4)) * 4;
@@ -329,8 +364,13 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
           float x = acc[mt][nt][v];
           if (g.c_nscale) x *= g.c_nscale[n];
           if (mscale) x *= mscale[m];
-          if (gadd) x += gadd[(int64_t)m * g.ld_add + n];
-          C[(int64_t)m * g.ldc + n] = x;
+          if constexpr (C_BF) {
+            if (g.addend) x += (float)reinterpret_cast<const bf16_t*>(g.addend)[(int64_t)m * g.ld_add + n];
+            reinterpret_cast<bf16_t*>(g.C)[(int64_t)m * g.ldc + n] = (bf16_t)x;
+          } else {
+            if (gadd) x += gadd[(int64_t)m * g.ld_add + n];
+            C[(int64_t)m * g.ldc + n] = x;
+          }
         }
       }
 }
@@ -357,8 +397,14 @@ constexpr GemmUseInfo kGemmUses[] = {
     {true, false, false, false, "gemm_f32_kernel<route_value_grad>"},
     {true, false, false, false, "gemm_f32_kernel<route_source_grad>"},
     {false, false, false, false, "gemm_f32_kernel<route_target_grad>"},
+    {true, true, false, true, "gemm_f32_kernel<project_bf16>"},
+    {true, false, false, true, "gemm_f32_kernel<grad_input_bf16>"},
+    {false, false, false, false, "gemm_f32_kernel<grad_weight_bf16>"},
 };
-static_assert(sizeof(kGemmUses) / sizeof(kGemmUses[0]) == kGemmRouteTargetGrad + 1, "one entry per GemmUse");
+static_assert(sizeof(kGemmUses) / sizeof(kGemmUses[0]) == kGemmGradWeightBf16 + 1, "one entry per GemmUse");
+constexpr bool gemm_use_bf16(GemmUse u) {
+  return u == kGemmProjectBf16 || u == kGemmGradInputBf16 || u == kGemmGradWeightBf16;
+}
 
 // ---- 128 x 128 path --------------------------------------------------------
 // Workgroup tile 128 x 128, K staged through LDS in slices of BK (double
@@ -691,13 +737,15 @@ static bool f4_aligned(const void* p) { return p == nullptr || (reinterpret_cast
 template <int USE>
 static void launch_use(const GemmArgs& g, bool fast, int zdim, hipStream_t stream) {
   constexpr GemmUseInfo u = kGemmUses[USE];
+  if constexpr (gemm_use_bf16((GemmUse)USE)) fast = false;  // the 128 x 128 kernel reads fp32 only
   if (fast) {
     const int tm = (g.M + kFT - 1) / kFT, tn = (g.N + kFT - 1) / kFT;
     const bool vec = g.N % 4 == 0 && g.ldc % 4 == 0 && g.c_bs % 4 == 0 && g.c_split_stride % 4 == 0 &&
                      f4_aligned(g.C) && f4_aligned(g.c_nscale) && f4_aligned(g.epi_ps) && f4_aligned(g.epi_E) &&
                      (g.addend == nullptr || (g.ld_add % 4 == 0 && g.add_bs % 4 == 0 && f4_aligned(g.addend)));
-    hipLaunchKernelGGL((gemm_f32_fast_kernel<u.a_kc, u.b_kc, USE, kFastBK>), dim3(tm * tn * zdim), dim3(256), 0,
-                       stream, g, tm, tn, vec ? 1 : 0);
+    if constexpr (!gemm_use_bf16((GemmUse)USE))
+      hipLaunchKernelGGL((gemm_f32_fast_kernel<u.a_kc, u.b_kc, USE, kFastBK>), dim3(tm * tn * zdim), dim3(256), 0,
+                         stream, g, tm, tn, vec ? 1 : 0);
   } else {
     dim3 grid((g.N + kGBM - 1) / kGBM, (g.M + kGBM - 1) / kGBM, zdim);
     hipLaunchKernelGGL((gemm_f32_kernel<u.a_kc, u.b_kc, USE, kGBM>), grid, dim3(256), 0, stream, g);
@@ -737,8 +785,9 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
   const int forced = g_gemm_tile.load(std::memory_order_relaxed);
   const bool big = forced ? forced == kFT : (g.M >= kFT && g.N >= kFT && tiles128 >= 256);
   // (the 128 x 128 kernel applies the k scale of a scaled use unconditionally)
+  // (bf16 operands run on the generic kernel)
   const bool fast = big && tiles128 < (1LL << 31) && fast_path_ok(g, info.a_kc, info.b_kc) &&
-                    (!info.a_kscale || g.a_kscale != nullptr);
+                    (!info.a_kscale || g.a_kscale != nullptr) && !gemm_use_bf16(use);
   JN_PROFILE(info.name, stream);
   switch (use) {
     case kGemmProject: launch_use<kGemmProject>(g, fast, (int)zdim, stream); break;
@@ -756,6 +805,9 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
     case kGemmRouteValueGrad: launch_use<kGemmRouteValueGrad>(g, fast, (int)zdim, stream); break;
     case kGemmRouteSourceGrad: launch_use<kGemmRouteSourceGrad>(g, fast, (int)zdim, stream); break;
     case kGemmRouteTargetGrad: launch_use<kGemmRouteTargetGrad>(g, fast, (int)zdim, stream); break;
+    case kGemmProjectBf16: launch_use<kGemmProjectBf16>(g, fast, (int)zdim, stream); break;
+    case kGemmGradInputBf16: launch_use<kGemmGradInputBf16>(g, fast, (int)zdim, stream); break;
+    case kGemmGradWeightBf16: launch_use<kGemmGradWeightBf16>(g, fast, (int)zdim, stream); break;
     default: JN_REQUIRE(false, kInvalidArgument, "unknown GEMM use %d", (int)use);
   }
   JN_LAUNCH_CHECK();
@@ -795,21 +847,23 @@ int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
 }
 
 // C[M][N] = X[M][K] . [W0;W1]^T with W0 rows [0, split) and W1 rows [split, N).
+// x_bf16: X holds bf16 elements.
 int gemm_project(const float* X, int64_t ldx, const float* W0, const float* W1, int split, int64_t ldw, float* C,
-                 int64_t ldc, int M, int N, int K, hipStream_t stream) {
+                 int64_t ldc, int M, int N, int K, hipStream_t stream, bool x_bf16) {
   GemmArgs g{};
   g.A = X; g.lda = ldx;
   g.B0 = W0; g.B1 = W1; g.ldb = ldw; g.b_split = split;
   g.C = C; g.ldc = ldc;
   g.M = M; g.N = N; g.K = K;
   g.k_chunk = K; g.c_split_stride = 0;
-  return launch_gemm(g, kGemmProject, 1, stream);
+  return launch_gemm(g, x_bf16 ? kGemmProjectBf16 : kGemmProject, 1, stream);
 }
 
 // dX[M][N] = dP[M][K] . [W0;W1] (+ addend), W0 rows [0, split) of K.
+// x_bf16: dX and the addend hold bf16 elements.
 int gemm_grad_input(const float* dP, int64_t ldp, const float* W0, const float* W1, int split, int64_t ldw,
                     const float* addend, int64_t ld_add, float* dX, int64_t ldx, int M, int N, int K,
-                    hipStream_t stream) {
+                    hipStream_t stream, bool x_bf16) {
   GemmArgs g{};
   g.A = dP; g.lda = ldp;
   g.B0 = W0; g.B1 = W1; g.ldb = ldw; g.b_split = split;
@@ -817,7 +871,7 @@ int gemm_grad_input(const float* dP, int64_t ldp, const float* W0, const float* 
   g.addend = addend; g.ld_add = ld_add;
   g.M = M; g.N = N; g.K = K;
   g.k_chunk = K; g.c_split_stride = 0;
-  return launch_gemm(g, kGemmGradInput, 1, stream);
+  return launch_gemm(g, x_bf16 ? kGemmGradInputBf16 : kGemmGradInput, 1, stream);
 }
 
 size_t gemm_grad_weight_workspace(int M, int N, int K) {
@@ -827,8 +881,9 @@ size_t gemm_grad_weight_workspace(int M, int N, int K) {
 
 // dW[M][N] = dP^T . X with dP [K][M] (row stride ldp), X [K][N] (row stride ldx).
 // Rows [0, m_split) of dW go to out0, the rest to out1.  Deterministic split-K.
+// x_bf16: X holds bf16 elements.
 int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, float* out0, float* out1, int m_split,
-                     int M, int N, int K, float* partial, hipStream_t stream) {
+                     int M, int N, int K, float* partial, hipStream_t stream, bool x_bf16) {
   int splits = K >= 4096 ? 64 : (K >= 512 ? 8 : 1);
   int k_chunk = (K + splits - 1) / splits;
   k_chunk = (k_chunk + kGBK - 1) / kGBK * kGBK;
@@ -838,7 +893,7 @@ int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, 
   g.C = partial; g.ldc = N;
   g.M = M; g.N = N; g.K = K;
   g.k_chunk = k_chunk; g.c_split_stride = (int64_t)M * N;
-  int rc = launch_gemm(g, kGemmGradWeight, splits, stream);
+  int rc = launch_gemm(g, x_bf16 ? kGemmGradWeightBf16 : kGemmGradWeight, splits, stream);
   if (rc != kOk) return rc;
   const int64_t total = (int64_t)M * N;
   JN_REQUIRE((total + 63) / 64 < (1LL << 31), kUnsupported, "weight gradient too large");

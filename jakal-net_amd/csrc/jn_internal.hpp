@@ -28,6 +28,9 @@ struct SelectArgs {
   // owning ranks [h * head_rank, (h + 1) * head_rank) of q, key and scale; bias
   // is [heads] or null.  A pair's score is max_h (dot_h + bias[h]) / T.
   int heads, head_rank;
+  // bf16 score operands (bf16 layers): bf16(q * scale) . bf16(key), accumulated
+  // in fp32 on bf16 MFMAs, whatever the select mode (one head only).
+  int bf16;
 };
 int launch_topk_select(const SelectArgs& a, hipStream_t stream);
 constexpr int kSelectMaxK = 64;
@@ -60,11 +63,12 @@ constexpr int kMaxHeads = 8;
 bool select_heads_fit(int64_t head_rank, int64_t heads);
 
 // ---- fp32 MFMA GEMMs (jn_gemm.hip) ----------------------------------------
+// x_bf16: the layer operand X (and dX with its addend) holds bf16 elements.
 int gemm_project(const float* X, int64_t ldx, const float* W0, const float* W1, int split, int64_t ldw, float* C,
-                 int64_t ldc, int M, int N, int K, hipStream_t stream);
+                 int64_t ldc, int M, int N, int K, hipStream_t stream, bool x_bf16 = false);
 int gemm_grad_input(const float* dP, int64_t ldp, const float* W0, const float* W1, int split, int64_t ldw,
                     const float* addend, int64_t ld_add, float* dX, int64_t ldx, int M, int N, int K,
-                    hipStream_t stream);
+                    hipStream_t stream, bool x_bf16 = false);
 size_t gemm_grad_weight_workspace(int M, int N, int K);
 // Batched fp32 GEMM C_b[M][N] = A_b . B_b (+ addend_b), b < batch.
 //   A(m, k) = a_kcontig ? A[m*lda + k] : A[k*lda + m], times a_kscale[k] if given
@@ -103,12 +107,13 @@ enum GemmUse {
   kGemmDenseSourceGrad,
   kGemmRouteLogits, kGemmRouteAggregate, kGemmRouteEdgeGrad, kGemmRouteValueGrad, kGemmRouteSourceGrad,
   kGemmRouteTargetGrad,
+  kGemmProjectBf16, kGemmGradInputBf16, kGemmGradWeightBf16,
 };
 int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream);
 // Workgroup tile of every later GEMM launch: 0 = chosen per call, 64 or 128 = forced.
 void set_gemm_tile(int tile);
 int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, float* out0, float* out1, int m_split,
-                     int M, int N, int K, float* partial, hipStream_t stream);
+                     int M, int N, int K, float* partial, hipStream_t stream, bool x_bf16 = false);
 
 // ---- edge-list kernels (jn_edges.hip) -------------------------------------
 struct RowsFwdArgs {
@@ -124,6 +129,7 @@ struct RowsFwdArgs {
   float* out_state;  // [rows]
   float* out_val;    // [rows, D]
   int slab;          // columns per slab (set by the launcher)
+  int bf16;          // pv and out_val hold bf16 elements (the pointers are reinterpreted)
 };
 int launch_rows_forward(const RowsFwdArgs& a, hipStream_t stream);
 
@@ -154,6 +160,7 @@ struct RowsBwdArgs {
   // and its bias partial column h.
   const uint8_t* ehead;   // [rows, k]
   int heads, head_rank;
+  int bf16;               // pv and gdv hold bf16 elements (the pointers are reinterpreted)
 };
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream);
 
@@ -209,6 +216,7 @@ struct RouteRowsBwdArgs {
   float* rowsum;         // [rows] ([rows, heads] with heads > 1)
   const uint8_t* ehead;  // multi-head: [rows, k] head of each edge (see RowsBwdArgs)
   int heads, head_rank;
+  int bf16;              // pv, gdv and grad_pv hold bf16 elements (the pointers are reinterpreted)
 };
 int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream);
 
@@ -278,6 +286,7 @@ struct ColsBwdArgs {
   const char* profile_name;  // label for the gather's kernel timer (null: "cols_gather_kernel")
   // Multi-head (heads > 1): a record's g_score reaches only its head's ranks of dk.
   int heads, head_rank;
+  int bf16;                  // gdv and grad_pv hold bf16 elements (the pointers are reinterpreted)
 };
 int cols_backward_parts(int64_t total_cols);
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream);

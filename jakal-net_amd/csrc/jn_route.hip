@@ -74,19 +74,21 @@ int launch_route_coef(const int32_t* idx, const float* logit, const float* rho, 
 // with 16-byte buffer loads.
 // MH: multi-head logits (a.heads > 1): edge e's gradient reaches only the ranks
 // of its head a.ehead[e] in dq, and the bias partials are per head.
-template <int W, int NV, int KP, bool MH>
+// T: element type of the value rows (pv, gdv) and of grad_pv.
+template <typename T, int W, int NV, int KP, bool MH>
 __global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdArgs a) {
   constexpr int NI = KP / 4;
   constexpr int P = 16 * W * NV;
+  constexpr uint32_t EB = sizeof(T);
   const int lane = lane_id();
   const int g = lane >> 4, c = lane & 15;
   const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
   if (row >= a.rows) return;
   const int64_t b = row / a.Ns;
   // 32-bit offsets into buffers of this batch element (sizes checked on the host)
-  const auto rs_gdv = make_rsrc(a.gdv + b * a.Nd * a.D, (uint32_t)(a.Nd * a.D * 4));
+  const auto rs_gdv = make_rsrc(reinterpret_cast<const T*>(a.gdv) + b * a.Nd * a.D, (uint32_t)(a.Nd * a.D * EB));
   const auto rs_key = make_rsrc(a.key + b * a.Nd * a.ldk, (uint32_t)(a.Nd * a.ldk * 4));
-  const auto rs_pv = make_rsrc(a.pv + row * a.ld_pv, (uint32_t)(a.D * 4));
+  const auto rs_pv = make_rsrc(reinterpret_cast<const T*>(a.pv) + row * a.ld_pv, (uint32_t)(a.D * EB));
   const float* gdsb = a.gds + b * a.Nd;
   const float ps_row = a.ps[row];
   const float rho = a.rho[row];
@@ -116,47 +118,44 @@ __global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdAr
   for (int i = 0; i < NI; ++i) dots[i] = 0.f;
   for (int d0 = 0; d0 < a.D; d0 += P) {
     uint32_t loff[NV];
-    float4 pvv[NV], acc[NV];
+    Pack<W> pvv[NV], acc[NV];
 #pragma unroll
     for (int t = 0; t < NV; ++t) {
       const int off = d0 + (16 * t + c) * W;
-      loff[t] = off < a.D ? (uint32_t)off * 4u : kOobOffset;
-      pvv[t] = buf_load_w<W>(rs_pv, loff[t]);
-      acc[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+      loff[t] = off < a.D ? (uint32_t)off * EB : kOobOffset;
+      pvv[t] = buf_load_pack<T, W>(rs_pv, loff[t]);
+      acc[t] = pack_zero<T, W>();
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       // absent edges and lanes past D read out of range: zeros, no traffic
-      const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.D * 4u : kOobOffset;
-      float4 v[NV];
+      const uint32_t roff = jg[i] >= 0 ? (uint32_t)jg[i] * (uint32_t)a.D * EB : kOobOffset;
+      Pack<W> v[NV];
 #pragma unroll
       for (int t = 0; t < NV; ++t)
-        v[t] = buf_load_w<W>(rs_gdv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
+        v[t] = buf_load_pack<T, W>(rs_gdv, (loff[t] == kOobOffset || roff == kOobOffset) ? kOobOffset : roff + loff[t]);
       float pdot = 0.f;
 #pragma unroll
       for (int t = 0; t < NV; ++t) {
-        pdot += dot4(pvv[t], v[t]);
-        fma4(acc[t], cg[i], v[t]);
+        pdot += dot_pack(pvv[t], v[t]);
+        fma_pack(acc[t], cg[i], v[t]);
       }
       dots[i] += pdot;
       if (((i + 1) * NV) % 16 == 0) __builtin_amdgcn_sched_barrier(0);
     }
     if (a.grad_pv) {
       // sum the four groups' partial rows; group g stores slices t = g, g + 4
-      float* out = a.grad_pv + row * a.ld_gpv;
+      T* out = reinterpret_cast<T*>(a.grad_pv) + row * a.ld_gpv;
 #pragma unroll
       for (int t = 0; t < NV; ++t) {
-        float4 x = acc[t];
-        x.x += xor16_f(x.x);
-        x.y += xor16_f(x.y);
-        x.z += xor16_f(x.z);
-        x.w += xor16_f(x.w);
-        x.x += xor32_f(x.x);
-        x.y += xor32_f(x.y);
-        x.z += xor32_f(x.z);
-        x.w += xor32_f(x.w);
+        Pack<W> x = acc[t];
+#pragma unroll
+        for (int u = 0; u < W; ++u) {
+          x.v[u] += xor16_f(x.v[u]);
+          x.v[u] += xor32_f(x.v[u]);
+        }
         const int off = d0 + (16 * t + c) * W;
-        if ((t & 3) == g && off < a.D) store_w<W>(out + off, x);
+        if ((t & 3) == g && off < a.D) store_pack<T, W>(out + off, x);
       }
     }
   }
@@ -260,21 +259,25 @@ __global__ __launch_bounds__(256) void route_rows_backward_kernel(RouteRowsBwdAr
   }
 }
 
-template <int W, int NV, bool MH>
+template <typename T, int W, int NV, bool MH>
 static void launch_route_bwd_kp(const RouteRowsBwdArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.k <= 8) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 8, MH>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 16) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 16, MH>), grid, dim3(256), 0, stream, a);
-  else if (a.k <= 32) hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 32, MH>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((route_rows_backward_kernel<W, NV, 64, MH>), grid, dim3(256), 0, stream, a);
+  if (a.k <= 8) hipLaunchKernelGGL((route_rows_backward_kernel<T, W, NV, 8, MH>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 16)
+    hipLaunchKernelGGL((route_rows_backward_kernel<T, W, NV, 16, MH>), grid, dim3(256), 0, stream, a);
+  else if (a.k <= 32)
+    hipLaunchKernelGGL((route_rows_backward_kernel<T, W, NV, 32, MH>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((route_rows_backward_kernel<T, W, NV, 64, MH>), grid, dim3(256), 0, stream, a);
 }
 
-template <bool MH>
+// One 16-byte pack per lane and pass slice (W elements), NV slices per 16-lane group.
+template <typename T, bool MH>
 static void launch_route_bwd(const RouteRowsBwdArgs& a, bool vec, dim3 grid, hipStream_t stream) {
-  if (!vec) launch_route_bwd_kp<1, 4, MH>(a, grid, stream);
-  else if (a.D > 256) launch_route_bwd_kp<4, 8, MH>(a, grid, stream);
-  else if (a.D > 128) launch_route_bwd_kp<4, 4, MH>(a, grid, stream);
-  else if (a.D > 64) launch_route_bwd_kp<4, 2, MH>(a, grid, stream);
-  else launch_route_bwd_kp<4, 1, MH>(a, grid, stream);
+  constexpr int W = 16 / (int)sizeof(T);  // passes of 512, 256, 128 (or 64) elements
+  if (!vec) launch_route_bwd_kp<T, 1, 4, MH>(a, grid, stream);
+  else if (a.D > 256) launch_route_bwd_kp<T, W, 512 / (16 * W), MH>(a, grid, stream);
+  else if (a.D > 128) launch_route_bwd_kp<T, W, 256 / (16 * W), MH>(a, grid, stream);
+  else if (a.D > 64 || W == 8) launch_route_bwd_kp<T, W, 128 / (16 * W), MH>(a, grid, stream);
+  else launch_route_bwd_kp<T, W, 1, MH>(a, grid, stream);
 }
 
 int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream) {
@@ -286,17 +289,23 @@ int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream) {
   JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
   JN_REQUIRE((int64_t)a.Nd * a.D * 4 < (1LL << 31) && (int64_t)a.Nd * a.ldk * 4 < (1LL << 31), kUnsupported,
              "one batch element of the destination rows must stay below 2 GiB");
-  const bool vec = (a.D % 4 == 0) && (a.ld_pv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
+  const int pw = a.bf16 ? 8 : 4;  // one 16-byte pack: 4 fp32 or 8 bf16 elements
+  const bool vec = (a.D % pw == 0) && (a.ld_pv % pw == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
                    (a.grad_pv == nullptr ||
-                    ((a.ld_gpv % 4 == 0) && (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0));
+                    ((a.ld_gpv % pw == 0) && (reinterpret_cast<uintptr_t>(a.grad_pv) & 15) == 0));
   dim3 grid((unsigned)blocks);
   const bool mh = a.heads > 1;
   JN_REQUIRE(!mh || (a.ehead && a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r),
              kInvalidArgument, "multi-head route backward needs edge heads and 2..%d heads of equal rank", kMaxHeads);
   JN_PROFILE("route_rows_backward_kernel", stream);
-  if (mh) launch_route_bwd<true>(a, vec, grid, stream);
-  else launch_route_bwd<false>(a, vec, grid, stream);
+  if (a.bf16) {
+    if (mh) launch_route_bwd<bf16_t, true>(a, vec, grid, stream);
+    else launch_route_bwd<bf16_t, false>(a, vec, grid, stream);
+  } else {
+    if (mh) launch_route_bwd<float, true>(a, vec, grid, stream);
+    else launch_route_bwd<float, false>(a, vec, grid, stream);
+  }
   JN_LAUNCH_CHECK();
   return kOk;
 }

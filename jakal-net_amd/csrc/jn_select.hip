@@ -52,7 +52,8 @@
 //     path, which keeps the lower key indices.  The kept set stays unsorted
 //     until one bitonic sort per row at the end.
 //   * Score arithmetic: fp16 MFMAs over two-term fp16 splits of the operands
-//     (see select_split_keys_kernel), or fp32 MFMAs (select mode 1).
+//     (see select_split_keys_kernel), or fp32 MFMAs (select mode 1), or, for
+//     bf16 layers, bf16 MFMAs over bf16 operands (select_bf16_keys_kernel).
 #include <atomic>
 #include <type_traits>
 
@@ -548,6 +549,29 @@ __global__ __launch_bounds__(256) void select_split_keys_kernel(const float* __r
 }
 
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// ---- bf16 score operands (bf16 layers) ---------------------------------------
+// Key rows rounded to bf16 (nearest even), [RP] each with ranks past r zero:
+// one plane of the split row layout.  The query is scaled by the core weight
+// and rounded to bf16 in registers, so a score is the fp32-accumulated dot
+// product of two bf16 vectors, (bf16(q * c) . bf16(key)), on
+// v_mfma_f32_16x16x32_bf16 -- one MFMA per K-step where the split path
+// issues three.
+__global__ __launch_bounds__(256) void select_bf16_keys_kernel(const float* __restrict__ key, int64_t ldk,
+                                                               int64_t kbs, int Nk, int r, int RP,
+                                                               bf16_t* __restrict__ out_rows) {
+  const int blk = blockIdx.x, b = blockIdx.y;
+  const int row0 = blk * kSplitRows;
+  const int rows = min(kSplitRows, Nk - row0);
+  const float* kb = key + (int64_t)b * kbs + (int64_t)row0 * ldk;
+  bf16_t* out = out_rows + ((int64_t)b * Nk + row0) * RP;
+  for (int e = threadIdx.x; e < rows * RP; e += 256) {
+    const int row = e / RP;
+    const int c = e - row * RP;
+    out[(int64_t)row * RP + c] = (bf16_t)(c < r ? kb[(int64_t)row * ldk + c] : 0.0f);
+  }
+}
 
 __device__ __forceinline__ halfx8 as_halfx8(float a, float b, float c, float d) {
   return __builtin_bit_cast(halfx8, floatx4{a, b, c, d});
@@ -574,7 +598,8 @@ __device__ __forceinline__ halfx8 as_halfx8(float a, float b, float c, float d) 
 // K-steps [h * head_ks, (h + 1) * head_ks) of the split rows; after a head's
 // last K-step its scores, unscaled and with its bias, are folded into a
 // running maximum, so the filter and merges see max_h (dot_h + bias[h]) / T.
-template <int RQ, bool VEC, int KEEP, int KS, int CW, bool MH = false>
+// BF (split layout, one plane): bf16 key rows and bf16 MFMAs (bf16 layers).
+template <int RQ, bool VEC, int KEEP, int KS, int CW, bool MH = false, bool BF = false>
 __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
                              CW == 8 ? 1 : CW == 4 ? 2 : ((KS > 0 ? KS > 2 : RQ > 16) ? 1 : 2)) void lowrank_topk_select_kernel(SelectArgs a) {
   constexpr bool COOP = CW > 0;
@@ -584,18 +609,20 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   constexpr int CAP = sel_lane_cap(KEEP);
   constexpr bool SPLIT = KS > 0;
   constexpr bool V4 = VEC && RQ % 4 == 0;
-  constexpr int FR = SPLIT ? 8 * KS : RQ;  // key fragment registers per tile
-  constexpr int RP = 32 * KS;              // split row: ranks per plane
+  constexpr int PLANES = BF ? 1 : 2;                  // split rows: fp16 hi + lo planes, or one bf16 plane
+  constexpr int FR = SPLIT ? 4 * PLANES * KS : RQ;    // key fragment registers per tile
+  constexpr int RP = 32 * KS;                         // split row: ranks per plane
   constexpr int ROWS = COOP ? CW * kSelRowsPerWave : KSP ? kSelRowsPerWave : kSelRows;  // query rows per workgroup
   constexpr int SLOTS = COOP ? CW * kSelRowsPerWave : kSelRows;  // row slots (16 per wave)
   static_assert(!KSP || KEEP == 48, "the key-split form serves k <= 16");
   static_assert(!COOP || (KS >= 1 && KS <= 2), "the cooperative select stages split keys of rank <= 64");
   static_assert(!MH || (SPLIT && CW == 0), "multi-head scores run on the per-wave split kernel");
-  // staged chunk: kSelChunk split rows of 2 RP halves plus 8 halves of padding,
-  // so the 16 rows one fragment read touches start 68 dwords apart (4 banks)
-  constexpr int KROW = 2 * RP + 8;
+  static_assert(!BF || (SPLIT && !MH), "bf16 operands use the split layout with one head");
+  // staged chunk: kSelChunk split rows of PLANES RP halves plus 8 halves of
+  // padding, so the 16 rows one fragment read touches start 4 banks apart
+  constexpr int KROW = PLANES * RP + 8;
   constexpr int KBUF = kSelChunk * KROW;
-  constexpr int F4 = kSelChunk * RP / 4;   // float4s per staged chunk
+  constexpr int F4 = kSelChunk * PLANES * RP / 8;  // float4s per staged chunk
   constexpr int PER = (F4 + NT - 1) / NT;  // of them per thread
 
   constexpr int KST = sel_kept_stride(KEEP), KIST = sel_kept_idx_stride(KEEP);
@@ -668,8 +695,14 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
     for (int s = 0; s < QN; ++s) qf[s] = (row_ok && qrank(s) >= 0) ? qf[s] * qs[s] : 0.0f;
   }
   halfx8 qh[SPLIT ? KS : 1], ql[SPLIT ? KS : 1];
-  int score_exp = 0;  // E (split path)
-  if constexpr (SPLIT) {
+  bf16x8 qbf[BF ? KS : 1];  // bf16 query fragment
+  int score_exp = 0;  // E (split path; 0 for bf16 operands)
+  if constexpr (BF) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qbf[s][e] = (bf16_t)qf[8 * s + e];
+  } else if constexpr (SPLIT) {
     float m = 0.0f;
 #pragma unroll
     for (int s = 0; s < QN; ++s) m = fmaxf(m, fabsf(qf[s]));
@@ -721,22 +754,34 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   // the end read as zeros with loop-invariant lane offsets.
   float kx[2][kSelTiles][FR];
   uint32_t kbase_off[kSelTiles];
-  // split rows: 4 RP bytes each; lane group g reads ranks [8g, 8g + 8) of every K-step
+  // split rows: 2 PLANES RP bytes each; lane group g reads ranks [8g, 8g + 8) of every K-step
 #pragma unroll
   for (int t = 0; t < kSelTiles; ++t)
-    kbase_off[t] = SPLIT ? (uint32_t)((16 * t + col) * 4 * RP + 16 * g) : (uint32_t)((16 * t + col) * ldk + g * RQ) * 4u;
+    kbase_off[t] = SPLIT ? (uint32_t)((16 * t + col) * 2 * PLANES * RP + 16 * g)
+                         : (uint32_t)((16 * t + col) * ldk + g * RQ) * 4u;
   const _Float16* split_b =
-      SPLIT ? reinterpret_cast<const _Float16*>(a.split_key) + (int64_t)b * a.Nk * 2 * RP : nullptr;
+      SPLIT ? reinterpret_cast<const _Float16*>(a.split_key) + (int64_t)b * a.Nk * PLANES * RP : nullptr;
   auto load_keys = [&](auto SET, int c) {
     constexpr int S = decltype(SET)::value;
     const int c0 = (chunk0 + c) * kSelChunk;
     const int rows = max(0, min(kSelChunk, key_end - c0));
     // uniform (readfirstlane keeps the resource in SGPRs)
-    const uint32_t nrec = __builtin_amdgcn_readfirstlane(SPLIT ? (uint32_t)(rows * 4 * RP) : (uint32_t)(rows * ldk) * 4u);
-    const auto rs = SPLIT ? make_rsrc(split_b + (int64_t)c0 * 2 * RP, nrec) : make_rsrc(kbase + (int64_t)c0 * ldk, nrec);
+    const uint32_t nrec = __builtin_amdgcn_readfirstlane(SPLIT ? (uint32_t)(rows * 2 * PLANES * RP)
+                                                                : (uint32_t)(rows * ldk) * 4u);
+    const auto rs =
+        SPLIT ? make_rsrc(split_b + (int64_t)c0 * PLANES * RP, nrec) : make_rsrc(kbase + (int64_t)c0 * ldk, nrec);
 #pragma unroll
     for (int t = 0; t < kSelTiles; ++t) {
-      if constexpr (SPLIT) {
+      if constexpr (BF) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const float4 h = buf_load4(rs, kbase_off[t] + 64u * s);
+          kx[S][t][4 * s + 0] = h.x;
+          kx[S][t][4 * s + 1] = h.y;
+          kx[S][t][4 * s + 2] = h.z;
+          kx[S][t][4 * s + 3] = h.w;
+        }
+      } else if constexpr (SPLIT) {
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
           const float4 h = buf_load4(rs, kbase_off[t] + 64u * s);
@@ -795,6 +840,13 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
           const float4 h = *reinterpret_cast<const float4*>(kb + 16 * t * KROW + 32 * s);
+          if constexpr (BF) {
+            kx[S][t][4 * s + 0] = h.x;
+            kx[S][t][4 * s + 1] = h.y;
+            kx[S][t][4 * s + 2] = h.z;
+            kx[S][t][4 * s + 3] = h.w;
+            continue;
+          }
           const float4 l = *reinterpret_cast<const float4*>(kb + 16 * t * KROW + 32 * s + RP);
           kx[S][t][8 * s + 0] = h.x;
           kx[S][t][8 * s + 1] = h.y;
@@ -810,7 +862,16 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
     floatx4 acc[kSelTiles];
 #pragma unroll
     for (int t = 0; t < kSelTiles; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (SPLIT) {
+    if constexpr (BF) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int t = 0; t < kSelTiles; ++t) {
+          const bf16x8 kv = __builtin_bit_cast(
+              bf16x8, floatx4{kx[S][t][4 * s], kx[S][t][4 * s + 1], kx[S][t][4 * s + 2], kx[S][t][4 * s + 3]});
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qbf[s], acc[t], 0, 0, 0);
+        }
+    } else if constexpr (SPLIT) {
       floatx4 best[MH ? kSelTiles : 1];
       if constexpr (MH) {
 #pragma unroll
@@ -940,8 +1001,8 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
     auto stage_load = [&](int c) {
       const int c0 = c * kSelChunk;
       const int rows = max(0, min(kSelChunk, a.Nk - c0));
-      const uint32_t nrec = __builtin_amdgcn_readfirstlane((uint32_t)(rows * 4 * RP));
-      const auto rs = make_rsrc(split_b + (int64_t)c0 * 2 * RP, nrec);
+      const uint32_t nrec = __builtin_amdgcn_readfirstlane((uint32_t)(rows * 2 * PLANES * RP));
+      const auto rs = make_rsrc(split_b + (int64_t)c0 * PLANES * RP, nrec);
 #pragma unroll
       for (int p = 0; p < PER; ++p) {
         const int f = (int)threadIdx.x + NT * p;
@@ -953,7 +1014,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
       for (int p = 0; p < PER; ++p) {
         const int f = (int)threadIdx.x + NT * p;
         if (f < F4) {
-          const int row = f / (RP / 4), part = f - row * (RP / 4);
+          const int row = f / (PLANES * RP / 8), part = f - row * (PLANES * RP / 8);
           *reinterpret_cast<float4*>(s_key + buf * KBUF + row * KROW + 8 * part) = pre[p];
         }
       }
@@ -1096,14 +1157,40 @@ static void launch_split_heads(const SelectArgs& a, dim3 grid, hipStream_t strea
     hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS, 0, true>), grid, dim3(256), 0, stream, a);
 }
 
-template <int KS, int CW>
+template <int KS, int CW, bool BF = false>
 static void launch_split(const SelectArgs& a, dim3 grid, hipStream_t stream) {
   const dim3 block(CW > 0 ? CW * kWave : 256);
   if constexpr (CW < 0) {
-    hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, CW>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, CW, false, BF>), grid, block, 0, stream, a);
   } else {
-    if (a.k <= 32) hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, CW>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS, CW>), grid, block, 0, stream, a);
+    if (a.k <= 32)
+      hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 48, KS, CW, false, BF>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((lowrank_topk_select_kernel<1, false, 80, KS, CW, false, BF>), grid, block, 0, stream, a);
+  }
+}
+
+// The split-layout kernels of one select: cooperative, key-split or per-wave.
+template <bool BF>
+static void launch_split_forms(const SelectArgs& a, int RP, bool coop4, bool ksp, dim3 grid, hipStream_t stream) {
+  if (coop4) {
+    if (RP == 32) launch_split<1, 4, BF>(a, grid, stream);
+    else launch_split<2, 4, BF>(a, grid, stream);
+  } else if (ksp) {
+    const dim3 kgrid((unsigned)((int64_t)((a.Nq + kSelRowsPerWave - 1) / kSelRowsPerWave) * a.B));
+    switch (RP / 32) {
+      case 1: launch_split<1, -1, BF>(a, kgrid, stream); break;
+      case 2: launch_split<2, -1, BF>(a, kgrid, stream); break;
+      case 3: launch_split<3, -1, BF>(a, kgrid, stream); break;
+      default: launch_split<4, -1, BF>(a, kgrid, stream); break;
+    }
+  } else {
+    switch (RP / 32) {
+      case 1: launch_split<1, 0, BF>(a, grid, stream); break;
+      case 2: launch_split<2, 0, BF>(a, grid, stream); break;
+      case 3: launch_split<3, 0, BF>(a, grid, stream); break;
+      default: launch_split<4, 0, BF>(a, grid, stream); break;
+    }
   }
 }
 
@@ -1174,11 +1261,14 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   JN_REQUIRE(blocks > 0 && blocks < (1LL << 31), kInvalidArgument, "bad grid size");
   dim3 grid((unsigned)blocks);
   const bool mh = a.heads > 1;
+  JN_REQUIRE(!(mh && a.bf16), kUnsupported, "bf16 score operands take one head");
   JN_REQUIRE(!mh || (select_heads_fit(a.head_rank, a.heads) && a.heads * a.head_rank == a.r), kUnsupported,
              "multi-head top-k select: %d heads of rank %d must fill 4 K-steps of 32 ranks at most (rank %d)",
              a.heads, a.head_rank, a.r);
-  // multi-head scores always run on the per-wave split kernel
-  const int mode = mh ? kSelectSplitF16Wave : select_mode();
+  // multi-head scores always run on the per-wave split kernel; bf16 operands
+  // take the split kernels' forms whatever the mode
+  int mode = mh ? kSelectSplitF16Wave : select_mode();
+  if (a.bf16 && mode == kSelectF32) mode = kSelectSplitF16;
 
   if (mode != kSelectF32) {
     const int head_rp = mh ? split_ranks(a.head_rank) : split_ranks(a.r);
@@ -1188,13 +1278,18 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
                "select workspace too small: need %zu bytes, got %zu", s.bytes, a.ws_bytes);
     const int nblk = (a.Nk + kSplitRows - 1) / kSplitRows;
     dim3 pgrid((unsigned)nblk, (unsigned)a.B);
-    {
-      JN_PROFILE("select_split_absmax_kernel", stream);
-      hipLaunchKernelGGL(select_split_absmax_kernel, pgrid, dim3(256), 0, stream, a.key, a.ldk, a.k_batch_stride,
-                         a.Nk, a.r, nblk, s.partial);
+    if (a.bf16) {
+      JN_PROFILE("select_bf16_keys_kernel", stream);
+      hipLaunchKernelGGL(select_bf16_keys_kernel, pgrid, dim3(256), 0, stream, a.key, a.ldk, a.k_batch_stride, a.Nk,
+                         a.r, RP, reinterpret_cast<bf16_t*>(s.split));
       JN_LAUNCH_CHECK();
-    }
-    {
+    } else {
+      {
+        JN_PROFILE("select_split_absmax_kernel", stream);
+        hipLaunchKernelGGL(select_split_absmax_kernel, pgrid, dim3(256), 0, stream, a.key, a.ldk, a.k_batch_stride,
+                           a.Nk, a.r, nblk, s.partial);
+        JN_LAUNCH_CHECK();
+      }
       JN_PROFILE("select_split_keys_kernel", stream);
       hipLaunchKernelGGL(select_split_keys_kernel, pgrid, dim3(256), 0, stream, a.key, a.ldk, a.k_batch_stride, a.Nk,
                          mh ? a.head_rank : a.r, head_rp, RP, nblk, s.partial,
@@ -1215,24 +1310,10 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
         case 3: launch_split_heads<3>(a, grid, stream); break;
         default: launch_split_heads<4>(a, grid, stream); break;
       }
-    } else if (coop4) {
-      if (RP == 32) launch_split<1, 4>(a, grid, stream);
-      else launch_split<2, 4>(a, grid, stream);
-    } else if (ksp) {
-      const dim3 kgrid((unsigned)((int64_t)((a.Nq + kSelRowsPerWave - 1) / kSelRowsPerWave) * a.B));
-      switch (RP / 32) {
-        case 1: launch_split<1, -1>(a, kgrid, stream); break;
-        case 2: launch_split<2, -1>(a, kgrid, stream); break;
-        case 3: launch_split<3, -1>(a, kgrid, stream); break;
-        default: launch_split<4, -1>(a, kgrid, stream); break;
-      }
+    } else if (a.bf16) {
+      launch_split_forms<true>(a, RP, coop4, ksp, grid, stream);
     } else {
-      switch (RP / 32) {
-        case 1: launch_split<1, 0>(a, grid, stream); break;
-        case 2: launch_split<2, 0>(a, grid, stream); break;
-        case 3: launch_split<3, 0>(a, grid, stream); break;
-        default: launch_split<4, 0>(a, grid, stream); break;
-      }
+      launch_split_forms<false>(a, RP, coop4, ksp, grid, stream);
     }
     JN_LAUNCH_CHECK();
     return kOk;

@@ -8,7 +8,10 @@ reference's own loader) dispatch to it unchanged.
 
 Each op flattens batch dimensions, casts to fp32 contiguous buffers and calls
 the C ABI of ``lib/libjakal_net_hip.so`` (declared in ``include/jakal_net_hip.h``)
-through ctypes on the current HIP stream.  Gradients come from
+through ctypes on the current HIP stream.  bf16 layers keep their value rows
+in bf16 on the edge-list ops (the *_bf16 entry points): the gathers move bf16
+rows, the top-k scores run on bf16 MFMAs, and the outputs and value gradients
+come back in bf16.  Gradients come from
 ``torch.autograd.Function`` wrappers whose backward calls the library's
 backward entry points.  Importing this module fails if the library cannot be
 loaded; nothing here computes on the CPU.
@@ -144,6 +147,11 @@ _declare(
     [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
      _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
+
+# bf16 layers: the fp32 entry points' argument lists with bf16 value tensors
+for _name in ("jn_propagation_topk_forward", "jn_propagation_topk_backward", "jn_propagation_window_forward",
+              "jn_propagation_window_backward", "jn_transition_topk_forward", "jn_transition_topk_backward"):
+    _declare(_name + "_bf16", list(getattr(_LIB, _name).argtypes))
 
 ABI_VERSION = int(_LIB.jn_abi_version())
 
@@ -281,6 +289,10 @@ _EDGE_OPS = {
                      "jn_propagation_topk_backward_multihead"),
     ("window", True): ("jn_propagation_window_forward_multihead", "jn_propagation_window_multihead_workspace_bytes",
                        "jn_propagation_window_backward_multihead"),
+    ("topk", "bf16"): ("jn_propagation_topk_forward_bf16", "jn_propagation_topk_workspace_bytes",
+                       "jn_propagation_topk_backward_bf16"),
+    ("window", "bf16"): ("jn_propagation_window_forward_bf16", "jn_propagation_window_workspace_bytes",
+                         "jn_propagation_window_backward_bf16"),
 }
 
 
@@ -296,10 +308,12 @@ class _PropagationEdges(torch.autograd.Function):
     fp32, contiguous): layer_val X [B,N,Din], projected_state [B,N],
     projected_val [B,N,Dout] or None when it is X itself, V and U [r,Din],
     w_hat [r], bias [] or None.  With heads > 1 the r ranks are `heads`
-    equal head slices (max-aggregated scores) and bias is [heads]."""
+    equal head slices (max-aggregated scores) and bias is [heads].  With
+    bf16, X and pv are bf16 (one head) and delta_val comes back in bf16."""
 
     @staticmethod
-    def forward(ctx, X, ps, pv, V, U, w_hat, bias, mode: str, param: int, compress: int, heads: int = 1):  # noqa: N803
+    def forward(ctx, X, ps, pv, V, U, w_hat, bias, mode: str, param: int, compress: int, heads: int = 1,  # noqa: N803
+                bf16: bool = False):
         B, N, Din = X.shape
         pv_is_x = pv is None
         pv_t = X if pv_is_x else pv
@@ -309,10 +323,11 @@ class _PropagationEdges(torch.autograd.Function):
         rank_arg = [r // heads, heads] if mh else [r]
         k = _edges_per_row(mode, param, N)
         dev = X.device
-        fwd = getattr(_LIB, _EDGE_OPS[mode, mh][0])
+        variant = "bf16" if bf16 else mh
+        fwd = getattr(_LIB, _EDGE_OPS[mode, variant][0])
         with torch.cuda.device(dev):
             ds = torch.empty(B, N, device=dev, dtype=torch.float32)
-            dv = torch.empty(B, N, Dout, device=dev, dtype=torch.float32)
+            dv = torch.empty(B, N, Dout, device=dev, dtype=torch.bfloat16 if bf16 else torch.float32)
             proj = torch.empty(B * N, 2 * r, device=dev, dtype=torch.float32)
             idx = torch.empty(B, N, k, device=dev, dtype=torch.int32)
             score = torch.empty(B, N, k, device=dev, dtype=torch.float32)
@@ -331,16 +346,16 @@ class _PropagationEdges(torch.autograd.Function):
                 args += [_ptr(ws), ws_bytes]
             _check(fwd(*args, _stream(dev)))
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, idx, score, head)
-        ctx.meta = (mode, param, compress, pv_is_x, bias is not None, heads)
+        ctx.meta = (mode, param, compress, pv_is_x, bias is not None, heads, bf16)
         ctx.mark_non_differentiable(idx, score)
         return ds, dv, idx, score
 
     @staticmethod
     def backward(ctx, g_ds, g_dv, _g_idx=None, _g_score=None):
         X, ps, pv, V, U, w_hat, proj, idx, score, head = ctx.saved_tensors
-        mode, param, compress, pv_is_x, has_bias, heads = ctx.meta
+        mode, param, compress, pv_is_x, has_bias, heads, bf16 = ctx.meta
         mh = heads > 1
-        _, ws_name, bwd_name = _EDGE_OPS[mode, mh]
+        _, ws_name, bwd_name = _EDGE_OPS[mode, "bf16" if bf16 else mh]
         B, N, Din = X.shape
         Dout = pv.shape[-1]
         r = U.shape[0]
@@ -348,8 +363,9 @@ class _PropagationEdges(torch.autograd.Function):
         dev = X.device
         need = ctx.needs_input_grad
         with torch.cuda.device(dev):
+            vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
-            g_dv = torch.zeros(B, N, Dout, device=dev) if g_dv is None else g_dv.float().contiguous()
+            g_dv = torch.zeros(B, N, Dout, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
             gX = torch.empty_like(X) if need[0] else None
             gps = torch.empty_like(ps) if need[1] else None
             gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
@@ -381,7 +397,17 @@ class _PropagationEdges(torch.autograd.Function):
             None,
             None,
             None,
+            None,
         )
+
+
+def _bf16_rows(*tensors: Tensor | None) -> bool:
+    """True when every given tensor (None: skipped) is bf16: the bf16 entry points apply."""
+    return all(t is None or t.dtype == torch.bfloat16 for t in tensors)
+
+
+def _bf16(t: Tensor | None) -> Tensor | None:
+    return None if t is None else t.contiguous()
 
 
 class _PropagationDense(torch.autograd.Function):
@@ -580,12 +606,15 @@ def _propagation_edges(mode, pairwise_kind, weight, bias, in_weight, in_bias, ou
     N, Din = layer_val.shape[-2], layer_val.shape[-1]
     Dout = projected_val.shape[-1]
     pv_is_x = _same_storage_view(projected_val, layer_val)
-    X = _f32(layer_val.reshape(-1, N, Din))
+    # bf16 layers keep bf16 value rows (one head); anything else computes in fp32
+    bf16 = heads == 1 and _bf16_rows(layer_val, projected_val)
+    rows = _bf16 if bf16 else _f32
+    X = rows(layer_val.reshape(-1, N, Din))
     ps = _f32(projected_state.reshape(-1, N))
-    pv = None if pv_is_x else _f32(projected_val.reshape(-1, N, Dout))
+    pv = None if pv_is_x else rows(projected_val.reshape(-1, N, Dout))
     ds, dv, idx, score = _PropagationEdges.apply(
         X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias), mode, int(param), _COMPRESS_KINDS[edge_compress_name],
-        heads,
+        heads, bf16,
     )
     k = idx.shape[-1]
     return (
@@ -743,7 +772,7 @@ class _TransitionTopK(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, rho, src, dst, ps, pv, Ws, Wt, w, bias, temperature: float, topk: int, compress: int,  # noqa: N803
-                heads: int = 1):
+                heads: int = 1, bf16: bool = False):
         B, Ns, Dsrc = src.shape
         Nd, Ddst = dst.shape[1], dst.shape[2]
         Dv = pv.shape[-1]
@@ -754,7 +783,7 @@ class _TransitionTopK(torch.autograd.Function):
         dev = src.device
         with torch.cuda.device(dev):
             ds = torch.empty(B, Nd, device=dev, dtype=torch.float32)
-            dv = torch.empty(B, Nd, Dv, device=dev, dtype=torch.float32)
+            dv = torch.empty(B, Nd, Dv, device=dev, dtype=torch.bfloat16 if bf16 else torch.float32)
             sp = torch.empty(B * Ns, r, device=dev, dtype=torch.float32)
             dp = torch.empty(B * Nd, r, device=dev, dtype=torch.float32)
             idx = torch.empty(B, Ns, k, device=dev, dtype=torch.int32)
@@ -763,7 +792,8 @@ class _TransitionTopK(torch.autograd.Function):
             ws_fn = _LIB.jn_transition_topk_multihead_workspace_bytes if mh else _LIB.jn_transition_topk_workspace_bytes
             ws_bytes = int(ws_fn(B, Ns, Nd, Dsrc, Ddst, Dv, *rank_arg, topk))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
-            fwd = _LIB.jn_transition_topk_forward_multihead if mh else _LIB.jn_transition_topk_forward
+            fwd = (_LIB.jn_transition_topk_forward_multihead if mh else
+                   _LIB.jn_transition_topk_forward_bf16 if bf16 else _LIB.jn_transition_topk_forward)
             _check(
                 fwd(
                     _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w), _ptr(bias),
@@ -773,14 +803,14 @@ class _TransitionTopK(torch.autograd.Function):
                 )
             )
         ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, idx, logit, head)
-        ctx.meta = (float(temperature), int(topk), compress, bias is not None, heads)
+        ctx.meta = (float(temperature), int(topk), compress, bias is not None, heads, bf16)
         ctx.mark_non_differentiable(idx, logit)
         return ds, dv, idx, logit
 
     @staticmethod
     def backward(ctx, g_ds, g_dv, _g_idx=None, _g_logit=None):
         rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, idx, logit, head = ctx.saved_tensors
-        temperature, topk, compress, has_bias, heads = ctx.meta
+        temperature, topk, compress, has_bias, heads, bf16 = ctx.meta
         B, Ns, Dsrc = src.shape
         Nd, Ddst = dst.shape[1], dst.shape[2]
         Dv = pv.shape[-1]
@@ -790,8 +820,9 @@ class _TransitionTopK(torch.autograd.Function):
         dev = src.device
         need = ctx.needs_input_grad
         with torch.cuda.device(dev):
+            vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, Nd, device=dev) if g_ds is None else g_ds.float().contiguous()
-            g_dv = torch.zeros(B, Nd, Dv, device=dev) if g_dv is None else g_dv.float().contiguous()
+            g_dv = torch.zeros(B, Nd, Dv, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
             out = [torch.empty_like(t) if n else None for t, n in zip((rho, src, dst, ps, pv), need[:5])]
             gWs = torch.empty_like(Ws) if need[5] else None
             gWt = torch.empty_like(Wt) if need[6] else None
@@ -800,7 +831,8 @@ class _TransitionTopK(torch.autograd.Function):
             ws_fn = _LIB.jn_transition_topk_multihead_workspace_bytes if mh else _LIB.jn_transition_topk_workspace_bytes
             ws_bytes = int(ws_fn(B, Ns, Nd, Dsrc, Ddst, Dv, *rank_arg, topk))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
-            bwd = _LIB.jn_transition_topk_backward_multihead if mh else _LIB.jn_transition_topk_backward
+            bwd = (_LIB.jn_transition_topk_backward_multihead if mh else
+                   _LIB.jn_transition_topk_backward_bf16 if bf16 else _LIB.jn_transition_topk_backward)
             _check(
                 bwd(
                     _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w),
@@ -811,7 +843,7 @@ class _TransitionTopK(torch.autograd.Function):
                 )
             )
         return (*out, gWs, gWt, gw if need[7] else None, gb if (has_bias and need[8]) else None, None, None, None,
-                None)
+                None, None)
 
 
 def transition_pairwise_topk_routes(
@@ -875,11 +907,14 @@ def transition_pairwise_topk_routes(
     elif Nd > MAX_ROUTE_TOPK:
         raise NotImplementedError("HIP sparse transition over every destination supports up to 64 destinations "
                                   "(transition_pairwise_topk runs more as the dense transition).")
+    # bf16 layers keep bf16 value rows (one head); anything else computes in fp32
+    bf16 = heads == 1 and _bf16_rows(src_val, dst_val, projected_val)
+    rows = _bf16 if bf16 else _f32
     ds, dv, idx, logit = _TransitionTopK.apply(
-        _f32(sender_strength.reshape(-1, Ns)), _f32(src_val.reshape(-1, Ns, Dsrc)),
-        _f32(dst_val.reshape(-1, Nd, Ddst)), _f32(projected_state.reshape(-1, Ns)),
-        _f32(projected_val.reshape(-1, Ns, Dv)), _f32(source_weight), _f32(target_weight), _f32(core_weight),
-        _f32(bias), float(temperature), k, _ROUTE_COMPRESS_KINDS[route_compress_name], heads,
+        _f32(sender_strength.reshape(-1, Ns)), rows(src_val.reshape(-1, Ns, Dsrc)),
+        rows(dst_val.reshape(-1, Nd, Ddst)), _f32(projected_state.reshape(-1, Ns)),
+        rows(projected_val.reshape(-1, Ns, Dv)), _f32(source_weight), _f32(target_weight), _f32(core_weight),
+        _f32(bias), float(temperature), k, _ROUTE_COMPRESS_KINDS[route_compress_name], heads, bf16,
     )
     return (
         ds.reshape(*batch_shape, Nd).to(projected_state.dtype),

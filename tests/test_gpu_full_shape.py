@@ -11,8 +11,8 @@ evaluation of the same op on the same selection (tests/parity.py):
   gradients of the layer values and states on every batch element, the
   gradients of U, V, w_hat and b over all 2,097,152 edges;
 * C4 dense (same inputs, every pair): the same tensors;
-* C3 (B=8, D=512, r=64, top-16 per source, both directions) with bf16
-  layers, at the bf16 tolerance rtol 2e-2.
+* C3 (B=8, D=512, r=64, top-16 per source, both directions) and C4 top-k
+  with bf16 layers, at the bf16 tolerance rtol 2e-2.
 
 Reference semantics: src/jakal_net/propagation.py:207-220, 453-480;
 src/jakal_net/transition.py:431-452.
@@ -23,7 +23,8 @@ import pytest
 import torch
 
 import jakal_oracle as O
-from parity import check, check_bf16, check_selection, np64, torch32_propagation
+from parity import (bf16_select_scores, check, check_bf16_calibrated, check_selection, np64, torch32_propagation,
+                    torch32_transition)
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 
@@ -170,17 +171,57 @@ def test_c3_bf16_transition_full_shape(dev, Ns, Nd):
     torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
     assert srcd.grad.dtype == torch.bfloat16
 
-    logits = O.lowrank_route_logits(np64(src), np64(dst), np64(Ws), np64(Wt), np64(w), bias)
-    frac = check_selection(idx.cpu().numpy(), logit.cpu().numpy(), logits, k)
+    # the select ranks bf16(P_s * w) . bf16(P_t) + b on bf16 MFMAs
+    logits, tol = bf16_select_scores(np64(src) @ np64(Ws).T, np64(dst) @ np64(Wt).T, np64(w), bias)
+    frac = check_selection(idx.cpu().numpy(), logit.cpu().numpy(), logits, k, gap=2 * tol, score_tol=tol)
     print(f"C3 bf16 {Ns}->{Nd}: rows with an unambiguous set {frac:.4f}", flush=True)
-    assert frac > 0.5
+    # bf16 operand rounding widens the ambiguity band: fewer rows are checked
+    # exactly (every one that is unambiguous), the rest within the band
+    assert frac > 0.3
     mask = O.mask_from_indices(idx.cpu().numpy(), Nd)
     rho_np = np64(rho)
     gr = O.transition_backward(np64(src), np64(dst), rho_np, np64(state), np64(src), np64(Ws), np64(Wt), np64(w),
                                bias, np64(gds), np64(gdv), topk=k, mask=mask)
-    check_bf16("delta_state", ds, gr["delta_state"])
-    check_bf16("delta_val", dv, gr["delta_val"])
-    check_bf16("grad src_val", srcd.grad, gr["src_val"] + gr["pv"], terms=(gr["src_val"], gr["pv"]))
-    check_bf16("grad dst_val", dstd.grad, gr["dst_val"])
+    t = torch32_transition(dev, src, dst, rho.detach().float().cpu(), state, src, Ws, Wt, w, bias, 1.0, mask,
+                           "softmax", gds, gdv, bf16_operands=True)
+    check_bf16_calibrated("delta_state", ds, gr["delta_state"], t["delta_state"])
+    check_bf16_calibrated("delta_val", dv, gr["delta_val"], t["delta_val"])
+    check_bf16_calibrated("grad src_val", srcd.grad, gr["src_val"] + gr["pv"], t["src_val"] + t["pv"])
+    check_bf16_calibrated("grad dst_val", dstd.grad, gr["dst_val"], t["dst_val"])
     sig = 1.0 / (1.0 + np.exp(-np64(state)))
-    check_bf16("grad state", psd.grad, gr["ps"] + gr["sender"] * sig, terms=(gr["ps"], gr["sender"] * sig))
+    check_bf16_calibrated("grad state", psd.grad, gr["ps"] + gr["sender"] * sig, t["ps"] + t["sender"] * sig)
+
+
+def test_c4_topk_bf16_forward_backward_full_shape(dev):
+    """BASELINE C4-topk bf16 row: the C4 inputs with bf16 layer states and
+    values (the c4-topk-bf16 bench workload).  The selection on every row
+    against the scores the bf16 select ranks; outputs and node gradients on
+    every batch element and the parameter gradients (sums over 2,097,152
+    edges) at rtol 2e-2 elementwise, or within twice the error of an fp32
+    torch evaluation with the same bf16 score operands (tests/parity.py,
+    check_bf16_calibrated)."""
+    state, val, U, V, w_hat, b, gds, gdv = _c4_inputs()
+    state, val = state.bfloat16(), val.bfloat16()
+    gds, gdv = gds.bfloat16(), gdv.bfloat16()
+    B, N, D = val.shape
+    k = 32
+    print("C4 top-k bf16: HIP forward + backward", flush=True)
+    got, idx, score = _run_hip(dev, "topk", state, val, U, V, w_hat, b, gds, gdv, k=k)
+    idx_np, score_np = idx.cpu().numpy(), score.cpu().numpy()
+    vn, Un, Vn, wn = np64(val), np64(U), np64(V), np64(w_hat)
+    fracs = []
+    for bb in range(B):
+        s, tol = bf16_select_scores(vn[bb:bb + 1] @ Un.T, vn[bb:bb + 1] @ Vn.T, wn, b)
+        fracs.append(check_selection(idx_np[bb:bb + 1], score_np[bb:bb + 1], s, k, gap=2 * tol, score_tol=tol))
+    print(f"C4 top-k bf16 selection: rows with an unambiguous set {np.mean(fracs):.4f}", flush=True)
+    # 4096 keys of small unit-norm scores crowd the 32nd / 33rd place: about a
+    # fifth of the rows (some 12,000) stay outside the bf16 ambiguity band and
+    # are checked exactly, the rest within it
+    assert np.mean(fracs) > 0.1
+    want = _oracle_by_batch(vn, np64(state), Un, Vn, wn, b, np64(gds), np64(gdv), "topk",
+                            masks=lambda bb: O.mask_from_indices(idx_np[bb:bb + 1], N))
+    ref = torch32_propagation(dev, val, state, None, U, V, w_hat, b, O.mask_from_indices(idx_np, N), "softsign",
+                              gds, gdv, bf16_operands=True)
+    for name in ("delta_state", "delta_val", "val", "ps", "U", "V", "w_hat", "b"):
+        check_bf16_calibrated(f"C4 bf16 {name}", got[name], want[name], ref[name],
+                              stored_bf16=name in ("delta_state", "delta_val", "val", "ps"))

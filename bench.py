@@ -17,13 +17,26 @@ Other workloads (--workload), one per hot-path row, same output format:
   c4-topk-bf16 BASELINE config 4 (C4-topk bf16 row): c4-topk with bf16 layer
               states and values; the value rows move as bf16 and the top-k
               scores run on bf16 MFMAs (sparse-byte budget 6.72 GB).
+  c4-dense-causal c4-dense with a full causal window (the masked half skipped).
+  c3-transition-dense C3 sizes with every source routed to every destination.
+  c5-progressive-b BASELINE config 5: the Progressive-B query-block training
+              step (forward, backward, AdamW; tokens/s).
 
 Inputs and parameters are resident in HBM before the timed region.
+
+Timing.  The step is first run `steps` times eagerly with the library's
+per-kernel HIP events on the launch stream (the kernel table and roofline).
+Then, for the operator workloads, it is captured once into a HIP graph
+(torch.cuda.CUDAGraph; the library only launches kernels, so the whole
+forward+backward captures) and `steps` back-to-back replays are timed:
+`value` and `ms_per_step` come from the replays, the eager figures are
+reported under `graph`.  --eager times the eager steps only; C5 (an optimizer
+step) always runs eager.
 
 Prints one JSON line:
   value        routed pairs per second (edges aggregated per step / step time)
   roofline     dominant kernel: algorithmic bytes (or flops) per launch / its
-               average duration, measured with HIP events inside the timed
+               average duration, measured with HIP events over the eager timed
                region; `traffic` = HBM-side bytes per launch measured by
                rocprofv3 FETCH_SIZE/WRITE_SIZE passes of this command
   kernels      the same figures for every kernel of the step
@@ -37,7 +50,7 @@ hi.lo + lo.hi of two-term fp16 operand splits, fp32 accumulation); that
 kernel entry also reports the executed fp16 MFMA rate against its own peak.
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload c4-topk] [--no-cpu-baseline]
-                  [--select-mode split-f16|f32] [--gemm-tile 0|64|128]
+                  [--select-mode split-f16|f32] [--gemm-tile 0|64|128] [--eager]
   python bench.py --calibrate-copy     # plain 1 GiB device copy (counter scale)
 """
 
@@ -640,6 +653,24 @@ WORKLOADS = {w.name: w for w in (TopkC4(), TopkC4Bf16(), WindowC2(), TransitionC
                                  TransitionDenseC3(), ProgressiveC5())}
 
 
+def capture_step(torch, step):
+    """Capture one call of `step` into a HIP graph and return its replay.
+    Two warm-up calls run first on a side stream (default priority), so lazy
+    initialisation happens outside the capture."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    return graph.replay
+
+
 def workload_step(wl, torch, dev, impl: str = "native", batch: int | None = None):
     """The timed step of a workload: its own make_step, or forward+backward of its operator."""
     if hasattr(wl, "make_step"):
@@ -674,6 +705,10 @@ def main() -> int:
                     help="score arithmetic of the top-k select (library default: split-f16)")
     ap.add_argument("--gemm-tile", type=int, choices=[0, 64, 128], default=0,
                     help="force the GEMM workgroup tile (0: chosen per call)")
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager steps only (default for the operator workloads: time replays of the step "
+                         "captured into one HIP graph, torch.cuda.CUDAGraph, after timing the same number of "
+                         "eager steps with per-kernel HIP events)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of known size (scale for HBM byte counters)")
     args = ap.parse_args()
@@ -693,26 +728,40 @@ def main() -> int:
     jn.set_select_mode(jn.SELECT_SPLIT_F16 if args.select_mode == "split-f16" else jn.SELECT_F32)
     wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
+    use_graph = not args.eager and not hasattr(wl, "make_step")  # C5's optimizer step runs eager
     step = workload_step(wl, torch, dev)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
+    def timed(fn):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(args.steps):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / args.steps, time.perf_counter() - t0
+
+    # eager steps with the library's per-kernel HIP events on the launch stream
     jn.profile_enable(True)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record()
-    for _ in range(args.steps):
-        step()
-    stop.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    eager_ms, wall = timed(step)
     prof = jn.profile_collect()
     jn.profile_enable(False)
-
-    ms_per_step = start.elapsed_time(stop) / args.steps
+    ms_per_step = eager_ms
+    graph_info = None
+    if use_graph:
+        replay = capture_step(torch, step)
+        for _ in range(args.warmup):
+            replay()
+        ms_per_step, wall = timed(replay)
+        graph_info = {"eager_ms_per_step": round(eager_ms, 5), "eager_value": wl.edges() / (eager_ms / 1e3),
+                      "note": "value and ms_per_step time back-to-back replays of one captured forward+backward "
+                              "step (every kernel runs each replay); the kernel table and roofline come from the "
+                              "eager steps timed just before with HIP events on the launch stream (same kernels)"}
     E = wl.edges()
     value = E / (ms_per_step / 1e3)
 
@@ -797,6 +846,7 @@ def main() -> int:
         "roofline": roofline,
         "kernels": kernels,
         "wall_s_timed": round(wall, 3),
+        "graph": graph_info,
         "device": torch.cuda.get_device_name(0),
     }
     if not args.no_cpu_baseline:

@@ -30,7 +30,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 6. */
+/* ABI revision of this header (bumped on any signature change); this is 7. */
 int jn_abi_version(void);
 
 /*
@@ -500,6 +500,19 @@ int jn_transition_topk_backward_bf16(
     uint16_t* grad_dst_val, float* grad_projected_state, uint16_t* grad_projected_val, float* grad_source_weight,
     float* grad_target_weight, float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
     jn_stream_t stream);
+
+/*
+ * Score scale vector of the low-rank pairwise scores: weight_hat[h] =
+ * weight[h] / max(||weight[h]||_2, eps) for each of `rows` rows of `rank`
+ * (LowRankBilinearPairwise.normalized_weight, modules.py:85-87; one row per
+ * head for stacked heads), and the gradient of that map.  No counterpart in
+ * the reference's native extension, whose callers compute it with a chain of
+ * PyTorch ops (kernel_common.py:182, 188, 196); one kernel each here.
+ */
+int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float eps, float* weight_hat,
+                          jn_stream_t stream);
+int jn_unit_scale_backward(const float* weight, const float* grad_weight_hat, int64_t rows, int64_t rank, float eps,
+                           float* grad_weight, jn_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -297,6 +297,8 @@ int check_transition_dense_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t
 // Backward of any edge-list propagation (top-k or window): the edge list
 // (edge_index, edge_score) [B*N, k] is what the forward aggregated.
 // rank: all ranks (heads * head rank); heads > 1 takes each edge's head.
+// band: the list is a window forward's causal band, whose transpose is known
+// in closed form (no CSR build; the column pass reads the edge arrays).
 int propagation_edges_backward(const float* layer_val, const float* projected_state, const float* projected_val,
                                const float* target_weight, const float* source_weight, const float* core_weight,
                                const float* projections, const int32_t* topk_index, const float* topk_score,
@@ -306,7 +308,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
                                int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
                                float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
                                float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
-                               hipStream_t stream, bool bf16 = false) {
+                               hipStream_t stream, bool bf16 = false, bool band = false) {
   int rc;
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
                  projections && topk_index && topk_score && grad_delta_state && grad_delta_val &&
@@ -357,7 +359,8 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   rc = launch_rows_backward(rb, st);
   if (rc) return rc;
 
-  // 2. transpose the edge list to source-major order (deterministic)
+  // 2. transpose the edge list to source-major order (deterministic; closed
+  //    form for a band)
   CsrArgs ca{};
   ca.idx = topk_index;
   ca.k = k;
@@ -371,8 +374,10 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   ca.g_score = s.g_score;
   ca.gds = grad_delta_state;
   ca.ehead = mh ? edge_head : nullptr;
-  rc = launch_csr(ca, st);
-  if (rc) return rc;
+  if (!band) {
+    rc = launch_csr(ca, st);
+    if (rc) return rc;
+  }
 
   // 3. columns: value/state grads of the sources, grad of source projection, w_hat grad partials
   float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
@@ -401,6 +406,13 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   if (mh) {
     cb.heads = (int)heads;
     cb.head_rank = (int)(rank / heads);
+  }
+  if (band) {
+    cb.band = 1;
+    cb.coef = s.coef;
+    cb.g_score = s.g_score;
+    cb.gds = grad_delta_state;
+    cb.ehead = mh ? edge_head : nullptr;
   }
   rc = launch_cols_backward(cb, st);
   if (rc) return rc;
@@ -589,7 +601,18 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 6; }
+int jn_abi_version(void) { return 7; }
+
+int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float eps, float* weight_hat,
+                          jn_stream_t stream) {
+  return launch_unit_scale(weight, nullptr, rows, rank, eps, weight_hat, static_cast<hipStream_t>(stream));
+}
+
+int jn_unit_scale_backward(const float* weight, const float* grad_weight_hat, int64_t rows, int64_t rank, float eps,
+                           float* grad_weight, jn_stream_t stream) {
+  JN_REQUIRE(grad_weight_hat, kInvalidArgument, "null tensor pointer");
+  return launch_unit_scale(weight, grad_weight_hat, rows, rank, eps, grad_weight, static_cast<hipStream_t>(stream));
+}
 
 int jn_profile_enable(int32_t on) {
   std::lock_guard<std::mutex> lock(jakal::g_prof_mu);
@@ -758,7 +781,8 @@ int jn_propagation_window_backward(const float* layer_val, const float* projecte
                                     grad_delta_val, batch, nodes, in_dim, out_dim, rank, 1, width, compress_kind,
                                     projected_val_is_layer_val, grad_layer_val, grad_projected_state,
                                     grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
-                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream), false,
+                                    true);
 }
 
 size_t jn_transition_topk_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
@@ -1176,7 +1200,8 @@ int jn_propagation_window_backward_multihead(
                                     grad_delta_val, batch, nodes, in_dim, out_dim, rank * heads, heads, width,
                                     compress_kind, projected_val_is_layer_val, grad_layer_val, grad_projected_state,
                                     grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
-                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream), false,
+                                    true);
 }
 
 size_t jn_transition_topk_multihead_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes,
@@ -1298,7 +1323,7 @@ int jn_propagation_window_backward_bf16(
                                     width, compress_kind, projected_val_is_layer_val, reinterpret_cast<float*>(grad_layer_val),
                                     grad_projected_state, reinterpret_cast<float*>(grad_projected_val), grad_target_weight,
                                     grad_source_weight, grad_core_weight, grad_bias, workspace, workspace_bytes,
-                                    static_cast<hipStream_t>(stream), true);
+                                    static_cast<hipStream_t>(stream), true, true);
 }
 
 int jn_transition_topk_forward_bf16(const float* sender_strength, const uint16_t* src_val, const uint16_t* dst_val,

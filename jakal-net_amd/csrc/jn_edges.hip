@@ -659,12 +659,49 @@ int launch_csr(const CsrArgs& a, hipStream_t stream) {
 //   part_c[w,r] = sum over the 16 columns of workgroup w of key[j, r] * sum_in g_s * q[i, r]
 // ---------------------------------------------------------------------------
 
+// A column's incoming edge records: CSR segment entries, or (BAND) the causal
+// band's records built from the edge arrays with the CSR fill's arithmetic.
+template <bool BAND>
+struct ColRecords {
+  const float4* rec;  // CSR: the segment's first record
+  int64_t row0;       // BAND: global row of the column's first incoming edge (the key itself)
+  int len;
+
+  __device__ __forceinline__ ColRecords(const ColsBwdArgs& a, int64_t col) {
+    const int b = (int)(col / a.Nk), j = (int)(col % a.Nk);
+    if constexpr (BAND) {
+      rec = nullptr;
+      row0 = (int64_t)b * a.Nq + j;
+      len = min(a.k, a.Nk - j);
+    } else {
+      const int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
+      const int beg = seg[j];
+      len = seg[j + 1] - beg;
+      rec = a.rec + (int64_t)b * a.Nq * a.k + beg;
+      row0 = 0;
+    }
+  }
+  __device__ __forceinline__ float4 get(const ColsBwdArgs& a, int q) const {
+    if constexpr (BAND) {
+      const int64_t row = row0 + q;
+      const int64_t eid = row * a.k + (a.k - 1 - q);
+      const float cf = a.coef ? a.coef[eid] : 0.f;
+      const float gs = a.g_score ? a.g_score[eid] : 0.f;
+      const float cd = a.gds ? cf * a.gds[row] : 0.f;
+      const int hd = a.ehead ? (int)a.ehead[eid] << kRecHeadShift : 0;
+      return make_float4(__int_as_float((int)row | hd), cf, gs, cd);
+    } else {
+      return rec[q];
+    }
+  }
+};
+
 // One wavefront per column and column slab: the gather-accumulate of
 // rows_forward_kernel over the column's records.  The grid is slab-major, so an
 // XCD gathers rows of one slab of one batch element at a time (Nq x slab floats,
 // sized to its L2).  Slab 0 also sums the state.
 // T: element type of the gathered rows (gdv) and of grad_pv.
-template <typename T, int W>
+template <typename T, int W, bool BAND>
 __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int slab_cols) {
   const int lane = lane_id();
   const int64_t total_cols = (int64_t)a.B * a.Nk;
@@ -673,10 +710,8 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
   const int slab = (int)(logical / col_blocks);
   const int64_t col = (logical % col_blocks) * 4 + wave_id();
   if (col >= total_cols) return;
-  const int b = (int)(col / a.Nk), j = (int)(col % a.Nk);
-  const int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
-  const int beg = seg[j], len = seg[j + 1] - beg;
-  const float4* rec = a.rec + (int64_t)b * a.Nq * a.k + beg;
+  const ColRecords<BAND> recs(a, col);
+  const int len = recs.len;
   const int d_begin = slab * slab_cols, d_end = min(a.D, d_begin + slab_cols);
   const T* gdv = reinterpret_cast<const T*>(a.gdv);
   T* out = a.grad_pv ? reinterpret_cast<T*>(a.grad_pv) + col * a.ld_gpv : nullptr;
@@ -689,7 +724,7 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
     int row = 0;
     float cf = 0.f, cd = 0.f;
     if (lane < n) {
-      const float4 r = rec[q0 + lane];
+      const float4 r = recs.get(a, q0 + lane);
       row = __float_as_int(r.x) & kRecRowMask;
       cf = r.y;
       cd = r.w;
@@ -735,7 +770,7 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
 // together.  The scale-vector partials of the 16 columns are summed in a fixed
 // order into one row of part_c per workgroup.
 // MH: each record's head (its row word's top bits) selects the ranks it reaches.
-template <bool VEC, bool MH>
+template <bool VEC, bool MH, bool BAND>
 __global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
   __shared__ float red[4][128];
   const int lane = lane_id(), g = lane >> 4, c = lane & 15, w = wave_id();
@@ -743,15 +778,8 @@ __global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
   const int64_t blk = xcd_swizzle(blockIdx.x, gridDim.x);
   const int64_t col = blk * 16 + w * 4 + g;
   const bool valid = col < total_cols;
-  int len = 0;
-  const float4* rec = a.rec;
-  if (valid) {
-    const int b = (int)(col / a.Nk), j = (int)(col % a.Nk);
-    const int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
-    const int beg = seg[j];
-    len = seg[j + 1] - beg;
-    rec = a.rec + (int64_t)b * a.Nq * a.k + beg;
-  }
+  const ColRecords<BAND> recs(a, valid ? col : 0);
+  const int len = valid ? recs.len : 0;
   int rk[8];  // rank of each slot
 #pragma unroll
   for (int m = 0; m < 8; ++m) rk[m] = VEC ? (m < 4 ? 4 * c + m : 64 + 4 * c + (m - 4)) : c + 16 * m;
@@ -767,7 +795,7 @@ __global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
     int row = -1;
     float gs = 0.f;
     if (q0 + c < len) {
-      const float4 r = rec[q0 + c];
+      const float4 r = recs.get(a, q0 + c);
       row = __float_as_int(r.x);
       gs = r.z;
     }
@@ -831,12 +859,55 @@ __global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
 
 int cols_backward_parts(int64_t total_cols) { return (int)((total_cols + 15) / 16); }
 
+// ---------------------------------------------------------------------------
+// Unit-norm scale vectors (the score scale w_hat = w / max(||w||_2, eps) of
+// LowRankBilinearPairwise, modules.py:85-87, one row per head) and the
+// gradient of that map,
+//   grad_w = g / d - [n >= eps] (g . w) / (d^2 n) w,   n = ||w||, d = max(n, eps)
+// (the clamp passes its gradient where n >= eps, as torch's clamp_min does).
+// One wavefront per row; both sums in a fixed order.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void unit_scale_kernel(const float* w, const float* grad, int r, float eps,
+                                                        float* out) {
+  const int64_t base = (int64_t)blockIdx.x * r;
+  float ss = 0.f, gw = 0.f;
+  for (int i = lane_id(); i < r; i += kWave) {
+    const float x = w[base + i];
+    ss += x * x;
+    if (grad) gw += grad[base + i] * x;
+  }
+  const float n = sqrtf(wave_sum(ss));
+  const float d = fmaxf(n, eps);
+  if (!grad) {
+    for (int i = lane_id(); i < r; i += kWave) out[base + i] = w[base + i] / d;
+    return;
+  }
+  gw = wave_sum(gw);
+  const float c = n >= eps ? gw / (d * d * n) : 0.f;
+  for (int i = lane_id(); i < r; i += kWave) out[base + i] = grad[base + i] / d - c * w[base + i];
+}
+
+int launch_unit_scale(const float* w, const float* grad, int64_t rows, int64_t r, float eps, float* out,
+                      hipStream_t stream) {
+  JN_REQUIRE(w && out, kInvalidArgument, "null tensor pointer");
+  JN_REQUIRE(rows >= 1 && r >= 1 && rows < (1LL << 31) && r < (1LL << 30), kInvalidArgument,
+             "unit scale needs 1 <= rows < 2^31 and 1 <= r < 2^30 (rows=%lld, r=%lld)", (long long)rows,
+             (long long)r);
+  JN_REQUIRE(eps > 0.0f, kInvalidArgument, "eps must be positive");
+  JN_PROFILE(grad ? "unit_scale_backward_kernel" : "unit_scale_kernel", stream);
+  hipLaunchKernelGGL(unit_scale_kernel, dim3((unsigned)rows), dim3(kWave), 0, stream, w, grad, (int)r, eps, out);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   const int64_t total_cols = (int64_t)a.B * a.Nk;
   if (total_cols == 0) return kOk;
   JN_REQUIRE(!a.q || (a.r >= 1 && a.r <= 128), kUnsupported, "rank must be in [1, 128]");
   JN_REQUIRE(!a.q || (a.key && a.dk), kInvalidArgument, "key-side gradient needs key and dk");
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
+  JN_REQUIRE(!a.band || (a.Nq == a.Nk && a.coef && a.g_score && (int64_t)a.B * a.Nq <= kRecRowMask),
+             kInvalidArgument, "band records need Nq == Nk, coef and g_score, and rows below 2^%d", kRecHeadShift);
   if (a.grad_pv || a.grad_ps) {
     const int eb = a.bf16 ? 2 : 4, pw = 16 / eb;  // one 16-byte pack: 4 fp32 or 8 bf16 elements
     const bool vec = (a.D % pw == 0) && (a.ld_gpv % pw == 0) && ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0) &&
@@ -850,12 +921,20 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
     JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
     JN_PROFILE(a.profile_name ? a.profile_name : "cols_gather_kernel", stream);
     const dim3 grid((unsigned)blocks);
-    if (a.bf16) {
-      if (vec) hipLaunchKernelGGL((cols_gather_kernel<bf16_t, 8>), grid, dim3(256), 0, stream, a, slab);
-      else hipLaunchKernelGGL((cols_gather_kernel<bf16_t, 1>), grid, dim3(256), 0, stream, a, slab);
+    if (a.band) {
+      if (a.bf16) {
+        if (vec) hipLaunchKernelGGL((cols_gather_kernel<bf16_t, 8, true>), grid, dim3(256), 0, stream, a, slab);
+        else hipLaunchKernelGGL((cols_gather_kernel<bf16_t, 1, true>), grid, dim3(256), 0, stream, a, slab);
+      } else {
+        if (vec) hipLaunchKernelGGL((cols_gather_kernel<float, 4, true>), grid, dim3(256), 0, stream, a, slab);
+        else hipLaunchKernelGGL((cols_gather_kernel<float, 1, true>), grid, dim3(256), 0, stream, a, slab);
+      }
+    } else if (a.bf16) {
+      if (vec) hipLaunchKernelGGL((cols_gather_kernel<bf16_t, 8, false>), grid, dim3(256), 0, stream, a, slab);
+      else hipLaunchKernelGGL((cols_gather_kernel<bf16_t, 1, false>), grid, dim3(256), 0, stream, a, slab);
     } else {
-      if (vec) hipLaunchKernelGGL((cols_gather_kernel<float, 4>), grid, dim3(256), 0, stream, a, slab);
-      else hipLaunchKernelGGL((cols_gather_kernel<float, 1>), grid, dim3(256), 0, stream, a, slab);
+      if (vec) hipLaunchKernelGGL((cols_gather_kernel<float, 4, false>), grid, dim3(256), 0, stream, a, slab);
+      else hipLaunchKernelGGL((cols_gather_kernel<float, 1, false>), grid, dim3(256), 0, stream, a, slab);
     }
     JN_LAUNCH_CHECK();
   }
@@ -869,12 +948,20 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
     JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
     JN_PROFILE("cols_keygrad_kernel", stream);
     const dim3 grid((unsigned)blocks);
-    if (mh) {
-      if (vec) hipLaunchKernelGGL((cols_keygrad_kernel<true, true>), grid, dim3(256), 0, stream, a);
-      else hipLaunchKernelGGL((cols_keygrad_kernel<false, true>), grid, dim3(256), 0, stream, a);
+    if (a.band) {
+      if (mh) {
+        if (vec) hipLaunchKernelGGL((cols_keygrad_kernel<true, true, true>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((cols_keygrad_kernel<false, true, true>), grid, dim3(256), 0, stream, a);
+      } else {
+        if (vec) hipLaunchKernelGGL((cols_keygrad_kernel<true, false, true>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((cols_keygrad_kernel<false, false, true>), grid, dim3(256), 0, stream, a);
+      }
+    } else if (mh) {
+      if (vec) hipLaunchKernelGGL((cols_keygrad_kernel<true, true, false>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((cols_keygrad_kernel<false, true, false>), grid, dim3(256), 0, stream, a);
     } else {
-      if (vec) hipLaunchKernelGGL((cols_keygrad_kernel<true, false>), grid, dim3(256), 0, stream, a);
-      else hipLaunchKernelGGL((cols_keygrad_kernel<false, false>), grid, dim3(256), 0, stream, a);
+      if (vec) hipLaunchKernelGGL((cols_keygrad_kernel<true, false, false>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((cols_keygrad_kernel<false, false, false>), grid, dim3(256), 0, stream, a);
     }
     JN_LAUNCH_CHECK();
   }

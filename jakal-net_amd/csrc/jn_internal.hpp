@@ -287,8 +287,23 @@ struct ColsBwdArgs {
   // Multi-head (heads > 1): a record's g_score reaches only its head's ranks of dk.
   int heads, head_rank;
   int bf16;                  // gdv and grad_pv hold bf16 elements (the pointers are reinterpreted)
+  // Causal band (window edge lists, Nq == Nk): band != 0 builds each record
+  // from the edge arrays instead of seg_start / rec.  Key j's incoming edges
+  // are rows j + t for 0 <= t < min(k, Nk - j), row j + t holding j in slot
+  // k - 1 - t, so the records come in increasing row order as the CSR lists
+  // them.
+  int band;
+  const float* coef;         // [B * Nq, k]
+  const float* g_score;      // [B * Nq, k]
+  const float* gds;          // [B * Nq] or null (record word 3 is then 0)
+  const uint8_t* ehead;      // [B * Nq, k] or null (head 0)
 };
 int cols_backward_parts(int64_t total_cols);
+
+// Unit-norm scale vectors: out = w / max(||w||, eps) per row of [rows, r], or
+// with grad (non-null) the gradient of that map at w.
+int launch_unit_scale(const float* w, const float* grad, int64_t rows, int64_t r, float eps, float* out,
+                      hipStream_t stream);
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream);
 
 // Scale-vector and bias gradients: grad_c[r] from the [nparts, r] partials,

@@ -112,22 +112,26 @@ def _stack(values: list) -> torch.Tensor | None:
     return None if values[0] is None else torch.stack(values)
 
 
-def pairwise_kernel_spec(pairwise_fn: object) -> PairwiseKernelSpec:
+def pairwise_kernel_spec(pairwise_fn: object, unit_scale=None) -> PairwiseKernelSpec:
+    """The kernel arguments of a score module.  unit_scale, when given, maps a
+    raw [r] weight or [H, r] stack to w / max(||w||, 1e-6) per row (the native
+    module's fused op); otherwise each module's normalized_weight() is used."""
     heads = _pairwise_heads(pairwise_fn)
     if heads is not None:
-        specs = [pairwise_kernel_spec(h) for h in heads]
+        weight = (torch.stack([h.normalized_weight() for h in heads]) if unit_scale is None
+                  else unit_scale(torch.stack([h.weight for h in heads])))
         return PairwiseKernelSpec(
             kind="multihead_max_low_rank_bilinear",
-            weight=_stack([p.weight for p in specs]),
-            bias=_stack([p.bias for p in specs]),
-            in_weight=_stack([p.in_weight for p in specs]),
-            out_weight=_stack([p.out_weight for p in specs]),
+            weight=weight,
+            bias=_stack([h.bias for h in heads]),
+            in_weight=_stack([h.source_proj.weight for h in heads]),
+            out_weight=_stack([h.target_proj.weight for h in heads]),
         )
     if not isinstance(pairwise_fn, LowRankBilinearPairwise):
         raise TypeError(f"no native kernel spec for a {type(pairwise_fn).__name__} score module.")
     return PairwiseKernelSpec(
         kind="low_rank_bilinear",
-        weight=pairwise_fn.normalized_weight(),
+        weight=pairwise_fn.normalized_weight() if unit_scale is None else unit_scale(pairwise_fn.weight),
         bias=pairwise_fn.bias,
         in_weight=pairwise_fn.source_proj.weight,
         out_weight=pairwise_fn.target_proj.weight,

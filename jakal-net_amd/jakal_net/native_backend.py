@@ -184,7 +184,7 @@ def propagation_topk_native(
 ) -> LayerDelta:
     if not supports_pairwise_kernel(pairwise_fn):
         raise TypeError("Unsupported pairwise_fn for native propagation.")
-    spec = pairwise_kernel_spec(pairwise_fn)
+    spec = pairwise_kernel_spec(pairwise_fn, unit_scale=getattr(_native_module(), "unit_scale", None))
     return _to_layer_delta(
         _native_module().propagation_topk(
             spec.kind, spec.weight, spec.bias, spec.in_weight, spec.in_bias, spec.out_weight, spec.out_bias,
@@ -207,7 +207,7 @@ def propagation_window_native(
 ) -> LayerDelta:
     if not supports_pairwise_kernel(pairwise_fn):
         raise TypeError("Unsupported pairwise_fn for native propagation.")
-    spec = pairwise_kernel_spec(pairwise_fn)
+    spec = pairwise_kernel_spec(pairwise_fn, unit_scale=getattr(_native_module(), "unit_scale", None))
     return _to_layer_delta(
         _native_module().propagation_window(
             spec.kind, spec.weight, spec.bias, spec.in_weight, spec.in_bias, spec.out_weight, spec.out_bias,
@@ -230,7 +230,7 @@ def propagation_dense_native(
 ) -> LayerDelta:
     if not supports_pairwise_kernel(pairwise_fn):
         raise TypeError("Unsupported pairwise_fn for native propagation.")
-    spec = pairwise_kernel_spec(pairwise_fn)
+    spec = pairwise_kernel_spec(pairwise_fn, unit_scale=getattr(_native_module(), "unit_scale", None))
     return _to_layer_delta(
         _native_module().propagation_dense(
             spec.kind, spec.weight, spec.bias, spec.in_weight, spec.in_bias, spec.out_weight, spec.out_bias,

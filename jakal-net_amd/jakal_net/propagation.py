@@ -58,12 +58,6 @@ from jakal_net.native_backend import (
 NATIVE_EDGE_COMPRESSIONS = ("softsign", "signed_abs_softmax", "signed_entmax15")
 
 
-def capturing_graph(t: Tensor) -> bool:
-    """True while ``t``'s device stream is being captured into a graph (the
-    reference sends such calls to its PyTorch form, propagation.py:775-776)."""
-    return t.is_cuda and torch.cuda.is_current_stream_capturing()
-
-
 class Propagation(nn.Module):
     """Dense same-layer propagation (reference propagation.py:108-404)."""
 
@@ -207,7 +201,11 @@ class Propagation(nn.Module):
     # ---- dispatch ------------------------------------------------------------
     def compute_delta(self, layer: Layer) -> LayerDelta:
         impl = self.implementation
-        if impl == "reference" or (impl == "native" and capturing_graph(layer.val)):
+        # The reference sends native calls made under graph capture to its
+        # PyTorch form (propagation.py:356-357, 775-776).  The HIP ops launch
+        # kernels only (no allocation, synchronisation or memset inside the
+        # library), so a captured step keeps them.
+        if impl == "reference":
             return self._compute_delta_reference(layer)
         if impl in ("native", "kernel"):
             delta = self._compute_delta_native(layer, strict=impl == "native")

@@ -51,7 +51,6 @@ from jakal_net.native_backend import (
     transition_pairwise_dense_native,
     transition_pairwise_topk_native,
 )
-from jakal_net.propagation import capturing_graph
 
 _POSITIONAL = (inspect.Parameter.POSITIONAL_ONLY, inspect.Parameter.POSITIONAL_OR_KEYWORD)
 
@@ -246,7 +245,10 @@ class Transition(nn.Module):
         if self.track_stats:
             self.last_stats = self._statistics(src_layer, dst_layer)
         impl = self.implementation
-        if impl == "reference" or (impl == "native" and capturing_graph(src_layer.val)):
+        # native calls stay native under graph capture (the reference's fall
+        # back to PyTorch there, transition.py:332-333, 660-661; the HIP ops
+        # only launch kernels)
+        if impl == "reference":
             return self._compute_delta_reference(src_layer, dst_layer)
         if impl in ("native", "kernel"):
             delta = self._compute_delta_native(src_layer, dst_layer, strict=impl == "native")

@@ -148,6 +148,9 @@ _declare(
      _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 
+_declare("jn_unit_scale_forward", [_P, _I64, _I64, _F, _P, _P])
+_declare("jn_unit_scale_backward", [_P, _P, _I64, _I64, _F, _P, _P])
+
 # bf16 layers: the fp32 entry points' argument lists with bf16 value tensors
 for _name in ("jn_propagation_topk_forward", "jn_propagation_topk_backward", "jn_propagation_window_forward",
               "jn_propagation_window_backward", "jn_transition_topk_forward", "jn_transition_topk_backward"):
@@ -348,6 +351,7 @@ class _PropagationEdges(torch.autograd.Function):
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, idx, score, head)
         ctx.meta = (mode, param, compress, pv_is_x, bias is not None, heads, bf16)
         ctx.mark_non_differentiable(idx, score)
+        ctx.set_materialize_grads(False)  # no zero-filled gradients for the edge-list outputs
         return ds, dv, idx, score
 
     @staticmethod
@@ -399,6 +403,45 @@ class _PropagationEdges(torch.autograd.Function):
             None,
             None,
         )
+
+
+UNIT_SCALE_EPS = 1e-6  # LowRankBilinearPairwise.normalized_weight's clamp (modules.py:85-87)
+
+
+class _UnitScale(torch.autograd.Function):
+    """w / max(||w||_2, 1e-6) per row of an fp32 [rows, r] stack, one kernel
+    forward and one backward (jn_unit_scale_*)."""
+
+    @staticmethod
+    def forward(ctx, w):  # noqa: D401
+        out = torch.empty_like(w)
+        with torch.cuda.device(w.device):
+            _check(_LIB.jn_unit_scale_forward(_ptr(w), w.shape[0], w.shape[1], UNIT_SCALE_EPS, _ptr(out),
+                                              _stream(w.device)))
+        ctx.save_for_backward(w)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (w,) = ctx.saved_tensors
+        g = g.float().contiguous()
+        gw = torch.empty_like(w)
+        with torch.cuda.device(w.device):
+            _check(_LIB.jn_unit_scale_backward(_ptr(w), _ptr(g), w.shape[0], w.shape[1], UNIT_SCALE_EPS,
+                                               _ptr(gw), _stream(w.device)))
+        return gw
+
+
+def unit_scale(weight: Tensor) -> Tensor:
+    """The low-rank score scale w / max(||w||_2, 1e-6) of a [r] vector, or of
+    each row of an [H, r] stack, on the HIP library (differentiable).  Same
+    values as LowRankBilinearPairwise.normalized_weight (modules.py:85-87) up
+    to fp32 rounding of the norm."""
+    if not weight.is_cuda or weight.dtype != torch.float32 or weight.dim() not in (1, 2):
+        raise NotImplementedError("unit_scale takes an fp32 [r] or [H, r] tensor on a HIP device")
+    w2 = weight.contiguous().view(1, -1) if weight.dim() == 1 else weight.contiguous()
+    out = _UnitScale.apply(w2)
+    return out.view(-1) if weight.dim() == 1 else out
 
 
 def _bf16_rows(*tensors: Tensor | None) -> bool:
@@ -805,6 +848,7 @@ class _TransitionTopK(torch.autograd.Function):
         ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, idx, logit, head)
         ctx.meta = (float(temperature), int(topk), compress, bias is not None, heads, bf16)
         ctx.mark_non_differentiable(idx, logit)
+        ctx.set_materialize_grads(False)  # no zero-filled gradients for the edge-list outputs
         return ds, dv, idx, logit
 
     @staticmethod

@@ -54,6 +54,16 @@ int jn_profile_collect(char* buffer, size_t size);
 int jn_set_gemm_tile(int32_t tile);
 
 /*
+ * Window kernels (no counterpart in the reference; for tests and tuning).
+ * mode 0 (the default) runs a window edge list's aggregation, value-row dot
+ * products and value gradient as MFMA tiles over each 64-row tile's span of
+ * the causal band whenever the band is at most 128 wide and the value rows
+ * are whole, aligned 16-byte packs; mode 1 runs the per-edge gather kernels
+ * for every window.  Process-wide; results agree up to fp32 summation order.
+ */
+int jn_set_window_kernels(int32_t mode);
+
+/*
  * Score arithmetic of the top-k select (no counterpart in the reference; for
  * tests and tuning).  mode 0 (the default) computes the low-rank score tiles
  * on fp16 MFMAs over two-term fp16 splits of the operands: every operand is

@@ -356,6 +356,27 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
     rb.heads = (int)heads;
     rb.head_rank = (int)(rank / heads);
   }
+  // a causal band: the value-row dot products as MFMA tiles over each row
+  // tile's span, then the row kernel without value rows
+  const bool band_mfma = band && window_kernels() == 0 &&
+                         band_kernels_fit(k, (int)out_dim, out_dim, out_dim, grad_delta_val, projected_val, bf16);
+  if (band_mfma) {
+    BandDotsArgs bd{};
+    bd.B = B;
+    bd.N = N;
+    bd.k = k;
+    bd.D = (int)out_dim;
+    bd.gdv = grad_delta_val;
+    bd.ld_gdv = out_dim;
+    bd.pv = projected_val;
+    bd.ld_pv = out_dim;
+    bd.g_score = s.g_score;
+    bd.coef = s.coef;
+    bd.bf16 = bf16 ? 1 : 0;
+    rc = launch_band_dots(bd, st);
+    if (rc) return rc;
+    rb.dots_given = 1;
+  }
   rc = launch_rows_backward(rb, st);
   if (rc) return rc;
 
@@ -413,6 +434,27 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
     cb.g_score = s.g_score;
     cb.gds = grad_delta_state;
     cb.ehead = mh ? edge_head : nullptr;
+  }
+  if (band_mfma && gpv && band_kernels_fit(k, (int)out_dim, out_dim, out_dim, grad_delta_val, gpv, bf16)) {
+    // the value and state gradients of the sources: the transposed band as MFMA tiles
+    BandAggArgs cg{};
+    cg.B = B;
+    cg.N = N;
+    cg.k = k;
+    cg.D = (int)out_dim;
+    cg.trans = 1;
+    cg.coef = s.coef;
+    cg.state = grad_delta_state;
+    cg.val = grad_delta_val;
+    cg.ld_val = out_dim;
+    cg.out_state = grad_projected_state;
+    cg.out = gpv;
+    cg.ld_out = out_dim;
+    cg.bf16 = bf16 ? 1 : 0;
+    rc = launch_band_aggregate(cg, st);
+    if (rc) return rc;
+    cb.grad_pv = nullptr;  // the column kernels still compute dK and the scale partials
+    cb.grad_ps = nullptr;
   }
   rc = launch_cols_backward(cb, st);
   if (rc) return rc;
@@ -574,6 +616,26 @@ int propagation_window_forward_impl(const float* layer_val, const float* project
   rc = launch_window_scores(w, st);
   if (rc) return rc;
 
+  if (window_kernels() == 0 &&
+      band_kernels_fit((int)width, (int)out_dim, out_dim, out_dim, projected_val, delta_val, bf16)) {
+    BandAggArgs f{};  // the band's aggregation as MFMA tiles
+    f.B = (int)batch;
+    f.N = (int)nodes;
+    f.k = (int)width;
+    f.D = (int)out_dim;
+    f.trans = 0;
+    f.compress = compress_kind;
+    f.idx = edge_index;
+    f.score = edge_score;
+    f.state = projected_state;
+    f.val = projected_val;
+    f.ld_val = out_dim;
+    f.out_state = delta_state;
+    f.out = delta_val;
+    f.ld_out = out_dim;
+    f.bf16 = bf16 ? 1 : 0;
+    return launch_band_aggregate(f, st);
+  }
   RowsFwdArgs f{};
   f.idx = edge_index;
   f.score = edge_score;
@@ -629,6 +691,13 @@ int jn_set_gemm_tile(int32_t tile) {
   JN_REQUIRE(tile == 0 || tile == 64 || tile == 128, kInvalidArgument, "GEMM tile must be 0, 64 or 128, got %d",
              (int)tile);
   jakal::set_gemm_tile(tile);
+  return kOk;
+}
+
+int jn_set_window_kernels(int32_t mode) {
+  JN_REQUIRE(mode == 0 || mode == 1, kInvalidArgument, "window kernel mode must be 0 (band) or 1 (edge), got %d",
+             (int)mode);
+  jakal::set_window_kernels(mode);
   return kOk;
 }
 

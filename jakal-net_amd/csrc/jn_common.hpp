@@ -447,4 +447,46 @@ __device__ __forceinline__ bool ranks_before(float as, int ai, float bs, int bi)
   return (as > bs) || (as == bs && ai < bi);
 }
 
+// ---- edge-list rows ---------------------------------------------------------
+// An edge list is (idx[row, e], score[row, e]), e < k, idx < 0 for an absent
+// edge; a row's coefficients are its compressed scores.
+
+// Row statistics for the signed |s| softmax (max |s| and 1/sum exp).
+__device__ __forceinline__ void row_abs_softmax_stats(const int32_t* idx, const float* score, int64_t row, int k,
+                                                      float& row_max, float& row_inv_sum) {
+  const int lane = lane_id();
+  float m = -INFINITY;
+  for (int e = lane; e < k; e += kWave)
+    if (idx[row * k + e] >= 0) m = fmaxf(m, fabsf(score[row * k + e]));
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, shfl_xor_f(m, s));
+  float sum = 0.0f;
+  for (int e = lane; e < k; e += kWave)
+    if (idx[row * k + e] >= 0) sum += __expf(fabsf(score[row * k + e]) - m);
+  sum = wave_sum(sum);
+  row_max = m;
+  row_inv_sum = sum > 0.f ? 1.0f / sum : 0.0f;
+}
+
+// Coefficient of edge e0 + lane of a row (0 for absent edges).
+__device__ __forceinline__ void row_coefficients(const int32_t* idx, const float* score, int64_t row, int k, int e0,
+                                                 int compress, float row_max, float row_inv_sum, int& j, float& c,
+                                                 float& s) {
+  const int e = e0 + lane_id();
+  j = -1;
+  c = 0.0f;
+  s = 0.0f;
+  if (e < k) {
+    j = idx[row * k + e];
+    if (j >= 0) {
+      s = score[row * k + e];
+      c = (compress == 0) ? softsign_f(s) : sign_f(s) * __expf(fabsf(s) - row_max) * row_inv_sum;
+    }
+  }
+  if (compress == 2) {  // uniform; the whole row is this wavefront's (k <= 64 checked on the host)
+    const float p = entmax15_lane(fabsf(s), j >= 0);
+    c = j >= 0 ? sign_f(s) * p : 0.0f;
+  }
+}
+
 }  // namespace jakal

@@ -21,44 +21,6 @@ namespace jakal {
 // Row forward: one wavefront per query row.
 // ---------------------------------------------------------------------------
 
-// Row statistics for the signed |s| softmax (max |s| and 1/sum exp).
-__device__ __forceinline__ void row_abs_softmax_stats(const int32_t* idx, const float* score, int64_t row, int k,
-                                                      float& row_max, float& row_inv_sum) {
-  const int lane = lane_id();
-  float m = -INFINITY;
-  for (int e = lane; e < k; e += kWave)
-    if (idx[row * k + e] >= 0) m = fmaxf(m, fabsf(score[row * k + e]));
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, shfl_xor_f(m, s));
-  float sum = 0.0f;
-  for (int e = lane; e < k; e += kWave)
-    if (idx[row * k + e] >= 0) sum += __expf(fabsf(score[row * k + e]) - m);
-  sum = wave_sum(sum);
-  row_max = m;
-  row_inv_sum = sum > 0.f ? 1.0f / sum : 0.0f;
-}
-
-// Coefficient of edge e0 + lane of a row (0 for absent edges).
-__device__ __forceinline__ void row_coefficients(const int32_t* idx, const float* score, int64_t row, int k, int e0,
-                                                 int compress, float row_max, float row_inv_sum, int& j, float& c,
-                                                 float& s) {
-  const int e = e0 + lane_id();
-  j = -1;
-  c = 0.0f;
-  s = 0.0f;
-  if (e < k) {
-    j = idx[row * k + e];
-    if (j >= 0) {
-      s = score[row * k + e];
-      c = (compress == 0) ? softsign_f(s) : sign_f(s) * __expf(fabsf(s) - row_max) * row_inv_sum;
-    }
-  }
-  if (compress == 2) {  // uniform; the whole row is this wavefront's (k <= 64 checked on the host)
-    const float p = entmax15_lane(fabsf(s), j >= 0);
-    c = j >= 0 ? sign_f(s) * p : 0.0f;
-  }
-}
-
 // The D columns are processed in slabs of a.slab columns, slab-major over the
 // grid: while an XCD works on one slab of a batch element, the value rows it
 // gathers (N x slab elements) stay within its L2.  Slab 0 also sums the state.
@@ -467,12 +429,21 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
   const bool vec = (a.D % pw == 0) && (a.ld_pv % pw == 0) && ((reinterpret_cast<uintptr_t>(a.pv) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.gdv) & 15) == 0);
   dim3 grid((unsigned)blocks);
-  if (a.heads > 1) {
-    JN_REQUIRE(a.ehead && a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r, kInvalidArgument,
-               "multi-head row backward needs edge heads and %d..%d heads of equal rank", 2, kMaxHeads);
+  JN_REQUIRE(a.heads <= 1 ||
+                 (a.ehead && a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r),
+             kInvalidArgument, "multi-head row backward needs edge heads and %d..%d heads of equal rank", 2,
+             kMaxHeads);
+  if (a.heads > 1 && !a.dots_given) {
     JN_PROFILE("rows_backward_kernel", stream);
     if (a.bf16) launch_rows_bwd_width<bf16_t, true>(a, vec, grid, stream);
     else launch_rows_bwd_width<float, true>(a, vec, grid, stream);
+    JN_LAUNCH_CHECK();
+    return kOk;
+  }
+  if (a.dots_given) {
+    JN_PROFILE("rows_backward_kernel", stream);
+    if (a.heads > 1) launch_rows_bwd_kp<float, 4, 1, true, true>(a, grid, stream);
+    else launch_rows_bwd_kp<float, 4, 1, true>(a, grid, stream);
     JN_LAUNCH_CHECK();
     return kOk;
   }

@@ -161,8 +161,50 @@ struct RowsBwdArgs {
   const uint8_t* ehead;   // [rows, k]
   int heads, head_rank;
   int bf16;               // pv and gdv hold bf16 elements (the pointers are reinterpreted)
+  // The dot products <gdv[i], pv[j]> of every edge are already in g_score + coef
+  // (two partial sums, e.g. from launch_band_dots): no value rows are read.
+  int dots_given;
 };
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream);
+
+// ---- causal-band kernels of window edge lists (jn_band.hip) --------------
+// Slot e of query row i is key i - (k - 1 - e) (absent below 0); N query rows
+// and N keys per batch element.
+constexpr int kBandMaxK = 128;
+struct BandAggArgs {
+  int B, N, k, D;
+  int trans;            // 0: forward over query rows; 1: column pass over key rows
+  int compress;         // forward: compress kind of the edge scores
+  const int32_t* idx;   // forward: [B*N, k] edge index
+  const float* score;   // forward: [B*N, k] edge scores
+  const float* coef;    // column pass: [B*N, k] edge coefficients
+  const float* state;   // forward: ps [B*N]; column pass: gds [B*N] (null: no state sums)
+  const float* val;     // forward: pv; column pass: gdv -- [B*N] rows of stride ld_val
+  int64_t ld_val;
+  float* out_state;     // forward: delta_state; column pass: grad_ps -- [B*N] or null
+  float* out;           // forward: delta_val; column pass: grad_pv -- [B*N] rows of stride ld_out
+  int64_t ld_out;
+  int bf16;             // val and out hold bf16 elements
+};
+struct BandDotsArgs {
+  int B, N, k, D;
+  const float* gdv;  // [B*N] rows of stride ld_gdv
+  int64_t ld_gdv;
+  const float* pv;   // [B*N] rows of stride ld_pv
+  int64_t ld_pv;
+  float* g_score;    // [B*N, k]: dot partial over the first half of D
+  float* coef;       // [B*N, k]: dot partial over the second half
+  int bf16;          // gdv and pv hold bf16 elements
+};
+// Whether the band kernels take these operands (k <= kBandMaxK, whole 16-byte
+// packs per row, 16-byte aligned rows); otherwise the edge kernels run.
+bool band_kernels_fit(int k, int D, int64_t ld_a, int64_t ld_b, const void* pa, const void* pb, bool bf16);
+// Window kernels of every later call (process-wide, atomic): 0 = band kernels
+// where they fit, 1 = edge kernels only.
+void set_window_kernels(int mode);
+int window_kernels();
+int launch_band_aggregate(const BandAggArgs& a, hipStream_t stream);
+int launch_band_dots(const BandDotsArgs& a, hipStream_t stream);
 
 // Fixed edge lists with low-rank scores: the causal band (all_keys = 0: slot e
 // of query row i is key i - (width - 1 - e), absent when negative) or every

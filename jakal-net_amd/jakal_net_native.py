@@ -52,6 +52,7 @@ _declare("jn_profile_enable", [_I32])
 _declare("jn_profile_collect", [ctypes.c_char_p, _SZ])
 _declare("jn_set_gemm_tile", [_I32])
 _declare("jn_set_select_mode", [_I32])
+_declare("jn_set_window_kernels", [_I32])
 _declare(
     "jn_lowrank_topk_select",
     [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _F, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
@@ -206,6 +207,18 @@ def profile_enable(on: bool = True) -> None:
 def set_gemm_tile(tile: int = 0) -> None:
     """Force the GEMM workgroup tile (64 or 128) for later calls; 0 restores the per-call choice."""
     _check(_LIB.jn_set_gemm_tile(int(tile)))
+
+
+WINDOW_BAND = 0
+WINDOW_EDGES = 1
+
+
+def set_window_kernels(mode: int = WINDOW_BAND) -> None:
+    """Window propagation kernels for later calls (process-wide): WINDOW_BAND
+    (default) multiplies each 64-row tile's span of the causal band on MFMAs
+    where it fits (band <= 128 wide, 16-byte value rows); WINDOW_EDGES runs the
+    per-edge gather kernels for every window."""
+    _check(_LIB.jn_set_window_kernels(int(mode)))
 
 
 SELECT_SPLIT_F16 = 0

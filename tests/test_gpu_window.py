@@ -174,3 +174,23 @@ def test_full_causal_window_runs_dense(dev, compress, separate_pv, window_extra)
     t32 = torch32_propagation(dev, val, state, pv_cpu if separate_pv else None, U, V, w_hat, float(b), mask,
                               compress, gds, gdv)
     _compare(gr, t32, ds, dv, X, ps, pv if separate_pv else None, Ud, Vd, wd, bd)
+
+
+@pytest.mark.parametrize("compress", ["softsign", "signed_entmax15"])
+def test_window_edge_kernels_forced(dev, compress):
+    """The per-edge gather kernels (jn_set_window_kernels(1)) against the oracle;
+    by default windows up to 128 wide with whole 16-byte value rows run on the
+    band's MFMA tiles, and the other tests here cover that path."""
+    import jakal_net_native as jn
+
+    jn.set_window_kernels(jn.WINDOW_EDGES)
+    try:
+        _run(dev, 2001, B=2, N=64, D=32, r=8, window=8, compress=compress, separate_pv=True)
+        _run(dev, 2003, B=1, N=200, D=384, r=32, window=63, compress=compress, separate_pv=False)
+    finally:
+        jn.set_window_kernels(jn.WINDOW_BAND)
+
+
+def test_window_unaligned_rows_take_the_edge_kernels(dev):
+    """D = 30 is not a whole number of 16-byte packs: the edge kernels run."""
+    _run(dev, 2004, B=2, N=90, D=30, r=6, window=20, compress="signed_entmax15", separate_pv=True)

@@ -427,6 +427,22 @@ constexpr bool gemm_use_bf16(GemmUse u) {
 constexpr int kFT = 128;
 constexpr uint32_t kFastRecords = 0x80000000u;
 
+// Four consecutive operand elements at a byte offset of a buffer resource as
+// fp32 (zeros when out of range): one 16-byte load of fp32, or one 8-byte load
+// of bf16 widened exactly.
+template <bool BF>
+__device__ __forceinline__ float4 fast_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  if constexpr (BF) {
+    const uint2 x = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0));
+    float4 f;
+    unpack_bf16x2(x.x, f.x, f.y);
+    unpack_bf16x2(x.y, f.z, f.w);
+    return f;
+  } else {
+    return buf_load4(r, byte_off);
+  }
+}
+
 template <bool KC, int BK>
 struct FastLds {
   static constexpr int stride = KC ? BK + 4 : kFT + 4;
@@ -491,13 +507,22 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
   int kbeg = split * g.k_chunk;
   int kend = min(g.K, kbeg + g.k_chunk);
   causal_k_range<kFT>(g, m0, n0, kbeg, kend);
-  const float* gA = g.A + bz * g.a_bs;
-  const float* gB0 = g.B0 + bz * g.b_bs;
-  const float* gB1 = g.B1 + bz * g.b_bs;
+  // bf16 uses: X is the A operand (project), the B operand (weight gradient)
+  // or C with its addend (input gradient); offsets below are in elements
+  constexpr bool A_BF = USE == kGemmProjectBf16;
+  constexpr bool B_BF = USE == kGemmGradWeightBf16;
+  constexpr bool C_BF = USE == kGemmGradInputBf16;
+  constexpr uint32_t AEB = A_BF ? 2 : 4, BEB = B_BF ? 2 : 4;
+  const char* gA = reinterpret_cast<const char*>(g.A) + bz * g.a_bs * AEB;
+  const char* gB0 = reinterpret_cast<const char*>(g.B0) + bz * g.b_bs * BEB;
+  const char* gB1 = reinterpret_cast<const char*>(g.B1) + bz * g.b_bs * BEB;
   const float* gadd = g.addend ? g.addend + bz * g.add_bs : nullptr;
   const float* kscale = g.a_kscale ? g.a_kscale + bz * g.ks_bs : nullptr;
   const float* mscale = g.c_mscale ? g.c_mscale + bz * g.ms_bs : nullptr;
   float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
+  [[maybe_unused]] bf16_t* Cb = reinterpret_cast<bf16_t*>(g.C) + (int64_t)split * g.c_split_stride + bz * g.c_bs;
+  [[maybe_unused]] const bf16_t* gaddb =
+      g.addend ? reinterpret_cast<const bf16_t*>(g.addend) + bz * g.add_bs : nullptr;
   const int lda = (int)g.lda, ldb = (int)g.ldb;
 
   // Registers of the prefetched slice.  Everything that combines loaded
@@ -511,7 +536,7 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
 
   auto load_slice = [&](int k0) {
     // ---- A ----
-    const float* abase = A_KC ? gA + (int64_t)m0 * lda + k0 : gA + (int64_t)k0 * lda + m0;
+    const char* abase = gA + (A_KC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0) * AEB;
     const auto ars = make_rsrc(abase, kFastRecords);
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
@@ -519,7 +544,7 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
       const int row = A_KC ? e / KCH : e / MCH;  // m (A_KC) or k offset in the slice
       const int c4 = A_KC ? (e % KCH) * 4 : (e % MCH) * 4;
       const bool ok = A_KC ? (m0 + row < g.M && k0 + c4 < kend) : (k0 + row < kend && m0 + c4 < g.M);
-      ra[u] = buf_load4(ars, ok ? (uint32_t)(row * lda + c4) * 4u : kOobOffset);
+      ra[u] = fast_load4<A_BF>(ars, ok ? (uint32_t)(row * lda + c4) * AEB : kOobOffset);
       if constexpr (KSCALE) {
         const auto srs = make_rsrc(kscale + k0, kFastRecords);
         if constexpr (A_KC) {
@@ -536,11 +561,11 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
     // be a multiple of 16), so the buffer is chosen per wave and instruction;
     // both resources address rows relative to the slice's first row.
     const int s0 = B_KC ? n0 : k0;
-    const float* base0 = B_KC ? gB0 + (int64_t)n0 * ldb + k0 : gB0 + (int64_t)k0 * ldb + n0;
+    const char* base0 = gB0 + (B_KC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0) * BEB;
     const auto brs0 = make_rsrc(base0, kFastRecords);
     [[maybe_unused]] const auto brs1 =
-        make_rsrc(BSPLIT ? (B_KC ? gB1 + (int64_t)(n0 - g.b_split) * ldb + k0
-                                 : gB1 + (int64_t)(k0 - g.b_split) * ldb + n0)
+        make_rsrc(BSPLIT ? gB1 + (B_KC ? (int64_t)(n0 - g.b_split) * ldb + k0 : (int64_t)(k0 - g.b_split) * ldb + n0) *
+                               BEB
                          : base0,
                   kFastRecords);
 #pragma unroll
@@ -549,12 +574,12 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
       const int row = B_KC ? e / KCH : e / MCH;  // n (B_KC) or k offset in the slice
       const int c4 = B_KC ? (e % KCH) * 4 : (e % MCH) * 4;
       const bool ok = B_KC ? (n0 + row < g.N && k0 + c4 < kend) : (k0 + row < kend && n0 + c4 < g.N);
-      const uint32_t off = ok ? (uint32_t)(row * ldb + c4) * 4u : kOobOffset;
+      const uint32_t off = ok ? (uint32_t)(row * ldb + c4) * BEB : kOobOffset;
       if constexpr (BSPLIT) {
         const int wrow = B_KC ? (wave * 64 + 256 * u) / KCH : (wave * 64 + 256 * u) / MCH;  // wave-uniform
-        rb[u] = buf_load4(s0 + wrow < g.b_split ? brs0 : brs1, off);
+        rb[u] = fast_load4<B_BF>(s0 + wrow < g.b_split ? brs0 : brs1, off);
       } else {
-        rb[u] = buf_load4(brs0, off);
+        rb[u] = fast_load4<B_BF>(brs0, off);
       }
     }
   };
@@ -669,11 +694,23 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
             const float sm = mscale[m];
             x.x *= sm; x.y *= sm; x.z *= sm; x.w *= sm;
           }
-          if (gadd) {
-            const float4 a = *reinterpret_cast<const float4*>(&gadd[(int64_t)m * g.ld_add + n]);
-            x.x += a.x; x.y += a.y; x.z += a.z; x.w += a.w;
+          if constexpr (C_BF) {
+            if (gaddb) {
+              const uint2 ab = *reinterpret_cast<const uint2*>(&gaddb[(int64_t)m * g.ld_add + n]);
+              float4 a;
+              unpack_bf16x2(ab.x, a.x, a.y);
+              unpack_bf16x2(ab.y, a.z, a.w);
+              x.x += a.x; x.y += a.y; x.z += a.z; x.w += a.w;
+            }
+            *reinterpret_cast<uint2*>(&Cb[(int64_t)m * g.ldc + n]) =
+                make_uint2(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w));
+          } else {
+            if (gadd) {
+              const float4 a = *reinterpret_cast<const float4*>(&gadd[(int64_t)m * g.ld_add + n]);
+              x.x += a.x; x.y += a.y; x.z += a.z; x.w += a.w;
+            }
+            *reinterpret_cast<float4*>(&C[(int64_t)m * g.ldc + n]) = x;
           }
-          *reinterpret_cast<float4*>(&C[(int64_t)m * g.ldc + n]) = x;
         }
       }
       __syncthreads();
@@ -697,8 +734,13 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
             float x = acc[mt][nt][v];
             if (g.c_nscale) x *= g.c_nscale[n];
             if (mscale) x *= mscale[m];
-            if (gadd) x += gadd[(int64_t)m * g.ld_add + n];
-            C[(int64_t)m * g.ldc + n] = x;
+            if constexpr (C_BF) {
+              if (gaddb) x += (float)gaddb[(int64_t)m * g.ld_add + n];
+              Cb[(int64_t)m * g.ldc + n] = (bf16_t)x;
+            } else {
+              if (gadd) x += gadd[(int64_t)m * g.ld_add + n];
+              C[(int64_t)m * g.ldc + n] = x;
+            }
           }
         }
   }
@@ -737,15 +779,13 @@ static bool f4_aligned(const void* p) { return p == nullptr || (reinterpret_cast
 template <int USE>
 static void launch_use(const GemmArgs& g, bool fast, int zdim, hipStream_t stream) {
   constexpr GemmUseInfo u = kGemmUses[USE];
-  if constexpr (gemm_use_bf16((GemmUse)USE)) fast = false;  // the 128 x 128 kernel reads fp32 only
   if (fast) {
     const int tm = (g.M + kFT - 1) / kFT, tn = (g.N + kFT - 1) / kFT;
     const bool vec = g.N % 4 == 0 && g.ldc % 4 == 0 && g.c_bs % 4 == 0 && g.c_split_stride % 4 == 0 &&
                      f4_aligned(g.C) && f4_aligned(g.c_nscale) && f4_aligned(g.epi_ps) && f4_aligned(g.epi_E) &&
                      (g.addend == nullptr || (g.ld_add % 4 == 0 && g.add_bs % 4 == 0 && f4_aligned(g.addend)));
-    if constexpr (!gemm_use_bf16((GemmUse)USE))
-      hipLaunchKernelGGL((gemm_f32_fast_kernel<u.a_kc, u.b_kc, USE, kFastBK>), dim3(tm * tn * zdim), dim3(256), 0,
-                         stream, g, tm, tn, vec ? 1 : 0);
+    hipLaunchKernelGGL((gemm_f32_fast_kernel<u.a_kc, u.b_kc, USE, kFastBK>), dim3(tm * tn * zdim), dim3(256), 0,
+                       stream, g, tm, tn, vec ? 1 : 0);
   } else {
     dim3 grid((g.N + kGBM - 1) / kGBM, (g.M + kGBM - 1) / kGBM, zdim);
     hipLaunchKernelGGL((gemm_f32_kernel<u.a_kc, u.b_kc, USE, kGBM>), grid, dim3(256), 0, stream, g);
@@ -785,9 +825,8 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
   const int forced = g_gemm_tile.load(std::memory_order_relaxed);
   const bool big = forced ? forced == kFT : (g.M >= kFT && g.N >= kFT && tiles128 >= 256);
   // (the 128 x 128 kernel applies the k scale of a scaled use unconditionally)
-  // (bf16 operands run on the generic kernel)
   const bool fast = big && tiles128 < (1LL << 31) && fast_path_ok(g, info.a_kc, info.b_kc) &&
-                    (!info.a_kscale || g.a_kscale != nullptr) && !gemm_use_bf16(use);
+                    (!info.a_kscale || g.a_kscale != nullptr);
   JN_PROFILE(info.name, stream);
   switch (use) {
     case kGemmProject: launch_use<kGemmProject>(g, fast, (int)zdim, stream); break;

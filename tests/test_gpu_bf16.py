@@ -48,10 +48,13 @@ def _pairwise_params(seed, D, r):
 
 @pytest.mark.parametrize("mode", ["topk", "window", "dense"])
 def test_bf16_propagation(dev, mode):
+    run_bf16_propagation(dev, mode, B=2, N=128, D=32, r=8)
+
+
+def run_bf16_propagation(dev, mode, B, N, D, r, k=8, seed=5001):
     import jakal_net_native as jn
 
-    B, N, D, r = 2, 128, 32, 8
-    g, U, V, w = _pairwise_params(5001, D, r)
+    g, U, V, w = _pairwise_params(seed, D, r)
     val = torch.randn(B, N, D, generator=g).bfloat16()
     state = torch.randn(B, N, generator=g).bfloat16()
     X = val.to(dev).requires_grad_(True)
@@ -59,11 +62,11 @@ def test_bf16_propagation(dev, mode):
     w_hat = (w / w.norm()).to(dev)
     args = ("low_rank_bilinear", w_hat, None, V.to(dev), None, U.to(dev), None, "softsign", X, ps, X)
     if mode == "topk":
-        ds, dv, idx, score = jn.propagation_topk_selection(*args, 8, N, N)
+        ds, dv, idx, score = jn.propagation_topk_selection(*args, k, N, N)
         scores, tol = bf16_select_scores(_np(val) @ _np(U).T, _np(val) @ _np(V).T, _np(w_hat))
-        assert check_selection(idx.cpu().numpy(), score.cpu().numpy(), scores, 8, gap=2 * tol, score_tol=tol) > 0.5
+        assert check_selection(idx.cpu().numpy(), score.cpu().numpy(), scores, k, gap=2 * tol, score_tol=tol) > 0.5
         mask = O.mask_from_indices(idx.cpu().numpy(), N)
-        kw = dict(mode="topk", topk=8, mask=mask)
+        kw = dict(mode="topk", topk=k, mask=mask)
     elif mode == "window":
         ds, dv = jn.propagation_window(*args, 16, N, N)
         kw = dict(mode="window", window=16)

@@ -18,6 +18,7 @@ import torch
 
 import jakal_oracle as O
 from parity import torch32_propagation
+import test_gpu_bf16 as TB
 import test_gpu_dense as TD
 import test_gpu_topk as TT
 import test_gpu_transition as TR
@@ -91,3 +92,11 @@ def test_causal_dense(dev, tile, compress):
     # full causal windows run the dense products with causal K ranges and skip
     # the score tiles above the diagonal (softsign epilogue), under both tiles
     TW.test_full_causal_window_runs_dense(dev, compress, True, 0)
+
+
+@pytest.mark.parametrize("mode", ["topk", "window"])
+def test_bf16_layers(dev, tile, mode):
+    # bf16 X in the projection (A), weight-gradient (B) and input-gradient (C)
+    # GEMMs; rank 16 splits the weight operands at a multiple of 16, so the
+    # 128 x 128 kernel takes all three uses when forced
+    TB.run_bf16_propagation(dev, mode, B=2, N=160, D=40, r=16, k=8, seed=5003)

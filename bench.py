@@ -431,25 +431,36 @@ class DenseC4:
         c = self.config
         return c["batch"] * c["nodes"] * c["nodes"]
 
+    def chunk_batch(self) -> int:
+        """Batch elements per launch of the N x N kernels: the library runs
+        dense propagation in batch chunks whose edge matrices fit
+        jakal_net_native.DENSE_EDGE_BYTES (the whole batch when it fits)."""
+        import jakal_net_native as jn
+
+        c = self.config
+        B, edge = c["batch"], 4 * c["nodes"] * c["nodes"]
+        return B if B * edge <= jn.DENSE_EDGE_BYTES else max(1, min(B, jn.DENSE_EDGE_BYTES // edge))
+
     def model(self, name):
         c = self.config
         B, N, D, r = (c[x] for x in ("batch", "nodes", "dim", "rank"))
+        Bc = self.chunk_batch()  # per launch of the N x N kernels
         dense = {
-            "gemm_f32_kernel<dense_scores>": 2.0 * B * N * N * r,
-            "gemm_f32_kernel<dense_aggregate>": 2.0 * B * N * N * D,
-            "gemm_f32_kernel<dense_edge_grad>": 2.0 * B * N * N * D,
-            "gemm_f32_kernel<dense_value_grad>": 2.0 * B * N * N * D,
-            "gemm_f32_kernel<dense_target_grad>": 2.0 * B * N * N * r,
-            "gemm_f32_kernel<dense_source_grad>": 2.0 * B * N * N * r,
+            "gemm_f32_kernel<dense_scores>": 2.0 * Bc * N * N * r,
+            "gemm_f32_kernel<dense_aggregate>": 2.0 * Bc * N * N * D,
+            "gemm_f32_kernel<dense_edge_grad>": 2.0 * Bc * N * N * D,
+            "gemm_f32_kernel<dense_value_grad>": 2.0 * Bc * N * N * D,
+            "gemm_f32_kernel<dense_target_grad>": 2.0 * Bc * N * N * r,
+            "gemm_f32_kernel<dense_source_grad>": 2.0 * Bc * N * N * r,
         }
         if name in dense:
             return "mfma", dense[name]
         if name.startswith("dense_compress_backward_kernel"):
-            return "hbm", 4.0 * 3 * B * N * N  # read G and E, write G_s
+            return "hbm", 4.0 * 3 * Bc * N * N  # read G and E, write G_s
         if name.startswith("dense_compress_kernel"):
-            return "hbm", 4.0 * 2 * B * N * N  # read S, write E
+            return "hbm", 4.0 * 2 * Bc * N * N  # read S, write E
         if name.startswith("dense_colsum_kernel"):
-            return "hbm", 4.0 * B * N * N
+            return "hbm", 4.0 * Bc * N * N
         if name.startswith("gemm_f32_kernel"):
             return "mfma", 2.0 * B * N * D * 2 * r
         return None

@@ -30,7 +30,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 7. */
+/* ABI revision of this header (bumped on any signature change); this is 8. */
 int jn_abi_version(void);
 
 /*
@@ -264,6 +264,38 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
                                   float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
                                   float* grad_source_weight, float* grad_core_weight, float* grad_bias,
                                   void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+/*
+ * Dense propagation in batch chunks (same reference function and outputs as
+ * jn_propagation_dense_forward / _backward): the edge matrices of
+ * chunk_batch batch elements at a time live in a chunk buffer at the start of
+ * the forward's workspace (chunk_batch * N * N floats), which holds the last
+ * chunk's edges when the forward returns.  The backward takes that buffer as
+ * edge_chunk; chunk_resident != 0 says it still holds them (so the last
+ * chunk is not rebuilt), and every other chunk's edges are rebuilt in it from
+ * the saved projections exactly as the forward built them (a rank-r score
+ * product).  A softsign backward writes its score gradient over the buffer.
+ * The backward workspace (backward != 0 in the query) holds a score-gradient
+ * chunk for the signed kinds and the row partials and projection gradients.
+ */
+size_t jn_propagation_dense_chunked_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                                    int64_t rank, int32_t compress_kind, int64_t chunk_batch,
+                                                    int32_t backward);
+int jn_propagation_dense_forward_chunked(const float* layer_val, const float* projected_state,
+                                         const float* projected_val, const float* target_weight,
+                                         const float* source_weight, const float* core_weight, const float* bias,
+                                         int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                         int32_t compress_kind, int32_t causal, int64_t chunk_batch,
+                                         float* delta_state, float* delta_val, float* projections, void* workspace,
+                                         size_t workspace_bytes, jn_stream_t stream);
+int jn_propagation_dense_backward_chunked(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* bias, const float* projections,
+    float* edge_chunk, const float* grad_delta_state, const float* grad_delta_val, int64_t batch, int64_t nodes,
+    int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
+    int32_t projected_val_is_layer_val, int64_t chunk_batch, int32_t chunk_resident, float* grad_layer_val,
+    float* grad_projected_state, float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
 /*
  * SparseTransition with LowRankBilinearRoute (optionally temperature-scaled):

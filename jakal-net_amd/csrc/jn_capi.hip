@@ -215,7 +215,8 @@ int check_transition_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t Dsrc,
 }
 
 struct DenseScratch {
-  float* G;       // [B, N, N] score gradient (absent when it overwrites the edge matrix)
+  float* E;       // [g_batch... e_batch, N, N] recomputed edge matrix of a chunk (chunked backward)
+  float* G;       // [g_batch, N, N] score gradient (absent when it overwrites the edge matrix)
   float* dP;      // [M, 2r]
   float* rowsum;  // [M]
   float* part_c;  // [M, r]
@@ -224,11 +225,15 @@ struct DenseScratch {
   size_t bytes;
 };
 
-DenseScratch carve_dense(void* base, size_t size, int64_t B, int64_t N, int64_t Din, int64_t r, bool with_g) {
+// g_batch / e_batch: batch elements of the score-gradient / edge-matrix buffers
+// (0: none)
+DenseScratch carve_dense(void* base, size_t size, int64_t B, int64_t N, int64_t Din, int64_t r, int64_t g_batch,
+                         int64_t e_batch) {
   Workspace ws(base, size);
   DenseScratch s{};
   const int64_t M = B * N;
-  s.G = with_g ? ws.take<float>(B * N * N) : nullptr;
+  s.E = e_batch ? ws.take<float>(e_batch * N * N) : nullptr;
+  s.G = g_batch ? ws.take<float>(g_batch * N * N) : nullptr;
   s.dP = ws.take<float>(M * 2 * r);
   s.rowsum = ws.take<float>(M * dense_epi_parts((int)N));  // per-row totals, or the epilogue's block partials
   s.part_c = ws.take<float>(M * r);
@@ -277,6 +282,182 @@ TransitionDenseScratch carve_transition_dense(void* base, size_t size, int64_t B
   s.splitk = ws.take<float>(sk / sizeof(float));
   s.bytes = ws.used;
   return s;
+}
+
+// Dense propagation forward over batch elements [b0, b0 + nb) (propagation.py:
+// 207-220): the edge matrix E of those elements (batch stride N*N), then
+// delta_state = E ps and delta_val = E pv.  projections holds every batch
+// element's [N, 2r] projection rows.
+int dense_forward_range(const float* projected_state, const float* projected_val, const float* core_weight,
+                        const float* bias, int b0, int nb, int N, int D, int r, int compress_kind, bool causal,
+                        const float* projections, float* E, float* delta_state, float* delta_val, hipStream_t st) {
+  const int64_t pr = (int64_t)b0 * N;  // first row of the range
+  // S_b = (P_t diag(w_hat)) P_s^T
+  BatchedGemm sg{};
+  sg.A = projections + pr * 2 * r; sg.lda = 2 * r; sg.a_bs = (int64_t)N * 2 * r; sg.a_kcontig = true;
+  sg.B = projections + pr * 2 * r + r; sg.ldb = 2 * r; sg.b_bs = (int64_t)N * 2 * r; sg.b_kcontig = true;
+  sg.C = E; sg.ldc = N; sg.c_bs = (int64_t)N * N;
+  sg.a_kscale = core_weight;
+  sg.M = N; sg.N = N; sg.K = r; sg.batch = nb;
+  // Softsign runs in the GEMM's epilogue, whose per-block partials of
+  // delta_state are staged in delta_val's storage (the aggregate GEMM below
+  // overwrites it); the row-wise compressions run as a pass of their own.
+  const int parts = dense_epi_parts(N);
+  const bool fused = compress_kind == 0 && parts <= D;
+  if (fused) {
+    sg.epi = 1; sg.epi_causal = causal; sg.epi_bias = bias; sg.epi_ps = projected_state + pr;
+    sg.epi_part = delta_val + pr * D;
+  }
+  int rc = gemm_batched(sg, kGemmDenseScores, st);
+  if (rc) return rc;
+  // E = compress(S + b) (in place when not fused), delta_state = E ps
+  rc = fused ? launch_dense_part_rowsum(delta_val + pr * D, parts, (int64_t)nb * N, delta_state + pr, st)
+             : launch_dense_compress(E, bias, projected_state + pr, nb, N, compress_kind, causal, delta_state + pr,
+                                     st);
+  if (rc) return rc;
+  // delta_val_b = E_b pv_b
+  BatchedGemm ag{};
+  ag.A = E; ag.lda = N; ag.a_bs = (int64_t)N * N; ag.a_kcontig = true;
+  ag.B = projected_val + pr * D; ag.ldb = D; ag.b_bs = (int64_t)N * D; ag.b_kcontig = false;
+  ag.C = delta_val + pr * D; ag.ldc = D; ag.c_bs = (int64_t)N * D;
+  ag.M = N; ag.N = D; ag.K = N; ag.batch = nb;
+  ag.causal_k = causal ? kCausalKLower : kCausalKNone;  // row i reads sources j <= i
+  return gemm_batched(ag, kGemmDenseAggregate, st);
+}
+
+// Dense propagation backward, chunk_batch batch elements at a time.  E holds
+// the chunk's edge matrix (the whole saved matrix when chunk_batch covers
+// every batch element and recompute is false; otherwise it is rebuilt from
+// the projections for each chunk, exactly as the forward built it), G the
+// chunk's score gradient (G == E: written over the edges, softsign only).
+// Chunks run last to first; with last_resident E already holds the last
+// chunk's edges (the chunked forward leaves them there), which are not rebuilt.
+// Each chunk writes its own rows of every per-row output, so the order does
+// not change the results.
+int dense_backward(const float* layer_val, const float* projected_state, const float* projected_val,
+                   const float* target_weight, const float* source_weight, const float* core_weight, const float* bias,
+                   const float* projections, float* E, float* G, int chunk_batch, bool recompute, bool last_resident,
+                   const float* grad_delta_state, const float* grad_delta_val, int64_t batch, int64_t nodes,
+                   int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
+                   int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
+                   float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
+                   float* grad_core_weight, float* grad_bias, const DenseScratch& s, hipStream_t st) {
+  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
+                 projections && E && G && grad_delta_state && grad_delta_val,
+             kInvalidArgument, "null tensor pointer");
+  JN_REQUIRE(!projected_val_is_layer_val || in_dim == out_dim, kInvalidArgument,
+             "projected_val_is_layer_val requires in_dim == out_dim");
+  JN_REQUIRE(G != E || compress_kind == 0, kInvalidArgument, "only the softsign gradient overwrites the edges");
+  const int B = (int)batch, N = (int)nodes, r = (int)rank, D = (int)out_dim;
+  const int M = B * N;
+  const bool fused = compress_kind == 0;  // softsign's derivative in the score-gradient GEMM's epilogue
+  const int parts = dense_epi_parts(N);
+  const int lower = causal ? kCausalKLower : kCausalKNone;  // A(i, j) = 0 for j > i
+  const int upper = causal ? kCausalKUpper : kCausalKNone;  // A = E^T: A(j, i) = 0 for i < j
+  float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
+  int rc;
+  const int nchunks = (B + chunk_batch - 1) / chunk_batch;
+  for (int c = nchunks - 1; c >= 0; --c) {
+    const int b0 = c * chunk_batch;
+    const int nb = std::min(chunk_batch, B - b0);
+    const int64_t pr = (int64_t)b0 * N;
+    float* rowsum = s.rowsum + (fused ? pr * parts : pr);
+    if (recompute && !(last_resident && c == nchunks - 1)) {
+      // the forward's edges of this chunk; its state sums go to scratch that
+      // later steps overwrite (the row sums, or the scale partials)
+      BatchedGemm sg{};
+      sg.A = projections + pr * 2 * r; sg.lda = 2 * r; sg.a_bs = (int64_t)N * 2 * r; sg.a_kcontig = true;
+      sg.B = projections + pr * 2 * r + r; sg.ldb = 2 * r; sg.b_bs = (int64_t)N * 2 * r; sg.b_kcontig = true;
+      sg.C = E; sg.ldc = N; sg.c_bs = (int64_t)N * N;
+      sg.a_kscale = core_weight;
+      sg.M = N; sg.N = N; sg.K = r; sg.batch = nb;
+      if (fused) {
+        sg.epi = 1; sg.epi_causal = causal != 0; sg.epi_bias = bias; sg.epi_ps = projected_state + pr;
+        sg.epi_part = rowsum;
+      }
+      rc = gemm_batched(sg, kGemmDenseScores, st);
+      if (rc) return rc;
+      if (!fused) {
+        rc = launch_dense_compress(E, bias, projected_state + pr, nb, N, compress_kind, causal != 0,
+                                   s.part_c + pr * r, st);
+        if (rc) return rc;
+      }
+    }
+
+    // 1. value and state grads of the sources: E^T gdv, E^T gds (before E is overwritten)
+    if (gpv) {
+      BatchedGemm vg{};
+      vg.A = E; vg.lda = N; vg.a_bs = (int64_t)N * N; vg.a_kcontig = false;
+      vg.B = grad_delta_val + pr * D; vg.ldb = D; vg.b_bs = (int64_t)N * D; vg.b_kcontig = false;
+      vg.C = gpv + pr * D; vg.ldc = D; vg.c_bs = (int64_t)N * D;
+      vg.M = N; vg.N = D; vg.K = N; vg.batch = nb;
+      vg.causal_k = upper;
+      rc = gemm_batched(vg, kGemmDenseValueGrad, st);
+      if (rc) return rc;
+    }
+    if (grad_projected_state) {
+      rc = launch_dense_colsum(E, grad_delta_state + pr, nb, N, grad_projected_state + pr, st);
+      if (rc) return rc;
+    }
+
+    // 2. G_b = gdv_b pv_b^T, then the score gradient (+ row sums)
+    BatchedGemm gg{};
+    gg.A = grad_delta_val + pr * D; gg.lda = D; gg.a_bs = (int64_t)N * D; gg.a_kcontig = true;
+    gg.B = projected_val + pr * D; gg.ldb = D; gg.b_bs = (int64_t)N * D; gg.b_kcontig = true;
+    gg.C = G; gg.ldc = N; gg.c_bs = (int64_t)N * N;
+    gg.M = N; gg.N = N; gg.K = D; gg.batch = nb;
+    if (fused) {
+      gg.epi = 1; gg.epi_causal = causal != 0; gg.epi_ps = projected_state + pr; gg.epi_gds = grad_delta_state + pr;
+      gg.epi_E = E; gg.epi_part = rowsum;
+    }
+    rc = gemm_batched(gg, kGemmDenseEdgeGrad, st);
+    if (rc) return rc;
+    if (!fused) {
+      rc = launch_dense_compress_backward(G, E, grad_delta_state + pr, projected_state + pr, nb, N, compress_kind,
+                                          causal != 0, rowsum, st);
+      if (rc) return rc;
+    }
+
+    // 3. projection grads: dP_t = w_hat * (G_s P_s), dP_s = w_hat * (G_s^T P_t) (+ w_hat partials)
+    BatchedGemm tg{};
+    tg.A = G; tg.lda = N; tg.a_bs = (int64_t)N * N; tg.a_kcontig = true;
+    tg.B = projections + pr * 2 * r + r; tg.ldb = 2 * r; tg.b_bs = (int64_t)N * 2 * r; tg.b_kcontig = false;
+    tg.C = s.dP + pr * 2 * r; tg.ldc = 2 * r; tg.c_bs = (int64_t)N * 2 * r;
+    tg.c_nscale = core_weight;
+    tg.M = N; tg.N = r; tg.K = N; tg.batch = nb;
+    tg.causal_k = lower;
+    rc = gemm_batched(tg, kGemmDenseTargetGrad, st);
+    if (rc) return rc;
+    BatchedGemm sg2{};
+    sg2.A = G; sg2.lda = N; sg2.a_bs = (int64_t)N * N; sg2.a_kcontig = false;
+    sg2.B = projections + pr * 2 * r; sg2.ldb = 2 * r; sg2.b_bs = (int64_t)N * 2 * r; sg2.b_kcontig = false;
+    sg2.C = s.dP + pr * 2 * r + r; sg2.ldc = 2 * r; sg2.c_bs = (int64_t)N * 2 * r;
+    sg2.M = N; sg2.N = r; sg2.K = N; sg2.batch = nb;
+    sg2.causal_k = upper;
+    rc = gemm_batched(sg2, kGemmDenseSourceGrad, st);
+    if (rc) return rc;
+    rc = launch_scale_grad_partials(s.dP + pr * 2 * r + r, 2 * r, projections + pr * 2 * r + r, 2 * r, core_weight, r,
+                                    (int64_t)nb * N, s.part_c + pr * r, st);
+    if (rc) return rc;
+  }
+  const int64_t n_rowsum = fused ? (int64_t)M * parts : M;
+
+  // 4. projection weight and input grads
+  if (grad_target_weight && grad_source_weight) {
+    rc = gemm_grad_weight(s.dP, 2 * r, layer_val, in_dim, grad_target_weight, grad_source_weight, r, 2 * r,
+                          (int)in_dim, M, s.splitk, st);
+    if (rc) return rc;
+  }
+  if (grad_layer_val) {
+    const float* addend = (projected_val_is_layer_val && gpv) ? grad_layer_val : nullptr;
+    rc = gemm_grad_input(s.dP, 2 * r, target_weight, source_weight, r, in_dim, addend, in_dim, grad_layer_val,
+                         in_dim, M, (int)in_dim, 2 * r, st);
+    if (rc) return rc;
+  }
+
+  // 5. w_hat and bias grads
+  return launch_finalize_small_grads(s.part_c, M, r, grad_core_weight, 0, s.rowsum, n_rowsum, grad_bias, s.stage,
+                                     st);
 }
 
 int check_transition_dense_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t Dsrc, int64_t Ddst, int64_t Dv,
@@ -663,7 +844,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 7; }
+int jn_abi_version(void) { return 8; }
 
 int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float eps, float* weight_hat,
                           jn_stream_t stream) {
@@ -1446,43 +1627,17 @@ int jn_propagation_dense_forward(const float* layer_val, const float* projected_
   rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, B * N, 2 * r,
                     (int)in_dim, st);
   if (rc) return rc;
-  // S_b = (P_t diag(w_hat)) P_s^T
-  BatchedGemm sg{};
-  sg.A = projections; sg.lda = 2 * r; sg.a_bs = (int64_t)N * 2 * r; sg.a_kcontig = true;
-  sg.B = projections + r; sg.ldb = 2 * r; sg.b_bs = (int64_t)N * 2 * r; sg.b_kcontig = true;
-  sg.C = edges; sg.ldc = N; sg.c_bs = (int64_t)N * N;
-  sg.a_kscale = core_weight;
-  sg.M = N; sg.N = N; sg.K = r; sg.batch = B;
-  // Softsign runs in the GEMM's epilogue, whose per-block partials of
-  // delta_state are staged in delta_val's storage (the aggregate GEMM below
-  // overwrites it); the row-wise compressions run as a pass of their own.
-  const int parts = dense_epi_parts(N);
-  const bool fused = compress_kind == 0 && parts <= D;
-  if (fused) {
-    sg.epi = 1; sg.epi_causal = causal != 0; sg.epi_bias = bias; sg.epi_ps = projected_state;
-    sg.epi_part = delta_val;
-  }
-  rc = gemm_batched(sg, kGemmDenseScores, st);
-  if (rc) return rc;
-  // E = compress(S + b) (in place when not fused), delta_state = E ps
-  rc = fused ? launch_dense_part_rowsum(delta_val, parts, (int64_t)B * N, delta_state, st)
-             : launch_dense_compress(edges, bias, projected_state, B, N, compress_kind, causal != 0, delta_state, st);
-  if (rc) return rc;
-  // delta_val_b = E_b pv_b
-  BatchedGemm ag{};
-  ag.A = edges; ag.lda = N; ag.a_bs = (int64_t)N * N; ag.a_kcontig = true;
-  ag.B = projected_val; ag.ldb = D; ag.b_bs = (int64_t)N * D; ag.b_kcontig = false;
-  ag.C = delta_val; ag.ldc = D; ag.c_bs = (int64_t)N * D;
-  ag.M = N; ag.N = D; ag.K = N; ag.batch = B;
-  ag.causal_k = causal ? kCausalKLower : kCausalKNone;  // row i reads sources j <= i
-  return gemm_batched(ag, kGemmDenseAggregate, st);
+  return dense_forward_range(projected_state, projected_val, core_weight, bias, 0, B, N, D, r, compress_kind,
+                             causal != 0, projections, edges, delta_state, delta_val, st);
 }
 
 size_t jn_propagation_dense_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                             int64_t rank, int32_t compress_kind, int32_t reuse_edges) {
   (void)out_dim;
   if (batch < 1 || nodes < 1 || rank < 1) return 0;
-  return carve_dense(nullptr, 0, batch, nodes, in_dim, rank, !(compress_kind == 0 && reuse_edges != 0)).bytes;
+  return carve_dense(nullptr, 0, batch, nodes, in_dim, rank, !(compress_kind == 0 && reuse_edges != 0) ? batch : 0,
+                     0)
+      .bytes;
 }
 
 int jn_propagation_dense_backward(const float* layer_val, const float* projected_state, const float* projected_val,
@@ -1496,99 +1651,85 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
                                   void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
   if (rc) return rc;
-  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
-                 projections && edges && grad_delta_state && grad_delta_val,
-             kInvalidArgument, "null tensor pointer");
-  JN_REQUIRE(!projected_val_is_layer_val || in_dim == out_dim, kInvalidArgument,
-             "projected_val_is_layer_val requires in_dim == out_dim");
+  JN_REQUIRE(edges, kInvalidArgument, "null tensor pointer");
   // softsign's derivative runs in the score-gradient GEMM's epilogue, which
   // reads each edge once before writing its gradient: with reuse_edges that
   // gradient overwrites the edge matrix and no [B, N, N] workspace is needed
-  const bool fused = compress_kind == 0;
-  const bool in_place = fused && reuse_edges != 0;
-  DenseScratch s = carve_dense(workspace, workspace_bytes, batch, nodes, in_dim, rank, !in_place);
+  const bool in_place = compress_kind == 0 && reuse_edges != 0;
+  DenseScratch s = carve_dense(workspace, workspace_bytes, batch, nodes, in_dim, rank, in_place ? 0 : batch, 0);
   JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
              "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dense_backward(layer_val, projected_state, projected_val, target_weight, source_weight, core_weight, nullptr,
+                        projections, edges, in_place ? edges : s.G, (int)batch, false, false, grad_delta_state,
+                        grad_delta_val, batch, nodes, in_dim, out_dim, rank, compress_kind, causal,
+                        projected_val_is_layer_val, grad_layer_val, grad_projected_state, grad_projected_val,
+                        grad_target_weight, grad_source_weight, grad_core_weight, grad_bias, s,
+                        static_cast<hipStream_t>(stream));
+}
+
+size_t jn_propagation_dense_chunked_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                                    int64_t rank, int32_t compress_kind, int64_t chunk_batch,
+                                                    int32_t backward) {
+  (void)out_dim;
+  if (batch < 1 || nodes < 1 || rank < 1 || chunk_batch < 1) return 0;
+  const int64_t cb = chunk_batch < batch ? chunk_batch : batch;
+  if (!backward) return (size_t)cb * nodes * nodes * sizeof(float) + 256;
+  return carve_dense(nullptr, 0, batch, nodes, in_dim, rank, compress_kind == 0 ? 0 : cb, 0).bytes;
+}
+
+int jn_propagation_dense_forward_chunked(const float* layer_val, const float* projected_state,
+                                         const float* projected_val, const float* target_weight,
+                                         const float* source_weight, const float* core_weight, const float* bias,
+                                         int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                         int32_t compress_kind, int32_t causal, int64_t chunk_batch,
+                                         float* delta_state, float* delta_val, float* projections, void* workspace,
+                                         size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
+  if (rc) return rc;
+  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
+                 delta_state && delta_val && projections,
+             kInvalidArgument, "null tensor pointer");
+  JN_REQUIRE(chunk_batch >= 1, kInvalidArgument, "chunk_batch must be positive");
   const int B = (int)batch, N = (int)nodes, r = (int)rank, D = (int)out_dim;
-  const int M = B * N;
-  float* G = in_place ? edges : s.G;
-  const int lower = causal ? kCausalKLower : kCausalKNone;  // A(i, j) = 0 for j > i
-  const int upper = causal ? kCausalKUpper : kCausalKNone;  // A = E^T: A(j, i) = 0 for i < j
-
-  // 1. value and state grads of the sources: E^T gdv, E^T gds (before E is overwritten)
-  float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
-  if (gpv) {
-    BatchedGemm vg{};
-    vg.A = edges; vg.lda = N; vg.a_bs = (int64_t)N * N; vg.a_kcontig = false;
-    vg.B = grad_delta_val; vg.ldb = D; vg.b_bs = (int64_t)N * D; vg.b_kcontig = false;
-    vg.C = gpv; vg.ldc = D; vg.c_bs = (int64_t)N * D;
-    vg.M = N; vg.N = D; vg.K = N; vg.batch = B;
-    vg.causal_k = upper;
-    rc = gemm_batched(vg, kGemmDenseValueGrad, st);
-    if (rc) return rc;
-  }
-  if (grad_projected_state) {
-    rc = launch_dense_colsum(edges, grad_delta_state, B, N, grad_projected_state, st);
-    if (rc) return rc;
-  }
-
-  // 2. G_b = gdv_b pv_b^T, then the score gradient (+ row sums)
-  BatchedGemm gg{};
-  gg.A = grad_delta_val; gg.lda = D; gg.a_bs = (int64_t)N * D; gg.a_kcontig = true;
-  gg.B = projected_val; gg.ldb = D; gg.b_bs = (int64_t)N * D; gg.b_kcontig = true;
-  gg.C = G; gg.ldc = N; gg.c_bs = (int64_t)N * N;
-  gg.M = N; gg.N = N; gg.K = D; gg.batch = B;
-  if (fused) {
-    gg.epi = 1; gg.epi_causal = causal != 0; gg.epi_ps = projected_state; gg.epi_gds = grad_delta_state;
-    gg.epi_E = edges; gg.epi_part = s.rowsum;
-  }
-  rc = gemm_batched(gg, kGemmDenseEdgeGrad, st);
+  const int cb = (int)(chunk_batch < batch ? chunk_batch : batch);
+  Workspace ws(workspace, workspace_bytes);
+  float* E = ws.take<float>((int64_t)cb * N * N);
+  JN_REQUIRE(workspace != nullptr && ws.used <= workspace_bytes, kWorkspaceTooSmall,
+             "workspace too small: need %zu bytes, got %zu", ws.used, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, B * N, 2 * r,
+                    (int)in_dim, st);
   if (rc) return rc;
-  if (!fused) {
-    rc = launch_dense_compress_backward(G, edges, grad_delta_state, projected_state, B, N, compress_kind,
-                                        causal != 0, s.rowsum, st);
+  for (int b0 = 0; b0 < B; b0 += cb) {
+    rc = dense_forward_range(projected_state, projected_val, core_weight, bias, b0, std::min(cb, B - b0), N, D, r,
+                             compress_kind, causal != 0, projections, E, delta_state, delta_val, st);
     if (rc) return rc;
   }
-  const int64_t n_rowsum = fused ? (int64_t)M * dense_epi_parts(N) : M;
+  return kOk;
+}
 
-  // 3. projection grads: dP_t = w_hat * (G_s P_s), dP_s = w_hat * (G_s^T P_t) (+ w_hat partials)
-  BatchedGemm tg{};
-  tg.A = G; tg.lda = N; tg.a_bs = (int64_t)N * N; tg.a_kcontig = true;
-  tg.B = projections + r; tg.ldb = 2 * r; tg.b_bs = (int64_t)N * 2 * r; tg.b_kcontig = false;
-  tg.C = s.dP; tg.ldc = 2 * r; tg.c_bs = (int64_t)N * 2 * r;
-  tg.c_nscale = core_weight;
-  tg.M = N; tg.N = r; tg.K = N; tg.batch = B;
-  tg.causal_k = lower;
-  rc = gemm_batched(tg, kGemmDenseTargetGrad, st);
+int jn_propagation_dense_backward_chunked(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* bias, const float* projections,
+    float* edge_chunk, const float* grad_delta_state, const float* grad_delta_val, int64_t batch, int64_t nodes,
+    int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
+    int32_t projected_val_is_layer_val, int64_t chunk_batch, int32_t chunk_resident, float* grad_layer_val,
+    float* grad_projected_state, float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
   if (rc) return rc;
-  BatchedGemm sg2{};
-  sg2.A = G; sg2.lda = N; sg2.a_bs = (int64_t)N * N; sg2.a_kcontig = false;
-  sg2.B = projections; sg2.ldb = 2 * r; sg2.b_bs = (int64_t)N * 2 * r; sg2.b_kcontig = false;
-  sg2.C = s.dP + r; sg2.ldc = 2 * r; sg2.c_bs = (int64_t)N * 2 * r;
-  sg2.M = N; sg2.N = r; sg2.K = N; sg2.batch = B;
-  sg2.causal_k = upper;
-  rc = gemm_batched(sg2, kGemmDenseSourceGrad, st);
-  if (rc) return rc;
-  rc = launch_scale_grad_partials(s.dP + r, 2 * r, projections + r, 2 * r, core_weight, r, M, s.part_c, st);
-  if (rc) return rc;
-
-  // 4. projection weight and input grads
-  if (grad_target_weight && grad_source_weight) {
-    rc = gemm_grad_weight(s.dP, 2 * r, layer_val, in_dim, grad_target_weight, grad_source_weight, r, 2 * r,
-                          (int)in_dim, M, s.splitk, st);
-    if (rc) return rc;
-  }
-  if (grad_layer_val) {
-    const float* addend = (projected_val_is_layer_val && gpv) ? grad_layer_val : nullptr;
-    rc = gemm_grad_input(s.dP, 2 * r, target_weight, source_weight, r, in_dim, addend, in_dim, grad_layer_val,
-                         in_dim, M, (int)in_dim, 2 * r, st);
-    if (rc) return rc;
-  }
-
-  // 5. w_hat and bias grads
-  return launch_finalize_small_grads(s.part_c, M, r, grad_core_weight, 0, s.rowsum, n_rowsum, grad_bias, s.stage,
-                                     st);
+  JN_REQUIRE(chunk_batch >= 1, kInvalidArgument, "chunk_batch must be positive");
+  JN_REQUIRE(edge_chunk, kInvalidArgument, "null tensor pointer");
+  const int cb = (int)(chunk_batch < batch ? chunk_batch : batch);
+  DenseScratch s = carve_dense(workspace, workspace_bytes, batch, nodes, in_dim, rank, compress_kind == 0 ? 0 : cb, 0);
+  JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
+             "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
+  return dense_backward(layer_val, projected_state, projected_val, target_weight, source_weight, core_weight, bias,
+                        projections, edge_chunk, compress_kind == 0 ? edge_chunk : s.G, cb, true, chunk_resident != 0,
+                        grad_delta_state, grad_delta_val,
+                        batch, nodes, in_dim, out_dim, rank, compress_kind, causal, projected_val_is_layer_val,
+                        grad_layer_val, grad_projected_state, grad_projected_val, grad_target_weight,
+                        grad_source_weight, grad_core_weight, grad_bias, s, static_cast<hipStream_t>(stream));
 }
 
 int jn_transition_dense_forward(const float* sender_strength, const float* src_val, const float* dst_val,

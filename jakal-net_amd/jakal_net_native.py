@@ -109,6 +109,16 @@ _declare(
     [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P, _P],
 )
 _declare("jn_propagation_dense_workspace_bytes", [_I64] * 5 + [_I32, _I32], _SZ)
+_declare("jn_propagation_dense_chunked_workspace_bytes", [_I64] * 5 + [_I32, _I64, _I32], _SZ)
+_declare(
+    "jn_propagation_dense_forward_chunked",
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I64, _P, _P, _P, _P, _SZ, _P],
+)
+_declare(
+    "jn_propagation_dense_backward_chunked",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I64, _I32,
+     _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
 _declare(
     "jn_propagation_dense_backward",
     [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32,
@@ -466,10 +476,23 @@ def _bf16(t: Tensor | None) -> Tensor | None:
     return None if t is None else t.contiguous()
 
 
+DENSE_EDGE_BYTES = 512 << 20  # edge-matrix bytes above which dense propagation runs in batch chunks
+
+
+def set_dense_edge_bytes(limit: int = 512 << 20) -> None:
+    """Edge-matrix bytes (B * N * N * 4) up to which dense propagation keeps the
+    whole edge matrix from forward to backward; above it the forward and
+    backward run chunks of batch elements whose edge matrices fit the limit,
+    and the backward rebuilds each chunk's edges from the saved projections."""
+    global DENSE_EDGE_BYTES
+    DENSE_EDGE_BYTES = int(limit)
+
+
 class _PropagationDense(torch.autograd.Function):
-    """Differentiable dense low-rank propagation on the HIP library (edge
-    matrix materialised).  Inputs as _PropagationEdges; causal keeps only
-    sources j <= i in row i."""
+    """Differentiable dense low-rank propagation on the HIP library.  Inputs as
+    _PropagationEdges; causal keeps only sources j <= i in row i.  Small
+    problems keep the edge matrix for the backward; larger ones run in batch
+    chunks of at most DENSE_EDGE_BYTES of edges and rebuild them."""
 
     @staticmethod
     def forward(ctx, X, ps, pv, V, U, w_hat, bias, compress: int, causal: bool = False):  # noqa: N803
@@ -479,27 +502,44 @@ class _PropagationDense(torch.autograd.Function):
         Dout = pv_t.shape[-1]
         r = U.shape[0]
         dev = X.device
+        edge_bytes = N * N * 4
+        chunk = B if B * edge_bytes <= DENSE_EDGE_BYTES else max(1, DENSE_EDGE_BYTES // edge_bytes)
         with torch.cuda.device(dev):
             ds = torch.empty(B, N, device=dev, dtype=torch.float32)
             dv = torch.empty(B, N, Dout, device=dev, dtype=torch.float32)
             proj = torch.empty(B * N, 2 * r, device=dev, dtype=torch.float32)
-            edges = torch.empty(B, N, N, device=dev, dtype=torch.float32)
-            _check(
-                _LIB.jn_propagation_dense_forward(
-                    _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
-                    B, N, Din, Dout, r, compress, 1 if causal else 0, _ptr(ds), _ptr(dv), _ptr(proj), _ptr(edges),
-                    _stream(dev),
+            if chunk >= B:
+                edges = torch.empty(B, N, N, device=dev, dtype=torch.float32)
+                _check(
+                    _LIB.jn_propagation_dense_forward(
+                        _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
+                        B, N, Din, Dout, r, compress, 1 if causal else 0, _ptr(ds), _ptr(dv), _ptr(proj),
+                        _ptr(edges), _stream(dev),
+                    )
                 )
-            )
-        ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, edges)
-        ctx.meta = (compress, pv_is_x, bias is not None, bool(causal))
+            else:
+                # the forward's chunk buffer keeps the last chunk's edges for the backward
+                ws_bytes = int(_LIB.jn_propagation_dense_chunked_workspace_bytes(B, N, Din, Dout, r, compress,
+                                                                                 chunk, 0))
+                edges = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+                _check(
+                    _LIB.jn_propagation_dense_forward_chunked(
+                        _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
+                        B, N, Din, Dout, r, compress, 1 if causal else 0, chunk, _ptr(ds), _ptr(dv), _ptr(proj),
+                        _ptr(edges), ws_bytes, _stream(dev),
+                    )
+                )
+        ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, edges, bias)
+        ctx.meta = (compress, pv_is_x, bias is not None, bool(causal), chunk)
         ctx.edges_consumed = False
         return ds, dv
 
     @staticmethod
     def backward(ctx, g_ds, g_dv):
-        X, ps, pv, V, U, w_hat, proj, edges = ctx.saved_tensors
-        compress, pv_is_x, has_bias, causal = ctx.meta
+        X, ps, pv, V, U, w_hat, proj, edges, bias = ctx.saved_tensors
+        compress, pv_is_x, has_bias, causal, chunk = ctx.meta
+        if chunk < X.shape[0]:
+            return _PropagationDense._backward_chunked(ctx, X, ps, pv, V, U, w_hat, proj, edges, bias, g_ds, g_dv)
         # a softsign backward writes the score gradient over the saved edge
         # matrix (no [B, N, N] workspace); it can therefore run once per forward
         if ctx.edges_consumed:
@@ -528,6 +568,39 @@ class _PropagationDense(torch.autograd.Function):
                     _ptr(g_ds), _ptr(g_dv), B, N, Din, Dout, r, compress, 1 if causal else 0, 1 if pv_is_x else 0,
                     reuse, _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
                     _ptr(ws), ws_bytes, _stream(dev),
+                )
+            )
+        return (gX, gps, gpv, gV if need[3] else None, gU if need[4] else None, gw if need[5] else None,
+                gb if (has_bias and need[6]) else None, None, None)
+
+    @staticmethod
+    def _backward_chunked(ctx, X, ps, pv, V, U, w_hat, proj, edge_chunk, bias, g_ds, g_dv):
+        compress, pv_is_x, has_bias, causal, chunk = ctx.meta
+        # the chunk buffer holds the forward's last chunk until a softsign
+        # backward writes its gradient there; a later backward rebuilds it too
+        resident = 0 if ctx.edges_consumed else 1
+        ctx.edges_consumed = ctx.edges_consumed or compress == 0
+        B, N, Din = X.shape
+        Dout = pv.shape[-1]
+        r = U.shape[0]
+        dev = X.device
+        need = ctx.needs_input_grad
+        with torch.cuda.device(dev):
+            g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
+            g_dv = torch.zeros(B, N, Dout, device=dev) if g_dv is None else g_dv.float().contiguous()
+            gX = torch.empty_like(X) if need[0] else None
+            gps = torch.empty_like(ps) if need[1] else None
+            gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
+            gV, gU, gw = torch.empty_like(V), torch.empty_like(U), torch.empty_like(w_hat)
+            gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
+            ws_bytes = int(_LIB.jn_propagation_dense_chunked_workspace_bytes(B, N, Din, Dout, r, compress, chunk, 1))
+            ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            _check(
+                _LIB.jn_propagation_dense_backward_chunked(
+                    _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias), _ptr(proj),
+                    _ptr(edge_chunk), _ptr(g_ds), _ptr(g_dv), B, N, Din, Dout, r, compress, 1 if causal else 0,
+                    1 if pv_is_x else 0, chunk, resident, _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV),
+                    _ptr(gw), _ptr(gb), _ptr(ws), ws_bytes, _stream(dev),
                 )
             )
         return (gX, gps, gpv, gV if need[3] else None, gU if need[4] else None, gw if need[5] else None,

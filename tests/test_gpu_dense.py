@@ -171,3 +171,33 @@ def test_dense_medium_shape_backward(dev):
     t32 = torch32_propagation(dev, val, state, None, U, V, w_hat, None, np.ones((B, N, N), dtype=bool),
                               "signed_abs_softmax", gds, gdv)
     compare_propagation(gr, t32, ds, dv, X, ps, None, Ud, Vd, wd, None)
+
+
+@pytest.fixture
+def chunk_batches():
+    """Dense propagation in batch chunks: set the edge budget so that each chunk
+    holds `n` batch elements (the default budget keeps small problems whole)."""
+    import jakal_net_native as jn
+
+    def use(n, N):
+        jn.set_dense_edge_bytes(n * N * N * 4)
+
+    yield use
+    jn.set_dense_edge_bytes()
+
+
+@pytest.mark.parametrize("compress", ["softsign", "signed_abs_softmax", "signed_entmax15"])
+@pytest.mark.parametrize("separate_pv", [False, True])
+def test_dense_batch_chunks(dev, chunk_batches, compress, separate_pv):
+    """Chunks of 2 of 3 batch elements (a ragged last chunk): no edge matrix is
+    kept; the backward rebuilds each chunk's edges from the projections."""
+    chunk_batches(2, 64)
+    _check_dense(dev, compress, separate_pv, 64, True, B=3, D=24, r=6)
+
+
+@pytest.mark.parametrize("compress", ["softsign", "signed_entmax15"])
+def test_dense_batch_chunks_causal(dev, chunk_batches, compress):
+    import test_gpu_window as TW
+
+    chunk_batches(1, 200)
+    TW.test_full_causal_window_runs_dense(dev, compress, True, 0)

@@ -26,12 +26,13 @@ Inputs and parameters are resident in HBM before the timed region.
 
 Timing.  The step is first run `steps` times eagerly with the library's
 per-kernel HIP events on the launch stream (the kernel table and roofline).
-Then, for the operator workloads, it is captured once into a HIP graph
+Then it is captured once into a HIP graph
 (torch.cuda.CUDAGraph; the library only launches kernels, so the whole
 forward+backward captures) and `steps` back-to-back replays are timed:
 `value` and `ms_per_step` come from the replays, the eager figures are
-reported under `graph`.  --eager times the eager steps only; C5 (an optimizer
-step) always runs eager.
+reported under `graph`.  --eager times the eager steps only.  C5's step
+(forward, backward, AdamW) captures as a whole with AdamW's capturable state
+and an autocast without cast cache.
 
 Prints one JSON line:
   value        routed pairs per second (edges aggregated per step / step time)
@@ -635,7 +636,9 @@ class ProgressiveC5:
     def sparse_bytes(self):
         return None
 
-    def make_step(self, torch, dev, impl: str = "native", batch: int | None = None):
+    def make_step(self, torch, dev, impl: str = "native", batch: int | None = None, graph: bool = False):
+        """graph: the step will be captured into a HIP graph -- AdamW keeps its
+        step counts on the device (capturable) and autocast keeps no cast cache."""
         from jakal_net.progressive import ProgressiveBConfig, ProgressiveBStep
 
         c = self.config
@@ -645,7 +648,7 @@ class ProgressiveC5:
                                  compressed=c["compressed"], s_window=c["s_window"])
         torch.manual_seed(1005)
         model = ProgressiveBStep(cfg, implementation=impl).to(dev)
-        opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-4, capturable=graph)
         g = torch.Generator().manual_seed(1005)
         prefix = torch.randint(0, c["vocab"] - 1, (B, c["prefix"]), generator=g).to(dev)
         target = torch.randint(0, c["vocab"] - 1, (B, c["query"]), generator=g).to(dev)
@@ -653,7 +656,8 @@ class ProgressiveC5:
 
         def step() -> None:
             opt.zero_grad(set_to_none=True)
-            with torch.autocast(device_type=dev.type, dtype=torch.bfloat16, enabled=use_autocast):
+            with torch.autocast(device_type=dev.type, dtype=torch.bfloat16, enabled=use_autocast,
+                                cache_enabled=not graph):
                 loss = model(prefix, target)
             loss.backward()
             opt.step()
@@ -682,10 +686,10 @@ def capture_step(torch, step):
     return graph.replay
 
 
-def workload_step(wl, torch, dev, impl: str = "native", batch: int | None = None):
+def workload_step(wl, torch, dev, impl: str = "native", batch: int | None = None, graph: bool = False):
     """The timed step of a workload: its own make_step, or forward+backward of its operator."""
     if hasattr(wl, "make_step"):
-        return wl.make_step(torch, dev, impl, batch)
+        return wl.make_step(torch, dev, impl, batch, graph=graph)
     op, layer = wl.build(torch, dev, impl=impl, batch=batch)
     return _make_step(torch, op, layer)
 
@@ -739,8 +743,8 @@ def main() -> int:
     jn.set_select_mode(jn.SELECT_SPLIT_F16 if args.select_mode == "split-f16" else jn.SELECT_F32)
     wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
-    use_graph = not args.eager and not hasattr(wl, "make_step")  # C5's optimizer step runs eager
-    step = workload_step(wl, torch, dev)
+    use_graph = not args.eager
+    step = workload_step(wl, torch, dev, graph=use_graph)
 
     for _ in range(args.warmup):
         step()

@@ -25,6 +25,14 @@ from parity import check, np64
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import jakal_net_native  # noqa: F401  (fails loudly when the library is missing)
+
+    return torch.device("cuda:0")
+
+
 def _cfg():
     from jakal_net.progressive import ProgressiveBConfig
 
@@ -116,3 +124,57 @@ def test_progressive_step_bf16_autocast():
     assert err <= 2e-2 * scale
     want_loss = float(ref64(prefix, target).detach())
     assert abs(float(loss) - want_loss) <= 2e-2 * abs(want_loss)
+
+
+def test_progressive_step_graph_replay_matches_eager(dev):
+    """The whole training step (forward, backward, AdamW with capturable state,
+    bf16 autocast without its cast cache) captured into one HIP graph: from the
+    same parameters and optimizer state, every replay gives the eager step's
+    loss and updated parameters bit for bit, with other eager GPU work between
+    replays."""
+    cfg, model, prefix, target = _models_and_batch(seed=31)
+    model = model.to(dev)
+    prefix, target = prefix.to(dev), target.to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, capturable=True)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16, cache_enabled=False):
+            loss = model(prefix, target)
+        loss.backward()
+        opt.step()
+        return loss
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    tensors = [p.data for p in model.parameters()]
+    for st in opt.state.values():
+        tensors += [v for v in st.values() if torch.is_tensor(v)]
+    snapshot = [t.clone() for t in tensors]
+
+    def restore():
+        for t, s in zip(tensors, snapshot):
+            t.copy_(s)
+        torch.cuda.synchronize()
+
+    want_loss = step().detach().clone()
+    want = [p.data.clone() for p in model.parameters()]
+    restore()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        loss = step()
+    for rep in range(3):
+        restore()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(loss, want_loss), f"replay {rep}: loss {float(loss)} != {float(want_loss)}"
+        for (name, p), w in zip(model.named_parameters(), want):
+            assert torch.equal(p.data, w), f"replay {rep}: {name} differs by {float((p.data - w).abs().max()):.3e}"
+        torch.randn(1 << 20, device=dev).sum()  # other eager work between replays
+        torch.cuda.synchronize()

@@ -89,8 +89,8 @@ int check_edge_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_
 
 int check_propagation_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
                              int64_t topk, int32_t compress_kind) {
-  JN_REQUIRE(topk >= 1 && topk <= kSelectMaxK, kUnsupported, "topk must be in [1, %d] (got %lld)", kSelectMaxK,
-             (long long)topk);
+  JN_REQUIRE(topk >= 1 && topk <= kSelectLargeMaxK, kUnsupported, "topk must be in [1, %d] (got %lld)",
+             kSelectLargeMaxK, (long long)topk);
   JN_REQUIRE(topk < nodes, kInvalidArgument, "topk (%lld) must be smaller than nodes (%lld); k == N is dense",
              (long long)topk, (long long)nodes);
   return check_edge_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);

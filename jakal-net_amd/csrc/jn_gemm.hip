@@ -400,8 +400,9 @@ constexpr GemmUseInfo kGemmUses[] = {
     {true, true, false, true, "gemm_f32_kernel<project_bf16>"},
     {true, false, false, true, "gemm_f32_kernel<grad_input_bf16>"},
     {false, false, false, false, "gemm_f32_kernel<grad_weight_bf16>"},
+    {true, true, true, false, "gemm_f32_kernel<select_scores>"},
 };
-static_assert(sizeof(kGemmUses) / sizeof(kGemmUses[0]) == kGemmGradWeightBf16 + 1, "one entry per GemmUse");
+static_assert(sizeof(kGemmUses) / sizeof(kGemmUses[0]) == kGemmSelectScores + 1, "one entry per GemmUse");
 constexpr bool gemm_use_bf16(GemmUse u) {
   return u == kGemmProjectBf16 || u == kGemmGradInputBf16 || u == kGemmGradWeightBf16;
 }
@@ -847,6 +848,7 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
     case kGemmProjectBf16: launch_use<kGemmProjectBf16>(g, fast, (int)zdim, stream); break;
     case kGemmGradInputBf16: launch_use<kGemmGradInputBf16>(g, fast, (int)zdim, stream); break;
     case kGemmGradWeightBf16: launch_use<kGemmGradWeightBf16>(g, fast, (int)zdim, stream); break;
+    case kGemmSelectScores: launch_use<kGemmSelectScores>(g, fast, (int)zdim, stream); break;
     default: JN_REQUIRE(false, kInvalidArgument, "unknown GEMM use %d", (int)use);
   }
   JN_LAUNCH_CHECK();
@@ -855,7 +857,8 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
 
 // Batched C_b = op(A_b) . op(B_b) for b < batch (see BatchedGemm).
 int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
-  JN_REQUIRE(use >= kGemmDenseScores && use <= kGemmRouteTargetGrad && m.a_kcontig == kGemmUses[use].a_kc &&
+  JN_REQUIRE(((use >= kGemmDenseScores && use <= kGemmRouteTargetGrad) || use == kGemmSelectScores) &&
+                 m.a_kcontig == kGemmUses[use].a_kc &&
                  m.b_kcontig == kGemmUses[use].b_kc,
              kInvalidArgument, "batched GEMM layout does not match its use");
   GemmArgs g{};

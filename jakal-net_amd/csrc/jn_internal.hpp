@@ -34,6 +34,11 @@ struct SelectArgs {
 };
 int launch_topk_select(const SelectArgs& a, hipStream_t stream);
 constexpr int kSelectMaxK = 64;
+// Selects beyond the register kernels' limits (k > kSelectMaxK or more than
+// 65,535 keys) score rows into the workspace with an fp32 MFMA GEMM and pick
+// each row's k best by radix select (jn_select_large.hip), up to this k.
+constexpr int kSelectLargeMaxK = 1024;
+int launch_topk_select_large(const SelectArgs& a, hipStream_t stream);
 // Score arithmetic of the select: kSelectSplitF16 (default) runs the score
 // tiles on fp16 MFMAs over two-term fp16 splits of the operands (about 22
 // significant bits per operand, fp32 accumulation); kSelectF32 runs them on
@@ -108,6 +113,7 @@ enum GemmUse {
   kGemmRouteLogits, kGemmRouteAggregate, kGemmRouteEdgeGrad, kGemmRouteValueGrad, kGemmRouteSourceGrad,
   kGemmRouteTargetGrad,
   kGemmProjectBf16, kGemmGradInputBf16, kGemmGradWeightBf16,
+  kGemmSelectScores,
 };
 int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream);
 // Workgroup tile of every later GEMM launch: 0 = chosen per call, 64 or 128 = forced.

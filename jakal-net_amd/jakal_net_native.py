@@ -173,7 +173,8 @@ _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
 # Limits of the library's kernels.  A call beyond one raises NotImplementedError
 # (a RuntimeError subclass) before anything is launched, so callers that have
 # another path for such shapes (implementation="kernel") can take it.
-MAX_TOPK = 64          # edges kept per row by the top-k select
+MAX_TOPK = 64          # edges per row of the register top-k select (multi-head scores, routes)
+MAX_TOPK_LARGE = 1024  # edges per row of a single-head propagation top-k (scored rows, radix select)
 MAX_RANK = 128         # low-rank score rank
 MAX_SELECT_KEYS = 65535  # keys a top-k select ranks per batch element
 MAX_ROW_COMPRESS_EDGES = 64  # edges per row of the row-normalising compressions on edge lists
@@ -705,11 +706,15 @@ def _check_rank(rank: int) -> None:
         raise NotImplementedError(f"the HIP library scores ranks up to {MAX_RANK} (got {rank}).")
 
 
-def _check_select(k: int, keys: int) -> None:
-    """A top-k select of k of `keys` candidates per row."""
-    if k > MAX_TOPK:
-        raise NotImplementedError(f"the HIP top-k select keeps up to {MAX_TOPK} edges per row (got {k}).")
-    if keys > MAX_SELECT_KEYS:
+def _check_select(k: int, keys: int, large: bool = False) -> None:
+    """A top-k select of k of `keys` candidates per row.  large: the library may
+    take the scored-rows select, which keeps up to MAX_TOPK_LARGE edges of any
+    number of keys (single-head propagation); otherwise the register select's
+    limits apply."""
+    limit = MAX_TOPK_LARGE if large else MAX_TOPK
+    if k > limit:
+        raise NotImplementedError(f"the HIP top-k select keeps up to {limit} edges per row (got {k}).")
+    if keys > MAX_SELECT_KEYS and not large:
         raise NotImplementedError(f"the HIP top-k select ranks up to {MAX_SELECT_KEYS} keys per row (got {keys}).")
 
 
@@ -726,6 +731,8 @@ def _propagation_edges(mode, pairwise_kind, weight, bias, in_weight, in_bias, ou
                                                       out_bias)
     if mode == "topk":
         _check_select_heads(U.shape[0] // heads, heads)
+        if heads > 1:
+            _check_select(param, layer_val.shape[-2])
     if edge_compress_name not in _COMPRESS_KINDS:
         raise RuntimeError(f"Unsupported edge_compress_name for the HIP backend: {edge_compress_name!r}.")
     if target_block_size <= 0 or source_block_size <= 0:
@@ -781,7 +788,7 @@ def propagation_topk_selection(
     if k == N:
         raise NotImplementedError("top-k with k == N keeps every source: that is dense propagation "
                                   "(propagation_dense, or propagation_topk, which routes it there).")
-    _check_select(k, N)
+    _check_select(k, N, large=True)
     _check_row_compress(edge_compress_name, k)
     return _propagation_edges("topk", pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
                               edge_compress_name, layer_val, projected_state, projected_val, k, target_block_size,

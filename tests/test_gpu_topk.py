@@ -234,3 +234,46 @@ def test_c4_shape_select_every_row(dev):
     print(f"C4 select, all rows: max |score - torch score| {worst_val:.2e}, max excluded-over-kth {worst_gap:.2e}")
     assert worst_val <= 1e-6
     assert worst_gap <= 1e-5
+
+
+@pytest.mark.parametrize("r,k,Nq,Nk", [(16, 100, 70, 500), (8, 1024, 20, 1500), (64, 65, 130, 4096),
+                                       (5, 700, 33, 701), (8, 16, 40, 70000)])
+def test_select_beyond_register_limits(dev, r, k, Nq, Nk):
+    """k above 64 or more than 65,535 keys: scored rows (fp32 MFMA GEMM) and a
+    radix select per row, with the register select's ordering and tie rule;
+    reported scores within fp32 accumulation error of the exact ones."""
+    import jakal_net_native as jn
+
+    g = torch.Generator().manual_seed(300 + r + k)
+    B = 2
+    q = torch.randn(B, Nq, r, generator=g)
+    key = torch.randn(B, Nk, r, generator=g)
+    scale = torch.rand(r, generator=g) + 0.5
+    bias = torch.tensor(-0.5)
+    for scale_on_query, temp in ((False, 1.0), (True, 0.8)):
+        idx, score = jn.low_rank_topk_select(q.to(dev), key.to(dev), scale.to(dev), bias.to(dev),
+                                             scale_on_query, temp, k)
+        sq = q.double().numpy() * (scale.double().numpy() if scale_on_query else 1.0)
+        sk = key.double().numpy() * (1.0 if scale_on_query else scale.double().numpy())
+        ref = (sq @ np.swapaxes(sk, 1, 2) - 0.5) / temp
+        tol = r * 2.0 ** -24 * (np.abs(sq) @ np.swapaxes(np.abs(sk), 1, 2)).max(-1) / temp
+        frac = check_selection(idx.cpu().numpy(), score.cpu().numpy(), ref, k, gap=2 * tol + 1e-5, score_tol=tol)
+        assert frac > 0.5
+
+
+@pytest.mark.parametrize("Nk,k", [(300, 100), (70000, 7)])
+def test_large_select_ties_go_to_lower_index(dev, Nk, k):
+    import jakal_net_native as jn
+
+    B, Nq, r = 1, 16, 8
+    q = torch.randn(B, Nq, r)
+    key = torch.ones(B, Nk, r)
+    idx, _ = jn.low_rank_topk_select(q.to(dev), key.to(dev), None, None, False, 1.0, k)
+    assert (idx.cpu() == torch.arange(k, dtype=torch.int32)).all()
+
+
+@pytest.mark.parametrize("k", [65, 200])
+def test_propagation_topk_large_k(dev, k):
+    """Top-k propagation beyond 64 edges per row (softsign), forward and
+    backward against the oracle on the GPU's selection."""
+    _run_topk(dev, _c1_inputs(seed=1200 + k, B=2, N=400, D=48, r=16), "softsign", True, k, min_checkable=0.3)

@@ -47,9 +47,12 @@ int jn_profile_collect(char* buffer, size_t size);
  * GEMM tiling control (no counterpart in the reference; for tests and tuning).
  * tile = 64 or 128 forces that square workgroup tile on every later dense
  * product (projections, their gradients, the dense-mode score, aggregation and
- * gradient products); 0 (the default) picks per call: 128 when both output
- * extents are >= 128 and the grid still has >= 256 workgroups, else 64.
- * Process-wide; results are the same up to fp32 summation order.
+ * gradient products); 32 forces the 32 x 32 tile on the projection products
+ * and their gradients (64 elsewhere); 0 (the default) picks per call: 128 when
+ * both output extents are >= 128 and the grid still has >= 256 workgroups,
+ * else 64, or 32 for the projection products when a 64 x 64 grid has fewer
+ * than 256 workgroups.  Process-wide; results are the same up to fp32
+ * summation order.
  */
 int jn_set_gemm_tile(int32_t tile);
 

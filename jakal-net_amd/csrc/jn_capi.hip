@@ -869,8 +869,8 @@ int jn_profile_enable(int32_t on) {
 }
 
 int jn_set_gemm_tile(int32_t tile) {
-  JN_REQUIRE(tile == 0 || tile == 64 || tile == 128, kInvalidArgument, "GEMM tile must be 0, 64 or 128, got %d",
-             (int)tile);
+  JN_REQUIRE(tile == 0 || tile == 32 || tile == 64 || tile == 128, kInvalidArgument,
+             "GEMM tile must be 0, 32, 64 or 128, got %d", (int)tile);
   jakal::set_gemm_tile(tile);
   return kOk;
 }

@@ -151,8 +151,10 @@ __device__ __forceinline__ bool aligned16(const float* p) { return (reinterpret_
 // traffic per use.
 template <bool A_KC, bool B_KC, int USE, int TILE>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
-  constexpr int LPT = TILE / 64;   // float4 loads per thread per operand and K slice
-  constexpr int MT = TILE / 32;    // 16x16 tiles per wave along M (and N)
+  constexpr int NF4 = TILE * kGBK / 4;        // float4s per operand and K slice
+  constexpr int LPT = (NF4 + 255) / 256;      // of them per thread (TILE 32: threads 0..127 load one)
+  constexpr int MT = TILE / 32;               // 16x16 tiles per wave along M (and N)
+  static_assert(TILE == 32 || TILE == 64, "generic GEMM tiles are 32 or 64");
   constexpr bool A_BF = USE == kGemmProjectBf16;     // A (k-contiguous) holds bf16
   constexpr bool B_BF = USE == kGemmGradWeightBf16;  // B (k-major) holds bf16
   constexpr bool C_BF = USE == kGemmGradInputBf16;   // C and the addend hold bf16
@@ -189,6 +191,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
       const int e = tid + 256 * u;
+      if (NF4 % 256 != 0 && e >= NF4) continue;
       // ---- A ----
       if constexpr (A_BF) {
         const int m = m0 + e / 4, kq = k0 + (e % 4) * 4;
@@ -274,6 +277,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
       const int e = tid + 256 * u;
+      if (NF4 % 256 != 0 && e >= NF4) continue;
       if (A_KC) {
         *reinterpret_cast<float4*>(&sA[buf][(e / 4) * kGStride + (e % 4) * 4]) =
             make_float4(ra[u][0], ra[u][1], ra[u][2], ra[u][3]);
@@ -777,9 +781,24 @@ constexpr int kFastBK = 16;
 static bool f4_aligned(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 
+// The projection uses (and their gradients) on the 32 x 32 tile when a 64 x 64
+// grid would leave most CUs idle (small row counts: transitions, C5's slot
+// layers); other uses keep 64 x 64 there.
+constexpr bool gemm_use_small_tile(int use) {
+  return use == kGemmProject || use == kGemmGradInput || use == kGemmGradWeight || use == kGemmProjectBf16 ||
+         use == kGemmGradInputBf16 || use == kGemmGradWeightBf16;
+}
+
 template <int USE>
-static void launch_use(const GemmArgs& g, bool fast, int zdim, hipStream_t stream) {
+static void launch_use(const GemmArgs& g, bool fast, bool small, int zdim, hipStream_t stream) {
   constexpr GemmUseInfo u = kGemmUses[USE];
+  if constexpr (gemm_use_small_tile(USE)) {
+    if (small) {
+      dim3 grid((g.N + 31) / 32, (g.M + 31) / 32, zdim);
+      hipLaunchKernelGGL((gemm_f32_kernel<u.a_kc, u.b_kc, USE, 32>), grid, dim3(256), 0, stream, g);
+      return;
+    }
+  }
   if (fast) {
     const int tm = (g.M + kFT - 1) / kFT, tn = (g.N + kFT - 1) / kFT;
     const bool vec = g.N % 4 == 0 && g.ldc % 4 == 0 && g.c_bs % 4 == 0 && g.c_split_stride % 4 == 0 &&
@@ -828,27 +847,32 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
   // (the 128 x 128 kernel applies the k scale of a scaled use unconditionally)
   const bool fast = big && tiles128 < (1LL << 31) && fast_path_ok(g, info.a_kc, info.b_kc) &&
                     (!info.a_kscale || g.a_kscale != nullptr);
+  // 32 x 32 tiles for the projection uses when a 64 x 64 grid would not reach
+  // one workgroup per CU
+  const int64_t tiles64 = (int64_t)((g.M + kGBM - 1) / kGBM) * ((g.N + kGBM - 1) / kGBM) * zdim;
+  const bool small = !fast && gemm_use_small_tile(use) && (g.M + 31) / 32 < 65536 &&
+                     (forced ? forced == 32 : tiles64 < 256);
   JN_PROFILE(info.name, stream);
   switch (use) {
-    case kGemmProject: launch_use<kGemmProject>(g, fast, (int)zdim, stream); break;
-    case kGemmGradInput: launch_use<kGemmGradInput>(g, fast, (int)zdim, stream); break;
-    case kGemmGradWeight: launch_use<kGemmGradWeight>(g, fast, (int)zdim, stream); break;
-    case kGemmDenseScores: launch_use<kGemmDenseScores>(g, fast, (int)zdim, stream); break;
-    case kGemmDenseAggregate: launch_use<kGemmDenseAggregate>(g, fast, (int)zdim, stream); break;
-    case kGemmDenseEdgeGrad: launch_use<kGemmDenseEdgeGrad>(g, fast, (int)zdim, stream); break;
-    case kGemmDenseValueGrad: launch_use<kGemmDenseValueGrad>(g, fast, (int)zdim, stream); break;
-    case kGemmDenseTargetGrad: launch_use<kGemmDenseTargetGrad>(g, fast, (int)zdim, stream); break;
-    case kGemmDenseSourceGrad: launch_use<kGemmDenseSourceGrad>(g, fast, (int)zdim, stream); break;
-    case kGemmRouteLogits: launch_use<kGemmRouteLogits>(g, fast, (int)zdim, stream); break;
-    case kGemmRouteAggregate: launch_use<kGemmRouteAggregate>(g, fast, (int)zdim, stream); break;
-    case kGemmRouteEdgeGrad: launch_use<kGemmRouteEdgeGrad>(g, fast, (int)zdim, stream); break;
-    case kGemmRouteValueGrad: launch_use<kGemmRouteValueGrad>(g, fast, (int)zdim, stream); break;
-    case kGemmRouteSourceGrad: launch_use<kGemmRouteSourceGrad>(g, fast, (int)zdim, stream); break;
-    case kGemmRouteTargetGrad: launch_use<kGemmRouteTargetGrad>(g, fast, (int)zdim, stream); break;
-    case kGemmProjectBf16: launch_use<kGemmProjectBf16>(g, fast, (int)zdim, stream); break;
-    case kGemmGradInputBf16: launch_use<kGemmGradInputBf16>(g, fast, (int)zdim, stream); break;
-    case kGemmGradWeightBf16: launch_use<kGemmGradWeightBf16>(g, fast, (int)zdim, stream); break;
-    case kGemmSelectScores: launch_use<kGemmSelectScores>(g, fast, (int)zdim, stream); break;
+    case kGemmProject: launch_use<kGemmProject>(g, fast, small, (int)zdim, stream); break;
+    case kGemmGradInput: launch_use<kGemmGradInput>(g, fast, small, (int)zdim, stream); break;
+    case kGemmGradWeight: launch_use<kGemmGradWeight>(g, fast, small, (int)zdim, stream); break;
+    case kGemmDenseScores: launch_use<kGemmDenseScores>(g, fast, small, (int)zdim, stream); break;
+    case kGemmDenseAggregate: launch_use<kGemmDenseAggregate>(g, fast, small, (int)zdim, stream); break;
+    case kGemmDenseEdgeGrad: launch_use<kGemmDenseEdgeGrad>(g, fast, small, (int)zdim, stream); break;
+    case kGemmDenseValueGrad: launch_use<kGemmDenseValueGrad>(g, fast, small, (int)zdim, stream); break;
+    case kGemmDenseTargetGrad: launch_use<kGemmDenseTargetGrad>(g, fast, small, (int)zdim, stream); break;
+    case kGemmDenseSourceGrad: launch_use<kGemmDenseSourceGrad>(g, fast, small, (int)zdim, stream); break;
+    case kGemmRouteLogits: launch_use<kGemmRouteLogits>(g, fast, small, (int)zdim, stream); break;
+    case kGemmRouteAggregate: launch_use<kGemmRouteAggregate>(g, fast, small, (int)zdim, stream); break;
+    case kGemmRouteEdgeGrad: launch_use<kGemmRouteEdgeGrad>(g, fast, small, (int)zdim, stream); break;
+    case kGemmRouteValueGrad: launch_use<kGemmRouteValueGrad>(g, fast, small, (int)zdim, stream); break;
+    case kGemmRouteSourceGrad: launch_use<kGemmRouteSourceGrad>(g, fast, small, (int)zdim, stream); break;
+    case kGemmRouteTargetGrad: launch_use<kGemmRouteTargetGrad>(g, fast, small, (int)zdim, stream); break;
+    case kGemmProjectBf16: launch_use<kGemmProjectBf16>(g, fast, small, (int)zdim, stream); break;
+    case kGemmGradInputBf16: launch_use<kGemmGradInputBf16>(g, fast, small, (int)zdim, stream); break;
+    case kGemmGradWeightBf16: launch_use<kGemmGradWeightBf16>(g, fast, small, (int)zdim, stream); break;
+    case kGemmSelectScores: launch_use<kGemmSelectScores>(g, fast, small, (int)zdim, stream); break;
     default: JN_REQUIRE(false, kInvalidArgument, "unknown GEMM use %d", (int)use);
   }
   JN_LAUNCH_CHECK();

@@ -216,7 +216,8 @@ def profile_enable(on: bool = True) -> None:
 
 
 def set_gemm_tile(tile: int = 0) -> None:
-    """Force the GEMM workgroup tile (64 or 128) for later calls; 0 restores the per-call choice."""
+    """Force the GEMM workgroup tile (64 or 128; 32 on the projection products)
+    for later calls; 0 restores the per-call choice."""
     _check(_LIB.jn_set_gemm_tile(int(tile)))
 
 

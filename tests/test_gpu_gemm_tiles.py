@@ -1,10 +1,11 @@
-"""Both GEMM workgroup tiles (64 x 64 and 128 x 128) against the oracle.
+"""Every GEMM workgroup tile (32 x 32, 64 x 64 and 128 x 128) against the oracle.
 
 The library picks the tile per call from the output extents; these tests force
-each tile in turn (jn_set_gemm_tile) on ops whose extents are ragged against
-both tiles, so every GEMM of the forward and backward passes (projections,
+each tile in turn (jn_set_gemm_tile; 32 applies to the projection products and
+their gradients, 64 to the others) on ops whose extents are ragged against
+every tile, so every GEMM of the forward and backward passes (projections,
 their input and weight gradients, dense scores, aggregation and its
-gradients) runs partial tiles, unaligned rows and split-K under both tilings.
+gradients) runs partial tiles, unaligned rows and split-K under every tiling.
 The 128 x 128 kernel has preconditions (extents and strides in float4 units,
 B split at a multiple of 16); shapes that miss them run the 64 x 64 kernel
 even when 128 is forced, and are included too.
@@ -27,7 +28,7 @@ import test_gpu_window as TW
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=[64, 128])
+@pytest.fixture(params=[32, 64, 128])
 def tile(request):
     assert torch.cuda.is_available(), "GPU tests need a HIP device"
     import jakal_net_native as jn

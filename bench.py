@@ -648,7 +648,9 @@ class ProgressiveC5:
                                  compressed=c["compressed"], s_window=c["s_window"])
         torch.manual_seed(1005)
         model = ProgressiveBStep(cfg, implementation=impl).to(dev)
-        opt = torch.optim.AdamW(model.parameters(), lr=1e-4, capturable=graph)
+        # one fused update kernel per parameter group on the GPU (with device-side step counts)
+        fused = dev.type == "cuda"
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-4, capturable=graph, fused=fused)
         g = torch.Generator().manual_seed(1005)
         prefix = torch.randint(0, c["vocab"] - 1, (B, c["prefix"]), generator=g).to(dev)
         target = torch.randint(0, c["vocab"] - 1, (B, c["query"]), generator=g).to(dev)

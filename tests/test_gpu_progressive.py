@@ -126,16 +126,17 @@ def test_progressive_step_bf16_autocast():
     assert abs(float(loss) - want_loss) <= 2e-2 * abs(want_loss)
 
 
-def test_progressive_step_graph_replay_matches_eager(dev):
-    """The whole training step (forward, backward, AdamW with capturable state,
-    bf16 autocast without its cast cache) captured into one HIP graph: from the
-    same parameters and optimizer state, every replay gives the eager step's
-    loss and updated parameters bit for bit, with other eager GPU work between
-    replays."""
+@pytest.mark.parametrize("fused", [False, True])
+def test_progressive_step_graph_replay_matches_eager(dev, fused):
+    """The whole training step (forward, backward, AdamW with capturable state
+    -- the multi-tensor or the fused update -- bf16 autocast without its cast
+    cache) captured into one HIP graph: from the same parameters and optimizer
+    state, every replay gives the eager step's loss and updated parameters bit
+    for bit, with other eager GPU work between replays."""
     cfg, model, prefix, target = _models_and_batch(seed=31)
     model = model.to(dev)
     prefix, target = prefix.to(dev), target.to(dev)
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, capturable=True)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, capturable=True, fused=fused)
 
     def step():
         opt.zero_grad(set_to_none=True)

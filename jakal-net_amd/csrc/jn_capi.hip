@@ -27,6 +27,36 @@ void set_error(const char* fmt, ...) {
 
 const char* last_error() { return g_last_error.c_str(); }
 
+SideStream* side_stream(hipStream_t origin) {
+  thread_local std::map<int, SideStream> per_device;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  auto it = per_device.find(dev);
+  if (it != per_device.end()) return &it->second;
+  // streams and events are made outside any capture (a first use under
+  // capture runs on `origin` alone)
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(origin, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+  SideStream s{};
+  if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess)
+    return nullptr;
+  return &per_device.emplace(dev, s).first->second;
+}
+
+int fork_to(const SideStream* s, hipStream_t origin) {
+  JN_HIP_TRY(hipEventRecord(s->fork, origin));
+  JN_HIP_TRY(hipStreamWaitEvent(s->stream, s->fork, 0));
+  return kOk;
+}
+
+int join_from(const SideStream* s, hipStream_t origin) {
+  JN_HIP_TRY(hipEventRecord(s->join, s->stream));
+  JN_HIP_TRY(hipStreamWaitEvent(origin, s->join, 0));
+  return kOk;
+}
+
 namespace {
 struct ProfRecord {
   const char* name;
@@ -537,6 +567,32 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
     rb.heads = (int)heads;
     rb.head_rank = (int)(rank / heads);
   }
+  // 2a. the CSR layout of the edge list (it reads only the edge index) runs on
+  //     a second stream beside the row pass
+  CsrArgs ca{};
+  ca.idx = topk_index;
+  ca.k = k;
+  ca.B = B;
+  ca.Nq = N;
+  ca.Nk = N;
+  ca.tile_base = s.tile_base;
+  ca.seg_start = s.seg_start;
+  ca.rec = s.rec;
+  ca.coef = s.coef;
+  ca.g_score = s.g_score;
+  ca.gds = grad_delta_state;
+  ca.ehead = mh ? edge_head : nullptr;
+  const SideStream* side = side_stream(st);
+  if (!band) {
+    hipStream_t cs = side ? side->stream : st;
+    if (side) {
+      rc = fork_to(side, st);
+      if (rc) return rc;
+    }
+    rc = launch_csr_layout(ca, cs);
+    if (rc) return rc;
+  }
+
   // a causal band: the value-row dot products as MFMA tiles over each row
   // tile's span, then the row kernel without value rows
   const bool band_mfma = band && window_kernels() == 0 &&
@@ -561,23 +617,14 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   rc = launch_rows_backward(rb, st);
   if (rc) return rc;
 
-  // 2. transpose the edge list to source-major order (deterministic; closed
-  //    form for a band)
-  CsrArgs ca{};
-  ca.idx = topk_index;
-  ca.k = k;
-  ca.B = B;
-  ca.Nq = N;
-  ca.Nk = N;
-  ca.tile_base = s.tile_base;
-  ca.seg_start = s.seg_start;
-  ca.rec = s.rec;
-  ca.coef = s.coef;
-  ca.g_score = s.g_score;
-  ca.gds = grad_delta_state;
-  ca.ehead = mh ? edge_head : nullptr;
+  // 2b. the edge records, grouped by key (deterministic transpose; a band's
+  //     is closed form and needs none)
   if (!band) {
-    rc = launch_csr(ca, st);
+    if (side) {
+      rc = join_from(side, st);
+      if (rc) return rc;
+    }
+    rc = launch_csr_fill(ca, st);
     if (rc) return rc;
   }
 
@@ -616,6 +663,17 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
     cb.gds = grad_delta_state;
     cb.ehead = mh ? edge_head : nullptr;
   }
+  // dK and the scale partials on the second stream, beside the value gather
+  if (side) {
+    ColsBwdArgs kg = cb;
+    kg.grad_pv = nullptr;
+    kg.grad_ps = nullptr;
+    rc = fork_to(side, st);
+    if (rc) return rc;
+    rc = launch_cols_backward(kg, side->stream);
+    if (rc) return rc;
+    cb.q = nullptr;  // the main stream gathers the values only
+  }
   if (band_mfma && gpv && band_kernels_fit(k, (int)out_dim, out_dim, out_dim, grad_delta_val, gpv, bf16)) {
     // the value and state gradients of the sources: the transposed band as MFMA tiles
     BandAggArgs cg{};
@@ -639,6 +697,10 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   }
   rc = launch_cols_backward(cb, st);
   if (rc) return rc;
+  if (side) {
+    rc = join_from(side, st);
+    if (rc) return rc;
+  }
 
   // 4. projection weight grads: [dU; dV] = dP^T . X  (split-K, fixed order)
   if (grad_target_weight && grad_source_weight) {

@@ -591,6 +591,12 @@ __global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs a) {
 }
 
 int launch_csr(const CsrArgs& a, hipStream_t stream) {
+  int rc = launch_csr_layout(a, stream);
+  if (rc) return rc;
+  return launch_csr_fill(a, stream);
+}
+
+int launch_csr_layout(const CsrArgs& a, hipStream_t stream) {
   const int T = (a.Nq + kCsrTile - 1) / kCsrTile;
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
   JN_REQUIRE((int64_t)a.B * a.Nq <= kRecRowMask, kUnsupported,
@@ -612,11 +618,15 @@ int launch_csr(const CsrArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(csr_segment_scan_kernel, dim3(a.B), dim3(1024), 0, stream, a);
     JN_LAUNCH_CHECK();
   }
-  {
-    JN_PROFILE("csr_fill_kernel", stream);
-    hipLaunchKernelGGL(csr_fill_kernel, g2, dim3(256), 0, stream, a);
-    JN_LAUNCH_CHECK();
-  }
+  return kOk;
+}
+
+int launch_csr_fill(const CsrArgs& a, hipStream_t stream) {
+  const int T = (a.Nq + kCsrTile - 1) / kCsrTile;
+  dim3 g2(T, a.B);
+  JN_PROFILE("csr_fill_kernel", stream);
+  hipLaunchKernelGGL(csr_fill_kernel, g2, dim3(256), 0, stream, a);
+  JN_LAUNCH_CHECK();
   return kOk;
 }
 

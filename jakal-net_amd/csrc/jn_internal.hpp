@@ -312,6 +312,23 @@ constexpr int kCsrTile = 64;
 constexpr int kRecHeadShift = 27;
 constexpr int kRecRowMask = (1 << kRecHeadShift) - 1;
 int launch_csr(const CsrArgs& a, hipStream_t stream);
+// The two halves of launch_csr: the layout (per-tile counts, tile bases and
+// segment starts; reads only the edge index) and the record fill (reads the
+// coefficients, score gradients and state gradients as well).
+int launch_csr_layout(const CsrArgs& a, hipStream_t stream);
+int launch_csr_fill(const CsrArgs& a, hipStream_t stream);
+
+// A second stream of the calling thread for the current device, with an event
+// pair to fork work onto it from `origin` and join it back: kernels that do not
+// depend on each other run side by side (and as parallel branches of a captured
+// graph).  Null when none can be made here (first use during a capture).
+struct SideStream {
+  hipStream_t stream;
+  hipEvent_t fork, join;
+};
+SideStream* side_stream(hipStream_t origin);
+int fork_to(const SideStream* s, hipStream_t origin);   // s->stream waits for origin's work so far
+int join_from(const SideStream* s, hipStream_t origin); // origin waits for s->stream's work so far
 
 struct ColsBwdArgs {
   const int32_t* seg_start;  // [B, Nk + 1]

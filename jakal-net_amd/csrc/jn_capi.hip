@@ -45,6 +45,13 @@ SideStream* side_stream(hipStream_t origin) {
   return &per_device.emplace(dev, s).first->second;
 }
 
+// Forking pays only when each branch has work enough to hide the extra event
+// nodes (on small problems they cost more than the overlap gains).
+constexpr int64_t kSideMinEdges = 1 << 20;
+const SideStream* side_stream_for(hipStream_t origin, int64_t edges) {
+  return edges >= kSideMinEdges ? side_stream(origin) : nullptr;
+}
+
 int fork_to(const SideStream* s, hipStream_t origin) {
   JN_HIP_TRY(hipEventRecord(s->fork, origin));
   JN_HIP_TRY(hipStreamWaitEvent(s->stream, s->fork, 0));
@@ -189,7 +196,8 @@ struct TransitionScratch {
   float* rowsum;
   float* part_c;
   float* stage;
-  float* splitk;
+  float* splitk;    // split-K partials of the destination-side weight gradient
+  float* splitk2;   // of the source-side one (the two run side by side)
   void* select_ws;  // split-fp16 key rows of the forward's select
   size_t select_ws_bytes;
   size_t bytes;
@@ -213,9 +221,8 @@ TransitionScratch carve_transition(void* base, size_t size, int64_t B, int64_t N
   s.rowsum = ws.take<float>(B * Ns * heads);
   s.part_c = ws.take<float>((size_t)cols_backward_parts(B * Nd) * r);
   s.stage = ws.take<float>(finalize_stage_floats((int)r, (int)heads));
-  const size_t sk = std::max(gemm_grad_weight_workspace((int)r, (int)Dsrc, (int)(B * Ns)),
-                             gemm_grad_weight_workspace((int)r, (int)Ddst, (int)(B * Nd)));
-  s.splitk = ws.take<float>(sk / sizeof(float));
+  s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)r, (int)Ddst, (int)(B * Nd)) / sizeof(float));
+  s.splitk2 = ws.take<float>(gemm_grad_weight_workspace((int)r, (int)Dsrc, (int)(B * Ns)) / sizeof(float));
   s.select_ws_bytes = heads > 1 ? select_workspace_bytes_heads(B, Nd, r / heads, heads)
                                 : select_workspace_bytes(B, Nd, r);
   s.select_ws = ws.take<char>(s.select_ws_bytes);
@@ -582,7 +589,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   ca.g_score = s.g_score;
   ca.gds = grad_delta_state;
   ca.ehead = mh ? edge_head : nullptr;
-  const SideStream* side = side_stream(st);
+  const SideStream* side = side_stream_for(st, (int64_t)M * k);
   if (!band) {
     hipStream_t cs = side ? side->stream : st;
     if (side) {
@@ -1131,13 +1138,22 @@ static int transition_topk_forward_impl(const float* sender_strength, const floa
              "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
   const int B = (int)batch, Ns = (int)src_nodes, Nd = (int)dst_nodes, r = (int)rank;
 
-  // 1. projections P_s = src . Ws^T, P_t = dst . Wt^T  (modules.py:435-437)
+  // 1. projections P_s = src . Ws^T, P_t = dst . Wt^T  (modules.py:435-437), side by side
+  const SideStream* side = side_stream_for(st, batch * src_nodes * k);
+  if (side) {
+    rc = fork_to(side, st);
+    if (rc) return rc;
+  }
+  rc = gemm_project(dst_val, dst_dim, target_weight, target_weight, r, dst_dim, dst_proj, r, B * Nd, r, (int)dst_dim,
+                    side ? side->stream : st, bf16);
+  if (rc) return rc;
   rc = gemm_project(src_val, src_dim, source_weight, source_weight, r, src_dim, src_proj, r, B * Ns, r, (int)src_dim,
                     st, bf16);
   if (rc) return rc;
-  rc = gemm_project(dst_val, dst_dim, target_weight, target_weight, r, dst_dim, dst_proj, r, B * Nd, r, (int)dst_dim,
-                    st, bf16);
-  if (rc) return rc;
+  if (side) {
+    rc = join_from(side, st);
+    if (rc) return rc;
+  }
 
   // 2. per-source edge list: logits ((P_s * w) . P_t + b) / T, top-k over destinations
   if (k < dst_nodes) {
@@ -1216,11 +1232,9 @@ static int transition_topk_forward_impl(const float* sender_strength, const floa
     if (rc) return rc;
   }
 
-  // 3. coefficients rho * p, then destination sums as gathers over the edges
+  // 3. coefficients rho * p (beside the CSR layout, which reads only the
+  //    edge index), then destination sums as gathers over the edges
   //    transposed by destination
-  rc = launch_route_coef(route_index, route_logit, sender_strength, (int)k, compress_kind, batch * src_nodes, s.coef,
-                         st);
-  if (rc) return rc;
   CsrArgs ca{};
   ca.idx = route_index;
   ca.k = (int)k;
@@ -1232,7 +1246,20 @@ static int transition_topk_forward_impl(const float* sender_strength, const floa
   ca.rec = s.rec;
   ca.coef = s.coef;
   ca.gds = projected_state;
-  rc = launch_csr(ca, st);
+  if (side) {
+    rc = fork_to(side, st);
+    if (rc) return rc;
+  }
+  rc = launch_csr_layout(ca, side ? side->stream : st);
+  if (rc) return rc;
+  rc = launch_route_coef(route_index, route_logit, sender_strength, (int)k, compress_kind, batch * src_nodes, s.coef,
+                         st);
+  if (rc) return rc;
+  if (side) {
+    rc = join_from(side, st);
+    if (rc) return rc;
+  }
+  rc = launch_csr_fill(ca, st);
   if (rc) return rc;
   ColsBwdArgs cb{};
   cb.seg_start = s.seg_start;
@@ -1314,10 +1341,7 @@ static int transition_topk_backward_impl(const float* sender_strength, const flo
     rb.heads = (int)heads;
     rb.head_rank = (int)(rank / heads);
   }
-  rc = launch_route_rows_backward(rb, st);
-  if (rc) return rc;
-
-  // 2. destination columns: grad of the destination projection and w partials
+  // the CSR layout of the routes (it reads only the edge index) beside the row pass
   CsrArgs ca{};
   ca.idx = route_index;
   ca.k = (int)k;
@@ -1329,8 +1353,39 @@ static int transition_topk_backward_impl(const float* sender_strength, const flo
   ca.rec = s.rec;
   ca.g_score = s.g_logit;
   ca.ehead = mh ? route_head : nullptr;
-  rc = launch_csr(ca, st);
+  const SideStream* side = side_stream_for(st, (int64_t)B * Ns * k);
+  if (side) {
+    rc = fork_to(side, st);
+    if (rc) return rc;
+  }
+  rc = launch_csr_layout(ca, side ? side->stream : st);
   if (rc) return rc;
+  rc = launch_route_rows_backward(rb, st);
+  if (rc) return rc;
+  if (side) {
+    rc = join_from(side, st);
+    if (rc) return rc;
+  }
+
+  // 2. destination columns: grad of the destination projection and w partials
+  rc = launch_csr_fill(ca, st);
+  if (rc) return rc;
+  // the source side's projection grads (ready after the row pass) run beside them
+  hipStream_t ss = side ? side->stream : st;
+  if (side) {
+    rc = fork_to(side, st);
+    if (rc) return rc;
+  }
+  if (grad_source_weight) {
+    rc = gemm_grad_weight(s.dPs, r, src_val, src_dim, grad_source_weight, grad_source_weight, r, r, (int)src_dim,
+                          B * Ns, s.splitk2, ss, bf16);
+    if (rc) return rc;
+  }
+  if (grad_src_val) {
+    rc = gemm_grad_input(s.dPs, r, source_weight, source_weight, r, src_dim, nullptr, 0, grad_src_val, src_dim,
+                         B * Ns, (int)src_dim, r, ss, bf16);
+    if (rc) return rc;
+  }
   ColsBwdArgs cb{};
   cb.seg_start = s.seg_start;
   cb.rec = s.rec;
@@ -1355,25 +1410,19 @@ static int transition_topk_backward_impl(const float* sender_strength, const flo
   rc = launch_cols_backward(cb, st);
   if (rc) return rc;
 
-  // 3. projection weight and input grads
-  if (grad_source_weight) {
-    rc = gemm_grad_weight(s.dPs, r, src_val, src_dim, grad_source_weight, grad_source_weight, r, r, (int)src_dim,
-                          B * Ns, s.splitk, st, bf16);
-    if (rc) return rc;
-  }
+  // 3. destination-side projection weight and input grads
   if (grad_target_weight) {
     rc = gemm_grad_weight(s.dPt, r, dst_val, dst_dim, grad_target_weight, grad_target_weight, r, r, (int)dst_dim,
                           B * Nd, s.splitk, st, bf16);
     if (rc) return rc;
   }
-  if (grad_src_val) {
-    rc = gemm_grad_input(s.dPs, r, source_weight, source_weight, r, src_dim, nullptr, 0, grad_src_val, src_dim,
-                         B * Ns, (int)src_dim, r, st, bf16);
-    if (rc) return rc;
-  }
   if (grad_dst_val) {
     rc = gemm_grad_input(s.dPt, r, target_weight, target_weight, r, dst_dim, nullptr, 0, grad_dst_val, dst_dim,
                          B * Nd, (int)dst_dim, r, st, bf16);
+    if (rc) return rc;
+  }
+  if (side) {
+    rc = join_from(side, st);
     if (rc) return rc;
   }
 

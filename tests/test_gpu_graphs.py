@@ -44,6 +44,25 @@ def _case(kind, dev):
     g = torch.Generator().manual_seed(7100)
     torch.manual_seed(7100)
     B, N, D, r = 2, 256, 64, 16
+    if kind == "topk_large":  # 2^20 edges: the backward forks work onto a second stream
+        layer = _layer(g, 4, 4096, D, dev)
+        op = J.SparsePropagation(J.LowRankBilinearPairwise(D, r), sparse_type="topk", topk=64,
+                                 implementation="native").to(dev)
+
+        def loss_terms():
+            d = op(layer)
+            return [d.delta_state, d.delta_val]
+
+        return [op], [layer.state, layer.val], loss_terms
+    if kind == "transition_large":  # 2^20 routes: projections and gradients on two streams
+        src, dst = _layer(g, 4, 4096, D, dev), _layer(g, 4, 512, D, dev)
+        op = J.SparseTransition(J.LowRankBilinearRoute(D, D, rank=r), topk=64, implementation="native").to(dev)
+
+        def loss_terms():
+            d = op.compute_delta(src, dst)
+            return [d.delta_state, d.delta_val]
+
+        return [op], [src.state, src.val, dst.state, dst.val], loss_terms
     if kind in ("topk", "window", "dense", "topk_bf16", "topk_multihead"):
         dtype = torch.bfloat16 if kind == "topk_bf16" else torch.float32
         layer = _layer(g, B, N, D, dev, dtype)
@@ -94,7 +113,8 @@ def _snapshot(modules, leaves, outs):
     return [None if t is None else t.detach().clone() for t in tensors]  # leaves the step does not reach: None
 
 
-@pytest.mark.parametrize("kind", ["topk", "window", "dense", "transition", "topk_bf16", "topk_multihead"])
+@pytest.mark.parametrize("kind", ["topk", "window", "dense", "transition", "topk_bf16", "topk_multihead", "topk_large",
+                                  "transition_large"])
 def test_captured_step_replays_match_eager(dev, kind, monkeypatch):
     import jakal_net_native as jn
 

@@ -5,7 +5,12 @@
  * a contiguous row-major float32 / int32 buffer on the current HIP device, and
  * `stream` is a hipStream_t (passed as void*).  Calls are asynchronous on
  * `stream`; none allocates device memory (scratch comes in through
- * `workspace`, sized by the matching *_workspace_bytes query).
+ * `workspace`, sized by the matching *_workspace_bytes query).  Edge-list
+ * backward passes and top-k transitions on at least 2^20 edges run part of
+ * their work on a library-owned side stream (one per host thread and device,
+ * created on first use outside graph capture), forked from and joined back to
+ * `stream` by events inside the call: work ordered after the call on `stream`
+ * sees all of its results.
  *
  * Every entry point returns 0 on success and a non-zero jn status on error;
  * jn_last_error() then holds a message for the calling host thread.

@@ -158,6 +158,8 @@ struct PropBwdScratch {
   int32_t* tile_base;
   int32_t* seg_start;
   float4* rec;
+  int32_t* pos;  // each edge's record index (fused column pass)
+  float* dots;   // slab-0 dot partials in record order (fused column pass)
   float* part_c;
   float* stage;
   float* splitk;
@@ -178,6 +180,8 @@ PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int
   s.tile_base = ws.take<int32_t>(B * T * N);
   s.seg_start = ws.take<int32_t>(B * (N + 1));
   s.rec = ws.take<float4>(M * k);
+  s.pos = ws.take<int32_t>(M * k);
+  s.dots = ws.take<float>(M * k);
   s.part_c = ws.take<float>((size_t)cols_backward_parts(M) * r);
   s.stage = ws.take<float>(finalize_stage_floats((int)r, (int)heads));
   s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)(2 * r), (int)Din, (int)M) / sizeof(float));
@@ -589,124 +593,210 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   ca.g_score = s.g_score;
   ca.gds = grad_delta_state;
   ca.ehead = mh ? edge_head : nullptr;
-  const SideStream* side = side_stream_for(st, (int64_t)M * k);
-  if (!band) {
-    hipStream_t cs = side ? side->stream : st;
+  float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
+
+  // Fused column pass (CSR edge lists whose value rows fit at most two slabs of
+  // 16-byte packs): each incoming edge's gdv row is gathered once per column,
+  // for the value gradient and for the edge's dot product <gdv[i], pv[j]>, so
+  // the row pass reads no value rows.
+  ColsBwdArgs fc{};
+  fc.seg_start = s.seg_start;
+  fc.rec = s.rec;
+  fc.k = k;
+  fc.gdv = grad_delta_val;
+  fc.r = r;
+  fc.B = B;
+  fc.Nq = N;
+  fc.Nk = N;
+  fc.D = (int)out_dim;
+  fc.grad_pv = gpv;
+  fc.ld_gpv = out_dim;
+  fc.grad_ps = grad_projected_state;
+  fc.bf16 = bf16 ? 1 : 0;
+  fc.rec_eid = 1;
+  fc.pv = projected_val;
+  fc.ld_pv = out_dim;
+  fc.dots0 = s.dots;
+  fc.dots1 = s.coef;
+  const int dot_slabs = band ? 0 : cols_gather_dots_slabs(fc);
+  if (dot_slabs) {
+    // a. the CSR layout (edge index only) on the second stream beside the
+    //    edge coefficients, then the records {row, coef, edge id, coef * gds}
+    ca.g_score = nullptr;
+    ca.rec_eid = 1;
+    ca.pos = s.pos;
+    const SideStream* side = side_stream_for(st, (int64_t)M * k);
     if (side) {
       rc = fork_to(side, st);
       if (rc) return rc;
     }
-    rc = launch_csr_layout(ca, cs);
+    rc = launch_csr_layout(ca, side ? side->stream : st);
     if (rc) return rc;
-  }
-
-  // a causal band: the value-row dot products as MFMA tiles over each row
-  // tile's span, then the row kernel without value rows
-  const bool band_mfma = band && window_kernels() == 0 &&
-                         band_kernels_fit(k, (int)out_dim, out_dim, out_dim, grad_delta_val, projected_val, bf16);
-  if (band_mfma) {
-    BandDotsArgs bd{};
-    bd.B = B;
-    bd.N = N;
-    bd.k = k;
-    bd.D = (int)out_dim;
-    bd.gdv = grad_delta_val;
-    bd.ld_gdv = out_dim;
-    bd.pv = projected_val;
-    bd.ld_pv = out_dim;
-    bd.g_score = s.g_score;
-    bd.coef = s.coef;
-    bd.bf16 = bf16 ? 1 : 0;
-    rc = launch_band_dots(bd, st);
+    rc = launch_edge_coefficients(topk_index, topk_score, M, k, compress_kind, s.coef, st);
     if (rc) return rc;
-    rb.dots_given = 1;
-  }
-  rc = launch_rows_backward(rb, st);
-  if (rc) return rc;
-
-  // 2b. the edge records, grouped by key (deterministic transpose; a band's
-  //     is closed form and needs none)
-  if (!band) {
     if (side) {
       rc = join_from(side, st);
       if (rc) return rc;
     }
     rc = launch_csr_fill(ca, st);
     if (rc) return rc;
+    // b. value and state grads of the sources, and the dot partials in record
+    //    order (slab 0 into dots, slab 1 into coef)
+    rc = launch_cols_gather_dots(fc, st);
+    if (rc) return rc;
+    // c. rows: compress backward from the given dots, grad of target projection
+    rb.dots_given = 1;
+    rb.dot_parts = dot_slabs;
+    rb.dot_pos = s.pos;
+    rb.dots0 = s.dots;
+    rc = launch_rows_backward(rb, st);
+    if (rc) return rc;
+    // d. grad of the source projection and the w_hat partials
+    ColsBwdArgs kg{};
+    kg.seg_start = s.seg_start;
+    kg.rec = s.rec;
+    kg.k = k;
+    kg.q = projections;
+    kg.ldq = 2 * r;
+    kg.key = src_proj;
+    kg.ldk = 2 * r;
+    kg.kscale = core_weight;
+    kg.r = r;
+    kg.B = B;
+    kg.Nq = N;
+    kg.Nk = N;
+    kg.D = (int)out_dim;
+    kg.dk = s.dP + r;
+    kg.lddk = 2 * r;
+    kg.part_c = s.part_c;
+    kg.rec_eid = 1;
+    kg.g_score = s.g_score;
+    if (mh) {
+      kg.heads = (int)heads;
+      kg.head_rank = (int)(rank / heads);
+    }
+    rc = launch_cols_backward(kg, st);
+    if (rc) return rc;
   }
+  if (!dot_slabs) {
+    const SideStream* side = side_stream_for(st, (int64_t)M * k);
+    if (!band) {
+      hipStream_t cs = side ? side->stream : st;
+      if (side) {
+        rc = fork_to(side, st);
+        if (rc) return rc;
+      }
+      rc = launch_csr_layout(ca, cs);
+      if (rc) return rc;
+    }
 
-  // 3. columns: value/state grads of the sources, grad of source projection, w_hat grad partials
-  float* gpv = projected_val_is_layer_val ? grad_layer_val : grad_projected_val;
-  ColsBwdArgs cb{};
-  cb.seg_start = s.seg_start;
-  cb.rec = s.rec;
-  cb.k = k;
-  cb.gdv = grad_delta_val;
-  cb.q = projections;
-  cb.ldq = 2 * r;
-  cb.key = src_proj;
-  cb.ldk = 2 * r;
-  cb.kscale = core_weight;
-  cb.r = r;
-  cb.B = B;
-  cb.Nq = N;
-  cb.Nk = N;
-  cb.D = (int)out_dim;
-  cb.grad_pv = gpv;
-  cb.ld_gpv = out_dim;
-  cb.grad_ps = grad_projected_state;
-  cb.dk = s.dP + r;
-  cb.lddk = 2 * r;
-  cb.part_c = s.part_c;
-  cb.bf16 = bf16 ? 1 : 0;
-  if (mh) {
-    cb.heads = (int)heads;
-    cb.head_rank = (int)(rank / heads);
-  }
-  if (band) {
-    cb.band = 1;
-    cb.coef = s.coef;
-    cb.g_score = s.g_score;
-    cb.gds = grad_delta_state;
-    cb.ehead = mh ? edge_head : nullptr;
-  }
-  // dK and the scale partials on the second stream, beside the value gather
-  if (side) {
-    ColsBwdArgs kg = cb;
-    kg.grad_pv = nullptr;
-    kg.grad_ps = nullptr;
-    rc = fork_to(side, st);
+    // a causal band: the value-row dot products as MFMA tiles over each row
+    // tile's span, then the row kernel without value rows
+    const bool band_mfma = band && window_kernels() == 0 &&
+                           band_kernels_fit(k, (int)out_dim, out_dim, out_dim, grad_delta_val, projected_val, bf16);
+    if (band_mfma) {
+      BandDotsArgs bd{};
+      bd.B = B;
+      bd.N = N;
+      bd.k = k;
+      bd.D = (int)out_dim;
+      bd.gdv = grad_delta_val;
+      bd.ld_gdv = out_dim;
+      bd.pv = projected_val;
+      bd.ld_pv = out_dim;
+      bd.g_score = s.g_score;
+      bd.coef = s.coef;
+      bd.bf16 = bf16 ? 1 : 0;
+      rc = launch_band_dots(bd, st);
+      if (rc) return rc;
+      rb.dots_given = 1;
+    }
+    rc = launch_rows_backward(rb, st);
     if (rc) return rc;
-    rc = launch_cols_backward(kg, side->stream);
+
+    // 2b. the edge records, grouped by key (deterministic transpose; a band's
+    //     is closed form and needs none)
+    if (!band) {
+      if (side) {
+        rc = join_from(side, st);
+        if (rc) return rc;
+      }
+      rc = launch_csr_fill(ca, st);
+      if (rc) return rc;
+    }
+
+    // 3. columns: value/state grads of the sources, grad of source projection, w_hat grad partials
+    ColsBwdArgs cb{};
+    cb.seg_start = s.seg_start;
+    cb.rec = s.rec;
+    cb.k = k;
+    cb.gdv = grad_delta_val;
+    cb.q = projections;
+    cb.ldq = 2 * r;
+    cb.key = src_proj;
+    cb.ldk = 2 * r;
+    cb.kscale = core_weight;
+    cb.r = r;
+    cb.B = B;
+    cb.Nq = N;
+    cb.Nk = N;
+    cb.D = (int)out_dim;
+    cb.grad_pv = gpv;
+    cb.ld_gpv = out_dim;
+    cb.grad_ps = grad_projected_state;
+    cb.dk = s.dP + r;
+    cb.lddk = 2 * r;
+    cb.part_c = s.part_c;
+    cb.bf16 = bf16 ? 1 : 0;
+    if (mh) {
+      cb.heads = (int)heads;
+      cb.head_rank = (int)(rank / heads);
+    }
+    if (band) {
+      cb.band = 1;
+      cb.coef = s.coef;
+      cb.g_score = s.g_score;
+      cb.gds = grad_delta_state;
+      cb.ehead = mh ? edge_head : nullptr;
+    }
+    // dK and the scale partials on the second stream, beside the value gather
+    if (side) {
+      ColsBwdArgs kg = cb;
+      kg.grad_pv = nullptr;
+      kg.grad_ps = nullptr;
+      rc = fork_to(side, st);
+      if (rc) return rc;
+      rc = launch_cols_backward(kg, side->stream);
+      if (rc) return rc;
+      cb.q = nullptr;  // the main stream gathers the values only
+    }
+    if (band_mfma && gpv && band_kernels_fit(k, (int)out_dim, out_dim, out_dim, grad_delta_val, gpv, bf16)) {
+      // the value and state gradients of the sources: the transposed band as MFMA tiles
+      BandAggArgs cg{};
+      cg.B = B;
+      cg.N = N;
+      cg.k = k;
+      cg.D = (int)out_dim;
+      cg.trans = 1;
+      cg.coef = s.coef;
+      cg.state = grad_delta_state;
+      cg.val = grad_delta_val;
+      cg.ld_val = out_dim;
+      cg.out_state = grad_projected_state;
+      cg.out = gpv;
+      cg.ld_out = out_dim;
+      cg.bf16 = bf16 ? 1 : 0;
+      rc = launch_band_aggregate(cg, st);
+      if (rc) return rc;
+      cb.grad_pv = nullptr;  // the column kernels still compute dK and the scale partials
+      cb.grad_ps = nullptr;
+    }
+    rc = launch_cols_backward(cb, st);
     if (rc) return rc;
-    cb.q = nullptr;  // the main stream gathers the values only
-  }
-  if (band_mfma && gpv && band_kernels_fit(k, (int)out_dim, out_dim, out_dim, grad_delta_val, gpv, bf16)) {
-    // the value and state gradients of the sources: the transposed band as MFMA tiles
-    BandAggArgs cg{};
-    cg.B = B;
-    cg.N = N;
-    cg.k = k;
-    cg.D = (int)out_dim;
-    cg.trans = 1;
-    cg.coef = s.coef;
-    cg.state = grad_delta_state;
-    cg.val = grad_delta_val;
-    cg.ld_val = out_dim;
-    cg.out_state = grad_projected_state;
-    cg.out = gpv;
-    cg.ld_out = out_dim;
-    cg.bf16 = bf16 ? 1 : 0;
-    rc = launch_band_aggregate(cg, st);
-    if (rc) return rc;
-    cb.grad_pv = nullptr;  // the column kernels still compute dK and the scale partials
-    cb.grad_ps = nullptr;
-  }
-  rc = launch_cols_backward(cb, st);
-  if (rc) return rc;
-  if (side) {
-    rc = join_from(side, st);
-    if (rc) return rc;
+    if (side) {
+      rc = join_from(side, st);
+      if (rc) return rc;
+    }
   }
 
   // 4. projection weight grads: [dU; dV] = dP^T . X  (split-K, fixed order)

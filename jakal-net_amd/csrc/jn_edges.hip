@@ -239,7 +239,14 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
     float dot = 0.f;
     if constexpr (SPLIT) {
       // slab partials of this lane's edge, summed in slab order
-      if (lane < ne) dot = a.g_score[row * a.k + e0 + lane] + a.coef[row * a.k + e0 + lane];
+      if (a.dot_pos) {  // record order: absent edges have no record
+        if (lane < ne && j >= 0 && j < a.Nk) {
+          const int p = a.dot_pos[row * a.k + e0 + lane];
+          dot = a.dots0[p] + (a.dot_parts == 1 ? 0.f : a.coef[p]);
+        }
+      } else if (lane < ne) {
+        dot = a.g_score[row * a.k + e0 + lane] + (a.dot_parts == 1 ? 0.f : a.coef[row * a.k + e0 + lane]);
+      }
     } else {
       const auto rs_pv =
           make_rsrc(reinterpret_cast<const T*>(a.pv) + b * a.Nk * a.ld_pv, (uint32_t)(a.Nk * a.ld_pv * EB));
@@ -299,7 +306,7 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
     gsc *= a.inv_temperature;
     if (lane < ne) {
       a.g_score[row * a.k + e0 + lane] = gsc;
-      a.coef[row * a.k + e0 + lane] = cf;
+      if (!(SPLIT && a.dot_pos)) a.coef[row * a.k + e0 + lane] = cf;  // coef holds other rows' partials
     }
     if constexpr (MH) {
       // per-head bias partials (a shift of one head's scores is no shift of the row)
@@ -580,10 +587,11 @@ __global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs a) {
         int pos = seg[j] + a.tile_base[((int64_t)b * T + t) * a.Nk + j] + __popcll(below);
         const int row = b * a.Nq + r0 + rl;
         const float cf = a.coef ? a.coef[eid] : 0.f;
-        const float gs = a.g_score ? a.g_score[eid] : 0.f;
+        const float gs = a.rec_eid ? __int_as_float((int)eid) : (a.g_score ? a.g_score[eid] : 0.f);
         const float cd = a.gds ? cf * a.gds[row] : 0.f;
         const int hd = a.ehead ? (int)a.ehead[eid] << kRecHeadShift : 0;
         a.rec[batch_base + pos] = make_float4(__int_as_float(row | hd), cf, gs, cd);
+        if (a.pos) a.pos[eid] = (int32_t)(batch_base + pos);
       }
     }
     __syncthreads();
@@ -743,6 +751,206 @@ __global__ __launch_bounds__(256) void cols_gather_kernel(ColsBwdArgs a, int sla
   }
 }
 
+// Sums each of v[0..7] over the 64 lanes; lane L receives the total of
+// v[L >> 3].  Each exchange halves the values a lane holds: the permlane swaps
+// pair lanes L ^ 32 and L ^ 16, a row mirror pairs opposite bit 3, and three
+// DPP steps finish the sum inside each 8-lane half-row (10 exchanges for 8
+// sums instead of 8 x 6).
+__device__ __forceinline__ float transpose_sum8(const float (&v)[8]) {
+  float w[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    // lanes < 32 keep v[m] (with lane + 32's), lanes >= 32 keep v[m + 4]
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[m]), __float_as_uint(v[m + 4]), false, false);
+    w[m] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  float x[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    // rows 0 and 2 keep w[m] (with the next row's), rows 1 and 3 keep w[m + 2]
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[m]), __float_as_uint(w[m + 2]), false, false);
+    x[m] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  const bool b3 = (lane_id() & 8) != 0;
+  float y = (b3 ? x[1] : x[0]) + dpp_f<0x140>(b3 ? x[0] : x[1]);  // row_mirror flips bit 3
+  y += dpp_f<0xB1>(y);   // quad_perm [1,0,3,2]
+  y += dpp_f<0x4E>(y);   // quad_perm [2,3,0,1]
+  y += dpp_f<0x141>(y);  // row_half_mirror
+  return y;
+}
+
+// Sums each of v[0..3] over the 64 lanes; lane L receives the total of
+// v[L >> 4] (two permlane steps, then a sum inside each 16-lane row).
+__device__ __forceinline__ float transpose_sum4(const float (&v)[4]) {
+  float w[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[m]), __float_as_uint(v[m + 2]), false, false);
+    w[m] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[0]), __float_as_uint(w[1]), false, false);
+  return row16_sum(__uint_as_float(p[0]) + __uint_as_float(p[1]));
+}
+
+template <int G>
+__device__ __forceinline__ float transpose_sum(const float (&v)[G]) {
+  if constexpr (G == 8) return transpose_sum8(v);
+  else return transpose_sum4(v);
+}
+
+// Streaming accesses (read or written once): non-temporal, so they do not
+// displace the gathered rows from L2.
+typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+  const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void store_nt16(void* p, uint4 x) {
+  u32x4_nt v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_nt*>(p));
+}
+
+// Fused column pass: one wavefront per key column and slab of kWave * W
+// columns (one 16-byte pack per lane), slab-major over the grid as in
+// cols_gather_kernel.  Each incoming edge's gdv row (slab) is read once and
+// serves both
+//   grad_pv[j] += coef * gdv[i]          (the column sum of cols_gather_kernel)
+//   dots_s[x]   = <gdv[i], pv[j]> over slab s, x = the edge's record index
+// the second being the edge-coefficient gradient the row backward needs (its
+// value-row gather is then not run; it finds x through CsrArgs::pos).
+// G records per group: their rows are in flight together, then G dot
+// partials are summed over the wave by one transpose-sum.
+template <typename T, int W, int G>
+__global__ __launch_bounds__(256) void cols_gather_dots_kernel(ColsBwdArgs a) {
+  constexpr int SLAB = kWave * W;
+  const int lane = lane_id();
+  const int64_t total_cols = (int64_t)a.B * a.Nk;
+  const int64_t col_blocks = (total_cols + 3) / 4;
+  const int64_t logical = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int slab = (int)(logical / col_blocks);
+  const int64_t col = (logical % col_blocks) * 4 + wave_id();
+  if (col >= total_cols) return;
+  const ColRecords<false> recs(a, col);
+  const int len = recs.len;
+  const int d = slab * SLAB + lane * W;
+  const bool on = d < a.D;  // a.D % W == 0 (host)
+  const T* gdv = reinterpret_cast<const T*>(a.gdv) + (on ? d : 0);
+  const Pack<W> pj =
+      on ? unpack16<T, W>(load_nt16(reinterpret_cast<const T*>(a.pv) + col * a.ld_pv + d)) : pack_zero<T, W>();
+  float* part = slab == 0 ? a.dots0 : a.dots1;
+  const int64_t rec_base = recs.rec - a.rec;  // record index of the column's first record
+
+  Pack<W> acc = pack_zero<T, W>(), acc1 = acc;  // even / odd records
+  float st = 0.f;
+  for (int q0 = 0; q0 < len; q0 += kWave) {
+    const int n = min(kWave, len - q0);
+    const int64_t rec0 = rec_base + q0;
+    int row = 0;
+    float cf = 0.f;
+    if (lane < n) {
+      const uint4 r = load_nt16(recs.rec + q0 + lane);
+      row = (int)r.x & kRecRowMask;
+      cf = __uint_as_float(r.y);
+      st += __uint_as_float(r.w);
+    }
+    for (int q = 0; q < n; q += G) {  // n and q are wave-uniform
+      // the group's rows as raw 16-byte packs (widened where used)
+      uint4 raw[G];
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        const int src = min(q + u, kWave - 1);
+        raw[u] = (q + u < n && on) ? *reinterpret_cast<const uint4*>(gdv + (int64_t)readlane_i(row, src) * a.D)
+                                   : make_uint4(0u, 0u, 0u, 0u);
+      }
+      // lanes (64 / G) u receive record q + u's total
+      constexpr int LPR = kWave / G;
+      const int ru = q + lane / LPR;
+      const bool writer = lane % LPR == 0 && ru < n;
+      float pd[G];
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        // records past the segment hold cf = 0 (and zero rows)
+        const Pack<W> v = unpack16<T, W>(raw[u]);
+        fma_pack((u & 1) ? acc1 : acc, readlane_f(cf, min(q + u, kWave - 1)), v);
+        pd[u] = dot_pack(v, pj);
+      }
+      const float tot = transpose_sum<G>(pd);
+      if (writer) part[rec0 + ru] = tot;  // record order: consecutive records, consecutive slots
+    }
+  }
+  if (a.grad_pv && on) {
+    const Pack<W> g = add_pack(acc, acc1);
+    uint4 x;
+    if constexpr (sizeof(T) == 4) {
+      x = make_uint4(__float_as_uint(g.v[0]), __float_as_uint(g.v[1]), __float_as_uint(g.v[2]), __float_as_uint(g.v[3]));
+    } else {
+      x = make_uint4(pack_bf16x2(g.v[0], g.v[1]), pack_bf16x2(g.v[2], g.v[3]), pack_bf16x2(g.v[4], g.v[5]),
+                     pack_bf16x2(g.v[6], g.v[7]));
+    }
+    store_nt16(reinterpret_cast<T*>(a.grad_pv) + col * a.ld_gpv + d, x);
+  }
+  if (slab == 0 && a.grad_ps) {
+    st = wave_sum(st);
+    if (lane == 0) a.grad_ps[col] = st;
+  }
+}
+
+int cols_gather_dots_slabs(const ColsBwdArgs& a) {
+  const int eb = a.bf16 ? 2 : 4, pw = 16 / eb;
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (a.band || !a.rec || !a.pv || !a.dots0 || a.D < 1) return 0;
+  if (a.D % pw || a.ld_pv % pw || !a16(a.gdv) || !a16(a.pv)) return 0;
+  if (a.grad_pv && (a.ld_gpv % pw || !a16(a.grad_pv))) return 0;
+  const int slabs = (a.D + kWave * pw - 1) / (kWave * pw);
+  if (slabs > 2 || (slabs == 2 && !a.dots1)) return 0;
+  return slabs;
+}
+
+int launch_cols_gather_dots(const ColsBwdArgs& a, hipStream_t stream) {
+  const int64_t total_cols = (int64_t)a.B * a.Nk;
+  if (total_cols == 0) return kOk;
+  const int slabs = cols_gather_dots_slabs(a);
+  JN_REQUIRE(slabs > 0, kInvalidArgument, "fused column pass needs CSR records with edge ids and aligned rows");
+  JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
+  const int64_t blocks = (total_cols + 3) / 4 * slabs;
+  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
+  JN_PROFILE("cols_gather_dots_kernel", stream);
+  const dim3 grid((unsigned)blocks);
+  if (a.bf16) hipLaunchKernelGGL((cols_gather_dots_kernel<bf16_t, 8, 4>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((cols_gather_dots_kernel<float, 4, 8>), grid, dim3(256), 0, stream, a);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
+// One wavefront per row: the coefficients row_coefficients gives the row
+// kernels, written out for the edge records.
+__global__ __launch_bounds__(256) void edge_coefficients_kernel(const int32_t* idx, const float* score, int64_t rows,
+                                                                int k, int compress, float* coef) {
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  if (row >= rows) return;
+  float rmax = 0.f, rinv = 0.f;
+  if (compress == 1) row_abs_softmax_stats(idx, score, row, k, rmax, rinv);
+  for (int e0 = 0; e0 < k; e0 += kWave) {
+    int j;
+    float c, s;
+    row_coefficients(idx, score, row, k, e0, compress, rmax, rinv, j, c, s);
+    if (e0 + lane_id() < k) coef[row * k + e0 + lane_id()] = c;
+  }
+}
+
+int launch_edge_coefficients(const int32_t* idx, const float* score, int64_t rows, int k, int compress, float* coef,
+                             hipStream_t stream) {
+  if (rows == 0) return kOk;
+  JN_REQUIRE(compress == 0 || k <= kWave, kUnsupported, "signed compress kinds take k <= %d", kWave);
+  const int64_t blocks = (rows + 3) / 4;
+  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
+  JN_PROFILE("edge_coefficients_kernel", stream);
+  hipLaunchKernelGGL(edge_coefficients_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, idx, score, rows, k,
+                     compress, coef);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
 // One 16-lane group per column (16 columns per workgroup).  Lane c of a group
 // holds 8 rank slots: ranks 4c..4c+3 and 64+4c..64+4c+3 when the query rows are
 // read as float4 (VEC), else ranks c + 16m.  The group walks its column's
@@ -778,7 +986,7 @@ __global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
     if (q0 + c < len) {
       const float4 r = recs.get(a, q0 + c);
       row = __float_as_int(r.x);
-      gs = r.z;
+      gs = (!BAND && a.rec_eid) ? a.g_score[__float_as_int(r.z)] : r.z;
     }
     const int nu = min(16, wlen - q0);
     for (int u0 = 0; u0 < nu; u0 += 8) {

@@ -170,6 +170,11 @@ struct RowsBwdArgs {
   // The dot products <gdv[i], pv[j]> of every edge are already in g_score + coef
   // (two partial sums, e.g. from launch_band_dots): no value rows are read.
   int dots_given;
+  int dot_parts;          // with dots_given: 1 = g_score alone holds the dots (0 or 2: both buffers)
+  // With dots_given: the partials are in record order, edge e's at
+  // dot_pos[e] of dots0 and coef (coef is then not written).
+  const int32_t* dot_pos; // [rows, k] or null
+  const float* dots0;     // [rows * k] (with dot_pos)
 };
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream);
 
@@ -305,6 +310,8 @@ struct CsrArgs {
   const float* g_score;  // [B * Nq, k] or null
   const float* gds;      // [B * Nq] or null
   const uint8_t* ehead;  // [B * Nq, k] head of each edge, or null (head 0)
+  int rec_eid;           // 1: record word 2 holds the edge id (int bits) instead of g_score[e]
+  int32_t* pos;          // [B * Nq * k] or null: each edge's record index (batch offset included)
 };
 constexpr int kCsrTile = 64;
 // An edge record's first word holds its row below bit kRecHeadShift and its
@@ -364,8 +371,29 @@ struct ColsBwdArgs {
   const float* g_score;      // [B * Nq, k]
   const float* gds;          // [B * Nq] or null (record word 3 is then 0)
   const uint8_t* ehead;      // [B * Nq, k] or null (head 0)
+  // CSR records whose word 2 is the edge id (CsrArgs::rec_eid): the key
+  // gradient reads g_score[id].
+  int rec_eid;
+  // Fused column pass (launch_cols_gather_dots): the value rows pv [B*Nk, D]
+  // (stride ld_pv) and the per-edge slab partials of <gdv[i], pv[j]>, slab 0
+  // into dots0 and slab 1 into dots1 ([B * Nq * k], by record index).
+  const float* pv;
+  int64_t ld_pv;
+  float* dots0;
+  float* dots1;
 };
 int cols_backward_parts(int64_t total_cols);
+// Column slabs of the fused column pass (kWave 16-byte packs each) when it
+// applies to these rows (CSR records, 16-byte aligned rows, at most two
+// slabs), else 0.
+int cols_gather_dots_slabs(const ColsBwdArgs& a);
+// grad_pv, grad_ps and the dot-product slab partials in one pass over the
+// columns' records (records with edge ids); needs cols_gather_dots_slabs(a) > 0.
+int launch_cols_gather_dots(const ColsBwdArgs& a, hipStream_t stream);
+// coef[row, e] = the row's compressed score of edge e (0 for absent edges),
+// as the row kernels compute it.
+int launch_edge_coefficients(const int32_t* idx, const float* score, int64_t rows, int k, int compress, float* coef,
+                             hipStream_t stream);
 
 // Unit-norm scale vectors: out = w / max(||w||, eps) per row of [rows, r], or
 // with grad (non-null) the gradient of that map at w.

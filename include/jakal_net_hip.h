@@ -6,8 +6,9 @@
  * `stream` is a hipStream_t (passed as void*).  Calls are asynchronous on
  * `stream`; none allocates device memory (scratch comes in through
  * `workspace`, sized by the matching *_workspace_bytes query).  Edge-list
- * backward passes and top-k transitions on at least 2^20 edges run part of
- * their work on a library-owned side stream (one per host thread and device,
+ * backward passes, top-k forwards that build an edge layout, and top-k
+ * transitions on at least 2^20 edges run part of their work on a
+ * library-owned side stream (one per host thread and device,
  * created on first use outside graph capture), forked from and joined back to
  * `stream` by events inside the call: work ordered after the call on `stream`
  * sees all of its results.
@@ -35,7 +36,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 8. */
+/* ABI revision of this header (bumped on any signature change); this is 9. */
 int jn_abi_version(void);
 
 /*
@@ -123,6 +124,9 @@ size_t jn_lowrank_topk_select_workspace_bytes(int64_t batch, int64_t nk, int64_t
  * compress_kind: 0 softsign, 1 signed_abs_softmax (sign(s) * softmax(|s|) over the
  * row's k edges), 2 signed_entmax15 (sign(s) * entmax15(|s|) over them,
  * native/jakal_net_native.cpp:1133-1205); 1 and 2 need k <= 64.
+ * edge_layout (NULL, or jn_propagation_topk_layout_bytes(batch, nodes, topk)
+ * bytes): the forward also groups the selected edges by key for the backward,
+ * beside its row pass; pass the same buffer, unchanged, to the backward.
  * Replaces propagation_topk (native/jakal_net_native.cpp:6305-6447) and
  * low_rank_propagation_topk_forward_cuda (native/jakal_net_native.cpp:191-213).
  */
@@ -131,13 +135,23 @@ int jn_propagation_topk_forward(const float* layer_val, const float* projected_s
                                 const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                 int64_t rank, int64_t topk, int32_t compress_kind, float* delta_state,
                                 float* delta_val, float* projections, int32_t* topk_index, float* topk_score,
-                                void* workspace, size_t workspace_bytes, jn_stream_t stream);
+                                void* edge_layout, size_t edge_layout_bytes, void* workspace,
+                                size_t workspace_bytes, jn_stream_t stream);
+
+/*
+ * Size of the edge layout the top-k forwards build for their backward (no
+ * counterpart in the reference, whose backward regroups the edges itself):
+ * the edges grouped by key (segment starts, 16-byte records), each edge's
+ * record index, and the build's scratch.
+ */
+size_t jn_propagation_topk_layout_bytes(int64_t batch, int64_t nodes, int64_t topk);
 
 /* Workspace of jn_propagation_topk_forward (the select's; unused in select mode 1). */
 size_t jn_propagation_topk_forward_workspace_bytes(int64_t batch, int64_t nodes, int64_t rank);
 
 /*
- * jn_propagation_topk_forward without a workspace argument: it allocates
+ * jn_propagation_topk_forward without workspace and edge-layout arguments
+ * (no layout is built): it allocates
  * nothing and takes its scratch from a static device array of
  * jn_static_scratch_bytes() bytes (48 MiB) held by each GPU the library runs
  * on.  No counterpart in the reference: it is for callers that cannot
@@ -169,6 +183,8 @@ size_t jn_propagation_topk_workspace_bytes(int64_t batch, int64_t nodes, int64_t
  * When projected_val_is_layer_val != 0 (identity val_proj_fn) the value
  * gradient is folded into grad_layer_val and grad_projected_val is unused.
  * grad_core_weight is the gradient wrt w_hat; grad_bias a single float.
+ * edge_layout: the buffer the forward filled for this edge list, or NULL (the
+ * backward then groups the edges itself, in its workspace).
  * Deterministic: no floating-point atomics.
  * Replaces _LowRankPropagationTopK.backward (src/jakal_net/native_backend.py:4872-4964):
  * query_topk_reduce_backward_cuda, softsign_backward_cuda and
@@ -182,7 +198,8 @@ int jn_propagation_topk_backward(const float* layer_val, const float* projected_
                                  int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val,
                                  float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
                                  float* grad_source_weight, float* grad_core_weight, float* grad_bias,
-                                 void* workspace, size_t workspace_bytes, jn_stream_t stream);
+                                 const void* edge_layout, void* workspace, size_t workspace_bytes,
+                                 jn_stream_t stream);
 
 /*
  * SparsePropagation(sparse_type="window", LowRankBilinearPairwise) forward.
@@ -433,7 +450,8 @@ int jn_propagation_topk_forward_multihead(const float* layer_val, const float* p
                                           int64_t rank, int64_t heads, int64_t topk, int32_t compress_kind,
                                           float* delta_state, float* delta_val, float* projections,
                                           int32_t* topk_index, float* topk_score, uint8_t* topk_head,
-                                          void* workspace, size_t workspace_bytes, jn_stream_t stream);
+                                          void* edge_layout, size_t edge_layout_bytes, void* workspace,
+                                          size_t workspace_bytes, jn_stream_t stream);
 size_t jn_propagation_topk_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                                      int64_t rank, int64_t heads, int64_t topk);
 int jn_propagation_topk_backward_multihead(
@@ -443,7 +461,7 @@ int jn_propagation_topk_backward_multihead(
     int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t heads, int64_t topk,
     int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
     float* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
-    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+    float* grad_bias, const void* edge_layout, void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
 int jn_propagation_window_forward_multihead(const float* layer_val, const float* projected_state,
                                             const float* projected_val, const float* target_weight,
@@ -507,8 +525,9 @@ int jn_propagation_topk_forward_bf16(const uint16_t* layer_val, const float* pro
                                      const float* source_weight, const float* core_weight, const float* bias,
                                      int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
                                      int64_t topk, int32_t compress_kind, float* delta_state, uint16_t* delta_val,
-                                     float* projections, int32_t* topk_index, float* topk_score, void* workspace,
-                                     size_t workspace_bytes, jn_stream_t stream);
+                                     float* projections, int32_t* topk_index, float* topk_score, void* edge_layout,
+                                     size_t edge_layout_bytes, void* workspace, size_t workspace_bytes,
+                                     jn_stream_t stream);
 int jn_propagation_topk_backward_bf16(
     const uint16_t* layer_val, const float* projected_state, const uint16_t* projected_val,
     const float* target_weight, const float* source_weight, const float* core_weight, const float* projections,
@@ -516,7 +535,8 @@ int jn_propagation_topk_backward_bf16(
     const uint16_t* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
     int64_t topk, int32_t compress_kind, int32_t projected_val_is_layer_val, uint16_t* grad_layer_val,
     float* grad_projected_state, uint16_t* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
-    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+    float* grad_core_weight, float* grad_bias, const void* edge_layout, void* workspace, size_t workspace_bytes,
+    jn_stream_t stream);
 int jn_propagation_window_forward_bf16(const uint16_t* layer_val, const float* projected_state,
                                        const uint16_t* projected_val, const float* target_weight,
                                        const float* source_weight, const float* core_weight, const float* bias,

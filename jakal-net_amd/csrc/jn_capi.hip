@@ -189,6 +189,58 @@ PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int
   return s;
 }
 
+// Edge layout of a top-k edge list, built by the forward for its backward: the
+// edges grouped by key (CSR segments and records {row | head << 27, coef,
+// edge id, 0}), each edge's record index, and the build's own scratch.  It
+// depends only on the edge list, so the forward builds it beside its row pass.
+struct EdgeLayout {
+  int32_t* seg_start;  // [B, N + 1]
+  float4* rec;         // [B * N * k]
+  int32_t* pos;        // [B * N * k]
+  int32_t* tile_base;  // build scratch
+  float* coef;         // build scratch
+  size_t bytes;
+};
+
+EdgeLayout carve_edge_layout(void* base, size_t size, int64_t B, int64_t N, int64_t k) {
+  Workspace ws(base, size);
+  EdgeLayout l{};
+  const int64_t T = (N + kCsrTile - 1) / kCsrTile;
+  l.seg_start = ws.take<int32_t>(B * (N + 1));
+  l.rec = ws.take<float4>(B * N * k);
+  l.pos = ws.take<int32_t>(B * N * k);
+  l.tile_base = ws.take<int32_t>(B * T * N);
+  l.coef = ws.take<float>(B * N * k);
+  l.bytes = ws.used;
+  return l;
+}
+
+int build_edge_layout(const EdgeLayout& l, const int32_t* idx, const float* score, const uint8_t* ehead, int B,
+                      int N, int k, int compress_kind, hipStream_t stream) {
+  CsrArgs ca{};
+  ca.idx = idx;
+  ca.k = k;
+  ca.B = B;
+  ca.Nq = N;
+  ca.Nk = N;
+  ca.tile_base = l.tile_base;
+  ca.seg_start = l.seg_start;
+  ca.rec = l.rec;
+  ca.ehead = ehead;
+  ca.rec_eid = 1;
+  ca.pos = l.pos;
+  int rc = launch_csr_layout(ca, stream);
+  if (rc) return rc;
+  if (compress_kind == 0) {  // softsign: the fill computes each coefficient from its score
+    ca.score = score;
+  } else {  // row-normalised: the coefficients first
+    rc = launch_edge_coefficients(idx, score, (int64_t)B * N, k, compress_kind, l.coef, stream);
+    if (rc) return rc;
+    ca.coef = l.coef;
+  }
+  return launch_csr_fill(ca, stream);
+}
+
 struct TransitionScratch {
   float* coef;
   int32_t* tile_base;
@@ -530,7 +582,8 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
                                int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
                                float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
                                float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
-                               hipStream_t stream, bool bf16 = false, bool band = false) {
+                               hipStream_t stream, bool bf16 = false, bool band = false,
+                               const void* edge_layout = nullptr) {
   int rc;
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
                  projections && topk_index && topk_score && grad_delta_state && grad_delta_val &&
@@ -620,41 +673,61 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   fc.dots1 = s.coef;
   const int dot_slabs = band ? 0 : cols_gather_dots_slabs(fc);
   if (dot_slabs) {
-    // a. the CSR layout (edge index only) on the second stream beside the
-    //    edge coefficients, then the records {row, coef, edge id, coef * gds}
-    ca.g_score = nullptr;
-    ca.rec_eid = 1;
-    ca.pos = s.pos;
-    const SideStream* side = side_stream_for(st, (int64_t)M * k);
-    if (side) {
-      rc = fork_to(side, st);
+    // a. the edges grouped by key: the forward's layout, or built here (the
+    //    CSR layout reads the edge index only and runs on the second stream
+    //    beside the edge coefficients; then the records {row, coef, edge id, 0})
+    const int32_t* seg = s.seg_start;
+    const float4* rec = s.rec;
+    const int32_t* pos = s.pos;
+    if (edge_layout) {
+      const EdgeLayout l = carve_edge_layout(const_cast<void*>(edge_layout), SIZE_MAX, B, N, k);
+      seg = l.seg_start;
+      rec = l.rec;
+      pos = l.pos;
+    } else {
+      ca.g_score = nullptr;
+      ca.gds = nullptr;
+      ca.rec_eid = 1;
+      ca.pos = s.pos;
+      const SideStream* side = side_stream_for(st, (int64_t)M * k);
+      if (side) {
+        rc = fork_to(side, st);
+        if (rc) return rc;
+      }
+      rc = launch_csr_layout(ca, side ? side->stream : st);
+      if (rc) return rc;
+      if (compress_kind == 0) {  // softsign: the fill computes each coefficient from its score
+        ca.coef = nullptr;
+        ca.score = topk_score;
+      } else {
+        rc = launch_edge_coefficients(topk_index, topk_score, M, k, compress_kind, s.coef, st);
+        if (rc) return rc;
+      }
+      if (side) {
+        rc = join_from(side, st);
+        if (rc) return rc;
+      }
+      rc = launch_csr_fill(ca, st);
       if (rc) return rc;
     }
-    rc = launch_csr_layout(ca, side ? side->stream : st);
-    if (rc) return rc;
-    rc = launch_edge_coefficients(topk_index, topk_score, M, k, compress_kind, s.coef, st);
-    if (rc) return rc;
-    if (side) {
-      rc = join_from(side, st);
-      if (rc) return rc;
-    }
-    rc = launch_csr_fill(ca, st);
-    if (rc) return rc;
     // b. value and state grads of the sources, and the dot partials in record
     //    order (slab 0 into dots, slab 1 into coef)
+    fc.seg_start = seg;
+    fc.rec = rec;
+    fc.gds = grad_delta_state;
     rc = launch_cols_gather_dots(fc, st);
     if (rc) return rc;
     // c. rows: compress backward from the given dots, grad of target projection
     rb.dots_given = 1;
     rb.dot_parts = dot_slabs;
-    rb.dot_pos = s.pos;
+    rb.dot_pos = pos;
     rb.dots0 = s.dots;
     rc = launch_rows_backward(rb, st);
     if (rc) return rc;
     // d. grad of the source projection and the w_hat partials
     ColsBwdArgs kg{};
-    kg.seg_start = s.seg_start;
-    kg.rec = s.rec;
+    kg.seg_start = seg;
+    kg.rec = rec;
     kg.k = k;
     kg.q = projections;
     kg.ldq = 2 * r;
@@ -827,7 +900,8 @@ int propagation_topk_forward_impl(const float* layer_val, const float* projected
                                   const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                   int64_t rank, int64_t heads, int64_t topk, int32_t compress_kind,
                                   float* delta_state, float* delta_val, float* projections, int32_t* topk_index,
-                                  float* topk_score, uint8_t* topk_head, void* workspace, size_t workspace_bytes,
+                                  float* topk_score, uint8_t* topk_head, void* edge_layout, size_t edge_layout_bytes,
+                                  void* workspace, size_t workspace_bytes,
                                   hipStream_t st, bool bf16 = false) {
   int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
   if (rc) return rc;
@@ -893,6 +967,22 @@ int propagation_topk_forward_impl(const float* layer_val, const float* projected
     if (rc) return rc;
   }
 
+  // the edges grouped by key for the backward, beside the row pass
+  const SideStream* side = nullptr;
+  if (edge_layout) {
+    const EdgeLayout l = carve_edge_layout(edge_layout, edge_layout_bytes, batch, nodes, topk);
+    JN_REQUIRE(l.bytes <= edge_layout_bytes, kWorkspaceTooSmall, "edge layout too small: need %zu bytes, got %zu",
+               l.bytes, edge_layout_bytes);
+    side = side_stream_for(st, (int64_t)M * k);
+    if (side) {
+      rc = fork_to(side, st);
+      if (rc) return rc;
+    }
+    rc = build_edge_layout(l, topk_index, topk_score, mh ? topk_head : nullptr, (int)batch, (int)nodes, k,
+                           compress_kind, side ? side->stream : st);
+    if (rc) return rc;
+  }
+
   RowsFwdArgs f{};
   f.idx = topk_index;
   f.score = topk_score;
@@ -908,7 +998,9 @@ int propagation_topk_forward_impl(const float* layer_val, const float* projected
   f.out_state = delta_state;
   f.out_val = delta_val;
   f.bf16 = bf16 ? 1 : 0;
-  return launch_rows_forward(f, st);
+  rc = launch_rows_forward(f, st);
+  if (rc) return rc;
+  return side ? join_from(side, st) : kOk;
 }
 
 // Window propagation forward over all ranks; heads > 1 also writes each edge's head.
@@ -1003,7 +1095,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 8; }
+int jn_abi_version(void) { return 9; }
 
 int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float eps, float* weight_hat,
                           jn_stream_t stream) {
@@ -1117,11 +1209,11 @@ int jn_propagation_topk_forward(const float* layer_val, const float* projected_s
                                 const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                 int64_t rank, int64_t topk, int32_t compress_kind, float* delta_state,
                                 float* delta_val, float* projections, int32_t* topk_index, float* topk_score,
-                                void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+                                void* edge_layout, size_t edge_layout_bytes, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   return propagation_topk_forward_impl(layer_val, projected_state, projected_val, target_weight, source_weight,
                                        core_weight, bias, batch, nodes, in_dim, out_dim, rank, 1, topk, compress_kind,
                                        delta_state, delta_val, projections, topk_index, topk_score, nullptr,
-                                       workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                                       edge_layout, edge_layout_bytes, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 size_t jn_propagation_topk_forward_workspace_bytes(int64_t batch, int64_t nodes, int64_t rank) {
@@ -1134,6 +1226,11 @@ size_t jn_propagation_topk_workspace_bytes(int64_t batch, int64_t nodes, int64_t
   return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank, topk).bytes;
 }
 
+size_t jn_propagation_topk_layout_bytes(int64_t batch, int64_t nodes, int64_t topk) {
+  if (batch < 1 || nodes < 1 || topk < 1) return 0;
+  return carve_edge_layout(nullptr, 0, batch, nodes, topk).bytes;
+}
+
 int jn_propagation_topk_backward(const float* layer_val, const float* projected_state, const float* projected_val,
                                  const float* target_weight, const float* source_weight, const float* core_weight,
                                  const float* projections, const int32_t* topk_index, const float* topk_score,
@@ -1142,7 +1239,7 @@ int jn_propagation_topk_backward(const float* layer_val, const float* projected_
                                  int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val,
                                  float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
                                  float* grad_source_weight, float* grad_core_weight, float* grad_bias,
-                                 void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+                                 const void* edge_layout, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   const int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
   if (rc) return rc;
   return propagation_edges_backward(layer_val, projected_state, projected_val, target_weight, source_weight,
@@ -1150,7 +1247,7 @@ int jn_propagation_topk_backward(const float* layer_val, const float* projected_
                                     grad_delta_val, batch, nodes, in_dim, out_dim, rank, 1, topk, compress_kind,
                                     projected_val_is_layer_val, grad_layer_val, grad_projected_state,
                                     grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
-                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream), false, false, edge_layout);
 }
 
 int jn_propagation_window_forward(const float* layer_val, const float* projected_state, const float* projected_val,
@@ -1580,13 +1677,13 @@ int jn_propagation_topk_forward_multihead(const float* layer_val, const float* p
                                           int64_t rank, int64_t heads, int64_t topk, int32_t compress_kind,
                                           float* delta_state, float* delta_val, float* projections,
                                           int32_t* topk_index, float* topk_score, uint8_t* topk_head,
-                                          void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+                                          void* edge_layout, size_t edge_layout_bytes, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   const int rc = check_heads(rank, heads, true);
   if (rc) return rc;
   return propagation_topk_forward_impl(layer_val, projected_state, projected_val, target_weight, source_weight,
                                        core_weight, bias, batch, nodes, in_dim, out_dim, rank * heads, heads, topk,
                                        compress_kind, delta_state, delta_val, projections, topk_index, topk_score,
-                                       topk_head, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                                       topk_head, edge_layout, edge_layout_bytes, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int jn_propagation_topk_backward_multihead(
@@ -1596,7 +1693,7 @@ int jn_propagation_topk_backward_multihead(
     int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t heads, int64_t topk,
     int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
     float* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
-    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+    float* grad_bias, const void* edge_layout, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   int rc = check_heads(rank, heads, true);
   if (rc) return rc;
   rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank * heads, topk, compress_kind);
@@ -1606,7 +1703,7 @@ int jn_propagation_topk_backward_multihead(
                                     grad_delta_val, batch, nodes, in_dim, out_dim, rank * heads, heads, topk,
                                     compress_kind, projected_val_is_layer_val, grad_layer_val, grad_projected_state,
                                     grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight,
-                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                                    grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream), false, false, edge_layout);
 }
 
 size_t jn_propagation_window_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim,
@@ -1715,12 +1812,12 @@ int jn_propagation_topk_forward_bf16(const uint16_t* layer_val, const float* pro
                                      const float* source_weight, const float* core_weight, const float* bias,
                                      int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
                                      int64_t topk, int32_t compress_kind, float* delta_state, uint16_t* delta_val,
-                                     float* projections, int32_t* topk_index, float* topk_score, void* workspace,
-                                     size_t workspace_bytes, jn_stream_t stream) {
+                                     float* projections, int32_t* topk_index, float* topk_score, void* edge_layout,
+                                     size_t edge_layout_bytes, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   return propagation_topk_forward_impl(reinterpret_cast<const float*>(layer_val), projected_state, reinterpret_cast<const float*>(projected_val), target_weight,
                                        source_weight, core_weight, bias, batch, nodes, in_dim, out_dim, rank, 1, topk,
                                        compress_kind, delta_state, reinterpret_cast<float*>(delta_val), projections, topk_index,
-                                       topk_score, nullptr, workspace, workspace_bytes,
+                                       topk_score, nullptr, edge_layout, edge_layout_bytes, workspace, workspace_bytes,
                                        static_cast<hipStream_t>(stream), true);
 }
 
@@ -1731,7 +1828,7 @@ int jn_propagation_topk_backward_bf16(
     const uint16_t* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
     int64_t topk, int32_t compress_kind, int32_t projected_val_is_layer_val, uint16_t* grad_layer_val,
     float* grad_projected_state, uint16_t* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
-    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+    float* grad_core_weight, float* grad_bias, const void* edge_layout, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   const int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
   if (rc) return rc;
   return propagation_edges_backward(reinterpret_cast<const float*>(layer_val), projected_state, reinterpret_cast<const float*>(projected_val), target_weight,
@@ -1740,7 +1837,7 @@ int jn_propagation_topk_backward_bf16(
                                     topk, compress_kind, projected_val_is_layer_val, reinterpret_cast<float*>(grad_layer_val),
                                     grad_projected_state, reinterpret_cast<float*>(grad_projected_val), grad_target_weight,
                                     grad_source_weight, grad_core_weight, grad_bias, workspace, workspace_bytes,
-                                    static_cast<hipStream_t>(stream), true);
+                                    static_cast<hipStream_t>(stream), true, false, edge_layout);
 }
 
 int jn_propagation_window_forward_bf16(const uint16_t* layer_val, const float* projected_state,

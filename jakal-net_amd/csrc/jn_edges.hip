@@ -13,6 +13,8 @@
 // Compress kinds: 0 softsign (propagation.py:85-88), 1 signed |s| softmax over the
 // row's selected edges (propagation.py:74-82), 2 signed entmax-1.5 over them
 // (kernels.py:221-237; native/jakal_net_native.cpp:1171-1205).
+#include <algorithm>
+
 #include "jn_internal.hpp"
 
 namespace jakal {
@@ -481,121 +483,161 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Deterministic transpose (CSR by key) of the edge list.
+// Deterministic transpose (CSR by key) of the edge list: a stable counting
+// sort of the edges, in row order, by key.
 //
-// Rows are cut into tiles of 64; inside a tile a key column's incoming rows
-// form a 64-bit mask in LDS.  The position of edge (row, j) in j's segment is
-//   seg_start[j] + rows of earlier tiles hitting j + popcount(mask_j below row).
+// Rows are cut into tiles of up to 1024 rows (about one tile per CU).
+//   1. csr_count_kernel: per tile, how many of its edges reach each key (LDS
+//      counters) -> tile_base[b, t, j].
+//   2. csr_fill_kernel: per tile, from the counts of all tiles, each key's
+//      segment start (an LDS scan of the keys' degrees) and its edges from
+//      earlier tiles give an LDS cursor per key; the tile is walked in 64-row
+//      chunks, where a key's incoming rows form a 64-bit mask, so edge
+//      (row, j) lands at
+//        cursor[j] + popcount(mask_j below row)
+//      and the cursors then advance by popcount(mask_j).  Tile 0 writes the
+//      segment starts.
+// Two launches of 256-thread workgroups, so the build keeps pace beside other
+// kernels.
 // Segments therefore list incoming edges in increasing row order and every
 // reduction over them is run-to-run reproducible.  Each slot receives the
-// edge's record (row, coef, g_s, coef * gds[row]), so the column pass reads
-// one contiguous 16-byte entry per incoming edge instead of chasing edge ids.
+// edge's record (row, coef, g_s or edge id, coef * gds[row]), so the column
+// pass reads one contiguous 16-byte entry per incoming edge instead of chasing
+// edge ids.  Keys are taken in LDS slices (at most 64 KiB per workgroup).
 // ---------------------------------------------------------------------------
-constexpr int kCsrSlice = 8192;  // key columns per LDS pass (64 KiB of masks)
+constexpr int kCsrCountSlice = 8192;  // keys per LDS pass of the count (int counters)
+constexpr int kCsrFillSlice = 4096;   // keys per LDS pass of the fill (64-bit masks + int cursors)
 
-
-__device__ void csr_build_masks(const CsrArgs& a, int b, int t, int s0, int s1, unsigned long long* masks) {
-  for (int x = threadIdx.x; x < s1 - s0; x += blockDim.x) masks[x] = 0ull;
-  __syncthreads();
-  const int r0 = t * kCsrTile;
-  const int nrows = min(kCsrTile, a.Nq - r0);
-  for (int x = threadIdx.x; x < nrows * a.k; x += blockDim.x) {
-    int rl = x / a.k;
-    int j = a.idx[((int64_t)b * a.Nq + r0 + rl) * a.k + (x % a.k)];
-    if (j >= s0 && j < s1) atomicOr(&masks[j - s0], 1ull << rl);
-  }
-  __syncthreads();
+// Rows per tile: whole 64-row chunks, about 256 tiles over the batch, at most
+// 1024 rows (tile_base then has at most B * ceil(Nq / 64) * Nk entries).
+static int csr_tile_rows(int64_t B, int64_t Nq) {
+  const int64_t want = (B * Nq + 255) / 256;
+  return (int)std::min<int64_t>(1024, std::max<int64_t>(kCsrTile, (want + kCsrTile - 1) / kCsrTile * kCsrTile));
+}
+static int csr_tiles(const CsrArgs& a) {
+  const int tr = csr_tile_rows(a.B, a.Nq);
+  return (a.Nq + tr - 1) / tr;
 }
 
-__global__ __launch_bounds__(256) void csr_count_kernel(CsrArgs a) {
-  __shared__ unsigned long long masks[kCsrSlice];
-  const int t = blockIdx.x, b = blockIdx.y;
-  const int T = gridDim.x;
-  for (int s0 = 0; s0 < a.Nk; s0 += kCsrSlice) {
-    const int s1 = min(a.Nk, s0 + kCsrSlice);
-    csr_build_masks(a, b, t, s0, s1, masks);
-    for (int x = threadIdx.x; x < s1 - s0; x += blockDim.x)
-      a.tile_base[((int64_t)b * T + t) * a.Nk + s0 + x] = __popcll(masks[x]);
+__global__ __launch_bounds__(256) void csr_count_kernel(CsrArgs a, int tile_rows) {
+  extern __shared__ int cnt[];  // min(Nk, kCsrCountSlice) counters
+  const int t = blockIdx.x, b = blockIdx.y, T = gridDim.x;
+  const int r0 = t * tile_rows, nrows = min(tile_rows, a.Nq - r0);
+  const int32_t* idx = a.idx + ((int64_t)b * a.Nq + r0) * a.k;
+  const int ne = nrows * a.k;
+  int32_t* out = a.tile_base + ((int64_t)b * T + t) * a.Nk;
+  for (int s0 = 0; s0 < a.Nk; s0 += kCsrCountSlice) {
+    const int s1 = min(a.Nk, s0 + kCsrCountSlice);
+    for (int x = threadIdx.x; x < s1 - s0; x += blockDim.x) cnt[x] = 0;
+    __syncthreads();
+    for (int x = threadIdx.x; x < ne; x += blockDim.x) {
+      const int j = idx[x];
+      if (j >= s0 && j < s1) atomicAdd(&cnt[j - s0], 1);
+    }
+    __syncthreads();
+    for (int x = threadIdx.x; x < s1 - s0; x += blockDim.x) out[s0 + x] = cnt[x];
     __syncthreads();
   }
 }
 
-// Exclusive scan over tiles for every (b, key); the total is the key's in-degree.
-__global__ void csr_tile_scan_kernel(CsrArgs a, int T) {
-  int64_t x = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (x >= (int64_t)a.B * a.Nk) return;
-  int b = (int)(x / a.Nk), j = (int)(x % a.Nk);
-  int run = 0;
-  for (int t = 0; t < T; ++t) {
-    int32_t* p = a.tile_base + ((int64_t)b * T + t) * a.Nk + j;
-    int c = *p;
-    *p = run;
-    run += c;
-  }
-  a.seg_start[(int64_t)b * (a.Nk + 1) + j] = run;  // degree, scanned next
-}
-
-// In-place exclusive scan of the degrees of one batch element (one workgroup).
-__global__ __launch_bounds__(1024) void csr_segment_scan_kernel(CsrArgs a) {
-  __shared__ int warp_tot[16];
-  __shared__ int carry;
-  const int b = blockIdx.x;
-  int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
-  if (threadIdx.x == 0) carry = 0;
-  __syncthreads();
+// Exclusive scan of v[0..n) in LDS by one 256-thread workgroup (16 entries
+// per thread, n <= 4096); returns the total.  Every thread must call it.
+__device__ int lds_exclusive_scan(int* v, int n, int* wave_tot) {
+  constexpr int PER = kCsrFillSlice / 256;
   const int lane = lane_id(), wave = wave_id();
-  for (int base = 0; base < a.Nk; base += 1024) {
-    int x = base + threadIdx.x;
-    int v = x < a.Nk ? seg[x] : 0;
-    // inclusive wave scan
-    int s = v;
+  const int x0 = threadIdx.x * PER;
+  int mine = 0;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      int y = __builtin_amdgcn_ds_bpermute(((lane - o) & 63) << 2, s);
-      if (lane >= o) s += y;
-    }
-    if (lane == 63) warp_tot[wave] = s;
-    __syncthreads();
-    int woff = 0;
-    for (int w = 0; w < wave; ++w) woff += warp_tot[w];
-    int excl = carry + woff + s - v;
-    __syncthreads();
-    if (x < a.Nk) seg[x] = excl;
-    if (threadIdx.x == 1023) carry = excl + v;
-    __syncthreads();
+  for (int u = 0; u < PER; ++u) mine += (x0 + u < n) ? v[x0 + u] : 0;
+  int incl = mine;  // inclusive wave scan of the threads' sums
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __builtin_amdgcn_ds_bpermute(((lane - o) & 63) << 2, incl);
+    if (lane >= o) incl += y;
   }
-  if (threadIdx.x == 0) seg[a.Nk] = carry;
+  if (lane == kWave - 1) wave_tot[wave] = incl;
+  __syncthreads();
+  int run = incl - mine;
+  for (int w = 0; w < wave; ++w) run += wave_tot[w];
+  const int total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    if (x0 + u < n) {
+      const int c = v[x0 + u];
+      v[x0 + u] = run;
+      run += c;
+    }
+  }
+  __syncthreads();  // wave_tot and v are reused by the caller
+  return total;
 }
 
-__global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs a) {
-  __shared__ unsigned long long masks[kCsrSlice];
-  const int t = blockIdx.x, b = blockIdx.y;
-  const int T = gridDim.x;
-  const int r0 = t * kCsrTile;
-  const int nrows = min(kCsrTile, a.Nq - r0);
+__global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs a, int tile_rows) {
+  extern __shared__ unsigned long long lds[];  // min(Nk, kCsrFillSlice) masks, then as many int cursors
+  __shared__ int wave_tot[4];
+  const int slice = min(a.Nk, kCsrFillSlice);
+  unsigned long long* masks = lds;
+  int* cursor = reinterpret_cast<int*>(lds + slice);
+  const int t = blockIdx.x, b = blockIdx.y, T = gridDim.x;
+  const int r0 = t * tile_rows, nrows = min(tile_rows, a.Nq - r0);
   const int64_t batch_base = (int64_t)b * a.Nq * a.k;
-  const int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
-  for (int s0 = 0; s0 < a.Nk; s0 += kCsrSlice) {
-    const int s1 = min(a.Nk, s0 + kCsrSlice);
-    csr_build_masks(a, b, t, s0, s1, masks);
-    for (int x = threadIdx.x; x < nrows * a.k; x += blockDim.x) {
-      int rl = x / a.k;
-      int64_t eid = ((int64_t)b * a.Nq + r0 + rl) * a.k + (x % a.k);
-      int j = a.idx[eid];
-      if (j >= s0 && j < s1) {
-        unsigned long long below = masks[j - s0] & ((1ull << rl) - 1ull);
-        int pos = seg[j] + a.tile_base[((int64_t)b * T + t) * a.Nk + j] + __popcll(below);
-        const int row = b * a.Nq + r0 + rl;
-        const float cf = a.coef ? a.coef[eid] : 0.f;
-        const float gs = a.rec_eid ? __int_as_float((int)eid) : (a.g_score ? a.g_score[eid] : 0.f);
-        const float cd = a.gds ? cf * a.gds[row] : 0.f;
-        const int hd = a.ehead ? (int)a.ehead[eid] << kRecHeadShift : 0;
-        a.rec[batch_base + pos] = make_float4(__int_as_float(row | hd), cf, gs, cd);
-        if (a.pos) a.pos[eid] = (int32_t)(batch_base + pos);
+  const int32_t* cnt = a.tile_base + (int64_t)b * T * a.Nk;  // [T, Nk] edge counts of the tiles
+  int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
+  int carry = 0;  // edges into the keys of earlier slices
+  for (int s0 = 0; s0 < a.Nk; s0 += kCsrFillSlice) {
+    const int s1 = min(a.Nk, s0 + kCsrFillSlice), ns = s1 - s0;
+    // per key: edges from earlier tiles (kept in the mask slots for now) and its degree
+    for (int x = threadIdx.x; x < ns; x += blockDim.x) {
+      int before = 0, deg = 0;
+      for (int tt = 0; tt < T; ++tt) {
+        const int c = cnt[(int64_t)tt * a.Nk + s0 + x];
+        before += tt < t ? c : 0;
+        deg += c;
       }
+      masks[x] = (unsigned long long)before;
+      cursor[x] = deg;
     }
     __syncthreads();
+    // segment starts: exclusive scan of the degrees, after the earlier slices
+    const int total = lds_exclusive_scan(cursor, ns, wave_tot);
+    for (int x = threadIdx.x; x < ns; x += blockDim.x) {
+      const int start = carry + cursor[x];
+      if (t == 0) seg[s0 + x] = start;
+      cursor[x] = start + (int)masks[x];
+    }
+    carry += total;
+    __syncthreads();
+    for (int c0 = 0; c0 < nrows; c0 += 64) {
+      const int crows = min(64, nrows - c0);
+      const int64_t e0 = ((int64_t)b * a.Nq + r0 + c0) * a.k;  // the chunk's first edge
+      for (int x = threadIdx.x; x < ns; x += blockDim.x) masks[x] = 0ull;
+      __syncthreads();
+      for (int x = threadIdx.x; x < crows * a.k; x += blockDim.x) {
+        const int j = a.idx[e0 + x];
+        if (j >= s0 && j < s1) atomicOr(&masks[j - s0], 1ull << (x / a.k));
+      }
+      __syncthreads();
+      for (int x = threadIdx.x; x < crows * a.k; x += blockDim.x) {
+        const int64_t eid = e0 + x;
+        const int j = a.idx[eid];
+        if (j >= s0 && j < s1) {
+          const int rl = x / a.k;
+          const int pos = cursor[j - s0] + __popcll(masks[j - s0] & ((1ull << rl) - 1ull));
+          const int row = b * a.Nq + r0 + c0 + rl;
+          const float cf = a.coef ? a.coef[eid] : (a.score ? softsign_f(a.score[eid]) : 0.f);
+          const float gs = a.rec_eid ? __int_as_float((int)eid) : (a.g_score ? a.g_score[eid] : 0.f);
+          const float cd = a.gds ? cf * a.gds[row] : 0.f;
+          const int hd = a.ehead ? (int)a.ehead[eid] << kRecHeadShift : 0;
+          a.rec[batch_base + pos] = make_float4(__int_as_float(row | hd), cf, gs, cd);
+          if (a.pos) a.pos[eid] = (int32_t)(batch_base + pos);
+        }
+      }
+      __syncthreads();
+      for (int x = threadIdx.x; x < ns; x += blockDim.x) cursor[x] += __popcll(masks[x]);
+      __syncthreads();
+    }
   }
+  if (t == 0 && threadIdx.x == 0) seg[a.Nk] = carry;
 }
 
 int launch_csr(const CsrArgs& a, hipStream_t stream) {
@@ -605,35 +647,24 @@ int launch_csr(const CsrArgs& a, hipStream_t stream) {
 }
 
 int launch_csr_layout(const CsrArgs& a, hipStream_t stream) {
-  const int T = (a.Nq + kCsrTile - 1) / kCsrTile;
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
   JN_REQUIRE((int64_t)a.B * a.Nq <= kRecRowMask, kUnsupported,
              "edge records hold rows below 2^%d (B * rows = %lld)", kRecHeadShift, (long long)a.B * a.Nq);
-  dim3 g2(T, a.B);
-  {
-    JN_PROFILE("csr_count_kernel", stream);
-    hipLaunchKernelGGL(csr_count_kernel, g2, dim3(256), 0, stream, a);
-    JN_LAUNCH_CHECK();
-  }
-  const int64_t n = (int64_t)a.B * a.Nk;
-  {
-    JN_PROFILE("csr_tile_scan_kernel", stream);
-    hipLaunchKernelGGL(csr_tile_scan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, T);
-    JN_LAUNCH_CHECK();
-  }
-  {
-    JN_PROFILE("csr_segment_scan_kernel", stream);
-    hipLaunchKernelGGL(csr_segment_scan_kernel, dim3(a.B), dim3(1024), 0, stream, a);
-    JN_LAUNCH_CHECK();
-  }
+  dim3 g2(csr_tiles(a), a.B);
+  JN_PROFILE("csr_count_kernel", stream);
+  hipLaunchKernelGGL(csr_count_kernel, g2, dim3(256), (size_t)min(a.Nk, kCsrCountSlice) * sizeof(int), stream, a,
+                     csr_tile_rows(a.B, a.Nq));
+  JN_LAUNCH_CHECK();
   return kOk;
 }
 
 int launch_csr_fill(const CsrArgs& a, hipStream_t stream) {
-  const int T = (a.Nq + kCsrTile - 1) / kCsrTile;
-  dim3 g2(T, a.B);
+  JN_REQUIRE(!a.score || a.compress == 0, kInvalidArgument, "records take inline coefficients for softsign only");
+  dim3 g2(csr_tiles(a), a.B);
   JN_PROFILE("csr_fill_kernel", stream);
-  hipLaunchKernelGGL(csr_fill_kernel, g2, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(csr_fill_kernel, g2, dim3(256),
+                     (size_t)min(a.Nk, kCsrFillSlice) * (sizeof(unsigned long long) + sizeof(int)), stream, a,
+                     csr_tile_rows(a.B, a.Nq));
   JN_LAUNCH_CHECK();
   return kOk;
 }
@@ -851,7 +882,7 @@ __global__ __launch_bounds__(256) void cols_gather_dots_kernel(ColsBwdArgs a) {
       const uint4 r = load_nt16(recs.rec + q0 + lane);
       row = (int)r.x & kRecRowMask;
       cf = __uint_as_float(r.y);
-      st += __uint_as_float(r.w);
+      if (a.gds) st += cf * a.gds[row];
     }
     for (int q = 0; q < n; q += G) {  // n and q are wave-uniform
       // the group's rows as raw 16-byte packs (widened where used)

@@ -300,7 +300,7 @@ struct CsrArgs {
   const int32_t* idx;
   int k;
   int B, Nq, Nk;
-  int32_t* tile_base;  // [B, T, Nk]: per-tile counts, then exclusive bases
+  int32_t* tile_base;  // [B, T, Nk], T <= ceil(Nq / kCsrTile): per-tile edge counts
   int32_t* seg_start;  // [B, Nk + 1]
   // [B * Nq * k] edge records grouped by key: {row | head << kRecHeadShift
   // (int bits), coef[e], g_score[e], coef[e] * gds[row]}; a null source
@@ -312,6 +312,9 @@ struct CsrArgs {
   const uint8_t* ehead;  // [B * Nq, k] head of each edge, or null (head 0)
   int rec_eid;           // 1: record word 2 holds the edge id (int bits) instead of g_score[e]
   int32_t* pos;          // [B * Nq * k] or null: each edge's record index (batch offset included)
+  // Without coef: record coefficients softsign(score[e]) (compress kind 0 only)
+  const float* score;    // [B * Nq, k] or null
+  int compress;
 };
 constexpr int kCsrTile = 64;
 // An edge record's first word holds its row below bit kRecHeadShift and its
@@ -319,8 +322,8 @@ constexpr int kCsrTile = 64;
 constexpr int kRecHeadShift = 27;
 constexpr int kRecRowMask = (1 << kRecHeadShift) - 1;
 int launch_csr(const CsrArgs& a, hipStream_t stream);
-// The two halves of launch_csr: the layout (per-tile counts, tile bases and
-// segment starts; reads only the edge index) and the record fill (reads the
+// The two halves of launch_csr: the layout (per-tile edge counts; reads only
+// the edge index) and the fill (segment starts and records; reads the
 // coefficients, score gradients and state gradients as well).
 int launch_csr_layout(const CsrArgs& a, hipStream_t stream);
 int launch_csr_fill(const CsrArgs& a, hipStream_t stream);
@@ -369,7 +372,7 @@ struct ColsBwdArgs {
   int band;
   const float* coef;         // [B * Nq, k]
   const float* g_score;      // [B * Nq, k]
-  const float* gds;          // [B * Nq] or null (record word 3 is then 0)
+  const float* gds;          // [B * Nq] or null (band records: word 3 is then 0; fused pass: grad_ps sums coef * gds[row])
   const uint8_t* ehead;      // [B * Nq, k] or null (head 0)
   // CSR records whose word 2 is the edge id (CsrArgs::rec_eid): the key
   // gradient reads g_score[id].

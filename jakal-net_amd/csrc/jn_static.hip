@@ -76,7 +76,7 @@ int jn_propagation_topk_forward_static(const float* layer_val, const float* proj
   if (rc) return rc;
   return jn_propagation_topk_forward(layer_val, projected_state, projected_val, target_weight, source_weight,
                                      core_weight, bias, batch, nodes, in_dim, out_dim, rank, topk, compress_kind,
-                                     delta_state, delta_val, projections, topk_index, topk_score, ws,
+                                     delta_state, delta_val, projections, topk_index, topk_score, nullptr, 0, ws,
                                      kStaticScratchBytes, stream);
 }
 

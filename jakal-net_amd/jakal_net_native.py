@@ -60,14 +60,16 @@ _declare(
 _declare("jn_lowrank_topk_select_workspace_bytes", [_I64] * 3, _SZ)
 _declare(
     "jn_propagation_topk_forward",
-    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P,
+     _P, _SZ, _P, _SZ, _P],
 )
 _declare("jn_propagation_topk_forward_workspace_bytes", [_I64] * 3, _SZ)
+_declare("jn_propagation_topk_layout_bytes", [_I64] * 3, _SZ)
 _declare("jn_propagation_topk_workspace_bytes", [_I64, _I64, _I64, _I64, _I64, _I64], _SZ)
 _declare(
     "jn_propagation_topk_backward",
     [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
-     _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+     _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 _declare(
     "jn_propagation_window_forward",
@@ -128,14 +130,14 @@ _declare(
 _declare("jn_propagation_topk_forward_multihead_workspace_bytes", [_I64] * 4, _SZ)
 _declare(
     "jn_propagation_topk_forward_multihead",
-    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ,
-     _P],
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P,
+     _P, _SZ, _P, _SZ, _P],
 )
 _declare("jn_propagation_topk_multihead_workspace_bytes", [_I64] * 7, _SZ)
 _declare(
     "jn_propagation_topk_backward_multihead",
     [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
-     _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+     _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 _declare(
     "jn_propagation_window_forward_multihead",
@@ -367,13 +369,24 @@ class _PropagationEdges(torch.autograd.Function):
             ]
             if mh:
                 args.append(_ptr(head))
-            if mode == "topk":  # the select's scratch
+            layout = None
+            if mode == "topk":
+                # the edges grouped by key for the backward, built beside the
+                # forward's row pass when a backward will follow
+                if EDGE_LAYOUT and any(ctx.needs_input_grad[:7]):
+                    layout_bytes = int(_LIB.jn_propagation_topk_layout_bytes(B, N, k))
+                    layout = torch.empty(layout_bytes, device=dev, dtype=torch.uint8)
+                    args += [_ptr(layout), layout_bytes]
+                else:
+                    args += [None, 0]
+                # the select's scratch
                 ws_bytes = int(_LIB.jn_propagation_topk_forward_multihead_workspace_bytes(B, N, *rank_arg) if mh
                                else _LIB.jn_propagation_topk_forward_workspace_bytes(B, N, r))
                 ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
                 args += [_ptr(ws), ws_bytes]
             _check(fwd(*args, _stream(dev)))
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, idx, score, head)
+        ctx.edge_layout = layout
         ctx.meta = (mode, param, compress, pv_is_x, bias is not None, heads, bf16)
         ctx.mark_non_differentiable(idx, score)
         ctx.set_materialize_grads(False)  # no zero-filled gradients for the edge-list outputs
@@ -405,13 +418,14 @@ class _PropagationEdges(torch.autograd.Function):
             ws_bytes = int(getattr(_LIB, ws_name)(B, N, Din, Dout, *rank_arg, param))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
             edge_args = [_ptr(idx), _ptr(score)] + ([_ptr(head)] if mh else [])
+            layout_arg = [_ptr(ctx.edge_layout)] if mode == "topk" else []
             _check(
                 getattr(_LIB, bwd_name)(
                     _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat),
                     _ptr(proj), *edge_args, _ptr(g_ds), _ptr(g_dv),
                     B, N, Din, Dout, *rank_arg, param, compress, 1 if pv_is_x else 0,
                     _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
-                    _ptr(ws), ws_bytes, _stream(dev),
+                    *layout_arg, _ptr(ws), ws_bytes, _stream(dev),
                 )
             )
         return (
@@ -476,6 +490,18 @@ def _bf16_rows(*tensors: Tensor | None) -> bool:
 
 def _bf16(t: Tensor | None) -> Tensor | None:
     return None if t is None else t.contiguous()
+
+
+EDGE_LAYOUT = True  # top-k forwards group their edges by key for the backward
+
+
+def set_edge_layout(on: bool = True) -> None:
+    """Whether top-k propagation forwards that a backward will follow build the
+    edge layout (the edges grouped by key) beside their row pass and hand it to
+    the backward (True, the default), or leave the grouping to the backward.
+    Results are identical either way."""
+    global EDGE_LAYOUT
+    EDGE_LAYOUT = bool(on)
 
 
 DENSE_EDGE_BYTES = 512 << 20  # edge-matrix bytes above which dense propagation runs in batch chunks

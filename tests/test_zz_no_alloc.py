@@ -23,7 +23,7 @@ def _lib():
     import jakal_net_native as jn
 
     lib = ctypes.CDLL(str(jn.library_path()))
-    lib.jn_propagation_topk_forward.argtypes = _FWD_ARGS + [_P, _SZ, _P]
+    lib.jn_propagation_topk_forward.argtypes = _FWD_ARGS + [_P, _SZ, _P, _SZ, _P]  # layout, workspace, stream
     lib.jn_propagation_topk_forward_static.argtypes = _FWD_ARGS + [_P]
     lib.jn_propagation_topk_forward_workspace_bytes.argtypes = [_I64] * 3
     lib.jn_propagation_topk_forward_workspace_bytes.restype = _SZ
@@ -50,7 +50,7 @@ def _run(lib, static, X, ps, U, V, w_hat, bias, k, compress):
     else:
         ws_bytes = int(lib.jn_propagation_topk_forward_workspace_bytes(B, N, r))
         ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
-        rc = lib.jn_propagation_topk_forward(*args, p(ws), ws_bytes, stream)
+        rc = lib.jn_propagation_topk_forward(*args, None, 0, p(ws), ws_bytes, stream)  # no edge layout
     assert rc == 0, lib.jn_last_error().decode()
     torch.cuda.synchronize()
     return ds, dv, proj, idx, score

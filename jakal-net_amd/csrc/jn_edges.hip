@@ -19,6 +19,31 @@
 
 namespace jakal {
 
+// Streaming accesses (read or written once): non-temporal, so they do not
+// displace the gathered rows from L2.
+typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+  const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void store_nt16(void* p, uint4 x) {
+  u32x4_nt v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_nt*>(p));
+}
+
+// A 16-byte pack as its raw bits (stored as computed: fp32, or bf16 rounded).
+template <typename T, int W>
+__device__ __forceinline__ uint4 pack_bits(const Pack<W>& g) {
+  static_assert(W * sizeof(T) == 16, "a 16-byte pack");
+  if constexpr (sizeof(T) == 4) {
+    return make_uint4(__float_as_uint(g.v[0]), __float_as_uint(g.v[1]), __float_as_uint(g.v[2]),
+                      __float_as_uint(g.v[3]));
+  } else {
+    return make_uint4(pack_bf16x2(g.v[0], g.v[1]), pack_bf16x2(g.v[2], g.v[3]), pack_bf16x2(g.v[4], g.v[5]),
+                      pack_bf16x2(g.v[6], g.v[7]));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Row forward: one wavefront per query row.
 // ---------------------------------------------------------------------------
@@ -77,7 +102,12 @@ __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
       }
       acc = add_pack(acc, acc1);
       if (e0 > 0) acc = add_pack(acc, load_pack<T, W>(out + d));
-      store_pack<T, W>(out + d, acc);
+      if constexpr (W * sizeof(T) == 16) {
+        if (a.k <= kWave) store_nt16(out + d, pack_bits<T, W>(acc));  // the row's only pass: written once
+        else store_pack<T, W>(out + d, acc);
+      } else {
+        store_pack<T, W>(out + d, acc);
+      }
     }
   }
   if (slab == 0) {
@@ -829,18 +859,6 @@ __device__ __forceinline__ float transpose_sum(const float (&v)[G]) {
   else return transpose_sum4(v);
 }
 
-// Streaming accesses (read or written once): non-temporal, so they do not
-// displace the gathered rows from L2.
-typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 load_nt16(const void* p) {
-  const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-__device__ __forceinline__ void store_nt16(void* p, uint4 x) {
-  u32x4_nt v = {x.x, x.y, x.z, x.w};
-  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_nt*>(p));
-}
-
 // Fused column pass: one wavefront per key column and slab of kWave * W
 // columns (one 16-byte pack per lane), slab-major over the grid as in
 // cols_gather_kernel.  Each incoming edge's gdv row (slab) is read once and
@@ -909,17 +927,8 @@ __global__ __launch_bounds__(256) void cols_gather_dots_kernel(ColsBwdArgs a) {
       if (writer) part[rec0 + ru] = tot;  // record order: consecutive records, consecutive slots
     }
   }
-  if (a.grad_pv && on) {
-    const Pack<W> g = add_pack(acc, acc1);
-    uint4 x;
-    if constexpr (sizeof(T) == 4) {
-      x = make_uint4(__float_as_uint(g.v[0]), __float_as_uint(g.v[1]), __float_as_uint(g.v[2]), __float_as_uint(g.v[3]));
-    } else {
-      x = make_uint4(pack_bf16x2(g.v[0], g.v[1]), pack_bf16x2(g.v[2], g.v[3]), pack_bf16x2(g.v[4], g.v[5]),
-                     pack_bf16x2(g.v[6], g.v[7]));
-    }
-    store_nt16(reinterpret_cast<T*>(a.grad_pv) + col * a.ld_gpv + d, x);
-  }
+  if (a.grad_pv && on)
+    store_nt16(reinterpret_cast<T*>(a.grad_pv) + col * a.ld_gpv + d, pack_bits<T, W>(add_pack(acc, acc1)));
   if (slab == 0 && a.grad_ps) {
     st = wave_sum(st);
     if (lane == 0) a.grad_ps[col] = st;

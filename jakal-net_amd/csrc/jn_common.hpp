@@ -376,6 +376,28 @@ __device__ __forceinline__ void store_pack(T* p, const Pack<W>& x) {
   }
 }
 
+// Streaming accesses (data read or written once): non-temporal, so they do
+// not displace data that is reused (gathered rows, GEMM operands) from L2.
+typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+  const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void store_nt16(void* p, uint4 x) {
+  u32x4_nt v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_nt*>(p));
+}
+
+typedef unsigned int u32x2_nt __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 load_nt8(const void* p) {
+  const u32x2_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_nt*>(p));
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ void store_nt8(void* p, uint2 x) {
+  u32x2_nt v = {x.x, x.y};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x2_nt*>(p));
+}
+
 // W elements at a byte offset of a buffer (zeros when out of range).
 template <typename T, int W>
 __device__ __forceinline__ Pack<W> buf_load_pack(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {

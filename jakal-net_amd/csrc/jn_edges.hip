@@ -19,18 +19,6 @@
 
 namespace jakal {
 
-// Streaming accesses (read or written once): non-temporal, so they do not
-// displace the gathered rows from L2.
-typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 load_nt16(const void* p) {
-  const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-__device__ __forceinline__ void store_nt16(void* p, uint4 x) {
-  u32x4_nt v = {x.x, x.y, x.z, x.w};
-  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_nt*>(p));
-}
-
 // A 16-byte pack as its raw bits (stored as computed: fp32, or bf16 rounded).
 template <typename T, int W>
 __device__ __forceinline__ uint4 pack_bits(const Pack<W>& g) {

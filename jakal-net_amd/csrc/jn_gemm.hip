@@ -699,16 +699,25 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
             const float sm = mscale[m];
             x.x *= sm; x.y *= sm; x.z *= sm; x.w *= sm;
           }
+          // the input gradient and its addend are read and written once: non-temporal
+          constexpr bool NT = USE == kGemmGradInput || USE == kGemmGradInputBf16;
           if constexpr (C_BF) {
             if (gaddb) {
-              const uint2 ab = *reinterpret_cast<const uint2*>(&gaddb[(int64_t)m * g.ld_add + n]);
+              const uint2 ab = load_nt8(&gaddb[(int64_t)m * g.ld_add + n]);
               float4 a;
               unpack_bf16x2(ab.x, a.x, a.y);
               unpack_bf16x2(ab.y, a.z, a.w);
               x.x += a.x; x.y += a.y; x.z += a.z; x.w += a.w;
             }
-            *reinterpret_cast<uint2*>(&Cb[(int64_t)m * g.ldc + n]) =
-                make_uint2(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w));
+            store_nt8(&Cb[(int64_t)m * g.ldc + n], make_uint2(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w)));
+          } else if constexpr (NT) {
+            if (gadd) {
+              const uint4 ab = load_nt16(&gadd[(int64_t)m * g.ld_add + n]);
+              x.x += __uint_as_float(ab.x); x.y += __uint_as_float(ab.y);
+              x.z += __uint_as_float(ab.z); x.w += __uint_as_float(ab.w);
+            }
+            store_nt16(&C[(int64_t)m * g.ldc + n],
+                       make_uint4(__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z), __float_as_uint(x.w)));
           } else {
             if (gadd) {
               const float4 a = *reinterpret_cast<const float4*>(&gadd[(int64_t)m * g.ld_add + n]);

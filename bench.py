@@ -87,7 +87,18 @@ def rows_backward_split(nk: int, D: int, vb: int = 4) -> bool:
     return 256 < D <= 1024 and nk * D * vb > (2 << 20)
 
 
-def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = False,
+def fused_column_slabs(D: int, vb: int = 4) -> int:
+    """Column slabs of the fused column pass of a top-k backward
+    (cols_gather_dots_kernel: 64 lanes x 16 bytes per slab), 0 when it does not
+    apply (rows not whole 16-byte packs, or more than two slabs;
+    jn_edges.hip, cols_gather_dots_slabs)."""
+    if (D * vb) % 16:
+        return 0
+    slabs = -(-D * vb // 1024)
+    return slabs if slabs <= 2 else 0
+
+
+def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool | str = False,
                       Mk: int | None = None, vb: float = 4.0) -> tuple | None:
     """(bound, algorithmic bytes or flops, compulsory bytes) of the edge-list kernels.
 
@@ -98,7 +109,8 @@ def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = F
     and each output once: the HBM bytes no schedule can avoid.  The gathers
     reuse each value row about k times from L2, so their algorithmic rate is an
     L2-side figure and their HBM roofline fraction is priced on compulsory bytes.
-    split: the row backward runs as dots + finish.  vb: bytes per value-row
+    split: the row backward runs as dots + finish ("fused": its dots come from
+    the fused column pass, read through the record indices).  vb: bytes per value-row
     element (4 fp32, 2 bf16); projections, scores and edge records stay fp32."""
     Mk = M if Mk is None else Mk
     D4 = vb * D  # bytes of one value row
@@ -110,7 +122,24 @@ def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool = F
         # idx, pv row, partial-dot write per edge; grad-delta row per row
         return ("hbm", E * (4.0 + D4 + 4.0) + M * D4,
                 E * 12.0 + (M + Mk) * D4)
+    if name.startswith("cols_gather_dots_kernel"):
+        # per edge and slab: record, grad-delta row slab, gds[row], partial-dot write;
+        # per column: segment bounds, pv row, grad_pv row, grad_ps
+        slabs = max(1, fused_column_slabs(D, int(vb)))
+        return ("hbm", E * (slabs * 24.0 + D4) + Mk * (8.0 + 2.0 * D4 + 4.0),
+                E * (16.0 + 4.0 * slabs) + M * (D4 + 4.0) + Mk * (2.0 * D4 + 8.0))
+    if name.startswith("csr_count_kernel"):
+        # edge index per edge; per-tile counts of every key
+        return ("hbm", E * 4.0, E * 4.0)
+    if name.startswith("csr_fill_kernel"):
+        # edge index twice, score, record and record index per edge
+        return ("hbm", E * (4.0 * 2 + 4.0 + 16.0 + 4.0), E * (4.0 + 4.0 + 16.0 + 4.0))
     if name.startswith("rows_backward_kernel"):
+        if split == "fused":
+            # idx+score, record index, two partial dots, ps, key row, gsc write per edge;
+            # grad-delta state, dq row, row sum per row
+            return ("hbm", E * (8.0 + 4.0 + 8.0 + 4.0 + 4.0 * r + 4.0) + M * (4.0 + 4.0 * r + 4.0),
+                    E * 28.0 + Mk * (4.0 + 4.0 * r) + M * (8.0 + 4.0 * r))
         if split:
             # idx+score, two partial dots, ps, key row, gsc+coef writes per edge;
             # grad-delta state, dq row, row sum per row
@@ -160,7 +189,8 @@ def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int, bf16: bool =
         rp = -(-r // 32) * 32
         return "hbm", B * N * (4.0 * r + 2.0 * rp), B * N * (4.0 * r + 2.0 * rp)
     vb = 2 if bf16 else 4
-    return edge_kernel_model(name, B * N, B * N * k, D, r, rows_backward_split(N, D, vb), vb=float(vb))
+    split = "fused" if fused_column_slabs(D, vb) else rows_backward_split(N, D, vb)
+    return edge_kernel_model(name, B * N, B * N * k, D, r, split, vb=float(vb))
 
 
 def _cpu_model() -> str:

@@ -172,7 +172,7 @@ PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int
   Workspace ws(base, size);
   PropBwdScratch s{};
   const int64_t M = B * N;
-  const int64_t T = (N + kCsrTile - 1) / kCsrTile;
+  const int64_t T = csr_tiles(B, N);
   s.dP = ws.take<float>(M * 2 * r);
   s.g_score = ws.take<float>(M * k);
   s.coef = ws.take<float>(M * k);
@@ -205,7 +205,7 @@ struct EdgeLayout {
 EdgeLayout carve_edge_layout(void* base, size_t size, int64_t B, int64_t N, int64_t k) {
   Workspace ws(base, size);
   EdgeLayout l{};
-  const int64_t T = (N + kCsrTile - 1) / kCsrTile;
+  const int64_t T = csr_tiles(B, N);
   l.seg_start = ws.take<int32_t>(B * (N + 1));
   l.rec = ws.take<float4>(B * N * k);
   l.pos = ws.take<int32_t>(B * N * k);
@@ -266,7 +266,7 @@ TransitionScratch carve_transition(void* base, size_t size, int64_t B, int64_t N
                                    int64_t Ddst, int64_t r, int64_t k, int64_t heads = 1) {
   Workspace ws(base, size);
   TransitionScratch s{};
-  const int64_t T = (Ns + kCsrTile - 1) / kCsrTile;
+  const int64_t T = csr_tiles(B, Ns);
   s.coef = ws.take<float>(B * Ns * k);
   s.tile_base = ws.take<int32_t>(B * T * Nd);
   s.seg_start = ws.take<int32_t>(B * (Nd + 1));

@@ -528,14 +528,11 @@ constexpr int kCsrFillSlice = 4096;   // keys per LDS pass of the fill (64-bit m
 
 // Rows per tile: whole 64-row chunks, about 256 tiles over the batch, at most
 // 1024 rows (tile_base then has at most B * ceil(Nq / 64) * Nk entries).
-static int csr_tile_rows(int64_t B, int64_t Nq) {
+int csr_tile_rows(int64_t B, int64_t Nq) {
   const int64_t want = (B * Nq + 255) / 256;
   return (int)std::min<int64_t>(1024, std::max<int64_t>(kCsrTile, (want + kCsrTile - 1) / kCsrTile * kCsrTile));
 }
-static int csr_tiles(const CsrArgs& a) {
-  const int tr = csr_tile_rows(a.B, a.Nq);
-  return (a.Nq + tr - 1) / tr;
-}
+static int csr_tiles(const CsrArgs& a) { return (int)csr_tiles(a.B, a.Nq); }
 
 __global__ __launch_bounds__(256) void csr_count_kernel(CsrArgs a, int tile_rows) {
   extern __shared__ int cnt[];  // min(Nk, kCsrCountSlice) counters

@@ -317,6 +317,13 @@ struct CsrArgs {
   int compress;
 };
 constexpr int kCsrTile = 64;
+// Rows per tile of the CSR build (whole kCsrTile-row chunks, at most 1024) and
+// the tiles of Nq rows: tile_base holds csr_tiles(B, Nq) * Nk counts per batch element.
+int csr_tile_rows(int64_t B, int64_t Nq);
+inline int64_t csr_tiles(int64_t B, int64_t Nq) {
+  const int64_t tr = csr_tile_rows(B, Nq);
+  return (Nq + tr - 1) / tr;
+}
 // An edge record's first word holds its row below bit kRecHeadShift and its
 // head above (multi-head scores), so rows stay below 2^27.
 constexpr int kRecHeadShift = 27;

@@ -872,10 +872,18 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
     }
   }
 
-  // 4. projection weight grads: [dU; dV] = dP^T . X  (split-K, fixed order)
+  // 4. projection weight grads: [dU; dV] = dP^T . X  (split-K, fixed order).
+  //    On large problems on the second stream, beside the input gradient: its
+  //    MFMA work fills the other's HBM-bound epilogue.
+  const SideStream* gside =
+      (grad_target_weight && grad_source_weight && grad_layer_val) ? side_stream_for(st, (int64_t)M * k) : nullptr;
+  if (gside) {
+    rc = fork_to(gside, st);
+    if (rc) return rc;
+  }
   if (grad_target_weight && grad_source_weight) {
     rc = gemm_grad_weight(s.dP, 2 * r, layer_val, in_dim, grad_target_weight, grad_source_weight, r, 2 * r,
-                          (int)in_dim, M, s.splitk, st, bf16);
+                          (int)in_dim, M, s.splitk, gside ? gside->stream : st, bf16);
     if (rc) return rc;
   }
 
@@ -889,8 +897,10 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
 
   // 6. w_hat and bias grads (one bias per head)
   const int nparts = cols_backward_parts(M);
-  return launch_finalize_small_grads(s.part_c, nparts, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st,
-                                     mh ? (int)heads : 1);
+  rc = launch_finalize_small_grads(s.part_c, nparts, r, grad_core_weight, 0, s.rowsum, M, grad_bias, s.stage, st,
+                                   mh ? (int)heads : 1);
+  if (rc) return rc;
+  return gside ? join_from(gside, st) : kOk;
 }
 
 // Top-k propagation forward over all ranks (heads * head rank); heads > 1

@@ -123,7 +123,7 @@ size_t jn_lowrank_topk_select_workspace_bytes(int64_t batch, int64_t nk, int64_t
  * projections [B*N,2r], topk_index [B,N,k] (int32), topk_score [B,N,k].
  * compress_kind: 0 softsign, 1 signed_abs_softmax (sign(s) * softmax(|s|) over the
  * row's k edges), 2 signed_entmax15 (sign(s) * entmax15(|s|) over them,
- * native/jakal_net_native.cpp:1133-1205); 1 and 2 need k <= 64.
+ * native/jakal_net_native.cpp:1133-1205), for rows of any length.
  * edge_layout (NULL, or jn_propagation_topk_layout_bytes(batch, nodes, topk)
  * bytes): the forward also groups the selected edges by key for the backward,
  * beside its row pass; pass the same buffer, unchanged, to the backward.

@@ -95,19 +95,21 @@ __global__ __launch_bounds__(256) void band_aggregate_kernel(BandAggArgs a) {
       cs[tt * kst + e] = c;
     }
   } else {
-    // row-normalising kinds (k <= 64): one row per wave pass
+    // row-normalising kinds: one row per wave pass, 64 slots at a time
     for (int tt = w; tt < kBandRows; tt += 4) {
       const int i = t0 + tt;
-      float c = 0.f;
-      if (i < a.N) {  // wave-uniform
-        const int64_t row = base + i;
-        float rmax = 0.f, rinv = 0.f;
-        if (a.compress == 1) row_abs_softmax_stats(a.idx, a.score, row, a.k, rmax, rinv);
-        int j;
-        float sc;
-        row_coefficients(a.idx, a.score, row, a.k, 0, a.compress, rmax, rinv, j, c, sc);  // absent: 0
+      const int64_t row = base + i;
+      RowStats rst;
+      if (i < a.N) rst = row_compress_stats(a.idx, a.score, row, a.k, a.compress);  // wave-uniform
+      for (int e0 = 0; e0 < a.k; e0 += kWave) {
+        float c = 0.f;
+        if (i < a.N) {
+          int j;
+          float sc;
+          row_coefficients(a.idx, a.score, row, a.k, e0, a.compress, rst, j, c, sc);  // absent: 0
+        }
+        if (e0 + lane < a.k) cs[tt * kst + e0 + lane] = c;
       }
-      if (lane < a.k) cs[tt * kst + lane] = c;
     }
   }
   __syncthreads();
@@ -319,8 +321,6 @@ int launch_band_aggregate(const BandAggArgs& a, hipStream_t stream) {
   JN_REQUIRE(band_kernels_fit(a.k, a.D, a.ld_val, a.ld_out, a.val, a.out, a.bf16), kInvalidArgument,
              "band aggregate: k in [1, %d], D and row strides in whole 16-byte packs, aligned rows", kBandMaxK);
   JN_REQUIRE(a.trans ? (a.coef != nullptr) : (a.idx && a.score), kInvalidArgument, "null tensor pointer");
-  JN_REQUIRE(a.trans || a.compress == 0 || a.k <= 64, kUnsupported,
-             "row-normalising compress kinds on the band need k <= 64");
   const int64_t tiles = (a.N + kBandRows - 1) / kBandRows, slabs = (a.D + kBandCols - 1) / kBandCols;
   const int64_t blocks = (int64_t)a.B * tiles * slabs;
   JN_REQUIRE(blocks < (1LL << 31) && (int64_t)a.B * a.N * a.k < (1LL << 31), kInvalidArgument, "too many rows");

@@ -116,8 +116,6 @@ int check_edge_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_
   JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported,
              "compress_kind must be 0 (softsign), 1 (signed_abs_softmax) or 2 (signed_entmax15), got %d",
              compress_kind);
-  JN_REQUIRE(compress_kind == 0 || edges <= 64, kUnsupported,
-             "signed_abs_softmax and signed_entmax15 support at most 64 edges per row (got %lld)", (long long)edges);
   JN_REQUIRE(edges >= 1 && fits_int(batch * nodes) && fits_int(batch * nodes * edges) &&
                  fits_int(nodes * 2 * rank) && fits_int(nodes * out_dim * 4),
              kUnsupported, "problem too large for 32-bit edge ids and offsets");

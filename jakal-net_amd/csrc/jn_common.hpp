@@ -490,10 +490,62 @@ __device__ __forceinline__ void row_abs_softmax_stats(const int32_t* idx, const 
   row_inv_sum = sum > 0.f ? 1.0f / sum : 0.0f;
 }
 
-// Coefficient of edge e0 + lane of a row (0 for absent edges).
+// Statistics of a row's compression, for rows of any length: kind 1:
+// a = max |s|, b = 1 / sum exp(|s| - a); kind 2: a = max |s|, b = the entmax
+// threshold tau of x = (|s| - a) / 2 (support refinement, as entmax15_lane),
+// c = the sum of the weights max(x - tau, 0)^2 (1 up to rounding).  Lane l
+// takes the row's edges l, l + 64, ...; absent edges do not count.  For rows
+// of at most 64 edges the sums are those of entmax15_lane, term for term.
+struct RowStats {
+  float a = 0.f, b = 0.f, c = 0.f;
+};
+
+__device__ __forceinline__ RowStats row_compress_stats(const int32_t* idx, const float* score, int64_t row, int k,
+                                                       int compress) {
+  RowStats st;
+  if (compress == 1) {
+    row_abs_softmax_stats(idx, score, row, k, st.a, st.b);
+  } else if (compress == 2) {
+    const int lane = lane_id();
+    float m = -INFINITY;
+    for (int e = lane; e < k; e += kWave)
+      if (idx[row * k + e] >= 0) m = fmaxf(m, fabsf(score[row * k + e]));
+    m = wave_max_f(m);
+    float tau = -INFINITY;
+    int n_prev = -1;
+    for (int it = 0; it < kEntmaxMaxIter; ++it) {
+      float s1 = 0.f, s2 = 0.f, n = 0.f;
+      for (int e = lane; e < k; e += kWave) {
+        if (idx[row * k + e] < 0) continue;
+        const float x = 0.5f * (fabsf(score[row * k + e]) - m);
+        if (x >= tau) {
+          s1 += x;
+          s2 += x * x;
+          n += 1.0f;
+        }
+      }
+      n = wave_sum(n);
+      if ((int)n == n_prev) break;
+      n_prev = (int)n;
+      tau = entmax15_tau_of(wave_sum(s1), wave_sum(s2), n);
+    }
+    float den = 0.f;
+    for (int e = lane; e < k; e += kWave) {
+      if (idx[row * k + e] < 0) continue;
+      const float d = fmaxf(0.5f * (fabsf(score[row * k + e]) - m) - tau, 0.0f);
+      den += d * d;
+    }
+    st.a = m;
+    st.b = tau;
+    st.c = wave_sum(den);
+  }
+  return st;
+}
+
+// Coefficient of edge e0 + lane of a row (0 for absent edges), given the
+// row's statistics (row_compress_stats).
 __device__ __forceinline__ void row_coefficients(const int32_t* idx, const float* score, int64_t row, int k, int e0,
-                                                 int compress, float row_max, float row_inv_sum, int& j, float& c,
-                                                 float& s) {
+                                                 int compress, const RowStats& st, int& j, float& c, float& s) {
   const int e = e0 + lane_id();
   j = -1;
   c = 0.0f;
@@ -502,12 +554,15 @@ __device__ __forceinline__ void row_coefficients(const int32_t* idx, const float
     j = idx[row * k + e];
     if (j >= 0) {
       s = score[row * k + e];
-      c = (compress == 0) ? softsign_f(s) : sign_f(s) * __expf(fabsf(s) - row_max) * row_inv_sum;
+      if (compress == 0) {
+        c = softsign_f(s);
+      } else if (compress == 1) {
+        c = sign_f(s) * __expf(fabsf(s) - st.a) * st.b;
+      } else {
+        const float d = fmaxf(0.5f * (fabsf(s) - st.a) - st.b, 0.0f);
+        c = st.c > 0.0f ? sign_f(s) * (d * d / st.c) : 0.0f;
+      }
     }
-  }
-  if (compress == 2) {  // uniform; the whole row is this wavefront's (k <= 64 checked on the host)
-    const float p = entmax15_lane(fabsf(s), j >= 0);
-    c = j >= 0 ? sign_f(s) * p : 0.0f;
   }
 }
 

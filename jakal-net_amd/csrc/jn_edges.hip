@@ -54,14 +54,13 @@ __global__ __launch_bounds__(256) void rows_forward_kernel(RowsFwdArgs a) {
   const float* psb = a.ps + b * a.Nk;
   T* out = reinterpret_cast<T*>(a.out_val) + row * a.D;
 
-  float rmax = 0.f, rinv = 0.f;
-  if (a.compress == 1) row_abs_softmax_stats(a.idx, a.score, row, a.k, rmax, rinv);
+  const RowStats rst = row_compress_stats(a.idx, a.score, row, a.k, a.compress);
 
   float st = 0.0f;
   for (int e0 = 0; e0 < a.k; e0 += kWave) {
     int j;
     float c, s;
-    row_coefficients(a.idx, a.score, row, a.k, e0, a.compress, rmax, rinv, j, c, s);
+    row_coefficients(a.idx, a.score, row, a.k, e0, a.compress, rst, j, c, s);
     if (slab == 0 && j >= 0) st += c * psb[j];
     const int ne = min(kWave, a.k - e0);
     for (int d = d_begin + lane * W; d < d_end; d += kWave * W) {
@@ -232,30 +231,13 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
     for (int m = 0; m < 8; ++m) hslot[m] = (kvec ? (m == 0 ? 4 * c : 64 + 4 * c) : c + 16 * m) / a.head_rank;
   }
 
-  float rmax = 0.f, rinv = 0.f;
-  if (a.compress == 1) row_abs_softmax_stats(a.idx, a.score, row, a.k, rmax, rinv);
+  const RowStats rst = row_compress_stats(a.idx, a.score, row, a.k, a.compress);
 
-  float4 dqa = make_float4(0.f, 0.f, 0.f, 0.f), dqb = dqa;  // kvec: ranks 4c.., 64+4c..
-  float dqs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // scalar: ranks c + 16m
-  float gsum = 0.f;
-  float hsum[MH ? kMaxHeads : 1] = {};
-  for (int e0 = 0; e0 < a.k; e0 += KP) {
-    int j;
-    float cf, s;
-    // lanes < KP hold edges e0 + lane (j = -1 past k)
-    row_coefficients(a.idx, a.score, row, a.k, e0, a.compress, rmax, rinv, j, cf, s);
-    if (lane >= KP) j = -1;
+  // The coefficient gradient g_c of this lane's edge in the block at e0
+  // (lanes < KP hold edges e0 + lane; jg: the block's edges as the 16-lane
+  // groups take them).
+  auto edge_gc = [&](int e0, int j, const int (&jg)[NI]) -> float {
     const int ne = min(KP, a.k - e0);
-    int jg[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) jg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, j);
-    int eh = 0, hg[MH ? NI : 1];
-    if constexpr (MH) {
-      if (j >= 0) eh = a.ehead[row * a.k + e0 + lane];  // j >= 0: lane < KP and e0 + lane < k
-#pragma unroll
-      for (int i = 0; i < NI; ++i) hg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, eh);
-    }
-
     float dot = 0.f;
     if constexpr (SPLIT) {
       // slab partials of this lane's edge, summed in slab order
@@ -310,16 +292,89 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
       }
       dot = __int_as_float(__builtin_amdgcn_ds_bpermute(edge_owner_lane(lane) << 2, __float_as_int(sel)));
     }
-    const float gc = (j >= 0) ? gs_row * psb[j] + dot : 0.f;
+    return (j >= 0) ? gs_row * psb[j] + dot : 0.f;
+  };
+
+  // Row-normalising kinds over more than one block of edges: a first pass
+  // stores every edge's g_c in g_score and forms the row sums their backward
+  // needs (kind 1: sum g_c c; kind 2: sum sign(s) g_c u and sum u with
+  // u = sqrt(|c|)) and whether all scores share one sign; the main pass reads
+  // g_c back.  One block: the same sums come from the block itself.
+  const bool two_pass = a.compress != 0 && a.k > KP;
+  float row_s1 = 0.f, row_s2 = 0.f;
+  bool row_shift_free = false;
+  if (two_pass) {
+    float npos = 0.f, nneg = 0.f, nall = 0.f;
+    for (int e0 = 0; e0 < a.k; e0 += KP) {
+      int j;
+      float cf, s;
+      row_coefficients(a.idx, a.score, row, a.k, e0, a.compress, rst, j, cf, s);
+      if (lane >= KP) j = -1;
+      int jg[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) jg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, j);
+      const float gc = edge_gc(e0, j, jg);
+      if (j >= 0) {  // j >= 0: lane < KP and e0 + lane < k
+        a.g_score[row * a.k + e0 + lane] = gc;
+        const float sg = sign_f(s);
+        if (a.compress == 1) {
+          row_s1 += gc * cf;
+        } else {
+          const float u = sqrtf(fabsf(cf));
+          row_s1 += gc * sg * u;
+          row_s2 += u;
+        }
+        npos += s > 0.f ? 1.f : 0.f;
+        nneg += s < 0.f ? 1.f : 0.f;
+        nall += 1.f;
+      }
+    }
+    row_s1 = wave_sum(row_s1);
+    row_s2 = wave_sum(row_s2);
+    npos = wave_sum(npos);
+    nneg = wave_sum(nneg);
+    nall = wave_sum(nall);
+    row_shift_free = npos == nall || nneg == nall;
+  }
+
+  float4 dqa = make_float4(0.f, 0.f, 0.f, 0.f), dqb = dqa;  // kvec: ranks 4c.., 64+4c..
+  float dqs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // scalar: ranks c + 16m
+  float gsum = 0.f;
+  float hsum[MH ? kMaxHeads : 1] = {};
+  for (int e0 = 0; e0 < a.k; e0 += KP) {
+    int j;
+    float cf, s;
+    // lanes < KP hold edges e0 + lane (j = -1 past k)
+    row_coefficients(a.idx, a.score, row, a.k, e0, a.compress, rst, j, cf, s);
+    if (lane >= KP) j = -1;
+    const int ne = min(KP, a.k - e0);
+    int jg[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) jg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, j);
+    int eh = 0, hg[MH ? NI : 1];
+    if constexpr (MH) {
+      if (j >= 0) eh = a.ehead[row * a.k + e0 + lane];  // j >= 0: lane < KP and e0 + lane < k
+#pragma unroll
+      for (int i = 0; i < NI; ++i) hg[i] = __builtin_amdgcn_ds_bpermute((4 * i + g) << 2, eh);
+    }
+
+    const float gc = two_pass ? (j >= 0 ? a.g_score[row * a.k + e0 + lane] : 0.f) : edge_gc(e0, j, jg);
     float gsc = 0.f;
     if (a.compress == 1) {
-      const float row_dot = wave_sum(gc * cf);  // single block: k <= 64 enforced on the host
+      const float row_dot = two_pass ? row_s1 : wave_sum(gc * cf);
       if (j >= 0) {
         const float sg = sign_f(s);
         gsc = sg * (sg * cf) * (sg * gc - row_dot);
       }
     } else if (a.compress == 2) {
-      gsc = signed_entmax15_backward_lane(s, cf, gc);  // absent edges: s = cf = gc = 0
+      if (two_pass) {  // as signed_entmax15_backward_lane, with the row's sums
+        const float sg = sign_f(s);
+        const float u = sqrtf(fabsf(cf));
+        const float corr = row_s2 > 0.0f ? row_s1 / row_s2 : 0.0f;
+        gsc = j >= 0 ? (gc * sg * u - corr * u) * sg : 0.f;
+      } else {
+        gsc = signed_entmax15_backward_lane(s, cf, gc);  // absent edges: s = cf = gc = 0
+      }
     } else if (j >= 0) {
       gsc = gc * softsign_grad_f(s);
     }
@@ -333,8 +388,8 @@ __global__ __launch_bounds__(256) void rows_backward_kernel(RowsBwdArgs a) {
 #pragma unroll
       for (int h = 0; h < kMaxHeads; ++h) hsum[h] += (eh == h) ? gsc : 0.f;
     } else {
-      // kinds 1 and 2 hold the whole row in this pass (k <= 64)
-      const bool shift_free = a.compress != 0 && row_one_sign(j >= 0, s);
+      // a row of one score sign has no bias gradient under kinds 1 and 2
+      const bool shift_free = a.compress != 0 && (two_pass ? row_shift_free : row_one_sign(j >= 0, s));
       gsum += shift_free ? 0.f : gsc;
     }
 
@@ -446,7 +501,6 @@ int rows_backward_slab(int64_t Nk, int D, bool vec, int elem_bytes) {
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
   if (a.rows == 0) return kOk;
   JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
-  JN_REQUIRE(a.compress == 0 || a.k <= 64, kUnsupported, "signed_abs_softmax backward supports k <= 64");
   const int64_t blocks = (a.rows + 3) / 4;
   JN_REQUIRE(2 * blocks < (1LL << 31), kInvalidArgument, "too many rows");
   JN_REQUIRE((int64_t)a.Nk * a.ld_pv * 4 < (1LL << 31) && (int64_t)a.Nk * a.ldk * 4 < (1LL << 31) &&
@@ -953,12 +1007,11 @@ __global__ __launch_bounds__(256) void edge_coefficients_kernel(const int32_t* i
                                                                 int k, int compress, float* coef) {
   const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
   if (row >= rows) return;
-  float rmax = 0.f, rinv = 0.f;
-  if (compress == 1) row_abs_softmax_stats(idx, score, row, k, rmax, rinv);
+  const RowStats rst = row_compress_stats(idx, score, row, k, compress);
   for (int e0 = 0; e0 < k; e0 += kWave) {
     int j;
     float c, s;
-    row_coefficients(idx, score, row, k, e0, compress, rmax, rinv, j, c, s);
+    row_coefficients(idx, score, row, k, e0, compress, rst, j, c, s);
     if (e0 + lane_id() < k) coef[row * k + e0 + lane_id()] = c;
   }
 }
@@ -966,7 +1019,6 @@ __global__ __launch_bounds__(256) void edge_coefficients_kernel(const int32_t* i
 int launch_edge_coefficients(const int32_t* idx, const float* score, int64_t rows, int k, int compress, float* coef,
                              hipStream_t stream) {
   if (rows == 0) return kOk;
-  JN_REQUIRE(compress == 0 || k <= kWave, kUnsupported, "signed compress kinds take k <= %d", kWave);
   const int64_t blocks = (rows + 3) / 4;
   JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
   JN_PROFILE("edge_coefficients_kernel", stream);

@@ -179,7 +179,6 @@ MAX_TOPK = 64          # edges per row of the register top-k select (multi-head 
 MAX_TOPK_LARGE = 1024  # edges per row of a single-head propagation top-k (scored rows, radix select)
 MAX_RANK = 128         # low-rank score rank
 MAX_SELECT_KEYS = 65535  # keys a top-k select ranks per batch element
-MAX_ROW_COMPRESS_EDGES = 64  # edges per row of the row-normalising compressions on edge lists
 CAUSAL_DENSE_MIN_NODES = 128  # full causal windows from this many nodes run on the dense MFMA path
 MAX_HEADS = 8          # heads of a max-aggregated multi-head score
 
@@ -745,12 +744,6 @@ def _check_select(k: int, keys: int, large: bool = False) -> None:
         raise NotImplementedError(f"the HIP top-k select ranks up to {MAX_SELECT_KEYS} keys per row (got {keys}).")
 
 
-def _check_row_compress(compress: str, edges: int) -> None:
-    if compress != "softsign" and edges > MAX_ROW_COMPRESS_EDGES:
-        raise NotImplementedError(f"HIP {compress} edge lists hold up to {MAX_ROW_COMPRESS_EDGES} edges per row "
-                                  f"(got {edges}).")
-
-
 def _propagation_edges(mode, pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
                        edge_compress_name, layer_val, projected_state, projected_val, param, target_block_size,
                        source_block_size):
@@ -816,7 +809,6 @@ def propagation_topk_selection(
         raise NotImplementedError("top-k with k == N keeps every source: that is dense propagation "
                                   "(propagation_dense, or propagation_topk, which routes it there).")
     _check_select(k, N, large=True)
-    _check_row_compress(edge_compress_name, k)
     return _propagation_edges("topk", pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
                               edge_compress_name, layer_val, projected_state, projected_val, k, target_block_size,
                               source_block_size)
@@ -844,7 +836,6 @@ def propagation_window_edges(
     (index -1 where that is negative) and its score."""
     if window < 0:
         raise RuntimeError("window must be non-negative.")
-    _check_row_compress(edge_compress_name, min(int(window) + 1, layer_val.shape[-2]))
     return _propagation_edges("window", pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
                               edge_compress_name, layer_val, projected_state, projected_val, int(window),
                               target_block_size, source_block_size)
@@ -871,13 +862,11 @@ def propagation_window(
     A window covering every earlier source (window >= N - 1, the causal dense
     query propagation of progressive_b_example.py:1990-2003) on at least
     CAUSAL_DENSE_MIN_NODES nodes runs as causal dense propagation on MFMA
-    GEMMs instead of an N-wide edge list, and so does one whose rows are too
-    wide for a row-normalising compression on an edge list (single-head
-    scores; multi-head ones stay on the edge list)."""
+    GEMMs instead of an N-wide edge list (single-head scores; multi-head ones
+    stay on the edge list)."""
     N = layer_val.shape[-2]
     full_causal = window >= N - 1 and not pairwise_kind.startswith("multihead_")
-    if full_causal and (N >= CAUSAL_DENSE_MIN_NODES or (edge_compress_name != "softsign"
-                                                        and N > MAX_ROW_COMPRESS_EDGES)):
+    if full_causal and N >= CAUSAL_DENSE_MIN_NODES:
         if window < 0:
             raise RuntimeError("window must be non-negative.")
         return propagation_dense(pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,

@@ -277,3 +277,17 @@ def test_propagation_topk_large_k(dev, k):
     """Top-k propagation beyond 64 edges per row (softsign), forward and
     backward against the oracle on the GPU's selection."""
     _run_topk(dev, _c1_inputs(seed=1200 + k, B=2, N=400, D=48, r=16), "softsign", True, k, min_checkable=0.3)
+
+
+@pytest.mark.parametrize("N,D,k,compress,separate_pv", [
+    (400, 48, 65, "signed_abs_softmax", True),    # fused column pass, one slab
+    (400, 48, 200, "signed_entmax15", False),
+    (300, 30, 100, "signed_entmax15", True),      # unaligned rows: the row pass gathers its value rows
+    (300, 30, 130, "signed_abs_softmax", False),
+    (600, 388, 96, "signed_entmax15", True),      # fused column pass, two slabs
+])
+def test_propagation_topk_signed_rows_beyond_one_block(dev, N, D, k, compress, separate_pv):
+    """The row-normalising compressions on rows of more than 64 edges: the row
+    statistics and, in the backward, the row sums of the compress backward
+    span several 64-edge blocks (two passes over the row)."""
+    _run_topk(dev, _c1_inputs(seed=1300 + k + D, B=2, N=N, D=D, r=16), compress, separate_pv, k, min_checkable=0.3)

@@ -191,6 +191,25 @@ def test_window_edge_kernels_forced(dev, compress):
         jn.set_window_kernels(jn.WINDOW_BAND)
 
 
+@pytest.mark.parametrize("window,N,compress,kernels", [
+    (90, 200, "signed_abs_softmax", "band"),      # 91 slots: band tiles, rows of two 64-slot blocks
+    (90, 200, "signed_entmax15", "band"),
+    (90, 200, "signed_entmax15", "edges"),
+    (150, 300, "signed_abs_softmax", "edges"),    # wider than the band: the edge kernels
+    (150, 300, "signed_entmax15", "edges"),
+    (99, 100, "signed_entmax15", "band"),         # full causal window below 128 nodes: an edge list
+])
+def test_window_signed_rows_beyond_one_block(dev, window, N, compress, kernels):
+    """The row-normalising compressions on windows of more than 64 slots."""
+    import jakal_net_native as jn
+
+    jn.set_window_kernels(jn.WINDOW_EDGES if kernels == "edges" else jn.WINDOW_BAND)
+    try:
+        _run(dev, 2200 + window, B=2, N=N, D=32, r=8, window=window, compress=compress, separate_pv=True)
+    finally:
+        jn.set_window_kernels(jn.WINDOW_BAND)
+
+
 def test_window_unaligned_rows_take_the_edge_kernels(dev):
     """D = 30 is not a whole number of 16-byte packs: the edge kernels run."""
     _run(dev, 2004, B=2, N=90, D=30, r=6, window=20, compress="signed_entmax15", separate_pv=True)

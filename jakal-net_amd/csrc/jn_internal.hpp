@@ -37,7 +37,7 @@ constexpr int kSelectMaxK = 64;
 // Selects beyond the register kernels' limits (k > kSelectMaxK or more than
 // 65,535 keys) score rows into the workspace with an fp32 MFMA GEMM and pick
 // each row's k best by radix select (jn_select_large.hip), up to this k.
-constexpr int kSelectLargeMaxK = 1024;
+constexpr int kSelectLargeMaxK = 4096;
 int launch_topk_select_large(const SelectArgs& a, hipStream_t stream);
 // Score arithmetic of the select: kSelectSplitF16 (default) runs the score
 // tiles on fp16 MFMAs over two-term fp16 splits of the operands (about 22

@@ -176,7 +176,7 @@ _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
 # (a RuntimeError subclass) before anything is launched, so callers that have
 # another path for such shapes (implementation="kernel") can take it.
 MAX_TOPK = 64          # edges per row of the register top-k select (multi-head scores, routes)
-MAX_TOPK_LARGE = 1024  # edges per row of a single-head propagation top-k (scored rows, radix select)
+MAX_TOPK_LARGE = 4096  # edges per row of a single-head propagation top-k (scored rows, radix select)
 MAX_RANK = 128         # low-rank score rank
 MAX_SELECT_KEYS = 65535  # keys a top-k select ranks per batch element
 CAUSAL_DENSE_MIN_NODES = 128  # full causal windows from this many nodes run on the dense MFMA path

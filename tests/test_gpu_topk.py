@@ -236,7 +236,7 @@ def test_c4_shape_select_every_row(dev):
     assert worst_gap <= 1e-5
 
 
-@pytest.mark.parametrize("r,k,Nq,Nk", [(16, 100, 70, 500), (8, 1024, 20, 1500), (64, 65, 130, 4096),
+@pytest.mark.parametrize("r,k,Nq,Nk", [(16, 100, 70, 500), (8, 1024, 20, 1500), (64, 65, 130, 4096), (8, 3000, 10, 3500),
                                        (5, 700, 33, 701), (8, 16, 40, 70000)])
 def test_select_beyond_register_limits(dev, r, k, Nq, Nk):
     """k above 64 or more than 65,535 keys: scored rows (fp32 MFMA GEMM) and a
@@ -277,6 +277,12 @@ def test_propagation_topk_large_k(dev, k):
     """Top-k propagation beyond 64 edges per row (softsign), forward and
     backward against the oracle on the GPU's selection."""
     _run_topk(dev, _c1_inputs(seed=1200 + k, B=2, N=400, D=48, r=16), "softsign", True, k, min_checkable=0.3)
+
+
+def test_propagation_topk_very_large_k(dev):
+    """2000 of 2600 sources per row (the scored-rows select's LDS sort over
+    2048 slots), forward and backward against the oracle."""
+    _run_topk(dev, _c1_inputs(seed=1250, B=1, N=2600, D=24, r=8), "signed_entmax15", True, 2000, min_checkable=0.3)
 
 
 @pytest.mark.parametrize("N,D,k,compress,separate_pv", [

@@ -1037,7 +1037,7 @@ int launch_edge_coefficients(const int32_t* idx, const float* score, int64_t row
 // order into one row of part_c per workgroup.
 // MH: each record's head (its row word's top bits) selects the ranks it reaches.
 template <bool VEC, bool MH, bool BAND>
-__global__ __launch_bounds__(256) void cols_keygrad_kernel(ColsBwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(VEC && !MH ? 5 : 1))) void cols_keygrad_kernel(ColsBwdArgs a) {
   __shared__ float red[4][128];
   const int lane = lane_id(), g = lane >> 4, c = lane & 15, w = wave_id();
   const int64_t total_cols = (int64_t)a.B * a.Nk;

@@ -151,7 +151,13 @@ __device__ __forceinline__ bool aligned16(const float* p) { return (reinterpret_
 // traffic per use.
 template <bool A_KC, bool B_KC, int USE, int TILE>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
-  constexpr int NF4 = TILE * kGBK / 4;        // float4s per operand and K slice
+  // K slice: 16, or 64 for the 32 x 32 tile, whose workgroups do too little
+  // per slice to hide a slice's load latency (four 16-wide sub-slices, summed
+  // in the same order as four slices)
+  constexpr int BK = TILE == 32 ? 64 : kGBK;
+  constexpr int GS = BK + 4;                  // LDS row stride (floats)
+  constexpr int KQ = BK / 4;                  // float4s of a k-contiguous row slice
+  constexpr int NF4 = TILE * BK / 4;          // float4s per operand and K slice
   constexpr int LPT = (NF4 + 255) / 256;      // of them per thread (TILE 32: threads 0..127 load one)
   constexpr int MT = TILE / 32;               // 16x16 tiles per wave along M (and N)
   static_assert(TILE == 32 || TILE == 64, "generic GEMM tiles are 32 or 64");
@@ -160,8 +166,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
   constexpr bool C_BF = USE == kGemmGradInputBf16;   // C and the addend hold bf16
   static_assert(!A_BF || A_KC, "bf16 A is k-contiguous");
   static_assert(!B_BF || !B_KC, "bf16 B is k-major");
-  __shared__ __align__(16) float sA[2][TILE * kGStride];
-  __shared__ __align__(16) float sB[2][TILE * kGStride];
+  __shared__ __align__(16) float sA[2][TILE * GS];
+  __shared__ __align__(16) float sB[2][TILE * GS];
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -194,7 +200,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
       if (NF4 % 256 != 0 && e >= NF4) continue;
       // ---- A ----
       if constexpr (A_BF) {
-        const int m = m0 + e / 4, kq = k0 + (e % 4) * 4;
+        const int m = m0 + e / KQ, kq = k0 + (e % KQ) * 4;
         const bf16_t* p = reinterpret_cast<const bf16_t*>(g.A) + bz * g.a_bs + (int64_t)m * g.lda + kq;
         if (m < g.M && kq + 3 < kend && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
           const uint2 v = *reinterpret_cast<const uint2*>(p);
@@ -205,7 +211,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
           for (int q = 0; q < 4; ++q) ra[u][q] = (m < g.M && kq + q < kend) ? (float)p[q] : 0.0f;
         }
       } else if (A_KC) {
-        const int m = m0 + e / 4, kq = k0 + (e % 4) * 4;
+        const int m = m0 + e / KQ, kq = k0 + (e % KQ) * 4;
         const float* p = gA + (int64_t)m * g.lda + kq;
         if (m < g.M && kq + 3 < kend && aligned16(p)) {
           const float4 v = *reinterpret_cast<const float4*>(p);
@@ -236,7 +242,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
       }
       // ---- B ----
       if (B_KC) {
-        const int n = n0 + e / 4, kq = k0 + (e % 4) * 4;
+        const int n = n0 + e / KQ, kq = k0 + (e % KQ) * 4;
         const float* base = (n < g.b_split) ? gB0 + (int64_t)n * g.ldb : gB1 + (int64_t)(n - g.b_split) * g.ldb;
         const float* p = base + kq;
         if (n < g.N && kq + 3 < kend && aligned16(p)) {
@@ -279,20 +285,20 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
       const int e = tid + 256 * u;
       if (NF4 % 256 != 0 && e >= NF4) continue;
       if (A_KC) {
-        *reinterpret_cast<float4*>(&sA[buf][(e / 4) * kGStride + (e % 4) * 4]) =
+        *reinterpret_cast<float4*>(&sA[buf][(e / KQ) * GS + (e % KQ) * 4]) =
             make_float4(ra[u][0], ra[u][1], ra[u][2], ra[u][3]);
       } else {
         const int kk = e / (TILE / 4), mq = (e % (TILE / 4)) * 4;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sA[buf][(mq + q) * kGStride + kk] = ra[u][q];
+        for (int q = 0; q < 4; ++q) sA[buf][(mq + q) * GS + kk] = ra[u][q];
       }
       if (B_KC) {
-        *reinterpret_cast<float4*>(&sB[buf][(e / 4) * kGStride + (e % 4) * 4]) =
+        *reinterpret_cast<float4*>(&sB[buf][(e / KQ) * GS + (e % KQ) * 4]) =
             make_float4(rb[u][0], rb[u][1], rb[u][2], rb[u][3]);
       } else {
         const int kk = e / (TILE / 4), nq = (e % (TILE / 4)) * 4;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sB[buf][(nq + q) * kGStride + kk] = rb[u][q];
+        for (int q = 0; q < 4; ++q) sB[buf][(nq + q) * GS + kk] = rb[u][q];
       }
     }
   };
@@ -311,7 +317,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
       for (int c = 0; c < 3; ++c) chain[c][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
 
-  const int nslices = kend > kbeg ? (kend - kbeg + kGBK - 1) / kGBK : 0;
+  const int nslices = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
   if (nslices > 0) {
     load_slice(kbeg);
     store_slice(0);
@@ -320,23 +326,26 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 
   for (int s = 0; s < nslices; ++s) {
     const int cur = s & 1;
-    if (s + 1 < nslices) load_slice(kbeg + (s + 1) * kGBK);
+    if (s + 1 < nslices) load_slice(kbeg + (s + 1) * BK);
 
-    float4 av[MT], bv[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      av[t] = *reinterpret_cast<const float4*>(&sA[cur][(wm * (TILE / 2) + t * 16 + col) * kGStride + grp * 4]);
-      bv[t] = *reinterpret_cast<const float4*>(&sB[cur][(wn * (TILE / 2) + t * 16 + col) * kGStride + grp * 4]);
-    }
+    for (int ss = 0; ss < BK / 16; ++ss) {
+      float4 av[MT], bv[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < MT; ++nt) {
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].x, bv[nt].x, acc[mt][nt], 0, 0, 0);
-        chain[0][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].y, bv[nt].y, chain[0][mt][nt], 0, 0, 0);
-        chain[1][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].z, bv[nt].z, chain[1][mt][nt], 0, 0, 0);
-        chain[2][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].w, bv[nt].w, chain[2][mt][nt], 0, 0, 0);
+      for (int t = 0; t < MT; ++t) {
+        av[t] = *reinterpret_cast<const float4*>(&sA[cur][(wm * (TILE / 2) + t * 16 + col) * GS + ss * 16 + grp * 4]);
+        bv[t] = *reinterpret_cast<const float4*>(&sB[cur][(wn * (TILE / 2) + t * 16 + col) * GS + ss * 16 + grp * 4]);
       }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < MT; ++nt) {
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].x, bv[nt].x, acc[mt][nt], 0, 0, 0);
+          chain[0][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].y, bv[nt].y, chain[0][mt][nt], 0, 0, 0);
+          chain[1][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].z, bv[nt].z, chain[1][mt][nt], 0, 0, 0);
+          chain[2][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt].w, bv[nt].w, chain[2][mt][nt], 0, 0, 0);
+        }
+    }
 
     if (s + 1 < nslices) store_slice(cur ^ 1);
     __syncthreads();

@@ -389,18 +389,26 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
   khi = max(khi, (uint32_t)xor32_i((int)khi));
   klo = min(klo, (uint32_t)xor16_i((int)klo));
   klo = min(klo, (uint32_t)xor32_i((int)klo));
-  const uint32_t diff = khi ^ klo;
-  const int start = diff ? 31 - __builtin_clz(diff) : -1;
-  uint32_t t = diff ? (khi & ~((2u << start) - 1u)) : khi;  // shared prefix of the row's keys
-  if (start == 31) t = 0;
-  const int wave_start = (int)wave_max_u32((uint32_t)(start + 1)) - 1;  // uniform loop bound
-  // a row whose entries all fit keeps every valid key; every valid key is >= t,
-  // so a row whose entries fit the window is done before the search
+  // A row whose entries all fit keeps every valid key (t = 1: every valid key
+  // is >= 1).  Otherwise the search keeps a bracket of order keys a <= b with
+  // count(>= a) = ca > hi and count(> b) = cb < kk and probes a key c in
+  // (a, b]: interpolated in score value toward a count of (kk + hi) / 2
+  // (regula falsi; scores near the threshold are close to linear in rank), or
+  // halfway in key space once eight probes have not landed (at most 32 more).
+  // A probe whose count lies in [kk, hi] ends the row's search with t = c; a
+  // bracket that closes (a == b) leaves the kk-th largest key tied at t = a
+  // with more copies than the window holds.
   bool done = total <= hi;
-  if (done) t = 1;
-  for (int bit = wave_start; bit >= 0; --bit) {
-    if (!__ballot(!done)) break;
-    const uint32_t c = t | (1u << bit);
+  uint32_t t = done ? 1u : klo;
+  uint32_t ba = klo, bb = khi;
+  float ca = (float)total, cb = 0.0f;
+  const float target = 0.5f * (float)(kk + hi);
+  for (int it = 0; __ballot(!done && ba != bb); ++it) {
+    const uint32_t mid = ba + ((bb - ba) >> 1) + 1u;  // in (ba, bb] when ba < bb
+    const float fa = key_to_float(ba), fb = key_to_float(bb);
+    const float frac = (ca - target) * __builtin_amdgcn_rcpf(ca - cb);
+    const uint32_t ci = order_key(fmaf(fb - fa, frac, fa));
+    const uint32_t c = (it < 8 && ci > ba && ci <= bb) ? ci : mid;
     int n = 0;
 #pragma unroll
     for (int q = 0; q < NK / 4; ++q) {
@@ -409,11 +417,20 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
       for (int v = 0; v < 4; ++v) n += (key[4 * q + v] >= c) ? 1 : 0;
     }
     n = row_sum4(n);
-    if (!done && n >= kk) {
-      t = c;
-      done = (n <= hi);
+    if (!done && ba != bb) {
+      if (n > hi) {
+        ba = c;
+        ca = (float)n;
+      } else if (n < kk) {
+        bb = c - 1u;
+        cb = (float)n;
+      } else {
+        t = c;
+        done = true;
+      }
     }
   }
+  if (!done) t = ba;
   // winners: the keys >= t (done), or the kk-th largest key is t itself with
   // more ties at t than the window holds
   uint64_t keep_bits = 0;

@@ -161,14 +161,14 @@ __device__ __forceinline__ int row_sum4(int v) {
 // (ties toward the lower key index) of its `kept` kept entries and the c_g
 // candidates of lane region g (lane g * 16 + trow of the wave's slot-major
 // candidate arrays), compacted to kept slots [0, k); k < kept + sum(c).
-// Returns the new k-th best score (wave-uniform).  Lane l holds row slots l,
-// l + 64, l + 128 (kept slots first, then region 0, 1, 2, 3).
+// Kept slots hold order keys.  Returns the new k-th best score
+// (wave-uniform).  Lane l holds row slots l, l + 64, l + 128 (kept slots
+// first, then region 0, 1, 2, 3).
 template <int KEEP>
-__device__ float merge_row_exact(float* row_s, uint16_t* row_i, const float* cand_s, const uint16_t* cand_i, int trow, int k,
-                                 int kept, int c0, int c1, int c2, int c3) {
+__device__ float merge_row_exact(uint32_t* row_k, uint16_t* row_i, const float* cand_s, const uint16_t* cand_i, int trow,
+                                 int k, int kept, int c0, int c1, int c2, int c3) {
   constexpr int CAP = sel_lane_cap(KEEP);
   const int lane = lane_id();
-  float f[3];
   int ix[3];
   uint32_t kk[3];
   bool v[3];
@@ -189,9 +189,8 @@ __device__ float merge_row_exact(float* row_s, uint16_t* row_i, const float* can
       ok = false;
     }
     v[j] = ok;
-    f[j] = ok ? (s < KEEP ? row_s[s] : cand_s[w]) : 0.f;
     ix[j] = ok ? (int)(s < KEEP ? row_i[s] : cand_i[w]) : 0;
-    kk[j] = ok ? order_key(f[j]) : 0u;
+    kk[j] = ok ? (s < KEEP ? row_k[s] : order_key(cand_s[w])) : 0u;
   }
 
   // Radix select of the k-th largest key.  All valid keys lie in [lo, hi]; the
@@ -263,13 +262,8 @@ __device__ float merge_row_exact(float* row_s, uint16_t* row_i, const float* can
       }
     }
   }
-  // the k-th best score: an element whose key equals theta_key
-  float theta = 0.f;
-#pragma unroll
-  for (int j = 2; j >= 0; --j) {
-    const uint64_t e = __ballot(v[j] && kk[j] == theta_key);
-    if (e) theta = readlane_f(f[j], __builtin_ctzll(e));
-  }
+  // the k-th best score
+  const float theta = key_to_float(theta_key);
   int base = 0;
   int pos[3];
 #pragma unroll
@@ -282,7 +276,7 @@ __device__ float merge_row_exact(float* row_s, uint16_t* row_i, const float* can
 #pragma unroll
   for (int j = 0; j < 3; ++j)
     if (keep[j]) {
-      row_s[pos[j]] = f[j];
+      row_k[pos[j]] = kk[j];
       row_i[pos[j]] = (uint16_t)ix[j];
     }
   wave_lds_sync();
@@ -295,22 +289,23 @@ __device__ float merge_row_exact(float* row_s, uint16_t* row_i, const float* can
 // keeps every entry at or above a threshold t with kk <= count(>= t) <= hi,
 // kk = min(k, total): hi = kk in the final merge (exactly the kk best), up to
 // KEEP during the scan, where any t not above the k-th best serves and the
-// search stops as soon as the count fits.  The search is a radix select over
-// order keys per lane, with row counts summed over the row's 4 lanes by
-// permlane swaps.  Only the first `cq` quads of each candidate region (the
+// search stops as soon as the count fits.  Kept slots hold order keys.  The
+// search probes order keys per lane (below), with row counts summed over the
+// row's 4 lanes by permlane swaps.  Only the first `cq` quads of each candidate region (the
 // wave's largest candidate count, rounded up to 4) are read and searched: a
 // wave that merges because another wave of its workgroup had to merges only
 // what it holds.  Returns the row's kept count (or -1 for a row with exact
 // ties at t that the window cannot separate: its slots are left untouched
-// for merge_row_exact).  The row's threshold becomes the smallest kept value
-// once it has seen k keys (else it stays `theta`).
+// for merge_row_exact).  Once the row has seen k keys its threshold becomes
+// the score of t (no higher than its smallest kept entry), else it stays
+// `theta`.
 struct MergeResult {
   int kept;     // entries now in the kept region, -1 for a tie row
   float theta;  // the row's new threshold
 };
 
 template <int KEEP>
-__device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t* row_i, float* cand_s, uint16_t* cand_i,
+__device__ __forceinline__ MergeResult merge_rows_batched(uint32_t* row_k, uint16_t* row_i, float* cand_s, uint16_t* cand_i,
                                                           int k, int kept, int cnt, int total, int hi_target, float theta,
                                                           int cq) {
   constexpr int KQ = KEEP / 4;
@@ -322,7 +317,7 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
   const int kk = min(k, total);  // entries the row keeps at least
   const int hi = max(kk, min(hi_target, KEEP));
   const int kv = max(0, min(KQ, kept - g * KQ));
-  const float* kept_s = row_s + g * KQ;
+  const uint32_t* kept_k = row_k + g * KQ;
   const uint16_t* kept_i = row_i + g * KQ;
   uint32_t key[NK];
   int id[NK];
@@ -333,20 +328,20 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
   // empty asm before its validity select: left alone, the compiler turns
   // "valid ? f(load) : 0" into a branch around the load and waits for each
   // load on its own.
-  float sv[NK];
+  uint32_t sv[NK];  // order keys (kept slots) or score bits (candidates)
 #pragma unroll
   for (int q = 0; q < NK / 4; ++q) {
     if (!act(q)) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        sv[4 * q + v] = 0.0f;
+        sv[4 * q + v] = 0u;
         id[4 * q + v] = 0;
       }
       continue;
     }
     if (4 * q < KQ) {
       const int o = 4 * q;
-      const float4 s4 = *reinterpret_cast<const float4*>(kept_s + o);
+      const uint4 s4 = *reinterpret_cast<const uint4*>(kept_k + o);
       const uint2 i4 = *reinterpret_cast<const uint2*>(kept_i + o);
       sv[4 * q + 0] = s4.x;
       sv[4 * q + 1] = s4.y;
@@ -360,7 +355,7 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
       const int o = 4 * q - KQ;  // candidate slots o .. o + 3 of this lane
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        sv[4 * q + v] = cand_s[(o + v) * kWave];
+        sv[4 * q + v] = __float_as_uint(cand_s[(o + v) * kWave]);
         id[4 * q + v] = (int)cand_i[(o + v) * kWave];
       }
     }
@@ -372,9 +367,9 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
     const int lim = kpt ? kv : cnt;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      float x = sv[4 * q + v];
+      uint32_t x = sv[4 * q + v];
       if (act(q)) asm volatile("" : "+v"(x));
-      key[4 * q + v] = (act(q) && o + v < lim) ? order_key(x) : 0u;
+      key[4 * q + v] = (act(q) && o + v < lim) ? (kpt ? x : order_key(__uint_as_float(x))) : 0u;
     }
   }
   // valid keys are > 0 (order keys of finite or infinite floats are nonzero)
@@ -400,6 +395,7 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
   // with more copies than the window holds.
   bool done = total <= hi;
   uint32_t t = done ? 1u : klo;
+  int wl = done ? kv + cnt : 0;  // this lane's entries >= t once done
   uint32_t ba = klo, bb = khi;
   float ca = (float)total, cb = 0.0f;
   const float target = 0.5f * (float)(kk + hi);
@@ -416,6 +412,7 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
 #pragma unroll
       for (int v = 0; v < 4; ++v) n += (key[4 * q + v] >= c) ? 1 : 0;
     }
+    const int nl = n;
     n = row_sum4(n);
     if (!done && ba != bb) {
       if (n > hi) {
@@ -427,64 +424,37 @@ __device__ __forceinline__ MergeResult merge_rows_batched(float* row_s, uint16_t
       } else {
         t = c;
         done = true;
+        wl = nl;
       }
     }
   }
-  if (!done) t = ba;
-  // winners: the keys >= t (done), or the kk-th largest key is t itself with
-  // more ties at t than the window holds
-  uint64_t keep_bits = 0;
-  uint32_t theta_key;
-  bool tie_row = false;
-  if (done) {
-    uint32_t m = 0xffffffffu;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      if (!act(i / 4)) continue;
-      const bool kp = key[i] >= t;
-      keep_bits |= kp ? (1ull << i) : 0ull;
-      m = kp ? min(m, key[i]) : m;
-    }
-    m = min(m, (uint32_t)xor16_i((int)m));
-    m = min(m, (uint32_t)xor32_i((int)m));
-    theta_key = m;
-  } else {
-    int gt = 0, eq = 0;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      gt += (key[i] > t) ? 1 : 0;
-      eq += (key[i] == t) ? 1 : 0;
-    }
-    gt = row_sum4(gt);
-    eq = row_sum4(eq);
-    tie_row = (eq != kk - gt);
-#pragma unroll
-    for (int i = 0; i < NK; ++i) keep_bits |= (key[i] >= t) ? (1ull << i) : 0ull;
-    theta_key = t;
-  }
+  // Winners: the keys >= t.  A row whose search did not land (its kk-th
+  // largest key is tied at ba with more copies than the window holds) is left
+  // to merge_row_exact.
+  const bool tie_row = !done;
   // compact the winners of non-tie rows to kept slots [0, n): lane g starts
   // after the winners of the row's lanes g' < g.  Branch-free: a lane writes
   // every entry, losers to a slot of its own candidate region (dead after the
   // merge), so no lane writes over another's winners.
-  const int w = popc64(keep_bits);
-  const int w1 = xor16_i(w);   // lane g ^ 1
-  const int w2 = xor32_i(w);   // lane g ^ 2
+  const int w1 = xor16_i(wl);  // lane g ^ 1
+  const int w2 = xor32_i(wl);  // lane g ^ 2
   const int w3 = xor16_i(w2);  // lane g ^ 3
-  const int n_row = w + w1 + w2 + w3;
+  const int n_row = wl + w1 + w2 + w3;
   int pos = ((g & 1) ? w1 : 0) + ((g & 2) ? (w2 + w3) : 0);
   if (!tie_row) {
-    float* trash_s = cand_s + (CAP - 1) * kWave;
+    uint32_t* trash_k = reinterpret_cast<uint32_t*>(cand_s) + (CAP - 1) * kWave;
     uint16_t* trash_i = cand_i + (CAP - 1) * kWave;
     // the reads above have returned (their values feed these stores)
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
       if (!act(i / 4)) continue;
-      const bool kp = (keep_bits >> i) & 1ull;
-      *(kp ? row_s + pos : trash_s) = key_to_float(key[i]);
+      const bool kp = key[i] >= t;
+      *(kp ? row_k + pos : trash_k) = key[i];
       *(kp ? row_i + pos : trash_i) = (uint16_t)id[i];
       pos += kp ? 1 : 0;
     }
-    if (total >= k) theta = key_to_float(theta_key);
+    // t = 1 keeps every entry: the threshold is then the smallest of them
+    if (total >= k) theta = key_to_float(total <= hi ? klo : t);
   }
   wave_lds_sync();
   return MergeResult{tie_row ? -1 : n_row, theta};
@@ -643,7 +613,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   constexpr int PER = (F4 + NT - 1) / NT;  // of them per thread
 
   constexpr int KST = sel_kept_stride(KEEP), KIST = sel_kept_idx_stride(KEEP);
-  __shared__ __align__(16) float s_kept_s[SLOTS * KST];
+  __shared__ __align__(16) uint32_t s_kept_k[SLOTS * KST];  // order keys
   __shared__ __align__(16) uint16_t s_kept_i[SLOTS * KIST];
   __shared__ __align__(16) float s_cand_s[SLOTS / kSelRowsPerWave * CAP * kWave];
   __shared__ __align__(16) uint16_t s_cand_i[SLOTS / kSelRowsPerWave * CAP * kWave];
@@ -838,7 +808,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
   float theta = row_ok ? -INFINITY : INFINITY;  // invalid rows never admit
   int cnt = 0;   // candidates in this lane's region of its row
   int kept = 0;  // valid kept entries of this lane's row (<= k)
-  float* my_kept_s = s_kept_s + lrow * KST;
+  uint32_t* my_kept_k = s_kept_k + lrow * KST;
   uint16_t* my_kept_i = s_kept_i + lrow * KIST;
   float* wave_cand_s = s_cand_s + wave * CAP * kWave;
   uint16_t* wave_cand_i = s_cand_i + wave * CAP * kWave;
@@ -984,7 +954,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
       const int total = kept + row_sum4(cnt);
       const int cq = (int)(__builtin_amdgcn_readfirstlane(wave_max_u32((uint32_t)cnt)) + 3) / 4;
       const MergeResult mr =
-          merge_rows_batched<KEEP>(my_kept_s, my_kept_i, my_cand_s, my_cand_i, k, kept, cnt, total, last ? k : KEEP,
+          merge_rows_batched<KEEP>(my_kept_k, my_kept_i, my_cand_s, my_cand_i, k, kept, cnt, total, last ? k : KEEP,
                                    theta, cq);
       const int n_kept = mr.kept;
       theta = mr.theta;
@@ -995,7 +965,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
         const int t = __builtin_ctzll(m);
         m &= m - 1;
         const int slot = wave * kSelRowsPerWave + t;
-        const float th = merge_row_exact<KEEP>(s_kept_s + slot * KST, s_kept_i + slot * KIST, wave_cand_s, wave_cand_i, t,
+        const float th = merge_row_exact<KEEP>(s_kept_k + slot * KST, s_kept_i + slot * KIST, wave_cand_s, wave_cand_i, t,
                                                k, readlane_i(kept, t), readlane_i(cnt, t), readlane_i(cnt, t + 16),
                                                readlane_i(cnt, t + 32), readlane_i(cnt, t + 48));
         if (col == t) theta = th;
@@ -1095,7 +1065,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
       float vs = -INFINITY;
       int vi = 0x7fffffff;
       if (e < s_kcnt[slot]) {
-        vs = s_kept_s[slot * KST + e];
+        vs = key_to_float(s_kept_k[slot * KST + e]);
         vi = s_kept_i[slot * KIST + e];
       }
       bitonic_sort64_desc(vs, vi);
@@ -1120,7 +1090,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
       float vs = -INFINITY;
       int vi = 0x7fffffff;
       if (e < k) {
-        vs = s_kept_s[slot * KST + e];
+        vs = key_to_float(s_kept_k[slot * KST + e]);
         vi = s_kept_i[slot * KIST + e];
       }
       bitonic_sort32x2_desc(vs, vi);
@@ -1142,7 +1112,7 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
     float vs = -INFINITY;
     int vi = 0x7fffffff;
     if (lane < k) {
-      vs = s_kept_s[slot * KST + lane];
+      vs = key_to_float(s_kept_k[slot * KST + lane]);
       vi = s_kept_i[slot * KIST + lane];
     }
     bitonic_sort64_desc(vs, vi);

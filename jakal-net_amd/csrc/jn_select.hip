@@ -104,6 +104,20 @@ __device__ __forceinline__ float key_to_float(uint32_t key) {
   return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
+// Exchange with lane ^ stride (stride a constant once the sort loops below
+// unroll): DPP quad permutes for 1 and 2, the permlane swaps for 16 and 32
+// (VALU ops), an LDS permute otherwise.
+__device__ __forceinline__ int sort_xor_i(int v, int stride) {
+  if (stride == 1) return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+  if (stride == 2) return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+  if (stride == 16) return xor16_i(v);
+  if (stride == 32) return xor32_i(v);
+  return shfl_xor_i(v, stride);
+}
+__device__ __forceinline__ float sort_xor_f(float v, int stride) {
+  return __int_as_float(sort_xor_i(__float_as_int(v), stride));
+}
+
 // Branchless bitonic sort of 64 (score, index) pairs into descending score,
 // ascending index on ties.
 __device__ __forceinline__ void bitonic_sort64_desc(float& vs, int& vi) {
@@ -112,8 +126,8 @@ __device__ __forceinline__ void bitonic_sort64_desc(float& vs, int& vi) {
   for (int size = 2; size <= 64; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const float ps = shfl_xor_f(vs, stride);
-      const int pi = shfl_xor_i(vi, stride);
+      const float ps = sort_xor_f(vs, stride);
+      const int pi = sort_xor_i(vi, stride);
       const bool partner_better = (ps > vs) | ((ps == vs) & (pi < vi));
       const bool self_better = (vs > ps) | ((vs == ps) & (vi < pi));
       const bool keep_better = ((lane & stride) == 0) == ((lane & size) == 0);
@@ -132,8 +146,8 @@ __device__ __forceinline__ void bitonic_sort32x2_desc(float& vs, int& vi) {
   for (int size = 2; size <= 32; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const float ps = shfl_xor_f(vs, stride);
-      const int pi = shfl_xor_i(vi, stride);
+      const float ps = sort_xor_f(vs, stride);
+      const int pi = sort_xor_i(vi, stride);
       const bool partner_better = (ps > vs) | ((ps == vs) & (pi < vi));
       const bool self_better = (vs > ps) | ((vs == ps) & (vi < pi));
       const bool keep_better = ((lane & stride) == 0) == ((lane & size & 31) == 0);

@@ -105,11 +105,19 @@ __device__ __forceinline__ float key_to_float(uint32_t key) {
 }
 
 // Exchange with lane ^ stride (stride a constant once the sort loops below
-// unroll): DPP quad permutes for 1 and 2, the permlane swaps for 16 and 32
-// (VALU ops), an LDS permute otherwise.
+// unroll), all VALU: DPP quad permutes for 1 and 2, a row shift each way for
+// 4 (lanes with bit 2 clear read lane + 4, the others lane - 4, both within
+// the 16-lane row), a rotation of the row by 8 for 8, the permlane swaps for
+// 16 and 32.
 __device__ __forceinline__ int sort_xor_i(int v, int stride) {
   if (stride == 1) return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
   if (stride == 2) return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+  if (stride == 4) {
+    const int up = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xf, 0xf, false);  // row_shl:4 (lane + 4)
+    const int dn = __builtin_amdgcn_update_dpp(v, v, 0x114, 0xf, 0xf, false);  // row_shr:4 (lane - 4)
+    return (lane_id() & 4) ? dn : up;
+  }
+  if (stride == 8) return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false);  // row_ror:8
   if (stride == 16) return xor16_i(v);
   if (stride == 32) return xor32_i(v);
   return shfl_xor_i(v, stride);

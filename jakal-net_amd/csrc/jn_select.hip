@@ -39,18 +39,19 @@
 //     registers.
 //   * Once any lane of a wave has filled its region to within one chunk of
 //     its capacity (or at the end), all 16 rows of the wave merge together:
-//     lane (g, row) loads a quarter of the row's kept entries and its own
-//     candidates into registers, and a radix select over order keys counts
-//     per lane and sums over the row's 4 lanes with permlane swaps; it starts
-//     below the bits shared by all of the row's keys.  A merge during the scan
-//     stops as soon as the entries at or above its threshold fit the kept
+//     lane (g, row) loads a quarter of the row's kept entries (held as order
+//     keys) and its own candidates into registers, and a threshold search
+//     over order keys counts per lane and sums over the row's 4 lanes with
+//     permlane swaps: probes interpolated in score value between a bracket of
+//     keys, bisection in key space after eight probes.  A merge during the
+//     scan stops as soon as the entries at or above its probe fit the kept
 //     region (between k and 48 of them for k <= 32): any threshold not above
-//     the k-th best filters safely, and this halves the radix steps.  The
-//     merge after the last chunk keeps exactly k.  Winners are compacted into
-//     the row's kept region without branches.  A row whose k-th value is tied
-//     (more equal keys than places) is merged again by the exact per-row
+//     the k-th best filters safely, and the probe becomes the row's threshold.
+//     The merge after the last chunk keeps exactly k.  Winners are compacted
+//     into the row's kept region without branches.  A row whose k-th value is
+//     tied (more equal keys than places) is merged again by the exact per-row
 //     path, which keeps the lower key indices.  The kept set stays unsorted
-//     until one bitonic sort per row at the end.
+//     until one bitonic sort per row at the end (DPP and permlane exchanges).
 //   * Score arithmetic: fp16 MFMAs over two-term fp16 splits of the operands
 //     (see select_split_keys_kernel), or fp32 MFMAs (select mode 1), or, for
 //     bf16 layers, bf16 MFMAs over bf16 operands (select_bf16_keys_kernel).

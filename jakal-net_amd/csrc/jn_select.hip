@@ -520,9 +520,19 @@ __global__ __launch_bounds__(256) void select_split_absmax_kernel(const float* _
   const int rows = min(kSplitRows, Nk - row0);
   const float* kb = key + (int64_t)b * kbs + (int64_t)row0 * ldk;
   float m = 0.0f;
-  for (int e = threadIdx.x; e < rows * r; e += 256) {
-    const int row = e / r;
-    m = fmaxf(m, fabsf(kb[(int64_t)row * ldk + (e - row * r)]));
+  // four ranks per thread when rows are whole aligned float4s
+  if (r % 4 == 0 && ldk % 4 == 0 && kbs % 4 == 0 && (reinterpret_cast<uintptr_t>(key) & 15) == 0) {
+    const int r4 = r / 4;
+    for (int e = threadIdx.x; e < rows * r4; e += 256) {
+      const int row = e / r4;
+      const float4 v = *reinterpret_cast<const float4*>(kb + (int64_t)row * ldk + 4 * (e - row * r4));
+      m = fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+    }
+  } else {
+    for (int e = threadIdx.x; e < rows * r; e += 256) {
+      const int row = e / r;
+      m = fmaxf(m, fabsf(kb[(int64_t)row * ldk + (e - row * r)]));
+    }
   }
   m = block_max_256(m);
   if (threadIdx.x == 0) partial[(int64_t)b * nblk + blk] = m;
@@ -547,6 +557,31 @@ __global__ __launch_bounds__(256) void select_split_keys_kernel(const float* __r
   const int rows = min(kSplitRows, Nk - row0);
   const float* kb = key + (int64_t)b * kbs + (int64_t)row0 * ldk;
   _Float16* out = split + ((int64_t)b * Nk + row0) * (2 * RP);
+  // four split positions per thread (one 16-byte key load, two 8-byte stores)
+  // when the head's ranks come in aligned fours; the same arithmetic per element
+  if (head_rank % 4 == 0 && ldk % 4 == 0 && kbs % 4 == 0 && (reinterpret_cast<uintptr_t>(key) & 15) == 0) {
+    const int RP4 = RP / 4;  // RP and head_rp are multiples of 32
+    for (int e = threadIdx.x; e < rows * RP4; e += 256) {
+      const int row = e / RP4;
+      const int c = 4 * (e - row * RP4);
+      const int h = c / head_rp, cc = c - h * head_rp;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (cc < head_rank) {  // then cc + 3 < head_rank too
+        x = *reinterpret_cast<const float4*>(kb + (int64_t)row * ldk + h * head_rank + cc);
+        x = make_float4(ldexpf(x.x, ek), ldexpf(x.y, ek), ldexpf(x.z, ek), ldexpf(x.w, ek));
+      }
+      typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+      halfx4 hi, lo;
+      hi[0] = (_Float16)x.x; hi[1] = (_Float16)x.y; hi[2] = (_Float16)x.z; hi[3] = (_Float16)x.w;
+      lo[0] = (_Float16)(x.x - (float)hi[0]);
+      lo[1] = (_Float16)(x.y - (float)hi[1]);
+      lo[2] = (_Float16)(x.z - (float)hi[2]);
+      lo[3] = (_Float16)(x.w - (float)hi[3]);
+      *reinterpret_cast<halfx4*>(&out[(int64_t)row * 2 * RP + c]) = hi;
+      *reinterpret_cast<halfx4*>(&out[(int64_t)row * 2 * RP + RP + c]) = lo;
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < rows * RP; e += 256) {
     const int row = e / RP;
     const int c = e - row * RP;

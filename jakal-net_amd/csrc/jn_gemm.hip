@@ -151,10 +151,10 @@ __device__ __forceinline__ bool aligned16(const float* p) { return (reinterpret_
 // traffic per use.
 template <bool A_KC, bool B_KC, int USE, int TILE>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
-  // K slice: 32 for the 64 x 64 tile, 64 for the 32 x 32 tile, whose
+  // K slice: 32 for the 64 x 64 tile, 128 for the 32 x 32 tile, whose
   // workgroups do too little per 16-wide slice to hide its load latency
   // (16-wide sub-slices, summed in the same order as separate slices)
-  constexpr int BK = TILE == 32 ? 64 : 32;
+  constexpr int BK = TILE == 32 ? 128 : 32;
   constexpr int GS = BK + 4;                  // LDS row stride (floats)
   constexpr int KQ = BK / 4;                  // float4s of a k-contiguous row slice
   constexpr int NF4 = TILE * BK / 4;          // float4s per operand and K slice

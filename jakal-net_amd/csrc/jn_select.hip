@@ -1083,11 +1083,19 @@ __global__ __launch_bounds__(CW > 0 ? CW * 64 : 256,
       if (need_merge() && lane == 0) s_flag[fl] = 1;
       const int fl_next = fl == 2 ? 0 : fl + 1;
       if (wave == 0 && lane == 0) s_flag[fl_next] = 0;
-      if constexpr (NBUF == 1) __syncthreads();
+      // With one buffer the flags are final after the first barrier: read
+      // there, the flag's LDS latency hides behind the staging store and the
+      // second barrier.
+      int flag = 0;
+      if constexpr (NBUF == 1) {
+        __syncthreads();
+        flag = s_flag[fl];
+      }
       if (!last) stage_store(NBUF == 2 ? (c + 1) & 1 : 0);
       __syncthreads();
       if (c + 2 < nchunks) stage_load(c + 2);
-      const bool go = last ? need_final() : __builtin_amdgcn_readfirstlane(s_flag[fl]) != 0;
+      if constexpr (NBUF == 2) flag = s_flag[fl];
+      const bool go = last ? need_final() : __builtin_amdgcn_readfirstlane(flag) != 0;
       merge(go, last);
       fl = fl_next;
     }

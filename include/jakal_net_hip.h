@@ -507,6 +507,77 @@ int jn_transition_topk_backward_multihead(
     void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
 /*
+ * Max-aggregated multi-head scores on the dense paths: every pair's score is
+ * max_h (P_t,h diag(w_h) P_s,h^T + b_h) (H heads of rank r stacked as in the
+ * multi-head edge-list entry points; bias [H] or NULL), one fp32 MFMA score
+ * GEMM per head folding into a running max whose epilogue records the first
+ * head attaining it; the backward passes each pair's score gradient to that
+ * head only (rank-r products on the gradient masked per head, per-head bias
+ * sums).  H * r <= 128.
+ *
+ * Dense propagation: arguments as jn_propagation_dense_forward_chunked /
+ * _backward_chunked with (rank, heads).  edge_chunk
+ * (jn_propagation_dense_multihead_chunk_bytes) holds a chunk of chunk_batch
+ * batch elements' edge matrices and winning heads; the forward leaves the
+ * last chunk there (chunk_resident = 1 in the backward reuses it), the
+ * backward rebuilds the other chunks from the projections.  A softsign
+ * backward writes its score gradient over the chunk's edges.
+ * Replace propagation_dense's multi-head branch (native/jakal_net_native.cpp:
+ * 5962-6076 over pairwise_scores, 724-752).
+ */
+size_t jn_propagation_dense_multihead_chunk_bytes(int64_t batch, int64_t nodes, int64_t chunk_batch);
+size_t jn_propagation_dense_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                                      int64_t rank, int64_t heads, int32_t compress_kind,
+                                                      int64_t chunk_batch);
+int jn_propagation_dense_forward_multihead(const float* layer_val, const float* projected_state,
+                                           const float* projected_val, const float* target_weight,
+                                           const float* source_weight, const float* core_weight, const float* bias,
+                                           int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                           int64_t rank, int64_t heads, int32_t compress_kind, int32_t causal,
+                                           int64_t chunk_batch, float* delta_state, float* delta_val,
+                                           float* projections, void* edge_chunk, size_t edge_chunk_bytes,
+                                           jn_stream_t stream);
+int jn_propagation_dense_backward_multihead(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* bias, const float* projections,
+    void* edge_chunk, size_t edge_chunk_bytes, const float* grad_delta_state, const float* grad_delta_val,
+    int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t heads,
+    int32_t compress_kind, int32_t causal, int32_t projected_val_is_layer_val, int64_t chunk_batch,
+    int32_t chunk_resident, float* grad_layer_val, float* grad_projected_state, float* grad_projected_val,
+    float* grad_target_weight, float* grad_source_weight, float* grad_core_weight, float* grad_bias,
+    void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+/*
+ * Dense transitions with max-aggregated multi-head route logits: arguments
+ * as jn_transition_dense_forward / _backward with (rank, heads), plus
+ * route_heads [B, Ns, Nd] (uint8), the winning head of every route, which the
+ * forward writes and the backward reads.
+ * Replace transition_pairwise_dense's multi-head branch
+ * (native/jakal_net_native.cpp:6705-6914 over route_scores, 889-917).
+ */
+int jn_transition_dense_forward_multihead(const float* sender_strength, const float* src_val, const float* dst_val,
+                                          const float* projected_state, const float* projected_val,
+                                          const float* source_weight, const float* target_weight,
+                                          const float* core_weight, const float* bias, float temperature,
+                                          int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                          int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
+                                          int32_t compress_kind, float* delta_state, float* delta_val,
+                                          float* src_proj, float* dst_proj, float* routes, uint8_t* route_heads,
+                                          jn_stream_t stream);
+size_t jn_transition_dense_multihead_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                                                     int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                                     int64_t heads);
+int jn_transition_dense_backward_multihead(
+    const float* sender_strength, const float* src_val, const float* dst_val, const float* projected_state,
+    const float* projected_val, const float* source_weight, const float* target_weight, const float* core_weight,
+    const float* src_proj, const float* dst_proj, const float* routes, const uint8_t* route_heads,
+    const float* grad_delta_state, const float* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes,
+    int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
+    int32_t compress_kind, float* grad_sender_strength, float* grad_src_val, float* grad_dst_val,
+    float* grad_projected_state, float* grad_projected_val, float* grad_source_weight, float* grad_target_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+
+/*
  * bf16 layers (layer values under autocast, src/jakal_net/modules.py:95-97;
  * bf16/fp16 score operands of native/jakal_net_native_cuda.cu:2492-2497).
  * The uint16_t tensors hold bf16 bit patterns: layer_val, projected_val and

@@ -133,17 +133,14 @@ int check_propagation_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64
 
 int64_t window_width(int64_t window, int64_t nodes) { return window + 1 < nodes ? window + 1 : nodes; }
 
-// Heads of a multi-head entry point (rank = one head's rank).  `select`: the
-// edges come from a top-k select, which scores at most four 32-rank K-steps.
-int check_heads(int64_t rank, int64_t heads, bool select) {
+// Heads of a multi-head entry point (rank = one head's rank).  A top-k select
+// of heads beyond the register kernels' four 32-rank K-steps, of k > 64 or of
+// more than 65,535 keys runs as the scored-rows select.
+int check_heads(int64_t rank, int64_t heads) {
   JN_REQUIRE(heads >= 2 && heads <= kMaxHeads, kUnsupported,
              "multi-head entry points take 2..%d heads (got %lld); one head is the single-head entry point",
              kMaxHeads, (long long)heads);
   JN_REQUIRE(rank >= 1 && heads * rank <= 128, kUnsupported, "heads x rank must be in [1, 128] (heads=%lld rank=%lld)",
-             (long long)heads, (long long)rank);
-  JN_REQUIRE(!select || select_heads_fit(rank, heads), kUnsupported,
-             "a multi-head top-k select scores heads x ceil(rank / 32) <= 4 K-steps of 32 ranks (heads=%lld "
-             "rank=%lld)",
              (long long)heads, (long long)rank);
   return kOk;
 }
@@ -311,15 +308,16 @@ struct DenseScratch {
   float* dP;      // [M, 2r]
   float* rowsum;  // [M]
   float* part_c;  // [M, r]
+  float* hrowsum; // [M, heads] per-head bias partials (multi-head only)
   float* stage;
   float* splitk;
   size_t bytes;
 };
 
 // g_batch / e_batch: batch elements of the score-gradient / edge-matrix buffers
-// (0: none)
+// (0: none); r counts every head's ranks
 DenseScratch carve_dense(void* base, size_t size, int64_t B, int64_t N, int64_t Din, int64_t r, int64_t g_batch,
-                         int64_t e_batch) {
+                         int64_t e_batch, int64_t heads = 1) {
   Workspace ws(base, size);
   DenseScratch s{};
   const int64_t M = B * N;
@@ -328,7 +326,8 @@ DenseScratch carve_dense(void* base, size_t size, int64_t B, int64_t N, int64_t 
   s.dP = ws.take<float>(M * 2 * r);
   s.rowsum = ws.take<float>(M * dense_epi_parts((int)N));  // per-row totals, or the epilogue's block partials
   s.part_c = ws.take<float>(M * r);
-  s.stage = ws.take<float>(finalize_stage_floats((int)r));
+  s.hrowsum = heads > 1 ? ws.take<float>(M * heads) : nullptr;
+  s.stage = ws.take<float>(finalize_stage_floats((int)r, (int)heads));
   s.splitk = ws.take<float>(gemm_grad_weight_workspace((int)(2 * r), (int)Din, (int)M) / sizeof(float));
   s.bytes = ws.used;
   return s;
@@ -351,23 +350,24 @@ struct TransitionDenseScratch {
   float* G;       // [B, Ns, Nd] route / logit gradient
   float* dPs;     // [B*Ns, r]
   float* dPt;     // [B*Nd, r]
-  float* rowsum;  // [B*Ns]
+  float* rowsum;  // [B*Ns] ([B*Ns, heads] with heads > 1)
   float* part_c;  // [B*Ns, r]
   float* stage;
   float* splitk;
   size_t bytes;
 };
 
+// r counts every head's ranks
 TransitionDenseScratch carve_transition_dense(void* base, size_t size, int64_t B, int64_t Ns, int64_t Nd,
-                                              int64_t Dsrc, int64_t Ddst, int64_t r) {
+                                              int64_t Dsrc, int64_t Ddst, int64_t r, int64_t heads = 1) {
   Workspace ws(base, size);
   TransitionDenseScratch s{};
   s.G = ws.take<float>(B * Ns * Nd);
   s.dPs = ws.take<float>(B * Ns * r);
   s.dPt = ws.take<float>(B * Nd * r);
-  s.rowsum = ws.take<float>(B * Ns);
+  s.rowsum = ws.take<float>(B * Ns * heads);
   s.part_c = ws.take<float>(B * Ns * r);
-  s.stage = ws.take<float>(finalize_stage_floats((int)r));
+  s.stage = ws.take<float>(finalize_stage_floats((int)r, (int)heads));
   const size_t sk = std::max(gemm_grad_weight_workspace((int)r, (int)Dsrc, (int)(B * Ns)),
                              gemm_grad_weight_workspace((int)r, (int)Ddst, (int)(B * Nd)));
   s.splitk = ws.take<float>(sk / sizeof(float));
@@ -375,14 +375,54 @@ TransitionDenseScratch carve_transition_dense(void* base, size_t size, int64_t B
   return s;
 }
 
+// Max-aggregated multi-head scores of batch elements [b0, b0 + nb)
+// (jakal_net_native.cpp:724-752): S = max_h (P_t,h diag(w_h) P_s,h^T + b_h)
+// over the heads' rank slices of the [N, 2r] projection rows (r = heads *
+// head rank), one fp32 MFMA GEMM per head whose epilogue folds its scores into
+// E; head_mat records the first head attaining each pair's max.
+int dense_head_scores(const float* core_weight, const float* bias, int b0, int nb, int N, int r, int heads,
+                      const float* projections, float* E, uint8_t* head_mat, hipStream_t st) {
+  const int64_t pr = (int64_t)b0 * N;
+  const int rh = r / heads;
+  for (int h = 0; h < heads; ++h) {
+    BatchedGemm sg{};
+    sg.A = projections + pr * 2 * r + h * rh; sg.lda = 2 * r; sg.a_bs = (int64_t)N * 2 * r; sg.a_kcontig = true;
+    sg.B = projections + pr * 2 * r + r + h * rh; sg.ldb = 2 * r; sg.b_bs = (int64_t)N * 2 * r; sg.b_kcontig = true;
+    sg.C = E; sg.ldc = N; sg.c_bs = (int64_t)N * N;
+    sg.a_kscale = core_weight + h * rh;
+    sg.M = N; sg.N = N; sg.K = rh; sg.batch = nb;
+    sg.fold = h == 0 ? 1 : 2; sg.fold_head = h; sg.fold_bias = bias ? bias + h : nullptr; sg.fold_heads = head_mat;
+    const int rc = gemm_batched(sg, kGemmDenseScores, st);
+    if (rc) return rc;
+  }
+  return kOk;
+}
+
 // Dense propagation forward over batch elements [b0, b0 + nb) (propagation.py:
 // 207-220): the edge matrix E of those elements (batch stride N*N), then
 // delta_state = E ps and delta_val = E pv.  projections holds every batch
-// element's [N, 2r] projection rows.
+// element's [N, 2r] projection rows.  heads > 1: max-aggregated scores over
+// the heads' rank slices (r = heads * head rank, bias [heads]), with the
+// winning head of every pair in head_mat [nb, N, N].
 int dense_forward_range(const float* projected_state, const float* projected_val, const float* core_weight,
                         const float* bias, int b0, int nb, int N, int D, int r, int compress_kind, bool causal,
-                        const float* projections, float* E, float* delta_state, float* delta_val, hipStream_t st) {
+                        const float* projections, float* E, float* delta_state, float* delta_val, hipStream_t st,
+                        int heads = 1, uint8_t* head_mat = nullptr) {
   const int64_t pr = (int64_t)b0 * N;  // first row of the range
+  if (heads > 1) {
+    int rc = dense_head_scores(core_weight, bias, b0, nb, N, r, heads, projections, E, head_mat, st);
+    if (rc) return rc;
+    // E = compress(S) in place (the heads' biases are in S), delta_state = E ps
+    rc = launch_dense_compress(E, nullptr, projected_state + pr, nb, N, compress_kind, causal, delta_state + pr, st);
+    if (rc) return rc;
+    BatchedGemm ag{};
+    ag.A = E; ag.lda = N; ag.a_bs = (int64_t)N * N; ag.a_kcontig = true;
+    ag.B = projected_val + pr * D; ag.ldb = D; ag.b_bs = (int64_t)N * D; ag.b_kcontig = false;
+    ag.C = delta_val + pr * D; ag.ldc = D; ag.c_bs = (int64_t)N * D;
+    ag.M = N; ag.N = D; ag.K = N; ag.batch = nb;
+    ag.causal_k = causal ? kCausalKLower : kCausalKNone;
+    return gemm_batched(ag, kGemmDenseAggregate, st);
+  }
   // S_b = (P_t diag(w_hat)) P_s^T
   BatchedGemm sg{};
   sg.A = projections + pr * 2 * r; sg.lda = 2 * r; sg.a_bs = (int64_t)N * 2 * r; sg.a_kcontig = true;
@@ -432,7 +472,8 @@ int dense_backward(const float* layer_val, const float* projected_state, const f
                    int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
                    int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
                    float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
-                   float* grad_core_weight, float* grad_bias, const DenseScratch& s, hipStream_t st) {
+                   float* grad_core_weight, float* grad_bias, const DenseScratch& s, hipStream_t st, int heads = 1,
+                   uint8_t* head_mat = nullptr) {
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
                  projections && E && G && grad_delta_state && grad_delta_val,
              kInvalidArgument, "null tensor pointer");
@@ -453,7 +494,14 @@ int dense_backward(const float* layer_val, const float* projected_state, const f
     const int nb = std::min(chunk_batch, B - b0);
     const int64_t pr = (int64_t)b0 * N;
     float* rowsum = s.rowsum + (fused ? pr * parts : pr);
-    if (recompute && !(last_resident && c == nchunks - 1)) {
+    if (recompute && !(last_resident && c == nchunks - 1) && heads > 1) {
+      // the forward's edges and winning heads of this chunk (state sums to scratch)
+      rc = dense_head_scores(core_weight, bias, b0, nb, N, r, heads, projections, E, head_mat, st);
+      if (rc) return rc;
+      rc = launch_dense_compress(E, nullptr, projected_state + pr, nb, N, compress_kind, causal != 0,
+                                 s.part_c + pr * r, st);
+      if (rc) return rc;
+    } else if (recompute && !(last_resident && c == nchunks - 1)) {
       // the forward's edges of this chunk; its state sums go to scratch that
       // later steps overwrite (the row sums, or the scale partials)
       BatchedGemm sg{};
@@ -509,24 +557,39 @@ int dense_backward(const float* layer_val, const float* projected_state, const f
       if (rc) return rc;
     }
 
+    // multi-head: each pair's score gradient reaches its winning head only --
+    // the per-head bias partials, and the rank-r products below on G masked
+    // to that head's pairs
+    if (heads > 1) {
+      rc = launch_head_rowsum(G, head_mat, N, N, (int64_t)nb * N, heads, s.hrowsum + pr * heads, st);
+      if (rc) return rc;
+    }
+
     // 3. projection grads: dP_t = w_hat * (G_s P_s), dP_s = w_hat * (G_s^T P_t) (+ w_hat partials)
-    BatchedGemm tg{};
-    tg.A = G; tg.lda = N; tg.a_bs = (int64_t)N * N; tg.a_kcontig = true;
-    tg.B = projections + pr * 2 * r + r; tg.ldb = 2 * r; tg.b_bs = (int64_t)N * 2 * r; tg.b_kcontig = false;
-    tg.C = s.dP + pr * 2 * r; tg.ldc = 2 * r; tg.c_bs = (int64_t)N * 2 * r;
-    tg.c_nscale = core_weight;
-    tg.M = N; tg.N = r; tg.K = N; tg.batch = nb;
-    tg.causal_k = lower;
-    rc = gemm_batched(tg, kGemmDenseTargetGrad, st);
-    if (rc) return rc;
-    BatchedGemm sg2{};
-    sg2.A = G; sg2.lda = N; sg2.a_bs = (int64_t)N * N; sg2.a_kcontig = false;
-    sg2.B = projections + pr * 2 * r; sg2.ldb = 2 * r; sg2.b_bs = (int64_t)N * 2 * r; sg2.b_kcontig = false;
-    sg2.C = s.dP + pr * 2 * r + r; sg2.ldc = 2 * r; sg2.c_bs = (int64_t)N * 2 * r;
-    sg2.M = N; sg2.N = r; sg2.K = N; sg2.batch = nb;
-    sg2.causal_k = upper;
-    rc = gemm_batched(sg2, kGemmDenseSourceGrad, st);
-    if (rc) return rc;
+    const int rh = r / heads;
+    for (int h = 0; h < heads; ++h) {
+      BatchedGemm tg{};
+      tg.A = G; tg.lda = N; tg.a_bs = (int64_t)N * N; tg.a_kcontig = true;
+      tg.B = projections + pr * 2 * r + r + h * rh; tg.ldb = 2 * r; tg.b_bs = (int64_t)N * 2 * r;
+      tg.b_kcontig = false;
+      tg.C = s.dP + pr * 2 * r + h * rh; tg.ldc = 2 * r; tg.c_bs = (int64_t)N * 2 * r;
+      tg.c_nscale = core_weight + h * rh;
+      tg.M = N; tg.N = rh; tg.K = N; tg.batch = nb;
+      tg.causal_k = lower;
+      if (heads > 1) { tg.a_heads = head_mat; tg.a_head = h; }
+      rc = gemm_batched(tg, kGemmDenseTargetGrad, st);
+      if (rc) return rc;
+      BatchedGemm sg2{};
+      sg2.A = G; sg2.lda = N; sg2.a_bs = (int64_t)N * N; sg2.a_kcontig = false;
+      sg2.B = projections + pr * 2 * r + h * rh; sg2.ldb = 2 * r; sg2.b_bs = (int64_t)N * 2 * r;
+      sg2.b_kcontig = false;
+      sg2.C = s.dP + pr * 2 * r + r + h * rh; sg2.ldc = 2 * r; sg2.c_bs = (int64_t)N * 2 * r;
+      sg2.M = N; sg2.N = rh; sg2.K = N; sg2.batch = nb;
+      sg2.causal_k = upper;
+      if (heads > 1) { sg2.a_heads = head_mat; sg2.a_head = h; }
+      rc = gemm_batched(sg2, kGemmDenseSourceGrad, st);
+      if (rc) return rc;
+    }
     rc = launch_scale_grad_partials(s.dP + pr * 2 * r + r, 2 * r, projections + pr * 2 * r + r, 2 * r, core_weight, r,
                                     (int64_t)nb * N, s.part_c + pr * r, st);
     if (rc) return rc;
@@ -547,6 +610,9 @@ int dense_backward(const float* layer_val, const float* projected_state, const f
   }
 
   // 5. w_hat and bias grads
+  if (heads > 1)
+    return launch_finalize_small_grads(s.part_c, M, r, grad_core_weight, 0, s.hrowsum, M, grad_bias, s.stage, st,
+                                       heads);
   return launch_finalize_small_grads(s.part_c, M, r, grad_core_weight, 0, s.rowsum, n_rowsum, grad_bias, s.stage,
                                      st);
 }
@@ -1686,7 +1752,7 @@ int jn_propagation_topk_forward_multihead(const float* layer_val, const float* p
                                           float* delta_state, float* delta_val, float* projections,
                                           int32_t* topk_index, float* topk_score, uint8_t* topk_head,
                                           void* edge_layout, size_t edge_layout_bytes, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
-  const int rc = check_heads(rank, heads, true);
+  const int rc = check_heads(rank, heads);
   if (rc) return rc;
   return propagation_topk_forward_impl(layer_val, projected_state, projected_val, target_weight, source_weight,
                                        core_weight, bias, batch, nodes, in_dim, out_dim, rank * heads, heads, topk,
@@ -1702,7 +1768,7 @@ int jn_propagation_topk_backward_multihead(
     int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
     float* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
     float* grad_bias, const void* edge_layout, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
-  int rc = check_heads(rank, heads, true);
+  int rc = check_heads(rank, heads);
   if (rc) return rc;
   rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank * heads, topk, compress_kind);
   if (rc) return rc;
@@ -1729,7 +1795,7 @@ int jn_propagation_window_forward_multihead(const float* layer_val, const float*
                                             float* delta_state, float* delta_val, float* projections,
                                             int32_t* edge_index, float* edge_score, uint8_t* edge_head,
                                             jn_stream_t stream) {
-  const int rc = check_heads(rank, heads, false);
+  const int rc = check_heads(rank, heads);
   if (rc) return rc;
   return propagation_window_forward_impl(layer_val, projected_state, projected_val, target_weight, source_weight,
                                          core_weight, bias, batch, nodes, in_dim, out_dim, rank * heads, heads,
@@ -1745,7 +1811,7 @@ int jn_propagation_window_backward_multihead(
     int32_t compress_kind, int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
     float* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
     float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
-  int rc = check_heads(rank, heads, false);
+  int rc = check_heads(rank, heads);
   if (rc) return rc;
   JN_REQUIRE(window >= 0, kInvalidArgument, "window must be non-negative (got %lld)", (long long)window);
   const int64_t width = window_width(window, nodes);
@@ -1764,8 +1830,7 @@ size_t jn_transition_topk_multihead_workspace_bytes(int64_t batch, int64_t src_n
                                                     int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
                                                     int64_t heads, int64_t topk) {
   (void)val_dim;
-  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || topk < 1 || heads < 2) return 0;
-  if (route_edges(topk, dst_nodes) < dst_nodes && !select_heads_fit(rank, heads)) return 0;
+  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || topk < 1 || heads < 2 || rank * heads > 128) return 0;
   return carve_transition(nullptr, 0, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank * heads,
                           route_edges(topk, dst_nodes), heads)
       .bytes;
@@ -1781,7 +1846,7 @@ int jn_transition_topk_forward_multihead(const float* sender_strength, const flo
                                          float* src_proj, float* dst_proj, int32_t* route_index, float* route_logit,
                                          uint8_t* route_head, void* workspace, size_t workspace_bytes,
                                          jn_stream_t stream) {
-  const int rc = check_heads(rank, heads, route_edges(topk, dst_nodes) < dst_nodes);
+  const int rc = check_heads(rank, heads);
   if (rc) return rc;
   return transition_topk_forward_impl(sender_strength, src_val, dst_val, projected_state, projected_val,
                                       source_weight, target_weight, core_weight, bias, temperature, batch, src_nodes,
@@ -1800,7 +1865,7 @@ int jn_transition_topk_backward_multihead(
     float* grad_src_val, float* grad_dst_val, float* grad_projected_state, float* grad_projected_val,
     float* grad_source_weight, float* grad_target_weight, float* grad_core_weight, float* grad_bias,
     void* workspace, size_t workspace_bytes, jn_stream_t stream) {
-  const int rc = check_heads(rank, heads, route_edges(topk, dst_nodes) < dst_nodes);
+  const int rc = check_heads(rank, heads);
   if (rc) return rc;
   return transition_topk_backward_impl(sender_strength, src_val, dst_val, projected_state, projected_val,
                                        source_weight, target_weight, core_weight, src_proj, dst_proj, route_index,
@@ -2038,16 +2103,22 @@ int jn_propagation_dense_backward_chunked(
                         grad_source_weight, grad_core_weight, grad_bias, s, static_cast<hipStream_t>(stream));
 }
 
-int jn_transition_dense_forward(const float* sender_strength, const float* src_val, const float* dst_val,
-                                const float* projected_state, const float* projected_val, const float* source_weight,
-                                const float* target_weight, const float* core_weight, const float* bias,
-                                float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
-                                int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
-                                int32_t compress_kind, float* delta_state, float* delta_val, float* src_proj,
-                                float* dst_proj, float* routes, jn_stream_t stream) {
+// Dense transition forward; heads > 1: max-aggregated route logits over the
+// heads' rank slices (rank = heads * head rank, bias [heads]), the winning
+// head of every (source, destination) pair in route_heads [B, Ns, Nd].
+static int transition_dense_forward_impl(const float* sender_strength, const float* src_val, const float* dst_val,
+                                         const float* projected_state, const float* projected_val,
+                                         const float* source_weight, const float* target_weight,
+                                         const float* core_weight, const float* bias, float temperature,
+                                         int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                         int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
+                                         int32_t compress_kind, float* delta_state, float* delta_val,
+                                         float* src_proj, float* dst_proj, float* routes, uint8_t* route_heads,
+                                         jn_stream_t stream) {
   int rc = check_transition_dense_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, compress_kind,
                                          temperature);
   if (rc) return rc;
+  JN_REQUIRE(heads == 1 || route_heads, kInvalidArgument, "null tensor pointer");
   JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
                  target_weight && core_weight && delta_state && delta_val && src_proj && dst_proj && routes,
              kInvalidArgument, "null tensor pointer");
@@ -2061,17 +2132,25 @@ int jn_transition_dense_forward(const float* sender_strength, const float* src_v
   rc = gemm_project(dst_val, dst_dim, target_weight, target_weight, r, dst_dim, dst_proj, r, B * Nd, r, (int)dst_dim,
                     st);
   if (rc) return rc;
-  // 2. raw logits L_b = (P_s diag(w)) P_t^T
-  BatchedGemm lg{};
-  lg.A = src_proj; lg.lda = r; lg.a_bs = (int64_t)Ns * r; lg.a_kcontig = true;
-  lg.B = dst_proj; lg.ldb = r; lg.b_bs = (int64_t)Nd * r; lg.b_kcontig = true;
-  lg.C = routes; lg.ldc = Nd; lg.c_bs = (int64_t)Ns * Nd;
-  lg.a_kscale = core_weight;
-  lg.M = Ns; lg.N = Nd; lg.K = r; lg.batch = B;
-  rc = gemm_batched(lg, kGemmRouteLogits, st);
-  if (rc) return rc;
+  // 2. raw logits L_b = (P_s diag(w)) P_t^T; with heads, max_h of each head's
+  //    logits plus its bias (one GEMM per head, folded in the epilogue)
+  const int H = (int)heads, rh = r / H;
+  for (int h = 0; h < H; ++h) {
+    BatchedGemm lg{};
+    lg.A = src_proj + h * rh; lg.lda = r; lg.a_bs = (int64_t)Ns * r; lg.a_kcontig = true;
+    lg.B = dst_proj + h * rh; lg.ldb = r; lg.b_bs = (int64_t)Nd * r; lg.b_kcontig = true;
+    lg.C = routes; lg.ldc = Nd; lg.c_bs = (int64_t)Ns * Nd;
+    lg.a_kscale = core_weight + h * rh;
+    lg.M = Ns; lg.N = Nd; lg.K = rh; lg.batch = B;
+    if (H > 1) {
+      lg.fold = h == 0 ? 1 : 2; lg.fold_head = h; lg.fold_bias = bias ? bias + h : nullptr;
+      lg.fold_heads = route_heads;
+    }
+    rc = gemm_batched(lg, kGemmRouteLogits, st);
+    if (rc) return rc;
+  }
   // 3. routes R = compress((L + b) / T) over destinations, in place
-  rc = launch_route_dense_compress(routes, bias, 1.0f / temperature, B, Ns, Nd, compress_kind, st);
+  rc = launch_route_dense_compress(routes, H > 1 ? nullptr : bias, 1.0f / temperature, B, Ns, Nd, compress_kind, st);
   if (rc) return rc;
   // 4. delta_state = R^T (rho * ps), delta_val = R^T diag(rho) pv
   rc = launch_route_dense_colsum(routes, sender_strength, projected_state, B, Ns, Nd, delta_state, st);
@@ -2085,6 +2164,19 @@ int jn_transition_dense_forward(const float* sender_strength, const float* src_v
   return gemm_batched(ag, kGemmRouteAggregate, st);
 }
 
+int jn_transition_dense_forward(const float* sender_strength, const float* src_val, const float* dst_val,
+                                const float* projected_state, const float* projected_val, const float* source_weight,
+                                const float* target_weight, const float* core_weight, const float* bias,
+                                float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                                int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                int32_t compress_kind, float* delta_state, float* delta_val, float* src_proj,
+                                float* dst_proj, float* routes, jn_stream_t stream) {
+  return transition_dense_forward_impl(sender_strength, src_val, dst_val, projected_state, projected_val,
+                                       source_weight, target_weight, core_weight, bias, temperature, batch, src_nodes,
+                                       dst_nodes, src_dim, dst_dim, val_dim, rank, 1, compress_kind, delta_state,
+                                       delta_val, src_proj, dst_proj, routes, nullptr, stream);
+}
+
 size_t jn_transition_dense_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
                                            int64_t dst_dim, int64_t val_dim, int64_t rank) {
   (void)val_dim;
@@ -2092,25 +2184,24 @@ size_t jn_transition_dense_workspace_bytes(int64_t batch, int64_t src_nodes, int
   return carve_transition_dense(nullptr, 0, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank).bytes;
 }
 
-int jn_transition_dense_backward(const float* sender_strength, const float* src_val, const float* dst_val,
-                                 const float* projected_state, const float* projected_val, const float* source_weight,
-                                 const float* target_weight, const float* core_weight, const float* src_proj,
-                                 const float* dst_proj, const float* routes, const float* grad_delta_state,
-                                 const float* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes,
-                                 int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
-                                 int32_t compress_kind, float* grad_sender_strength, float* grad_src_val,
-                                 float* grad_dst_val, float* grad_projected_state, float* grad_projected_val,
-                                 float* grad_source_weight, float* grad_target_weight, float* grad_core_weight,
-                                 float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+static int transition_dense_backward_impl(
+    const float* sender_strength, const float* src_val, const float* dst_val, const float* projected_state,
+    const float* projected_val, const float* source_weight, const float* target_weight, const float* core_weight,
+    const float* src_proj, const float* dst_proj, const float* routes, const uint8_t* route_heads,
+    const float* grad_delta_state, const float* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes,
+    int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
+    int32_t compress_kind, float* grad_sender_strength, float* grad_src_val, float* grad_dst_val,
+    float* grad_projected_state, float* grad_projected_val, float* grad_source_weight, float* grad_target_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   int rc = check_transition_dense_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, compress_kind,
                                          temperature);
   if (rc) return rc;
   JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
                  target_weight && core_weight && src_proj && dst_proj && routes && grad_delta_state &&
-                 grad_delta_val,
+                 grad_delta_val && (heads == 1 || route_heads),
              kInvalidArgument, "null tensor pointer");
-  TransitionDenseScratch s =
-      carve_transition_dense(workspace, workspace_bytes, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank);
+  TransitionDenseScratch s = carve_transition_dense(workspace, workspace_bytes, batch, src_nodes, dst_nodes, src_dim,
+                                                    dst_dim, rank, heads);
   JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
              "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -2139,24 +2230,37 @@ int jn_transition_dense_backward(const float* sender_strength, const float* src_
     rc = gemm_batched(vg, kGemmRouteValueGrad, st);
     if (rc) return rc;
   }
+  // multi-head: each pair's logit gradient reaches its winning head only (per-head
+  // bias partials; the rank-r products below on G masked to that head's pairs)
+  const int H = (int)heads, rh = r / H;
+  if (H > 1) {
+    rc = launch_head_rowsum(s.G, route_heads, Nd, Nd, (int64_t)B * Ns, H, s.rowsum, st);
+    if (rc) return rc;
+  }
   // 3. projection grads: dP_s = w * (G P_t) (+ w partials), dP_t = w * (G^T P_s)
-  BatchedGemm sg{};
-  sg.A = s.G; sg.lda = Nd; sg.a_bs = (int64_t)Ns * Nd; sg.a_kcontig = true;
-  sg.B = dst_proj; sg.ldb = r; sg.b_bs = (int64_t)Nd * r; sg.b_kcontig = false;
-  sg.C = s.dPs; sg.ldc = r; sg.c_bs = (int64_t)Ns * r;
-  sg.M = Ns; sg.N = r; sg.K = Nd; sg.batch = B;
-  rc = gemm_batched(sg, kGemmRouteSourceGrad, st);
-  if (rc) return rc;
+  for (int h = 0; h < H; ++h) {
+    BatchedGemm sg{};
+    sg.A = s.G; sg.lda = Nd; sg.a_bs = (int64_t)Ns * Nd; sg.a_kcontig = true;
+    sg.B = dst_proj + h * rh; sg.ldb = r; sg.b_bs = (int64_t)Nd * r; sg.b_kcontig = false;
+    sg.C = s.dPs + h * rh; sg.ldc = r; sg.c_bs = (int64_t)Ns * r;
+    sg.M = Ns; sg.N = rh; sg.K = Nd; sg.batch = B;
+    if (H > 1) { sg.a_heads = route_heads; sg.a_head = h; }
+    rc = gemm_batched(sg, kGemmRouteSourceGrad, st);
+    if (rc) return rc;
+  }
   rc = launch_scale_grad_partials(s.dPs, r, src_proj, r, core_weight, r, (int64_t)B * Ns, s.part_c, st);
   if (rc) return rc;
-  BatchedGemm tg{};
-  tg.A = s.G; tg.lda = Nd; tg.a_bs = (int64_t)Ns * Nd; tg.a_kcontig = false;
-  tg.B = src_proj; tg.ldb = r; tg.b_bs = (int64_t)Ns * r; tg.b_kcontig = false;
-  tg.C = s.dPt; tg.ldc = r; tg.c_bs = (int64_t)Nd * r;
-  tg.c_nscale = core_weight;
-  tg.M = Nd; tg.N = r; tg.K = Ns; tg.batch = B;
-  rc = gemm_batched(tg, kGemmRouteTargetGrad, st);
-  if (rc) return rc;
+  for (int h = 0; h < H; ++h) {
+    BatchedGemm tg{};
+    tg.A = s.G; tg.lda = Nd; tg.a_bs = (int64_t)Ns * Nd; tg.a_kcontig = false;
+    tg.B = src_proj + h * rh; tg.ldb = r; tg.b_bs = (int64_t)Ns * r; tg.b_kcontig = false;
+    tg.C = s.dPt + h * rh; tg.ldc = r; tg.c_bs = (int64_t)Nd * r;
+    tg.c_nscale = core_weight + h * rh;
+    tg.M = Nd; tg.N = rh; tg.K = Ns; tg.batch = B;
+    if (H > 1) { tg.a_heads = route_heads; tg.a_head = h; }
+    rc = gemm_batched(tg, kGemmRouteTargetGrad, st);
+    if (rc) return rc;
+  }
   // 4. projection weight and input grads
   const int Ms = B * Ns, Mt = B * Nd;
   if (grad_source_weight) {
@@ -2179,9 +2283,172 @@ int jn_transition_dense_backward(const float* sender_strength, const float* src_
                          Mt, (int)dst_dim, r, st);
     if (rc) return rc;
   }
-  // 5. w and bias grads (exactly 0 for softmax routes: shifting a row's logits leaves it unchanged)
+  // 5. w and bias grads (one head: exactly 0 for softmax routes, since shifting a
+  //    row's logits leaves it unchanged; several: each head's pairs only)
+  if (H > 1)
+    return launch_finalize_small_grads(s.part_c, Ms, r, grad_core_weight, 0, s.rowsum, Ms, grad_bias, s.stage, st, H);
   return launch_finalize_small_grads(s.part_c, Ms, r, grad_core_weight, 0, s.rowsum, compress_kind == 0 ? 0 : Ms,
                                      grad_bias, s.stage, st);
+}
+
+int jn_transition_dense_backward(const float* sender_strength, const float* src_val, const float* dst_val,
+                                 const float* projected_state, const float* projected_val, const float* source_weight,
+                                 const float* target_weight, const float* core_weight, const float* src_proj,
+                                 const float* dst_proj, const float* routes, const float* grad_delta_state,
+                                 const float* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes,
+                                 int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                 int32_t compress_kind, float* grad_sender_strength, float* grad_src_val,
+                                 float* grad_dst_val, float* grad_projected_state, float* grad_projected_val,
+                                 float* grad_source_weight, float* grad_target_weight, float* grad_core_weight,
+                                 float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  return transition_dense_backward_impl(
+      sender_strength, src_val, dst_val, projected_state, projected_val, source_weight, target_weight, core_weight,
+      src_proj, dst_proj, routes, nullptr, grad_delta_state, grad_delta_val, temperature, batch, src_nodes, dst_nodes,
+      src_dim, dst_dim, val_dim, rank, 1, compress_kind, grad_sender_strength, grad_src_val, grad_dst_val,
+      grad_projected_state, grad_projected_val, grad_source_weight, grad_target_weight, grad_core_weight, grad_bias,
+      workspace, workspace_bytes, stream);
+}
+
+// ---- max-aggregated multi-head dense forms ---------------------------------
+
+int jn_transition_dense_forward_multihead(const float* sender_strength, const float* src_val, const float* dst_val,
+                                          const float* projected_state, const float* projected_val,
+                                          const float* source_weight, const float* target_weight,
+                                          const float* core_weight, const float* bias, float temperature,
+                                          int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
+                                          int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
+                                          int32_t compress_kind, float* delta_state, float* delta_val,
+                                          float* src_proj, float* dst_proj, float* routes, uint8_t* route_heads,
+                                          jn_stream_t stream) {
+  int rc = check_heads(rank, heads);
+  if (rc) return rc;
+  return transition_dense_forward_impl(sender_strength, src_val, dst_val, projected_state, projected_val,
+                                       source_weight, target_weight, core_weight, bias, temperature, batch, src_nodes,
+                                       dst_nodes, src_dim, dst_dim, val_dim, rank * heads, heads, compress_kind,
+                                       delta_state, delta_val, src_proj, dst_proj, routes, route_heads, stream);
+}
+
+size_t jn_transition_dense_multihead_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+                                                     int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
+                                                     int64_t heads) {
+  (void)val_dim;
+  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || rank < 1 || heads < 1) return 0;
+  return carve_transition_dense(nullptr, 0, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank * heads, heads).bytes;
+}
+
+int jn_transition_dense_backward_multihead(
+    const float* sender_strength, const float* src_val, const float* dst_val, const float* projected_state,
+    const float* projected_val, const float* source_weight, const float* target_weight, const float* core_weight,
+    const float* src_proj, const float* dst_proj, const float* routes, const uint8_t* route_heads,
+    const float* grad_delta_state, const float* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes,
+    int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
+    int32_t compress_kind, float* grad_sender_strength, float* grad_src_val, float* grad_dst_val,
+    float* grad_projected_state, float* grad_projected_val, float* grad_source_weight, float* grad_target_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_heads(rank, heads);
+  if (rc) return rc;
+  return transition_dense_backward_impl(
+      sender_strength, src_val, dst_val, projected_state, projected_val, source_weight, target_weight, core_weight,
+      src_proj, dst_proj, routes, route_heads, grad_delta_state, grad_delta_val, temperature, batch, src_nodes,
+      dst_nodes, src_dim, dst_dim, val_dim, rank * heads, heads, compress_kind, grad_sender_strength, grad_src_val,
+      grad_dst_val, grad_projected_state, grad_projected_val, grad_source_weight, grad_target_weight,
+      grad_core_weight, grad_bias, workspace, workspace_bytes, stream);
+}
+
+// The edge chunk of the multi-head dense propagation entry points: E
+// [cb, N, N] fp32, then the winning head of every pair [cb, N, N] u8.
+struct DenseHeadChunk {
+  float* E;
+  uint8_t* heads;
+  size_t bytes;
+};
+static DenseHeadChunk carve_dense_head_chunk(void* base, size_t size, int64_t cb, int64_t N) {
+  Workspace ws(base, size);
+  DenseHeadChunk c{};
+  c.E = ws.take<float>(cb * N * N);
+  c.heads = ws.take<uint8_t>(cb * N * N);
+  c.bytes = ws.used;
+  return c;
+}
+
+size_t jn_propagation_dense_multihead_chunk_bytes(int64_t batch, int64_t nodes, int64_t chunk_batch) {
+  if (batch < 1 || nodes < 1 || chunk_batch < 1) return 0;
+  return carve_dense_head_chunk(nullptr, 0, chunk_batch < batch ? chunk_batch : batch, nodes).bytes;
+}
+
+size_t jn_propagation_dense_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                                      int64_t rank, int64_t heads, int32_t compress_kind,
+                                                      int64_t chunk_batch) {
+  (void)out_dim;
+  if (batch < 1 || nodes < 1 || rank < 1 || heads < 1 || chunk_batch < 1) return 0;
+  const int64_t cb = chunk_batch < batch ? chunk_batch : batch;
+  return carve_dense(nullptr, 0, batch, nodes, in_dim, rank * heads, compress_kind == 0 ? 0 : cb, 0, heads).bytes;
+}
+
+int jn_propagation_dense_forward_multihead(const float* layer_val, const float* projected_state,
+                                           const float* projected_val, const float* target_weight,
+                                           const float* source_weight, const float* core_weight, const float* bias,
+                                           int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                           int64_t rank, int64_t heads, int32_t compress_kind, int32_t causal,
+                                           int64_t chunk_batch, float* delta_state, float* delta_val,
+                                           float* projections, void* edge_chunk, size_t edge_chunk_bytes,
+                                           jn_stream_t stream) {
+  int rc = check_heads(rank, heads);
+  if (rc) return rc;
+  rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank * heads, compress_kind);
+  if (rc) return rc;
+  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
+                 delta_state && delta_val && projections && edge_chunk,
+             kInvalidArgument, "null tensor pointer");
+  JN_REQUIRE(chunk_batch >= 1, kInvalidArgument, "chunk_batch must be positive");
+  const int B = (int)batch, N = (int)nodes, R = (int)(rank * heads), D = (int)out_dim;
+  const int cb = (int)(chunk_batch < batch ? chunk_batch : batch);
+  const DenseHeadChunk ch = carve_dense_head_chunk(edge_chunk, edge_chunk_bytes, cb, N);
+  JN_REQUIRE(ch.bytes <= edge_chunk_bytes, kWorkspaceTooSmall, "edge chunk too small: need %zu bytes, got %zu",
+             ch.bytes, edge_chunk_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, R, in_dim, projections, 2 * R, B * N, 2 * R,
+                    (int)in_dim, st);
+  if (rc) return rc;
+  for (int b0 = 0; b0 < B; b0 += cb) {
+    rc = dense_forward_range(projected_state, projected_val, core_weight, bias, b0, std::min(cb, B - b0), N, D, R,
+                             compress_kind, causal != 0, projections, ch.E, delta_state, delta_val, st, (int)heads,
+                             ch.heads);
+    if (rc) return rc;
+  }
+  return kOk;
+}
+
+int jn_propagation_dense_backward_multihead(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* bias, const float* projections,
+    void* edge_chunk, size_t edge_chunk_bytes, const float* grad_delta_state, const float* grad_delta_val,
+    int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int64_t heads,
+    int32_t compress_kind, int32_t causal, int32_t projected_val_is_layer_val, int64_t chunk_batch,
+    int32_t chunk_resident, float* grad_layer_val, float* grad_projected_state, float* grad_projected_val,
+    float* grad_target_weight, float* grad_source_weight, float* grad_core_weight, float* grad_bias,
+    void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  int rc = check_heads(rank, heads);
+  if (rc) return rc;
+  rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank * heads, compress_kind);
+  if (rc) return rc;
+  JN_REQUIRE(chunk_batch >= 1, kInvalidArgument, "chunk_batch must be positive");
+  JN_REQUIRE(edge_chunk, kInvalidArgument, "null tensor pointer");
+  const int cb = (int)(chunk_batch < batch ? chunk_batch : batch);
+  const DenseHeadChunk ch = carve_dense_head_chunk(edge_chunk, edge_chunk_bytes, cb, nodes);
+  JN_REQUIRE(ch.bytes <= edge_chunk_bytes, kWorkspaceTooSmall, "edge chunk too small: need %zu bytes, got %zu",
+             ch.bytes, edge_chunk_bytes);
+  const int64_t R = rank * heads;
+  DenseScratch s = carve_dense(workspace, workspace_bytes, batch, nodes, in_dim, R, compress_kind == 0 ? 0 : cb, 0,
+                               heads);
+  JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
+             "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
+  return dense_backward(layer_val, projected_state, projected_val, target_weight, source_weight, core_weight, bias,
+                        projections, ch.E, compress_kind == 0 ? ch.E : s.G, cb, true, chunk_resident != 0,
+                        grad_delta_state, grad_delta_val, batch, nodes, in_dim, out_dim, R, compress_kind, causal,
+                        projected_val_is_layer_val, grad_layer_val, grad_projected_state, grad_projected_val,
+                        grad_target_weight, grad_source_weight, grad_core_weight, grad_bias, s,
+                        static_cast<hipStream_t>(stream), (int)heads, ch.heads);
 }
 
 }  // extern "C"

@@ -321,6 +321,60 @@ int launch_dense_part_rowsum(const float* part, int P, int64_t rows, float* out,
   return kOk;
 }
 
+// rowsum[row, h] = sum_j G[row, j] over the columns j whose winning head
+// head[row, j] is h (the bias gradients of max-aggregated multi-head scores),
+// h < H, in a fixed order: one wave per row, lane l sums columns 4l + 256t
+// (VEC) or l + 64t, then a butterfly per head.
+template <bool VEC>
+__global__ __launch_bounds__(256) void head_rowsum_kernel(const float* G, const uint8_t* head, int N, int64_t ld,
+                                                          int64_t rows, int H, float* rowsum) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  if (row >= rows) return;
+  const float* g = G + row * ld;
+  const uint8_t* hd = head + row * ld;
+  float acc[kMaxHeads];
+#pragma unroll
+  for (int h = 0; h < kMaxHeads; ++h) acc[h] = 0.0f;
+  auto add = [&](float v, uint32_t h) {
+#pragma unroll
+    for (int t = 0; t < kMaxHeads; ++t) acc[t] += (uint32_t)t == h ? v : 0.0f;
+  };
+  if constexpr (VEC) {
+    for (int j = 4 * lane; j < N; j += 256) {
+      const float4 v = *reinterpret_cast<const float4*>(g + j);
+      const uint32_t hb = *reinterpret_cast<const uint32_t*>(hd + j);
+      add(v.x, hb & 0xFFu);
+      add(v.y, (hb >> 8) & 0xFFu);
+      add(v.z, (hb >> 16) & 0xFFu);
+      add(v.w, hb >> 24);
+    }
+  } else {
+    for (int j = lane; j < N; j += kWave) add(g[j], hd[j]);
+  }
+  for (int h = 0; h < H; ++h) {
+    const float t = wave_sum(acc[h]);
+    if (lane == 0) rowsum[row * H + h] = t;
+  }
+}
+
+int launch_head_rowsum(const float* G, const uint8_t* head, int N, int64_t ld, int64_t rows, int H, float* rowsum,
+                       hipStream_t stream) {
+  JN_REQUIRE(H >= 1 && H <= kMaxHeads, kUnsupported, "1 to %d heads", kMaxHeads);
+  const int64_t blocks = (rows + 3) / 4;
+  JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "too many rows");
+  if (rows == 0) return kOk;
+  const bool vec = (N % 4 == 0) && (ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(G) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(head) & 3) == 0);
+  JN_PROFILE("head_rowsum_kernel", stream);
+  if (vec) hipLaunchKernelGGL(head_rowsum_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, G, head, N, ld,
+                              rows, H, rowsum);
+  else hipLaunchKernelGGL(head_rowsum_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, G, head, N, ld,
+                          rows, H, rowsum);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
 int launch_dense_colsum(const float* E, const float* w, int B, int N, float* out, hipStream_t stream) {
   return launch_colsum_rows(E, w, nullptr, B, N, N, out, "dense_colsum_kernel", stream);
 }

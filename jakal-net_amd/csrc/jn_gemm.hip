@@ -61,9 +61,75 @@ struct GemmArgs {
   const float* epi_gds;    // [batch, M]
   const float* epi_E;      // indexed like C
   float* epi_part;
+  // Head-max fold of multi-head scores (BatchedGemm::fold, score uses only).
+  int fold, fold_head;
+  const float* fold_bias;  // this head's bias (scalar) or null
+  uint8_t* fold_heads;     // winning head per element (bytes indexed like C) or null
+  // Head mask of the A operand (BatchedGemm::a_heads, score-gradient uses only).
+  const uint8_t* a_heads;
+  int a_head;
 };
 
 constexpr int kEpiBlock = 32;  // columns per epilogue partial sum
+
+// Uses whose epilogue may fold a head's scores into a running max, and uses
+// whose A operand (a score gradient) may be masked to one head's pairs.
+constexpr bool gemm_use_fold(int use) {
+  return use == kGemmDenseScores || use == kGemmRouteLogits || use == kGemmSelectScores;
+}
+constexpr bool gemm_use_amask(int use) {
+  return use == kGemmDenseTargetGrad || use == kGemmDenseSourceGrad || use == kGemmRouteSourceGrad ||
+         use == kGemmRouteTargetGrad;
+}
+
+// One element of the head-max fold: y = acc + this head's bias; the first
+// head (fold == 1) stores y, a later head (fold == 2) stores y only where it
+// exceeds the stored value (ties keep the earlier head) and records itself as
+// the winning head.
+__device__ __forceinline__ void fold_store(const GemmArgs& g, float acc, float* c, uint8_t* hd) {
+  const float y = acc + (g.fold_bias ? g.fold_bias[0] : 0.0f);
+  if (g.fold == 1) {
+    *c = y;
+    if (hd) *hd = (uint8_t)g.fold_head;
+  } else if (y > *c) {
+    *c = y;
+    if (hd) *hd = (uint8_t)g.fold_head;
+  }
+}
+
+// Four consecutive elements of the fold (c float4 aligned, hd 4-byte aligned).
+__device__ __forceinline__ void fold_store4(const GemmArgs& g, float4 x, float* c, uint8_t* hd) {
+  const float b = g.fold_bias ? g.fold_bias[0] : 0.0f;
+  x.x += b; x.y += b; x.z += b; x.w += b;
+  const uint32_t h = (uint32_t)g.fold_head * 0x01010101u;
+  if (g.fold == 1) {
+    *reinterpret_cast<float4*>(c) = x;
+    if (hd) *reinterpret_cast<uint32_t*>(hd) = h;
+    return;
+  }
+  float4 o = *reinterpret_cast<const float4*>(c);
+  uint32_t keep = 0;  // byte q set where the stored value stays
+  if (!(x.x > o.x)) { x.x = o.x; keep |= 0xFFu; }
+  if (!(x.y > o.y)) { x.y = o.y; keep |= 0xFF00u; }
+  if (!(x.z > o.z)) { x.z = o.z; keep |= 0xFF0000u; }
+  if (!(x.w > o.w)) { x.w = o.w; keep |= 0xFF000000u; }
+  if (keep == 0xFFFFFFFFu) return;
+  *reinterpret_cast<float4*>(c) = x;
+  if (hd) {
+    const uint32_t old = *reinterpret_cast<const uint32_t*>(hd);
+    *reinterpret_cast<uint32_t*>(hd) = (old & keep) | (h & ~keep);
+  }
+}
+
+// The A-operand mask of four consecutive elements: bytes of `heads` equal to
+// `head` keep their element.
+__device__ __forceinline__ float4 head_mask4(float4 a, uint32_t heads, int head) {
+  a.x = (int)(heads & 0xFFu) == head ? a.x : 0.0f;
+  a.y = (int)((heads >> 8) & 0xFFu) == head ? a.y : 0.0f;
+  a.z = (int)((heads >> 16) & 0xFFu) == head ? a.z : 0.0f;
+  a.w = (int)(heads >> 24) == head ? a.w : 0.0f;
+  return a;
+}
 
 // One element of the softsign epilogue: returns the value to store and adds
 // its share of the row's partial sum to `part`.
@@ -224,6 +290,14 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) ra[u][q] *= (kq + q < kend) ? kscale[kq + q] : 0.0f;
         }
+        if constexpr (gemm_use_amask(USE)) {
+          if (g.a_heads) {
+            const uint8_t* hp = g.a_heads + bz * g.a_bs + (int64_t)m * g.lda + kq;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (m < g.M && kq + q < kend && (int)hp[q] != g.a_head) ra[u][q] = 0.0f;
+          }
+        }
       } else {
         const int kk = k0 + e / (TILE / 4), mq = m0 + (e % (TILE / 4)) * 4;
         const float* p = gA + (int64_t)kk * g.lda + mq;
@@ -238,6 +312,14 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
           const float sc = kk < kend ? kscale[kk] : 0.0f;
 #pragma unroll
           for (int q = 0; q < 4; ++q) ra[u][q] *= sc;
+        }
+        if constexpr (gemm_use_amask(USE)) {
+          if (g.a_heads) {
+            const uint8_t* hp = g.a_heads + bz * g.a_bs + (int64_t)kk * g.lda + mq;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (kk < kend && mq + q < g.M && (int)hp[q] != g.a_head) ra[u][q] = 0.0f;
+          }
         }
       }
       // ---- B ----
@@ -375,6 +457,13 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
         const int n = n0 + wn * (TILE / 2) + nt * 16 + col;
         if (m < g.M && n < g.N) {
           float x = acc[mt][nt][v];
+          if constexpr (gemm_use_fold(USE)) {
+            if (g.fold) {
+              const int64_t o = (int64_t)m * g.ldc + n;
+              fold_store(g, x, C + o, g.fold_heads ? g.fold_heads + bz * g.c_bs + o : nullptr);
+              continue;
+            }
+          }
           if (g.c_nscale) x *= g.c_nscale[n];
           if (mscale) x *= mscale[m];
           if constexpr (C_BF) {
@@ -547,11 +636,18 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
   constexpr int NSC = KSCALE ? (A_KC ? 4 : 1) : 0;
   float4 ra[LPT], rb[LPT];
   [[maybe_unused]] float rs[LPT][NSC > 0 ? NSC : 1];
+  // head bytes of the masked A elements (gemm_use_amask), applied at the LDS store
+  constexpr bool AMASK = gemm_use_amask(USE);
+  [[maybe_unused]] uint32_t rh[AMASK ? LPT : 1];
 
   auto load_slice = [&](int k0) {
     // ---- A ----
-    const char* abase = gA + (A_KC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0) * AEB;
+    const int64_t aoff = A_KC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0;
+    const char* abase = gA + aoff * AEB;
     const auto ars = make_rsrc(abase, kFastRecords);
+    [[maybe_unused]] const auto hrs = make_rsrc(AMASK && g.a_heads ? static_cast<const void*>(g.a_heads + bz * g.a_bs + aoff)
+                                                                        : static_cast<const void*>(abase),
+                                                kFastRecords);
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
       const int e = tid + 256 * u;
@@ -559,6 +655,10 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
       const int c4 = A_KC ? (e % KCH) * 4 : (e % MCH) * 4;
       const bool ok = A_KC ? (m0 + row < g.M && k0 + c4 < kend) : (k0 + row < kend && m0 + c4 < g.M);
       ra[u] = fast_load4<A_BF>(ars, ok ? (uint32_t)(row * lda + c4) * AEB : kOobOffset);
+      if constexpr (AMASK) {
+        if (g.a_heads)
+          rh[u] = __builtin_amdgcn_raw_buffer_load_b32(hrs, ok ? (uint32_t)(row * lda + c4) : kOobOffset, 0, 0);
+      }
       if constexpr (KSCALE) {
         const auto srs = make_rsrc(kscale + k0, kFastRecords);
         if constexpr (A_KC) {
@@ -606,6 +706,9 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
       float4 a = ra[u];
       if constexpr (KSCALE) {
         a.x *= rs[u][0]; a.y *= rs[u][NSC > 1 ? 1 : 0]; a.z *= rs[u][NSC > 2 ? 2 : 0]; a.w *= rs[u][NSC - 1];
+      }
+      if constexpr (AMASK) {
+        if (g.a_heads) a = head_mask4(a, rh[u], g.a_head);
       }
       *reinterpret_cast<float4*>(&sA[buf][ia]) = a;
       *reinterpret_cast<float4*>(&sB[buf][ib]) = rb[u];
@@ -699,6 +802,15 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
             continue;
           }
         }
+        if constexpr (gemm_use_fold(USE)) {
+          if (g.fold) {
+            if (m < g.M && n < g.N) {
+              const int64_t o = (int64_t)m * g.ldc + n;
+              fold_store4(g, x, C + o, g.fold_heads ? g.fold_heads + bz * g.c_bs + o : nullptr);
+            }
+            continue;
+          }
+        }
         if (m < g.M && n < g.N) {
           if (g.c_nscale) {
             const float4 sc = *reinterpret_cast<const float4*>(&g.c_nscale[n]);
@@ -755,6 +867,13 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
           const int n = n0 + wn * 64 + nt * 16 + col;
           if (m < g.M && n < g.N) {
             float x = acc[mt][nt][v];
+            if constexpr (gemm_use_fold(USE)) {
+              if (g.fold) {
+                const int64_t o = (int64_t)m * g.ldc + n;
+                fold_store(g, x, C + o, g.fold_heads ? g.fold_heads + bz * g.c_bs + o : nullptr);
+                continue;
+              }
+            }
             if (g.c_nscale) x *= g.c_nscale[n];
             if (mscale) x *= mscale[m];
             if constexpr (C_BF) {
@@ -821,6 +940,7 @@ static void launch_use(const GemmArgs& g, bool fast, bool small, int zdim, hipSt
     const int tm = (g.M + kFT - 1) / kFT, tn = (g.N + kFT - 1) / kFT;
     const bool vec = g.N % 4 == 0 && g.ldc % 4 == 0 && g.c_bs % 4 == 0 && g.c_split_stride % 4 == 0 &&
                      f4_aligned(g.C) && f4_aligned(g.c_nscale) && f4_aligned(g.epi_ps) && f4_aligned(g.epi_E) &&
+                     (reinterpret_cast<uintptr_t>(g.fold_heads) & 3) == 0 &&
                      (g.addend == nullptr || (g.ld_add % 4 == 0 && g.add_bs % 4 == 0 && f4_aligned(g.addend)));
     hipLaunchKernelGGL((gemm_f32_fast_kernel<u.a_kc, u.b_kc, USE, kFastBK>), dim3(tm * tn * zdim), dim3(256), 0,
                        stream, g, tm, tn, vec ? 1 : 0);
@@ -842,6 +962,7 @@ static bool fast_path_ok(const GemmArgs& g, bool a_kc, bool b_kc) {
   if ((!a_kc && g.M % 4 != 0) || (!b_kc && g.N % 4 != 0)) return false;
   if (g.lda % 4 != 0 || g.ldb % 4 != 0 || g.a_bs % 4 != 0 || g.b_bs % 4 != 0 || g.ks_bs % 4 != 0) return false;
   if (g.lda >= kMaxLd || g.ldb >= kMaxLd) return false;
+  if ((reinterpret_cast<uintptr_t>(g.a_heads) & 3) != 0) return false;
   return f4_aligned(g.A) && f4_aligned(g.B0) && f4_aligned(g.B1) && f4_aligned(g.a_kscale);
 }
 
@@ -926,6 +1047,17 @@ int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
     g.epi = 1; g.epi_causal = m.epi_causal ? 1 : 0;
     g.epi_bias = m.epi_bias; g.epi_ps = m.epi_ps; g.epi_gds = m.epi_gds; g.epi_E = m.epi_E;
     g.epi_part = m.epi_part;
+  }
+  if (m.fold) {
+    JN_REQUIRE(gemm_use_fold(use) && (m.fold == 1 || m.fold == 2) && !m.epi && m.addend == nullptr &&
+                   m.c_nscale == nullptr && m.c_mscale == nullptr && m.fold_head >= 0 && m.fold_head < 256,
+               kInvalidArgument, "head fold needs a plain score use");
+    g.fold = m.fold; g.fold_head = m.fold_head; g.fold_bias = m.fold_bias; g.fold_heads = m.fold_heads;
+  }
+  if (m.a_heads) {
+    JN_REQUIRE(gemm_use_amask(use) && m.a_head >= 0 && m.a_head < 256, kInvalidArgument,
+               "head mask needs a score-gradient use");
+    g.a_heads = m.a_heads; g.a_head = m.a_head;
   }
   return launch_gemm(g, use, 1, stream);
 }

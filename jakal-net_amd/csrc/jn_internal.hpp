@@ -102,6 +102,20 @@ struct BatchedGemm {
   const float* epi_gds;
   const float* epi_E;
   float* epi_part;
+  // Head-max fold of max-aggregated multi-head scores (uses dense_scores,
+  // route_logits, select_scores; no other epilogue): the product is one
+  // head's scores, y = C + fold_bias[0] (null: 0).  fold = 1 (the first head)
+  // stores y; fold = 2 stores y where it exceeds the stored value (ties keep
+  // the earlier head).  fold_heads (bytes indexed like C, or null) records
+  // fold_head wherever y is stored.
+  int fold, fold_head;
+  const float* fold_bias;
+  uint8_t* fold_heads;
+  // Head mask of A (uses dense_target_grad, dense_source_grad,
+  // route_source_grad, route_target_grad): A(m, k) counts only where
+  // a_heads (bytes indexed like A: same strides, in elements) equals a_head.
+  const uint8_t* a_heads;
+  int a_head;
 };
 constexpr int kCausalKNone = 0, kCausalKLower = 1, kCausalKUpper = 2;
 // Partial sums per row that the dense softsign epilogue writes (32 columns each).
@@ -281,6 +295,11 @@ int launch_dense_compress_backward(float* G, const float* E, const float* gds, c
 int launch_dense_colsum(const float* E, const float* w, int B, int N, float* out, hipStream_t stream);
 // out[row] = sum_t part[row * P + t], t < P (fixed order)
 int launch_dense_part_rowsum(const float* part, int P, int64_t rows, float* out, hipStream_t stream);
+// rowsum[row, h] = sum_j G[row, j] [head[row, j] == h] over the N columns of
+// each of `rows` rows (row stride ld), h < H: bias gradients of max-aggregated
+// multi-head scores, in a fixed order.
+int launch_head_rowsum(const float* G, const uint8_t* head, int N, int64_t ld, int64_t rows, int H, float* rowsum,
+                       hipStream_t stream);
 // out[b, j] = sum_i M[b, i, j] a[b, i] (c[b, i] if given), i < Nr, j < Nc, fixed order
 int launch_colsum_rows(const float* M, const float* a, const float* c, int B, int Nr, int Nc, float* out,
                        const char* name, hipStream_t stream);

@@ -1293,15 +1293,18 @@ bool select_heads_fit(int64_t head_rank, int64_t heads) {
   return heads >= 2 && heads <= kMaxHeads && head_rank >= 1 && heads * split_ranks(head_rank) <= 128;
 }
 
+// Heads beyond the register kernels' K-steps run the scored-rows select,
+// whose score blocks take this much workspace too.
 size_t select_workspace_bytes_heads(int64_t B, int64_t Nk, int64_t head_rank, int64_t heads) {
   if (heads <= 1) return select_workspace_bytes(B, Nk, head_rank);
-  if (!select_heads_fit(head_rank, heads)) return 0;
+  if (heads > kMaxHeads || head_rank < 1 || heads * head_rank > 128) return 0;
   return select_workspace_bytes(B, Nk, heads * split_ranks(head_rank));
 }
 
 int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   SelectArgs a = a_in;
-  if ((a.k > kSelectMaxK || a.Nk > kSelMaxKeys) && a.heads <= 1) return launch_topk_select_large(a, stream);
+  const bool large_heads = a.heads > 1 && !(a.bf16 == 0 && select_heads_fit(a.head_rank, a.heads));
+  if (a.k > kSelectMaxK || a.Nk > kSelMaxKeys || large_heads) return launch_topk_select_large(a, stream);
   JN_REQUIRE(a.k >= 1 && a.k <= kSelectMaxK, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)", kSelectMaxK,
              a.k);
   JN_REQUIRE(a.k < a.Nk, kInvalidArgument, "top-k select needs k < key count (k=%d, Nk=%d)", a.k, a.Nk);

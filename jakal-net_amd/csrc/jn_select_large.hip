@@ -16,6 +16,10 @@
 //   3. a bitonic sort in LDS orders the k entries by descending score,
 //      ascending index, and the row is written.
 // Score arithmetic is fp32 MFMA (as select mode 1), whatever the layer dtype.
+// Max-aggregated multi-head scores (heads > 1) run one GEMM per head over its
+// rank slice, each folding its scores plus its bias into the block's running
+// max (ties keep the earlier head), so any number of heads, keys and k <=
+// kSelectLargeMaxK is taken.
 #include <algorithm>
 #include "jn_internal.hpp"
 
@@ -160,7 +164,9 @@ int launch_topk_select_large(const SelectArgs& a, hipStream_t stream) {
   JN_REQUIRE(a.k >= 1 && a.k <= kSelectLargeMaxK, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)",
              kSelectLargeMaxK, a.k);
   JN_REQUIRE(a.k < a.Nk, kInvalidArgument, "top-k select needs k < key count (k=%d, Nk=%d)", a.k, a.Nk);
-  JN_REQUIRE(a.heads <= 1, kUnsupported, "multi-head scores take k <= %d and at most 65535 keys", kSelectMaxK);
+  const bool mh = a.heads > 1;
+  JN_REQUIRE(!mh || (a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r), kUnsupported,
+             "multi-head select: %d heads of rank %d (rank %d)", a.heads, a.head_rank, a.r);
   JN_REQUIRE(a.temperature > 0.0f, kInvalidArgument, "temperature must be positive");
   JN_REQUIRE(a.r >= 1 && a.Nq >= 1 && a.B >= 1, kInvalidArgument, "empty select");
   // score rows that fit the workspace (the register select's split-key scratch)
@@ -172,20 +178,26 @@ int launch_topk_select_large(const SelectArgs& a, hipStream_t stream) {
   auto block = [&](int b0, int nb, int r0, int nr) -> int {
     // scores of rows [r0, r0 + nr) of batch elements [b0, b0 + nb): the scale
     // multiplies the query side (the same product as scaling the keys)
-    BatchedGemm m{};
-    m.A = a.q + (int64_t)b0 * a.q_batch_stride + (int64_t)r0 * a.ldq;
-    m.lda = a.ldq; m.a_bs = a.q_batch_stride; m.a_kcontig = true;
-    m.B = a.key + (int64_t)b0 * a.k_batch_stride;
-    m.ldb = a.ldk; m.b_bs = a.k_batch_stride; m.b_kcontig = true;
-    m.C = S; m.ldc = a.Nk; m.c_bs = (int64_t)nr * a.Nk;
-    m.a_kscale = a.scale;
-    m.M = nr; m.N = a.Nk; m.K = a.r; m.batch = nb;
-    int rc = gemm_batched(m, kGemmSelectScores, stream);
-    if (rc) return rc;
+    const int heads = mh ? a.heads : 1, rh = mh ? a.head_rank : a.r;
+    for (int h = 0; h < heads; ++h) {
+      BatchedGemm m{};
+      m.A = a.q + (int64_t)b0 * a.q_batch_stride + (int64_t)r0 * a.ldq + h * rh;
+      m.lda = a.ldq; m.a_bs = a.q_batch_stride; m.a_kcontig = true;
+      m.B = a.key + (int64_t)b0 * a.k_batch_stride + h * rh;
+      m.ldb = a.ldk; m.b_bs = a.k_batch_stride; m.b_kcontig = true;
+      m.C = S; m.ldc = a.Nk; m.c_bs = (int64_t)nr * a.Nk;
+      m.a_kscale = a.scale ? a.scale + h * rh : nullptr;
+      m.M = nr; m.N = a.Nk; m.K = rh; m.batch = nb;
+      if (mh) {  // running max over the heads, each with its own bias
+        m.fold = h == 0 ? 1 : 2; m.fold_head = h; m.fold_bias = a.bias ? a.bias + h : nullptr;
+      }
+      const int rc = gemm_batched(m, kGemmSelectScores, stream);
+      if (rc) return rc;
+    }
     const int64_t rows = (int64_t)nb * nr;
     JN_PROFILE("topk_rows_kernel", stream);
     hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)rows), dim3(256), 0, stream, S, (int64_t)a.Nk, a.Nk, a.k,
-                       a.bias, inv_temp, (int64_t)b0 * a.Nq + r0, a.out_idx, a.out_score);
+                       mh ? nullptr : a.bias, inv_temp, (int64_t)b0 * a.Nq + r0, a.out_idx, a.out_score);
     JN_LAUNCH_CHECK();
     return kOk;
   };

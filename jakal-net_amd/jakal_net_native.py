@@ -127,6 +127,29 @@ _declare(
      _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 
+_declare("jn_propagation_dense_multihead_chunk_bytes", [_I64] * 3, _SZ)
+_declare("jn_propagation_dense_multihead_workspace_bytes", [_I64] * 6 + [_I32, _I64], _SZ)
+_declare(
+    "jn_propagation_dense_forward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I64, _P, _P, _P, _P, _SZ, _P],
+)
+_declare(
+    "jn_propagation_dense_backward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I64,
+     _I32, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+_declare(
+    "jn_transition_dense_forward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P,
+     _P, _P, _P],
+)
+_declare("jn_transition_dense_multihead_workspace_bytes", [_I64] * 8, _SZ)
+_declare(
+    "jn_transition_dense_backward_multihead",
+    [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+     _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+)
+
 _declare("jn_propagation_topk_forward_multihead_workspace_bytes", [_I64] * 4, _SZ)
 _declare(
     "jn_propagation_topk_forward_multihead",
@@ -175,10 +198,10 @@ _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
 # Limits of the library's kernels.  A call beyond one raises NotImplementedError
 # (a RuntimeError subclass) before anything is launched, so callers that have
 # another path for such shapes (implementation="kernel") can take it.
-MAX_TOPK = 64          # edges per row of the register top-k select (multi-head scores, routes)
-MAX_TOPK_LARGE = 4096  # edges per row of a single-head propagation top-k (scored rows, radix select)
-MAX_RANK = 128         # low-rank score rank
-MAX_SELECT_KEYS = 65535  # keys a top-k select ranks per batch element
+MAX_TOPK = 64          # edges per row of the register top-k select (larger k: scored rows)
+MAX_TOPK_LARGE = 4096  # edges per row of a propagation top-k (scored rows, radix select)
+MAX_RANK = 128         # low-rank score rank (over every head)
+MAX_SELECT_KEYS = 65535  # keys the register select ranks per batch element (more: scored rows)
 CAUSAL_DENSE_MIN_NODES = 128  # full causal windows from this many nodes run on the dense MFMA path
 MAX_HEADS = 8          # heads of a max-aggregated multi-head score
 
@@ -565,13 +588,12 @@ class _PropagationDense(torch.autograd.Function):
     def backward(ctx, g_ds, g_dv):
         X, ps, pv, V, U, w_hat, proj, edges, bias = ctx.saved_tensors
         compress, pv_is_x, has_bias, causal, chunk = ctx.meta
-        if chunk < X.shape[0]:
-            return _PropagationDense._backward_chunked(ctx, X, ps, pv, V, U, w_hat, proj, edges, bias, g_ds, g_dv)
         # a softsign backward writes the score gradient over the saved edge
-        # matrix (no [B, N, N] workspace); it can therefore run once per forward
-        if ctx.edges_consumed:
-            raise RuntimeError("the dense propagation backward consumed its saved edge matrix; run the forward "
-                               "again instead of back-propagating through it twice (retain_graph).")
+        # matrix (no [B, N, N] workspace); a later backward (retain_graph)
+        # rebuilds the edges there from the saved projections, as the chunked
+        # backward does for its chunks
+        if chunk < X.shape[0] or ctx.edges_consumed:
+            return _PropagationDense._backward_chunked(ctx, X, ps, pv, V, U, w_hat, proj, edges, bias, g_ds, g_dv)
         reuse = 1 if compress == 0 else 0
         ctx.edges_consumed = bool(reuse)
         B, N, Din = X.shape
@@ -603,6 +625,7 @@ class _PropagationDense(torch.autograd.Function):
     @staticmethod
     def _backward_chunked(ctx, X, ps, pv, V, U, w_hat, proj, edge_chunk, bias, g_ds, g_dv):
         compress, pv_is_x, has_bias, causal, chunk = ctx.meta
+        chunk = min(chunk, X.shape[0])  # a whole saved edge matrix is one chunk
         # the chunk buffer holds the forward's last chunk until a softsign
         # backward writes its gradient there; a later backward rebuilds it too
         resident = 0 if ctx.edges_consumed else 1
@@ -634,6 +657,79 @@ class _PropagationDense(torch.autograd.Function):
                 gb if (has_bias and need[6]) else None, None, None)
 
 
+class _PropagationDenseMultihead(torch.autograd.Function):
+    """Dense low-rank propagation with max-aggregated multi-head scores on the
+    HIP library.  Inputs as _PropagationEdges with heads > 1 (U, V, w_hat the
+    heads' ranks stacked flat, bias [heads] or None); causal keeps only
+    sources j <= i.  The forward keeps a chunk of batch elements' edge
+    matrices and winning heads (the whole batch when it fits DENSE_EDGE_BYTES)
+    for the backward, which rebuilds the other chunks from the projections."""
+
+    @staticmethod
+    def forward(ctx, X, ps, pv, V, U, w_hat, bias, compress: int, causal: bool, heads: int):  # noqa: N803
+        B, N, Din = X.shape
+        pv_is_x = pv is None
+        pv_t = X if pv_is_x else pv
+        Dout = pv_t.shape[-1]
+        R = U.shape[0]
+        dev = X.device
+        per = N * N * 5  # fp32 edge and uint8 head per pair
+        chunk = B if B * per <= DENSE_EDGE_BYTES else max(1, DENSE_EDGE_BYTES // per)
+        with torch.cuda.device(dev):
+            ds = torch.empty(B, N, device=dev, dtype=torch.float32)
+            dv = torch.empty(B, N, Dout, device=dev, dtype=torch.float32)
+            proj = torch.empty(B * N, 2 * R, device=dev, dtype=torch.float32)
+            cbytes = int(_LIB.jn_propagation_dense_multihead_chunk_bytes(B, N, chunk))
+            edge_chunk = torch.empty(max(cbytes, 1), device=dev, dtype=torch.uint8)
+            _check(
+                _LIB.jn_propagation_dense_forward_multihead(
+                    _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
+                    B, N, Din, Dout, R // heads, heads, compress, 1 if causal else 0, chunk,
+                    _ptr(ds), _ptr(dv), _ptr(proj), _ptr(edge_chunk), cbytes, _stream(dev),
+                )
+            )
+        ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, edge_chunk, bias)
+        ctx.meta = (compress, pv_is_x, bias is not None, bool(causal), chunk, heads)
+        ctx.edges_consumed = False
+        return ds, dv
+
+    @staticmethod
+    def backward(ctx, g_ds, g_dv):
+        X, ps, pv, V, U, w_hat, proj, edge_chunk, bias = ctx.saved_tensors
+        compress, pv_is_x, has_bias, causal, chunk, heads = ctx.meta
+        # the chunk holds the forward's last edges until a softsign backward
+        # writes its gradient there; a later backward rebuilds them
+        resident = 0 if ctx.edges_consumed else 1
+        ctx.edges_consumed = ctx.edges_consumed or compress == 0
+        B, N, Din = X.shape
+        Dout = pv.shape[-1]
+        R = U.shape[0]
+        dev = X.device
+        need = ctx.needs_input_grad
+        with torch.cuda.device(dev):
+            g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
+            g_dv = torch.zeros(B, N, Dout, device=dev) if g_dv is None else g_dv.float().contiguous()
+            gX = torch.empty_like(X) if need[0] else None
+            gps = torch.empty_like(ps) if need[1] else None
+            gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
+            gV, gU, gw = torch.empty_like(V), torch.empty_like(U), torch.empty_like(w_hat)
+            gb = torch.empty(heads, device=dev, dtype=torch.float32) if has_bias else None
+            ws_bytes = int(_LIB.jn_propagation_dense_multihead_workspace_bytes(B, N, Din, Dout, R // heads, heads,
+                                                                               compress, chunk))
+            ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            _check(
+                _LIB.jn_propagation_dense_backward_multihead(
+                    _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias), _ptr(proj),
+                    _ptr(edge_chunk), edge_chunk.numel(), _ptr(g_ds), _ptr(g_dv), B, N, Din, Dout, R // heads,
+                    heads, compress, 1 if causal else 0, 1 if pv_is_x else 0, chunk, resident,
+                    _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
+                    _ptr(ws), ws_bytes, _stream(dev),
+                )
+            )
+        return (gX, gps, gpv, gV if need[3] else None, gU if need[4] else None, gw if need[5] else None,
+                gb if (has_bias and need[6]) else None, None, None, None)
+
+
 def propagation_dense(
     pairwise_kind: str,
     weight: Tensor,
@@ -661,9 +757,6 @@ def propagation_dense(
     (jakal_net_native.cpp:5991-6015); the fold is done here, differentiably."""
     w_hat, bias, V, U, heads = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight,
                                                       out_bias)
-    if heads > 1:
-        raise NotImplementedError("the HIP library runs multi-head scores on edge lists (top-k and window), "
-                                  "not on the dense path.")
     if edge_compress_name not in _COMPRESS_KINDS:
         raise RuntimeError(f"Unsupported edge_compress_name for the HIP backend: {edge_compress_name!r}.")
     if target_block_size <= 0 or source_block_size <= 0:
@@ -679,8 +772,12 @@ def propagation_dense(
     X = _f32(layer_val.reshape(-1, N, Din))
     ps = _f32(projected_state.reshape(-1, N))
     pv = None if pv_is_x else _f32(projected_val.reshape(-1, N, Dout))
-    ds, dv = _PropagationDense.apply(X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias),
-                                     _COMPRESS_KINDS[edge_compress_name], _causal)
+    if heads > 1:
+        ds, dv = _PropagationDenseMultihead.apply(X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias),
+                                                  _COMPRESS_KINDS[edge_compress_name], _causal, heads)
+    else:
+        ds, dv = _PropagationDense.apply(X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias),
+                                         _COMPRESS_KINDS[edge_compress_name], _causal)
     return (ds.reshape(*batch_shape, N).to(projected_state.dtype),
             dv.reshape(*batch_shape, N, Dout).to(projected_val.dtype))
 
@@ -720,28 +817,19 @@ def _flatten_heads(core, bias, first, second):
     return core.reshape(-1), flat_bias, first.reshape(heads * rank, -1), second.reshape(heads * rank, -1), heads
 
 
-def _check_select_heads(rank: int, heads: int) -> None:
-    """A multi-head top-k select scores each head on whole 32-rank K-steps, four at most."""
-    if heads > 1 and heads * (-(-rank // 32)) > 4:
-        raise NotImplementedError(f"the HIP multi-head top-k select takes heads x ceil(rank / 32) <= 4 "
-                                  f"(heads={heads}, rank={rank}).")
-
-
 def _check_rank(rank: int) -> None:
     if rank > MAX_RANK:
         raise NotImplementedError(f"the HIP library scores ranks up to {MAX_RANK} (got {rank}).")
 
 
-def _check_select(k: int, keys: int, large: bool = False) -> None:
-    """A top-k select of k of `keys` candidates per row.  large: the library may
-    take the scored-rows select, which keeps up to MAX_TOPK_LARGE edges of any
-    number of keys (single-head propagation); otherwise the register select's
-    limits apply."""
-    limit = MAX_TOPK_LARGE if large else MAX_TOPK
+def _check_select(k: int, limit: int = MAX_TOPK_LARGE) -> None:
+    """A top-k select of k edges per row of any number of keys: the register
+    select takes k <= MAX_TOPK of at most MAX_SELECT_KEYS keys (and multi-head
+    scores of at most four 32-rank K-steps), the scored-rows select the rest up
+    to MAX_TOPK_LARGE; `limit` is the caller's own bound (routes keep up to
+    MAX_ROUTE_TOPK edges per source)."""
     if k > limit:
-        raise NotImplementedError(f"the HIP top-k select keeps up to {limit} edges per row (got {k}).")
-    if keys > MAX_SELECT_KEYS and not large:
-        raise NotImplementedError(f"the HIP top-k select ranks up to {MAX_SELECT_KEYS} keys per row (got {keys}).")
+        raise NotImplementedError(f"the HIP top-k select keeps up to {limit} edges per row here (got {k}).")
 
 
 def _propagation_edges(mode, pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
@@ -749,10 +837,6 @@ def _propagation_edges(mode, pairwise_kind, weight, bias, in_weight, in_bias, ou
                        source_block_size):
     w_hat, bias, V, U, heads = _lowrank_pairwise_args(pairwise_kind, weight, bias, in_weight, in_bias, out_weight,
                                                       out_bias)
-    if mode == "topk":
-        _check_select_heads(U.shape[0] // heads, heads)
-        if heads > 1:
-            _check_select(param, layer_val.shape[-2])
     if edge_compress_name not in _COMPRESS_KINDS:
         raise RuntimeError(f"Unsupported edge_compress_name for the HIP backend: {edge_compress_name!r}.")
     if target_block_size <= 0 or source_block_size <= 0:
@@ -808,7 +892,7 @@ def propagation_topk_selection(
     if k == N:
         raise NotImplementedError("top-k with k == N keeps every source: that is dense propagation "
                                   "(propagation_dense, or propagation_topk, which routes it there).")
-    _check_select(k, N, large=True)
+    _check_select(k)
     return _propagation_edges("topk", pairwise_kind, weight, bias, in_weight, in_bias, out_weight, out_bias,
                               edge_compress_name, layer_val, projected_state, projected_val, k, target_block_size,
                               source_block_size)
@@ -862,10 +946,9 @@ def propagation_window(
     A window covering every earlier source (window >= N - 1, the causal dense
     query propagation of progressive_b_example.py:1990-2003) on at least
     CAUSAL_DENSE_MIN_NODES nodes runs as causal dense propagation on MFMA
-    GEMMs instead of an N-wide edge list (single-head scores; multi-head ones
-    stay on the edge list)."""
+    GEMMs instead of an N-wide edge list."""
     N = layer_val.shape[-2]
-    full_causal = window >= N - 1 and not pairwise_kind.startswith("multihead_")
+    full_causal = window >= N - 1
     if full_causal and N >= CAUSAL_DENSE_MIN_NODES:
         if window < 0:
             raise RuntimeError("window must be non-negative.")
@@ -1055,8 +1138,7 @@ def transition_pairwise_topk_routes(
     k = min(int(topk), Nd)
     _check_rank(source_weight.shape[0])
     if k < Nd:
-        _check_select(k, Nd)
-        _check_select_heads(source_weight.shape[0] // heads, heads)
+        _check_select(k, MAX_ROUTE_TOPK)
     elif Nd > MAX_ROUTE_TOPK:
         raise NotImplementedError("HIP sparse transition over every destination supports up to 64 destinations "
                                   "(transition_pairwise_topk runs more as the dense transition).")
@@ -1108,9 +1190,6 @@ def transition_pairwise_topk(
     or "signed_entmax15") has no counterpart in the reference's composite op,
     which is softmax-only."""
     if topk >= dst_val.shape[-2] > 64:
-        if route_kind.startswith("multihead_"):
-            raise NotImplementedError("the HIP library runs multi-head routes on edge lists (top-k, or every "
-                                      "destination up to 64), not on the dense transition.")
         # every destination kept (transition.py:437-440): the dense transition
         return transition_pairwise_dense(
             route_kind, source_weight, source_bias, target_weight, target_bias, core_weight, bias, hidden_weight,
@@ -1133,33 +1212,39 @@ class _TransitionDense(torch.autograd.Function):
     Ws [r,Dsrc], Wt [r,Ddst], w [r] (raw), bias [] or None."""
 
     @staticmethod
-    def forward(ctx, rho, src, dst, ps, pv, Ws, Wt, w, bias, temperature: float, compress: int):  # noqa: N803
+    def forward(ctx, rho, src, dst, ps, pv, Ws, Wt, w, bias, temperature: float, compress: int,  # noqa: N803
+                heads: int = 1):
         B, Ns, Dsrc = src.shape
         Nd, Ddst = dst.shape[1], dst.shape[2]
         Dv = pv.shape[-1]
         r = Ws.shape[0]
         dev = src.device
+        mh = heads > 1
         with torch.cuda.device(dev):
             ds = torch.empty(B, Nd, device=dev, dtype=torch.float32)
             dv = torch.empty(B, Nd, Dv, device=dev, dtype=torch.float32)
             sp = torch.empty(B * Ns, r, device=dev, dtype=torch.float32)
             dp = torch.empty(B * Nd, r, device=dev, dtype=torch.float32)
             routes = torch.empty(B, Ns, Nd, device=dev, dtype=torch.float32)
+            route_heads = torch.empty(B, Ns, Nd, device=dev, dtype=torch.uint8) if mh else None
+            fwd = _LIB.jn_transition_dense_forward_multihead if mh else _LIB.jn_transition_dense_forward
             _check(
-                _LIB.jn_transition_dense_forward(
+                fwd(
                     _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w), _ptr(bias),
-                    float(temperature), B, Ns, Nd, Dsrc, Ddst, Dv, r, compress,
-                    _ptr(ds), _ptr(dv), _ptr(sp), _ptr(dp), _ptr(routes), _stream(dev),
+                    float(temperature), B, Ns, Nd, Dsrc, Ddst, Dv, *([r // heads, heads] if mh else [r]), compress,
+                    _ptr(ds), _ptr(dv), _ptr(sp), _ptr(dp), _ptr(routes), *([_ptr(route_heads)] if mh else []),
+                    _stream(dev),
                 )
             )
-        ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, routes)
-        ctx.meta = (float(temperature), compress, bias is not None)
+        ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, routes, route_heads)
+        ctx.meta = (float(temperature), compress, bias is not None, heads)
         return ds, dv
 
     @staticmethod
     def backward(ctx, g_ds, g_dv):
-        rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, routes = ctx.saved_tensors
-        temperature, compress, has_bias = ctx.meta
+        rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, routes, route_heads = ctx.saved_tensors
+        temperature, compress, has_bias, heads = ctx.meta
+        mh = heads > 1
         B, Ns, Dsrc = src.shape
         Nd, Ddst = dst.shape[1], dst.shape[2]
         Dv = pv.shape[-1]
@@ -1173,28 +1258,30 @@ class _TransitionDense(torch.autograd.Function):
             gWs = torch.empty_like(Ws) if need[5] else None
             gWt = torch.empty_like(Wt) if need[6] else None
             gw = torch.empty_like(w)
-            gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
-            ws_bytes = int(_LIB.jn_transition_dense_workspace_bytes(B, Ns, Nd, Dsrc, Ddst, Dv, r))
+            gb = torch.empty((heads,) if mh else (), device=dev, dtype=torch.float32) if has_bias else None
+            rank_arg = [r // heads, heads] if mh else [r]
+            ws_fn = (_LIB.jn_transition_dense_multihead_workspace_bytes if mh else
+                     _LIB.jn_transition_dense_workspace_bytes)
+            ws_bytes = int(ws_fn(B, Ns, Nd, Dsrc, Ddst, Dv, *rank_arg))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+            bwd = _LIB.jn_transition_dense_backward_multihead if mh else _LIB.jn_transition_dense_backward
             _check(
-                _LIB.jn_transition_dense_backward(
+                bwd(
                     _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w),
-                    _ptr(sp), _ptr(dp), _ptr(routes), _ptr(g_ds), _ptr(g_dv), float(temperature),
-                    B, Ns, Nd, Dsrc, Ddst, Dv, r, compress,
+                    _ptr(sp), _ptr(dp), _ptr(routes), *([_ptr(route_heads)] if mh else []), _ptr(g_ds), _ptr(g_dv),
+                    float(temperature), B, Ns, Nd, Dsrc, Ddst, Dv, *rank_arg, compress,
                     _ptr(out[0]), _ptr(out[1]), _ptr(out[2]), _ptr(out[3]), _ptr(out[4]), _ptr(gWs), _ptr(gWt),
                     _ptr(gw), _ptr(gb), _ptr(ws), ws_bytes, _stream(dev),
                 )
             )
-        return (*out, gWs, gWt, gw if need[7] else None, gb if (has_bias and need[8]) else None, None, None)
+        return (*out, gWs, gWt, gw if need[7] else None, gb if (has_bias and need[8]) else None, None, None, None)
 
 
 def _check_route_spec(route_kind, source_weight, source_bias, target_weight, target_bias, hidden_weight, out_weight,
                       route_compress_name, temperature):
-    if route_kind.startswith("multihead_"):
-        raise NotImplementedError("the HIP library runs multi-head routes on edge lists (top-k, or every "
-                                  "destination up to 64), not on the dense transition.")
-    if route_kind != "low_rank_bilinear_route":
-        raise TypeError(f"jakal_net_native supports route kind 'low_rank_bilinear_route', got {route_kind!r}.")
+    if route_kind not in ("low_rank_bilinear_route", "multihead_max_low_rank_bilinear_route"):
+        raise TypeError(f"jakal_net_native supports route kinds 'low_rank_bilinear_route' and "
+                        f"'multihead_max_low_rank_bilinear_route', got {route_kind!r}.")
     if source_weight is None or target_weight is None:
         raise RuntimeError("Low-rank bilinear route is missing projection weights.")
     if source_bias is not None or target_bias is not None or hidden_weight is not None or out_weight is not None:
@@ -1235,6 +1322,10 @@ def transition_pairwise_dense(
     ignored: the HIP kernels tile for gfx950 themselves."""
     _check_route_spec(route_kind, source_weight, source_bias, target_weight, target_bias, hidden_weight, out_weight,
                       route_compress_name, temperature)
+    heads = 1
+    if route_kind.startswith("multihead_"):
+        core_weight, bias, source_weight, target_weight, heads = _flatten_heads(core_weight, bias, source_weight,
+                                                                                target_weight)
     _check_rank(source_weight.shape[0])
     if src_block_size < 0 or dst_block_size < 0:
         raise RuntimeError("block sizes must be non-negative.")
@@ -1248,7 +1339,7 @@ def transition_pairwise_dense(
         _f32(sender_strength.reshape(-1, Ns)), _f32(src_val.reshape(-1, Ns, Dsrc)),
         _f32(dst_val.reshape(-1, Nd, Ddst)), _f32(projected_state.reshape(-1, Ns)),
         _f32(projected_val.reshape(-1, Ns, Dv)), _f32(source_weight), _f32(target_weight), _f32(core_weight),
-        _f32(bias), float(temperature), _ROUTE_COMPRESS_KINDS[route_compress_name],
+        _f32(bias), float(temperature), _ROUTE_COMPRESS_KINDS[route_compress_name], heads,
     )
     return ds.reshape(*batch_shape, Nd).to(projected_state.dtype), dv.reshape(*batch_shape, Nd, Dv).to(
         projected_val.dtype)

@@ -123,7 +123,10 @@ def test_multihead_workspace_queries_without_gpu():
     # each head's ranks are padded to 32: 2 heads of rank 20 take the split rows of rank 64
     assert fwd(2, 100, 20, 2) == one(2, 100, 64)
     assert fwd(2, 100, 64, 2) == one(2, 100, 128)
-    assert fwd(2, 100, 64, 3) == 0  # 3 x 64 ranks exceed the select's four K-steps
+    assert fwd(2, 100, 64, 3) == 0  # 3 x 64 ranks exceed the 128 ranks of a score
+    # 3 heads of rank 40 pad to 3 x 64 split ranks, beyond the register select's
+    # four K-steps: the scored-rows select takes them, in the same workspace size
+    assert fwd(2, 100, 40, 3) == one(2, 100, 192)
     bwd = lib.jn_propagation_topk_multihead_workspace_bytes
     bwd.argtypes, bwd.restype = [I64] * 7, ctypes.c_size_t
     single = lib.jn_propagation_topk_workspace_bytes
@@ -134,4 +137,5 @@ def test_multihead_workspace_queries_without_gpu():
     tr.argtypes, tr.restype = [I64] * 9, ctypes.c_size_t
     assert tr(2, 50, 40, 8, 8, 8, 16, 2, 4) > 0
     assert tr(2, 50, 40, 8, 8, 8, 64, 3, 4) == 0
+    assert tr(2, 50, 40, 8, 8, 8, 40, 3, 4) > 0  # scored-rows select of 3 heads of rank 40
     assert tr(2, 50, 40, 8, 8, 8, 40, 3, 40) > 0  # every destination: no select, 3 x 40 <= 128 ranks

@@ -40,7 +40,17 @@ Prints one JSON line:
                average duration, measured with HIP events over the eager timed
                region; `traffic` = HBM-side bytes per launch measured by
                rocprofv3 FETCH_SIZE/WRITE_SIZE passes of this command
-  kernels      the same figures for every kernel of the step
+  kernels      the same figures for every kernel of the step; avg_ms_alone (and the
+               HBM kernels' frac_alone) from a few more eager steps with the library's
+               side streams off, so that no kernel shares the GPU with another
+  hbm_measured_GBps, hbm_frac
+               step-level HBM-side traffic: the rocprofv3 FETCH_SIZE + WRITE_SIZE bytes
+               per launch of every kernel (profiles/<workload>_hbm_traffic.json) times
+               its launches per step, over ms_per_step, and its fraction of 8 TB/s
+               (details under `hbm`, with the compulsory bytes of the HBM-bound kernels)
+  sparse_phase_algorithmic_GBps
+               BASELINE's sparse-phase bytes (no cache reuse) over ms_per_step: an
+               algorithmic rate; above 8 TB/s it says the step is not HBM-bound
   cpu_baseline the same workload through the operator API's implementation="reference"
                backend on the host cores (warmup 1, median of 3)
 
@@ -98,8 +108,18 @@ def fused_column_slabs(D: int, vb: int = 4) -> int:
     return slabs if slabs <= 2 else 0
 
 
+def csr_table_bytes(M: int, Mk: int, B: int) -> float:
+    """Bytes of the edge grouping's per-tile key counts for M query rows and Mk
+    keys over B batch elements: tiles of whole 64-row chunks, about 256 over
+    the batch, at most 1024 rows (jn_edges.hip, csr_tile_rows)."""
+    nq, nk = M // B, Mk // B
+    want = (M + 255) // 256
+    rows = min(1024, max(64, -(-want // 64) * 64))
+    return 4.0 * B * (-(-nq // rows)) * nk
+
+
 def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool | str = False,
-                      Mk: int | None = None, vb: float = 4.0) -> tuple | None:
+                      Mk: int | None = None, vb: float = 4.0, batch: int = 1) -> tuple | None:
     """(bound, algorithmic bytes or flops, compulsory bytes) of the edge-list kernels.
 
     M = aggregated (query) rows, Mk = source (key) rows (M for propagation),
@@ -111,7 +131,8 @@ def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool | s
     L2-side figure and their HBM roofline fraction is priced on compulsory bytes.
     split: the row backward runs as dots + finish ("fused": its dots come from
     the fused column pass, read through the record indices).  vb: bytes per value-row
-    element (4 fp32, 2 bf16); projections, scores and edge records stay fp32."""
+    element (4 fp32, 2 bf16); projections, scores and edge records stay fp32.
+    batch: batch elements of the edge list (the edge grouping's tiling)."""
     Mk = M if Mk is None else Mk
     D4 = vb * D  # bytes of one value row
     if name.startswith("rows_forward_kernel"):
@@ -130,10 +151,19 @@ def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool | s
                 E * (16.0 + 4.0 * slabs) + M * (D4 + 4.0) + Mk * (2.0 * D4 + 8.0))
     if name.startswith("csr_count_kernel"):
         # edge index per edge; per-tile counts of every key
-        return ("hbm", E * 4.0, E * 4.0)
+        table = csr_table_bytes(M, Mk, batch)
+        return ("hbm", E * 4.0 + table, E * 4.0 + table)
+    if name.startswith("csr_tile_prefix_kernel"):
+        # the per-tile counts read and rewritten, the degree row written
+        table = csr_table_bytes(M, Mk, batch)
+        return ("hbm", 2.0 * table + Mk * 4.0, 2.0 * table + Mk * 4.0)
     if name.startswith("csr_fill_kernel"):
-        # edge index twice, score, record and record index per edge
-        return ("hbm", E * (4.0 * 2 + 4.0 + 16.0 + 4.0), E * (4.0 + 4.0 + 16.0 + 4.0))
+        # edge index, score, record and record index per edge; each tile's row
+        # of the table and the batch element's degree row (read by every tile)
+        table = csr_table_bytes(M, Mk, batch)
+        tiles = table / (4.0 * Mk)
+        return ("hbm", E * (4.0 + 4.0 + 16.0 + 4.0) + table + tiles * Mk * 4.0,
+                E * (4.0 + 4.0 + 16.0 + 4.0) + table + Mk * 4.0)
     if name.startswith("rows_backward_kernel"):
         if split == "fused":
             # idx+score, record index, two partial dots, ps, key row, gsc write per edge;
@@ -190,7 +220,7 @@ def kernel_model(name: str, B: int, N: int, D: int, r: int, k: int, bf16: bool =
         return "hbm", B * N * (4.0 * r + 2.0 * rp), B * N * (4.0 * r + 2.0 * rp)
     vb = 2 if bf16 else 4
     split = "fused" if fused_column_slabs(D, vb) else rows_backward_split(N, D, vb)
-    return edge_kernel_model(name, B * N, B * N * k, D, r, split, vb=float(vb))
+    return edge_kernel_model(name, B * N, B * N * k, D, r, split, vb=float(vb), batch=B)
 
 
 def _cpu_model() -> str:
@@ -797,7 +827,16 @@ def main() -> int:
     jn.profile_enable(True)
     eager_ms, wall = timed(step)
     prof = jn.profile_collect()
+    # the same kernels once more with the side streams off: each kernel alone
+    # (the timings above include the overlap of the two streams' kernels)
+    jn.set_side_streams(False)
+    alone_steps = max(1, min(args.steps, 5))
+    for _ in range(alone_steps):
+        step()
+    torch.cuda.synchronize()
+    prof_alone = jn.profile_collect()
     jn.profile_enable(False)
+    jn.set_side_streams(True)
     ms_per_step = eager_ms
     graph_info = None
     if use_graph:
@@ -817,6 +856,8 @@ def main() -> int:
         avg_ms = total_ms / count
         entry = {"launches_per_step": count / args.steps, "avg_ms": round(avg_ms, 5),
                  "ms_per_step": round(total_ms / args.steps, 5)}
+        if name in prof_alone:
+            entry["avg_ms_alone"] = round(prof_alone[name][1] / prof_alone[name][0], 5)
         model = wl.model(name)
         if model is not None:
             bound, work = model[0], model[1]
@@ -828,6 +869,9 @@ def main() -> int:
                 entry.update(bound="hbm", compulsory_bytes=compulsory, achieved_GBps=round(achieved, 1),
                              frac=round(achieved / HBM_PEAK_GBS, 4), algorithmic_bytes=work,
                              l2_side_GBps=round(work / (avg_ms / 1e3) / 1e9, 1))
+                if "avg_ms_alone" in entry:
+                    alone = compulsory / (entry["avg_ms_alone"] / 1e3) / 1e9
+                    entry.update(achieved_GBps_alone=round(alone, 1), frac_alone=round(alone / HBM_PEAK_GBS, 4))
             else:
                 achieved = work / (avg_ms / 1e3) / 1e12
                 peak = model[3] if len(model) > 3 else FP32_MFMA_PEAK_TFLOPS
@@ -858,6 +902,32 @@ def main() -> int:
             entry["traffic_bytes"] = measured[name]["traffic_bytes"]
             entry["traffic_GBps"] = round(measured[name]["traffic_bytes"] / (entry["avg_ms"] / 1e3) / 1e9, 1)
 
+    # step-level HBM-side traffic: every kernel's measured bytes per launch
+    # (rocprofv3 FETCH_SIZE + WRITE_SIZE of this workload) times its launches
+    # per step, over the step time; and the compulsory bytes of the modelled
+    # HBM-bound kernels over the same time
+    hbm = None
+    if measured:
+        traffic = sum(measured[n]["traffic_bytes"] * e["launches_per_step"] for n, e in kernels.items()
+                      if n in measured)
+        missing = sorted(n for n in kernels if n not in measured)
+        compulsory = sum(e["compulsory_bytes"] * e["launches_per_step"] for e in kernels.values()
+                         if e.get("bound") == "hbm")
+        traffic_json = json.loads(traffic_file.read_text())
+        hbm = {
+            "measured_bytes_per_step": traffic,
+            "measured_GBps": round(traffic / (ms_per_step / 1e3) / 1e9, 1),
+            "measured_frac": round(traffic / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "compulsory_bytes_per_step": compulsory,
+            "compulsory_GBps": round(compulsory / (ms_per_step / 1e3) / 1e9, 1),
+            "compulsory_frac": round(compulsory / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "counter_source": f"profiles/{wl.traffic_file} (commit {traffic_json.get('commit')})",
+            "kernels_without_counters": missing,
+            "note": "measured: rocprofv3 FETCH_SIZE + WRITE_SIZE bytes per launch (L2-to-fabric traffic, scaled by "
+                    "a device copy of known size) x launches per step / ms_per_step; compulsory: each distinct "
+                    "input row and output of the HBM-bound kernels once",
+        }
+
     modeled = [(n, e) for n, e in kernels.items() if "bound" in e]
     dom_name, dom = max(modeled or list(kernels.items()), key=lambda ne: ne[1]["ms_per_step"])
     if not modeled:  # an end-to-end step: the hottest kernel, without a roofline
@@ -874,6 +944,15 @@ def main() -> int:
         if "arith" in dom:
             roofline["arith"] = dom["arith"]
 
+    sparse_rate = (None if wl.sparse_bytes() is None
+                   else round(wl.sparse_bytes() / (ms_per_step / 1e3) / 1e9, 1))
+    sparse_note = None
+    if sparse_rate is not None:
+        sparse_note = ("BASELINE's sparse-phase bytes (every operand once per use, no cache reuse) / ms_per_step: "
+                       "an algorithmic rate, not bytes moved")
+        if sparse_rate > HBM_PEAK_GBS:
+            sparse_note += (f"; above the {HBM_PEAK_GBS:.0f} GB/s HBM peak, so the step is not HBM-bound at this "
+                            "shape (the gathers re-read rows from L2); hbm_measured_GBps is the bytes moved")
     result = {
         "metric": wl.metric,
         "value": value,
@@ -888,8 +967,11 @@ def main() -> int:
         "dtype": getattr(wl, "dtype", "f32"),
         "data": wl.data,
         "config": {"workload": wl.workload, **wl.config},
-        "sparse_phase_GBps": (None if wl.sparse_bytes() is None
-                              else round(wl.sparse_bytes() / (ms_per_step / 1e3) / 1e9, 1)),
+        "hbm_measured_GBps": None if hbm is None else hbm["measured_GBps"],
+        "hbm_frac": None if hbm is None else hbm["measured_frac"],
+        "hbm": hbm,
+        "sparse_phase_algorithmic_GBps": sparse_rate,
+        "sparse_phase_note": sparse_note,
         "roofline": roofline,
         "kernels": kernels,
         "wall_s_timed": round(wall, 3),

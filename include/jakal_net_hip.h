@@ -36,7 +36,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 9. */
+/* ABI revision of this header (bumped on any signature change); this is 10. */
 int jn_abi_version(void);
 
 /*
@@ -71,6 +71,15 @@ int jn_set_gemm_tile(int32_t tile);
  * for every window.  Process-wide; results agree up to fp32 summation order.
  */
 int jn_set_window_kernels(int32_t mode);
+
+/*
+ * Side streams (no counterpart in the reference; for measurement and tests).
+ * on = 1 (the default) lets the edge-list entry points run independent work on
+ * the library's side stream beside the caller's (see the top of this file);
+ * on = 0 runs every kernel on the caller's stream in the same order, so each
+ * kernel can be timed alone.  Process-wide; results are bit-identical.
+ */
+int jn_set_side_streams(int32_t on);
 
 /*
  * Score arithmetic of the top-k select (no counterpart in the reference; for

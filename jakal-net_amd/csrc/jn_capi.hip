@@ -2,6 +2,7 @@
 // validates shapes on the host, carves its scratch from the caller's
 // workspace and enqueues kernels on the caller's stream.
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -48,7 +49,9 @@ SideStream* side_stream(hipStream_t origin) {
 // Forking pays only when each branch has work enough to hide the extra event
 // nodes (on small problems they cost more than the overlap gains).
 constexpr int64_t kSideMinEdges = 1 << 20;
+static std::atomic<int> g_side_streams{1};
 const SideStream* side_stream_for(hipStream_t origin, int64_t edges) {
+  if (g_side_streams.load(std::memory_order_relaxed) == 0) return nullptr;
   return edges >= kSideMinEdges ? side_stream(origin) : nullptr;
 }
 
@@ -162,20 +165,21 @@ struct PropBwdScratch {
 };
 
 // r: all ranks (heads * head rank); heads > 1 keeps one bias column per head.
+// csr: the edges are grouped by key (top-k lists); a window's causal band has
+// a closed-form transpose and takes no grouping space.
 PropBwdScratch carve_prop_bwd(void* base, size_t size, int64_t B, int64_t N, int64_t Din, int64_t r, int64_t k,
-                              int64_t heads = 1) {
+                              int64_t heads = 1, bool csr = true) {
   Workspace ws(base, size);
   PropBwdScratch s{};
   const int64_t M = B * N;
-  const int64_t T = csr_tiles(B, N);
   s.dP = ws.take<float>(M * 2 * r);
   s.g_score = ws.take<float>(M * k);
   s.coef = ws.take<float>(M * k);
   s.rowsum = ws.take<float>(M * heads);
-  s.tile_base = ws.take<int32_t>(B * T * N);
-  s.seg_start = ws.take<int32_t>(B * (N + 1));
-  s.rec = ws.take<float4>(M * k);
-  s.pos = ws.take<int32_t>(M * k);
+  s.tile_base = ws.take<int32_t>(csr ? csr_table_entries(B, N, N) : 0);
+  s.seg_start = ws.take<int32_t>(csr ? B * (N + 1) : 0);
+  s.rec = ws.take<float4>(csr ? M * k : 0);
+  s.pos = ws.take<int32_t>(csr ? M * k : 0);
   s.dots = ws.take<float>(M * k);
   s.part_c = ws.take<float>((size_t)cols_backward_parts(M) * r);
   s.stage = ws.take<float>(finalize_stage_floats((int)r, (int)heads));
@@ -200,11 +204,10 @@ struct EdgeLayout {
 EdgeLayout carve_edge_layout(void* base, size_t size, int64_t B, int64_t N, int64_t k) {
   Workspace ws(base, size);
   EdgeLayout l{};
-  const int64_t T = csr_tiles(B, N);
   l.seg_start = ws.take<int32_t>(B * (N + 1));
   l.rec = ws.take<float4>(B * N * k);
   l.pos = ws.take<int32_t>(B * N * k);
-  l.tile_base = ws.take<int32_t>(B * T * N);
+  l.tile_base = ws.take<int32_t>(csr_table_entries(B, N, N));
   l.coef = ws.take<float>(B * N * k);
   l.bytes = ws.used;
   return l;
@@ -261,9 +264,8 @@ TransitionScratch carve_transition(void* base, size_t size, int64_t B, int64_t N
                                    int64_t Ddst, int64_t r, int64_t k, int64_t heads = 1) {
   Workspace ws(base, size);
   TransitionScratch s{};
-  const int64_t T = csr_tiles(B, Ns);
   s.coef = ws.take<float>(B * Ns * k);
-  s.tile_base = ws.take<int32_t>(B * T * Nd);
+  s.tile_base = ws.take<int32_t>(csr_table_entries(B, Ns, Nd));
   s.seg_start = ws.take<int32_t>(B * (Nd + 1));
   s.rec = ws.take<float4>(B * Ns * k);
   s.dPs = ws.take<float>(B * Ns * r);
@@ -656,7 +658,8 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
   JN_REQUIRE(!projected_val_is_layer_val || in_dim == out_dim, kInvalidArgument,
              "projected_val_is_layer_val requires in_dim == out_dim");
   const bool mh = heads > 1;
-  PropBwdScratch s = carve_prop_bwd(workspace, workspace_bytes, batch, nodes, in_dim, rank, topk, mh ? heads : 1);
+  PropBwdScratch s =
+      carve_prop_bwd(workspace, workspace_bytes, batch, nodes, in_dim, rank, topk, mh ? heads : 1, !band);
   JN_REQUIRE(workspace != nullptr && s.bytes <= workspace_bytes, kWorkspaceTooSmall,
              "workspace too small: need %zu bytes, got %zu", s.bytes, workspace_bytes);
   hipStream_t st = stream;
@@ -1169,7 +1172,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 9; }
+int jn_abi_version(void) { return 10; }
 
 int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float eps, float* weight_hat,
                           jn_stream_t stream) {
@@ -1204,6 +1207,12 @@ int jn_set_window_kernels(int32_t mode) {
   JN_REQUIRE(mode == 0 || mode == 1, kInvalidArgument, "window kernel mode must be 0 (band) or 1 (edge), got %d",
              (int)mode);
   jakal::set_window_kernels(mode);
+  return kOk;
+}
+
+int jn_set_side_streams(int32_t on) {
+  JN_REQUIRE(on == 0 || on == 1, kInvalidArgument, "side streams: 0 (off) or 1 (on), got %d", (int)on);
+  jakal::g_side_streams.store(on, std::memory_order_relaxed);
   return kOk;
 }
 
@@ -1297,11 +1306,12 @@ size_t jn_propagation_topk_forward_workspace_bytes(int64_t batch, int64_t nodes,
 size_t jn_propagation_topk_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                            int64_t rank, int64_t topk) {
   (void)out_dim;
+  if (!csr_table_fits(batch, nodes, nodes)) return 0;  // the edge grouping is beyond its size limit
   return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank, topk).bytes;
 }
 
 size_t jn_propagation_topk_layout_bytes(int64_t batch, int64_t nodes, int64_t topk) {
-  if (batch < 1 || nodes < 1 || topk < 1) return 0;
+  if (batch < 1 || nodes < 1 || topk < 1 || !csr_table_fits(batch, nodes, nodes)) return 0;
   return carve_edge_layout(nullptr, 0, batch, nodes, topk).bytes;
 }
 
@@ -1340,7 +1350,7 @@ size_t jn_propagation_window_workspace_bytes(int64_t batch, int64_t nodes, int64
                                              int64_t rank, int64_t window) {
   (void)out_dim;
   if (window < 0 || nodes < 1) return 0;
-  return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank, window_width(window, nodes)).bytes;
+  return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank, window_width(window, nodes), 1, false).bytes;
 }
 
 int jn_propagation_window_backward(const float* layer_val, const float* projected_state, const float* projected_val,
@@ -1368,7 +1378,8 @@ int jn_propagation_window_backward(const float* layer_val, const float* projecte
 size_t jn_transition_topk_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t src_dim,
                                           int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t topk) {
   (void)val_dim;
-  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || topk < 1) return 0;
+  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || topk < 1 || !csr_table_fits(batch, src_nodes, dst_nodes))
+    return 0;
   return carve_transition(nullptr, 0, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank,
                           route_edges(topk, dst_nodes))
       .bytes;
@@ -1740,7 +1751,7 @@ size_t jn_propagation_topk_forward_multihead_workspace_bytes(int64_t batch, int6
 size_t jn_propagation_topk_multihead_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                                      int64_t rank, int64_t heads, int64_t topk) {
   (void)out_dim;
-  if (batch < 1 || nodes < 1 || heads < 2 || topk < 1) return 0;
+  if (batch < 1 || nodes < 1 || heads < 2 || topk < 1 || !csr_table_fits(batch, nodes, nodes)) return 0;
   return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank * heads, topk, heads).bytes;
 }
 
@@ -1784,7 +1795,8 @@ size_t jn_propagation_window_multihead_workspace_bytes(int64_t batch, int64_t no
                                                        int64_t out_dim, int64_t rank, int64_t heads, int64_t window) {
   (void)out_dim;
   if (window < 0 || nodes < 1 || batch < 1 || heads < 2) return 0;
-  return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank * heads, window_width(window, nodes), heads).bytes;
+  return carve_prop_bwd(nullptr, 0, batch, nodes, in_dim, rank * heads, window_width(window, nodes), heads, false)
+      .bytes;
 }
 
 int jn_propagation_window_forward_multihead(const float* layer_val, const float* projected_state,
@@ -1830,7 +1842,9 @@ size_t jn_transition_topk_multihead_workspace_bytes(int64_t batch, int64_t src_n
                                                     int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank,
                                                     int64_t heads, int64_t topk) {
   (void)val_dim;
-  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || topk < 1 || heads < 2 || rank * heads > 128) return 0;
+  if (batch < 1 || src_nodes < 1 || dst_nodes < 1 || topk < 1 || heads < 2 || rank * heads > 128 ||
+      !csr_table_fits(batch, src_nodes, dst_nodes))
+    return 0;
   return carve_transition(nullptr, 0, batch, src_nodes, dst_nodes, src_dim, dst_dim, rank * heads,
                           route_edges(topk, dst_nodes), heads)
       .bytes;

@@ -561,24 +561,30 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
 // Rows are cut into tiles of up to 1024 rows (about one tile per CU).
 //   1. csr_count_kernel: per tile, how many of its edges reach each key (LDS
 //      counters) -> tile_base[b, t, j].
-//   2. csr_fill_kernel: per tile, from the counts of all tiles, each key's
-//      segment start (an LDS scan of the keys' degrees) and its edges from
-//      earlier tiles give an LDS cursor per key; the tile is walked in 64-row
-//      chunks, where a key's incoming rows form a 64-bit mask, so edge
-//      (row, j) lands at
-//        cursor[j] + popcount(mask_j below row)
-//      and the cursors then advance by popcount(mask_j).  Tile 0 writes the
-//      segment starts.
-// Two launches of 256-thread workgroups, so the build keeps pace beside other
-// kernels.
+//   2. csr_tile_prefix_kernel (thread per key): the counts' prefix over the
+//      tiles, written over them (edges into j from tiles before t), and per
+//      256-key block the degrees' exclusive prefix and their sum (two extra
+//      rows of the table).
+//   3. csr_fill_kernel: per tile, the segment starts (a scan of the block
+//      sums plus the in-block prefix; tile 0 writes them) plus
+//      tile_base[b, t, j] become LDS cursors (the tile's first slot in each
+//      key's segment); the next chunk's keys load during a chunk; the tile is
+//      walked in chunks of at most 32 rows, where a key's incoming rows form a
+//      32-bit LDS mask, so edge (row, j) lands at
+//        cursor[j] + popcount(mask_j below row).
+//      Each chunk costs work per edge only: the edge holding a key's highest
+//      mask bit advances its cursor by popcount(mask_j) and clears the mask
+//      during the next chunk, whose masks go to the other of two buffers.
 // Segments therefore list incoming edges in increasing row order and every
 // reduction over them is run-to-run reproducible.  Each slot receives the
 // edge's record (row, coef, g_s or edge id, coef * gds[row]), so the column
 // pass reads one contiguous 16-byte entry per incoming edge instead of chasing
-// edge ids.  Keys are taken in LDS slices (at most 64 KiB per workgroup).
+// edge ids.  Keys are taken in LDS slices of kCsrFillSlice.
 // ---------------------------------------------------------------------------
 constexpr int kCsrCountSlice = 8192;  // keys per LDS pass of the count (int counters)
-constexpr int kCsrFillSlice = 4096;   // keys per LDS pass of the fill (64-bit masks + int cursors)
+constexpr int kCsrFillSlice = 4096;   // keys per LDS pass of the fill (two 32-bit masks + an int cursor)
+constexpr int kCsrChunkRows = 32;     // rows per fill chunk (one mask bit per row)
+constexpr int kCsrFillEpt = 16;       // edges per thread of a fill chunk at most
 
 // Rows per tile: whole 64-row chunks, about 256 tiles over the batch, at most
 // 1024 rows (tile_base then has at most B * ceil(Nq / 64) * Nk entries).
@@ -588,20 +594,28 @@ int csr_tile_rows(int64_t B, int64_t Nq) {
 }
 static int csr_tiles(const CsrArgs& a) { return (int)csr_tiles(a.B, a.Nq); }
 
+bool csr_table_fits(int64_t B, int64_t Nq, int64_t Nk) {
+  return B >= 1 && Nq >= 1 && Nk >= 1 && csr_table_entries(B, Nq, Nk) <= kCsrMaxTableEntries;
+}
+
 __global__ __launch_bounds__(256) void csr_count_kernel(CsrArgs a, int tile_rows) {
   extern __shared__ int cnt[];  // min(Nk, kCsrCountSlice) counters
   const int t = blockIdx.x, b = blockIdx.y, T = gridDim.x;
   const int r0 = t * tile_rows, nrows = min(tile_rows, a.Nq - r0);
   const int32_t* idx = a.idx + ((int64_t)b * a.Nq + r0) * a.k;
   const int ne = nrows * a.k;
-  int32_t* out = a.tile_base + ((int64_t)b * T + t) * a.Nk;
+  int32_t* out = a.tile_base + ((int64_t)b * (T + 2) + t) * a.Nk;
   for (int s0 = 0; s0 < a.Nk; s0 += kCsrCountSlice) {
     const int s1 = min(a.Nk, s0 + kCsrCountSlice);
     for (int x = threadIdx.x; x < s1 - s0; x += blockDim.x) cnt[x] = 0;
     __syncthreads();
-    for (int x = threadIdx.x; x < ne; x += blockDim.x) {
-      const int j = idx[x];
-      if (j >= s0 && j < s1) atomicAdd(&cnt[j - s0], 1);
+    for (int x0 = threadIdx.x; x0 < ne; x0 += 256 * 8) {
+      int j[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) j[u] = x0 + 256 * u < ne ? idx[x0 + 256 * u] : -1;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (j[u] >= s0 && j[u] < s1) atomicAdd(&cnt[j[u] - s0], 1);
     }
     __syncthreads();
     for (int x = threadIdx.x; x < s1 - s0; x += blockDim.x) out[s0 + x] = cnt[x];
@@ -609,16 +623,37 @@ __global__ __launch_bounds__(256) void csr_count_kernel(CsrArgs a, int tile_rows
   }
 }
 
-// Exclusive scan of v[0..n) in LDS by one 256-thread workgroup (16 entries
-// per thread, n <= 4096); returns the total.  Every thread must call it.
-__device__ int lds_exclusive_scan(int* v, int n, int* wave_tot) {
-  constexpr int PER = kCsrFillSlice / 256;
-  const int lane = lane_id(), wave = wave_id();
-  const int x0 = threadIdx.x * PER;
-  int mine = 0;
+// Thread per key j of a batch element (256-key blocks): the prefix of its
+// counts over the T tiles is written over them (tile t then holds the edges
+// into j from tiles before t); row T of the table receives the exclusive
+// prefix of the degrees within the key's block, and row T + 1 the block's
+// degree sum at the block's index.
+__global__ __launch_bounds__(256) void csr_tile_prefix_kernel(int32_t* tile_base, int T, int Nk) {
+  __shared__ int wave_tot[4];
+  const int b = blockIdx.y, lane = lane_id(), wave = wave_id();
+  const int j = blockIdx.x * 256 + (int)threadIdx.x;
+  int32_t* table = tile_base + (int64_t)b * (T + 2) * Nk;
+  int run = 0;
+  if (j < Nk) {
+    int32_t* cnt = table + j;
+    int t = 0;
+    for (; t + 8 <= T; t += 8) {
+      int c[8];
 #pragma unroll
-  for (int u = 0; u < PER; ++u) mine += (x0 + u < n) ? v[x0 + u] : 0;
-  int incl = mine;  // inclusive wave scan of the threads' sums
+      for (int u = 0; u < 8; ++u) c[u] = cnt[(int64_t)(t + u) * Nk];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        cnt[(int64_t)(t + u) * Nk] = run;
+        run += c[u];
+      }
+    }
+    for (; t < T; ++t) {
+      const int c = cnt[(int64_t)t * Nk];
+      cnt[(int64_t)t * Nk] = run;
+      run += c;
+    }
+  }
+  int incl = run;  // the block's exclusive scan of the degrees
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {
     const int y = __builtin_amdgcn_ds_bpermute(((lane - o) & 63) << 2, incl);
@@ -626,87 +661,157 @@ __device__ int lds_exclusive_scan(int* v, int n, int* wave_tot) {
   }
   if (lane == kWave - 1) wave_tot[wave] = incl;
   __syncthreads();
-  int run = incl - mine;
-  for (int w = 0; w < wave; ++w) run += wave_tot[w];
-  const int total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
-#pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    if (x0 + u < n) {
-      const int c = v[x0 + u];
-      v[x0 + u] = run;
-      run += c;
-    }
-  }
-  __syncthreads();  // wave_tot and v are reused by the caller
-  return total;
+  int excl = incl - run;
+  for (int w = 0; w < wave; ++w) excl += wave_tot[w];
+  if (j < Nk) table[(int64_t)T * Nk + j] = excl;
+  if (threadIdx.x == 0)
+    table[(int64_t)(T + 1) * Nk + blockIdx.x] = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
 }
 
-__global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs a, int tile_rows) {
-  extern __shared__ unsigned long long lds[];  // min(Nk, kCsrFillSlice) masks, then as many int cursors
-  __shared__ int wave_tot[4];
+// PLAIN: records {row | head, coef, edge id, 0} (no score or state
+// gradients): every per-edge load of a chunk is issued before its barrier, so
+// the record pass after it waits on nothing but LDS.
+template <bool PLAIN>
+__global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs a, int tile_rows, int chunk_rows) {
+  extern __shared__ uint32_t lds[];  // masks[2][slice], then slice int cursors
+  __shared__ int block_start[kCsrFillSlice / 256];
+  __shared__ int slice_total;
   const int slice = min(a.Nk, kCsrFillSlice);
-  unsigned long long* masks = lds;
-  int* cursor = reinterpret_cast<int*>(lds + slice);
+  int* cursor = reinterpret_cast<int*>(lds + 2 * slice);
+  const int tid = threadIdx.x, lane = lane_id();
   const int t = blockIdx.x, b = blockIdx.y, T = gridDim.x;
   const int r0 = t * tile_rows, nrows = min(tile_rows, a.Nq - r0);
   const int64_t batch_base = (int64_t)b * a.Nq * a.k;
-  const int32_t* cnt = a.tile_base + (int64_t)b * T * a.Nk;  // [T, Nk] edge counts of the tiles
+  const int32_t* table = a.tile_base + (int64_t)b * (T + 2) * a.Nk;
+  const int32_t* before = table + (int64_t)t * a.Nk;        // edges into each key from earlier tiles
+  const int32_t* in_block = table + (int64_t)T * a.Nk;      // degree prefix within each 256-key block
+  const int32_t* block_sum = table + (int64_t)(T + 1) * a.Nk;
   int32_t* seg = a.seg_start + (int64_t)b * (a.Nk + 1);
+  const int nchunks = (nrows + chunk_rows - 1) / chunk_rows;
+  // the tile's edge index and coefficients (or softsign scores) through
+  // buffer resources: loads of a chunk issue together, branch-free
+  const int64_t tile_e0 = ((int64_t)b * a.Nq + r0) * a.k;
+  const uint32_t tile_bytes = (uint32_t)(nrows * a.k) * 4u;
+  const auto rs_idx = make_rsrc(a.idx + tile_e0, tile_bytes);
+  const float* cf_src = a.coef ? a.coef : a.score;
+  const auto rs_cf = make_rsrc(cf_src ? static_cast<const void*>(cf_src + tile_e0) : static_cast<const void*>(a.idx),
+                               cf_src ? tile_bytes : 0u);
+  [[maybe_unused]] const auto rs_head =
+      make_rsrc(a.ehead ? static_cast<const void*>(a.ehead + tile_e0) : static_cast<const void*>(a.idx),
+                a.ehead ? (uint32_t)(nrows * a.k) : 0u);
   int carry = 0;  // edges into the keys of earlier slices
   for (int s0 = 0; s0 < a.Nk; s0 += kCsrFillSlice) {
-    const int s1 = min(a.Nk, s0 + kCsrFillSlice), ns = s1 - s0;
-    // per key: edges from earlier tiles (kept in the mask slots for now) and its degree
-    for (int x = threadIdx.x; x < ns; x += blockDim.x) {
-      int before = 0, deg = 0;
-      for (int tt = 0; tt < T; ++tt) {
-        const int c = cnt[(int64_t)tt * a.Nk + s0 + x];
-        before += tt < t ? c : 0;
-        deg += c;
+    const int ns = min(a.Nk, s0 + kCsrFillSlice) - s0;
+    // segment starts: the slice's block sums scanned by one wave (every tile
+    // forms the same numbers; tile 0 writes them), then this tile's first slot
+    if (wave_id() == 0) {
+      const int nb = (ns + 255) / 256;
+      const int v = lane < nb ? block_sum[s0 / 256 + lane] : 0;
+      int incl = v;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int y = __builtin_amdgcn_ds_bpermute(((lane - o) & 63) << 2, incl);
+        if (lane >= o) incl += y;
       }
-      masks[x] = (unsigned long long)before;
-      cursor[x] = deg;
+      if (lane < nb) block_start[lane] = carry + incl - v;
+      if (lane == kWave - 1) slice_total = incl;
     }
     __syncthreads();
-    // segment starts: exclusive scan of the degrees, after the earlier slices
-    const int total = lds_exclusive_scan(cursor, ns, wave_tot);
-    for (int x = threadIdx.x; x < ns; x += blockDim.x) {
-      const int start = carry + cursor[x];
+    for (int x = tid; x < ns; x += 256) {
+      const int start = block_start[x / 256] + in_block[s0 + x];
       if (t == 0) seg[s0 + x] = start;
-      cursor[x] = start + (int)masks[x];
+      cursor[x] = start + before[s0 + x];
+      lds[x] = 0u;
+      lds[slice + x] = 0u;
     }
-    carry += total;
+    carry += slice_total;
     __syncthreads();
-    for (int c0 = 0; c0 < nrows; c0 += 64) {
-      const int crows = min(64, nrows - c0);
-      const int64_t e0 = ((int64_t)b * a.Nq + r0 + c0) * a.k;  // the chunk's first edge
-      for (int x = threadIdx.x; x < ns; x += blockDim.x) masks[x] = 0ull;
-      __syncthreads();
-      for (int x = threadIdx.x; x < crows * a.k; x += blockDim.x) {
-        const int j = a.idx[e0 + x];
-        if (j >= s0 && j < s1) atomicOr(&masks[j - s0], 1ull << (x / a.k));
+    // the previous chunk's edges that hold their key's last row there: key
+    // (slice-relative, -1 if none) and mask
+    int pk[kCsrFillEpt];
+    uint32_t pm[kCsrFillEpt];
+    int jn[kCsrFillEpt];  // keys of the next chunk (prefetched; slots past it hold 0)
+#pragma unroll
+    for (int u = 0; u < kCsrFillEpt; ++u) {
+      pk[u] = -1;
+      const int x = tid + 256 * u;
+      const bool in = x < min(chunk_rows, nrows) * a.k;  // (the chunk's test x < ne covers the rest)
+      jn[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_idx, in ? (uint32_t)x * 4u : kOobOffset, 0, 0);
+    }
+    for (int c = 0; c < nchunks; ++c) {
+      uint32_t* M = lds + (c & 1) * slice;
+      uint32_t* Mp = lds + ((c & 1) ^ 1) * slice;
+      const int crow0 = c * chunk_rows;
+      const int ne = min(chunk_rows, nrows - crow0) * a.k;
+      const int64_t e0 = ((int64_t)b * a.Nq + r0 + crow0) * a.k;  // the chunk's first edge
+      // the previous chunk's cursor advances and mask clears, beside this chunk's masks
+#pragma unroll
+      for (int u = 0; u < kCsrFillEpt; ++u) {
+        if (pk[u] >= 0) {
+          cursor[pk[u]] += __popc(pm[u]);
+          Mp[pk[u]] = 0u;
+        }
+      }
+      int jj[kCsrFillEpt];
+      float raw[kCsrFillEpt];                  // coefficient, or the score softsign applies to
+      [[maybe_unused]] int eh[kCsrFillEpt];    // head (PLAIN)
+#pragma unroll
+      for (int u = 0; u < kCsrFillEpt; ++u) {
+        const int x = tid + 256 * u;
+        const int j = jn[u] - s0;
+        const bool in = x < ne && j >= 0 && j < ns;
+        raw[u] = buf_load1(rs_cf, in ? (uint32_t)(crow0 * a.k + x) * 4u : kOobOffset);
+        if constexpr (PLAIN)
+          eh[u] = (int)__builtin_amdgcn_raw_buffer_load_b8(rs_head, in ? (uint32_t)(crow0 * a.k + x) : kOobOffset, 0,
+                                                           0);
+        if (in) atomicOr(&M[j], 1u << (x / a.k));
+        jj[u] = in ? j : -1;
+      }
+      if (c + 1 < nchunks) {  // the next chunk's keys, in flight during this one
+        const int nne = min(chunk_rows, nrows - crow0 - chunk_rows) * a.k;
+        const int nx0 = (crow0 + chunk_rows) * a.k;
+#pragma unroll
+        for (int u = 0; u < kCsrFillEpt; ++u) {
+          const int x = tid + 256 * u;
+          // read as zeros past the chunk (x < ne rejects those slots); no
+          // select here, so the loads stay in flight across the barrier
+          jn[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_idx, x < nne ? (uint32_t)(nx0 + x) * 4u : kOobOffset,
+                                                            0, 0);
+        }
       }
       __syncthreads();
-      for (int x = threadIdx.x; x < crows * a.k; x += blockDim.x) {
+#pragma unroll
+      for (int u = 0; u < kCsrFillEpt; ++u) {
+        pk[u] = -1;
+        const int j = jj[u];
+        if (j < 0) continue;
+        const int x = tid + 256 * u;
+        const int rl = x / a.k;
+        const uint32_t m = M[j];
+        const int pos = cursor[j] + __popc(m & ((1u << rl) - 1u));
         const int64_t eid = e0 + x;
-        const int j = a.idx[eid];
-        if (j >= s0 && j < s1) {
-          const int rl = x / a.k;
-          const int pos = cursor[j - s0] + __popcll(masks[j - s0] & ((1ull << rl) - 1ull));
-          const int row = b * a.Nq + r0 + c0 + rl;
-          const float cf = a.coef ? a.coef[eid] : (a.score ? softsign_f(a.score[eid]) : 0.f);
+        const int row = b * a.Nq + r0 + crow0 + rl;
+        const float cf = a.coef ? raw[u] : (a.score ? softsign_f(raw[u]) : 0.f);
+        if constexpr (PLAIN) {
+          a.rec[batch_base + pos] =
+              make_float4(__int_as_float(row | (eh[u] << kRecHeadShift)), cf, __int_as_float((int)eid), 0.f);
+        } else {
           const float gs = a.rec_eid ? __int_as_float((int)eid) : (a.g_score ? a.g_score[eid] : 0.f);
           const float cd = a.gds ? cf * a.gds[row] : 0.f;
           const int hd = a.ehead ? (int)a.ehead[eid] << kRecHeadShift : 0;
           a.rec[batch_base + pos] = make_float4(__int_as_float(row | hd), cf, gs, cd);
-          if (a.pos) a.pos[eid] = (int32_t)(batch_base + pos);
+        }
+        if (a.pos) a.pos[eid] = (int32_t)(batch_base + pos);
+        if (31 - __clz(m) == rl) {  // the key's last row in this chunk
+          pk[u] = j;
+          pm[u] = m;
         }
       }
       __syncthreads();
-      for (int x = threadIdx.x; x < ns; x += blockDim.x) cursor[x] += __popcll(masks[x]);
-      __syncthreads();
     }
+    __syncthreads();  // the cursors, masks and block starts are reset for the next slice
   }
-  if (t == 0 && threadIdx.x == 0) seg[a.Nk] = carry;
+  if (t == 0 && tid == 0) seg[a.Nk] = carry;
 }
 
 int launch_csr(const CsrArgs& a, hipStream_t stream) {
@@ -719,21 +824,35 @@ int launch_csr_layout(const CsrArgs& a, hipStream_t stream) {
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
   JN_REQUIRE((int64_t)a.B * a.Nq <= kRecRowMask, kUnsupported,
              "edge records hold rows below 2^%d (B * rows = %lld)", kRecHeadShift, (long long)a.B * a.Nq);
+  JN_REQUIRE(csr_table_fits(a.B, a.Nq, a.Nk), kUnsupported,
+             "edge grouping table of %lld tiles x %d keys exceeds %lld entries", (long long)a.B * csr_tiles(a),
+             a.Nk, (long long)kCsrMaxTableEntries);
   dim3 g2(csr_tiles(a), a.B);
-  JN_PROFILE("csr_count_kernel", stream);
-  hipLaunchKernelGGL(csr_count_kernel, g2, dim3(256), (size_t)min(a.Nk, kCsrCountSlice) * sizeof(int), stream, a,
-                     csr_tile_rows(a.B, a.Nq));
+  {
+    JN_PROFILE("csr_count_kernel", stream);
+    hipLaunchKernelGGL(csr_count_kernel, g2, dim3(256), (size_t)min(a.Nk, kCsrCountSlice) * sizeof(int), stream, a,
+                       csr_tile_rows(a.B, a.Nq));
+    JN_LAUNCH_CHECK();
+  }
+  JN_PROFILE("csr_tile_prefix_kernel", stream);
+  hipLaunchKernelGGL(csr_tile_prefix_kernel, dim3((a.Nk + 255) / 256, a.B), dim3(256), 0, stream, a.tile_base,
+                     csr_tiles(a), a.Nk);
   JN_LAUNCH_CHECK();
   return kOk;
 }
 
 int launch_csr_fill(const CsrArgs& a, hipStream_t stream) {
   JN_REQUIRE(!a.score || a.compress == 0, kInvalidArgument, "records take inline coefficients for softsign only");
+  JN_REQUIRE(a.k >= 1 && a.k <= 256 * kCsrFillEpt, kUnsupported, "edge grouping takes up to %d edges per row",
+             256 * kCsrFillEpt);
+  const int chunk_rows = std::max(1, std::min(kCsrChunkRows, 256 * kCsrFillEpt / a.k));
   dim3 g2(csr_tiles(a), a.B);
+  const size_t lds = (size_t)min(a.Nk, kCsrFillSlice) * 3 * sizeof(uint32_t);
   JN_PROFILE("csr_fill_kernel", stream);
-  hipLaunchKernelGGL(csr_fill_kernel, g2, dim3(256),
-                     (size_t)min(a.Nk, kCsrFillSlice) * (sizeof(unsigned long long) + sizeof(int)), stream, a,
-                     csr_tile_rows(a.B, a.Nq));
+  if (a.rec_eid && !a.g_score && !a.gds)
+    hipLaunchKernelGGL(csr_fill_kernel<true>, g2, dim3(256), lds, stream, a, csr_tile_rows(a.B, a.Nq), chunk_rows);
+  else
+    hipLaunchKernelGGL(csr_fill_kernel<false>, g2, dim3(256), lds, stream, a, csr_tile_rows(a.B, a.Nq), chunk_rows);
   JN_LAUNCH_CHECK();
   return kOk;
 }

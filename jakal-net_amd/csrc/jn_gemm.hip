@@ -192,7 +192,7 @@ __device__ __forceinline__ void dense_epilogue_tiles(const GemmArgs& g, int64_t 
     }
 }
 
-constexpr int kGBM = 64, kGBK = 16, kGStride = kGBK + 4;
+constexpr int kGBM = 64, kGBK = 16;
 
 // The K range [kbeg, kend) of the output tile whose rows start at m0 (TILE rows,
 // columns from n0): a causal product reads only the k its rows can reach, and a

@@ -319,7 +319,7 @@ struct CsrArgs {
   const int32_t* idx;
   int k;
   int B, Nq, Nk;
-  int32_t* tile_base;  // [B, T, Nk], T <= ceil(Nq / kCsrTile): per-tile edge counts
+  int32_t* tile_base;  // [B, T + 1, Nk], T = csr_tiles(B, Nq): build scratch (csr_table_entries)
   int32_t* seg_start;  // [B, Nk + 1]
   // [B * Nq * k] edge records grouped by key: {row | head << kRecHeadShift
   // (int bits), coef[e], g_score[e], coef[e] * gds[row]}; a null source
@@ -343,14 +343,21 @@ inline int64_t csr_tiles(int64_t B, int64_t Nq) {
   const int64_t tr = csr_tile_rows(B, Nq);
   return (Nq + tr - 1) / tr;
 }
+inline int64_t csr_table_entries(int64_t B, int64_t Nq, int64_t Nk) { return B * (csr_tiles(B, Nq) + 2) * Nk; }
+// The build's table of per-tile key counts and key degree prefixes (int32)
+// has csr_table_entries(B, Nq, Nk) = B * (csr_tiles + 2) * Nk entries, at most
+// kCsrMaxTableEntries (1 GiB); larger groupings are rejected as unsupported.
+constexpr int64_t kCsrMaxTableEntries = 1LL << 28;
+bool csr_table_fits(int64_t B, int64_t Nq, int64_t Nk);
 // An edge record's first word holds its row below bit kRecHeadShift and its
 // head above (multi-head scores), so rows stay below 2^27.
 constexpr int kRecHeadShift = 27;
 constexpr int kRecRowMask = (1 << kRecHeadShift) - 1;
 int launch_csr(const CsrArgs& a, hipStream_t stream);
-// The two halves of launch_csr: the layout (per-tile edge counts; reads only
-// the edge index) and the fill (segment starts and records; reads the
-// coefficients, score gradients and state gradients as well).
+// The two halves of launch_csr: the layout (per-tile edge counts, segment
+// starts and per-tile slots; reads only the edge index) and the fill (the
+// records; reads the coefficients, score gradients and state gradients as
+// well).
 int launch_csr_layout(const CsrArgs& a, hipStream_t stream);
 int launch_csr_fill(const CsrArgs& a, hipStream_t stream);
 

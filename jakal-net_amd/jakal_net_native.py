@@ -53,6 +53,7 @@ _declare("jn_profile_collect", [ctypes.c_char_p, _SZ])
 _declare("jn_set_gemm_tile", [_I32])
 _declare("jn_set_select_mode", [_I32])
 _declare("jn_set_window_kernels", [_I32])
+_declare("jn_set_side_streams", [_I32])
 _declare(
     "jn_lowrank_topk_select",
     [_P, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _F, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
@@ -255,6 +256,14 @@ def set_window_kernels(mode: int = WINDOW_BAND) -> None:
     where it fits (band <= 128 wide, 16-byte value rows); WINDOW_EDGES runs the
     per-edge gather kernels for every window."""
     _check(_LIB.jn_set_window_kernels(int(mode)))
+
+
+def set_side_streams(on: bool = True) -> None:
+    """Whether the library may run independent kernels of a call on its side
+    stream beside the caller's (True, the default) or runs every kernel on the
+    caller's stream (False: each kernel can be timed alone).  Process-wide;
+    results are bit-identical either way."""
+    _check(_LIB.jn_set_side_streams(1 if on else 0))
 
 
 SELECT_SPLIT_F16 = 0

@@ -139,3 +139,26 @@ def test_multihead_workspace_queries_without_gpu():
     assert tr(2, 50, 40, 8, 8, 8, 64, 3, 4) == 0
     assert tr(2, 50, 40, 8, 8, 8, 40, 3, 4) > 0  # scored-rows select of 3 heads of rank 40
     assert tr(2, 50, 40, 8, 8, 8, 40, 3, 40) > 0  # every destination: no select, 3 x 40 <= 128 ranks
+
+
+def test_edge_grouping_beyond_its_size_limit_is_rejected():
+    """The top-k backward groups edges by key with per-tile key counts (B x
+    (tiles + 1) x N int32, tiles of up to 1024 rows); the workspace and layout
+    queries return 0 (unsupported) where that table would exceed 2^28 entries,
+    and stay positive below it."""
+    lib = ctypes.CDLL(str(LIB))
+    I64 = ctypes.c_int64
+    lay = lib.jn_propagation_topk_layout_bytes
+    lay.argtypes, lay.restype = [I64] * 3, ctypes.c_size_t
+    ws = lib.jn_propagation_topk_workspace_bytes
+    ws.argtypes, ws.restype = [I64] * 6, ctypes.c_size_t
+    tr = lib.jn_transition_topk_workspace_bytes
+    tr.argtypes, tr.restype = [I64] * 8, ctypes.c_size_t
+    assert lay(1, 70000, 8) > 0 and ws(1, 70000, 16, 16, 8, 8) > 0
+    assert lay(1, 500000, 8) > 0  # (489 tiles + the degree row) x 500,000 keys: below the 2^28 entries
+    assert lay(1, 1 << 20, 32) == 0 and ws(1, 1 << 20, 16, 16, 8, 32) == 0
+    assert tr(1, 1 << 20, 1 << 20, 8, 8, 8, 8, 4) == 0 and tr(1, 4096, 1 << 20, 8, 8, 8, 8, 4) > 0
+    # windows need no grouping: their workspace stays linear in N
+    win = lib.jn_propagation_window_workspace_bytes
+    win.argtypes, win.restype = [I64] * 6, ctypes.c_size_t
+    assert 0 < win(1, 1 << 20, 16, 16, 8, 31) < 1 << 31

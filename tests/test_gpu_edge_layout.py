@@ -76,3 +76,78 @@ def test_forward_layout_matches_backward_grouping(dev, B, N, D, r, k, compress, 
     assert len(with_layout) == len(without) >= 6
     for i, (a, b) in enumerate(zip(with_layout, without)):
         assert torch.equal(a, b), f"output {i} differs: max |diff| {(a.float() - b.float()).abs().max().item():.3e}"
+
+
+def _layout_views(buf, B, N, k):
+    """(seg_start [B, N+1], records [B*N*k, 4] as int32 words, pos [B*N*k]) of
+    the edge-layout buffer: three 256-byte-aligned regions in that order."""
+    def up(n):
+        return (n + 255) // 256 * 256
+    raw = buf.cpu()
+    o_rec = up(B * (N + 1) * 4)
+    o_pos = o_rec + up(B * N * k * 16)
+    seg = raw[: B * (N + 1) * 4].view(torch.int32).view(B, N + 1)
+    rec = raw[o_rec: o_rec + B * N * k * 16].view(torch.int32).view(-1, 4)
+    pos = raw[o_pos: o_pos + B * N * k * 4].view(torch.int32)
+    return seg.numpy(), rec.numpy(), pos.numpy()
+
+
+@pytest.mark.parametrize("B,N,k", [
+    (3, 1000, 40),    # 64-row tiles, 32-row fill chunks
+    (1, 5000, 8),     # two LDS key slices of the fill
+    (2, 700, 300),    # 13-row fill chunks
+    (4, 4096, 32),    # the C4 tiling (256-row tiles), one batch element's worth of keys per slice
+])
+def test_edge_layout_is_the_stable_key_sort(dev, B, N, k):
+    """The grouping the forward builds is a stable sort of the edges by key:
+    segment starts are the exclusive prefix of the key degrees, each segment
+    lists its edges in increasing row order, records carry (row, softsign
+    coefficient, edge id) and pos maps each edge to its record."""
+    import ctypes
+
+    import numpy as np
+
+    import jakal_net_native as jn
+
+    print(f"layout sort: B={B} N={N} k={k}", flush=True)
+    g = torch.Generator().manual_seed(9300 + k)
+    D, r = 16, 8
+    X = torch.randn(B, N, D, generator=g).to(dev)
+    ps = torch.randn(B, N, generator=g).to(dev)
+    U = (0.5 * torch.randn(r, D, generator=g)).to(dev)
+    V = (0.5 * torch.randn(r, D, generator=g)).to(dev)
+    w = torch.full((r,), r ** -0.5).to(dev)
+    ds = torch.empty(B, N, device=dev)
+    dv = torch.empty(B, N, D, device=dev)
+    proj = torch.empty(B * N, 2 * r, device=dev)
+    idx = torch.empty(B, N, k, device=dev, dtype=torch.int32)
+    score = torch.empty(B, N, k, device=dev)
+    lb = int(jn._LIB.jn_propagation_topk_layout_bytes(B, N, k))
+    layout = torch.empty(lb, device=dev, dtype=torch.uint8)
+    wb = int(jn._LIB.jn_propagation_topk_forward_workspace_bytes(B, N, r))
+    ws = torch.empty(max(wb, 1), device=dev, dtype=torch.uint8)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    rc = jn._LIB.jn_propagation_topk_forward(
+        P(X), P(ps), P(X), P(U), P(V), P(w), None, B, N, D, D, r, k, 0, P(ds), P(dv), P(proj), P(idx), P(score),
+        P(layout), lb, P(ws), wb, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, jn._LIB.jn_last_error().decode()
+    torch.cuda.synchronize()
+    seg, rec, pos = _layout_views(layout, B, N, k)
+    I = idx.cpu().numpy().reshape(B, N * k)
+    S = score.cpu().numpy().reshape(B, N * k)
+    for b in range(B):
+        keys = I[b]
+        rows = np.repeat(np.arange(N), k)
+        order = np.lexsort((rows, keys))  # by key, then row
+        deg = np.bincount(keys, minlength=N)
+        assert (seg[b, :N] == np.concatenate([[0], np.cumsum(deg)[:-1]])).all()
+        assert seg[b, N] == N * k
+        base = b * N * k
+        got = rec[base: base + N * k]
+        assert (got[:, 0] == b * N + rows[order]).all(), "records out of key/row order"
+        assert (got[:, 2] == base + order).all(), "record edge ids"
+        cf = S[b][order] / (1.0 + np.abs(S[b][order]))
+        np.testing.assert_allclose(np.ascontiguousarray(got[:, 1]).view(np.float32), cf, rtol=1e-6, atol=0)
+        want_pos = np.empty(N * k, np.int64)
+        want_pos[order] = base + np.arange(N * k)
+        assert (pos[base: base + N * k] == want_pos).all()

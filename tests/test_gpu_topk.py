@@ -297,3 +297,61 @@ def test_propagation_topk_signed_rows_beyond_one_block(dev, N, D, k, compress, s
     statistics and, in the backward, the row sums of the compress backward
     span several 64-edge blocks (two passes over the row)."""
     _run_topk(dev, _c1_inputs(seed=1300 + k + D, B=2, N=N, D=D, r=16), compress, separate_pv, k, min_checkable=0.3)
+
+
+def test_propagation_topk_beyond_select_key_limit(dev):
+    """Top-k propagation forward and backward over 70,000 nodes (more keys than
+    the register select ranks: the scored-rows select, and the edge grouping's
+    per-tile key counts at that size).  The N x N oracle is out of reach here,
+    so the check is a float64 restatement of the same op on the GPU's
+    selection (propagation.py:453-480 over the selected edges, differentiated
+    by autograd), plus the selection itself on sampled rows against float64
+    scores of every key."""
+    import jakal_net_native as jn
+
+    B, N, D, r, k = 1, 70000, 16, 8, 8
+    g = torch.Generator().manual_seed(1400)
+    val = torch.randn(B, N, D, generator=g)
+    state = torch.randn(B, N, generator=g)
+    bound = (6.0 / (D + r)) ** 0.5
+    U = (torch.rand(r, D, generator=g) * 2 - 1) * bound
+    V = (torch.rand(r, D, generator=g) * 2 - 1) * bound
+    w = torch.rand(r, generator=g) + 0.5
+    w_hat = w / w.norm()
+    leaves = [t.to(dev).requires_grad_(True) for t in (val, state, U, V, w_hat)]
+    X, ps, Ud, Vd, wd = leaves
+    ds, dv, idx, score = jn.propagation_topk_selection("low_rank_bilinear", wd, None, Vd, None, Ud, None, "softsign",
+                                                       X, ps, X, k, 128, 128)
+    gds = torch.randn(B, N, generator=g).to(dev)
+    gdv = torch.randn(B, N, D, generator=g).to(dev)
+    torch.autograd.backward([ds, dv], [gds, gdv])
+
+    # selection on sampled rows against float64 scores of every key
+    Xd = val.double().to(dev)
+    Pt = Xd @ U.double().to(dev).T * w_hat.double().to(dev)
+    Ps = Xd @ V.double().to(dev).T
+    rows = torch.arange(0, N, N // 64, device=dev)[:64]
+    full = (Pt[0, rows] @ Ps[0].T).cpu().numpy()
+    frac = check_selection(idx[0, rows].cpu().numpy()[None], score[0, rows].cpu().numpy()[None], full[None], k)
+    assert frac > 0.5
+
+    # float64 reference of the op on the selected edges
+    ref = [t.double().detach().to(dev).requires_grad_(True) for t in (val, state, U, V, w_hat)]
+    xv, sv, u64, v64, w64 = ref
+    e = idx.long()[0]                                         # [N, k]
+    pt = (xv[0] @ u64.T) * w64                               # [N, r]
+    pk = xv[0] @ v64.T                                       # [N, r]
+    s = (pt[:, None, :] * pk[e]).sum(-1)                     # [N, k]
+    c = s / (1 + s.abs())
+    ref_ds = (c * sv[0][e]).sum(-1)
+    ref_dv = (c[..., None] * xv[0][e]).sum(1)
+    torch.autograd.backward([ref_ds, ref_dv], [gds[0].double(), gdv[0].double()])
+    check("delta_state", ds[0], ref_ds)
+    check("delta_val", dv[0], ref_dv)
+    # absolute tolerance scaled to the tensor: 1e-5 of its largest entry for
+    # the per-node gradients, 1e-4 for the weight gradients, which are fp32
+    # sums over all 560,000 edges
+    for got, want, name, rel in ((X.grad, xv.grad, "grad val", 1e-5), (ps.grad, sv.grad, "grad state", 1e-5),
+                                 (Ud.grad, u64.grad, "U", 1e-4), (Vd.grad, v64.grad, "V", 1e-4),
+                                 (wd.grad, w64.grad, "w_hat", 1e-4)):
+        check(name, got, want, atol=rel * max(1.0, float(want.abs().max())))

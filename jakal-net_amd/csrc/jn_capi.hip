@@ -28,8 +28,17 @@ void set_error(const char* fmt, ...) {
 
 const char* last_error() { return g_last_error.c_str(); }
 
+namespace {
+thread_local std::map<int, SideStream> g_side_per_device;
+}
+
+SideForkGuard::~SideForkGuard() {
+  for (auto& kv : g_side_per_device)
+    if (kv.second.open) join_from(&kv.second, kv.second.origin);
+}
+
 SideStream* side_stream(hipStream_t origin) {
-  thread_local std::map<int, SideStream> per_device;
+  auto& per_device = g_side_per_device;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   auto it = per_device.find(dev);
@@ -58,10 +67,13 @@ const SideStream* side_stream_for(hipStream_t origin, int64_t edges) {
 int fork_to(const SideStream* s, hipStream_t origin) {
   JN_HIP_TRY(hipEventRecord(s->fork, origin));
   JN_HIP_TRY(hipStreamWaitEvent(s->stream, s->fork, 0));
+  s->open = true;
+  s->origin = origin;
   return kOk;
 }
 
 int join_from(const SideStream* s, hipStream_t origin) {
+  s->open = false;
   JN_HIP_TRY(hipEventRecord(s->join, s->stream));
   JN_HIP_TRY(hipStreamWaitEvent(origin, s->join, 0));
   return kOk;
@@ -650,6 +662,7 @@ int propagation_edges_backward(const float* layer_val, const float* projected_st
                                float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
                                hipStream_t stream, bool bf16 = false, bool band = false,
                                const void* edge_layout = nullptr) {
+  SideForkGuard join_guard;  // joins a fork left open by an error return
   int rc;
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
                  projections && topk_index && topk_score && grad_delta_state && grad_delta_val &&
@@ -980,6 +993,7 @@ int propagation_topk_forward_impl(const float* layer_val, const float* projected
                                   float* topk_score, uint8_t* topk_head, void* edge_layout, size_t edge_layout_bytes,
                                   void* workspace, size_t workspace_bytes,
                                   hipStream_t st, bool bf16 = false) {
+  SideForkGuard join_guard;  // joins a fork left open by an error return
   int rc = check_propagation_shapes(batch, nodes, in_dim, out_dim, rank, topk, compress_kind);
   if (rc) return rc;
   const bool mh = heads > 1;
@@ -1395,6 +1409,7 @@ static int transition_topk_forward_impl(const float* sender_strength, const floa
                                  float* src_proj, float* dst_proj, int32_t* route_index, float* route_logit,
                                  uint8_t* route_head, void* workspace, size_t workspace_bytes, hipStream_t st,
                                  bool bf16 = false) {
+  SideForkGuard join_guard;  // joins a fork left open by an error return
   int rc = check_transition_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, topk, compress_kind,
                                    temperature);
   if (rc) return rc;
@@ -1562,6 +1577,7 @@ static int transition_topk_backward_impl(const float* sender_strength, const flo
                                   float* grad_projected_val, float* grad_source_weight, float* grad_target_weight,
                                   float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
                                   hipStream_t st, bool bf16 = false) {
+  SideForkGuard join_guard;  // joins a fork left open by an error return
   int rc = check_transition_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, topk, compress_kind,
                                    temperature);
   if (rc) return rc;

@@ -368,12 +368,26 @@ int launch_csr_fill(const CsrArgs& a, hipStream_t stream);
 struct SideStream {
   hipStream_t stream;
   hipEvent_t fork, join;
+  // set by fork_to, cleared by join_from: the stream forked from
+  mutable bool open;
+  mutable hipStream_t origin;
 };
 SideStream* side_stream(hipStream_t origin);
 // side_stream(origin) for problems of at least 2^20 edges, else null
 const SideStream* side_stream_for(hipStream_t origin, int64_t edges);
 int fork_to(const SideStream* s, hipStream_t origin);   // s->stream waits for origin's work so far
 int join_from(const SideStream* s, hipStream_t origin); // origin waits for s->stream's work so far
+// Declared at the top of a call that forks: when the call returns (an error
+// return between fork_to and join_from included), a side stream of this
+// thread still forked is joined back into the stream it was forked from, so
+// no return leaves its origin stream -- or a graph under capture -- with an
+// unjoined fork.
+struct SideForkGuard {
+  SideForkGuard() = default;
+  SideForkGuard(const SideForkGuard&) = delete;
+  SideForkGuard& operator=(const SideForkGuard&) = delete;
+  ~SideForkGuard();
+};
 
 struct ColsBwdArgs {
   const int32_t* seg_start;  // [B, Nk + 1]

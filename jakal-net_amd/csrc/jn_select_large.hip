@@ -169,8 +169,14 @@ int launch_topk_select_large(const SelectArgs& a, hipStream_t stream) {
              "multi-head select: %d heads of rank %d (rank %d)", a.heads, a.head_rank, a.r);
   JN_REQUIRE(a.temperature > 0.0f, kInvalidArgument, "temperature must be positive");
   JN_REQUIRE(a.r >= 1 && a.Nq >= 1 && a.B >= 1, kInvalidArgument, "empty select");
-  // score rows that fit the workspace (the register select's split-key scratch)
-  const int64_t rows_fit = a.ws ? (int64_t)(a.ws_bytes / sizeof(float)) / a.Nk : 0;
+  // score rows per block: as many as the select's own workspace size holds
+  // (the register select's split-key scratch for this shape), whatever a
+  // larger buffer the caller passes, so the blocks -- and with them the GEMM
+  // tiles and every score bit -- depend on the shape only
+  const size_t own = mh ? select_workspace_bytes_heads(a.B, a.Nk, a.head_rank, a.heads)
+                        : select_workspace_bytes(a.B, a.Nk, a.r);
+  const size_t usable = std::min(own, a.ws_bytes);
+  const int64_t rows_fit = a.ws ? (int64_t)(usable / sizeof(float)) / a.Nk : 0;
   JN_REQUIRE(rows_fit >= 1, kWorkspaceTooSmall, "select workspace holds no score row (%zu bytes for %d keys)",
              a.ws_bytes, a.Nk);
   float* S = static_cast<float*>(a.ws);

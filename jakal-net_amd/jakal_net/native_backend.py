@@ -49,10 +49,6 @@ class NativeStatus:
     error: str | None
 
 
-_NATIVE_MODULE: Any | None = None
-_NATIVE_STATUS: NativeStatus | None = None
-
-
 def _module_name() -> str:
     return os.environ.get(NATIVE_MODULE_ENV, DEFAULT_NATIVE_MODULE)
 
@@ -61,67 +57,71 @@ def native_disabled_by_env() -> bool:
     return os.environ.get(DISABLE_NATIVE_ENV, "").strip() in _TRUE_FLAGS
 
 
-def _candidate_module_paths() -> tuple[Path, ...]:
-    repo_root = Path(__file__).resolve().parents[2]
-    return (repo_root / "build_native", repo_root / "native" / "build", repo_root)
+class _NativeLoader:
+    """Finds, imports and describes the native module once per process (again
+    on ``force_reload``); keeps the module and its status."""
 
+    def __init__(self) -> None:
+        self.module: Any | None = None
+        self.status: NativeStatus | None = None
 
-def _import_native_module(module_name: str) -> Any:
-    try:
-        return importlib.import_module(module_name)
-    except Exception as first:  # noqa: BLE001
-        errors = [f"default import: {type(first).__name__}: {first}"]
-        for candidate in _candidate_module_paths():
-            if not candidate.exists():
-                continue
-            if str(candidate) not in sys.path:
-                sys.path.insert(0, str(candidate))
+    @staticmethod
+    def search_dirs() -> list[Path]:
+        """Directories tried, in order, after a plain import fails."""
+        root = Path(__file__).resolve().parents[2]
+        return [root / "build_native", root / "native" / "build", root]
+
+    def _locate(self, name: str) -> Any:
+        failures: list[str] = []
+        for where in [None, *(d for d in self.search_dirs() if d.is_dir())]:
+            if where is not None and str(where) not in sys.path:
+                sys.path.insert(0, str(where))
             try:
-                return importlib.import_module(module_name)
+                return importlib.import_module(name)
+            except Exception as exc:  # noqa: BLE001  (every failure is reported)
+                failures.append(f"{where or 'sys.path'} -> {exc.__class__.__name__}: {exc}")
+        raise ImportError(f"cannot import native module {name!r}: " + "; ".join(failures))
+
+    @staticmethod
+    def _describe(module: Any, name: str) -> NativeStatus:
+        def listed(fn_name: str, const_name: str, fallback: tuple[str, ...]) -> tuple[str, ...]:
+            source = getattr(module, fn_name, None)
+            values = source() if callable(source) else getattr(module, const_name, fallback)
+            return tuple(map(str, values))
+
+        backend = getattr(module, "backend_name", None)
+        backend = backend() if callable(backend) else backend
+        return NativeStatus(
+            available=True,
+            module_name=name,
+            backend_name=None if backend is None else str(backend),
+            supported_ops=listed("supported_ops", "SUPPORTED_OPS", ()),
+            supported_devices=listed("supported_devices", "SUPPORTED_DEVICES", ("cpu",)),
+            error=None,
+        )
+
+    def load(self, force_reload: bool = False) -> NativeStatus:
+        name = _module_name()
+        if native_disabled_by_env():  # the switch wins over a module already loaded
+            self.module = None
+            self.status = NativeStatus(False, name, None, (), (),
+                                       f"native backend switched off by {DISABLE_NATIVE_ENV}")
+        elif self.status is None or force_reload:
+            try:
+                module = self._locate(name)
             except Exception as exc:  # noqa: BLE001
-                errors.append(f"{candidate}: {type(exc).__name__}: {exc}")
-        raise ImportError("; ".join(errors)) from first
+                self.module = None
+                self.status = NativeStatus(False, name, None, (), (), f"{exc.__class__.__name__}: {exc}")
+            else:
+                self.module, self.status = module, self._describe(module, name)
+        return self.status
 
 
-def _names(module: Any, fn_name: str, const_name: str, default: tuple[str, ...]) -> tuple[str, ...]:
-    fn = getattr(module, fn_name, None)
-    if callable(fn):
-        return tuple(str(x) for x in fn())
-    return tuple(str(x) for x in getattr(module, const_name, default))
-
-
-def _load_native_module(force_reload: bool = False) -> NativeStatus:
-    global _NATIVE_MODULE, _NATIVE_STATUS
-    module_name = _module_name()
-    if native_disabled_by_env():
-        _NATIVE_MODULE = None
-        _NATIVE_STATUS = NativeStatus(False, module_name, None, (), (), f"{DISABLE_NATIVE_ENV} is set.")
-        return _NATIVE_STATUS
-    if _NATIVE_STATUS is not None and not force_reload:
-        return _NATIVE_STATUS
-    try:
-        module = _import_native_module(module_name)
-    except Exception as exc:  # noqa: BLE001
-        _NATIVE_MODULE = None
-        _NATIVE_STATUS = NativeStatus(False, module_name, None, (), (), f"{type(exc).__name__}: {exc}")
-        return _NATIVE_STATUS
-    backend = getattr(module, "backend_name", None)
-    if callable(backend):
-        backend = backend()
-    _NATIVE_MODULE = module
-    _NATIVE_STATUS = NativeStatus(
-        available=True,
-        module_name=module_name,
-        backend_name=None if backend is None else str(backend),
-        supported_ops=_names(module, "supported_ops", "SUPPORTED_OPS", ()),
-        supported_devices=_names(module, "supported_devices", "SUPPORTED_DEVICES", ("cpu",)),
-        error=None,
-    )
-    return _NATIVE_STATUS
+_LOADER = _NativeLoader()
 
 
 def native_status(*, force_reload: bool = False) -> NativeStatus:
-    return _load_native_module(force_reload=force_reload)
+    return _LOADER.load(force_reload=force_reload)
 
 
 def native_available() -> bool:
@@ -155,17 +155,19 @@ def require_native_for_device(op_name: str, device_type: str) -> None:
 
 def _native_module() -> Any:
     status = native_status()
-    if not status.available or _NATIVE_MODULE is None:
-        raise RuntimeError(status.error or "Native backend is unavailable.")
-    return _NATIVE_MODULE
+    if status.available and _LOADER.module is not None:
+        return _LOADER.module
+    raise RuntimeError(f"no native module to call: {status.error or 'not loaded'}")
 
 
-def _to_layer_delta(result: Any) -> LayerDelta:
+def _as_layer_delta(result: Any) -> LayerDelta:
     if isinstance(result, LayerDelta):
         return result
     if isinstance(result, tuple) and len(result) == 2 and all(isinstance(t, Tensor) for t in result):
-        return LayerDelta(delta_state=result[0], delta_val=result[1])
-    raise TypeError("Native backend must return LayerDelta or (delta_state, delta_val).")
+        delta_state, delta_val = result
+        return LayerDelta(delta_state=delta_state, delta_val=delta_val)
+    raise TypeError(f"a native op returned {type(result).__name__}; expected a LayerDelta or a "
+                    f"(delta_state, delta_val) pair")
 
 
 # ---------------------------------------------------------------------------
@@ -185,7 +187,7 @@ def propagation_topk_native(
     if not supports_pairwise_kernel(pairwise_fn):
         raise TypeError("Unsupported pairwise_fn for native propagation.")
     spec = pairwise_kernel_spec(pairwise_fn, unit_scale=getattr(_native_module(), "unit_scale", None))
-    return _to_layer_delta(
+    return _as_layer_delta(
         _native_module().propagation_topk(
             spec.kind, spec.weight, spec.bias, spec.in_weight, spec.in_bias, spec.out_weight, spec.out_bias,
             edge_compress_name, layer_val, projected_state, projected_val, topk, target_block_size,
@@ -208,7 +210,7 @@ def propagation_window_native(
     if not supports_pairwise_kernel(pairwise_fn):
         raise TypeError("Unsupported pairwise_fn for native propagation.")
     spec = pairwise_kernel_spec(pairwise_fn, unit_scale=getattr(_native_module(), "unit_scale", None))
-    return _to_layer_delta(
+    return _as_layer_delta(
         _native_module().propagation_window(
             spec.kind, spec.weight, spec.bias, spec.in_weight, spec.in_bias, spec.out_weight, spec.out_bias,
             edge_compress_name, layer_val, projected_state, projected_val, window, target_block_size,
@@ -231,7 +233,7 @@ def propagation_dense_native(
     if not supports_pairwise_kernel(pairwise_fn):
         raise TypeError("Unsupported pairwise_fn for native propagation.")
     spec = pairwise_kernel_spec(pairwise_fn, unit_scale=getattr(_native_module(), "unit_scale", None))
-    return _to_layer_delta(
+    return _as_layer_delta(
         _native_module().propagation_dense(
             spec.kind, spec.weight, spec.bias, spec.in_weight, spec.in_bias, spec.out_weight, spec.out_bias,
             edge_compress_name, layer_val, projected_state, projected_val, source_state, target_block_size,
@@ -259,7 +261,7 @@ def transition_pairwise_topk_native(
         raise TypeError("Native sparse pairwise transition supports softmax, signed_abs_softmax and signed_entmax15 "
                         "routes.")
     spec = pairwise_route_kernel_spec(route_fn)
-    return _to_layer_delta(
+    return _as_layer_delta(
         _native_module().transition_pairwise_topk(
             spec.kind, spec.source_weight, spec.source_bias, spec.target_weight, spec.target_bias,
             spec.core_weight, spec.bias, spec.hidden_weight, spec.hidden_bias, spec.out_weight, spec.out_bias,
@@ -284,7 +286,7 @@ def transition_pairwise_dense_native(
     if not supports_pairwise_route_kernel(route_fn):
         raise TypeError("Unsupported pairwise route_fn for native dense transition.")
     spec = pairwise_route_kernel_spec(route_fn)
-    return _to_layer_delta(
+    return _as_layer_delta(
         _native_module().transition_pairwise_dense(
             spec.kind, spec.source_weight, spec.source_bias, spec.target_weight, spec.target_bias,
             spec.core_weight, spec.bias, spec.hidden_weight, spec.hidden_bias, spec.out_weight, spec.out_bias,

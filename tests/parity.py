@@ -56,7 +56,7 @@ def check(what, got, want, ref32=None, rtol=RTOL, atol=ATOL, factor=FACTOR) -> N
 
 
 def _bool_mask(mask, dev, b0, b1):
-    m = torch.from_numpy(np.ascontiguousarray(mask[b0:b1])).to(dev)
+    m = torch.from_numpy(np.array(mask[b0:b1], dtype=bool, copy=True)).to(dev)
     return m
 
 

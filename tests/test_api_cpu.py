@@ -250,8 +250,8 @@ def fake_native(monkeypatch):
         fake = _FakeNative(fail_with)
         status = NB.NativeStatus(True, "fake", "fake", ("propagation_topk", "transition_pairwise_topk"), ("cpu",),
                                  None)
-        monkeypatch.setattr(NB, "_NATIVE_MODULE", fake)
-        monkeypatch.setattr(NB, "_NATIVE_STATUS", status)
+        monkeypatch.setattr(NB._LOADER, "module", fake)
+        monkeypatch.setattr(NB._LOADER, "status", status)
         monkeypatch.delenv(NB.DISABLE_NATIVE_ENV, raising=False)
         return fake
     return install

@@ -121,6 +121,10 @@ def test_c4_topk_forward_backward_full_shape(dev):
         s = O.lowrank_pairwise_scores(vn[bb:bb + 1], vn[bb:bb + 1], Un, Vn, wn, b)
         fracs.append(check_selection(idx_np[bb:bb + 1], score_np[bb:bb + 1], s, k))
     print(f"C4 top-k selection: rows with an unambiguous set {np.mean(fracs):.4f}", flush=True)
+    # C4 scores are small (unit-norm rows, default init: std ~6.5e-4), so the
+    # 32nd/33rd gap exceeds 1e-5 on about a quarter of the rows (0.254 of the
+    # 65,536, some 16,600, checked as exact sets; the rest within 1e-5)
+    assert np.mean(fracs) > 0.2
     want = _oracle_by_batch(vn, np64(state), Un, Vn, wn, b, np64(gds), np64(gdv), "topk",
                             masks=lambda bb: O.mask_from_indices(idx_np[bb:bb + 1], N))
     mask = O.mask_from_indices(idx_np, N)
@@ -215,9 +219,9 @@ def test_c4_topk_bf16_forward_backward_full_shape(dev):
         fracs.append(check_selection(idx_np[bb:bb + 1], score_np[bb:bb + 1], s, k, gap=2 * tol, score_tol=tol))
     print(f"C4 top-k bf16 selection: rows with an unambiguous set {np.mean(fracs):.4f}", flush=True)
     # 4096 keys of small unit-norm scores crowd the 32nd / 33rd place: about a
-    # fifth of the rows (some 12,000) stay outside the bf16 ambiguity band and
-    # are checked exactly, the rest within it
-    assert np.mean(fracs) > 0.1
+    # fifth of the rows (0.179 of them, some 11,700) stay outside the bf16
+    # ambiguity band and are checked exactly, the rest within it
+    assert np.mean(fracs) > 0.15
     want = _oracle_by_batch(vn, np64(state), Un, Vn, wn, b, np64(gds), np64(gdv), "topk",
                             masks=lambda bb: O.mask_from_indices(idx_np[bb:bb + 1], N))
     ref = torch32_propagation(dev, val, state, None, U, V, w_hat, b, O.mask_from_indices(idx_np, N), "softsign",

@@ -258,7 +258,8 @@ def test_select_beyond_register_limits(dev, r, k, Nq, Nk):
         ref = (sq @ np.swapaxes(sk, 1, 2) - 0.5) / temp
         tol = r * 2.0 ** -24 * (np.abs(sq) @ np.swapaxes(np.abs(sk), 1, 2)).max(-1) / temp
         frac = check_selection(idx.cpu().numpy(), score.cpu().numpy(), ref, k, gap=2 * tol + 1e-5, score_tol=tol)
-        assert frac > 0.5
+        print(f"scored-rows select r={r} k={k} Nq={Nq} Nk={Nk}: rows with an unambiguous set {frac:.4f}", flush=True)
+        assert frac > 0.9  # 0.98 at k = 65 of 4096 keys, 1.0 at the other shapes
 
 
 @pytest.mark.parametrize("Nk,k", [(300, 100), (70000, 7)])

@@ -56,21 +56,28 @@ def _run(lib, static, X, ps, U, V, w_hat, bias, k, compress):
     return ds, dv, proj, idx, score
 
 
+def _inputs(seed, B, N, D, r, dev):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(B, N, D, generator=g).to(dev)
+    ps = torch.randn(B, N, generator=g).to(dev)
+    U = (torch.randn(r, D, generator=g) / D ** 0.5).to(dev)
+    V = (torch.randn(r, D, generator=g) / D ** 0.5).to(dev)
+    w = torch.rand(r, generator=g) + 0.5
+    return X, ps, U, V, (w / w.norm()).to(dev), torch.tensor([0.1], device=dev)
+
+
 @pytest.mark.parametrize("compress", [0, 2])
-def test_static_scratch_forward_matches_workspace_forward(compress):
+@pytest.mark.parametrize("shapes", [
+    ((16, 4096, 128, 64, 32), (3, 700, 72, 24, 9)),   # register select
+    ((4, 1500, 64, 32, 100), (2, 600, 40, 16, 70)),   # k > 64: score blocks of the scored-rows select in the array
+])
+def test_static_scratch_forward_matches_workspace_forward(compress, shapes):
     assert torch.cuda.is_available(), "GPU tests need a HIP device"
     lib = _lib()
     dev = torch.device("cuda:0")
     # the second call is smaller: nothing of the first may leak into it
-    for seed, (B, N, D, r, k) in ((31, (16, 4096, 128, 64, 32)), (32, (3, 700, 72, 24, 9))):
-        g = torch.Generator().manual_seed(seed)
-        X = torch.randn(B, N, D, generator=g).to(dev)
-        ps = torch.randn(B, N, generator=g).to(dev)
-        U = (torch.randn(r, D, generator=g) / D ** 0.5).to(dev)
-        V = (torch.randn(r, D, generator=g) / D ** 0.5).to(dev)
-        w = torch.rand(r, generator=g) + 0.5
-        w_hat = (w / w.norm()).to(dev)
-        bias = torch.tensor([0.1], device=dev)
+    for seed, (B, N, D, r, k) in zip((31, 32), shapes):
+        X, ps, U, V, w_hat, bias = _inputs(seed, B, N, D, r, dev)
         want = _run(lib, False, X, ps, U, V, w_hat, bias, k, compress)
         got = _run(lib, True, X, ps, U, V, w_hat, bias, k, compress)
         for a, b, name in zip(got, want, ("delta_state", "delta_val", "projections", "index", "score")):
@@ -87,3 +94,35 @@ def test_static_scratch_rejects_oversize():
     rc = lib.jn_propagation_topk_forward_static(*nul)
     assert rc != 0
     assert b"static scratch holds" in lib.jn_last_error()
+
+
+@pytest.mark.parametrize("k", [32, 100])
+def test_static_scratch_forward_captures_without_allocating(k):
+    """Captured in a global-mode stream capture (where any device allocation
+    fails the capture) the static forward records kernels only; three replays,
+    with eager GPU work between them, equal the eager call bit for bit."""
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    lib = _lib()
+    dev = torch.device("cuda:0")
+    B, N, D, r = 2, 1200, 48, 32
+    X, ps, U, V, w_hat, bias = _inputs(40 + k, B, N, D, r, dev)
+    want = _run(lib, True, X, ps, U, V, w_hat, bias, k, 0)  # eager (also the per-device set-up)
+    outs = [torch.empty_like(t) for t in want]
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    args = [p(X), p(ps), p(X), p(U), p(V), p(w_hat), p(bias), B, N, D, D, r, k, 0] + [p(t) for t in outs]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side, capture_error_mode="global"):
+            rc = lib.jn_propagation_topk_forward_static(*args, ctypes.c_void_p(side.cuda_stream))
+    assert rc == 0, lib.jn_last_error().decode()
+    torch.cuda.current_stream().wait_stream(side)
+    for rep in range(3):
+        for t in outs:
+            t.fill_(float("nan")) if t.is_floating_point() else t.fill_(-7)
+        torch.randn(1 << 20, device=dev).sum()  # other GPU work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b, name in zip(outs, want, ("delta_state", "delta_val", "projections", "index", "score")):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs (k={k})"

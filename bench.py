@@ -192,6 +192,9 @@ def edge_kernel_model(name: str, M: int, E: int, D: int, r: int, split: bool | s
         return ("hbm", E * (4.0 * r + 8.0) + M * 4.0 * r, E * 8.0 + (M + Mk) * 4.0 * r)
     if name.startswith("gemm_f32_kernel"):
         return ("mfma", 2.0 * M * D * 2 * r, None)
+    if name.startswith("gemm_bf16_kernel"):
+        # bf16 layers: projections and their gradients on bf16 MFMA
+        return ("mfma", 2.0 * M * D * 2 * r, None, BF16_MFMA_PEAK_TFLOPS)
     return None
 
 

@@ -121,6 +121,17 @@ __device__ __forceinline__ void fold_store4(const GemmArgs& g, float4 x, float* 
   }
 }
 
+// bf16 layers multiply as autocast's nn.Linear does: the operands that are
+// not bf16 already (the fp32 weights and projection gradients) are rounded to
+// bf16 (nearest even), products accumulate in fp32.  The projection's B (W),
+// the input gradient's A (dP) and B (W), the weight gradient's A (dP^T).
+constexpr bool gemm_use_round_a(int use) { return use == kGemmGradInputBf16 || use == kGemmGradWeightBf16; }
+constexpr bool gemm_use_round_b(int use) { return use == kGemmProjectBf16 || use == kGemmGradInputBf16; }
+__device__ __forceinline__ float bf16_round(float x) { return (float)(bf16_t)x; }
+__device__ __forceinline__ float4 bf16_round4(float4 v) {
+  return make_float4(bf16_round(v.x), bf16_round(v.y), bf16_round(v.z), bf16_round(v.w));
+}
+
 // The A-operand mask of four consecutive elements: bytes of `heads` equal to
 // `head` keep their element.
 __device__ __forceinline__ float4 head_mask4(float4 a, uint32_t heads, int head) {
@@ -366,6 +377,14 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs g) {
     for (int u = 0; u < LPT; ++u) {
       const int e = tid + 256 * u;
       if (NF4 % 256 != 0 && e >= NF4) continue;
+      if constexpr (gemm_use_round_a(USE)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ra[u][q] = bf16_round(ra[u][q]);
+      }
+      if constexpr (gemm_use_round_b(USE)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) rb[u][q] = bf16_round(rb[u][q]);
+      }
       if (A_KC) {
         *reinterpret_cast<float4*>(&sA[buf][(e / KQ) * GS + (e % KQ) * 4]) =
             make_float4(ra[u][0], ra[u][1], ra[u][2], ra[u][3]);
@@ -710,8 +729,9 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
       if constexpr (AMASK) {
         if (g.a_heads) a = head_mask4(a, rh[u], g.a_head);
       }
+      if constexpr (gemm_use_round_a(USE)) a = bf16_round4(a);
       *reinterpret_cast<float4*>(&sA[buf][ia]) = a;
-      *reinterpret_cast<float4*>(&sB[buf][ib]) = rb[u];
+      *reinterpret_cast<float4*>(&sB[buf][ib]) = gemm_use_round_b(USE) ? bf16_round4(rb[u]) : rb[u];
     }
   };
 
@@ -888,6 +908,281 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
   }
 }
 
+// ---- bf16 MFMA path (bf16 layers) ------------------------------------------
+// The projection of bf16 layer values and its two gradients on
+// v_mfma_f32_16x16x32_bf16: workgroup tile 128 x 128, 2 x 2 waves of 64 x 64
+// (4 x 4 tiles of 16 x 16), K in slices of 64 (two K-steps of 32), LDS double
+// buffered with register prefetch.  Both operands sit in LDS as [row][k]
+// bf16 (row = m for A, n for B; 8 elements of padding per row), so a lane's
+// fragment -- 8 consecutive k of one row -- is one 16-byte LDS read.  fp32
+// operands are rounded to bf16 (nearest even) on their way into LDS; K-major
+// operands are transposed there in 4 x 4 (fp32) or 4 x 8 (bf16) blocks.
+// Accumulation is fp32.  The epilogue stages each wave's 64 x 64 block in LDS
+// and writes whole 8-element rows (one 16-byte store of bf16, two of fp32).
+// Preconditions (host-checked, else the fp32 kernels run): M, N >= 128, N and
+// the output strides multiples of 8, K and the split-K chunk multiples of 64
+// ... of 8 for K-contiguous bf16 rows; row strides and batch strides
+// multiples of 8 elements, base pointers 16-byte aligned.  Loads go through
+// buffer resources: a vector outside its operand reads as zeros.
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+constexpr int kBfT = 128;           // tile M and N
+constexpr int kBfK = 64;            // K per slice
+constexpr int kBfS = kBfK + 8;      // LDS row stride in bf16 elements (144 bytes)
+constexpr int kBfStage = 64 + 4;    // epilogue row stride in floats
+
+// Operand loader of one slice: R = 128 rows (m or n) x 64 k into LDS [row][k].
+//   KC: row-major with k contiguous (row stride ld); else k-major (k rows of stride ld).
+//   BF: the source holds bf16; else fp32, rounded to bf16.
+template <bool KC, bool BF>
+struct BfLoader {
+  // 16-byte loads per thread and slice
+  static constexpr int kLoads = KC ? (BF ? 4 : 8) : (BF ? 4 : 8);
+  uint4 r[kLoads];
+
+  // rs0 addresses row 0 of the tile; K-contiguous rows from split_row on
+  // (tile-relative, a multiple of 8) are read through rs1, which addresses
+  // the tile's row 0 as if the second buffer continued the first (the rows a
+  // wave loads with one instruction never straddle it: a wave-uniform choice)
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs0, __amdgpu_buffer_rsrc_t rs1, int split_row, int ld,
+                                       int row0, int rows, int k0, int kend, int tid) {
+    constexpr uint32_t EB = BF ? 2 : 4;
+    [[maybe_unused]] const int wbase = tid & ~63;
+    if constexpr (KC && BF) {  // 128 rows x 8 groups of 8 k
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = tid + 256 * u, row = e >> 3, kq = (e & 7) * 8;
+        const bool ok = row0 + row < rows && k0 + kq < kend;
+        const auto rs = ((wbase + 256 * u) >> 3) < split_row ? rs0 : rs1;
+        r[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rs, ok ? (uint32_t)(row * ld + k0 + kq) * EB : kOobOffset, 0, 0));
+      }
+    } else if constexpr (KC) {  // 128 rows x 16 groups of 4 k
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = tid + 256 * u, row = e >> 4, kq = (e & 15) * 4;
+        const bool ok = row0 + row < rows && k0 + kq < kend;
+        const auto rs = ((wbase + 256 * u) >> 4) < split_row ? rs0 : rs1;
+        r[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rs, ok ? (uint32_t)(row * ld + k0 + kq) * EB : kOobOffset, 0, 0));
+      }
+    } else if constexpr (BF) {  // 16 groups of 4 k x 16 groups of 8 rows: one 4 x 8 block per thread
+      const int kb = tid >> 4, rb = (tid & 15) * 8;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kk = k0 + 4 * kb + i;
+        const bool ok = kk < kend && row0 + rb < rows;
+        r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rs0, ok ? (uint32_t)(kk * ld + rb) * EB : kOobOffset, 0, 0));
+      }
+    } else {  // 16 groups of 4 k x 32 groups of 4 rows: two 4 x 4 blocks per thread
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int blk = tid + 256 * h, kb = blk >> 5, rb = (blk & 31) * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kk = k0 + 4 * kb + i;
+          const bool ok = kk < kend && row0 + rb < rows;
+          r[4 * h + i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       rs0, ok ? (uint32_t)(kk * ld + rb) * EB : kOobOffset, 0, 0));
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ static uint32_t pack2(uint32_t lo, uint32_t hi) {  // two fp32 bit patterns -> bf16x2
+    return pack_bf16x2(__uint_as_float(lo), __uint_as_float(hi));
+  }
+
+  __device__ __forceinline__ void store(bf16_t* s, int tid) const {
+    if constexpr (KC && BF) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = tid + 256 * u, row = e >> 3, kq = (e & 7) * 8;
+        *reinterpret_cast<uint4*>(&s[row * kBfS + kq]) = r[u];
+      }
+    } else if constexpr (KC) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = tid + 256 * u, row = e >> 4, kq = (e & 15) * 4;
+        *reinterpret_cast<uint2*>(&s[row * kBfS + kq]) = make_uint2(pack2(r[u].x, r[u].y), pack2(r[u].z, r[u].w));
+      }
+    } else if constexpr (BF) {
+      // r[i] holds k = 4 kb + i, rows rb .. rb + 7 (two bf16 per word)
+      const int kb = tid >> 4, rb = (tid & 15) * 8;
+      const uint32_t w[4][4] = {{r[0].x, r[0].y, r[0].z, r[0].w}, {r[1].x, r[1].y, r[1].z, r[1].w},
+                                {r[2].x, r[2].y, r[2].z, r[2].w}, {r[3].x, r[3].y, r[3].z, r[3].w}};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int sh = (j & 1) * 16, q = j >> 1;
+        const uint32_t e0 = (w[0][q] >> sh) & 0xFFFFu, e1 = (w[1][q] >> sh) & 0xFFFFu;
+        const uint32_t e2 = (w[2][q] >> sh) & 0xFFFFu, e3 = (w[3][q] >> sh) & 0xFFFFu;
+        *reinterpret_cast<uint2*>(&s[(rb + j) * kBfS + 4 * kb]) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int blk = tid + 256 * h, kb = blk >> 5, rb = (blk & 31) * 4;
+        const uint4* v = &r[4 * h];  // v[i]: k = 4 kb + i, rows rb .. rb + 3
+        const uint32_t c[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w}, {v[1].x, v[1].y, v[1].z, v[1].w},
+                                  {v[2].x, v[2].y, v[2].z, v[2].w}, {v[3].x, v[3].y, v[3].z, v[3].w}};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<uint2*>(&s[(rb + j) * kBfS + 4 * kb]) =
+              make_uint2(pack2(c[0][j], c[1][j]), pack2(c[2][j], c[3][j]));
+      }
+    }
+  }
+};
+
+// C_BF: C and the addend hold bf16 (the input gradient).
+template <bool A_KC, bool A_BF, bool B_KC, bool B_BF, bool C_BF, int USE>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g, int tiles_m, int tiles_n) {
+  __shared__ __align__(16) bf16_t smem[4 * kBfT * kBfS];  // A[2], B[2]; the epilogue reuses it
+  auto sA = [&](int i) { return smem + i * kBfT * kBfS; };
+  auto sB = [&](int i) { return smem + (2 + i) * kBfT * kBfS; };
+  static_assert(4 * 64 * kBfStage * 4 <= 4 * kBfT * kBfS * 2, "epilogue strips must fit in LDS");
+
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int wm = wave >> 1, wn = wave & 1;
+  const int grp = lane >> 4, col = lane & 15;
+
+  // logical tile: contiguous ranges per XCD, bands of 8 M-tiles sweeping N
+  const int id = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int per = tiles_m * tiles_n;
+  const int z = id / per, t = id - z * per;
+  constexpr int kBand = 8;
+  const int band = t / (kBand * tiles_n);
+  const int bm = min(kBand, tiles_m - band * kBand);
+  const int tb = t - band * kBand * tiles_n;
+  const int m0 = (band * kBand + tb % bm) * kBfT;
+  const int n0 = (tb / bm) * kBfT;
+  const bool batched = g.batch > 1;
+  const int split = batched ? 0 : z;
+  const int64_t bz = batched ? z : 0;
+  const int kbeg = split * g.k_chunk;
+  const int kend = min(g.K, kbeg + g.k_chunk);
+
+  constexpr uint32_t AEB = A_BF ? 2 : 4, BEB = B_BF ? 2 : 4;
+  const int lda = (int)g.lda, ldb = (int)g.ldb;
+  // buffer resources from each operand's tile origin (row0 = m0 / n0 along
+  // the row axis, k measured from 0)
+  const char* abase = reinterpret_cast<const char*>(g.A) + (bz * g.a_bs + (A_KC ? (int64_t)m0 * lda : m0)) * AEB;
+  const auto ars = make_rsrc(abase, kFastRecords);
+  auto brsrc = [&](const float* Bp, int64_t rofs) {
+    return make_rsrc(reinterpret_cast<const char*>(Bp) + (bz * g.b_bs + (B_KC ? rofs * ldb : rofs)) * BEB,
+                     kFastRecords);
+  };
+  // B's rows below b_split come from B0, the rest from B1: along n for a
+  // K-contiguous B, along k for a k-major B (whole slices: the host keeps
+  // b_split a multiple of 64 there)
+  const auto brs0 = brsrc(g.B0, n0);
+  const auto brs1 = B_KC ? brsrc(g.B1, (int64_t)n0 - g.b_split) : brsrc(g.B1, n0);
+  const int b_split_row = B_KC ? g.b_split - n0 : 1 << 30;
+
+  BfLoader<A_KC, A_BF> la;
+  BfLoader<B_KC, B_BF> lb;
+  auto load_slice = [&](int k0) {
+    la.load(ars, ars, 1 << 30, lda, m0, g.M, k0, kend, tid);
+    if constexpr (!B_KC) {
+      if (k0 >= g.b_split) lb.load(brs1, brs1, 1 << 30, ldb, n0, g.N, k0 - g.b_split, kend - g.b_split, tid);
+      else lb.load(brs0, brs0, 1 << 30, ldb, n0, g.N, k0, min(kend, g.b_split), tid);
+    } else {
+      lb.load(brs0, brs1, b_split_row, ldb, n0, g.N, k0, kend, tid);
+    }
+  };
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int nslices = kend > kbeg ? (kend - kbeg + kBfK - 1) / kBfK : 0;
+  if (nslices > 0) {
+    load_slice(kbeg);
+    la.store(sA(0), tid);
+    lb.store(sB(0), tid);
+  }
+  __syncthreads();
+  for (int s = 0; s < nslices; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < nslices) load_slice(kbeg + (s + 1) * kBfK);
+#pragma unroll
+    for (int ks = 0; ks < kBfK / 32; ++ks) {
+      bf16x8v av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        av[i] = *reinterpret_cast<const bf16x8v*>(&sA(cur)[(wm * 64 + i * 16 + col) * kBfS + ks * 32 + grp * 8]);
+        bv[i] = *reinterpret_cast<const bf16x8v*>(&sB(cur)[(wn * 64 + i * 16 + col) * kBfS + ks * 32 + grp * 8]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0);
+    }
+    if (s + 1 < nslices) {
+      la.store(sA(cur ^ 1), tid);
+      lb.store(sB(cur ^ 1), tid);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: each wave's 64 x 64 block through LDS, then rows of 8 elements
+  float* stage = reinterpret_cast<float*>(smem) + wave * 64 * kBfStage;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) stage[(mt * 16 + grp * 4 + v) * kBfStage + nt * 16 + col] = acc[mt][nt][v];
+  __syncthreads();
+  float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
+  [[maybe_unused]] bf16_t* Cb = reinterpret_cast<bf16_t*>(g.C) + bz * g.c_bs;
+  [[maybe_unused]] const bf16_t* addb =
+      g.addend ? reinterpret_cast<const bf16_t*>(g.addend) + bz * g.add_bs : nullptr;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int r = it * 8 + (lane >> 3), c0 = (lane & 7) * 8;
+    const int m = m0 + wm * 64 + r, n = n0 + wn * 64 + c0;
+    if (m >= g.M || n >= g.N) continue;
+    const float4 x0 = *reinterpret_cast<const float4*>(&stage[r * kBfStage + c0]);
+    const float4 x1 = *reinterpret_cast<const float4*>(&stage[r * kBfStage + c0 + 4]);
+    if constexpr (C_BF) {
+      float4 y0 = x0, y1 = x1;
+      if (addb) {
+        const uint4 ab = load_nt16(&addb[(int64_t)m * g.ld_add + n]);
+        float a0, a1;
+        unpack_bf16x2(ab.x, a0, a1); y0.x += a0; y0.y += a1;
+        unpack_bf16x2(ab.y, a0, a1); y0.z += a0; y0.w += a1;
+        unpack_bf16x2(ab.z, a0, a1); y1.x += a0; y1.y += a1;
+        unpack_bf16x2(ab.w, a0, a1); y1.z += a0; y1.w += a1;
+      }
+      store_nt16(&Cb[(int64_t)m * g.ldc + n], make_uint4(pack_bf16x2(y0.x, y0.y), pack_bf16x2(y0.z, y0.w),
+                                                         pack_bf16x2(y1.x, y1.y), pack_bf16x2(y1.z, y1.w)));
+    } else {
+      *reinterpret_cast<float4*>(&C[(int64_t)m * g.ldc + n]) = x0;
+      *reinterpret_cast<float4*>(&C[(int64_t)m * g.ldc + n + 4]) = x1;
+    }
+  }
+}
+
+// Whether a bf16 use runs on the bf16 MFMA kernel (see its preconditions).
+static bool bf16_path_ok(const GemmArgs& g, int use, int splits) {
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (g.M < kBfT || g.N < kBfT || g.N % 8 != 0 || g.ldc % 8 != 0 || g.lda % 8 != 0 || g.ldb % 8 != 0) return false;
+  if (g.a_bs % 8 != 0 || g.b_bs % 8 != 0 || g.c_bs % 8 != 0 || g.c_split_stride % 8 != 0) return false;
+  if (g.lda >= (1 << 20) || g.ldb >= (1 << 20)) return false;
+  if (!al16(g.A) || !al16(g.B0) || !al16(g.B1) || !al16(g.C)) return false;
+  if (g.addend && (g.ld_add % 8 != 0 || g.add_bs % 8 != 0 || !al16(g.addend))) return false;
+  if (g.a_kscale || g.c_nscale || g.c_mscale || g.epi || g.fold || g.a_heads) return false;
+  if (splits > 1 && g.k_chunk % kBfK != 0) return false;
+  if (use == kGemmProjectBf16) return g.K % 8 == 0 && g.b_split % 16 == 0;          // A bf16, B fp32, K-contiguous
+  if (use == kGemmGradInputBf16) return g.K % 4 == 0 && g.b_split % kBfK == 0;       // A fp32 K-contig, B fp32 K-major
+  if (use == kGemmGradWeightBf16) return g.M % 4 == 0 && g.b_split >= g.K;            // both K-major
+  return false;
+}
+
 // Sum split-K partials in a fixed order; rows < m_split go to out0, the rest to out1.
 // out = sum over splits of part[z] (fixed order).  A workgroup owns 64
 // consecutive outputs; wave w sums splits z = w, w + 4, ... for its lane's
@@ -991,6 +1286,26 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
   const int64_t tiles64 = (int64_t)((g.M + kGBM - 1) / kGBM) * ((g.N + kGBM - 1) / kGBM) * zdim;
   const bool small = !fast && gemm_use_small_tile(use) && (g.M + 31) / 32 < 65536 &&
                      (forced ? forced == 32 : tiles64 < 256);
+  if (gemm_use_bf16(use) && forced != 32 && forced != 64 && bf16_path_ok(g, use, splits)) {
+    const int tm = (g.M + kBfT - 1) / kBfT, tn = (g.N + kBfT - 1) / kBfT;
+    const int64_t blocks = (int64_t)tm * tn * zdim;
+    JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "GEMM grid too large");
+    JN_PROFILE(use == kGemmProjectBf16 ? "gemm_bf16_kernel<project_bf16>"
+               : use == kGemmGradInputBf16 ? "gemm_bf16_kernel<grad_input_bf16>"
+                                           : "gemm_bf16_kernel<grad_weight_bf16>",
+               stream);
+    if (use == kGemmProjectBf16)
+      hipLaunchKernelGGL((gemm_bf16_kernel<true, true, true, false, false, kGemmProjectBf16>), dim3((unsigned)blocks),
+                         dim3(256), 0, stream, g, tm, tn);
+    else if (use == kGemmGradInputBf16)
+      hipLaunchKernelGGL((gemm_bf16_kernel<true, false, false, false, true, kGemmGradInputBf16>),
+                         dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
+    else
+      hipLaunchKernelGGL((gemm_bf16_kernel<false, false, false, true, false, kGemmGradWeightBf16>),
+                         dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
+    JN_LAUNCH_CHECK();
+    return kOk;
+  }
   JN_PROFILE(info.name, stream);
   switch (use) {
     case kGemmProject: launch_use<kGemmProject>(g, fast, small, (int)zdim, stream); break;
@@ -1102,7 +1417,9 @@ int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, 
                      int M, int N, int K, float* partial, hipStream_t stream, bool x_bf16) {
   int splits = K >= 4096 ? 64 : (K >= 512 ? 8 : 1);
   int k_chunk = (K + splits - 1) / splits;
-  k_chunk = (k_chunk + kGBK - 1) / kGBK * kGBK;
+  // chunks of whole K slices: 16 (fp32 kernels), 64 (the bf16 MFMA kernel)
+  const int kq = x_bf16 ? kBfK : kGBK;
+  k_chunk = (k_chunk + kq - 1) / kq * kq;
   GemmArgs g{};
   g.A = dP; g.lda = ldp;
   g.B0 = X; g.B1 = X; g.ldb = ldx; g.b_split = 1 << 30;

@@ -91,8 +91,31 @@ def _bf16_st(t):
     return t + (t.bfloat16().float() - t).detach()
 
 
+class _Bf16Grad(torch.autograd.Function):
+    """The identity, whose incoming gradient is rounded to bf16: the bf16
+    grad_output that autocast's nn.Linear backward multiplies."""
+
+    @staticmethod
+    def forward(ctx, t):
+        return t.clone()
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.bfloat16().float()
+
+
+def _linear32(x, W, bf16_linear):
+    """x . W^T; bf16_linear: as autocast's nn.Linear on bf16 x -- the weight
+    rounded to bf16 (straight-through), fp32 accumulation, the gradient into
+    the product rounded to bf16 before it reaches x and W (the library's bf16
+    projection GEMMs)."""
+    if not bf16_linear:
+        return x @ W.T
+    return _Bf16Grad.apply(x @ _bf16_st(W).T)
+
+
 def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, chunk=4,
-                        bf16_operands=False) -> dict:
+                        bf16_operands=False, bf16_linear=None) -> dict:
     """fp32 torch forward + autograd backward of low-rank propagation on a given mask.
 
     val [B,N,D], ps [B,N], pv [B,N,Dv] or None (pv is val itself), U/V [r,D],
@@ -101,7 +124,11 @@ def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, 
     bool (numpy), gds [B,N] / gdv [B,N,Dv] the upstream gradients.  Returns
     the oracle's keys: delta_state, delta_val, val (whole gradient of val),
     ps, pv, U, V, w_hat, b.  bf16_operands: the score is
-    bf16(P_t * w_hat) . bf16(P_s), the operands of the bf16 top-k select."""
+    bf16(P_t * w_hat) . bf16(P_s), the operands of the bf16 top-k select.
+    bf16_linear (default: bf16_operands): the projections as the bf16 entry
+    points compute them (_linear32)."""
+    if bf16_linear is None:
+        bf16_linear = bf16_operands
     f32 = dict(device=dev, dtype=torch.float32)
     Ud = torch.as_tensor(U).to(**f32).requires_grad_(True)
     Vd = torch.as_tensor(V).to(**f32).requires_grad_(True)
@@ -123,13 +150,12 @@ def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, 
             if bd is not None:
                 s = s + bd[:, None, None]
             s = s.max(dim=1).values
-        elif bf16_operands:
-            s = _bf16_st((x @ Ud.T) * wd) @ _bf16_st(x @ Vd.T).transpose(-1, -2).contiguous()
-            if bd is not None:
-                s = s + bd
         else:
-            key = ((x @ Vd.T) * wd).transpose(-1, -2).contiguous()
-            s = (x @ Ud.T) @ key
+            pt, pk = _linear32(x, Ud, bf16_linear), _linear32(x, Vd, bf16_linear)
+            if bf16_operands:
+                s = _bf16_st(pt * wd) @ _bf16_st(pk).transpose(-1, -2).contiguous()
+            else:
+                s = pt @ (pk * wd).transpose(-1, -2).contiguous()
             if bd is not None:
                 s = s + bd
         e = _compress32(s, m, kind)
@@ -154,7 +180,7 @@ def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, 
 
 
 def torch32_transition(dev, src, dst, rho, ps, pv, Ws, Wt, w, b, temperature, mask, kind, gds, gdv,
-                       chunk=4, bf16_operands=False) -> dict:
+                       chunk=4, bf16_operands=False, bf16_linear=None) -> dict:
     """fp32 torch forward + autograd backward of low-rank routing on a given mask.
 
     src [B,Ns,Ds], dst [B,Nd,Dd], rho [B,Ns] (sender strength, a leaf), ps
@@ -163,7 +189,10 @@ def torch32_transition(dev, src, dst, rho, ps, pv, Ws, Wt, w, b, temperature, ma
     (numpy) or None (every destination).  Returns the
     oracle's keys: delta_state, delta_val, sender, src_val, dst_val, ps, pv,
     Ws, Wt, w, b.  bf16_operands: the logit is bf16(P_s * w) . bf16(P_t),
-    the operands of the bf16 top-k select."""
+    the operands of the bf16 top-k select; bf16_linear (default:
+    bf16_operands): the projections as the bf16 entry points compute them."""
+    if bf16_linear is None:
+        bf16_linear = bf16_operands
     f32 = dict(device=dev, dtype=torch.float32)
     Wsd = torch.as_tensor(Ws).to(**f32).requires_grad_(True)
     Wtd = torch.as_tensor(Wt).to(**f32).requires_grad_(True)
@@ -185,13 +214,12 @@ def torch32_transition(dev, src, dst, rho, ps, pv, Ws, Wt, w, b, temperature, ma
             if bd is not None:
                 l = l + bd[:, None, None]
             l = l.max(dim=1).values
-        elif bf16_operands:
-            l = _bf16_st((s_ @ Wsd.T) * wd) @ _bf16_st(d_ @ Wtd.T).transpose(-1, -2).contiguous()
-            if bd is not None:
-                l = l + bd
         else:
-            tgt = (d_ @ Wtd.T).transpose(-1, -2).contiguous()
-            l = ((s_ @ Wsd.T) * wd) @ tgt
+            p_src, p_dst = _linear32(s_, Wsd, bf16_linear), _linear32(d_, Wtd, bf16_linear)
+            if bf16_operands:
+                l = _bf16_st(p_src * wd) @ _bf16_st(p_dst).transpose(-1, -2).contiguous()
+            else:
+                l = (p_src * wd) @ p_dst.transpose(-1, -2).contiguous()
             if bd is not None:
                 l = l + bd
         l = l / float(temperature)
@@ -256,6 +284,13 @@ def bf16_round(x) -> np.ndarray:
     """x rounded to fp32 and then to bf16 (nearest even), as float64."""
     t = torch.from_numpy(np.ascontiguousarray(np.asarray(x, dtype=np.float32)))
     return t.bfloat16().double().numpy()
+
+
+def bf16_linear64(x, W):
+    """x . bf16(W)^T in float64: the projection of a bf16 layer, whose GEMM
+    rounds the fp32 weight to bf16 (as autocast's nn.Linear) and accumulates
+    exact products."""
+    return np.asarray(x, np.float64) @ bf16_round(W).T
 
 
 def bf16_select_scores(q, key, scale, bias=None, temperature=1.0):

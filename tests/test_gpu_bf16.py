@@ -18,7 +18,7 @@ import pytest
 import torch
 
 import jakal_oracle as O
-from parity import (bf16_select_scores, check_bf16_calibrated, check_selection, torch32_propagation,
+from parity import (bf16_linear64, bf16_select_scores, check_bf16_calibrated, check_selection, torch32_propagation,
                     torch32_transition)
 
 pytestmark = pytest.mark.gpu
@@ -51,6 +51,16 @@ def test_bf16_propagation(dev, mode):
     run_bf16_propagation(dev, mode, B=2, N=128, D=32, r=8)
 
 
+@pytest.mark.parametrize("mode", ["topk", "window"])
+def test_bf16_projection_gemms_on_ragged_tiles(dev, mode):
+    """Projection and gradient GEMMs of a bf16 layer on the bf16 MFMA kernel
+    (128 x 128 tiles) with every extent ragged: 2,100 rows, D = 200 (K of the
+    projection: three whole 64-wide slices and a partial one; N of the input
+    gradient), and the weight gradient's K of 2,100 rows in split-K chunks of
+    320 (the last chunk empty)."""
+    run_bf16_propagation(dev, mode, B=3, N=700, D=200, r=64, k=12, seed=5011)
+
+
 def run_bf16_propagation(dev, mode, B, N, D, r, k=8, seed=5001):
     import jakal_net_native as jn
 
@@ -63,7 +73,8 @@ def run_bf16_propagation(dev, mode, B, N, D, r, k=8, seed=5001):
     args = ("low_rank_bilinear", w_hat, None, V.to(dev), None, U.to(dev), None, "softsign", X, ps, X)
     if mode == "topk":
         ds, dv, idx, score = jn.propagation_topk_selection(*args, k, N, N)
-        scores, tol = bf16_select_scores(_np(val) @ _np(U).T, _np(val) @ _np(V).T, _np(w_hat))
+        scores, tol = bf16_select_scores(bf16_linear64(_np(val), _np(U)), bf16_linear64(_np(val), _np(V)),
+                                         _np(w_hat))
         assert check_selection(idx.cpu().numpy(), score.cpu().numpy(), scores, k, gap=2 * tol, score_tol=tol) > 0.5
         mask = O.mask_from_indices(idx.cpu().numpy(), N)
         kw = dict(mode="topk", topk=k, mask=mask)
@@ -82,9 +93,10 @@ def run_bf16_propagation(dev, mode, B, N, D, r, k=8, seed=5001):
                                 kind="softsign", **kw)
     mask = O.propagation_forward(_np(val), _np(state), _np(val), _np(U), _np(V), _np(w), 0.0, kind="softsign",
                                  **kw)["mask"]
-    # the top-k scores come from bf16 operands; window and dense scores are fp32
+    # the top-k scores come from bf16 operands; window and dense scores are fp32;
+    # the top-k and window projections are bf16 GEMMs (dense upcasts to fp32)
     t = torch32_propagation(dev, val, state, None, U, V, w / w.norm(), None, np.ascontiguousarray(mask), "softsign",
-                            gds, gdv, bf16_operands=mode == "topk")
+                            gds, gdv, bf16_operands=mode == "topk", bf16_linear=mode != "dense")
     check_bf16_calibrated("delta_state", ds, gr["delta_state"], t["delta_state"])
     check_bf16_calibrated("delta_val", dv, gr["delta_val"], t["delta_val"])
     check_bf16_calibrated("grad layer_val", X.grad, gr["val"] + gr["pv"], t["val"])
@@ -113,7 +125,7 @@ def test_bf16_transition(dev):
     gds = torch.randn(B, Nd, generator=g).bfloat16()
     gdv = torch.randn(B, Nd, D, generator=g).bfloat16()
     torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
-    logits, tol = bf16_select_scores(_np(src) @ _np(Ws).T, _np(dst) @ _np(Wt).T, _np(w))
+    logits, tol = bf16_select_scores(bf16_linear64(_np(src), _np(Ws)), bf16_linear64(_np(dst), _np(Wt)), _np(w))
     assert check_selection(idx.cpu().numpy(), logit.cpu().numpy(), logits, k, gap=2 * tol, score_tol=tol) > 0.5
     mask = O.mask_from_indices(idx.cpu().numpy(), Nd)
     rho_np = _np(rho)

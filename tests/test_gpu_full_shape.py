@@ -23,8 +23,8 @@ import pytest
 import torch
 
 import jakal_oracle as O
-from parity import (bf16_select_scores, check, check_bf16_calibrated, check_selection, np64, torch32_propagation,
-                    torch32_transition)
+from parity import (bf16_linear64, bf16_select_scores, check, check_bf16_calibrated, check_selection, np64,
+                    torch32_propagation, torch32_transition)
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 
@@ -176,7 +176,8 @@ def test_c3_bf16_transition_full_shape(dev, Ns, Nd):
     assert srcd.grad.dtype == torch.bfloat16
 
     # the select ranks bf16(P_s * w) . bf16(P_t) + b on bf16 MFMAs
-    logits, tol = bf16_select_scores(np64(src) @ np64(Ws).T, np64(dst) @ np64(Wt).T, np64(w), bias)
+    logits, tol = bf16_select_scores(bf16_linear64(np64(src), np64(Ws)), bf16_linear64(np64(dst), np64(Wt)), np64(w),
+                                     bias)
     frac = check_selection(idx.cpu().numpy(), logit.cpu().numpy(), logits, k, gap=2 * tol, score_tol=tol)
     print(f"C3 bf16 {Ns}->{Nd}: rows with an unambiguous set {frac:.4f}", flush=True)
     # bf16 operand rounding widens the ambiguity band: fewer rows are checked
@@ -215,7 +216,7 @@ def test_c4_topk_bf16_forward_backward_full_shape(dev):
     vn, Un, Vn, wn = np64(val), np64(U), np64(V), np64(w_hat)
     fracs = []
     for bb in range(B):
-        s, tol = bf16_select_scores(vn[bb:bb + 1] @ Un.T, vn[bb:bb + 1] @ Vn.T, wn, b)
+        s, tol = bf16_select_scores(bf16_linear64(vn[bb:bb + 1], Un), bf16_linear64(vn[bb:bb + 1], Vn), wn, b)
         fracs.append(check_selection(idx_np[bb:bb + 1], score_np[bb:bb + 1], s, k, gap=2 * tol, score_tol=tol))
     print(f"C4 top-k bf16 selection: rows with an unambiguous set {np.mean(fracs):.4f}", flush=True)
     # 4096 keys of small unit-norm scores crowd the 32nd / 33rd place: about a

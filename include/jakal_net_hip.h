@@ -36,7 +36,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 10. */
+/* ABI revision of this header (bumped on any signature change); this is 11. */
 int jn_abi_version(void);
 
 /*
@@ -663,6 +663,130 @@ int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float
                           jn_stream_t stream);
 int jn_unit_scale_backward(const float* weight, const float* grad_weight_hat, int64_t rows, int64_t rank, float eps,
                            float* grad_weight, jn_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Raw edge ops: the reference extension's *_cuda ops that its Python
+ * dispatcher composes into its own autograd functions
+ * (src/jakal_net/native_backend.py:4408-4600 _LowRankTransitionPairwiseTopK,
+ * 4002-4134 _LowRankPropagationQueryTopK; availability probes 657-667 and
+ * 5962-5975).  Sums over a node's incoming edges walk the edges grouped by
+ * that node (fixed order): results repeat bit for bit, where the reference
+ * scatters with float atomics.  Index arrays are int32 ([B, rows, k],
+ * batch-local, -1 = absent edge).
+ * ------------------------------------------------------------------------- */
+
+/*
+ * Per-row top-k of max_h (query_h[b,i] . key_h[b,j] + bias[h]) over `heads`
+ * heads of rank head_rank (heads == 1: one dot product), sorted descending,
+ * ties toward the lower j; 1 <= k <= nk (k == nk keeps every key in score
+ * order).  query [B, nq, heads*head_rank], key [B, nk, heads*head_rank] with
+ * head h in ranks [h*head_rank, (h+1)*head_rank); bias [heads] or NULL.
+ * Replaces the select of low_rank_pairwise_topk_forward_cuda
+ * (native/jakal_net_native_cuda.cu:740-813, multi-head 881-930: [B, H, N, r]
+ * operands, which the caller lays out heads-innermost) and of
+ * low_rank_propagation_topk_forward_cuda (cu:1029-1065).
+ */
+int jn_lowrank_topk_select_heads(const float* query, const float* key, const float* bias, int64_t batch, int64_t nq,
+                                 int64_t nk, int64_t head_rank, int64_t heads, int64_t topk, int32_t* out_index,
+                                 float* out_score, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+size_t jn_lowrank_topk_select_heads_workspace_bytes(int64_t batch, int64_t nk, int64_t head_rank, int64_t heads);
+
+/*
+ * grad_scores = grad_edges / (1 + |scores|)^2 over `count` elements.
+ * Replaces softsign_backward_cuda (native/jakal_net_native.cpp:398-405,
+ * native/jakal_net_native_cuda.cu:2177-2190).
+ */
+int jn_softsign_backward(const float* scores, const float* grad_edges, int64_t count, float* grad_scores,
+                         jn_stream_t stream);
+
+/*
+ * Softmax backward over rows of k: grad_scores = p * (g - sum_e p g).
+ * Replaces softmax_backward_cuda (native/jakal_net_native.cpp:407-414,
+ * native/jakal_net_native_cuda.cu:2192-2212).
+ */
+int jn_softmax_backward(const float* routes, const float* grad_routes, int64_t rows, int64_t k, float* grad_scores,
+                        jn_stream_t stream);
+
+/*
+ * delta_state[b,i] = sum_e c[b,i,e] ps[b,j]; delta_val[b,i] = sum_e c[b,i,e] pv[b,j],
+ * j = edge_index[b,i,e], c = compress(edge_score) per row: 0 softsign,
+ * 1 signed |s| softmax, 2 signed entmax-1.5, 3 the scores are the
+ * coefficients.  projected_state [B, source_nodes], projected_val
+ * [B, source_nodes, dim].
+ * Replaces query_topk_reduce_cuda (native/jakal_net_native.cpp:140-150,
+ * kind 3) and the edge sums of low_rank_propagation_topk_forward_cuda
+ * (native/jakal_net_native_cuda.cu:1084-1175, kinds 0-2).
+ */
+int jn_edge_aggregate(const int32_t* edge_index, const float* edge_score, int64_t batch, int64_t query_nodes,
+                      int64_t source_nodes, int64_t edges, int64_t dim, int32_t compress_kind,
+                      const float* projected_state, const float* projected_val, float* delta_state,
+                      float* delta_val, jn_stream_t stream);
+
+/*
+ * Backward of jn_edge_aggregate with given coefficients (edge_weight):
+ *   grad_edge_weight[b,i,e] = gds[b,i] ps[b,j] + <gdv[b,i], pv[b,j]>
+ *   grad_projected_state[b,j] = sum over edges into j of edge_weight * gds[b,i]
+ *   grad_projected_val[b,j]   = sum over edges into j of edge_weight * gdv[b,i]
+ * Any of the three outputs may be NULL (not computed).  The workspace (edges
+ * grouped by source) is needed when a projected gradient is asked for; the
+ * grouping needs every row's nodes distinct (as in top-k index rows) and in
+ * [0, source_nodes) or -1.
+ * Replaces query_topk_reduce_backward_cuda (native/jakal_net_native.cpp:
+ * 152-165, native/jakal_net_native_cuda.cu:2112-2175).
+ */
+int jn_edge_reduce_backward(const float* edge_weight, const int32_t* edge_index, const float* projected_state,
+                            const float* projected_val, const float* grad_delta_state, const float* grad_delta_val,
+                            int64_t batch, int64_t query_nodes, int64_t source_nodes, int64_t edges, int64_t dim,
+                            float* grad_edge_weight, float* grad_projected_state, float* grad_projected_val,
+                            void* workspace, size_t workspace_bytes, jn_stream_t stream);
+size_t jn_edge_reduce_backward_workspace_bytes(int64_t batch, int64_t query_nodes, int64_t source_nodes,
+                                               int64_t edges);
+
+/*
+ * Routes of a top-k transition and their destination sums:
+ *   route[b,i,e] = compress(route_score[b,i,:])[e] (0 softmax, 1 signed |s|
+ *   softmax, 2 signed entmax-1.5), k <= 64 per source;
+ *   delta_state[b,j] = sum over routes into j of route * weighted_state[b,i];
+ *   delta_val[b,j]   = sum over routes into j of route * weighted_val[b,i].
+ * Each source's destinations must be distinct and in [0, dst_nodes) or -1
+ * (the routes are grouped by destination), as a top-k select returns them.
+ * Replaces the route and destination stage of
+ * low_rank_pairwise_topk_forward_cuda (native/jakal_net_native.cpp:167-189,
+ * native/jakal_net_native_cuda.cu:2420-2543, kernel 788-878).
+ */
+int jn_route_topk_aggregate(const int32_t* route_index, const float* route_score, int64_t batch, int64_t src_nodes,
+                            int64_t dst_nodes, int64_t edges, int64_t dim, int32_t compress_kind,
+                            const float* weighted_state, const float* weighted_val, float* delta_state,
+                            float* delta_val, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+size_t jn_route_topk_aggregate_workspace_bytes(int64_t batch, int64_t src_nodes, int64_t dst_nodes, int64_t edges);
+
+/*
+ * Low-rank pair-score backward.  With g = grad_scores / temperature on the
+ * edges (i, j = edge_index[b,i,e]), Pq = projected_query [B, query_nodes, r],
+ * Ps = projected_source [B, source_nodes, r], w = core_weight [r]:
+ *   dPq[i] = w * sum_e g Ps[j]              dPs[j] = w * sum over edges into j of g Pq[i]
+ *   grad_query  = dPq . target_weight       grad_source = dPs . source_weight
+ *   grad_target_weight = dPq^T query_val    grad_source_weight = dPs^T source_val
+ *   grad_core_weight = sum g Pq * Ps        grad_bias = sum g
+ * query_val [B, query_nodes, query_dim] with target_weight [r, query_dim];
+ * source_val [B, source_nodes, source_dim] with source_weight [r, source_dim];
+ * grad_bias is one float.  Each row's source nodes must be distinct and in
+ * [0, source_nodes) or -1 (the edges are grouped by source).  (The reference
+ * kernel indexes both sides with
+ * query_val's feature dim, so it agrees where the two dims are equal.)
+ * Replaces low_rank_pairwise_topk_backward_cuda (native/jakal_net_native.cpp:
+ * 449-477, native/jakal_net_native_cuda.cu:2259-2322, 3792-3866).
+ */
+int jn_lowrank_pair_backward(const float* query_val, const float* source_val, const float* source_weight,
+                             const float* target_weight, const float* core_weight, const float* projected_query,
+                             const float* projected_source, const int32_t* edge_index, const float* grad_scores,
+                             float temperature, int64_t batch, int64_t query_nodes, int64_t source_nodes,
+                             int64_t query_dim, int64_t source_dim, int64_t rank, int64_t edges, float* grad_query,
+                             float* grad_source, float* grad_source_weight, float* grad_target_weight,
+                             float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
+                             jn_stream_t stream);
+size_t jn_lowrank_pair_backward_workspace_bytes(int64_t batch, int64_t query_nodes, int64_t source_nodes,
+                                                int64_t query_dim, int64_t source_dim, int64_t rank, int64_t edges);
 
 #ifdef __cplusplus
 }

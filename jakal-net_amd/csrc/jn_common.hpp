@@ -542,6 +542,10 @@ __device__ __forceinline__ RowStats row_compress_stats(const int32_t* idx, const
   return st;
 }
 
+// Compress kind whose "scores" are the edge coefficients themselves (edge
+// lists that arrive already compressed); it needs no row statistics.
+constexpr int kCoefGiven = 3;
+
 // Coefficient of edge e0 + lane of a row (0 for absent edges), given the
 // row's statistics (row_compress_stats).
 __device__ __forceinline__ void row_coefficients(const int32_t* idx, const float* score, int64_t row, int k, int e0,
@@ -556,6 +560,8 @@ __device__ __forceinline__ void row_coefficients(const int32_t* idx, const float
       s = score[row * k + e];
       if (compress == 0) {
         c = softsign_f(s);
+      } else if (compress == kCoefGiven) {
+        c = s;
       } else if (compress == 1) {
         c = sign_f(s) * __expf(fabsf(s) - st.a) * st.b;
       } else {

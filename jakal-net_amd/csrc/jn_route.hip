@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void route_coef_kernel(const int32_t* idx, con
     if (j >= 0) s = logit[row * k + lane];
   }
   const float p = route_probability(j, s, compress);
-  if (lane < k) coef[row * k + lane] = rho[row] * p;
+  if (lane < k) coef[row * k + lane] = rho ? rho[row] * p : p;
 }
 
 int launch_route_coef(const int32_t* idx, const float* logit, const float* rho, int k, int compress, int64_t rows,

@@ -1304,7 +1304,8 @@ size_t select_workspace_bytes_heads(int64_t B, int64_t Nk, int64_t head_rank, in
 int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   SelectArgs a = a_in;
   const bool large_heads = a.heads > 1 && !(a.bf16 == 0 && select_heads_fit(a.head_rank, a.heads));
-  if (a.k > kSelectMaxK || a.Nk > kSelMaxKeys || large_heads) return launch_topk_select_large(a, stream);
+  // k == Nk (every key kept, in score order) runs on the scored rows too
+  if (a.k > kSelectMaxK || a.Nk > kSelMaxKeys || large_heads || a.k >= a.Nk) return launch_topk_select_large(a, stream);
   JN_REQUIRE(a.k >= 1 && a.k <= kSelectMaxK, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)", kSelectMaxK,
              a.k);
   JN_REQUIRE(a.k < a.Nk, kInvalidArgument, "top-k select needs k < key count (k=%d, Nk=%d)", a.k, a.Nk);

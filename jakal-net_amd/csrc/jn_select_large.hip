@@ -1,8 +1,8 @@
 // Exact top-k over whole score rows (gfx950), for the selects the register
 // and LDS kernels of jn_select.hip do not take: k above 64 (up to
-// kSelectLargeMaxK) or more than 65,535 keys per batch element.  The
-// reference's composite op takes any k (native/jakal_net_native.cpp:
-// 6399-6424: blockwise scores, then torch.topk).
+// kSelectLargeMaxK), k equal to the key count, or more than 65,535 keys per
+// batch element.  The reference's composite op takes any k
+// (native/jakal_net_native.cpp:6399-6424: blockwise scores, then torch.topk).
 //
 // Rows are scored in blocks: a batched fp32 MFMA GEMM writes the low-rank
 // scores q_i . (scale * k_j) of as many query rows as the select workspace
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* S, int64_t 
 int launch_topk_select_large(const SelectArgs& a, hipStream_t stream) {
   JN_REQUIRE(a.k >= 1 && a.k <= kSelectLargeMaxK, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)",
              kSelectLargeMaxK, a.k);
-  JN_REQUIRE(a.k < a.Nk, kInvalidArgument, "top-k select needs k < key count (k=%d, Nk=%d)", a.k, a.Nk);
+  JN_REQUIRE(a.k <= a.Nk, kInvalidArgument, "top-k select needs k <= key count (k=%d, Nk=%d)", a.k, a.Nk);
   const bool mh = a.heads > 1;
   JN_REQUIRE(!mh || (a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r), kUnsupported,
              "multi-head select: %d heads of rank %d (rank %d)", a.heads, a.head_rank, a.r);

@@ -185,6 +185,21 @@ _declare(
      _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
 )
 
+_declare("jn_lowrank_topk_select_heads", [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P])
+_declare("jn_lowrank_topk_select_heads_workspace_bytes", [_I64] * 4, _SZ)
+_declare("jn_softsign_backward", [_P, _P, _I64, _P, _P])
+_declare("jn_softmax_backward", [_P, _P, _I64, _I64, _P, _P])
+_declare("jn_edge_aggregate", [_P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P])
+_declare("jn_edge_reduce_backward",
+         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P])
+_declare("jn_edge_reduce_backward_workspace_bytes", [_I64] * 4, _SZ)
+_declare("jn_route_topk_aggregate", [_P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _SZ, _P])
+_declare("jn_route_topk_aggregate_workspace_bytes", [_I64] * 4, _SZ)
+_declare("jn_lowrank_pair_backward",
+         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+          _P, _P, _P, _P, _P, _P, _P, _SZ, _P])
+_declare("jn_lowrank_pair_backward_workspace_bytes", [_I64] * 7, _SZ)
+
 _declare("jn_unit_scale_forward", [_P, _I64, _I64, _F, _P, _P])
 _declare("jn_unit_scale_backward", [_P, _P, _I64, _I64, _F, _P, _P])
 
@@ -213,6 +228,14 @@ _SUPPORTED_OPS = (
     "transition_pairwise_topk",
     "transition_pairwise_dense",
     "low_rank_topk_select",
+    # the reference extension's raw edge ops (see the raw-op section below)
+    "softsign_backward_cuda",
+    "softmax_backward_cuda",
+    "query_topk_reduce_cuda",
+    "query_topk_reduce_backward_cuda",
+    "low_rank_propagation_topk_forward_cuda",
+    "low_rank_pairwise_topk_forward_cuda",
+    "low_rank_pairwise_topk_backward_cuda",
 )
 _ROUTE_COMPRESS_KINDS = {"softmax": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
 MAX_ROUTE_TOPK = 64  # below the destination count; every destination up to 64
@@ -1388,3 +1411,301 @@ def low_rank_topk_select(
             )
         )
     return idx, score
+
+
+# ---------------------------------------------------------------------------
+# Raw edge ops: the reference extension's *_cuda ops, which its Python
+# dispatcher composes into its own autograd functions
+# (src/jakal_net/native_backend.py:4002-4134 _LowRankPropagationQueryTopK,
+# 4408-4600 _LowRankTransitionPairwiseTopK; probed at 657-667 and 5962-5975).
+# Same names, argument order, shapes and return layouts
+# (native/jakal_net_native.cpp:140-189, 398-414, 449-477); index tensors are
+# int64 as there.  Outputs are fp32 accumulators except where the reference
+# returns the input dtype (query_topk_reduce_cuda, the forward deltas).
+# ---------------------------------------------------------------------------
+def _raw_f32(name: str, t: Tensor) -> Tensor:
+    if not t.is_floating_point():
+        raise RuntimeError(f"{name} must be a floating-point tensor.")
+    return t.float().contiguous()
+
+
+def _raw_index(name: str, t: Tensor, limit: int, distinct: bool = False) -> Tensor:
+    """int32 copy of an index tensor [..., k] whose entries lie in [-1, limit)
+    (-1: no edge) and, with `distinct`, name each node at most once per row
+    (the edge grouping of the backward ops keys its records by (row, node), as
+    top-k index rows are); anything else is refused here, before a kernel
+    could read out of bounds with it (one device-to-host read)."""
+    if t.dtype not in (torch.int64, torch.int32):
+        raise RuntimeError(f"{name} must use torch.long dtype.")
+    if limit >= 2**31:
+        raise NotImplementedError(f"{name}: node counts beyond 2^31 are not supported here.")
+    if t.numel():
+        lo, hi = torch.aminmax(t)
+        flags = [lo, hi]
+        if distinct and t.shape[-1] > 1:
+            srt = torch.sort(t, dim=-1).values
+            flags.append(((srt[..., 1:] == srt[..., :-1]) & (srt[..., 1:] >= 0)).any())
+        vals = torch.stack([f.to(torch.int64) for f in flags]).tolist()
+        if vals[0] < -1 or vals[1] >= limit:
+            raise RuntimeError(f"{name} must lie in [0, {limit}) (-1 for no edge); got [{vals[0]}, {vals[1]}].")
+        if len(vals) > 2 and vals[2]:
+            raise RuntimeError(f"{name} names a node twice in one row; rows of distinct nodes (top-k index rows) "
+                               "are supported.")
+    return t.to(torch.int32).contiguous()
+
+
+def _raw_dims(name: str, t: Tensor, dims: int) -> None:
+    if t.dim() != dims:
+        raise RuntimeError(f"{name} must have {dims} dimensions (got shape {tuple(t.shape)}).")
+
+
+def softsign_backward_cuda(scores: Tensor, grad_edges: Tensor) -> Tensor:
+    """grad_scores = grad_edges / (1 + |scores|)^2 (native/jakal_net_native_cuda.cu:3426-3453)."""
+    dev = _require_gpu(scores, grad_edges)
+    if scores.shape != grad_edges.shape:
+        raise RuntimeError("scores and grad_edges must share shape.")
+    s = _raw_f32("scores", scores)
+    g = _raw_f32("grad_edges", grad_edges)
+    out = torch.empty(s.shape, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        _check(_LIB.jn_softsign_backward(_ptr(s), _ptr(g), s.numel(), _ptr(out), _stream(dev)))
+    return out
+
+
+def softmax_backward_cuda(routes: Tensor, grad_routes: Tensor) -> Tensor:
+    """Softmax backward over the last axis of [batch, query_nodes, topk]:
+    grad = p (g - sum p g) (native/jakal_net_native_cuda.cu:3455-3483)."""
+    dev = _require_gpu(routes, grad_routes)
+    if routes.shape != grad_routes.shape or routes.dim() != 3:
+        raise RuntimeError("routes and grad_routes must be shaped [batch, query_nodes, topk].")
+    p = _raw_f32("routes", routes)
+    g = _raw_f32("grad_routes", grad_routes)
+    out = torch.empty(p.shape, device=dev, dtype=torch.float32)
+    rows, k = p.shape[0] * p.shape[1], p.shape[2]
+    if rows and k:
+        with torch.cuda.device(dev):
+            _check(_LIB.jn_softmax_backward(_ptr(p), _ptr(g), rows, k, _ptr(out), _stream(dev)))
+    return out
+
+
+def _edge_aggregate(index: Tensor, score: Tensor, compress: int, ps: Tensor, pv: Tensor):
+    B, Nq, k = score.shape
+    Ns, D = ps.shape[1], pv.shape[2]
+    dev = score.device
+    ds = torch.empty(B, Nq, device=dev, dtype=torch.float32)
+    dv = torch.empty(B, Nq, D, device=dev, dtype=torch.float32)
+    if B * Nq * k == 0 or Ns == 0:
+        return ds.zero_(), dv.zero_()
+    with torch.cuda.device(dev):
+        _check(_LIB.jn_edge_aggregate(_ptr(index), _ptr(score), B, Nq, Ns, k, D, compress, _ptr(ps), _ptr(pv),
+                                      _ptr(ds), _ptr(dv), _stream(dev)))
+    return ds, dv
+
+
+def _check_reduce_shapes(edges, indices, projected_state, projected_val):
+    _raw_dims("edges", edges, 3)
+    if indices.shape != edges.shape:
+        raise RuntimeError("indices must have the same shape as edges.")
+    _raw_dims("projected_state", projected_state, 2)
+    _raw_dims("projected_val", projected_val, 3)
+    if projected_state.shape[0] != edges.shape[0] or projected_val.shape[0] != edges.shape[0]:
+        raise RuntimeError("projected tensors must share the edge batch dimension.")
+    if projected_state.shape[1] != projected_val.shape[1]:
+        raise RuntimeError("projected_state and projected_val must share source_nodes.")
+
+
+def query_topk_reduce_cuda(edges: Tensor, indices: Tensor, projected_state: Tensor,
+                           projected_val: Tensor) -> tuple[Tensor, Tensor]:
+    """delta_state[b,i] = sum_e edges[b,i,e] ps[b,j], delta_val likewise over pv,
+    j = indices[b,i,e] (native/jakal_net_native_cuda.cu:2335-2418); outputs in
+    the projected tensors' dtype."""
+    dev = _require_gpu(edges, indices, projected_state, projected_val)
+    _check_reduce_shapes(edges, indices, projected_state, projected_val)
+    idx = _raw_index("indices", indices, projected_state.shape[1])
+    ds, dv = _edge_aggregate(idx, _raw_f32("edges", edges), 3, _raw_f32("projected_state", projected_state),
+                             _raw_f32("projected_val", projected_val))
+    return ds.to(projected_state.dtype), dv.to(projected_val.dtype)
+
+
+def query_topk_reduce_backward_cuda(edges: Tensor, indices: Tensor, projected_state: Tensor, projected_val: Tensor,
+                                    grad_delta_state: Tensor,
+                                    grad_delta_val: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(grad_edges, grad_projected_state, grad_projected_val) of query_topk_reduce_cuda
+    (native/jakal_net_native_cuda.cu:2112-2175, 3352-3424), fp32."""
+    dev = _require_gpu(edges, indices, projected_state, projected_val, grad_delta_state, grad_delta_val)
+    _check_reduce_shapes(edges, indices, projected_state, projected_val)
+    dtypes = {t.dtype for t in (edges, projected_state, projected_val, grad_delta_state, grad_delta_val)}
+    if len(dtypes) != 1:
+        raise RuntimeError("query_topk_reduce_backward_cuda inputs must share dtype.")
+    B, Nq, k = edges.shape
+    Ns, D = projected_state.shape[1], projected_val.shape[2]
+    if tuple(grad_delta_state.shape) != (B, Nq) or tuple(grad_delta_val.shape) != (B, Nq, D):
+        raise RuntimeError("grad_delta_state / grad_delta_val must be shaped [batch, query_nodes(, out_dim)].")
+    idx = _raw_index("indices", indices, Ns, distinct=True)
+    e, ps, pv = (_raw_f32(n, t) for n, t in (("edges", edges), ("projected_state", projected_state),
+                                              ("projected_val", projected_val)))
+    gs, gv = _raw_f32("grad_delta_state", grad_delta_state), _raw_f32("grad_delta_val", grad_delta_val)
+    g_edges = torch.empty(B, Nq, k, device=dev, dtype=torch.float32)
+    g_ps = torch.empty(B, Ns, device=dev, dtype=torch.float32)
+    g_pv = torch.empty(B, Ns, D, device=dev, dtype=torch.float32)
+    if B * Nq * k == 0:
+        return g_edges, g_ps.zero_(), g_pv.zero_()
+    with torch.cuda.device(dev):
+        ws_bytes = int(_LIB.jn_edge_reduce_backward_workspace_bytes(B, Nq, Ns, k))
+        if ws_bytes == 0:
+            raise NotImplementedError("query_topk_reduce_backward_cuda: edge list too large for the edge grouping.")
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        _check(_LIB.jn_edge_reduce_backward(_ptr(e), _ptr(idx), _ptr(ps), _ptr(pv), _ptr(gs), _ptr(gv), B, Nq, Ns, k,
+                                            D, _ptr(g_edges), _ptr(g_ps), _ptr(g_pv), _ptr(ws), ws_bytes,
+                                            _stream(dev)))
+    return g_edges, g_ps, g_pv
+
+
+def _raw_select(wps: Tensor, pt: Tensor, topk: int, score_bias: float, limit: int):
+    """Top-k of (wps[b,i] . pt[b,j] + bias) per row i, max over heads for
+    [batch, heads, nodes, rank] operands (cu:740-813, 881-930)."""
+    multihead = wps.dim() == 4 and pt.dim() == 4
+    if not multihead and (wps.dim() != 3 or pt.dim() != 3):
+        raise RuntimeError("weighted_projected_source and projected_target must be shaped [batch, nodes, rank] or "
+                           "[batch, heads, nodes, rank].")
+    if wps.shape[0] != pt.shape[0] or wps.shape[-1] != pt.shape[-1] or (multihead and wps.shape[1] != pt.shape[1]):
+        raise RuntimeError("weighted_projected_source and projected_target must share batch, heads and rank_dim.")
+    H = wps.shape[1] if multihead else 1
+    if multihead:  # heads innermost: [B, N, H * r]
+        q = wps.float().permute(0, 2, 1, 3).reshape(wps.shape[0], wps.shape[2], -1).contiguous()
+        kk = pt.float().permute(0, 2, 1, 3).reshape(pt.shape[0], pt.shape[2], -1).contiguous()
+    else:
+        q, kk = wps.float().contiguous(), pt.float().contiguous()
+    B, Nq, R = q.shape
+    Nk = kk.shape[1]
+    rh = R // H
+    if R > MAX_RANK or H > MAX_HEADS:
+        raise NotImplementedError(f"the HIP select takes up to {MAX_HEADS} heads and {MAX_RANK} ranks in all.")
+    if topk <= 0 or topk > limit:
+        raise RuntimeError(f"topk must be in the supported fused range [1, {limit}].")
+    k = min(int(topk), Nk)
+    dev = q.device
+    bias = torch.full((H,), float(score_bias), device=dev, dtype=torch.float32)
+    idx = torch.empty(B, Nq, k, device=dev, dtype=torch.int32)
+    score = torch.empty(B, Nq, k, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        ws_bytes = int(_LIB.jn_lowrank_topk_select_heads_workspace_bytes(B, Nk, rh, H))
+        ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+        _check(_LIB.jn_lowrank_topk_select_heads(_ptr(q), _ptr(kk), _ptr(bias), B, Nq, Nk, rh, H, k, _ptr(idx),
+                                                 _ptr(score), _ptr(ws), ws_bytes, _stream(dev)))
+    return idx, score
+
+
+def low_rank_propagation_topk_forward_cuda(weighted_projected_source: Tensor, projected_target: Tensor,
+                                           projected_state: Tensor, projected_val: Tensor, topk: int,
+                                           score_bias: float, compress_kind: int) -> tuple[Tensor, Tensor]:
+    """Each target row keeps its top-k sources by pt . wps, compresses
+    (score + bias) (0 softsign, 1 signed |s| softmax, 2 signed entmax-1.5) and
+    sums the chosen sources' projected state and values
+    (native/jakal_net_native_cuda.cu:1029-1175, 2545-2630); fp32 outputs."""
+    dev = _require_gpu(weighted_projected_source, projected_target, projected_state, projected_val)
+    if compress_kind not in (0, 1, 2):
+        raise RuntimeError("compress_kind must be 0 (softsign), 1 (signed_abs_softmax), or 2 (signed_entmax15).")
+    _raw_dims("projected_state", projected_state, 2)
+    _raw_dims("projected_val", projected_val, 3)
+    if projected_state.dtype != torch.float32 or projected_val.dtype != torch.float32:
+        raise RuntimeError("projected_state and projected_val must be float32 accumulators.")
+    Ns = weighted_projected_source.shape[-2]
+    if projected_state.shape[1] != Ns or projected_val.shape[1] != Ns:
+        raise RuntimeError("projected_state/projected_val must share source_nodes.")
+    # rows are the targets, keys the sources
+    idx, score = _raw_select(projected_target, weighted_projected_source, topk, score_bias, MAX_TOPK_LARGE)
+    return _edge_aggregate(idx, score, int(compress_kind), projected_state.contiguous(), projected_val.contiguous())
+
+
+def low_rank_pairwise_topk_forward_cuda(weighted_projected_source: Tensor, projected_target: Tensor,
+                                        weighted_projected_state: Tensor, weighted_projected_val: Tensor, topk: int,
+                                        score_bias: float,
+                                        compress_kind: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Each source row keeps its top-k destinations by wps . pt + bias, routes
+    them (0 softmax, 1 signed |s| softmax, 2 signed entmax-1.5) and sums the
+    weighted state and values per destination.  Returns (delta_state
+    [B, Nd], delta_val [B, Nd, D], scores [B, Ns, k], indices int64
+    [B, Ns, k]) (native/jakal_net_native_cuda.cu:740-878, 2420-2543)."""
+    dev = _require_gpu(weighted_projected_source, projected_target, weighted_projected_state,
+                       weighted_projected_val)
+    if compress_kind not in (0, 1, 2):
+        raise RuntimeError("compress_kind must be 0 (softmax), 1 (signed_abs_softmax), or 2 (signed_entmax15).")
+    if weighted_projected_state.dim() != 2 or weighted_projected_val.dim() != 3:
+        raise RuntimeError("weighted projected tensors must be shaped [batch, src_nodes] and "
+                           "[batch, src_nodes, out_dim].")
+    if weighted_projected_state.dtype != torch.float32 or weighted_projected_val.dtype != torch.float32:
+        raise RuntimeError("weighted projected state/val must be float32 accumulators.")
+    Ns = weighted_projected_source.shape[-2]
+    if weighted_projected_state.shape[1] != Ns or weighted_projected_val.shape[1] != Ns:
+        raise RuntimeError("weighted projected tensors must share src_nodes.")
+    idx, score = _raw_select(weighted_projected_source, projected_target, topk, score_bias, MAX_ROUTE_TOPK)
+    B, _, k = score.shape
+    Nd = projected_target.shape[-2]
+    D = weighted_projected_val.shape[2]
+    ws_state = weighted_projected_state.contiguous()
+    ws_val = weighted_projected_val.contiguous()
+    ds = torch.empty(B, Nd, device=dev, dtype=torch.float32)
+    dv = torch.empty(B, Nd, D, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        ws_bytes = int(_LIB.jn_route_topk_aggregate_workspace_bytes(B, Ns, Nd, k))
+        if ws_bytes == 0:
+            raise NotImplementedError("low_rank_pairwise_topk_forward_cuda: route list too large for the grouping.")
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        _check(_LIB.jn_route_topk_aggregate(_ptr(idx), _ptr(score), B, Ns, Nd, k, D, int(compress_kind),
+                                            _ptr(ws_state), _ptr(ws_val), _ptr(ds), _ptr(dv), _ptr(ws), ws_bytes,
+                                            _stream(dev)))
+    return ds, dv, score, idx.to(torch.int64)
+
+
+def low_rank_pairwise_topk_backward_cuda(query_val: Tensor, source_val: Tensor, source_weight: Tensor,
+                                         target_weight: Tensor, core_weight: Tensor, projected_query: Tensor,
+                                         projected_source: Tensor, indices: Tensor, grad_scores: Tensor,
+                                         temperature: float) -> tuple[Tensor, ...]:
+    """Gradients of the pair scores (Pq[i] * core) . Ps[j] / T + bias on the
+    edges (i, indices[b,i,e]): (grad_query, grad_source, grad_source_weight,
+    grad_target_weight, grad_core_weight, grad_bias), fp32, with grad_bias =
+    sum grad_scores / T as the reference computes it
+    (native/jakal_net_native_cuda.cu:2259-2322, 3792-3866).  query_val is
+    projected by target_weight, source_val by source_weight."""
+    dev = _require_gpu(query_val, source_val, source_weight, target_weight, core_weight, projected_query,
+                       projected_source, indices, grad_scores)
+    if temperature <= 0.0:
+        raise RuntimeError("temperature must be positive.")
+    for n, t, d in (("query_val", query_val, 3), ("source_val", source_val, 3), ("source_weight", source_weight, 2),
+                    ("target_weight", target_weight, 2), ("core_weight", core_weight, 1),
+                    ("projected_query", projected_query, 3), ("projected_source", projected_source, 3),
+                    ("indices", indices, 3), ("grad_scores", grad_scores, 3)):
+        _raw_dims(n, t, d)
+    B, Nq, Dq = query_val.shape
+    Ns, Ds = source_val.shape[1], source_val.shape[2]
+    r = core_weight.shape[0]
+    k = indices.shape[2]
+    if (tuple(target_weight.shape) != (r, Dq) or tuple(source_weight.shape) != (r, Ds)
+            or tuple(projected_query.shape) != (B, Nq, r) or tuple(projected_source.shape) != (B, Ns, r)
+            or tuple(indices.shape[:2]) != (B, Nq) or grad_scores.shape != indices.shape
+            or source_val.shape[0] != B):
+        raise RuntimeError("low_rank_pairwise_topk_backward_cuda: inconsistent shapes.")
+    _check_rank(r)
+    f32 = dict(device=dev, dtype=torch.float32)
+    if B * Nq * k == 0 or Ns == 0:
+        return (torch.zeros(B, Nq, Dq, **f32), torch.zeros(B, Ns, Ds, **f32), torch.zeros(r, Ds, **f32),
+                torch.zeros(r, Dq, **f32), torch.zeros(r, **f32), torch.zeros((), **f32))
+    idx = _raw_index("indices", indices, Ns, distinct=True)
+    xq, xs, ws_, wt, w, pq, ps, g = (_raw_f32(n, t) for n, t in (
+        ("query_val", query_val), ("source_val", source_val), ("source_weight", source_weight),
+        ("target_weight", target_weight), ("core_weight", core_weight), ("projected_query", projected_query),
+        ("projected_source", projected_source), ("grad_scores", grad_scores)))
+    g_q, g_s = torch.empty(B, Nq, Dq, **f32), torch.empty(B, Ns, Ds, **f32)
+    g_ws, g_wt = torch.empty(r, Ds, **f32), torch.empty(r, Dq, **f32)
+    g_w, g_b = torch.empty(r, **f32), torch.empty((), **f32)
+    with torch.cuda.device(dev):
+        ws_bytes = int(_LIB.jn_lowrank_pair_backward_workspace_bytes(B, Nq, Ns, Dq, Ds, r, k))
+        if ws_bytes == 0:
+            raise NotImplementedError("low_rank_pairwise_topk_backward_cuda: edge list too large for the grouping.")
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        _check(_LIB.jn_lowrank_pair_backward(_ptr(xq), _ptr(xs), _ptr(ws_), _ptr(wt), _ptr(w), _ptr(pq), _ptr(ps),
+                                             _ptr(idx), _ptr(g), float(temperature), B, Nq, Ns, Dq, Ds, r, k,
+                                             _ptr(g_q), _ptr(g_s), _ptr(g_ws), _ptr(g_wt), _ptr(g_w), _ptr(g_b),
+                                             _ptr(ws), ws_bytes, _stream(dev)))
+    return g_q, g_s, g_ws, g_wt, g_w, g_b

@@ -789,6 +789,9 @@ def main() -> int:
                     help="time eager steps only (default for the operator workloads: time replays of the step "
                          "captured into one HIP graph, torch.cuda.CUDAGraph, after timing the same number of "
                          "eager steps with per-kernel HIP events)")
+    ap.add_argument("--no-alone", action="store_true",
+                    help="skip the serial pass (side streams off) that times each kernel alone; for profiler "
+                         "runs that should see the timed steps only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of known size (scale for HBM byte counters)")
     args = ap.parse_args()
@@ -833,11 +836,11 @@ def main() -> int:
     # the same kernels once more with the side streams off: each kernel alone
     # (the timings above include the overlap of the two streams' kernels)
     jn.set_side_streams(False)
-    alone_steps = max(1, min(args.steps, 5))
+    alone_steps = 0 if args.no_alone else max(1, min(args.steps, 5))
     for _ in range(alone_steps):
         step()
     torch.cuda.synchronize()
-    prof_alone = jn.profile_collect()
+    prof_alone = jn.profile_collect() if alone_steps else {}
     jn.profile_enable(False)
     jn.set_side_streams(True)
     ms_per_step = eager_ms

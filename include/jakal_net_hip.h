@@ -108,7 +108,7 @@ int jn_set_select_mode(int32_t mode);
  *   s[b,i,j] = ((sum_r query[b,i,r]*cq[r] * key[b,j,r]*ck[r]) + bias) / temperature
  * where the scale vector multiplies the query rows when scale_on_query != 0,
  * else the key rows.  Writes the k best (j, s) per row, sorted descending,
- * ties toward the lower j.  1 <= k <= 64, k < nk, 1 <= rank <= 128.
+ * ties toward the lower j.  1 <= k <= 4096, k <= nk, 1 <= rank <= 128.
  * Replaces the score/select stage of
  *   propagation_topk            (native/jakal_net_native.cpp:6399-6424)
  *   low_rank_propagation_topk_forward_cuda (native/jakal_net_native_cuda.cu:1028-1110)
@@ -344,7 +344,7 @@ int jn_propagation_dense_backward_chunked(
  * projected_state [B,Ns], projected_val [B,Ns,Dv], Ws [r,Dsrc], Wt [r,Ddst],
  * w [r], bias scalar or NULL.  Outputs delta_state [B,Nd], delta_val [B,Nd,Dv],
  * and for the backward src_proj [B*Ns,r], dst_proj [B*Nd,r], route_index
- * [B,Ns,k] (int32) and route_logit [B,Ns,k].  k <= 64 when k < dst_nodes;
+ * [B,Ns,k] (int32) and route_logit [B,Ns,k].  k <= 4096 when k < dst_nodes;
  * k == dst_nodes <= 64 takes every destination.  Deterministic (the
  * destination sums are gathers over the edges grouped by destination).
  * Replaces transition_pairwise_topk (native/jakal_net_native.cpp:6916-7087) and
@@ -745,7 +745,7 @@ size_t jn_edge_reduce_backward_workspace_bytes(int64_t batch, int64_t query_node
 /*
  * Routes of a top-k transition and their destination sums:
  *   route[b,i,e] = compress(route_score[b,i,:])[e] (0 softmax, 1 signed |s|
- *   softmax, 2 signed entmax-1.5), k <= 64 per source;
+ *   softmax, 2 signed entmax-1.5), k <= 4096 per source;
  *   delta_state[b,j] = sum over routes into j of route * weighted_state[b,i];
  *   delta_val[b,j]   = sum over routes into j of route * weighted_val[b,i].
  * Each source's destinations must be distinct and in [0, dst_nodes) or -1

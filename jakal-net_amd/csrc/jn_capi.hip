@@ -302,10 +302,10 @@ int check_transition_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t Dsrc,
   JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
   JN_REQUIRE(topk >= 1, kInvalidArgument, "topk must be positive");
   const int64_t k = route_edges(topk, Nd);
-  JN_REQUIRE(k == Nd ? k <= 64 : k <= kSelectMaxK, kUnsupported,
+  JN_REQUIRE(k == Nd ? k <= 64 : k <= kSelectLargeMaxK, kUnsupported,
              "routes support topk <= %d below the destination count, or up to 64 destinations in all (topk=%lld, "
              "dst_nodes=%lld)",
-             kSelectMaxK, (long long)topk, (long long)Nd);
+             kSelectLargeMaxK, (long long)topk, (long long)Nd);
   JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported,
              "route compress kind must be 0 (softmax), 1 (signed_abs_softmax) or 2 (signed_entmax15), got %d",
              compress_kind);

@@ -313,8 +313,8 @@ int jn_route_topk_aggregate(const int32_t* route_index, const float* route_score
                             float* delta_val, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
   int rc = check_raw_edges(batch, src_nodes, dst_nodes, edges, dim);
   if (rc) return rc;
-  JN_REQUIRE(edges <= kWave, kUnsupported, "routes take up to %d edges per source (got %lld)", kWave,
-             (long long)edges);
+  JN_REQUIRE(edges <= kSelectLargeMaxK, kUnsupported, "routes take up to %d edges per source (got %lld)",
+             kSelectLargeMaxK, (long long)edges);
   JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported, "route compress kind must be 0, 1 or 2");
   JN_REQUIRE(route_index && route_score && weighted_state && weighted_val && delta_state && delta_val,
              kInvalidArgument, "null tensor pointer");

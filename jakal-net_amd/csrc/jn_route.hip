@@ -56,15 +56,68 @@ __global__ __launch_bounds__(256) void route_coef_kernel(const int32_t* idx, con
   if (lane < k) coef[row * k + lane] = rho ? rho[row] * p : p;
 }
 
+// ---- routes of more than 64 edges per source (up to kSelectLargeMaxK) -----
+// The rows run one wavefront each with loops over 64-edge blocks: the row's
+// statistics first, then the edges.
+// Statistics of a route row of any length: kind 0 a = max l, b = 1 / sum
+// exp(l - a); kinds 1 and 2 those of the signed edge compressions
+// (row_compress_stats: signed |l| softmax, signed entmax-1.5 of |l|).
+__device__ __forceinline__ RowStats route_row_stats(const int32_t* idx, const float* logit, int64_t row, int k,
+                                                    int kind) {
+  if (kind != 0) return row_compress_stats(idx, logit, row, k, kind);
+  const int lane = lane_id();
+  float m = -INFINITY;
+  for (int e = lane; e < k; e += kWave)
+    if (idx[row * k + e] >= 0) m = fmaxf(m, logit[row * k + e]);
+  m = wave_max_f(m);
+  float sum = 0.0f;
+  for (int e = lane; e < k; e += kWave)
+    if (idx[row * k + e] >= 0) sum += __expf(logit[row * k + e] - m);
+  sum = wave_sum(sum);
+  RowStats st;
+  st.a = m;
+  st.b = sum > 0.0f ? 1.0f / sum : 0.0f;
+  return st;
+}
+
+// Route probability of an edge (signed for kinds 1 and 2) from its row's
+// statistics; 0 for an absent edge.
+__device__ __forceinline__ float route_prob_row(int j, float l, int kind, const RowStats& st) {
+  if (j < 0) return 0.0f;
+  if (kind == 0) return __expf(l - st.a) * st.b;
+  if (kind == 1) return sign_f(l) * __expf(fabsf(l) - st.a) * st.b;
+  const float d = fmaxf(0.5f * (fabsf(l) - st.a) - st.b, 0.0f);
+  return st.c > 0.0f ? sign_f(l) * (d * d / st.c) : 0.0f;
+}
+
+__global__ __launch_bounds__(256) void route_coef_large_kernel(const int32_t* idx, const float* logit,
+                                                               const float* rho, int k, int kind, int64_t rows,
+                                                               float* coef) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  if (row >= rows) return;
+  const RowStats st = route_row_stats(idx, logit, row, k, kind);
+  const float rh = rho ? rho[row] : 1.0f;
+  for (int e = lane; e < k; e += kWave) {
+    const int j = idx[row * k + e];
+    coef[row * k + e] = rh * route_prob_row(j, j >= 0 ? logit[row * k + e] : 0.0f, kind, st);
+  }
+}
+
 int launch_route_coef(const int32_t* idx, const float* logit, const float* rho, int k, int compress, int64_t rows,
                       float* coef, hipStream_t stream) {
-  JN_REQUIRE(k >= 1 && k <= kWave, kUnsupported, "routes support 1..64 edges per source (got %d)", k);
+  JN_REQUIRE(k >= 1 && k <= kSelectLargeMaxK, kUnsupported, "routes support 1..%d edges per source (got %d)",
+             kSelectLargeMaxK, k);
   if (rows == 0) return kOk;
   const int64_t blocks = (rows + 3) / 4;
   JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
-  JN_PROFILE("route_coef_kernel", stream);
-  hipLaunchKernelGGL(route_coef_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, idx, logit, rho, k, compress,
-                     rows, coef);
+  JN_PROFILE(k > kWave ? "route_coef_large_kernel" : "route_coef_kernel", stream);
+  if (k > kWave)
+    hipLaunchKernelGGL(route_coef_large_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, idx, logit, rho, k,
+                       compress, rows, coef);
+  else
+    hipLaunchKernelGGL(route_coef_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, idx, logit, rho, k, compress,
+                       rows, coef);
   JN_LAUNCH_CHECK();
   return kOk;
 }
@@ -270,6 +323,151 @@ static void launch_route_bwd_kp(const RouteRowsBwdArgs& a, dim3 grid, hipStream_
 }
 
 // One 16-byte pack per lane and pass slice (W elements), NV slices per 16-lane group.
+// The row backward of route_rows_backward_kernel for rows of more than 64
+// edges.  Pass 1 (lane e of each 64-edge block): g_c = gds[j] ps + <gdv[j], pv>
+// into g_logit, with the row sums the compress backward needs; the value
+// gradient grad_pv = sum_e c_e gdv[j_e] (lanes over the columns); pass 2: the
+// compress backward into g_logit, the bias partials and dQ (lanes over the
+// ranks, the block's edges in turn).  T: element type of pv, gdv and grad_pv;
+// W: elements per load of the dot products (16 bytes, or 1).
+template <typename T, int W, bool MH>
+__global__ __launch_bounds__(256) void route_rows_backward_large_kernel(RouteRowsBwdArgs a) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  if (row >= a.rows) return;
+  const int64_t b = row / a.Ns;
+  const int k = a.k;
+  const int32_t* idxr = a.idx + row * k;
+  const float* lgr = a.logit + row * k;
+  float* glr = a.g_logit + row * k;  // g_c after pass 1, g_l after pass 2 (each lane its own slots)
+  const T* gdvb = reinterpret_cast<const T*>(a.gdv) + b * a.Nd * a.D;
+  const T* pvr = reinterpret_cast<const T*>(a.pv) + row * a.ld_pv;
+  const float* gdsb = a.gds + b * a.Nd;
+  const float ps_row = a.ps[row];
+  const float rho = a.rho[row];
+  const RowStats st = route_row_stats(a.idx, a.logit, row, k, a.compress);
+
+  float gps = 0.f, grho = 0.f, pg = 0.f, us = 0.f, gis = 0.f;
+  bool all_pos = true, all_neg = true;
+  for (int e0 = 0; e0 < k; e0 += kWave) {
+    const int e = e0 + lane;
+    const int j = e < k ? idxr[e] : -1;
+    const float l = j >= 0 ? lgr[e] : 0.f;
+    const float p = route_prob_row(j, l, a.compress, st);
+    float gc = 0.f;
+    if (j >= 0) {
+      const T* gv = gdvb + (int64_t)j * a.D;
+      float dot = 0.f;
+      for (int d = 0; d < a.D; d += W) {
+        const Pack<W> x = load_pack<T, W>(pvr + d), y = load_pack<T, W>(gv + d);
+#pragma unroll
+        for (int u = 0; u < W; ++u) dot += x.v[u] * y.v[u];
+      }
+      const float gd = gdsb[j];
+      gc = gd * ps_row + dot;
+      gps += rho * p * gd;
+    }
+    if (e < k) glr[e] = gc;
+    grho += p * gc;
+    const float gp = rho * gc;
+    if (a.compress == 2) {
+      const float u = sqrtf(fabsf(p));
+      us += u;
+      gis += gp * sign_f(l) * u;
+    } else {
+      pg += p * gp;
+    }
+    const uint64_t live = __ballot(j >= 0);
+    all_pos = all_pos && __ballot(j >= 0 && l > 0.f) == live;
+    all_neg = all_neg && __ballot(j >= 0 && l < 0.f) == live;
+  }
+  gps = wave_sum(gps);
+  grho = wave_sum(grho);
+  pg = wave_sum(pg);
+  us = wave_sum(us);
+  gis = wave_sum(gis);
+  const float corr = us > 0.f ? gis / us : 0.f;
+
+  if (a.grad_pv) {  // lanes over the columns, the row's edges in turn
+    T* out = reinterpret_cast<T*>(a.grad_pv) + row * a.ld_gpv;
+    for (int d = lane; d < a.D; d += kWave) {
+      float acc = 0.f;
+      for (int e = 0; e < k; ++e) {
+        const int j = idxr[e];
+        if (j < 0) continue;
+        acc += rho * route_prob_row(j, lgr[e], a.compress, st) * (float)gdvb[(int64_t)j * a.D + d];
+      }
+      out[d] = (T)acc;
+    }
+  }
+
+  const float* keyb = a.key + b * a.Nd * a.ldk;
+  float dq0 = 0.f, dq1 = 0.f, gsum = 0.f;
+  float hs[kMaxHeads];
+#pragma unroll
+  for (int h = 0; h < kMaxHeads; ++h) hs[h] = 0.f;
+  const int h0 = MH ? lane / a.head_rank : 0, h1 = MH ? (lane + kWave) / a.head_rank : 0;
+  for (int e0 = 0; e0 < k; e0 += kWave) {
+    const int e = e0 + lane;
+    const int j = e < k ? idxr[e] : -1;
+    const float l = j >= 0 ? lgr[e] : 0.f;
+    const float p = route_prob_row(j, l, a.compress, st);
+    const float gp = rho * (e < k ? glr[e] : 0.f);
+    const float sg = sign_f(l);
+    float gl;
+    if (a.compress == 0) {
+      gl = p * (gp - pg);
+    } else if (a.compress == 2) {
+      const float u = sqrtf(fabsf(p));
+      gl = (gp * sg * u - corr * u) * sg;
+    } else {
+      gl = sg * (sg * p) * (sg * gp - pg);
+    }
+    gl = j >= 0 ? gl * a.inv_temperature : 0.f;
+    if (e < k) glr[e] = gl;
+    const int eh = (MH && j >= 0) ? (int)a.ehead[row * k + e] : 0;
+    if constexpr (MH) {
+      for (int h = 0; h < a.heads; ++h) hs[h] += eh == h ? gl : 0.f;
+    } else {
+      gsum += gl;
+    }
+    const int ne = min(kWave, k - e0);
+    for (int q = 0; q < ne; ++q) {
+      const int jj = readlane_i(j, q);
+      if (jj < 0) continue;
+      const float gg = readlane_f(gl, q);
+      const int hq = MH ? readlane_i(eh, q) : 0;
+      const float* kr = keyb + (int64_t)jj * a.ldk;
+      if (lane < a.r && (!MH || h0 == hq)) dq0 += gg * kr[lane];
+      if (lane + kWave < a.r && (!MH || h1 == hq)) dq1 += gg * kr[lane + kWave];
+    }
+  }
+  float* dqrow = a.dq + row * a.lddq;
+  if (lane < a.r) dqrow[lane] = dq0 * (a.qscale ? a.qscale[lane] : 1.f);
+  if (lane + kWave < a.r) dqrow[lane + kWave] = dq1 * (a.qscale ? a.qscale[lane + kWave] : 1.f);
+  if constexpr (MH) {
+    for (int h = 0; h < a.heads; ++h) {  // uniform
+      const float t = wave_sum(hs[h]);
+      if (lane == 0) a.rowsum[row * a.heads + h] = t;
+    }
+  } else {
+    // one-sign rows of the signed compressions: exactly 0 (as the 64-edge kernel)
+    const float t = (a.compress != 0 && (all_pos || all_neg)) ? 0.f : wave_sum(gsum);
+    if (lane == 0) a.rowsum[row] = t;
+  }
+  if (lane == 0) {
+    if (a.grad_ps) a.grad_ps[row] = gps;
+    if (a.grad_rho) a.grad_rho[row] = grho;
+  }
+}
+
+template <typename T, bool MH>
+static void launch_route_bwd_large(const RouteRowsBwdArgs& a, bool vec, dim3 grid, hipStream_t stream) {
+  constexpr int W = 16 / (int)sizeof(T);
+  if (vec) hipLaunchKernelGGL((route_rows_backward_large_kernel<T, W, MH>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((route_rows_backward_large_kernel<T, 1, MH>), grid, dim3(256), 0, stream, a);
+}
+
 template <typename T, bool MH>
 static void launch_route_bwd(const RouteRowsBwdArgs& a, bool vec, dim3 grid, hipStream_t stream) {
   constexpr int W = 16 / (int)sizeof(T);  // passes of 512, 256, 128 (or 64) elements
@@ -283,7 +481,8 @@ static void launch_route_bwd(const RouteRowsBwdArgs& a, bool vec, dim3 grid, hip
 int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream) {
   if (a.rows == 0) return kOk;
   JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
-  JN_REQUIRE(a.k >= 1 && a.k <= kWave, kUnsupported, "routes support 1..64 edges per source (got %d)", a.k);
+  JN_REQUIRE(a.k >= 1 && a.k <= kSelectLargeMaxK, kUnsupported, "routes support 1..%d edges per source (got %d)",
+             kSelectLargeMaxK, a.k);
   JN_REQUIRE(a.compress >= 0 && a.compress <= 2, kUnsupported, "route compress kind must be 0, 1 or 2");
   const int64_t blocks = (a.rows + 3) / 4;
   JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
@@ -298,6 +497,18 @@ int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream) {
   const bool mh = a.heads > 1;
   JN_REQUIRE(!mh || (a.ehead && a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r),
              kInvalidArgument, "multi-head route backward needs edge heads and 2..%d heads of equal rank", kMaxHeads);
+  if (a.k > kWave) {
+    JN_PROFILE("route_rows_backward_large_kernel", stream);
+    if (a.bf16) {
+      if (mh) launch_route_bwd_large<bf16_t, true>(a, vec, grid, stream);
+      else launch_route_bwd_large<bf16_t, false>(a, vec, grid, stream);
+    } else {
+      if (mh) launch_route_bwd_large<float, true>(a, vec, grid, stream);
+      else launch_route_bwd_large<float, false>(a, vec, grid, stream);
+    }
+    JN_LAUNCH_CHECK();
+    return kOk;
+  }
   JN_PROFILE("route_rows_backward_kernel", stream);
   if (a.bf16) {
     if (mh) launch_route_bwd<bf16_t, true>(a, vec, grid, stream);

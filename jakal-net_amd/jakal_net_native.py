@@ -238,7 +238,7 @@ _SUPPORTED_OPS = (
     "low_rank_pairwise_topk_backward_cuda",
 )
 _ROUTE_COMPRESS_KINDS = {"softmax": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
-MAX_ROUTE_TOPK = 64  # below the destination count; every destination up to 64
+MAX_ROUTE_TOPK = 64  # routes over every destination (more run dense); the raw pairwise op's k range
 
 
 def supported_ops() -> list[str]:
@@ -858,8 +858,7 @@ def _check_select(k: int, limit: int = MAX_TOPK_LARGE) -> None:
     """A top-k select of k edges per row of any number of keys: the register
     select takes k <= MAX_TOPK of at most MAX_SELECT_KEYS keys (and multi-head
     scores of at most four 32-rank K-steps), the scored-rows select the rest up
-    to MAX_TOPK_LARGE; `limit` is the caller's own bound (routes keep up to
-    MAX_ROUTE_TOPK edges per source)."""
+    to MAX_TOPK_LARGE; `limit` is the caller's own bound."""
     if k > limit:
         raise NotImplementedError(f"the HIP top-k select keeps up to {limit} edges per row here (got {k}).")
 
@@ -1170,7 +1169,7 @@ def transition_pairwise_topk_routes(
     k = min(int(topk), Nd)
     _check_rank(source_weight.shape[0])
     if k < Nd:
-        _check_select(k, MAX_ROUTE_TOPK)
+        _check_select(k)
     elif Nd > MAX_ROUTE_TOPK:
         raise NotImplementedError("HIP sparse transition over every destination supports up to 64 destinations "
                                   "(transition_pairwise_topk runs more as the dense transition).")

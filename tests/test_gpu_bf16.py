@@ -103,10 +103,14 @@ def run_bf16_propagation(dev, mode, B, N, D, r, k=8, seed=5001):
     check_bf16_calibrated("grad projected_state", ps.grad, gr["ps"], t["ps"])
 
 
-def test_bf16_transition(dev):
+# min_ok: the fraction of rows whose k-th / (k+1)-th gap exceeds twice the bf16
+# score tolerance; at k = 80 of 200 destinations few do (the fp32 tests pin
+# those selections), so that case asserts only that some rows are checked.
+@pytest.mark.parametrize("Nd,k,min_ok", [(24, 4, 0.5), (200, 80, 0.03)])
+def test_bf16_transition(dev, Nd, k, min_ok):
     import jakal_net_native as jn
 
-    B, Ns, Nd, D, r, k = 2, 96, 24, 32, 8, 4
+    B, Ns, D, r = 2, 96, 32, 8
     g = torch.Generator().manual_seed(5002)
     src = torch.randn(B, Ns, D, generator=g).bfloat16()
     dst = torch.randn(B, Nd, D, generator=g).bfloat16()
@@ -126,7 +130,7 @@ def test_bf16_transition(dev):
     gdv = torch.randn(B, Nd, D, generator=g).bfloat16()
     torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
     logits, tol = bf16_select_scores(bf16_linear64(_np(src), _np(Ws)), bf16_linear64(_np(dst), _np(Wt)), _np(w))
-    assert check_selection(idx.cpu().numpy(), logit.cpu().numpy(), logits, k, gap=2 * tol, score_tol=tol) > 0.5
+    assert check_selection(idx.cpu().numpy(), logit.cpu().numpy(), logits, k, gap=2 * tol, score_tol=tol) > min_ok
     mask = O.mask_from_indices(idx.cpu().numpy(), Nd)
     rho_np = _np(rho)
     gr = O.transition_backward(_np(src), _np(dst), rho_np, _np(state), _np(src), _np(Ws), _np(Wt), _np(w), 0.0,

@@ -166,6 +166,7 @@ def _run_transition(dev, H, r, topk, kind, Ns, Nd, D, temperature, B=2, seed=520
     (4, 8, 12, "signed_abs_softmax", 50, 200, 0.8),
     (2, 8, 40, "softmax", 48, 40, 1.0),   # every destination (no select): heads from the all-keys scores
     (3, 40, 8, "signed_abs_softmax", 64, 90, 1.0),  # beyond the register select's K-steps: scored rows
+    (3, 8, 100, "signed_entmax15", 40, 250, 1.1),   # more than 64 routes per source
 ])
 def test_multihead_transition_matches_oracle(dev, H, r, topk, kind, Ns, Nd, T):
     _run_transition(dev, H, r, topk, kind, Ns, Nd, 24, T)

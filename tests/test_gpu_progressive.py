@@ -179,3 +179,63 @@ def test_progressive_step_graph_replay_matches_eager(dev, fused):
             assert torch.equal(p.data, w), f"replay {rep}: {name} differs by {float((p.data - w).abs().max()):.3e}"
         torch.randn(1 << 20, device=dev).sum()  # other eager work between replays
         torch.cuda.synchronize()
+
+
+def test_progressive_step_at_the_c5_size(dev):
+    """BASELINE config 5 at its stated size (vocab 16384, d 512, prefix 512,
+    64 query slots, 4 joint blocks, B_exp 256, B_cmp 64, top-k 16, rank 64,
+    batch 16) under bf16 autocast with a fused AdamW update: finite loss and
+    gradients on every parameter the loss reaches, the update applied to
+    every parameter with a non-zero gradient, and the step repeated from the
+    same parameters and optimizer state giving the same loss and update bit
+    for bit (the library sums in fixed orders).  The graph-capture check runs
+    at the reduced size above; bench.py captures this size itself."""
+    from jakal_net.progressive import ProgressiveBConfig, ProgressiveBStep
+
+    cfg = ProgressiveBConfig(vocab=16384, dim=512, prefix=512, query=64, rank=64, topk=16, blocks=4, expanded=256,
+                             compressed=64, s_window=32)
+    torch.manual_seed(1005)
+    model = ProgressiveBStep(cfg, implementation="native").to(dev)
+    g = torch.Generator().manual_seed(1005)
+    prefix = torch.randint(0, cfg.vocab - 1, (16, cfg.prefix), generator=g).to(dev)
+    target = torch.randint(0, cfg.vocab - 1, (16, cfg.query), generator=g).to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            loss = model(prefix, target)
+        loss.backward()
+        opt.step()
+        return loss.detach()
+
+    step()  # optimizer state exists from here on
+    torch.cuda.synchronize()
+    tensors = [p.data for p in model.parameters()]
+    for st in opt.state.values():
+        tensors += [v for v in st.values() if torch.is_tensor(v)]
+    snapshot = [t.clone() for t in tensors]
+    before = [p.detach().clone() for p in model.parameters()]
+    loss = step()
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(loss)), f"loss {float(loss)}"
+    # a freshly initialised head over 16384 tokens starts near log(vocab)
+    assert abs(float(loss) - float(np.log(cfg.vocab))) < 2.0, float(loss)
+    reached = {n for n, p in model.named_parameters() if p.grad is not None}
+    assert reached == {n for n, _ in model.named_parameters()} - _unused(model)
+    for n, p in model.named_parameters():
+        if p.grad is not None:
+            assert bool(torch.isfinite(p.grad).all()), f"non-finite gradient in {n}"
+    # every parameter with a non-zero gradient moved (zero-initialised ones whose
+    # gradient is exactly 0, e.g. the bias of one-sign signed routes, stay put)
+    stuck = [n for (n, p), b in zip(model.named_parameters(), before)
+             if p.grad is not None and bool((p.grad != 0).any()) and torch.equal(p.detach(), b)]
+    assert not stuck, f"parameters with gradients that the update did not change: {stuck}"
+    want = [p.data.clone() for p in model.parameters()]
+    for t, v in zip(tensors, snapshot):
+        t.copy_(v)
+    again = step()
+    torch.cuda.synchronize()
+    assert torch.equal(again, loss), f"repeated step: loss {float(again)} != {float(loss)}"
+    for (name, p), w in zip(model.named_parameters(), want):
+        assert torch.equal(p.data, w), f"repeated step: {name} differs by {float((p.data - w).abs().max()):.3e}"

@@ -119,6 +119,19 @@ def test_transition_topk_above_32(dev, kind):
     _run(dev, 3004, B=2, Ns=80, Nd=100, Dsrc=16, Ddst=12, r=4, topk=48, temperature=1.1, kind=kind)
 
 
+@pytest.mark.parametrize("kind", ["softmax", "signed_abs_softmax", "signed_entmax15"])
+def test_transition_topk_above_64(dev, kind):
+    """More than 64 destinations per source: the scored-rows select and the
+    route kernels' 64-edge blocks."""
+    _run(dev, 3006, B=2, Ns=40, Nd=300, Dsrc=16, Ddst=12, r=6, topk=100, temperature=1.2, kind=kind)
+
+
+def test_transition_topk_above_64_odd_rows(dev):
+    # value rows of 10 elements (no 16-byte packs), no bias
+    _run(dev, 3007, B=2, Ns=33, Nd=150, Dsrc=9, Ddst=10, r=3, topk=70, temperature=0.9, kind="signed_abs_softmax",
+         with_bias=False)
+
+
 @pytest.mark.parametrize("topk", [16, 40])
 def test_transition_every_destination(dev, topk):
     # k >= Nd keeps every destination (transition.py:437-440)

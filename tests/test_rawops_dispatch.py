@@ -115,9 +115,9 @@ def test_raw_op_entry_points_validate_before_any_device_call():
     rc = lib.jn_lowrank_pair_backward(None, None, None, None, None, None, None, None, None, 0.0, 1, 8, 8, 4, 4, 8,
                                       2, None, None, None, None, None, None, None, 0, None)
     assert rc != 0 and b"temperature" in lib.jn_last_error()
-    # routes keep at most 64 destinations per source
-    rc = lib.jn_route_topk_aggregate(None, None, 1, 8, 100, 65, 4, 0, None, None, None, None, None, 0, None)
-    assert rc != 0 and b"64" in lib.jn_last_error()
+    # routes keep at most 4096 destinations per source
+    rc = lib.jn_route_topk_aggregate(None, None, 1, 8, 10000, 5000, 4, 0, None, None, None, None, None, 0, None)
+    assert rc != 0 and b"4096" in lib.jn_last_error()
     rc = lib.jn_edge_aggregate(None, None, 1, 8, 8, 2, 4, 5, None, None, None, None, None)
     assert rc != 0 and b"compress" in lib.jn_last_error()
     # empty inputs need no launch

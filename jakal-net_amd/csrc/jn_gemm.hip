@@ -1183,6 +1183,259 @@ static bool bf16_path_ok(const GemmArgs& g, int use, int splits) {
   return false;
 }
 
+// ---- fp32 products as three-term bf16 splits --------------------------------
+// An fp32 value x splits exactly into three bf16 terms x = h + m + l: h is x
+// truncated to bf16 (sign, exponent, 7 fraction bits); r = x - h (exact: the
+// 16 low significand bits of x) splits the same way into m and l = r - m, which
+// has at most 8 significant bits and so is a bf16 value.  A product a.b is
+// taken as the six terms h.h + h.m + m.h + h.l + l.h + m.m, each exact in fp32,
+// on v_mfma_f32_16x16x32_bf16 with fp32 accumulation; the three dropped terms
+// (m.l, l.m, l.l) stay below 2^-23 |a b| together, about one fp32 rounding of
+// the product.  Six 16-cycle bf16 MFMAs per 16 x 16 x 32 block replace eight
+// 32-cycle fp32 ones.
+//
+// gemm_x3_kernel is gemm_bf16_kernel for fp32 operands in this form: the three
+// planes of both operands sit in LDS as [row][k] bf16, K in slices of 32, in
+// one LDS buffer (61 KB, 70 KB with the epilogue's strips: two workgroups per
+// CU) refilled from registers that prefetch the next slice, split on their way
+// into LDS; each slice's operand resources start at the slice, so 32-bit
+// offsets cover any K.  Used for the projection and its gradients and for the
+// dense aggregation E.pv and its value gradient E^T.gdv (causal K ranges
+// included) when the 128 x 128 tiles apply (x3_path_ok); jn_set_gemm_tile(128)
+// keeps them on fp32 MFMA.
+constexpr int kX3K = 32;                 // K per slice
+constexpr int kX3S = kX3K + 8;           // LDS row stride in bf16 elements (80 bytes: conflict-free fragments)
+constexpr int kX3Plane = kBfT * kX3S;    // one plane of one operand
+
+__device__ __forceinline__ void x3_split(uint32_t u, uint32_t& h, uint32_t& m, uint32_t& l) {
+  h = u & 0xFFFF0000u;
+  const float r = __uint_as_float(u) - __uint_as_float(h);
+  m = __float_as_uint(r) & 0xFFFF0000u;
+  l = __float_as_uint(r - __uint_as_float(m));
+}
+
+// the bf16 values in the high halves of two words as one bf16x2 word (first in the low half)
+__device__ __forceinline__ uint32_t x3_pair(uint32_t first, uint32_t second) {
+  return __builtin_amdgcn_perm(second, first, 0x07060302u);  // bytes 2, 3 of first, then of second
+}
+
+// Operand loader of one slice: 128 rows (m or n) x 32 k of fp32 into the three
+// LDS planes [row][k].  KC: rows with k contiguous (row stride ld); else k rows
+// of stride ld.  `base` addresses the slice's (row 0, k 0).
+template <bool KC>
+struct X3Loader {
+  uint4 r[4];
+
+  // rs1 serves the rows from split_row on (KC only, a multiple of 8: one wave's
+  // load never straddles it)
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs0, __amdgpu_buffer_rsrc_t rs1, int split_row, int ld,
+                                       int row0, int rows, int k0, int kend, int tid) {
+    if constexpr (KC) {  // 128 rows x 8 groups of 4 k
+      const int wbase = tid & ~63;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = tid + 256 * u, row = e >> 3, kq = (e & 7) * 4;
+        const bool ok = row0 + row < rows && k0 + kq < kend;
+        const auto rs = ((wbase + 256 * u) >> 3) < split_row ? rs0 : rs1;
+        r[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rs, ok ? (uint32_t)(row * ld + kq) * 4u : kOobOffset, 0, 0));
+      }
+    } else {  // 8 groups of 4 k x 32 groups of 4 rows: one 4 x 4 block per thread
+      const int kb = tid >> 5, rb = (tid & 31) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kk = 4 * kb + i;
+        const bool ok = k0 + kk < kend && row0 + rb < rows;
+        r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rs0, ok ? (uint32_t)(kk * ld + rb) * 4u : kOobOffset, 0, 0));
+      }
+    }
+  }
+
+  // planes h, m, l at s, s + kX3Plane, s + 2 kX3Plane
+  __device__ __forceinline__ void store(bf16_t* s, int tid) const {
+    if constexpr (KC) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = tid + 256 * u, row = e >> 3, kq = (e & 7) * 4;
+        uint32_t h[4], m[4], l[4];
+        x3_split(r[u].x, h[0], m[0], l[0]);
+        x3_split(r[u].y, h[1], m[1], l[1]);
+        x3_split(r[u].z, h[2], m[2], l[2]);
+        x3_split(r[u].w, h[3], m[3], l[3]);
+        bf16_t* d = &s[row * kX3S + kq];
+        *reinterpret_cast<uint2*>(d) = make_uint2(x3_pair(h[0], h[1]), x3_pair(h[2], h[3]));
+        *reinterpret_cast<uint2*>(d + kX3Plane) = make_uint2(x3_pair(m[0], m[1]), x3_pair(m[2], m[3]));
+        *reinterpret_cast<uint2*>(d + 2 * kX3Plane) = make_uint2(x3_pair(l[0], l[1]), x3_pair(l[2], l[3]));
+      }
+    } else {
+      // r[i] holds k = 4 kb + i, rows rb .. rb + 3
+      const int kb = tid >> 5, rb = (tid & 31) * 4;
+      const uint32_t c[4][4] = {{r[0].x, r[0].y, r[0].z, r[0].w}, {r[1].x, r[1].y, r[1].z, r[1].w},
+                                {r[2].x, r[2].y, r[2].z, r[2].w}, {r[3].x, r[3].y, r[3].z, r[3].w}};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t h[4], m[4], l[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x3_split(c[i][j], h[i], m[i], l[i]);
+        bf16_t* d = &s[(rb + j) * kX3S + 4 * kb];
+        *reinterpret_cast<uint2*>(d) = make_uint2(x3_pair(h[0], h[1]), x3_pair(h[2], h[3]));
+        *reinterpret_cast<uint2*>(d + kX3Plane) = make_uint2(x3_pair(m[0], m[1]), x3_pair(m[2], m[3]));
+        *reinterpret_cast<uint2*>(d + 2 * kX3Plane) = make_uint2(x3_pair(l[0], l[1]), x3_pair(l[2], l[3]));
+      }
+    }
+  }
+};
+
+template <bool A_KC, bool B_KC, int USE>
+__global__ __launch_bounds__(256, 2) void gemm_x3_kernel(GemmArgs g, int tiles_m, int tiles_n) {
+  // [A, B][plane] (61 KB), or the epilogue's four 64-row strips (70 KB)
+  constexpr int kWords = 4 * 64 * kBfStage > 3 * kX3Plane ? 4 * 64 * kBfStage : 3 * kX3Plane;
+  __shared__ __align__(16) uint32_t smem32[kWords];
+  bf16_t* smem = reinterpret_cast<bf16_t*>(smem32);
+  auto sA = [&](int) { return smem; };
+  auto sB = [&](int) { return smem + 3 * kX3Plane; };
+
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int wm = wave >> 1, wn = wave & 1;
+  const int grp = lane >> 4, col = lane & 15;
+
+  // logical tile: contiguous ranges per XCD, bands of 8 M-tiles sweeping N
+  const int id = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int per = tiles_m * tiles_n;
+  const int z = id / per, t = id - z * per;
+  constexpr int kBand = 8;
+  const int band = t / (kBand * tiles_n);
+  const int bm = min(kBand, tiles_m - band * kBand);
+  const int tb = t - band * kBand * tiles_n;
+  int mi = band * kBand + tb % bm;
+  if (g.causal_k == kCausalKLower) mi = tiles_m - 1 - mi;  // longest K ranges first
+  const int m0 = mi * kBfT;
+  const int n0 = (tb / bm) * kBfT;
+  const bool batched = g.batch > 1;
+  const int split = batched ? 0 : z;
+  const int64_t bz = batched ? z : 0;
+  int kbeg = split * g.k_chunk;
+  int kend = min(g.K, kbeg + g.k_chunk);
+  causal_k_range<kBfT>(g, m0, n0, kbeg, kend);
+  const int lda = (int)g.lda, ldb = (int)g.ldb;
+  const float* gA = g.A + bz * g.a_bs;
+  const float* gB0 = g.B0 + bz * g.b_bs;
+  const float* gB1 = g.B1 + bz * g.b_bs;
+
+  X3Loader<A_KC> la;
+  X3Loader<B_KC> lb;
+  auto load_slice = [&](int k0) {
+    const auto ars = make_rsrc(gA + (A_KC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0), kFastRecords);
+    la.load(ars, ars, 1 << 30, lda, m0, g.M, k0, kend, tid);
+    if constexpr (B_KC) {  // B0 rows below b_split, B1 from there (along n)
+      const auto b0 = make_rsrc(gB0 + (int64_t)n0 * ldb + k0, kFastRecords);
+      const auto b1 = make_rsrc(gB1 + (int64_t)(n0 - g.b_split) * ldb + k0, kFastRecords);
+      lb.load(b0, b1, g.b_split - n0, ldb, n0, g.N, k0, kend, tid);
+    } else {  // along k: whole slices (the host keeps b_split a multiple of kX3K)
+      const bool second = k0 >= g.b_split;
+      const auto b = make_rsrc(second ? gB1 + (int64_t)(k0 - g.b_split) * ldb + n0 : gB0 + (int64_t)k0 * ldb + n0,
+                               kFastRecords);
+      lb.load(b, b, 1 << 30, ldb, n0, g.N, k0, second ? kend : min(kend, g.b_split), tid);
+    }
+  };
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int nslices = kend > kbeg ? (kend - kbeg + kX3K - 1) / kX3K : 0;
+  if (nslices > 0) {
+    load_slice(kbeg);
+    la.store(sA(0), tid);
+    lb.store(sB(0), tid);
+  }
+  __syncthreads();
+  for (int s = 0; s < nslices; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < nslices) load_slice(kbeg + (s + 1) * kX3K);
+    const bf16_t* a = sA(cur) + (wm * 64 + col) * kX3S + grp * 8;
+    const bf16_t* b = sB(cur) + (wn * 64 + col) * kX3S + grp * 8;
+    bf16x8v ah[4], am[4], al[4], bh[4], bm[4], bl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ah[i] = *reinterpret_cast<const bf16x8v*>(a + i * 16 * kX3S);
+      am[i] = *reinterpret_cast<const bf16x8v*>(a + i * 16 * kX3S + kX3Plane);
+      al[i] = *reinterpret_cast<const bf16x8v*>(a + i * 16 * kX3S + 2 * kX3Plane);
+      bh[i] = *reinterpret_cast<const bf16x8v*>(b + i * 16 * kX3S);
+      bm[i] = *reinterpret_cast<const bf16x8v*>(b + i * 16 * kX3S + kX3Plane);
+      bl[i] = *reinterpret_cast<const bf16x8v*>(b + i * 16 * kX3S + 2 * kX3Plane);
+    }
+    // the small terms first
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        floatx4 c = acc[mt][nt];
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[mt], bh[nt], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[mt], bl[nt], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am[mt], bm[nt], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am[mt], bh[nt], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[mt], bm[nt], c, 0, 0, 0);
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[mt], bh[nt], c, 0, 0, 0);
+      }
+    __syncthreads();  // the slice is consumed: the next one replaces it
+    if (s + 1 < nslices) {
+      la.store(sA(cur ^ 1), tid);
+      lb.store(sB(cur ^ 1), tid);
+      __syncthreads();
+    }
+  }
+
+  // epilogue: each wave's 64 x 64 block through LDS, then rows of 8 elements
+  float* stage = reinterpret_cast<float*>(smem) + wave * 64 * kBfStage;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) stage[(mt * 16 + grp * 4 + v) * kBfStage + nt * 16 + col] = acc[mt][nt][v];
+  __syncthreads();
+  float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
+  const float* add = g.addend ? g.addend + bz * g.add_bs : nullptr;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int r = it * 8 + (lane >> 3), c0 = (lane & 7) * 8;
+    const int m = m0 + wm * 64 + r, n = n0 + wn * 64 + c0;
+    if (m >= g.M || n >= g.N) continue;
+    float4 x0 = *reinterpret_cast<const float4*>(&stage[r * kBfStage + c0]);
+    float4 x1 = *reinterpret_cast<const float4*>(&stage[r * kBfStage + c0 + 4]);
+    if (add) {
+      const float4 a0 = *reinterpret_cast<const float4*>(&add[(int64_t)m * g.ld_add + n]);
+      const float4 a1 = *reinterpret_cast<const float4*>(&add[(int64_t)m * g.ld_add + n + 4]);
+      x0.x += a0.x; x0.y += a0.y; x0.z += a0.z; x0.w += a0.w;
+      x1.x += a1.x; x1.y += a1.y; x1.z += a1.z; x1.w += a1.w;
+    }
+    *reinterpret_cast<float4*>(&C[(int64_t)m * g.ldc + n]) = x0;
+    *reinterpret_cast<float4*>(&C[(int64_t)m * g.ldc + n + 4]) = x1;
+  }
+}
+
+// Whether an fp32 projection use runs on gemm_x3_kernel (its preconditions).
+static bool x3_path_ok(const GemmArgs& g, int use, int splits) {
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (g.M < kBfT || g.N < kBfT || g.N % 8 != 0 || g.ldc % 4 != 0 || g.lda % 4 != 0 || g.ldb % 4 != 0) return false;
+  if (g.a_bs % 4 != 0 || g.b_bs % 4 != 0 || g.c_bs % 4 != 0 || g.c_split_stride % 4 != 0) return false;
+  if (g.lda >= (1 << 20) || g.ldb >= (1 << 20)) return false;
+  if (!al16(g.A) || !al16(g.B0) || !al16(g.B1) || !al16(g.C)) return false;
+  if (g.addend && (g.ld_add % 4 != 0 || g.add_bs % 4 != 0 || !al16(g.addend))) return false;
+  if (g.a_kscale || g.c_nscale || g.c_mscale || g.epi || g.fold || g.a_heads) return false;
+  if (splits > 1 && g.k_chunk % kX3K != 0) return false;
+  if (use == kGemmProject) return g.K % 4 == 0 && g.b_split % 16 == 0;               // both K-contiguous
+  if (use == kGemmGradInput) return g.K % 4 == 0 && g.b_split % kX3K == 0;            // B K-major, split along k
+  if (use == kGemmGradWeight) return g.M % 4 == 0 && g.b_split >= g.K;               // both K-major
+  if (use == kGemmDenseAggregate) return g.K % 4 == 0 && g.b_split >= g.K;           // E . pv
+  if (use == kGemmDenseValueGrad) return g.M % 4 == 0 && g.b_split >= g.K;           // E^T . gdv
+  return false;
+}
+
 // Sum split-K partials in a fixed order; rows < m_split go to out0, the rest to out1.
 // out = sum over splits of part[z] (fixed order).  A workgroup owns 64
 // consecutive outputs; wave w sums splits z = w, w + 4, ... for its lane's
@@ -1306,6 +1559,45 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
     JN_LAUNCH_CHECK();
     return kOk;
   }
+  if ((use == kGemmProject || use == kGemmGradInput || use == kGemmGradWeight || use == kGemmDenseAggregate ||
+       use == kGemmDenseValueGrad) &&
+      forced == 0 && x3_path_ok(g, use, splits)) {
+    const int tm = (g.M + kBfT - 1) / kBfT, tn = (g.N + kBfT - 1) / kBfT;
+    const int64_t blocks = (int64_t)tm * tn * zdim;
+    JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "GEMM grid too large");
+    const dim3 grid((unsigned)blocks);
+    switch (use) {
+      case kGemmProject: {
+        JN_PROFILE("gemm_x3_kernel<project>", stream);
+        hipLaunchKernelGGL((gemm_x3_kernel<true, true, kGemmProject>), grid, dim3(256), 0, stream, g, tm, tn);
+        break;
+      }
+      case kGemmGradInput: {
+        JN_PROFILE("gemm_x3_kernel<grad_input>", stream);
+        hipLaunchKernelGGL((gemm_x3_kernel<true, false, kGemmGradInput>), grid, dim3(256), 0, stream, g, tm, tn);
+        break;
+      }
+      case kGemmGradWeight: {
+        JN_PROFILE("gemm_x3_kernel<grad_weight>", stream);
+        hipLaunchKernelGGL((gemm_x3_kernel<false, false, kGemmGradWeight>), grid, dim3(256), 0, stream, g, tm, tn);
+        break;
+      }
+      case kGemmDenseAggregate: {
+        JN_PROFILE("gemm_x3_kernel<dense_aggregate>", stream);
+        hipLaunchKernelGGL((gemm_x3_kernel<true, false, kGemmDenseAggregate>), grid, dim3(256), 0, stream, g, tm,
+                           tn);
+        break;
+      }
+      default: {
+        JN_PROFILE("gemm_x3_kernel<dense_value_grad>", stream);
+        hipLaunchKernelGGL((gemm_x3_kernel<false, false, kGemmDenseValueGrad>), grid, dim3(256), 0, stream, g, tm,
+                           tn);
+        break;
+      }
+    }
+    JN_LAUNCH_CHECK();
+    return kOk;
+  }
   JN_PROFILE(info.name, stream);
   switch (use) {
     case kGemmProject: launch_use<kGemmProject>(g, fast, small, (int)zdim, stream); break;
@@ -1405,9 +1697,12 @@ int gemm_grad_input(const float* dP, int64_t ldp, const float* W0, const float* 
   return launch_gemm(g, x_bf16 ? kGemmGradInputBf16 : kGemmGradInput, 1, stream);
 }
 
+// Split-K of the weight gradients: enough chunks for two workgroups per CU
+// over a few 128 x 128 output tiles.
+static int grad_weight_splits(int K) { return K >= 32768 ? 128 : (K >= 4096 ? 64 : (K >= 512 ? 8 : 1)); }
+
 size_t gemm_grad_weight_workspace(int M, int N, int K) {
-  int splits = K >= 4096 ? 64 : (K >= 512 ? 8 : 1);
-  return (size_t)splits * M * N * sizeof(float);
+  return (size_t)grad_weight_splits(K) * M * N * sizeof(float);
 }
 
 // dW[M][N] = dP^T . X with dP [K][M] (row stride ldp), X [K][N] (row stride ldx).
@@ -1415,10 +1710,11 @@ size_t gemm_grad_weight_workspace(int M, int N, int K) {
 // x_bf16: X holds bf16 elements.
 int gemm_grad_weight(const float* dP, int64_t ldp, const float* X, int64_t ldx, float* out0, float* out1, int m_split,
                      int M, int N, int K, float* partial, hipStream_t stream, bool x_bf16) {
-  int splits = K >= 4096 ? 64 : (K >= 512 ? 8 : 1);
+  int splits = grad_weight_splits(K);
   int k_chunk = (K + splits - 1) / splits;
-  // chunks of whole K slices: 16 (fp32 kernels), 64 (the bf16 MFMA kernel)
-  const int kq = x_bf16 ? kBfK : kGBK;
+  // chunks of whole K slices: 32 (the fp32 kernels' 16, gemm_x3_kernel's 32), 64 (the bf16 MFMA kernel)
+  static_assert(kX3K % kGBK == 0 && kX3K % kFastBK == 0, "fp32 split-K chunks serve every fp32 kernel");
+  const int kq = x_bf16 ? kBfK : kX3K;
   k_chunk = (k_chunk + kq - 1) / kq * kq;
   GemmArgs g{};
   g.A = dP; g.lda = ldp;

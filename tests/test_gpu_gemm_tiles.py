@@ -1,4 +1,6 @@
-"""Every GEMM workgroup tile (32 x 32, 64 x 64 and 128 x 128) against the oracle.
+"""Every GEMM workgroup tile (32 x 32, 64 x 64 and 128 x 128) and the automatic
+choice (0: the fp32 projection GEMMs of 128+ extents on bf16 thirds) against
+the oracle.
 
 The library picks the tile per call from the output extents; these tests force
 each tile in turn (jn_set_gemm_tile; 32 applies to the projection products and
@@ -28,7 +30,7 @@ import test_gpu_window as TW
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=[32, 64, 128])
+@pytest.fixture(params=[0, 32, 64, 128])
 def tile(request):
     assert torch.cuda.is_available(), "GPU tests need a HIP device"
     import jakal_net_native as jn
@@ -101,3 +103,14 @@ def test_bf16_layers(dev, tile, mode):
     # GEMMs; rank 16 splits the weight operands at a multiple of 16, so the
     # 128 x 128 kernel takes all three uses when forced
     TB.run_bf16_propagation(dev, mode, B=2, N=160, D=40, r=16, k=8, seed=5003)
+
+
+@pytest.mark.parametrize("D,r,separate_pv", [(136, 64, True), (512, 64, False), (200, 96, True)])
+def test_fp32_projection_gemms_in_bf16_thirds(dev, D, r, separate_pv):
+    """The automatic choice (tile 0) runs the fp32 projection, input-gradient
+    and weight-gradient GEMMs with extents of 128 and more on gemm_x3_kernel
+    (each fp32 operand split exactly into three bf16 terms, six bf16 MFMA
+    products): ragged K (D = 136, 200) and N tails, the addend of grad X when
+    pv is X, split-K over the rows; the fp32 tolerance of the per-op tests."""
+    TT._run_topk(dev, TT._c1_inputs(seed=4500 + D, B=2, N=640, D=D, r=r), "softsign", separate_pv, 16,
+                 min_checkable=0.5)

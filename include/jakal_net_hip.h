@@ -7,7 +7,7 @@
  * `stream`; none allocates device memory (scratch comes in through
  * `workspace`, sized by the matching *_workspace_bytes query).  Edge-list
  * backward passes, top-k forwards that build an edge layout, and top-k
- * transitions on at least 2^20 edges run part of their work on a
+ * transitions on at least 2^18 edges run part of their work on a
  * library-owned side stream (one per host thread and device,
  * created on first use outside graph capture), forked from and joined back to
  * `stream` by events inside the call: work ordered after the call on `stream`

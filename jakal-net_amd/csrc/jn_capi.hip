@@ -57,7 +57,7 @@ SideStream* side_stream(hipStream_t origin) {
 
 // Forking pays only when each branch has work enough to hide the extra event
 // nodes (on small problems they cost more than the overlap gains).
-constexpr int64_t kSideMinEdges = 1 << 20;
+constexpr int64_t kSideMinEdges = 1 << 18;
 static std::atomic<int> g_side_streams{1};
 const SideStream* side_stream_for(hipStream_t origin, int64_t edges) {
   if (g_side_streams.load(std::memory_order_relaxed) == 0) return nullptr;

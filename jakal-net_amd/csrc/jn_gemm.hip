@@ -1202,7 +1202,11 @@ static bool bf16_path_ok(const GemmArgs& g, int use, int splits) {
 // offsets cover any K.  Used for the projection and its gradients and for the
 // dense aggregation E.pv and its value gradient E^T.gdv (causal K ranges
 // included) when the 128 x 128 tiles apply (x3_path_ok); jn_set_gemm_tile(128)
-// keeps them on fp32 MFMA.
+// keeps them on fp32 MFMA.  Measured against float64, the bf16 MFMA's
+// accumulation leans slightly negative (of order 2^-33 of the accumulator per
+// instruction): harmless per element, but summed over the 16.8M score
+// gradients of C4's dense bias gradient it left the fp32 tolerance (3.6 of
+// 1.6e4), so the score-gradient product gdv.pv^T stays on fp32 MFMA.
 constexpr int kX3K = 32;                 // K per slice
 constexpr int kX3S = kX3K + 8;           // LDS row stride in bf16 elements (80 bytes: conflict-free fragments)
 constexpr int kX3Plane = kBfT * kX3S;    // one plane of one operand

@@ -373,7 +373,7 @@ struct SideStream {
   mutable hipStream_t origin;
 };
 SideStream* side_stream(hipStream_t origin);
-// side_stream(origin) for problems of at least 2^20 edges, else null
+// side_stream(origin) for problems of at least 2^18 edges, else null
 const SideStream* side_stream_for(hipStream_t origin, int64_t edges);
 int fork_to(const SideStream* s, hipStream_t origin);   // s->stream waits for origin's work so far
 int join_from(const SideStream* s, hipStream_t origin); // origin waits for s->stream's work so far

@@ -17,6 +17,8 @@ Other workloads (--workload), one per hot-path row, same output format:
   c4-topk-bf16 BASELINE config 4 (C4-topk bf16 row): c4-topk with bf16 layer
               states and values; the value rows move as bf16 and the top-k
               scores run on bf16 MFMAs (sparse-byte budget 6.72 GB).
+  c4-dense-bf16 c4-dense with bf16 layer states and values: the N x N
+              products on bf16 MFMA.
   c4-dense-causal c4-dense with a full causal window (the masked half skipped).
   c3-transition-dense C3 sizes with every source routed to every destination.
   c5-progressive-b BASELINE config 5: the Progressive-B query-block training
@@ -553,6 +555,43 @@ class DenseC4:
                          val=val.to(dev).requires_grad_(True))
 
 
+class DenseC4Bf16(DenseC4):
+    """c4-dense with bf16 layer states and values: the three N x N products
+    on bf16 MFMA (the edge matrix rounded to bf16 where it multiplies
+    values), the projections on the bf16 projection GEMMs."""
+
+    name = "c4-dense-bf16"
+    metric = "routed pairs/sec + MFMA TFLOP/s (% peak), Propagation dense N=4096 D=512 r=64 fwd+bwd, bf16 activations"
+    workload = "C4-dense bf16 Propagation fwd+bwd (all N x N pairs), LowRankBilinearPairwise, softsign, bf16 layers, native"
+    data = ("synthetic (seeded N(0,1) state, unit-norm N(0,1) val rows, both rounded to bf16; default module "
+            "init, fp32 weights)")
+    dtype = "bf16"
+    traffic_file = "c4_dense_bf16_hbm_traffic.json"
+    cpu_batch = 2
+
+    def model(self, name):
+        c = self.config
+        B, N, D, r = (c[x] for x in ("batch", "nodes", "dim", "rank"))
+        Bc = self.chunk_batch()
+        dense = {
+            "gemm_bf16_kernel<dense_aggregate_bf16>": 2.0 * Bc * N * N * D,
+            "gemm_bf16_kernel<dense_edge_grad_bf16>": 2.0 * Bc * N * N * D,
+            "gemm_bf16_kernel<dense_value_grad_bf16>": 2.0 * Bc * N * N * D,
+        }
+        if name in dense:
+            return "mfma", dense[name], None, BF16_MFMA_PEAK_TFLOPS
+        if name.startswith("gemm_bf16_kernel"):
+            return "mfma", 2.0 * B * N * D * 2 * r, None, BF16_MFMA_PEAK_TFLOPS
+        return super().model(name)
+
+    def build(self, torch, dev, impl: str = "native", batch: int | None = None):
+        from jakal_net import Layer
+
+        op, layer = super().build(torch, dev, impl=impl, batch=batch)
+        bf = lambda t: t.detach().bfloat16().requires_grad_(True)  # noqa: E731
+        return op, Layer(dim=layer.dim, num_nodes=layer.num_nodes, state=bf(layer.state), val=bf(layer.val))
+
+
 class DenseCausalC4(DenseC4):
     """C4 shapes with a full causal window (window = N - 1): row i keeps the
     sources j <= i (the causal dense query propagation of
@@ -734,8 +773,8 @@ class ProgressiveC5:
         return step
 
 
-WORKLOADS = {w.name: w for w in (TopkC4(), TopkC4Bf16(), WindowC2(), TransitionC3(), DenseC4(), DenseCausalC4(),
-                                 TransitionDenseC3(), ProgressiveC5())}
+WORKLOADS = {w.name: w for w in (TopkC4(), TopkC4Bf16(), WindowC2(), TransitionC3(), DenseC4(), DenseC4Bf16(),
+                                 DenseCausalC4(), TransitionDenseC3(), ProgressiveC5())}
 
 
 def capture_step(torch, step):

@@ -36,7 +36,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 11. */
+/* ABI revision of this header (bumped on any signature change); this is 12. */
 int jn_abi_version(void);
 
 /*
@@ -649,6 +649,49 @@ int jn_transition_topk_backward_bf16(
     int64_t topk, int32_t compress_kind, float* grad_sender_strength, uint16_t* grad_src_val,
     uint16_t* grad_dst_val, float* grad_projected_state, uint16_t* grad_projected_val, float* grad_source_weight,
     float* grad_target_weight, float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
+    jn_stream_t stream);
+
+/*
+ * bf16 dense layers (one head): jn_propagation_dense_* with bf16 value
+ * tensors, as above.  The edge matrix, the score gradient and the workspaces
+ * stay fp32 (the fp32 entry points' workspace queries apply).  E . pv and
+ * E^T . gdv take E rounded to bf16 (nearest even), gdv . pv^T multiplies the
+ * bf16 rows exactly; all three accumulate in fp32 on
+ * v_mfma_f32_16x16x32_bf16, and the score-gradient product keeps softsign's
+ * derivative in its epilogue.  nodes and out_dim must be at least 128 and
+ * multiples of 8 (kUnsupported otherwise: the fp32 entry points take any
+ * shape).
+ */
+int jn_propagation_dense_forward_bf16(const uint16_t* layer_val, const float* projected_state,
+                                      const uint16_t* projected_val, const float* target_weight,
+                                      const float* source_weight, const float* core_weight, const float* bias,
+                                      int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                      int32_t compress_kind, int32_t causal, float* delta_state, uint16_t* delta_val,
+                                      float* projections, float* edges, jn_stream_t stream);
+int jn_propagation_dense_backward_bf16(
+    const uint16_t* layer_val, const float* projected_state, const uint16_t* projected_val,
+    const float* target_weight, const float* source_weight, const float* core_weight, const float* projections,
+    float* edges, const float* grad_delta_state, const uint16_t* grad_delta_val, int64_t batch, int64_t nodes,
+    int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
+    int32_t projected_val_is_layer_val, int32_t reuse_edges, uint16_t* grad_layer_val, float* grad_projected_state,
+    uint16_t* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
+    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
+int jn_propagation_dense_forward_chunked_bf16(const uint16_t* layer_val, const float* projected_state,
+                                              const uint16_t* projected_val, const float* target_weight,
+                                              const float* source_weight, const float* core_weight, const float* bias,
+                                              int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                              int64_t rank, int32_t compress_kind, int32_t causal,
+                                              int64_t chunk_batch, float* delta_state, uint16_t* delta_val,
+                                              float* projections, void* workspace, size_t workspace_bytes,
+                                              jn_stream_t stream);
+int jn_propagation_dense_backward_chunked_bf16(
+    const uint16_t* layer_val, const float* projected_state, const uint16_t* projected_val,
+    const float* target_weight, const float* source_weight, const float* core_weight, const float* bias,
+    const float* projections, float* edge_chunk, const float* grad_delta_state, const uint16_t* grad_delta_val,
+    int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind,
+    int32_t causal, int32_t projected_val_is_layer_val, int64_t chunk_batch, int32_t chunk_resident,
+    uint16_t* grad_layer_val, float* grad_projected_state, uint16_t* grad_projected_val, float* grad_target_weight,
+    float* grad_source_weight, float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
     jn_stream_t stream);
 
 /*

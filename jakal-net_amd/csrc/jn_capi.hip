@@ -389,6 +389,12 @@ TransitionDenseScratch carve_transition_dense(void* base, size_t size, int64_t B
   return s;
 }
 
+// Row e of a value tensor (elements, not bytes): bf16 tensors travel as float
+// pointers to the GEMMs, which address them in bf16 elements.
+inline const float* value_rows(const float* p, int64_t e, bool bf16) {
+  return bf16 ? reinterpret_cast<const float*>(reinterpret_cast<const bf16_t*>(p) + e) : p + e;
+}
+
 // Max-aggregated multi-head scores of batch elements [b0, b0 + nb)
 // (jakal_net_native.cpp:724-752): S = max_h (P_t,h diag(w_h) P_s,h^T + b_h)
 // over the heads' rank slices of the [N, 2r] projection rows (r = heads *
@@ -417,12 +423,15 @@ int dense_head_scores(const float* core_weight, const float* bias, int b0, int n
 // delta_state = E ps and delta_val = E pv.  projections holds every batch
 // element's [N, 2r] projection rows.  heads > 1: max-aggregated scores over
 // the heads' rank slices (r = heads * head rank, bias [heads]), with the
-// winning head of every pair in head_mat [nb, N, N].
+// winning head of every pair in head_mat [nb, N, N].  bf16 (one head):
+// projected_val and delta_val hold bf16 elements; E stays fp32 and is rounded
+// to bf16 as the aggregate's operand.
 int dense_forward_range(const float* projected_state, const float* projected_val, const float* core_weight,
                         const float* bias, int b0, int nb, int N, int D, int r, int compress_kind, bool causal,
                         const float* projections, float* E, float* delta_state, float* delta_val, hipStream_t st,
-                        int heads = 1, uint8_t* head_mat = nullptr) {
+                        int heads = 1, uint8_t* head_mat = nullptr, bool bf16 = false) {
   const int64_t pr = (int64_t)b0 * N;  // first row of the range
+  JN_REQUIRE(!bf16 || heads == 1, kInvalidArgument, "bf16 dense layers have one head");
   if (heads > 1) {
     int rc = dense_head_scores(core_weight, bias, b0, nb, N, r, heads, projections, E, head_mat, st);
     if (rc) return rc;
@@ -448,26 +457,27 @@ int dense_forward_range(const float* projected_state, const float* projected_val
   // delta_state are staged in delta_val's storage (the aggregate GEMM below
   // overwrites it); the row-wise compressions run as a pass of their own.
   const int parts = dense_epi_parts(N);
-  const bool fused = compress_kind == 0 && parts <= D;
+  const bool fused = compress_kind == 0 && parts <= (bf16 ? D / 2 : D);
+  float* vstage = bf16 ? reinterpret_cast<float*>(reinterpret_cast<bf16_t*>(delta_val) + pr * D) : delta_val + pr * D;
   if (fused) {
     sg.epi = 1; sg.epi_causal = causal; sg.epi_bias = bias; sg.epi_ps = projected_state + pr;
-    sg.epi_part = delta_val + pr * D;
+    sg.epi_part = vstage;
   }
   int rc = gemm_batched(sg, kGemmDenseScores, st);
   if (rc) return rc;
   // E = compress(S + b) (in place when not fused), delta_state = E ps
-  rc = fused ? launch_dense_part_rowsum(delta_val + pr * D, parts, (int64_t)nb * N, delta_state + pr, st)
+  rc = fused ? launch_dense_part_rowsum(vstage, parts, (int64_t)nb * N, delta_state + pr, st)
              : launch_dense_compress(E, bias, projected_state + pr, nb, N, compress_kind, causal, delta_state + pr,
                                      st);
   if (rc) return rc;
   // delta_val_b = E_b pv_b
   BatchedGemm ag{};
   ag.A = E; ag.lda = N; ag.a_bs = (int64_t)N * N; ag.a_kcontig = true;
-  ag.B = projected_val + pr * D; ag.ldb = D; ag.b_bs = (int64_t)N * D; ag.b_kcontig = false;
-  ag.C = delta_val + pr * D; ag.ldc = D; ag.c_bs = (int64_t)N * D;
+  ag.B = value_rows(projected_val, pr * D, bf16); ag.ldb = D; ag.b_bs = (int64_t)N * D; ag.b_kcontig = false;
+  ag.C = const_cast<float*>(value_rows(delta_val, pr * D, bf16)); ag.ldc = D; ag.c_bs = (int64_t)N * D;
   ag.M = N; ag.N = D; ag.K = N; ag.batch = nb;
   ag.causal_k = causal ? kCausalKLower : kCausalKNone;  // row i reads sources j <= i
-  return gemm_batched(ag, kGemmDenseAggregate, st);
+  return gemm_batched(ag, bf16 ? kGemmDenseAggregateBf16 : kGemmDenseAggregate, st);
 }
 
 // Dense propagation backward, chunk_batch batch elements at a time.  E holds
@@ -487,13 +497,14 @@ int dense_backward(const float* layer_val, const float* projected_state, const f
                    int32_t projected_val_is_layer_val, float* grad_layer_val, float* grad_projected_state,
                    float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
                    float* grad_core_weight, float* grad_bias, const DenseScratch& s, hipStream_t st, int heads = 1,
-                   uint8_t* head_mat = nullptr) {
+                   uint8_t* head_mat = nullptr, bool bf16 = false) {
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
                  projections && E && G && grad_delta_state && grad_delta_val,
              kInvalidArgument, "null tensor pointer");
   JN_REQUIRE(!projected_val_is_layer_val || in_dim == out_dim, kInvalidArgument,
              "projected_val_is_layer_val requires in_dim == out_dim");
   JN_REQUIRE(G != E || compress_kind == 0, kInvalidArgument, "only the softsign gradient overwrites the edges");
+  JN_REQUIRE(!bf16 || heads == 1, kInvalidArgument, "bf16 dense layers have one head");
   const int B = (int)batch, N = (int)nodes, r = (int)rank, D = (int)out_dim;
   const int M = B * N;
   const bool fused = compress_kind == 0;  // softsign's derivative in the score-gradient GEMM's epilogue
@@ -541,11 +552,11 @@ int dense_backward(const float* layer_val, const float* projected_state, const f
     if (gpv) {
       BatchedGemm vg{};
       vg.A = E; vg.lda = N; vg.a_bs = (int64_t)N * N; vg.a_kcontig = false;
-      vg.B = grad_delta_val + pr * D; vg.ldb = D; vg.b_bs = (int64_t)N * D; vg.b_kcontig = false;
-      vg.C = gpv + pr * D; vg.ldc = D; vg.c_bs = (int64_t)N * D;
+      vg.B = value_rows(grad_delta_val, pr * D, bf16); vg.ldb = D; vg.b_bs = (int64_t)N * D; vg.b_kcontig = false;
+      vg.C = const_cast<float*>(value_rows(gpv, pr * D, bf16)); vg.ldc = D; vg.c_bs = (int64_t)N * D;
       vg.M = N; vg.N = D; vg.K = N; vg.batch = nb;
       vg.causal_k = upper;
-      rc = gemm_batched(vg, kGemmDenseValueGrad, st);
+      rc = gemm_batched(vg, bf16 ? kGemmDenseValueGradBf16 : kGemmDenseValueGrad, st);
       if (rc) return rc;
     }
     if (grad_projected_state) {
@@ -555,15 +566,15 @@ int dense_backward(const float* layer_val, const float* projected_state, const f
 
     // 2. G_b = gdv_b pv_b^T, then the score gradient (+ row sums)
     BatchedGemm gg{};
-    gg.A = grad_delta_val + pr * D; gg.lda = D; gg.a_bs = (int64_t)N * D; gg.a_kcontig = true;
-    gg.B = projected_val + pr * D; gg.ldb = D; gg.b_bs = (int64_t)N * D; gg.b_kcontig = true;
+    gg.A = value_rows(grad_delta_val, pr * D, bf16); gg.lda = D; gg.a_bs = (int64_t)N * D; gg.a_kcontig = true;
+    gg.B = value_rows(projected_val, pr * D, bf16); gg.ldb = D; gg.b_bs = (int64_t)N * D; gg.b_kcontig = true;
     gg.C = G; gg.ldc = N; gg.c_bs = (int64_t)N * N;
     gg.M = N; gg.N = N; gg.K = D; gg.batch = nb;
     if (fused) {
       gg.epi = 1; gg.epi_causal = causal != 0; gg.epi_ps = projected_state + pr; gg.epi_gds = grad_delta_state + pr;
       gg.epi_E = E; gg.epi_part = rowsum;
     }
-    rc = gemm_batched(gg, kGemmDenseEdgeGrad, st);
+    rc = gemm_batched(gg, bf16 ? kGemmDenseEdgeGradBf16 : kGemmDenseEdgeGrad, st);
     if (rc) return rc;
     if (!fused) {
       rc = launch_dense_compress_backward(G, E, grad_delta_state + pr, projected_state + pr, nb, N, compress_kind,
@@ -613,13 +624,13 @@ int dense_backward(const float* layer_val, const float* projected_state, const f
   // 4. projection weight and input grads
   if (grad_target_weight && grad_source_weight) {
     rc = gemm_grad_weight(s.dP, 2 * r, layer_val, in_dim, grad_target_weight, grad_source_weight, r, 2 * r,
-                          (int)in_dim, M, s.splitk, st);
+                          (int)in_dim, M, s.splitk, st, bf16);
     if (rc) return rc;
   }
   if (grad_layer_val) {
     const float* addend = (projected_val_is_layer_val && gpv) ? grad_layer_val : nullptr;
     rc = gemm_grad_input(s.dP, 2 * r, target_weight, source_weight, r, in_dim, addend, in_dim, grad_layer_val,
-                         in_dim, M, (int)in_dim, 2 * r, st);
+                         in_dim, M, (int)in_dim, 2 * r, st, bf16);
     if (rc) return rc;
   }
 
@@ -1186,7 +1197,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 11; }
+int jn_abi_version(void) { return 12; }
 
 int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float eps, float* weight_hat,
                           jn_stream_t stream) {
@@ -2013,23 +2024,57 @@ int jn_transition_topk_backward_bf16(
       workspace_bytes, static_cast<hipStream_t>(stream), true);
 }
 
+// bf16 dense layers (one head): the bf16 MFMA kernel runs the three N x N
+// products, so its preconditions hold for every chunk.
+static int check_dense_bf16_shapes(int64_t nodes, int64_t out_dim) {
+  JN_REQUIRE(nodes >= 128 && out_dim >= 128 && nodes % 8 == 0 && out_dim % 8 == 0, kUnsupported,
+             "bf16 dense propagation needs nodes and out_dim >= 128 and multiples of 8 (got %lld, %lld)",
+             (long long)nodes, (long long)out_dim);
+  return kOk;
+}
+
+static int propagation_dense_forward_impl(const float* layer_val, const float* projected_state,
+                                          const float* projected_val, const float* target_weight,
+                                          const float* source_weight, const float* core_weight, const float* bias,
+                                          int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                          int32_t compress_kind, int32_t causal, float* delta_state, float* delta_val,
+                                          float* projections, float* edges, hipStream_t st, bool bf16) {
+  int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
+  if (rc) return rc;
+  if (bf16 && (rc = check_dense_bf16_shapes(nodes, out_dim))) return rc;
+  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
+                 delta_state && delta_val && projections && edges,
+             kInvalidArgument, "null tensor pointer");
+  const int B = (int)batch, N = (int)nodes, r = (int)rank, D = (int)out_dim;
+  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, B * N, 2 * r,
+                    (int)in_dim, st, bf16);
+  if (rc) return rc;
+  return dense_forward_range(projected_state, projected_val, core_weight, bias, 0, B, N, D, r, compress_kind,
+                             causal != 0, projections, edges, delta_state, delta_val, st, 1, nullptr, bf16);
+}
+
 int jn_propagation_dense_forward(const float* layer_val, const float* projected_state, const float* projected_val,
                                  const float* target_weight, const float* source_weight, const float* core_weight,
                                  const float* bias, int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
                                  int64_t rank, int32_t compress_kind, int32_t causal, float* delta_state,
                                  float* delta_val, float* projections, float* edges, jn_stream_t stream) {
-  int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
-  if (rc) return rc;
-  JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
-                 delta_state && delta_val && projections && edges,
-             kInvalidArgument, "null tensor pointer");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int B = (int)batch, N = (int)nodes, r = (int)rank, D = (int)out_dim;
-  rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, B * N, 2 * r,
-                    (int)in_dim, st);
-  if (rc) return rc;
-  return dense_forward_range(projected_state, projected_val, core_weight, bias, 0, B, N, D, r, compress_kind,
-                             causal != 0, projections, edges, delta_state, delta_val, st);
+  return propagation_dense_forward_impl(layer_val, projected_state, projected_val, target_weight, source_weight,
+                                        core_weight, bias, batch, nodes, in_dim, out_dim, rank, compress_kind, causal,
+                                        delta_state, delta_val, projections, edges, static_cast<hipStream_t>(stream),
+                                        false);
+}
+
+int jn_propagation_dense_forward_bf16(const uint16_t* layer_val, const float* projected_state,
+                                      const uint16_t* projected_val, const float* target_weight,
+                                      const float* source_weight, const float* core_weight, const float* bias,
+                                      int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                      int32_t compress_kind, int32_t causal, float* delta_state, uint16_t* delta_val,
+                                      float* projections, float* edges, jn_stream_t stream) {
+  return propagation_dense_forward_impl(reinterpret_cast<const float*>(layer_val), projected_state,
+                                        reinterpret_cast<const float*>(projected_val), target_weight, source_weight,
+                                        core_weight, bias, batch, nodes, in_dim, out_dim, rank, compress_kind, causal,
+                                        delta_state, reinterpret_cast<float*>(delta_val), projections, edges,
+                                        static_cast<hipStream_t>(stream), true);
 }
 
 size_t jn_propagation_dense_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
@@ -2041,17 +2086,17 @@ size_t jn_propagation_dense_workspace_bytes(int64_t batch, int64_t nodes, int64_
       .bytes;
 }
 
-int jn_propagation_dense_backward(const float* layer_val, const float* projected_state, const float* projected_val,
-                                  const float* target_weight, const float* source_weight, const float* core_weight,
-                                  const float* projections, float* edges, const float* grad_delta_state,
-                                  const float* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim,
-                                  int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
-                                  int32_t projected_val_is_layer_val, int32_t reuse_edges, float* grad_layer_val,
-                                  float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
-                                  float* grad_source_weight, float* grad_core_weight, float* grad_bias,
-                                  void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+static int propagation_dense_backward_impl(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* projections, float* edges,
+    const float* grad_delta_state, const float* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim,
+    int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal, int32_t projected_val_is_layer_val,
+    int32_t reuse_edges, float* grad_layer_val, float* grad_projected_state, float* grad_projected_val,
+    float* grad_target_weight, float* grad_source_weight, float* grad_core_weight, float* grad_bias, void* workspace,
+    size_t workspace_bytes, hipStream_t st, bool bf16) {
   int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
   if (rc) return rc;
+  if (bf16 && (rc = check_dense_bf16_shapes(nodes, out_dim))) return rc;
   JN_REQUIRE(edges, kInvalidArgument, "null tensor pointer");
   // softsign's derivative runs in the score-gradient GEMM's epilogue, which
   // reads each edge once before writing its gradient: with reuse_edges that
@@ -2064,8 +2109,41 @@ int jn_propagation_dense_backward(const float* layer_val, const float* projected
                         projections, edges, in_place ? edges : s.G, (int)batch, false, false, grad_delta_state,
                         grad_delta_val, batch, nodes, in_dim, out_dim, rank, compress_kind, causal,
                         projected_val_is_layer_val, grad_layer_val, grad_projected_state, grad_projected_val,
-                        grad_target_weight, grad_source_weight, grad_core_weight, grad_bias, s,
-                        static_cast<hipStream_t>(stream));
+                        grad_target_weight, grad_source_weight, grad_core_weight, grad_bias, s, st, 1, nullptr, bf16);
+}
+
+int jn_propagation_dense_backward(const float* layer_val, const float* projected_state, const float* projected_val,
+                                  const float* target_weight, const float* source_weight, const float* core_weight,
+                                  const float* projections, float* edges, const float* grad_delta_state,
+                                  const float* grad_delta_val, int64_t batch, int64_t nodes, int64_t in_dim,
+                                  int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
+                                  int32_t projected_val_is_layer_val, int32_t reuse_edges, float* grad_layer_val,
+                                  float* grad_projected_state, float* grad_projected_val, float* grad_target_weight,
+                                  float* grad_source_weight, float* grad_core_weight, float* grad_bias,
+                                  void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  return propagation_dense_backward_impl(
+      layer_val, projected_state, projected_val, target_weight, source_weight, core_weight, projections, edges,
+      grad_delta_state, grad_delta_val, batch, nodes, in_dim, out_dim, rank, compress_kind, causal,
+      projected_val_is_layer_val, reuse_edges, grad_layer_val, grad_projected_state, grad_projected_val,
+      grad_target_weight, grad_source_weight, grad_core_weight, grad_bias, workspace, workspace_bytes,
+      static_cast<hipStream_t>(stream), false);
+}
+
+int jn_propagation_dense_backward_bf16(
+    const uint16_t* layer_val, const float* projected_state, const uint16_t* projected_val,
+    const float* target_weight, const float* source_weight, const float* core_weight, const float* projections,
+    float* edges, const float* grad_delta_state, const uint16_t* grad_delta_val, int64_t batch, int64_t nodes,
+    int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
+    int32_t projected_val_is_layer_val, int32_t reuse_edges, uint16_t* grad_layer_val, float* grad_projected_state,
+    uint16_t* grad_projected_val, float* grad_target_weight, float* grad_source_weight, float* grad_core_weight,
+    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  return propagation_dense_backward_impl(
+      reinterpret_cast<const float*>(layer_val), projected_state, reinterpret_cast<const float*>(projected_val),
+      target_weight, source_weight, core_weight, projections, edges, grad_delta_state,
+      reinterpret_cast<const float*>(grad_delta_val), batch, nodes, in_dim, out_dim, rank, compress_kind, causal,
+      projected_val_is_layer_val, reuse_edges, reinterpret_cast<float*>(grad_layer_val), grad_projected_state,
+      reinterpret_cast<float*>(grad_projected_val), grad_target_weight, grad_source_weight, grad_core_weight,
+      grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream), true);
 }
 
 size_t jn_propagation_dense_chunked_workspace_bytes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
@@ -2078,15 +2156,15 @@ size_t jn_propagation_dense_chunked_workspace_bytes(int64_t batch, int64_t nodes
   return carve_dense(nullptr, 0, batch, nodes, in_dim, rank, compress_kind == 0 ? 0 : cb, 0).bytes;
 }
 
-int jn_propagation_dense_forward_chunked(const float* layer_val, const float* projected_state,
-                                         const float* projected_val, const float* target_weight,
-                                         const float* source_weight, const float* core_weight, const float* bias,
-                                         int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
-                                         int32_t compress_kind, int32_t causal, int64_t chunk_batch,
-                                         float* delta_state, float* delta_val, float* projections, void* workspace,
-                                         size_t workspace_bytes, jn_stream_t stream) {
+static int propagation_dense_forward_chunked_impl(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* bias, int64_t batch, int64_t nodes,
+    int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal, int64_t chunk_batch,
+    float* delta_state, float* delta_val, float* projections, void* workspace, size_t workspace_bytes,
+    hipStream_t st, bool bf16) {
   int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
   if (rc) return rc;
+  if (bf16 && (rc = check_dense_bf16_shapes(nodes, out_dim))) return rc;
   JN_REQUIRE(layer_val && projected_state && projected_val && target_weight && source_weight && core_weight &&
                  delta_state && delta_val && projections,
              kInvalidArgument, "null tensor pointer");
@@ -2097,28 +2175,58 @@ int jn_propagation_dense_forward_chunked(const float* layer_val, const float* pr
   float* E = ws.take<float>((int64_t)cb * N * N);
   JN_REQUIRE(workspace != nullptr && ws.used <= workspace_bytes, kWorkspaceTooSmall,
              "workspace too small: need %zu bytes, got %zu", ws.used, workspace_bytes);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   rc = gemm_project(layer_val, in_dim, target_weight, source_weight, r, in_dim, projections, 2 * r, B * N, 2 * r,
-                    (int)in_dim, st);
+                    (int)in_dim, st, bf16);
   if (rc) return rc;
   for (int b0 = 0; b0 < B; b0 += cb) {
     rc = dense_forward_range(projected_state, projected_val, core_weight, bias, b0, std::min(cb, B - b0), N, D, r,
-                             compress_kind, causal != 0, projections, E, delta_state, delta_val, st);
+                             compress_kind, causal != 0, projections, E, delta_state, delta_val, st, 1, nullptr,
+                             bf16);
     if (rc) return rc;
   }
   return kOk;
 }
 
-int jn_propagation_dense_backward_chunked(
+int jn_propagation_dense_forward_chunked(const float* layer_val, const float* projected_state,
+                                         const float* projected_val, const float* target_weight,
+                                         const float* source_weight, const float* core_weight, const float* bias,
+                                         int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank,
+                                         int32_t compress_kind, int32_t causal, int64_t chunk_batch,
+                                         float* delta_state, float* delta_val, float* projections, void* workspace,
+                                         size_t workspace_bytes, jn_stream_t stream) {
+  return propagation_dense_forward_chunked_impl(layer_val, projected_state, projected_val, target_weight,
+                                                source_weight, core_weight, bias, batch, nodes, in_dim, out_dim, rank,
+                                                compress_kind, causal, chunk_batch, delta_state, delta_val,
+                                                projections, workspace, workspace_bytes,
+                                                static_cast<hipStream_t>(stream), false);
+}
+
+int jn_propagation_dense_forward_chunked_bf16(const uint16_t* layer_val, const float* projected_state,
+                                              const uint16_t* projected_val, const float* target_weight,
+                                              const float* source_weight, const float* core_weight, const float* bias,
+                                              int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim,
+                                              int64_t rank, int32_t compress_kind, int32_t causal,
+                                              int64_t chunk_batch, float* delta_state, uint16_t* delta_val,
+                                              float* projections, void* workspace, size_t workspace_bytes,
+                                              jn_stream_t stream) {
+  return propagation_dense_forward_chunked_impl(
+      reinterpret_cast<const float*>(layer_val), projected_state, reinterpret_cast<const float*>(projected_val),
+      target_weight, source_weight, core_weight, bias, batch, nodes, in_dim, out_dim, rank, compress_kind, causal,
+      chunk_batch, delta_state, reinterpret_cast<float*>(delta_val), projections, workspace, workspace_bytes,
+      static_cast<hipStream_t>(stream), true);
+}
+
+static int propagation_dense_backward_chunked_impl(
     const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
     const float* source_weight, const float* core_weight, const float* bias, const float* projections,
     float* edge_chunk, const float* grad_delta_state, const float* grad_delta_val, int64_t batch, int64_t nodes,
     int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
     int32_t projected_val_is_layer_val, int64_t chunk_batch, int32_t chunk_resident, float* grad_layer_val,
     float* grad_projected_state, float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
-    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, hipStream_t st, bool bf16) {
   int rc = check_dense_shapes(batch, nodes, in_dim, out_dim, rank, compress_kind);
   if (rc) return rc;
+  if (bf16 && (rc = check_dense_bf16_shapes(nodes, out_dim))) return rc;
   JN_REQUIRE(chunk_batch >= 1, kInvalidArgument, "chunk_batch must be positive");
   JN_REQUIRE(edge_chunk, kInvalidArgument, "null tensor pointer");
   const int cb = (int)(chunk_batch < batch ? chunk_batch : batch);
@@ -2130,7 +2238,41 @@ int jn_propagation_dense_backward_chunked(
                         grad_delta_state, grad_delta_val,
                         batch, nodes, in_dim, out_dim, rank, compress_kind, causal, projected_val_is_layer_val,
                         grad_layer_val, grad_projected_state, grad_projected_val, grad_target_weight,
-                        grad_source_weight, grad_core_weight, grad_bias, s, static_cast<hipStream_t>(stream));
+                        grad_source_weight, grad_core_weight, grad_bias, s, st, 1, nullptr, bf16);
+}
+
+int jn_propagation_dense_backward_chunked(
+    const float* layer_val, const float* projected_state, const float* projected_val, const float* target_weight,
+    const float* source_weight, const float* core_weight, const float* bias, const float* projections,
+    float* edge_chunk, const float* grad_delta_state, const float* grad_delta_val, int64_t batch, int64_t nodes,
+    int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind, int32_t causal,
+    int32_t projected_val_is_layer_val, int64_t chunk_batch, int32_t chunk_resident, float* grad_layer_val,
+    float* grad_projected_state, float* grad_projected_val, float* grad_target_weight, float* grad_source_weight,
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  return propagation_dense_backward_chunked_impl(
+      layer_val, projected_state, projected_val, target_weight, source_weight, core_weight, bias, projections,
+      edge_chunk, grad_delta_state, grad_delta_val, batch, nodes, in_dim, out_dim, rank, compress_kind, causal,
+      projected_val_is_layer_val, chunk_batch, chunk_resident, grad_layer_val, grad_projected_state,
+      grad_projected_val, grad_target_weight, grad_source_weight, grad_core_weight, grad_bias, workspace,
+      workspace_bytes, static_cast<hipStream_t>(stream), false);
+}
+
+int jn_propagation_dense_backward_chunked_bf16(
+    const uint16_t* layer_val, const float* projected_state, const uint16_t* projected_val,
+    const float* target_weight, const float* source_weight, const float* core_weight, const float* bias,
+    const float* projections, float* edge_chunk, const float* grad_delta_state, const uint16_t* grad_delta_val,
+    int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_dim, int64_t rank, int32_t compress_kind,
+    int32_t causal, int32_t projected_val_is_layer_val, int64_t chunk_batch, int32_t chunk_resident,
+    uint16_t* grad_layer_val, float* grad_projected_state, uint16_t* grad_projected_val, float* grad_target_weight,
+    float* grad_source_weight, float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
+    jn_stream_t stream) {
+  return propagation_dense_backward_chunked_impl(
+      reinterpret_cast<const float*>(layer_val), projected_state, reinterpret_cast<const float*>(projected_val),
+      target_weight, source_weight, core_weight, bias, projections, edge_chunk, grad_delta_state,
+      reinterpret_cast<const float*>(grad_delta_val), batch, nodes, in_dim, out_dim, rank, compress_kind, causal,
+      projected_val_is_layer_val, chunk_batch, chunk_resident, reinterpret_cast<float*>(grad_layer_val),
+      grad_projected_state, reinterpret_cast<float*>(grad_projected_val), grad_target_weight, grad_source_weight,
+      grad_core_weight, grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream), true);
 }
 
 // Dense transition forward; heads > 1: max-aggregated route logits over the

@@ -522,10 +522,18 @@ constexpr GemmUseInfo kGemmUses[] = {
     {true, false, false, true, "gemm_f32_kernel<grad_input_bf16>"},
     {false, false, false, false, "gemm_f32_kernel<grad_weight_bf16>"},
     {true, true, true, false, "gemm_f32_kernel<select_scores>"},
+    {true, false, false, false, "gemm_bf16_kernel<dense_aggregate_bf16>"},
+    {false, false, false, false, "gemm_bf16_kernel<dense_value_grad_bf16>"},
+    {true, true, false, false, "gemm_bf16_kernel<dense_edge_grad_bf16>"},
 };
-static_assert(sizeof(kGemmUses) / sizeof(kGemmUses[0]) == kGemmSelectScores + 1, "one entry per GemmUse");
+static_assert(sizeof(kGemmUses) / sizeof(kGemmUses[0]) == kGemmDenseEdgeGradBf16 + 1, "one entry per GemmUse");
 constexpr bool gemm_use_bf16(GemmUse u) {
   return u == kGemmProjectBf16 || u == kGemmGradInputBf16 || u == kGemmGradWeightBf16;
+}
+// The bf16 dense uses run on the bf16 MFMA kernel only (their callers check
+// its preconditions first).
+constexpr bool gemm_use_dense_bf16(int u) {
+  return u == kGemmDenseAggregateBf16 || u == kGemmDenseValueGradBf16 || u == kGemmDenseEdgeGradBf16;
 }
 
 // ---- 128 x 128 path --------------------------------------------------------
@@ -909,7 +917,9 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
 }
 
 // ---- bf16 MFMA path (bf16 layers) ------------------------------------------
-// The projection of bf16 layer values and its two gradients on
+// The projection of bf16 layer values and its two gradients, and a bf16
+// dense layer's three N x N products (E . pv, E^T . gdv, gdv . pv^T, causal
+// K ranges included), on
 // v_mfma_f32_16x16x32_bf16: workgroup tile 128 x 128, 2 x 2 waves of 64 x 64
 // (4 x 4 tiles of 16 x 16), K in slices of 64 (two K-steps of 32), LDS double
 // buffered with register prefetch.  Both operands sit in LDS as [row][k]
@@ -918,7 +928,8 @@ __global__ __launch_bounds__(256, 4) void gemm_f32_fast_kernel(GemmArgs g, int t
 // operands are rounded to bf16 (nearest even) on their way into LDS; K-major
 // operands are transposed there in 4 x 4 (fp32) or 4 x 8 (bf16) blocks.
 // Accumulation is fp32.  The epilogue stages each wave's 64 x 64 block in LDS
-// and writes whole 8-element rows (one 16-byte store of bf16, two of fp32).
+// and writes whole 8-element rows (one 16-byte store of bf16, two of fp32);
+// the dense score gradient's softsign epilogue works from the accumulators.
 // Preconditions (host-checked, else the fp32 kernels run): M, N >= 128, N and
 // the output strides multiples of 8, K and the split-K chunk multiples of 64
 // ... of 8 for K-contiguous bf16 rows; row strides and batch strides
@@ -939,10 +950,12 @@ struct BfLoader {
   static constexpr int kLoads = KC ? (BF ? 4 : 8) : (BF ? 4 : 8);
   uint4 r[kLoads];
 
-  // rs0 addresses row 0 of the tile; K-contiguous rows from split_row on
-  // (tile-relative, a multiple of 8) are read through rs1, which addresses
-  // the tile's row 0 as if the second buffer continued the first (the rows a
-  // wave loads with one instruction never straddle it: a wave-uniform choice)
+  // rs0 addresses the slice's (row 0, k = k0) -- offsets stay within one
+  // slice of rows, so 32-bit offsets reach any K; K-contiguous rows from
+  // split_row on (tile-relative, a multiple of 8) are read through rs1, which
+  // addresses the slice's row 0 as if the second buffer continued the first
+  // (the rows a wave loads with one instruction never straddle it: a
+  // wave-uniform choice)
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs0, __amdgpu_buffer_rsrc_t rs1, int split_row, int ld,
                                        int row0, int rows, int k0, int kend, int tid) {
     constexpr uint32_t EB = BF ? 2 : 4;
@@ -954,7 +967,7 @@ struct BfLoader {
         const bool ok = row0 + row < rows && k0 + kq < kend;
         const auto rs = ((wbase + 256 * u) >> 3) < split_row ? rs0 : rs1;
         r[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rs, ok ? (uint32_t)(row * ld + k0 + kq) * EB : kOobOffset, 0, 0));
+                                             rs, ok ? (uint32_t)(row * ld + kq) * EB : kOobOffset, 0, 0));
       }
     } else if constexpr (KC) {  // 128 rows x 16 groups of 4 k
 #pragma unroll
@@ -963,14 +976,14 @@ struct BfLoader {
         const bool ok = row0 + row < rows && k0 + kq < kend;
         const auto rs = ((wbase + 256 * u) >> 4) < split_row ? rs0 : rs1;
         r[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rs, ok ? (uint32_t)(row * ld + k0 + kq) * EB : kOobOffset, 0, 0));
+                                             rs, ok ? (uint32_t)(row * ld + kq) * EB : kOobOffset, 0, 0));
       }
     } else if constexpr (BF) {  // 16 groups of 4 k x 16 groups of 8 rows: one 4 x 8 block per thread
       const int kb = tid >> 4, rb = (tid & 15) * 8;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int kk = k0 + 4 * kb + i;
-        const bool ok = kk < kend && row0 + rb < rows;
+        const int kk = 4 * kb + i;
+        const bool ok = k0 + kk < kend && row0 + rb < rows;
         r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                              rs0, ok ? (uint32_t)(kk * ld + rb) * EB : kOobOffset, 0, 0));
       }
@@ -980,8 +993,8 @@ struct BfLoader {
         const int blk = tid + 256 * h, kb = blk >> 5, rb = (blk & 31) * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int kk = k0 + 4 * kb + i;
-          const bool ok = kk < kend && row0 + rb < rows;
+          const int kk = 4 * kb + i;
+          const bool ok = k0 + kk < kend && row0 + rb < rows;
           r[4 * h + i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                                        rs0, ok ? (uint32_t)(kk * ld + rb) * EB : kOobOffset, 0, 0));
         }
@@ -1034,7 +1047,8 @@ struct BfLoader {
   }
 };
 
-// C_BF: C and the addend hold bf16 (the input gradient).
+// C_BF: C and the addend hold bf16 (the input gradient, the dense aggregate
+// and value gradient).
 template <bool A_KC, bool A_BF, bool B_KC, bool B_BF, bool C_BF, int USE>
 __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g, int tiles_m, int tiles_n) {
   __shared__ __align__(16) bf16_t smem[4 * kBfT * kBfS];  // A[2], B[2]; the epilogue reuses it
@@ -1054,40 +1068,52 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g, int tiles
   const int band = t / (kBand * tiles_n);
   const int bm = min(kBand, tiles_m - band * kBand);
   const int tb = t - band * kBand * tiles_n;
-  const int m0 = (band * kBand + tb % bm) * kBfT;
+  int mi = band * kBand + tb % bm;
+  // causal products: the longest K ranges (or the epilogue's non-empty rows) first
+  if (g.causal_k == kCausalKLower || (g.epi && g.epi_causal)) mi = tiles_m - 1 - mi;
+  const int m0 = mi * kBfT;
   const int n0 = (tb / bm) * kBfT;
   const bool batched = g.batch > 1;
   const int split = batched ? 0 : z;
   const int64_t bz = batched ? z : 0;
-  const int kbeg = split * g.k_chunk;
-  const int kend = min(g.K, kbeg + g.k_chunk);
+  int kbeg = split * g.k_chunk;
+  int kend = min(g.K, kbeg + g.k_chunk);
+  causal_k_range<kBfT>(g, m0, n0, kbeg, kend);
 
   constexpr uint32_t AEB = A_BF ? 2 : 4, BEB = B_BF ? 2 : 4;
   const int lda = (int)g.lda, ldb = (int)g.ldb;
-  // buffer resources from each operand's tile origin (row0 = m0 / n0 along
-  // the row axis, k measured from 0)
+  // operand origins (row0 = m0 / n0 along the row axis, k = 0); each slice's
+  // buffer resources start at the slice
   const char* abase = reinterpret_cast<const char*>(g.A) + (bz * g.a_bs + (A_KC ? (int64_t)m0 * lda : m0)) * AEB;
-  const auto ars = make_rsrc(abase, kFastRecords);
-  auto brsrc = [&](const float* Bp, int64_t rofs) {
-    return make_rsrc(reinterpret_cast<const char*>(Bp) + (bz * g.b_bs + (B_KC ? rofs * ldb : rofs)) * BEB,
-                     kFastRecords);
+  auto borigin = [&](const float* Bp, int64_t rofs) {
+    return reinterpret_cast<const char*>(Bp) + (bz * g.b_bs + (B_KC ? rofs * ldb : rofs)) * BEB;
   };
   // B's rows below b_split come from B0, the rest from B1: along n for a
   // K-contiguous B, along k for a k-major B (whole slices: the host keeps
   // b_split a multiple of 64 there)
-  const auto brs0 = brsrc(g.B0, n0);
-  const auto brs1 = B_KC ? brsrc(g.B1, (int64_t)n0 - g.b_split) : brsrc(g.B1, n0);
+  const char* b0base = borigin(g.B0, n0);
+  const char* b1base = B_KC ? borigin(g.B1, (int64_t)n0 - g.b_split) : borigin(g.B1, n0);
   const int b_split_row = B_KC ? g.b_split - n0 : 1 << 30;
+  auto at_k = [](const char* origin, bool kc, int ld, int64_t k, uint32_t eb) {
+    return make_rsrc(origin + (kc ? k : k * ld) * eb, kFastRecords);
+  };
 
   BfLoader<A_KC, A_BF> la;
   BfLoader<B_KC, B_BF> lb;
   auto load_slice = [&](int k0) {
+    const auto ars = at_k(abase, A_KC, lda, k0, AEB);
     la.load(ars, ars, 1 << 30, lda, m0, g.M, k0, kend, tid);
     if constexpr (!B_KC) {
-      if (k0 >= g.b_split) lb.load(brs1, brs1, 1 << 30, ldb, n0, g.N, k0 - g.b_split, kend - g.b_split, tid);
-      else lb.load(brs0, brs0, 1 << 30, ldb, n0, g.N, k0, min(kend, g.b_split), tid);
+      if (k0 >= g.b_split) {
+        const auto rs = at_k(b1base, false, ldb, (int64_t)k0 - g.b_split, BEB);
+        lb.load(rs, rs, 1 << 30, ldb, n0, g.N, k0 - g.b_split, kend - g.b_split, tid);
+      } else {
+        const auto rs = at_k(b0base, false, ldb, k0, BEB);
+        lb.load(rs, rs, 1 << 30, ldb, n0, g.N, k0, min(kend, g.b_split), tid);
+      }
     } else {
-      lb.load(brs0, brs1, b_split_row, ldb, n0, g.N, k0, kend, tid);
+      lb.load(at_k(b0base, true, ldb, k0, BEB), at_k(b1base, true, ldb, k0, BEB), b_split_row, ldb, n0, g.N, k0,
+              kend, tid);
     }
   };
 
@@ -1128,6 +1154,16 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g, int tiles
     __syncthreads();
   }
 
+  float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
+  // the score gradient of a bf16 dense layer: softsign's derivative straight
+  // from the accumulators (the 16 x 16 output layout of every MFMA shape)
+  if constexpr (USE == kGemmDenseEdgeGradBf16) {
+    if (g.epi) {
+      dense_epilogue_tiles<kGemmDenseEdgeGrad, 4>(g, bz, acc, m0 + wm * 64, n0 + wn * 64, C, lane);
+      return;
+    }
+  }
+
   // epilogue: each wave's 64 x 64 block through LDS, then rows of 8 elements
   float* stage = reinterpret_cast<float*>(smem) + wave * 64 * kBfStage;
 #pragma unroll
@@ -1137,7 +1173,6 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g, int tiles
 #pragma unroll
       for (int v = 0; v < 4; ++v) stage[(mt * 16 + grp * 4 + v) * kBfStage + nt * 16 + col] = acc[mt][nt][v];
   __syncthreads();
-  float* C = g.C + (int64_t)split * g.c_split_stride + bz * g.c_bs;
   [[maybe_unused]] bf16_t* Cb = reinterpret_cast<bf16_t*>(g.C) + bz * g.c_bs;
   [[maybe_unused]] const bf16_t* addb =
       g.addend ? reinterpret_cast<const bf16_t*>(g.addend) + bz * g.add_bs : nullptr;
@@ -1175,11 +1210,15 @@ static bool bf16_path_ok(const GemmArgs& g, int use, int splits) {
   if (g.lda >= (1 << 20) || g.ldb >= (1 << 20)) return false;
   if (!al16(g.A) || !al16(g.B0) || !al16(g.B1) || !al16(g.C)) return false;
   if (g.addend && (g.ld_add % 8 != 0 || g.add_bs % 8 != 0 || !al16(g.addend))) return false;
-  if (g.a_kscale || g.c_nscale || g.c_mscale || g.epi || g.fold || g.a_heads) return false;
+  if (g.a_kscale || g.c_nscale || g.c_mscale || g.fold || g.a_heads) return false;
+  if (g.epi && use != kGemmDenseEdgeGradBf16) return false;
   if (splits > 1 && g.k_chunk % kBfK != 0) return false;
   if (use == kGemmProjectBf16) return g.K % 8 == 0 && g.b_split % 16 == 0;          // A bf16, B fp32, K-contiguous
   if (use == kGemmGradInputBf16) return g.K % 4 == 0 && g.b_split % kBfK == 0;       // A fp32 K-contig, B fp32 K-major
   if (use == kGemmGradWeightBf16) return g.M % 4 == 0 && g.b_split >= g.K;            // both K-major
+  if (use == kGemmDenseAggregateBf16) return g.K % 4 == 0 && g.b_split >= g.K && !g.addend;  // A fp32 K-contig (E)
+  if (use == kGemmDenseValueGradBf16) return g.M % 4 == 0 && g.b_split >= g.K && !g.addend;  // A fp32 K-major (E)
+  if (use == kGemmDenseEdgeGradBf16) return g.K % 8 == 0 && g.b_split >= g.N && !g.addend;   // both bf16 K-contig
   return false;
 }
 
@@ -1543,6 +1582,25 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
   const int64_t tiles64 = (int64_t)((g.M + kGBM - 1) / kGBM) * ((g.N + kGBM - 1) / kGBM) * zdim;
   const bool small = !fast && gemm_use_small_tile(use) && (g.M + 31) / 32 < 65536 &&
                      (forced ? forced == 32 : tiles64 < 256);
+  if (gemm_use_dense_bf16(use)) {
+    JN_REQUIRE(bf16_path_ok(g, use, splits), kUnsupported,
+               "%s needs M, N >= 128, N and the strides multiples of 8 and 16-byte aligned operands", info.name);
+    const int tm = (g.M + kBfT - 1) / kBfT, tn = (g.N + kBfT - 1) / kBfT;
+    const int64_t blocks = (int64_t)tm * tn * zdim;
+    JN_REQUIRE(blocks < (1LL << 31), kUnsupported, "GEMM grid too large");
+    JN_PROFILE(info.name, stream);
+    if (use == kGemmDenseAggregateBf16)
+      hipLaunchKernelGGL((gemm_bf16_kernel<true, false, false, true, true, kGemmDenseAggregateBf16>),
+                         dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
+    else if (use == kGemmDenseValueGradBf16)
+      hipLaunchKernelGGL((gemm_bf16_kernel<false, false, false, true, true, kGemmDenseValueGradBf16>),
+                         dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
+    else
+      hipLaunchKernelGGL((gemm_bf16_kernel<true, true, true, true, false, kGemmDenseEdgeGradBf16>),
+                         dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
+    JN_LAUNCH_CHECK();
+    return kOk;
+  }
   if (gemm_use_bf16(use) && forced != 32 && forced != 64 && bf16_path_ok(g, use, splits)) {
     const int tm = (g.M + kBfT - 1) / kBfT, tn = (g.N + kBfT - 1) / kBfT;
     const int64_t blocks = (int64_t)tm * tn * zdim;
@@ -1631,7 +1689,8 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
 
 // Batched C_b = op(A_b) . op(B_b) for b < batch (see BatchedGemm).
 int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
-  JN_REQUIRE(((use >= kGemmDenseScores && use <= kGemmRouteTargetGrad) || use == kGemmSelectScores) &&
+  JN_REQUIRE(((use >= kGemmDenseScores && use <= kGemmRouteTargetGrad) || use == kGemmSelectScores ||
+              gemm_use_dense_bf16(use)) &&
                  m.a_kcontig == kGemmUses[use].a_kc &&
                  m.b_kcontig == kGemmUses[use].b_kc,
              kInvalidArgument, "batched GEMM layout does not match its use");
@@ -1651,7 +1710,8 @@ int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream) {
              kInvalidArgument, "a causal K range needs a square A over one element's nodes");
   g.causal_k = m.causal_k;
   if (m.epi) {
-    JN_REQUIRE((use == kGemmDenseScores || use == kGemmDenseEdgeGrad) && m.M == m.N && m.epi_ps && m.epi_part &&
+    JN_REQUIRE((use == kGemmDenseScores || use == kGemmDenseEdgeGrad || use == kGemmDenseEdgeGradBf16) &&
+                   m.M == m.N && m.epi_ps && m.epi_part &&
                    (use == kGemmDenseScores || (m.epi_gds && m.epi_E)) && m.addend == nullptr &&
                    m.c_nscale == nullptr && m.c_mscale == nullptr,
                kInvalidArgument, "softsign epilogue needs a square dense score use and its operands");

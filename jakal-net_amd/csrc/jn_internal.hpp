@@ -128,6 +128,9 @@ enum GemmUse {
   kGemmRouteTargetGrad,
   kGemmProjectBf16, kGemmGradInputBf16, kGemmGradWeightBf16,
   kGemmSelectScores,
+  // bf16 dense layers: E . pv and E^T . gdv with E rounded to bf16 (bf16 C),
+  // gdv . pv^T from bf16 operands (fp32 C, softsign epilogue as dense_edge_grad)
+  kGemmDenseAggregateBf16, kGemmDenseValueGradBf16, kGemmDenseEdgeGradBf16,
 };
 int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream);
 // Workgroup tile of every later GEMM launch: 0 = chosen per call, 64 or 128 = forced.

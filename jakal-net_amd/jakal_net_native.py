@@ -205,7 +205,9 @@ _declare("jn_unit_scale_backward", [_P, _P, _I64, _I64, _F, _P, _P])
 
 # bf16 layers: the fp32 entry points' argument lists with bf16 value tensors
 for _name in ("jn_propagation_topk_forward", "jn_propagation_topk_backward", "jn_propagation_window_forward",
-              "jn_propagation_window_backward", "jn_transition_topk_forward", "jn_transition_topk_backward"):
+              "jn_propagation_window_backward", "jn_transition_topk_forward", "jn_transition_topk_backward",
+              "jn_propagation_dense_forward", "jn_propagation_dense_backward", "jn_propagation_dense_forward_chunked",
+              "jn_propagation_dense_backward_chunked"):
     _declare(_name + "_bf16", list(getattr(_LIB, _name).argtypes))
 
 ABI_VERSION = int(_LIB.jn_abi_version())
@@ -574,10 +576,17 @@ class _PropagationDense(torch.autograd.Function):
     """Differentiable dense low-rank propagation on the HIP library.  Inputs as
     _PropagationEdges; causal keeps only sources j <= i in row i.  Small
     problems keep the edge matrix for the backward; larger ones run in batch
-    chunks of at most DENSE_EDGE_BYTES of edges and rebuild them."""
+    chunks of at most DENSE_EDGE_BYTES of edges and rebuild them.  With bf16,
+    X and pv are bf16 and delta_val comes back in bf16 (the *_bf16 entry
+    points); the edge matrix stays fp32."""
 
     @staticmethod
-    def forward(ctx, X, ps, pv, V, U, w_hat, bias, compress: int, causal: bool = False):  # noqa: N803
+    def _entry(name: str, bf16: bool):
+        return getattr(_LIB, name + "_bf16" if bf16 else name)
+
+    @staticmethod
+    def forward(ctx, X, ps, pv, V, U, w_hat, bias, compress: int, causal: bool = False,  # noqa: N803
+                bf16: bool = False):
         B, N, Din = X.shape
         pv_is_x = pv is None
         pv_t = X if pv_is_x else pv
@@ -588,12 +597,12 @@ class _PropagationDense(torch.autograd.Function):
         chunk = B if B * edge_bytes <= DENSE_EDGE_BYTES else max(1, DENSE_EDGE_BYTES // edge_bytes)
         with torch.cuda.device(dev):
             ds = torch.empty(B, N, device=dev, dtype=torch.float32)
-            dv = torch.empty(B, N, Dout, device=dev, dtype=torch.float32)
+            dv = torch.empty(B, N, Dout, device=dev, dtype=torch.bfloat16 if bf16 else torch.float32)
             proj = torch.empty(B * N, 2 * r, device=dev, dtype=torch.float32)
             if chunk >= B:
                 edges = torch.empty(B, N, N, device=dev, dtype=torch.float32)
                 _check(
-                    _LIB.jn_propagation_dense_forward(
+                    _PropagationDense._entry("jn_propagation_dense_forward", bf16)(
                         _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
                         B, N, Din, Dout, r, compress, 1 if causal else 0, _ptr(ds), _ptr(dv), _ptr(proj),
                         _ptr(edges), _stream(dev),
@@ -605,21 +614,21 @@ class _PropagationDense(torch.autograd.Function):
                                                                                  chunk, 0))
                 edges = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
                 _check(
-                    _LIB.jn_propagation_dense_forward_chunked(
+                    _PropagationDense._entry("jn_propagation_dense_forward_chunked", bf16)(
                         _ptr(X), _ptr(ps), _ptr(pv_t), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias),
                         B, N, Din, Dout, r, compress, 1 if causal else 0, chunk, _ptr(ds), _ptr(dv), _ptr(proj),
                         _ptr(edges), ws_bytes, _stream(dev),
                     )
                 )
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, edges, bias)
-        ctx.meta = (compress, pv_is_x, bias is not None, bool(causal), chunk)
+        ctx.meta = (compress, pv_is_x, bias is not None, bool(causal), chunk, bool(bf16))
         ctx.edges_consumed = False
         return ds, dv
 
     @staticmethod
     def backward(ctx, g_ds, g_dv):
         X, ps, pv, V, U, w_hat, proj, edges, bias = ctx.saved_tensors
-        compress, pv_is_x, has_bias, causal, chunk = ctx.meta
+        compress, pv_is_x, has_bias, causal, chunk, bf16 = ctx.meta
         # a softsign backward writes the score gradient over the saved edge
         # matrix (no [B, N, N] workspace); a later backward (retain_graph)
         # rebuilds the edges there from the saved projections, as the chunked
@@ -634,8 +643,9 @@ class _PropagationDense(torch.autograd.Function):
         dev = X.device
         need = ctx.needs_input_grad
         with torch.cuda.device(dev):
+            vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
-            g_dv = torch.zeros(B, N, Dout, device=dev) if g_dv is None else g_dv.float().contiguous()
+            g_dv = torch.zeros(B, N, Dout, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
             gX = torch.empty_like(X) if need[0] else None
             gps = torch.empty_like(ps) if need[1] else None
             gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
@@ -644,7 +654,7 @@ class _PropagationDense(torch.autograd.Function):
             ws_bytes = int(_LIB.jn_propagation_dense_workspace_bytes(B, N, Din, Dout, r, compress, reuse))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
             _check(
-                _LIB.jn_propagation_dense_backward(
+                _PropagationDense._entry("jn_propagation_dense_backward", bf16)(
                     _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(proj), _ptr(edges),
                     _ptr(g_ds), _ptr(g_dv), B, N, Din, Dout, r, compress, 1 if causal else 0, 1 if pv_is_x else 0,
                     reuse, _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV), _ptr(gw), _ptr(gb),
@@ -652,11 +662,11 @@ class _PropagationDense(torch.autograd.Function):
                 )
             )
         return (gX, gps, gpv, gV if need[3] else None, gU if need[4] else None, gw if need[5] else None,
-                gb if (has_bias and need[6]) else None, None, None)
+                gb if (has_bias and need[6]) else None, None, None, None)
 
     @staticmethod
     def _backward_chunked(ctx, X, ps, pv, V, U, w_hat, proj, edge_chunk, bias, g_ds, g_dv):
-        compress, pv_is_x, has_bias, causal, chunk = ctx.meta
+        compress, pv_is_x, has_bias, causal, chunk, bf16 = ctx.meta
         chunk = min(chunk, X.shape[0])  # a whole saved edge matrix is one chunk
         # the chunk buffer holds the forward's last chunk until a softsign
         # backward writes its gradient there; a later backward rebuilds it too
@@ -668,8 +678,9 @@ class _PropagationDense(torch.autograd.Function):
         dev = X.device
         need = ctx.needs_input_grad
         with torch.cuda.device(dev):
+            vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
-            g_dv = torch.zeros(B, N, Dout, device=dev) if g_dv is None else g_dv.float().contiguous()
+            g_dv = torch.zeros(B, N, Dout, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
             gX = torch.empty_like(X) if need[0] else None
             gps = torch.empty_like(ps) if need[1] else None
             gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
@@ -678,7 +689,7 @@ class _PropagationDense(torch.autograd.Function):
             ws_bytes = int(_LIB.jn_propagation_dense_chunked_workspace_bytes(B, N, Din, Dout, r, compress, chunk, 1))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
             _check(
-                _LIB.jn_propagation_dense_backward_chunked(
+                _PropagationDense._entry("jn_propagation_dense_backward_chunked", bf16)(
                     _ptr(X), _ptr(ps), _ptr(pv), _ptr(U), _ptr(V), _ptr(w_hat), _ptr(bias), _ptr(proj),
                     _ptr(edge_chunk), _ptr(g_ds), _ptr(g_dv), B, N, Din, Dout, r, compress, 1 if causal else 0,
                     1 if pv_is_x else 0, chunk, resident, _ptr(gX), _ptr(gps), _ptr(gpv), _ptr(gU), _ptr(gV),
@@ -686,7 +697,7 @@ class _PropagationDense(torch.autograd.Function):
                 )
             )
         return (gX, gps, gpv, gV if need[3] else None, gU if need[4] else None, gw if need[5] else None,
-                gb if (has_bias and need[6]) else None, None, None)
+                gb if (has_bias and need[6]) else None, None, None, None)
 
 
 class _PropagationDenseMultihead(torch.autograd.Function):
@@ -762,6 +773,12 @@ class _PropagationDenseMultihead(torch.autograd.Function):
                 gb if (has_bias and need[6]) else None, None, None, None)
 
 
+def dense_bf16_shapes_ok(nodes: int, out_dim: int) -> bool:
+    """Whether a bf16 dense layer of these sizes runs on the bf16 entry points
+    (their N x N products need 128 x 128 tiles of 8-element rows)."""
+    return nodes >= 128 and out_dim >= 128 and nodes % 8 == 0 and out_dim % 8 == 0
+
+
 def propagation_dense(
     pairwise_kind: str,
     weight: Tensor,
@@ -801,15 +818,19 @@ def propagation_dense(
     N, Din = layer_val.shape[-2], layer_val.shape[-1]
     Dout = projected_val.shape[-1]
     pv_is_x = _same_storage_view(projected_val, layer_val)
-    X = _f32(layer_val.reshape(-1, N, Din))
+    # bf16 layers keep bf16 value rows on the bf16 MFMA products when the
+    # shapes fit their tiles (one head); anything else computes in fp32
+    bf16 = heads == 1 and _bf16_rows(layer_val, projected_val) and dense_bf16_shapes_ok(N, Dout)
+    rows = _bf16 if bf16 else _f32
+    X = rows(layer_val.reshape(-1, N, Din))
     ps = _f32(projected_state.reshape(-1, N))
-    pv = None if pv_is_x else _f32(projected_val.reshape(-1, N, Dout))
+    pv = None if pv_is_x else rows(projected_val.reshape(-1, N, Dout))
     if heads > 1:
         ds, dv = _PropagationDenseMultihead.apply(X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias),
                                                   _COMPRESS_KINDS[edge_compress_name], _causal, heads)
     else:
         ds, dv = _PropagationDense.apply(X, ps, pv, _f32(V), _f32(U), _f32(w_hat), _f32(bias),
-                                         _COMPRESS_KINDS[edge_compress_name], _causal)
+                                         _COMPRESS_KINDS[edge_compress_name], _causal, bf16)
     return (ds.reshape(*batch_shape, N).to(projected_state.dtype),
             dv.reshape(*batch_shape, N, Dout).to(projected_val.dtype))
 

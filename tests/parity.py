@@ -115,7 +115,7 @@ def _linear32(x, W, bf16_linear):
 
 
 def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, chunk=4,
-                        bf16_operands=False, bf16_linear=None) -> dict:
+                        bf16_operands=False, bf16_linear=None, bf16_edges=False) -> dict:
     """fp32 torch forward + autograd backward of low-rank propagation on a given mask.
 
     val [B,N,D], ps [B,N], pv [B,N,Dv] or None (pv is val itself), U/V [r,D],
@@ -126,7 +126,9 @@ def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, 
     ps, pv, U, V, w_hat, b.  bf16_operands: the score is
     bf16(P_t * w_hat) . bf16(P_s), the operands of the bf16 top-k select.
     bf16_linear (default: bf16_operands): the projections as the bf16 entry
-    points compute them (_linear32)."""
+    points compute them (_linear32).  bf16_edges: the edge matrix rounded to
+    bf16 (straight-through) where it multiplies the values, as the bf16 dense
+    entry points' E . pv and E^T . gdv take it."""
     if bf16_linear is None:
         bf16_linear = bf16_operands
     f32 = dict(device=dev, dtype=torch.float32)
@@ -160,7 +162,7 @@ def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, 
                 s = s + bd
         e = _compress32(s, m, kind)
         ds = (e * p_s[:, None, :]).sum(-1)
-        dv = e @ p_v
+        dv = (_bf16_st(e) if bf16_edges else e) @ p_v
         loss = (ds * torch.as_tensor(gds[b0:b1]).to(**f32)).sum() + (dv * torch.as_tensor(gdv[b0:b1]).to(**f32)).sum()
         leaves = [x, p_s] + ([p_v] if pv is not None else []) + params
         grads = torch.autograd.grad(loss, leaves)

@@ -7,8 +7,10 @@ bf16(q * w) . bf16(key) on bf16 MFMAs.  Outputs and the gradients that reach
 the bf16 leaves differ from the oracle -- evaluated on the same bf16 inputs --
 by bf16 rounding: rtol 2e-2, the bf16 tolerance of the hot path.  Index
 parity is exact on rows whose k-th/(k+1)-th gap exceeds twice the bound of
-the operand rounding (tests/parity.py, bf16_select_scores); the dense path
-computes in fp32 from the bf16 inputs.
+the operand rounding (tests/parity.py, bf16_select_scores).  Dense layers of
+at least 128 nodes and value columns (multiples of 8) run their N x N
+products on bf16 MFMA with the fp32 edge matrix rounded to bf16 where it
+multiplies values; smaller ones compute in fp32 from the bf16 inputs.
 """
 
 import math
@@ -94,13 +96,91 @@ def run_bf16_propagation(dev, mode, B, N, D, r, k=8, seed=5001):
     mask = O.propagation_forward(_np(val), _np(state), _np(val), _np(U), _np(V), _np(w), 0.0, kind="softsign",
                                  **kw)["mask"]
     # the top-k scores come from bf16 operands; window and dense scores are fp32;
-    # the top-k and window projections are bf16 GEMMs (dense upcasts to fp32)
+    # the projections are bf16 GEMMs, except for dense layers off the bf16
+    # dense path (upcast to fp32), whose edges multiply the values in bf16
+    dense_bf16 = mode == "dense" and jn.dense_bf16_shapes_ok(N, D)
     t = torch32_propagation(dev, val, state, None, U, V, w / w.norm(), None, np.ascontiguousarray(mask), "softsign",
-                            gds, gdv, bf16_operands=mode == "topk", bf16_linear=mode != "dense")
+                            gds, gdv, bf16_operands=mode == "topk", bf16_linear=mode != "dense" or dense_bf16,
+                            bf16_edges=dense_bf16)
     check_bf16_calibrated("delta_state", ds, gr["delta_state"], t["delta_state"])
     check_bf16_calibrated("delta_val", dv, gr["delta_val"], t["delta_val"])
     check_bf16_calibrated("grad layer_val", X.grad, gr["val"] + gr["pv"], t["val"])
     check_bf16_calibrated("grad projected_state", ps.grad, gr["ps"], t["ps"])
+
+
+def test_bf16_dense_layer_runs_bf16_products(dev):
+    """A bf16 dense layer at the bf16 dense entry points' sizes (softsign, pv
+    the layer values): the three N x N products on bf16 MFMA, the edge matrix
+    rounded to bf16 where it multiplies values."""
+    import jakal_net_native as jn
+
+    assert jn.dense_bf16_shapes_ok(256, 128) and not jn.dense_bf16_shapes_ok(256, 120)
+    run_bf16_propagation(dev, "dense", B=2, N=256, D=128, r=16, seed=5021)
+
+
+@pytest.fixture
+def chunk_batches():
+    import jakal_net_native as jn
+
+    def use(n, N):
+        jn.set_dense_edge_bytes(n * N * N * 4)
+
+    yield use
+    jn.set_dense_edge_bytes()
+
+
+# (compress, causal, separate_pv, chunk): the signed kinds' separate score
+# gradient pass, the causal K ranges and epilogue tiles, batch chunks
+@pytest.mark.parametrize("compress,causal,separate_pv,chunk", [
+    ("softsign", True, True, None),
+    ("signed_abs_softmax", False, True, None),
+    ("signed_entmax15", True, False, 1),
+    ("softsign", False, True, 2),
+])
+def test_bf16_dense_variants(dev, chunk_batches, compress, causal, separate_pv, chunk):
+    import jakal_net_native as jn
+
+    B, N, D, r = 3, 264, 136, 24
+    if chunk:
+        chunk_batches(chunk, N)
+    g, U, V, w = _pairwise_params(5031, D, r)
+    val = torch.randn(B, N, D, generator=g).bfloat16()
+    state = torch.randn(B, N, generator=g).bfloat16()
+    pv_cpu = torch.randn(B, N, D, generator=g).bfloat16() if separate_pv else val
+    b = 0.15
+    X = val.to(dev).requires_grad_(True)
+    ps = state.to(dev).requires_grad_(True)
+    pv = pv_cpu.to(dev).requires_grad_(True) if separate_pv else X
+    w_hat = w / w.norm()
+    Ud, Vd, wd = (t.to(dev).requires_grad_(True) for t in (U, V, w_hat))
+    bd = torch.tensor(b, device=dev, requires_grad=True)
+    args = ("low_rank_bilinear", wd, bd, Vd, None, Ud, None, compress, X, ps, pv)
+    if causal:
+        ds, dv = jn.propagation_window(*args, N - 1, N, N)
+        kw = dict(mode="window", window=N - 1)
+        mask = np.broadcast_to(O.causal_window_mask(N, N - 1), (B, N, N))
+    else:
+        ds, dv = jn.propagation_dense(*args, None, N, N)
+        kw = dict(mode="dense")
+        mask = np.ones((B, N, N), dtype=bool)
+    assert ds.dtype == torch.bfloat16 and dv.dtype == torch.bfloat16
+    gds = torch.randn(B, N, generator=g).bfloat16()
+    gdv = torch.randn(B, N, D, generator=g).bfloat16()
+    torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
+    gr = O.propagation_backward(_np(val), _np(state), _np(pv_cpu), _np(U), _np(V), _np(w), b, _np(gds), _np(gdv),
+                                kind=compress, **kw)
+    t = torch32_propagation(dev, val, state, pv_cpu if separate_pv else None, U, V, w_hat, b,
+                            np.ascontiguousarray(mask), compress, gds, gdv, bf16_linear=True, bf16_edges=True)
+    check_bf16_calibrated("delta_state", ds, gr["delta_state"], t["delta_state"])
+    check_bf16_calibrated("delta_val", dv, gr["delta_val"], t["delta_val"])
+    if separate_pv:
+        check_bf16_calibrated("grad layer_val", X.grad, gr["val"], t["val"])
+        check_bf16_calibrated("grad projected_val", pv.grad, gr["pv"], t["pv"])
+    else:
+        check_bf16_calibrated("grad layer_val", X.grad, gr["val"] + gr["pv"], t["val"])
+    check_bf16_calibrated("grad projected_state", ps.grad, gr["ps"], t["ps"])
+    for p, name in ((Ud, "U"), (Vd, "V"), (wd, "w_hat"), (bd, "b")):
+        check_bf16_calibrated(f"grad {name}", p.grad, gr[name], t[name])
 
 
 # min_ok: the fraction of rows whose k-th / (k+1)-th gap exceeds twice the bf16

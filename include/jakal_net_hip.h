@@ -36,7 +36,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 12. */
+/* ABI revision of this header (bumped on any signature change); this is 13. */
 int jn_abi_version(void);
 
 /*
@@ -693,6 +693,32 @@ int jn_propagation_dense_backward_chunked_bf16(
     uint16_t* grad_layer_val, float* grad_projected_state, uint16_t* grad_projected_val, float* grad_target_weight,
     float* grad_source_weight, float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes,
     jn_stream_t stream);
+
+/*
+ * bf16 dense transitions (one head): jn_transition_dense_* with bf16 value
+ * tensors (src_val, dst_val, projected_val, delta_val and their gradients),
+ * the other arguments and the workspace query as for fp32.  The route matrix
+ * stays fp32: R^T diag(rho) pv takes R rho rounded to bf16, diag(rho) R gdv
+ * takes R rounded to bf16, pv . gdv^T multiplies the bf16 rows exactly; all
+ * accumulate in fp32 on v_mfma_f32_16x16x32_bf16.  src_nodes, dst_nodes and
+ * val_dim must be at least 128 and multiples of 8 (kUnsupported otherwise).
+ */
+int jn_transition_dense_forward_bf16(const float* sender_strength, const uint16_t* src_val, const uint16_t* dst_val,
+                                     const float* projected_state, const uint16_t* projected_val,
+                                     const float* source_weight, const float* target_weight, const float* core_weight,
+                                     const float* bias, float temperature, int64_t batch, int64_t src_nodes,
+                                     int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim,
+                                     int64_t rank, int32_t compress_kind, float* delta_state, uint16_t* delta_val,
+                                     float* src_proj, float* dst_proj, float* routes, jn_stream_t stream);
+int jn_transition_dense_backward_bf16(
+    const float* sender_strength, const uint16_t* src_val, const uint16_t* dst_val, const float* projected_state,
+    const uint16_t* projected_val, const float* source_weight, const float* target_weight, const float* core_weight,
+    const float* src_proj, const float* dst_proj, const float* routes, const float* grad_delta_state,
+    const uint16_t* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+    int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int32_t compress_kind,
+    float* grad_sender_strength, uint16_t* grad_src_val, uint16_t* grad_dst_val, float* grad_projected_state,
+    uint16_t* grad_projected_val, float* grad_source_weight, float* grad_target_weight, float* grad_core_weight,
+    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream);
 
 /*
  * Score scale vector of the low-rank pairwise scores: weight_hat[h] =

@@ -1197,7 +1197,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 12; }
+int jn_abi_version(void) { return 13; }
 
 int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float eps, float* weight_hat,
                           jn_stream_t stream) {
@@ -2278,6 +2278,19 @@ int jn_propagation_dense_backward_chunked_bf16(
 // Dense transition forward; heads > 1: max-aggregated route logits over the
 // heads' rank slices (rank = heads * head rank, bias [heads]), the winning
 // head of every (source, destination) pair in route_heads [B, Ns, Nd].
+// bf16 dense transitions (one head): the bf16 MFMA kernel runs the three
+// Ns x Nd products, so its preconditions hold.
+static int check_transition_dense_bf16_shapes(int64_t src_nodes, int64_t dst_nodes, int64_t val_dim, int64_t heads) {
+  JN_REQUIRE(heads == 1, kUnsupported, "bf16 dense transitions have one head");
+  JN_REQUIRE(src_nodes >= 128 && dst_nodes >= 128 && val_dim >= 128 && src_nodes % 8 == 0 && dst_nodes % 8 == 0 &&
+                 val_dim % 8 == 0,
+             kUnsupported,
+             "bf16 dense transitions need src_nodes, dst_nodes and val_dim >= 128 and multiples of 8 (got %lld, %lld, "
+             "%lld)",
+             (long long)src_nodes, (long long)dst_nodes, (long long)val_dim);
+  return kOk;
+}
+
 static int transition_dense_forward_impl(const float* sender_strength, const float* src_val, const float* dst_val,
                                          const float* projected_state, const float* projected_val,
                                          const float* source_weight, const float* target_weight,
@@ -2286,10 +2299,11 @@ static int transition_dense_forward_impl(const float* sender_strength, const flo
                                          int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
                                          int32_t compress_kind, float* delta_state, float* delta_val,
                                          float* src_proj, float* dst_proj, float* routes, uint8_t* route_heads,
-                                         jn_stream_t stream) {
+                                         jn_stream_t stream, bool bf16 = false) {
   int rc = check_transition_dense_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, compress_kind,
                                          temperature);
   if (rc) return rc;
+  if (bf16 && (rc = check_transition_dense_bf16_shapes(src_nodes, dst_nodes, val_dim, heads))) return rc;
   JN_REQUIRE(heads == 1 || route_heads, kInvalidArgument, "null tensor pointer");
   JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
                  target_weight && core_weight && delta_state && delta_val && src_proj && dst_proj && routes,
@@ -2299,10 +2313,10 @@ static int transition_dense_forward_impl(const float* sender_strength, const flo
 
   // 1. projections P_s = src . Ws^T, P_t = dst . Wt^T  (modules.py:435-437)
   rc = gemm_project(src_val, src_dim, source_weight, source_weight, r, src_dim, src_proj, r, B * Ns, r, (int)src_dim,
-                    st);
+                    st, bf16);
   if (rc) return rc;
   rc = gemm_project(dst_val, dst_dim, target_weight, target_weight, r, dst_dim, dst_proj, r, B * Nd, r, (int)dst_dim,
-                    st);
+                    st, bf16);
   if (rc) return rc;
   // 2. raw logits L_b = (P_s diag(w)) P_t^T; with heads, max_h of each head's
   //    logits plus its bias (one GEMM per head, folded in the epilogue)
@@ -2333,7 +2347,7 @@ static int transition_dense_forward_impl(const float* sender_strength, const flo
   ag.C = delta_val; ag.ldc = Dv; ag.c_bs = (int64_t)Nd * Dv;
   ag.a_kscale = sender_strength; ag.ks_bs = Ns;
   ag.M = Nd; ag.N = Dv; ag.K = Ns; ag.batch = B;
-  return gemm_batched(ag, kGemmRouteAggregate, st);
+  return gemm_batched(ag, bf16 ? kGemmRouteAggregateBf16 : kGemmRouteAggregate, st);
 }
 
 int jn_transition_dense_forward(const float* sender_strength, const float* src_val, const float* dst_val,
@@ -2364,10 +2378,12 @@ static int transition_dense_backward_impl(
     int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int64_t heads,
     int32_t compress_kind, float* grad_sender_strength, float* grad_src_val, float* grad_dst_val,
     float* grad_projected_state, float* grad_projected_val, float* grad_source_weight, float* grad_target_weight,
-    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+    float* grad_core_weight, float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream,
+    bool bf16 = false) {
   int rc = check_transition_dense_shapes(batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, compress_kind,
                                          temperature);
   if (rc) return rc;
+  if (bf16 && (rc = check_transition_dense_bf16_shapes(src_nodes, dst_nodes, val_dim, heads))) return rc;
   JN_REQUIRE(sender_strength && src_val && dst_val && projected_state && projected_val && source_weight &&
                  target_weight && core_weight && src_proj && dst_proj && routes && grad_delta_state &&
                  grad_delta_val && (heads == 1 || route_heads),
@@ -2385,7 +2401,7 @@ static int transition_dense_backward_impl(
   hg.B = grad_delta_val; hg.ldb = Dv; hg.b_bs = (int64_t)Nd * Dv; hg.b_kcontig = true;
   hg.C = s.G; hg.ldc = Nd; hg.c_bs = (int64_t)Ns * Nd;
   hg.M = Ns; hg.N = Nd; hg.K = Dv; hg.batch = B;
-  rc = gemm_batched(hg, kGemmRouteEdgeGrad, st);
+  rc = gemm_batched(hg, bf16 ? kGemmRouteEdgeGradBf16 : kGemmRouteEdgeGrad, st);
   if (rc) return rc;
   rc = launch_route_dense_compress_backward(s.G, routes, sender_strength, projected_state, grad_delta_state, B, Ns,
                                             Nd, compress_kind, 1.0f / temperature, grad_sender_strength,
@@ -2399,7 +2415,7 @@ static int transition_dense_backward_impl(
     vg.C = grad_projected_val; vg.ldc = Dv; vg.c_bs = (int64_t)Ns * Dv;
     vg.c_mscale = sender_strength; vg.ms_bs = Ns;
     vg.M = Ns; vg.N = Dv; vg.K = Nd; vg.batch = B;
-    rc = gemm_batched(vg, kGemmRouteValueGrad, st);
+    rc = gemm_batched(vg, bf16 ? kGemmRouteValueGradBf16 : kGemmRouteValueGrad, st);
     if (rc) return rc;
   }
   // multi-head: each pair's logit gradient reaches its winning head only (per-head
@@ -2437,22 +2453,22 @@ static int transition_dense_backward_impl(
   const int Ms = B * Ns, Mt = B * Nd;
   if (grad_source_weight) {
     rc = gemm_grad_weight(s.dPs, r, src_val, src_dim, grad_source_weight, grad_source_weight, r, r, (int)src_dim, Ms,
-                          s.splitk, st);
+                          s.splitk, st, bf16);
     if (rc) return rc;
   }
   if (grad_target_weight) {
     rc = gemm_grad_weight(s.dPt, r, dst_val, dst_dim, grad_target_weight, grad_target_weight, r, r, (int)dst_dim, Mt,
-                          s.splitk, st);
+                          s.splitk, st, bf16);
     if (rc) return rc;
   }
   if (grad_src_val) {
     rc = gemm_grad_input(s.dPs, r, source_weight, source_weight, r, src_dim, nullptr, src_dim, grad_src_val, src_dim,
-                         Ms, (int)src_dim, r, st);
+                         Ms, (int)src_dim, r, st, bf16);
     if (rc) return rc;
   }
   if (grad_dst_val) {
     rc = gemm_grad_input(s.dPt, r, target_weight, target_weight, r, dst_dim, nullptr, dst_dim, grad_dst_val, dst_dim,
-                         Mt, (int)dst_dim, r, st);
+                         Mt, (int)dst_dim, r, st, bf16);
     if (rc) return rc;
   }
   // 5. w and bias grads (one head: exactly 0 for softmax routes, since shifting a
@@ -2479,6 +2495,39 @@ int jn_transition_dense_backward(const float* sender_strength, const float* src_
       src_dim, dst_dim, val_dim, rank, 1, compress_kind, grad_sender_strength, grad_src_val, grad_dst_val,
       grad_projected_state, grad_projected_val, grad_source_weight, grad_target_weight, grad_core_weight, grad_bias,
       workspace, workspace_bytes, stream);
+}
+
+int jn_transition_dense_forward_bf16(const float* sender_strength, const uint16_t* src_val, const uint16_t* dst_val,
+                                     const float* projected_state, const uint16_t* projected_val,
+                                     const float* source_weight, const float* target_weight, const float* core_weight,
+                                     const float* bias, float temperature, int64_t batch, int64_t src_nodes,
+                                     int64_t dst_nodes, int64_t src_dim, int64_t dst_dim, int64_t val_dim,
+                                     int64_t rank, int32_t compress_kind, float* delta_state, uint16_t* delta_val,
+                                     float* src_proj, float* dst_proj, float* routes, jn_stream_t stream) {
+  return transition_dense_forward_impl(
+      sender_strength, reinterpret_cast<const float*>(src_val), reinterpret_cast<const float*>(dst_val),
+      projected_state, reinterpret_cast<const float*>(projected_val), source_weight, target_weight, core_weight, bias,
+      temperature, batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, 1, compress_kind, delta_state,
+      reinterpret_cast<float*>(delta_val), src_proj, dst_proj, routes, nullptr, stream, true);
+}
+
+int jn_transition_dense_backward_bf16(
+    const float* sender_strength, const uint16_t* src_val, const uint16_t* dst_val, const float* projected_state,
+    const uint16_t* projected_val, const float* source_weight, const float* target_weight, const float* core_weight,
+    const float* src_proj, const float* dst_proj, const float* routes, const float* grad_delta_state,
+    const uint16_t* grad_delta_val, float temperature, int64_t batch, int64_t src_nodes, int64_t dst_nodes,
+    int64_t src_dim, int64_t dst_dim, int64_t val_dim, int64_t rank, int32_t compress_kind,
+    float* grad_sender_strength, uint16_t* grad_src_val, uint16_t* grad_dst_val, float* grad_projected_state,
+    uint16_t* grad_projected_val, float* grad_source_weight, float* grad_target_weight, float* grad_core_weight,
+    float* grad_bias, void* workspace, size_t workspace_bytes, jn_stream_t stream) {
+  return transition_dense_backward_impl(
+      sender_strength, reinterpret_cast<const float*>(src_val), reinterpret_cast<const float*>(dst_val),
+      projected_state, reinterpret_cast<const float*>(projected_val), source_weight, target_weight, core_weight,
+      src_proj, dst_proj, routes, nullptr, grad_delta_state, reinterpret_cast<const float*>(grad_delta_val),
+      temperature, batch, src_nodes, dst_nodes, src_dim, dst_dim, val_dim, rank, 1, compress_kind,
+      grad_sender_strength, reinterpret_cast<float*>(grad_src_val), reinterpret_cast<float*>(grad_dst_val),
+      grad_projected_state, reinterpret_cast<float*>(grad_projected_val), grad_source_weight, grad_target_weight,
+      grad_core_weight, grad_bias, workspace, workspace_bytes, stream, true);
 }
 
 // ---- max-aggregated multi-head dense forms ---------------------------------

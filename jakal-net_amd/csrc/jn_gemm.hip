@@ -525,15 +525,19 @@ constexpr GemmUseInfo kGemmUses[] = {
     {true, false, false, false, "gemm_bf16_kernel<dense_aggregate_bf16>"},
     {false, false, false, false, "gemm_bf16_kernel<dense_value_grad_bf16>"},
     {true, true, false, false, "gemm_bf16_kernel<dense_edge_grad_bf16>"},
+    {false, false, true, false, "gemm_bf16_kernel<route_aggregate_bf16>"},
+    {true, false, false, false, "gemm_bf16_kernel<route_value_grad_bf16>"},
+    {true, true, false, false, "gemm_bf16_kernel<route_edge_grad_bf16>"},
 };
-static_assert(sizeof(kGemmUses) / sizeof(kGemmUses[0]) == kGemmDenseEdgeGradBf16 + 1, "one entry per GemmUse");
+static_assert(sizeof(kGemmUses) / sizeof(kGemmUses[0]) == kGemmRouteEdgeGradBf16 + 1, "one entry per GemmUse");
 constexpr bool gemm_use_bf16(GemmUse u) {
   return u == kGemmProjectBf16 || u == kGemmGradInputBf16 || u == kGemmGradWeightBf16;
 }
-// The bf16 dense uses run on the bf16 MFMA kernel only (their callers check
-// its preconditions first).
+// The bf16 dense and dense-route uses run on the bf16 MFMA kernel only (their
+// callers check its preconditions first).
 constexpr bool gemm_use_dense_bf16(int u) {
-  return u == kGemmDenseAggregateBf16 || u == kGemmDenseValueGradBf16 || u == kGemmDenseEdgeGradBf16;
+  return u == kGemmDenseAggregateBf16 || u == kGemmDenseValueGradBf16 || u == kGemmDenseEdgeGradBf16 ||
+         u == kGemmRouteAggregateBf16 || u == kGemmRouteValueGradBf16 || u == kGemmRouteEdgeGradBf16;
 }
 
 // ---- 128 x 128 path --------------------------------------------------------
@@ -944,11 +948,25 @@ constexpr int kBfStage = 64 + 4;    // epilogue row stride in floats
 // Operand loader of one slice: R = 128 rows (m or n) x 64 k into LDS [row][k].
 //   KC: row-major with k contiguous (row stride ld); else k-major (k rows of stride ld).
 //   BF: the source holds bf16; else fp32, rounded to bf16.
-template <bool KC, bool BF>
+//   KS: (k-major fp32 only) each element is first multiplied by a scale per k.
+template <bool KC, bool BF, bool KS = false>
 struct BfLoader {
+  static_assert(!KS || (!KC && !BF), "k scales apply to k-major fp32 operands");
   // 16-byte loads per thread and slice
   static constexpr int kLoads = KC ? (BF ? 4 : 8) : (BF ? 4 : 8);
   uint4 r[kLoads];
+  float4 sc[KS ? 2 : 1];  // the scales of a thread's two 4 x 4 blocks (k = 4 kb .. 4 kb + 3)
+
+  // the k scales of the slice's (from k0; ks_rs addresses the scale of k0)
+  __device__ __forceinline__ void load_scales(__amdgpu_buffer_rsrc_t ks_rs, int k0, int kend, int tid) {
+    if constexpr (KS) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kb = (tid + 256 * h) >> 5;
+        sc[h] = buf_load4(ks_rs, k0 + 4 * kb < kend ? (uint32_t)(16 * kb) : kOobOffset);
+      }
+    }
+  }
 
   // rs0 addresses the slice's (row 0, k = k0) -- offsets stay within one
   // slice of rows, so 32-bit offsets reach any K; K-contiguous rows from
@@ -1036,8 +1054,15 @@ struct BfLoader {
       for (int h = 0; h < 2; ++h) {
         const int blk = tid + 256 * h, kb = blk >> 5, rb = (blk & 31) * 4;
         const uint4* v = &r[4 * h];  // v[i]: k = 4 kb + i, rows rb .. rb + 3
-        const uint32_t c[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w}, {v[1].x, v[1].y, v[1].z, v[1].w},
-                                  {v[2].x, v[2].y, v[2].z, v[2].w}, {v[3].x, v[3].y, v[3].z, v[3].w}};
+        uint32_t c[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w}, {v[1].x, v[1].y, v[1].z, v[1].w},
+                            {v[2].x, v[2].y, v[2].z, v[2].w}, {v[3].x, v[3].y, v[3].z, v[3].w}};
+        if constexpr (KS) {
+          const float f[4] = {sc[h].x, sc[h].y, sc[h].z, sc[h].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) c[i][j] = __float_as_uint(__uint_as_float(c[i][j]) * f[i]);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           *reinterpret_cast<uint2*>(&s[(rb + j) * kBfS + 4 * kb]) =
@@ -1098,11 +1123,14 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g, int tiles
     return make_rsrc(origin + (kc ? k : k * ld) * eb, kFastRecords);
   };
 
-  BfLoader<A_KC, A_BF> la;
+  constexpr bool KS = kGemmUses[USE].a_kscale;  // A scaled along k (k-major fp32 A)
+  BfLoader<A_KC, A_BF, KS> la;
   BfLoader<B_KC, B_BF> lb;
+  [[maybe_unused]] const float* kscale = KS ? g.a_kscale + bz * g.ks_bs : nullptr;
   auto load_slice = [&](int k0) {
     const auto ars = at_k(abase, A_KC, lda, k0, AEB);
     la.load(ars, ars, 1 << 30, lda, m0, g.M, k0, kend, tid);
+    if constexpr (KS) la.load_scales(make_rsrc(kscale + k0, kFastRecords), k0, kend, tid);
     if constexpr (!B_KC) {
       if (k0 >= g.b_split) {
         const auto rs = at_k(b1base, false, ldb, (int64_t)k0 - g.b_split, BEB);
@@ -1176,6 +1204,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g, int tiles
   [[maybe_unused]] bf16_t* Cb = reinterpret_cast<bf16_t*>(g.C) + bz * g.c_bs;
   [[maybe_unused]] const bf16_t* addb =
       g.addend ? reinterpret_cast<const bf16_t*>(g.addend) + bz * g.add_bs : nullptr;
+  [[maybe_unused]] const float* mscale = g.c_mscale ? g.c_mscale + bz * g.ms_bs : nullptr;
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int r = it * 8 + (lane >> 3), c0 = (lane & 7) * 8;
@@ -1185,6 +1214,11 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g, int tiles
     const float4 x1 = *reinterpret_cast<const float4*>(&stage[r * kBfStage + c0 + 4]);
     if constexpr (C_BF) {
       float4 y0 = x0, y1 = x1;
+      if (mscale) {  // C row m scaled (the route value gradient's diag(rho))
+        const float sm = mscale[m];
+        y0.x *= sm; y0.y *= sm; y0.z *= sm; y0.w *= sm;
+        y1.x *= sm; y1.y *= sm; y1.z *= sm; y1.w *= sm;
+      }
       if (addb) {
         const uint4 ab = load_nt16(&addb[(int64_t)m * g.ld_add + n]);
         float a0, a1;
@@ -1210,8 +1244,10 @@ static bool bf16_path_ok(const GemmArgs& g, int use, int splits) {
   if (g.lda >= (1 << 20) || g.ldb >= (1 << 20)) return false;
   if (!al16(g.A) || !al16(g.B0) || !al16(g.B1) || !al16(g.C)) return false;
   if (g.addend && (g.ld_add % 8 != 0 || g.add_bs % 8 != 0 || !al16(g.addend))) return false;
-  if (g.a_kscale || g.c_nscale || g.c_mscale || g.fold || g.a_heads) return false;
+  if (g.c_nscale || g.fold || g.a_heads) return false;
   if (g.epi && use != kGemmDenseEdgeGradBf16) return false;
+  if (g.a_kscale && (use != kGemmRouteAggregateBf16 || !al16(g.a_kscale) || g.ks_bs % 4 != 0)) return false;
+  if (g.c_mscale && use != kGemmRouteValueGradBf16) return false;
   if (splits > 1 && g.k_chunk % kBfK != 0) return false;
   if (use == kGemmProjectBf16) return g.K % 8 == 0 && g.b_split % 16 == 0;          // A bf16, B fp32, K-contiguous
   if (use == kGemmGradInputBf16) return g.K % 4 == 0 && g.b_split % kBfK == 0;       // A fp32 K-contig, B fp32 K-major
@@ -1219,6 +1255,10 @@ static bool bf16_path_ok(const GemmArgs& g, int use, int splits) {
   if (use == kGemmDenseAggregateBf16) return g.K % 4 == 0 && g.b_split >= g.K && !g.addend;  // A fp32 K-contig (E)
   if (use == kGemmDenseValueGradBf16) return g.M % 4 == 0 && g.b_split >= g.K && !g.addend;  // A fp32 K-major (E)
   if (use == kGemmDenseEdgeGradBf16) return g.K % 8 == 0 && g.b_split >= g.N && !g.addend;   // both bf16 K-contig
+  if (use == kGemmRouteAggregateBf16)  // A fp32 K-major (R^T, k-scaled), B bf16 K-major
+    return g.M % 4 == 0 && g.K % 4 == 0 && g.a_kscale && g.b_split >= g.K && !g.addend;
+  if (use == kGemmRouteValueGradBf16) return g.K % 4 == 0 && g.b_split >= g.K && !g.addend;  // A fp32 K-contig (R)
+  if (use == kGemmRouteEdgeGradBf16) return g.K % 8 == 0 && g.b_split >= g.N && !g.addend;   // both bf16 K-contig
   return false;
 }
 
@@ -1595,8 +1635,17 @@ int launch_gemm(const GemmArgs& g, GemmUse use, int splits, hipStream_t stream) 
     else if (use == kGemmDenseValueGradBf16)
       hipLaunchKernelGGL((gemm_bf16_kernel<false, false, false, true, true, kGemmDenseValueGradBf16>),
                          dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
-    else
+    else if (use == kGemmDenseEdgeGradBf16)
       hipLaunchKernelGGL((gemm_bf16_kernel<true, true, true, true, false, kGemmDenseEdgeGradBf16>),
+                         dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
+    else if (use == kGemmRouteAggregateBf16)
+      hipLaunchKernelGGL((gemm_bf16_kernel<false, false, false, true, true, kGemmRouteAggregateBf16>),
+                         dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
+    else if (use == kGemmRouteValueGradBf16)
+      hipLaunchKernelGGL((gemm_bf16_kernel<true, false, false, true, true, kGemmRouteValueGradBf16>),
+                         dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
+    else
+      hipLaunchKernelGGL((gemm_bf16_kernel<true, true, true, true, false, kGemmRouteEdgeGradBf16>),
                          dim3((unsigned)blocks), dim3(256), 0, stream, g, tm, tn);
     JN_LAUNCH_CHECK();
     return kOk;

@@ -131,6 +131,9 @@ enum GemmUse {
   // bf16 dense layers: E . pv and E^T . gdv with E rounded to bf16 (bf16 C),
   // gdv . pv^T from bf16 operands (fp32 C, softsign epilogue as dense_edge_grad)
   kGemmDenseAggregateBf16, kGemmDenseValueGradBf16, kGemmDenseEdgeGradBf16,
+  // bf16 dense transitions: R^T diag(rho) pv with R rounded to bf16 after
+  // its k scale (bf16 C), diag(rho) R gdv (bf16 C), pv . gdv^T (fp32 C)
+  kGemmRouteAggregateBf16, kGemmRouteValueGradBf16, kGemmRouteEdgeGradBf16,
 };
 int gemm_batched(const BatchedGemm& m, GemmUse use, hipStream_t stream);
 // Workgroup tile of every later GEMM launch: 0 = chosen per call, 64 or 128 = forced.

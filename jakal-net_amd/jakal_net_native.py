@@ -207,7 +207,7 @@ _declare("jn_unit_scale_backward", [_P, _P, _I64, _I64, _F, _P, _P])
 for _name in ("jn_propagation_topk_forward", "jn_propagation_topk_backward", "jn_propagation_window_forward",
               "jn_propagation_window_backward", "jn_transition_topk_forward", "jn_transition_topk_backward",
               "jn_propagation_dense_forward", "jn_propagation_dense_backward", "jn_propagation_dense_forward_chunked",
-              "jn_propagation_dense_backward_chunked"):
+              "jn_propagation_dense_backward_chunked", "jn_transition_dense_forward", "jn_transition_dense_backward"):
     _declare(_name + "_bf16", list(getattr(_LIB, _name).argtypes))
 
 ABI_VERSION = int(_LIB.jn_abi_version())
@@ -1261,11 +1261,13 @@ class _TransitionDense(torch.autograd.Function):
 
     Inputs (fp32, contiguous): sender strength rho [B,Ns], src_val [B,Ns,Dsrc],
     dst_val [B,Nd,Ddst], projected_state [B,Ns], projected_val [B,Ns,Dv],
-    Ws [r,Dsrc], Wt [r,Ddst], w [r] (raw), bias [] or None."""
+    Ws [r,Dsrc], Wt [r,Ddst], w [r] (raw), bias [] or None.  With bf16,
+    src_val, dst_val and projected_val are bf16 and delta_val comes back in
+    bf16 (the *_bf16 entry points)."""
 
     @staticmethod
     def forward(ctx, rho, src, dst, ps, pv, Ws, Wt, w, bias, temperature: float, compress: int,  # noqa: N803
-                heads: int = 1):
+                heads: int = 1, bf16: bool = False):
         B, Ns, Dsrc = src.shape
         Nd, Ddst = dst.shape[1], dst.shape[2]
         Dv = pv.shape[-1]
@@ -1274,12 +1276,13 @@ class _TransitionDense(torch.autograd.Function):
         mh = heads > 1
         with torch.cuda.device(dev):
             ds = torch.empty(B, Nd, device=dev, dtype=torch.float32)
-            dv = torch.empty(B, Nd, Dv, device=dev, dtype=torch.float32)
+            dv = torch.empty(B, Nd, Dv, device=dev, dtype=torch.bfloat16 if bf16 else torch.float32)
             sp = torch.empty(B * Ns, r, device=dev, dtype=torch.float32)
             dp = torch.empty(B * Nd, r, device=dev, dtype=torch.float32)
             routes = torch.empty(B, Ns, Nd, device=dev, dtype=torch.float32)
             route_heads = torch.empty(B, Ns, Nd, device=dev, dtype=torch.uint8) if mh else None
-            fwd = _LIB.jn_transition_dense_forward_multihead if mh else _LIB.jn_transition_dense_forward
+            fwd = (_LIB.jn_transition_dense_forward_multihead if mh else
+                   _LIB.jn_transition_dense_forward_bf16 if bf16 else _LIB.jn_transition_dense_forward)
             _check(
                 fwd(
                     _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w), _ptr(bias),
@@ -1289,13 +1292,13 @@ class _TransitionDense(torch.autograd.Function):
                 )
             )
         ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, routes, route_heads)
-        ctx.meta = (float(temperature), compress, bias is not None, heads)
+        ctx.meta = (float(temperature), compress, bias is not None, heads, bool(bf16))
         return ds, dv
 
     @staticmethod
     def backward(ctx, g_ds, g_dv):
         rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, routes, route_heads = ctx.saved_tensors
-        temperature, compress, has_bias, heads = ctx.meta
+        temperature, compress, has_bias, heads, bf16 = ctx.meta
         mh = heads > 1
         B, Ns, Dsrc = src.shape
         Nd, Ddst = dst.shape[1], dst.shape[2]
@@ -1304,8 +1307,9 @@ class _TransitionDense(torch.autograd.Function):
         dev = src.device
         need = ctx.needs_input_grad
         with torch.cuda.device(dev):
+            vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, Nd, device=dev) if g_ds is None else g_ds.float().contiguous()
-            g_dv = torch.zeros(B, Nd, Dv, device=dev) if g_dv is None else g_dv.float().contiguous()
+            g_dv = torch.zeros(B, Nd, Dv, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
             out = [torch.empty_like(t) if n else None for t, n in zip((rho, src, dst, ps, pv), need[:5])]
             gWs = torch.empty_like(Ws) if need[5] else None
             gWt = torch.empty_like(Wt) if need[6] else None
@@ -1316,7 +1320,8 @@ class _TransitionDense(torch.autograd.Function):
                      _LIB.jn_transition_dense_workspace_bytes)
             ws_bytes = int(ws_fn(B, Ns, Nd, Dsrc, Ddst, Dv, *rank_arg))
             ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
-            bwd = _LIB.jn_transition_dense_backward_multihead if mh else _LIB.jn_transition_dense_backward
+            bwd = (_LIB.jn_transition_dense_backward_multihead if mh else
+                   _LIB.jn_transition_dense_backward_bf16 if bf16 else _LIB.jn_transition_dense_backward)
             _check(
                 bwd(
                     _ptr(rho), _ptr(src), _ptr(dst), _ptr(ps), _ptr(pv), _ptr(Ws), _ptr(Wt), _ptr(w),
@@ -1326,7 +1331,8 @@ class _TransitionDense(torch.autograd.Function):
                     _ptr(gw), _ptr(gb), _ptr(ws), ws_bytes, _stream(dev),
                 )
             )
-        return (*out, gWs, gWt, gw if need[7] else None, gb if (has_bias and need[8]) else None, None, None, None)
+        return (*out, gWs, gWt, gw if need[7] else None, gb if (has_bias and need[8]) else None, None, None, None,
+                None)
 
 
 def _check_route_spec(route_kind, source_weight, source_bias, target_weight, target_bias, hidden_weight, out_weight,
@@ -1342,6 +1348,12 @@ def _check_route_spec(route_kind, source_weight, source_bias, target_weight, tar
         raise TypeError(f"Unsupported route_compress_name for the HIP backend: {route_compress_name!r}.")
     if not temperature > 0:
         raise RuntimeError("temperature must be positive.")
+
+
+def dense_transition_bf16_shapes_ok(src_nodes: int, dst_nodes: int, val_dim: int) -> bool:
+    """Whether a bf16 dense transition of these sizes runs on the bf16 entry
+    points (their Ns x Nd products need 128 x 128 tiles of 8-element rows)."""
+    return all(n >= 128 and n % 8 == 0 for n in (src_nodes, dst_nodes, val_dim))
 
 
 def transition_pairwise_dense(
@@ -1387,11 +1399,16 @@ def transition_pairwise_dense(
     Ns, Dsrc = src_val.shape[-2], src_val.shape[-1]
     Nd, Ddst = dst_val.shape[-2], dst_val.shape[-1]
     Dv = projected_val.shape[-1]
+    # bf16 layers keep bf16 value rows on the bf16 MFMA products when the
+    # shapes fit their tiles (one head); anything else computes in fp32
+    bf16 = (heads == 1 and _bf16_rows(src_val, dst_val, projected_val)
+            and dense_transition_bf16_shapes_ok(Ns, Nd, Dv))
+    rows = _bf16 if bf16 else _f32
     ds, dv = _TransitionDense.apply(
-        _f32(sender_strength.reshape(-1, Ns)), _f32(src_val.reshape(-1, Ns, Dsrc)),
-        _f32(dst_val.reshape(-1, Nd, Ddst)), _f32(projected_state.reshape(-1, Ns)),
-        _f32(projected_val.reshape(-1, Ns, Dv)), _f32(source_weight), _f32(target_weight), _f32(core_weight),
-        _f32(bias), float(temperature), _ROUTE_COMPRESS_KINDS[route_compress_name], heads,
+        _f32(sender_strength.reshape(-1, Ns)), rows(src_val.reshape(-1, Ns, Dsrc)),
+        rows(dst_val.reshape(-1, Nd, Ddst)), _f32(projected_state.reshape(-1, Ns)),
+        rows(projected_val.reshape(-1, Ns, Dv)), _f32(source_weight), _f32(target_weight), _f32(core_weight),
+        _f32(bias), float(temperature), _ROUTE_COMPRESS_KINDS[route_compress_name], heads, bf16,
     )
     return ds.reshape(*batch_shape, Nd).to(projected_state.dtype), dv.reshape(*batch_shape, Nd, Dv).to(
         projected_val.dtype)

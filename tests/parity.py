@@ -182,7 +182,7 @@ def torch32_propagation(dev, val, ps, pv, U, V, w_hat, b, mask, kind, gds, gdv, 
 
 
 def torch32_transition(dev, src, dst, rho, ps, pv, Ws, Wt, w, b, temperature, mask, kind, gds, gdv,
-                       chunk=4, bf16_operands=False, bf16_linear=None) -> dict:
+                       chunk=4, bf16_operands=False, bf16_linear=None, bf16_routes=False) -> dict:
     """fp32 torch forward + autograd backward of low-rank routing on a given mask.
 
     src [B,Ns,Ds], dst [B,Nd,Dd], rho [B,Ns] (sender strength, a leaf), ps
@@ -192,7 +192,9 @@ def torch32_transition(dev, src, dst, rho, ps, pv, Ws, Wt, w, b, temperature, ma
     oracle's keys: delta_state, delta_val, sender, src_val, dst_val, ps, pv,
     Ws, Wt, w, b.  bf16_operands: the logit is bf16(P_s * w) . bf16(P_t),
     the operands of the bf16 top-k select; bf16_linear (default:
-    bf16_operands): the projections as the bf16 entry points compute them."""
+    bf16_operands): the projections as the bf16 entry points compute them;
+    bf16_routes: the sender-weighted routes rounded to bf16 (straight-through)
+    where they multiply the values, as the bf16 dense transitions take them."""
     if bf16_linear is None:
         bf16_linear = bf16_operands
     f32 = dict(device=dev, dtype=torch.float32)
@@ -227,7 +229,7 @@ def torch32_transition(dev, src, dst, rho, ps, pv, Ws, Wt, w, b, temperature, ma
         l = l / float(temperature)
         wr = _route32(l, m, kind) * r_[..., :, None]
         ds = (wr * p_s[..., :, None]).sum(-2)
-        dv = wr.transpose(-1, -2).contiguous() @ p_v
+        dv = (_bf16_st(wr) if bf16_routes else wr).transpose(-1, -2).contiguous() @ p_v
         loss = (ds * torch.as_tensor(gds[b0:b1]).to(**f32)).sum() + (dv * torch.as_tensor(gdv[b0:b1]).to(**f32)).sum()
         grads = torch.autograd.grad(loss, leaves + params)
         out["delta_state"].append(ds.detach().cpu())

@@ -183,6 +183,54 @@ def test_bf16_dense_variants(dev, chunk_batches, compress, causal, separate_pv, 
         check_bf16_calibrated(f"grad {name}", p.grad, gr[name], t[name])
 
 
+@pytest.mark.parametrize("kind", ["softmax", "signed_abs_softmax", "signed_entmax15"])
+def test_bf16_dense_transition(dev, kind):
+    """A bf16 dense transition (every source to every destination) at the bf16
+    entry points' sizes: the three Ns x Nd products on bf16 MFMA, the routes
+    rounded to bf16 where they multiply values; every gradient checked."""
+    import jakal_net_native as jn
+
+    B, Ns, Nd, D, r = 2, 256, 136, 128, 16
+    assert jn.dense_transition_bf16_shapes_ok(Ns, Nd, D) and not jn.dense_transition_bf16_shapes_ok(Ns, 120, D)
+    g = torch.Generator().manual_seed(5041)
+    src = torch.randn(B, Ns, D, generator=g).bfloat16()
+    dst = torch.randn(B, Nd, D, generator=g).bfloat16()
+    state = torch.randn(B, Ns, generator=g).bfloat16()
+    pv_cpu = torch.randn(B, Ns, D, generator=g).bfloat16()
+    bound = math.sqrt(6.0 / (D + r))
+    Ws = torch.empty(r, D).uniform_(-bound, bound, generator=g)
+    Wt = torch.empty(r, D).uniform_(-bound, bound, generator=g)
+    w = torch.rand(r, generator=g) + 0.5
+    b, temperature = 0.2, 1.3
+    srcd, dstd, pvd = (t.to(dev).requires_grad_(True) for t in (src, dst, pv_cpu))
+    psd = state.to(dev).requires_grad_(True)
+    Wsd, Wtd, wd = (t.to(dev).requires_grad_(True) for t in (Ws, Wt, w))
+    bd = torch.tensor(b, device=dev, requires_grad=True)
+    rho = torch.nn.functional.softplus(psd.float())
+    ds, dv = jn.transition_pairwise_dense("low_rank_bilinear_route", Wsd, None, Wtd, None, wd, bd, None, None, None,
+                                          None, kind, temperature, rho, srcd, dstd, psd, pvd, Ns, Nd)
+    assert dv.dtype == torch.bfloat16
+    gds = torch.randn(B, Nd, generator=g).bfloat16()
+    gdv = torch.randn(B, Nd, D, generator=g).bfloat16()
+    torch.autograd.backward([ds, dv], [gds.to(dev), gdv.to(dev)])
+    rho_np = _np(rho)
+    mask = np.ones((B, Ns, Nd), dtype=bool)
+    gr = O.transition_backward(_np(src), _np(dst), rho_np, _np(state), _np(pv_cpu), _np(Ws), _np(Wt), _np(w), b,
+                               _np(gds), _np(gdv), topk=Nd, temperature=temperature, mask=mask, kind=kind)
+    t = torch32_transition(dev, src, dst, rho.detach().float().cpu(), state, pv_cpu, Ws, Wt, w, b, temperature, None,
+                           kind, gds, gdv, bf16_linear=True, bf16_routes=True)
+    check_bf16_calibrated("delta_state", ds, gr["delta_state"], t["delta_state"])
+    check_bf16_calibrated("delta_val", dv, gr["delta_val"], t["delta_val"])
+    check_bf16_calibrated("grad src_val", srcd.grad, gr["src_val"], t["src_val"])
+    check_bf16_calibrated("grad dst_val", dstd.grad, gr["dst_val"], t["dst_val"])
+    check_bf16_calibrated("grad projected_val", pvd.grad, gr["pv"], t["pv"])
+    # state reaches both the projected state and (through softplus) the sender strength
+    sig = 1.0 / (1.0 + np.exp(-_np(state)))
+    check_bf16_calibrated("grad state", psd.grad, gr["ps"] + gr["sender"] * sig, t["ps"] + t["sender"] * sig)
+    for p, name in ((Wsd, "Ws"), (Wtd, "Wt"), (wd, "w"), (bd, "b")):
+        check_bf16_calibrated(f"grad {name}", p.grad, gr[name], t[name])
+
+
 # min_ok: the fraction of rows whose k-th / (k+1)-th gap exceeds twice the bf16
 # score tolerance; at k = 80 of 200 destinations few do (the fp32 tests pin
 # those selections), so that case asserts only that some rows are checked.

@@ -712,13 +712,15 @@ class _TwoWayTransition:
 
 class ProgressiveC5:
     """the Progressive-B query-block training step
-    (jakal_net.progressive.ProgressiveBStep) -- prefix encoding through S
-    warmup windows, 4 joint blocks (expand, expanded top-k, B->S, compress,
-    S->B, compressed top-k) and S refine windows, then 64 teacher-forced query
-    slots refined by query transitions and causal dense query propagation,
-    the vocabulary head and the cross entropy -- forward, backward and an AdamW
-    update of the fp32 master weights, under bf16 autocast.  The unit is
-    processed tokens (prefix + query slots) per second."""
+    (jakal_net.progressive.ProgressiveBStep, the reference's
+    ProgressiveBExampleLM glue with low-rank operators) -- prefix encoding
+    through S warmup windows, 4 joint blocks (S window, B_cmp -> B_exp expand,
+    expanded top-k, B_exp -> S, compress, S -> B_cmp, compressed top-k; each
+    update the scaled delta, then tanh / LayerNorm) and S refine windows, then 64
+    teacher-forced query slots refined by query transitions and causal query
+    propagation, the vocabulary head and the cross entropy -- forward, backward
+    and an AdamW update of the fp32 master weights, under bf16 autocast.  The
+    unit is processed tokens (prefix + query slots) per second."""
 
     name = "c5-progressive-b"
     metric = ("tokens/sec, Progressive-B query-block fwd+bwd+AdamW step (vocab 16384, d=512, prefix 512, "

@@ -460,12 +460,13 @@ class _PropagationEdges(torch.autograd.Function):
         rank_arg = [r // heads, heads] if mh else [r]
         dev = X.device
         need = ctx.needs_input_grad
+        ds_used = g_ds is not None  # projected_state reaches delta_state only
         with torch.cuda.device(dev):
             vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
             g_dv = torch.zeros(B, N, Dout, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
             gX = torch.empty_like(X) if need[0] else None
-            gps = torch.empty_like(ps) if need[1] else None
+            gps = torch.empty_like(ps) if need[1] and ds_used else None
             gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
             gV = torch.empty_like(V)
             gU = torch.empty_like(U)
@@ -623,6 +624,7 @@ class _PropagationDense(torch.autograd.Function):
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, edges, bias)
         ctx.meta = (compress, pv_is_x, bias is not None, bool(causal), chunk, bool(bf16))
         ctx.edges_consumed = False
+        ctx.set_materialize_grads(False)  # an unused delta_state arrives as None
         return ds, dv
 
     @staticmethod
@@ -642,12 +644,13 @@ class _PropagationDense(torch.autograd.Function):
         r = U.shape[0]
         dev = X.device
         need = ctx.needs_input_grad
+        ds_used = g_ds is not None  # projected_state reaches delta_state only
         with torch.cuda.device(dev):
             vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
             g_dv = torch.zeros(B, N, Dout, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
             gX = torch.empty_like(X) if need[0] else None
-            gps = torch.empty_like(ps) if need[1] else None
+            gps = torch.empty_like(ps) if need[1] and ds_used else None
             gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
             gV, gU, gw = torch.empty_like(V), torch.empty_like(U), torch.empty_like(w_hat)
             gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
@@ -677,12 +680,13 @@ class _PropagationDense(torch.autograd.Function):
         r = U.shape[0]
         dev = X.device
         need = ctx.needs_input_grad
+        ds_used = g_ds is not None  # projected_state reaches delta_state only
         with torch.cuda.device(dev):
             vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
             g_dv = torch.zeros(B, N, Dout, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
             gX = torch.empty_like(X) if need[0] else None
-            gps = torch.empty_like(ps) if need[1] else None
+            gps = torch.empty_like(ps) if need[1] and ds_used else None
             gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
             gV, gU, gw = torch.empty_like(V), torch.empty_like(U), torch.empty_like(w_hat)
             gb = torch.empty((), device=dev, dtype=torch.float32) if has_bias else None
@@ -734,6 +738,7 @@ class _PropagationDenseMultihead(torch.autograd.Function):
         ctx.save_for_backward(X, ps, pv_t, V, U, w_hat, proj, edge_chunk, bias)
         ctx.meta = (compress, pv_is_x, bias is not None, bool(causal), chunk, heads)
         ctx.edges_consumed = False
+        ctx.set_materialize_grads(False)  # an unused delta_state arrives as None
         return ds, dv
 
     @staticmethod
@@ -749,11 +754,12 @@ class _PropagationDenseMultihead(torch.autograd.Function):
         R = U.shape[0]
         dev = X.device
         need = ctx.needs_input_grad
+        ds_used = g_ds is not None  # projected_state reaches delta_state only
         with torch.cuda.device(dev):
             g_ds = torch.zeros(B, N, device=dev) if g_ds is None else g_ds.float().contiguous()
             g_dv = torch.zeros(B, N, Dout, device=dev) if g_dv is None else g_dv.float().contiguous()
             gX = torch.empty_like(X) if need[0] else None
-            gps = torch.empty_like(ps) if need[1] else None
+            gps = torch.empty_like(ps) if need[1] and ds_used else None
             gpv = torch.empty_like(pv) if (not pv_is_x and need[2]) else None
             gV, gU, gw = torch.empty_like(V), torch.empty_like(U), torch.empty_like(w_hat)
             gb = torch.empty(heads, device=dev, dtype=torch.float32) if has_bias else None
@@ -1107,11 +1113,14 @@ class _TransitionTopK(torch.autograd.Function):
         rank_arg = [r // heads, heads] if mh else [r]
         dev = src.device
         need = ctx.needs_input_grad
+        # the projected source state reaches delta_state only
+        need_in = list(need[:5])
+        need_in[3] = need_in[3] and g_ds is not None
         with torch.cuda.device(dev):
             vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, Nd, device=dev) if g_ds is None else g_ds.float().contiguous()
             g_dv = torch.zeros(B, Nd, Dv, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
-            out = [torch.empty_like(t) if n else None for t, n in zip((rho, src, dst, ps, pv), need[:5])]
+            out = [torch.empty_like(t) if n else None for t, n in zip((rho, src, dst, ps, pv), need_in)]
             gWs = torch.empty_like(Ws) if need[5] else None
             gWt = torch.empty_like(Wt) if need[6] else None
             gw = torch.empty_like(w)
@@ -1293,6 +1302,7 @@ class _TransitionDense(torch.autograd.Function):
             )
         ctx.save_for_backward(rho, src, dst, ps, pv, Ws, Wt, w, sp, dp, routes, route_heads)
         ctx.meta = (float(temperature), compress, bias is not None, heads, bool(bf16))
+        ctx.set_materialize_grads(False)  # an unused delta_state arrives as None
         return ds, dv
 
     @staticmethod
@@ -1306,11 +1316,14 @@ class _TransitionDense(torch.autograd.Function):
         r = Ws.shape[0]
         dev = src.device
         need = ctx.needs_input_grad
+        # the projected source state reaches delta_state only
+        need_in = list(need[:5])
+        need_in[3] = need_in[3] and g_ds is not None
         with torch.cuda.device(dev):
             vdt = torch.bfloat16 if bf16 else torch.float32
             g_ds = torch.zeros(B, Nd, device=dev) if g_ds is None else g_ds.float().contiguous()
             g_dv = torch.zeros(B, Nd, Dv, device=dev, dtype=vdt) if g_dv is None else g_dv.to(vdt).contiguous()
-            out = [torch.empty_like(t) if n else None for t, n in zip((rho, src, dst, ps, pv), need[:5])]
+            out = [torch.empty_like(t) if n else None for t, n in zip((rho, src, dst, ps, pv), need_in)]
             gWs = torch.empty_like(Ws) if need[5] else None
             gWt = torch.empty_like(Wt) if need[6] else None
             gw = torch.empty_like(w)

@@ -11,8 +11,8 @@ operator on the HIP library, on a reduced configuration.
 * the step under bf16 autocast (bf16 activations, fp32 master weights, as
   BASELINE config 5 runs) against the float64 logits at the bf16 tolerance.
 
-Reference composition: scripts/progressive_b_example.py:1108-1323, 1957-2021,
-2059-2152.
+Reference composition: scripts/progressive_b_example.py:282-292, 1011-1024,
+1108-1323, 1691-1719, 1857-1908, 1957-2021, 2059-2152.
 """
 
 import numpy as np
@@ -53,11 +53,27 @@ def _models_and_batch(seed=21):
 
 
 def _unused(model):
-    """Parameters outside the loss: the last block's updates of B_cmp (compress, S -> B_cmp, its top-k
-    propagation and norm) feed only the next block, as in the reference's query-block step."""
-    last = f"blocks.{model.cfg.blocks - 1}."
-    return {n for n, _ in model.named_parameters()
-            if n.startswith(tuple(last + m for m in ("compress.", "s_to_b.", "cmp_prop.", "cmp_norm.")))}
+    """Parameters outside the loss, as in the reference's block: every block's
+    expanded-slot state (a transition's destination state enters no delta, and
+    B_exp is replaced by the expand delta), the compressed-slot templates of the
+    blocks after the first (B_cmp is carried from there), and the last block's
+    compress and S -> B_cmp routes (that B_cmp feeds only a next block; with one
+    block its shared top-k pairwise module too).  The state head is outside the
+    loss too: the sequence state it starts is replaced by the B_exp -> S delta
+    before any operator reads it, and a query slot's state only enters a
+    transition as its destination."""
+    n = model.cfg.blocks
+    out = {"state_init.weight", "state_init.bias"}
+    for name, _ in model.named_parameters():
+        parts = name.split(".")
+        if parts[0] != "blocks":
+            continue
+        i, rest = int(parts[1]), ".".join(parts[2:])
+        if rest == "exp_slot_state" or (i > 0 and rest.startswith("cmp_slot_")):
+            out.add(name)
+        elif i == n - 1 and rest.startswith(("compress.", "s_to_b.") + (("cmp_prop.",) if n == 1 else ())):
+            out.add(name)
+    return out
 
 
 def _grads(model, prefix, target):

@@ -127,7 +127,8 @@ int check_edge_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out_
   JN_REQUIRE(batch >= 1 && nodes >= 1 && in_dim >= 1 && out_dim >= 1, kInvalidArgument,
              "batch, nodes and dims must be positive (B=%lld N=%lld Din=%lld Dout=%lld)", (long long)batch,
              (long long)nodes, (long long)in_dim, (long long)out_dim);
-  JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
+  JN_REQUIRE(rank >= 1 && rank <= kMaxRank, kUnsupported, "rank must be in [1, %d] (got %lld)", kMaxRank,
+             (long long)rank);
   JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported,
              "compress_kind must be 0 (softsign), 1 (signed_abs_softmax) or 2 (signed_entmax15), got %d",
              compress_kind);
@@ -299,7 +300,8 @@ int check_transition_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t Dsrc,
                             int64_t rank, int64_t topk, int32_t compress_kind, float temperature) {
   JN_REQUIRE(batch >= 1 && Ns >= 1 && Nd >= 1 && Dsrc >= 1 && Ddst >= 1 && Dv >= 1, kInvalidArgument,
              "batch, node counts and dims must be positive");
-  JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
+  JN_REQUIRE(rank >= 1 && rank <= kMaxRank, kUnsupported, "rank must be in [1, %d] (got %lld)", kMaxRank,
+             (long long)rank);
   JN_REQUIRE(topk >= 1, kInvalidArgument, "topk must be positive");
   const int64_t k = route_edges(topk, Nd);
   JN_REQUIRE(k == Nd ? k <= 64 : k <= kSelectLargeMaxK, kUnsupported,
@@ -351,7 +353,8 @@ int check_dense_shapes(int64_t batch, int64_t nodes, int64_t in_dim, int64_t out
                        int32_t compress_kind) {
   JN_REQUIRE(batch >= 1 && nodes >= 1 && in_dim >= 1 && out_dim >= 1, kInvalidArgument,
              "batch, nodes and dims must be positive");
-  JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
+  JN_REQUIRE(rank >= 1 && rank <= kMaxRank, kUnsupported, "rank must be in [1, %d] (got %lld)", kMaxRank,
+             (long long)rank);
   JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported,
              "compress_kind must be 0 (softsign), 1 (signed_abs_softmax) or 2 (signed_entmax15), got %d",
              compress_kind);
@@ -646,7 +649,8 @@ int check_transition_dense_shapes(int64_t batch, int64_t Ns, int64_t Nd, int64_t
                                   int64_t rank, int32_t compress_kind, float temperature) {
   JN_REQUIRE(batch >= 1 && Ns >= 1 && Nd >= 1 && Dsrc >= 1 && Ddst >= 1 && Dv >= 1, kInvalidArgument,
              "batch, node counts and dims must be positive");
-  JN_REQUIRE(rank >= 1 && rank <= 128, kUnsupported, "rank must be in [1, 128] (got %lld)", (long long)rank);
+  JN_REQUIRE(rank >= 1 && rank <= kMaxRank, kUnsupported, "rank must be in [1, %d] (got %lld)", kMaxRank,
+             (long long)rank);
   JN_REQUIRE(compress_kind >= 0 && compress_kind <= 2, kUnsupported,
              "route compress kind must be 0 (softmax), 1 (signed_abs_softmax) or 2 (signed_entmax15), got %d",
              compress_kind);

@@ -478,13 +478,20 @@ __device__ __forceinline__ void row_abs_softmax_stats(const int32_t* idx, const 
                                                       float& row_max, float& row_inv_sum) {
   const int lane = lane_id();
   float m = -INFINITY;
-  for (int e = lane; e < k; e += kWave)
-    if (idx[row * k + e] >= 0) m = fmaxf(m, fabsf(score[row * k + e]));
+  // (an edge's score loads beside its index: the slot exists for absent edges too)
+  for (int e = lane; e < k; e += kWave) {
+    const int32_t j = idx[row * k + e];
+    const float a = fabsf(score[row * k + e]);
+    if (j >= 0) m = fmaxf(m, a);
+  }
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, shfl_xor_f(m, s));
   float sum = 0.0f;
-  for (int e = lane; e < k; e += kWave)
-    if (idx[row * k + e] >= 0) sum += __expf(fabsf(score[row * k + e]) - m);
+  for (int e = lane; e < k; e += kWave) {
+    const int32_t j = idx[row * k + e];
+    const float a = fabsf(score[row * k + e]);
+    if (j >= 0) sum += __expf(a - m);
+  }
   sum = wave_sum(sum);
   row_max = m;
   row_inv_sum = sum > 0.f ? 1.0f / sum : 0.0f;
@@ -508,16 +515,20 @@ __device__ __forceinline__ RowStats row_compress_stats(const int32_t* idx, const
   } else if (compress == 2) {
     const int lane = lane_id();
     float m = -INFINITY;
-    for (int e = lane; e < k; e += kWave)
-      if (idx[row * k + e] >= 0) m = fmaxf(m, fabsf(score[row * k + e]));
+    for (int e = lane; e < k; e += kWave) {
+      const int32_t j = idx[row * k + e];
+      const float a = fabsf(score[row * k + e]);
+      if (j >= 0) m = fmaxf(m, a);
+    }
     m = wave_max_f(m);
     float tau = -INFINITY;
     int n_prev = -1;
     for (int it = 0; it < kEntmaxMaxIter; ++it) {
       float s1 = 0.f, s2 = 0.f, n = 0.f;
       for (int e = lane; e < k; e += kWave) {
-        if (idx[row * k + e] < 0) continue;
+        const int32_t j = idx[row * k + e];
         const float x = 0.5f * (fabsf(score[row * k + e]) - m);
+        if (j < 0) continue;
         if (x >= tau) {
           s1 += x;
           s2 += x * x;
@@ -531,8 +542,9 @@ __device__ __forceinline__ RowStats row_compress_stats(const int32_t* idx, const
     }
     float den = 0.f;
     for (int e = lane; e < k; e += kWave) {
-      if (idx[row * k + e] < 0) continue;
+      const int32_t j = idx[row * k + e];
       const float d = fmaxf(0.5f * (fabsf(score[row * k + e]) - m) - tau, 0.0f);
+      if (j < 0) continue;
       den += d * d;
     }
     st.a = m;
@@ -555,9 +567,12 @@ __device__ __forceinline__ void row_coefficients(const int32_t* idx, const float
   c = 0.0f;
   s = 0.0f;
   if (e < k) {
+    // the score loads beside the index (its slot exists for absent edges too),
+    // so the row's gathers wait for one memory round trip, not two
     j = idx[row * k + e];
+    const float se = score[row * k + e];
     if (j >= 0) {
-      s = score[row * k + e];
+      s = se;
       if (compress == 0) {
         c = softsign_f(s);
       } else if (compress == kCoefGiven) {

@@ -500,7 +500,33 @@ int rows_backward_slab(int64_t Nk, int D, bool vec, int elem_bytes) {
 
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
   if (a.rows == 0) return kOk;
-  JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
+  if (a.r > kRegRank) {
+    // ranks beyond the kernel's rank slots: the row kernel writes the score
+    // gradients only (rank 0: its dQ loads read out of range and store
+    // nothing), then the rank-chunked kernel forms dQ from them
+    JN_REQUIRE(a.r <= kMaxRank && a.heads <= 1, kUnsupported,
+               "rank must be at most %d (%d over several heads), got %d", kMaxRank, kRegRank, a.r);
+    JN_REQUIRE(a.g_score && a.dq, kInvalidArgument, "wide-rank row backward needs g_score and dq");
+    RowsBwdArgs b = a;
+    b.r = 0;
+    int rc = launch_rows_backward(b, stream);
+    if (rc) return rc;
+    RankRowsArgs rr{};
+    rr.idx = a.idx;
+    rr.g = a.g_score;
+    rr.k = a.k;
+    rr.key = a.key;
+    rr.ldk = a.ldk;
+    rr.qscale = a.qscale;
+    rr.r = a.r;
+    rr.Nq = a.Nq;
+    rr.Nk = a.Nk;
+    rr.rows = a.rows;
+    rr.dq = a.dq;
+    rr.lddq = a.lddq;
+    return launch_rank_rows_grad(rr, stream);
+  }
+  JN_REQUIRE(a.r >= 0 && a.r <= kRegRank, kUnsupported, "rank must be in [1, %d]", kRegRank);
   const int64_t blocks = (a.rows + 3) / 4;
   JN_REQUIRE(2 * blocks < (1LL << 31), kInvalidArgument, "too many rows");
   JN_REQUIRE((int64_t)a.Nk * a.ld_pv * 4 < (1LL << 31) && (int64_t)a.Nk * a.ldk * 4 < (1LL << 31) &&
@@ -550,6 +576,82 @@ int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream) {
   JN_PROFILE("rows_backward_kernel", stream);
   if (a.bf16) launch_rows_bwd_width<bf16_t, false>(a, vec, grid, stream);
   else launch_rows_bwd_width<float, false>(a, vec, grid, stream);
+  JN_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------------------
+// Rank-chunked gradients for ranks beyond the row and column kernels' rank
+// slots (one head, up to kMaxRank ranks).  One wavefront per row (per column
+// below); the ranks go in chunks of 64 lanes x 4 (VEC: 16-byte key rows) or
+// 64 lanes x 1, each chunk summing the row's edges in index order with eight
+// key rows in flight.
+// ---------------------------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(256) void rank_rows_grad_kernel(RankRowsArgs a) {
+  constexpr int RC = VEC ? 4 * kWave : kWave;  // ranks per chunk
+  const int lane = lane_id();
+  const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave_id();
+  if (row >= a.rows) return;
+  const int64_t b = row / a.Nq;
+  const auto rs = make_rsrc(a.key + b * a.Nk * a.ldk, (uint32_t)(a.Nk * a.ldk * 4));
+  float* dqrow = a.dq + row * a.lddq;
+  for (int r0 = 0; r0 < a.r; r0 += RC) {
+    const int rr = r0 + (VEC ? 4 * lane : lane);
+    const bool on = rr < a.r;  // VEC: r % 4 == 0, so the lane's four ranks are all in
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int e0 = 0; e0 < a.k; e0 += kWave) {
+      const int e = e0 + lane;
+      const int j = e < a.k ? a.idx[row * a.k + e] : -1;
+      const float gv = e < a.k ? a.g[row * a.k + e] : 0.f;
+      const int ne = min(kWave, a.k - e0);
+      for (int q = 0; q < ne; q += 8) {
+        float4 v[8];
+        float gq[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int src = min(q + u, kWave - 1);
+          const int jj = q + u < ne ? readlane_i(j, src) : -1;
+          gq[u] = jj >= 0 ? readlane_f(gv, src) : 0.f;
+          const uint32_t off = (jj >= 0 && on) ? (uint32_t)(jj * a.ldk + rr) * 4u : kOobOffset;
+          if constexpr (VEC) {
+            v[u] = buf_load4(rs, off);
+          } else {
+            v[u] = make_float4(buf_load1(rs, off), 0.f, 0.f, 0.f);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) fma4(acc, gq[u], v[u]);
+      }
+    }
+    if (on) {
+      if constexpr (VEC) {
+        const float4 sc = a.qscale ? *reinterpret_cast<const float4*>(a.qscale + rr) : make_float4(1.f, 1.f, 1.f, 1.f);
+        dqrow[rr] = acc.x * sc.x;
+        dqrow[rr + 1] = acc.y * sc.y;
+        dqrow[rr + 2] = acc.z * sc.z;
+        dqrow[rr + 3] = acc.w * sc.w;
+      } else {
+        dqrow[rr] = acc.x * (a.qscale ? a.qscale[rr] : 1.f);
+      }
+    }
+  }
+}
+
+int launch_rank_rows_grad(const RankRowsArgs& a, hipStream_t stream) {
+  if (a.rows == 0) return kOk;
+  JN_REQUIRE(a.r >= 1 && a.r <= kMaxRank && a.k >= 1, kUnsupported, "rank must be in [1, %d]", kMaxRank);
+  JN_REQUIRE(a.idx && a.g && a.key && a.dq, kInvalidArgument, "null tensor pointer");
+  JN_REQUIRE((int64_t)a.Nk * a.ldk * 4 < (1LL << 31), kUnsupported,
+             "one batch element of the key rows must stay below 2 GiB");
+  const int64_t blocks = (a.rows + 3) / 4;
+  JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many rows");
+  const bool vec = (a.r % 4 == 0) && (a.ldk % 4 == 0) && (a.lddq % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(a.key) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(a.qscale) & 15) == 0);
+  JN_PROFILE("rank_rows_grad_kernel", stream);
+  if (vec) hipLaunchKernelGGL(rank_rows_grad_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL(rank_rows_grad_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
   JN_LAUNCH_CHECK();
   return kOk;
 }
@@ -1285,10 +1387,82 @@ int launch_unit_scale(const float* w, const float* grad, int64_t rows, int64_t r
   return kOk;
 }
 
+// Key-side gradient and scale-vector partials for ranks beyond the column
+// kernel's rank slots (one head): dk[j, :] = kscale * sum over j's records
+// of g * q[row, :], and partial key[j, :] * (sum g q[row, :]).  Each wave takes
+// four of the workgroup's sixteen columns in turn (cols_backward_parts rows of
+// part_c, as the column kernel), keeping its columns' partial sums in its own
+// LDS row; the four rows are then summed in wave order.
+template <bool VEC, bool BAND>
+__global__ __launch_bounds__(256) void rank_cols_grad_kernel(ColsBwdArgs a) {
+  __shared__ float red[4][kMaxRank];
+  constexpr int RC = VEC ? 4 * kWave : kWave;  // ranks per chunk
+  const int lane = lane_id(), w = wave_id();
+  const int64_t total_cols = (int64_t)a.B * a.Nk;
+  const int64_t blk = xcd_swizzle(blockIdx.x, gridDim.x);
+  for (int rr = lane; rr < a.r; rr += kWave) red[w][rr] = 0.f;
+  wave_lds_sync();
+  for (int t = 0; t < 4; ++t) {
+    const int64_t col = blk * 16 + w * 4 + t;
+    if (col >= total_cols) break;  // wave-uniform; the barrier below is outside the loop
+    const ColRecords<BAND> recs(a, col);
+    const int len = recs.len;
+    for (int r0 = 0; r0 < a.r; r0 += RC) {
+      const int rr = r0 + (VEC ? 4 * lane : lane);
+      const bool on = rr < a.r;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int q0 = 0; q0 < len; q0 += kWave) {
+        int row = -1;
+        float gs = 0.f;
+        if (q0 + lane < len) {
+          const float4 rc = recs.get(a, q0 + lane);
+          row = __float_as_int(rc.x) & kRecRowMask;
+          gs = (!BAND && a.rec_eid) ? a.g_score[__float_as_int(rc.z)] : rc.z;
+        }
+        const int n = min(kWave, len - q0);
+        for (int q = 0; q < n; q += 8) {
+          float4 v[8];
+          float gq[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int src = min(q + u, kWave - 1);
+            const int rw = q + u < n ? readlane_i(row, src) : -1;
+            gq[u] = rw >= 0 ? readlane_f(gs, src) : 0.f;
+            const float* qr = a.q + (int64_t)(rw >= 0 ? rw : 0) * a.ldq + (on ? rr : 0);
+            if constexpr (VEC) {
+              v[u] = (rw >= 0 && on) ? *reinterpret_cast<const float4*>(qr) : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+              v[u] = make_float4((rw >= 0 && on) ? *qr : 0.f, 0.f, 0.f, 0.f);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) fma4(acc, gq[u], v[u]);
+        }
+      }
+      if (on) {
+        const float* kr = a.key + col * a.ldk + rr;
+        float* dkr = a.dk + col * a.lddk + rr;
+        const int nr = VEC ? 4 : 1;
+        const float av[4] = {acc.x, acc.y, acc.z, acc.w};
+        for (int m = 0; m < nr; ++m) {
+          dkr[m] = av[m] * (a.kscale ? a.kscale[rr + m] : 1.f);
+          red[w][rr + m] += kr[m] * av[m];
+        }
+      }
+      wave_lds_sync();
+    }
+  }
+  if (!a.part_c) return;  // uniform over the workgroup
+  __syncthreads();
+  for (int rr = threadIdx.x; rr < a.r; rr += blockDim.x)
+    a.part_c[blk * a.r + rr] = (red[0][rr] + red[1][rr]) + (red[2][rr] + red[3][rr]);
+}
+
 int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
   const int64_t total_cols = (int64_t)a.B * a.Nk;
   if (total_cols == 0) return kOk;
-  JN_REQUIRE(!a.q || (a.r >= 1 && a.r <= 128), kUnsupported, "rank must be in [1, 128]");
+  JN_REQUIRE(!a.q || (a.r >= 1 && (a.r <= kRegRank || (a.r <= kMaxRank && a.heads <= 1))), kUnsupported,
+             "rank must be in [1, %d] (%d over several heads), got %d", kMaxRank, kRegRank, a.r);
   JN_REQUIRE(!a.q || (a.key && a.dk), kInvalidArgument, "key-side gradient needs key and dk");
   JN_REQUIRE((int64_t)a.B * a.Nq * a.k < (1LL << 31), kUnsupported, "edge count exceeds int32 ids");
   JN_REQUIRE(!a.band || (a.Nq == a.Nk && a.coef && a.g_score && (int64_t)a.B * a.Nq <= kRecRowMask),
@@ -1323,7 +1497,21 @@ int launch_cols_backward(const ColsBwdArgs& a, hipStream_t stream) {
     }
     JN_LAUNCH_CHECK();
   }
-  if (a.q) {
+  if (a.q && a.r > kRegRank) {  // ranks beyond the column kernel's rank slots
+    const bool vec = (a.r % 4 == 0) && (a.ldq % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0);
+    const int64_t blocks = cols_backward_parts(total_cols);
+    JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
+    JN_PROFILE("rank_cols_grad_kernel", stream);
+    const dim3 grid((unsigned)blocks);
+    if (a.band) {
+      if (vec) hipLaunchKernelGGL((rank_cols_grad_kernel<true, true>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((rank_cols_grad_kernel<false, true>), grid, dim3(256), 0, stream, a);
+    } else {
+      if (vec) hipLaunchKernelGGL((rank_cols_grad_kernel<true, false>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((rank_cols_grad_kernel<false, false>), grid, dim3(256), 0, stream, a);
+    }
+    JN_LAUNCH_CHECK();
+  } else if (a.q) {
     const bool mh = a.heads > 1;
     JN_REQUIRE(!mh || (a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r), kInvalidArgument,
                "multi-head column backward needs 2..%d heads of equal rank", kMaxHeads);
@@ -1369,21 +1557,26 @@ __global__ __launch_bounds__(256) void finalize_partials_kernel(const float* par
   __shared__ float red[256];
   const int t = threadIdx.x, blk = blockIdx.x;
   const int64_t width = r + nbias;
-  // r_pad columns (power of two >= r, <= 128) x 256 / r_pad row lanes
-  int r_pad = 1;
-  while (r_pad < r) r_pad <<= 1;
-  const int col = t & (r_pad - 1), sub = t / r_pad, nsub = 256 / r_pad;
   const int64_t p0 = (int64_t)nparts * blk / kFinBlocks, p1 = (int64_t)nparts * (blk + 1) / kFinBlocks;
-  float s = 0.f;
-  if (col < r)
-    for (int64_t p = p0 + sub; p < p1; p += nsub) s += part_c[p * r + col];
-  red[t] = s;
-  __syncthreads();
-  for (int o = 128; o >= r_pad; o >>= 1) {  // sum the row lanes of each column
-    if (t < o) red[t] += red[t + o];
+  // columns in chunks of at most 256; a chunk of cw columns takes r_pad
+  // columns (power of two >= cw) x 256 / r_pad row lanes
+  for (int c0 = 0; c0 < r; c0 += 256) {
+    const int cw = min(256, r - c0);
+    int r_pad = 1;
+    while (r_pad < cw) r_pad <<= 1;
+    const int col = t & (r_pad - 1), sub = t / r_pad, nsub = 256 / r_pad;
+    float s = 0.f;
+    if (col < cw)
+      for (int64_t p = p0 + sub; p < p1; p += nsub) s += part_c[p * r + c0 + col];
+    __syncthreads();  // the previous chunk's reads of red are done
+    red[t] = s;
     __syncthreads();
+    for (int o = 128; o >= r_pad; o >>= 1) {  // sum the row lanes of each column
+      if (t < o) red[t] += red[t + o];
+      __syncthreads();
+    }
+    if (t < cw) stage[blk * width + c0 + t] = red[t];
   }
-  if (t < r) stage[blk * width + t] = red[t];
   const int64_t i0 = nrows * blk / kFinBlocks, i1 = nrows * (blk + 1) / kFinBlocks;
   for (int h = 0; h < nbias; ++h) {
     __syncthreads();
@@ -1422,7 +1615,7 @@ __global__ __launch_bounds__(256) void finalize_small_grads_kernel(const float* 
 int launch_finalize_small_grads(const float* part_c, int nparts, int r, float* grad_c, int accumulate_c,
                                 const float* rowsum, int64_t nrows, float* grad_bias, float* stage,
                                 hipStream_t stream, int nbias) {
-  JN_REQUIRE(r >= 1 && r <= 128, kUnsupported, "rank must be in [1, 128]");
+  JN_REQUIRE(r >= 1 && r <= kMaxRank, kUnsupported, "rank must be in [1, %d]", kMaxRank);
   JN_REQUIRE(nbias >= 1 && nbias <= kMaxHeads, kUnsupported, "1..%d bias columns", kMaxHeads);
   static_assert(kFinBlocks == 256, "the second stage maps one thread per stage row");
   {

@@ -66,6 +66,12 @@ size_t select_workspace_bytes_heads(int64_t B, int64_t Nk, int64_t head_rank, in
 // ranks over all heads (heads * ceil(head_rank / 32) <= 4).
 constexpr int kMaxHeads = 8;
 bool select_heads_fit(int64_t head_rank, int64_t heads);
+// Ranks.  The register paths (the register select, the row and column kernels'
+// rank slots, multi-head scores) hold up to kRegRank ranks over all heads; one
+// head takes up to kMaxRank, the ranks beyond kRegRank running the
+// scored-rows select and the rank-chunked gradient kernels below.
+constexpr int kRegRank = 128;
+constexpr int kMaxRank = 1024;
 
 // ---- fp32 MFMA GEMMs (jn_gemm.hip) ----------------------------------------
 // x_bf16: the layer operand X (and dX with its addend) holds bf16 elements.
@@ -197,6 +203,23 @@ struct RowsBwdArgs {
   const float* dots0;     // [rows * k] (with dot_pos)
 };
 int launch_rows_backward(const RowsBwdArgs& a, hipStream_t stream);
+
+// Rank-chunked query-side gradient for ranks beyond kRegRank (one head):
+//   dq[i, :] = qscale * sum_e g[i, e] key[b * Nk + idx[i, e], :]
+// over row i's edges in index order (absent edges: idx < 0).
+struct RankRowsArgs {
+  const int32_t* idx;    // [rows, k]
+  const float* g;        // [rows, k] per-edge score gradient
+  int k;
+  const float* key;      // key rows of batch element b at b * Nk, stride ldk
+  int64_t ldk;
+  const float* qscale;   // [r] (null = 1)
+  int r, Nq, Nk;
+  int64_t rows;          // B * Nq
+  float* dq;             // [rows, r], stride lddq
+  int64_t lddq;
+};
+int launch_rank_rows_grad(const RankRowsArgs& a, hipStream_t stream);
 
 // ---- causal-band kernels of window edge lists (jn_band.hip) --------------
 // Slot e of query row i is key i - (k - 1 - e) (absent below 0); N query rows

@@ -67,12 +67,19 @@ __device__ __forceinline__ RowStats route_row_stats(const int32_t* idx, const fl
   if (kind != 0) return row_compress_stats(idx, logit, row, k, kind);
   const int lane = lane_id();
   float m = -INFINITY;
-  for (int e = lane; e < k; e += kWave)
-    if (idx[row * k + e] >= 0) m = fmaxf(m, logit[row * k + e]);
+  // (a route's logit loads beside its index: the slot exists for absent routes too)
+  for (int e = lane; e < k; e += kWave) {
+    const int32_t j = idx[row * k + e];
+    const float l = logit[row * k + e];
+    if (j >= 0) m = fmaxf(m, l);
+  }
   m = wave_max_f(m);
   float sum = 0.0f;
-  for (int e = lane; e < k; e += kWave)
-    if (idx[row * k + e] >= 0) sum += __expf(logit[row * k + e] - m);
+  for (int e = lane; e < k; e += kWave) {
+    const int32_t j = idx[row * k + e];
+    const float l = logit[row * k + e];
+    if (j >= 0) sum += __expf(l - m);
+  }
   sum = wave_sum(sum);
   RowStats st;
   st.a = m;
@@ -100,7 +107,8 @@ __global__ __launch_bounds__(256) void route_coef_large_kernel(const int32_t* id
   const float rh = rho ? rho[row] : 1.0f;
   for (int e = lane; e < k; e += kWave) {
     const int j = idx[row * k + e];
-    coef[row * k + e] = rh * route_prob_row(j, j >= 0 ? logit[row * k + e] : 0.0f, kind, st);
+    const float l = logit[row * k + e];
+    coef[row * k + e] = rh * route_prob_row(j, j >= 0 ? l : 0.0f, kind, st);
   }
 }
 
@@ -480,7 +488,33 @@ static void launch_route_bwd(const RouteRowsBwdArgs& a, bool vec, dim3 grid, hip
 
 int launch_route_rows_backward(const RouteRowsBwdArgs& a, hipStream_t stream) {
   if (a.rows == 0) return kOk;
-  JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
+  if (a.r > kRegRank) {
+    // ranks beyond the kernels' rank slots: the row kernel writes the logit
+    // gradients only (rank 0: no dQ loads or stores), then the rank-chunked
+    // kernel forms dQ from them
+    JN_REQUIRE(a.r <= kMaxRank && a.heads <= 1, kUnsupported,
+               "rank must be at most %d (%d over several heads), got %d", kMaxRank, kRegRank, a.r);
+    JN_REQUIRE(a.g_logit && a.dq, kInvalidArgument, "wide-rank route backward needs g_logit and dq");
+    RouteRowsBwdArgs b = a;
+    b.r = 0;
+    int rc = launch_route_rows_backward(b, stream);
+    if (rc) return rc;
+    RankRowsArgs rr{};
+    rr.idx = a.idx;
+    rr.g = a.g_logit;
+    rr.k = a.k;
+    rr.key = a.key;
+    rr.ldk = a.ldk;
+    rr.qscale = a.qscale;
+    rr.r = a.r;
+    rr.Nq = a.Ns;
+    rr.Nk = a.Nd;
+    rr.rows = a.rows;
+    rr.dq = a.dq;
+    rr.lddq = a.lddq;
+    return launch_rank_rows_grad(rr, stream);
+  }
+  JN_REQUIRE(a.r >= 0 && a.r <= kRegRank, kUnsupported, "rank must be in [1, %d]", kRegRank);
   JN_REQUIRE(a.k >= 1 && a.k <= kSelectLargeMaxK, kUnsupported, "routes support 1..%d edges per source (got %d)",
              kSelectLargeMaxK, a.k);
   JN_REQUIRE(a.compress >= 0 && a.compress <= 2, kUnsupported, "route compress kind must be 0, 1 or 2");

@@ -1305,7 +1305,9 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   SelectArgs a = a_in;
   const bool large_heads = a.heads > 1 && !(a.bf16 == 0 && select_heads_fit(a.head_rank, a.heads));
   // k == Nk (every key kept, in score order) runs on the scored rows too
-  if (a.k > kSelectMaxK || a.Nk > kSelMaxKeys || large_heads || a.k >= a.Nk) return launch_topk_select_large(a, stream);
+  // so does one head of more ranks than the register kernels hold
+  if (a.k > kSelectMaxK || a.Nk > kSelMaxKeys || large_heads || a.k >= a.Nk || (a.heads <= 1 && a.r > kRegRank))
+    return launch_topk_select_large(a, stream);
   JN_REQUIRE(a.k >= 1 && a.k <= kSelectMaxK, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)", kSelectMaxK,
              a.k);
   JN_REQUIRE(a.k < a.Nk, kInvalidArgument, "top-k select needs k < key count (k=%d, Nk=%d)", a.k, a.Nk);

@@ -47,7 +47,7 @@ __device__ __forceinline__ float rank_dot(const float* a, const float* b, int n)
 // writes only the heads (the edges of a top-k select).
 template <bool VEC, bool MH>
 __global__ __launch_bounds__(256) void window_scores_kernel(WindowScoreArgs a) {
-  __shared__ __align__(16) float s_q[4][128];
+  __shared__ __align__(16) float s_q[4][kMaxRank];
   const int lane = lane_id(), wave = wave_id();
   const int64_t row = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wave;
   if (row >= (int64_t)a.B * a.Nq) return;  // wave-uniform; no workgroup barrier below
@@ -94,7 +94,8 @@ __global__ __launch_bounds__(256) void window_scores_kernel(WindowScoreArgs a) {
 
 int launch_window_scores(const WindowScoreArgs& a, hipStream_t stream) {
   const bool mh = a.heads > 1;
-  JN_REQUIRE(a.r >= 1 && a.r <= 128, kUnsupported, "rank must be in [1, 128]");
+  JN_REQUIRE(a.r >= 1 && a.r <= (mh ? kRegRank : kMaxRank), kUnsupported, "rank must be in [1, %d] (got %d)",
+             mh ? kRegRank : kMaxRank, a.r);
   JN_REQUIRE(a.width >= 1, kInvalidArgument, "window width must be positive");
   JN_REQUIRE(a.all_keys != 1 || a.width == a.Nk, kInvalidArgument, "an all-keys edge list has one slot per key");
   JN_REQUIRE(!mh || (a.heads <= kMaxHeads && a.head_rank >= 1 && a.heads * a.head_rank == a.r), kUnsupported,

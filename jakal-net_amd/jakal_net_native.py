@@ -218,7 +218,8 @@ _COMPRESS_KINDS = {"softsign": 0, "signed_abs_softmax": 1, "signed_entmax15": 2}
 # another path for such shapes (implementation="kernel") can take it.
 MAX_TOPK = 64          # edges per row of the register top-k select (larger k: scored rows)
 MAX_TOPK_LARGE = 4096  # edges per row of a propagation top-k (scored rows, radix select)
-MAX_RANK = 128         # low-rank score rank (over every head)
+MAX_RANK = 1024        # low-rank score rank of one head
+MAX_RANK_HEADS = 128   # ranks over all heads of a multi-head score
 MAX_SELECT_KEYS = 65535  # keys the register select ranks per batch element (more: scored rows)
 CAUSAL_DENSE_MIN_NODES = 128  # full causal windows from this many nodes run on the dense MFMA path
 MAX_HEADS = 8          # heads of a max-aggregated multi-head score
@@ -867,7 +868,7 @@ def _flatten_heads(core, bias, first, second):
     heads, rank = core.shape
     if heads > MAX_HEADS:
         raise NotImplementedError(f"the HIP library takes up to {MAX_HEADS} heads (got {heads}).")
-    _check_rank(heads * rank)
+    _check_rank(heads * rank, MAX_RANK_HEADS)
     if bias is not None and bias.numel() != heads:
         raise RuntimeError("multi-head bias must hold one value per head.")
     flat_bias = None if bias is None else bias.reshape(heads)
@@ -876,9 +877,9 @@ def _flatten_heads(core, bias, first, second):
     return core.reshape(-1), flat_bias, first.reshape(heads * rank, -1), second.reshape(heads * rank, -1), heads
 
 
-def _check_rank(rank: int) -> None:
-    if rank > MAX_RANK:
-        raise NotImplementedError(f"the HIP library scores ranks up to {MAX_RANK} (got {rank}).")
+def _check_rank(rank: int, limit: int = MAX_RANK) -> None:
+    if rank > limit:
+        raise NotImplementedError(f"the HIP library scores ranks up to {limit} here (got {rank}).")
 
 
 def _check_select(k: int, limit: int = MAX_TOPK_LARGE) -> None:
@@ -1629,8 +1630,9 @@ def _raw_select(wps: Tensor, pt: Tensor, topk: int, score_bias: float, limit: in
     B, Nq, R = q.shape
     Nk = kk.shape[1]
     rh = R // H
-    if R > MAX_RANK or H > MAX_HEADS:
-        raise NotImplementedError(f"the HIP select takes up to {MAX_HEADS} heads and {MAX_RANK} ranks in all.")
+    if R > (MAX_RANK if H == 1 else MAX_RANK_HEADS) or H > MAX_HEADS:
+        raise NotImplementedError(f"the HIP select takes {MAX_RANK} ranks of one head, or up to {MAX_HEADS} heads "
+                                  f"of {MAX_RANK_HEADS} ranks in all.")
     if topk <= 0 or topk > limit:
         raise RuntimeError(f"topk must be in the supported fused range [1, {limit}].")
     k = min(int(topk), Nk)
@@ -1736,7 +1738,7 @@ def low_rank_pairwise_topk_backward_cuda(query_val: Tensor, source_val: Tensor, 
             or tuple(indices.shape[:2]) != (B, Nq) or grad_scores.shape != indices.shape
             or source_val.shape[0] != B):
         raise RuntimeError("low_rank_pairwise_topk_backward_cuda: inconsistent shapes.")
-    _check_rank(r)
+    _check_rank(r, MAX_RANK_HEADS)  # the raw backward's rank slots
     f32 = dict(device=dev, dtype=torch.float32)
     if B * Nq * k == 0 or Ns == 0:
         return (torch.zeros(B, Nq, Dq, **f32), torch.zeros(B, Ns, Ds, **f32), torch.zeros(r, Ds, **f32),

@@ -17,6 +17,9 @@
  * jn_last_error() then holds a message for the calling host thread.
  *
  * Index conventions: B = flattened batch, N = nodes, r = rank, k = top-k.
+ * Ranks: single-head entry points take 1 <= r <= 1024 (the reference's
+ * composites take any rank, native/jakal_net_native.cpp:714-832); the
+ * multi-head ones at most 128 ranks over all heads.
  * "projections" is one [B*N, 2r] buffer: columns [0, r) hold the target
  * projection layer_val . U^T, columns [r, 2r) the unscaled source projection
  * layer_val . V^T (U = target_proj.weight, V = source_proj.weight).
@@ -36,7 +39,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature change); this is 13. */
+/* ABI revision of this header (bumped on any signature or accepted-range change); this is 14. */
 int jn_abi_version(void);
 
 /*
@@ -108,7 +111,8 @@ int jn_set_select_mode(int32_t mode);
  *   s[b,i,j] = ((sum_r query[b,i,r]*cq[r] * key[b,j,r]*ck[r]) + bias) / temperature
  * where the scale vector multiplies the query rows when scale_on_query != 0,
  * else the key rows.  Writes the k best (j, s) per row, sorted descending,
- * ties toward the lower j.  1 <= k <= 4096, k <= nk, 1 <= rank <= 128.
+ * ties toward the lower j.  1 <= k <= 4096, k <= nk, rank >= 1 (past 128 ranks
+ * the select scores rows in its workspace).
  * Replaces the score/select stage of
  *   propagation_topk            (native/jakal_net_native.cpp:6399-6424)
  *   low_rank_propagation_topk_forward_cuda (native/jakal_net_native_cuda.cu:1028-1110)

@@ -1201,7 +1201,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 13; }
+int jn_abi_version(void) { return 14; }
 
 int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float eps, float* weight_hat,
                           jn_stream_t stream) {

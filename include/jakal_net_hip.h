@@ -39,7 +39,7 @@ typedef void* jn_stream_t;
 /* Message of the last failing call on this host thread ("" if none). */
 const char* jn_last_error(void);
 
-/* ABI revision of this header (bumped on any signature or accepted-range change); this is 14. */
+/* ABI revision of this header (bumped on any signature or accepted-range change); this is 15. */
 int jn_abi_version(void);
 
 /*
@@ -99,7 +99,11 @@ int jn_set_side_streams(int32_t on);
  * the keys) whenever k <= 16.  Mode 0 picks the cooperative kernel for
  * rank <= 64 when the grid has at least 512 of its 64-row workgroups, the
  * key-split kernel for k <= 16 on grids below 256 of them with >= 192 keys,
- * else the per-wave kernel.  All pick the same entries.  Mode 3 is retired
+ * else the per-wave kernel; rows of at most 1024 keys (one head, fp32
+ * operands, k <= 64) it runs on the small-key select instead, which scores
+ * each workgroup's 16 rows against every key on fp32 MFMAs into LDS and
+ * radix-selects each row (mode 1's arithmetic).  Mode 6 is mode 0 without the
+ * small-key select.  All pick the same entries.  Mode 3 is retired
  * (rejected).  The *_workspace_bytes queries report the split workspace in
  * every mode, so a size query and a later launch agree whatever mode another
  * thread sets in between.  Process-wide (atomic); each launch reads it once.

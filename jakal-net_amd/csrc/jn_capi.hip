@@ -1201,7 +1201,7 @@ extern "C" {
 
 const char* jn_last_error(void) { return jakal::last_error(); }
 
-int jn_abi_version(void) { return 14; }
+int jn_abi_version(void) { return 15; }
 
 int jn_unit_scale_forward(const float* weight, int64_t rows, int64_t rank, float eps, float* weight_hat,
                           jn_stream_t stream) {
@@ -1246,10 +1246,11 @@ int jn_set_side_streams(int32_t on) {
 }
 
 int jn_set_select_mode(int32_t mode) {
-  JN_REQUIRE(mode >= jakal::kSelectSplitF16 && mode <= jakal::kSelectSplitF16KeySplit && mode != 3,
+  JN_REQUIRE(mode >= jakal::kSelectSplitF16 && mode <= jakal::kSelectSplitF16Register && mode != 3,
              kInvalidArgument,
-             "select mode must be 0 (split fp16), 1 (fp32), 2 (split fp16, per-wave kernel), 4 (split fp16, "
-             "cooperative kernel) or 5 (split fp16, key-split per-wave kernel), got %d",
+             "select mode must be 0 (split fp16; the small-key select for rows of up to 1024 keys), 1 (fp32), 2 "
+             "(split fp16, per-wave kernel), 4 (split fp16, cooperative kernel), 5 (split fp16, key-split per-wave "
+             "kernel) or 6 (split fp16 on the register kernels only), got %d",
              (int)mode);
   jakal::set_select_mode(mode);
   return kOk;

@@ -55,7 +55,16 @@ constexpr int kSelectSplitF16Coop4 = 4;
 // Split fp16 on the key-split per-wave kernel whenever k <= 16 (tests); mode 0
 // picks it for k <= 16 on grids below 256 workgroups with >= 192 keys.
 constexpr int kSelectSplitF16KeySplit = 5;
+// Split fp16 on the register kernels only: mode 0 as it was before the
+// small-key select (tests and A/B timing).
+constexpr int kSelectSplitF16Register = 6;
 constexpr int kSelectF32 = 1;
+// Rows of at most kSelectSmallMaxKeys keys (one head, fp32 operands, k <= 64):
+// mode 0 scores the whole row into LDS on fp32 MFMAs and radix-selects it
+// (jn_select_small.hip) instead of running the register select's merges.
+constexpr int kSelectSmallMaxKeys = 1024;
+bool select_small_fits(const SelectArgs& a);
+int launch_topk_select_small(const SelectArgs& a, hipStream_t stream);
 // The mode is process-wide and atomic; each launch reads it once.
 int select_mode();
 void set_select_mode(int mode);

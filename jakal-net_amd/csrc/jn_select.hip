@@ -1308,6 +1308,8 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   // so does one head of more ranks than the register kernels hold
   if (a.k > kSelectMaxK || a.Nk > kSelMaxKeys || large_heads || a.k >= a.Nk || (a.heads <= 1 && a.r > kRegRank))
     return launch_topk_select_large(a, stream);
+  // rows of few keys: the whole score row in LDS, one radix select per row
+  if (select_mode() == kSelectSplitF16 && select_small_fits(a)) return launch_topk_select_small(a, stream);
   JN_REQUIRE(a.k >= 1 && a.k <= kSelectMaxK, kUnsupported, "top-k select supports 1 <= k <= %d (got %d)", kSelectMaxK,
              a.k);
   JN_REQUIRE(a.k < a.Nk, kInvalidArgument, "top-k select needs k < key count (k=%d, Nk=%d)", a.k, a.Nk);
@@ -1328,6 +1330,7 @@ int launch_topk_select(const SelectArgs& a_in, hipStream_t stream) {
   // multi-head scores always run on the per-wave split kernel; bf16 operands
   // take the split kernels' forms whatever the mode
   int mode = mh ? kSelectSplitF16Wave : select_mode();
+  if (mode == kSelectSplitF16Register) mode = kSelectSplitF16;
   if (a.bf16 && mode == kSelectF32) mode = kSelectSplitF16;
 
   if (mode != kSelectF32) {

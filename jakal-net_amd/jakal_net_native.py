@@ -297,6 +297,7 @@ SELECT_F32 = 1
 SELECT_SPLIT_F16_WAVE = 2
 SELECT_SPLIT_F16_COOP4 = 4
 SELECT_SPLIT_F16_KEYSPLIT = 5
+SELECT_SPLIT_F16_REGISTER = 6
 
 
 def set_select_mode(mode: int = SELECT_SPLIT_F16) -> None:
@@ -307,7 +308,10 @@ def set_select_mode(mode: int = SELECT_SPLIT_F16) -> None:
     The split arithmetic on one kernel only: SELECT_SPLIT_F16_WAVE (per-wave
     streaming), SELECT_SPLIT_F16_COOP4 (LDS-staged cooperative, rank <= 64)
     and SELECT_SPLIT_F16_KEYSPLIT (the four waves of a workgroup split the keys
-    of 16 query rows, k <= 16).  Every mode selects the same entries."""
+    of 16 query rows, k <= 16).  The default takes rows of at most 1024 keys
+    (one head, fp32, k <= 64) on the small-key select instead (fp32 MFMA score
+    rows in LDS, a radix select per row); SELECT_SPLIT_F16_REGISTER keeps them
+    on the split kernels.  Every mode selects the same entries."""
     _check(_LIB.jn_set_select_mode(int(mode)))
 
 

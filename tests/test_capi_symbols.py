@@ -69,7 +69,7 @@ def test_select_workspace_is_mode_independent_without_gpu():
         assert lib.jn_lowrank_topk_select_workspace_bytes(16, 4096, 64) == fwd(16, 4096, 64)
         # the size does not depend on the mode: a query and a launch agree whatever mode is set in between
         split_size = fwd(16, 4096, 64)
-        for mode in (1, 2, 4, 5):
+        for mode in (1, 2, 4, 5, 6):
             assert lib.jn_set_select_mode(mode) == 0
             assert fwd(16, 4096, 64) == split_size
         assert lib.jn_set_select_mode(3) != 0  # retired

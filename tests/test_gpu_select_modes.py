@@ -4,8 +4,8 @@ The per-op tests run the default split-fp16 select (fp16 MFMAs over two-term
 fp16 splits of power-of-two-scaled operands, fp32 accumulation).  These tests
 cover the fp32-MFMA select (jn_set_select_mode(1)) and each split-fp16 kernel
 on its own (per-wave streaming, mode 2; LDS-staged cooperative, mode 4;
-key-split per-wave, mode 5) on the
-same select, top-k propagation and transition cases, check that the split
+key-split per-wave, mode 5; mode 0 on the register kernels only, mode 6) on
+the same select, top-k propagation and transition cases, check that the split
 kernels pick identical entries and values up to the C4 shape, and the split path on what its scaling has
 to survive: key and query rows whose magnitudes span many octaves, all-zero
 rows, ranks that are not a multiple of the 32-rank K-step, and bias and
@@ -37,10 +37,11 @@ def _mode_value(name):
     import jakal_net_native as jn
 
     return {"split_f16": jn.SELECT_SPLIT_F16, "f32": jn.SELECT_F32, "split_wave": jn.SELECT_SPLIT_F16_WAVE,
-            "split_coop4": jn.SELECT_SPLIT_F16_COOP4, "split_keysplit": jn.SELECT_SPLIT_F16_KEYSPLIT}[name]
+            "split_coop4": jn.SELECT_SPLIT_F16_COOP4, "split_keysplit": jn.SELECT_SPLIT_F16_KEYSPLIT,
+            "split_register": jn.SELECT_SPLIT_F16_REGISTER}[name]
 
 
-@pytest.fixture(params=["split_f16", "f32", "split_wave", "split_coop4", "split_keysplit"])
+@pytest.fixture(params=["split_f16", "f32", "split_wave", "split_coop4", "split_keysplit", "split_register"])
 def mode(request):
     import jakal_net_native as jn
 
@@ -90,6 +91,62 @@ def test_select_both_modes(dev, mode, r, k, Nq, Nk, spread):
             check_selection(idx, score / row, ref / row, k)
         else:
             check_selection(idx, score, ref, k)
+
+
+@pytest.mark.parametrize("r,k,B,Nq,Nk", [(64, 64, 2, 100, 65), (64, 64, 3, 50, 1024), (1, 4, 2, 33, 512),
+                                         (3, 16, 2, 40, 513), (127, 20, 1, 17, 300), (128, 64, 2, 64, 700),
+                                         (8, 1, 4, 16, 2)])
+def test_small_key_select_matches_oracle(dev, r, k, B, Nq, Nk):
+    """Rows of at most 1024 keys take the small-key select in the default
+    mode: every key's score is kept in LDS (512- and 1024-key tiles, so the
+    513-key case is the first of the larger tile) and each row is
+    radix-selected.  k = 64 against 65 keys leaves one key out of every row; a
+    rank of 1 or 3 runs the rank loop's tail alone; Nq off the 16-row tile
+    leaves a partial last tile.  Checked against the oracle on the three
+    scale / bias / temperature placements, and against the register kernels
+    (mode 6) for identical index sets where the k-th/(k+1)-th gap is clear."""
+    import jakal_net_native as jn
+
+    g = torch.Generator().manual_seed(8100 + r + k + Nk)
+    q = torch.randn(B, Nq, r, generator=g) * 0.5
+    key = torch.randn(B, Nk, r, generator=g) * 0.5
+    scale = torch.rand(r, generator=g) + 0.5
+    for scale_on_query, temp, bias in ((False, 1.0, None), (True, 1.7, torch.tensor(0.25)),
+                                       (False, 0.6, torch.tensor(-0.5))):
+        idx, score, ref = _select(dev, q, key, scale, bias, scale_on_query, temp, k)
+        check_selection(idx, score, ref, k)
+        try:
+            jn.set_select_mode(jn.SELECT_SPLIT_F16_REGISTER)
+            idx6, score6, _ = _select(dev, q, key, scale, bias, scale_on_query, temp, k)
+        finally:
+            jn.set_select_mode(jn.SELECT_SPLIT_F16)
+        srt = np.sort(ref, axis=-1)[..., ::-1]
+        clear = (srt[..., k - 1] - srt[..., k]) > 1e-4 if k < Nk else np.ones(srt.shape[:-1], bool)
+        same = np.sort(idx, -1) == np.sort(idx6, -1)
+        assert same[clear].all()
+        assert np.abs(score - score6)[clear].max() < 1e-5 * max(1.0, np.abs(ref).max())
+
+
+def test_small_key_select_ties_keep_lowest_index(dev):
+    """Equal scores across the k-th boundary: the radix select's tie rule keeps
+    the lowest key indices, like the register kernels, and emits them in key
+    order within each run of equal scores."""
+    import jakal_net_native as jn
+
+    g = torch.Generator().manual_seed(8200)
+    key = torch.randn(2, 600, 16, generator=g)
+    key[:, 7] *= 3.0  # |key 7|^2 ~ 144, far above any other key's score against it
+    key[:, 100:400] = key[:, 7:8]  # 300 copies of key 7
+    q = key[:, 7:8].repeat(1, 40, 1) + 0.0
+    idx, score = jn.low_rank_topk_select(q.to(dev), key.to(dev), None, None, False, 1.0, 50)
+    idx = idx.cpu()
+    ref = (q.double() @ key.double().transpose(1, 2))
+    top = ref.max(-1).values
+    # every row's winners: key 7 and keys 100..148, all of the tied maximum
+    expect = torch.cat([torch.tensor([7]), torch.arange(100, 149)]).to(torch.int32)
+    tied = (ref == top[..., None]).sum(-1)
+    assert bool((tied >= 50).all())
+    assert torch.equal(idx, expect.expand_as(idx))
 
 
 @pytest.mark.parametrize("Nk", [200, 2100])

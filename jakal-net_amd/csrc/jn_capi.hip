@@ -1151,7 +1151,26 @@ int propagation_window_forward_impl(const float* layer_val, const float* project
     w.head_rank = (int)(rank / heads);
     w.head = edge_head;
   }
-  rc = launch_window_scores(w, st);
+  if (!mh && window_kernels() == 0 &&
+      band_kernels_fit((int)width, r, 2 * r, 2 * r, projections, projections + r, false)) {
+    BandDotsArgs sd{};  // the band's scores as MFMA tiles of queries against their key span
+    sd.B = (int)batch;
+    sd.N = (int)nodes;
+    sd.k = (int)width;
+    sd.D = r;
+    sd.gdv = projections;
+    sd.ld_gdv = 2 * r;
+    sd.pv = projections + r;
+    sd.ld_pv = 2 * r;
+    sd.ascale = core_weight;
+    sd.bias = bias;
+    sd.inv_temperature = 1.0f;
+    sd.score_out = edge_score;
+    sd.idx_out = edge_index;
+    rc = launch_band_dots(sd, st);
+  } else {
+    rc = launch_window_scores(w, st);
+  }
   if (rc) return rc;
 
   if (window_kernels() == 0 &&

@@ -258,6 +258,16 @@ struct BandDotsArgs {
   float* g_score;    // [B*N, k]: dot partial over the first half of D
   float* coef;       // [B*N, k]: dot partial over the second half
   int bf16;          // gdv and pv hold bf16 elements
+  // Score mode (score_out non-null, fp32 rows): the window's pairwise scores.
+  // One pass over all D columns of gdv (the query projection, column d times
+  // ascale[d] when given) against pv (the key projection); slot e of row i
+  // gets score_out = (dot + bias[0]) * inv_temperature and idx_out = its key
+  // i - (k - 1) + e, or 0 and -1 before the first row.
+  const float* ascale;
+  const float* bias;
+  float inv_temperature;
+  float* score_out;
+  int32_t* idx_out;
 };
 // Whether the band kernels take these operands (k <= kBandMaxK, whole 16-byte
 // packs per row, 16-byte aligned rows); otherwise the edge kernels run.

@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256) void band_aggregate_kernel(BandAggArgs a) {
 // (double buffered, one barrier per slice); a wave owns 16 rows and only
 // multiplies the span tiles its band meets.
 // ---------------------------------------------------------------------------
-template <typename T, int NT>
+template <typename T, int NT, bool SCORES>
 __global__ __launch_bounds__(256) void band_dots_kernel(BandDotsArgs a) {
   __shared__ __align__(16) float sA[2][kBandRows * kBandKStride];
   __shared__ __align__(16) float sB[2][NT * 16 * kBandKStride];
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(256) void band_dots_kernel(BandDotsArgs a) {
   const int tiles = (a.N + kBandRows - 1) / kBandRows;
   const int64_t logical = xcd_swizzle(blockIdx.x, gridDim.x);
   const int t = (int)(logical % tiles);
-  const bool scores = a.score_out != nullptr;
+  constexpr bool scores = SCORES;  // score mode: a.score_out is set
   const int halves = scores ? 1 : 2;
   const int half = (int)((logical / tiles) % halves);
   const int64_t b = logical / tiles / halves;
@@ -430,12 +430,12 @@ int launch_band_aggregate(const BandAggArgs& a, hipStream_t stream) {
   return kOk;
 }
 
-template <typename T>
+template <typename T, bool SCORES>
 static void launch_band_dots_nt(const BandDotsArgs& a, dim3 grid, hipStream_t stream) {
   const int nt = (kBandRows - 1 + a.k + 15) / 16;  // span tiles of 16 rows
-  if (nt <= 6) hipLaunchKernelGGL((band_dots_kernel<T, 6>), grid, dim3(256), 0, stream, a);
-  else if (nt <= 8) hipLaunchKernelGGL((band_dots_kernel<T, 8>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((band_dots_kernel<T, 12>), grid, dim3(256), 0, stream, a);
+  if (nt <= 6) hipLaunchKernelGGL((band_dots_kernel<T, 6, SCORES>), grid, dim3(256), 0, stream, a);
+  else if (nt <= 8) hipLaunchKernelGGL((band_dots_kernel<T, 8, SCORES>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((band_dots_kernel<T, 12, SCORES>), grid, dim3(256), 0, stream, a);
 }
 
 int launch_band_dots(const BandDotsArgs& a, hipStream_t stream) {
@@ -450,8 +450,9 @@ int launch_band_dots(const BandDotsArgs& a, hipStream_t stream) {
   JN_REQUIRE(blocks < (1LL << 31) && (int64_t)a.B * a.N * a.k < (1LL << 31), kInvalidArgument, "too many rows");
   const dim3 grid((unsigned)blocks);
   JN_PROFILE(scores ? "band_scores_kernel" : "band_dots_kernel", stream);
-  if (a.bf16) launch_band_dots_nt<bf16_t>(a, grid, stream);
-  else launch_band_dots_nt<float>(a, grid, stream);
+  if (scores) launch_band_dots_nt<float, true>(a, grid, stream);
+  else if (a.bf16) launch_band_dots_nt<bf16_t, false>(a, grid, stream);
+  else launch_band_dots_nt<float, false>(a, grid, stream);
   JN_LAUNCH_CHECK();
   return kOk;
 }

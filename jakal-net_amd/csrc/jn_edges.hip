@@ -1129,7 +1129,12 @@ __device__ __forceinline__ float transpose_sum(const float (&v)[G]) {
 // value-row gather is then not run; it finds x through CsrArgs::pos).
 // G records per group: their rows are in flight together, then G dot
 // partials are summed over the wave by one transpose-sum.
-template <typename T, int W, int G>
+// BUF (a batch element's gdv rows span less than 2^31 bytes): the rows load
+// through a buffer resource over the column's batch element, the record's row
+// offset in the scalar offset and the lane's column offset in the vector
+// offset; records past the segment and lanes past D read zeros out of range,
+// so a group's loads need no per-lane branch, zeroing or 64-bit address.
+template <typename T, int W, int G, bool BUF>
 __global__ __launch_bounds__(256) void cols_gather_dots_kernel(ColsBwdArgs a) {
   constexpr int SLAB = kWave * W;
   const int lane = lane_id();
@@ -1148,6 +1153,12 @@ __global__ __launch_bounds__(256) void cols_gather_dots_kernel(ColsBwdArgs a) {
       on ? unpack16<T, W>(load_nt16(reinterpret_cast<const T*>(a.pv) + col * a.ld_pv + d)) : pack_zero<T, W>();
   float* part = slab == 0 ? a.dots0 : a.dots1;
   const int64_t rec_base = recs.rec - a.rec;  // record index of the column's first record
+  const int64_t bq = col / a.Nk;              // the column's batch element
+  const int row0 = (int)(bq * a.Nq);          // its first global row
+  const uint32_t row_bytes = (uint32_t)a.D * (uint32_t)sizeof(T);
+  const auto rs_g = make_rsrc(reinterpret_cast<const T*>(a.gdv) + (BUF ? bq * a.Nq * a.D : 0),
+                              BUF ? (uint32_t)((int64_t)a.Nq * row_bytes) : 0u);
+  const uint32_t voff = on ? (uint32_t)d * (uint32_t)sizeof(T) : kOobOffset;
 
   Pack<W> acc = pack_zero<T, W>(), acc1 = acc;  // even / odd records
   float st = 0.f;
@@ -1168,8 +1179,15 @@ __global__ __launch_bounds__(256) void cols_gather_dots_kernel(ColsBwdArgs a) {
 #pragma unroll
       for (int u = 0; u < G; ++u) {
         const int src = min(q + u, kWave - 1);
-        raw[u] = (q + u < n && on) ? *reinterpret_cast<const uint4*>(gdv + (int64_t)readlane_i(row, src) * a.D)
-                                   : make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (BUF) {
+          const bool live = q + u < n;  // wave-uniform
+          const uint32_t so = live ? (uint32_t)(readlane_i(row, src) - row0) * row_bytes : 0u;
+          raw[u] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(rs_g, live ? voff : kOobOffset, so, 0));
+        } else {
+          raw[u] = (q + u < n && on) ? *reinterpret_cast<const uint4*>(gdv + (int64_t)readlane_i(row, src) * a.D)
+                                     : make_uint4(0u, 0u, 0u, 0u);
+        }
       }
       // lanes (64 / G) u receive record q + u's total
       constexpr int LPR = kWave / G;
@@ -1216,8 +1234,14 @@ int launch_cols_gather_dots(const ColsBwdArgs& a, hipStream_t stream) {
   JN_REQUIRE(blocks < (1LL << 31), kInvalidArgument, "too many columns");
   JN_PROFILE("cols_gather_dots_kernel", stream);
   const dim3 grid((unsigned)blocks);
-  if (a.bf16) hipLaunchKernelGGL((cols_gather_dots_kernel<bf16_t, 8, 4>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((cols_gather_dots_kernel<float, 4, 8>), grid, dim3(256), 0, stream, a);
+  const bool buf = (int64_t)a.Nq * a.D * (a.bf16 ? 2 : 4) < (int64_t)kOobOffset;
+  if (a.bf16) {
+    if (buf) hipLaunchKernelGGL((cols_gather_dots_kernel<bf16_t, 8, 4, true>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((cols_gather_dots_kernel<bf16_t, 8, 4, false>), grid, dim3(256), 0, stream, a);
+  } else {
+    if (buf) hipLaunchKernelGGL((cols_gather_dots_kernel<float, 4, 8, true>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((cols_gather_dots_kernel<float, 4, 8, false>), grid, dim3(256), 0, stream, a);
+  }
   JN_LAUNCH_CHECK();
   return kOk;
 }

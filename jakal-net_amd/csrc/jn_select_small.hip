@@ -6,11 +6,11 @@
 // merge and sort machinery sets a fixed cost of tens of microseconds per
 // launch (C3's and C5's transitions and slot propagations select over 64 to
 // 1024 keys).  Here the whole score row fits LDS instead:
-//   1. a workgroup (4 waves) takes 16 query rows of one batch element; wave w
-//      scores key tiles w, w + 4, ... of 16 keys on v_mfma_f32_16x16x4f32
+//   1. a workgroup (8 or 16 waves) takes 16 query rows of one batch element;
+//      wave w scores key tiles w, w + WV, ... of 16 keys on v_mfma_f32_16x16x4f32
 //      (fp32 operands, fp32 accumulation: the arithmetic of select mode 1)
 //      and writes each score as an order key into the row's LDS line;
-//   2. wave w then selects rows 4w .. 4w + 3: a radix select over the order
+//   2. each wave then selects one or two of the rows: a radix select over the order
 //      keys (four 8-bit digits, LDS histograms with integer atomics) finds the
 //      exact k-th key T; the keys above T and the lowest-index keys equal to T
 //      (index order is lane order within each 64-key block) are the row's k
@@ -90,14 +90,18 @@ __device__ __forceinline__ int sm_wave_scan(int v) {
 
 // NK: keys per row at most (512 or 1024); RQ: rank quads per lane group
 // (ranks up to 16 * RQ); VEC: 16-byte operand rows.
-template <int NK, int RQ, bool VEC>
-__global__ __launch_bounds__(256) void select_small_kernel(SelectArgs a) {
+// WV waves per workgroup: they split the key tiles of phase 1 and take
+// 16 / WV rows each in phase 2.
+template <int NK, int RQ, bool VEC, int WV>
+__global__ __launch_bounds__(WV * 64) void select_small_kernel(SelectArgs a) {
+  static_assert(kSmRows % WV == 0, "whole rows per wave");
+  constexpr int RPW = kSmRows / WV;  // rows per wave in the selection
   constexpr int KSTR = NK + 1;  // LDS row stride of the order keys
   constexpr int PL = NK / kWave;  // keys per lane in the selection
   __shared__ uint32_t s_key[kSmRows * KSTR];
-  __shared__ __align__(16) uint32_t s_hist[4][256];
-  __shared__ float s_win_s[4][kWave];
-  __shared__ int s_win_i[4][kWave];
+  __shared__ __align__(16) uint32_t s_hist[WV][256];
+  __shared__ float s_win_s[WV][kWave];
+  __shared__ int s_win_i[WV][kWave];
 
   const int lane = lane_id(), wave = wave_id();
   const int g = lane >> 4, col = lane & 15;
@@ -140,31 +144,48 @@ __global__ __launch_bounds__(256) void select_small_kernel(SelectArgs a) {
       kscale[u][3] = on_q ? 1.f : sv.w;
     }
   }
+  // wave w scores tiles w, w + WV, ...; PD of its tiles' key loads are in
+  // flight at a time (slot i of the ring holds tile t0 + WV i), each slot
+  // refilled with the tile PD steps ahead as soon as its own is scored
+  constexpr int PD = RQ <= 4 ? 4 : 2;
   const int ntiles = (a.Nk + 15) / 16;
-  for (int t = wave; t < ntiles; t += 4) {
+  float4 kring[PD][RQ];
+  auto load_tile = [&](float4 (&kv)[RQ], int t) {
     const int j = 16 * t + col;  // this lane's key (A operand row)
     const float* kr = kb + (int64_t)min(j, a.Nk - 1) * a.ldk;
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < RQ; ++u) {
-      const float4 kv = j < a.Nk ? load4(kr, u) : make_float4(0.f, 0.f, 0.f, 0.f);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x * kscale[u][0], qf[u][0], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y * kscale[u][1], qf[u][1], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z * kscale[u][2], qf[u][2], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w * kscale[u][3], qf[u][3], acc, 0, 0, 0);
-    }
-    // lane (g, col) holds keys 16t + 4g + v of row col
+    for (int u = 0; u < RQ; ++u) kv[u] = (t < ntiles && j < a.Nk) ? load4(kr, u) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int jj = 16 * t + 4 * g + v;
-      if (jj < a.Nk) s_key[col * KSTR + jj] = small_order_key((acc[v] + bias) * inv_temp);
+  for (int i = 0; i < PD; ++i) load_tile(kring[i], wave + WV * i);
+  for (int t0 = wave; t0 < ntiles; t0 += WV * PD) {
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+      const int t = t0 + WV * i;
+      if (t >= ntiles) break;  // wave-uniform
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < RQ; ++u) {
+        const float4 kv = kring[i][u];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x * kscale[u][0], qf[u][0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y * kscale[u][1], qf[u][1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z * kscale[u][2], qf[u][2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w * kscale[u][3], qf[u][3], acc, 0, 0, 0);
+      }
+      load_tile(kring[i], t + WV * PD);
+      // lane (g, col) holds keys 16t + 4g + v of row col
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int jj = 16 * t + 4 * g + v;
+        if (jj < a.Nk) s_key[col * KSTR + jj] = small_order_key((acc[v] + bias) * inv_temp);
+      }
     }
   }
   __syncthreads();
 
   // ---- 2. wave w selects rows 4w .. 4w + 3 ------------------------------------
   const int k = a.k;
-  for (int rr = 4 * wave; rr < 4 * wave + 4; ++rr) {
+  for (int rr = RPW * wave; rr < RPW * (wave + 1); ++rr) {
     const int row = row0 + rr;
     if (row >= a.Nq) break;  // wave-uniform; no workgroup barrier below
     uint32_t kv[PL];
@@ -233,15 +254,18 @@ __global__ __launch_bounds__(256) void select_small_kernel(SelectArgs a) {
   }
 }
 
+// 16 waves (one row each) where the registers allow four waves per SIMD
+// (512-key rows of rank <= 64), else 8 waves (two rows each)
 template <int NK, bool VEC>
 void launch_small_rq(const SelectArgs& a, dim3 grid, hipStream_t stream) {
   const int rq = (a.r + 15) / 16;
+  constexpr int W16 = NK == 512 ? 16 : 8;
   switch (rq) {
-    case 1: hipLaunchKernelGGL((select_small_kernel<NK, 1, VEC>), grid, dim3(256), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((select_small_kernel<NK, 2, VEC>), grid, dim3(256), 0, stream, a); break;
+    case 1: hipLaunchKernelGGL((select_small_kernel<NK, 1, VEC, W16>), grid, dim3(W16 * 64), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((select_small_kernel<NK, 2, VEC, W16>), grid, dim3(W16 * 64), 0, stream, a); break;
     case 3:
-    case 4: hipLaunchKernelGGL((select_small_kernel<NK, 4, VEC>), grid, dim3(256), 0, stream, a); break;
-    default: hipLaunchKernelGGL((select_small_kernel<NK, 8, VEC>), grid, dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((select_small_kernel<NK, 4, VEC, W16>), grid, dim3(W16 * 64), 0, stream, a); break;
+    default: hipLaunchKernelGGL((select_small_kernel<NK, 8, VEC, 8>), grid, dim3(8 * 64), 0, stream, a); break;
   }
 }
 

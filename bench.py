@@ -434,8 +434,8 @@ class TransitionC3:
         c = self.config
         B, S, Bn, D, r, k = (c[x] for x in ("batch", "s_nodes", "b_nodes", "dim", "rank", "topk"))
         E, rows = self.edges(), B * (S + Bn)
-        if name.startswith("lowrank_topk_select_kernel"):
-            return "mfma", 2.0 * B * S * Bn * r * 2  # both directions score S x B pairs
+        if name.startswith("lowrank_topk_select_kernel") or name.startswith("select_small_kernel"):
+            return "mfma", 2.0 * B * S * Bn * r  # per launch: one direction scores its S x B pairs
         if name.startswith("select_split_"):
             return split_prep_model(name, B * (S + Bn) / 2, r)  # keys: B rows one way, S rows the other
         # per launch = half of both directions; `rows` counts source rows of both

@@ -1636,12 +1636,58 @@ __global__ __launch_bounds__(256) void finalize_small_grads_kernel(const float* 
   }
 }
 
+// Small problems in one launch: workgroup c sums output column c over every
+// partial row (c < r) or row sum (the bias columns), strided by thread, then
+// by a fixed tree.  Rows past the end add zeros (no reads).
+__global__ __launch_bounds__(256) void finalize_direct_kernel(const float* part_c, int nparts, int r,
+                                                              const float* rowsum, int64_t nrows, int nbias,
+                                                              float* grad_c, int accumulate_c, float* grad_bias) {
+  __shared__ float red[256];
+  const int b = blockIdx.x, t = threadIdx.x;
+  // eight loads in flight per thread, added in index order
+  constexpr int kB = 8;
+  const bool bias_col = b >= r;
+  const int64_t n = bias_col ? nrows : nparts;
+  const float* src = bias_col ? rowsum + (b - r) : part_c + b;
+  const int64_t stride = bias_col ? nbias : r;
+  float s = 0.f;
+  for (int64_t p0 = t; p0 < n; p0 += 256 * kB) {
+    float v[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) v[u] = p0 + 256 * u < n ? src[(p0 + 256 * u) * stride] : 0.f;
+#pragma unroll
+    for (int u = 0; u < kB; ++u) s += v[u];
+  }
+  red[t] = s;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (t < o) red[t] += red[t + o];
+    __syncthreads();
+  }
+  if (t == 0) {
+    if (b < r) {
+      if (grad_c) grad_c[b] = accumulate_c ? grad_c[b] + red[0] : red[0];
+    } else if (grad_bias) {
+      grad_bias[b - r] = red[0];
+    }
+  }
+}
+constexpr int kFinDirectParts = 4096;   // partial rows summed by one workgroup at most
+constexpr int64_t kFinDirectRows = 16384;  // row sums likewise
+
 int launch_finalize_small_grads(const float* part_c, int nparts, int r, float* grad_c, int accumulate_c,
                                 const float* rowsum, int64_t nrows, float* grad_bias, float* stage,
                                 hipStream_t stream, int nbias) {
   JN_REQUIRE(r >= 1 && r <= kMaxRank, kUnsupported, "rank must be in [1, %d]", kMaxRank);
   JN_REQUIRE(nbias >= 1 && nbias <= kMaxHeads, kUnsupported, "1..%d bias columns", kMaxHeads);
   static_assert(kFinBlocks == 256, "the second stage maps one thread per stage row");
+  if (nparts <= kFinDirectParts && nrows <= kFinDirectRows) {
+    JN_PROFILE("finalize_direct_kernel", stream);
+    hipLaunchKernelGGL(finalize_direct_kernel, dim3(r + nbias), dim3(256), 0, stream, part_c, nparts, r, rowsum,
+                       nrows, nbias, grad_c, accumulate_c, grad_bias);
+    JN_LAUNCH_CHECK();
+    return kOk;
+  }
   {
     JN_PROFILE("finalize_partials_kernel", stream);
     hipLaunchKernelGGL(finalize_partials_kernel, dim3(kFinBlocks), dim3(256), 0, stream, part_c, nparts, r, rowsum,
